@@ -1,0 +1,306 @@
+"""ctypes binding of libb2c_hip.so (include/b2c.h, include/b2c_kernels.h).
+
+Python is plumbing here: tests and the benchmark drive the C ABI through these wrappers. There is no
+fallback: if the HIP library is missing the import of ``lib()`` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libb2c_hip.so")
+
+GRAD_LANES = 13
+RT_W = 8
+
+
+class Camera(C.Structure):
+    _fields_ = [("width", C.c_int), ("height", C.c_int), ("fx", C.c_float), ("fy", C.c_float), ("cx", C.c_float),
+                ("cy", C.c_float), ("R", C.c_float * 9), ("t", C.c_float * 3)]
+
+
+class CameraGPU(C.Structure):
+    _fields_ = [("R", C.c_float * 9), ("t", C.c_float * 3), ("pos", C.c_float * 3), ("fx", C.c_float),
+                ("fy", C.c_float), ("cx", C.c_float), ("cy", C.c_float), ("W", C.c_int), ("H", C.c_int),
+                ("lim_pos_x", C.c_float), ("lim_pos_y", C.c_float), ("lim_neg_x", C.c_float), ("lim_neg_y", C.c_float)]
+
+
+class RenderOpts(C.Structure):
+    _fields_ = [("cam", Camera), ("W", C.c_int), ("H", C.c_int), ("bg", C.c_float * 3), ("sh_degree", C.c_int),
+                ("bwd_info", C.c_int)]
+
+
+class LossOpts(C.Structure):
+    _fields_ = [("l1_w", C.c_float), ("ssim_w", C.c_float), ("bg", C.c_float * 3), ("composite", C.c_int),
+                ("mask", C.c_int), ("alpha_lane", C.c_int), ("match_alpha_weight", C.c_float), ("scale", C.c_float),
+                ("grad_scale", C.c_float)]
+
+
+class CtxInfo(C.Structure):
+    _fields_ = [("W", C.c_int), ("H", C.c_int), ("tiles_x", C.c_int), ("tiles_y", C.c_int), ("n_tiles", C.c_int),
+                ("tile_bits", C.c_int), ("num_isect", C.c_uint32), ("isect_cap", C.c_uint64)]
+
+
+class StepTimes(C.Structure):
+    _fields_ = [("project_ms", C.c_float), ("bin_ms", C.c_float), ("forward_ms", C.c_float), ("loss_ms", C.c_float),
+                ("backward_ms", C.c_float), ("vjp_ms", C.c_float), ("total_ms", C.c_float)]
+
+    def as_dict(self):
+        return {k: float(getattr(self, k)) for k, _ in self._fields_}
+
+
+# Every symbol include/b2c.h and include/b2c_kernels.h declare.
+EXPORTS = [
+    "b2c_last_error", "b2c_get_device_count", "b2c_camera_gpu_from", "b2c_model_create", "b2c_model_destroy",
+    "b2c_model_upload", "b2c_model_read", "b2c_ctx_create", "b2c_ctx_destroy", "b2c_ctx_setup", "b2c_ctx_info_get",
+    "b2c_ctx_read", "b2c_ctx_write", "b2c_ctx_zero", "b2c_ctx_synchronize", "b2c_ctx_stream", "b2c_view_create",
+    "b2c_view_destroy", "b2c_render_forward", "b2c_project_splats", "b2c_bin_and_sort", "b2c_rasterize_forward",
+    "b2c_photometric_loss", "b2c_accumulate_loss", "b2c_rasterize_backward", "b2c_optimizer_grad", "b2c_train_step",
+    # launcher layer
+    "b2c_hip_project", "b2c_radix_sort_temp_bytes", "b2c_hip_radix_sort_pairs", "b2c_hip_depth_keys",
+    "b2c_scan_temp_bytes", "b2c_hip_scan_counts", "b2c_hip_emit", "b2c_hip_tile_ranges", "b2c_hip_raster_fwd",
+    "b2c_hip_raster_bwd", "b2c_hip_photometric", "b2c_hip_accumulate_loss", "b2c_hip_vjp", "b2c_hip_fill_u32",
+]
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"HIP library not built: {LIB_PATH} (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        p, i, f = C.c_void_p, C.c_int, C.c_float
+        L.b2c_last_error.restype = C.c_char_p
+        L.b2c_get_device_count.argtypes = [C.POINTER(i)]
+        L.b2c_camera_gpu_from.argtypes = [C.POINTER(Camera), i, i, C.POINTER(CameraGPU)]
+        L.b2c_model_create.restype = p
+        L.b2c_model_destroy.argtypes = [p]
+        L.b2c_model_upload.argtypes = [p, i, i, i, p, p, p, p, p, p]
+        L.b2c_model_read.argtypes = [p, C.c_char_p, p, C.c_size_t]
+        L.b2c_ctx_create.restype = p
+        L.b2c_ctx_destroy.argtypes = [p]
+        L.b2c_ctx_setup.argtypes = [p, i, i, i]
+        L.b2c_ctx_info_get.argtypes = [p, C.POINTER(CtxInfo)]
+        L.b2c_ctx_read.argtypes = [p, C.c_char_p, p, C.c_size_t]
+        L.b2c_ctx_write.argtypes = [p, C.c_char_p, p, C.c_size_t]
+        L.b2c_ctx_zero.argtypes = [p, C.c_char_p]
+        L.b2c_ctx_synchronize.argtypes = [p]
+        L.b2c_ctx_stream.argtypes = [p]
+        L.b2c_ctx_stream.restype = p
+        L.b2c_view_create.restype = p
+        L.b2c_view_create.argtypes = [i, i, p, p]
+        L.b2c_view_destroy.argtypes = [p]
+        L.b2c_render_forward.argtypes = [p, p, C.POINTER(RenderOpts)]
+        L.b2c_project_splats.argtypes = [p, p, C.POINTER(RenderOpts)]
+        L.b2c_bin_and_sort.argtypes = [p, p]
+        L.b2c_rasterize_forward.argtypes = [p, C.POINTER(RenderOpts)]
+        L.b2c_photometric_loss.argtypes = [p, p, C.POINTER(LossOpts)]
+        L.b2c_accumulate_loss.argtypes = [p]
+        L.b2c_rasterize_backward.argtypes = [p, p, C.POINTER(RenderOpts), i, f]
+        L.b2c_optimizer_grad.argtypes = [p, p, C.POINTER(RenderOpts), i, i]
+        L.b2c_train_step.argtypes = [p, p, p, C.POINTER(RenderOpts), C.POINTER(LossOpts), i, i, C.POINTER(StepTimes)]
+        L.b2c_radix_sort_temp_bytes.restype = C.c_size_t
+        L.b2c_radix_sort_temp_bytes.argtypes = [C.c_uint32]
+        L.b2c_scan_temp_bytes.restype = C.c_size_t
+        L.b2c_scan_temp_bytes.argtypes = [C.c_uint32]
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        raise RuntimeError(f"b2c {what} failed ({rc}): {lib().b2c_last_error().decode()}")
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def camera_struct(cam) -> Camera:
+    c = Camera()
+    c.width, c.height = int(cam.width), int(cam.height)
+    c.fx, c.fy, c.cx, c.cy = float(cam.fx), float(cam.fy), float(cam.cx), float(cam.cy)
+    for k in range(9):
+        c.R[k] = float(cam.R[k])
+    for k in range(3):
+        c.t[k] = float(cam.t[k])
+    return c
+
+
+def camera_gpu_from(cam, W=None, H=None) -> dict:
+    g = CameraGPU()
+    check(lib().b2c_camera_gpu_from(C.byref(camera_struct(cam)), cam.width if W is None else W,
+                                    cam.height if H is None else H, C.byref(g)), "camera_gpu_from")
+    return dict(R=np.array(g.R[:], np.float32), t=np.array(g.t[:], np.float32), pos=np.array(g.pos[:], np.float32),
+                fx=np.float32(g.fx), fy=np.float32(g.fy), cx=np.float32(g.cx), cy=np.float32(g.cy), W=g.W, H=g.H,
+                lim_pos_x=np.float32(g.lim_pos_x), lim_pos_y=np.float32(g.lim_pos_y),
+                lim_neg_x=np.float32(g.lim_neg_x), lim_neg_y=np.float32(g.lim_neg_y))
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    rc = lib().b2c_get_device_count(C.byref(n))
+    return n.value if rc == 0 else 0
+
+
+_FIELD_SPEC = {
+    # name: (dtype, per-element shape, size key)  size key: n splats, P pixels, M isects, T tiles
+    "proj0": (np.float32, (4,), "n"), "proj1": (np.float32, (4,), "n"), "proj2": (np.float32, (4,), "n"),
+    "proj3": (np.float32, (2,), "n"), "tile_count": (np.uint32, (), "n"), "tile_off": (np.uint32, (), "n"),
+    "hit_info": (np.uint32, (2,), "n"), "order": (np.uint32, (), "n"), "depth_keys_sorted": (np.uint32, (), "n"),
+    "keys": (np.uint32, (), "M"), "vals": (np.uint32, (), "M"), "keys_sorted": (np.uint32, (), "M"),
+    "vals_sorted": (np.uint32, (), "M"), "tile_ranges": (np.uint32, (2,), "T"), "out_rgba": (np.float32, (4,), "P"),
+    "out_feat": (np.float32, (4,), "P"), "last_idx": (np.uint32, (), "P"), "v_out": (np.float32, (4,), "P"),
+    "v_splat": (np.float32, (GRAD_LANES,), "n"), "vis_flag": (np.uint32, (), "n"), "loss_accum": (np.float32, (16,), "1"),
+}
+
+
+class Renderer:
+    """One model + one render context + one view, driven through the C ABI."""
+
+    def __init__(self, scene, W=None, H=None):
+        self.L = lib()
+        self.scene = scene
+        self.W = scene.W if W is None else W
+        self.H = scene.H if H is None else H
+        self.model = self.L.b2c_model_create()
+        self.ctx = self.L.b2c_ctx_create()
+        if not self.ctx:
+            raise RuntimeError(self.L.b2c_last_error().decode())
+        self.view = None
+        self.upload(scene)
+        check(self.L.b2c_ctx_setup(self.ctx, self.W, self.H, scene.n), "ctx_setup")
+        self.set_target(scene.gt, scene.weights)
+
+    def upload(self, scene, floor=None):
+        n = scene.n
+        arrs = [np.ascontiguousarray(a, np.float32) for a in (scene.pos_op[:, :3], scene.lscale[:, :3], scene.quat,
+                                                              scene.pos_op[:, 3], scene.sh.reshape(n, -1))]
+        fl = None if floor is None else np.ascontiguousarray(floor, np.float32)
+        check(self.L.b2c_model_upload(self.model, n, scene.degree, int(scene.sh_fp16), *[_ptr(a) for a in arrs], _ptr(fl)),
+              "model_upload")
+        self.n = n
+        self.degree = scene.degree
+
+    def set_target(self, gt, weights=None):
+        if self.view:
+            self.L.b2c_view_destroy(self.view)
+        g = np.ascontiguousarray(gt, np.uint32)
+        w = None if weights is None else np.ascontiguousarray(weights, np.uint8)
+        self.view = self.L.b2c_view_create(self.W, self.H, _ptr(g), _ptr(w))
+        if not self.view:
+            raise RuntimeError(self.L.b2c_last_error().decode())
+
+    def close(self):
+        if self.view:
+            self.L.b2c_view_destroy(self.view)
+        if self.ctx:
+            self.L.b2c_ctx_destroy(self.ctx)
+        if self.model:
+            self.L.b2c_model_destroy(self.model)
+        self.view = self.ctx = self.model = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- options
+    def render_opts(self, cam=None, bg=None, sh_degree=None, bwd_info=True) -> RenderOpts:
+        o = RenderOpts()
+        o.cam = camera_struct(self.scene.cam if cam is None else cam)
+        o.W, o.H = self.W, self.H
+        b = self.scene.bg if bg is None else bg
+        for k in range(3):
+            o.bg[k] = float(b[k])
+        o.sh_degree = self.degree if sh_degree is None else sh_degree
+        o.bwd_info = int(bwd_info)
+        return o
+
+    def loss_opts(self, grad_scale=1.0, bg=None) -> LossOpts:
+        s = self.scene
+        lo = LossOpts()
+        lo.l1_w, lo.ssim_w = s.l1_w, s.ssim_w
+        b = s.bg if bg is None else bg
+        for k in range(3):
+            lo.bg[k] = float(b[k])
+        lo.composite, lo.mask, lo.alpha_lane = int(s.composite), int(s.mask), int(s.alpha_lane)
+        lo.match_alpha_weight, lo.scale, lo.grad_scale = s.match_alpha_weight, s.scale, grad_scale
+        return lo
+
+    # -- stages
+    def project(self, **kw):
+        check(self.L.b2c_project_splats(self.ctx, self.model, C.byref(self.render_opts(**kw))), "project_splats")
+
+    def bin(self):
+        check(self.L.b2c_bin_and_sort(self.ctx, self.model), "bin_and_sort")
+
+    def raster_fwd(self, **kw):
+        check(self.L.b2c_rasterize_forward(self.ctx, C.byref(self.render_opts(**kw))), "rasterize_forward")
+
+    def forward(self, **kw):
+        check(self.L.b2c_render_forward(self.ctx, self.model, C.byref(self.render_opts(**kw))), "render_forward")
+
+    def loss(self, grad_scale=1.0, bg=None, zero=True):
+        if zero:
+            self.zero("loss_accum")
+        check(self.L.b2c_photometric_loss(self.ctx, self.view, C.byref(self.loss_opts(grad_scale, bg))), "photometric_loss")
+        return float(self.read("loss_accum")[0])
+
+    def backward(self, mode=1, grad_scale=1.0, **kw):
+        check(self.L.b2c_rasterize_backward(self.ctx, self.model, C.byref(self.render_opts(**kw)), mode, grad_scale),
+              "rasterize_backward")
+
+    def vjp(self, accumulate=False, active_deg=None, **kw):
+        check(self.L.b2c_optimizer_grad(self.ctx, self.model, C.byref(self.render_opts(**kw)),
+                                        self.degree if active_deg is None else active_deg, int(accumulate)),
+              "optimizer_grad")
+
+    def step(self, mode=1, grad_scale=None, accumulate=False, timed=False, cam=None, bg=None):
+        gs = 3.0 * self.W * self.H if grad_scale is None else grad_scale
+        t = StepTimes() if timed else None
+        check(self.L.b2c_train_step(self.ctx, self.model, self.view, C.byref(self.render_opts(cam=cam, bg=bg)),
+                                    C.byref(self.loss_opts(gs, bg)), mode, int(accumulate),
+                                    C.byref(t) if timed else None), "train_step")
+        return t.as_dict() if timed else None
+
+    # -- buffers
+    def info(self) -> CtxInfo:
+        i = CtxInfo()
+        self.L.b2c_ctx_info_get(self.ctx, C.byref(i))
+        return i
+
+    def _count(self, key):
+        inf = self.info()
+        return {"n": self.n, "P": self.W * self.H, "M": inf.num_isect, "T": inf.n_tiles, "1": 1}[key]
+
+    def read(self, field):
+        if field == "grads":
+            per = 11 + 3 * (self.degree + 1) ** 2
+            out = np.empty((self.n, per), np.float32)
+        else:
+            dt, shape, key = _FIELD_SPEC[field]
+            out = np.empty((self._count(key),) + shape, dt)
+        check(self.L.b2c_ctx_read(self.ctx, field.encode(), _ptr(out), out.nbytes), f"read {field}")
+        return out[0] if field == "loss_accum" else out
+
+    def write(self, field, arr):
+        a = np.ascontiguousarray(arr)
+        check(self.L.b2c_ctx_write(self.ctx, field.encode(), _ptr(a), a.nbytes), f"write {field}")
+
+    def zero(self, field):
+        check(self.L.b2c_ctx_zero(self.ctx, field.encode()), f"zero {field}")
+
+    def read_model(self, field):
+        out = np.empty((self.n, 4) if field in ("pos_op", "quat", "lscale") else (self.n,), np.float32)
+        check(self.L.b2c_model_read(self.model, field.encode(), _ptr(out), out.nbytes), f"model_read {field}")
+        return out
+
+    def sync(self):
+        check(self.L.b2c_ctx_synchronize(self.ctx), "synchronize")

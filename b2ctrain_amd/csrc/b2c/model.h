@@ -1,0 +1,69 @@
+// Splat model and its host cloud (replaces src/model.h:8-40 and the SplatCloud of src/ply.h:10-42, path
+// fields only). Layout is the reference's, unchanged, because refine / cage / evidence code reads it:
+//   pos_op : float4 (mean x, y, z, opacity logit)
+//   quat   : float4 (w, x, y, z), unnormalised
+//   lscale : float4 (log sx, log sy, log sz, floor f), f frozen (0 = none)
+//   SH     : planar, lane k*3+ch of splat i; DC lanes in sh_dc[lane*cap + i] (fp32); lanes >= 3 in
+//            sh_hi[(lane-3)*cap + i] as IEEE fp16 when sh_fp16, else sh_hi32 (fp32).
+#pragma once
+#include <vector>
+
+#include "util.h"
+
+namespace b2c {
+
+constexpr float SH_C0 = 0.28209479177387814f;
+inline int sh_coeffs_for_degree(int d) { return (d + 1) * (d + 1); }
+
+// Host-side splat cloud in brush's parameterisation (src/ply.h:10-42, the fields the rasterizer uses).
+struct SplatCloud {
+  size_t n = 0;
+  int sh_degree = 0;
+  std::vector<float> pos;        // [n][3]
+  std::vector<float> log_scale;  // [n][3]
+  std::vector<float> quat;       // [n][4] (w, x, y, z)
+  std::vector<float> opacity;    // [n] logit
+  std::vector<float> sh;         // [n][K][3] coefficient-major
+  int K() const { return sh_coeffs_for_degree(sh_degree); }
+  void resize(size_t count, int degree);  // src/ply.cpp:15-22: zero, identity quaternions
+};
+
+// Planar SH view handed to the kernels (ShBuf, util.cuh:129-164).
+struct ShBuf {
+  float* dc = nullptr;
+  uint16_t* hi = nullptr;  // fp16 bits
+  float* hi32 = nullptr;
+  size_t stride = 0;
+  b2c_sh_view view() const { return b2c_sh_view{dc, hi, hi32, stride}; }
+};
+
+struct Model {
+  int n = 0, cap = 0, degree = 3;
+  bool sh_fp16 = false;  // choose before upload(): fp16 storage for SH bands >= 1
+  DevBuf<float4> pos_op, quat, lscale;
+  DevBuf<float> sh_dc, sh_hi32;
+  DevBuf<uint16_t> sh_hi;
+  // statistics updated as side effects of the path (model.h:27-30)
+  DevBuf<float> refine_norm, max_screen, vis_count, vis_weight;
+
+  ShBuf sh() const {
+    ShBuf b;
+    b.dc = sh_dc.ptr; b.hi = sh_hi.ptr; b.hi32 = sh_hi32.ptr; b.stride = (size_t)cap;
+    return b;
+  }
+  int K() const { return sh_coeffs_for_degree(degree); }
+  // Ensure capacity for `want` splats (doubling from 1024), preserving contents (model.cu:8-42).
+  void reserve(int want, hipStream_t stream = nullptr);
+  // Upload a cloud (model.cu:44-80): lscale.w = 0, fp16 bands rounded to nearest even, stats zeroed.
+  void upload(const SplatCloud& c, hipStream_t stream = nullptr);
+  SplatCloud download(hipStream_t stream = nullptr) const;
+  // Set the frozen per-splat floor f (lscale.w); not part of the reference's upload.
+  void set_floor(const std::vector<float>& f, hipStream_t stream = nullptr);
+  void zero_stats(hipStream_t stream = nullptr);
+};
+
+// IEEE binary16 encode (round to nearest even) / decode on the host.
+uint16_t float_to_half_rne(float f);
+float half_to_float(uint16_t h);
+
+}  // namespace b2c

@@ -1,0 +1,216 @@
+// Rendering entry points (replaces src/gpu/render.cu:5-27, project.cu:104-126, binning.cu:109-145,
+// raster_fwd.cu:75-90, raster_bwd.cu:239-248, raster_bwd_tc.cu:210-225).
+#include "render.h"
+
+#include <algorithm>
+#include <cmath>
+
+namespace b2c {
+
+void Camera::set_w2c_quat(float qw, float qx, float qy, float qz, float tx, float ty, float tz) {
+  float n = std::sqrt(qw * qw + qx * qx + qy * qy + qz * qz);
+  qw /= n; qx /= n; qy /= n; qz /= n;
+  R[0] = 1 - 2 * (qy * qy + qz * qz); R[1] = 2 * (qx * qy - qz * qw);     R[2] = 2 * (qx * qz + qy * qw);
+  R[3] = 2 * (qx * qy + qz * qw);     R[4] = 1 - 2 * (qx * qx + qz * qz); R[5] = 2 * (qy * qz - qx * qw);
+  R[6] = 2 * (qx * qz - qy * qw);     R[7] = 2 * (qy * qz + qx * qw);     R[8] = 1 - 2 * (qx * qx + qy * qy);
+  t[0] = tx; t[1] = ty; t[2] = tz;
+  update_pos();
+}
+
+void Camera::update_pos() {
+  pos[0] = -(R[0] * t[0] + R[3] * t[1] + R[6] * t[2]);
+  pos[1] = -(R[1] * t[0] + R[4] * t[1] + R[7] * t[2]);
+  pos[2] = -(R[2] * t[0] + R[5] * t[1] + R[8] * t[2]);
+}
+
+CameraGPU CameraGPU::from(const Camera& c, int W, int H) {
+  CameraGPU g;
+  for (int i = 0; i < 9; i++) g.R[i] = c.R[i];
+  for (int i = 0; i < 3; i++) { g.t[i] = c.t[i]; g.pos[i] = c.pos[i]; }
+  const float sx = (float)W / c.width, sy = (float)H / c.height;
+  g.fx = c.fx * sx; g.fy = c.fy * sy; g.cx = c.cx * sx; g.cy = c.cy * sy; g.W = W; g.H = H;
+  g.lim_pos_x = (1.15f * W - g.cx) / g.fx; g.lim_pos_y = (1.15f * H - g.cy) / g.fy;
+  g.lim_neg_x = (-0.15f * W - g.cx) / g.fx; g.lim_neg_y = (-0.15f * H - g.cy) / g.fy;
+  return g;
+}
+
+b2c_camera_gpu CameraGPU::dev() const {
+  b2c_camera_gpu d;
+  for (int i = 0; i < 9; i++) d.R[i] = R[i];
+  for (int i = 0; i < 3; i++) { d.t[i] = t[i]; d.pos[i] = pos[i]; }
+  d.fx = fx; d.fy = fy; d.cx = cx; d.cy = cy; d.W = W; d.H = H;
+  d.lim_pos_x = lim_pos_x; d.lim_pos_y = lim_pos_y; d.lim_neg_x = lim_neg_x; d.lim_neg_y = lim_neg_y;
+  return d;
+}
+
+void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
+  W = w; H = h;
+  tiles_x = (W + RT_W - 1) / RT_W; tiles_y = (H + RT_W - 1) / RT_W; n_tiles = tiles_x * tiles_y;
+  tile_bits = 1;
+  while ((1 << tile_bits) < n_tiles + 1) tile_bits++;
+  depth_bits = 32 - tile_bits;
+  if (depth_bits > 20) depth_bits = 20;
+  const size_t nn = (size_t)(n > 0 ? n : 1);
+  proj0.reserve(nn); proj1.reserve(nn); proj2.reserve(nn); proj3.reserve(nn);
+  tile_count.reserve(nn); tile_off.reserve(nn); hit_info.reserve(nn);
+  depth_keys.reserve(nn); depth_keys_sorted.reserve(nn); order_in.reserve(nn); order.reserve(nn);
+  depth_alt_k.reserve(nn); depth_alt_v.reserve(nn);
+  big_list.reserve(nn); big_base.reserve(nn);
+  counters.reserve(4);
+  if (v_splat.count < nn * GRAD_LANES) { v_splat.reserve(nn * GRAD_LANES); v_splat.zero(stream); }
+  if (vis_flag.count < nn) { vis_flag.reserve(nn); vis_flag.zero(stream); }
+  tile_ranges.reserve((size_t)n_tiles);
+  const size_t npx = (size_t)W * H;
+  out_rgba.reserve(npx); out_feat.reserve(npx); last_idx.reserve(npx); v_out.reserve(npx);
+  loss_accum.reserve(16);
+  h_count.reserve(4);
+  if (isect_cap == 0) ensure_isect_capacity((size_t)1 << 22, stream);
+  const size_t need_tmp = std::max({b2c_radix_sort_temp_bytes((uint32_t)nn), b2c_radix_sort_temp_bytes((uint32_t)isect_cap),
+                                    b2c_scan_temp_bytes((uint32_t)nn)});
+  sort_tmp.reserve(need_tmp);
+}
+
+void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
+  if (m <= isect_cap && isect_cap) return;
+  size_t ncap = isect_cap ? isect_cap : ((size_t)1 << 22);
+  while (ncap < m) ncap *= 2;
+  keys.reserve(ncap, false, stream); vals.reserve(ncap, false, stream);
+  keys_sorted.reserve(ncap, false, stream); vals_sorted.reserve(ncap, false, stream);
+  isect_alt_k.reserve(ncap, false, stream); isect_alt_v.reserve(ncap, false, stream);
+  isect_cap = ncap;
+  sort_tmp.reserve(b2c_radix_sort_temp_bytes((uint32_t)ncap));
+}
+
+namespace {
+
+void check_supported(const RenderParams& p) {
+  if (p.feat != FeatureMode::None) throw std::runtime_error("render: feature lanes (normals/buffer) are not supported by this build");
+  if (p.mip) throw std::runtime_error("render: mip filtering is not supported (the reference trainer rejects it too)");
+  if (p.warp || p.pos_override || p.quat_override || p.lscale_override || p.sh_frame || p.app || p.col_base)
+    throw std::runtime_error("render: warp / deformation overrides / appearance are not supported by this build");
+  if (p.hollow_z) throw std::runtime_error("render: the hollow loss is not supported by this build");
+}
+
+}  // namespace
+
+void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipStream_t stream) {
+  if (m.n == 0) return;
+  check_supported(p);
+  if (m.degree < 0 || m.degree > 4) throw std::runtime_error("unsupported SH degree");
+  b2c_project_args a{};
+  a.n = m.n; a.degree = m.degree; a.active_deg = p.sh_degree;
+  a.pos_op = reinterpret_cast<const float*>(m.pos_op.ptr);
+  a.quat = reinterpret_cast<const float*>(m.quat.ptr);
+  a.lscale = reinterpret_cast<const float*>(m.lscale.ptr);
+  a.sh = m.sh().view();
+  a.cam = p.cam.dev();
+  a.tiles_x = ctx.tiles_x; a.tiles_y = ctx.tiles_y;
+  a.proj0 = reinterpret_cast<float*>(ctx.proj0.ptr); a.proj1 = reinterpret_cast<float*>(ctx.proj1.ptr);
+  a.proj2 = reinterpret_cast<float*>(ctx.proj2.ptr); a.proj3 = reinterpret_cast<float*>(ctx.proj3.ptr);
+  a.tile_count = ctx.tile_count.ptr;
+  a.hit_info = reinterpret_cast<uint32_t*>(ctx.hit_info.ptr);
+  a.max_screen = m.max_screen.ptr;
+  a.big_list = ctx.big_list.ptr;
+  a.big_count = ctx.counters.ptr;
+  LAUNCH_CHECK(b2c_hip_project(&a, stream));
+}
+
+void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
+  if (m.n == 0) {
+    ctx.num_isect = 0;
+    ctx.tile_ranges.zero(stream);
+    return;
+  }
+  const int n = m.n;
+  // 1. depth sort of the splats (culled ones sort last), stable on the 32 z bits
+  LAUNCH_CHECK(b2c_hip_depth_keys(n, ctx.tile_count, reinterpret_cast<const float*>(ctx.proj1.ptr), ctx.depth_keys,
+                                  ctx.order_in, stream));
+  LAUNCH_CHECK(b2c_hip_radix_sort_pairs(ctx.depth_keys, ctx.order_in, ctx.depth_keys_sorted, ctx.order, ctx.depth_alt_k,
+                                        ctx.depth_alt_v, (uint32_t)n, nullptr, 0, 32, ctx.sort_tmp.ptr,
+                                        ctx.sort_tmp.bytes(), stream));
+  // 2. inclusive scan of the tile counts in depth order; the total comes back to the host (binning.cu:125-133)
+  LAUNCH_CHECK(b2c_hip_scan_counts(n, ctx.order, ctx.tile_count, ctx.tile_off, ctx.counters.ptr + 1, ctx.sort_tmp.ptr,
+                                   ctx.sort_tmp.bytes(), stream));
+  HIP_CHECK(hipMemcpyAsync(ctx.h_count.ptr, ctx.counters.ptr + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+  HIP_CHECK(hipStreamSynchronize(stream));
+  const uint32_t total = ctx.h_count.ptr[0];
+  ctx.num_isect = total;
+  ctx.ensure_isect_capacity(total, stream);
+  if (total == 0) {
+    ctx.tile_ranges.zero(stream);
+    return;
+  }
+  // 3. emit in depth order, then a stable sort on the tile id alone keeps each tile's list in depth order
+  b2c_emit_args e{};
+  e.n = n; e.order = ctx.order; e.tile_count = ctx.tile_count; e.tile_off = ctx.tile_off;
+  e.hit_info = reinterpret_cast<const uint32_t*>(ctx.hit_info.ptr);
+  e.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr); e.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
+  e.tiles_x = ctx.tiles_x; e.tiles_y = ctx.tiles_y; e.cap = (uint32_t)ctx.isect_cap;
+  e.keys = ctx.keys; e.vals = ctx.vals;
+  e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
+  LAUNCH_CHECK(b2c_hip_emit(&e, stream));
+  LAUNCH_CHECK(b2c_hip_radix_sort_pairs(ctx.keys, ctx.vals, ctx.keys_sorted, ctx.vals_sorted, ctx.isect_alt_k,
+                                        ctx.isect_alt_v, total, nullptr, 0, ctx.tile_bits, ctx.sort_tmp.ptr,
+                                        ctx.sort_tmp.bytes(), stream));
+  LAUNCH_CHECK(b2c_hip_tile_ranges(total, nullptr, ctx.keys_sorted, (uint32_t)ctx.n_tiles,
+                                   reinterpret_cast<uint32_t*>(ctx.tile_ranges.ptr), stream));
+}
+
+void rasterize_forward(RenderCtx& ctx, const RenderParams& p, hipStream_t stream) {
+  check_supported(p);
+  b2c_raster_fwd_args a{};
+  a.tile_ranges = reinterpret_cast<uint32_t*>(ctx.tile_ranges.ptr);
+  a.vals_sorted = ctx.vals_sorted;
+  a.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr);
+  a.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
+  a.proj2 = reinterpret_cast<const float*>(ctx.proj2.ptr);
+  a.W = ctx.W; a.H = ctx.H; a.tiles_x = ctx.tiles_x; a.tiles_y = ctx.tiles_y;
+  for (int k = 0; k < 3; k++) a.bg[k] = p.bg[k];
+  a.bwd_info = p.bwd_info ? 1 : 0;
+  a.out_rgba = reinterpret_cast<float*>(ctx.out_rgba.ptr);
+  a.out_feat = reinterpret_cast<float*>(ctx.out_feat.ptr);
+  a.last_idx = ctx.last_idx;
+  LAUNCH_CHECK(b2c_hip_raster_fwd(&a, stream));
+}
+
+void render_forward(RenderCtx& ctx, const Model& m, const RenderParams& p, hipStream_t stream) {
+  project_splats(ctx, m, p, stream);
+  bin_and_sort(ctx, m, stream);
+  rasterize_forward(ctx, p, stream);
+}
+
+namespace {
+
+void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, float inv_gscale, hipStream_t stream) {
+  check_supported(p);
+  b2c_raster_bwd_args a{};
+  a.tile_ranges = reinterpret_cast<const uint32_t*>(ctx.tile_ranges.ptr);
+  a.vals_sorted = ctx.vals_sorted;
+  a.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr);
+  a.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
+  a.proj2 = reinterpret_cast<const float*>(ctx.proj2.ptr);
+  a.out_rgba = reinterpret_cast<const float*>(ctx.out_rgba.ptr);
+  a.out_feat = reinterpret_cast<const float*>(ctx.out_feat.ptr);
+  a.last_idx = ctx.last_idx;
+  a.v_out = reinterpret_cast<const float*>(ctx.v_out.ptr);
+  a.W = ctx.W; a.H = ctx.H; a.tiles_x = ctx.tiles_x; a.tiles_y = ctx.tiles_y;
+  for (int k = 0; k < 3; k++) a.bg[k] = p.bg[k];
+  a.inv_gscale = inv_gscale;
+  a.mode = mode;
+  a.v_splat = ctx.v_splat;
+  a.vis_flag = ctx.vis_flag;
+  a.vis_weight = m.vis_weight.ptr;
+  LAUNCH_CHECK(b2c_hip_raster_bwd(&a, stream));
+}
+
+}  // namespace
+
+void rasterize_backward(RenderCtx& ctx, const Model& m, const RenderParams& p, hipStream_t stream) {
+  backward(ctx, m, p, 0, 1.f, stream);
+}
+
+void rasterize_backward_tc(RenderCtx& ctx, const Model& m, const RenderParams& p, float grad_scale, hipStream_t stream) {
+  backward(ctx, m, p, 1, 1.f / grad_scale, stream);
+}
+
+}  // namespace b2c

@@ -1,0 +1,106 @@
+// Rendering API of the drop-in (replaces src/gpu/render.h:1-111 and src/dataset/camera.h:8-36): same
+// type names, fields and entry points, hipStream_t in place of cudaStream_t. Features outside this build's
+// scope (feature lanes, hollow loss, render-side warp, articulated/cage overrides, pose-dependent
+// appearance, mip filtering) keep their RenderParams fields so callers compile, and make the entry points
+// throw std::runtime_error when set.
+#pragma once
+#include "model.h"
+
+namespace b2c {
+
+// Pinhole camera, world->camera R/t (OpenCV axes), R row major (camera.h:8-36).
+struct Camera {
+  int width = 0, height = 0;
+  float fx = 0, fy = 0, cx = 0, cy = 0;
+  float R[9] = {1, 0, 0, 0, 1, 0, 0, 0, 1};
+  float t[3] = {0, 0, 0};
+  float pos[3] = {0, 0, 0};
+  void set_w2c_quat(float qw, float qx, float qy, float qz, float tx, float ty, float tz);
+  void update_pos();  // pos = -R^T t
+};
+
+struct CameraGPU {
+  float R[9];
+  float t[3];
+  float pos[3];
+  float fx, fy, cx, cy;
+  int W, H;
+  float lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y;  // EWA Jacobian clamp
+  static CameraGPU from(const Camera& c, int W, int H);
+  b2c_camera_gpu dev() const;
+};
+
+enum class FeatureMode { None, Normals, Buffer };
+
+struct RenderParams {
+  CameraGPU cam;
+  float bg[3] = {0, 0, 0};
+  int sh_degree = 3;  // active degree (<= model degree)
+  FeatureMode feat = FeatureMode::None;
+  const float* feat_buffer = nullptr;
+  bool mip = false;
+  bool bwd_info = true;  // write per-pixel last index / shrink tile ranges
+  const float2* warp = nullptr;
+  int warp_w = 0, warp_h = 0;
+  const float4* pos_override = nullptr;
+  const float4* quat_override = nullptr;
+  const float4* lscale_override = nullptr;
+  const float4* sh_frame = nullptr;
+  const float4* app = nullptr;
+  float4* col_base = nullptr;
+  bool app_add = false;
+  const float* hollow_z = nullptr;
+  float hollow_margin = 0.05f;
+  float hollow_lam = 0.f;
+};
+
+// Persistent scratch for rendering one view; grows on demand (render.h:66-95).
+struct RenderCtx {
+  int W = 0, H = 0, tiles_x = 0, tiles_y = 0, n_tiles = 0, tile_bits = 0, depth_bits = 0;
+  // per splat (global index)
+  DevBuf<float4> proj0, proj1, proj2;  // (xy, c00, c01) | (c11, opac, depth, power = ln(255 opac)) | (r, g, b, feat_x)
+  DevBuf<float2> proj3;                // (feat_y, feat_z)
+  DevBuf<uint32_t> tile_count, tile_off;  // hit count; inclusive scan in depth order
+  DevBuf<uint2> hit_info;                 // (hit mask within the bbox or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24)
+  DevBuf<uint32_t> depth_keys, depth_keys_sorted, order_in, order;  // depth sort
+  DevBuf<uint32_t> count_perm;  // kept for layout compatibility; the count scan gathers in place
+  // intersections
+  DevBuf<uint32_t> keys, vals, keys_sorted, vals_sorted;
+  size_t isect_cap = 0;
+  uint32_t num_isect = 0;
+  PinnedBuf<uint32_t> h_count;
+  // per tile / per pixel
+  DevBuf<uint2> tile_ranges;
+  DevBuf<float4> out_rgba;  // final rgb (with bg) + alpha
+  DevBuf<float4> out_feat;  // feat xyz + final transmittance
+  DevBuf<float> hollow_pen;
+  DevBuf<uint32_t> last_idx;  // one past the last contributing intersection per pixel
+  // backward
+  DevBuf<float> v_splat;      // [n][13]: xy(2) conic(3) rgb(3) opac(1) refine(1) feat(3)
+  DevBuf<uint32_t> vis_flag;  // [n]
+  DevBuf<float4> v_out;       // dL/d(rgba) per pixel
+  DevBuf<float4> v_feat;
+  DevBuf<float> loss_accum;   // [16] scalar accumulators
+  // MI355X build scratch: big-splat list, sort ping-pong buffers, sort/scan temporaries, device counters
+  DevBuf<uint32_t> big_list, big_base, counters;  // counters[0] big splats, [1] intersection total
+  DevBuf<uint32_t> depth_alt_k, depth_alt_v, isect_alt_k, isect_alt_v;
+  DevBuf<unsigned char> sort_tmp;
+
+  void setup(int W, int H, int n_splats, hipStream_t stream);
+  void ensure_isect_capacity(size_t m, hipStream_t stream);
+};
+
+// Full forward: projection, binning, sort, rasterisation. Leaves outputs in ctx.
+void render_forward(RenderCtx& ctx, const Model& m, const RenderParams& p, hipStream_t stream);
+
+// Individual stages.
+void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipStream_t stream);
+void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream);
+void rasterize_forward(RenderCtx& ctx, const RenderParams& p, hipStream_t stream);
+
+// Backward through rasterisation: consumes ctx.v_out, produces ctx.v_splat; accumulates Model::vis_weight.
+void rasterize_backward(RenderCtx& ctx, const Model& m, const RenderParams& p, hipStream_t stream);
+// MFMA variant. ctx.v_out must carry `grad_scale`; the accumulated per-splat gradients are divided by it.
+void rasterize_backward_tc(RenderCtx& ctx, const Model& m, const RenderParams& p, float grad_scale, hipStream_t stream);
+
+}  // namespace b2c

@@ -1,0 +1,359 @@
+// C ABI over the C++ drop-in API (declared in include/b2c.h).
+#include "b2c.h"
+
+#include <cstring>
+#include <map>
+#include <string>
+
+#include "b2c/loss.h"
+#include "b2c/optim.h"
+#include "b2c/render.h"
+
+struct b2c_model {
+  b2c::Model m;
+};
+
+struct b2c_ctx {
+  b2c::RenderCtx ctx;
+  hipStream_t stream = nullptr;
+  b2c::DevBuf<float> grads;
+  int n = 0;
+  int degree = 0;
+  hipEvent_t ev[8] = {};
+};
+
+struct b2c_view {
+  b2c::DevBuf<uint32_t> rgba;
+  b2c::DevBuf<uint8_t> weights;
+  b2c::ViewGPU view;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  } catch (...) {
+    g_err = "unknown error";
+    return -1;
+  }
+}
+
+b2c::Camera to_camera(const b2c_camera& c) {
+  b2c::Camera cam;
+  cam.width = c.width; cam.height = c.height;
+  cam.fx = c.fx; cam.fy = c.fy; cam.cx = c.cx; cam.cy = c.cy;
+  for (int i = 0; i < 9; i++) cam.R[i] = c.R[i];
+  for (int i = 0; i < 3; i++) cam.t[i] = c.t[i];
+  cam.update_pos();
+  return cam;
+}
+
+b2c::RenderParams to_params(const b2c_render_opts& o) {
+  b2c::RenderParams p;
+  p.cam = b2c::CameraGPU::from(to_camera(o.cam), o.W, o.H);
+  for (int k = 0; k < 3; k++) p.bg[k] = o.bg[k];
+  p.sh_degree = o.sh_degree;
+  p.bwd_info = o.bwd_info != 0;
+  return p;
+}
+
+b2c::LossParams to_loss(const b2c_loss_opts& o) {
+  b2c::LossParams lp;
+  lp.l1_w = o.l1_w; lp.ssim_w = o.ssim_w;
+  for (int k = 0; k < 3; k++) lp.bg[k] = o.bg[k];
+  lp.composite = o.composite != 0; lp.mask = o.mask != 0; lp.alpha_lane = o.alpha_lane != 0;
+  lp.match_alpha_weight = o.match_alpha_weight; lp.scale = o.scale; lp.grad_scale = o.grad_scale;
+  return lp;
+}
+
+struct Field {
+  void* ptr;
+  size_t bytes;
+};
+
+Field ctx_field(b2c_ctx* c, const std::string& name) {
+  b2c::RenderCtx& x = c->ctx;
+  const size_t n = (size_t)c->n;
+  const size_t P = (size_t)x.W * x.H;
+  const size_t M = x.num_isect;
+  std::map<std::string, Field> f = {
+      {"proj0", {x.proj0.ptr, n * 16}},
+      {"proj1", {x.proj1.ptr, n * 16}},
+      {"proj2", {x.proj2.ptr, n * 16}},
+      {"proj3", {x.proj3.ptr, n * 8}},
+      {"tile_count", {x.tile_count.ptr, n * 4}},
+      {"tile_off", {x.tile_off.ptr, n * 4}},
+      {"hit_info", {x.hit_info.ptr, n * 8}},
+      {"order", {x.order.ptr, n * 4}},
+      {"depth_keys_sorted", {x.depth_keys_sorted.ptr, n * 4}},
+      {"keys", {x.keys.ptr, M * 4}},
+      {"vals", {x.vals.ptr, M * 4}},
+      {"keys_sorted", {x.keys_sorted.ptr, M * 4}},
+      {"vals_sorted", {x.vals_sorted.ptr, M * 4}},
+      {"tile_ranges", {x.tile_ranges.ptr, (size_t)x.n_tiles * 8}},
+      {"out_rgba", {x.out_rgba.ptr, P * 16}},
+      {"out_feat", {x.out_feat.ptr, P * 16}},
+      {"last_idx", {x.last_idx.ptr, P * 4}},
+      {"v_out", {x.v_out.ptr, P * 16}},
+      {"v_splat", {x.v_splat.ptr, n * b2c::GRAD_LANES * 4}},
+      {"vis_flag", {x.vis_flag.ptr, n * 4}},
+      {"loss_accum", {x.loss_accum.ptr, 16 * 4}},
+      {"grads", {c->grads.ptr, c->grads.bytes()}},
+  };
+  auto it = f.find(name);
+  if (it == f.end()) throw std::runtime_error("unknown context field: " + name);
+  return it->second;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* b2c_last_error(void) { return g_err.c_str(); }
+
+int b2c_get_device_count(int* count) {
+  return guarded([&] { HIP_CHECK(hipGetDeviceCount(count)); });
+}
+
+int b2c_camera_gpu_from(const b2c_camera* cam, int W, int H, b2c_camera_gpu* out) {
+  return guarded([&] { *out = b2c::CameraGPU::from(to_camera(*cam), W, H).dev(); });
+}
+
+b2c_model* b2c_model_create(void) { return new b2c_model(); }
+void b2c_model_destroy(b2c_model* m) { delete m; }
+
+int b2c_model_upload(b2c_model* m, int n, int degree, int sh_fp16, const float* pos, const float* log_scale,
+                     const float* quat, const float* opacity, const float* sh, const float* floor_) {
+  return guarded([&] {
+    if (n < 0 || degree < 0 || degree > 4) throw std::runtime_error("model_upload: bad n or degree");
+    b2c::SplatCloud c;
+    c.resize((size_t)n, degree);
+    std::memcpy(c.pos.data(), pos, sizeof(float) * 3 * n);
+    std::memcpy(c.log_scale.data(), log_scale, sizeof(float) * 3 * n);
+    std::memcpy(c.quat.data(), quat, sizeof(float) * 4 * n);
+    std::memcpy(c.opacity.data(), opacity, sizeof(float) * n);
+    std::memcpy(c.sh.data(), sh, sizeof(float) * 3 * (size_t)c.K() * n);
+    m->m.sh_fp16 = sh_fp16 != 0;
+    m->m.upload(c);
+    if (floor_) m->m.set_floor(std::vector<float>(floor_, floor_ + n));
+  });
+}
+
+int b2c_model_read(const b2c_model* m, const char* field, void* host, size_t bytes) {
+  return guarded([&] {
+    const b2c::Model& x = m->m;
+    const size_t n = (size_t)x.n;
+    std::map<std::string, Field> f = {
+        {"pos_op", {x.pos_op.ptr, n * 16}},         {"quat", {x.quat.ptr, n * 16}},
+        {"lscale", {x.lscale.ptr, n * 16}},         {"vis_weight", {x.vis_weight.ptr, n * 4}},
+        {"vis_count", {x.vis_count.ptr, n * 4}},    {"refine_norm", {x.refine_norm.ptr, n * 4}},
+        {"max_screen", {x.max_screen.ptr, n * 4}},
+    };
+    auto it = f.find(field);
+    if (it == f.end()) throw std::runtime_error(std::string("unknown model field: ") + field);
+    if (bytes > it->second.bytes) throw std::runtime_error(std::string("model_read: too many bytes for ") + field);
+    HIP_CHECK(hipDeviceSynchronize());
+    HIP_CHECK(hipMemcpy(host, it->second.ptr, bytes, hipMemcpyDeviceToHost));
+  });
+}
+
+b2c_ctx* b2c_ctx_create(void) {
+  b2c_ctx* c = new b2c_ctx();
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    g_err = "hipStreamCreateWithFlags failed";
+    delete c;
+    return nullptr;
+  }
+  for (auto& e : c->ev) (void)hipEventCreate(&e);
+  return c;
+}
+
+void b2c_ctx_destroy(b2c_ctx* c) {
+  if (!c) return;
+  (void)hipStreamSynchronize(c->stream);
+  for (auto& e : c->ev) (void)hipEventDestroy(e);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+int b2c_ctx_setup(b2c_ctx* c, int W, int H, int n) {
+  return guarded([&] {
+    c->ctx.setup(W, H, n, c->stream);
+    c->n = n;
+    HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+int b2c_ctx_info_get(const b2c_ctx* c, b2c_ctx_info* o) {
+  const b2c::RenderCtx& x = c->ctx;
+  o->W = x.W; o->H = x.H; o->tiles_x = x.tiles_x; o->tiles_y = x.tiles_y; o->n_tiles = x.n_tiles;
+  o->tile_bits = x.tile_bits; o->num_isect = x.num_isect; o->isect_cap = x.isect_cap;
+  return 0;
+}
+
+int b2c_ctx_read(b2c_ctx* c, const char* field, void* host, size_t bytes) {
+  return guarded([&] {
+    Field f = ctx_field(c, field);
+    if (bytes > f.bytes) throw std::runtime_error(std::string("ctx_read: too many bytes for ") + field);
+    HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (bytes) HIP_CHECK(hipMemcpy(host, f.ptr, bytes, hipMemcpyDeviceToHost));
+  });
+}
+
+int b2c_ctx_write(b2c_ctx* c, const char* field, const void* host, size_t bytes) {
+  return guarded([&] {
+    Field f = ctx_field(c, field);
+    if (bytes > f.bytes) throw std::runtime_error(std::string("ctx_write: too many bytes for ") + field);
+    HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (bytes) HIP_CHECK(hipMemcpy(f.ptr, host, bytes, hipMemcpyHostToDevice));
+  });
+}
+
+int b2c_ctx_zero(b2c_ctx* c, const char* field) {
+  return guarded([&] {
+    Field f = ctx_field(c, field);
+    if (f.bytes % 4) throw std::runtime_error("ctx_zero: field size not a multiple of 4");
+    if (f.bytes) LAUNCH_CHECK(b2c_hip_fill_u32(static_cast<uint32_t*>(f.ptr), 0u, f.bytes / 4, c->stream));
+  });
+}
+
+int b2c_ctx_synchronize(b2c_ctx* c) {
+  return guarded([&] { HIP_CHECK(hipStreamSynchronize(c->stream)); });
+}
+
+void* b2c_ctx_stream(b2c_ctx* c) { return c->stream; }
+
+b2c_view* b2c_view_create(int W, int H, const uint32_t* rgba, const uint8_t* weights) {
+  b2c_view* v = new b2c_view();
+  int rc = guarded([&] {
+    const size_t P = (size_t)W * H;
+    v->rgba.upload(rgba, P);
+    if (weights) v->weights.upload(weights, P);
+    HIP_CHECK(hipDeviceSynchronize());
+    v->view.rgba = v->rgba.ptr;
+    v->view.weights = weights ? v->weights.ptr : nullptr;
+    v->view.W = W;
+    v->view.H = H;
+  });
+  if (rc) {
+    delete v;
+    return nullptr;
+  }
+  return v;
+}
+
+void b2c_view_destroy(b2c_view* v) { delete v; }
+
+int b2c_render_forward(b2c_ctx* c, const b2c_model* m, const b2c_render_opts* o) {
+  return guarded([&] { b2c::render_forward(c->ctx, m->m, to_params(*o), c->stream); });
+}
+
+int b2c_project_splats(b2c_ctx* c, const b2c_model* m, const b2c_render_opts* o) {
+  return guarded([&] { b2c::project_splats(c->ctx, m->m, to_params(*o), c->stream); });
+}
+
+int b2c_bin_and_sort(b2c_ctx* c, const b2c_model* m) {
+  return guarded([&] { b2c::bin_and_sort(c->ctx, m->m, c->stream); });
+}
+
+int b2c_rasterize_forward(b2c_ctx* c, const b2c_render_opts* o) {
+  return guarded([&] { b2c::rasterize_forward(c->ctx, to_params(*o), c->stream); });
+}
+
+int b2c_photometric_loss(b2c_ctx* c, const b2c_view* v, const b2c_loss_opts* o) {
+  return guarded([&] {
+    if (v->view.W != c->ctx.W || v->view.H != c->ctx.H) throw std::runtime_error("photometric_loss: view size != render size");
+    b2c::photometric_loss(c->ctx, v->view, to_loss(*o), c->stream);
+  });
+}
+
+int b2c_accumulate_loss(b2c_ctx* c) {
+  return guarded([&] { b2c::accumulate_loss(c->ctx, c->stream); });
+}
+
+int b2c_rasterize_backward(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int mode, float grad_scale) {
+  return guarded([&] {
+    if (mode == 0)
+      b2c::rasterize_backward(c->ctx, m->m, to_params(*o), c->stream);
+    else
+      b2c::rasterize_backward_tc(c->ctx, m->m, to_params(*o), grad_scale, c->stream);
+  });
+}
+
+int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int active_deg, int accumulate) {
+  return guarded([&] {
+    const size_t per = 11 + 3 * (size_t)m->m.K();
+    const size_t need = (size_t)m->m.n * per;
+    if (c->grads.count < need || c->degree != m->m.degree) {
+      c->grads.free();
+      c->grads.reserve(need);
+      c->grads.zero(c->stream);
+      c->degree = m->m.degree;
+    }
+    b2c::OptimParams op;
+    op.cam = to_params(*o).cam;
+    op.active_sh_degree = active_deg;
+    op.grad_out = c->grads.ptr;
+    op.grad_accumulate = accumulate != 0;
+    b2c::optimizer_step(c->ctx, m->m, op, c->stream);
+  });
+}
+
+int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
+                   int mode, int accumulate, b2c_step_times* times) {
+  return guarded([&] {
+    const b2c::RenderParams p = to_params(*ro);
+    const b2c::LossParams lp = to_loss(*lo);
+    hipStream_t s = c->stream;
+    auto mark = [&](int k) {
+      if (times) HIP_CHECK(hipEventRecord(c->ev[k], s));
+    };
+    const size_t per = 11 + 3 * (size_t)m->m.K();
+    if (c->grads.count < (size_t)m->m.n * per || c->degree != m->m.degree) {
+      c->grads.free();
+      c->grads.reserve((size_t)m->m.n * per);
+      c->grads.zero(s);
+      c->degree = m->m.degree;
+    }
+    mark(0);
+    c->ctx.loss_accum.zero(s, 2);
+    b2c::project_splats(c->ctx, m->m, p, s);
+    mark(1);
+    b2c::bin_and_sort(c->ctx, m->m, s);
+    mark(2);
+    b2c::rasterize_forward(c->ctx, p, s);
+    mark(3);
+    b2c::photometric_loss(c->ctx, v->view, lp, s);
+    mark(4);
+    if (mode == 0)
+      b2c::rasterize_backward(c->ctx, m->m, p, s);
+    else
+      b2c::rasterize_backward_tc(c->ctx, m->m, p, lp.grad_scale, s);
+    mark(5);
+    b2c::OptimParams op;
+    op.cam = p.cam;
+    op.active_sh_degree = p.sh_degree;
+    op.grad_out = c->grads.ptr;
+    op.grad_accumulate = accumulate != 0;
+    b2c::optimizer_step(c->ctx, m->m, op, s);
+    b2c::accumulate_loss(c->ctx, s);
+    mark(6);
+    if (times) {
+      HIP_CHECK(hipEventSynchronize(c->ev[6]));
+      float* out[6] = {&times->project_ms, &times->bin_ms, &times->forward_ms, &times->loss_ms, &times->backward_ms,
+                       &times->vjp_ms};
+      for (int k = 0; k < 6; k++) HIP_CHECK(hipEventElapsedTime(out[k], c->ev[k], c->ev[k + 1]));
+      HIP_CHECK(hipEventElapsedTime(&times->total_ms, c->ev[0], c->ev[6]));
+    }
+  });
+}
+
+}  // extern "C"

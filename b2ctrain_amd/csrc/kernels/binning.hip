@@ -1,0 +1,437 @@
+// Binning and sorting (replaces src/gpu/binning.cu:10-143 and its CUB calls).
+//
+// * Radix sort: stable LSD key/value sort, 8-bit digits, reduce-then-scan (no inter-workgroup spin
+//   waits): per 4096-key tile an LDS digit histogram built from wave64 ballot "match" masks, a per-digit
+//   exclusive scan over tiles, then a stable scatter whose in-tile ranks come from the same ballot masks
+//   (lanes below with the same digit) plus per-wave prefix counts in LDS.
+// * Count scan: reduce-then-scan of tile_count gathered in depth order.
+// * Emit: one wave64 sweeps the contiguous slot range of 64 depth-consecutive splats, 64 slots per step
+//   (owner lane by binary search over lane starts, tile by k-th set bit of the owner's hit mask). Splats
+//   whose bbox exceeds 32 tiles are emitted by one wave each over the bbox in row-major order.
+#pragma clang fp contract(off)
+#include "b2c_kernels.h"
+#include "device_math.h"
+
+namespace b2c {
+namespace dev {
+namespace {
+
+constexpr int SORT_THREADS = 256;
+constexpr int SORT_ROUNDS = 16;
+constexpr int SORT_TILE = SORT_THREADS * SORT_ROUNDS;  // keys per workgroup
+constexpr int RADIX = 256;
+constexpr int NWAVES = SORT_THREADS / 64;
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int l = lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+// Lanes of this wave whose `bits`-bit digit equals mine (among lanes with `active` set).
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, int bits, bool active) {
+  uint64_t m = ballot64(active);
+  for (int b = 0; b < bits; b++) {
+    const uint64_t bal = ballot64(((d >> b) & 1u) != 0u);
+    m &= ((d >> b) & 1u) ? bal : ~bal;
+  }
+  return m;
+}
+
+// Inclusive scan within a wave64 (Hillis-Steele over shuffles).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    uint32_t t = __shfl_up(v, o);
+    if (l >= o) v += t;
+  }
+  return v;
+}
+
+// Exclusive scan over a 256-thread block; returns the exclusive prefix, writes the block total.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* s_wsum, uint32_t& total) {
+  const int w = threadIdx.x >> 6, l = lane_id();
+  uint32_t inc = wave_incl_scan(v);
+  if (l == 63) s_wsum[w] = inc;
+  __syncthreads();
+  uint32_t wbase = 0, tot = 0;
+#pragma unroll
+  for (int k = 0; k < NWAVES; k++) {
+    uint32_t s = s_wsum[k];
+    if (k < w) wbase += s;
+    tot += s;
+  }
+  __syncthreads();
+  total = tot;
+  return wbase + inc - v;
+}
+
+__device__ __forceinline__ uint32_t live_count(uint32_t cap, const uint32_t* n_dev) {
+  if (!n_dev) return cap;
+  uint32_t n = *n_dev;
+  return n < cap ? n : cap;
+}
+
+__global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __restrict__ keys, uint32_t cap,
+                                                              const uint32_t* __restrict__ n_dev, int shift, int bits,
+                                                              uint32_t* __restrict__ block_hist, uint32_t nblocks) {
+  __shared__ uint32_t hist[RADIX];
+  const uint32_t n = live_count(cap, n_dev);
+  hist[threadIdx.x] = 0;
+  __syncthreads();
+  const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
+  const uint32_t dmask = (1u << bits) - 1u;
+  for (int r = 0; r < SORT_ROUNDS; r++) {
+    const uint32_t rb = base + (uint32_t)r * SORT_THREADS;
+    if (rb >= n) break;
+    const uint32_t idx = rb + threadIdx.x;
+    const bool valid = idx < n;
+    const uint32_t d = valid ? (keys[idx] >> shift) & dmask : 0u;
+    const uint64_t peers = match_digit(d, bits, valid);
+    if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&hist[d], popc64(peers));
+  }
+  __syncthreads();
+  block_hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = hist[threadIdx.x];
+}
+
+// One workgroup per digit: exclusive scan of the digit's per-tile counts, total into digit_total.
+__global__ void __launch_bounds__(SORT_THREADS) radix_scan_digits(uint32_t* __restrict__ block_hist, uint32_t nblocks,
+                                                                  uint32_t* __restrict__ digit_total) {
+  __shared__ uint32_t s_wsum[NWAVES];
+  uint32_t* row = block_hist + (size_t)blockIdx.x * nblocks;
+  uint32_t running = 0;
+  for (uint32_t c = 0; c < nblocks; c += SORT_THREADS) {
+    const uint32_t j = c + threadIdx.x;
+    const uint32_t v = j < nblocks ? row[j] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan(v, s_wsum, tot);
+    if (j < nblocks) row[j] = running + ex;
+    running += tot;
+  }
+  if (threadIdx.x == 0) digit_total[blockIdx.x] = running;
+}
+
+__global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, uint32_t cap, const uint32_t* __restrict__ n_dev, int shift, int bits,
+    const uint32_t* __restrict__ block_hist, uint32_t nblocks, const uint32_t* __restrict__ digit_total) {
+  __shared__ uint32_t s_base[RADIX];
+  __shared__ uint32_t s_wcnt[NWAVES][RADIX];
+  __shared__ uint32_t s_wsum[NWAVES];
+  const uint32_t n = live_count(cap, n_dev);
+  const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
+  if (base >= n) return;
+  const int w = threadIdx.x >> 6;
+  {
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan(digit_total[threadIdx.x], s_wsum, tot);
+    s_base[threadIdx.x] = ex + block_hist[(size_t)threadIdx.x * nblocks + blockIdx.x];
+  }
+  const uint32_t dmask = (1u << bits) - 1u;
+  for (int r = 0; r < SORT_ROUNDS; r++) {
+    const uint32_t rb = base + (uint32_t)r * SORT_THREADS;
+    if (rb >= n) break;
+    const uint32_t idx = rb + threadIdx.x;
+    const bool valid = idx < n;
+    const uint32_t key = valid ? keys_in[idx] : 0u;
+    const uint32_t val = valid ? vals_in[idx] : 0u;
+    const uint32_t d = (key >> shift) & dmask;
+#pragma unroll
+    for (int k = 0; k < NWAVES; k++) s_wcnt[k][threadIdx.x] = 0u;
+    __syncthreads();
+    const uint64_t peers = match_digit(d, bits, valid);
+    const uint32_t rank = popc64(peers & lanemask_lt());
+    if (valid && rank == 0) s_wcnt[w][d] = popc64(peers);
+    __syncthreads();
+    {  // thread t owns digit t: turn per-wave counts into offsets, advance the digit base
+      const uint32_t t = threadIdx.x;
+      uint32_t run = s_base[t];
+#pragma unroll
+      for (int k = 0; k < NWAVES; k++) {
+        const uint32_t c = s_wcnt[k][t];
+        s_wcnt[k][t] = run;
+        run += c;
+      }
+      s_base[t] = run;
+    }
+    __syncthreads();
+    if (valid) {
+      const uint32_t pos = s_wcnt[w][d] + rank;
+      keys_out[pos] = key;
+      vals_out[pos] = val;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void __launch_bounds__(256) depth_keys_kernel(int n, const uint32_t* __restrict__ tile_count,
+                                                         const float4* __restrict__ proj1, uint32_t* __restrict__ keys,
+                                                         uint32_t* __restrict__ vals) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  keys[i] = tile_count[i] ? __float_as_uint(proj1[i].z) : 0xFFFFFFFFu;
+  vals[i] = (uint32_t)i;
+}
+
+// ---- count scan in depth order ----
+__global__ void __launch_bounds__(SORT_THREADS) scan_reduce(int n, const uint32_t* __restrict__ order,
+                                                            const uint32_t* __restrict__ tile_count,
+                                                            uint32_t* __restrict__ block_sums) {
+  __shared__ uint32_t s_wsum[NWAVES];
+  const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
+  uint32_t acc = 0;
+  for (int r = 0; r < SORT_ROUNDS; r++) {
+    const uint32_t idx = base + (uint32_t)r * SORT_THREADS + threadIdx.x;
+    if (idx < (uint32_t)n) acc += tile_count[order[idx]];
+  }
+  uint32_t tot;
+  block_excl_scan(acc, s_wsum, tot);
+  if (threadIdx.x == 0) block_sums[blockIdx.x] = tot;
+}
+
+__global__ void __launch_bounds__(1024) scan_top(uint32_t nblocks, uint32_t* __restrict__ block_sums,
+                                                 uint32_t* __restrict__ total_dev) {
+  __shared__ uint32_t s_wsum[16];
+  const int w = threadIdx.x >> 6, l = lane_id();
+  uint32_t running = 0;
+  for (uint32_t c = 0; c < nblocks; c += 1024) {
+    const uint32_t j = c + threadIdx.x;
+    const uint32_t v = j < nblocks ? block_sums[j] : 0u;
+    const uint32_t inc = wave_incl_scan(v);
+    if (l == 63) s_wsum[w] = inc;
+    __syncthreads();
+    uint32_t wbase = 0, tot = 0;
+    for (int k = 0; k < 16; k++) {
+      const uint32_t s = s_wsum[k];
+      if (k < w) wbase += s;
+      tot += s;
+    }
+    __syncthreads();
+    if (j < nblocks) block_sums[j] = running + wbase + inc - v;
+    running += tot;
+  }
+  if (threadIdx.x == 0) *total_dev = running;
+}
+
+__global__ void __launch_bounds__(SORT_THREADS) scan_down(int n, const uint32_t* __restrict__ order,
+                                                          const uint32_t* __restrict__ tile_count,
+                                                          const uint32_t* __restrict__ block_sums,
+                                                          uint32_t* __restrict__ tile_off) {
+  __shared__ uint32_t s_wsum[NWAVES];
+  const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
+  uint32_t running = block_sums[blockIdx.x];
+  for (int r = 0; r < SORT_ROUNDS; r++) {
+    const uint32_t rb = base + (uint32_t)r * SORT_THREADS;
+    if (rb >= (uint32_t)n) break;
+    const uint32_t idx = rb + threadIdx.x;
+    const uint32_t v = idx < (uint32_t)n ? tile_count[order[idx]] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan(v, s_wsum, tot);
+    if (idx < (uint32_t)n) tile_off[idx] = running + ex + v;
+    running += tot;
+  }
+}
+
+// Position of the (k+1)-th set bit of m (m has more than k set bits).
+__device__ __forceinline__ int kth_set_bit(uint32_t m, uint32_t k) {
+  int pos = 0;
+#pragma unroll
+  for (int w = 16; w >= 1; w >>= 1) {
+    const uint32_t c = (uint32_t)__popc(m & ((1u << w) - 1u));
+    if (k >= c) { k -= c; m >>= w; pos += w; }
+  }
+  return pos;
+}
+
+__global__ void __launch_bounds__(256) emit_small_kernel(b2c_emit_args a, uint32_t* __restrict__ big_base) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  const int lane = lane_id();
+  const bool valid = r < a.n;
+  const uint32_t i = valid ? a.order[r] : 0u;
+  uint32_t cnt = valid ? a.tile_count[i] : 0u;
+  const uint32_t end = valid ? a.tile_off[r] : 0u;
+  const uint32_t base = end - cnt;
+  const uint2 hi = (valid && cnt) ? reinterpret_cast<const uint2*>(a.hit_info)[i] : make_uint2(0u, 0u);
+  const bool big = cnt && hi.x == 0xFFFFFFFFu;
+  if (big) {
+    big_base[i] = base;
+    cnt = 0;
+  }
+  const uint32_t my_start = valid ? base : 0xFFFFFFFFu;
+  uint32_t my_cnt = cnt;
+  if (base + cnt > a.cap) my_cnt = 0;
+  const uint64_t active = ballot64(my_cnt > 0);
+  if (!active) return;
+  const int first = __ffsll((unsigned long long)active) - 1;
+  const int last = 63 - __clzll((long long)active);
+  const uint32_t wstart = __shfl(my_start, first);
+  const uint32_t wend = __shfl(my_start + my_cnt, last);
+  const int min_x = (int)(hi.y & 0xFFFu), min_y = (int)((hi.y >> 12) & 0xFFFu), bw = (int)(hi.y >> 24);
+  for (uint32_t sb = wstart; sb < wend; sb += 64) {
+    const uint32_t s = sb + (uint32_t)lane;
+    int lo = 0, hi_l = 63;
+#pragma unroll
+    for (int step = 0; step < 6; step++) {
+      const int mid = (lo + hi_l + 1) >> 1;
+      const uint32_t st = __shfl(my_start, mid);
+      if (st <= s) lo = mid; else hi_l = mid - 1;
+    }
+    const int o = lo;
+    const uint32_t o_start = __shfl(my_start, o);
+    const uint32_t o_cnt = __shfl(my_cnt, o);
+    const uint32_t o_mask = __shfl(hi.x, o);
+    const int o_minx = __shfl(min_x, o), o_miny = __shfl(min_y, o), o_bw = __shfl(bw, o);
+    const uint32_t o_i = __shfl(i, o);
+    if (s < wend && o_cnt > 0 && s < o_start + o_cnt) {
+      const int bit = kth_set_bit(o_mask, s - o_start);
+      const int tx = o_minx + bit % o_bw, ty = o_miny + bit / o_bw;
+      a.keys[s] = (uint32_t)(ty * a.tiles_x + tx);
+      a.vals[s] = o_i;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) emit_big_kernel(b2c_emit_args a, const uint32_t* __restrict__ big_base) {
+  const int lane = lane_id();
+  const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
+  const uint32_t nwaves = (gridDim.x * 256u) >> 6;
+  const uint32_t count = *a.big_count;
+  const uint32_t sentinel = (uint32_t)(a.tiles_x * a.tiles_y);
+  for (uint32_t e = wave; e < count; e += nwaves) {
+    const uint32_t i = a.big_list[e];
+    const uint32_t cnt = a.tile_count[i];
+    if (cnt == 0) continue;
+    const uint32_t base = big_base[i];
+    if (base + cnt > a.cap) continue;
+    const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
+    const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
+    Sym2 conic{p0.z, p0.w, p1.x};
+    float ex, ey;
+    extent_from_conic(conic, p1.w, ex, ey);
+    TileBox bb = tile_bbox(p0.x, p0.y, ex, ey, a.tiles_x, a.tiles_y);
+    const int bw = bb.max_x - bb.min_x;
+    const int area = bw * (bb.max_y - bb.min_y);
+    uint32_t written = 0;
+    for (int b0 = 0; b0 < area && written < cnt; b0 += 64) {
+      const int b = b0 + lane;
+      bool h = false;
+      int tx = 0, ty = 0;
+      if (b < area) {
+        tx = bb.min_x + b % bw;
+        ty = bb.min_y + b / bw;
+        const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
+        h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, p0.x, p0.y, conic, p1.w);
+      }
+      const uint64_t m = ballot64(h);
+      if (h) {
+        const uint32_t slot = written + mbcnt64(m);
+        if (slot < cnt) {
+          a.keys[base + slot] = (uint32_t)(ty * a.tiles_x + tx);
+          a.vals[base + slot] = i;
+        }
+      }
+      written += popc64(m);
+    }
+    for (uint32_t s = written + lane; s < cnt; s += 64) {
+      a.keys[base + s] = sentinel;
+      a.vals[base + s] = i;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const uint32_t* __restrict__ m_dev,
+                                                          const uint32_t* __restrict__ keys, uint32_t n_tiles,
+                                                          uint2* __restrict__ ranges) {
+  const uint32_t m = live_count(cap, m_dev);
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (i >= m) return;
+  const uint32_t tile = keys[i];
+  const uint32_t prev = i == 0 ? 0xFFFFFFFFu : keys[i - 1];
+  if (i == 0 || tile != prev) {
+    if (tile < n_tiles) ranges[tile].x = i;
+    if (i > 0 && prev < n_tiles) ranges[prev].y = i;
+  }
+  if (i == m - 1 && tile < n_tiles) ranges[tile].y = m;
+}
+
+inline uint32_t sort_blocks(uint32_t n) { return (n + SORT_TILE - 1) / SORT_TILE; }
+
+}  // namespace
+}  // namespace dev
+}  // namespace b2c
+
+using namespace b2c::dev;
+
+extern "C" size_t b2c_radix_sort_temp_bytes(uint32_t n) {
+  const size_t nb = sort_blocks(n > 0 ? n : 1);
+  return (nb * RADIX + RADIX) * sizeof(uint32_t);
+}
+
+extern "C" int b2c_hip_radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in, uint32_t* keys_out,
+                                        uint32_t* vals_out, uint32_t* keys_alt, uint32_t* vals_alt, uint32_t n,
+                                        const uint32_t* n_dev, int begin_bit, int end_bit, void* temp, size_t temp_bytes,
+                                        hipStream_t stream) {
+  if (n == 0 || end_bit <= begin_bit) return 0;
+  if (temp_bytes < b2c_radix_sort_temp_bytes(n) || begin_bit < 0 || end_bit > 32) return (int)hipErrorInvalidValue;
+  const uint32_t nb = sort_blocks(n);
+  uint32_t* block_hist = static_cast<uint32_t*>(temp);
+  uint32_t* digit_total = block_hist + (size_t)nb * RADIX;
+  const int passes = (end_bit - begin_bit + 7) / 8;
+  const uint32_t* src_k = keys_in;
+  const uint32_t* src_v = vals_in;
+  for (int p = 0; p < passes; p++) {
+    const int shift = begin_bit + 8 * p;
+    const int bits = end_bit - shift < 8 ? end_bit - shift : 8;
+    // route the passes so that the last one lands in keys_out
+    const bool to_out = ((passes - 1 - p) % 2) == 0;
+    uint32_t* dk = to_out ? keys_out : keys_alt;
+    uint32_t* dv = to_out ? vals_out : vals_alt;
+    radix_upsweep<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, n, n_dev, shift, bits, block_hist, nb);
+    radix_scan_digits<<<dim3(RADIX), dim3(SORT_THREADS), 0, stream>>>(block_hist, nb, digit_total);
+    radix_scatter<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, dk, dv, n, n_dev, shift, bits, block_hist,
+                                                                 nb, digit_total);
+    int e = (int)hipGetLastError();
+    if (e) return e;
+    src_k = dk;
+    src_v = dv;
+  }
+  return 0;
+}
+
+extern "C" int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const float* proj1, uint32_t* keys, uint32_t* vals,
+                                  hipStream_t stream) {
+  if (n <= 0) return 0;
+  depth_keys_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(n, tile_count, reinterpret_cast<const float4*>(proj1),
+                                                                      keys, vals);
+  return (int)hipGetLastError();
+}
+
+extern "C" size_t b2c_scan_temp_bytes(uint32_t n) { return ((size_t)sort_blocks(n > 0 ? n : 1) + 1) * sizeof(uint32_t); }
+
+extern "C" int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
+                                   uint32_t* total_dev, void* temp, size_t temp_bytes, hipStream_t stream) {
+  if (n <= 0) return b2c_hip_fill_u32(total_dev, 0u, 1, stream);
+  if (temp_bytes < b2c_scan_temp_bytes((uint32_t)n)) return (int)hipErrorInvalidValue;
+  const uint32_t nb = sort_blocks((uint32_t)n);
+  uint32_t* block_sums = static_cast<uint32_t*>(temp);
+  scan_reduce<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums);
+  scan_top<<<dim3(1), dim3(1024), 0, stream>>>(nb, block_sums, total_dev);
+  scan_down<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums, tile_off);
+  return (int)hipGetLastError();
+}
+
+extern "C" int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream) {
+  if (a->n <= 0) return 0;
+  emit_small_kernel<<<dim3((a->n + 255) / 256), dim3(256), 0, stream>>>(*a, a->big_base);
+  emit_big_kernel<<<dim3(512), dim3(256), 0, stream>>>(*a, a->big_base);
+  return (int)hipGetLastError();
+}
+
+extern "C" int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_sorted, uint32_t n_tiles,
+                                   uint32_t* ranges, hipStream_t stream) {
+  int e = b2c_hip_fill_u32(ranges, 0u, (size_t)n_tiles * 2, stream);
+  if (e || m == 0) return e;
+  tile_ranges_kernel<<<dim3((m + 255) / 256), dim3(256), 0, stream>>>(m, m_dev, keys_sorted, n_tiles,
+                                                                      reinterpret_cast<uint2*>(ranges));
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,160 @@
+// Projection (replaces src/gpu/project.cu:8-126): one thread per splat, EWA projection, SH colour, exact
+// ellipse/8x8-tile test over the splat's tile bounding box. Splats with more than 32 bbox tiles are not
+// counted inline (one thread walking hundreds of tiles stalls its whole wave): they are appended to a
+// list and counted by one wave64 each in project_big_kernel, 64 tiles per step.
+#pragma clang fp contract(off)
+#include "b2c_kernels.h"
+#include "device_math.h"
+#include "project_one.h"
+
+namespace b2c {
+namespace dev {
+namespace {
+
+constexpr int PROJ_BLOCK = 256;
+
+template <int DEG>
+__global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a) {
+  const int i = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+  bool big = false;
+  if (i < a.n) {
+    const float4 po = reinterpret_cast<const float4*>(a.pos_op)[i];
+    const float4 q = reinterpret_cast<const float4*>(a.quat)[i];
+    const float4 ls = reinterpret_cast<const float4*>(a.lscale)[i];
+    Proj pr = project_one(po, q, ls, a.cam);
+    if (!pr.ok) {
+      a.tile_count[i] = 0u;
+    } else {
+      const float power = det_logf(pr.opac * 255.f);
+      TileBox bb = tile_bbox(pr.mean2d[0], pr.mean2d[1], pr.ex, pr.ey, a.tiles_x, a.tiles_y);
+      const int bw = bb.max_x - bb.min_x, bh = bb.max_y - bb.min_y;
+      big = bw * bh > 32;
+      uint32_t hits = 0, mask = 0;
+      if (!big) {
+        int bit = 0;
+        for (int ty = bb.min_y; ty < bb.max_y; ty++)
+          for (int tx = bb.min_x; tx < bb.max_x; tx++, bit++) {
+            float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
+            if (tile_hit(rx, ry, rx + RT_W, ry + RT_W, pr.mean2d[0], pr.mean2d[1], pr.conic, power)) {
+              hits++;
+              mask |= 1u << bit;
+            }
+          }
+        a.tile_count[i] = hits;
+      }
+      reinterpret_cast<uint2*>(a.hit_info)[i] =
+          make_uint2(big ? 0xFFFFFFFFu : mask, (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)bw << 24));
+      // SH colour, view direction camera -> splat (project.cu:44-55)
+      float vx = po.x - a.cam.pos[0], vy = po.y - a.cam.pos[1], vz = po.z - a.cam.pos[2];
+      float vl = sqrtf(vx * vx + vy * vy + vz * vz);
+      float inv = 1.f / fmaxf(vl, 1e-12f);
+      vx = vx * inv; vy = vy * inv; vz = vz * inv;
+      constexpr int K = (DEG + 1) * (DEG + 1);
+      float b[K];
+      sh_basis<DEG>(vx, vy, vz, b);
+      const int ka = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
+      ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
+      float cr = sv.get(0, i) * b[0], cg = sv.get(1, i) * b[0], cb = sv.get(2, i) * b[0];
+#pragma unroll
+      for (int k = 1; k < K; k++) {
+        if (k < ka) {
+          cr = cr + sv.get(k * 3, i) * b[k];
+          cg = cg + sv.get(k * 3 + 1, i) * b[k];
+          cb = cb + sv.get(k * 3 + 2, i) * b[k];
+        }
+      }
+      cr = cr + 0.5f; cg = cg + 0.5f; cb = cb + 0.5f;
+      cr = __builtin_isfinite(cr) ? fminf(fmaxf(cr, -100.f), 100.f) : 0.f;
+      cg = __builtin_isfinite(cg) ? fminf(fmaxf(cg, -100.f), 100.f) : 0.f;
+      cb = __builtin_isfinite(cb) ? fminf(fmaxf(cb, -100.f), 100.f) : 0.f;
+      reinterpret_cast<float4*>(a.proj0)[i] = make_float4(pr.mean2d[0], pr.mean2d[1], pr.conic.c00, pr.conic.c01);
+      reinterpret_cast<float4*>(a.proj1)[i] = make_float4(pr.conic.c11, pr.opac, pr.mc[2], power);
+      reinterpret_cast<float4*>(a.proj2)[i] = make_float4(cr, cg, cb, 0.f);
+      reinterpret_cast<float2*>(a.proj3)[i] = make_float2(0.f, 0.f);
+      if (a.max_screen) {
+        float ms = fmaxf(pr.ex / (float)a.cam.W, pr.ey / (float)a.cam.H);
+        a.max_screen[i] = fmaxf(a.max_screen[i], ms);
+      }
+    }
+  }
+  // wave-aggregated append of big splats
+  const uint64_t bm = ballot64(big);
+  if (bm) {
+    const int leader = __ffsll((unsigned long long)bm) - 1;
+    uint32_t base = 0;
+    if (lane_id() == leader) base = atomicAdd(a.big_count, popc64(bm));
+    base = __shfl(base, leader);
+    if (big) a.big_list[base + mbcnt64(bm)] = (uint32_t)i;
+  }
+}
+
+// One wave64 per big splat: count the tiles of its bbox that pass tile_hit, 64 tiles per step in row-major
+// order. The grid is fixed; waves stride over the device-side list length.
+__global__ void __launch_bounds__(256) project_big_kernel(b2c_project_args a) {
+  const int lane = lane_id();
+  const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
+  const uint32_t nwaves = (gridDim.x * 256u) >> 6;
+  const uint32_t count = *a.big_count;
+  for (uint32_t e = wave; e < count; e += nwaves) {
+    const uint32_t i = a.big_list[e];
+    const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
+    const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
+    Sym2 conic{p0.z, p0.w, p1.x};
+    float ex, ey;
+    extent_from_conic(conic, p1.w, ex, ey);
+    TileBox bb = tile_bbox(p0.x, p0.y, ex, ey, a.tiles_x, a.tiles_y);
+    const int bw = bb.max_x - bb.min_x;
+    const int area = bw * (bb.max_y - bb.min_y);
+    uint32_t hits = 0;
+    for (int b0 = 0; b0 < area; b0 += 64) {
+      const int b = b0 + lane;
+      bool h = false;
+      if (b < area) {
+        const int tx = bb.min_x + b % bw, ty = bb.min_y + b / bw;
+        const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
+        h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, p0.x, p0.y, conic, p1.w);
+      }
+      hits += popc64(ballot64(h));
+    }
+    if (lane == 0) a.tile_count[i] = hits;
+  }
+}
+
+__global__ void fill_u32_kernel(uint32_t* p, uint32_t v, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = v;
+}
+
+}  // namespace
+}  // namespace dev
+}  // namespace b2c
+
+using namespace b2c::dev;
+
+extern "C" int b2c_hip_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t stream) {
+  if (count == 0) return 0;
+  size_t blocks = (count + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  fill_u32_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(p, value, count);
+  return (int)hipGetLastError();
+}
+
+extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
+  if (a->n <= 0) return 0;
+  if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
+  int e = b2c_hip_fill_u32(a->big_count, 0u, 1, stream);
+  if (e) return e;
+  dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);
+  switch (a->degree) {
+    case 0: project_kernel<0><<<grid, block, 0, stream>>>(*a); break;
+    case 1: project_kernel<1><<<grid, block, 0, stream>>>(*a); break;
+    case 2: project_kernel<2><<<grid, block, 0, stream>>>(*a); break;
+    case 3: project_kernel<3><<<grid, block, 0, stream>>>(*a); break;
+    default: project_kernel<4><<<grid, block, 0, stream>>>(*a); break;
+  }
+  e = (int)hipGetLastError();
+  if (e) return e;
+  project_big_kernel<<<dim3(512), dim3(256), 0, stream>>>(*a);
+  return (int)hipGetLastError();
+}

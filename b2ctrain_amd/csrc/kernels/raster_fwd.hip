@@ -1,0 +1,89 @@
+// Forward compositing (replaces src/gpu/raster_fwd.cu:8-90, FEAT none, HOLLOW none): one wave64 per 8x8
+// tile, one lane per pixel, the tile's depth-ordered list staged through LDS 64 splats at a time,
+// front-to-back alpha blending with the 1/255 cutoff (sigma <= power), the 0.999 clamp and the 1e-4
+// transmittance stop. The whole wave leaves as soon as every lane is done. With bwd_info the tile's range
+// end is shrunk to one past the last fragment any pixel composited.
+#include "b2c_kernels.h"
+#include "raster_common.h"
+
+namespace b2c {
+namespace dev {
+namespace {
+
+__global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
+  __shared__ float4 s0[64], s1[64], s2[64];
+  const int n_tiles = a.tiles_x * a.tiles_y;
+  const int tile = xcd_tile(blockIdx.x, n_tiles);
+  if (tile >= n_tiles) return;
+  const int lane = threadIdx.x;
+  const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
+  const int px = tx * RT_W + (lane & 7), py = ty * RT_W + (lane >> 3);
+  const bool inside = px < a.W && py < a.H;
+  const float pcx = px + 0.5f, pcy = py + 0.5f;
+  uint2* ranges = reinterpret_cast<uint2*>(a.tile_ranges);
+  const uint2 range = ranges[tile];
+  const float4* proj0 = reinterpret_cast<const float4*>(a.proj0);
+  const float4* proj1 = reinterpret_cast<const float4*>(a.proj1);
+  const float4* proj2 = reinterpret_cast<const float4*>(a.proj2);
+  float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
+  bool done = !inside;
+  uint32_t last = range.x;
+  for (uint32_t start = range.x; start < range.y; start += 64) {
+    if (ballot64(!done) == 0) break;
+    const uint32_t remaining = min(64u, range.y - start);
+    __syncthreads();
+    if ((uint32_t)lane < remaining) {
+      const uint32_t gid = a.vals_sorted[start + lane];
+      s0[lane] = proj0[gid];
+      s1[lane] = proj1[gid];
+      s2[lane] = proj2[gid];
+    }
+    __syncthreads();
+    if (!done) {
+      for (uint32_t t = 0; t < remaining; t++) {
+        const float4 p0 = s0[t];
+        const float4 p1 = s1[t];
+        const float sigma = calc_sigma(pcx, pcy, p0.z, p0.w, p1.x, p0.x, p0.y);
+        if (sigma < 0.f || sigma > p1.w) continue;
+        const float alpha = fminf(ALPHA_MAX, p1.y * gauss_weight(sigma));
+        const float next_T = T * (1.f - alpha);
+        if (next_T <= T_CUTOFF) {
+          done = true;
+          break;
+        }
+        const float vis = alpha * T;
+        const float4 col = s2[t];
+        r += fmaxf(col.x, 0.f) * vis;
+        g += fmaxf(col.y, 0.f) * vis;
+        b += fmaxf(col.z, 0.f) * vis;
+        T = next_T;
+        last = start + t + 1;
+      }
+    }
+  }
+  if (inside) {
+    const int pix = py * a.W + px;
+    reinterpret_cast<float4*>(a.out_rgba)[pix] = make_float4(r + T * a.bg[0], g + T * a.bg[1], b + T * a.bg[2], 1.f - T);
+    reinterpret_cast<float4*>(a.out_feat)[pix] = make_float4(0.f, 0.f, 0.f, T);
+    if (a.bwd_info) a.last_idx[pix] = last;
+  }
+  if (a.bwd_info) {
+    uint32_t m = last;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = max(m, (uint32_t)__shfl_xor(m, o));
+    if (lane == 0) ranges[tile].y = m;
+  }
+}
+
+}  // namespace
+}  // namespace dev
+}  // namespace b2c
+
+using namespace b2c::dev;
+
+extern "C" int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream) {
+  const int n_tiles = a->tiles_x * a->tiles_y;
+  if (n_tiles <= 0) return 0;
+  raster_fwd_kernel<<<dim3(NUM_XCD * xcd_tiles_per(n_tiles)), dim3(64), 0, stream>>>(*a);
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,341 @@
+"""Synthetic scenes for the five BASELINE.json configurations and for the reference's FD-harness scene.
+
+Every scene is a plain bundle of numpy arrays in the layouts the C ABI takes:
+
+* ``pos_op``  [n][4] f32  (x, y, z, opacity logit)              -- Model::pos_op, src/model.h:8-23
+* ``quat``    [n][4] f32  (w, x, y, z), unnormalised            -- Model::quat
+* ``lscale``  [n][4] f32  (log sx, log sy, log sz, floor f)     -- Model::lscale (floor 0 = none)
+* ``sh``      [n][K][3] f32 coefficient-major (SplatCloud order, src/ply.h); when ``sh_fp16`` the bands
+  above DC are already rounded to fp16 (round to nearest even), which is what Model::upload stores
+  (src/model.cu:66-71).
+* ``gt``      [H*W] u32 packed RGBA8 ``r | g<<8 | b<<16 | a<<24`` (premultiplied for transparent views,
+  src/dataset/views.cpp:178-183), ``weights`` [H*W] u8 or None.
+
+Random numbers come from numpy's PCG64 generator seeded with ``0xB2C0 + config``. Data is synthetic; no
+dataset or checkpoint is read.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+SH_C0 = 0.28209479177387814
+
+
+@dataclass
+class Camera:
+    """Pinhole camera, world->camera R (row major) and t; OpenCV axes (+x right, +y down, +z forward).
+
+    Mirrors b2c::Camera (src/dataset/camera.h:8-36)."""
+
+    width: int
+    height: int
+    fx: float
+    fy: float
+    cx: float
+    cy: float
+    R: np.ndarray  # (9,) f32
+    t: np.ndarray  # (3,) f32
+
+    @property
+    def pos(self) -> np.ndarray:
+        R = self.R.reshape(3, 3).astype(np.float32)
+        t = self.t.astype(np.float32)
+        # pos = -R^T t, evaluated in float like Camera::update_pos (camera.h:24-29)
+        out = np.zeros(3, np.float32)
+        for i in range(3):
+            out[i] = -(R[0, i] * t[0] + R[1, i] * t[1] + R[2, i] * t[2])
+        return out
+
+
+def camera_gpu(cam: Camera, W: int | None = None, H: int | None = None) -> dict:
+    """CameraGPU::from (src/gpu/render.h:15-24) in float32 arithmetic."""
+    W = cam.width if W is None else W
+    H = cam.height if H is None else H
+    f = np.float32
+    sx = f(W) / f(cam.width)
+    sy = f(H) / f(cam.height)
+    fx, fy, cx, cy = f(cam.fx) * sx, f(cam.fy) * sy, f(cam.cx) * sx, f(cam.cy) * sy
+    return dict(
+        R=cam.R.astype(np.float32).copy(), t=cam.t.astype(np.float32).copy(), pos=cam.pos,
+        fx=fx, fy=fy, cx=cx, cy=cy, W=W, H=H,
+        lim_pos_x=(f(1.15) * f(W) - cx) / fx, lim_pos_y=(f(1.15) * f(H) - cy) / fy,
+        lim_neg_x=(f(-0.15) * f(W) - cx) / fx, lim_neg_y=(f(-0.15) * f(H) - cy) / fy,
+    )
+
+
+@dataclass
+class Scene:
+    name: str
+    degree: int
+    pos_op: np.ndarray
+    quat: np.ndarray
+    lscale: np.ndarray
+    sh: np.ndarray
+    cam: Camera
+    gt: np.ndarray
+    weights: np.ndarray | None = None
+    sh_fp16: bool = False
+    # LossParams (src/gpu/loss.h:20-30)
+    l1_w: float = 0.8
+    ssim_w: float = -0.2
+    composite: bool = False
+    mask: bool = False
+    alpha_lane: bool = False
+    match_alpha_weight: float = 0.1
+    scale: float = 1.0
+    bg: tuple = (0.0, 0.0, 0.0)
+    extra_cams: list = field(default_factory=list)
+
+    @property
+    def n(self) -> int:
+        return self.pos_op.shape[0]
+
+    @property
+    def K(self) -> int:
+        return (self.degree + 1) ** 2
+
+    @property
+    def W(self) -> int:
+        return self.cam.width
+
+    @property
+    def H(self) -> int:
+        return self.cam.height
+
+    def subset(self, n: int) -> "Scene":
+        """First n splats of the scene (same camera, target and loss options)."""
+        s = Scene(**{k: getattr(self, k) for k in self.__dataclass_fields__})
+        s.pos_op, s.quat, s.lscale, s.sh = (a[:n].copy() for a in (self.pos_op, self.quat, self.lscale, self.sh))
+        s.name = f"{self.name}[:{n}]"
+        return s
+
+    def with_camera(self, cam: Camera) -> "Scene":
+        s = Scene(**{k: getattr(self, k) for k in self.__dataclass_fields__})
+        s.cam = cam
+        return s
+
+
+def _rand_quat(rng, n):
+    # Shoemake's uniform random rotation (K. Shoemake, "Uniform random rotations", Graphics Gems III)
+    u1, u2, u3 = rng.random(n), rng.random(n), rng.random(n)
+    a, b = np.sqrt(1 - u1), np.sqrt(u1)
+    w = b * np.cos(2 * np.pi * u3)
+    x = a * np.sin(2 * np.pi * u2)
+    y = a * np.cos(2 * np.pi * u2)
+    z = b * np.sin(2 * np.pi * u3)
+    return np.stack([w, x, y, z], 1).astype(np.float32)
+
+
+def look_at(eye, target, down_hint=(0.0, 1.0, 0.0)) -> tuple[np.ndarray, np.ndarray]:
+    """World->camera (R, t) for a camera at ``eye`` looking at ``target`` (OpenCV axes, +y down)."""
+    eye = np.asarray(eye, np.float64)
+    fwd = np.asarray(target, np.float64) - eye
+    fwd /= np.linalg.norm(fwd)
+    right = np.cross(np.asarray(down_hint, np.float64), fwd)
+    right /= np.linalg.norm(right)
+    down = np.cross(fwd, right)
+    R = np.stack([right, down, fwd], 0)
+    t = -R @ eye
+    return R.reshape(9).astype(np.float32), t.astype(np.float32)
+
+
+def _pack_rgba(r, g, b, a):
+    q = lambda v: np.clip(np.floor(np.asarray(v) * 255.0 + 0.5), 0, 255).astype(np.uint32)
+    return q(r) | (q(g) << 8) | (q(b) << 16) | (q(a) << 24)
+
+
+def _smooth_target(rng, W, H, n_blobs=32, noise=0.02):
+    yy, xx = np.mgrid[0:H, 0:W].astype(np.float32)
+    img = np.zeros((H, W, 3), np.float32)
+    for _ in range(n_blobs):
+        cx, cy = rng.random() * W, rng.random() * H
+        s = (0.05 + 0.2 * rng.random()) * min(W, H)
+        amp = rng.random(3).astype(np.float32)
+        g = np.exp(-((xx - cx) ** 2 + (yy - cy) ** 2) / (2 * s * s))
+        img += g[..., None] * amp[None, None, :]
+    img /= max(img.max(), 1e-6)
+    img += rng.normal(0, noise, img.shape).astype(np.float32)
+    return np.clip(img, 0, 1)
+
+
+def _colour_to_dc(c):
+    return ((c - 0.5) / SH_C0).astype(np.float32)
+
+
+def _fp16_bands(sh):
+    out = sh.copy()
+    out[:, 1:, :] = out[:, 1:, :].astype(np.float16).astype(np.float32)
+    return out
+
+
+def config1(seed: int | None = None) -> Scene:
+    """1,024 splats, SH0, 64x64, fx=fy=64, cx=cy=32; means in a unit cube centred 3 units ahead."""
+    rng = np.random.default_rng(0xB2C0 + 1 if seed is None else seed)
+    n, W, H = 1024, 64, 64
+    pos = rng.random((n, 3)) - 0.5
+    pos[:, 2] += 3.0
+    op = rng.normal(0, 1, n)
+    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
+    lscale = np.zeros((n, 4), np.float32)
+    lscale[:, :3] = rng.normal(-3.0, 0.5, (n, 3))
+    sh = _colour_to_dc(rng.random((n, 1, 3)))
+    R, t = np.eye(3, dtype=np.float32).reshape(9), np.zeros(3, np.float32)
+    cam = Camera(W, H, 64.0, 64.0, 32.0, 32.0, R, t)
+    noise = rng.random((H * W, 3))
+    gt = _pack_rgba(noise[:, 0], noise[:, 1], noise[:, 2], np.ones(H * W))
+    return Scene("cfg1", 0, pos_op, _rand_quat(rng, n), lscale, sh, cam, gt)
+
+
+def config2(seed: int | None = None, n: int = 100_000) -> Scene:
+    """100k splats, SH3 (bands N(0, 0.05)), 800x800, 50 deg FOV; means N(0,1) within r <= 2, 4 units away."""
+    rng = np.random.default_rng(0xB2C0 + 2 if seed is None else seed)
+    W = H = 800
+    pos = rng.normal(0, 1, (n, 3))
+    r = np.linalg.norm(pos, axis=1)
+    bad = r > 2
+    while bad.any():
+        pos[bad] = rng.normal(0, 1, (int(bad.sum()), 3))
+        bad = np.linalg.norm(pos, axis=1) > 2
+    op = rng.normal(-1.0, 1.5, n)
+    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
+    lscale = np.zeros((n, 4), np.float32)
+    lscale[:, :3] = rng.normal(-4.5, 0.6, (n, 3))
+    sh = np.zeros((n, 16, 3), np.float32)
+    sh[:, 0, :] = _colour_to_dc(rng.random((n, 3)))
+    sh[:, 1:, :] = rng.normal(0, 0.05, (n, 15, 3))
+    f = 400.0 / math.tan(math.radians(25.0))
+    R, t = look_at((0.0, 0.0, -4.0), (0.0, 0.0, 0.0))
+    cam = Camera(W, H, f, f, 400.0, 400.0, R, t)
+    img = _smooth_target(rng, W, H).reshape(-1, 3)
+    gt = _pack_rgba(img[:, 0], img[:, 1], img[:, 2], np.ones(H * W))
+    return Scene("cfg2", 3, pos_op, _rand_quat(rng, n), lscale, sh, cam, gt)
+
+
+def _ellipse_alpha(W, H):
+    yy, xx = np.mgrid[0:H, 0:W].astype(np.float64)
+    # semi-axes a, b with pi*a*b = W*H/2 and a/b = W/H
+    b = math.sqrt(W * H / (2 * math.pi) * H / W)
+    a = b * W / H
+    inside = ((xx + 0.5 - W / 2) / a) ** 2 + ((yy + 0.5 - H / 2) / b) ** 2 <= 1.0
+    return inside.reshape(-1)
+
+
+def config3(seed: int | None = None, n: int = 1_000_000, masked: bool = False) -> Scene:
+    """1M splats, SH3, 1920x1080; means uniform in a 6x4x6 box of which ~60% lie in the frustum.
+
+    Fused L1+SSIM with alpha lane, per-pixel weights in [0.5, 1.5] (u8 in [85, 255] with scale 1.5),
+    binary elliptic alpha over half the image. ``masked=False`` is the transparent-view mode
+    (composite + alpha lane, trainer.cpp:495-497), ``masked=True`` the masked-view mode."""
+    rng = np.random.default_rng(0xB2C0 + 3 if seed is None else seed)
+    W, H = 1920, 1080
+    pos = np.empty((n, 3))
+    pos[:, 0] = rng.uniform(-3, 3, n)
+    pos[:, 1] = rng.uniform(-2, 2, n)
+    pos[:, 2] = rng.uniform(0, 6, n)
+    op = rng.normal(-0.5, 2.0, n)
+    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
+    lscale = np.zeros((n, 4), np.float32)
+    lscale[:, :3] = rng.normal(-5.0, 0.7, (n, 3))
+    sh = np.zeros((n, 16, 3), np.float32)
+    sh[:, 0, :] = _colour_to_dc(rng.random((n, 3)))
+    sh[:, 1:, :] = rng.normal(0, 0.05, (n, 15, 3))
+    f = 1000.0
+    # camera just in front of the box's near face, looking down +z through its centre: ~62% of the
+    # means project inside the image
+    R, t = look_at((0.0, 0.0, -0.05), (0.0, 0.0, 3.0))
+    cam = Camera(W, H, f, f, W / 2.0, H / 2.0, R, t)
+    img = _smooth_target(rng, W, H).reshape(-1, 3)
+    alpha = _ellipse_alpha(W, H).astype(np.float64)
+    prem = img * alpha[:, None] if not masked else img
+    gt = _pack_rgba(prem[:, 0], prem[:, 1], prem[:, 2], alpha)
+    weights = rng.integers(85, 256, W * H).astype(np.uint8)
+    return Scene("cfg3" + ("m" if masked else ""), 3, pos_op, _rand_quat(rng, n), lscale, sh, cam, gt, weights,
+                 composite=not masked, mask=masked, alpha_lane=not masked, match_alpha_weight=0.1, scale=1.5)
+
+
+def config4(seed: int | None = None, n: int = 3_000_000) -> Scene:
+    """3M splats, SH4, 1920x1080; a slab 0.5 deep facing the camera (high depth complexity); 8 poses."""
+    rng = np.random.default_rng(0xB2C0 + 4 if seed is None else seed)
+    W, H = 1920, 1080
+    f = 1000.0
+    pos = np.empty((n, 3))
+    pos[:, 0] = rng.uniform(-2.2, 2.2, n)
+    pos[:, 1] = rng.uniform(-1.25, 1.25, n)
+    pos[:, 2] = rng.uniform(-0.25, 0.25, n)
+    op = rng.normal(-2.0, 1.0, n)
+    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
+    lscale = np.zeros((n, 4), np.float32)
+    lscale[:, :3] = rng.normal(-4.0, 0.5, (n, 3))
+    sh = np.zeros((n, 25, 3), np.float32)
+    sh[:, 0, :] = _colour_to_dc(rng.random((n, 3)))
+    sh[:, 1:, :] = rng.normal(0, 0.05, (n, 24, 3))
+    cams = []
+    for v in range(8):
+        ang = math.radians(-14.0 + 4.0 * v)
+        eye = (2.4 * math.sin(ang), 0.15 * math.cos(3 * ang), -2.4 * math.cos(ang))
+        R, t = look_at(eye, (0.0, 0.0, 0.0))
+        cams.append(Camera(W, H, f, f, W / 2.0, H / 2.0, R, t))
+    img = _smooth_target(rng, W, H).reshape(-1, 3)
+    gt = _pack_rgba(img[:, 0], img[:, 1], img[:, 2], np.ones(W * H))
+    return Scene("cfg4", 4, pos_op, _rand_quat(rng, n), lscale, sh, cams[0], gt, extra_cams=cams)
+
+
+def config5(seed: int | None = None, n: int = 500_000) -> Scene:
+    """500k splats, 3840x2160, SH3 with fp16 bands; 95% tiny splats, 5% large anisotropic ones."""
+    rng = np.random.default_rng(0xB2C0 + 5 if seed is None else seed)
+    W, H = 3840, 2160
+    f = 2000.0
+    pos = np.empty((n, 3))
+    pos[:, 0] = rng.uniform(-3, 3, n)
+    pos[:, 1] = rng.uniform(-1.8, 1.8, n)
+    pos[:, 2] = rng.uniform(1.0, 7.0, n)
+    op = rng.normal(0.0, 2.0, n)
+    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
+    lscale = np.zeros((n, 4), np.float32)
+    lscale[:, :3] = rng.normal(-7.0, 0.3, (n, 3))
+    big = rng.random(n) < 0.05
+    lscale[big, :3] = rng.choice(np.array([-1.0, -3.0, -6.0], np.float32), (int(big.sum()), 3))
+    sh = np.zeros((n, 16, 3), np.float32)
+    sh[:, 0, :] = _colour_to_dc(rng.random((n, 3)))
+    sh[:, 1:, :] = rng.normal(0, 0.05, (n, 15, 3))
+    R, t = look_at((0.0, 0.0, -1.0), (0.0, 0.0, 4.0))
+    cam = Camera(W, H, f, f, W / 2.0, H / 2.0, R, t)
+    img = _smooth_target(rng, W, H).reshape(-1, 3)
+    gt = _pack_rgba(img[:, 0], img[:, 1], img[:, 2], np.ones(W * H))
+    return Scene("cfg5", 3, pos_op, _rand_quat(rng, n), lscale, _fp16_bands(sh), cam, gt, sh_fp16=True)
+
+
+def fd_scene(seed: int, n: int = 24, masked: bool = False, degree: int = 2) -> Scene:
+    """The reference FD harness scene shape (tests/tests.cpp:23-59): 48x40, fx=fy=40, SH degree 2,
+    means in [-0.6,0.6]x[-0.5,0.5]x[1.5,2.5], scales 0.05-0.13, jittered quaternions, opacity logits
+    in [-2, 2], random RGBA target with u8 weights in [64, 255]. Transparent views use composite +
+    alpha lane (match weight 0.3), masked views the mask with scale 1.7 (tests.cpp:67-71)."""
+    rng = np.random.default_rng(seed)
+    W, H = 48, 40
+    K = (degree + 1) ** 2
+    u = lambda *s: rng.random(s)
+    un = lambda *s: rng.random(s) * 2 - 1
+    pos = np.stack([un(n) * 0.6, un(n) * 0.5, 2.0 + un(n) * 0.5], 1)
+    op = un(n) * 2.0
+    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
+    lscale = np.zeros((n, 4), np.float32)
+    lscale[:, :3] = np.log(0.05 + 0.08 * u(n, 3))
+    quat = np.stack([1.0 + un(n) * 0.5, un(n) * 0.5, un(n) * 0.5, un(n) * 0.5], 1).astype(np.float32)
+    sh = np.zeros((n, K, 3), np.float32)
+    sh[:, 0, :] = un(n, 3) * 1.5
+    if K > 1:
+        sh[:, 1:, :] = un(n, K - 1, 3) * 0.3
+    R, t = np.eye(3, dtype=np.float32).reshape(9), np.zeros(3, np.float32)
+    cam = Camera(W, H, 40.0, 40.0, W / 2.0, H / 2.0, R, t)
+    rgba = (u(W * H, 4) * 255).astype(np.uint32)
+    gt = rgba[:, 0] | (rgba[:, 1] << 8) | (rgba[:, 2] << 16) | (rgba[:, 3] << 24)
+    weights = (64 + u(W * H) * 191).astype(np.uint8)
+    return Scene(f"fd{seed}{'m' if masked else 't'}", degree, pos_op, quat, lscale, sh, cam, gt.astype(np.uint32),
+                 weights, composite=not masked, mask=masked, alpha_lane=not masked, match_alpha_weight=0.3,
+                 scale=1.7 if masked else 1.0, bg=(0.2, 0.1, 0.3))
+
+
+CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}

@@ -1,0 +1,113 @@
+/*
+ * b2c.h — C ABI over the MI355X splat rasterizer's C++ drop-in API (b2ctrain_amd/csrc/b2c/), for
+ * callers that bind through an FFI (ctypes, cgo, JNI, N-API). Opaque handles own the C++ objects; every
+ * function returns 0 on success or a nonzero code, with the message in b2c_last_error().
+ *
+ * The reference (Erant/b2ctrain) has no FFI: its callers use the C++ API directly. Each entry point below
+ * cites the C++ function it wraps, which in turn replaces the cited reference function.
+ */
+#ifndef B2C_H
+#define B2C_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "b2c_kernels.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct b2c_model b2c_model; /* b2c::Model     (src/model.h:14-40) */
+typedef struct b2c_ctx b2c_ctx;     /* b2c::RenderCtx (src/gpu/render.h:66-95) + its HIP stream */
+typedef struct b2c_view b2c_view;   /* b2c::ViewGPU   (src/gpu/loss.h:7-18) + owned device copies */
+
+/* b2c::Camera (src/dataset/camera.h:8-36); pos is derived (-R^T t). */
+typedef struct b2c_camera {
+  int width, height;
+  float fx, fy, cx, cy;
+  float R[9];
+  float t[3];
+} b2c_camera;
+
+/* The RenderParams fields this build supports (src/gpu/render.h:29-63). */
+typedef struct b2c_render_opts {
+  b2c_camera cam;
+  int W, H; /* render size (CameraGPU::from rescales the intrinsics) */
+  float bg[3];
+  int sh_degree;
+  int bwd_info;
+} b2c_render_opts;
+
+/* LossParams (src/gpu/loss.h:20-30). */
+typedef struct b2c_loss_opts {
+  float l1_w, ssim_w;
+  float bg[3];
+  int composite, mask, alpha_lane;
+  float match_alpha_weight, scale, grad_scale;
+} b2c_loss_opts;
+
+typedef struct b2c_ctx_info {
+  int W, H, tiles_x, tiles_y, n_tiles, tile_bits;
+  uint32_t num_isect;
+  uint64_t isect_cap;
+} b2c_ctx_info;
+
+/* Per-stage GPU times of one training step (hipEvents on the context's stream), milliseconds. */
+typedef struct b2c_step_times {
+  float project_ms, bin_ms, forward_ms, loss_ms, backward_ms, vjp_ms, total_ms;
+} b2c_step_times;
+
+const char* b2c_last_error(void);
+int b2c_get_device_count(int* count);
+/* CameraGPU::from (src/gpu/render.h:15-24), host only. */
+int b2c_camera_gpu_from(const b2c_camera* cam, int W, int H, b2c_camera_gpu* out);
+
+/* Model::upload (src/model.cu:44-80). floor [n] may be NULL (lscale.w = 0 as the reference uploads). */
+b2c_model* b2c_model_create(void);
+void b2c_model_destroy(b2c_model* m);
+int b2c_model_upload(b2c_model* m, int n, int degree, int sh_fp16, const float* pos, const float* log_scale,
+                     const float* quat, const float* opacity, const float* sh, const float* floor_);
+/* Copy a model buffer to host: "pos_op", "quat", "lscale", "vis_weight", "vis_count", "refine_norm", "max_screen". */
+int b2c_model_read(const b2c_model* m, const char* field, void* host, size_t bytes);
+
+/* RenderCtx and RenderCtx::setup (src/gpu/render.cu:5-21). */
+b2c_ctx* b2c_ctx_create(void);
+void b2c_ctx_destroy(b2c_ctx* c);
+int b2c_ctx_setup(b2c_ctx* c, int W, int H, int n_splats);
+int b2c_ctx_info_get(const b2c_ctx* c, b2c_ctx_info* out);
+/* Copy a RenderCtx buffer to / from host memory by field name ("proj0", "tile_count", "keys_sorted",
+ * "vals_sorted", "tile_ranges", "out_rgba", "v_out", "v_splat", "grads", ...). Synchronous. */
+int b2c_ctx_read(b2c_ctx* c, const char* field, void* host, size_t bytes);
+int b2c_ctx_write(b2c_ctx* c, const char* field, const void* host, size_t bytes);
+int b2c_ctx_zero(b2c_ctx* c, const char* field);
+int b2c_ctx_synchronize(b2c_ctx* c);
+/* The context's HIP stream (hipStream_t) for callers that enqueue their own work around the path. */
+void* b2c_ctx_stream(b2c_ctx* c);
+
+/* A view: device copies of packed RGBA8 and optional u8 weights. */
+b2c_view* b2c_view_create(int W, int H, const uint32_t* rgba, const uint8_t* weights);
+void b2c_view_destroy(b2c_view* v);
+
+/* render_forward / project_splats / bin_and_sort / rasterize_forward (src/gpu/render.h:97-103). */
+int b2c_render_forward(b2c_ctx* c, const b2c_model* m, const b2c_render_opts* o);
+int b2c_project_splats(b2c_ctx* c, const b2c_model* m, const b2c_render_opts* o);
+int b2c_bin_and_sort(b2c_ctx* c, const b2c_model* m);
+int b2c_rasterize_forward(b2c_ctx* c, const b2c_render_opts* o);
+/* photometric_loss / accumulate_loss (src/gpu/loss.h:33-37). */
+int b2c_photometric_loss(b2c_ctx* c, const b2c_view* v, const b2c_loss_opts* o);
+int b2c_accumulate_loss(b2c_ctx* c);
+/* rasterize_backward (mode 0) / rasterize_backward_tc (mode 1, divides by grad_scale) (src/gpu/render.h:105-109). */
+int b2c_rasterize_backward(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int mode, float grad_scale);
+/* optimizer_step with grad_out = the context's "grads" buffer [n][11 + 3K] (src/gpu/optim.h:50,
+ * optim.cu:292-296); accumulate = 1 sums into it instead of overwriting. */
+int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int active_deg, int accumulate);
+/* One training step as trainer.cpp:487-529 orders it (forward, loss with grad_scale, backward in `mode`,
+ * projection VJP), loss_accum[0..1] zeroed first. times may be NULL (no events recorded). */
+int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
+                   int mode, int accumulate, b2c_step_times* times);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

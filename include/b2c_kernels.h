@@ -1,0 +1,185 @@
+/*
+ * b2c_kernels.h — the C-ABI launcher layer of the MI355X (gfx950) splat rasterizer.
+ *
+ * Plain structs of device pointers and sizes; every launcher enqueues its HIP kernels on `stream`
+ * and returns a hipError_t as int (0 = success). No allocation happens in any launcher: scratch
+ * buffers are passed in by the caller (the C++ RenderCtx owns them). The C++ drop-in API in
+ * b2ctrain_amd/csrc/b2c/{render,loss,optim}.h is built on these; the reference's equivalents are
+ * the static kernels and launch code cited on each entry point (paths relative to Erant/b2ctrain).
+ */
+#ifndef B2C_KERNELS_H
+#define B2C_KERNELS_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* CameraGPU after CameraGPU::from (src/gpu/render.h:8-25); also the kernels' CamDev (splat_math.cuh:219-221). */
+typedef struct b2c_camera_gpu {
+  float R[9]; /* world -> camera, row major */
+  float t[3];
+  float pos[3]; /* camera centre, world */
+  float fx, fy, cx, cy;
+  int W, H;
+  float lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y; /* EWA Jacobian clamp */
+} b2c_camera_gpu;
+
+/* Planar SH view (ShBuf, src/gpu/util.cuh:129-164): DC lanes fp32 in dc[lane*stride + i]; lanes >= 3 in
+ * hi32 (fp32) or hi16 (IEEE binary16) at [(lane-3)*stride + i]. Exactly one of hi16/hi32 is used when
+ * the degree is > 0 (hi32 wins when both are set). */
+typedef struct b2c_sh_view {
+  const float* dc;
+  const uint16_t* hi16;
+  const float* hi32;
+  size_t stride;
+} b2c_sh_view;
+
+/* ---- projection: replaces project_kernel / project_splats (src/gpu/project.cu:8-126) ---- */
+typedef struct b2c_project_args {
+  int n, degree, active_deg;
+  const float* pos_op; /* [n] float4 (x, y, z, opacity logit) */
+  const float* quat;   /* [n] float4 (w, x, y, z) */
+  const float* lscale; /* [n] float4 (log s xyz, floor) */
+  b2c_sh_view sh;
+  b2c_camera_gpu cam;
+  int tiles_x, tiles_y;
+  float* proj0;        /* [n] float4 (x, y, c00, c01) */
+  float* proj1;        /* [n] float4 (c11, opacity, depth, power) */
+  float* proj2;        /* [n] float4 (r, g, b, feat.x) */
+  float* proj3;        /* [n] float2 (feat.y, feat.z) */
+  uint32_t* tile_count;/* [n] */
+  uint32_t* hit_info;  /* [n] uint2 (hit mask or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24) */
+  float* max_screen;   /* [n] or NULL: max(., max(ex/W, ey/H)) (project.cu:82-83) */
+  uint32_t* big_list;  /* [n] scratch: splats whose bbox exceeds 32 tiles */
+  uint32_t* big_count; /* [1] scratch counter */
+} b2c_project_args;
+int b2c_hip_project(const b2c_project_args* a, hipStream_t stream);
+
+/* ---- binning (src/gpu/binning.cu:10-143) ---- */
+
+/* Radix-sort scratch: bytes needed to sort up to n pairs (LSD, 8-bit digits, reduce-then-scan). */
+size_t b2c_radix_sort_temp_bytes(uint32_t n);
+
+/* Stable LSD key-value radix sort of keys_in/vals_in over bits [begin_bit, end_bit) into keys_out/vals_out
+ * (replaces cub::DeviceRadixSort::SortPairs, binning.cu:116-118,140-142). keys_alt/vals_alt are ping-pong
+ * buffers of n entries; the inputs are not modified. n_dev (may be NULL) points at a device copy of n: the
+ * launch covers n entries, the kernels read the live count from n_dev when it is set (n is then the
+ * capacity). */
+int b2c_hip_radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in, uint32_t* keys_out, uint32_t* vals_out,
+                             uint32_t* keys_alt, uint32_t* vals_alt, uint32_t n, const uint32_t* n_dev, int begin_bit,
+                             int end_bit, void* temp, size_t temp_bytes, hipStream_t stream);
+
+/* depth_keys_kernel (binning.cu:10-15): key = bits of view z if tile_count > 0 else 0xFFFFFFFF, val = index. */
+int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const float* proj1, uint32_t* keys, uint32_t* vals,
+                       hipStream_t stream);
+
+/* Scratch bytes of b2c_hip_scan_counts for n splats. */
+size_t b2c_scan_temp_bytes(uint32_t n);
+
+/* permute_counts_kernel + cub::DeviceScan::InclusiveSum (binning.cu:16-19,120-124): tile_off[r] = sum over
+ * r' <= r of tile_count[order[r']]; the total is written to *total_dev. */
+int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
+                        uint32_t* total_dev, void* temp, size_t temp_bytes, hipStream_t stream);
+
+/* emit_kernel (binning.cu:25-93): intersections in depth order, key = tile id, val = splat index. Small
+ * splats (hit mask) are emitted by a wave-cooperative coalesced sweep; splats with more than 32 bbox tiles
+ * by one wave each over their bbox in row-major order. Slots missing from a big splat get key = n_tiles. */
+typedef struct b2c_emit_args {
+  int n;
+  const uint32_t* order, *tile_count, *tile_off, *hit_info;
+  const float* proj0, *proj1;
+  int tiles_x, tiles_y;
+  uint32_t cap;
+  uint32_t* keys, *vals;
+  const uint32_t* big_list, *big_count; /* from b2c_hip_project */
+  uint32_t* big_base;                   /* [n] scratch: first slot of each big splat */
+} b2c_emit_args;
+int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream);
+
+/* tile_ranges_kernel (binning.cu:95-105) after zeroing ranges: ranges[t] = [first, last) of tile t. */
+int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_sorted, uint32_t n_tiles,
+                        uint32_t* ranges, hipStream_t stream);
+
+/* ---- rasterization ---- */
+
+/* raster_fwd_kernel<FEAT=none, BWD, HOLLOW=none> / rasterize_forward (src/gpu/raster_fwd.cu:8-90). */
+typedef struct b2c_raster_fwd_args {
+  uint32_t* tile_ranges;      /* [n_tiles] uint2; .y shrunk in place when bwd_info */
+  const uint32_t* vals_sorted;
+  const float* proj0, *proj1, *proj2;
+  int W, H, tiles_x, tiles_y;
+  float bg[3];
+  int bwd_info;
+  float* out_rgba;            /* [P] float4 */
+  float* out_feat;            /* [P] float4 (feat xyz, T) */
+  uint32_t* last_idx;         /* [P] */
+} b2c_raster_fwd_args;
+int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream);
+
+/* Backward through compositing: raster_bwd_kernel (fp32 reduction, src/gpu/raster_bwd.cu:10-156) when
+ * mode = 0, raster_bwd_tc_kernel (src/gpu/raster_bwd_tc.cu:29-225; here MFMA f16 split hi/lo with fp32
+ * accumulation) when mode = 1. Gradients are multiplied by inv_gscale (mode 1 semantics; pass 1 for mode 0
+ * to match the reference's fp32 kernel). */
+typedef struct b2c_raster_bwd_args {
+  const uint32_t* tile_ranges;
+  const uint32_t* vals_sorted;
+  const float* proj0, *proj1, *proj2;
+  const float* out_rgba, *out_feat;
+  const uint32_t* last_idx;
+  const float* v_out;         /* [P] float4 dL/d(rgb, alpha) */
+  int W, H, tiles_x, tiles_y;
+  float bg[3];
+  float inv_gscale;
+  int mode;
+  float* v_splat;             /* [n][13], accumulated */
+  uint32_t* vis_flag;         /* [n] */
+  float* vis_weight;          /* [n] or NULL */
+} b2c_raster_bwd_args;
+int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stream);
+
+/* ---- loss: photometric_kernel / photometric_loss (src/gpu/loss.cu:18-195,296-315) ---- */
+typedef struct b2c_loss_args {
+  const float* pred;          /* [P] float4 out_rgba */
+  const uint32_t* gt;         /* [P] packed RGBA8 */
+  const uint8_t* weights;     /* [P] or NULL */
+  int W, H;
+  float l1_w, ssim_w, bg[3];
+  int composite, mask, alpha_lane;
+  float match_alpha_weight, scale, grad_scale;
+  float* v_out;               /* [P] float4 */
+  float* loss_accum;          /* [0] += loss */
+} b2c_loss_args;
+int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream);
+
+/* accumulate_kernel (loss.cu:317,324): a[2] += a[0] + a[1]; a[3] += 1. */
+int b2c_hip_accumulate_loss(float* loss_accum, hipStream_t stream);
+
+/* ---- projection VJP: optim_kernel's gradient part with op.grad_out (src/gpu/optim.cu:99-253,292-296) ----
+ * Reads and clears v_splat / vis_flag. accumulate = 1 adds into grad_out instead of overwriting (for
+ * gradients summed over several views). */
+typedef struct b2c_vjp_args {
+  int n, degree, active_deg;
+  const float* pos_op, *quat, *lscale;
+  b2c_sh_view sh;
+  b2c_camera_gpu cam;
+  float* v_splat;
+  uint32_t* vis_flag;
+  const uint32_t* tile_count;
+  float* grad_out;            /* [n][11 + 3K] */
+  int accumulate;
+  float* refine_norm;         /* [n] or NULL: max(., clamp(g[9], 0, 1e32)) (optim.cu:175-176) */
+  float* vis_count;           /* [n] or NULL: += visible (optim.cu:174) */
+} b2c_vjp_args;
+int b2c_hip_vjp(const b2c_vjp_args* a, hipStream_t stream);
+
+/* ---- utilities ---- */
+int b2c_hip_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,985 @@
+/*
+ * TEST INFRASTRUCTURE ONLY — CPU restatement of Erant/b2ctrain's splat rasterizer (the checker).
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use it.
+ * Build: gcc -O2 -std=c11 -ffp-contract=off (oracle/Makefile). Contraction must stay off: the
+ * projection and binning below are bit-exact restatements that the HIP kernels must reproduce.
+ */
+#include "b2c_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define RT_W 8
+#define ALPHA_CUTOFF (1.0f / 255.0f) /* splat_math.cuh:7 */
+#define T_CUTOFF 1e-4f              /* splat_math.cuh:8 */
+#define ALPHA_MAX 0.999f            /* splat_math.cuh:9 */
+#define GRAD_LANES 13               /* splat_math.cuh:10 */
+#define SH_C0 0.28209479177387814f
+
+/* ------------------------------------------------------------------------------------------------
+ * Cephes single-precision exp and log (Stephen L. Moshier, Cephes Math Library, single/expf.c and
+ * single/logf.c): Cody-Waite reduction by ln 2 split in two constants, then a degree-6 (exp) or
+ * degree-9 (log) polynomial. Replaces the reference's __expf/__logf fast-math intrinsics
+ * (splat_math.cuh:232,282; project.cu:31). Below -86 the result is returned as 0 so that no
+ * subnormal is ever produced (the GPU version follows the same rule).
+ * ---------------------------------------------------------------------------------------------- */
+float orc_expf(float xx) {
+  float x = xx;
+  if (!(x <= 88.0f)) return x != x ? x : INFINITY;
+  if (x < -86.0f) return 0.0f;
+  float t = 1.44269504088896341f * x;
+  t = t + 0.5f;
+  float z = floorf(t);
+  x = x - z * 0.693359375f;
+  x = x - z * -2.12194440e-4f;
+  int n = (int)z;
+  z = x * x;
+  float p = 1.9875691500e-4f;
+  p = p * x + 1.3981999507e-3f;
+  p = p * x + 8.3334519073e-3f;
+  p = p * x + 4.1665795894e-2f;
+  p = p * x + 1.6666665459e-1f;
+  p = p * x + 5.0000001201e-1f;
+  p = p * z;
+  p = p + x;
+  p = p + 1.0f;
+  return ldexpf(p, n);
+}
+
+float orc_logf(float xx) {
+  float x = xx;
+  if (!(x > 0.0f)) return x == 0.0f ? -INFINITY : NAN;
+  if (isinf(x)) return x;
+  int e;
+  x = frexpf(x, &e);
+  if (x < 0.707106781186547524f) {
+    e -= 1;
+    x = x + x;
+    x = x - 1.0f;
+  } else {
+    x = x - 1.0f;
+  }
+  float z = x * x;
+  float y = 7.0376836292e-2f;
+  y = y * x - 1.1514610310e-1f;
+  y = y * x + 1.1676998740e-1f;
+  y = y * x - 1.2420140846e-1f;
+  y = y * x + 1.4249322787e-1f;
+  y = y * x - 1.6668057665e-1f;
+  y = y * x + 2.0000714765e-1f;
+  y = y * x - 2.4999993993e-1f;
+  y = y * x + 3.3333331174e-1f;
+  y = y * x;
+  y = y * z;
+  float fe = (float)e;
+  if (e) y = y + -2.12194440e-4f * fe;
+  y = y + -0.5f * z;
+  z = x + y;
+  if (e) z = z + 0.693359375f * fe;
+  return z;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * Small fp32 helpers (util.cuh:210-243 semantics, left-to-right evaluation).
+ * ---------------------------------------------------------------------------------------------- */
+typedef struct { float c00, c01, c11; } sym2;
+
+static int finitef(float a) { return isfinite(a) != 0; }
+
+/* util.cuh:235-243: rotation matrix from a normalised (w, x, y, z) quaternion. */
+static void quat_to_mat(const float q[4], float R[9]) {
+  float w = q[0], x = q[1], y = q[2], z = q[3];
+  float x2 = x * x, y2 = y * y, z2 = z * z, xy = x * y, xz = x * z, yz = y * z, wx = w * x, wy = w * y, wz = w * z;
+  R[0] = 1.f - 2.f * (y2 + z2); R[1] = 2.f * (xy - wz);       R[2] = 2.f * (xz + wy);
+  R[3] = 2.f * (xy + wz);       R[4] = 1.f - 2.f * (x2 + z2); R[5] = 2.f * (yz - wx);
+  R[6] = 2.f * (xz - wy);       R[7] = 2.f * (yz + wx);       R[8] = 1.f - 2.f * (x2 + y2);
+}
+
+/* util.cuh:226-233 */
+static void mat3_mul(const float A[9], const float B[9], float C[9]) {
+  for (int i = 0; i < 3; i++)
+    for (int j = 0; j < 3; j++) C[i * 3 + j] = A[i * 3] * B[j] + A[i * 3 + 1] * B[3 + j] + A[i * 3 + 2] * B[6 + j];
+}
+
+/* splat_math.cuh:21-24 */
+static float calc_sigma(float px, float py, sym2 c, float mx, float my) {
+  float dx = px - mx, dy = py - my;
+  return 0.5f * (c.c00 * dx * dx + c.c11 * dy * dy) + c.c01 * dx * dy;
+}
+
+/* splat_math.cuh:27-41: conservative ellipse-vs-rectangle test (nearest edge point in the conic metric). */
+static int tile_hit(float rmin_x, float rmin_y, float rmax_x, float rmax_y, float mx, float my, sym2 conic, float power) {
+  int x_left = mx < rmin_x, x_right = mx > rmax_x, in_x = !(x_left || x_right);
+  int y_above = my < rmin_y, y_below = my > rmax_y, in_y = !(y_above || y_below);
+  if (in_x && in_y) return 1;
+  float corner_x = x_left ? rmin_x : rmax_x, corner_y = y_above ? rmin_y : rmax_y;
+  float width = rmax_x - rmin_x, height = rmax_y - rmin_y;
+  float dxf = x_left ? width : -width, dyf = y_above ? height : -height;
+  float diff_x = mx - corner_x, diff_y = my - corner_y;
+  float tx_raw = (dxf * conic.c00 * diff_x + dxf * conic.c01 * diff_y) / (dxf * conic.c00 * dxf);
+  float ty_raw = (dyf * conic.c01 * diff_x + dyf * conic.c11 * diff_y) / (dyf * conic.c11 * dyf);
+  float tx = in_y ? 0.f : fminf(fmaxf(tx_raw, 0.f), 1.f);
+  float ty = in_x ? 0.f : fminf(fmaxf(ty_raw, 0.f), 1.f);
+  float px = corner_x + tx * dxf, py = corner_y + ty * dyf;
+  return calc_sigma(px, py, conic, mx, my) <= power;
+}
+
+typedef struct { int min_x, min_y, max_x, max_y; } tilebox;
+
+/* splat_math.cuh:43-53 */
+static tilebox tile_bbox(float mx, float my, float ex, float ey, int tiles_x, int tiles_y) {
+  float tw = (float)RT_W;
+  float cx = mx / tw, cy = my / tw, dx = ex / tw, dy = ey / tw;
+  tilebox b;
+  b.min_x = (int)fminf(fmaxf(cx - dx, 0.f), (float)tiles_x);
+  b.min_y = (int)fminf(fmaxf(cy - dy, 0.f), (float)tiles_y);
+  b.max_x = (int)fminf(fmaxf(cx + dx + 1.f, 0.f), (float)tiles_x);
+  b.max_y = (int)fminf(fmaxf(cy + dy + 1.f, 0.f), (float)tiles_y);
+  return b;
+}
+
+/* splat_math.cuh:122-145: real SH basis (Sloan order) for degree <= 4 into b[0..(deg+1)^2). */
+static void sh_basis_f(int deg, float vx, float vy, float vz, float* b) {
+  b[0] = SH_C0;
+  if (deg < 1) return;
+  const float f0a = 0.4886025f;
+  b[1] = -f0a * vy; b[2] = f0a * vz; b[3] = -f0a * vx;
+  if (deg < 2) return;
+  float z2 = vz * vz, f0b = -1.0925485f * vz, f1a = 0.54627424f;
+  float fc1 = vx * vx - vy * vy, fs1 = 2.f * vx * vy;
+  b[4] = f1a * fs1; b[5] = f0b * vy; b[6] = 0.9461747f * z2 - 0.31539157f; b[7] = f0b * vx; b[8] = f1a * fc1;
+  if (deg < 3) return;
+  float f0c = -2.285229f * z2 + 0.4570458f, f1b = 1.4453057f * vz, f2a = -0.5900436f;
+  float fc2 = vx * fc1 - vy * fs1, fs2 = vx * fs1 + vy * fc1;
+  b[9] = f2a * fs2; b[10] = f1b * fs1; b[11] = f0c * vy; b[12] = vz * (1.8658817f * z2 - 1.119529f);
+  b[13] = f0c * vx; b[14] = f1b * fc1; b[15] = f2a * fc2;
+  if (deg < 4) return;
+  float f0d = vz * (-4.683326f * z2 + 2.0071396f), f1c = 3.3116114f * z2 - 0.47308735f, f2b = -1.7701308f * vz, f3a = 0.62583575f;
+  float fc3 = vx * fc2 - vy * fs2, fs3 = vx * fs2 + vy * fc2;
+  b[16] = f3a * fs3; b[17] = f2b * fs2; b[18] = f1c * fs1; b[19] = f0d * vy;
+  b[20] = 1.9843135f * vz * b[12] - 1.0062306f * b[6];
+  b[21] = f0d * vx; b[22] = f1c * fc1; b[23] = f2b * fc2; b[24] = f3a * fc3;
+}
+
+static int imin(int a, int b) { return a < b ? a : b; }
+
+/* Everything project_one produces that the VJP needs (splat_math.cuh:199-217). */
+typedef struct {
+  float mc[3], s[3], s2_raw[3], comp_floor;
+  float Rq[9], J[6];
+  int clamp_x, clamp_y;
+  sym2 cov, conic;
+  float opac, sig;
+  float mean2d[2];
+  float ex, ey;
+  int ok;
+} proj_t;
+
+/* splat_math.cuh:224-293 with mip = false. rsqrtf of the reference becomes 1/sqrtf (IEEE both sides),
+ * __expf/__logf become the Cephes functions above. */
+static void project_one(const float* po, const float* q, const float* ls, const orc_cam_t* cam, proj_t* r) {
+  r->ok = 0;
+  const float* Rv = cam->R;
+  float mcx = Rv[0] * po[0] + Rv[1] * po[1] + Rv[2] * po[2];
+  float mcy = Rv[3] * po[0] + Rv[4] * po[1] + Rv[5] * po[2];
+  float mcz = Rv[6] * po[0] + Rv[7] * po[1] + Rv[8] * po[2];
+  mcx = mcx + cam->t[0]; mcy = mcy + cam->t[1]; mcz = mcz + cam->t[2];
+  r->mc[0] = mcx; r->mc[1] = mcy; r->mc[2] = mcz;
+  if (!(finitef(mcx) && finitef(mcy) && finitef(mcz) && mcz <= 1e10f)) return;
+  if (!(mcz >= 0.01f)) return;
+  float s2x = orc_expf(2.f * ls[0]), s2y = orc_expf(2.f * ls[1]), s2z = orc_expf(2.f * ls[2]);
+  r->s2_raw[0] = s2x; r->s2_raw[1] = s2y; r->s2_raw[2] = s2z;
+  float f2 = ls[3] * ls[3];
+  float s2fx = s2x + f2, s2fy = s2y + f2, s2fz = s2z + f2;
+  r->s[0] = sqrtf(s2fx); r->s[1] = sqrtf(s2fy); r->s[2] = sqrtf(s2fz);
+  r->comp_floor = ls[3] > 0.f ? sqrtf((s2x * s2y * s2z) / (s2fx * s2fy * s2fz)) : 1.f;
+  if (!(finitef(r->s[0]) && finitef(r->s[1]) && finitef(r->s[2]))) return;
+  float qn2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
+  if (!(qn2 >= 1e-6f && finitef(qn2))) return;
+  if (!finitef(po[3])) return;
+  float inv_qn = 1.f / sqrtf(qn2);
+  float qn[4] = {q[0] * inv_qn, q[1] * inv_qn, q[2] * inv_qn, q[3] * inv_qn};
+  quat_to_mat(qn, r->Rq);
+  float M[9];
+  mat3_mul(Rv, r->Rq, M);
+  for (int i = 0; i < 3; i++) { M[i * 3] *= r->s[0]; M[i * 3 + 1] *= r->s[1]; M[i * 3 + 2] *= r->s[2]; }
+  float inv_z = 1.f / mcz;
+  float rx = mcx * inv_z, ry = mcy * inv_z;
+  float cxr = fminf(fmaxf(rx, cam->lim_neg_x), cam->lim_pos_x), cyr = fminf(fmaxf(ry, cam->lim_neg_y), cam->lim_pos_y);
+  r->clamp_x = !(rx <= cam->lim_pos_x && rx >= cam->lim_neg_x);
+  r->clamp_y = !(ry <= cam->lim_pos_y && ry >= cam->lim_neg_y);
+  float dx = cam->fx * inv_z, dy = cam->fy * inv_z;
+  r->J[0] = dx; r->J[1] = 0.f; r->J[2] = -dx * cxr;
+  r->J[3] = 0.f; r->J[4] = dy; r->J[5] = -dy * cyr;
+  float V[6];
+  for (int i = 0; i < 2; i++)
+    for (int j = 0; j < 3; j++) V[i * 3 + j] = r->J[i * 3] * M[j] + r->J[i * 3 + 1] * M[3 + j] + r->J[i * 3 + 2] * M[6 + j];
+  sym2 raw;
+  raw.c00 = V[0] * V[0] + V[1] * V[1] + V[2] * V[2];
+  raw.c01 = V[0] * V[3] + V[1] * V[4] + V[2] * V[5];
+  raw.c11 = V[3] * V[3] + V[4] * V[4] + V[5] * V[5];
+  float max_abs = fmaxf(fabsf(raw.c00), fmaxf(fabsf(raw.c01), fabsf(raw.c11)));
+  if (max_abs > 1e18f) { float k = 1e18f / max_abs; raw.c00 *= k; raw.c01 *= k; raw.c11 *= k; }
+  sym2 cov = raw;
+  cov.c00 += 0.3f; cov.c11 += 0.3f;
+  r->cov = cov;
+  r->sig = 1.f / (1.f + orc_expf(-po[3]));
+  r->opac = r->sig * 1.f * r->comp_floor;
+  if (!(finitef(cov.c00) && finitef(cov.c01) && finitef(cov.c11))) return;
+  float det = cov.c00 * cov.c11 - cov.c01 * cov.c01;
+  if (!(det > 0.f)) return;
+  float inv_det = 1.f / det;
+  r->conic.c00 = cov.c11 * inv_det; r->conic.c01 = -cov.c01 * inv_det; r->conic.c11 = cov.c00 * inv_det;
+  r->mean2d[0] = cam->fx * rx + cam->cx; r->mean2d[1] = cam->fy * ry + cam->cy;
+  if (!(r->opac >= ALPHA_CUTOFF)) return;
+  float power = orc_logf(r->opac * 255.f);
+  float detc = r->conic.c00 * r->conic.c11 - r->conic.c01 * r->conic.c01;
+  if (!(detc > 0.f)) return;
+  float inv_detc = 1.f / detc;
+  r->ex = sqrtf(2.f * power * r->conic.c11 * inv_detc);
+  r->ey = sqrtf(2.f * power * r->conic.c00 * inv_detc);
+  if (!(r->ex >= 0.f && r->ey >= 0.f)) return;
+  int on_screen = r->mean2d[0] + r->ex > 0.f && r->mean2d[0] - r->ex < (float)cam->W && r->mean2d[1] + r->ey > 0.f &&
+                  r->mean2d[1] - r->ey < (float)cam->H;
+  if (!on_screen) return;
+  r->ok = 1;
+}
+
+int orc_tile_bits(int n_tiles) {
+  int b = 1;
+  while ((1 << b) < n_tiles + 1) b++;
+  return b;
+}
+
+/* project.cu:8-84 (DEG from the model, FEAT none). */
+void orc_project(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int tiles_x, int tiles_y, float* proj0,
+                 float* proj1, float* proj2, float* proj3, uint32_t* tile_count, uint32_t* hit_info) {
+  const int K = (m->degree + 1) * (m->degree + 1);
+  int deg = active_deg < m->degree ? active_deg : m->degree;
+  if (deg < 0) deg = 0;
+  const int Ka = (deg + 1) * (deg + 1);
+  for (int i = 0; i < m->n; i++) {
+    const float* po = m->pos_op + (size_t)i * 4;
+    proj_t pr;
+    project_one(po, m->quat + (size_t)i * 4, m->lscale + (size_t)i * 4, cam, &pr);
+    if (!pr.ok) { tile_count[i] = 0; continue; }
+    float power = orc_logf(pr.opac * 255.f);
+    tilebox bb = tile_bbox(pr.mean2d[0], pr.mean2d[1], pr.ex, pr.ey, tiles_x, tiles_y);
+    uint32_t hits = 0, mask = 0;
+    int bw = bb.max_x - bb.min_x, bh = bb.max_y - bb.min_y;
+    int small = bw * bh <= 32;
+    int bit = 0;
+    for (int ty = bb.min_y; ty < bb.max_y; ty++)
+      for (int tx = bb.min_x; tx < bb.max_x; tx++, bit++) {
+        float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
+        if (tile_hit(rx, ry, rx + RT_W, ry + RT_W, pr.mean2d[0], pr.mean2d[1], pr.conic, power)) {
+          hits++;
+          if (small) mask |= 1u << bit;
+        }
+      }
+    tile_count[i] = hits;
+    hit_info[i * 2] = small ? mask : 0xFFFFFFFFu;
+    hit_info[i * 2 + 1] = (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)bw << 24);
+    /* colour: view direction camera -> splat (project.cu:44-55) */
+    float vx = po[0] - cam->pos[0], vy = po[1] - cam->pos[1], vz = po[2] - cam->pos[2];
+    float vl = sqrtf(vx * vx + vy * vy + vz * vz);
+    float inv = 1.f / fmaxf(vl, 1e-12f);
+    vx = vx * inv; vy = vy * inv; vz = vz * inv;
+    float b[25];
+    sh_basis_f(deg, vx, vy, vz, b);
+    const float* c = m->sh + (size_t)i * K * 3;
+    float cr = c[0] * b[0], cg = c[1] * b[0], cb = c[2] * b[0];
+    for (int k = 1; k < Ka; k++) {
+      cr = cr + c[k * 3] * b[k];
+      cg = cg + c[k * 3 + 1] * b[k];
+      cb = cb + c[k * 3 + 2] * b[k];
+    }
+    cr = cr + 0.5f; cg = cg + 0.5f; cb = cb + 0.5f;
+    cr = finitef(cr) ? fminf(fmaxf(cr, -100.f), 100.f) : 0.f;
+    cg = finitef(cg) ? fminf(fmaxf(cg, -100.f), 100.f) : 0.f;
+    cb = finitef(cb) ? fminf(fmaxf(cb, -100.f), 100.f) : 0.f;
+    float* p0 = proj0 + (size_t)i * 4; float* p1 = proj1 + (size_t)i * 4; float* p2 = proj2 + (size_t)i * 4;
+    p0[0] = pr.mean2d[0]; p0[1] = pr.mean2d[1]; p0[2] = pr.conic.c00; p0[3] = pr.conic.c01;
+    p1[0] = pr.conic.c11; p1[1] = pr.opac; p1[2] = pr.mc[2]; p1[3] = power;
+    p2[0] = cr; p2[1] = cg; p2[2] = cb; p2[3] = 0.f;
+    proj3[(size_t)i * 2] = 0.f; proj3[(size_t)i * 2 + 1] = 0.f;
+  }
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * Binning (binning.cu:10-143).
+ * ---------------------------------------------------------------------------------------------- */
+typedef struct { uint32_t key, idx; } kv_t;
+static int kv_cmp(const void* a, const void* b) {
+  const kv_t* x = (const kv_t*)a; const kv_t* y = (const kv_t*)b;
+  if (x->key != y->key) return x->key < y->key ? -1 : 1;
+  return x->idx < y->idx ? -1 : (x->idx > y->idx);
+}
+
+static uint32_t float_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+uint32_t orc_bin(int n, const uint32_t* tile_count, const uint32_t* hit_info, const float* proj0, const float* proj1,
+                 int tiles_x, int tiles_y, uint32_t cap, uint32_t* order, uint32_t* tile_off, uint32_t* keys_sorted,
+                 uint32_t* vals_sorted, uint32_t* tile_ranges) {
+  const uint32_t n_tiles = (uint32_t)(tiles_x * tiles_y);
+  memset(tile_ranges, 0, sizeof(uint32_t) * 2 * n_tiles);
+  if (n == 0) return 0;
+  /* 1. depth sort: key = z bits for splats with hits, 0xFFFFFFFF otherwise; stable (binning.cu:10-15,116-118).
+   * Sorting on (key, index) is the same total order as a stable sort on key. */
+  kv_t* kv = (kv_t*)malloc(sizeof(kv_t) * (size_t)n);
+  for (int i = 0; i < n; i++) {
+    kv[i].key = tile_count[i] ? float_bits(proj1[(size_t)i * 4 + 2]) : 0xFFFFFFFFu;
+    kv[i].idx = (uint32_t)i;
+  }
+  qsort(kv, (size_t)n, sizeof(kv_t), kv_cmp);
+  for (int r = 0; r < n; r++) order[r] = kv[r].idx;
+  free(kv);
+  /* 2. inclusive scan of counts in depth order (binning.cu:16-19,120-124). */
+  uint32_t run = 0;
+  for (int r = 0; r < n; r++) { run += tile_count[order[r]]; tile_off[r] = run; }
+  const uint32_t M = run;
+  if (M > cap || M == 0) return M;
+  /* 3. emit in depth order (binning.cu:25-93): hit-mask bits in increasing (row-major bbox) order;
+   * big splats re-test the bbox with ex/ey recomputed from proj0/proj1; shortfall gets the sentinel. */
+  uint32_t* keys = (uint32_t*)malloc(sizeof(uint32_t) * M);
+  uint32_t* vals = (uint32_t*)malloc(sizeof(uint32_t) * M);
+  const uint32_t sentinel = n_tiles;
+  for (int r = 0; r < n; r++) {
+    uint32_t i = order[r];
+    uint32_t cnt = tile_count[i];
+    if (!cnt) continue;
+    uint32_t base = tile_off[r] - cnt;
+    uint32_t mask = hit_info[i * 2], info = hit_info[i * 2 + 1];
+    if (mask != 0xFFFFFFFFu) {
+      int min_x = (int)(info & 0xFFFu), min_y = (int)((info >> 12) & 0xFFFu), bw = (int)(info >> 24);
+      uint32_t k = 0;
+      for (int bit = 0; bit < 32 && k < cnt; bit++) {
+        if (!(mask >> bit & 1u)) continue;
+        int tx = min_x + bit % bw, ty = min_y + bit / bw;
+        keys[base + k] = (uint32_t)(ty * tiles_x + tx); vals[base + k] = i; k++;
+      }
+      for (; k < cnt; k++) { keys[base + k] = sentinel; vals[base + k] = i; }
+    } else {
+      const float* a = proj0 + (size_t)i * 4; const float* b = proj1 + (size_t)i * 4;
+      sym2 conic = {a[2], a[3], b[0]};
+      float power = b[3];
+      float detc = conic.c00 * conic.c11 - conic.c01 * conic.c01;
+      float inv_detc = 1.f / detc;
+      float ex = sqrtf(2.f * power * conic.c11 * inv_detc), ey = sqrtf(2.f * power * conic.c00 * inv_detc);
+      tilebox bb = tile_bbox(a[0], a[1], ex, ey, tiles_x, tiles_y);
+      uint32_t written = 0;
+      for (int ty = bb.min_y; ty < bb.max_y && written < cnt; ty++)
+        for (int tx = bb.min_x; tx < bb.max_x && written < cnt; tx++) {
+          float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
+          if (tile_hit(rx, ry, rx + RT_W, ry + RT_W, a[0], a[1], conic, power)) {
+            keys[base + written] = (uint32_t)(ty * tiles_x + tx); vals[base + written] = i; written++;
+          }
+        }
+      for (; written < cnt; written++) { keys[base + written] = sentinel; vals[base + written] = i; }
+    }
+  }
+  /* 4. stable sort by tile id (binning.cu:140-142): counting sort over n_tiles + 1 buckets. */
+  uint32_t* start = (uint32_t*)calloc((size_t)n_tiles + 2, sizeof(uint32_t));
+  for (uint32_t s = 0; s < M; s++) start[keys[s] + 1]++;
+  for (uint32_t t = 0; t <= n_tiles; t++) start[t + 1] += start[t];
+  for (uint32_t s = 0; s < M; s++) {
+    uint32_t p = start[keys[s]]++;
+    keys_sorted[p] = keys[s]; vals_sorted[p] = vals[s];
+  }
+  free(start); free(keys); free(vals);
+  /* 5. per-tile [first, last) (binning.cu:95-105); absent tiles stay (0, 0). */
+  for (uint32_t s = 0; s < M; s++) {
+    uint32_t t = keys_sorted[s];
+    if (t >= n_tiles) continue;
+    if (s == 0 || keys_sorted[s - 1] != t) tile_ranges[t * 2] = s;
+    if (s == M - 1 || keys_sorted[s + 1] != t) tile_ranges[t * 2 + 1] = s + 1;
+  }
+  return M;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * Forward raster (raster_fwd.cu:8-71). Each pixel walks its tile's list front to back; the whole
+ * tile's early exit only skips pixels that are already done, so a per-pixel loop is equivalent.
+ * ---------------------------------------------------------------------------------------------- */
+void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], uint32_t* tile_ranges,
+                    const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
+                    float* out_rgba, float* out_T, uint32_t* last_idx) {
+  for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
+    int tx = tile % tiles_x, ty = tile / tiles_x;
+    uint32_t rx = tile_ranges[tile * 2], ry = tile_ranges[tile * 2 + 1];
+    uint32_t max_last = rx;
+    for (int l = 0; l < RT_W * RT_W; l++) {
+      int px = tx * RT_W + l % RT_W, py = ty * RT_W + l / RT_W;
+      if (!(px < W && py < H)) continue;
+      float pcx = px + 0.5f, pcy = py + 0.5f;
+      float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
+      uint32_t last = rx;
+      for (uint32_t idx = rx; idx < ry; idx++) {
+        uint32_t gid = vals_sorted[idx];
+        const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
+        float dx = pcx - a[0], dy = pcy - a[1];
+        float sigma = 0.5f * (a[2] * dx * dx + c[0] * dy * dy) + a[3] * dx * dy;
+        if (sigma < 0.f || sigma > c[3]) continue;
+        float alpha = fminf(ALPHA_MAX, c[1] * expf(-sigma));
+        float next_T = T * (1.f - alpha);
+        if (next_T <= T_CUTOFF) break;
+        float vis = alpha * T;
+        const float* col = proj2 + (size_t)gid * 4;
+        r += fmaxf(col[0], 0.f) * vis; g += fmaxf(col[1], 0.f) * vis; b += fmaxf(col[2], 0.f) * vis;
+        T = next_T;
+        last = idx + 1;
+      }
+      size_t pix = (size_t)py * W + px;
+      out_rgba[pix * 4] = r + T * bg[0]; out_rgba[pix * 4 + 1] = g + T * bg[1]; out_rgba[pix * 4 + 2] = b + T * bg[2];
+      out_rgba[pix * 4 + 3] = 1.f - T;
+      out_T[pix] = T;
+      last_idx[pix] = last;
+      if (last > max_last) max_last = last;
+    }
+    tile_ranges[tile * 2 + 1] = max_last;
+  }
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * Photometric loss (loss.cu:18-195, 296-303), whole image, double precision.
+ * ---------------------------------------------------------------------------------------------- */
+static void gauss11(double w[11]) {
+  double sum = 0;
+  for (int i = 0; i < 11; i++) { double x = i - 5.0; w[i] = exp(-x * x / (2 * 1.5 * 1.5)); sum += w[i]; }
+  for (int i = 0; i < 11; i++) w[i] /= sum;
+}
+
+/* separable 11-tap blur with zero padding outside the image */
+static void blur_d(int W, int H, const double* w, const double* in, double* tmp, double* out) {
+  for (int y = 0; y < H; y++)
+    for (int x = 0; x < W; x++) {
+      double s = 0;
+      for (int d = -5; d <= 5; d++) { int xx = x + d; if (xx >= 0 && xx < W) s += w[d + 5] * in[(size_t)y * W + xx]; }
+      tmp[(size_t)y * W + x] = s;
+    }
+  for (int y = 0; y < H; y++)
+    for (int x = 0; x < W; x++) {
+      double s = 0;
+      for (int d = -5; d <= 5; d++) { int yy = y + d; if (yy >= 0 && yy < H) s += w[d + 5] * tmp[(size_t)yy * W + x]; }
+      out[(size_t)y * W + x] = s;
+    }
+}
+
+/* loss.cu:58 decodes with a multiply by 1/255; tests/reference.cpp:107 divides by 255. */
+static double gtc(uint32_t packed, int c) { return (double)((packed >> (8 * c)) & 0xffu) * (1.0 / 255.0); }
+static double gtc_div(uint32_t packed, int c) { return (double)((packed >> (8 * c)) & 0xffu) / 255.0; }
+
+double orc_photometric(int W, int H, const float* pred, const uint32_t* gt, const uint8_t* weights,
+                       const orc_loss_params_t* lp, float* v_out) {
+  const size_t P = (size_t)W * H;
+  double w[11];
+  gauss11(w);
+  const double C1 = 0.01 * 0.01, C2 = 0.03 * 0.03;
+  const double norm = (double)lp->scale / (3.0 * (double)W * (double)H);
+  double* buf = (double*)malloc(sizeof(double) * P * 17);
+  double *X = buf, *Y = buf + P, *tmp = buf + 2 * P, *mu1 = buf + 3 * P, *mu2 = buf + 4 * P, *ex2 = buf + 5 * P,
+         *ey2 = buf + 6 * P, *exy = buf + 7 * P, *A = buf + 8 * P, *B = buf + 9 * P, *Bm = buf + 10 * P,
+         *Cc = buf + 11 * P, *Cm = buf + 12 * P, *bA = buf + 13 * P, *bB = buf + 14 * P, *bBm = buf + 15 * P,
+         *bC = buf + 16 * P;
+  double* bCm = (double*)malloc(sizeof(double) * P);
+  double* sq = (double*)malloc(sizeof(double) * P);
+  double loss = 0;
+  for (int ch = 0; ch < 3; ch++) {
+    for (size_t i = 0; i < P; i++) {
+      X[i] = pred[i * 4 + ch];
+      Y[i] = gtc(gt[i], ch) + (lp->composite ? (1.0 - gtc(gt[i], 3)) * lp->bg[ch] : 0.0);
+    }
+    blur_d(W, H, w, X, tmp, mu1);
+    blur_d(W, H, w, Y, tmp, mu2);
+    for (size_t i = 0; i < P; i++) sq[i] = X[i] * X[i];
+    blur_d(W, H, w, sq, tmp, ex2);
+    for (size_t i = 0; i < P; i++) sq[i] = Y[i] * Y[i];
+    blur_d(W, H, w, sq, tmp, ey2);
+    for (size_t i = 0; i < P; i++) sq[i] = X[i] * Y[i];
+    blur_d(W, H, w, sq, tmp, exy);
+    for (size_t i = 0; i < P; i++) {
+      double wp = weights ? weights[i] / 255.0 : 1.0;
+      double M = wp * (lp->mask ? gtc(gt[i], 3) : 1.0) * norm;
+      double m1 = mu1[i], m2 = mu2[i];
+      double s1_raw = ex2[i] - m1 * m1, s2_raw = ey2[i] - m2 * m2;
+      double s1 = s1_raw > 0 ? s1_raw : 0, s2 = s2_raw > 0 ? s2_raw : 0, s12 = exy[i] - m1 * m2;
+      double A1 = 2 * m1 * m2 + C1, A2 = 2 * s12 + C2, B1 = m1 * m1 + m2 * m2 + C1, B2 = s1 + s2 + C2;
+      double raw = (A1 * A2) / (B1 * B2);
+      double ssim = raw < -1 ? -1 : (raw > 1 ? 1 : raw);
+      loss += M * (lp->l1_w * fabs(X[i] - Y[i]) + lp->ssim_w * ssim);
+      A[i] = B[i] = Bm[i] = Cc[i] = Cm[i] = 0;
+      if (raw > -1 && raw < 1) { /* loss.cu:165-172 */
+        double k = M * lp->ssim_w;
+        double inv_BB = 1.0 / (B1 * B2);
+        double d_mu1 = 2 * m2 * A2 * inv_BB - 2 * m1 * ssim / B1;
+        double d_s1 = s1_raw > 0 ? -ssim / B2 : 0.0;
+        double d_s12 = 2 * A1 * inv_BB;
+        A[i] = k * d_mu1; B[i] = k * d_s1; Bm[i] = B[i] * m1; Cc[i] = k * d_s12; Cm[i] = Cc[i] * m2;
+      }
+    }
+    if (v_out) {
+      blur_d(W, H, w, A, tmp, bA); blur_d(W, H, w, B, tmp, bB); blur_d(W, H, w, Bm, tmp, bBm);
+      blur_d(W, H, w, Cc, tmp, bC); blur_d(W, H, w, Cm, tmp, bCm);
+      for (size_t i = 0; i < P; i++) {
+        double wp = weights ? weights[i] / 255.0 : 1.0;
+        double M = wp * (lp->mask ? gtc(gt[i], 3) : 1.0) * norm;
+        double p = X[i], g = Y[i];
+        double sgn = p > g ? 1.0 : (p < g ? -1.0 : 0.0);
+        double grad = M * lp->l1_w * sgn + bA[i] + 2 * p * bB[i] - 2 * bBm[i] + g * bC[i] - bCm[i];  /* loss.cu:213 */
+        v_out[i * 4 + ch] = (float)(grad * lp->grad_scale);
+      }
+    }
+  }
+  for (size_t i = 0; i < P; i++) { /* alpha lane (loss.cu:215-225); not masked */
+    double va = 0;
+    if (lp->alpha_lane) {
+      double wp = weights ? weights[i] / 255.0 : 1.0;
+      double da = (double)pred[i * 4 + 3] - gtc(gt[i], 3);
+      double sa = da > 0 ? 1.0 : (da < 0 ? -1.0 : 0.0);
+      double Ma = wp * lp->match_alpha_weight * lp->scale / ((double)W * (double)H);
+      va = Ma * sa * lp->grad_scale;
+      loss += Ma * fabs(da);
+    }
+    if (v_out) v_out[i * 4 + 3] = (float)va;
+  }
+  free(buf); free(bCm); free(sq);
+  return loss;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * Backward raster (raster_bwd.cu:37-139): reverse replay per pixel from the shrunk range end,
+ * T_before = T / (1 - alpha), 13 gradient lanes per fragment.
+ * ---------------------------------------------------------------------------------------------- */
+void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], const uint32_t* tile_ranges,
+                    const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
+                    const float* out_rgba, const float* out_T, const uint32_t* last_idx, const float* v_out,
+                    float inv_gscale, double* v_splat, uint32_t* vis_flag, double* vis_weight) {
+  const float Wf = (float)W, Hf = (float)H;
+  for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
+    int tx = tile % tiles_x, ty = tile / tiles_x;
+    uint32_t rx = tile_ranges[tile * 2], ry = tile_ranges[tile * 2 + 1];
+    if (ry <= rx) continue;
+    for (int l = 0; l < RT_W * RT_W; l++) {
+      int px = tx * RT_W + l % RT_W, py = ty * RT_W + l / RT_W;
+      if (!(px < W && py < H)) continue;
+      size_t pix = (size_t)py * W + px;
+      float pcx = px + 0.5f, pcy = py + 0.5f;
+      float final_a = out_rgba[pix * 4 + 3], T = out_T[pix];
+      uint32_t last = last_idx[pix];
+      const float* vo = v_out + pix * 4;
+      float v_o_w = (vo[3] - (bg[0] * vo[0] + bg[1] * vo[1] + bg[2] * vo[2])) * T;
+      float Sx = 0.f, Sy = 0.f, Sz = 0.f;
+      const float inv_final_a = 1.f / fmaxf(final_a, 1e-5f);
+      for (uint32_t idx = ry; idx-- > rx;) {
+        if (!(idx < last)) continue;
+        uint32_t gid = vals_sorted[idx];
+        const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
+        float dx = pcx - a[0], dy = pcy - a[1];
+        float sigma = 0.5f * (a[2] * dx * dx + c[0] * dy * dy) + a[3] * dx * dy;
+        if (!(sigma >= 0.f && sigma <= c[3])) continue;
+        float g[GRAD_LANES];
+        for (int k = 0; k < GRAD_LANES; k++) g[k] = 0.f;
+        float gauss = expf(-sigma);
+        float alpha = fminf(ALPHA_MAX, c[1] * gauss);
+        float ra = 1.f / (1.f - alpha);
+        float T_before = T * ra;
+        float vis = alpha * T_before;
+        const float* col = proj2 + (size_t)gid * 4;
+        float cr = fmaxf(col[0], 0.f), cg = fmaxf(col[1], 0.f), cb = fmaxf(col[2], 0.f);
+        g[5] = col[0] >= 0.f ? vis * vo[0] : 0.f;
+        g[6] = col[1] >= 0.f ? vis * vo[1] : 0.f;
+        g[7] = col[2] >= 0.f ? vis * vo[2] : 0.f;
+        float v_alpha = (T_before * cr - Sx * ra) * vo[0] + (T_before * cg - Sy * ra) * vo[1] +
+                        (T_before * cb - Sz * ra) * vo[2] + v_o_w * ra;
+        float v_sigma = -alpha * v_alpha;
+        if (c[1] * gauss <= ALPHA_MAX) {
+          g[2] = 0.5f * v_sigma * dx * dx; g[3] = v_sigma * dx * dy; g[4] = 0.5f * v_sigma * dy * dy;
+          g[0] = -v_sigma * (a[2] * dx + a[3] * dy);
+          g[1] = -v_sigma * (a[3] * dx + c[0] * dy);
+          g[8] = v_alpha * gauss;
+          float len = sqrtf(g[0] * Wf * g[0] * Wf + g[1] * Hf * g[1] * Hf);
+          g[9] = len * inv_final_a;
+        }
+        Sx += cr * vis; Sy += cg * vis; Sz += cb * vis;
+        T = T_before;
+        vis_flag[gid] = 1u;
+        vis_weight[gid] += (double)vis;
+        for (int k = 0; k < GRAD_LANES; k++) v_splat[(size_t)gid * GRAD_LANES + k] += (double)g[k] * (double)inv_gscale;
+      }
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * Projection VJP (optim.cu:10-97, 148-253) with the grad_out write (292-296).
+ * ---------------------------------------------------------------------------------------------- */
+static void apply_normalize_vjp(const float q[4], const float g[4], float out[4]) { /* optim.cu:10-21 */
+  float lsq = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
+  float l = sqrtf(lsq);
+  float inv = 1.f / (l * lsq);
+  float qw = q[0], qx = q[1], qy = q[2], qz = q[3];
+  float gw = g[0], gx = g[1], gy = g[2], gz = g[3];
+  float cc0 = -qw * qx, cc1 = -qx * qy, cc2 = -qy * qw, cs0 = -qw * qz, cs1 = -qx * qz, cs2 = -qy * qz;
+  out[0] = ((lsq - qw * qw) * gw + cc0 * gx + cc2 * gy + cs0 * gz) * inv;
+  out[1] = (cc0 * gw + (lsq - qx * qx) * gx + cc1 * gy + cs1 * gz) * inv;
+  out[2] = (cc2 * gw + cc1 * gx + (lsq - qy * qy) * gy + cs2 * gz) * inv;
+  out[3] = (cs0 * gw + cs1 * gx + cs2 * gy + (lsq - qz * qz) * gz) * inv;
+}
+
+static void quat_to_mat_vjp(const float q[4], const float* m, float out[4]) { /* optim.cu:24-33 */
+  float qw = q[0], qx = q[1], qy = q[2], qz = q[3];
+  float v00 = m[0], v01 = m[1], v02 = m[2], v10 = m[3], v11 = m[4], v12 = m[5], v20 = m[6], v21 = m[7], v22 = m[8];
+  float w_grad = qx * (v21 - v12) + qy * (v02 - v20) + qz * (v10 - v01);
+  float x_grad = -2.f * qx * (v11 + v22) + qy * (v10 + v01) + qz * (v20 + v02) + qw * (v21 - v12);
+  float y_grad = qx * (v10 + v01) - 2.f * qy * (v00 + v22) + qz * (v21 + v12) + qw * (v02 - v20);
+  float z_grad = qx * (v20 + v02) + qy * (v21 + v12) - 2.f * qz * (v00 + v11) + qw * (v10 - v01);
+  out[0] = 2.f * w_grad; out[1] = 2.f * x_grad; out[2] = 2.f * y_grad; out[3] = 2.f * z_grad;
+}
+
+static sym2 inverse2x2_vjp(sym2 minv, sym2 v) { /* optim.cu:35-45 */
+  float tmp00 = -minv.c00 * v.c00 + -minv.c01 * v.c01;
+  float tmp01 = -minv.c01 * v.c00 + -minv.c11 * v.c01;
+  float tmp10 = -minv.c00 * v.c01 + -minv.c01 * v.c11;
+  float tmp11 = -minv.c01 * v.c01 + -minv.c11 * v.c11;
+  sym2 r;
+  r.c00 = tmp00 * minv.c00 + tmp10 * minv.c01;
+  r.c01 = tmp01 * minv.c00 + tmp11 * minv.c01;
+  r.c11 = tmp01 * minv.c01 + tmp11 * minv.c11;
+  return r;
+}
+
+/* optim.cu:48-88: d colour / d view direction, c[k][ch] coefficient-major. */
+static void sh_viewdir_vjp(int deg, const float* c, float x, float y, float z, const float vc[3], float g[3]) {
+  float gx = 0.f, gy = 0.f, gz = 0.f;
+#define DOTC(k) (c[(k) * 3] * vc[0] + c[(k) * 3 + 1] * vc[1] + c[(k) * 3 + 2] * vc[2])
+  if (deg >= 1) {
+    const float f0a = 0.4886025f;
+    float s_n1 = DOTC(1), s_z0 = DOTC(2), s_p1 = DOTC(3);
+    gx += -f0a * s_p1; gy += -f0a * s_n1; gz += f0a * s_z0;
+    if (deg >= 2) {
+      const float c2 = -1.0925485f, f1a = 0.54627424f;
+      float s_n2 = DOTC(4), s_n1b = DOTC(5), s_z0b = DOTC(6), s_p1b = DOTC(7), s_p2 = DOTC(8);
+      gx += 2.f * f1a * y * s_n2 + c2 * z * s_p1b + 2.f * f1a * x * s_p2;
+      gy += 2.f * f1a * x * s_n2 + c2 * z * s_n1b - 2.f * f1a * y * s_p2;
+      gz += c2 * y * s_n1b + 2.f * 0.9461747f * z * s_z0b + c2 * x * s_p1b;
+      if (deg >= 3) {
+        float z2 = z * z, x2 = x * x, y2 = y * y;
+        const float f2a = -0.5900436f, c1b = 1.4453057f, c0c = -2.285229f;
+        float f1b = c1b * z, f0c = c0c * z2 + 0.4570458f, f0c_dz = 2.f * c0c * z;
+        float s_n3 = DOTC(9), s_n2c = DOTC(10), s_n1c = DOTC(11), s_z0c = DOTC(12), s_p1c = DOTC(13), s_p2c = DOTC(14), s_p3 = DOTC(15);
+        float d12_z = 3.f * 1.8658817f * z2 - 1.119529f;
+        gx += f2a * 6.f * x * y * s_n3 + 2.f * f1b * y * s_n2c + f0c * s_p1c + 2.f * f1b * x * s_p2c + f2a * 3.f * (x2 - y2) * s_p3;
+        gy += f2a * 3.f * (x2 - y2) * s_n3 + 2.f * f1b * x * s_n2c + f0c * s_n1c + (-2.f) * f1b * y * s_p2c + f2a * (-6.f) * x * y * s_p3;
+        gz += 2.f * c1b * x * y * s_n2c + f0c_dz * y * s_n1c + d12_z * s_z0c + f0c_dz * x * s_p1c + c1b * (x2 - y2) * s_p2c;
+        if (deg >= 4) {
+          float fc1 = x2 - y2, fs1 = 2.f * x * y, fc2 = x * fc1 - y * fs1, fs2 = x * fs1 + y * fc1;
+          float f0d = z * (-4.683326f * z2 + 2.0071396f), f0d_dz = -14.049978f * z2 + 2.0071396f;
+          float f1c = 3.3116114f * z2 - 0.47308735f, f1c_dz = 2.f * 3.3116114f * z;
+          const float f2b_c = -1.7701308f; float f2b = f2b_c * z; const float f3a = 0.62583575f;
+          float p12 = z * (1.8658817f * z2 - 1.119529f), dp12 = 3.f * 1.8658817f * z2 - 1.119529f, dp6 = 2.f * 0.9461747f * z;
+          float dp20 = 1.9843135f * (p12 + z * dp12) - 1.0062306f * dp6;
+          float s_n4 = DOTC(16), s_n3d = DOTC(17), s_n2d = DOTC(18), s_n1d = DOTC(19), s_z0d = DOTC(20), s_p1d = DOTC(21), s_p2d = DOTC(22), s_p3d = DOTC(23), s_p4 = DOTC(24);
+          gx += f3a * 4.f * fs2 * s_n4 + f2b * 3.f * fs1 * s_n3d + f1c * 2.f * y * s_n2d + f0d * s_p1d + f1c * 2.f * x * s_p2d + f2b * 3.f * fc1 * s_p3d + f3a * 4.f * fc2 * s_p4;
+          gy += f3a * 4.f * fc2 * s_n4 + f2b * 3.f * fc1 * s_n3d + f1c * 2.f * x * s_n2d + f0d * s_n1d + f1c * (-2.f) * y * s_p2d + f2b * (-3.f) * fs1 * s_p3d + f3a * (-4.f) * fs2 * s_p4;
+          gz += f2b_c * fs2 * s_n3d + f1c_dz * fs1 * s_n2d + f0d_dz * y * s_n1d + dp20 * s_z0d + f0d_dz * x * s_p1d + f1c_dz * fc1 * s_p2d + f2b_c * fc2 * s_p3d;
+        }
+      }
+    }
+  }
+#undef DOTC
+  g[0] = gx; g[1] = gy; g[2] = gz;
+}
+
+void orc_vjp(const orc_model_t* m, const orc_cam_t* cam, int active_deg, const float* v_splat, const uint32_t* vis_flag,
+             const uint32_t* tile_count, float* grad_out) {
+  const int K = (m->degree + 1) * (m->degree + 1);
+  int deg = active_deg < m->degree ? active_deg : m->degree;
+  if (deg < 0) deg = 0;
+  const int kmax = (deg + 1) * (deg + 1);
+  const int per = 11 + 3 * K;
+  for (int i = 0; i < m->n; i++) {
+    float* o = grad_out + (size_t)i * per;
+    for (int k = 0; k < per; k++) o[k] = 0.f;
+    uint32_t vis = vis_flag[i];
+    int visible = vis != 0u && tile_count[i] != 0u;
+    float g[GRAD_LANES];
+    for (int k = 0; k < GRAD_LANES; k++) g[k] = vis ? v_splat[(size_t)i * GRAD_LANES + k] : 0.f;
+    int any = 0;
+    for (int k = 0; k < GRAD_LANES; k++) if (k != 9 && g[k] != 0.f) any = 1;
+    any = any && visible;
+    for (int k = 0; k < GRAD_LANES; k++) if (!finitef(g[k])) any = 0;
+    if (!any) continue;
+    const float* po = m->pos_op + (size_t)i * 4; const float* q = m->quat + (size_t)i * 4;
+    const float* ls = m->lscale + (size_t)i * 4;
+    proj_t pr;
+    project_one(po, q, ls, cam, &pr);
+    if (!pr.ok) continue;
+    float basis[25];
+    for (int k = 0; k < 25; k++) basis[k] = 0.f;
+    float ux = po[0] - cam->pos[0], uy = po[1] - cam->pos[1], uz = po[2] - cam->pos[2];
+    float ul = sqrtf(ux * ux + uy * uy + uz * uz);
+    float iul = 1.f / ul;
+    float vx = ux * iul, vy = uy * iul, vz = uz * iul;
+    sh_basis_f(deg, vx, vy, vz, basis);
+    for (int k = kmax; k < 25; k++) basis[k] = 0.f;
+    float vc[3] = {g[5], g[6], g[7]};
+    float v_v[3];
+    sh_viewdir_vjp(deg, m->sh + (size_t)i * K * 3, vx, vy, vz, vc, v_v);
+    float vdot = vx * v_v[0] + vy * v_v[1] + vz * v_v[2];
+    float v_mean_sh[3] = {(v_v[0] - vx * vdot) * (1.f / ul), (v_v[1] - vy * vdot) * (1.f / ul), (v_v[2] - vz * vdot) * (1.f / ul)};
+    float v_alpha = g[8];
+    float g_op = v_alpha * 1.f * pr.comp_floor * pr.sig * (1.f - pr.sig);
+    sym2 v_inv = {g[2], 0.5f * g[3], g[4]};
+    sym2 v_cov = inverse2x2_vjp(pr.conic, v_inv);
+    const float* Rv = cam->R;
+    float M[9];
+    for (int r = 0; r < 3; r++) { M[r * 3] = pr.Rq[r * 3] * pr.s[0]; M[r * 3 + 1] = pr.Rq[r * 3 + 1] * pr.s[1]; M[r * 3 + 2] = pr.Rq[r * 3 + 2] * pr.s[2]; }
+    float covar[9];
+    for (int r = 0; r < 3; r++)
+      for (int cc = 0; cc < 3; cc++) covar[r * 3 + cc] = M[r * 3] * M[cc * 3] + M[r * 3 + 1] * M[cc * 3 + 1] + M[r * 3 + 2] * M[cc * 3 + 2];
+    float RvC[9];
+    mat3_mul(Rv, covar, RvC);
+    float cov_c[9];
+    for (int r = 0; r < 3; r++)
+      for (int cc = 0; cc < 3; cc++) cov_c[r * 3 + cc] = RvC[r * 3] * Rv[cc * 3] + RvC[r * 3 + 1] * Rv[cc * 3 + 1] + RvC[r * 3 + 2] * Rv[cc * 3 + 2];
+    float mcx = pr.mc[0], mcy = pr.mc[1], mcz = pr.mc[2];
+    float inv_z = 1.f / mcz, inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z;
+    float v2x = g[0], v2y = g[1];
+    float vcov[2][2] = {{v_cov.c00, v_cov.c01}, {v_cov.c01, v_cov.c11}};
+    float tmp[2][3];
+    for (int r = 0; r < 2; r++)
+      for (int j = 0; j < 3; j++) tmp[r][j] = vcov[r][0] * pr.J[j] + vcov[r][1] * pr.J[3 + j];
+#define ROWDOT(r, cr) (tmp[r][0] * cov_c[(cr) * 3] + tmp[r][1] * cov_c[(cr) * 3 + 1] + tmp[r][2] * cov_c[(cr) * 3 + 2])
+    float vj00 = 2.f * ROWDOT(0, 0), vj11 = 2.f * ROWDOT(1, 1), vj20 = 2.f * ROWDOT(0, 2), vj21 = 2.f * ROWDOT(1, 2);
+#undef ROWDOT
+    float rx = mcx * inv_z, ry = mcy * inv_z;
+    float txc = mcz * fminf(fmaxf(rx, cam->lim_neg_x), cam->lim_pos_x), tyc = mcz * fminf(fmaxf(ry, cam->lim_neg_y), cam->lim_pos_y);
+    float v_mx = cam->fx * inv_z * v2x, v_my = cam->fy * inv_z * v2y;
+    float v_mz = -(cam->fx * mcx * v2x + cam->fy * mcy * v2y) * inv_z2;
+    if (!pr.clamp_x) v_mx += -cam->fx * inv_z2 * vj20; else v_mz += -cam->fx * inv_z3 * vj20 * txc;
+    if (!pr.clamp_y) v_my += -cam->fy * inv_z2 * vj21; else v_mz += -cam->fy * inv_z3 * vj21 * tyc;
+    v_mz += -cam->fx * inv_z2 * vj00 - cam->fy * inv_z2 * vj11 + 2.f * cam->fx * txc * inv_z3 * vj20 + 2.f * cam->fy * tyc * inv_z3 * vj21;
+    float vcc[9];
+    for (int r = 0; r < 3; r++)
+      for (int cc = 0; cc < 3; cc++) {
+        float s = 0.f;
+        for (int a = 0; a < 2; a++)
+          for (int b = 0; b < 2; b++) s += pr.J[a * 3 + r] * vcov[a][b] * pr.J[b * 3 + cc];
+        vcc[r * 3 + cc] = s;
+      }
+    float t1[9];
+    for (int r = 0; r < 3; r++)
+      for (int cc = 0; cc < 3; cc++) t1[r * 3 + cc] = Rv[r] * vcc[cc] + Rv[3 + r] * vcc[3 + cc] + Rv[6 + r] * vcc[6 + cc];
+    float v_covar[9];
+    mat3_mul(t1, Rv, v_covar);
+    float v_M[9];
+    mat3_mul(v_covar, M, v_M);
+    for (int k = 0; k < 9; k++) v_M[k] *= 2.f;
+    /* g_pos = Rv^T v_mean_c + v_mean_sh */
+    float gpx = Rv[0] * v_mx + Rv[3] * v_my + Rv[6] * v_mz;
+    float gpy = Rv[1] * v_mx + Rv[4] * v_my + Rv[7] * v_mz;
+    float gpz = Rv[2] * v_mx + Rv[5] * v_my + Rv[8] * v_mz;
+    gpx = gpx + v_mean_sh[0]; gpy = gpy + v_mean_sh[1]; gpz = gpz + v_mean_sh[2];
+    float f2 = ls[3] * ls[3];
+    float vs0 = pr.Rq[0] * v_M[0] + pr.Rq[3] * v_M[3] + pr.Rq[6] * v_M[6];
+    float vs1 = pr.Rq[1] * v_M[1] + pr.Rq[4] * v_M[4] + pr.Rq[7] * v_M[7];
+    float vs2 = pr.Rq[2] * v_M[2] + pr.Rq[5] * v_M[5] + pr.Rq[8] * v_M[8];
+    float glx = vs0 * pr.s2_raw[0] / pr.s[0] + v_alpha * pr.opac * f2 / (pr.s2_raw[0] + f2);
+    float gly = vs1 * pr.s2_raw[1] / pr.s[1] + v_alpha * pr.opac * f2 / (pr.s2_raw[1] + f2);
+    float glz = vs2 * pr.s2_raw[2] / pr.s[2] + v_alpha * pr.opac * f2 / (pr.s2_raw[2] + f2);
+    float vR[9];
+    for (int r = 0; r < 3; r++) { vR[r * 3] = v_M[r * 3] * pr.s[0]; vR[r * 3 + 1] = v_M[r * 3 + 1] * pr.s[1]; vR[r * 3 + 2] = v_M[r * 3 + 2] * pr.s[2]; }
+    float qn2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
+    float inv_qn = 1.f / sqrtf(qn2);
+    float qn[4] = {q[0] * inv_qn, q[1] * inv_qn, q[2] * inv_qn, q[3] * inv_qn};
+    float qg[4], gq[4];
+    quat_to_mat_vjp(qn, vR, qg);
+    apply_normalize_vjp(q, qg, gq);
+    int ok = finitef(gpx) && finitef(gpy) && finitef(gpz) && finitef(g_op) && finitef(glx) && finitef(gly) && finitef(glz) &&
+             finitef(gq[0] + gq[1] + gq[2] + gq[3]);
+    if (!ok) { gpx = gpy = gpz = g_op = glx = gly = glz = 0.f; gq[0] = gq[1] = gq[2] = gq[3] = 0.f; }
+    o[0] = gpx; o[1] = gpy; o[2] = gpz; o[3] = g_op; o[4] = gq[0]; o[5] = gq[1]; o[6] = gq[2]; o[7] = gq[3];
+    o[8] = glx; o[9] = gly; o[10] = glz;
+    for (int k = 0; k < K; k++) { o[11 + k * 3] = basis[k] * vc[0]; o[12 + k * 3] = basis[k] * vc[1]; o[13 + k * 3] = basis[k] * vc[2]; }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * fp64 brute force (tests/reference.cpp:34-143), photometric + alpha lane.
+ * ---------------------------------------------------------------------------------------------- */
+static void sh_basis_d(int deg, double x, double y, double z, double* b) { /* reference.cpp:16-30 (+ degree 4) */
+  int K = (deg + 1) * (deg + 1);
+  for (int k = 0; k < K; k++) b[k] = 0.0;
+  b[0] = 0.28209479177387814;
+  if (deg >= 1) { b[1] = -0.4886025 * y; b[2] = 0.4886025 * z; b[3] = -0.4886025 * x; }
+  if (deg >= 2) {
+    double z2 = z * z, f0b = -1.0925485 * z, f1a = 0.54627424, fc1 = x * x - y * y, fs1 = 2 * x * y;
+    b[4] = f1a * fs1; b[5] = f0b * y; b[6] = 0.9461747 * z2 - 0.31539157; b[7] = f0b * x; b[8] = f1a * fc1;
+    if (deg >= 3) {
+      double f0c = -2.285229 * z2 + 0.4570458, f1b = 1.4453057 * z, f2a = -0.5900436, fc2 = x * fc1 - y * fs1, fs2 = x * fs1 + y * fc1;
+      b[9] = f2a * fs2; b[10] = f1b * fs1; b[11] = f0c * y; b[12] = z * (1.8658817 * z2 - 1.119529); b[13] = f0c * x;
+      b[14] = f1b * fc1; b[15] = f2a * fc2;
+      if (deg >= 4) { /* extension: splat_math.cuh:136-141 */
+        double f0d = z * (-4.683326 * z2 + 2.0071396), f1c = 3.3116114 * z2 - 0.47308735, f2b = -1.7701308 * z, f3a = 0.62583575;
+        double fc3 = x * fc2 - y * fs2, fs3 = x * fs2 + y * fc2;
+        b[16] = f3a * fs3; b[17] = f2b * fs2; b[18] = f1c * fs1; b[19] = f0d * y; b[20] = 1.9843135 * z * b[12] - 1.0062306 * b[6];
+        b[21] = f0d * x; b[22] = f1c * fc1; b[23] = f2b * fc2; b[24] = f3a * fc3;
+      }
+    }
+  }
+}
+
+typedef struct { int ok; double mx, my, c00, c01, c11, opac, depth, r, g, b; } dproj_t;
+
+static const dproj_t* g_sort_pr;
+static int depth_cmp(const void* a, const void* b) {
+  double da = g_sort_pr[*(const int*)a].depth, db = g_sort_pr[*(const int*)b].depth;
+  if (da < db) return -1;
+  if (da > db) return 1;
+  return *(const int*)a - *(const int*)b;
+}
+
+double orc_ref_loss(int n, int degree, const double* pos, const double* log_scale, const double* quat, const double* opacity,
+                    const double* sh, const double* floor_, const orc_cam_t* cam, int W, int H, const double bg[3],
+                    const uint32_t* gt, const uint8_t* weights, int composite, int mask, int alpha_lane, double l1_w,
+                    double ssim_w, double match_alpha_weight, double scale, int float_exp, double* out_img) {
+  double R[9];
+  for (int i = 0; i < 9; i++) R[i] = cam->R[i];
+  const double fx = cam->fx, fy = cam->fy, cx = cam->cx, cy = cam->cy;
+  double lim_pos_x = (1.15 * W - cx) / fx, lim_neg_x = (-0.15 * W - cx) / fx;
+  double lim_pos_y = (1.15 * H - cy) / fy, lim_neg_y = (-0.15 * H - cy) / fy;
+  const int K = (degree + 1) * (degree + 1);
+  dproj_t* pr = (dproj_t*)calloc((size_t)(n > 0 ? n : 1), sizeof(dproj_t));
+  for (int i = 0; i < n; i++) {
+    double mean[3] = {pos[i * 3], pos[i * 3 + 1], pos[i * 3 + 2]};
+    double mc[3];
+    for (int r = 0; r < 3; r++) mc[r] = R[r * 3] * mean[0] + R[r * 3 + 1] * mean[1] + R[r * 3 + 2] * mean[2] + cam->t[r];
+    if (!(mc[2] >= 0.01)) continue;
+    double s[3], f2 = floor_ ? floor_[i] * floor_[i] : 0.0, comp = 1.0;
+    /* reference.cpp:45,56 pass float parameters to std::exp, which selects the float overload;
+     * float_exp = 1 reproduces that, 0 keeps the exponentials in double (smooth for finite differences). */
+    for (int k = 0; k < 3; k++) s[k] = float_exp ? (double)expf((float)log_scale[i * 3 + k]) : exp(log_scale[i * 3 + k]);
+    if (f2 > 0) { /* extension: Mip-Splatting floor, splat_math.cuh:232-237 */
+      double num = 1, den = 1;
+      for (int k = 0; k < 3; k++) { double s2 = s[k] * s[k]; num *= s2; den *= s2 + f2; s[k] = sqrt(s2 + f2); }
+      comp = sqrt(num / den);
+    }
+    double w = quat[i * 4], x = quat[i * 4 + 1], y = quat[i * 4 + 2], z = quat[i * 4 + 3];
+    double qn = sqrt(w * w + x * x + y * y + z * z);
+    w /= qn; x /= qn; y /= qn; z /= qn;
+    double Rq[9] = {1 - 2 * (y * y + z * z), 2 * (x * y - z * w), 2 * (x * z + y * w),
+                    2 * (x * y + z * w), 1 - 2 * (x * x + z * z), 2 * (y * z - x * w),
+                    2 * (x * z - y * w), 2 * (y * z + x * w), 1 - 2 * (x * x + y * y)};
+    double M[9];
+    for (int r = 0; r < 3; r++)
+      for (int c = 0; c < 3; c++) {
+        double v = 0;
+        for (int k = 0; k < 3; k++) v += R[r * 3 + k] * Rq[k * 3 + c];
+        M[r * 3 + c] = v * s[c];
+      }
+    double inv_z = 1.0 / mc[2], rx = mc[0] * inv_z, ry = mc[1] * inv_z;
+    double cxr = fmin(fmax(rx, lim_neg_x), lim_pos_x), cyr = fmin(fmax(ry, lim_neg_y), lim_pos_y);
+    double J[6] = {fx * inv_z, 0, -fx * inv_z * cxr, 0, fy * inv_z, -fy * inv_z * cyr};
+    double V[6];
+    for (int r = 0; r < 2; r++)
+      for (int c = 0; c < 3; c++) V[r * 3 + c] = J[r * 3] * M[c] + J[r * 3 + 1] * M[3 + c] + J[r * 3 + 2] * M[6 + c];
+    double c00 = V[0] * V[0] + V[1] * V[1] + V[2] * V[2] + 0.3, c01 = V[0] * V[3] + V[1] * V[4] + V[2] * V[5];
+    double c11 = V[3] * V[3] + V[4] * V[4] + V[5] * V[5] + 0.3;
+    double det = c00 * c11 - c01 * c01;
+    if (!(det > 0)) continue;
+    dproj_t q;
+    q.c00 = c11 / det; q.c01 = -c01 / det; q.c11 = c00 / det;
+    q.opac = 1.0 / (1.0 + (float_exp ? (double)expf(-(float)opacity[i]) : exp(-opacity[i]))) * comp;
+    if (!(q.opac >= 1.0 / 255.0)) continue;
+    q.mx = fx * rx + cx; q.my = fy * ry + cy; q.depth = mc[2];
+    double power = log(q.opac * 255.0), detc = q.c00 * q.c11 - q.c01 * q.c01;
+    double ex = sqrt(2 * power * q.c11 / detc), ey = sqrt(2 * power * q.c00 / detc);
+    if (!(q.mx + ex > 0 && q.mx - ex < W && q.my + ey > 0 && q.my - ey < H)) continue;
+    double v[3] = {mean[0] - cam->pos[0], mean[1] - cam->pos[1], mean[2] - cam->pos[2]};
+    double vl = sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+    v[0] /= vl; v[1] /= vl; v[2] /= vl;
+    double b[25];
+    sh_basis_d(degree, v[0], v[1], v[2], b);
+    double col[3] = {0, 0, 0};
+    for (int k = 0; k < K; k++)
+      for (int ch = 0; ch < 3; ch++) col[ch] += b[k] * sh[((size_t)i * K + k) * 3 + ch];
+    q.r = fmin(fmax(col[0] + 0.5, -100.0), 100.0);
+    q.g = fmin(fmax(col[1] + 0.5, -100.0), 100.0);
+    q.b = fmin(fmax(col[2] + 0.5, -100.0), 100.0);
+    q.ok = 1;
+    pr[i] = q;
+  }
+  int* order = (int*)malloc(sizeof(int) * (size_t)(n > 0 ? n : 1));
+  int no = 0;
+  for (int i = 0; i < n; i++) if (pr[i].ok) order[no++] = i;
+  g_sort_pr = pr;
+  qsort(order, (size_t)no, sizeof(int), depth_cmp);
+  const size_t P = (size_t)W * H;
+  float* img = (float*)malloc(sizeof(float) * P * 4);
+  double* imgd = (double*)malloc(sizeof(double) * P * 4);
+  for (int py = 0; py < H; py++)
+    for (int px = 0; px < W; px++) {
+      double T = 1, r = 0, g = 0, b = 0, pcx = px + 0.5, pcy = py + 0.5;
+      for (int oi = 0; oi < no; oi++) {
+        const dproj_t* q = &pr[order[oi]];
+        double dx = pcx - q->mx, dy = pcy - q->my;
+        double sigma = 0.5 * (q->c00 * dx * dx + q->c11 * dy * dy) + q->c01 * dx * dy;
+        double alpha = fmin(0.999, q->opac * exp(-sigma));
+        if (!(sigma >= 0 && alpha >= 1.0 / 255.0)) continue;
+        double nT = T * (1 - alpha);
+        if (nT <= 1e-4) break;
+        double vis = alpha * T;
+        r += fmax(q->r, 0.0) * vis; g += fmax(q->g, 0.0) * vis; b += fmax(q->b, 0.0) * vis;
+        T = nT;
+      }
+      size_t o = (size_t)py * W + px;
+      imgd[o * 4] = r + T * bg[0]; imgd[o * 4 + 1] = g + T * bg[1]; imgd[o * 4 + 2] = b + T * bg[2]; imgd[o * 4 + 3] = 1 - T;
+    }
+  if (out_img) memcpy(out_img, imgd, sizeof(double) * P * 4);
+  /* loss in double over the double image (reference.cpp:105-131) */
+  double w[11];
+  gauss11(w);
+  double* X = (double*)malloc(sizeof(double) * P * 9);
+  double *Y = X + P, *tmp = X + 2 * P, *mu1 = X + 3 * P, *mu2 = X + 4 * P, *ex2 = X + 5 * P, *ey2 = X + 6 * P, *exy = X + 7 * P, *sq = X + 8 * P;
+  const double norm = scale / (3.0 * W * H);
+  double loss = 0;
+  for (int ch = 0; ch < 3; ch++) {
+    for (size_t i = 0; i < P; i++) { X[i] = imgd[i * 4 + ch]; Y[i] = gtc_div(gt[i], ch) + (composite ? (1 - gtc_div(gt[i], 3)) * bg[ch] : 0.0); }
+    blur_d(W, H, w, X, tmp, mu1);
+    blur_d(W, H, w, Y, tmp, mu2);
+    for (size_t i = 0; i < P; i++) sq[i] = X[i] * X[i];
+    blur_d(W, H, w, sq, tmp, ex2);
+    for (size_t i = 0; i < P; i++) sq[i] = Y[i] * Y[i];
+    blur_d(W, H, w, sq, tmp, ey2);
+    for (size_t i = 0; i < P; i++) sq[i] = X[i] * Y[i];
+    blur_d(W, H, w, sq, tmp, exy);
+    for (size_t i = 0; i < P; i++) {
+      double s1 = fmax(0.0, ex2[i] - mu1[i] * mu1[i]), s2 = fmax(0.0, ey2[i] - mu2[i] * mu2[i]), s12 = exy[i] - mu1[i] * mu2[i];
+      double ssim = ((2 * mu1[i] * mu2[i] + 1e-4) * (2 * s12 + 9e-4)) / ((mu1[i] * mu1[i] + mu2[i] * mu2[i] + 1e-4) * (s1 + s2 + 9e-4));
+      ssim = fmin(fmax(ssim, -1.0), 1.0);
+      double wp = weights ? weights[i] / 255.0 : 1.0;
+      double Mw = wp * (mask ? gtc_div(gt[i], 3) : 1.0) * norm;
+      loss += Mw * (l1_w * fabs(X[i] - Y[i]) + ssim_w * ssim);
+    }
+  }
+  if (alpha_lane)
+    for (size_t i = 0; i < P; i++) {
+      double wp = weights ? weights[i] / 255.0 : 1.0;
+      loss += wp * match_alpha_weight * scale / (double)(W * H) * fabs(imgd[i * 4 + 3] - gtc_div(gt[i], 3));
+    }
+  free(X); free(img); free(imgd); free(order); free(pr);
+  return loss;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * Exports of internal pieces so the tests can pin them against closed forms.
+ * ---------------------------------------------------------------------------------------------- */
+void orc_sh_basis_f(int deg, float x, float y, float z, float* out) { sh_basis_f(deg, x, y, z, out); }
+void orc_sh_basis_d(int deg, double x, double y, double z, double* out) { sh_basis_d(deg, x, y, z, out); }
+void orc_quat_to_mat(const float* q, float* R) { quat_to_mat(q, R); }
+int orc_tile_hit(float rmin_x, float rmin_y, float rmax_x, float rmax_y, float mx, float my, float c00, float c01,
+                 float c11, float power) {
+  sym2 c = {c00, c01, c11};
+  return tile_hit(rmin_x, rmin_y, rmax_x, rmax_y, mx, my, c, power);
+}

@@ -1,0 +1,128 @@
+/*
+ * TEST INFRASTRUCTURE ONLY — the checker, never the product.
+ *
+ * CPU restatement of Erant/b2ctrain's differentiable splat rasterizer, used by tests/, by
+ * __graft_entry__.smoke() and by bench.py's cpu_baseline leg. Nothing in b2ctrain_amd/ may link,
+ * load or call it.
+ *
+ * Two independent paths:
+ *   1. fp64 brute force (orc_ref_loss): restates tests/reference.cpp:34-143 — per-pixel compositing
+ *      over every depth-sorted splat, full-image L1 + SSIM + alpha lane. No tiles.
+ *   2. fp32 tiled (orc_project .. orc_vjp): restates the reference GPU pipeline step by step —
+ *      src/gpu/splat_math.cuh, project.cu, binning.cu, raster_fwd.cu, raster_bwd.cu, loss.cu,
+ *      optim.cu (grad_out path). Projection and binning are written so that, compiled with
+ *      -ffp-contract=off, they are bit-exact with the HIP kernels (same operation order, IEEE
+ *      division/sqrt, exp/log from the Cephes single-precision method in both).
+ *
+ * Every function cites the reference lines it follows. Pinning of each function (how it is checked
+ * against something other than itself) is listed in tests/test_oracle_*.py.
+ */
+#ifndef B2C_ORACLE_H
+#define B2C_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* CameraGPU after CameraGPU::from (src/gpu/render.h:8-25). R is world->camera, row major. */
+typedef struct {
+  float R[9];
+  float t[3];
+  float pos[3];
+  float fx, fy, cx, cy;
+  int W, H;
+  float lim_pos_x, lim_pos_y, lim_neg_x, lim_neg_y;
+} orc_cam_t;
+
+/* Splat parameters in the Model's float4 layout (src/model.h:8-23); SH coefficient-major [n][K][3]
+ * (SplatCloud layout, src/ply.h), already fp16-rounded when the model stores bands as fp16. */
+typedef struct {
+  int n, degree;
+  const float* pos_op; /* [n][4] x, y, z, opacity logit */
+  const float* quat;   /* [n][4] w, x, y, z (unnormalised) */
+  const float* lscale; /* [n][4] log sx, log sy, log sz, floor f */
+  const float* sh;     /* [n][K][3] */
+} orc_model_t;
+
+/* LossParams (src/gpu/loss.h:20-30). */
+typedef struct {
+  float l1_w, ssim_w;
+  float bg[3];
+  int composite, mask, alpha_lane;
+  float match_alpha_weight, scale, grad_scale;
+} orc_loss_params_t;
+
+/* ---- deterministic single-precision math (Cephes expf / logf, S. L. Moshier) ---- */
+float orc_expf(float x);
+float orc_logf(float x);
+
+/* ---- fp32 tiled path ---- */
+
+/* RenderCtx::setup tile geometry (src/gpu/render.cu:5-8). */
+int orc_tile_bits(int n_tiles);
+
+/* project.cu:8-84 with splat_math.cuh:224-293 (mip off, no feature lane, no warp / overrides).
+ * Culled splats write only tile_count = 0 (the other outputs are left untouched). */
+void orc_project(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int tiles_x, int tiles_y,
+                 float* proj0, float* proj1, float* proj2, float* proj3,
+                 uint32_t* tile_count, uint32_t* hit_info /* [n][2] */);
+
+/* binning.cu:109-143: depth sort (stable on z bits, culled last), count scan in depth order, emit
+ * in depth order, stable sort by tile id, per-tile ranges. Returns M (number of intersections).
+ * keys/vals are written only when M <= cap. order/tile_off are [n]; tile_ranges is [n_tiles][2]. */
+uint32_t orc_bin(int n, const uint32_t* tile_count, const uint32_t* hit_info, const float* proj0,
+                 const float* proj1, int tiles_x, int tiles_y, uint32_t cap,
+                 uint32_t* order, uint32_t* tile_off, uint32_t* keys_sorted, uint32_t* vals_sorted,
+                 uint32_t* tile_ranges);
+
+/* raster_fwd.cu:8-71 (BWD on, no feature, no hollow). Shrinks tile_ranges[t].y in place.
+ * out_rgba [P][4], out_T [P], last_idx [P]. */
+void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], uint32_t* tile_ranges,
+                    const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
+                    float* out_rgba, float* out_T, uint32_t* last_idx);
+
+/* loss.cu:18-195 restated over the whole image in double precision (zero padding, 11-tap
+ * Gaussian sigma 1.5 normalised, loss.cu:296-303). pred is [P][4] float (rgb + alpha), gt packed
+ * RGBA8, weights u8 or NULL. Returns the loss value; writes v_out [P][4] (scaled by grad_scale)
+ * when v_out is not NULL. */
+double orc_photometric(int W, int H, const float* pred, const uint32_t* gt, const uint8_t* weights,
+                       const orc_loss_params_t* lp, float* v_out);
+
+/* raster_bwd.cu:37-139 (fp32 per-fragment math, double accumulators). v_splat [n][13] and
+ * vis_weight [n] are accumulated (caller zeroes them); vis_flag [n] set to 1 for contributors.
+ * Every accumulated lane is multiplied by inv_gscale (1 for the fp32 kernel's semantics). */
+void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], const uint32_t* tile_ranges,
+                    const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
+                    const float* out_rgba, const float* out_T, const uint32_t* last_idx, const float* v_out,
+                    float inv_gscale, double* v_splat, uint32_t* vis_flag, double* vis_weight);
+
+/* optim.cu:99-253 + grad_out (292-296): projection VJP, fp32. grad_out [n][11 + 3K]. */
+void orc_vjp(const orc_model_t* m, const orc_cam_t* cam, int active_deg, const float* v_splat,
+             const uint32_t* vis_flag, const uint32_t* tile_count, float* grad_out);
+
+/* ---- fp64 brute force (tests/reference.cpp:34-143) ----
+ * Parameters in SplatCloud layout, double: pos [n][3], log_scale [n][3], quat [n][4] (w,x,y,z),
+ * opacity [n], sh [n][K][3]. floor [n] (may be NULL = 0) and degree 4 extend the reference
+ * (which has neither); with floor 0 and degree <= 3 the arithmetic is the reference's.
+ * The camera is used as given (fx/fy/cx/cy at the render size; the clamp limits are recomputed in
+ * double from W/H as reference.cpp:37-38 does). float_exp = 1 evaluates exp(log scale) and
+ * exp(-opacity logit) in single precision, as the reference does (its std::exp receives floats);
+ * 0 keeps them in double. out_img [P][4] (rgb + bg, alpha) may be NULL. */
+double orc_ref_loss(int n, int degree, const double* pos, const double* log_scale, const double* quat,
+                    const double* opacity, const double* sh, const double* floor_, const orc_cam_t* cam,
+                    int W, int H, const double bg[3], const uint32_t* gt, const uint8_t* weights,
+                    int composite, int mask, int alpha_lane, double l1_w, double ssim_w,
+                    double match_alpha_weight, double scale, int float_exp, double* out_img);
+
+/* ---- internal pieces exported for the pinning tests ---- */
+void orc_sh_basis_f(int deg, float x, float y, float z, float* out);      /* splat_math.cuh:122-145 */
+void orc_sh_basis_d(int deg, double x, double y, double z, double* out);  /* reference.cpp:16-30 (+ degree 4) */
+void orc_quat_to_mat(const float* q, float* R);                           /* util.cuh:235-243 */
+int orc_tile_hit(float rmin_x, float rmin_y, float rmax_x, float rmax_y, float mx, float my, float c00, float c01,
+                 float c11, float power);                                 /* splat_math.cuh:27-41 */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,307 @@
+"""TEST INFRASTRUCTURE ONLY: ctypes bindings for the CPU oracle (oracle/liborc.so) and for the
+reference's own fp64 CPU loss compiled from /root/reference (oracle/_ref/libb2c_ref.so).
+
+Used by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg only — never by the product.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liborc.so")
+REF_PATH = os.path.join(HERE, "_ref", "libb2c_ref.so")
+
+RT_W = 8
+GRAD_LANES = 13
+
+
+class OrcCam(C.Structure):
+    _fields_ = [("R", C.c_float * 9), ("t", C.c_float * 3), ("pos", C.c_float * 3), ("fx", C.c_float),
+                ("fy", C.c_float), ("cx", C.c_float), ("cy", C.c_float), ("W", C.c_int), ("H", C.c_int),
+                ("lim_pos_x", C.c_float), ("lim_pos_y", C.c_float), ("lim_neg_x", C.c_float),
+                ("lim_neg_y", C.c_float)]
+
+
+class OrcModel(C.Structure):
+    _fields_ = [("n", C.c_int), ("degree", C.c_int), ("pos_op", C.c_void_p), ("quat", C.c_void_p),
+                ("lscale", C.c_void_p), ("sh", C.c_void_p)]
+
+
+class OrcLoss(C.Structure):
+    _fields_ = [("l1_w", C.c_float), ("ssim_w", C.c_float), ("bg", C.c_float * 3), ("composite", C.c_int),
+                ("mask", C.c_int), ("alpha_lane", C.c_int), ("match_alpha_weight", C.c_float),
+                ("scale", C.c_float), ("grad_scale", C.c_float)]
+
+
+_lib = None
+_ref = None
+
+
+def build(with_ref: bool | None = None) -> None:
+    """Compile liborc.so (and _ref/ when the reference tree is mounted)."""
+    subprocess.check_call(["make", "-s", "-B", "-C", HERE, "all"])
+    if with_ref is None:
+        with_ref = os.path.isdir("/root/reference/tests")
+    if with_ref:
+        subprocess.check_call(["make", "-s", "-B", "-C", HERE, "ref"])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build(with_ref=False)
+        _lib = C.CDLL(LIB_PATH)
+        f = C.c_float
+        p = C.c_void_p
+        _lib.orc_expf.restype = f; _lib.orc_expf.argtypes = [f]
+        _lib.orc_logf.restype = f; _lib.orc_logf.argtypes = [f]
+        _lib.orc_tile_bits.restype = C.c_int; _lib.orc_tile_bits.argtypes = [C.c_int]
+        _lib.orc_project.restype = None
+        _lib.orc_project.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcCam), C.c_int, C.c_int, C.c_int] + [p] * 6
+        _lib.orc_bin.restype = C.c_uint32
+        _lib.orc_bin.argtypes = [C.c_int, p, p, p, p, C.c_int, C.c_int, C.c_uint32, p, p, p, p, p]
+        _lib.orc_raster_fwd.restype = None
+        _lib.orc_raster_fwd.argtypes = [C.c_int] * 4 + [p] * 9
+        _lib.orc_photometric.restype = C.c_double
+        _lib.orc_photometric.argtypes = [C.c_int, C.c_int, p, p, p, C.POINTER(OrcLoss), p]
+        _lib.orc_raster_bwd.restype = None
+        _lib.orc_raster_bwd.argtypes = [C.c_int] * 4 + [p] * 10 + [f, p, p, p]
+        _lib.orc_vjp.restype = None
+        _lib.orc_vjp.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcCam), C.c_int, p, p, p, p]
+        _lib.orc_sh_basis_f.restype = None
+        _lib.orc_sh_basis_f.argtypes = [C.c_int, f, f, f, p]
+        _lib.orc_sh_basis_d.restype = None
+        _lib.orc_sh_basis_d.argtypes = [C.c_int, C.c_double, C.c_double, C.c_double, p]
+        _lib.orc_quat_to_mat.restype = None
+        _lib.orc_quat_to_mat.argtypes = [p, p]
+        _lib.orc_tile_hit.restype = C.c_int
+        _lib.orc_tile_hit.argtypes = [f] * 10
+        _lib.orc_ref_loss.restype = C.c_double
+        _lib.orc_ref_loss.argtypes = [C.c_int, C.c_int] + [p] * 6 + [C.POINTER(OrcCam), C.c_int, C.c_int, p, p, p,
+                                                                    C.c_int, C.c_int, C.c_int] + [C.c_double] * 4 + [
+                                                                    C.c_int, p]
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref_lib():
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise FileNotFoundError(REF_PATH)
+        _ref = C.CDLL(REF_PATH)
+        p = C.c_void_p
+        _ref.ref_reference_loss.restype = C.c_double
+        _ref.ref_reference_loss.argtypes = [C.c_int, C.c_int] + [p] * 5 + [C.c_int, C.c_int, p, p] + [C.c_float] * 4 + [
+            p, p, p, C.c_int, C.c_int, C.c_int] + [C.c_double] * 4
+    return _ref
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def make_cam(camd: dict) -> OrcCam:
+    c = OrcCam()
+    for i in range(9):
+        c.R[i] = float(camd["R"][i])
+    for i in range(3):
+        c.t[i] = float(camd["t"][i])
+        c.pos[i] = float(camd["pos"][i])
+    for k in ("fx", "fy", "cx", "cy", "lim_pos_x", "lim_pos_y", "lim_neg_x", "lim_neg_y"):
+        setattr(c, k, float(camd[k]))
+    c.W, c.H = int(camd["W"]), int(camd["H"])
+    return c
+
+
+class _Model:
+    def __init__(self, scene):
+        self.arrays = [np.ascontiguousarray(a, np.float32) for a in (scene.pos_op, scene.quat, scene.lscale, scene.sh)]
+        self.m = OrcModel(scene.n, scene.degree, *[_ptr(a) for a in self.arrays])
+
+
+def loss_params(scene, grad_scale=1.0, bg=None) -> OrcLoss:
+    lp = OrcLoss()
+    lp.l1_w, lp.ssim_w = scene.l1_w, scene.ssim_w
+    b = scene.bg if bg is None else bg
+    for i in range(3):
+        lp.bg[i] = float(b[i])
+    lp.composite, lp.mask, lp.alpha_lane = int(scene.composite), int(scene.mask), int(scene.alpha_lane)
+    lp.match_alpha_weight, lp.scale, lp.grad_scale = scene.match_alpha_weight, scene.scale, grad_scale
+    return lp
+
+
+def expf(x: float) -> float:
+    return lib().orc_expf(x)
+
+
+def logf(x: float) -> float:
+    return lib().orc_logf(x)
+
+
+def tile_geometry(W, H):
+    tx, ty = (W + RT_W - 1) // RT_W, (H + RT_W - 1) // RT_W
+    return tx, ty, tx * ty, lib().orc_tile_bits(tx * ty)
+
+
+def project(scene, camd, active_deg=None):
+    from b2ctrain_amd.scenes import camera_gpu  # noqa: F401 (camd built by the caller)
+    n = scene.n
+    tx, ty, _, _ = tile_geometry(camd["W"], camd["H"])
+    out = dict(proj0=np.zeros((n, 4), np.float32), proj1=np.zeros((n, 4), np.float32),
+               proj2=np.zeros((n, 4), np.float32), proj3=np.zeros((n, 2), np.float32),
+               tile_count=np.zeros(n, np.uint32), hit_info=np.zeros((n, 2), np.uint32))
+    m = _Model(scene)
+    cam = make_cam(camd)
+    lib().orc_project(C.byref(m.m), C.byref(cam), scene.degree if active_deg is None else active_deg, tx, ty,
+                      *[_ptr(out[k]) for k in ("proj0", "proj1", "proj2", "proj3", "tile_count", "hit_info")])
+    return out
+
+
+def bin_(pr, W, H):
+    n = pr["tile_count"].shape[0]
+    tx, ty, T, _ = tile_geometry(W, H)
+    M = int(pr["tile_count"].astype(np.uint64).sum())
+    out = dict(order=np.zeros(n, np.uint32), tile_off=np.zeros(n, np.uint32), keys_sorted=np.zeros(M, np.uint32),
+               vals_sorted=np.zeros(M, np.uint32), tile_ranges=np.zeros((T, 2), np.uint32))
+    got = lib().orc_bin(n, _ptr(pr["tile_count"]), _ptr(pr["hit_info"]), _ptr(pr["proj0"]), _ptr(pr["proj1"]), tx, ty,
+                        M, *[_ptr(out[k]) for k in ("order", "tile_off", "keys_sorted", "vals_sorted", "tile_ranges")])
+    assert got == M
+    out["M"] = M
+    return out
+
+
+def raster_fwd(pr, bn, W, H, bg):
+    tx, ty, T, _ = tile_geometry(W, H)
+    P = W * H
+    ranges = bn["tile_ranges"].copy()
+    out = dict(out_rgba=np.zeros((P, 4), np.float32), out_T=np.zeros(P, np.float32), last_idx=np.zeros(P, np.uint32))
+    bgv = np.asarray(bg, np.float32)
+    lib().orc_raster_fwd(W, H, tx, ty, _ptr(bgv), _ptr(ranges), _ptr(bn["vals_sorted"]), _ptr(pr["proj0"]),
+                         _ptr(pr["proj1"]), _ptr(pr["proj2"]), *[_ptr(out[k]) for k in ("out_rgba", "out_T", "last_idx")])
+    out["tile_ranges"] = ranges
+    return out
+
+
+def photometric(scene, pred, grad_scale=1.0, bg=None, want_grad=True):
+    lp = loss_params(scene, grad_scale, bg)
+    v_out = np.zeros((scene.W * scene.H, 4), np.float32) if want_grad else None
+    pred = np.ascontiguousarray(pred, np.float32)
+    loss = lib().orc_photometric(scene.W, scene.H, _ptr(pred), _ptr(np.ascontiguousarray(scene.gt, np.uint32)),
+                                 _ptr(scene.weights), C.byref(lp), _ptr(v_out))
+    return loss, v_out
+
+
+def raster_bwd(pr, bn, fw, v_out, W, H, bg, n, inv_gscale=1.0):
+    tx, ty, T, _ = tile_geometry(W, H)
+    v_splat = np.zeros((n, GRAD_LANES), np.float64)
+    vis_flag = np.zeros(n, np.uint32)
+    vis_weight = np.zeros(n, np.float64)
+    bgv = np.asarray(bg, np.float32)
+    lib().orc_raster_bwd(W, H, tx, ty, _ptr(bgv), _ptr(fw["tile_ranges"]), _ptr(bn["vals_sorted"]), _ptr(pr["proj0"]),
+                         _ptr(pr["proj1"]), _ptr(pr["proj2"]), _ptr(fw["out_rgba"]), _ptr(fw["out_T"]),
+                         _ptr(fw["last_idx"]), _ptr(np.ascontiguousarray(v_out, np.float32)), inv_gscale,
+                         _ptr(v_splat), _ptr(vis_flag), _ptr(vis_weight))
+    return v_splat, vis_flag, vis_weight
+
+
+def vjp(scene, camd, v_splat, vis_flag, tile_count, active_deg=None):
+    m = _Model(scene)
+    cam = make_cam(camd)
+    per = 11 + 3 * scene.K
+    g = np.zeros((scene.n, per), np.float32)
+    vs = np.ascontiguousarray(v_splat, np.float32)
+    lib().orc_vjp(C.byref(m.m), C.byref(cam), scene.degree if active_deg is None else active_deg, _ptr(vs),
+                  _ptr(np.ascontiguousarray(vis_flag, np.uint32)), _ptr(np.ascontiguousarray(tile_count, np.uint32)),
+                  _ptr(g))
+    return g
+
+
+def pipeline(scene, camd=None, bg=None, grad_scale=1.0):
+    """Full fp32 tiled oracle step: project -> bin -> forward -> loss -> backward -> VJP."""
+    from b2ctrain_amd.scenes import camera_gpu
+    camd = camera_gpu(scene.cam) if camd is None else camd
+    bg = scene.bg if bg is None else bg
+    W, H = camd["W"], camd["H"]
+    pr = project(scene, camd)
+    bn = bin_(pr, W, H)
+    fw = raster_fwd(pr, bn, W, H, bg)
+    loss, v_out = photometric(scene, fw["out_rgba"], grad_scale=grad_scale, bg=bg)
+    v_splat, vis_flag, vis_weight = raster_bwd(pr, bn, fw, v_out, W, H, bg, scene.n, inv_gscale=1.0 / grad_scale)
+    grads = vjp(scene, camd, v_splat, vis_flag, pr["tile_count"])
+    return dict(proj=pr, bin=bn, fwd=fw, loss=loss, v_out=v_out, v_splat=v_splat, vis_flag=vis_flag,
+                vis_weight=vis_weight, grads=grads)
+
+
+# ---- fp64 brute force -------------------------------------------------------------------------------------
+
+def ref_loss(scene, params=None, camd=None, bg=None, want_img=False, floor=None, float_exp=False):
+    """orc_ref_loss on double parameters. ``params`` = dict(pos, log_scale, quat, opacity, sh) in
+    SplatCloud layout (float64); defaults to the scene's own values."""
+    from b2ctrain_amd.scenes import camera_gpu
+    if params is None:
+        params = scene_params64(scene)
+    camd = camera_gpu(scene.cam) if camd is None else camd
+    cam = make_cam(camd)
+    bg = np.asarray(scene.bg if bg is None else bg, np.float64)
+    img = np.zeros((scene.W * scene.H, 4), np.float64) if want_img else None
+    arrs = [np.ascontiguousarray(params[k], np.float64) for k in ("pos", "log_scale", "quat", "opacity", "sh")]
+    fl = None if floor is None else np.ascontiguousarray(floor, np.float64)
+    loss = lib().orc_ref_loss(scene.n, scene.degree, *[_ptr(a) for a in arrs], _ptr(fl), C.byref(cam), scene.W,
+                              scene.H, _ptr(bg), _ptr(np.ascontiguousarray(scene.gt, np.uint32)), _ptr(scene.weights),
+                              int(scene.composite), int(scene.mask), int(scene.alpha_lane), scene.l1_w, scene.ssim_w,
+                              scene.match_alpha_weight, scene.scale, int(float_exp), _ptr(img))
+    return (loss, img) if want_img else loss
+
+
+def scene_params64(scene):
+    return dict(pos=scene.pos_op[:, :3].astype(np.float64).copy(), log_scale=scene.lscale[:, :3].astype(np.float64).copy(),
+                quat=scene.quat.astype(np.float64).copy(), opacity=scene.pos_op[:, 3].astype(np.float64).copy(),
+                sh=scene.sh.astype(np.float64).reshape(scene.n, -1).copy())
+
+
+def reference_loss(scene, bg=None):
+    """The reference's own tests/reference.cpp:34-143 (compiled from /root/reference), float params."""
+    r = ref_lib()
+    bgv = np.asarray(scene.bg if bg is None else bg, np.float64)
+    cam = scene.cam
+    arrs = [np.ascontiguousarray(a, np.float32) for a in (scene.pos_op[:, :3], scene.lscale[:, :3], scene.quat,
+                                                          scene.pos_op[:, 3], scene.sh.reshape(scene.n, -1))]
+    return r.ref_reference_loss(scene.n, scene.degree, *[_ptr(a) for a in arrs], scene.W, scene.H,
+                                _ptr(np.ascontiguousarray(cam.R, np.float32)), _ptr(np.ascontiguousarray(cam.t, np.float32)),
+                                cam.fx, cam.fy, cam.cx, cam.cy, _ptr(bgv), _ptr(np.ascontiguousarray(scene.gt, np.uint32)),
+                                _ptr(scene.weights), int(scene.composite), int(scene.mask), int(scene.alpha_lane),
+                                scene.l1_w, scene.ssim_w, scene.match_alpha_weight, scene.scale)
+
+
+# ---- internal pieces (for the pinning tests) -----------------------------------------------------------
+
+def sh_basis(deg, v, double=False):
+    K = (deg + 1) ** 2
+    if double:
+        out = np.zeros(25, np.float64)
+        lib().orc_sh_basis_d(deg, float(v[0]), float(v[1]), float(v[2]), _ptr(out))
+    else:
+        out = np.zeros(25, np.float32)
+        lib().orc_sh_basis_f(deg, float(v[0]), float(v[1]), float(v[2]), _ptr(out))
+    return out[:K]
+
+
+def quat_to_mat(q):
+    qa = np.ascontiguousarray(q, np.float32)
+    R = np.zeros(9, np.float32)
+    lib().orc_quat_to_mat(_ptr(qa), _ptr(R))
+    return R.reshape(3, 3)
+
+
+def tile_hit(rect, mean, conic, power) -> bool:
+    return bool(lib().orc_tile_hit(*[float(x) for x in rect], float(mean[0]), float(mean[1]), *[float(c) for c in conic],
+                                   float(power)))

@@ -1,0 +1,37 @@
+// TEST INFRASTRUCTURE ONLY. A C-ABI entry into the reference's own double-precision CPU loss,
+// tests/reference.cpp:34-143, compiled unmodified from /root/reference by oracle/Makefile into
+// oracle/_ref/. Used to pin the restatement in b2c_oracle.c (orc_ref_loss) and to write the
+// fixtures under tests/golden/. This file is this repository's code; no reference source is copied.
+#include <cstdint>
+#include <vector>
+
+#include "reference.h"
+
+extern "C" double ref_reference_loss(int n, int degree, const float* pos, const float* log_scale, const float* quat,
+                                     const float* opacity, const float* sh, int W, int H, const float* R,
+                                     const float* t, float fx, float fy, float cx, float cy, const double* bg,
+                                     const uint32_t* gt, const uint8_t* wts, int composite, int mask, int alpha_lane,
+                                     double l1_w, double ssim_w, double match_alpha_weight, double scale) {
+  b2c::SplatCloud c;
+  c.resize((size_t)n, degree);
+  const int K = c.K();
+  for (int i = 0; i < n * 3; i++) { c.pos[i] = pos[i]; c.log_scale[i] = log_scale[i]; }
+  for (int i = 0; i < n * 4; i++) c.quat[i] = quat[i];
+  for (int i = 0; i < n; i++) c.opacity[i] = opacity[i];
+  for (int i = 0; i < n * K * 3; i++) c.sh[i] = sh[i];
+  std::vector<uint32_t> g(gt, gt + (size_t)W * H);
+  std::vector<uint8_t> w;
+  if (wts) w.assign(wts, wts + (size_t)W * H);
+  RefParams p{};
+  p.W = W; p.H = H;
+  p.cam.width = W; p.cam.height = H;
+  p.cam.fx = fx; p.cam.fy = fy; p.cam.cx = cx; p.cam.cy = cy;
+  for (int i = 0; i < 9; i++) p.cam.R[i] = R[i];
+  for (int i = 0; i < 3; i++) p.cam.t[i] = t[i];
+  p.cam.update_pos();
+  for (int i = 0; i < 3; i++) p.bg[i] = bg[i];
+  p.composite = composite != 0; p.mask = mask != 0; p.alpha_lane = alpha_lane != 0; p.normals = false;
+  p.l1_w = l1_w; p.ssim_w = ssim_w; p.match_alpha_weight = match_alpha_weight; p.scale = scale; p.normal_scale = 0;
+  p.gt = &g; p.gtn = nullptr; p.wts = wts ? &w : nullptr;
+  return reference_loss(c, p);
+}

@@ -1,0 +1,135 @@
+"""Shared GPU-vs-oracle checks (imported by the gpu tests and by smoke-style scripts).
+
+Each stage of the HIP path is compared with the CPU oracle fed the GPU's own upstream outputs, so a
+mismatch names its stage. Tolerances:
+
+* projection outputs, tile counts, hit info, depth order, count scan, tile key/value lists and tile
+  ranges: bit-exact (integer / index work and the fp32 projection both sides evaluate identically);
+* rendered RGBA: max abs error <= 1e-5 vs the fp32 oracle (the GPU uses the hardware exponential);
+* loss value: relative 1e-5; per-pixel gradient: <= 1e-4 of the largest |v_out| (a pixel whose L1 sign
+  flips between fp32 and fp64 evaluation is allowed in at most 1e-4 of the entries);
+* v_splat: <= 2e-3 of each lane's largest |value| (float atomics sum in arbitrary order; mode 1 reduces
+  through fp16 hi/lo MFMA products);
+* parameter gradients from the GPU's own v_splat: <= 1e-4 of each column's largest |value|.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from b2ctrain_amd import _native
+from oracle import oracle as O
+
+
+def emit(msg):
+    print(msg, flush=True)
+
+
+def check_projection(r, scene, camd):
+    pr = O.project(scene, camd)
+    g = {k: r.read(k) for k in ("proj0", "proj1", "proj2", "tile_count", "hit_info")}
+    assert np.array_equal(g["tile_count"], pr["tile_count"]), \
+        f"tile_count differs at {np.flatnonzero(g['tile_count'] != pr['tile_count'])[:10]}"
+    ok = pr["tile_count"] > 0
+    for k in ("proj0", "proj1", "proj2"):
+        a, b = g[k][ok], pr[k][ok]
+        bad = ~((a == b) | (np.isnan(a) & np.isnan(b)))
+        assert not bad.any(), f"{k} differs for splats {np.flatnonzero(ok)[np.flatnonzero(bad.any(1))[:10]]}"
+    assert np.array_equal(g["hit_info"][ok], pr["hit_info"][ok]), "hit_info differs"
+    return {**pr, **{k: g[k] for k in g}}
+
+
+def check_binning(r, pr, W, H):
+    bn = O.bin_(pr, W, H)
+    info = r.info()
+    assert info.num_isect == bn["M"], (info.num_isect, bn["M"])
+    for k in ("order", "tile_off", "keys_sorted", "vals_sorted", "tile_ranges"):
+        g = r.read(k)
+        assert np.array_equal(g, bn[k]), f"{k} differs at {np.flatnonzero((g != bn[k]).reshape(len(g), -1).any(1))[:10]}"
+    return bn
+
+
+def check_forward(r, pr, bn, W, H, bg, tol=1e-5):
+    fw = O.raster_fwd(pr, bn, W, H, bg)
+    rgba = r.read("out_rgba")
+    T = r.read("out_feat")[:, 3]
+    last = r.read("last_idx")
+    err = float(np.abs(rgba - fw["out_rgba"]).max()) if len(rgba) else 0.0
+    assert err <= tol, f"rgba max abs err {err}"
+    mism = float((last != fw["last_idx"]).mean())
+    assert mism <= 1e-4, f"last_idx mismatch fraction {mism}"
+    ranges = r.read("tile_ranges")
+    rm = float((ranges != fw["tile_ranges"]).any(1).mean())
+    assert rm <= 1e-3, f"shrunk tile range mismatch fraction {rm}"
+    return dict(out_rgba=rgba, out_T=T, last_idx=last, tile_ranges=ranges, err=err)
+
+
+def check_loss(r, scene, rgba, grad_scale, bg):
+    loss = r.loss(grad_scale=grad_scale, bg=bg)
+    ref, v_ref = O.photometric(scene, rgba, grad_scale=grad_scale, bg=bg)
+    assert abs(loss - ref) <= 1e-5 * abs(ref) + 1e-9, f"loss {loss} vs oracle {ref}"
+    v = r.read("v_out")
+    scale = float(np.abs(v_ref).max()) + 1e-30
+    bad = np.abs(v - v_ref) > 1e-4 * scale
+    assert bad.mean() <= 1e-4, f"v_out: {bad.sum()} entries off (max {np.abs(v - v_ref).max() / scale:.2e} rel)"
+    return loss, v
+
+
+def check_backward(r, scene, pr, bn, fw, v_out, W, H, bg, mode, grad_scale):
+    r.zero("v_splat")
+    r.zero("vis_flag")
+    r.backward(mode=mode, grad_scale=grad_scale)
+    vs = r.read("v_splat")
+    vf = r.read("vis_flag")
+    inv = 1.0 / grad_scale if mode == 1 else 1.0
+    ref_vs, ref_vf, _ = O.raster_bwd(pr, bn, dict(tile_ranges=fw["tile_ranges"], out_rgba=fw["out_rgba"],
+                                                  out_T=fw["out_T"], last_idx=fw["last_idx"]), v_out, W, H, bg,
+                                     scene.n, inv_gscale=inv)
+    assert np.array_equal(vf, ref_vf), f"vis_flag differs for {np.flatnonzero(vf != ref_vf)[:10]}"
+    lane_scale = np.abs(ref_vs).max(axis=0) + 1e-30
+    err = np.abs(vs - ref_vs) / lane_scale
+    worst = float(err.max()) if err.size else 0.0
+    assert worst <= 2e-3, f"v_splat mode {mode}: worst lane-relative err {worst:.2e} at lane {int(err.max(0).argmax())}"
+    return vs, vf, worst
+
+
+def check_vjp(r, scene, camd, vs, vf, tile_count):
+    r.vjp()
+    g = r.read("grads")
+    ref = O.vjp(scene, camd, vs, vf, tile_count)
+    col = np.abs(ref).max(axis=0) + 1e-30
+    err = float((np.abs(g - ref) / col).max())
+    assert err <= 1e-4, f"grads vs oracle VJP (same v_splat): {err:.2e}"
+    assert not r.read("vis_flag").any(), "vis_flag not cleared by the VJP"
+    assert not r.read("v_splat").any(), "v_splat not cleared by the VJP"
+    return g
+
+
+def full_check(scene, mode=1, bg=None, loss=True, backward=True):
+    """Run every stage on the GPU and check it; returns a dict of GPU outputs."""
+    bg = scene.bg if bg is None else bg
+    W, H = scene.W, scene.H
+    gs = 3.0 * W * H if mode == 1 else 1.0
+    r = _native.Renderer(scene)
+    try:
+        camd = _native.camera_gpu_from(scene.cam)
+        emit(f"  [{scene.name}] projection")
+        r.project(bg=bg)
+        pr = check_projection(r, scene, camd)
+        emit(f"  [{scene.name}] binning")
+        r.bin()
+        bn = check_binning(r, pr, W, H)
+        emit(f"  [{scene.name}] forward (M={bn['M']})")
+        r.raster_fwd(bg=bg)
+        fw = check_forward(r, pr, bn, W, H, bg)
+        out = dict(M=bn["M"], rgba_err=fw["err"])
+        if loss:
+            emit(f"  [{scene.name}] loss")
+            out["loss"], v = check_loss(r, scene, fw["out_rgba"], gs, bg)
+            if backward:
+                emit(f"  [{scene.name}] backward mode {mode}")
+                vs, vf, out["v_splat_err"] = check_backward(r, scene, pr, bn, fw, v, W, H, bg, mode, gs)
+                emit(f"  [{scene.name}] vjp")
+                out["grads"] = check_vjp(r, scene, camd, vs, vf, pr["tile_count"])
+        return out
+    finally:
+        r.close()

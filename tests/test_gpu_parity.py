@@ -1,0 +1,63 @@
+"""GPU parity: every stage of the HIP path against the CPU oracle (tests/gpu_harness.py states the bars),
+on the five BASELINE configurations (reduced splat counts where the CPU oracle would be slow, full size for
+configuration 3) and on the reference's FD-harness scene shape."""
+import numpy as np
+import pytest
+
+from b2ctrain_amd import scenes as S
+from tests.gpu_harness import emit, full_check
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_config1_all_stages(mode):
+    sc = S.config1()
+    sc.bg = (0.25, 0.5, 0.75)
+    emit(f"config1 mode={mode}")
+    out = full_check(sc, mode=mode)
+    assert out["M"] > 1000
+
+
+@pytest.mark.parametrize("seed,masked,degree", [(1234, False, 2), (1235, True, 2), (1236, False, 3), (1237, False, 4)])
+def test_fd_scene_all_stages(seed, masked, degree):
+    sc = S.fd_scene(seed, masked=masked, degree=degree)
+    emit(f"fd scene {sc.name} deg={degree}")
+    full_check(sc, mode=1)
+
+
+def test_config2_subset():
+    sc = S.config2(n=20_000)
+    sc.bg = (0.1, 0.1, 0.1)
+    emit("config2 n=20000")
+    full_check(sc, mode=1)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_config3_subset(masked):
+    sc = S.config3(n=40_000, masked=masked)
+    sc.bg = (0.4, 0.3, 0.2)
+    emit(f"config3 n=40000 masked={masked}")
+    full_check(sc, mode=1)
+
+
+def test_config4_subset_sh4():
+    sc = S.config4(n=30_000)
+    emit("config4 n=30000 SH4")
+    full_check(sc, mode=1)
+
+
+def test_config5_subset_fp16_big_splats():
+    sc = S.config5(n=20_000)
+    emit("config5 n=20000 4K fp16 bands")
+    out = full_check(sc, mode=1, backward=False)
+    assert out["M"] > 0
+
+
+def test_config3_full_size():
+    sc = S.config3()
+    sc.bg = (0.5, 0.5, 0.5)
+    emit("config3 full size (1M splats, 1920x1080)")
+    out = full_check(sc, mode=1)
+    assert out["M"] > 1_000_000
+    assert np.isfinite(out["grads"]).all()
