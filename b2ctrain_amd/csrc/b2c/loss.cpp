@@ -16,6 +16,7 @@ void photometric_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp,
   a.match_alpha_weight = lp.match_alpha_weight; a.scale = lp.scale; a.grad_scale = lp.grad_scale;
   a.v_out = reinterpret_cast<float*>(ctx.v_out.ptr);
   a.loss_accum = ctx.loss_accum.ptr;
+  a.partials = ctx.loss_partials.ptr;
   LAUNCH_CHECK(b2c_hip_photometric(&a, stream));
 }
 

@@ -63,6 +63,7 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   const size_t npx = (size_t)W * H;
   out_rgba.reserve(npx); out_feat.reserve(npx); last_idx.reserve(npx); v_out.reserve(npx);
   loss_accum.reserve(16);
+  loss_partials.reserve(b2c_loss_partials(W, H));
   h_count.reserve(4);
   if (isect_cap == 0) ensure_isect_capacity((size_t)1 << 22, stream);
   const size_t need_tmp = std::max({b2c_radix_sort_temp_bytes((uint32_t)nn), b2c_radix_sort_temp_bytes((uint32_t)isect_cap),

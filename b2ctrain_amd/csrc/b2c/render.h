@@ -85,6 +85,7 @@ struct RenderCtx {
   DevBuf<uint32_t> big_list, big_base, counters;  // counters[0] big splats, [1] intersection total
   DevBuf<uint32_t> depth_alt_k, depth_alt_v, isect_alt_k, isect_alt_v;
   DevBuf<unsigned char> sort_tmp;
+  DevBuf<float> loss_partials;  // per-workgroup loss sums, reduced in a fixed order
 
   void setup(int W, int H, int n_splats, hipStream_t stream);
   void ensure_isect_capacity(size_t m, hipStream_t stream);

@@ -107,6 +107,9 @@ Field ctx_field(b2c_ctx* c, const std::string& name) {
       {"vis_flag", {x.vis_flag.ptr, n * 4}},
       {"loss_accum", {x.loss_accum.ptr, 16 * 4}},
       {"grads", {c->grads.ptr, c->grads.bytes()}},
+      {"big_list", {x.big_list.ptr, n * 4}},
+      {"big_base", {x.big_base.ptr, n * 4}},
+      {"counters", {x.counters.ptr, x.counters.bytes()}},
   };
   auto it = f.find(name);
   if (it == f.end()) throw std::runtime_error("unknown context field: " + name);

@@ -24,6 +24,22 @@ __device__ __forceinline__ float gt_channel(uint32_t packed, int c) {
   return (float)((packed >> (8 * c)) & 0xffu) * (1.f / 255.f);
 }
 
+// Effective target of channel c (loss.cu:85-87), uncontracted: the L1 sign compares the prediction with
+// exactly this fp32 value, so it must round the same way everywhere.
+__device__ __forceinline__ float gt_effective(uint32_t gp, int c, bool composite, float bg_c) {
+#pragma clang fp contract(off)
+  float g = gt_channel(gp, c);
+  if (composite) g = g + (1.f - gt_channel(gp, 3)) * bg_c;
+  return g;
+}
+
+__device__ __forceinline__ void store_partial(const b2c_loss_args& a, float t) {
+  if (a.partials)
+    a.partials[blockIdx.y * gridDim.x + blockIdx.x] = t;
+  else if (t != 0.f)
+    atomicAdd(a.loss_accum, t);
+}
+
 __device__ __forceinline__ float block_sum_256(float v, float* s_red) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -47,6 +63,16 @@ __global__ void __launch_bounds__(TILE_PX) photometric_kernel(b2c_loss_args a, G
   const int W = a.W, H = a.H;
   const float4* pred = reinterpret_cast<const float4*>(a.pred);
   const float bg_c = a.composite ? a.bg[c] : 0.f;
+  // The statistics are accumulated for p - c1 and g - c2, with c1 / c2 the values at the tile centre:
+  // variances and covariances are shift-invariant, and in the gradient 2p*blur(B) - 2*blur(B*mu1) the shift
+  // cancels exactly, so both lose far less to fp32 cancellation than the unshifted form (loss.cu:122-170).
+  float c1, c2;
+  {
+    const int cpix = min(ty0 + TILE_W / 2, H - 1) * W + min(tx0 + TILE_W / 2, W - 1);
+    const float4 pv = pred[cpix];
+    c1 = c == 0 ? pv.x : (c == 1 ? pv.y : pv.z);
+    c2 = gt_effective(a.gt[cpix], c, a.composite, bg_c);
+  }
   float flat_diff = 0.f;
   for (int i = tid; i < IN_W * IN_W; i += TILE_PX) {
     const int ly = i / IN_W, lx = i % IN_W;
@@ -56,12 +82,10 @@ __global__ void __launch_bounds__(TILE_PX) photometric_kernel(b2c_loss_args a, G
       const int pix = gy * W + gx;
       const float4 pv = pred[pix];
       p = c == 0 ? pv.x : (c == 1 ? pv.y : pv.z);
-      const uint32_t gp = a.gt[pix];
-      g = gt_channel(gp, c);
-      if (a.composite) g += (1.f - gt_channel(gp, 3)) * bg_c;
+      g = gt_effective(a.gt[pix], c, a.composite, bg_c);
     }
-    s_in[0][i] = p;
-    s_in[1][i] = g;
+    s_in[0][i] = p - c1;
+    s_in[1][i] = g - c2;
     flat_diff = fmaxf(flat_diff, fabsf(p - g));
   }
   if (c == 0 && a.alpha_lane) {
@@ -85,7 +109,7 @@ __global__ void __launch_bounds__(TILE_PX) photometric_kernel(b2c_loss_args a, G
       if (c == 0) a.v_out[(size_t)pix * 4 + 3] = 0.f;
     }
     const float t = block_sum_256(loss_local, s_red);
-    if (tid == 0 && t != 0.f) atomicAdd(a.loss_accum, t);
+    if (tid == 0) store_partial(a, t);
     return;
   }
   // horizontal blur of the five statistics: rows 0..35, output columns 0..25
@@ -121,17 +145,19 @@ __global__ void __launch_bounds__(TILE_PX) photometric_kernel(b2c_loss_args a, G
       const uint32_t gp = a.gt[pix];
       const float wp = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
       const float M = wp * (a.mask ? gt_channel(gp, 3) : 1.f) * norm;
-      const float mu1 = st[0], mu2 = st[2];
+      const float mu1 = st[0] + c1, mu2 = st[2] + c2;  // st[0], st[2]: shifted means
       const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
-      const float s1_raw = st[1] - mu1_sq, s2_raw = st[3] - mu2_sq;
+      const float s1_raw = st[1] - st[0] * st[0], s2_raw = st[3] - st[2] * st[2];
       const float sigma1_sq = fmaxf(0.f, s1_raw), sigma2_sq = fmaxf(0.f, s2_raw);
-      const float sigma12 = st[4] - mu1 * mu2;
+      const float sigma12 = st[4] - st[0] * st[2];
       const float A1 = 2.f * mu1 * mu2 + C1, A2 = 2.f * sigma12 + C2;
       const float B1 = mu1_sq + mu2_sq + C1, B2 = sigma1_sq + sigma2_sq + C2;
       const float raw = (A1 * A2) / (B1 * B2);
       const float ssim = fminf(fmaxf(raw, -1.f), 1.f);
       if (oy >= HALO && oy < HALO + TILE_W && ox >= HALO && ox < HALO + TILE_W) {
-        const float p = s_in[0][(oy + HALO) * IN_W + ox + HALO], g = s_in[1][(oy + HALO) * IN_W + ox + HALO];
+        const float4 pv = pred[pix];
+        const float p = c == 0 ? pv.x : (c == 1 ? pv.y : pv.z);
+        const float g = gt_effective(gp, c, a.composite, bg_c);
         loss_local += M * (a.l1_w * fabsf(p - g) + a.ssim_w * ssim);
       }
       if (raw > -1.f && raw < 1.f) {
@@ -140,7 +166,7 @@ __global__ void __launch_bounds__(TILE_PX) photometric_kernel(b2c_loss_args a, G
         const float d_mu1 = 2.f * mu2 * A2 * inv_BB - 2.f * mu1 * ssim / B1;
         const float d_s1 = s1_raw > 0.f ? -ssim / B2 : 0.f;
         const float d_s12 = 2.f * A1 * inv_BB;
-        A = k * d_mu1; B = k * d_s1; Bm = B * mu1; Cc = k * d_s12; Cm = Cc * mu2;
+        A = k * d_mu1; B = k * d_s1; Bm = B * st[0]; Cc = k * d_s12; Cm = Cc * st[2];
       }
     }
     float* o = s_v + i * 5;
@@ -177,13 +203,17 @@ __global__ void __launch_bounds__(TILE_PX) photometric_kernel(b2c_loss_args a, G
         for (int k = 0; k < 5; k++) acc[k] += w * v[k];
       }
       const int pix = gy * W + gx;
-      const float p = s_in[0][(ly + 2 * HALO) * IN_W + lx + 2 * HALO], g = s_in[1][(ly + 2 * HALO) * IN_W + lx + 2 * HALO];
+      // shifted values for the SSIM terms, exact ones for the L1 sign
+      const float ps = s_in[0][(ly + 2 * HALO) * IN_W + lx + 2 * HALO], gs = s_in[1][(ly + 2 * HALO) * IN_W + lx + 2 * HALO];
+      const float4 pv = pred[pix];
+      const float p = c == 0 ? pv.x : (c == 1 ? pv.y : pv.z);
       const uint32_t gp = a.gt[pix];
+      const float g = gt_effective(gp, c, a.composite, bg_c);
       const float gt_a = gt_channel(gp, 3);
       const float wp = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
       const float M = wp * (a.mask ? gt_a : 1.f) * norm;
       const float sgn = p > g ? 1.f : (p < g ? -1.f : 0.f);
-      const float grad = M * a.l1_w * sgn + acc[0] + 2.f * p * acc[1] - 2.f * acc[2] + g * acc[3] - acc[4];
+      const float grad = M * a.l1_w * sgn + acc[0] + 2.f * ps * acc[1] - 2.f * acc[2] + gs * acc[3] - acc[4];
       a.v_out[(size_t)pix * 4 + c] = grad * a.grad_scale;
       if (c == 0) {
         float va = 0.f;
@@ -199,7 +229,24 @@ __global__ void __launch_bounds__(TILE_PX) photometric_kernel(b2c_loss_args a, G
     }
   }
   const float t = block_sum_256(loss_local, s_red);
-  if (tid == 0 && t != 0.f) atomicAdd(a.loss_accum, t);
+  if (tid == 0) store_partial(a, t);
+}
+
+// Fixed-order double-precision sum of the per-workgroup partials into loss_accum[0].
+__global__ void __launch_bounds__(1024) reduce_partials_kernel(const float* __restrict__ partials, int count,
+                                                                float* __restrict__ loss_accum) {
+  __shared__ double s_red[16];
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < count; i += 1024) acc += (double)partials[i];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int k = 0; k < 16; k++) t += s_red[k];
+    loss_accum[0] = (float)((double)loss_accum[0] + t);
+  }
 }
 
 __global__ void accumulate_kernel(float* acc) {
@@ -225,7 +272,12 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   for (int i = 0; i < 11; i++) g.w[i] = (float)(w[i] / sum);
   const int tiles_x = (a->W + TILE_W - 1) / TILE_W, tiles_y = (a->H + TILE_W - 1) / TILE_W;
   photometric_kernel<<<dim3(tiles_x * tiles_y, 3), dim3(TILE_PX), 0, stream>>>(*a, g, tiles_x);
+  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, tiles_x * tiles_y * 3, a->loss_accum);
   return (int)hipGetLastError();
+}
+
+extern "C" size_t b2c_loss_partials(int W, int H) {
+  return (size_t)((W + TILE_W - 1) / TILE_W) * ((H + TILE_W - 1) / TILE_W) * 3;
 }
 
 extern "C" int b2c_hip_accumulate_loss(float* loss_accum, hipStream_t stream) {

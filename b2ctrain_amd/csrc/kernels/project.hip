@@ -41,6 +41,9 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
             }
           }
         a.tile_count[i] = hits;
+        // A 32-tile bbox with every tile hit encodes to the same mask as "recompute" (0xFFFFFFFF); the
+        // emit then treats it as a big splat (binning.cu:37,75), so it goes on the big list too.
+        big = mask == 0xFFFFFFFFu;
       }
       reinterpret_cast<uint2*>(a.hit_info)[i] =
           make_uint2(big ? 0xFFFFFFFFu : mask, (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)bw << 24));

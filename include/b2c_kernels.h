@@ -152,7 +152,10 @@ typedef struct b2c_loss_args {
   float match_alpha_weight, scale, grad_scale;
   float* v_out;               /* [P] float4 */
   float* loss_accum;          /* [0] += loss */
+  float* partials;            /* scratch, b2c_loss_partials(W, H) floats: per-workgroup sums, reduced in a
+                                 fixed order in double (deterministic); NULL = float atomics as the reference */
 } b2c_loss_args;
+size_t b2c_loss_partials(int W, int H);
 int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream);
 
 /* accumulate_kernel (loss.cu:317,324): a[2] += a[0] + a[1]; a[3] += 1. */

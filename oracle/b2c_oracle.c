@@ -468,6 +468,14 @@ static void blur_d(int W, int H, const double* w, const double* in, double* tmp,
 
 /* loss.cu:58 decodes with a multiply by 1/255; tests/reference.cpp:107 divides by 255. */
 static double gtc(uint32_t packed, int c) { return (double)((packed >> (8 * c)) & 0xffu) * (1.0 / 255.0); }
+/* loss.cu:58,85-87 in fp32: the effective target the kernel compares the prediction with (the L1 sign and
+ * the alpha-lane sign are decided on these fp32 values). */
+static float gt_chan_f(uint32_t packed, int c) { return (float)((packed >> (8 * c)) & 0xffu) * (1.0f / 255.0f); }
+static float gt_eff_f(uint32_t packed, int c, int composite, float bg) {
+  float g = gt_chan_f(packed, c);
+  if (composite) g = g + (1.f - gt_chan_f(packed, 3)) * bg;
+  return g;
+}
 static double gtc_div(uint32_t packed, int c) { return (double)((packed >> (8 * c)) & 0xffu) / 255.0; }
 
 double orc_photometric(int W, int H, const float* pred, const uint32_t* gt, const uint8_t* weights,
@@ -488,7 +496,7 @@ double orc_photometric(int W, int H, const float* pred, const uint32_t* gt, cons
   for (int ch = 0; ch < 3; ch++) {
     for (size_t i = 0; i < P; i++) {
       X[i] = pred[i * 4 + ch];
-      Y[i] = gtc(gt[i], ch) + (lp->composite ? (1.0 - gtc(gt[i], 3)) * lp->bg[ch] : 0.0);
+      Y[i] = (double)gt_eff_f(gt[i], ch, lp->composite, lp->bg[ch]);
     }
     blur_d(W, H, w, X, tmp, mu1);
     blur_d(W, H, w, Y, tmp, mu2);
@@ -535,7 +543,7 @@ double orc_photometric(int W, int H, const float* pred, const uint32_t* gt, cons
     double va = 0;
     if (lp->alpha_lane) {
       double wp = weights ? weights[i] / 255.0 : 1.0;
-      double da = (double)pred[i * 4 + 3] - gtc(gt[i], 3);
+      double da = (double)(pred[i * 4 + 3] - gt_chan_f(gt[i], 3));
       double sa = da > 0 ? 1.0 : (da < 0 ? -1.0 : 0.0);
       double Ma = wp * lp->match_alpha_weight * lp->scale / ((double)W * (double)H);
       va = Ma * sa * lp->grad_scale;

@@ -106,7 +106,16 @@ def ref_lib():
 
 
 def _ptr(a):
-    return None if a is None else a.ctypes.data_as(C.c_void_p)
+    if a is None:
+        return None
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("oracle arrays must be C-contiguous (a strided view would be read as packed)")
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _in(a, dtype):
+    """Contiguous copy (if needed) of an input array."""
+    return np.ascontiguousarray(a, dtype)
 
 
 def make_cam(camd: dict) -> OrcCam:
@@ -206,10 +215,11 @@ def raster_bwd(pr, bn, fw, v_out, W, H, bg, n, inv_gscale=1.0):
     vis_flag = np.zeros(n, np.uint32)
     vis_weight = np.zeros(n, np.float64)
     bgv = np.asarray(bg, np.float32)
-    lib().orc_raster_bwd(W, H, tx, ty, _ptr(bgv), _ptr(fw["tile_ranges"]), _ptr(bn["vals_sorted"]), _ptr(pr["proj0"]),
-                         _ptr(pr["proj1"]), _ptr(pr["proj2"]), _ptr(fw["out_rgba"]), _ptr(fw["out_T"]),
-                         _ptr(fw["last_idx"]), _ptr(np.ascontiguousarray(v_out, np.float32)), inv_gscale,
-                         _ptr(v_splat), _ptr(vis_flag), _ptr(vis_weight))
+    u32, f32 = np.uint32, np.float32
+    lib().orc_raster_bwd(W, H, tx, ty, _ptr(bgv), _ptr(_in(fw["tile_ranges"], u32)), _ptr(_in(bn["vals_sorted"], u32)),
+                         _ptr(_in(pr["proj0"], f32)), _ptr(_in(pr["proj1"], f32)), _ptr(_in(pr["proj2"], f32)),
+                         _ptr(_in(fw["out_rgba"], f32)), _ptr(_in(fw["out_T"], f32)), _ptr(_in(fw["last_idx"], u32)),
+                         _ptr(_in(v_out, f32)), inv_gscale, _ptr(v_splat), _ptr(vis_flag), _ptr(vis_weight))
     return v_splat, vis_flag, vis_weight
 
 
