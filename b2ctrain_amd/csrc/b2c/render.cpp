@@ -59,7 +59,7 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   counters.reserve(4);
   if (v_splat.count < nn * GRAD_LANES) { v_splat.reserve(nn * GRAD_LANES); v_splat.zero(stream); }
   if (vis_flag.count < nn) { vis_flag.reserve(nn); vis_flag.zero(stream); }
-  tile_ranges.reserve((size_t)n_tiles);
+  tile_ranges.reserve((size_t)n_tiles); tile_end.reserve((size_t)n_tiles + 1);
   const size_t npx = (size_t)W * H;
   out_rgba.reserve(npx); out_feat.reserve(npx); last_idx.reserve(npx); v_out.reserve(npx);
   loss_accum.reserve(16);
@@ -78,6 +78,7 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
   keys.reserve(ncap, false, stream); vals.reserve(ncap, false, stream);
   keys_sorted.reserve(ncap, false, stream); vals_sorted.reserve(ncap, false, stream);
   isect_alt_k.reserve(ncap, false, stream); isect_alt_v.reserve(ncap, false, stream);
+  slot_sorted.reserve(ncap, false, stream); isect_rows.reserve(ncap * 3, false, stream);
   isect_cap = ncap;
   sort_tmp.reserve(b2c_radix_sort_temp_bytes((uint32_t)ncap));
 }
@@ -150,11 +151,15 @@ void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   e.keys = ctx.keys; e.vals = ctx.vals;
   e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
   LAUNCH_CHECK(b2c_hip_emit(&e, stream));
-  LAUNCH_CHECK(b2c_hip_radix_sort_pairs(ctx.keys, ctx.vals, ctx.keys_sorted, ctx.vals_sorted, ctx.isect_alt_k,
+  // The tile pass sorts emit positions rather than splat ids: the permutation tells the backward where
+  // each (tile, splat) gradient row goes (a splat's rows are then contiguous); the splat ids in list order
+  // are gathered from it while the ranges are built.
+  LAUNCH_CHECK(b2c_hip_radix_sort_pairs(ctx.keys, nullptr, ctx.keys_sorted, ctx.slot_sorted, ctx.isect_alt_k,
                                         ctx.isect_alt_v, total, nullptr, 0, ctx.tile_bits, ctx.sort_tmp.ptr,
                                         ctx.sort_tmp.bytes(), stream));
-  LAUNCH_CHECK(b2c_hip_tile_ranges(total, nullptr, ctx.keys_sorted, (uint32_t)ctx.n_tiles,
-                                   reinterpret_cast<uint32_t*>(ctx.tile_ranges.ptr), stream));
+  LAUNCH_CHECK(b2c_hip_tile_ranges(total, nullptr, ctx.keys_sorted, ctx.slot_sorted, ctx.vals, ctx.vals_sorted,
+                                   (uint32_t)ctx.n_tiles, reinterpret_cast<uint32_t*>(ctx.tile_ranges.ptr),
+                                   ctx.tile_end, stream));
 }
 
 void rasterize_forward(RenderCtx& ctx, const RenderParams& p, hipStream_t stream) {
@@ -201,6 +206,11 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.v_splat = ctx.v_splat;
   a.vis_flag = ctx.vis_flag;
   a.vis_weight = m.vis_weight.ptr;
+  a.num_isect = ctx.num_isect;
+  a.slot_sorted = ctx.slot_sorted;
+  a.isect_vals = ctx.vals;
+  a.tile_end = ctx.tile_end;
+  a.isect_rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);
   LAUNCH_CHECK(b2c_hip_raster_bwd(&a, stream));
 }
 

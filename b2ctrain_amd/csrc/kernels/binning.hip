@@ -134,7 +134,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     const uint32_t idx = rb + threadIdx.x;
     const bool valid = idx < n;
     const uint32_t key = valid ? keys_in[idx] : 0u;
-    const uint32_t val = valid ? vals_in[idx] : 0u;
+    const uint32_t val = valid ? (vals_in ? vals_in[idx] : idx) : 0u;  // no values: sort the positions
     const uint32_t d = (key >> shift) & dmask;
 #pragma unroll
     for (int k = 0; k < NWAVES; k++) s_wcnt[k][threadIdx.x] = 0u;
@@ -339,19 +339,37 @@ __global__ void __launch_bounds__(256) emit_big_kernel(b2c_emit_args a, const ui
   }
 }
 
+// Per-tile [first, last) of the sorted keys (binning.cu:95-105); tile_end keeps a copy of `last` that the
+// forward does not shrink, and tile_end[n_tiles] = where the sentinel keys start (m if there are none). With slot_sorted set (an index sort: the sorted emit positions), also gathers
+// the splat ids into list order: vals_sorted[i] = vals[slot_sorted[i]].
 __global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const uint32_t* __restrict__ m_dev,
-                                                          const uint32_t* __restrict__ keys, uint32_t n_tiles,
-                                                          uint2* __restrict__ ranges) {
+                                                          const uint32_t* __restrict__ keys,
+                                                          const uint32_t* __restrict__ slot_sorted,
+                                                          const uint32_t* __restrict__ vals,
+                                                          uint32_t* __restrict__ vals_sorted, uint32_t n_tiles,
+                                                          uint2* __restrict__ ranges, uint32_t* __restrict__ tile_end) {
   const uint32_t m = live_count(cap, m_dev);
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
   if (i >= m) return;
+  if (slot_sorted) vals_sorted[i] = vals[slot_sorted[i]];
   const uint32_t tile = keys[i];
   const uint32_t prev = i == 0 ? 0xFFFFFFFFu : keys[i - 1];
   if (i == 0 || tile != prev) {
     if (tile < n_tiles) ranges[tile].x = i;
-    if (i > 0 && prev < n_tiles) ranges[prev].y = i;
+    if (i > 0 && prev < n_tiles) {
+      ranges[prev].y = i;
+      if (tile_end) tile_end[prev] = i;
+    }
+    // start of the run of sentinel keys (emit shortfall of big splats), which sorts last
+    if (tile_end && tile >= n_tiles && (i == 0 || prev < n_tiles)) tile_end[n_tiles] = i;
   }
-  if (i == m - 1 && tile < n_tiles) ranges[tile].y = m;
+  if (i == m - 1 && tile < n_tiles) {
+    ranges[tile].y = m;
+    if (tile_end) {
+      tile_end[tile] = m;
+      tile_end[n_tiles] = m;  // no sentinel keys
+    }
+  }
 }
 
 inline uint32_t sort_blocks(uint32_t n) { return (n + SORT_TILE - 1) / SORT_TILE; }
@@ -427,11 +445,15 @@ extern "C" int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream) {
   return (int)hipGetLastError();
 }
 
-extern "C" int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_sorted, uint32_t n_tiles,
-                                   uint32_t* ranges, hipStream_t stream) {
+extern "C" int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_sorted,
+                                   const uint32_t* slot_sorted, const uint32_t* vals, uint32_t* vals_sorted,
+                                   uint32_t n_tiles, uint32_t* ranges, uint32_t* tile_end, hipStream_t stream) {
   int e = b2c_hip_fill_u32(ranges, 0u, (size_t)n_tiles * 2, stream);
+  if (!e && tile_end) e = b2c_hip_fill_u32(tile_end, 0u, (size_t)n_tiles + 1, stream);
   if (e || m == 0) return e;
-  tile_ranges_kernel<<<dim3((m + 255) / 256), dim3(256), 0, stream>>>(m, m_dev, keys_sorted, n_tiles,
-                                                                      reinterpret_cast<uint2*>(ranges));
+  if (slot_sorted && (!vals || !vals_sorted)) return (int)hipErrorInvalidValue;
+  tile_ranges_kernel<<<dim3((m + 255) / 256), dim3(256), 0, stream>>>(m, m_dev, keys_sorted, slot_sorted, vals,
+                                                                      vals_sorted, n_tiles,
+                                                                      reinterpret_cast<uint2*>(ranges), tile_end);
   return (int)hipGetLastError();
 }

@@ -151,14 +151,16 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
 }
 
 // ------------------------------------------------------------------------------------------------------
-// mode 1: MFMA reduction
+// mode 1: MFMA reduction into per-(tile, splat) rows, then a per-splat reduce (no atomics)
 // ------------------------------------------------------------------------------------------------------
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int GROUP = 16;  // splats per MFMA group (N)
-constexpr int NTYPES = 4;  // vis, v_alpha * gauss, v_sigma, refine
-// basis rows (M): 0-2 v_rgb, 3-5 v_feat, 6 one, 7 u, 8 v, 9 u^2, 10 uv, 11 v^2, 12-15 zero
+constexpr int BATCH = 64;  // splats staged in LDS per step
+constexpr int G = 8;       // splats per MFMA group
+constexpr int SROW = 68;   // pixel stride of the per-fragment scalar rows (64 + 4: spreads the B reads over banks)
+constexpr int ROW = 12;    // floats per (tile, splat) gradient row: g0..g9, sum of blend weights, 0
+// basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero), 6 one, 7 u, 8 v, 9 u^2, 10 uv, 11 v^2, 12-15 zero
 constexpr int B_ONE = 6, B_U = 7, B_V = 8, B_UU = 9, B_UV = 10, B_VV = 11;
 
 __device__ __forceinline__ float clamp_h(float x) {
@@ -176,178 +178,292 @@ __device__ __forceinline__ void split8(const float* x, half8& hi, half8& lo) {
   }
 }
 
+__device__ __forceinline__ void load8(const float* p, float* x) {
+  const float4 q0 = reinterpret_cast<const float4*>(p)[0], q1 = reinterpret_cast<const float4*>(p)[1];
+  x[0] = q0.x; x[1] = q0.y; x[2] = q0.z; x[3] = q0.w; x[4] = q1.x; x[5] = q1.y; x[6] = q1.z; x[7] = q1.w;
+}
+
+// One wave64 per 8x8 tile, one lane per pixel. The tile's list is replayed back to front in batches of 64
+// splats staged in LDS and groups of 8: for each splat of a group every lane writes three scalars of its
+// fragment (blend weight vis, v_sigma, refine) into LDS; then two 16x16x32 f16 MFMA products per 32 pixels
+// contract them against the per-pixel basis (columns 0-7 vis, 8-15 v_sigma of the group's splats; second
+// product: refine), with hi/lo fp16 splits so ~22 bits of the fp32 inputs survive. The opacity lane needs
+// no product of its own: where a fragment is unclamped v_alpha * gauss = -v_sigma / opacity, and both are
+// zero where it is clamped, so g8 = -(sum v_sigma) / opacity.
 __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args a) {
-  __shared__ float4 s0[64], s1[64], s2[64];
-  __shared__ uint32_t s_gid[64];
-  __shared__ __attribute__((aligned(16))) float sS[NTYPES][GROUP][64];  // per-fragment scalars, [type][splat][pixel]
-  __shared__ float sC[NTYPES][16][GROUP];                              // reduced [type][basis row][splat]
+  __shared__ float4 s_g0[BATCH];   // (mx, my, c00 / 2, c01)
+  __shared__ float4 s_g1[BATCH];   // (c11 / 2, opacity, power, 0)
+  __shared__ float4 s_col[BATCH];  // (max(r, 0), max(g, 0), max(b, 0), sign bits of r, g, b)
+  __shared__ uint32_t s_slot[BATCH];
+  __shared__ __attribute__((aligned(16))) float sS[3 * G][SROW];  // rows 0-7 vis, 8-15 v_sigma, 16-23 refine
+  __shared__ float sC[2][16][17];                                 // products: [which][basis row][column]
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
   const uint2 range = reinterpret_cast<const uint2*>(a.tile_ranges)[tile];
-  if (range.y <= range.x) return;
+  const uint32_t full_end = a.tile_end[tile];
   const int lane = threadIdx.x;
+  float4* rows = reinterpret_cast<float4*>(a.isect_rows);
+  // pairs past the shrunk end never composited: zero rows, so the reduce reads no stale data; the last
+  // tile's wave also clears the rows of sentinel keys (in no tile's list)
+  for (uint32_t i = max(range.y, range.x) + lane; i < full_end; i += 64) {
+    float4* r = rows + (size_t)a.slot_sorted[i] * (ROW / 4);
+    r[0] = r[1] = r[2] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (tile == n_tiles - 1) {
+    for (uint32_t i = a.tile_end[n_tiles] + lane; i < a.num_isect; i += 64) {
+      float4* r = rows + (size_t)a.slot_sorted[i] * (ROW / 4);
+      r[0] = r[1] = r[2] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  if (range.y <= range.x) return;
   const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
   const int lx = lane & 7, ly = lane >> 3;
   const int px = tx * RT_W + lx, py = ty * RT_W + ly;
   const float ox = tx * RT_W + RT_W * 0.5f, oy = ty * RT_W + RT_W * 0.5f;  // tile centre
   const float u = lx + 0.5f - RT_W * 0.5f, v = ly + 0.5f - RT_W * 0.5f;
   PixelState ps = load_pixel(a, px, py, range.x);
-  const float Wf = (float)a.W, Hf = (float)a.H;
+  const float W2 = (float)a.W * (float)a.W, H2 = (float)a.H * (float)a.H;
+  const float r_scale = ps.inv_final_a * R_SCALE;
+  const float cv_x = ps.vo.x, cv_y = ps.vo.y, cv_z = ps.vo.z;
 
-  // Basis operand A (16 rows x 64 px), built once per tile through sS[0] as scratch.
-  {
-    float* bm = &sS[0][0][0];  // [16][64]
-    const float row[16] = {ps.vo.x, ps.vo.y, ps.vo.z, 0.f, 0.f, 0.f, 1.f, u, v, u * u, u * v, v * v, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int m = 0; m < 16; m++) bm[m * 64 + lane] = row[m];
-  }
-  __syncthreads();
+  // Basis operand A (16 rows x 64 px), built once per tile through sS as scratch.
   const int nl = lane & 15, kg = lane >> 4;
   half8 A_hi[2], A_lo[2];
   {
-    const float* bm = &sS[0][0][0];
+    float* bm = &sS[0][0];  // [16][SROW]
+    const float row[16] = {cv_x, cv_y, cv_z, 0.f, 0.f, 0.f, 1.f, u, v, u * u, u * v, v * v, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < 16; m++) bm[m * SROW + lane] = row[m];
+    __syncthreads();
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
       float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; e++) x[e] = bm[nl * 64 + kb * 32 + kg * 8 + e];
+      load8(&bm[nl * SROW + kb * 32 + kg * 8], x);
       split8(x, A_hi[kb], A_lo[kb]);
     }
+    __syncthreads();
   }
-  __syncthreads();
 
-  float Sx = 0.f, Sy = 0.f, Sz = 0.f;
+  float T = ps.T;
+  float Q = -ps.v_o_w;  // sum over composited splats behind of (colour . v_rgb) * vis, minus the v_o_w term
+  const bool live_px = ps.inside;
   const float4* proj0 = reinterpret_cast<const float4*>(a.proj0);
   const float4* proj1 = reinterpret_cast<const float4*>(a.proj1);
   const float4* proj2 = reinterpret_cast<const float4*>(a.proj2);
   for (uint32_t batch_end = range.y; batch_end > range.x;) {
-    const uint32_t batch_start = batch_end > range.x + 64 ? batch_end - 64 : range.x;
+    const uint32_t batch_start = batch_end > range.x + BATCH ? batch_end - BATCH : range.x;
     const int count = (int)(batch_end - batch_start);
     __syncthreads();
     if (lane < count) {
       const uint32_t gid = a.vals_sorted[batch_start + lane];
-      s_gid[lane] = gid;
-      s0[lane] = proj0[gid];
-      s1[lane] = proj1[gid];
-      s2[lane] = proj2[gid];
+      s_slot[lane] = a.slot_sorted[batch_start + lane];
+      const float4 p0 = proj0[gid], p1 = proj1[gid], p2 = proj2[gid];
+      s_g0[lane] = make_float4(p0.x, p0.y, 0.5f * p0.z, p0.w);
+      s_g1[lane] = make_float4(0.5f * p1.x, p1.y, p1.w, 0.f);
+      const uint32_t sgn = (p2.x >= 0.f ? 1u : 0u) | (p2.y >= 0.f ? 2u : 0u) | (p2.z >= 0.f ? 4u : 0u);
+      s_col[lane] = make_float4(fmaxf(p2.x, 0.f), fmaxf(p2.y, 0.f), fmaxf(p2.z, 0.f), __uint_as_float(sgn));
     }
     __syncthreads();
-    const int ngroups = (count + GROUP - 1) / GROUP;
+    const int ngroups = (count + G - 1) / G;
     for (int grp = ngroups - 1; grp >= 0; grp--) {
-      const int gbase = grp * GROUP;
-      const int gcount = min(GROUP, count - gbase);
-      // ---- replay: this pixel's four scalars for each splat of the group (zero when not contributing)
-      for (int j = GROUP - 1; j >= 0; j--) {
-        float s_vis = 0.f, s_va = 0.f, s_vs = 0.f, s_r = 0.f;
-        const int sj = gbase + j;
-        if (j < gcount && ps.inside && batch_start + (uint32_t)sj < ps.last) {
-          const float4 p0 = s0[sj], p1 = s1[sj];
-          const float sigma = calc_sigma(ps.pcx, ps.pcy, p0.z, p0.w, p1.x, p0.x, p0.y);
-          if (sigma >= 0.f && sigma <= p1.w) {
-            const float dx = ps.pcx - p0.x, dy = ps.pcy - p0.y;
-            const float gauss = gauss_weight(sigma);
-            const float alpha = fminf(ALPHA_MAX, p1.y * gauss);
-            const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
-            const float T_before = ps.T * ra;
-            const float vis = alpha * T_before;
-            const float4 col = s2[sj];
-            const float cr = fmaxf(col.x, 0.f), cg = fmaxf(col.y, 0.f), cb = fmaxf(col.z, 0.f);
-            const float v_alpha = (T_before * cr - Sx * ra) * ps.vo.x + (T_before * cg - Sy * ra) * ps.vo.y +
-                                  (T_before * cb - Sz * ra) * ps.vo.z + ps.v_o_w * ra;
-            const float v_sigma = -alpha * v_alpha;
-            if (p1.y * gauss <= ALPHA_MAX) {
-              s_va = v_alpha * gauss;
-              s_vs = v_sigma;
-              const float vx = -v_sigma * (p0.z * dx + p0.w * dy), vy = -v_sigma * (p0.w * dx + p1.x * dy);
-              s_r = __builtin_amdgcn_sqrtf(vx * Wf * vx * Wf + vy * Hf * vy * Hf) * ps.inv_final_a * R_SCALE;
-            }
-            Sx += cr * vis; Sy += cg * vis; Sz += cb * vis;
-            ps.T = T_before;
-            s_vis = vis;
+      const int gbase = grp * G;
+      const int gcount = min(G, count - gbase);
+      // ---- replay: this pixel's three scalars for each splat of the group (zero when not composited)
+#pragma unroll
+      for (int jj = G - 1; jj >= 0; jj--) {
+        float o_vis = 0.f, o_vs = 0.f, o_r = 0.f;
+        if (jj < gcount) {
+          const int sj = gbase + jj;
+          const float4 g0 = s_g0[sj], g1 = s_g1[sj];
+          const float dx = ps.pcx - g0.x, dy = ps.pcy - g0.y;
+          float sigma, t1, t2, c01dx;
+          {
+#pragma clang fp contract(off)
+            // = 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy, bit for bit (halving is exact)
+            t1 = g0.z * dx;
+            t2 = g1.x * dy;
+            c01dx = g0.w * dx;
+            sigma = (t1 * dx + t2 * dy) + c01dx * dy;
+          }
+          const bool in = live_px && (batch_start + (uint32_t)sj < ps.last) && sigma >= 0.f && sigma <= g1.z;
+          if (ballot64(in) != 0) {
+          const float gauss = gauss_weight(sigma);
+          const float araw = g1.y * gauss;
+          const float alpha = fminf(ALPHA_MAX, araw);
+          const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+          const float Tb = T * ra;
+          const float vis = alpha * Tb;
+          const float4 col = s_col[sj];
+          const float cv = col.x * cv_x + col.y * cv_y + col.z * cv_z;
+          const float v_alpha = Tb * cv - ra * Q;
+          const float v_sigma = -alpha * v_alpha;
+          // refine statistic: |d(loss)/d(mean2d)| scaled to pixels, over the final alpha
+          const float gx = 2.f * t1 + g0.w * dy, gy = c01dx + 2.f * t2;
+          const float rf = fabsf(v_sigma) * __builtin_amdgcn_sqrtf(W2 * gx * gx + H2 * gy * gy) * r_scale;
+          const bool unclamped = araw <= ALPHA_MAX;
+          o_vis = in ? vis : 0.f;
+          o_vs = (in && unclamped) ? v_sigma : 0.f;
+          o_r = (in && unclamped) ? rf : 0.f;
+          T = in ? Tb : T;
+          Q = in ? Q + vis * cv : Q;
           }
         }
-        sS[0][j][lane] = s_vis;
-        sS[1][j][lane] = s_va;
-        sS[2][j][lane] = s_vs;
-        sS[3][j][lane] = s_r;
+        sS[jj][lane] = o_vis;
+        sS[G + jj][lane] = o_vs;
+        sS[2 * G + jj][lane] = o_r;
       }
       __syncthreads();
-      // ---- reduction over the 64 pixels on MFMA: D[t] (16 basis rows x 16 splats) = A (16 x 64) * S[t]^T
-      floatx4 acc_hi[NTYPES], acc_lo[NTYPES];
-#pragma unroll
-      for (int t = 0; t < NTYPES; t++) {
-        acc_hi[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-        acc_lo[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-      }
+      // ---- reduction over the 64 pixels on MFMA
+      floatx4 d0_hi = {0.f, 0.f, 0.f, 0.f}, d0_lo = {0.f, 0.f, 0.f, 0.f};
+      floatx4 d1_hi = {0.f, 0.f, 0.f, 0.f}, d1_lo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < 2; kb++) {
+        float x[8];
+        half8 b_hi, b_lo;
+        load8(&sS[nl][kb * 32 + kg * 8], x);
+        split8(x, b_hi, b_lo);
+        d0_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_hi, d0_hi, 0, 0, 0);
+        d0_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_lo, d0_lo, 0, 0, 0);
+        d0_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_lo[kb], b_hi, d0_lo, 0, 0, 0);
+        load8(&sS[2 * G + (nl & (G - 1))][kb * 32 + kg * 8], x);
+        if (nl >= G) {
 #pragma unroll
-        for (int t = 0; t < NTYPES; t++) {
-          const float4* src = reinterpret_cast<const float4*>(&sS[t][nl][kb * 32 + kg * 8]);
-          const float4 q0 = src[0], q1 = src[1];
-          const float x[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-          half8 b_hi, b_lo;
-          split8(x, b_hi, b_lo);
-          acc_hi[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_hi, acc_hi[t], 0, 0, 0);
-          acc_lo[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_lo, acc_lo[t], 0, 0, 0);
-          if (t == 0) acc_lo[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_lo[kb], b_hi, acc_lo[t], 0, 0, 0);
+          for (int e = 0; e < 8; e++) x[e] = 0.f;
         }
+        split8(x, b_hi, b_lo);
+        d1_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_hi, d1_hi, 0, 0, 0);
+        d1_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_lo, d1_lo, 0, 0, 0);
       }
       // D layout: this lane holds rows 4*kg .. 4*kg+3 of column nl
 #pragma unroll
-      for (int t = 0; t < NTYPES; t++)
-#pragma unroll
-        for (int rr = 0; rr < 4; rr++) sC[t][kg * 4 + rr][nl] = acc_hi[t][rr] + acc_lo[t][rr] * (1.f / LO_SCALE);
+      for (int rr = 0; rr < 4; rr++) {
+        sC[0][kg * 4 + rr][nl] = d0_hi[rr] + d0_lo[rr] * (1.f / LO_SCALE);
+        sC[1][kg * 4 + rr][nl] = d1_hi[rr] + d1_lo[rr] * (1.f / LO_SCALE);
+      }
       __syncthreads();
-      // ---- per-splat gradients: lane = (part, splat); 16 splats x 4 parts
-      {
-        const int j = nl, part = kg;
-        const float sum_vis = sC[0][B_ONE][j];
-        if (j < gcount && sum_vis > 0.f) {
-          const int sj = gbase + j;
-          const uint32_t gid = s_gid[sj];
-          float* dst = a.v_splat + (size_t)gid * GRAD_LANES;
-          const float sc = a.inv_gscale;
-          if (part == 0 || part == 1) {
-            const float4 p0 = s0[sj], p1 = s1[sj];
-            const float mx = p0.x - ox, my = p0.y - oy;
-            const float sv = sC[2][B_ONE][j], svu = sC[2][B_U][j], svv = sC[2][B_V][j];
-            if (part == 0) {
-              const float m1u = svu - mx * sv, m1v = svv - my * sv;  // sum v_sigma (u - mx), (v - my)
-              const float g0 = -(p0.z * m1u + p0.w * m1v), g1 = -(p0.w * m1u + p1.x * m1v);
-              if (g0 != 0.f) atomicAdd(dst + 0, g0 * sc);
-              if (g1 != 0.f) atomicAdd(dst + 1, g1 * sc);
-            } else {
-              const float svuu = sC[2][B_UU][j], svuv = sC[2][B_UV][j], svvv = sC[2][B_VV][j];
-              const float m2uu = svuu - 2.f * mx * svu + mx * mx * sv;
-              const float m2uv = svuv - my * svu - mx * svv + mx * my * sv;
-              const float m2vv = svvv - 2.f * my * svv + my * my * sv;
-              const float g2 = 0.5f * m2uu, g3 = m2uv, g4 = 0.5f * m2vv;
-              if (g2 != 0.f) atomicAdd(dst + 2, g2 * sc);
-              if (g3 != 0.f) atomicAdd(dst + 3, g3 * sc);
-              if (g4 != 0.f) atomicAdd(dst + 4, g4 * sc);
-            }
-          } else if (part == 2) {
-            const float4 col = s2[sj];
-            const float g5 = col.x >= 0.f ? sC[0][0][j] : 0.f;
-            const float g6 = col.y >= 0.f ? sC[0][1][j] : 0.f;
-            const float g7 = col.z >= 0.f ? sC[0][2][j] : 0.f;
-            if (g5 != 0.f) atomicAdd(dst + 5, g5 * sc);
-            if (g6 != 0.f) atomicAdd(dst + 6, g6 * sc);
-            if (g7 != 0.f) atomicAdd(dst + 7, g7 * sc);
+      // ---- per-splat rows: lane = (part, splat), three float4 parts per row
+      if (nl < gcount && kg < 3) {
+        const int j = nl, sj = gbase + j;
+        const float sc = a.inv_gscale;
+        float4 out;
+        const float sv = sC[0][B_ONE][G + j];
+        if (kg == 2) {
+          const float op = s_g1[sj].y;
+          out = make_float4(-sv / op * sc, sC[1][B_ONE][j] * (1.f / R_SCALE) * sc, sC[0][B_ONE][j], 0.f);
+        } else {
+          const float4 g0 = s_g0[sj];
+          const float hc11 = s_g1[sj].x;
+          const float mx = g0.x - ox, my = g0.y - oy;
+          const float svu = sC[0][B_U][G + j], svv = sC[0][B_V][G + j];
+          const float svuu = sC[0][B_UU][G + j], svuv = sC[0][B_UV][G + j], svvv = sC[0][B_VV][G + j];
+          const float m2vv = svvv - 2.f * my * svv + my * my * sv;
+          if (kg == 0) {
+            const float m1u = svu - mx * sv, m1v = svv - my * sv;  // sum v_sigma (u - mx), (v - my)
+            const float m2uu = svuu - 2.f * mx * svu + mx * mx * sv;
+            const float m2uv = svuv - my * svu - mx * svv + mx * my * sv;
+            out = make_float4(-(2.f * g0.z * m1u + g0.w * m1v) * sc, -(g0.w * m1u + 2.f * hc11 * m1v) * sc,
+                              0.5f * m2uu * sc, m2uv * sc);
           } else {
-            const float g8 = sC[1][B_ONE][j];
-            const float g9 = sC[3][B_ONE][j] * (1.f / R_SCALE);
-            if (g8 != 0.f) atomicAdd(dst + 8, g8 * sc);
-            if (g9 != 0.f) atomicAdd(dst + 9, g9 * sc);
-            a.vis_flag[gid] = 1u;
-            if (a.vis_weight) atomicAdd(a.vis_weight + gid, sum_vis);
+            const uint32_t sgn = __float_as_uint(s_col[sj].w);
+            out = make_float4(0.5f * m2vv * sc, (sgn & 1u) ? sC[0][0][j] * sc : 0.f,
+                              (sgn & 2u) ? sC[0][1][j] * sc : 0.f, (sgn & 4u) ? sC[0][2][j] * sc : 0.f);
           }
         }
+        rows[(size_t)s_slot[sj] * (ROW / 4) + kg] = out;
       }
     }
     batch_end = batch_start;
+  }
+}
+
+// Per-splat sum of the (tile, splat) rows. In emit order the rows of one splat are one contiguous run and
+// isect_vals[slot] (the emitted splat id) names the run, so this is a segmented reduction over a
+// contiguous array: wave w owns the runs that start in rows [64 w, 64 w + 64) and sums them 64 rows at a
+// time (coalesced 48-byte rows, a segmented Hillis-Steele scan across lanes, a carry for runs longer than
+// one chunk). Each run's last lane adds its sums to v_splat[0..9], vis_weight and vis_flag (the
+// raster_bwd_tc.cu:195-198 updates without atomics). Summation order is fixed: the result is deterministic.
+constexpr int RED_VALS = 11;  // g0..g9 and the blend-weight sum
+
+__global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a) {
+  const uint32_t m = a.num_isect;
+  const int lane = threadIdx.x & 63;
+  const uint32_t lo = (blockIdx.x * 4u + (threadIdx.x >> 6)) * 64u;
+  if (lo >= m) return;
+  const uint32_t* ids = a.isect_vals;
+  const float4* rows = reinterpret_cast<const float4*>(a.isect_rows);
+  const uint32_t NONE = 0xFFFFFFFFu;
+  // the first run head in the window
+  uint32_t s = lo + lane;
+  uint32_t id = s < m ? ids[s] : NONE;
+  uint32_t prev = __shfl_up(id, 1);
+  if (lane == 0) prev = lo == 0 ? NONE : ids[lo - 1];
+  const uint64_t heads = ballot64(s < m && id != prev);
+  if (heads == 0) return;  // a run that started in an earlier window covers this one
+  uint32_t pos = lo + (uint32_t)__builtin_ctzll(heads);
+  const uint32_t win_end = lo + 64u;
+  float carry[RED_VALS];
+#pragma unroll
+  for (int k = 0; k < RED_VALS; k++) carry[k] = 0.f;
+  uint32_t carry_id = NONE;
+  for (;;) {
+    s = pos + lane;
+    id = s < m ? ids[s] : NONE;
+    prev = __shfl_up(id, 1);
+    if (lane == 0) prev = carry_id;  // a continuing run, or a head
+    // rows past the window belong to this wave only while they continue a run that started inside it
+    const uint64_t ext_heads = ballot64(s < m && s >= win_end && id != prev);
+    const uint32_t first_ext = ext_heads ? pos + (uint32_t)__builtin_ctzll(ext_heads) : 0xFFFFFFFFu;
+    const bool active = s < m && s < first_ext;
+    if (!active) id = NONE;
+    float v[RED_VALS];
+    {
+      float4 q0 = make_float4(0.f, 0.f, 0.f, 0.f), q1 = q0, q2 = q0;
+      if (active) {
+        q0 = rows[(size_t)s * 3];
+        q1 = rows[(size_t)s * 3 + 1];
+        q2 = rows[(size_t)s * 3 + 2];
+      }
+      v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w; v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+      v[8] = q2.x; v[9] = q2.y; v[10] = q2.z;
+    }
+    if (lane == 0 && id == carry_id) {
+#pragma unroll
+      for (int k = 0; k < RED_VALS; k++) v[k] += carry[k];
+    }
+    // segmented inclusive scan: a lane adds the partial of lane - o when both lie in the same run
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t oid = __shfl_up(id, o);
+      const bool same = lane >= o && oid == id;
+#pragma unroll
+      for (int k = 0; k < RED_VALS; k++) {
+        const float t = __shfl_up(v[k], o);
+        v[k] = same ? v[k] + t : v[k];
+      }
+    }
+    // does the last run of this chunk continue into the next one?
+    const uint32_t next = pos + 64u;
+    const uint32_t id63 = __shfl(id, 63);
+    const bool continues = id63 != NONE && next < m && next < first_ext && ids[next] == id63;
+    const uint32_t nid = __shfl_down(id, 1);
+    const bool tail = id != NONE && (lane == 63 ? !continues : nid != id);
+    if (tail && v[10] > 0.f) {  // no composited fragment: every lane of the run is zero
+      float* dst = a.v_splat + (size_t)id * GRAD_LANES;
+#pragma unroll
+      for (int k = 0; k < 10; k++) dst[k] += v[k];
+      a.vis_flag[id] = 1u;
+      if (a.vis_weight) a.vis_weight[id] += v[10];
+    }
+    if (!continues) {
+      if (first_ext != 0xFFFFFFFFu || next >= m) break;
+      carry_id = NONE;
+    } else {
+#pragma unroll
+      for (int k = 0; k < RED_VALS; k++) carry[k] = __shfl(v[k], 63);
+      carry_id = id63;
+    }
+    pos = next;
   }
 }
 
@@ -361,9 +477,13 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
   const int n_tiles = a->tiles_x * a->tiles_y;
   if (n_tiles <= 0) return 0;
   const dim3 grid(NUM_XCD * xcd_tiles_per(n_tiles)), block(64);
-  if (a->mode == 0)
+  if (a->mode == 0) {
     raster_bwd_fp32_kernel<<<grid, block, 0, stream>>>(*a);
-  else
+  } else {
+    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals) return (int)hipErrorInvalidValue;
     raster_bwd_mfma_kernel<<<grid, block, 0, stream>>>(*a);
+    const uint32_t windows = (a->num_isect + 63u) / 64u;
+    if (windows) isect_reduce_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
+  }
   return (int)hipGetLastError();
 }

@@ -10,8 +10,13 @@ namespace b2c {
 namespace dev {
 namespace {
 
+// The splat loop is wave-uniform and branch-free per lane: a lane that has terminated (or a fragment that
+// fails the cutoff) contributes alpha = 0, which leaves T, the colour and the last index unchanged; a splat
+// no live lane passes is skipped by the whole wave. Per splat the LDS holds (mx, my, c00/2, c01),
+// (c11/2, opacity, power, 0) and the colour clamped at 0; halving c00 and c11 is exact, so sigma is the
+// reference's 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy bit for bit (uncontracted).
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
-  __shared__ float4 s0[64], s1[64], s2[64];
+  __shared__ float4 s_g0[64], s_g1[64], s_col[64];
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
@@ -26,39 +31,41 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   const float4* proj1 = reinterpret_cast<const float4*>(a.proj1);
   const float4* proj2 = reinterpret_cast<const float4*>(a.proj2);
   float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
-  bool done = !inside;
+  bool live = inside;
   uint32_t last = range.x;
   for (uint32_t start = range.x; start < range.y; start += 64) {
-    if (ballot64(!done) == 0) break;
+    if (ballot64(live) == 0) break;
     const uint32_t remaining = min(64u, range.y - start);
     __syncthreads();
     if ((uint32_t)lane < remaining) {
       const uint32_t gid = a.vals_sorted[start + lane];
-      s0[lane] = proj0[gid];
-      s1[lane] = proj1[gid];
-      s2[lane] = proj2[gid];
+      const float4 p0 = proj0[gid], p1 = proj1[gid], p2 = proj2[gid];
+      s_g0[lane] = make_float4(p0.x, p0.y, 0.5f * p0.z, p0.w);
+      s_g1[lane] = make_float4(0.5f * p1.x, p1.y, p1.w, 0.f);
+      s_col[lane] = make_float4(fmaxf(p2.x, 0.f), fmaxf(p2.y, 0.f), fmaxf(p2.z, 0.f), 0.f);
     }
     __syncthreads();
-    if (!done) {
-      for (uint32_t t = 0; t < remaining; t++) {
-        const float4 p0 = s0[t];
-        const float4 p1 = s1[t];
-        const float sigma = calc_sigma(pcx, pcy, p0.z, p0.w, p1.x, p0.x, p0.y);
-        if (sigma < 0.f || sigma > p1.w) continue;
-        const float alpha = fminf(ALPHA_MAX, p1.y * gauss_weight(sigma));
-        const float next_T = T * (1.f - alpha);
-        if (next_T <= T_CUTOFF) {
-          done = true;
-          break;
-        }
-        const float vis = alpha * T;
-        const float4 col = s2[t];
-        r += fmaxf(col.x, 0.f) * vis;
-        g += fmaxf(col.y, 0.f) * vis;
-        b += fmaxf(col.z, 0.f) * vis;
-        T = next_T;
-        last = start + t + 1;
+    for (uint32_t t = 0; t < remaining; t++) {
+      const float4 g0 = s_g0[t], g1 = s_g1[t];
+      float sigma;
+      {
+#pragma clang fp contract(off)
+        const float dx = pcx - g0.x, dy = pcy - g0.y;
+        sigma = ((g0.z * dx) * dx + (g1.x * dy) * dy) + (g0.w * dx) * dy;
       }
+      const bool valid = live && sigma >= 0.f && sigma <= g1.z;
+      if (ballot64(valid) == 0) continue;
+      const float alpha = valid ? fminf(ALPHA_MAX, g1.y * gauss_weight(sigma)) : 0.f;
+      const float next_T = T * (1.f - alpha);
+      const bool stop = next_T <= T_CUTOFF;  // only a valid fragment can stop a lane
+      live = live && !stop;
+      const float vis = stop ? 0.f : alpha * T;
+      const float4 col = s_col[t];
+      r += col.x * vis;
+      g += col.y * vis;
+      b += col.z * vis;
+      T = stop ? T : next_T;
+      last = vis > 0.f ? start + t + 1 : last;
     }
   }
   if (inside) {

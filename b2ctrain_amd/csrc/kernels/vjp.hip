@@ -3,6 +3,10 @@
 // gradients [pos3, opacity, quat4, log-scale3, SH 3K]. Reads and clears v_splat and vis_flag (the
 // consumed-and-zeroed contract of optim.cu:110-121). accumulate = 1 adds into grad_out so gradients of
 // several views can be summed; 0 overwrites like the reference.
+// Evaluated without FMA contraction, in the operation order of the reference's VJP: the chain through the
+// 2x2 inverse and the 3x3 covariance amplifies rounding differences by the conic's condition number
+// (large for the thin splats of the stress configuration), so the kernel keeps IEEE single-op rounding.
+#pragma clang fp contract(off)
 #include "b2c_kernels.h"
 #include "device_math.h"
 #include "project_one.h"

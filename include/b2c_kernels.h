@@ -66,9 +66,10 @@ size_t b2c_radix_sort_temp_bytes(uint32_t n);
 
 /* Stable LSD key-value radix sort of keys_in/vals_in over bits [begin_bit, end_bit) into keys_out/vals_out
  * (replaces cub::DeviceRadixSort::SortPairs, binning.cu:116-118,140-142). keys_alt/vals_alt are ping-pong
- * buffers of n entries; the inputs are not modified. n_dev (may be NULL) points at a device copy of n: the
- * launch covers n entries, the kernels read the live count from n_dev when it is set (n is then the
- * capacity). */
+ * buffers of n entries; the inputs are not modified. vals_in may be NULL: the values are then the input
+ * positions 0 .. n-1 (vals_out receives the sorting permutation). n_dev (may be NULL) points at a device
+ * copy of n: the launch covers n entries, the kernels read the live count from n_dev when it is set (n is
+ * then the capacity). */
 int b2c_hip_radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in, uint32_t* keys_out, uint32_t* vals_out,
                              uint32_t* keys_alt, uint32_t* vals_alt, uint32_t n, const uint32_t* n_dev, int begin_bit,
                              int end_bit, void* temp, size_t temp_bytes, hipStream_t stream);
@@ -100,9 +101,14 @@ typedef struct b2c_emit_args {
 } b2c_emit_args;
 int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream);
 
-/* tile_ranges_kernel (binning.cu:95-105) after zeroing ranges: ranges[t] = [first, last) of tile t. */
-int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_sorted, uint32_t n_tiles,
-                        uint32_t* ranges, hipStream_t stream);
+/* tile_ranges_kernel (binning.cu:95-105) after zeroing ranges: ranges[t] = [first, last) of tile t, and
+ * tile_end[t] = last (may be NULL; a copy the forward does not shrink; n_tiles + 1 entries, the last = the
+ * position where the sentinel keys of an emit shortfall start, m if there are none). When slot_sorted is set (the
+ * permutation from an index sort of the emitted keys), also writes vals_sorted[i] = vals[slot_sorted[i]]:
+ * the splat ids in list order, as the reference's key-value sort leaves them. */
+int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_sorted, const uint32_t* slot_sorted,
+                        const uint32_t* vals, uint32_t* vals_sorted, uint32_t n_tiles, uint32_t* ranges,
+                        uint32_t* tile_end, hipStream_t stream);
 
 /* ---- rasterization ---- */
 
@@ -123,7 +129,13 @@ int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream);
 /* Backward through compositing: raster_bwd_kernel (fp32 reduction, src/gpu/raster_bwd.cu:10-156) when
  * mode = 0, raster_bwd_tc_kernel (src/gpu/raster_bwd_tc.cu:29-225; here MFMA f16 split hi/lo with fp32
  * accumulation) when mode = 1. Gradients are multiplied by inv_gscale (mode 1 semantics; pass 1 for mode 0
- * to match the reference's fp32 kernel). */
+ * to match the reference's fp32 kernel).
+ *
+ * Mode 0 accumulates into v_splat / vis_weight with float atomics, as the reference does. Mode 1 uses no
+ * atomics: each (tile, splat) pair writes its 12-float row [g0..g9, sum of blend weights, 0] to
+ * isect_rows[slot_sorted[i]] (rows of pairs past the shrunk range end are written as zeros); the rows of
+ * one splat are then a contiguous run in emit order, which a segmented reduction sums in a fixed order
+ * and adds to v_splat, vis_weight and vis_flag. The result is deterministic. */
 typedef struct b2c_raster_bwd_args {
   const uint32_t* tile_ranges;
   const uint32_t* vals_sorted;
@@ -138,6 +150,12 @@ typedef struct b2c_raster_bwd_args {
   float* v_splat;             /* [n][13], accumulated */
   uint32_t* vis_flag;         /* [n] */
   float* vis_weight;          /* [n] or NULL */
+  /* mode 1 only */
+  uint32_t num_isect;         /* M */
+  const uint32_t* slot_sorted;/* [M] emit position of list entry i */
+  const uint32_t* isect_vals; /* [M] splat id of emit position s (the emit kernel's values) */
+  const uint32_t* tile_end;   /* [n_tiles + 1] list end before the forward's shrink; [n_tiles] = sentinel start */
+  float* isect_rows;          /* [M][12] scratch */
 } b2c_raster_bwd_args;
 int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stream);
 

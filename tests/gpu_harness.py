@@ -100,8 +100,12 @@ def check_vjp(r, scene, camd, vs, vf, tile_count):
     g = r.read("grads")
     ref = O.vjp(scene, camd, vs, vf, tile_count)
     col = np.abs(ref).max(axis=0) + 1e-30
-    err = float((np.abs(g - ref) / col).max())
-    assert err <= 1e-3, f"grads vs oracle VJP (same v_splat): {err:.2e}"
+    rel = np.abs(g - ref) / col
+    err = float(rel.max())
+    if err > 1e-3:
+        i, k = np.unravel_index(int(rel.argmax()), rel.shape)
+        raise AssertionError(f"grads vs oracle VJP (same v_splat): {err:.2e} at splat {i} column {k}: "
+                             f"gpu {g[i, k]:.6g} oracle {ref[i, k]:.6g} column max {col[k]:.3g}")
     assert not r.read("vis_flag").any(), "vis_flag not cleared by the VJP"
     assert not r.read("v_splat").any(), "v_splat not cleared by the VJP"
     return g

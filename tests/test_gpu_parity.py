@@ -50,7 +50,7 @@ def test_config4_subset_sh4():
 def test_config5_subset_fp16_big_splats():
     sc = S.config5(n=20_000)
     emit("config5 n=20000 4K fp16 bands")
-    out = full_check(sc, mode=1, backward=False)
+    out = full_check(sc, mode=1)
     assert out["M"] > 0
 
 
