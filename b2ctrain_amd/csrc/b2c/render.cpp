@@ -79,6 +79,7 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
   keys_sorted.reserve(ncap, false, stream); vals_sorted.reserve(ncap, false, stream);
   isect_alt_k.reserve(ncap, false, stream); isect_alt_v.reserve(ncap, false, stream);
   slot_sorted.reserve(ncap, false, stream); isect_rows.reserve(ncap * 3, false, stream);
+  isect_part.reserve((ncap / 64 + 1) * 6, false, stream); isect_part_flags.reserve(ncap / 64 + 1, false, stream);
   isect_cap = ncap;
   sort_tmp.reserve(b2c_radix_sort_temp_bytes((uint32_t)ncap));
 }
@@ -211,6 +212,8 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.isect_vals = ctx.vals;
   a.tile_end = ctx.tile_end;
   a.isect_rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);
+  a.isect_part = reinterpret_cast<float*>(ctx.isect_part.ptr);
+  a.isect_part_flags = ctx.isect_part_flags;
   LAUNCH_CHECK(b2c_hip_raster_bwd(&a, stream));
 }
 

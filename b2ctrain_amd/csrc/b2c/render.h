@@ -89,6 +89,8 @@ struct RenderCtx {
   // list end before the forward shrinks it, isect_rows[slot] = that (tile, splat)'s 12-float gradient row.
   DevBuf<uint32_t> slot_sorted, tile_end;
   DevBuf<float4> isect_rows;
+  DevBuf<float4> isect_part;          // per 64-row window: partial sums of runs crossing the window's edges
+  DevBuf<uint32_t> isect_part_flags;  // per 64-row window
   DevBuf<unsigned char> sort_tmp;
   DevBuf<float> loss_partials;  // per-workgroup loss sums, reduced in a fixed order
 

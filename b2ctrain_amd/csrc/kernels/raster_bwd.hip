@@ -163,9 +163,8 @@ constexpr int ROW = 12;    // floats per (tile, splat) gradient row: g0..g9, sum
 // basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero), 6 one, 7 u, 8 v, 9 u^2, 10 uv, 11 v^2, 12-15 zero
 constexpr int B_ONE = 6, B_U = 7, B_V = 8, B_UU = 9, B_UV = 10, B_VV = 11;
 
-__device__ __forceinline__ float clamp_h(float x) {
-  return __builtin_isfinite(x) ? fminf(fmaxf(x, -60000.f), 60000.f) : 0.f;
-}
+// Clamp into the fp16 range (one v_med3_f32; infinities saturate).
+__device__ __forceinline__ float clamp_h(float x) { return __builtin_amdgcn_fmed3f(x, -60000.f, 60000.f); }
 
 // Split 8 fp32 values into fp16 hi and 2^11-scaled fp16 lo parts.
 __device__ __forceinline__ void split8(const float* x, half8& hi, half8& lo) {
@@ -178,6 +177,14 @@ __device__ __forceinline__ void split8(const float* x, half8& hi, half8& lo) {
   }
 }
 
+// fp16 only (the refine statistic: a sum of non-negative terms, 2^-11 relative rounding each).
+__device__ __forceinline__ half8 to_half8(const float* x) {
+  half8 h;
+#pragma unroll
+  for (int e = 0; e < 8; e++) h[e] = (_Float16)clamp_h(x[e]);
+  return h;
+}
+
 __device__ __forceinline__ void load8(const float* p, float* x) {
   const float4 q0 = reinterpret_cast<const float4*>(p)[0], q1 = reinterpret_cast<const float4*>(p)[1];
   x[0] = q0.x; x[1] = q0.y; x[2] = q0.z; x[3] = q0.w; x[4] = q1.x; x[5] = q1.y; x[6] = q1.z; x[7] = q1.w;
@@ -187,7 +194,7 @@ __device__ __forceinline__ void load8(const float* p, float* x) {
 // splats staged in LDS and groups of 8: for each splat of a group every lane writes three scalars of its
 // fragment (blend weight vis, v_sigma, refine) into LDS; then two 16x16x32 f16 MFMA products per 32 pixels
 // contract them against the per-pixel basis (columns 0-7 vis, 8-15 v_sigma of the group's splats; second
-// product: refine), with hi/lo fp16 splits so ~22 bits of the fp32 inputs survive. The opacity lane needs
+// product: refine, fp16 only), with hi/lo fp16 splits so ~22 bits of the fp32 inputs survive. The opacity lane needs
 // no product of its own: where a fragment is unclamped v_alpha * gauss = -v_sigma / opacity, and both are
 // zero where it is clamped, so g8 = -(sum v_sigma) / opacity.
 __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args a) {
@@ -287,7 +294,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             sigma = (t1 * dx + t2 * dy) + c01dx * dy;
           }
           const bool in = live_px && (batch_start + (uint32_t)sj < ps.last) && sigma >= 0.f && sigma <= g1.z;
-          if (ballot64(in) != 0) {
+          if (__builtin_amdgcn_ballot_w64(in) != 0) {
           const float gauss = gauss_weight(sigma);
           const float araw = g1.y * gauss;
           const float alpha = fminf(ALPHA_MAX, araw);
@@ -316,7 +323,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       __syncthreads();
       // ---- reduction over the 64 pixels on MFMA
       floatx4 d0_hi = {0.f, 0.f, 0.f, 0.f}, d0_lo = {0.f, 0.f, 0.f, 0.f};
-      floatx4 d1_hi = {0.f, 0.f, 0.f, 0.f}, d1_lo = {0.f, 0.f, 0.f, 0.f};
+      floatx4 d1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < 2; kb++) {
         float x[8];
@@ -331,15 +338,13 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 #pragma unroll
           for (int e = 0; e < 8; e++) x[e] = 0.f;
         }
-        split8(x, b_hi, b_lo);
-        d1_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_hi, d1_hi, 0, 0, 0);
-        d1_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_lo, d1_lo, 0, 0, 0);
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], to_half8(x), d1, 0, 0, 0);
       }
       // D layout: this lane holds rows 4*kg .. 4*kg+3 of column nl
 #pragma unroll
       for (int rr = 0; rr < 4; rr++) {
         sC[0][kg * 4 + rr][nl] = d0_hi[rr] + d0_lo[rr] * (1.f / LO_SCALE);
-        sC[1][kg * 4 + rr][nl] = d1_hi[rr] + d1_lo[rr] * (1.f / LO_SCALE);
+        sC[1][kg * 4 + rr][nl] = d1[rr];
       }
       __syncthreads();
       // ---- per-splat rows: lane = (part, splat), three float4 parts per row
@@ -379,92 +384,149 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 
 // Per-splat sum of the (tile, splat) rows. In emit order the rows of one splat are one contiguous run and
 // isect_vals[slot] (the emitted splat id) names the run, so this is a segmented reduction over a
-// contiguous array: wave w owns the runs that start in rows [64 w, 64 w + 64) and sums them 64 rows at a
-// time (coalesced 48-byte rows, a segmented Hillis-Steele scan across lanes, a carry for runs longer than
-// one chunk). Each run's last lane adds its sums to v_splat[0..9], vis_weight and vis_flag (the
-// raster_bwd_tc.cu:195-198 updates without atomics). Summation order is fixed: the result is deterministic.
+// contiguous array, in two kernels:
+//  * isect_reduce_kernel: one wave per aligned window of 64 rows (coalesced 48-byte rows), a segmented
+//    inclusive scan across lanes on DPP row shifts and row broadcasts. A run that starts and ends inside
+//    the window is finished there: its last lane adds the sums to v_splat[0..9], vis_weight and vis_flag
+//    (the raster_bwd_tc.cu:195-198 updates, without atomics). A run crossing a window edge leaves its
+//    per-window partial sums in isect_part (first run of the window, last run of the window) with flags.
+//  * isect_fixup_kernel: one thread per window; the window where a crossing run starts adds the partials
+//    of the following windows the run covers, in order, and finishes the run.
+// Every window does the same amount of work whatever the run lengths (splats spanning thousands of tiles
+// do not serialise), and the summation order is fixed: the result is deterministic.
 constexpr int RED_VALS = 11;  // g0..g9 and the blend-weight sum
+constexpr uint32_t NO_RUN = 0xFFFFFFFFu;
+constexpr uint32_t W_CONT_BEFORE = 1u, W_CONT_AFTER = 2u, W_HAS_HEAD = 4u;
+
+// DPP controls (GCN/CDNA): row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143,
+// wave_shl:1 = 0x130, wave_shr:1 = 0x138.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x, uint32_t fill) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+
+// One Hillis-Steele step of the segmented scan: add the partial of the DPP source lane when it lies in
+// the same run (runs are contiguous, so equal ids at both ends mean no run boundary in between).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void seg_scan_step(uint32_t id, float (&v)[RED_VALS]) {
+  const bool same = dpp_u32<CTRL, ROW_MASK>(id, NO_RUN) == id;
+#pragma unroll
+  for (int k = 0; k < RED_VALS; k++) {
+    const float t = __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v[k]), 0u));
+    v[k] = same ? v[k] + t : v[k];
+  }
+}
+
+__device__ __forceinline__ void seg_scan(uint32_t id, float (&v)[RED_VALS]) {
+  seg_scan_step<0x111, 0xF>(id, v);  // row_shr:1
+  seg_scan_step<0x112, 0xF>(id, v);  // row_shr:2
+  seg_scan_step<0x114, 0xF>(id, v);  // row_shr:4
+  seg_scan_step<0x118, 0xF>(id, v);  // row_shr:8
+  seg_scan_step<0x142, 0xA>(id, v);  // row_bcast:15 into rows 1 and 3
+  seg_scan_step<0x143, 0xC>(id, v);  // row_bcast:31 into rows 2 and 3
+}
+
+__device__ __forceinline__ void prefetch_old(const b2c_raster_bwd_args& a, uint32_t id, float (&old)[RED_VALS]) {
+  const float* dst = a.v_splat + (size_t)id * GRAD_LANES;
+#pragma unroll
+  for (int k = 0; k < 10; k++) old[k] = dst[k];
+  old[10] = a.vis_weight ? a.vis_weight[id] : 0.f;
+}
+
+// Adds a finished run's sums to v_splat / vis_weight (previous contents in `old`) and flags the splat.
+__device__ __forceinline__ void finish_run(const b2c_raster_bwd_args& a, uint32_t id, const float (&v)[RED_VALS],
+                                           const float (&old)[RED_VALS]) {
+  if (!(v[10] > 0.f)) return;  // no composited fragment: every lane of the run is zero
+  float* dst = a.v_splat + (size_t)id * GRAD_LANES;
+#pragma unroll
+  for (int k = 0; k < 10; k++) dst[k] = old[k] + v[k];
+  a.vis_flag[id] = 1u;
+  if (a.vis_weight) a.vis_weight[id] = old[10] + v[10];
+}
+
+__device__ __forceinline__ void store_part(float4* p, const float (&v)[RED_VALS]) {
+  p[0] = make_float4(v[0], v[1], v[2], v[3]);
+  p[1] = make_float4(v[4], v[5], v[6], v[7]);
+  p[2] = make_float4(v[8], v[9], v[10], 0.f);
+}
+
+__device__ __forceinline__ void add_part(const float4* p, float (&v)[RED_VALS]) {
+  const float4 q0 = p[0], q1 = p[1], q2 = p[2];
+  v[0] += q0.x; v[1] += q0.y; v[2] += q0.z; v[3] += q0.w; v[4] += q1.x; v[5] += q1.y; v[6] += q1.z; v[7] += q1.w;
+  v[8] += q2.x; v[9] += q2.y; v[10] += q2.z;
+}
 
 __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a) {
   const uint32_t m = a.num_isect;
   const int lane = threadIdx.x & 63;
-  const uint32_t lo = (blockIdx.x * 4u + (threadIdx.x >> 6)) * 64u;
+  const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t lo = w * 64u;
   if (lo >= m) return;
   const uint32_t* ids = a.isect_vals;
   const float4* rows = reinterpret_cast<const float4*>(a.isect_rows);
-  const uint32_t NONE = 0xFFFFFFFFu;
-  // the first run head in the window
-  uint32_t s = lo + lane;
-  uint32_t id = s < m ? ids[s] : NONE;
-  uint32_t prev = __shfl_up(id, 1);
-  if (lane == 0) prev = lo == 0 ? NONE : ids[lo - 1];
-  const uint64_t heads = ballot64(s < m && id != prev);
-  if (heads == 0) return;  // a run that started in an earlier window covers this one
-  uint32_t pos = lo + (uint32_t)__builtin_ctzll(heads);
-  const uint32_t win_end = lo + 64u;
-  float carry[RED_VALS];
-#pragma unroll
-  for (int k = 0; k < RED_VALS; k++) carry[k] = 0.f;
-  uint32_t carry_id = NONE;
-  for (;;) {
-    s = pos + lane;
-    id = s < m ? ids[s] : NONE;
-    prev = __shfl_up(id, 1);
-    if (lane == 0) prev = carry_id;  // a continuing run, or a head
-    // rows past the window belong to this wave only while they continue a run that started inside it
-    const uint64_t ext_heads = ballot64(s < m && s >= win_end && id != prev);
-    const uint32_t first_ext = ext_heads ? pos + (uint32_t)__builtin_ctzll(ext_heads) : 0xFFFFFFFFu;
-    const bool active = s < m && s < first_ext;
-    if (!active) id = NONE;
-    float v[RED_VALS];
-    {
-      float4 q0 = make_float4(0.f, 0.f, 0.f, 0.f), q1 = q0, q2 = q0;
-      if (active) {
-        q0 = rows[(size_t)s * 3];
-        q1 = rows[(size_t)s * 3 + 1];
-        q2 = rows[(size_t)s * 3 + 2];
-      }
-      v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w; v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
-      v[8] = q2.x; v[9] = q2.y; v[10] = q2.z;
+  const uint32_t s = lo + lane;
+  const bool valid = s < m;
+  const uint32_t id = valid ? ids[s] : NO_RUN;
+  const uint32_t before = lo == 0 ? NO_RUN : ids[lo - 1];
+  const uint32_t after = lo + 64u < m ? ids[lo + 64u] : NO_RUN;
+  float v[RED_VALS];
+  {
+    float4 q0 = make_float4(0.f, 0.f, 0.f, 0.f), q1 = q0, q2 = q0;
+    if (valid) {
+      q0 = rows[(size_t)s * 3];
+      q1 = rows[(size_t)s * 3 + 1];
+      q2 = rows[(size_t)s * 3 + 2];
     }
-    if (lane == 0 && id == carry_id) {
-#pragma unroll
-      for (int k = 0; k < RED_VALS; k++) v[k] += carry[k];
-    }
-    // segmented inclusive scan: a lane adds the partial of lane - o when both lie in the same run
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t oid = __shfl_up(id, o);
-      const bool same = lane >= o && oid == id;
-#pragma unroll
-      for (int k = 0; k < RED_VALS; k++) {
-        const float t = __shfl_up(v[k], o);
-        v[k] = same ? v[k] + t : v[k];
-      }
-    }
-    // does the last run of this chunk continue into the next one?
-    const uint32_t next = pos + 64u;
-    const uint32_t id63 = __shfl(id, 63);
-    const bool continues = id63 != NONE && next < m && next < first_ext && ids[next] == id63;
-    const uint32_t nid = __shfl_down(id, 1);
-    const bool tail = id != NONE && (lane == 63 ? !continues : nid != id);
-    if (tail && v[10] > 0.f) {  // no composited fragment: every lane of the run is zero
-      float* dst = a.v_splat + (size_t)id * GRAD_LANES;
-#pragma unroll
-      for (int k = 0; k < 10; k++) dst[k] += v[k];
-      a.vis_flag[id] = 1u;
-      if (a.vis_weight) a.vis_weight[id] += v[10];
-    }
-    if (!continues) {
-      if (first_ext != 0xFFFFFFFFu || next >= m) break;
-      carry_id = NONE;
-    } else {
-#pragma unroll
-      for (int k = 0; k < RED_VALS; k++) carry[k] = __shfl(v[k], 63);
-      carry_id = id63;
-    }
-    pos = next;
+    v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w; v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+    v[8] = q2.x; v[9] = q2.y; v[10] = q2.z;
   }
+  const uint32_t prev = dpp_u32<0x138, 0xF>(id, before);  // wave_shr:1; lane 0 gets `before`
+  const bool head = valid && id != prev;
+  const uint64_t heads = ballot64(head);
+  const uint32_t id63 = (uint32_t)__builtin_amdgcn_readlane((int)id, 63);
+  const bool cont_after = id63 != NO_RUN && after == id63;
+  const bool cont_before = (heads & 1ull) == 0;  // row 0 continues a run from the previous window
+  const uint32_t nid = dpp_u32<0x130, 0xF>(id, cont_after ? id63 : NO_RUN);  // wave_shl:1; lane 63 gets the fill
+  const bool tail = valid && nid != id;
+  // the first run of the window ends at the lane before the second head (or 63)
+  const uint64_t later_heads = heads & ~1ull;
+  const int last_valid = (int)min(63u, m - 1u - lo);
+  const int first_tail = later_heads ? __builtin_ctzll(later_heads) - 1 : last_valid;
+  const bool is_first = lane == first_tail;
+  const bool is_last = lane == 63;
+  const bool complete = tail && !(is_first && cont_before) && !(is_last && cont_after);
+  float old[RED_VALS];
+  if (complete) prefetch_old(a, id, old);
+  seg_scan(valid ? id : NO_RUN, v);
+  if (complete) finish_run(a, id, v, old);
+  float4* part = reinterpret_cast<float4*>(a.isect_part) + (size_t)w * 6;
+  if (is_first && cont_before) store_part(part, v);            // continuation of an earlier run
+  if (is_last && cont_after && !(is_first && cont_before)) store_part(part + 3, v);  // a run that starts here
+  if (lane == 0) a.isect_part_flags[w] = (cont_before ? W_CONT_BEFORE : 0u) | (cont_after ? W_CONT_AFTER : 0u) |
+                                         (heads ? W_HAS_HEAD : 0u);
+}
+
+__global__ void __launch_bounds__(256) isect_fixup_kernel(b2c_raster_bwd_args a) {
+  const uint32_t nwin = (a.num_isect + 63u) / 64u;
+  const uint32_t w = blockIdx.x * 256u + threadIdx.x;
+  if (w >= nwin) return;
+  const uint32_t f = a.isect_part_flags[w];
+  // owner: the last run of window w starts in w (w has a head) and continues into w + 1
+  if (!(f & W_CONT_AFTER) || !(f & W_HAS_HEAD)) return;
+  const float4* part = reinterpret_cast<const float4*>(a.isect_part);
+  const uint32_t run = a.isect_vals[w * 64u + 63u];
+  float v[RED_VALS];
+#pragma unroll
+  for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
+  add_part(part + (size_t)w * 6 + 3, v);
+  for (uint32_t x = w + 1; x < nwin; x++) {
+    add_part(part + (size_t)x * 6, v);  // the run's rows at the start of window x
+    const uint32_t fx = a.isect_part_flags[x];
+    if ((fx & W_HAS_HEAD) || !(fx & W_CONT_AFTER)) break;  // the run ends in window x
+  }
+  float old[RED_VALS];
+  prefetch_old(a, run, old);
+  finish_run(a, run, v, old);
 }
 
 }  // namespace
@@ -483,7 +545,11 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
     if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals) return (int)hipErrorInvalidValue;
     raster_bwd_mfma_kernel<<<grid, block, 0, stream>>>(*a);
     const uint32_t windows = (a->num_isect + 63u) / 64u;
-    if (windows) isect_reduce_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
+    if (windows) {
+      if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;
+      isect_reduce_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
+      isect_fixup_kernel<<<dim3((windows + 255u) / 256u), dim3(256), 0, stream>>>(*a);
+    }
   }
   return (int)hipGetLastError();
 }

@@ -156,6 +156,8 @@ typedef struct b2c_raster_bwd_args {
   const uint32_t* isect_vals; /* [M] splat id of emit position s (the emit kernel's values) */
   const uint32_t* tile_end;   /* [n_tiles + 1] list end before the forward's shrink; [n_tiles] = sentinel start */
   float* isect_rows;          /* [M][12] scratch */
+  float* isect_part;          /* [ceil(M / 64)][24] scratch: partial sums of runs crossing 64-row windows */
+  uint32_t* isect_part_flags; /* [ceil(M / 64)] scratch */
 } b2c_raster_bwd_args;
 int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stream);
 
