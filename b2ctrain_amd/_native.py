@@ -60,7 +60,8 @@ EXPORTS = [
     "b2c_view_destroy", "b2c_render_forward", "b2c_project_splats", "b2c_bin_and_sort", "b2c_rasterize_forward",
     "b2c_photometric_loss", "b2c_accumulate_loss", "b2c_rasterize_backward", "b2c_optimizer_grad", "b2c_train_step",
     # launcher layer
-    "b2c_hip_project", "b2c_radix_sort_temp_bytes", "b2c_hip_radix_sort_pairs", "b2c_hip_depth_keys",
+    "b2c_hip_project", "b2c_radix_sort_temp_bytes", "b2c_hip_radix_sort_pairs", "b2c_hip_radix_sort_kv2",
+    "b2c_hip_depth_keys",
     "b2c_scan_temp_bytes", "b2c_hip_scan_counts", "b2c_hip_emit", "b2c_hip_tile_ranges", "b2c_hip_raster_fwd",
     "b2c_hip_raster_bwd", "b2c_hip_photometric", "b2c_loss_partials", "b2c_hip_accumulate_loss", "b2c_hip_vjp",
     "b2c_hip_fill_u32",

@@ -78,6 +78,7 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
   keys.reserve(ncap, false, stream); vals.reserve(ncap, false, stream);
   keys_sorted.reserve(ncap, false, stream); vals_sorted.reserve(ncap, false, stream);
   isect_alt_k.reserve(ncap, false, stream); isect_alt_v.reserve(ncap, false, stream);
+  isect_alt_v2.reserve(ncap, false, stream);
   slot_sorted.reserve(ncap, false, stream); isect_rows.reserve(ncap * 3, false, stream);
   isect_part.reserve((ncap / 64 + 1) * 6, false, stream); isect_part_flags.reserve(ncap / 64 + 1, false, stream);
   isect_cap = ncap;
@@ -152,15 +153,13 @@ void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   e.keys = ctx.keys; e.vals = ctx.vals;
   e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
   LAUNCH_CHECK(b2c_hip_emit(&e, stream));
-  // The tile pass sorts emit positions rather than splat ids: the permutation tells the backward where
-  // each (tile, splat) gradient row goes (a splat's rows are then contiguous); the splat ids in list order
-  // are gathered from it while the ranges are built.
-  LAUNCH_CHECK(b2c_hip_radix_sort_pairs(ctx.keys, nullptr, ctx.keys_sorted, ctx.slot_sorted, ctx.isect_alt_k,
-                                        ctx.isect_alt_v, total, nullptr, 0, ctx.tile_bits, ctx.sort_tmp.ptr,
-                                        ctx.sort_tmp.bytes(), stream));
-  LAUNCH_CHECK(b2c_hip_tile_ranges(total, nullptr, ctx.keys_sorted, ctx.slot_sorted, ctx.vals, ctx.vals_sorted,
-                                   (uint32_t)ctx.n_tiles, reinterpret_cast<uint32_t*>(ctx.tile_ranges.ptr),
-                                   ctx.tile_end, stream));
+  // The tile pass carries the emit positions next to the splat ids: the backward writes each (tile, splat)
+  // gradient row at its emit position, where a splat's rows are contiguous.
+  LAUNCH_CHECK(b2c_hip_radix_sort_kv2(ctx.keys, nullptr, ctx.vals, ctx.keys_sorted, ctx.slot_sorted, ctx.vals_sorted,
+                                      ctx.isect_alt_k, ctx.isect_alt_v, ctx.isect_alt_v2, total, nullptr, 0,
+                                      ctx.tile_bits, ctx.sort_tmp.ptr, ctx.sort_tmp.bytes(), stream));
+  LAUNCH_CHECK(b2c_hip_tile_ranges(total, nullptr, ctx.keys_sorted, nullptr, nullptr, nullptr, (uint32_t)ctx.n_tiles,
+                                   reinterpret_cast<uint32_t*>(ctx.tile_ranges.ptr), ctx.tile_end, stream));
 }
 
 void rasterize_forward(RenderCtx& ctx, const RenderParams& p, hipStream_t stream) {
@@ -210,6 +209,7 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.num_isect = ctx.num_isect;
   a.slot_sorted = ctx.slot_sorted;
   a.isect_vals = ctx.vals;
+  a.tile_count = ctx.tile_count;
   a.tile_end = ctx.tile_end;
   a.isect_rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);
   a.isect_part = reinterpret_cast<float*>(ctx.isect_part.ptr);

@@ -111,30 +111,51 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scan_digits(uint32_t* __re
   if (threadIdx.x == 0) digit_total[blockIdx.x] = running;
 }
 
+// Stable scatter of one digit pass. The workgroup ranks its SORT_TILE keys by digit (ballot match masks
+// within each wave, per-wave digit counts in LDS across rounds), stages keys and values in LDS sorted by
+// digit, then writes the staging buffer out in order: each digit's keys of this tile form one contiguous
+// run in the output, so consecutive lanes write consecutive addresses (coalesced) instead of one 4-byte
+// write per key to a different bucket. NV = 1 or 2 value arrays ride along with the keys.
+template <int NV>
 __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
-    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out, uint32_t cap, const uint32_t* __restrict__ n_dev, int shift, int bits,
-    const uint32_t* __restrict__ block_hist, uint32_t nblocks, const uint32_t* __restrict__ digit_total) {
-  __shared__ uint32_t s_base[RADIX];
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ vals2_in,
+    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ vals2_out, uint32_t cap,
+    const uint32_t* __restrict__ n_dev, int shift, int bits, const uint32_t* __restrict__ block_hist, uint32_t nblocks,
+    const uint32_t* __restrict__ digit_total) {
+  __shared__ uint32_t s_key[SORT_TILE];
+  __shared__ uint32_t s_val[NV][SORT_TILE];
+  __shared__ uint32_t s_gbase[RADIX];  // global position of the tile's first key of each digit
+  __shared__ uint32_t s_loff[RADIX];   // local (staging) offset of each digit
+  __shared__ uint32_t s_run[RADIX];    // running local position while ranking
   __shared__ uint32_t s_wcnt[NWAVES][RADIX];
   __shared__ uint32_t s_wsum[NWAVES];
   const uint32_t n = live_count(cap, n_dev);
   const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
   if (base >= n) return;
+  const uint32_t tile_n = min((uint32_t)SORT_TILE, n - base);
   const int w = threadIdx.x >> 6;
-  {
+  {  // thread t owns digit t: global base, this tile's count, local offset
+    const uint32_t t = threadIdx.x;
     uint32_t tot;
-    const uint32_t ex = block_excl_scan(digit_total[threadIdx.x], s_wsum, tot);
-    s_base[threadIdx.x] = ex + block_hist[(size_t)threadIdx.x * nblocks + blockIdx.x];
+    const uint32_t digit_start = block_excl_scan(digit_total[t], s_wsum, tot);
+    const uint32_t mine = block_hist[(size_t)t * nblocks + blockIdx.x];
+    const uint32_t next = blockIdx.x + 1 < nblocks ? block_hist[(size_t)t * nblocks + blockIdx.x + 1] : digit_total[t];
+    const uint32_t loff = block_excl_scan(next - mine, s_wsum, tot);
+    s_gbase[t] = digit_start + mine;
+    s_loff[t] = loff;
+    s_run[t] = loff;
   }
   const uint32_t dmask = (1u << bits) - 1u;
   for (int r = 0; r < SORT_ROUNDS; r++) {
-    const uint32_t rb = base + (uint32_t)r * SORT_THREADS;
-    if (rb >= n) break;
-    const uint32_t idx = rb + threadIdx.x;
-    const bool valid = idx < n;
+    const uint32_t rb = (uint32_t)r * SORT_THREADS;
+    if (rb >= tile_n) break;
+    const uint32_t li = rb + threadIdx.x;
+    const bool valid = li < tile_n;
+    const uint32_t idx = base + li;
     const uint32_t key = valid ? keys_in[idx] : 0u;
-    const uint32_t val = valid ? (vals_in ? vals_in[idx] : idx) : 0u;  // no values: sort the positions
+    uint32_t val[NV];
+    val[0] = valid ? (vals_in ? vals_in[idx] : idx) : 0u;  // no values: sort the positions
+    if constexpr (NV > 1) val[1] = valid ? vals2_in[idx] : 0u;
     const uint32_t d = (key >> shift) & dmask;
 #pragma unroll
     for (int k = 0; k < NWAVES; k++) s_wcnt[k][threadIdx.x] = 0u;
@@ -143,24 +164,33 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     const uint32_t rank = popc64(peers & lanemask_lt());
     if (valid && rank == 0) s_wcnt[w][d] = popc64(peers);
     __syncthreads();
-    {  // thread t owns digit t: turn per-wave counts into offsets, advance the digit base
+    {  // thread t owns digit t: per-wave counts become local positions, the running position advances
       const uint32_t t = threadIdx.x;
-      uint32_t run = s_base[t];
+      uint32_t run = s_run[t];
 #pragma unroll
       for (int k = 0; k < NWAVES; k++) {
         const uint32_t c = s_wcnt[k][t];
         s_wcnt[k][t] = run;
         run += c;
       }
-      s_base[t] = run;
+      s_run[t] = run;
     }
     __syncthreads();
     if (valid) {
-      const uint32_t pos = s_wcnt[w][d] + rank;
-      keys_out[pos] = key;
-      vals_out[pos] = val;
+      const uint32_t lp = s_wcnt[w][d] + rank;
+      s_key[lp] = key;
+#pragma unroll
+      for (int v = 0; v < NV; v++) s_val[v][lp] = val[v];
     }
-    __syncthreads();
+    __syncthreads();  // s_wcnt is cleared at the top of the next round
+  }
+  for (uint32_t j = threadIdx.x; j < tile_n; j += SORT_THREADS) {
+    const uint32_t key = s_key[j];
+    const uint32_t d = (key >> shift) & dmask;
+    const uint32_t g = s_gbase[d] + (j - s_loff[d]);
+    keys_out[g] = key;
+    vals_out[g] = s_val[0][j];
+    if constexpr (NV > 1) vals2_out[g] = s_val[1][j];
   }
 }
 
@@ -385,35 +415,52 @@ extern "C" size_t b2c_radix_sort_temp_bytes(uint32_t n) {
   return (nb * RADIX + RADIX) * sizeof(uint32_t);
 }
 
-extern "C" int b2c_hip_radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in, uint32_t* keys_out,
-                                        uint32_t* vals_out, uint32_t* keys_alt, uint32_t* vals_alt, uint32_t n,
-                                        const uint32_t* n_dev, int begin_bit, int end_bit, void* temp, size_t temp_bytes,
-                                        hipStream_t stream) {
+extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* vals_in, const uint32_t* vals2_in,
+                                      uint32_t* keys_out, uint32_t* vals_out, uint32_t* vals2_out, uint32_t* keys_alt,
+                                      uint32_t* vals_alt, uint32_t* vals2_alt, uint32_t n, const uint32_t* n_dev,
+                                      int begin_bit, int end_bit, void* temp, size_t temp_bytes, hipStream_t stream) {
   if (n == 0 || end_bit <= begin_bit) return 0;
   if (temp_bytes < b2c_radix_sort_temp_bytes(n) || begin_bit < 0 || end_bit > 32) return (int)hipErrorInvalidValue;
+  const bool two = vals2_in != nullptr;
+  if (two && (!vals2_out || !vals2_alt)) return (int)hipErrorInvalidValue;
   const uint32_t nb = sort_blocks(n);
   uint32_t* block_hist = static_cast<uint32_t*>(temp);
   uint32_t* digit_total = block_hist + (size_t)nb * RADIX;
   const int passes = (end_bit - begin_bit + 7) / 8;
   const uint32_t* src_k = keys_in;
   const uint32_t* src_v = vals_in;
+  const uint32_t* src_v2 = vals2_in;
   for (int p = 0; p < passes; p++) {
     const int shift = begin_bit + 8 * p;
     const int bits = end_bit - shift < 8 ? end_bit - shift : 8;
-    // route the passes so that the last one lands in keys_out
+    // route the passes so that the last one lands in the output buffers
     const bool to_out = ((passes - 1 - p) % 2) == 0;
     uint32_t* dk = to_out ? keys_out : keys_alt;
     uint32_t* dv = to_out ? vals_out : vals_alt;
+    uint32_t* dv2 = to_out ? vals2_out : vals2_alt;
     radix_upsweep<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, n, n_dev, shift, bits, block_hist, nb);
     radix_scan_digits<<<dim3(RADIX), dim3(SORT_THREADS), 0, stream>>>(block_hist, nb, digit_total);
-    radix_scatter<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, dk, dv, n, n_dev, shift, bits, block_hist,
-                                                                 nb, digit_total);
+    if (two)
+      radix_scatter<2><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift,
+                                                                     bits, block_hist, nb, digit_total);
+    else
+      radix_scatter<1><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, nullptr, dk, dv, nullptr, n, n_dev,
+                                                                     shift, bits, block_hist, nb, digit_total);
     int e = (int)hipGetLastError();
     if (e) return e;
     src_k = dk;
     src_v = dv;
+    src_v2 = dv2;
   }
   return 0;
+}
+
+extern "C" int b2c_hip_radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in, uint32_t* keys_out,
+                                        uint32_t* vals_out, uint32_t* keys_alt, uint32_t* vals_alt, uint32_t n,
+                                        const uint32_t* n_dev, int begin_bit, int end_bit, void* temp, size_t temp_bytes,
+                                        hipStream_t stream) {
+  return b2c_hip_radix_sort_kv2(keys_in, vals_in, nullptr, keys_out, vals_out, nullptr, keys_alt, vals_alt, nullptr, n,
+                                n_dev, begin_bit, end_bit, temp, temp_bytes, stream);
 }
 
 extern "C" int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const float* proj1, uint32_t* keys, uint32_t* vals,

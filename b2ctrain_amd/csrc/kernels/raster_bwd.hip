@@ -501,7 +501,10 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
   if (complete) finish_run(a, id, v, old);
   float4* part = reinterpret_cast<float4*>(a.isect_part) + (size_t)w * 6;
   if (is_first && cont_before) store_part(part, v);            // continuation of an earlier run
-  if (is_last && cont_after && !(is_first && cont_before)) store_part(part + 3, v);  // a run that starts here
+  if (is_last && cont_after && !(is_first && cont_before)) {  // a run that starts here: sums and head slot
+    store_part(part + 3, v);
+    part[5].w = __uint_as_float(lo + 63u - (uint32_t)__builtin_clzll(heads));
+  }
   if (lane == 0) a.isect_part_flags[w] = (cont_before ? W_CONT_BEFORE : 0u) | (cont_after ? W_CONT_AFTER : 0u) |
                                          (heads ? W_HAS_HEAD : 0u);
 }
@@ -515,15 +518,16 @@ __global__ void __launch_bounds__(256) isect_fixup_kernel(b2c_raster_bwd_args a)
   if (!(f & W_CONT_AFTER) || !(f & W_HAS_HEAD)) return;
   const float4* part = reinterpret_cast<const float4*>(a.isect_part);
   const uint32_t run = a.isect_vals[w * 64u + 63u];
+  // the run covers emit positions [head, head + tile_count), so its last window is known up front and the
+  // partial sums of the windows it covers can be loaded independently
+  const uint32_t head = __float_as_uint(part[(size_t)w * 6 + 5].w);
+  const uint32_t last_win = (head + a.tile_count[run] - 1u) / 64u;
   float v[RED_VALS];
 #pragma unroll
   for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
   add_part(part + (size_t)w * 6 + 3, v);
-  for (uint32_t x = w + 1; x < nwin; x++) {
-    add_part(part + (size_t)x * 6, v);  // the run's rows at the start of window x
-    const uint32_t fx = a.isect_part_flags[x];
-    if ((fx & W_HAS_HEAD) || !(fx & W_CONT_AFTER)) break;  // the run ends in window x
-  }
+#pragma unroll 4
+  for (uint32_t x = w + 1; x <= last_win && x < nwin; x++) add_part(part + (size_t)x * 6, v);
   float old[RED_VALS];
   prefetch_old(a, run, old);
   finish_run(a, run, v, old);
@@ -542,7 +546,8 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
   if (a->mode == 0) {
     raster_bwd_fp32_kernel<<<grid, block, 0, stream>>>(*a);
   } else {
-    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals) return (int)hipErrorInvalidValue;
+    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->tile_count)
+      return (int)hipErrorInvalidValue;
     raster_bwd_mfma_kernel<<<grid, block, 0, stream>>>(*a);
     const uint32_t windows = (a->num_isect + 63u) / 64u;
     if (windows) {

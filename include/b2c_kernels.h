@@ -74,6 +74,13 @@ int b2c_hip_radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in, u
                              uint32_t* keys_alt, uint32_t* vals_alt, uint32_t n, const uint32_t* n_dev, int begin_bit,
                              int end_bit, void* temp, size_t temp_bytes, hipStream_t stream);
 
+/* The same sort carrying a second value array (vals2_in -> vals2_out, ping-pong vals2_alt); the tile pass
+ * uses it to sort (tile, emit position, splat id) in one go. vals_in may be NULL as above. */
+int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* vals_in, const uint32_t* vals2_in,
+                           uint32_t* keys_out, uint32_t* vals_out, uint32_t* vals2_out, uint32_t* keys_alt,
+                           uint32_t* vals_alt, uint32_t* vals2_alt, uint32_t n, const uint32_t* n_dev, int begin_bit,
+                           int end_bit, void* temp, size_t temp_bytes, hipStream_t stream);
+
 /* depth_keys_kernel (binning.cu:10-15): key = bits of view z if tile_count > 0 else 0xFFFFFFFF, val = index. */
 int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const float* proj1, uint32_t* keys, uint32_t* vals,
                        hipStream_t stream);
@@ -154,6 +161,7 @@ typedef struct b2c_raster_bwd_args {
   uint32_t num_isect;         /* M */
   const uint32_t* slot_sorted;/* [M] emit position of list entry i */
   const uint32_t* isect_vals; /* [M] splat id of emit position s (the emit kernel's values) */
+  const uint32_t* tile_count; /* [n] intersections per splat (the length of its run of emit positions) */
   const uint32_t* tile_end;   /* [n_tiles + 1] list end before the forward's shrink; [n_tiles] = sentinel start */
   float* isect_rows;          /* [M][12] scratch */
   float* isect_part;          /* [ceil(M / 64)][24] scratch: partial sums of runs crossing 64-row windows */
