@@ -55,7 +55,8 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   tile_count.reserve(nn); tile_off.reserve(nn); hit_info.reserve(nn);
   depth_keys.reserve(nn); depth_keys_sorted.reserve(nn); order_in.reserve(nn); order.reserve(nn);
   depth_alt_k.reserve(nn); depth_alt_v.reserve(nn);
-  big_list.reserve(nn); big_base.reserve(nn);
+  big_list.reserve(nn); big_base.reserve(nn); big_info.reserve(nn); big_chunk.reserve(nn * B2C_BIG_CHUNKS);
+  big_items.reserve(nn * B2C_BIG_CHUNKS);
   counters.reserve(4);
   if (v_splat.count < nn * GRAD_LANES) { v_splat.reserve(nn * GRAD_LANES); v_splat.zero(stream); }
   if (vis_flag.count < nn) { vis_flag.reserve(nn); vis_flag.zero(stream); }
@@ -116,6 +117,10 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   a.max_screen = m.max_screen.ptr;
   a.big_list = ctx.big_list.ptr;
   a.big_count = ctx.counters.ptr;
+  a.big_info = reinterpret_cast<uint32_t*>(ctx.big_info.ptr);
+  a.big_chunk = ctx.big_chunk.ptr;
+  a.big_items = ctx.big_items.ptr;
+  a.big_items_count = ctx.counters.ptr + 2;
   LAUNCH_CHECK(b2c_hip_project(&a, stream));
 }
 
@@ -152,6 +157,8 @@ void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   e.tiles_x = ctx.tiles_x; e.tiles_y = ctx.tiles_y; e.cap = (uint32_t)ctx.isect_cap;
   e.keys = ctx.keys; e.vals = ctx.vals;
   e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
+  e.big_info = reinterpret_cast<const uint32_t*>(ctx.big_info.ptr); e.big_chunk = ctx.big_chunk;
+  e.big_items = ctx.big_items; e.big_items_count = ctx.counters.ptr + 2;
   LAUNCH_CHECK(b2c_hip_emit(&e, stream));
   // The tile pass carries the emit positions next to the splat ids: the backward writes each (tile, splat)
   // gradient row at its emit position, where a splat's rows are contiguous.

@@ -5,9 +5,8 @@
 //   exclusive scan over tiles, then a stable scatter whose in-tile ranks come from the same ballot masks
 //   (lanes below with the same digit) plus per-wave prefix counts in LDS.
 // * Count scan: reduce-then-scan of tile_count gathered in depth order.
-// * Emit: one wave64 sweeps the contiguous slot range of 64 depth-consecutive splats, 64 slots per step
-//   (owner lane by binary search over lane starts, tile by k-th set bit of the owner's hit mask). Splats
-//   whose bbox exceeds 32 tiles are emitted by one wave each over the bbox in row-major order.
+// * Emit: small splats one thread each over the set bits of their hit mask; splats whose bbox exceeds 32
+//   tiles one wave per chunk of the bbox, in row-major order.
 #pragma clang fp contract(off)
 #include "b2c_kernels.h"
 #include "device_math.h"
@@ -262,107 +261,80 @@ __global__ void __launch_bounds__(SORT_THREADS) scan_down(int n, const uint32_t*
   }
 }
 
-// Position of the (k+1)-th set bit of m (m has more than k set bits).
-__device__ __forceinline__ int kth_set_bit(uint32_t m, uint32_t k) {
-  int pos = 0;
-#pragma unroll
-  for (int w = 16; w >= 1; w >>= 1) {
-    const uint32_t c = (uint32_t)__popc(m & ((1u << w) - 1u));
-    if (k >= c) { k -= c; m >>= w; pos += w; }
-  }
-  return pos;
-}
-
+// Small splats: one thread per depth rank writes its slots [tile_off - count, tile_off) walking the set
+// bits of its hit mask (row-major bbox order). Depth-consecutive splats own adjacent slot ranges, so a
+// wave's stores land in one short stretch of the key/value arrays. Big splats only record their base.
 __global__ void __launch_bounds__(256) emit_small_kernel(b2c_emit_args a, uint32_t* __restrict__ big_base) {
   const int r = blockIdx.x * 256 + threadIdx.x;
-  const int lane = lane_id();
-  const bool valid = r < a.n;
-  const uint32_t i = valid ? a.order[r] : 0u;
-  uint32_t cnt = valid ? a.tile_count[i] : 0u;
-  const uint32_t end = valid ? a.tile_off[r] : 0u;
-  const uint32_t base = end - cnt;
-  const uint2 hi = (valid && cnt) ? reinterpret_cast<const uint2*>(a.hit_info)[i] : make_uint2(0u, 0u);
-  const bool big = cnt && hi.x == 0xFFFFFFFFu;
-  if (big) {
+  if (r >= a.n) return;
+  const uint32_t i = a.order[r];
+  const uint32_t cnt = a.tile_count[i];
+  if (cnt == 0) return;
+  const uint32_t base = a.tile_off[r] - cnt;
+  const uint2 hi = reinterpret_cast<const uint2*>(a.hit_info)[i];
+  if (hi.x == 0xFFFFFFFFu) {
     big_base[i] = base;
-    cnt = 0;
+    return;
   }
-  const uint32_t my_start = valid ? base : 0xFFFFFFFFu;
-  uint32_t my_cnt = cnt;
-  if (base + cnt > a.cap) my_cnt = 0;
-  const uint64_t active = ballot64(my_cnt > 0);
-  if (!active) return;
-  const int first = __ffsll((unsigned long long)active) - 1;
-  const int last = 63 - __clzll((long long)active);
-  const uint32_t wstart = __shfl(my_start, first);
-  const uint32_t wend = __shfl(my_start + my_cnt, last);
-  const int min_x = (int)(hi.y & 0xFFFu), min_y = (int)((hi.y >> 12) & 0xFFFu), bw = (int)(hi.y >> 24);
-  for (uint32_t sb = wstart; sb < wend; sb += 64) {
-    const uint32_t s = sb + (uint32_t)lane;
-    int lo = 0, hi_l = 63;
-#pragma unroll
-    for (int step = 0; step < 6; step++) {
-      const int mid = (lo + hi_l + 1) >> 1;
-      const uint32_t st = __shfl(my_start, mid);
-      if (st <= s) lo = mid; else hi_l = mid - 1;
-    }
-    const int o = lo;
-    const uint32_t o_start = __shfl(my_start, o);
-    const uint32_t o_cnt = __shfl(my_cnt, o);
-    const uint32_t o_mask = __shfl(hi.x, o);
-    const int o_minx = __shfl(min_x, o), o_miny = __shfl(min_y, o), o_bw = __shfl(bw, o);
-    const uint32_t o_i = __shfl(i, o);
-    if (s < wend && o_cnt > 0 && s < o_start + o_cnt) {
-      const int bit = kth_set_bit(o_mask, s - o_start);
-      const int tx = o_minx + bit % o_bw, ty = o_miny + bit / o_bw;
-      a.keys[s] = (uint32_t)(ty * a.tiles_x + tx);
-      a.vals[s] = o_i;
-    }
+  if (base + cnt > a.cap) return;
+  const uint32_t min_x = hi.y & 0xFFFu, min_y = (hi.y >> 12) & 0xFFFu, bw = hi.y >> 24;
+  uint32_t m = hi.x;
+  for (uint32_t k = 0; k < cnt && m; k++) {
+    const uint32_t bit = (uint32_t)__builtin_ctz(m);
+    m &= m - 1u;
+    const uint32_t row = bit / bw;
+    a.keys[base + k] = (min_y + row) * (uint32_t)a.tiles_x + min_x + (bit - row * bw);
+    a.vals[base + k] = i;
   }
 }
 
+// Big splats: one wave per (big-list entry, chunk), the chunk's tiles tested 64 at a time; hits go to
+// the entry's slots at the chunk's offset (counted by b2c_hip_project with the same test, in the same
+// order), so each chunk writes its own stretch independently.
 __global__ void __launch_bounds__(256) emit_big_kernel(b2c_emit_args a, const uint32_t* __restrict__ big_base) {
   const int lane = lane_id();
   const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
   const uint32_t nwaves = (gridDim.x * 256u) >> 6;
-  const uint32_t count = *a.big_count;
+  const uint32_t items = *a.big_items_count;
   const uint32_t sentinel = (uint32_t)(a.tiles_x * a.tiles_y);
-  for (uint32_t e = wave; e < count; e += nwaves) {
+  for (uint32_t it = wave; it < items; it += nwaves) {
+    const uint32_t code = a.big_items[it];
+    const uint32_t e = code >> 5, k = code & 31u;
+    const uint4 info = reinterpret_cast<const uint4*>(a.big_info)[e];
+    const uint32_t begin = k * info.w, end = min(begin + info.w, info.z);
     const uint32_t i = a.big_list[e];
     const uint32_t cnt = a.tile_count[i];
-    if (cnt == 0) continue;
     const uint32_t base = big_base[i];
     if (base + cnt > a.cap) continue;
+    const uint32_t* chunk = a.big_chunk + (size_t)e * B2C_BIG_CHUNKS;
+    const uint32_t off = chunk[k];
+    const uint32_t off_end = end < info.z ? chunk[k + 1] : cnt;
     const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
     const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
-    Sym2 conic{p0.z, p0.w, p1.x};
-    float ex, ey;
-    extent_from_conic(conic, p1.w, ex, ey);
-    TileBox bb = tile_bbox(p0.x, p0.y, ex, ey, a.tiles_x, a.tiles_y);
-    const int bw = bb.max_x - bb.min_x;
-    const int area = bw * (bb.max_y - bb.min_y);
-    uint32_t written = 0;
-    for (int b0 = 0; b0 < area && written < cnt; b0 += 64) {
-      const int b = b0 + lane;
+    const Sym2 conic{p0.z, p0.w, p1.x};
+    const int min_x = (int)(info.x & 0xFFFFu), min_y = (int)(info.x >> 16), bw = (int)info.y;
+    uint32_t written = off;
+    for (uint32_t b0 = begin; b0 < end; b0 += 64) {
+      const uint32_t b = b0 + (uint32_t)lane;
       bool h = false;
       int tx = 0, ty = 0;
-      if (b < area) {
-        tx = bb.min_x + b % bw;
-        ty = bb.min_y + b / bw;
+      if (b < end) {
+        tx = min_x + (int)(b % (uint32_t)bw);
+        ty = min_y + (int)(b / (uint32_t)bw);
         const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
         h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, p0.x, p0.y, conic, p1.w);
       }
-      const uint64_t m = ballot64(h);
+      const uint64_t mk = ballot64(h);
       if (h) {
-        const uint32_t slot = written + mbcnt64(m);
-        if (slot < cnt) {
+        const uint32_t slot = written + mbcnt64(mk);
+        if (slot < off_end) {
           a.keys[base + slot] = (uint32_t)(ty * a.tiles_x + tx);
           a.vals[base + slot] = i;
         }
       }
-      written += popc64(m);
+      written += popc64(mk);
     }
-    for (uint32_t s = written + lane; s < cnt; s += 64) {
+    for (uint32_t s = written + lane; s < off_end; s += 64) {
       a.keys[base + s] = sentinel;
       a.vals[base + s] = i;
     }
@@ -487,8 +459,9 @@ extern "C" int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t*
 
 extern "C" int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
+  if (!a->big_info || !a->big_chunk || !a->big_items || !a->big_items_count) return (int)hipErrorInvalidValue;
   emit_small_kernel<<<dim3((a->n + 255) / 256), dim3(256), 0, stream>>>(*a, a->big_base);
-  emit_big_kernel<<<dim3(512), dim3(256), 0, stream>>>(*a, a->big_base);
+  emit_big_kernel<<<dim3(B2C_BIG_GRID), dim3(256), 0, stream>>>(*a, a->big_base);
   return (int)hipGetLastError();
 }
 

@@ -1,10 +1,9 @@
-// Fused photometric loss (replaces photometric_kernel, src/gpu/loss.cu:18-195, 296-315): per 16x16 output
-// tile and channel, a 36x36 footprint of prediction and effective target in LDS (zero outside the image),
-// separable 11-tap Gaussian (sigma 1.5) statistics at the 26x26 positions the output's SSIM gradient
-// depends on, SSIM and its five partial maps, a second separable blur, L1 sign, and the alpha-match lane.
-// The per-pixel gradient goes to v_out (times grad_scale); the loss value is reduced per workgroup and
-// added to loss_accum[0]. A footprint where prediction equals target exactly has SSIM 1 and zero gradient
-// and is finished without the blurs (loss.cu:51-74).
+// Fused photometric loss (replaces photometric_kernel, src/gpu/loss.cu:18-195, 296-315): L1 + SSIM
+// (separable 11-tap Gaussian, sigma 1.5, zero padding, C1 = 1e-4, C2 = 9e-4) with the alpha-match lane.
+// The per-pixel gradient (SSIM partial maps through the second blur, L1 sign, alpha sign) goes to v_out
+// times grad_scale; the loss value is summed per wave into `partials` and reduced in a fixed order in
+// double precision. A footprint where prediction equals target exactly gives SSIM = 1 and a zero gradient
+// by the same arithmetic (the reference's early exit, loss.cu:51-74, is an optimisation only).
 #include "b2c_kernels.h"
 #include "device_math.h"
 
@@ -12,10 +11,7 @@ namespace b2c {
 namespace dev {
 namespace {
 
-constexpr int TILE_W = 16, TILE_PX = TILE_W * TILE_W;
 constexpr int HALO = 5;
-constexpr int STAT_W = TILE_W + 2 * HALO;  // 26
-constexpr int IN_W = STAT_W + 2 * HALO;    // 36
 constexpr float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
 
 struct Gauss11 { float w[11]; };
@@ -33,203 +29,228 @@ __device__ __forceinline__ float gt_effective(uint32_t gp, int c, bool composite
   return g;
 }
 
-__device__ __forceinline__ void store_partial(const b2c_loss_args& a, float t) {
-  if (a.partials)
-    a.partials[blockIdx.y * gridDim.x + blockIdx.x] = t;
-  else if (t != 0.f)
-    atomicAdd(a.loss_accum, t);
+// One wave64 per (strip, channel): a strip is SW = 54 output columns by SH = 35 output rows. Lane l owns
+// statistics column x0 - 5 + l and walks down the rows: each step loads one input row (p, g shifted by the
+// strip's centre values) into a one-row LDS buffer, blurs it horizontally at the lane's column (11 taps,
+// five statistics), pushes the result into an 11-row register ring and, once 11 rows are in, blurs the
+// ring vertically: SSIM and its five partial maps at that row. The partial-map row goes through a second
+// one-row LDS buffer for the horizontal pass of the second blur, whose results fill a second register
+// ring; its vertical pass gives the gradient five rows further down. The loop is unrolled by 11 so that
+// the ring slots are static registers.
+constexpr int SW = 54, SH = 35;
+constexpr int ROWS = SH + 4 * HALO;  // input rows walked per strip: a multiple of 11 (the ring length)
+static_assert(ROWS % 11 == 0, "the row loop is unrolled by the ring length");
+
+struct PixelIn {
+  float p, g;
+};
+
+__device__ __forceinline__ bool in_image(const b2c_loss_args& a, int x, int y) {
+  return x >= 0 && x < a.W && y >= 0 && y < a.H;
 }
 
-__device__ __forceinline__ float block_sum_256(float v, float* s_red) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float t = 0.f;
-  if (threadIdx.x == 0)
-    for (int i = 0; i < TILE_PX / 64; i++) t += s_red[i];
-  return t;
+__device__ __forceinline__ PixelIn load_in(const b2c_loss_args& a, int c, float bg_c, int gx, int gy) {
+  PixelIn v{0.f, 0.f};
+  if (in_image(a, gx, gy)) {
+    const int pix = gy * a.W + gx;
+    v.p = a.pred[(size_t)pix * 4 + c];
+    v.g = gt_effective(a.gt[pix], c, a.composite, bg_c);
+  }
+  return v;
 }
 
-__global__ void __launch_bounds__(TILE_PX) photometric_kernel(b2c_loss_args a, Gauss11 gw, int tiles_x) {
-  __shared__ float s_in[2][IN_W * IN_W];
-  __shared__ float s_h[IN_W * STAT_W * 5];
-  __shared__ float s_v[STAT_W * STAT_W * 5];
-  __shared__ float s_red[TILE_PX / 64];
+// The raw words one step of the walk reads from memory: the input row (this lane's column and, for lanes
+// 0-9, the 10 columns past 64), the SSIM row's weight inputs and L1 operands, and the output row's
+// operands. They are fetched one step ahead so the loads overlap the previous step's arithmetic.
+struct StepRaw {
+  float p_in, p_in2, p_ss, p_out, a_out;
+  uint32_t g_in, g_in2, g_ss, g_out;
+  float w_ss, w_out;
+};
+
+__device__ __forceinline__ StepRaw fetch_step(const b2c_loss_args& a, int c, int x0, int y0, int lane, int r) {
+  StepRaw f{};
+  const int y_in = y0 - 2 * HALO + r, xs = x0 - HALO + lane;
+  const int xi = x0 - 2 * HALO + lane;
+  if (in_image(a, xi, y_in)) {
+    const int pix = y_in * a.W + xi;
+    f.p_in = a.pred[(size_t)pix * 4 + c];
+    f.g_in = a.gt[pix];
+  }
+  if (lane < 2 * HALO && in_image(a, xi + 64, y_in)) {
+    const int pix = y_in * a.W + xi + 64;
+    f.p_in2 = a.pred[(size_t)pix * 4 + c];
+    f.g_in2 = a.gt[pix];
+  }
+  const int ys = y_in - HALO, yo = y_in - 2 * HALO;
+  if (r >= 2 * HALO && in_image(a, xs, ys)) {
+    const int pix = ys * a.W + xs;
+    f.p_ss = a.pred[(size_t)pix * 4 + c];
+    f.g_ss = a.gt[pix];
+    f.w_ss = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
+  }
+  if (r >= 4 * HALO && in_image(a, xs, yo)) {
+    const int pix = yo * a.W + xs;
+    f.p_out = a.pred[(size_t)pix * 4 + c];
+    if (c == 0 && a.alpha_lane) f.a_out = a.pred[(size_t)pix * 4 + 3];
+    f.g_out = a.gt[pix];
+    f.w_out = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
+  }
+  return f;
+}
+
+__global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss11 gw, int strips_x) {
+  __shared__ float s_p[2][64 + 2 * HALO], s_g[2][64 + 2 * HALO];  // one input row (double buffered)
+  __shared__ float s_pm[2][5][64];                                 // one partial-map row (double buffered)
   const int c = blockIdx.y;
-  const int tile = blockIdx.x;
-  const int tx0 = (tile % tiles_x) * TILE_W, ty0 = (tile / tiles_x) * TILE_W;
-  const int tid = threadIdx.x;
+  const int lane = threadIdx.x;
+  const int x0 = (blockIdx.x % strips_x) * SW, y0 = (blockIdx.x / strips_x) * SH;
   const int W = a.W, H = a.H;
-  const float4* pred = reinterpret_cast<const float4*>(a.pred);
   const float bg_c = a.composite ? a.bg[c] : 0.f;
-  // The statistics are accumulated for p - c1 and g - c2, with c1 / c2 the values at the tile centre:
-  // variances and covariances are shift-invariant, and in the gradient 2p*blur(B) - 2*blur(B*mu1) the shift
-  // cancels exactly, so both lose far less to fp32 cancellation than the unshifted form (loss.cu:122-170).
+  const float norm = a.scale / (3.f * (float)W * (float)H);
+  // statistics are accumulated for p - c1 and g - c2 (values at the strip centre): variances and
+  // covariances are shift-invariant, and in the gradient 2p*blur(B) - 2*blur(B*mu1) the shift cancels
+  // exactly, so both lose far less to fp32 cancellation (loss.cu:122-170)
   float c1, c2;
   {
-    const int cpix = min(ty0 + TILE_W / 2, H - 1) * W + min(tx0 + TILE_W / 2, W - 1);
-    const float4 pv = pred[cpix];
-    c1 = c == 0 ? pv.x : (c == 1 ? pv.y : pv.z);
-    c2 = gt_effective(a.gt[cpix], c, a.composite, bg_c);
+    const PixelIn cv = load_in(a, c, bg_c, min(x0 + SW / 2, W - 1), min(y0 + SH / 2, H - 1));
+    c1 = cv.p;
+    c2 = cv.g;
   }
-  float flat_diff = 0.f;
-  for (int i = tid; i < IN_W * IN_W; i += TILE_PX) {
-    const int ly = i / IN_W, lx = i % IN_W;
-    const int gy = ty0 + ly - 2 * HALO, gx = tx0 + lx - 2 * HALO;
-    float p = 0.f, g = 0.f;
-    if (gy >= 0 && gy < H && gx >= 0 && gx < W) {
-      const int pix = gy * W + gx;
-      const float4 pv = pred[pix];
-      p = c == 0 ? pv.x : (c == 1 ? pv.y : pv.z);
-      g = gt_effective(a.gt[pix], c, a.composite, bg_c);
-    }
-    s_in[0][i] = p - c1;
-    s_in[1][i] = g - c2;
-    flat_diff = fmaxf(flat_diff, fabsf(p - g));
-  }
-  if (c == 0 && a.alpha_lane) {
-    const int gy = ty0 + tid / TILE_W, gx = tx0 + tid % TILE_W;
-    if (gy < H && gx < W) {
-      const int pix = gy * W + gx;
-      flat_diff = fmaxf(flat_diff, fabsf(pred[pix].w - gt_channel(a.gt[pix], 3)));
-    }
-  }
-  const float norm = a.scale / (3.f * (float)W * (float)H);
-  if (__syncthreads_or(flat_diff > 0.f) == 0) {
-    const int gy = ty0 + tid / TILE_W, gx = tx0 + tid % TILE_W;
-    float loss_local = 0.f;
-    if (gy < H && gx < W) {
-      const int pix = gy * W + gx;
-      const uint32_t gp = a.gt[pix];
-      const float wp = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
-      const float M = wp * (a.mask ? gt_channel(gp, 3) : 1.f) * norm;
-      loss_local = M * a.ssim_w;  // SSIM == 1 exactly
-      a.v_out[(size_t)pix * 4 + c] = 0.f;
-      if (c == 0) a.v_out[(size_t)pix * 4 + 3] = 0.f;
-    }
-    const float t = block_sum_256(loss_local, s_red);
-    if (tid == 0) store_partial(a, t);
-    return;
-  }
-  // horizontal blur of the five statistics: rows 0..35, output columns 0..25
-  for (int i = tid; i < IN_W * STAT_W; i += TILE_PX) {
-    const int ly = i / STAT_W, ox = i % STAT_W;
-    float sx = 0.f, sx2 = 0.f, sy = 0.f, sy2 = 0.f, sxy = 0.f;
-#pragma unroll
-    for (int d = 0; d < 11; d++) {
-      const float w = gw.w[d];
-      const float x = s_in[0][ly * IN_W + ox + d], y = s_in[1][ly * IN_W + ox + d];
-      sx += w * x; sx2 += w * x * x; sy += w * y; sy2 += w * y * y; sxy += w * x * y;
-    }
-    float* o = s_h + i * 5;
-    o[0] = sx; o[1] = sx2; o[2] = sy; o[3] = sy2; o[4] = sxy;
-  }
-  __syncthreads();
-  // vertical blur -> statistics at 26x26, SSIM, and the partial maps scaled by M * ssim_w
+  const int xs = x0 - HALO + lane;  // this lane's statistics column
+  const bool out_lane = lane >= HALO && lane < HALO + SW;
+  float ring1[11][5];  // horizontal blur of the statistics, by row mod 11
+  float ring2[11][5];  // horizontal blur of the partial maps, by row mod 11
   float loss_local = 0.f;
-  for (int i = tid; i < STAT_W * STAT_W; i += TILE_PX) {
-    const int oy = i / STAT_W, ox = i % STAT_W;
-    float st[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+  StepRaw nxt = fetch_step(a, c, x0, y0, lane, 0);
+  for (int base = 0; base < ROWS; base += 11) {
 #pragma unroll
-    for (int d = 0; d < 11; d++) {
-      const float w = gw.w[d];
-      const float* h = s_h + ((oy + d) * STAT_W + ox) * 5;
-#pragma unroll
-      for (int k = 0; k < 5; k++) st[k] += w * h[k];
-    }
-    const int gy = ty0 + oy - HALO, gx = tx0 + ox - HALO;
-    float A = 0.f, B = 0.f, Bm = 0.f, Cc = 0.f, Cm = 0.f;
-    if (gy >= 0 && gy < H && gx >= 0 && gx < W) {
-      const int pix = gy * W + gx;
-      const uint32_t gp = a.gt[pix];
-      const float wp = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
-      const float M = wp * (a.mask ? gt_channel(gp, 3) : 1.f) * norm;
-      const float mu1 = st[0] + c1, mu2 = st[2] + c2;  // st[0], st[2]: shifted means
-      const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
-      const float s1_raw = st[1] - st[0] * st[0], s2_raw = st[3] - st[2] * st[2];
-      const float sigma1_sq = fmaxf(0.f, s1_raw), sigma2_sq = fmaxf(0.f, s2_raw);
-      const float sigma12 = st[4] - st[0] * st[2];
-      const float A1 = 2.f * mu1 * mu2 + C1, A2 = 2.f * sigma12 + C2;
-      const float B1 = mu1_sq + mu2_sq + C1, B2 = sigma1_sq + sigma2_sq + C2;
-      const float raw = (A1 * A2) / (B1 * B2);
-      const float ssim = fminf(fmaxf(raw, -1.f), 1.f);
-      if (oy >= HALO && oy < HALO + TILE_W && ox >= HALO && ox < HALO + TILE_W) {
-        const float4 pv = pred[pix];
-        const float p = c == 0 ? pv.x : (c == 1 ? pv.y : pv.z);
-        const float g = gt_effective(gp, c, a.composite, bg_c);
-        loss_local += M * (a.l1_w * fabsf(p - g) + a.ssim_w * ssim);
-      }
-      if (raw > -1.f && raw < 1.f) {
-        const float k = M * a.ssim_w;
-        const float inv_BB = 1.f / (B1 * B2);
-        const float d_mu1 = 2.f * mu2 * A2 * inv_BB - 2.f * mu1 * ssim / B1;
-        const float d_s1 = s1_raw > 0.f ? -ssim / B2 : 0.f;
-        const float d_s12 = 2.f * A1 * inv_BB;
-        A = k * d_mu1; B = k * d_s1; Bm = B * st[0]; Cc = k * d_s12; Cm = Cc * st[2];
-      }
-    }
-    float* o = s_v + i * 5;
-    o[0] = A; o[1] = B; o[2] = Bm; o[3] = Cc; o[4] = Cm;
-  }
-  __syncthreads();
-  // second blur, horizontal: rows 0..25, output columns 0..15
-  for (int i = tid; i < STAT_W * TILE_W; i += TILE_PX) {
-    const int ly = i / TILE_W, ox = i % TILE_W;
-    float acc[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < 11; d++) {
-      const float w = gw.w[d];
-      const float* v = s_v + (ly * STAT_W + ox + d) * 5;
-#pragma unroll
-      for (int k = 0; k < 5; k++) acc[k] += w * v[k];
-    }
-    float* o = s_h + i * 5;
-#pragma unroll
-    for (int k = 0; k < 5; k++) o[k] = acc[k];
-  }
-  __syncthreads();
-  // vertical, one output pixel per thread
-  {
-    const int ly = tid / TILE_W, lx = tid % TILE_W;
-    const int gy = ty0 + ly, gx = tx0 + lx;
-    if (gy < H && gx < W) {
-      float acc[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int d = 0; d < 11; d++) {
-        const float w = gw.w[d];
-        const float* v = s_h + ((ly + d) * TILE_W + lx) * 5;
-#pragma unroll
-        for (int k = 0; k < 5; k++) acc[k] += w * v[k];
-      }
-      const int pix = gy * W + gx;
-      // shifted values for the SSIM terms, exact ones for the L1 sign
-      const float ps = s_in[0][(ly + 2 * HALO) * IN_W + lx + 2 * HALO], gs = s_in[1][(ly + 2 * HALO) * IN_W + lx + 2 * HALO];
-      const float4 pv = pred[pix];
-      const float p = c == 0 ? pv.x : (c == 1 ? pv.y : pv.z);
-      const uint32_t gp = a.gt[pix];
-      const float g = gt_effective(gp, c, a.composite, bg_c);
-      const float gt_a = gt_channel(gp, 3);
-      const float wp = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
-      const float M = wp * (a.mask ? gt_a : 1.f) * norm;
-      const float sgn = p > g ? 1.f : (p < g ? -1.f : 0.f);
-      const float grad = M * a.l1_w * sgn + acc[0] + 2.f * ps * acc[1] - 2.f * acc[2] + gs * acc[3] - acc[4];
-      a.v_out[(size_t)pix * 4 + c] = grad * a.grad_scale;
-      if (c == 0) {
-        float va = 0.f;
-        if (a.alpha_lane) {
-          const float da = pred[pix].w - gt_a;
-          const float sa = da > 0.f ? 1.f : (da < 0.f ? -1.f : 0.f);
-          const float Ma = wp * a.match_alpha_weight * a.scale / ((float)W * (float)H);
-          va = Ma * sa * a.grad_scale;
-          loss_local += Ma * fabsf(da);
+    for (int j = 0; j < 11; j++) {
+      const int r = base + j;
+      const int buf = r & 1;
+      const StepRaw cur = nxt;
+      if (r + 1 < ROWS) nxt = fetch_step(a, c, x0, y0, lane, r + 1);
+      // ---- input row y_in: columns x0 - 10 .. x0 + 63
+      const int y_in = y0 - 2 * HALO + r;
+      {
+        const int xi = x0 - 2 * HALO + lane;
+        const bool v1 = in_image(a, xi, y_in);
+        s_p[buf][lane] = (v1 ? cur.p_in : 0.f) - c1;
+        s_g[buf][lane] = (v1 ? gt_effective(cur.g_in, c, a.composite, bg_c) : 0.f) - c2;
+        if (lane < 2 * HALO) {
+          const bool v2 = in_image(a, xi + 64, y_in);
+          s_p[buf][64 + lane] = (v2 ? cur.p_in2 : 0.f) - c1;
+          s_g[buf][64 + lane] = (v2 ? gt_effective(cur.g_in2, c, a.composite, bg_c) : 0.f) - c2;
         }
-        a.v_out[(size_t)pix * 4 + 3] = va;
+      }
+      __syncthreads();
+      {
+        float sx = 0.f, sx2 = 0.f, sy = 0.f, sy2 = 0.f, sxy = 0.f;
+#pragma unroll
+        for (int d = 0; d < 11; d++) {
+          const float w = gw.w[d];
+          const float x = s_p[buf][lane + d], y = s_g[buf][lane + d];
+          const float wx = w * x, wy = w * y;
+          sx += wx; sx2 += wx * x; sy += wy; sy2 += wy * y; sxy += wx * y;
+        }
+        ring1[j][0] = sx; ring1[j][1] = sx2; ring1[j][2] = sy; ring1[j][3] = sy2; ring1[j][4] = sxy;
+      }
+      if (r >= 2 * HALO) {
+        // ---- statistics row ys complete: vertical blur, SSIM, partial maps
+        const int ys = y_in - HALO;
+        float st[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int d = 0; d < 11; d++) {
+          const int slot = (j + 1 + d) % 11;  // oldest row first
+          const float w = gw.w[d];
+#pragma unroll
+          for (int k = 0; k < 5; k++) st[k] += w * ring1[slot][k];
+        }
+        float A = 0.f, B = 0.f, Bm = 0.f, Cc = 0.f, Cm = 0.f;
+        if (in_image(a, xs, ys)) {
+          const float M = cur.w_ss * (a.mask ? gt_channel(cur.g_ss, 3) : 1.f) * norm;
+          const float mu1 = st[0] + c1, mu2 = st[2] + c2;
+          const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
+          const float s1_raw = st[1] - st[0] * st[0], s2_raw = st[3] - st[2] * st[2];
+          const float sigma1_sq = fmaxf(0.f, s1_raw), sigma2_sq = fmaxf(0.f, s2_raw);
+          const float sigma12 = st[4] - st[0] * st[2];
+          const float A1 = 2.f * mu1 * mu2 + C1, A2 = 2.f * sigma12 + C2;
+          const float B1 = mu1_sq + mu2_sq + C1, B2 = sigma1_sq + sigma2_sq + C2;
+          const float raw = (A1 * A2) / (B1 * B2);
+          const float ssim = fminf(fmaxf(raw, -1.f), 1.f);
+          if (out_lane && ys >= y0 && ys < y0 + SH) {
+            const float g = gt_effective(cur.g_ss, c, a.composite, bg_c);
+            loss_local += M * (a.l1_w * fabsf(cur.p_ss - g) + a.ssim_w * ssim);
+          }
+          if (raw > -1.f && raw < 1.f) {
+            const float k = M * a.ssim_w;
+            const float inv_BB = 1.f / (B1 * B2);
+            const float d_mu1 = 2.f * mu2 * A2 * inv_BB - 2.f * mu1 * ssim / B1;
+            const float d_s1 = s1_raw > 0.f ? -ssim / B2 : 0.f;
+            const float d_s12 = 2.f * A1 * inv_BB;
+            A = k * d_mu1; B = k * d_s1; Bm = B * st[0]; Cc = k * d_s12; Cm = Cc * st[2];
+          }
+        }
+        s_pm[buf][0][lane] = A; s_pm[buf][1][lane] = B; s_pm[buf][2][lane] = Bm;
+        s_pm[buf][3][lane] = Cc; s_pm[buf][4][lane] = Cm;
+        __syncthreads();
+        // ---- horizontal pass of the second blur at output column x0 + lane - 5
+        const int j2 = (j + 1) % 11;  // slot of partial-map row ys (stats row index r - 10)
+#pragma unroll
+        for (int k = 0; k < 5; k++) ring2[j2][k] = 0.f;
+        if (out_lane) {
+#pragma unroll
+          for (int d = 0; d < 11; d++) {
+            const float w = gw.w[d];
+#pragma unroll
+            for (int k = 0; k < 5; k++) ring2[j2][k] += w * s_pm[buf][k][lane - HALO + d];
+          }
+        }
+        if (r >= 4 * HALO) {
+          // ---- output row yo = ys - 5 complete: vertical pass, gradient
+          const int yo = ys - HALO, xo = xs;
+          float acc[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int d = 0; d < 11; d++) {
+            const int slot = (j2 + 1 + d) % 11;
+            const float w = gw.w[d];
+#pragma unroll
+            for (int k = 0; k < 5; k++) acc[k] += w * ring2[slot][k];
+          }
+          if (out_lane && yo < H && xo < W) {
+            const int pix = yo * W + xo;
+            const float p = cur.p_out, g = gt_effective(cur.g_out, c, a.composite, bg_c);
+            const float ps = p - c1, gs = g - c2;
+            const float gt_a = gt_channel(cur.g_out, 3);
+            const float M = cur.w_out * (a.mask ? gt_a : 1.f) * norm;
+            const float sgn = p > g ? 1.f : (p < g ? -1.f : 0.f);
+            const float grad = M * a.l1_w * sgn + acc[0] + 2.f * ps * acc[1] - 2.f * acc[2] + gs * acc[3] - acc[4];
+            a.v_out[(size_t)pix * 4 + c] = grad * a.grad_scale;
+            if (c == 0) {
+              float va = 0.f;
+              if (a.alpha_lane) {
+                const float da = cur.a_out - gt_a;
+                const float sa = da > 0.f ? 1.f : (da < 0.f ? -1.f : 0.f);
+                const float Ma = cur.w_out * a.match_alpha_weight * a.scale / ((float)W * (float)H);
+                va = Ma * sa * a.grad_scale;
+                loss_local += Ma * fabsf(da);
+              }
+              a.v_out[(size_t)pix * 4 + 3] = va;
+            }
+          }
+        }
       }
     }
   }
-  const float t = block_sum_256(loss_local, s_red);
-  if (tid == 0) store_partial(a, t);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) loss_local += __shfl_xor(loss_local, o);
+  if (lane == 0) {
+    const int idx = blockIdx.y * gridDim.x + blockIdx.x;
+    if (a.partials)
+      a.partials[idx] = loss_local;
+    else if (loss_local != 0.f)
+      atomicAdd(a.loss_accum, loss_local);
+  }
 }
 
 // Fixed-order double-precision sum of the per-workgroup partials into loss_accum[0].
@@ -270,14 +291,14 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
     sum += w[i];
   }
   for (int i = 0; i < 11; i++) g.w[i] = (float)(w[i] / sum);
-  const int tiles_x = (a->W + TILE_W - 1) / TILE_W, tiles_y = (a->H + TILE_W - 1) / TILE_W;
-  photometric_kernel<<<dim3(tiles_x * tiles_y, 3), dim3(TILE_PX), 0, stream>>>(*a, g, tiles_x);
-  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, tiles_x * tiles_y * 3, a->loss_accum);
+  const int strips_x = (a->W + SW - 1) / SW, strips_y = (a->H + SH - 1) / SH;
+  photometric_kernel<<<dim3(strips_x * strips_y, 3), dim3(64), 0, stream>>>(*a, g, strips_x);
+  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, strips_x * strips_y * 3, a->loss_accum);
   return (int)hipGetLastError();
 }
 
 extern "C" size_t b2c_loss_partials(int W, int H) {
-  return (size_t)((W + TILE_W - 1) / TILE_W) * ((H + TILE_W - 1) / TILE_W) * 3;
+  return (size_t)((W + SW - 1) / SW) * ((H + SH - 1) / SH) * 3;
 }
 
 extern "C" int b2c_hip_accumulate_loss(float* loss_accum, hipStream_t stream) {

@@ -1,7 +1,7 @@
 // Projection (replaces src/gpu/project.cu:8-126): one thread per splat, EWA projection, SH colour, exact
 // ellipse/8x8-tile test over the splat's tile bounding box. Splats with more than 32 bbox tiles are not
 // counted inline (one thread walking hundreds of tiles stalls its whole wave): they are appended to a
-// list and counted by one wave64 each in project_big_kernel, 64 tiles per step.
+// list and counted in parallel chunks of their bbox, one wave per chunk.
 #pragma clang fp contract(off)
 #include "b2c_kernels.h"
 #include "device_math.h"
@@ -91,36 +91,96 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
   }
 }
 
-// One wave64 per big splat: count the tiles of its bbox that pass tile_hit, 64 tiles per step in row-major
-// order. The grid is fixed; waves stride over the device-side list length.
-__global__ void __launch_bounds__(256) project_big_kernel(b2c_project_args a) {
+// Big splats (bbox over 32 tiles) are counted in parallel chunks of their row-major bbox order: an entry
+// of the big list with area A gets ceil(A / len) chunks of len tiles, len = 64 up to 64 * B2C_BIG_CHUNKS
+// tiles and longer (a multiple of 64) beyond, so no splat has more than B2C_BIG_CHUNKS chunks. Each chunk
+// is one work item of a flat item list (filled in any order: items are independent), processed by one
+// wave that tests its tiles 64 at a time. A splat spanning thousands of tiles is spread over up to
+// B2C_BIG_CHUNKS waves instead of serialising one. big_setup_kernel records each entry's bbox and chunk
+// length and appends its items, big_count_kernel the per-chunk hits, big_sum_kernel the per-chunk
+// exclusive offsets (used by the emit) and the tile count.
+__device__ __forceinline__ uint4 big_bbox_info(const b2c_project_args& a, uint32_t i) {
+  const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
+  const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
+  float ex, ey;
+  extent_from_conic(Sym2{p0.z, p0.w, p1.x}, p1.w, ex, ey);
+  const TileBox bb = tile_bbox(p0.x, p0.y, ex, ey, a.tiles_x, a.tiles_y);
+  const uint32_t bw = (uint32_t)(bb.max_x - bb.min_x);
+  const uint32_t area = bw * (uint32_t)(bb.max_y - bb.min_y);
+  const uint32_t per = (area + B2C_BIG_CHUNKS - 1) / B2C_BIG_CHUNKS;
+  const uint32_t len = per <= 64u ? 64u : ((per + 63u) / 64u) * 64u;
+  return make_uint4((uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), bw, area, len);
+}
+
+__device__ __forceinline__ uint32_t big_nchunks(uint4 info) { return (info.z + info.w - 1u) / info.w; }
+
+__global__ void __launch_bounds__(256) big_setup_kernel(b2c_project_args a) {
+  const uint32_t e = blockIdx.x * 256u + threadIdx.x;
+  const bool live = e < *a.big_count;
+  uint32_t nch = 0;
+  if (live) {
+    const uint4 info = big_bbox_info(a, a.big_list[e]);
+    reinterpret_cast<uint4*>(a.big_info)[e] = info;
+    nch = big_nchunks(info);
+  }
+  // wave-aggregated allocation of this wave's items
+  uint32_t incl = nch;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(incl, o);
+    if (lane_id() >= o) incl += t;
+  }
+  const uint32_t total = __shfl(incl, 63);
+  uint32_t base = 0;
+  if (lane_id() == 63 && total) base = atomicAdd(a.big_items_count, total);
+  base = __shfl(base, 63) + incl - nch;
+  for (uint32_t k = 0; k < nch; k++) a.big_items[base + k] = (e << 5) | k;
+}
+
+// Hits of tiles [k * len, min((k + 1) * len, area)) of entry e's bbox, tested 64 at a time.
+__global__ void __launch_bounds__(256) big_count_kernel(b2c_project_args a) {
   const int lane = lane_id();
   const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
   const uint32_t nwaves = (gridDim.x * 256u) >> 6;
-  const uint32_t count = *a.big_count;
-  for (uint32_t e = wave; e < count; e += nwaves) {
+  const uint32_t items = *a.big_items_count;
+  for (uint32_t it = wave; it < items; it += nwaves) {
+    const uint32_t code = a.big_items[it];
+    const uint32_t e = code >> 5, k = code & 31u;
+    const uint4 info = reinterpret_cast<const uint4*>(a.big_info)[e];
     const uint32_t i = a.big_list[e];
+    const uint32_t begin = k * info.w, end = min(begin + info.w, info.z);
     const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
     const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
-    Sym2 conic{p0.z, p0.w, p1.x};
-    float ex, ey;
-    extent_from_conic(conic, p1.w, ex, ey);
-    TileBox bb = tile_bbox(p0.x, p0.y, ex, ey, a.tiles_x, a.tiles_y);
-    const int bw = bb.max_x - bb.min_x;
-    const int area = bw * (bb.max_y - bb.min_y);
+    const Sym2 conic{p0.z, p0.w, p1.x};
+    const int min_x = (int)(info.x & 0xFFFFu), min_y = (int)(info.x >> 16), bw = (int)info.y;
     uint32_t hits = 0;
-    for (int b0 = 0; b0 < area; b0 += 64) {
-      const int b = b0 + lane;
+    for (uint32_t b0 = begin; b0 < end; b0 += 64) {
+      const uint32_t b = b0 + (uint32_t)lane;
       bool h = false;
-      if (b < area) {
-        const int tx = bb.min_x + b % bw, ty = bb.min_y + b / bw;
+      if (b < end) {
+        const int tx = min_x + (int)(b % (uint32_t)bw), ty = min_y + (int)(b / (uint32_t)bw);
         const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
         h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, p0.x, p0.y, conic, p1.w);
       }
       hits += popc64(ballot64(h));
     }
-    if (lane == 0) a.tile_count[i] = hits;
+    if (lane == 0) a.big_chunk[(size_t)e * B2C_BIG_CHUNKS + k] = hits;
   }
+}
+
+// Per entry: exclusive offsets of its chunks (in place) and the splat's tile count.
+__global__ void __launch_bounds__(256) big_sum_kernel(b2c_project_args a) {
+  const uint32_t e = blockIdx.x * 256u + threadIdx.x;
+  if (e >= *a.big_count) return;
+  const uint32_t nch = big_nchunks(reinterpret_cast<const uint4*>(a.big_info)[e]);
+  uint32_t* c = a.big_chunk + (size_t)e * B2C_BIG_CHUNKS;
+  uint32_t run = 0;
+  for (uint32_t k = 0; k < nch; k++) {
+    const uint32_t h = c[k];
+    c[k] = run;
+    run += h;
+  }
+  a.tile_count[a.big_list[e]] = run;
 }
 
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, size_t n) {
@@ -147,6 +207,7 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
   int e = b2c_hip_fill_u32(a->big_count, 0u, 1, stream);
+  if (!e && a->big_items_count) e = b2c_hip_fill_u32(a->big_items_count, 0u, 1, stream);
   if (e) return e;
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);
   switch (a->degree) {
@@ -158,6 +219,10 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   }
   e = (int)hipGetLastError();
   if (e) return e;
-  project_big_kernel<<<dim3(512), dim3(256), 0, stream>>>(*a);
+  if (!a->big_info || !a->big_chunk || !a->big_items || !a->big_items_count) return (int)hipErrorInvalidValue;
+  const dim3 per_entry((unsigned)((a->n + 255) / 256));
+  big_setup_kernel<<<per_entry, dim3(256), 0, stream>>>(*a);
+  big_count_kernel<<<dim3(B2C_BIG_GRID), dim3(256), 0, stream>>>(*a);
+  big_sum_kernel<<<per_entry, dim3(256), 0, stream>>>(*a);
   return (int)hipGetLastError();
 }

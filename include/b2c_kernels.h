@@ -56,7 +56,16 @@ typedef struct b2c_project_args {
   float* max_screen;   /* [n] or NULL: max(., max(ex/W, ey/H)) (project.cu:82-83) */
   uint32_t* big_list;  /* [n] scratch: splats whose bbox exceeds 32 tiles */
   uint32_t* big_count; /* [1] scratch counter */
+  uint32_t* big_info;  /* [n][4] scratch: per big-list entry, bbox origin, width, area, chunk length */
+  uint32_t* big_chunk; /* [n][B2C_BIG_CHUNKS] scratch: per-chunk exclusive hit offsets of each entry */
+  uint32_t* big_items; /* [n][B2C_BIG_CHUNKS] scratch: work items (entry << 5 | chunk) */
+  uint32_t* big_items_count; /* [1] scratch counter */
 } b2c_project_args;
+
+/* At most this many chunks per big splat (one wave each); and the grid (workgroups of 256) that the
+ * chunk kernels stride over. */
+#define B2C_BIG_CHUNKS 32
+#define B2C_BIG_GRID 8192
 int b2c_hip_project(const b2c_project_args* a, hipStream_t stream);
 
 /* ---- binning (src/gpu/binning.cu:10-143) ---- */
@@ -94,8 +103,10 @@ int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t* tile_count
                         uint32_t* total_dev, void* temp, size_t temp_bytes, hipStream_t stream);
 
 /* emit_kernel (binning.cu:25-93): intersections in depth order, key = tile id, val = splat index. Small
- * splats (hit mask) are emitted by a wave-cooperative coalesced sweep; splats with more than 32 bbox tiles
- * by one wave each over their bbox in row-major order. Slots missing from a big splat get key = n_tiles. */
+ * splats (hit mask) are emitted by one thread each, walking the set bits of the mask; splats with more
+ * than 32 bbox tiles by one wave per chunk of their bbox (the chunks b2c_hip_project counted), in
+ * row-major order. Slots a big splat does not fill get key = n_tiles (cannot happen when the counts come
+ * from b2c_hip_project; kept as the reference's guard). */
 typedef struct b2c_emit_args {
   int n;
   const uint32_t* order, *tile_count, *tile_off, *hit_info;
@@ -104,6 +115,8 @@ typedef struct b2c_emit_args {
   uint32_t cap;
   uint32_t* keys, *vals;
   const uint32_t* big_list, *big_count; /* from b2c_hip_project */
+  const uint32_t* big_info, *big_chunk; /* from b2c_hip_project */
+  const uint32_t* big_items, *big_items_count; /* from b2c_hip_project */
   uint32_t* big_base;                   /* [n] scratch: first slot of each big splat */
 } b2c_emit_args;
 int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream);
