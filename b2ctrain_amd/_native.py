@@ -55,8 +55,9 @@ class StepTimes(C.Structure):
 # Every symbol include/b2c.h and include/b2c_kernels.h declare.
 EXPORTS = [
     "b2c_last_error", "b2c_get_device_count", "b2c_camera_gpu_from", "b2c_model_create", "b2c_model_destroy",
-    "b2c_model_upload", "b2c_model_read", "b2c_ctx_create", "b2c_ctx_destroy", "b2c_ctx_setup", "b2c_ctx_info_get",
-    "b2c_ctx_read", "b2c_ctx_write", "b2c_ctx_zero", "b2c_ctx_synchronize", "b2c_ctx_stream", "b2c_view_create",
+    "b2c_model_upload", "b2c_model_read", "b2c_model_device_ptr", "b2c_model_sh_view", "b2c_ctx_create",
+    "b2c_ctx_destroy", "b2c_ctx_setup", "b2c_ctx_info_get", "b2c_ctx_read", "b2c_ctx_device_ptr", "b2c_ctx_write",
+    "b2c_ctx_zero", "b2c_ctx_synchronize", "b2c_ctx_stream", "b2c_view_create",
     "b2c_view_destroy", "b2c_render_forward", "b2c_project_splats", "b2c_bin_and_sort", "b2c_rasterize_forward",
     "b2c_photometric_loss", "b2c_accumulate_loss", "b2c_rasterize_backward", "b2c_optimizer_grad", "b2c_train_step",
     # launcher layer
@@ -94,6 +95,8 @@ def lib():
         L.b2c_ctx_synchronize.argtypes = [p]
         L.b2c_ctx_stream.argtypes = [p]
         L.b2c_ctx_stream.restype = p
+        L.b2c_ctx_device_ptr.argtypes = [p, C.c_char_p, C.POINTER(p), C.POINTER(C.c_size_t)]
+        L.b2c_model_device_ptr.argtypes = [p, C.c_char_p, C.POINTER(p), C.POINTER(C.c_size_t)]
         L.b2c_view_create.restype = p
         L.b2c_view_create.argtypes = [i, i, p, p]
         L.b2c_view_destroy.argtypes = [p]
@@ -303,6 +306,13 @@ class Renderer:
         out = np.empty((self.n, 4) if field in ("pos_op", "quat", "lscale") else (self.n,), np.float32)
         check(self.L.b2c_model_read(self.model, field.encode(), _ptr(out), out.nbytes), f"model_read {field}")
         return out
+
+    def device_ptr(self, field, model=False):
+        """Device address and byte size of a context (or model) buffer."""
+        ptr, size = C.c_void_p(), C.c_size_t()
+        fn = lib().b2c_model_device_ptr if model else lib().b2c_ctx_device_ptr
+        check(fn(self.model if model else self.ctx, field.encode(), C.byref(ptr), C.byref(size)), f"device_ptr {field}")
+        return ptr.value, size.value
 
     def sync(self):
         check(self.L.b2c_ctx_synchronize(self.ctx), "synchronize")

@@ -110,6 +110,12 @@ Field ctx_field(b2c_ctx* c, const std::string& name) {
       {"big_list", {x.big_list.ptr, n * 4}},
       {"big_base", {x.big_base.ptr, n * 4}},
       {"counters", {x.counters.ptr, x.counters.bytes()}},
+      {"slot_sorted", {x.slot_sorted.ptr, M * 4}},
+      {"tile_end", {x.tile_end.ptr, ((size_t)x.n_tiles + 1) * 4}},
+      {"isect_rows", {x.isect_rows.ptr, M * 48}},
+      {"depth_keys", {x.depth_keys.ptr, n * 4}},
+      {"order_in", {x.order_in.ptr, n * 4}},
+      {"sort_tmp", {x.sort_tmp.ptr, x.sort_tmp.bytes()}},
   };
   auto it = f.find(name);
   if (it == f.end()) throw std::runtime_error("unknown context field: " + name);
@@ -150,22 +156,41 @@ int b2c_model_upload(b2c_model* m, int n, int degree, int sh_fp16, const float* 
   });
 }
 
+namespace {
+Field model_field(const b2c_model* m, const std::string& name) {
+  const b2c::Model& x = m->m;
+  const size_t n = (size_t)x.n;
+  std::map<std::string, Field> f = {
+      {"pos_op", {x.pos_op.ptr, n * 16}},         {"quat", {x.quat.ptr, n * 16}},
+      {"lscale", {x.lscale.ptr, n * 16}},         {"vis_weight", {x.vis_weight.ptr, n * 4}},
+      {"vis_count", {x.vis_count.ptr, n * 4}},    {"refine_norm", {x.refine_norm.ptr, n * 4}},
+      {"max_screen", {x.max_screen.ptr, n * 4}},
+  };
+  auto it = f.find(name);
+  if (it == f.end()) throw std::runtime_error("unknown model field: " + name);
+  return it->second;
+}
+}  // namespace
+
 int b2c_model_read(const b2c_model* m, const char* field, void* host, size_t bytes) {
   return guarded([&] {
-    const b2c::Model& x = m->m;
-    const size_t n = (size_t)x.n;
-    std::map<std::string, Field> f = {
-        {"pos_op", {x.pos_op.ptr, n * 16}},         {"quat", {x.quat.ptr, n * 16}},
-        {"lscale", {x.lscale.ptr, n * 16}},         {"vis_weight", {x.vis_weight.ptr, n * 4}},
-        {"vis_count", {x.vis_count.ptr, n * 4}},    {"refine_norm", {x.refine_norm.ptr, n * 4}},
-        {"max_screen", {x.max_screen.ptr, n * 4}},
-    };
-    auto it = f.find(field);
-    if (it == f.end()) throw std::runtime_error(std::string("unknown model field: ") + field);
-    if (bytes > it->second.bytes) throw std::runtime_error(std::string("model_read: too many bytes for ") + field);
+    const Field f = model_field(m, field);
+    if (bytes > f.bytes) throw std::runtime_error(std::string("model_read: too many bytes for ") + field);
     HIP_CHECK(hipDeviceSynchronize());
-    HIP_CHECK(hipMemcpy(host, it->second.ptr, bytes, hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(host, f.ptr, bytes, hipMemcpyDeviceToHost));
   });
+}
+
+int b2c_model_device_ptr(const b2c_model* m, const char* field, void** ptr, size_t* bytes) {
+  return guarded([&] {
+    const Field f = model_field(m, field);
+    *ptr = f.ptr;
+    if (bytes) *bytes = f.bytes;
+  });
+}
+
+int b2c_model_sh_view(const b2c_model* m, b2c_sh_view* out) {
+  return guarded([&] { *out = m->m.sh().view(); });
 }
 
 b2c_ctx* b2c_ctx_create(void) {
@@ -200,6 +225,14 @@ int b2c_ctx_info_get(const b2c_ctx* c, b2c_ctx_info* o) {
   o->W = x.W; o->H = x.H; o->tiles_x = x.tiles_x; o->tiles_y = x.tiles_y; o->n_tiles = x.n_tiles;
   o->tile_bits = x.tile_bits; o->num_isect = x.num_isect; o->isect_cap = x.isect_cap;
   return 0;
+}
+
+int b2c_ctx_device_ptr(b2c_ctx* c, const char* field, void** ptr, size_t* bytes) {
+  return guarded([&] {
+    const Field f = ctx_field(c, field);
+    *ptr = f.ptr;
+    if (bytes) *bytes = f.bytes;
+  });
 }
 
 int b2c_ctx_read(b2c_ctx* c, const char* field, void* host, size_t bytes) {

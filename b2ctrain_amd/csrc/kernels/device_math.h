@@ -176,6 +176,21 @@ struct ShView {
     size_t o = (size_t)(lane - 3) * stride + i;
     return hi32 ? hi32[o] : (float)hi16[o];
   }
+  // All 3 (DEG + 1)^2 coefficients of splat i, issued back to back (one memory round trip); lanes beyond
+  // the active degree are loaded too and weighted by zero by the caller.
+  template <int DEG>
+  __device__ __forceinline__ void load_all(int i, float* c) const {
+    constexpr int L = 3 * (DEG + 1) * (DEG + 1);
+#pragma unroll
+    for (int k = 0; k < 3; k++) c[k] = dc[(size_t)k * stride + i];
+    if (hi32) {
+#pragma unroll
+      for (int k = 3; k < L; k++) c[k] = hi32[(size_t)(k - 3) * stride + i];
+    } else {
+#pragma unroll
+      for (int k = 3; k < L; k++) c[k] = (float)hi16[(size_t)(k - 3) * stride + i];
+    }
+  }
 };
 
 // Row-major 3x3 helpers and the quaternion rotation (util.cuh:218-243).

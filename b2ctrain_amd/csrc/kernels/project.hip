@@ -11,12 +11,30 @@ namespace b2c {
 namespace dev {
 namespace {
 
-constexpr int PROJ_BLOCK = 256;
+constexpr int PROJ_BLOCK = 1024;  // one big-list append per workgroup (same-address atomics serialise)
+
+// Tile tests of the wave's small splats (bbox of at most 32 tiles) are shared out over all 64 lanes: the
+// splats' bbox areas are prefix-summed across the wave, test t goes to lane t mod 64, which finds the
+// owning splat by binary search over the prefix and sets the hit bit in the owner's mask in LDS. A wave
+// then costs ceil(sum of areas / 64) tile tests per lane instead of its largest bbox.
+struct WaveRec {
+  float mx, my, c00, c01, c11, power;
+  uint32_t origin;  // min_x | min_y << 16
+  uint32_t bw;
+};
 
 template <int DEG>
 __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a) {
+  __shared__ WaveRec s_rec[PROJ_BLOCK];
+  __shared__ uint32_t s_incl[PROJ_BLOCK];
+  __shared__ uint32_t s_mask[PROJ_BLOCK];
   const int i = blockIdx.x * PROJ_BLOCK + threadIdx.x;
+  const int lane = lane_id();
+  const int wbase = threadIdx.x & ~63;
   bool big = false;
+  bool small = false;
+  uint32_t area = 0;
+  TileBox bb{0, 0, 0, 0};
   if (i < a.n) {
     const float4 po = reinterpret_cast<const float4*>(a.pos_op)[i];
     const float4 q = reinterpret_cast<const float4*>(a.quat)[i];
@@ -26,27 +44,15 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       a.tile_count[i] = 0u;
     } else {
       const float power = det_logf(pr.opac * 255.f);
-      TileBox bb = tile_bbox(pr.mean2d[0], pr.mean2d[1], pr.ex, pr.ey, a.tiles_x, a.tiles_y);
+      bb = tile_bbox(pr.mean2d[0], pr.mean2d[1], pr.ex, pr.ey, a.tiles_x, a.tiles_y);
       const int bw = bb.max_x - bb.min_x, bh = bb.max_y - bb.min_y;
       big = bw * bh > 32;
-      uint32_t hits = 0, mask = 0;
-      if (!big) {
-        int bit = 0;
-        for (int ty = bb.min_y; ty < bb.max_y; ty++)
-          for (int tx = bb.min_x; tx < bb.max_x; tx++, bit++) {
-            float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
-            if (tile_hit(rx, ry, rx + RT_W, ry + RT_W, pr.mean2d[0], pr.mean2d[1], pr.conic, power)) {
-              hits++;
-              mask |= 1u << bit;
-            }
-          }
-        a.tile_count[i] = hits;
-        // A 32-tile bbox with every tile hit encodes to the same mask as "recompute" (0xFFFFFFFF); the
-        // emit then treats it as a big splat (binning.cu:37,75), so it goes on the big list too.
-        big = mask == 0xFFFFFFFFu;
+      small = !big;
+      if (small) {
+        area = (uint32_t)(bw * bh);
+        s_rec[threadIdx.x] = WaveRec{pr.mean2d[0], pr.mean2d[1], pr.conic.c00, pr.conic.c01, pr.conic.c11, power,
+                                     (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), (uint32_t)bw};
       }
-      reinterpret_cast<uint2*>(a.hit_info)[i] =
-          make_uint2(big ? 0xFFFFFFFFu : mask, (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)bw << 24));
       // SH colour, view direction camera -> splat (project.cu:44-55)
       float vx = po.x - a.cam.pos[0], vy = po.y - a.cam.pos[1], vz = po.z - a.cam.pos[2];
       float vl = sqrtf(vx * vx + vy * vy + vz * vz);
@@ -56,14 +62,16 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       float b[K];
       sh_basis<DEG>(vx, vy, vz, b);
       const int ka = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
-      ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
-      float cr = sv.get(0, i) * b[0], cg = sv.get(1, i) * b[0], cb = sv.get(2, i) * b[0];
+      const ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
+      float coef[3 * K];
+      sv.load_all<DEG>(i, coef);
+      float cr = coef[0] * b[0], cg = coef[1] * b[0], cb = coef[2] * b[0];
 #pragma unroll
       for (int k = 1; k < K; k++) {
-        if (k < ka) {
-          cr = cr + sv.get(k * 3, i) * b[k];
-          cg = cg + sv.get(k * 3 + 1, i) * b[k];
-          cb = cb + sv.get(k * 3 + 2, i) * b[k];
+        if (k < ka) {  // uniform: the active degree
+          cr = cr + coef[k * 3] * b[k];
+          cg = cg + coef[k * 3 + 1] * b[k];
+          cb = cb + coef[k * 3 + 2] * b[k];
         }
       }
       cr = cr + 0.5f; cg = cg + 0.5f; cb = cb + 0.5f;
@@ -80,15 +88,70 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       }
     }
   }
-  // wave-aggregated append of big splats
-  const uint64_t bm = ballot64(big);
-  if (bm) {
-    const int leader = __ffsll((unsigned long long)bm) - 1;
-    uint32_t base = 0;
-    if (lane_id() == leader) base = atomicAdd(a.big_count, popc64(bm));
-    base = __shfl(base, leader);
-    if (big) a.big_list[base + mbcnt64(bm)] = (uint32_t)i;
+  // ---- wave-cooperative tile tests of the small splats
+  uint32_t incl = area;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
   }
+  const uint32_t total = __shfl(incl, 63);
+  s_incl[threadIdx.x] = incl;
+  s_mask[threadIdx.x] = 0u;
+  __syncthreads();
+  for (uint32_t t0 = 0; t0 < total; t0 += 64) {
+    const uint32_t t = t0 + (uint32_t)lane;
+    if (t < total) {
+      int lo = 0, hi = 63;  // owner: the first lane whose inclusive prefix exceeds t
+#pragma unroll
+      for (int step = 0; step < 6; step++) {
+        const int mid = (lo + hi) >> 1;
+        if (s_incl[wbase + mid] > t) hi = mid; else lo = mid + 1;
+      }
+      const int owner = lo;
+      const WaveRec rec = s_rec[wbase + owner];
+      const uint32_t prev = owner == 0 ? 0u : s_incl[wbase + owner - 1];
+      const uint32_t bit = t - prev;
+      const uint32_t row = bit / rec.bw;
+      const int tx = (int)(rec.origin & 0xFFFFu) + (int)(bit - row * rec.bw);
+      const int ty = (int)(rec.origin >> 16) + (int)row;
+      const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
+      if (tile_hit(rx, ry, rx + RT_W, ry + RT_W, rec.mx, rec.my, Sym2{rec.c00, rec.c01, rec.c11}, rec.power))
+        atomicOr(&s_mask[wbase + owner], 1u << bit);
+    }
+  }
+  __syncthreads();
+  if (small) {
+    const uint32_t mask = s_mask[threadIdx.x];
+    a.tile_count[i] = (uint32_t)__popc(mask);
+    // A 32-tile bbox with every tile hit encodes to the same mask as "recompute" (0xFFFFFFFF); the
+    // emit then treats it as a big splat (binning.cu:37,75), so it goes on the big list too.
+    big = mask == 0xFFFFFFFFu;
+    reinterpret_cast<uint2*>(a.hit_info)[i] =
+        make_uint2(mask, (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)(bb.max_x - bb.min_x) << 24));
+  } else if (big) {
+    reinterpret_cast<uint2*>(a.hit_info)[i] =
+        make_uint2(0xFFFFFFFFu, (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)(bb.max_x - bb.min_x) << 24));
+  }
+  // workgroup-aggregated append of big splats: one device-scope atomic per workgroup (contended atomics
+  // on one address are serialised at the memory side and cost ~10 ns each)
+  __shared__ uint32_t s_wcount[PROJ_BLOCK / 64];
+  __shared__ uint32_t s_base;
+  const uint64_t bm = ballot64(big);
+  const int w = threadIdx.x >> 6;
+  if (lane == 0) s_wcount[w] = popc64(bm);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t tot = 0;
+    for (int k = 0; k < PROJ_BLOCK / 64; k++) {
+      const uint32_t c = s_wcount[k];
+      s_wcount[k] = tot;
+      tot += c;
+    }
+    s_base = tot ? atomicAdd(a.big_count, tot) : 0u;
+  }
+  __syncthreads();
+  if (big) a.big_list[s_base + s_wcount[w] + mbcnt64(bm)] = (uint32_t)i;
 }
 
 // Big splats (bbox over 32 tiles) are counted in parallel chunks of their row-major bbox order: an entry
@@ -116,24 +179,38 @@ __device__ __forceinline__ uint32_t big_nchunks(uint4 info) { return (info.z + i
 
 __global__ void __launch_bounds__(256) big_setup_kernel(b2c_project_args a) {
   const uint32_t e = blockIdx.x * 256u + threadIdx.x;
-  const bool live = e < *a.big_count;
+  const uint32_t count = *a.big_count;
+  if (blockIdx.x * 256u >= count) return;  // whole workgroup past the list
+  const bool live = e < count;
   uint32_t nch = 0;
   if (live) {
     const uint4 info = big_bbox_info(a, a.big_list[e]);
     reinterpret_cast<uint4*>(a.big_info)[e] = info;
     nch = big_nchunks(info);
   }
-  // wave-aggregated allocation of this wave's items
+  // workgroup-aggregated allocation of the items (one device-scope atomic per workgroup)
+  __shared__ uint32_t s_wsum[4];
+  __shared__ uint32_t s_base;
   uint32_t incl = nch;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const uint32_t t = __shfl_up(incl, o);
     if (lane_id() >= o) incl += t;
   }
-  const uint32_t total = __shfl(incl, 63);
-  uint32_t base = 0;
-  if (lane_id() == 63 && total) base = atomicAdd(a.big_items_count, total);
-  base = __shfl(base, 63) + incl - nch;
+  const int w = threadIdx.x >> 6;
+  if (lane_id() == 63) s_wsum[w] = incl;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t tot = 0;
+    for (int k = 0; k < 4; k++) {
+      const uint32_t c = s_wsum[k];
+      s_wsum[k] = tot;
+      tot += c;
+    }
+    s_base = tot ? atomicAdd(a.big_items_count, tot) : 0u;
+  }
+  __syncthreads();
+  const uint32_t base = s_base + s_wsum[w] + incl - nch;
   for (uint32_t k = 0; k < nch; k++) a.big_items[base + k] = (e << 5) | k;
 }
 

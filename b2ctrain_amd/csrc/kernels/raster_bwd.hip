@@ -509,28 +509,40 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
                                          (heads ? W_HAS_HEAD : 0u);
 }
 
+// One wave per window: the window where a crossing run starts sums the partials of the windows the run
+// covers (its last window follows from the run length), 64 windows per step across the lanes, in a fixed
+// reduction order, and finishes the run.
 __global__ void __launch_bounds__(256) isect_fixup_kernel(b2c_raster_bwd_args a) {
   const uint32_t nwin = (a.num_isect + 63u) / 64u;
-  const uint32_t w = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   if (w >= nwin) return;
   const uint32_t f = a.isect_part_flags[w];
   // owner: the last run of window w starts in w (w has a head) and continues into w + 1
   if (!(f & W_CONT_AFTER) || !(f & W_HAS_HEAD)) return;
   const float4* part = reinterpret_cast<const float4*>(a.isect_part);
   const uint32_t run = a.isect_vals[w * 64u + 63u];
-  // the run covers emit positions [head, head + tile_count), so its last window is known up front and the
-  // partial sums of the windows it covers can be loaded independently
+  // the run covers emit positions [head, head + tile_count)
   const uint32_t head = __float_as_uint(part[(size_t)w * 6 + 5].w);
-  const uint32_t last_win = (head + a.tile_count[run] - 1u) / 64u;
+  const uint32_t last_win = min((head + a.tile_count[run] - 1u) / 64u, nwin - 1u);
   float v[RED_VALS];
 #pragma unroll
   for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
-  add_part(part + (size_t)w * 6 + 3, v);
-#pragma unroll 4
-  for (uint32_t x = w + 1; x <= last_win && x < nwin; x++) add_part(part + (size_t)x * 6, v);
-  float old[RED_VALS];
-  prefetch_old(a, run, old);
-  finish_run(a, run, v, old);
+  for (uint32_t x0 = w + 1; x0 <= last_win; x0 += 64u) {
+    const uint32_t x = x0 + (uint32_t)lane;
+    if (x <= last_win) add_part(part + (size_t)x * 6, v);  // the run's rows at the start of window x
+  }
+#pragma unroll
+  for (int k = 0; k < RED_VALS; k++) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v[k] += __shfl_xor(v[k], o);
+  }
+  if (lane == 0) {
+    add_part(part + (size_t)w * 6 + 3, v);
+    float old[RED_VALS];
+    prefetch_old(a, run, old);
+    finish_run(a, run, v, old);
+  }
 }
 
 }  // namespace
@@ -553,7 +565,7 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
     if (windows) {
       if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;
       isect_reduce_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
-      isect_fixup_kernel<<<dim3((windows + 255u) / 256u), dim3(256), 0, stream>>>(*a);
+      isect_fixup_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
     }
   }
   return (int)hipGetLastError();

@@ -51,10 +51,10 @@ __device__ __forceinline__ Sym2 inverse2x2_vjp(Sym2 minv, Sym2 v) {  // optim.cu
 
 // d colour / d view direction (optim.cu:48-88); dotc(k) = sum_ch c[k][ch] * vc[ch].
 template <int DEG>
-__device__ __forceinline__ void sh_viewdir_vjp(const ShView& sv, int i, float x, float y, float z, float3 vc, int active,
+__device__ __forceinline__ void sh_viewdir_vjp(const float* coef, float x, float y, float z, float3 vc, int active,
                                                float& gx, float& gy, float& gz) {
   gx = gy = gz = 0.f;
-  auto dotc = [&](int k) { return sv.get(k * 3, i) * vc.x + sv.get(k * 3 + 1, i) * vc.y + sv.get(k * 3 + 2, i) * vc.z; };
+  auto dotc = [&](int k) { return coef[k * 3] * vc.x + coef[k * 3 + 1] * vc.y + coef[k * 3 + 2] * vc.z; };
   if constexpr (DEG >= 1) if (active >= 1) {
     const float f0a = 0.4886025f;
     const float s_n1 = dotc(1), s_z0 = dotc(2), s_p1 = dotc(3);
@@ -97,26 +97,36 @@ __device__ __forceinline__ void sh_viewdir_vjp(const ShView& sv, int i, float x,
   }
 }
 
+// The per-splat rows of v_splat (13 floats) and grad_out (11 + 3K floats) are read and written through
+// LDS by the whole workgroup, so consecutive lanes touch consecutive addresses (a lane-per-row access
+// would touch one cache line per lane per instruction).
+constexpr int VJP_BLOCK = 128;
+
 template <int DEG>
-__global__ void __launch_bounds__(128) vjp_kernel(b2c_vjp_args a) {
+__global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   constexpr int K = (DEG + 1) * (DEG + 1);
   constexpr int PER = 11 + 3 * K;
-  const int i = blockIdx.x * 128 + threadIdx.x;
-  if (i >= a.n) return;
-  float g[GRAD_LANES];
-  const uint32_t vis = a.vis_flag[i];
+  __shared__ float s_buf[VJP_BLOCK * PER];  // v_splat rows in, then grad_out rows out
+  __shared__ uint32_t s_vis[VJP_BLOCK];
+  const int i0 = blockIdx.x * VJP_BLOCK;
+  const int i = i0 + threadIdx.x;
+  const int rows = min(VJP_BLOCK, a.n - i0);
+  const bool in_range = i < a.n;
+  const uint32_t vis = in_range ? a.vis_flag[i] : 0u;
   if (vis) a.vis_flag[i] = 0u;
+  s_vis[threadIdx.x] = vis;
+  for (int j = threadIdx.x; j < rows * GRAD_LANES; j += VJP_BLOCK) s_buf[j] = a.v_splat[(size_t)i0 * GRAD_LANES + j];
+  __syncthreads();
+  // read then clear the consumed rows (optim.cu:110-121)
+  for (int j = threadIdx.x; j < rows * GRAD_LANES; j += VJP_BLOCK)
+    if (s_vis[j / GRAD_LANES]) a.v_splat[(size_t)i0 * GRAD_LANES + j] = 0.f;
+  float g[GRAD_LANES];
+#pragma unroll
+  for (int k = 0; k < GRAD_LANES; k++) g[k] = vis ? s_buf[threadIdx.x * GRAD_LANES + k] : 0.f;
+  __syncthreads();
   const bool visible = vis != 0u && a.tile_count[i] != 0u;
-  float* vs = a.v_splat + (size_t)i * GRAD_LANES;
-  if (vis) {
-#pragma unroll
-    for (int k = 0; k < GRAD_LANES; k++) { g[k] = vs[k]; vs[k] = 0.f; }
-  } else {
-#pragma unroll
-    for (int k = 0; k < GRAD_LANES; k++) g[k] = 0.f;
-  }
-  if (a.vis_count) a.vis_count[i] += visible ? 1.f : 0.f;
-  if (a.refine_norm) {
+  if (a.vis_count && in_range) a.vis_count[i] += visible ? 1.f : 0.f;
+  if (a.refine_norm && in_range) {
     const float rn = __builtin_isfinite(g[9]) ? fminf(fmaxf(g[9], 0.f), 1e32f) : 0.f;
     a.refine_norm[i] = fmaxf(a.refine_norm[i], rn);
   }
@@ -147,7 +157,9 @@ __global__ void __launch_bounds__(128) vjp_kernel(b2c_vjp_args a) {
       const int kmax = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
       const float3 vc = make_float3(g[5], g[6], g[7]);
       float vvx, vvy, vvz;
-      sh_viewdir_vjp<DEG>(sv, i, vx, vy, vz, vc, a.active_deg, vvx, vvy, vvz);
+      float coef[3 * K];
+      sv.load_all<DEG>(i, coef);
+      sh_viewdir_vjp<DEG>(coef, vx, vy, vz, vc, a.active_deg, vvx, vvy, vvz);
       const float vdot = vx * vvx + vy * vvy + vz * vvz;
       const float msx = (vvx - vx * vdot) * (1.f / ul), msy = (vvy - vy * vdot) * (1.f / ul), msz = (vvz - vz * vdot) * (1.f / ul);
       const float v_alpha = g[8];
@@ -255,15 +267,16 @@ __global__ void __launch_bounds__(128) vjp_kernel(b2c_vjp_args a) {
       }
     }
   }
-  float* o = a.grad_out + (size_t)i * PER;
+#pragma unroll
+  for (int k = 0; k < PER; k++) s_buf[threadIdx.x * PER + k] = out[k];
+  s_vis[threadIdx.x] = any ? 1u : 0u;
+  __syncthreads();
+  float* o = a.grad_out + (size_t)i0 * PER;
   if (a.accumulate) {
-    if (any) {
-#pragma unroll
-      for (int k = 0; k < PER; k++) o[k] += out[k];
-    }
+    for (int j = threadIdx.x; j < rows * PER; j += VJP_BLOCK)
+      if (s_vis[j / PER]) o[j] += s_buf[j];
   } else {
-#pragma unroll
-    for (int k = 0; k < PER; k++) o[k] = out[k];
+    for (int j = threadIdx.x; j < rows * PER; j += VJP_BLOCK) o[j] = s_buf[j];
   }
 }
 
@@ -275,7 +288,7 @@ using namespace b2c::dev;
 
 extern "C" int b2c_hip_vjp(const b2c_vjp_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
-  const dim3 grid((unsigned)((a->n + 127) / 128)), block(128);
+  const dim3 grid((unsigned)((a->n + VJP_BLOCK - 1) / VJP_BLOCK)), block(VJP_BLOCK);
   switch (a->degree) {
     case 0: vjp_kernel<0><<<grid, block, 0, stream>>>(*a); break;
     case 1: vjp_kernel<1><<<grid, block, 0, stream>>>(*a); break;

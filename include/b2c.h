@@ -70,6 +70,11 @@ int b2c_model_upload(b2c_model* m, int n, int degree, int sh_fp16, const float* 
                      const float* quat, const float* opacity, const float* sh, const float* floor_);
 /* Copy a model buffer to host: "pos_op", "quat", "lscale", "vis_weight", "vis_count", "refine_norm", "max_screen". */
 int b2c_model_read(const b2c_model* m, const char* field, void* host, size_t bytes);
+/* Device address and size of a model buffer (same names), and the planar SH view the kernels take: for
+ * FFI callers that launch their own kernels on the model, as the reference's refine / cage code reads
+ * Model fields directly (src/model.h:14-40). */
+int b2c_model_device_ptr(const b2c_model* m, const char* field, void** ptr, size_t* bytes);
+int b2c_model_sh_view(const b2c_model* m, b2c_sh_view* out);
 
 /* RenderCtx and RenderCtx::setup (src/gpu/render.cu:5-21). */
 b2c_ctx* b2c_ctx_create(void);
@@ -79,6 +84,10 @@ int b2c_ctx_info_get(const b2c_ctx* c, b2c_ctx_info* out);
 /* Copy a RenderCtx buffer to / from host memory by field name ("proj0", "tile_count", "keys_sorted",
  * "vals_sorted", "tile_ranges", "out_rgba", "v_out", "v_splat", "grads", ...). Synchronous. */
 int b2c_ctx_read(b2c_ctx* c, const char* field, void* host, size_t bytes);
+/* Device address and size of a RenderCtx buffer by the same names: the reference's evidence / probe /
+ * cage code reads ctx.tile_ranges, vals_sorted, proj0..3, last_idx and v_splat directly
+ * (src/train/evidence.cu:224-229, src/gpu/probe.cu:52, src/gpu/cage_app.cu:454). */
+int b2c_ctx_device_ptr(b2c_ctx* c, const char* field, void** ptr, size_t* bytes);
 int b2c_ctx_write(b2c_ctx* c, const char* field, const void* host, size_t bytes);
 int b2c_ctx_zero(b2c_ctx* c, const char* field);
 int b2c_ctx_synchronize(b2c_ctx* c);
