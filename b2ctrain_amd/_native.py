@@ -46,7 +46,8 @@ class CtxInfo(C.Structure):
 
 class StepTimes(C.Structure):
     _fields_ = [("project_ms", C.c_float), ("bin_ms", C.c_float), ("forward_ms", C.c_float), ("loss_ms", C.c_float),
-                ("backward_ms", C.c_float), ("vjp_ms", C.c_float), ("total_ms", C.c_float)]
+                ("backward_ms", C.c_float), ("vjp_ms", C.c_float), ("total_ms", C.c_float),
+                ("raster_bwd_ms", C.c_float), ("reduce_ms", C.c_float)]
 
     def as_dict(self):
         return {k: float(getattr(self, k)) for k, _ in self._fields_}

@@ -221,6 +221,7 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.isect_rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);
   a.isect_part = reinterpret_cast<float*>(ctx.isect_part.ptr);
   a.isect_part_flags = ctx.isect_part_flags;
+  a.split_event = ctx.bwd_split_event;
   LAUNCH_CHECK(b2c_hip_raster_bwd(&a, stream));
 }
 

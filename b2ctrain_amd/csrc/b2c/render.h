@@ -95,6 +95,7 @@ struct RenderCtx {
   DevBuf<uint32_t> isect_part_flags;  // per 64-row window
   DevBuf<unsigned char> sort_tmp;
   DevBuf<float> loss_partials;  // per-workgroup loss sums, reduced in a fixed order
+  hipEvent_t bwd_split_event = nullptr;  // if set: recorded between the backward raster kernel and its reduce
 
   void setup(int W, int H, int n_splats, hipStream_t stream);
   void ensure_isect_capacity(size_t m, hipStream_t stream);

@@ -369,10 +369,12 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
     mark(3);
     b2c::photometric_loss(c->ctx, v->view, lp, s);
     mark(4);
+    c->ctx.bwd_split_event = (times && mode != 0) ? c->ev[7] : nullptr;
     if (mode == 0)
       b2c::rasterize_backward(c->ctx, m->m, p, s);
     else
       b2c::rasterize_backward_tc(c->ctx, m->m, p, lp.grad_scale, s);
+    c->ctx.bwd_split_event = nullptr;
     mark(5);
     b2c::OptimParams op;
     op.cam = p.cam;
@@ -388,6 +390,13 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
                        &times->vjp_ms};
       for (int k = 0; k < 6; k++) HIP_CHECK(hipEventElapsedTime(out[k], c->ev[k], c->ev[k + 1]));
       HIP_CHECK(hipEventElapsedTime(&times->total_ms, c->ev[0], c->ev[6]));
+      if (mode != 0) {
+        HIP_CHECK(hipEventElapsedTime(&times->raster_bwd_ms, c->ev[4], c->ev[7]));
+        HIP_CHECK(hipEventElapsedTime(&times->reduce_ms, c->ev[7], c->ev[5]));
+      } else {
+        times->raster_bwd_ms = times->backward_ms;
+        times->reduce_ms = 0.f;
+      }
     }
   });
 }

@@ -561,6 +561,10 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
     if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->tile_count)
       return (int)hipErrorInvalidValue;
     raster_bwd_mfma_kernel<<<grid, block, 0, stream>>>(*a);
+    if (a->split_event) {
+      const int e = (int)hipEventRecord(static_cast<hipEvent_t>(a->split_event), stream);
+      if (e) return e;
+    }
     const uint32_t windows = (a->num_isect + 63u) / 64u;
     if (windows) {
       if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;

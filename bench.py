@@ -37,6 +37,34 @@ def projection_bytes(n, n_ok, sh_bytes):
     return n * 52 + n_ok * (sh_bytes + 72)
 
 
+def binning_bytes(n, m, tile_bits):
+    """Algorithmic bytes of binning: depth keys (read proj1 z + tile_count, write key/value), 4 depth-sort
+    passes (16 B per splat each), the count scan in depth order (12 B per splat), the emit (20 B per splat +
+    8 B per intersection), ceil(tile_bits / 8) tile-sort passes (24 B per intersection each: key and two
+    values, read and written) and the range pass (4 B per intersection)."""
+    tile_passes = (int(tile_bits) + 7) // 8
+    return n * (8 + 8) + 4 * 16 * n + 12 * n + 20 * n + 8 * m + tile_passes * 24 * m + 4 * m
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE in
+    KiB per dispatch, scaled by the plain-copy calibration recorded in the same file); None if absent."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_cfg3_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    kv = {}
+    for line in open(path):
+        if ":" in line and not line.startswith("#"):
+            k, v = line.split(":", 1)
+            kv[k.strip()] = v.strip()
+    try:
+        fetch = float(kv["fetch_kib_per_dispatch"]) * float(kv["fetch_scale"])
+        write = float(kv["write_kib_per_dispatch"]) * float(kv["write_scale"])
+    except (KeyError, ValueError):
+        return None
+    return int((fetch + write) * 1024)
+
+
 def cpu_baseline(r, scene, bg):
     """The CPU port (oracle, fp32 tiled restatement, one host core) timed on the same frame: forward raster
     + backward raster over the GPU's own tile lists and per-pixel loss gradient."""
@@ -89,7 +117,20 @@ def main():
     ap.add_argument("--splats", type=int, default=1_000_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", type=int, default=1, help="backward: 1 = MFMA reduction, 0 = fp32 reduction")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device-to-device copy (three times), the known-size kernel that "
+                         "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        a = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": a.numel() * 4, "copies": 3}), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the path would shard "
               "by screen tiles or by views, see DESIGN.md)", file=sys.stderr)
@@ -132,22 +173,44 @@ def main():
     t_fb = mean["forward_ms"] + mean["backward_ms"]
     gfrag = f_sweep / (t_fb * 1e-3) / 1e9
 
-    # roofline: projection is the HBM-bound stage the metric prices; the dominant kernel is reported too
-    proj_bytes = projection_bytes(scene.n, n_ok, 4 * 3 * scene.K)
-    proj_gbs = proj_bytes / (mean["project_ms"] * 1e-3) / 1e9
-    dominant = max(("forward_ms", "backward_ms", "loss_ms", "project_ms", "vjp_ms", "bin_ms"), key=lambda k: mean[k])
+    # Roofline of the dominant kernel, the MFMA backward raster (raster_bwd_mfma_kernel), timed alone with
+    # hipEvents on the context's stream. Algorithmic bytes per launch: per composited-range intersection its
+    # list entry, emit position and projected splat (4 + 4 + 48 B) plus its gradient row (48 B, written);
+    # per intersection past the shrunk end its zero row (48 B); per pixel out_rgba, out_feat, last_idx and
+    # v_out (52 B). MFMA: 10 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
+    m_shrunk = f_sweep // 64
+    m_total = int(info.num_isect)
+    bwd_bytes = 104 * m_shrunk + 48 * (m_total - m_shrunk) + 52 * W * H
+    t_bwd = mean["raster_bwd_ms"] * 1e-3
+    bwd_gbs = bwd_bytes / t_bwd / 1e9
+    groups = int(np.ceil(m_shrunk / 8.0))
+    mfma_tflops = groups * 10 * 16384 / t_bwd / 1e12
+    traffic = read_traffic("raster_bwd_mfma_kernel")
     roofline = {
-        "kernel": "project_kernel + project_big_kernel (projection stage)",
+        "kernel": "raster_bwd_mfma_kernel",
         "bound": "hbm",
-        "achieved": round(proj_gbs, 1),
+        "achieved": round(bwd_gbs, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
-        "frac": round(proj_gbs / HBM_PEAK_GBS, 4),
-        "traffic": None,
-        "algorithmic_bytes": proj_bytes,
-        "avg_launch_ms": round(mean["project_ms"], 4),
-        "dominant_stage": dominant,
+        "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
+        "traffic": traffic,
+        "algorithmic_bytes": bwd_bytes,
+        "avg_launch_ms": round(mean["raster_bwd_ms"], 4),
+        "mfma": {"achieved": round(mfma_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                 "frac": round(mfma_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
+        "note": "VALU-issue bound (per-fragment replay); HBM and MFMA fractions are both low by design",
     }
+    # HBM rooflines of the stages the north star prices: projection, binning/sort, loss
+    proj_bytes = projection_bytes(scene.n, n_ok, 4 * 3 * scene.K)
+    bin_bytes = binning_bytes(scene.n, m_total, info.tile_bits)
+    loss_bytes = 37 * W * H
+    stage_rooflines = {}
+    for name, nbytes, key in (("projection", proj_bytes, "project_ms"), ("binning_sort", bin_bytes, "bin_ms"),
+                              ("loss", loss_bytes, "loss_ms")):
+        gbs = nbytes / (mean[key] * 1e-3) / 1e9
+        stage_rooflines[name] = {"bound": "hbm", "algorithmic_bytes": int(nbytes), "ms": round(mean[key], 4),
+                                 "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(gbs / HBM_PEAK_GBS, 4)}
     out = {
         "metric": METRIC,
         "value": round(gfrag, 3),
@@ -178,6 +241,7 @@ def main():
         "stages_ms_median": {k: round(v, 4) for k, v in med.items()},
         "raster_fwd_bwd_ms": round(t_fb, 4),
         "roofline": roofline,
+        "stage_rooflines": stage_rooflines,
     }
     if not args.no_cpu_baseline:
         log("bench: CPU baseline (oracle port, one core)")

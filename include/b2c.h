@@ -53,9 +53,11 @@ typedef struct b2c_ctx_info {
   uint64_t isect_cap;
 } b2c_ctx_info;
 
-/* Per-stage GPU times of one training step (hipEvents on the context's stream), milliseconds. */
+/* Per-stage GPU times of one training step (hipEvents on the context's stream), milliseconds. backward_ms
+ * covers the backward raster kernel (raster_bwd_ms) and the per-splat reduce that follows it (reduce_ms). */
 typedef struct b2c_step_times {
   float project_ms, bin_ms, forward_ms, loss_ms, backward_ms, vjp_ms, total_ms;
+  float raster_bwd_ms, reduce_ms;
 } b2c_step_times;
 
 const char* b2c_last_error(void);

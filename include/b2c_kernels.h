@@ -179,6 +179,7 @@ typedef struct b2c_raster_bwd_args {
   float* isect_rows;          /* [M][12] scratch */
   float* isect_part;          /* [ceil(M / 64)][24] scratch: partial sums of runs crossing 64-row windows */
   uint32_t* isect_part_flags; /* [ceil(M / 64)] scratch */
+  void* split_event;          /* optional hipEvent_t recorded between the raster kernel and the reduce */
 } b2c_raster_bwd_args;
 int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stream);
 
