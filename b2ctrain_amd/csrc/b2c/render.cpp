@@ -51,7 +51,7 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   depth_bits = 32 - tile_bits;
   if (depth_bits > 20) depth_bits = 20;
   const size_t nn = (size_t)(n > 0 ? n : 1);
-  proj0.reserve(nn); proj1.reserve(nn); proj2.reserve(nn); proj3.reserve(nn);
+  proj0.reserve(nn); proj1.reserve(nn); proj2.reserve(nn); proj3.reserve(nn); raster_rec.reserve(nn * 4);
   tile_count.reserve(nn); tile_off.reserve(nn); hit_info.reserve(nn);
   depth_keys.reserve(nn); depth_keys_sorted.reserve(nn); order_in.reserve(nn); order.reserve(nn);
   depth_alt_k.reserve(nn); depth_alt_v.reserve(nn);
@@ -112,6 +112,7 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   a.tiles_x = ctx.tiles_x; a.tiles_y = ctx.tiles_y;
   a.proj0 = reinterpret_cast<float*>(ctx.proj0.ptr); a.proj1 = reinterpret_cast<float*>(ctx.proj1.ptr);
   a.proj2 = reinterpret_cast<float*>(ctx.proj2.ptr); a.proj3 = reinterpret_cast<float*>(ctx.proj3.ptr);
+  a.raster_rec = reinterpret_cast<float*>(ctx.raster_rec.ptr);
   a.tile_count = ctx.tile_count.ptr;
   a.hit_info = reinterpret_cast<uint32_t*>(ctx.hit_info.ptr);
   a.max_screen = m.max_screen.ptr;
@@ -177,6 +178,7 @@ void rasterize_forward(RenderCtx& ctx, const RenderParams& p, hipStream_t stream
   a.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr);
   a.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
   a.proj2 = reinterpret_cast<const float*>(ctx.proj2.ptr);
+  a.raster_rec = reinterpret_cast<const float*>(ctx.raster_rec.ptr);
   a.W = ctx.W; a.H = ctx.H; a.tiles_x = ctx.tiles_x; a.tiles_y = ctx.tiles_y;
   for (int k = 0; k < 3; k++) a.bg[k] = p.bg[k];
   a.bwd_info = p.bwd_info ? 1 : 0;
@@ -202,6 +204,7 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr);
   a.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
   a.proj2 = reinterpret_cast<const float*>(ctx.proj2.ptr);
+  a.raster_rec = reinterpret_cast<const float*>(ctx.raster_rec.ptr);
   a.out_rgba = reinterpret_cast<const float*>(ctx.out_rgba.ptr);
   a.out_feat = reinterpret_cast<const float*>(ctx.out_feat.ptr);
   a.last_idx = ctx.last_idx;

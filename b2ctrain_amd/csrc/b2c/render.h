@@ -60,6 +60,7 @@ struct RenderCtx {
   // per splat (global index)
   DevBuf<float4> proj0, proj1, proj2;  // (xy, c00, c01) | (c11, opac, depth, power = ln(255 opac)) | (r, g, b, feat_x)
   DevBuf<float2> proj3;                // (feat_y, feat_z)
+  DevBuf<float4> raster_rec;           // [n][4]: the raster kernels' 64-byte per-splat record (same values)
   DevBuf<uint32_t> tile_count, tile_off;  // hit count; inclusive scan in depth order
   DevBuf<uint2> hit_info;                 // (hit mask within the bbox or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24)
   DevBuf<uint32_t> depth_keys, depth_keys_sorted, order_in, order;  // depth sort

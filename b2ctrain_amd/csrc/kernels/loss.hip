@@ -99,12 +99,19 @@ __device__ __forceinline__ StepRaw fetch_step(const b2c_loss_args& a, int c, int
   return f;
 }
 
-__global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss11 gw, int strips_x) {
+// Workgroup b runs on XCD b mod 8; each XCD gets a contiguous band of strips, and the three channel waves of
+// a strip are consecutive on their XCD, so the strip's input lines are read from that XCD's L2 three times
+// rather than from memory.
+__global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss11 gw, int strips_x, int nstrips) {
   __shared__ float s_p[2][64 + 2 * HALO], s_g[2][64 + 2 * HALO];  // one input row (double buffered)
   __shared__ float s_pm[2][5][64];                                 // one partial-map row (double buffered)
-  const int c = blockIdx.y;
+  constexpr int NXCD = 8;
+  const int per = (nstrips * 3 + NXCD - 1) / NXCD;  // work items per XCD
+  const int item = (blockIdx.x % NXCD) * per + blockIdx.x / NXCD;
+  if (item >= nstrips * 3) return;
+  const int strip = item / 3, c = item % 3;
   const int lane = threadIdx.x;
-  const int x0 = (blockIdx.x % strips_x) * SW, y0 = (blockIdx.x / strips_x) * SH;
+  const int x0 = (strip % strips_x) * SW, y0 = (strip / strips_x) * SH;
   const int W = a.W, H = a.H;
   const float bg_c = a.composite ? a.bg[c] : 0.f;
   const float norm = a.scale / (3.f * (float)W * (float)H);
@@ -245,7 +252,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) loss_local += __shfl_xor(loss_local, o);
   if (lane == 0) {
-    const int idx = blockIdx.y * gridDim.x + blockIdx.x;
+    const int idx = item;
     if (a.partials)
       a.partials[idx] = loss_local;
     else if (loss_local != 0.f)
@@ -292,7 +299,8 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   }
   for (int i = 0; i < 11; i++) g.w[i] = (float)(w[i] / sum);
   const int strips_x = (a->W + SW - 1) / SW, strips_y = (a->H + SH - 1) / SH;
-  photometric_kernel<<<dim3(strips_x * strips_y, 3), dim3(64), 0, stream>>>(*a, g, strips_x);
+  const int nstrips = strips_x * strips_y;
+  photometric_kernel<<<dim3(8 * ((nstrips * 3 + 7) / 8)), dim3(64), 0, stream>>>(*a, g, strips_x, nstrips);
   if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, strips_x * strips_y * 3, a->loss_accum);
   return (int)hipGetLastError();
 }

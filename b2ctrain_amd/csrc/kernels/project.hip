@@ -82,6 +82,13 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       reinterpret_cast<float4*>(a.proj1)[i] = make_float4(pr.conic.c11, pr.opac, pr.mc[2], power);
       reinterpret_cast<float4*>(a.proj2)[i] = make_float4(cr, cg, cb, 0.f);
       reinterpret_cast<float2*>(a.proj3)[i] = make_float2(0.f, 0.f);
+      if (a.raster_rec) {  // halving the conic diagonal is exact: the raster evaluates the reference's sigma
+        float4* rec = reinterpret_cast<float4*>(a.raster_rec) + (size_t)i * 4;
+        const uint32_t sgn = (cr >= 0.f ? 1u : 0u) | (cg >= 0.f ? 2u : 0u) | (cb >= 0.f ? 4u : 0u);
+        rec[0] = make_float4(pr.mean2d[0], pr.mean2d[1], 0.5f * pr.conic.c00, pr.conic.c01);
+        rec[1] = make_float4(0.5f * pr.conic.c11, pr.opac, power, __uint_as_float(sgn));
+        rec[2] = make_float4(fmaxf(cr, 0.f), fmaxf(cg, 0.f), fmaxf(cb, 0.f), 0.f);
+      }
       if (a.max_screen) {
         float ms = fmaxf(pr.ex / (float)a.cam.W, pr.ey / (float)a.cam.H);
         a.max_screen[i] = fmaxf(a.max_screen[i], ms);

@@ -255,9 +255,6 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   float T = ps.T;
   float Q = -ps.v_o_w;  // sum over composited splats behind of (colour . v_rgb) * vis, minus the v_o_w term
   const bool live_px = ps.inside;
-  const float4* proj0 = reinterpret_cast<const float4*>(a.proj0);
-  const float4* proj1 = reinterpret_cast<const float4*>(a.proj1);
-  const float4* proj2 = reinterpret_cast<const float4*>(a.proj2);
   for (uint32_t batch_end = range.y; batch_end > range.x;) {
     const uint32_t batch_start = batch_end > range.x + BATCH ? batch_end - BATCH : range.x;
     const int count = (int)(batch_end - batch_start);
@@ -265,11 +262,11 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
     if (lane < count) {
       const uint32_t gid = a.vals_sorted[batch_start + lane];
       s_slot[lane] = a.slot_sorted[batch_start + lane];
-      const float4 p0 = proj0[gid], p1 = proj1[gid], p2 = proj2[gid];
-      s_g0[lane] = make_float4(p0.x, p0.y, 0.5f * p0.z, p0.w);
-      s_g1[lane] = make_float4(0.5f * p1.x, p1.y, p1.w, 0.f);
-      const uint32_t sgn = (p2.x >= 0.f ? 1u : 0u) | (p2.y >= 0.f ? 2u : 0u) | (p2.z >= 0.f ? 4u : 0u);
-      s_col[lane] = make_float4(fmaxf(p2.x, 0.f), fmaxf(p2.y, 0.f), fmaxf(p2.z, 0.f), __uint_as_float(sgn));
+      const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
+      const float4 r1 = rec[1], r2 = rec[2];
+      s_g0[lane] = rec[0];
+      s_g1[lane] = make_float4(r1.x, r1.y, r1.z, 0.f);
+      s_col[lane] = make_float4(r2.x, r2.y, r2.z, r1.w);
     }
     __syncthreads();
     const int ngroups = (count + G - 1) / G;
@@ -558,7 +555,7 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
   if (a->mode == 0) {
     raster_bwd_fp32_kernel<<<grid, block, 0, stream>>>(*a);
   } else {
-    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->tile_count)
+    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->tile_count || !a->raster_rec)
       return (int)hipErrorInvalidValue;
     raster_bwd_mfma_kernel<<<grid, block, 0, stream>>>(*a);
     if (a->split_event) {

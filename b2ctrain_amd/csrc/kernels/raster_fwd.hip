@@ -13,8 +13,9 @@ namespace {
 // The splat loop is wave-uniform and branch-free per lane: a lane that has terminated (or a fragment that
 // fails the cutoff) contributes alpha = 0, which leaves T, the colour and the last index unchanged; a splat
 // no live lane passes is skipped by the whole wave. Per splat the LDS holds (mx, my, c00/2, c01),
-// (c11/2, opacity, power, 0) and the colour clamped at 0; halving c00 and c11 is exact, so sigma is the
-// reference's 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy bit for bit (uncontracted).
+// (c11/2, opacity, power, 0) and the colour clamped at 0, staged from the projection's 64-byte per-splat
+// record (one cache line per gather); halving c00 and c11 is exact, so sigma is the reference's
+// 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy bit for bit (uncontracted).
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   __shared__ float4 s_g0[64], s_g1[64], s_col[64];
   const int n_tiles = a.tiles_x * a.tiles_y;
@@ -27,9 +28,6 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   const float pcx = px + 0.5f, pcy = py + 0.5f;
   uint2* ranges = reinterpret_cast<uint2*>(a.tile_ranges);
   const uint2 range = ranges[tile];
-  const float4* proj0 = reinterpret_cast<const float4*>(a.proj0);
-  const float4* proj1 = reinterpret_cast<const float4*>(a.proj1);
-  const float4* proj2 = reinterpret_cast<const float4*>(a.proj2);
   float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
   bool live = inside;
   uint32_t last = range.x;
@@ -39,10 +37,11 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     __syncthreads();
     if ((uint32_t)lane < remaining) {
       const uint32_t gid = a.vals_sorted[start + lane];
-      const float4 p0 = proj0[gid], p1 = proj1[gid], p2 = proj2[gid];
-      s_g0[lane] = make_float4(p0.x, p0.y, 0.5f * p0.z, p0.w);
-      s_g1[lane] = make_float4(0.5f * p1.x, p1.y, p1.w, 0.f);
-      s_col[lane] = make_float4(fmaxf(p2.x, 0.f), fmaxf(p2.y, 0.f), fmaxf(p2.z, 0.f), 0.f);
+      const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
+      const float4 r1 = rec[1];
+      s_g0[lane] = rec[0];
+      s_g1[lane] = make_float4(r1.x, r1.y, r1.z, 0.f);
+      s_col[lane] = rec[2];
     }
     __syncthreads();
     for (uint32_t t = 0; t < remaining; t++) {
@@ -91,6 +90,7 @@ using namespace b2c::dev;
 extern "C" int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream) {
   const int n_tiles = a->tiles_x * a->tiles_y;
   if (n_tiles <= 0) return 0;
+  if (!a->raster_rec) return (int)hipErrorInvalidValue;
   raster_fwd_kernel<<<dim3(NUM_XCD * xcd_tiles_per(n_tiles)), dim3(64), 0, stream>>>(*a);
   return (int)hipGetLastError();
 }

@@ -54,6 +54,8 @@ typedef struct b2c_project_args {
   uint32_t* tile_count;/* [n] */
   uint32_t* hit_info;  /* [n] uint2 (hit mask or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24) */
   float* max_screen;   /* [n] or NULL: max(., max(ex/W, ey/H)) (project.cu:82-83) */
+  float* raster_rec;   /* [n][16]: the raster kernels' per-splat record, one 64-byte line: (mx, my, c00/2, c01),
+                          (c11/2, opacity, power, sign bits of r, g, b), (max(r,0), max(g,0), max(b,0), 0), 0 */
   uint32_t* big_list;  /* [n] scratch: splats whose bbox exceeds 32 tiles */
   uint32_t* big_count; /* [1] scratch counter */
   uint32_t* big_info;  /* [n][4] scratch: per big-list entry, bbox origin, width, area, chunk length */
@@ -137,6 +139,7 @@ typedef struct b2c_raster_fwd_args {
   uint32_t* tile_ranges;      /* [n_tiles] uint2; .y shrunk in place when bwd_info */
   const uint32_t* vals_sorted;
   const float* proj0, *proj1, *proj2;
+  const float* raster_rec;    /* [n][16] from b2c_hip_project (the same values, one line per splat) */
   int W, H, tiles_x, tiles_y;
   float bg[3];
   int bwd_info;
@@ -160,6 +163,7 @@ typedef struct b2c_raster_bwd_args {
   const uint32_t* tile_ranges;
   const uint32_t* vals_sorted;
   const float* proj0, *proj1, *proj2;
+  const float* raster_rec;    /* [n][16] from b2c_hip_project */
   const float* out_rgba, *out_feat;
   const uint32_t* last_idx;
   const float* v_out;         /* [P] float4 dL/d(rgb, alpha) */
