@@ -1,10 +1,14 @@
 // Binning and sorting (replaces src/gpu/binning.cu:10-143 and its CUB calls).
 //
 // * Radix sort: stable LSD key/value sort, 8-bit digits, reduce-then-scan (no inter-workgroup spin
-//   waits): per 4096-key tile an LDS digit histogram built from wave64 ballot "match" masks, a per-digit
-//   exclusive scan over tiles, then a stable scatter whose in-tile ranks come from the same ballot masks
-//   (lanes below with the same digit) plus per-wave prefix counts in LDS.
-// * Count scan: reduce-then-scan of tile_count gathered in depth order.
+//   waits). Per tile of 256 * KPT keys: an LDS digit histogram (upsweep), a per-digit exclusive scan over
+//   tiles, then a stable scatter. In the scatter each wave owns a contiguous 64 * KPT stretch of the tile
+//   and ranks it round by round in input order (ballot "match" masks for the lanes below with the same
+//   digit, plus the wave's running per-digit count in LDS), so no block barrier sits inside the ranking
+//   loop; keys and values are staged in LDS sorted by digit and written out in runs. Every thread loads
+//   its KPT keys before it computes anything, so the loads of a tile are all in flight at once. KPT is 16
+//   for large sorts and 4 for small ones (enough workgroups to cover the chip).
+// * Count scan: reduce-then-scan of tile_count gathered in depth order, four contiguous entries a thread.
 // * Emit: small splats one thread each over the set bits of their hit mask; splats whose bbox exceeds 32
 //   tiles one wave per chunk of the bbox, in row-major order.
 #pragma clang fp contract(off)
@@ -16,10 +20,13 @@ namespace dev {
 namespace {
 
 constexpr int SORT_THREADS = 256;
-constexpr int SORT_ROUNDS = 16;
-constexpr int SORT_TILE = SORT_THREADS * SORT_ROUNDS;  // keys per workgroup
+constexpr int KPT_BIG = 16;  // keys per thread of a large sort (4096-key tiles)
+constexpr int KPT_SMALL = 4;  // below BIG_SORT_MIN keys (1024-key tiles)
+constexpr uint32_t BIG_SORT_MIN = 1u << 22;
 constexpr int RADIX = 256;
 constexpr int NWAVES = SORT_THREADS / 64;
+constexpr int SCAN_PER = 4;                         // count scan: contiguous entries per thread
+constexpr int SCAN_TILE = SORT_THREADS * SCAN_PER;  // entries per workgroup
 
 __device__ __forceinline__ uint64_t lanemask_lt() {
   const int l = lane_id();
@@ -71,69 +78,91 @@ __device__ __forceinline__ uint32_t live_count(uint32_t cap, const uint32_t* n_d
   return n < cap ? n : cap;
 }
 
+// Per-tile digit histogram. Every thread loads its KPT keys first, then counts them with LDS atomics.
+template <int KPT>
 __global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __restrict__ keys, uint32_t cap,
                                                               const uint32_t* __restrict__ n_dev, int shift, int bits,
                                                               uint32_t* __restrict__ block_hist, uint32_t nblocks) {
+  constexpr uint32_t TILE = SORT_THREADS * KPT;
   __shared__ uint32_t hist[RADIX];
   const uint32_t n = live_count(cap, n_dev);
   hist[threadIdx.x] = 0;
   __syncthreads();
-  const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
-  const uint32_t dmask = (1u << bits) - 1u;
-  for (int r = 0; r < SORT_ROUNDS; r++) {
-    const uint32_t rb = base + (uint32_t)r * SORT_THREADS;
-    if (rb >= n) break;
-    const uint32_t idx = rb + threadIdx.x;
-    const bool valid = idx < n;
-    const uint32_t d = valid ? (keys[idx] >> shift) & dmask : 0u;
-    const uint64_t peers = match_digit(d, bits, valid);
-    if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&hist[d], popc64(peers));
+  const uint32_t base = blockIdx.x * TILE;
+  if (base < n) {  // a tile past the live count (n_dev) reports zeros
+    const uint32_t dmask = (1u << bits) - 1u;
+    uint32_t key[KPT];
+#pragma unroll
+    for (int r = 0; r < KPT; r++) {
+      const uint32_t idx = base + (uint32_t)r * SORT_THREADS + threadIdx.x;
+      key[r] = idx < n ? keys[idx] : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < KPT; r++) {
+      const uint32_t idx = base + (uint32_t)r * SORT_THREADS + threadIdx.x;
+      if (idx < n) atomicAdd(&hist[(key[r] >> shift) & dmask], 1u);
+    }
   }
   __syncthreads();
   block_hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = hist[threadIdx.x];
 }
 
-// One workgroup per digit: exclusive scan of the digit's per-tile counts, total into digit_total.
+// One workgroup per digit: exclusive scan of the digit's per-tile counts (each thread a contiguous run of
+// tiles), total into digit_total.
 __global__ void __launch_bounds__(SORT_THREADS) radix_scan_digits(uint32_t* __restrict__ block_hist, uint32_t nblocks,
                                                                   uint32_t* __restrict__ digit_total) {
   __shared__ uint32_t s_wsum[NWAVES];
   uint32_t* row = block_hist + (size_t)blockIdx.x * nblocks;
-  uint32_t running = 0;
-  for (uint32_t c = 0; c < nblocks; c += SORT_THREADS) {
-    const uint32_t j = c + threadIdx.x;
-    const uint32_t v = j < nblocks ? row[j] : 0u;
-    uint32_t tot;
-    const uint32_t ex = block_excl_scan(v, s_wsum, tot);
-    if (j < nblocks) row[j] = running + ex;
-    running += tot;
+  const uint32_t per = (nblocks + SORT_THREADS - 1) / SORT_THREADS;
+  const uint32_t lo = min(nblocks, threadIdx.x * per), hi = min(nblocks, lo + per);
+  uint32_t sum = 0;
+  for (uint32_t j = lo; j < hi; j++) sum += row[j];
+  uint32_t tot;
+  uint32_t run = block_excl_scan(sum, s_wsum, tot);
+  for (uint32_t j = lo; j < hi; j++) {
+    const uint32_t v = row[j];
+    row[j] = run;
+    run += v;
   }
-  if (threadIdx.x == 0) digit_total[blockIdx.x] = running;
+  if (threadIdx.x == 0) digit_total[blockIdx.x] = tot;
 }
 
-// Stable scatter of one digit pass. The workgroup ranks its SORT_TILE keys by digit (ballot match masks
-// within each wave, per-wave digit counts in LDS across rounds), stages keys and values in LDS sorted by
-// digit, then writes the staging buffer out in order: each digit's keys of this tile form one contiguous
-// run in the output, so consecutive lanes write consecutive addresses (coalesced) instead of one 4-byte
-// write per key to a different bucket. NV = 1 or 2 value arrays ride along with the keys.
-template <int NV>
+// Stable scatter of one digit pass over tiles of 256 * KPT keys. Wave w owns keys [w * 64 KPT, (w + 1) *
+// 64 KPT) of the tile and ranks them in input order (ballot match masks within a round, the wave's running
+// per-digit counts in LDS across rounds); per-wave offsets then give each key its position in an LDS
+// staging buffer sorted by digit, which is written out in order: each digit's keys of this tile form one
+// contiguous run in the output, so consecutive lanes write consecutive addresses. NV = 1 or 2 value arrays
+// ride along with the keys.
+template <int NV, int KPT>
 __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ vals2_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ vals2_out, uint32_t cap,
     const uint32_t* __restrict__ n_dev, int shift, int bits, const uint32_t* __restrict__ block_hist, uint32_t nblocks,
     const uint32_t* __restrict__ digit_total) {
-  __shared__ uint32_t s_key[SORT_TILE];
-  __shared__ uint32_t s_val[NV][SORT_TILE];
+  constexpr uint32_t TILE = SORT_THREADS * KPT, CHUNK = 64 * KPT;
+  __shared__ uint32_t s_key[TILE];
+  __shared__ uint32_t s_val[NV][TILE];
   __shared__ uint32_t s_gbase[RADIX];  // global position of the tile's first key of each digit
   __shared__ uint32_t s_loff[RADIX];   // local (staging) offset of each digit
-  __shared__ uint32_t s_run[RADIX];    // running local position while ranking
   __shared__ uint32_t s_wcnt[NWAVES][RADIX];
   __shared__ uint32_t s_wsum[NWAVES];
   const uint32_t n = live_count(cap, n_dev);
-  const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
+  const uint32_t base = blockIdx.x * TILE;
   if (base >= n) return;
-  const uint32_t tile_n = min((uint32_t)SORT_TILE, n - base);
-  const int w = threadIdx.x >> 6;
-  {  // thread t owns digit t: global base, this tile's count, local offset
+  const uint32_t tile_n = min(TILE, n - base);
+  const int w = threadIdx.x >> 6, lane = lane_id();
+  const uint32_t dmask = (1u << bits) - 1u;
+  // 1. all loads of this thread in flight at once
+  uint32_t key[KPT], val[NV][KPT];
+#pragma unroll
+  for (int r = 0; r < KPT; r++) {
+    const uint32_t li = w * CHUNK + (uint32_t)r * 64 + lane;
+    const bool valid = li < tile_n;
+    key[r] = valid ? keys_in[base + li] : 0u;
+    val[0][r] = valid ? (vals_in ? vals_in[base + li] : base + li) : 0u;  // no values: sort the positions
+    if constexpr (NV > 1) val[1][r] = valid ? vals2_in[base + li] : 0u;
+  }
+  {  // 2. thread t owns digit t: global base and local offset of the digit in this tile
     const uint32_t t = threadIdx.x;
     uint32_t tot;
     const uint32_t digit_start = block_excl_scan(digit_total[t], s_wsum, tot);
@@ -142,52 +171,53 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     const uint32_t loff = block_excl_scan(next - mine, s_wsum, tot);
     s_gbase[t] = digit_start + mine;
     s_loff[t] = loff;
-    s_run[t] = loff;
-  }
-  const uint32_t dmask = (1u << bits) - 1u;
-  for (int r = 0; r < SORT_ROUNDS; r++) {
-    const uint32_t rb = (uint32_t)r * SORT_THREADS;
-    if (rb >= tile_n) break;
-    const uint32_t li = rb + threadIdx.x;
-    const bool valid = li < tile_n;
-    const uint32_t idx = base + li;
-    const uint32_t key = valid ? keys_in[idx] : 0u;
-    uint32_t val[NV];
-    val[0] = valid ? (vals_in ? vals_in[idx] : idx) : 0u;  // no values: sort the positions
-    if constexpr (NV > 1) val[1] = valid ? vals2_in[idx] : 0u;
-    const uint32_t d = (key >> shift) & dmask;
 #pragma unroll
-    for (int k = 0; k < NWAVES; k++) s_wcnt[k][threadIdx.x] = 0u;
-    __syncthreads();
+    for (int k = 0; k < NWAVES; k++) s_wcnt[k][t] = 0u;
+  }
+  __syncthreads();
+  // 3. rank within the wave: rank = keys of the same digit earlier in this wave's stretch. All lanes read
+  //    the running count before the round's leaders advance it (LDS instructions of a wave run in order).
+  uint32_t rank[KPT];
+  uint32_t* wc = s_wcnt[w];
+#pragma unroll
+  for (int r = 0; r < KPT; r++) {
+    const bool valid = w * CHUNK + (uint32_t)r * 64 + lane < tile_n;
+    const uint32_t d = (key[r] >> shift) & dmask;
     const uint64_t peers = match_digit(d, bits, valid);
-    const uint32_t rank = popc64(peers & lanemask_lt());
-    if (valid && rank == 0) s_wcnt[w][d] = popc64(peers);
-    __syncthreads();
-    {  // thread t owns digit t: per-wave counts become local positions, the running position advances
-      const uint32_t t = threadIdx.x;
-      uint32_t run = s_run[t];
-#pragma unroll
-      for (int k = 0; k < NWAVES; k++) {
-        const uint32_t c = s_wcnt[k][t];
-        s_wcnt[k][t] = run;
-        run += c;
-      }
-      s_run[t] = run;
-    }
-    __syncthreads();
-    if (valid) {
-      const uint32_t lp = s_wcnt[w][d] + rank;
-      s_key[lp] = key;
-#pragma unroll
-      for (int v = 0; v < NV; v++) s_val[v][lp] = val[v];
-    }
-    __syncthreads();  // s_wcnt is cleared at the top of the next round
+    const uint32_t lt = popc64(peers & lanemask_lt());
+    const uint32_t before = wc[d];
+    if (valid && lt == 0) wc[d] = before + popc64(peers);
+    rank[r] = before + lt;
   }
+  __syncthreads();
+  {  // 4. thread t owns digit t: per-wave counts become staging offsets
+    const uint32_t t = threadIdx.x;
+    uint32_t run = s_loff[t];
+#pragma unroll
+    for (int k = 0; k < NWAVES; k++) {
+      const uint32_t c = s_wcnt[k][t];
+      s_wcnt[k][t] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  // 5. stage sorted by digit
+#pragma unroll
+  for (int r = 0; r < KPT; r++) {
+    if (w * CHUNK + (uint32_t)r * 64 + lane < tile_n) {
+      const uint32_t lp = wc[(key[r] >> shift) & dmask] + rank[r];
+      s_key[lp] = key[r];
+#pragma unroll
+      for (int v = 0; v < NV; v++) s_val[v][lp] = val[v][r];
+    }
+  }
+  __syncthreads();
+  // 6. write out in digit runs
   for (uint32_t j = threadIdx.x; j < tile_n; j += SORT_THREADS) {
-    const uint32_t key = s_key[j];
-    const uint32_t d = (key >> shift) & dmask;
+    const uint32_t k = s_key[j];
+    const uint32_t d = (k >> shift) & dmask;
     const uint32_t g = s_gbase[d] + (j - s_loff[d]);
-    keys_out[g] = key;
+    keys_out[g] = k;
     vals_out[g] = s_val[0][j];
     if constexpr (NV > 1) vals2_out[g] = s_val[1][j];
   }
@@ -203,43 +233,55 @@ __global__ void __launch_bounds__(256) depth_keys_kernel(int n, const uint32_t* 
 }
 
 // ---- count scan in depth order ----
+// Thread t of workgroup b owns entries [b * SCAN_TILE + 4t, +4): the order gather and the count gathers
+// are issued before any arithmetic.
+__device__ __forceinline__ void gather_counts(int n, const uint32_t* __restrict__ order,
+                                              const uint32_t* __restrict__ tile_count, uint32_t first, uint32_t* c) {
+  uint32_t o[SCAN_PER];
+#pragma unroll
+  for (int k = 0; k < SCAN_PER; k++) o[k] = first + k < (uint32_t)n ? order[first + k] : 0xFFFFFFFFu;
+#pragma unroll
+  for (int k = 0; k < SCAN_PER; k++) c[k] = o[k] != 0xFFFFFFFFu ? tile_count[o[k]] : 0u;
+}
+
 __global__ void __launch_bounds__(SORT_THREADS) scan_reduce(int n, const uint32_t* __restrict__ order,
                                                             const uint32_t* __restrict__ tile_count,
                                                             uint32_t* __restrict__ block_sums) {
   __shared__ uint32_t s_wsum[NWAVES];
-  const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
+  uint32_t c[SCAN_PER];
+  gather_counts(n, order, tile_count, blockIdx.x * (uint32_t)SCAN_TILE + threadIdx.x * SCAN_PER, c);
   uint32_t acc = 0;
-  for (int r = 0; r < SORT_ROUNDS; r++) {
-    const uint32_t idx = base + (uint32_t)r * SORT_THREADS + threadIdx.x;
-    if (idx < (uint32_t)n) acc += tile_count[order[idx]];
-  }
+#pragma unroll
+  for (int k = 0; k < SCAN_PER; k++) acc += c[k];
   uint32_t tot;
   block_excl_scan(acc, s_wsum, tot);
   if (threadIdx.x == 0) block_sums[blockIdx.x] = tot;
 }
 
+// Exclusive scan of the per-workgroup sums (each thread a contiguous run), total into total_dev.
 __global__ void __launch_bounds__(1024) scan_top(uint32_t nblocks, uint32_t* __restrict__ block_sums,
                                                  uint32_t* __restrict__ total_dev) {
   __shared__ uint32_t s_wsum[16];
   const int w = threadIdx.x >> 6, l = lane_id();
-  uint32_t running = 0;
-  for (uint32_t c = 0; c < nblocks; c += 1024) {
-    const uint32_t j = c + threadIdx.x;
-    const uint32_t v = j < nblocks ? block_sums[j] : 0u;
-    const uint32_t inc = wave_incl_scan(v);
-    if (l == 63) s_wsum[w] = inc;
-    __syncthreads();
-    uint32_t wbase = 0, tot = 0;
-    for (int k = 0; k < 16; k++) {
-      const uint32_t s = s_wsum[k];
-      if (k < w) wbase += s;
-      tot += s;
-    }
-    __syncthreads();
-    if (j < nblocks) block_sums[j] = running + wbase + inc - v;
-    running += tot;
+  const uint32_t per = (nblocks + 1023) / 1024;
+  const uint32_t lo = min(nblocks, threadIdx.x * per), hi = min(nblocks, lo + per);
+  uint32_t sum = 0;
+  for (uint32_t j = lo; j < hi; j++) sum += block_sums[j];
+  const uint32_t inc = wave_incl_scan(sum);
+  if (l == 63) s_wsum[w] = inc;
+  __syncthreads();
+  uint32_t run = inc - sum, tot = 0;
+  for (int k = 0; k < 16; k++) {
+    const uint32_t s = s_wsum[k];
+    if (k < w) run += s;
+    tot += s;
   }
-  if (threadIdx.x == 0) *total_dev = running;
+  for (uint32_t j = lo; j < hi; j++) {
+    const uint32_t v = block_sums[j];
+    block_sums[j] = run;
+    run += v;
+  }
+  if (threadIdx.x == 0) *total_dev = tot;
 }
 
 __global__ void __launch_bounds__(SORT_THREADS) scan_down(int n, const uint32_t* __restrict__ order,
@@ -247,17 +289,18 @@ __global__ void __launch_bounds__(SORT_THREADS) scan_down(int n, const uint32_t*
                                                           const uint32_t* __restrict__ block_sums,
                                                           uint32_t* __restrict__ tile_off) {
   __shared__ uint32_t s_wsum[NWAVES];
-  const uint32_t base = blockIdx.x * (uint32_t)SORT_TILE;
-  uint32_t running = block_sums[blockIdx.x];
-  for (int r = 0; r < SORT_ROUNDS; r++) {
-    const uint32_t rb = base + (uint32_t)r * SORT_THREADS;
-    if (rb >= (uint32_t)n) break;
-    const uint32_t idx = rb + threadIdx.x;
-    const uint32_t v = idx < (uint32_t)n ? tile_count[order[idx]] : 0u;
-    uint32_t tot;
-    const uint32_t ex = block_excl_scan(v, s_wsum, tot);
-    if (idx < (uint32_t)n) tile_off[idx] = running + ex + v;
-    running += tot;
+  const uint32_t first = blockIdx.x * (uint32_t)SCAN_TILE + threadIdx.x * SCAN_PER;
+  uint32_t c[SCAN_PER];
+  gather_counts(n, order, tile_count, first, c);
+  uint32_t acc = 0;
+#pragma unroll
+  for (int k = 0; k < SCAN_PER; k++) acc += c[k];
+  uint32_t tot;
+  uint32_t run = block_sums[blockIdx.x] + block_excl_scan(acc, s_wsum, tot);
+#pragma unroll
+  for (int k = 0; k < SCAN_PER; k++) {
+    run += c[k];
+    if (first + k < (uint32_t)n) tile_off[first + k] = run;
   }
 }
 
@@ -374,7 +417,27 @@ __global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const ui
   }
 }
 
-inline uint32_t sort_blocks(uint32_t n) { return (n + SORT_TILE - 1) / SORT_TILE; }
+inline int sort_kpt(uint32_t n) { return n >= BIG_SORT_MIN ? KPT_BIG : KPT_SMALL; }
+inline uint32_t sort_blocks(uint32_t n, int kpt) {
+  const uint32_t tile = (uint32_t)(SORT_THREADS * kpt);
+  return (n + tile - 1) / tile;
+}
+inline uint32_t scan_blocks(uint32_t n) { return (n + SCAN_TILE - 1) / SCAN_TILE; }
+
+template <int KPT>
+void sort_pass(const uint32_t* src_k, const uint32_t* src_v, const uint32_t* src_v2, uint32_t* dk, uint32_t* dv,
+               uint32_t* dv2, uint32_t n, const uint32_t* n_dev, int shift, int bits, uint32_t* block_hist,
+               uint32_t* digit_total, hipStream_t stream) {
+  const uint32_t nb = sort_blocks(n, KPT);
+  radix_upsweep<KPT><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, n, n_dev, shift, bits, block_hist, nb);
+  radix_scan_digits<<<dim3(RADIX), dim3(SORT_THREADS), 0, stream>>>(block_hist, nb, digit_total);
+  if (src_v2)
+    radix_scatter<2, KPT><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev,
+                                                                        shift, bits, block_hist, nb, digit_total);
+  else
+    radix_scatter<1, KPT><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, nullptr, dk, dv, nullptr, n, n_dev,
+                                                                        shift, bits, block_hist, nb, digit_total);
+}
 
 }  // namespace
 }  // namespace dev
@@ -383,7 +446,8 @@ inline uint32_t sort_blocks(uint32_t n) { return (n + SORT_TILE - 1) / SORT_TILE
 using namespace b2c::dev;
 
 extern "C" size_t b2c_radix_sort_temp_bytes(uint32_t n) {
-  const size_t nb = sort_blocks(n > 0 ? n : 1);
+  // sized for the smaller tiles, so the bound is monotone in n whichever tile size a sort of n picks
+  const size_t nb = sort_blocks(n > 0 ? n : 1, KPT_SMALL);
   return (nb * RADIX + RADIX) * sizeof(uint32_t);
 }
 
@@ -395,9 +459,9 @@ extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* v
   if (temp_bytes < b2c_radix_sort_temp_bytes(n) || begin_bit < 0 || end_bit > 32) return (int)hipErrorInvalidValue;
   const bool two = vals2_in != nullptr;
   if (two && (!vals2_out || !vals2_alt)) return (int)hipErrorInvalidValue;
-  const uint32_t nb = sort_blocks(n);
+  const int kpt = sort_kpt(n);
   uint32_t* block_hist = static_cast<uint32_t*>(temp);
-  uint32_t* digit_total = block_hist + (size_t)nb * RADIX;
+  uint32_t* digit_total = block_hist + (size_t)sort_blocks(n, kpt) * RADIX;
   const int passes = (end_bit - begin_bit + 7) / 8;
   const uint32_t* src_k = keys_in;
   const uint32_t* src_v = vals_in;
@@ -409,15 +473,11 @@ extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* v
     const bool to_out = ((passes - 1 - p) % 2) == 0;
     uint32_t* dk = to_out ? keys_out : keys_alt;
     uint32_t* dv = to_out ? vals_out : vals_alt;
-    uint32_t* dv2 = to_out ? vals2_out : vals2_alt;
-    radix_upsweep<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, n, n_dev, shift, bits, block_hist, nb);
-    radix_scan_digits<<<dim3(RADIX), dim3(SORT_THREADS), 0, stream>>>(block_hist, nb, digit_total);
-    if (two)
-      radix_scatter<2><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift,
-                                                                     bits, block_hist, nb, digit_total);
+    uint32_t* dv2 = two ? (to_out ? vals2_out : vals2_alt) : nullptr;
+    if (kpt == KPT_BIG)
+      sort_pass<KPT_BIG>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total, stream);
     else
-      radix_scatter<1><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, nullptr, dk, dv, nullptr, n, n_dev,
-                                                                     shift, bits, block_hist, nb, digit_total);
+      sort_pass<KPT_SMALL>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total, stream);
     int e = (int)hipGetLastError();
     if (e) return e;
     src_k = dk;
@@ -443,13 +503,13 @@ extern "C" int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const float
   return (int)hipGetLastError();
 }
 
-extern "C" size_t b2c_scan_temp_bytes(uint32_t n) { return ((size_t)sort_blocks(n > 0 ? n : 1) + 1) * sizeof(uint32_t); }
+extern "C" size_t b2c_scan_temp_bytes(uint32_t n) { return ((size_t)scan_blocks(n > 0 ? n : 1) + 1) * sizeof(uint32_t); }
 
 extern "C" int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
                                    uint32_t* total_dev, void* temp, size_t temp_bytes, hipStream_t stream) {
   if (n <= 0) return b2c_hip_fill_u32(total_dev, 0u, 1, stream);
   if (temp_bytes < b2c_scan_temp_bytes((uint32_t)n)) return (int)hipErrorInvalidValue;
-  const uint32_t nb = sort_blocks((uint32_t)n);
+  const uint32_t nb = scan_blocks((uint32_t)n);
   uint32_t* block_sums = static_cast<uint32_t*>(temp);
   scan_reduce<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums);
   scan_top<<<dim3(1), dim3(1024), 0, stream>>>(nb, block_sums, total_dev);

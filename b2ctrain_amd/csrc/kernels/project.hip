@@ -6,6 +6,7 @@
 #include "b2c_kernels.h"
 #include "device_math.h"
 #include "project_one.h"
+#include "raster_common.h"
 
 namespace b2c {
 namespace dev {
@@ -87,7 +88,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
         const uint32_t sgn = (cr >= 0.f ? 1u : 0u) | (cg >= 0.f ? 2u : 0u) | (cb >= 0.f ? 4u : 0u);
         rec[0] = make_float4(pr.mean2d[0], pr.mean2d[1], 0.5f * pr.conic.c00, pr.conic.c01);
         rec[1] = make_float4(0.5f * pr.conic.c11, pr.opac, power, __uint_as_float(sgn));
-        rec[2] = make_float4(fmaxf(cr, 0.f), fmaxf(cg, 0.f), fmaxf(cb, 0.f), 0.f);
+        rec[2] = make_float4(fmaxf(cr, 0.f), fmaxf(cg, 0.f), fmaxf(cb, 0.f), log2_opacity(pr.opac));
       }
       if (a.max_screen) {
         float ms = fmaxf(pr.ex / (float)a.cam.W, pr.ey / (float)a.cam.H);

@@ -103,7 +103,8 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
         contrib = sigma >= 0.f && sigma <= p1.w;
         if (contrib) {
           const float gauss = gauss_weight(sigma);
-          const float alpha = fminf(ALPHA_MAX, p1.y * gauss);
+          const float araw = fragment_alpha(sigma, log2_opacity(p1.y));
+          const float alpha = fminf(ALPHA_MAX, araw);
           const float ra = 1.f / (1.f - alpha);
           const float T_before = ps.T * ra;
           const float vis = alpha * T_before;
@@ -115,7 +116,7 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
           const float v_alpha = (T_before * cr - Sx * ra) * ps.vo.x + (T_before * cg - Sy * ra) * ps.vo.y +
                                 (T_before * cb - Sz * ra) * ps.vo.z + ps.v_o_w * ra;
           const float v_sigma = -alpha * v_alpha;
-          if (p1.y * gauss <= ALPHA_MAX) {
+          if (araw <= ALPHA_MAX) {
             g[2] = 0.5f * v_sigma * dx * dx;
             g[3] = v_sigma * dx * dy;
             g[4] = 0.5f * v_sigma * dy * dy;
@@ -199,7 +200,7 @@ __device__ __forceinline__ void load8(const float* p, float* x) {
 // zero where it is clamped, so g8 = -(sum v_sigma) / opacity.
 __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args a) {
   __shared__ float4 s_g0[BATCH];   // (mx, my, c00 / 2, c01)
-  __shared__ float4 s_g1[BATCH];   // (c11 / 2, opacity, power, 0)
+  __shared__ float4 s_g1[BATCH];   // (c11 / 2, opacity, power, log2 opacity)
   __shared__ float4 s_col[BATCH];  // (max(r, 0), max(g, 0), max(b, 0), sign bits of r, g, b)
   __shared__ uint32_t s_slot[BATCH];
   __shared__ __attribute__((aligned(16))) float sS[3 * G][SROW];  // rows 0-7 vis, 8-15 v_sigma, 16-23 refine
@@ -265,7 +266,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
       const float4 r1 = rec[1], r2 = rec[2];
       s_g0[lane] = rec[0];
-      s_g1[lane] = make_float4(r1.x, r1.y, r1.z, 0.f);
+      s_g1[lane] = make_float4(r1.x, r1.y, r1.z, r2.w);
       s_col[lane] = make_float4(r2.x, r2.y, r2.z, r1.w);
     }
     __syncthreads();
@@ -290,10 +291,9 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             c01dx = g0.w * dx;
             sigma = (t1 * dx + t2 * dy) + c01dx * dy;
           }
-          const bool in = live_px && (batch_start + (uint32_t)sj < ps.last) && sigma >= 0.f && sigma <= g1.z;
+          const bool in = live_px & (batch_start + (uint32_t)sj < ps.last) & (sigma >= 0.f) & (sigma <= g1.z);
           if (__builtin_amdgcn_ballot_w64(in) != 0) {
-          const float gauss = gauss_weight(sigma);
-          const float araw = g1.y * gauss;
+          const float araw = fragment_alpha(sigma, g1.w);
           const float alpha = fminf(ALPHA_MAX, araw);
           const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
           const float Tb = T * ra;

@@ -10,12 +10,11 @@ namespace b2c {
 namespace dev {
 namespace {
 
-// The splat loop is wave-uniform and branch-free per lane: a lane that has terminated (or a fragment that
-// fails the cutoff) contributes alpha = 0, which leaves T, the colour and the last index unchanged; a splat
-// no live lane passes is skipped by the whole wave. Per splat the LDS holds (mx, my, c00/2, c01),
-// (c11/2, opacity, power, 0) and the colour clamped at 0, staged from the projection's 64-byte per-splat
-// record (one cache line per gather); halving c00 and c11 is exact, so sigma is the reference's
-// 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy bit for bit (uncontracted).
+// The splat loop is wave-uniform and branch-free: a lane that has terminated (or a fragment that fails the
+// cutoff) contributes alpha = 0, which leaves T, the colour and the last index unchanged. Per splat the LDS
+// holds (mx, my, c00/2, c01), (c11/2, log2 opacity, power, 0) and the colour clamped at 0, staged from the
+// projection's 64-byte per-splat record (one cache line per gather); halving c00 and c11 is exact, so
+// sigma is the reference's 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy bit for bit (uncontracted).
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   __shared__ float4 s_g0[64], s_g1[64], s_col[64];
   const int n_tiles = a.tiles_x * a.tiles_y;
@@ -38,28 +37,31 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     if ((uint32_t)lane < remaining) {
       const uint32_t gid = a.vals_sorted[start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
-      const float4 r1 = rec[1];
+      const float4 r1 = rec[1], r2 = rec[2];
       s_g0[lane] = rec[0];
-      s_g1[lane] = make_float4(r1.x, r1.y, r1.z, 0.f);
-      s_col[lane] = rec[2];
+      s_g1[lane] = make_float4(r1.x, r2.w, r1.z, 0.f);
+      s_col[lane] = r2;
     }
     __syncthreads();
-    for (uint32_t t = 0; t < remaining; t++) {
-      const float4 g0 = s_g0[t], g1 = s_g1[t];
+    const uint32_t n_splats = __builtin_amdgcn_readfirstlane(remaining);  // scalar loop bound
+    for (uint32_t t = 0; t < n_splats; t++) {
+      const float4 g0 = s_g0[t], g1 = s_g1[t], col = s_col[t];
       float sigma;
       {
 #pragma clang fp contract(off)
         const float dx = pcx - g0.x, dy = pcy - g0.y;
         sigma = ((g0.z * dx) * dx + (g1.x * dy) * dy) + (g0.w * dx) * dy;
       }
-      const bool valid = live && sigma >= 0.f && sigma <= g1.z;
-      if (ballot64(valid) == 0) continue;
-      const float alpha = valid ? fminf(ALPHA_MAX, g1.y * gauss_weight(sigma)) : 0.f;
+      // straight-line: every lane evaluates every splat; failing lanes carry alpha = 0 (bitwise & keeps the
+      // compiler from branching on the compares)
+      const bool valid = live & (sigma >= 0.f) & (sigma <= g1.z);
+      float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));  // sigma < 0: discarded by the select
+      asm volatile("" : "+v"(a_cl));  // keeps the exp out of an exec-masked branch
+      const float alpha = valid ? a_cl : 0.f;
       const float next_T = T * (1.f - alpha);
       const bool stop = next_T <= T_CUTOFF;  // only a valid fragment can stop a lane
-      live = live && !stop;
+      live = live & !stop;
       const float vis = stop ? 0.f : alpha * T;
-      const float4 col = s_col[t];
       r += col.x * vis;
       g += col.y * vis;
       b += col.z * vis;

@@ -55,7 +55,7 @@ typedef struct b2c_project_args {
   uint32_t* hit_info;  /* [n] uint2 (hit mask or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24) */
   float* max_screen;   /* [n] or NULL: max(., max(ex/W, ey/H)) (project.cu:82-83) */
   float* raster_rec;   /* [n][16]: the raster kernels' per-splat record, one 64-byte line: (mx, my, c00/2, c01),
-                          (c11/2, opacity, power, sign bits of r, g, b), (max(r,0), max(g,0), max(b,0), 0), 0 */
+                          (c11/2, opacity, power, sign bits of r, g, b), (max(r,0), max(g,0), max(b,0), log2 opacity), 0 */
   uint32_t* big_list;  /* [n] scratch: splats whose bbox exceeds 32 tiles */
   uint32_t* big_count; /* [1] scratch counter */
   uint32_t* big_info;  /* [n][4] scratch: per big-list entry, bbox origin, width, area, chunk length */
@@ -72,7 +72,7 @@ int b2c_hip_project(const b2c_project_args* a, hipStream_t stream);
 
 /* ---- binning (src/gpu/binning.cu:10-143) ---- */
 
-/* Radix-sort scratch: bytes needed to sort up to n pairs (LSD, 8-bit digits, reduce-then-scan). */
+/* Radix-sort scratch: bytes needed to sort up to n pairs (LSD, 8-bit digits, reduce-then-scan); monotone in n. */
 size_t b2c_radix_sort_temp_bytes(uint32_t n);
 
 /* Stable LSD key-value radix sort of keys_in/vals_in over bits [begin_bit, end_bit) into keys_out/vals_out
