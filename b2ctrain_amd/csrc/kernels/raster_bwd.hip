@@ -388,7 +388,8 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 //    (the raster_bwd_tc.cu:195-198 updates, without atomics). A run crossing a window edge leaves its
 //    per-window partial sums in isect_part (first run of the window, last run of the window) with flags.
 //  * isect_fixup_kernel: one thread per window; the window where a crossing run starts adds the partials
-//    of the following windows the run covers, in order, and finishes the run.
+//    of the following windows the run covers, in order, and finishes the run (the whole wave helps with
+//    runs over many windows).
 // Every window does the same amount of work whatever the run lengths (splats spanning thousands of tiles
 // do not serialise), and the summation order is fixed: the result is deterministic.
 constexpr int RED_VALS = 11;  // g0..g9 and the blend-weight sum
@@ -506,39 +507,69 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
                                          (heads ? W_HAS_HEAD : 0u);
 }
 
-// One wave per window: the window where a crossing run starts sums the partials of the windows the run
-// covers (its last window follows from the run length), 64 windows per step across the lanes, in a fixed
-// reduction order, and finishes the run.
+// One thread per window: the window where a crossing run starts (it has a head and continues into the next
+// window) sums its own piece and the partials of the windows the run covers (the last one follows from the
+// run length), in window order, and finishes the run. A run over more than SHORT_SPAN further windows (a
+// splat covering hundreds of tiles) is summed by the whole wave instead, 64 windows a step, in a fixed
+// order: one wave step per such run, so no lane walks a long chain alone.
+constexpr uint32_t SHORT_SPAN = 4;
+
 __global__ void __launch_bounds__(256) isect_fixup_kernel(b2c_raster_bwd_args a) {
   const uint32_t nwin = (a.num_isect + 63u) / 64u;
-  const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const uint32_t w = blockIdx.x * 256u + threadIdx.x;
   const int lane = threadIdx.x & 63;
-  if (w >= nwin) return;
-  const uint32_t f = a.isect_part_flags[w];
-  // owner: the last run of window w starts in w (w has a head) and continues into w + 1
-  if (!(f & W_CONT_AFTER) || !(f & W_HAS_HEAD)) return;
   const float4* part = reinterpret_cast<const float4*>(a.isect_part);
-  const uint32_t run = a.isect_vals[w * 64u + 63u];
-  // the run covers emit positions [head, head + tile_count)
-  const uint32_t head = __float_as_uint(part[(size_t)w * 6 + 5].w);
-  const uint32_t last_win = min((head + a.tile_count[run] - 1u) / 64u, nwin - 1u);
-  float v[RED_VALS];
-#pragma unroll
-  for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
-  for (uint32_t x0 = w + 1; x0 <= last_win; x0 += 64u) {
-    const uint32_t x = x0 + (uint32_t)lane;
-    if (x <= last_win) add_part(part + (size_t)x * 6, v);  // the run's rows at the start of window x
+  bool owner = false;
+  uint32_t run = NO_RUN, last_win = 0;
+  if (w < nwin) {
+    const uint32_t f = a.isect_part_flags[w];
+    owner = (f & W_CONT_AFTER) && (f & W_HAS_HEAD);
+    if (owner) {
+      run = a.isect_vals[w * 64u + 63u];
+      // the run covers emit positions [head, head + tile_count)
+      const uint32_t head = __float_as_uint(part[(size_t)w * 6 + 5].w);
+      last_win = min((head + a.tile_count[run] - 1u) / 64u, nwin - 1u);
+    }
   }
+  const bool short_run = owner && last_win - w <= SHORT_SPAN;
+  if (short_run) {
+    float v[RED_VALS];
 #pragma unroll
-  for (int k = 0; k < RED_VALS; k++) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v[k] += __shfl_xor(v[k], o);
-  }
-  if (lane == 0) {
+    for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
     add_part(part + (size_t)w * 6 + 3, v);
+#pragma unroll
+    for (uint32_t d = 1; d <= SHORT_SPAN; d++)
+      if (w + d <= last_win) add_part(part + (size_t)(w + d) * 6, v);  // the run's rows at the start of w + d
     float old[RED_VALS];
     prefetch_old(a, run, old);
     finish_run(a, run, v, old);
+  }
+  // long runs: every lane of the wave stays to here (no early exit), so the cross-lane sums are whole
+  uint64_t longs = ballot64(owner && !short_run);
+  while (longs) {
+    const int src = __builtin_ctzll(longs);
+    longs &= longs - 1ull;
+    const uint32_t lw = (uint32_t)__builtin_amdgcn_readlane((int)w, src);
+    const uint32_t lrun = (uint32_t)__builtin_amdgcn_readlane((int)run, src);
+    const uint32_t llast = (uint32_t)__builtin_amdgcn_readlane((int)last_win, src);
+    float v[RED_VALS];
+#pragma unroll
+    for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
+    for (uint32_t x0 = lw + 1; x0 <= llast; x0 += 64u) {
+      const uint32_t x = x0 + (uint32_t)lane;
+      if (x <= llast) add_part(part + (size_t)x * 6, v);
+    }
+#pragma unroll
+    for (int k = 0; k < RED_VALS; k++) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) v[k] += __shfl_xor(v[k], o);
+    }
+    if (lane == src) {
+      add_part(part + (size_t)lw * 6 + 3, v);
+      float old[RED_VALS];
+      prefetch_old(a, lrun, old);
+      finish_run(a, lrun, v, old);
+    }
   }
 }
 
@@ -566,7 +597,7 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
     if (windows) {
       if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;
       isect_reduce_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
-      isect_fixup_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
+      isect_fixup_kernel<<<dim3((windows + 255u) / 256u), dim3(256), 0, stream>>>(*a);
     }
   }
   return (int)hipGetLastError();

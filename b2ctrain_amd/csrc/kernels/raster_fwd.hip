@@ -1,5 +1,6 @@
 // Forward compositing (replaces src/gpu/raster_fwd.cu:8-90, FEAT none, HOLLOW none): one wave64 per 8x8
-// tile, one lane per pixel, the tile's depth-ordered list staged through LDS 64 splats at a time,
+// tile, one lane per pixel, the tile's depth-ordered list staged through LDS 64 splats at a time and
+// split per 4x4 quadrant,
 // front-to-back alpha blending with the 1/255 cutoff (sigma <= power), the 0.999 clamp and the 1e-4
 // transmittance stop. The whole wave leaves as soon as every lane is done. With bwd_info the tile's range
 // end is shrunk to one past the last fragment any pixel composited.
@@ -10,19 +11,28 @@ namespace b2c {
 namespace dev {
 namespace {
 
-// The splat loop is wave-uniform and branch-free: a lane that has terminated (or a fragment that fails the
-// cutoff) contributes alpha = 0, which leaves T, the colour and the last index unchanged. Per splat the LDS
-// holds (mx, my, c00/2, c01), (c11/2, log2 opacity, power, 0) and the colour clamped at 0, staged from the
-// projection's 64-byte per-splat record (one cache line per gather); halving c00 and c11 is exact, so
+// Lanes are grouped by quadrant: lane 16 q + p is pixel p (row-major 4x4) of quadrant q (2x2 over the
+// tile). Each batch of up to 64 splats is staged in LDS together with one list per quadrant of the splats
+// whose ellipse can reach it (quadrant_mask), in depth order; the wave then runs max over quadrants of the
+// list lengths iterations, each lane group taking the next splat of its own quadrant's list. A splat that
+// reaches no pixel of a quadrant would contribute alpha = 0 there, so the result equals the plain sweep.
+// The loop is branch-free: a lane that has terminated, has run out of its list, or whose fragment fails
+// the cutoff contributes alpha = 0, which leaves T, the colour and the last index unchanged. Per splat the
+// LDS holds (mx, my, c00/2, c01), (c11/2, log2 opacity, power, 0) and the colour clamped at 0, staged from
+// the projection's 64-byte per-splat record (one cache line per gather); halving c00 and c11 is exact, so
 // sigma is the reference's 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy bit for bit (uncontracted).
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
-  __shared__ float4 s_g0[64], s_g1[64], s_col[64];
+  // slot 64 is a null splat (power = -inf: no fragment passes) that pads the shorter quadrant lists
+  __shared__ float4 s_g0[65], s_g1[65], s_col[65];
+  __shared__ uint32_t s_list[4][65];  // per quadrant: LDS byte offsets of its splats, in depth order
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
   const int lane = threadIdx.x;
+  const int q = lane >> 4, p = lane & 15;
   const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
-  const int px = tx * RT_W + (lane & 7), py = ty * RT_W + (lane >> 3);
+  const int px = tx * RT_W + (q & 1) * 4 + (p & 3), py = ty * RT_W + (q >> 1) * 4 + (p >> 2);
+  const float x0 = tx * RT_W + 0.5f, y0 = ty * RT_W + 0.5f;  // the tile's first pixel centre
   const bool inside = px < a.W && py < a.H;
   const float pcx = px + 0.5f, pcy = py + 0.5f;
   uint2* ranges = reinterpret_cast<uint2*>(a.tile_ranges);
@@ -30,30 +40,59 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
   bool live = inside;
   uint32_t last = range.x;
+  if (lane < 4) s_list[lane][64] = 64u * 16u;  // read (never used) by the last iteration's prefetch
+  if (lane == 0) {
+    s_g0[64] = make_float4(0.f, 0.f, 0.f, 0.f);
+    s_g1[64] = make_float4(0.f, 0.f, -__builtin_inff(), 0.f);
+    s_col[64] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  const char* lds_g0 = reinterpret_cast<const char*>(s_g0);
+  const char* lds_g1 = reinterpret_cast<const char*>(s_g1);
+  const char* lds_col = reinterpret_cast<const char*>(s_col);
+  constexpr uint32_t NO_OFF = 0xFFFFFFFFu;
   for (uint32_t start = range.x; start < range.y; start += 64) {
     if (ballot64(live) == 0) break;
     const uint32_t remaining = min(64u, range.y - start);
     __syncthreads();
+    uint32_t qmask = 0;
     if ((uint32_t)lane < remaining) {
       const uint32_t gid = a.vals_sorted[start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
-      const float4 r1 = rec[1], r2 = rec[2];
-      s_g0[lane] = rec[0];
+      const float4 r0 = rec[0], r1 = rec[1], r2 = rec[2];
+      s_g0[lane] = r0;
       s_g1[lane] = make_float4(r1.x, r2.w, r1.z, 0.f);
       s_col[lane] = r2;
+      qmask = quadrant_mask(r0.x, r0.y, r0.z, r0.w, r1.x, r1.z, x0, y0);
     }
+    // per-quadrant lists: the lanes with bit qq set, in lane (depth) order, padded with the null splat
+    uint32_t n_iter = 0;
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) {
+      const bool mine = (qmask >> qq) & 1u;
+      const uint64_t bal = ballot64(mine);
+      const uint32_t c = popc64(bal);
+      if (mine) s_list[qq][popc64(bal & below)] = (uint32_t)lane * 16u;
+      if ((uint32_t)lane >= c) s_list[qq][lane] = 64u * 16u;
+      n_iter = max(n_iter, c);
+    }
+    n_iter = __builtin_amdgcn_readfirstlane(n_iter);
     __syncthreads();
-    const uint32_t n_splats = __builtin_amdgcn_readfirstlane(remaining);  // scalar loop bound
-    for (uint32_t t = 0; t < n_splats; t++) {
-      const float4 g0 = s_g0[t], g1 = s_g1[t], col = s_col[t];
+    const uint32_t* my_list = s_list[q];
+    uint32_t last_off = NO_OFF;  // LDS offset of this batch's last contributing splat
+    uint32_t off = my_list[0];
+    for (uint32_t i = 0; i < n_iter; i++) {
+      const uint32_t off_next = my_list[i + 1];  // one entry ahead: the splat reads need not wait for it
+      const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + off);
+      const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + off);
+      const float4 col = *reinterpret_cast<const float4*>(lds_col + off);
       float sigma;
       {
 #pragma clang fp contract(off)
         const float dx = pcx - g0.x, dy = pcy - g0.y;
         sigma = ((g0.z * dx) * dx + (g1.x * dy) * dy) + (g0.w * dx) * dy;
       }
-      // straight-line: every lane evaluates every splat; failing lanes carry alpha = 0 (bitwise & keeps the
-      // compiler from branching on the compares)
+      // bitwise & keeps the compiler from branching on the compares
       const bool valid = live & (sigma >= 0.f) & (sigma <= g1.z);
       float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));  // sigma < 0: discarded by the select
       asm volatile("" : "+v"(a_cl));  // keeps the exp out of an exec-masked branch
@@ -66,8 +105,10 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
       g += col.y * vis;
       b += col.z * vis;
       T = stop ? T : next_T;
-      last = vis > 0.f ? start + t + 1 : last;
+      last_off = vis > 0.f ? off : last_off;
+      off = off_next;
     }
+    if (last_off != NO_OFF) last = start + (last_off >> 4) + 1u;
   }
   if (inside) {
     const int pix = py * a.W + px;

@@ -1,0 +1,93 @@
+"""The raster kernels' quadrant culling test (quadrant_mask in b2ctrain_amd/csrc/kernels/raster_common.h),
+restated in float32 numpy, must be conservative: a quadrant whose pixel centres include one where the
+reference's sigma (src/gpu/raster_fwd.cu:44-50, 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy, uncontracted fp32)
+passes 0 <= sigma <= power must keep its bit. Checked by brute force over all 64 pixel centres on random
+splats, including needle-thin ellipses (axis ratio up to 1e4) whose terms cancel, splats centred inside,
+on the edges and far outside the tile. The GPU parity tests check the device code itself (a wrongly
+culled fragment changes the rendered colour by at least alpha = 1/255 of its weight)."""
+import numpy as np
+
+f32 = np.float32
+
+
+def edge_lb(ah, b, ch, dx, dy):
+    t1 = ah * dx * dx
+    t2 = ch * dy * dy
+    t3 = b * dx * dy
+    return (t1 + t2 + t3) - f32(1e-5) * (np.abs(t1) + np.abs(t2) + np.abs(t3))
+
+
+def quadrant_mask(mx, my, ah, b, ch, power, x0, y0):
+    with np.errstate(all="ignore"):
+        ky = -b / (f32(2) * ch)
+        kx = -b / (f32(2) * ah)
+        ex = [x0 - mx, x0 + f32(3) - mx, x0 + f32(4) - mx, x0 + f32(7) - mx]
+        ey = [y0 - my, y0 + f32(3) - my, y0 + f32(4) - my, y0 + f32(7) - my]
+        mask = np.zeros(mx.shape, np.uint32)
+        for qy in range(2):
+            for qx in range(2):
+                xlo, xhi, ylo, yhi = ex[2 * qx], ex[2 * qx + 1], ey[2 * qy], ey[2 * qy + 1]
+                inside = (xlo <= 0) & (xhi >= 0) & (ylo <= 0) & (yhi >= 0)
+                m = [edge_lb(ah, b, ch, xlo, np.fmin(np.fmax(ky * xlo, ylo), yhi)),
+                     edge_lb(ah, b, ch, xhi, np.fmin(np.fmax(ky * xhi, ylo), yhi)),
+                     edge_lb(ah, b, ch, np.fmin(np.fmax(kx * ylo, xlo), xhi), ylo),
+                     edge_lb(ah, b, ch, np.fmin(np.fmax(kx * yhi, xlo), xhi), yhi)]
+                reach = np.zeros(mx.shape, bool)
+                for mm in m:
+                    reach |= ~(mm > power)
+                mask |= np.where(inside | reach, np.uint32(1 << (2 * qy + qx)), np.uint32(0))
+        degenerate = ~((ah > 0) & (ch > 0))
+        return np.where(degenerate, np.uint32(0xF), mask)
+
+
+def pixel_truth(mx, my, c00, c01, c11, power, x0, y0):
+    """Per quadrant: does any pixel centre pass the reference's cutoff (fp32, uncontracted)?"""
+    truth = np.zeros(mx.shape, np.uint32)
+    for j in range(8):
+        for i in range(8):
+            dx = (x0 + f32(i)) - mx
+            dy = (y0 + f32(j)) - my
+            sig = ((f32(0.5) * c00 * dx) * dx + (f32(0.5) * c11 * dy) * dy) + (c01 * dx) * dy
+            hit = (sig >= 0) & (sig <= power)
+            truth |= np.where(hit, np.uint32(1 << (2 * (j // 4) + i // 4)), np.uint32(0))
+    return truth
+
+
+def _splats(rng, n, spread, log_ratio_max):
+    theta = rng.uniform(0, np.pi, n)
+    s1 = np.exp(rng.uniform(-1.0, 4.0, n))
+    s2 = s1 * np.exp(-rng.uniform(0, log_ratio_max, n))
+    c, s = np.cos(theta), np.sin(theta)
+    # covariance R diag(s1^2, s2^2) R^T (+0.3 px dilation as the projection adds), conic = inverse
+    a = c * c * s1**2 + s * s * s2**2 + 0.3
+    bb = c * s * (s1**2 - s2**2)
+    d = s * s * s1**2 + c * c * s2**2 + 0.3
+    det = a * d - bb * bb
+    c00, c01, c11 = (d / det).astype(f32), (-bb / det).astype(f32), (a / det).astype(f32)
+    x0, y0 = f32(8 * 37 + 0.5), f32(8 * 11 + 0.5)
+    mx = (x0 + 3.5 + rng.normal(0, spread, n)).astype(f32)
+    my = (y0 + 3.5 + rng.normal(0, spread, n)).astype(f32)
+    power = rng.uniform(0.0, 8.0, n).astype(f32)
+    return mx, my, c00, c01, c11, power, x0, y0
+
+
+def test_quadrant_mask_is_conservative():
+    rng = np.random.default_rng(0)
+    checked = culled = 0
+    for spread, ratio in [(3.0, 2.0), (10.0, 5.0), (40.0, 9.2), (1.0, 9.2)]:
+        mx, my, c00, c01, c11, power, x0, y0 = _splats(rng, 200_000, spread, ratio)
+        got = quadrant_mask(mx, my, f32(0.5) * c00, c01, f32(0.5) * c11, power, x0, y0)
+        truth = pixel_truth(mx, my, c00, c01, c11, power, x0, y0)
+        missed = truth & ~got
+        assert not missed.any(), f"culled a reachable quadrant: {np.flatnonzero(missed)[:5]}"
+        checked += int(np.count_nonzero(truth))
+        culled += int(np.count_nonzero(~got & np.uint32(0xF)))
+    assert checked > 100_000 and culled > 100_000  # both outcomes well exercised
+
+
+def test_quadrant_mask_centre_inside_and_degenerate():
+    f = lambda *v: [np.array([x], f32) for x in v]
+    mx, my, ah, b, ch, p = f(101.0, 101.0, 0.5, 0.0, 0.5, 0.0)
+    assert quadrant_mask(mx, my, ah, b, ch, p, f32(96.5), f32(96.5))[0] == 1 << 3  # centre in quadrant (1, 1)
+    mx, my, ah, b, ch, p = f(0.0, 0.0, 0.0, 0.0, 0.5, 1.0)
+    assert quadrant_mask(mx, my, ah, b, ch, p, f32(96.5), f32(96.5))[0] == 0xF
