@@ -164,25 +164,38 @@ constexpr int ROW = 12;    // floats per (tile, splat) gradient row: g0..g9, sum
 // basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero), 6 one, 7 u, 8 v, 9 u^2, 10 uv, 11 v^2, 12-15 zero
 constexpr int B_ONE = 6, B_U = 7, B_V = 8, B_UU = 9, B_UV = 10, B_VV = 11;
 
-// Clamp into the fp16 range (one v_med3_f32; infinities saturate).
-__device__ __forceinline__ float clamp_h(float x) { return __builtin_amdgcn_fmed3f(x, -60000.f, 60000.f); }
+typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-// Split 8 fp32 values into fp16 hi and 2^11-scaled fp16 lo parts.
+// Two fp32 values to fp16, rounding toward zero (v_cvt_pkrtz_f16_f32: one instruction per pair; values
+// beyond the fp16 range saturate to the largest finite value instead of becoming infinite).
+__device__ __forceinline__ half2v pk_rtz(float a, float b) {
+  return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+
+// Split 8 fp32 values into fp16 hi (truncated) and 2^11-scaled fp16 lo parts: x - hi is exact, and the
+// truncated lo keeps the pair to ~2^-21 relative.
 __device__ __forceinline__ void split8(const float* x, half8& hi, half8& lo) {
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const float v = clamp_h(x[e]);
-    const _Float16 h = (_Float16)v;
-    hi[e] = h;
-    lo[e] = (_Float16)((v - (float)h) * LO_SCALE);
+  for (int e = 0; e < 8; e += 2) {
+    const half2v h = pk_rtz(x[e], x[e + 1]);
+    hi[e] = h.x;
+    hi[e + 1] = h.y;
+    const half2v l = pk_rtz((x[e] - (float)h.x) * LO_SCALE, (x[e + 1] - (float)h.y) * LO_SCALE);
+    lo[e] = l.x;
+    lo[e + 1] = l.y;
   }
 }
 
-// fp16 only (the refine statistic: a sum of non-negative terms, 2^-11 relative rounding each).
+// fp16 only, truncated (the refine statistic: a sum of non-negative terms, under 2^-10 relative each).
 __device__ __forceinline__ half8 to_half8(const float* x) {
   half8 h;
 #pragma unroll
-  for (int e = 0; e < 8; e++) h[e] = (_Float16)clamp_h(x[e]);
+  for (int e = 0; e < 8; e += 2) {
+    const half2v p = pk_rtz(x[e], x[e + 1]);
+    h[e] = p.x;
+    h[e + 1] = p.y;
+  }
   return h;
 }
 
@@ -330,11 +343,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
         d0_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_hi, d0_hi, 0, 0, 0);
         d0_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_lo, d0_lo, 0, 0, 0);
         d0_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_lo[kb], b_hi, d0_lo, 0, 0, 0);
-        load8(&sS[2 * G + (nl & (G - 1))][kb * 32 + kg * 8], x);
-        if (nl >= G) {
-#pragma unroll
-          for (int e = 0; e < 8; e++) x[e] = 0.f;
-        }
+        load8(&sS[2 * G + (nl & (G - 1))][kb * 32 + kg * 8], x);  // columns 8-15 of d1 are unused
         d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], to_half8(x), d1, 0, 0, 0);
       }
       // D layout: this lane holds rows 4*kg .. 4*kg+3 of column nl
