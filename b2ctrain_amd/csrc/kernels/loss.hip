@@ -7,6 +7,8 @@
 #include "b2c_kernels.h"
 #include "device_math.h"
 
+#include <stdlib.h>
+
 namespace b2c {
 namespace dev {
 namespace {
@@ -29,7 +31,7 @@ __device__ __forceinline__ float gt_effective(uint32_t gp, int c, bool composite
   return g;
 }
 
-// One wave64 per (strip, channel): a strip is SW = 54 output columns by SH = 35 output rows. Lane l owns
+// One wave64 per (strip, channel): a strip is SW = 54 output columns by SH output rows. Lane l owns
 // statistics column x0 - 5 + l and walks down the rows: each step loads one input row (p, g shifted by the
 // strip's centre values) into a one-row LDS buffer, blurs it horizontally at the lane's column (11 taps,
 // five statistics), pushes the result into an 11-row register ring and, once 11 rows are in, blurs the
@@ -37,9 +39,11 @@ __device__ __forceinline__ float gt_effective(uint32_t gp, int c, bool composite
 // one-row LDS buffer for the horizontal pass of the second blur, whose results fill a second register
 // ring; its vertical pass gives the gradient five rows further down. The loop is unrolled by 11 so that
 // the ring slots are static registers.
-constexpr int SW = 54, SH = 35;
-constexpr int ROWS = SH + 4 * HALO;  // input rows walked per strip: a multiple of 11 (the ring length)
-static_assert(ROWS % 11 == 0, "the row loop is unrolled by the ring length");
+// SH + 4 HALO input rows are walked per strip, a multiple of 11 (the ring length). Taller strips repeat
+// fewer halo rows but make fewer, longer waves; the launcher picks SH per image size (see pick_strip_rows).
+constexpr int SW = 54;
+constexpr int SH_CHOICES[] = {35, 46, 57, 79};
+constexpr int SH_MIN = 35;
 
 struct PixelIn {
   float p, g;
@@ -102,7 +106,10 @@ __device__ __forceinline__ StepRaw fetch_step(const b2c_loss_args& a, int c, int
 // Workgroup b runs on XCD b mod 8; each XCD gets a contiguous band of strips, and the three channel waves of
 // a strip are consecutive on their XCD, so the strip's input lines are read from that XCD's L2 three times
 // rather than from memory.
+template <int SH>
 __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss11 gw, int strips_x, int nstrips) {
+  constexpr int ROWS = SH + 4 * HALO;
+  static_assert(ROWS % 11 == 0, "the row loop is unrolled by the ring length");
   __shared__ float s_p[2][64 + 2 * HALO], s_g[2][64 + 2 * HALO];  // one input row (double buffered)
   __shared__ float s_pm[2][5][64];                                 // one partial-map row (double buffered)
   constexpr int NXCD = 8;
@@ -288,6 +295,49 @@ __global__ void accumulate_kernel(float* acc) {
 
 using namespace b2c::dev;
 
+namespace {
+
+// Waves of the photometric kernel that fit on the device at once (per-CU occupancy from the runtime).
+int resident_waves() {
+  static int cached = 0;
+  if (cached) return cached;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, photometric_kernel<35>, 64, 0) != hipSuccess ||
+      cus <= 0 || per_cu <= 0) {
+    (void)hipGetLastError();
+    return 256 * 12;  // MI355X: 256 CUs, 3 waves of this size per SIMD
+  }
+  cached = cus * per_cu;
+  return cached;
+}
+
+// Strip height: every wave walks SH + 20 rows, so the kernel takes about (rounds of resident waves) x
+// (rows per walk); pick the height that minimises that product for this image.
+// B2C_LOSS_STRIP_ROWS (one of the SH_CHOICES) overrides the choice, for tests and tuning.
+int pick_strip_rows(int W, int H) {
+  if (const char* env = getenv("B2C_LOSS_STRIP_ROWS")) {
+    const int v = atoi(env);
+    for (int sh : SH_CHOICES)
+      if (v == sh) return sh;
+  }
+  const int strips_x = (W + SW - 1) / SW, slots = resident_waves();
+  int best = SH_MIN;
+  long best_cost = -1;
+  for (int sh : SH_CHOICES) {
+    const long waves = (long)strips_x * ((H + sh - 1) / sh) * 3;
+    const long cost = ((waves + slots - 1) / slots) * (sh + 4 * HALO);
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = sh;
+    }
+  }
+  return best;
+}
+
+}  // namespace
+
 extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   if (a->W <= 0 || a->H <= 0) return 0;
   Gauss11 g;
@@ -298,15 +348,22 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
     sum += w[i];
   }
   for (int i = 0; i < 11; i++) g.w[i] = (float)(w[i] / sum);
-  const int strips_x = (a->W + SW - 1) / SW, strips_y = (a->H + SH - 1) / SH;
-  const int nstrips = strips_x * strips_y;
-  photometric_kernel<<<dim3(8 * ((nstrips * 3 + 7) / 8)), dim3(64), 0, stream>>>(*a, g, strips_x, nstrips);
-  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, strips_x * strips_y * 3, a->loss_accum);
+  const int strips_x = (a->W + SW - 1) / SW;
+  const int sh = pick_strip_rows(a->W, a->H);
+  const int nstrips = strips_x * ((a->H + sh - 1) / sh);
+  const dim3 grid(8 * ((nstrips * 3 + 7) / 8)), block(64);
+  switch (sh) {
+    case 35: photometric_kernel<35><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
+    case 46: photometric_kernel<46><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
+    case 57: photometric_kernel<57><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
+    default: photometric_kernel<79><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
+  }
+  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum);
   return (int)hipGetLastError();
 }
 
 extern "C" size_t b2c_loss_partials(int W, int H) {
-  return (size_t)((W + SW - 1) / SW) * ((H + SH - 1) / SH) * 3;
+  return (size_t)((W + SW - 1) / SW) * ((H + SH_MIN - 1) / SH_MIN) * 3;  // the most strips any choice makes
 }
 
 extern "C" int b2c_hip_accumulate_loss(float* loss_accum, hipStream_t stream) {
