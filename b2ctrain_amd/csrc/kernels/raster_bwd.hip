@@ -160,7 +160,10 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int BATCH = 64;  // splats staged in LDS per step
 constexpr int G = 8;       // splats per MFMA group
 constexpr int SROW = 68;   // pixel stride of the per-fragment scalar rows (64 + 4: spreads the B reads over banks)
-constexpr int ROW = 12;    // floats per (tile, splat) gradient row: g0..g9, sum of blend weights, 0
+// (tile, splat) row: raw moments of the tile's fragments about the tile centre, 12 floats: sum v_sigma *
+// [1, u, v, u^2, uv, v^2], refine sum, sum vis, sum vis * v_rgb, unused
+constexpr int ROW = 12;
+constexpr int R_SV = 0, R_REF = 6, R_VIS = 7, R_VRGB = 8;
 // basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero), 6 one, 7 u, 8 v, 9 u^2, 10 uv, 11 v^2, 12-15 zero
 constexpr int B_ONE = 6, B_U = 7, B_V = 8, B_UU = 9, B_UV = 10, B_VV = 11;
 
@@ -217,7 +220,6 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   __shared__ float4 s_col[BATCH];  // (max(r, 0), max(g, 0), max(b, 0), sign bits of r, g, b)
   __shared__ uint32_t s_slot[BATCH];
   __shared__ __attribute__((aligned(16))) float sS[3 * G][SROW];  // rows 0-7 vis, 8-15 v_sigma, 16-23 refine
-  __shared__ float sC[2][16][17];                                 // products: [which][basis row][column]
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
@@ -241,7 +243,6 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
   const int lx = lane & 7, ly = lane >> 3;
   const int px = tx * RT_W + lx, py = ty * RT_W + ly;
-  const float ox = tx * RT_W + RT_W * 0.5f, oy = ty * RT_W + RT_W * 0.5f;  // tile centre
   const float u = lx + 0.5f - RT_W * 0.5f, v = ly + 0.5f - RT_W * 0.5f;
   PixelState ps = load_pixel(a, px, py, range.x);
   const float W2 = (float)a.W * (float)a.W, H2 = (float)a.H * (float)a.H;
@@ -306,24 +307,24 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
           }
           const bool in = live_px & (batch_start + (uint32_t)sj < ps.last) & (sigma >= 0.f) & (sigma <= g1.z);
           if (__builtin_amdgcn_ballot_w64(in) != 0) {
-          const float araw = fragment_alpha(sigma, g1.w);
-          const float alpha = fminf(ALPHA_MAX, araw);
-          const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
-          const float Tb = T * ra;
-          const float vis = alpha * Tb;
-          const float4 col = s_col[sj];
-          const float cv = col.x * cv_x + col.y * cv_y + col.z * cv_z;
-          const float v_alpha = Tb * cv - ra * Q;
-          const float v_sigma = -alpha * v_alpha;
-          // refine statistic: |d(loss)/d(mean2d)| scaled to pixels, over the final alpha
-          const float gx = 2.f * t1 + g0.w * dy, gy = c01dx + 2.f * t2;
-          const float rf = fabsf(v_sigma) * __builtin_amdgcn_sqrtf(W2 * gx * gx + H2 * gy * gy) * r_scale;
-          const bool unclamped = araw <= ALPHA_MAX;
-          o_vis = in ? vis : 0.f;
-          o_vs = (in && unclamped) ? v_sigma : 0.f;
-          o_r = (in && unclamped) ? rf : 0.f;
-          T = in ? Tb : T;
-          Q = in ? Q + vis * cv : Q;
+            // a lane without this fragment runs the same arithmetic with alpha = 0: ra = 1, vis = 0,
+            // v_sigma = 0 and T, Q unchanged (every operand stays finite)
+            const float araw = fragment_alpha(sigma, g1.w);
+            const float alpha = in ? fminf(ALPHA_MAX, araw) : 0.f;
+            const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
+            const float Tb = T * ra;
+            const float vis = alpha * Tb;
+            const float4 col = s_col[sj];
+            const float cv = col.x * cv_x + col.y * cv_y + col.z * cv_z;
+            const float v_alpha = Tb * cv - ra * Q;
+            const float v_sigma = araw <= ALPHA_MAX ? -alpha * v_alpha : 0.f;  // clamped: no sigma gradient
+            // refine statistic: |d(loss)/d(mean2d)| scaled to pixels, over the final alpha
+            const float gx = 2.f * t1 + g0.w * dy, gy = c01dx + 2.f * t2;
+            o_r = fabsf(v_sigma) * __builtin_amdgcn_sqrtf(W2 * gx * gx + H2 * gy * gy) * r_scale;
+            o_vis = vis;
+            o_vs = v_sigma;
+            T = Tb;
+            Q = Q + vis * cv;
           }
         }
         sS[jj][lane] = o_vis;
@@ -346,42 +347,36 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
         load8(&sS[2 * G + (nl & (G - 1))][kb * 32 + kg * 8], x);  // columns 8-15 of d1 are unused
         d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], to_half8(x), d1, 0, 0, 0);
       }
-      // D layout: this lane holds rows 4*kg .. 4*kg+3 of column nl
+      // D layout: lane (nl, kg) holds rows 4 kg .. 4 kg + 3 of column nl. The lanes holding wanted rows
+      // store them as the (tile, splat) row's raw moments (the reduce turns them into gradients).
+      {
+        const int j = nl & (G - 1);
+        if (j < gcount) {
+          float* row = a.isect_rows + (size_t)s_slot[gbase + j] * ROW;
+          float dv[4];
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
-        sC[0][kg * 4 + rr][nl] = d0_hi[rr] + d0_lo[rr] * (1.f / LO_SCALE);
-        sC[1][kg * 4 + rr][nl] = d1[rr];
-      }
-      __syncthreads();
-      // ---- per-splat rows: lane = (part, splat), three float4 parts per row
-      if (nl < gcount && kg < 3) {
-        const int j = nl, sj = gbase + j;
-        const float sc = a.inv_gscale;
-        float4 out;
-        const float sv = sC[0][B_ONE][G + j];
-        if (kg == 2) {
-          const float op = s_g1[sj].y;
-          out = make_float4(-sv / op * sc, sC[1][B_ONE][j] * (1.f / R_SCALE) * sc, sC[0][B_ONE][j], 0.f);
-        } else {
-          const float4 g0 = s_g0[sj];
-          const float hc11 = s_g1[sj].x;
-          const float mx = g0.x - ox, my = g0.y - oy;
-          const float svu = sC[0][B_U][G + j], svv = sC[0][B_V][G + j];
-          const float svuu = sC[0][B_UU][G + j], svuv = sC[0][B_UV][G + j], svvv = sC[0][B_VV][G + j];
-          const float m2vv = svvv - 2.f * my * svv + my * my * sv;
-          if (kg == 0) {
-            const float m1u = svu - mx * sv, m1v = svv - my * sv;  // sum v_sigma (u - mx), (v - my)
-            const float m2uu = svuu - 2.f * mx * svu + mx * mx * sv;
-            const float m2uv = svuv - my * svu - mx * svv + mx * my * sv;
-            out = make_float4(-(2.f * g0.z * m1u + g0.w * m1v) * sc, -(g0.w * m1u + 2.f * hc11 * m1v) * sc,
-                              0.5f * m2uu * sc, m2uv * sc);
-          } else {
-            const uint32_t sgn = __float_as_uint(s_col[sj].w);
-            out = make_float4(0.5f * m2vv * sc, (sgn & 1u) ? sC[0][0][j] * sc : 0.f,
-                              (sgn & 2u) ? sC[0][1][j] * sc : 0.f, (sgn & 4u) ? sC[0][2][j] * sc : 0.f);
+          for (int rr = 0; rr < 4; rr++) dv[rr] = d0_hi[rr] + d0_lo[rr] * (1.f / LO_SCALE);
+          if (nl < G) {  // vis column: rows 0-2 (v_rgb) and 6 (one); the refine product's row 6
+            if (kg == 0) {
+              row[R_VRGB] = dv[0];
+              row[R_VRGB + 1] = dv[1];
+              row[R_VRGB + 2] = dv[2];
+            } else if (kg == 1) {
+              row[R_VIS] = dv[2];
+              row[R_REF] = d1[2];
+            }
+          } else {  // v_sigma column: rows 6-11 (one, u, v, u^2, uv, v^2)
+            if (kg == 1) {
+              row[R_SV] = dv[2];
+              row[R_SV + 1] = dv[3];
+            } else if (kg == 2) {
+              row[R_SV + 2] = dv[0];
+              row[R_SV + 3] = dv[1];
+              row[R_SV + 4] = dv[2];
+              row[R_SV + 5] = dv[3];
+            }
           }
         }
-        rows[(size_t)s_slot[sj] * (ROW / 4) + kg] = out;
       }
     }
     batch_end = batch_start;
@@ -463,6 +458,40 @@ __device__ __forceinline__ void add_part(const float4* p, float (&v)[RED_VALS]) 
   v[8] += q2.x; v[9] += q2.y; v[10] += q2.z;
 }
 
+// Gradient lanes g0..g9 and the blend-weight sum of one (tile, splat) row from its raw moments about the
+// tile centre (raster_bwd_tc.cu:172-198 accumulates the same quantities per fragment): with (mx, my) the
+// splat centre relative to the tile centre, the first and second moments of v_sigma about the splat centre
+// give the mean and conic gradients, the vis moments the colour gradients, and where a fragment is
+// unclamped v_alpha * gauss = -v_sigma / opacity gives g8. The tile comes from the row's emit-order key.
+__device__ __forceinline__ void row_gradients(const b2c_raster_bwd_args& a, uint32_t s, uint32_t id,
+                                              float (&v)[RED_VALS]) {
+  const float4* rw = reinterpret_cast<const float4*>(a.isect_rows) + (size_t)s * (ROW / 4);
+  const float4 q0 = rw[0], q1 = rw[1], q2 = rw[2];
+  const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)id * 4;
+  const float4 r0 = rec[0], r1 = rec[1];  // (mx, my, c00 / 2, c01), (c11 / 2, opacity, power, sign bits)
+  const uint32_t t = a.isect_keys[s];
+  const uint32_t ty = t / (uint32_t)a.tiles_x, tx = t - ty * (uint32_t)a.tiles_x;
+  const float mx = r0.x - ((float)(tx * RT_W) + RT_W * 0.5f), my = r0.y - ((float)(ty * RT_W) + RT_W * 0.5f);
+  const float sv = q0.x, svu = q0.y, svv = q0.z, svuu = q0.w, svuv = q1.x, svvv = q1.y;
+  const float sc = a.inv_gscale;
+  const float m1u = svu - mx * sv, m1v = svv - my * sv;  // sum v_sigma (u - mx), (v - my)
+  const float m2uu = svuu - 2.f * mx * svu + mx * mx * sv;
+  const float m2uv = svuv - my * svu - mx * svv + mx * my * sv;
+  const float m2vv = svvv - 2.f * my * svv + my * my * sv;
+  const uint32_t sgn = __float_as_uint(r1.w);
+  v[0] = -(2.f * r0.z * m1u + r0.w * m1v) * sc;
+  v[1] = -(r0.w * m1u + 2.f * r1.x * m1v) * sc;
+  v[2] = 0.5f * m2uu * sc;
+  v[3] = m2uv * sc;
+  v[4] = 0.5f * m2vv * sc;
+  v[5] = (sgn & 1u) ? q2.x * sc : 0.f;
+  v[6] = (sgn & 2u) ? q2.y * sc : 0.f;
+  v[7] = (sgn & 4u) ? q2.z * sc : 0.f;
+  v[8] = -sv / r1.y * sc;
+  v[9] = q1.z * (1.f / R_SCALE) * sc;  // the raster pre-scales refine terms into the fp16 range
+  v[10] = q1.w;
+}
+
 __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a) {
   const uint32_t m = a.num_isect;
   const int lane = threadIdx.x & 63;
@@ -477,16 +506,9 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
   const uint32_t before = lo == 0 ? NO_RUN : ids[lo - 1];
   const uint32_t after = lo + 64u < m ? ids[lo + 64u] : NO_RUN;
   float v[RED_VALS];
-  {
-    float4 q0 = make_float4(0.f, 0.f, 0.f, 0.f), q1 = q0, q2 = q0;
-    if (valid) {
-      q0 = rows[(size_t)s * 3];
-      q1 = rows[(size_t)s * 3 + 1];
-      q2 = rows[(size_t)s * 3 + 2];
-    }
-    v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w; v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
-    v[8] = q2.x; v[9] = q2.y; v[10] = q2.z;
-  }
+#pragma unroll
+  for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
+  if (valid) row_gradients(a, s, id, v);
   const uint32_t prev = dpp_u32<0x138, 0xF>(id, before);  // wave_shr:1; lane 0 gets `before`
   const bool head = valid && id != prev;
   const uint64_t heads = ballot64(head);
@@ -595,7 +617,8 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
   if (a->mode == 0) {
     raster_bwd_fp32_kernel<<<grid, block, 0, stream>>>(*a);
   } else {
-    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->tile_count || !a->raster_rec)
+    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->isect_keys || !a->tile_count ||
+        !a->raster_rec)
       return (int)hipErrorInvalidValue;
     raster_bwd_mfma_kernel<<<grid, block, 0, stream>>>(*a);
     if (a->split_event) {

@@ -155,10 +155,12 @@ int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream);
  * to match the reference's fp32 kernel).
  *
  * Mode 0 accumulates into v_splat / vis_weight with float atomics, as the reference does. Mode 1 uses no
- * atomics: each (tile, splat) pair writes its 12-float row [g0..g9, sum of blend weights, 0] to
+ * atomics: each (tile, splat) pair writes a 12-float row of raw moments about the tile centre (sum v_sigma
+ * * [1, u, v, u^2, uv, v^2], refine sum, sum of blend weights, sum vis * v_rgb, unused) to
  * isect_rows[slot_sorted[i]] (rows of pairs past the shrunk range end are written as zeros); the rows of
- * one splat are then a contiguous run in emit order, which a segmented reduction sums in a fixed order
- * and adds to v_splat, vis_weight and vis_flag. The result is deterministic. */
+ * one splat are then a contiguous run in emit order, which a segmented reduction turns into gradient
+ * lanes (tile centre from isect_keys), sums in a fixed order and adds to v_splat, vis_weight and
+ * vis_flag. The result is deterministic. */
 typedef struct b2c_raster_bwd_args {
   const uint32_t* tile_ranges;
   const uint32_t* vals_sorted;
@@ -178,6 +180,7 @@ typedef struct b2c_raster_bwd_args {
   uint32_t num_isect;         /* M */
   const uint32_t* slot_sorted;/* [M] emit position of list entry i */
   const uint32_t* isect_vals; /* [M] splat id of emit position s (the emit kernel's values) */
+  const uint32_t* isect_keys; /* [M] tile id of emit position s (the emit kernel's keys, before the sort) */
   const uint32_t* tile_count; /* [n] intersections per splat (the length of its run of emit positions) */
   const uint32_t* tile_end;   /* [n_tiles + 1] list end before the forward's shrink; [n_tiles] = sentinel start */
   float* isect_rows;          /* [M][12] scratch */
