@@ -274,6 +274,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
     const uint32_t batch_start = batch_end > range.x + BATCH ? batch_end - BATCH : range.x;
     const int count = (int)(batch_end - batch_start);
     __syncthreads();
+    const int ngroups = (count + G - 1) / G;
     if (lane < count) {
       const uint32_t gid = a.vals_sorted[batch_start + lane];
       s_slot[lane] = a.slot_sorted[batch_start + lane];
@@ -282,19 +283,30 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       s_g0[lane] = rec[0];
       s_g1[lane] = make_float4(r1.x, r1.y, r1.z, r2.w);
       s_col[lane] = make_float4(r2.x, r2.y, r2.z, r1.w);
+    } else if (lane < ngroups * G) {  // pad the last group with null splats (power = -inf: never composited)
+      s_g0[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
+      s_g1[lane] = make_float4(0.f, 1.f, -__builtin_inff(), 0.f);
+      s_col[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
-    const int ngroups = (count + G - 1) / G;
     for (int grp = ngroups - 1; grp >= 0; grp--) {
       const int gbase = grp * G;
       const int gcount = min(G, count - gbase);
       // ---- replay: this pixel's three scalars for each splat of the group (zero when not composited)
+      // the group's LDS byte offset, kept in one VGPR for the whole group (immediate offsets per splat)
+      uint32_t goff = (uint32_t)gbase * 16u;
+      asm volatile("" : "+v"(goff));
+      const char* lds_g0 = reinterpret_cast<const char*>(s_g0) + goff;
+      const char* lds_g1 = reinterpret_cast<const char*>(s_g1) + goff;
+      const char* lds_col = reinterpret_cast<const char*>(s_col) + goff;
+      // the last list index of the group this pixel composited, relative to the group start
+      const int last_rel = (int)ps.last - (int)(batch_start + (uint32_t)gbase);
 #pragma unroll
       for (int jj = G - 1; jj >= 0; jj--) {
         float o_vis = 0.f, o_vs = 0.f, o_r = 0.f;
-        if (jj < gcount) {
-          const int sj = gbase + jj;
-          const float4 g0 = s_g0[sj], g1 = s_g1[sj];
+        {
+          const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + jj * 16);
+          const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + jj * 16);
           const float dx = ps.pcx - g0.x, dy = ps.pcy - g0.y;
           float sigma, t1, t2, c01dx;
           {
@@ -305,7 +317,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             c01dx = g0.w * dx;
             sigma = (t1 * dx + t2 * dy) + c01dx * dy;
           }
-          const bool in = live_px & (batch_start + (uint32_t)sj < ps.last) & (sigma >= 0.f) & (sigma <= g1.z);
+          const bool in = live_px & (jj < last_rel) & (sigma >= 0.f) & (sigma <= g1.z);
           if (__builtin_amdgcn_ballot_w64(in) != 0) {
             // a lane without this fragment runs the same arithmetic with alpha = 0: ra = 1, vis = 0,
             // v_sigma = 0 and T, Q unchanged (every operand stays finite)
@@ -314,7 +326,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             const float ra = __builtin_amdgcn_rcpf(1.f - alpha);
             const float Tb = T * ra;
             const float vis = alpha * Tb;
-            const float4 col = s_col[sj];
+            const float4 col = *reinterpret_cast<const float4*>(lds_col + jj * 16);
             const float cv = col.x * cv_x + col.y * cv_y + col.z * cv_z;
             const float v_alpha = Tb * cv - ra * Q;
             const float v_sigma = araw <= ALPHA_MAX ? -alpha * v_alpha : 0.f;  // clamped: no sigma gradient
