@@ -304,30 +304,63 @@ __global__ void __launch_bounds__(SORT_THREADS) scan_down(int n, const uint32_t*
   }
 }
 
-// Small splats: one thread per depth rank writes its slots [tile_off - count, tile_off) walking the set
-// bits of its hit mask (row-major bbox order). Depth-consecutive splats own adjacent slot ranges, so a
-// wave's stores land in one short stretch of the key/value arrays. Big splats only record their base.
-__global__ void __launch_bounds__(256) emit_small_kernel(b2c_emit_args a, uint32_t* __restrict__ big_base) {
-  const int r = blockIdx.x * 256 + threadIdx.x;
-  if (r >= a.n) return;
-  const uint32_t i = a.order[r];
-  const uint32_t cnt = a.tile_count[i];
-  if (cnt == 0) return;
-  const uint32_t base = a.tile_off[r] - cnt;
-  const uint2 hi = reinterpret_cast<const uint2*>(a.hit_info)[i];
-  if (hi.x == 0xFFFFFFFFu) {
-    big_base[i] = base;
-    return;
+// Position of the k-th set bit (k counted from 0) of m, by halving: five popcounts.
+__device__ __forceinline__ uint32_t select_bit(uint32_t m, uint32_t k) {
+  uint32_t pos = 0;
+#pragma unroll
+  for (int half = 16; half >= 1; half >>= 1) {
+    const uint32_t low = (uint32_t)__builtin_popcount(m & ((1u << half) - 1u));
+    const bool up = k >= low;
+    k = up ? k - low : k;
+    m = up ? m >> half : m;
+    pos = up ? pos + half : pos;
   }
-  if (base + cnt > a.cap) return;
-  const uint32_t min_x = hi.y & 0xFFFu, min_y = (hi.y >> 12) & 0xFFFu, bw = hi.y >> 24;
-  uint32_t m = hi.x;
-  for (uint32_t k = 0; k < cnt && m; k++) {
-    const uint32_t bit = (uint32_t)__builtin_ctz(m);
-    m &= m - 1u;
+  return pos;
+}
+
+// Small splats: each wave takes 64 consecutive depth ranks, whose slot ranges [tile_off - count, tile_off)
+// are adjacent (big splats' ranges, filled by emit_big_kernel, interleave). The wave's intersections are
+// dealt to the lanes round-robin: intersection q belongs to the last rank whose running start is <= q (a
+// binary search over the wave's 64 starts in LDS) and is the k-th set bit of that splat's hit mask
+// (row-major bbox order). Every lane does the same work and consecutive lanes write consecutive slots.
+// Big splats only record their base.
+__global__ void __launch_bounds__(256) emit_small_kernel(b2c_emit_args a, uint32_t* __restrict__ big_base) {
+  __shared__ uint32_t s_start[4][64], s_base[4][64], s_mask[4][64], s_info[4][64], s_id[4][64];
+  const int w = threadIdx.x >> 6, lane = lane_id();
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  uint32_t i = 0, cnt = 0, base = 0;
+  uint2 hi = make_uint2(0u, 0u);
+  if (r < a.n) {
+    i = a.order[r];
+    cnt = a.tile_count[i];
+    if (cnt) {
+      base = a.tile_off[r] - cnt;
+      hi = reinterpret_cast<const uint2*>(a.hit_info)[i];
+      if (hi.x == 0xFFFFFFFFu) big_base[i] = base;
+    }
+  }
+  const uint32_t c = (cnt && hi.x != 0xFFFFFFFFu && base + cnt <= a.cap) ? cnt : 0u;
+  const uint32_t incl = wave_incl_scan(c);
+  const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+  s_start[w][lane] = incl - c;
+  s_base[w][lane] = base;
+  s_mask[w][lane] = hi.x;
+  s_info[w][lane] = hi.y;
+  s_id[w][lane] = i;
+  __syncthreads();
+  for (uint32_t q = (uint32_t)lane; q < total; q += 64u) {
+    int j = 0;  // last lane with start <= q (the lanes after the owner start past q)
+#pragma unroll
+    for (int step = 32; step >= 1; step >>= 1)
+      if (s_start[w][j + step] <= q) j += step;
+    const uint32_t k = q - s_start[w][j];
+    const uint32_t info = s_info[w][j];
+    const uint32_t min_x = info & 0xFFFu, min_y = (info >> 12) & 0xFFFu, bw = info >> 24;
+    const uint32_t bit = select_bit(s_mask[w][j], k);
     const uint32_t row = bit / bw;
-    a.keys[base + k] = (min_y + row) * (uint32_t)a.tiles_x + min_x + (bit - row * bw);
-    a.vals[base + k] = i;
+    const uint32_t slot = s_base[w][j] + k;
+    a.keys[slot] = (min_y + row) * (uint32_t)a.tiles_x + min_x + (bit - row * bw);
+    a.vals[slot] = s_id[w][j];
   }
 }
 
