@@ -177,14 +177,14 @@ def main():
     # hipEvents on the context's stream. Algorithmic bytes per launch: per composited-range intersection its
     # list entry, emit position and projected splat (4 + 4 + 48 B) plus its gradient row (48 B, written);
     # per intersection past the shrunk end its zero row (48 B); per pixel out_rgba, out_feat, last_idx and
-    # v_out (52 B). MFMA: 10 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
+    # v_out (52 B). MFMA: 8 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
     m_shrunk = f_sweep // 64
     m_total = int(info.num_isect)
     bwd_bytes = 104 * m_shrunk + 48 * (m_total - m_shrunk) + 52 * W * H
     t_bwd = mean["raster_bwd_ms"] * 1e-3
     bwd_gbs = bwd_bytes / t_bwd / 1e9
     groups = int(np.ceil(m_shrunk / 8.0))
-    mfma_tflops = groups * 10 * 16384 / t_bwd / 1e12
+    mfma_tflops = groups * 8 * 16384 / t_bwd / 1e12
     traffic = read_traffic("raster_bwd_mfma_kernel")
     roofline = {
         "kernel": "raster_bwd_mfma_kernel",
