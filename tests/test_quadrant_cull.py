@@ -1,10 +1,11 @@
-"""The raster kernels' quadrant culling test (quadrant_mask in b2ctrain_amd/csrc/kernels/raster_common.h),
-restated in float32 numpy, must be conservative: a quadrant whose pixel centres include one where the
-reference's sigma (src/gpu/raster_fwd.cu:44-50, 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy, uncontracted fp32)
-passes 0 <= sigma <= power must keep its bit. Checked by brute force over all 64 pixel centres on random
-splats, including needle-thin ellipses (axis ratio up to 1e4) whose terms cancel, splats centred inside,
-on the edges and far outside the tile. The GPU parity tests check the device code itself (a wrongly
-culled fragment changes the rendered colour by at least alpha = 1/255 of its weight)."""
+"""The forward raster's quadrant culling test (quadrant_mask in b2ctrain_amd/csrc/kernels/raster_common.h),
+restated in float32 numpy, must be conservative: a quadrant with a pixel centre where the reference's
+sigma (src/gpu/raster_fwd.cu:44-50, 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy, uncontracted fp32) passes
+0 <= sigma <= power must keep its bit. Checked by brute force over all 64 pixel centres on random splats,
+including needle-thin ellipses (axis ratio up to 1e5) whose terms cancel, splats centred inside, on the
+edges and far outside the tile, and adversarially: power set to the fp32 sigma of one pixel, which puts
+that pixel exactly on the cutoff. The GPU parity tests check the device code itself (a wrongly culled
+fragment changes the rendered colour by at least alpha = 1/255 of its weight)."""
 import numpy as np
 
 f32 = np.float32
@@ -38,6 +39,12 @@ def quadrant_mask(mx, my, ah, b, ch, power, x0, y0):
                 mask |= np.where(inside | reach, np.uint32(1 << (2 * qy + qx)), np.uint32(0))
         degenerate = ~((ah > 0) & (ch > 0))
         return np.where(degenerate, np.uint32(0xF), mask)
+
+
+def sigma_at(mx, my, c00, c01, c11, x0, y0, i, j):
+    dx = (x0 + f32(i)) - mx
+    dy = (y0 + f32(j)) - my
+    return ((f32(0.5) * c00 * dx) * dx + (f32(0.5) * c11 * dy) * dy) + (c01 * dx) * dy
 
 
 def pixel_truth(mx, my, c00, c01, c11, power, x0, y0):
@@ -91,3 +98,17 @@ def test_quadrant_mask_centre_inside_and_degenerate():
     assert quadrant_mask(mx, my, ah, b, ch, p, f32(96.5), f32(96.5))[0] == 1 << 3  # centre in quadrant (1, 1)
     mx, my, ah, b, ch, p = f(0.0, 0.0, 0.0, 0.0, 0.5, 1.0)
     assert quadrant_mask(mx, my, ah, b, ch, p, f32(96.5), f32(96.5))[0] == 0xF
+
+
+def test_quadrant_mask_keeps_pixels_exactly_on_the_cutoff():
+    rng = np.random.default_rng(7)
+    for spread, ratio in [(3.0, 2.0), (1.0, 9.2), (5.0, 11.5), (30.0, 9.2), (100.0, 11.5)]:
+        mx, my, c00, c01, c11, _, x0, y0 = _splats(rng, 200_000, spread, ratio)
+        i = rng.integers(0, 8, mx.size)
+        j = rng.integers(0, 8, mx.size)
+        sig = sigma_at(mx, my, c00, c01, c11, x0, y0, i.astype(f32), j.astype(f32))
+        power = np.where(sig >= 0, sig, f32(0)).astype(f32)  # pixel (i, j) passes with sigma == power
+        on = sig >= 0
+        qm = quadrant_mask(mx, my, f32(0.5) * c00, c01, f32(0.5) * c11, power, x0, y0)
+        qbit = np.uint32(1) << (2 * (j // 4) + i // 4).astype(np.uint32)
+        assert not (on & ((qm & qbit) == 0)).any(), "quadrant mask dropped a pixel on the cutoff"
