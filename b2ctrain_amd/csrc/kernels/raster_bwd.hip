@@ -318,7 +318,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             sigma = (t1 * dx + t2 * dy) + c01dx * dy;
           }
           const bool in = live_px & (jj < last_rel) & (sigma >= 0.f) & (sigma <= g1.z);
-          if (__builtin_amdgcn_ballot_w64(in) != 0) {
+          {  // straight-line: a lane without this fragment computes zeros (alpha = 0)
             // a lane without this fragment runs the same arithmetic with alpha = 0: ra = 1, vis = 0,
             // v_sigma = 0 and T, Q unchanged (every operand stays finite)
             const float araw = fragment_alpha(sigma, g1.w);
