@@ -106,7 +106,7 @@ template <int DEG>
 __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   constexpr int K = (DEG + 1) * (DEG + 1);
   constexpr int PER = 11 + 3 * K;
-  __shared__ float s_buf[VJP_BLOCK * PER];  // v_splat rows in, then grad_out rows out
+  __shared__ __attribute__((aligned(16))) float s_buf[VJP_BLOCK * PER];  // v_splat rows in, grad_out rows out
   __shared__ uint32_t s_vis[VJP_BLOCK];
   const int i0 = blockIdx.x * VJP_BLOCK;
   const int i = i0 + threadIdx.x;
@@ -115,7 +115,12 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   const uint32_t vis = in_range ? a.vis_flag[i] : 0u;
   if (vis) a.vis_flag[i] = 0u;
   s_vis[threadIdx.x] = vis;
-  for (int j = threadIdx.x; j < rows * GRAD_LANES; j += VJP_BLOCK) s_buf[j] = a.v_splat[(size_t)i0 * GRAD_LANES + j];
+  // the block's v_splat rows are one contiguous, 16-byte aligned stretch (VJP_BLOCK * 13 floats per block)
+  const int nin = rows * GRAD_LANES;
+  const float* vin = a.v_splat + (size_t)i0 * GRAD_LANES;
+  for (int j = threadIdx.x; j < nin / 4; j += VJP_BLOCK)
+    reinterpret_cast<float4*>(s_buf)[j] = reinterpret_cast<const float4*>(vin)[j];
+  for (int j = (nin & ~3) + threadIdx.x; j < nin; j += VJP_BLOCK) s_buf[j] = vin[j];
   __syncthreads();
   // read then clear the consumed rows (optim.cu:110-121)
   for (int j = threadIdx.x; j < rows * GRAD_LANES; j += VJP_BLOCK)
@@ -137,9 +142,10 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
 #pragma unroll
   for (int k = 0; k < GRAD_LANES; k++) if (!__builtin_isfinite(g[k])) any = false;
 
-  float out[PER];
-#pragma unroll
-  for (int k = 0; k < PER; k++) out[k] = 0.f;
+  // this splat's grad_out row is built in LDS as it is computed (the SH part first), so no 11 + 3K
+  // register array stays live across the projection VJP
+  float* out = s_buf + threadIdx.x * PER;
+  bool done = false;
   if (any) {
     const float4 po = reinterpret_cast<const float4*>(a.pos_op)[i];
     const float4 q = reinterpret_cast<const float4*>(a.quat)[i];
@@ -152,10 +158,17 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
       const float ul = sqrtf(ux * ux + uy * uy + uz * uz);
       const float iul = 1.f / ul;
       const float vx = ux * iul, vy = uy * iul, vz = uz * iul;
-      float basis[K];
-      sh_basis<DEG>(vx, vy, vz, basis);
       const int kmax = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
       const float3 vc = make_float3(g[5], g[6], g[7]);
+      {
+        float basis[K];
+        sh_basis<DEG>(vx, vy, vz, basis);
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+          const float bk = k < kmax ? basis[k] : 0.f;
+          out[11 + k * 3] = bk * vc.x; out[12 + k * 3] = bk * vc.y; out[13 + k * 3] = bk * vc.z;
+        }
+      }
       float vvx, vvy, vvz;
       float coef[3 * K];
       sv.load_all<DEG>(i, coef);
@@ -260,23 +273,25 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
       out[0] = gpx; out[1] = gpy; out[2] = gpz; out[3] = g_op;
       out[4] = gq.x; out[5] = gq.y; out[6] = gq.z; out[7] = gq.w;
       out[8] = glx; out[9] = gly; out[10] = glz;
-#pragma unroll
-      for (int k = 0; k < K; k++) {
-        const float bk = k < kmax ? basis[k] : 0.f;
-        out[11 + k * 3] = bk * vc.x; out[12 + k * 3] = bk * vc.y; out[13 + k * 3] = bk * vc.z;
-      }
+      done = true;
     }
   }
+  if (!done) {
 #pragma unroll
-  for (int k = 0; k < PER; k++) s_buf[threadIdx.x * PER + k] = out[k];
+    for (int k = 0; k < PER; k++) out[k] = 0.f;
+  }
   s_vis[threadIdx.x] = any ? 1u : 0u;
   __syncthreads();
+  // the block's grad_out rows: one contiguous stretch, 16-byte aligned (VJP_BLOCK * PER floats per block)
   float* o = a.grad_out + (size_t)i0 * PER;
+  const int nout = rows * PER;
   if (a.accumulate) {
-    for (int j = threadIdx.x; j < rows * PER; j += VJP_BLOCK)
+    for (int j = threadIdx.x; j < nout; j += VJP_BLOCK)
       if (s_vis[j / PER]) o[j] += s_buf[j];
   } else {
-    for (int j = threadIdx.x; j < rows * PER; j += VJP_BLOCK) o[j] = s_buf[j];
+    for (int j = threadIdx.x; j < nout / 4; j += VJP_BLOCK)
+      reinterpret_cast<float4*>(o)[j] = reinterpret_cast<const float4*>(s_buf)[j];
+    for (int j = (nout & ~3) + threadIdx.x; j < nout; j += VJP_BLOCK) o[j] = s_buf[j];
   }
 }
 
