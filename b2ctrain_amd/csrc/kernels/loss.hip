@@ -35,7 +35,8 @@ __device__ __forceinline__ float gt_effective(uint32_t gp, int c, bool composite
 // statistics column x0 - 5 + l and walks down the rows: each step loads one input row (p, g shifted by the
 // strip's centre values) into a one-row LDS buffer, blurs it horizontally at the lane's column (11 taps,
 // five statistics), pushes the result into an 11-row register ring and, once 11 rows are in, blurs the
-// ring vertically: SSIM and its five partial maps at that row. The partial-map row goes through a second
+// ring vertically: SSIM and its partial maps at that row (three: the terms without a per-pixel factor are
+// summed before the blur). The partial-map row goes through a second
 // one-row LDS buffer for the horizontal pass of the second blur, whose results fill a second register
 // ring; its vertical pass gives the gradient five rows further down. The loop is unrolled by 11 so that
 // the ring slots are static registers.
@@ -111,7 +112,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
   constexpr int ROWS = SH + 4 * HALO;
   static_assert(ROWS % 11 == 0, "the row loop is unrolled by the ring length");
   __shared__ float s_p[2][64 + 2 * HALO], s_g[2][64 + 2 * HALO];  // one input row (double buffered)
-  __shared__ float s_pm[2][5][64];                                 // one partial-map row (double buffered)
+  __shared__ float s_pm[2][3][64];                                 // one partial-map row (double buffered)
   constexpr int NXCD = 8;
   const int per = (nstrips * 3 + NXCD - 1) / NXCD;  // work items per XCD
   const int item = (blockIdx.x % NXCD) * per + blockIdx.x / NXCD;
@@ -134,7 +135,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
   const int xs = x0 - HALO + lane;  // this lane's statistics column
   const bool out_lane = lane >= HALO && lane < HALO + SW;
   float ring1[11][5];  // horizontal blur of the statistics, by row mod 11
-  float ring2[11][5];  // horizontal blur of the partial maps, by row mod 11
+  float ring2[11][3];  // horizontal blur of the partial maps, by row mod 11
   float loss_local = 0.f;
   StepRaw nxt = fetch_step(a, c, x0, y0, lane, 0);
   for (int base = 0; base < ROWS; base += 11) {
@@ -205,31 +206,32 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
             A = k * d_mu1; B = k * d_s1; Bm = B * st[0]; Cc = k * d_s12; Cm = Cc * st[2];
           }
         }
-        s_pm[buf][0][lane] = A; s_pm[buf][1][lane] = B; s_pm[buf][2][lane] = Bm;
-        s_pm[buf][3][lane] = Cc; s_pm[buf][4][lane] = Cm;
+        // the gradient is blur(A) + 2 p blur(B) - 2 blur(B mu1) + g blur(C) - blur(C mu2): the three terms
+        // without a per-output factor are blurred as one map
+        s_pm[buf][0][lane] = A - 2.f * Bm - Cm; s_pm[buf][1][lane] = B; s_pm[buf][2][lane] = Cc;
         __syncthreads();
         // ---- horizontal pass of the second blur at output column x0 + lane - 5
         const int j2 = (j + 1) % 11;  // slot of partial-map row ys (stats row index r - 10)
 #pragma unroll
-        for (int k = 0; k < 5; k++) ring2[j2][k] = 0.f;
+        for (int k = 0; k < 3; k++) ring2[j2][k] = 0.f;
         if (out_lane) {
 #pragma unroll
           for (int d = 0; d < 11; d++) {
             const float w = gw.w[d];
 #pragma unroll
-            for (int k = 0; k < 5; k++) ring2[j2][k] += w * s_pm[buf][k][lane - HALO + d];
+            for (int k = 0; k < 3; k++) ring2[j2][k] += w * s_pm[buf][k][lane - HALO + d];
           }
         }
         if (r >= 4 * HALO) {
           // ---- output row yo = ys - 5 complete: vertical pass, gradient
           const int yo = ys - HALO, xo = xs;
-          float acc[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+          float acc[3] = {0.f, 0.f, 0.f};
 #pragma unroll
           for (int d = 0; d < 11; d++) {
             const int slot = (j2 + 1 + d) % 11;
             const float w = gw.w[d];
 #pragma unroll
-            for (int k = 0; k < 5; k++) acc[k] += w * ring2[slot][k];
+            for (int k = 0; k < 3; k++) acc[k] += w * ring2[slot][k];
           }
           if (out_lane && yo < H && xo < W) {
             const int pix = yo * W + xo;
@@ -238,7 +240,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
             const float gt_a = gt_channel(cur.g_out, 3);
             const float M = cur.w_out * (a.mask ? gt_a : 1.f) * norm;
             const float sgn = p > g ? 1.f : (p < g ? -1.f : 0.f);
-            const float grad = M * a.l1_w * sgn + acc[0] + 2.f * ps * acc[1] - 2.f * acc[2] + gs * acc[3] - acc[4];
+            const float grad = M * a.l1_w * sgn + acc[0] + 2.f * ps * acc[1] + gs * acc[2];
             a.v_out[(size_t)pix * 4 + c] = grad * a.grad_scale;
             if (c == 0) {
               float va = 0.f;
