@@ -67,7 +67,8 @@ def read_traffic(kernel):
 
 def cpu_baseline(r, scene, bg):
     """The CPU port (oracle, fp32 tiled restatement, one host core) timed on the same frame: forward raster
-    + backward raster over the GPU's own tile lists and per-pixel loss gradient."""
+    + backward raster over the GPU's own tile lists and per-pixel loss gradient. Returns the frame's
+    composited-fragment count (F_contrib) and the cpu_baseline record."""
     from oracle import oracle as O
 
     W, H = scene.W, scene.H
@@ -87,7 +88,7 @@ def cpu_baseline(r, scene, bg):
     shr = fw["tile_ranges"].astype(np.int64)
     f_sweep = int(64 * (shr[:, 1] - shr[:, 0]).clip(min=0).sum())
     secs = (t1 - t0) + (t2 - t1)
-    return {
+    return fw["f_contrib"], {
         "value": f_sweep / secs / 1e9,
         "unit": "Gfrag/s",
         "cores": 1,
@@ -112,7 +113,7 @@ def _cpu_model():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--splats", type=int, default=1_000_000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -245,6 +246,8 @@ def main():
         "stages_ms_mean": {k: round(v, 4) for k, v in mean.items()},
         "stages_ms_median": {k: round(v, 4) for k, v in med.items()},
         "raster_fwd_bwd_ms": round(t_fb, 4),
+        # the step without the projection VJP, the reference's own timed subtotal
+        "step_without_vjp_ms": round(mean["total_ms"] - mean["vjp_ms"], 4),
         "roofline": roofline,
         "stage_rooflines": stage_rooflines,
     }
@@ -252,7 +255,10 @@ def main():
         log("bench: CPU baseline (oracle port, one core)")
         r.step(mode=args.mode, bg=bgs[-1])
         r.sync()
-        out["cpu_baseline"] = cpu_baseline(r, scene, bgs[-1])
+        f_contrib, out["cpu_baseline"] = cpu_baseline(r, scene, bgs[-1])
+        # composited fragments of that frame, counted by the CPU port over the GPU's own lists
+        out["config"]["F_contrib"] = f_contrib
+        out["gfrag_contrib_per_s"] = round(f_contrib / (t_fb * 1e-3) / 1e9, 3)
     else:
         out["cpu_baseline"] = None
     r.close()

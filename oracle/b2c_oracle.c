@@ -402,9 +402,14 @@ uint32_t orc_bin(int n, const uint32_t* tile_count, const uint32_t* hit_info, co
  * Forward raster (raster_fwd.cu:8-71). Each pixel walks its tile's list front to back; the whole
  * tile's early exit only skips pixels that are already done, so a per-pixel loop is equivalent.
  * ---------------------------------------------------------------------------------------------- */
+/* Fragments the last orc_raster_fwd call composited (F_contrib: alpha >= 1/255, before termination). */
+static uint64_t g_fwd_contrib = 0;
+uint64_t orc_last_fwd_contrib(void) { return g_fwd_contrib; }
+
 void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], uint32_t* tile_ranges,
                     const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
                     float* out_rgba, float* out_T, uint32_t* last_idx) {
+  uint64_t contrib = 0;
   for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
     int tx = tile % tiles_x, ty = tile / tiles_x;
     uint32_t rx = tile_ranges[tile * 2], ry = tile_ranges[tile * 2 + 1];
@@ -429,6 +434,7 @@ void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], u
         r += fmaxf(col[0], 0.f) * vis; g += fmaxf(col[1], 0.f) * vis; b += fmaxf(col[2], 0.f) * vis;
         T = next_T;
         last = idx + 1;
+        contrib++;
       }
       size_t pix = (size_t)py * W + px;
       out_rgba[pix * 4] = r + T * bg[0]; out_rgba[pix * 4 + 1] = g + T * bg[1]; out_rgba[pix * 4 + 2] = b + T * bg[2];
@@ -439,6 +445,7 @@ void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], u
     }
     tile_ranges[tile * 2 + 1] = max_last;
   }
+  g_fwd_contrib = contrib;
 }
 
 /* ------------------------------------------------------------------------------------------------

@@ -66,6 +66,7 @@ def lib():
         _lib.orc_bin.restype = C.c_uint32
         _lib.orc_bin.argtypes = [C.c_int, p, p, p, p, C.c_int, C.c_int, C.c_uint32, p, p, p, p, p]
         _lib.orc_raster_fwd.restype = None
+        _lib.orc_last_fwd_contrib.restype = C.c_uint64
         _lib.orc_raster_fwd.argtypes = [C.c_int] * 4 + [p] * 9
         _lib.orc_photometric.restype = C.c_double
         _lib.orc_photometric.argtypes = [C.c_int, C.c_int, p, p, p, C.POINTER(OrcLoss), p]
@@ -197,6 +198,7 @@ def raster_fwd(pr, bn, W, H, bg):
     lib().orc_raster_fwd(W, H, tx, ty, _ptr(bgv), _ptr(ranges), _ptr(bn["vals_sorted"]), _ptr(pr["proj0"]),
                          _ptr(pr["proj1"]), _ptr(pr["proj2"]), *[_ptr(out[k]) for k in ("out_rgba", "out_T", "last_idx")])
     out["tile_ranges"] = ranges
+    out["f_contrib"] = int(lib().orc_last_fwd_contrib())
     return out
 
 
