@@ -398,11 +398,13 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 // Per-splat sum of the (tile, splat) rows. In emit order the rows of one splat are one contiguous run and
 // isect_vals[slot] (the emitted splat id) names the run, so this is a segmented reduction over a
 // contiguous array, in two kernels:
-//  * isect_reduce_kernel: one wave per aligned window of 64 rows (coalesced 48-byte rows), a segmented
-//    inclusive scan across lanes on DPP row shifts and row broadcasts. A run that starts and ends inside
-//    the window is finished there: its last lane adds the sums to v_splat[0..9], vis_weight and vis_flag
-//    (the raster_bwd_tc.cu:195-198 updates, without atomics). A run crossing a window edge leaves its
-//    per-window partial sums in isect_part (first run of the window, last run of the window) with flags.
+//  * isect_reduce_kernel: one wave per aligned window of RED_WIN = 256 rows, walked as four 64-row
+//    sub-windows (coalesced 48-byte rows), each a segmented inclusive scan across lanes on DPP row shifts
+//    and row broadcasts; the sums of a run that continues into the next sub-window are carried in
+//    registers. A run that starts and ends inside the window is finished there: its last lane adds the
+//    sums to v_splat[0..9], vis_weight and vis_flag (the raster_bwd_tc.cu:195-198 updates, without
+//    atomics). A run crossing a window edge leaves its per-window partial sums in isect_part (first run of
+//    the window, last run of the window) with flags.
 //  * isect_fixup_kernel: one thread per window; the window where a crossing run starts adds the partials
 //    of the following windows the run covers, in order, and finishes the run (the whole wave helps with
 //    runs over many windows).
@@ -411,6 +413,8 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 constexpr int RED_VALS = 11;  // g0..g9 and the blend-weight sum
 constexpr uint32_t NO_RUN = 0xFFFFFFFFu;
 constexpr uint32_t W_CONT_BEFORE = 1u, W_CONT_AFTER = 2u, W_HAS_HEAD = 4u;
+constexpr int RED_SUB = 4;                  // 64-row sub-windows per reduce wave
+constexpr uint32_t RED_WIN = 64u * RED_SUB;  // rows per window (one wave)
 
 // DPP controls (GCN/CDNA): row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143,
 // wave_shl:1 = 0x130, wave_shr:1 = 0x138.
@@ -508,46 +512,85 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
   const uint32_t m = a.num_isect;
   const int lane = threadIdx.x & 63;
   const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
-  const uint32_t lo = w * 64u;
-  if (lo >= m) return;
+  const uint32_t wlo = w * RED_WIN;
+  if (wlo >= m) return;
   const uint32_t* ids = a.isect_vals;
-  const float4* rows = reinterpret_cast<const float4*>(a.isect_rows);
-  const uint32_t s = lo + lane;
-  const bool valid = s < m;
-  const uint32_t id = valid ? ids[s] : NO_RUN;
-  const uint32_t before = lo == 0 ? NO_RUN : ids[lo - 1];
-  const uint32_t after = lo + 64u < m ? ids[lo + 64u] : NO_RUN;
-  float v[RED_VALS];
+  const uint32_t before = wlo == 0 ? NO_RUN : ids[wlo - 1];
+  // wave-uniform state across the window's 64-row sub-windows: the partial sums of the run that continues
+  // into the next sub-window, whether that run started before the window, and where it started
+  float carry[RED_VALS];
 #pragma unroll
-  for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
-  if (valid) row_gradients(a, s, id, v);
-  const uint32_t prev = dpp_u32<0x138, 0xF>(id, before);  // wave_shr:1; lane 0 gets `before`
-  const bool head = valid && id != prev;
-  const uint64_t heads = ballot64(head);
-  const uint32_t id63 = (uint32_t)__builtin_amdgcn_readlane((int)id, 63);
-  const bool cont_after = id63 != NO_RUN && after == id63;
-  const bool cont_before = (heads & 1ull) == 0;  // row 0 continues a run from the previous window
-  const uint32_t nid = dpp_u32<0x130, 0xF>(id, cont_after ? id63 : NO_RUN);  // wave_shl:1; lane 63 gets the fill
-  const bool tail = valid && nid != id;
-  // the first run of the window ends at the lane before the second head (or 63)
-  const uint64_t later_heads = heads & ~1ull;
-  const int last_valid = (int)min(63u, m - 1u - lo);
-  const int first_tail = later_heads ? __builtin_ctzll(later_heads) - 1 : last_valid;
-  const bool is_first = lane == first_tail;
-  const bool is_last = lane == 63;
-  const bool complete = tail && !(is_first && cont_before) && !(is_last && cont_after);
-  float old[RED_VALS];
-  if (complete) prefetch_old(a, id, old);
-  seg_scan(valid ? id : NO_RUN, v);
-  if (complete) finish_run(a, id, v, old);
+  for (int k = 0; k < RED_VALS; k++) carry[k] = 0.f;
+  bool carry_from_before = false;
+  uint32_t carry_head = 0;
+  uint32_t prev_id = before;
+  bool window_cont_before = false, window_has_head = false;
   float4* part = reinterpret_cast<float4*>(a.isect_part) + (size_t)w * 6;
-  if (is_first && cont_before) store_part(part, v);            // continuation of an earlier run
-  if (is_last && cont_after && !(is_first && cont_before)) {  // a run that starts here: sums and head slot
-    store_part(part + 3, v);
-    part[5].w = __uint_as_float(lo + 63u - (uint32_t)__builtin_clzll(heads));
+  for (int sub = 0; sub < RED_SUB; sub++) {
+    const uint32_t lo = wlo + 64u * (uint32_t)sub;
+    if (lo >= m) break;
+    const uint32_t s = lo + lane;
+    const bool valid = s < m;
+    const uint32_t id = valid ? ids[s] : NO_RUN;
+    const uint32_t next_id = lo + 64u < m ? ids[lo + 64u] : NO_RUN;
+    float v[RED_VALS];
+#pragma unroll
+    for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
+    if (valid) row_gradients(a, s, id, v);
+    const uint32_t prev = dpp_u32<0x138, 0xF>(id, prev_id);  // wave_shr:1; lane 0 gets the row before
+    const bool head = valid && id != prev;
+    const uint64_t heads = ballot64(head);
+    const uint32_t id63 = (uint32_t)__builtin_amdgcn_readlane((int)id, 63);
+    const bool cont_after = id63 != NO_RUN && next_id == id63;
+    const bool cont_before = (heads & 1ull) == 0;  // row 0 continues the run of the row before
+    if (sub == 0) window_cont_before = cont_before;
+    window_has_head = window_has_head || heads != 0ull;
+    const uint32_t nid = dpp_u32<0x130, 0xF>(id, cont_after ? id63 : NO_RUN);  // wave_shl:1; lane 63 gets the fill
+    const bool tail = valid && nid != id;
+    // the first run of the sub-window ends at the lane before the second head (or at the last valid row)
+    const uint64_t later_heads = heads & ~1ull;
+    const int last_valid = (int)min(63u, m - 1u - lo);
+    const int first_tail = later_heads ? __builtin_ctzll(later_heads) - 1 : last_valid;
+    const bool in_first = lane <= first_tail;
+    const bool last_is_first = later_heads == 0ull;  // the sub-window holds one run only
+    // the first run started before the window (then it is the window's first piece, finished by the fixup)
+    const bool first_from_before = cont_before && (sub == 0 ? before != NO_RUN : carry_from_before);
+    const bool is_first = lane == first_tail;
+    const bool is_last = lane == 63;
+    const bool crosses_window = cont_after && sub == RED_SUB - 1;
+    const bool complete = tail && !(is_first && first_from_before);
+    float old[RED_VALS];
+    if (complete) prefetch_old(a, id, old);
+    seg_scan(valid ? id : NO_RUN, v);
+    if (cont_before && sub > 0 && in_first) {  // the run carried from the previous sub-window
+#pragma unroll
+      for (int k = 0; k < RED_VALS; k++) v[k] += carry[k];
+    }
+    if (complete) finish_run(a, id, v, old);
+    if (is_first && first_from_before && (!cont_after || !last_is_first || sub == RED_SUB - 1))
+      store_part(part, v);  // the window's first piece ends here (or spans the whole window)
+    // the last run of the sub-window continues: carry it, or leave it for the fixup at the window's edge
+    const uint32_t last_head = lo + 63u - (heads ? (uint32_t)__builtin_clzll(heads) : 63u);
+    const bool last_from_before = last_is_first ? first_from_before : false;
+    if (cont_after) {
+      if (!crosses_window) {
+#pragma unroll
+        for (int k = 0; k < RED_VALS; k++) carry[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[k]), 63));
+        carry_from_before = last_from_before;
+        carry_head = (heads && !(last_is_first && cont_before)) ? last_head : carry_head;
+      } else if (is_last && !last_from_before) {  // a run that starts in this window: sums and head slot
+        store_part(part + 3, v);
+        part[5].w = __uint_as_float((heads && !(last_is_first && cont_before)) ? last_head : carry_head);
+      }
+    }
+    prev_id = id63;
+    if (!cont_after) carry_from_before = false;
   }
-  if (lane == 0) a.isect_part_flags[w] = (cont_before ? W_CONT_BEFORE : 0u) | (cont_after ? W_CONT_AFTER : 0u) |
-                                         (heads ? W_HAS_HEAD : 0u);
+  const uint32_t wend = min(wlo + RED_WIN, m);
+  const bool window_cont_after = wend < m && ids[wend - 1] == ids[wend];
+  if (lane == 0)
+    a.isect_part_flags[w] = (window_cont_before && before != NO_RUN ? W_CONT_BEFORE : 0u) |
+                            (window_cont_after ? W_CONT_AFTER : 0u) | (window_has_head ? W_HAS_HEAD : 0u);
 }
 
 // One thread per window: the window where a crossing run starts (it has a head and continues into the next
@@ -558,7 +601,7 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
 constexpr uint32_t SHORT_SPAN = 4;
 
 __global__ void __launch_bounds__(256) isect_fixup_kernel(b2c_raster_bwd_args a) {
-  const uint32_t nwin = (a.num_isect + 63u) / 64u;
+  const uint32_t nwin = (a.num_isect + RED_WIN - 1u) / RED_WIN;
   const uint32_t w = blockIdx.x * 256u + threadIdx.x;
   const int lane = threadIdx.x & 63;
   const float4* part = reinterpret_cast<const float4*>(a.isect_part);
@@ -568,10 +611,10 @@ __global__ void __launch_bounds__(256) isect_fixup_kernel(b2c_raster_bwd_args a)
     const uint32_t f = a.isect_part_flags[w];
     owner = (f & W_CONT_AFTER) && (f & W_HAS_HEAD);
     if (owner) {
-      run = a.isect_vals[w * 64u + 63u];
+      run = a.isect_vals[w * RED_WIN + RED_WIN - 1u];
       // the run covers emit positions [head, head + tile_count)
       const uint32_t head = __float_as_uint(part[(size_t)w * 6 + 5].w);
-      last_win = min((head + a.tile_count[run] - 1u) / 64u, nwin - 1u);
+      last_win = min((head + a.tile_count[run] - 1u) / RED_WIN, nwin - 1u);
     }
   }
   const bool short_run = owner && last_win - w <= SHORT_SPAN;
@@ -637,7 +680,7 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
       const int e = (int)hipEventRecord(static_cast<hipEvent_t>(a->split_event), stream);
       if (e) return e;
     }
-    const uint32_t windows = (a->num_isect + 63u) / 64u;
+    const uint32_t windows = (a->num_isect + RED_WIN - 1u) / RED_WIN;
     if (windows) {
       if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;
       isect_reduce_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);

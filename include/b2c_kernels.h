@@ -184,8 +184,8 @@ typedef struct b2c_raster_bwd_args {
   const uint32_t* tile_count; /* [n] intersections per splat (the length of its run of emit positions) */
   const uint32_t* tile_end;   /* [n_tiles + 1] list end before the forward's shrink; [n_tiles] = sentinel start */
   float* isect_rows;          /* [M][12] scratch */
-  float* isect_part;          /* [ceil(M / 64)][24] scratch: partial sums of runs crossing 64-row windows */
-  uint32_t* isect_part_flags; /* [ceil(M / 64)] scratch */
+  float* isect_part;          /* [ceil(M / 256)][24] scratch: partial sums of runs crossing 256-row windows */
+  uint32_t* isect_part_flags; /* [ceil(M / 256)] scratch */
   void* split_event;          /* optional hipEvent_t recorded between the raster kernel and the reduce */
 } b2c_raster_bwd_args;
 int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stream);
