@@ -43,7 +43,14 @@ b2c_camera_gpu CameraGPU::dev() const {
   return d;
 }
 
+RenderCtx::~RenderCtx() {
+  if (count_event) (void)hipEventDestroy(count_event);
+}
+
 void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
+  // no system-scope fence on this event: its writeback of the L2s stalls the queue for ~5 us, and the count
+  // lands in coherent pinned memory without it (bin_and_sort checks a sentinel)
+  if (!count_event) HIP_CHECK(hipEventCreateWithFlags(&count_event, hipEventDisableTiming | hipEventDisableSystemFence));
   W = w; H = h;
   tiles_x = (W + RT_W - 1) / RT_W; tiles_y = (H + RT_W - 1) / RT_W; n_tiles = tiles_x * tiles_y;
   tile_bits = 1;
@@ -81,7 +88,7 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
   isect_alt_k.reserve(ncap, false, stream); isect_alt_v.reserve(ncap, false, stream);
   isect_alt_v2.reserve(ncap, false, stream);
   slot_sorted.reserve(ncap, false, stream); isect_rows.reserve(ncap * 3, false, stream);
-  isect_part.reserve((ncap / 64 + 1) * 6, false, stream); isect_part_flags.reserve(ncap / 64 + 1, false, stream);
+  isect_part.reserve((ncap / 256 + 1) * 6, false, stream); isect_part_flags.reserve(ncap / 256 + 1, false, stream);
   isect_cap = ncap;
   sort_tmp.reserve(b2c_radix_sort_temp_bytes((uint32_t)ncap));
 }
@@ -125,6 +132,34 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   LAUNCH_CHECK(b2c_hip_project(&a, stream));
 }
 
+namespace {
+
+// 3. emit in depth order, then a stable sort on the tile id alone keeps each tile's list in depth order;
+// 4. tile ranges. Sized for ctx.isect_cap; the live intersection count is read from counters[1].
+void emit_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
+  const uint32_t cap = (uint32_t)ctx.isect_cap;
+  const uint32_t* total_dev = ctx.counters.ptr + 1;
+  b2c_emit_args e{};
+  e.n = m.n; e.order = ctx.order; e.tile_count = ctx.tile_count; e.tile_off = ctx.tile_off;
+  e.hit_info = reinterpret_cast<const uint32_t*>(ctx.hit_info.ptr);
+  e.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr); e.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
+  e.tiles_x = ctx.tiles_x; e.tiles_y = ctx.tiles_y; e.cap = cap;
+  e.keys = ctx.keys; e.vals = ctx.vals;
+  e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
+  e.big_info = reinterpret_cast<const uint32_t*>(ctx.big_info.ptr); e.big_chunk = ctx.big_chunk;
+  e.big_items = ctx.big_items; e.big_items_count = ctx.counters.ptr + 2;
+  LAUNCH_CHECK(b2c_hip_emit(&e, stream));
+  // The tile pass carries the emit positions next to the splat ids: the backward writes each (tile, splat)
+  // gradient row at its emit position, where a splat's rows are contiguous.
+  LAUNCH_CHECK(b2c_hip_radix_sort_kv2(ctx.keys, nullptr, ctx.vals, ctx.keys_sorted, ctx.slot_sorted, ctx.vals_sorted,
+                                      ctx.isect_alt_k, ctx.isect_alt_v, ctx.isect_alt_v2, cap, total_dev, 0,
+                                      ctx.tile_bits, ctx.sort_tmp.ptr, ctx.sort_tmp.bytes(), stream));
+  LAUNCH_CHECK(b2c_hip_tile_ranges(cap, total_dev, ctx.keys_sorted, nullptr, nullptr, nullptr, (uint32_t)ctx.n_tiles,
+                                   reinterpret_cast<uint32_t*>(ctx.tile_ranges.ptr), ctx.tile_end, stream));
+}
+
+}  // namespace
+
 void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   if (m.n == 0) {
     ctx.num_isect = 0;
@@ -141,33 +176,28 @@ void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   // 2. inclusive scan of the tile counts in depth order; the total comes back to the host (binning.cu:125-133)
   LAUNCH_CHECK(b2c_hip_scan_counts(n, ctx.order, ctx.tile_count, ctx.tile_off, ctx.counters.ptr + 1, ctx.sort_tmp.ptr,
                                    ctx.sort_tmp.bytes(), stream));
+  constexpr uint32_t NO_COUNT = 0xFFFFFFFFu;  // not a possible total (the emit capacity is far below it)
+  volatile uint32_t* h_total = ctx.h_count.ptr;
+  *h_total = NO_COUNT;  // the previous copy into it completed in the previous call
   HIP_CHECK(hipMemcpyAsync(ctx.h_count.ptr, ctx.counters.ptr + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
-  HIP_CHECK(hipStreamSynchronize(stream));
-  const uint32_t total = ctx.h_count.ptr[0];
-  ctx.num_isect = total;
-  ctx.ensure_isect_capacity(total, stream);
-  if (total == 0) {
-    ctx.tile_ranges.zero(stream);
-    return;
+  HIP_CHECK(hipEventRecord(ctx.count_event, stream));
+  // 3-4 are queued before the host has the total: they are sized for the current capacity and read the
+  // live count on the device (the emit skips splats whose slots would not fit), so the GPU does not idle
+  // while the count travels to the host. A total beyond the capacity grows the buffers and runs them again.
+  emit_and_sort(ctx, m, stream);
+  HIP_CHECK(hipEventSynchronize(ctx.count_event));
+  // the copy has completed; without the event's fence its value may reach host memory a little later
+  for (int spin = 0; *h_total == NO_COUNT && spin < (1 << 20); spin++) {
   }
-  // 3. emit in depth order, then a stable sort on the tile id alone keeps each tile's list in depth order
-  b2c_emit_args e{};
-  e.n = n; e.order = ctx.order; e.tile_count = ctx.tile_count; e.tile_off = ctx.tile_off;
-  e.hit_info = reinterpret_cast<const uint32_t*>(ctx.hit_info.ptr);
-  e.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr); e.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
-  e.tiles_x = ctx.tiles_x; e.tiles_y = ctx.tiles_y; e.cap = (uint32_t)ctx.isect_cap;
-  e.keys = ctx.keys; e.vals = ctx.vals;
-  e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
-  e.big_info = reinterpret_cast<const uint32_t*>(ctx.big_info.ptr); e.big_chunk = ctx.big_chunk;
-  e.big_items = ctx.big_items; e.big_items_count = ctx.counters.ptr + 2;
-  LAUNCH_CHECK(b2c_hip_emit(&e, stream));
-  // The tile pass carries the emit positions next to the splat ids: the backward writes each (tile, splat)
-  // gradient row at its emit position, where a splat's rows are contiguous.
-  LAUNCH_CHECK(b2c_hip_radix_sort_kv2(ctx.keys, nullptr, ctx.vals, ctx.keys_sorted, ctx.slot_sorted, ctx.vals_sorted,
-                                      ctx.isect_alt_k, ctx.isect_alt_v, ctx.isect_alt_v2, total, nullptr, 0,
-                                      ctx.tile_bits, ctx.sort_tmp.ptr, ctx.sort_tmp.bytes(), stream));
-  LAUNCH_CHECK(b2c_hip_tile_ranges(total, nullptr, ctx.keys_sorted, nullptr, nullptr, nullptr, (uint32_t)ctx.n_tiles,
-                                   reinterpret_cast<uint32_t*>(ctx.tile_ranges.ptr), ctx.tile_end, stream));
+  if (*h_total == NO_COUNT) HIP_CHECK(hipStreamSynchronize(stream));  // full fence, then it must be there
+  const uint32_t total = *h_total;
+  if (total == NO_COUNT) throw std::runtime_error("bin_and_sort: the intersection count did not arrive");
+  ctx.num_isect = total;
+  if (total > ctx.isect_cap) {
+    HIP_CHECK(hipStreamSynchronize(stream));  // the speculative launches still use the old buffers
+    ctx.ensure_isect_capacity(total, stream);
+    emit_and_sort(ctx, m, stream);
+  }
 }
 
 void rasterize_forward(RenderCtx& ctx, const RenderParams& p, hipStream_t stream) {

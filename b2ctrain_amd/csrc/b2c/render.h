@@ -92,12 +92,17 @@ struct RenderCtx {
   // list end before the forward shrinks it, isect_rows[slot] = that (tile, splat)'s 12-float gradient row.
   DevBuf<uint32_t> slot_sorted, tile_end;
   DevBuf<float4> isect_rows;
-  DevBuf<float4> isect_part;          // per 64-row window: partial sums of runs crossing the window's edges
-  DevBuf<uint32_t> isect_part_flags;  // per 64-row window
+  DevBuf<float4> isect_part;          // per 256-row window: partial sums of runs crossing the window's edges
+  DevBuf<uint32_t> isect_part_flags;  // per 256-row window
   DevBuf<unsigned char> sort_tmp;
   DevBuf<float> loss_partials;  // per-workgroup loss sums, reduced in a fixed order
   hipEvent_t bwd_split_event = nullptr;  // if set: recorded between the backward raster kernel and its reduce
+  hipEvent_t count_event = nullptr;      // owned: recorded after the intersection count's copy to h_count
 
+  RenderCtx() = default;
+  RenderCtx(const RenderCtx&) = delete;
+  RenderCtx& operator=(const RenderCtx&) = delete;
+  ~RenderCtx();
   void setup(int W, int H, int n_splats, hipStream_t stream);
   void ensure_isect_capacity(size_t m, hipStream_t stream);
 };
