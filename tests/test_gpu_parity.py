@@ -59,5 +59,7 @@ def test_config3_full_size():
     sc.bg = (0.5, 0.5, 0.5)
     emit("config3 full size (1M splats, 1920x1080)")
     out = full_check(sc, mode=1)
-    assert out["M"] > 1_000_000
+    # more intersections than a fresh context's capacity (2^22): the emit, tile sort and ranges queued
+    # before the host had the count ran short, and were redone after growing the buffers
+    assert out["M"] > 1 << 22
     assert np.isfinite(out["grads"]).all()
