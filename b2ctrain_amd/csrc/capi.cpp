@@ -89,6 +89,7 @@ Field ctx_field(b2c_ctx* c, const std::string& name) {
       {"proj1", {x.proj1.ptr, n * 16}},
       {"proj2", {x.proj2.ptr, n * 16}},
       {"proj3", {x.proj3.ptr, n * 8}},
+      {"raster_rec", {x.raster_rec.ptr, n * 64}},
       {"tile_count", {x.tile_count.ptr, n * 4}},
       {"tile_off", {x.tile_off.ptr, n * 4}},
       {"hit_info", {x.hit_info.ptr, n * 8}},

@@ -12,7 +12,10 @@ namespace b2c {
 namespace dev {
 namespace {
 
-constexpr int PROJ_BLOCK = 1024;  // one big-list append per workgroup (same-address atomics serialise)
+// Four waves per workgroup: with ~92 VGPRs five waves fit per SIMD, and small workgroups desynchronise, so
+// one workgroup's memory waits overlap another's arithmetic (1024-thread workgroups, one per CU, ran 25%
+// slower). One big-list append per workgroup (same-address atomics serialise).
+constexpr int PROJ_BLOCK = 256;
 
 // Tile tests of the wave's small splats (bbox of at most 32 tiles) are shared out over all 64 lanes: the
 // splats' bbox areas are prefix-summed across the wave, test t goes to lane t mod 64, which finds the
@@ -89,6 +92,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
         rec[0] = make_float4(pr.mean2d[0], pr.mean2d[1], 0.5f * pr.conic.c00, pr.conic.c01);
         rec[1] = make_float4(0.5f * pr.conic.c11, pr.opac, power, __uint_as_float(sgn));
         rec[2] = make_float4(fmaxf(cr, 0.f), fmaxf(cg, 0.f), fmaxf(cb, 0.f), log2_opacity(pr.opac));
+        rec[3] = make_float4(0.f, 0.f, 0.f, 0.f);  // unused; whole lines are written (no partial-line writes)
       }
       if (a.max_screen) {
         float ms = fmaxf(pr.ex / (float)a.cam.W, pr.ey / (float)a.cam.H);
