@@ -245,8 +245,9 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   const int px = tx * RT_W + lx, py = ty * RT_W + ly;
   const float u = lx + 0.5f - RT_W * 0.5f, v = ly + 0.5f - RT_W * 0.5f;
   PixelState ps = load_pixel(a, px, py, range.x);
-  const float W2 = (float)a.W * (float)a.W, H2 = (float)a.H * (float)a.H;
-  const float r_scale = ps.inv_final_a * R_SCALE;
+  // refine: sqrt(W^2 gx^2 + H^2 gy^2) = W sqrt(gx^2 + rho gy^2), W folded into the per-pixel scale
+  const float rho = ((float)a.H * (float)a.H) / ((float)a.W * (float)a.W);
+  const float r_scale = ps.inv_final_a * R_SCALE * (float)a.W;
   const float cv_x = ps.vo.x, cv_y = ps.vo.y, cv_z = ps.vo.z;
 
   // Basis operand A (16 rows x 64 px), built once per tile through sS as scratch.
@@ -283,9 +284,9 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       s_g0[lane] = rec[0];
       s_g1[lane] = make_float4(r1.x, r1.y, r1.z, r2.w);
       s_col[lane] = make_float4(r2.x, r2.y, r2.z, r1.w);
-    } else if (lane < ngroups * G) {  // pad the last group with null splats (power = -inf: never composited)
-      s_g0[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
-      s_g1[lane] = make_float4(0.f, 1.f, -__builtin_inff(), 0.f);
+    } else if (lane < ngroups * G) {  // pad the last group with null splats, never composited: power = 0
+      s_g0[lane] = make_float4(0.f, 0.f, 0.f, 0.f);  // and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1)
+      s_g1[lane] = make_float4(1.f, 1.f, 0.f, 0.f);
       s_col[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
@@ -317,7 +318,10 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             c01dx = g0.w * dx;
             sigma = (t1 * dx + t2 * dy) + c01dx * dy;
           }
-          const bool in = live_px & (jj < last_rel) & (sigma >= 0.f) & (sigma <= g1.z);
+          // 0 <= sigma <= power as one unsigned compare of the bit patterns: every listed splat has
+          // power >= +0 (its tile test passed, and sigma >= 0 for a positive-definite conic), and sigma is
+          // never -0 (c00 dx^2 + c11 dy^2 >= +0 and +0 + -0 = +0); a NaN sigma fails either way
+          const bool in = live_px & (jj < last_rel) & (__float_as_uint(sigma) <= __float_as_uint(g1.z));
           {  // straight-line: a lane without this fragment computes zeros (alpha = 0)
             // a lane without this fragment runs the same arithmetic with alpha = 0: ra = 1, vis = 0,
             // v_sigma = 0 and T, Q unchanged (every operand stays finite)
@@ -332,7 +336,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             const float v_sigma = araw <= ALPHA_MAX ? -alpha * v_alpha : 0.f;  // clamped: no sigma gradient
             // refine statistic: |d(loss)/d(mean2d)| scaled to pixels, over the final alpha
             const float gx = 2.f * t1 + g0.w * dy, gy = c01dx + 2.f * t2;
-            o_r = fabsf(v_sigma) * __builtin_amdgcn_sqrtf(W2 * gx * gx + H2 * gy * gy) * r_scale;
+            o_r = fabsf(v_sigma) * __builtin_amdgcn_sqrtf(gx * gx + rho * gy * gy) * r_scale;
             o_vis = vis;
             o_vs = v_sigma;
             T = Tb;
