@@ -21,10 +21,18 @@ namespace {
 // LDS holds (mx, my, c00/2, c01), (c11/2, log2 opacity, power, 0) and the colour clamped at 0, staged from
 // the projection's 64-byte per-splat record (one cache line per gather); halving c00 and c11 is exact, so
 // sigma is the reference's 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy bit for bit (uncontracted).
+// The reference's sigma 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy, uncontracted, from (mx, my, c00 / 2, c01) and
+// (c11 / 2, ...): halving c00 and c11 is exact, so the result is bit for bit the same.
+__device__ __forceinline__ float splat_sigma(float4 g0, float4 g1, float pcx, float pcy) {
+#pragma clang fp contract(off)
+  const float dx = pcx - g0.x, dy = pcy - g0.y;
+  return ((g0.z * dx) * dx + (g1.x * dy) * dy) + (g0.w * dx) * dy;
+}
+
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
-  // slot 64 is a null splat (power = -inf: no fragment passes) that pads the shorter quadrant lists
+  // slot 64 is a null splat (no fragment passes) that pads the shorter quadrant lists
   __shared__ float4 s_g0[65], s_g1[65], s_col[65];
-  __shared__ uint32_t s_list[4][65];  // per quadrant: LDS byte offsets of its splats, in depth order
+  __shared__ uint32_t s_list[4][66];  // per quadrant: LDS byte offsets of its splats, in depth order
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
@@ -40,10 +48,10 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
   bool live = inside;
   uint32_t last = range.x;
-  if (lane < 4) s_list[lane][64] = 64u * 16u;  // read (never used) by the last iteration's prefetch
-  if (lane == 0) {
+  if (lane < 8) s_list[lane >> 1][64 + (lane & 1)] = 64u * 16u;  // read by the last pair's prefetch
+  if (lane == 0) {  // power = 0 and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1): fails the cutoff
     s_g0[64] = make_float4(0.f, 0.f, 0.f, 0.f);
-    s_g1[64] = make_float4(0.f, 0.f, -__builtin_inff(), 0.f);
+    s_g1[64] = make_float4(1.f, 0.f, 0.f, 0.f);
     s_col[64] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const char* lds_g0 = reinterpret_cast<const char*>(s_g0);
@@ -79,35 +87,41 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     n_iter = __builtin_amdgcn_readfirstlane(n_iter);
     __syncthreads();
     const uint32_t* my_list = s_list[q];
+    // The lists are walked in pairs (an odd count runs one null entry more); each offset register is
+    // reloaded with the entry two ahead at the end of its step, while the other step of the pair runs.
     uint32_t last_off = NO_OFF;  // LDS offset of this batch's last contributing splat
-    uint32_t off = my_list[0];
-    for (uint32_t i = 0; i < n_iter; i++) {
-      const uint32_t off_next = my_list[i + 1];  // one entry ahead: the splat reads need not wait for it
-      const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + off);
-      const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + off);
-      const float4 col = *reinterpret_cast<const float4*>(lds_col + off);
-      float sigma;
-      {
-#pragma clang fp contract(off)
-        const float dx = pcx - g0.x, dy = pcy - g0.y;
-        sigma = ((g0.z * dx) * dx + (g1.x * dy) * dy) + (g0.w * dx) * dy;
-      }
-      // bitwise & keeps the compiler from branching on the compares
-      const bool valid = live & (sigma >= 0.f) & (sigma <= g1.z);
-      float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));  // sigma < 0: discarded by the select
-      asm volatile("" : "+v"(a_cl));  // keeps the exp out of an exec-masked branch
-      const float alpha = valid ? a_cl : 0.f;
-      const float next_T = T * (1.f - alpha);
-      const bool stop = next_T <= T_CUTOFF;  // only a valid fragment can stop a lane
-      live = live & !stop;
-      const float vis = stop ? 0.f : alpha * T;
-      r += col.x * vis;
-      g += col.y * vis;
-      b += col.z * vis;
-      T = stop ? T : next_T;
-      last_off = vis > 0.f ? off : last_off;
-      off = off_next;
+    uint32_t off0 = my_list[0], off1 = my_list[1];
+    // One step: 0 <= sigma <= power as one unsigned compare of the bit patterns (every listed splat has
+    // power >= +0, since its tile test passed and sigma >= 0 for a positive-definite conic, and sigma is
+    // never -0: c00 dx^2 + c11 dy^2 >= +0 and +0 + -0 = +0; a NaN sigma fails either way), bitwise & so the
+    // compiler does not branch on the compares; the exp is kept out of an exec-masked branch (a lane with
+    // sigma < 0 has its alpha discarded by the select); only a valid fragment can stop a lane.
+#define B2C_COMPOSITE(off, next)                                                                       \
+  do {                                                                                                 \
+    const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + (off));                                \
+    const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + (off));                                \
+    const float4 col = *reinterpret_cast<const float4*>(lds_col + (off));                              \
+    const float sigma = splat_sigma(g0, g1, pcx, pcy);                                                 \
+    const bool valid = live & (__float_as_uint(sigma) <= __float_as_uint(g1.z));                       \
+    float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));                                        \
+    asm volatile("" : "+v"(a_cl));                                                                     \
+    const float alpha = valid ? a_cl : 0.f;                                                            \
+    const float next_T = T * (1.f - alpha);                                                            \
+    const bool stop = next_T <= T_CUTOFF;                                                              \
+    live = live & !stop;                                                                               \
+    const float vis = stop ? 0.f : alpha * T;                                                          \
+    r += col.x * vis;                                                                                  \
+    g += col.y * vis;                                                                                  \
+    b += col.z * vis;                                                                                  \
+    T = stop ? T : next_T;                                                                             \
+    last_off = vis > 0.f ? (off) : last_off;                                                           \
+    (off) = my_list[next];                                                                             \
+  } while (0)
+    for (uint32_t i = 0; i < n_iter; i += 2) {
+      B2C_COMPOSITE(off0, i + 2);
+      B2C_COMPOSITE(off1, i + 3);
     }
+#undef B2C_COMPOSITE
     if (last_off != NO_OFF) last = start + (last_off >> 4) + 1u;
   }
   if (inside) {
