@@ -29,9 +29,11 @@ struct LossParams {
   float scale = 1.f;                  // multiplier on the whole photometric loss
   float normal_scale = 0.f;
   float grad_scale = 1.f;             // multiplies the per-pixel gradients (not the loss value)
+  bool assign_loss = false;           // store into loss_accum[0] (and clear [1]) instead of adding
 };
 
-// Fused L1 + SSIM (+ alpha lane): gradient into ctx.v_out, loss added to ctx.loss_accum[0].
+// Fused L1 + SSIM (+ alpha lane): gradient into ctx.v_out, loss added to ctx.loss_accum[0] (stored, with
+// loss_accum[1] cleared, when lp.assign_loss).
 void photometric_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp, hipStream_t stream);
 void normal_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp, hipStream_t stream);
 // loss_accum[2] += loss_accum[0] + loss_accum[1]; loss_accum[3] += 1.

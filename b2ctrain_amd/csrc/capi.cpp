@@ -348,7 +348,8 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
                    int mode, int accumulate, b2c_step_times* times) {
   return guarded([&] {
     const b2c::RenderParams p = to_params(*ro);
-    const b2c::LossParams lp = to_loss(*lo);
+    b2c::LossParams lp = to_loss(*lo);
+    lp.assign_loss = true;  // the step's loss replaces loss_accum[0..1] (no separate clear)
     hipStream_t s = c->stream;
     auto mark = [&](int k) {
       if (times) HIP_CHECK(hipEventRecord(c->ev[k], s));
@@ -361,7 +362,6 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
       c->degree = m->m.degree;
     }
     mark(0);
-    c->ctx.loss_accum.zero(s, 2);
     b2c::project_splats(c->ctx, m->m, p, s);
     mark(1);
     b2c::bin_and_sort(c->ctx, m->m, s);

@@ -417,9 +417,20 @@ __global__ void __launch_bounds__(256) emit_big_kernel(b2c_emit_args a, const ui
   }
 }
 
-// Per-tile [first, last) of the sorted keys (binning.cu:95-105); tile_end keeps a copy of `last` that the
-// forward does not shrink, and tile_end[n_tiles] = where the sentinel keys start (m if there are none). With slot_sorted set (an index sort: the sorted emit positions), also gathers
-// the splat ids into list order: vals_sorted[i] = vals[slot_sorted[i]].
+// Per-tile [first, last) of the sorted keys (binning.cu:95-105), every tile written: the thread at each key
+// boundary writes the bounds of the runs on either side and clears the tiles with no key between them (the
+// first and last threads those before the first key and after the last), so the ranges need no clearing
+// beforehand; with no keys at all the grid clears every tile. tile_end keeps a copy of `last` that the
+// forward does not shrink, and tile_end[n_tiles] = where the sentinel keys start (m if there are none).
+// With slot_sorted set (an index sort: the sorted emit positions), also gathers the splat ids into list
+// order: vals_sorted[i] = vals[slot_sorted[i]].
+__device__ __forceinline__ void clear_tiles(uint2* ranges, uint32_t* tile_end, uint32_t lo, uint32_t hi) {
+  for (uint32_t t = lo; t < hi; t++) {
+    ranges[t] = make_uint2(0u, 0u);
+    if (tile_end) tile_end[t] = 0u;
+  }
+}
+
 __global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const uint32_t* __restrict__ m_dev,
                                                           const uint32_t* __restrict__ keys,
                                                           const uint32_t* __restrict__ slot_sorted,
@@ -428,11 +439,21 @@ __global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const ui
                                                           uint2* __restrict__ ranges, uint32_t* __restrict__ tile_end) {
   const uint32_t m = live_count(cap, m_dev);
   const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  if (m == 0) {
+    for (uint32_t t = i; t < n_tiles; t += gridDim.x * 256u) {
+      ranges[t] = make_uint2(0u, 0u);
+      if (tile_end) tile_end[t] = 0u;
+    }
+    if (i == 0 && tile_end) tile_end[n_tiles] = 0u;
+    return;
+  }
   if (i >= m) return;
   if (slot_sorted) vals_sorted[i] = vals[slot_sorted[i]];
   const uint32_t tile = keys[i];
   const uint32_t prev = i == 0 ? 0xFFFFFFFFu : keys[i - 1];
   if (i == 0 || tile != prev) {
+    // tiles after the previous run (or from 0) up to this run (or the end), which no key names
+    clear_tiles(ranges, tile_end, i == 0 ? 0u : min(prev + 1u, n_tiles), min(tile, n_tiles));
     if (tile < n_tiles) ranges[tile].x = i;
     if (i > 0 && prev < n_tiles) {
       ranges[prev].y = i;
@@ -443,6 +464,7 @@ __global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const ui
   }
   if (i == m - 1 && tile < n_tiles) {
     ranges[tile].y = m;
+    clear_tiles(ranges, tile_end, tile + 1u, n_tiles);
     if (tile_end) {
       tile_end[tile] = m;
       tile_end[n_tiles] = m;  // no sentinel keys
@@ -561,12 +583,12 @@ extern "C" int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream) {
 extern "C" int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_sorted,
                                    const uint32_t* slot_sorted, const uint32_t* vals, uint32_t* vals_sorted,
                                    uint32_t n_tiles, uint32_t* ranges, uint32_t* tile_end, hipStream_t stream) {
-  int e = b2c_hip_fill_u32(ranges, 0u, (size_t)n_tiles * 2, stream);
-  if (!e && tile_end) e = b2c_hip_fill_u32(tile_end, 0u, (size_t)n_tiles + 1, stream);
-  if (e || m == 0) return e;
+  if (n_tiles == 0) return 0;
   if (slot_sorted && (!vals || !vals_sorted)) return (int)hipErrorInvalidValue;
-  tile_ranges_kernel<<<dim3((m + 255) / 256), dim3(256), 0, stream>>>(m, m_dev, keys_sorted, slot_sorted, vals,
-                                                                      vals_sorted, n_tiles,
-                                                                      reinterpret_cast<uint2*>(ranges), tile_end);
+  // at least enough threads to clear every tile when there are no keys
+  const uint32_t threads = max(m, min(n_tiles, 65536u));
+  tile_ranges_kernel<<<dim3((threads + 255) / 256), dim3(256), 0, stream>>>(m, m_dev, keys_sorted, slot_sorted, vals,
+                                                                            vals_sorted, n_tiles,
+                                                                            reinterpret_cast<uint2*>(ranges), tile_end);
   return (int)hipGetLastError();
 }

@@ -271,7 +271,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
 
 // Fixed-order double-precision sum of the per-workgroup partials into loss_accum[0].
 __global__ void __launch_bounds__(1024) reduce_partials_kernel(const float* __restrict__ partials, int count,
-                                                                float* __restrict__ loss_accum) {
+                                                                float* __restrict__ loss_accum, int assign) {
   __shared__ double s_red[16];
   double acc = 0.0;
   for (int i = threadIdx.x; i < count; i += 1024) acc += (double)partials[i];
@@ -282,7 +282,12 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const float* __re
   if (threadIdx.x == 0) {
     double t = 0.0;
     for (int k = 0; k < 16; k++) t += s_red[k];
-    loss_accum[0] = (float)((double)loss_accum[0] + t);
+    if (assign) {
+      loss_accum[0] = (float)t;
+      loss_accum[1] = 0.f;
+    } else {
+      loss_accum[0] = (float)((double)loss_accum[0] + t);
+    }
   }
 }
 
@@ -342,6 +347,7 @@ int pick_strip_rows(int W, int H) {
 
 extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   if (a->W <= 0 || a->H <= 0) return 0;
+  if (a->assign && !a->partials) return (int)hipErrorInvalidValue;  // float atomics can only add
   Gauss11 g;
   double w[11], sum = 0.0;
   for (int i = 0; i < 11; i++) {
@@ -360,7 +366,7 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
     case 57: photometric_kernel<57><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
     default: photometric_kernel<79><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
   }
-  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum);
+  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum, a->assign);
   return (int)hipGetLastError();
 }
 

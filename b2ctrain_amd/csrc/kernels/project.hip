@@ -272,6 +272,11 @@ __global__ void __launch_bounds__(256) big_sum_kernel(b2c_project_args a) {
   a.tile_count[a.big_list[e]] = run;
 }
 
+__global__ void clear_counters_kernel(uint32_t* a, uint32_t* b) {
+  *a = 0u;
+  if (b) *b = 0u;
+}
+
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -295,9 +300,8 @@ extern "C" int b2c_hip_fill_u32(uint32_t* p, uint32_t value, size_t count, hipSt
 extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
-  int e = b2c_hip_fill_u32(a->big_count, 0u, 1, stream);
-  if (!e && a->big_items_count) e = b2c_hip_fill_u32(a->big_items_count, 0u, 1, stream);
-  if (e) return e;
+  if (!a->big_count || !a->big_list) return (int)hipErrorInvalidValue;
+  clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);  // one launch for both
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);
   switch (a->degree) {
     case 0: project_kernel<0><<<grid, block, 0, stream>>>(*a); break;
@@ -306,7 +310,7 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
     case 3: project_kernel<3><<<grid, block, 0, stream>>>(*a); break;
     default: project_kernel<4><<<grid, block, 0, stream>>>(*a); break;
   }
-  e = (int)hipGetLastError();
+  const int e = (int)hipGetLastError();
   if (e) return e;
   if (!a->big_info || !a->big_chunk || !a->big_items || !a->big_items_count) return (int)hipErrorInvalidValue;
   const dim3 per_entry((unsigned)((a->n + 255) / 256));

@@ -123,7 +123,7 @@ typedef struct b2c_emit_args {
 } b2c_emit_args;
 int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream);
 
-/* tile_ranges_kernel (binning.cu:95-105) after zeroing ranges: ranges[t] = [first, last) of tile t, and
+/* tile_ranges_kernel (binning.cu:95-105), every tile written (empty tiles [0, 0)): ranges[t] = [first, last) of tile t, and
  * tile_end[t] = last (may be NULL; a copy the forward does not shrink; n_tiles + 1 entries, the last = the
  * position where the sentinel keys of an emit shortfall start, m if there are none). When slot_sorted is set (the
  * permutation from an index sort of the emitted keys), also writes vals_sorted[i] = vals[slot_sorted[i]]:
@@ -203,6 +203,8 @@ typedef struct b2c_loss_args {
   float* loss_accum;          /* [0] += loss */
   float* partials;            /* scratch, b2c_loss_partials(W, H) floats: per-workgroup sums, reduced in a
                                  fixed order in double (deterministic); NULL = float atomics as the reference */
+  int assign;                 /* with partials: loss_accum[0] = loss and loss_accum[1] = 0 (the second loss
+                                 term, absent from this build) instead of adding, so the caller need not clear */
 } b2c_loss_args;
 size_t b2c_loss_partials(int W, int H);
 int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream);

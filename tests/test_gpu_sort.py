@@ -136,3 +136,61 @@ def test_count_scan_matches_cumsum(n):
     exp = np.cumsum(counts[order].astype(np.uint64)).astype(np.uint32)
     assert np.array_equal(off.cpu().numpy().view(np.uint32), exp)
     assert int(tot.cpu().numpy().view(np.uint32)[0]) == int(exp[-1])
+
+
+def _ranges_expect(keys, n_tiles):
+    """[first, last) of each tile in sorted keys, empty tiles [0, 0); tile_end = last, and tile_end[n_tiles] =
+    the first sentinel key (>= n_tiles) or the key count (src/gpu/binning.cu:95-105 plus this build's copy)."""
+    m = keys.size
+    ranges = np.zeros((n_tiles, 2), np.uint32)
+    tile_end = np.zeros(n_tiles + 1, np.uint32)
+    for t in np.unique(keys[keys < n_tiles]):
+        lo, hi = np.searchsorted(keys, t, "left"), np.searchsorted(keys, t, "right")
+        ranges[t] = (lo, hi)
+        tile_end[t] = hi
+    tile_end[n_tiles] = np.searchsorted(keys, n_tiles, "left") if m else 0
+    return ranges, tile_end
+
+
+@pytest.mark.parametrize("case", ["dense", "gaps", "sentinels", "one", "empty", "all_sentinel", "live"])
+def test_tile_ranges_write_every_tile(case):
+    """b2c_hip_tile_ranges on outputs poisoned beforehand: every tile is written (the kernel clears the tiles
+    no key names itself), including no keys at all, sentinel keys (>= n_tiles) and a device-side live count."""
+    L = _native.lib()
+    n_tiles = 5000
+    rng = np.random.default_rng(len(case))
+    live = None
+    if case == "dense":
+        keys = np.sort(rng.integers(0, n_tiles, 200_000)).astype(np.uint32)
+    elif case == "gaps":
+        keys = np.sort(rng.choice([3, 4, 900, 901, 2500, 4998], 3000)).astype(np.uint32)
+    elif case == "sentinels":
+        keys = np.sort(np.concatenate([rng.integers(10, 4000, 5000), np.full(77, n_tiles)])).astype(np.uint32)
+    elif case == "one":
+        keys = np.array([1234], np.uint32)
+    elif case == "empty":
+        keys = np.zeros(0, np.uint32)
+    elif case == "all_sentinel":
+        keys = np.full(10, n_tiles, np.uint32)
+    else:  # launched for a capacity of 50,000 keys, 31,000 live (the binning's queued-before-the-count form)
+        keys = np.sort(rng.integers(0, n_tiles, 50_000)).astype(np.uint32)
+        live = 31_000
+        keys[live:] = 0xFFFFFFFF  # past the live count: must not be read as keys
+        keys[:live] = np.sort(keys[:live])
+    m = keys.size
+    kd = _dev(keys if m else np.zeros(1, np.uint32))
+    ranges = _dev(np.full(n_tiles * 2, 0xDEADBEEF, np.uint32).view(np.int32))
+    tile_end = _dev(np.full(n_tiles + 1, 0xDEADBEEF, np.uint32).view(np.int32))
+    m_dev = None if live is None else _dev(np.array([live], np.uint32))
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    print(f"tile ranges case={case} m={m} live={live}", flush=True)
+    rc = L.b2c_hip_tile_ranges(C.c_uint32(m), _p(m_dev), _p(kd), None, None, None, C.c_uint32(n_tiles), _p(ranges),
+                               _p(tile_end), stream)
+    _native.check(rc, "tile ranges")
+    torch.cuda.synchronize()
+    exp_r, exp_e = _ranges_expect(keys[: (m if live is None else live)], n_tiles)
+    got_r = ranges.cpu().numpy().view(np.uint32).reshape(n_tiles, 2)
+    got_e = tile_end.cpu().numpy().view(np.uint32)
+    bad = np.flatnonzero((got_r != exp_r).any(1))
+    assert bad.size == 0, f"ranges differ at tiles {bad[:10]}: {got_r[bad[:3]]} vs {exp_r[bad[:3]]}"
+    assert np.array_equal(got_e, exp_e), f"tile_end differs at {np.flatnonzero(got_e != exp_e)[:10]}"
