@@ -160,12 +160,20 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int BATCH = 64;  // splats staged in LDS per step
 constexpr int G = 8;       // splats per MFMA group
 constexpr int SROW = 68;   // pixel stride of the per-fragment scalar rows (64 + 4: spreads the B reads over banks)
-// (tile, splat) row: raw moments of the tile's fragments about the tile centre, 12 floats: sum v_sigma *
-// [1, u, v, u^2, uv, v^2], refine sum, sum vis, sum vis * v_rgb, unused
+// (tile, splat) row: raw moments of the tile's fragments about the tile centre, 12 floats in three 16-byte
+// quarters, each written by one lane with one store: sum v_sigma * [v, u^2, uv, v^2] | sum v_sigma * [1, u],
+// sum vis, refine sum | sum vis * v_rgb, 0
 constexpr int ROW = 12;
-constexpr int R_SV = 0, R_REF = 6, R_VIS = 7, R_VRGB = 8;
 // basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero), 6 one, 7 u, 8 v, 9 u^2, 10 uv, 11 v^2, 12-15 zero
 constexpr int B_ONE = 6, B_U = 7, B_V = 8, B_UU = 9, B_UV = 10, B_VV = 11;
+
+// DPP controls (GCN/CDNA): row_shr:n = 0x110 + n, row_ror:n = 0x120 + n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143, wave_shl:1 = 0x130, wave_shr:1 = 0x138. Lanes whose source is outside the row mask or
+// the wave get `fill`.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x, uint32_t fill) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
 
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -363,35 +371,24 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
         load8(&sS[2 * G + (nl & (G - 1))][kb * 32 + kg * 8], x);  // columns 8-15 of d1 are unused
         d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], to_half8(x), d1, 0, 0, 0);
       }
-      // D layout: lane (nl, kg) holds rows 4 kg .. 4 kg + 3 of column nl. The lanes holding wanted rows
-      // store them as the (tile, splat) row's raw moments (the reduce turns them into gradients).
+      // D layout: lane (nl, kg) holds rows 4 kg .. 4 kg + 3 of column nl. Three lanes per splat j store the
+      // (tile, splat) row's raw moments (the reduce turns them into gradients), one 16-byte quarter each:
+      // (j + 8, kg 2) the v_sigma column's rows 8-11; (j, kg 1) the v_sigma column's rows 6-7, taken from
+      // lane j + 8 of its row of 16 lanes, then the vis column's row 6 and the refine product's row 6;
+      // (j, kg 0) the vis column's rows 0-2.
       {
         const int j = nl & (G - 1);
-        if (j < gcount) {
-          float* row = a.isect_rows + (size_t)s_slot[gbase + j] * ROW;
-          float dv[4];
+        float dv[4];
 #pragma unroll
-          for (int rr = 0; rr < 4; rr++) dv[rr] = d0_hi[rr] + d0_lo[rr] * (1.f / LO_SCALE);
-          if (nl < G) {  // vis column: rows 0-2 (v_rgb) and 6 (one); the refine product's row 6
-            if (kg == 0) {
-              row[R_VRGB] = dv[0];
-              row[R_VRGB + 1] = dv[1];
-              row[R_VRGB + 2] = dv[2];
-            } else if (kg == 1) {
-              row[R_VIS] = dv[2];
-              row[R_REF] = d1[2];
-            }
-          } else {  // v_sigma column: rows 6-11 (one, u, v, u^2, uv, v^2)
-            if (kg == 1) {
-              row[R_SV] = dv[2];
-              row[R_SV + 1] = dv[3];
-            } else if (kg == 2) {
-              row[R_SV + 2] = dv[0];
-              row[R_SV + 3] = dv[1];
-              row[R_SV + 4] = dv[2];
-              row[R_SV + 5] = dv[3];
-            }
-          }
+        for (int rr = 0; rr < 4; rr++) dv[rr] = d0_hi[rr] + d0_lo[rr] * (1.f / LO_SCALE);
+        // row_ror:8 within each row of 16 lanes: lane nl gets lane nl ^ 8 (every lane takes part)
+        const float sv = __uint_as_float(dpp_u32<0x128, 0xF>(__float_as_uint(dv[2]), 0u));
+        const float svu = __uint_as_float(dpp_u32<0x128, 0xF>(__float_as_uint(dv[3]), 0u));
+        if (j < gcount) {
+          float4* row = reinterpret_cast<float4*>(a.isect_rows) + (size_t)s_slot[gbase + j] * (ROW / 4);
+          if (nl >= G && kg == 2) row[0] = make_float4(dv[0], dv[1], dv[2], dv[3]);
+          if (nl < G && kg == 1) row[1] = make_float4(sv, svu, dv[2], d1[2]);
+          if (nl < G && kg == 0) row[2] = make_float4(dv[0], dv[1], dv[2], 0.f);
         }
       }
     }
@@ -419,13 +416,6 @@ constexpr uint32_t NO_RUN = 0xFFFFFFFFu;
 constexpr uint32_t W_CONT_BEFORE = 1u, W_CONT_AFTER = 2u, W_HAS_HEAD = 4u;
 constexpr int RED_SUB = 4;                  // 64-row sub-windows per reduce wave
 constexpr uint32_t RED_WIN = 64u * RED_SUB;  // rows per window (one wave)
-
-// DPP controls (GCN/CDNA): row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143,
-// wave_shl:1 = 0x130, wave_shr:1 = 0x138.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t x, uint32_t fill) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)x, CTRL, ROW_MASK, 0xF, false);
-}
 
 // One Hillis-Steele step of the segmented scan: add the partial of the DPP source lane when it lies in
 // the same run (runs are contiguous, so equal ids at both ends mean no run boundary in between).
@@ -492,7 +482,7 @@ __device__ __forceinline__ void row_gradients(const b2c_raster_bwd_args& a, uint
   const uint32_t t = a.isect_keys[s];
   const uint32_t ty = t / (uint32_t)a.tiles_x, tx = t - ty * (uint32_t)a.tiles_x;
   const float mx = r0.x - ((float)(tx * RT_W) + RT_W * 0.5f), my = r0.y - ((float)(ty * RT_W) + RT_W * 0.5f);
-  const float sv = q0.x, svu = q0.y, svv = q0.z, svuu = q0.w, svuv = q1.x, svvv = q1.y;
+  const float sv = q1.x, svu = q1.y, svv = q0.x, svuu = q0.y, svuv = q0.z, svvv = q0.w;
   const float sc = a.inv_gscale;
   const float m1u = svu - mx * sv, m1v = svv - my * sv;  // sum v_sigma (u - mx), (v - my)
   const float m2uu = svuu - 2.f * mx * svu + mx * mx * sv;
@@ -508,8 +498,8 @@ __device__ __forceinline__ void row_gradients(const b2c_raster_bwd_args& a, uint
   v[6] = (sgn & 2u) ? q2.y * sc : 0.f;
   v[7] = (sgn & 4u) ? q2.z * sc : 0.f;
   v[8] = -sv / r1.y * sc;
-  v[9] = q1.z * (1.f / R_SCALE) * sc;  // the raster pre-scales refine terms into the fp16 range
-  v[10] = q1.w;
+  v[9] = q1.w * (1.f / R_SCALE) * sc;  // the raster pre-scales refine terms into the fp16 range
+  v[10] = q1.z;
 }
 
 __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a) {

@@ -156,7 +156,7 @@ int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream);
  *
  * Mode 0 accumulates into v_splat / vis_weight with float atomics, as the reference does. Mode 1 uses no
  * atomics: each (tile, splat) pair writes a 12-float row of raw moments about the tile centre (sum v_sigma
- * * [1, u, v, u^2, uv, v^2], refine sum, sum of blend weights, sum vis * v_rgb, unused) to
+ * * [v, u^2, uv, v^2] | sum v_sigma * [1, u], sum of blend weights, refine sum | sum vis * v_rgb, 0) to
  * isect_rows[slot_sorted[i]] (rows of pairs past the shrunk range end are written as zeros); the rows of
  * one splat are then a contiguous run in emit order, which a segmented reduction turns into gradient
  * lanes (tile centre from isect_keys), sums in a fixed order and adds to v_splat, vis_weight and
