@@ -249,7 +249,6 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.num_isect = ctx.num_isect;
   a.slot_sorted = ctx.slot_sorted;
   a.isect_vals = ctx.vals;
-  a.isect_keys = ctx.keys;
   a.tile_count = ctx.tile_count;
   a.tile_end = ctx.tile_end;
   a.isect_rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);

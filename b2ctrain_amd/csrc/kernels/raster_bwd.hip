@@ -162,7 +162,7 @@ constexpr int G = 8;       // splats per MFMA group
 constexpr int SROW = 68;   // pixel stride of the per-fragment scalar rows (64 + 4: spreads the B reads over banks)
 // (tile, splat) row: raw moments of the tile's fragments about the tile centre, 12 floats in three 16-byte
 // quarters, each written by one lane with one store: sum v_sigma * [v, u^2, uv, v^2] | sum v_sigma * [1, u],
-// sum vis, refine sum | sum vis * v_rgb, 0
+// sum vis, refine sum | sum vis * v_rgb, the tile id (bits)
 constexpr int ROW = 12;
 // basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero), 6 one, 7 u, 8 v, 9 u^2, 10 uv, 11 v^2, 12-15 zero
 constexpr int B_ONE = 6, B_U = 7, B_V = 8, B_UU = 9, B_UV = 10, B_VV = 11;
@@ -375,7 +375,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       // (tile, splat) row's raw moments (the reduce turns them into gradients), one 16-byte quarter each:
       // (j + 8, kg 2) the v_sigma column's rows 8-11; (j, kg 1) the v_sigma column's rows 6-7, taken from
       // lane j + 8 of its row of 16 lanes, then the vis column's row 6 and the refine product's row 6;
-      // (j, kg 0) the vis column's rows 0-2.
+      // (j, kg 0) the vis column's rows 0-2 and the tile id.
       {
         const int j = nl & (G - 1);
         float dv[4];
@@ -388,7 +388,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
           float4* row = reinterpret_cast<float4*>(a.isect_rows) + (size_t)s_slot[gbase + j] * (ROW / 4);
           if (nl >= G && kg == 2) row[0] = make_float4(dv[0], dv[1], dv[2], dv[3]);
           if (nl < G && kg == 1) row[1] = make_float4(sv, svu, dv[2], d1[2]);
-          if (nl < G && kg == 0) row[2] = make_float4(dv[0], dv[1], dv[2], 0.f);
+          if (nl < G && kg == 0) row[2] = make_float4(dv[0], dv[1], dv[2], __uint_as_float((uint32_t)tile));
         }
       }
     }
@@ -472,14 +472,14 @@ __device__ __forceinline__ void add_part(const float4* p, float (&v)[RED_VALS]) 
 // tile centre (raster_bwd_tc.cu:172-198 accumulates the same quantities per fragment): with (mx, my) the
 // splat centre relative to the tile centre, the first and second moments of v_sigma about the splat centre
 // give the mean and conic gradients, the vis moments the colour gradients, and where a fragment is
-// unclamped v_alpha * gauss = -v_sigma / opacity gives g8. The tile comes from the row's emit-order key.
+// unclamped v_alpha * gauss = -v_sigma / opacity gives g8. The tile id rides in the row's last float.
 __device__ __forceinline__ void row_gradients(const b2c_raster_bwd_args& a, uint32_t s, uint32_t id,
                                               float (&v)[RED_VALS]) {
   const float4* rw = reinterpret_cast<const float4*>(a.isect_rows) + (size_t)s * (ROW / 4);
   const float4 q0 = rw[0], q1 = rw[1], q2 = rw[2];
   const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)id * 4;
   const float4 r0 = rec[0], r1 = rec[1];  // (mx, my, c00 / 2, c01), (c11 / 2, opacity, power, sign bits)
-  const uint32_t t = a.isect_keys[s];
+  const uint32_t t = __float_as_uint(q2.w);  // the tile (a zero row: tile 0, and every moment is zero)
   const uint32_t ty = t / (uint32_t)a.tiles_x, tx = t - ty * (uint32_t)a.tiles_x;
   const float mx = r0.x - ((float)(tx * RT_W) + RT_W * 0.5f), my = r0.y - ((float)(ty * RT_W) + RT_W * 0.5f);
   const float sv = q1.x, svu = q1.y, svv = q0.x, svuu = q0.y, svuv = q0.z, svvv = q0.w;
@@ -666,7 +666,7 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
   if (a->mode == 0) {
     raster_bwd_fp32_kernel<<<grid, block, 0, stream>>>(*a);
   } else {
-    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->isect_keys || !a->tile_count ||
+    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->tile_count ||
         !a->raster_rec)
       return (int)hipErrorInvalidValue;
     raster_bwd_mfma_kernel<<<grid, block, 0, stream>>>(*a);

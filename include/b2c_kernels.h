@@ -156,10 +156,10 @@ int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream);
  *
  * Mode 0 accumulates into v_splat / vis_weight with float atomics, as the reference does. Mode 1 uses no
  * atomics: each (tile, splat) pair writes a 12-float row of raw moments about the tile centre (sum v_sigma
- * * [v, u^2, uv, v^2] | sum v_sigma * [1, u], sum of blend weights, refine sum | sum vis * v_rgb, 0) to
+ * * [v, u^2, uv, v^2] | sum v_sigma * [1, u], sum of blend weights, refine sum | sum vis * v_rgb, tile id) to
  * isect_rows[slot_sorted[i]] (rows of pairs past the shrunk range end are written as zeros); the rows of
  * one splat are then a contiguous run in emit order, which a segmented reduction turns into gradient
- * lanes (tile centre from isect_keys), sums in a fixed order and adds to v_splat, vis_weight and
+ * lanes (tile centre from the tile id stored in the row), sums in a fixed order and adds to v_splat, vis_weight and
  * vis_flag. The result is deterministic. */
 typedef struct b2c_raster_bwd_args {
   const uint32_t* tile_ranges;
@@ -180,7 +180,6 @@ typedef struct b2c_raster_bwd_args {
   uint32_t num_isect;         /* M */
   const uint32_t* slot_sorted;/* [M] emit position of list entry i */
   const uint32_t* isect_vals; /* [M] splat id of emit position s (the emit kernel's values) */
-  const uint32_t* isect_keys; /* [M] tile id of emit position s (the emit kernel's keys, before the sort) */
   const uint32_t* tile_count; /* [n] intersections per splat (the length of its run of emit positions) */
   const uint32_t* tile_end;   /* [n_tiles + 1] list end before the forward's shrink; [n_tiles] = sentinel start */
   float* isect_rows;          /* [M][12] scratch */
