@@ -11,7 +11,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libb2c_hip.so")
+# B2C_HIP_LIB selects another build of the library (for example to compare two builds in one process tree)
+LIB_PATH = os.environ.get("B2C_HIP_LIB") or os.path.join(HERE, "lib", "libb2c_hip.so")
 
 GRAD_LANES = 13
 RT_W = 8
