@@ -8,7 +8,8 @@
 //   loop; keys and values are staged in LDS sorted by digit and written out in runs. Every thread loads
 //   its KPT keys before it computes anything, so the loads of a tile are all in flight at once. KPT is 16
 //   for large sorts and 4 for small ones (enough workgroups to cover the chip).
-// * Count scan: reduce-then-scan of tile_count gathered in depth order, four contiguous entries a thread.
+// * Count scan: reduce-then-scan of tile_count gathered in depth order, four contiguous entries a thread;
+//   each workgroup of the second pass sums its predecessors' totals itself (no middle kernel).
 // * Emit: small splats one thread each over the set bits of their hit mask; splats whose bbox exceeds 32
 //   tiles one wave per chunk of the bbox, in row-major order.
 #pragma clang fp contract(off)
@@ -258,50 +259,32 @@ __global__ void __launch_bounds__(SORT_THREADS) scan_reduce(int n, const uint32_
   if (threadIdx.x == 0) block_sums[blockIdx.x] = tot;
 }
 
-// Exclusive scan of the per-workgroup sums (each thread a contiguous run), total into total_dev.
-__global__ void __launch_bounds__(1024) scan_top(uint32_t nblocks, uint32_t* __restrict__ block_sums,
-                                                 uint32_t* __restrict__ total_dev) {
-  __shared__ uint32_t s_wsum[16];
-  const int w = threadIdx.x >> 6, l = lane_id();
-  const uint32_t per = (nblocks + 1023) / 1024;
-  const uint32_t lo = min(nblocks, threadIdx.x * per), hi = min(nblocks, lo + per);
-  uint32_t sum = 0;
-  for (uint32_t j = lo; j < hi; j++) sum += block_sums[j];
-  const uint32_t inc = wave_incl_scan(sum);
-  if (l == 63) s_wsum[w] = inc;
-  __syncthreads();
-  uint32_t run = inc - sum, tot = 0;
-  for (int k = 0; k < 16; k++) {
-    const uint32_t s = s_wsum[k];
-    if (k < w) run += s;
-    tot += s;
-  }
-  for (uint32_t j = lo; j < hi; j++) {
-    const uint32_t v = block_sums[j];
-    block_sums[j] = run;
-    run += v;
-  }
-  if (threadIdx.x == 0) *total_dev = tot;
-}
-
+// Each workgroup sums the totals of the workgroups before it (at most a few thousand, read from L2) as its
+// offset, then scans its own entries; the last workgroup writes the grand total to total_dev.
 __global__ void __launch_bounds__(SORT_THREADS) scan_down(int n, const uint32_t* __restrict__ order,
                                                           const uint32_t* __restrict__ tile_count,
                                                           const uint32_t* __restrict__ block_sums,
-                                                          uint32_t* __restrict__ tile_off) {
+                                                          uint32_t* __restrict__ tile_off,
+                                                          uint32_t* __restrict__ total_dev) {
   __shared__ uint32_t s_wsum[NWAVES];
   const uint32_t first = blockIdx.x * (uint32_t)SCAN_TILE + threadIdx.x * SCAN_PER;
   uint32_t c[SCAN_PER];
   gather_counts(n, order, tile_count, first, c);
+  uint32_t before = 0;
+  for (uint32_t j = threadIdx.x; j < blockIdx.x; j += SORT_THREADS) before += block_sums[j];
+  uint32_t offset;
+  block_excl_scan(before, s_wsum, offset);
   uint32_t acc = 0;
 #pragma unroll
   for (int k = 0; k < SCAN_PER; k++) acc += c[k];
   uint32_t tot;
-  uint32_t run = block_sums[blockIdx.x] + block_excl_scan(acc, s_wsum, tot);
+  uint32_t run = offset + block_excl_scan(acc, s_wsum, tot);
 #pragma unroll
   for (int k = 0; k < SCAN_PER; k++) {
     run += c[k];
     if (first + k < (uint32_t)n) tile_off[first + k] = run;
   }
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *total_dev = offset + tot;
 }
 
 // Position of the k-th set bit (k counted from 0) of m, by halving: five popcounts.
@@ -567,8 +550,7 @@ extern "C" int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t*
   const uint32_t nb = scan_blocks((uint32_t)n);
   uint32_t* block_sums = static_cast<uint32_t*>(temp);
   scan_reduce<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums);
-  scan_top<<<dim3(1), dim3(1024), 0, stream>>>(nb, block_sums, total_dev);
-  scan_down<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums, tile_off);
+  scan_down<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums, tile_off, total_dev);
   return (int)hipGetLastError();
 }
 

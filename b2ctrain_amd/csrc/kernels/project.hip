@@ -189,41 +189,46 @@ __device__ __forceinline__ uint4 big_bbox_info(const b2c_project_args& a, uint32
 
 __device__ __forceinline__ uint32_t big_nchunks(uint4 info) { return (info.z + info.w - 1u) / info.w; }
 
+// Grid-stride over the big list (its length is known on the device only): BIG_ENTRY_GRID workgroups.
+constexpr uint32_t BIG_ENTRY_GRID = 256;
+
 __global__ void __launch_bounds__(256) big_setup_kernel(b2c_project_args a) {
-  const uint32_t e = blockIdx.x * 256u + threadIdx.x;
   const uint32_t count = *a.big_count;
-  if (blockIdx.x * 256u >= count) return;  // whole workgroup past the list
-  const bool live = e < count;
-  uint32_t nch = 0;
-  if (live) {
-    const uint4 info = big_bbox_info(a, a.big_list[e]);
-    reinterpret_cast<uint4*>(a.big_info)[e] = info;
-    nch = big_nchunks(info);
-  }
-  // workgroup-aggregated allocation of the items (one device-scope atomic per workgroup)
   __shared__ uint32_t s_wsum[4];
   __shared__ uint32_t s_base;
-  uint32_t incl = nch;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t t = __shfl_up(incl, o);
-    if (lane_id() >= o) incl += t;
-  }
-  const int w = threadIdx.x >> 6;
-  if (lane_id() == 63) s_wsum[w] = incl;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t tot = 0;
-    for (int k = 0; k < 4; k++) {
-      const uint32_t c = s_wsum[k];
-      s_wsum[k] = tot;
-      tot += c;
+  for (uint32_t e0 = blockIdx.x * 256u; e0 < count; e0 += BIG_ENTRY_GRID * 256u) {  // uniform per workgroup
+    const uint32_t e = e0 + threadIdx.x;
+    const bool live = e < count;
+    uint32_t nch = 0;
+    if (live) {
+      const uint4 info = big_bbox_info(a, a.big_list[e]);
+      reinterpret_cast<uint4*>(a.big_info)[e] = info;
+      nch = big_nchunks(info);
     }
-    s_base = tot ? atomicAdd(a.big_items_count, tot) : 0u;
+    // workgroup-aggregated allocation of the items (one device-scope atomic per workgroup and stretch)
+    uint32_t incl = nch;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t t = __shfl_up(incl, o);
+      if (lane_id() >= o) incl += t;
+    }
+    const int w = threadIdx.x >> 6;
+    __syncthreads();  // s_wsum / s_base of the previous stretch are consumed
+    if (lane_id() == 63) s_wsum[w] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t tot = 0;
+      for (int k = 0; k < 4; k++) {
+        const uint32_t c = s_wsum[k];
+        s_wsum[k] = tot;
+        tot += c;
+      }
+      s_base = tot ? atomicAdd(a.big_items_count, tot) : 0u;
+    }
+    __syncthreads();
+    const uint32_t base = s_base + s_wsum[w] + incl - nch;
+    for (uint32_t k = 0; k < nch; k++) a.big_items[base + k] = (e << 5) | k;
   }
-  __syncthreads();
-  const uint32_t base = s_base + s_wsum[w] + incl - nch;
-  for (uint32_t k = 0; k < nch; k++) a.big_items[base + k] = (e << 5) | k;
 }
 
 // Hits of tiles [k * len, min((k + 1) * len, area)) of entry e's bbox, tested 64 at a time.
@@ -259,17 +264,18 @@ __global__ void __launch_bounds__(256) big_count_kernel(b2c_project_args a) {
 
 // Per entry: exclusive offsets of its chunks (in place) and the splat's tile count.
 __global__ void __launch_bounds__(256) big_sum_kernel(b2c_project_args a) {
-  const uint32_t e = blockIdx.x * 256u + threadIdx.x;
-  if (e >= *a.big_count) return;
-  const uint32_t nch = big_nchunks(reinterpret_cast<const uint4*>(a.big_info)[e]);
-  uint32_t* c = a.big_chunk + (size_t)e * B2C_BIG_CHUNKS;
-  uint32_t run = 0;
-  for (uint32_t k = 0; k < nch; k++) {
-    const uint32_t h = c[k];
-    c[k] = run;
-    run += h;
+  const uint32_t count = *a.big_count;
+  for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < count; e += BIG_ENTRY_GRID * 256u) {
+    const uint32_t nch = big_nchunks(reinterpret_cast<const uint4*>(a.big_info)[e]);
+    uint32_t* c = a.big_chunk + (size_t)e * B2C_BIG_CHUNKS;
+    uint32_t run = 0;
+    for (uint32_t k = 0; k < nch; k++) {
+      const uint32_t h = c[k];
+      c[k] = run;
+      run += h;
+    }
+    a.tile_count[a.big_list[e]] = run;
   }
-  a.tile_count[a.big_list[e]] = run;
 }
 
 __global__ void clear_counters_kernel(uint32_t* a, uint32_t* b) {
@@ -313,7 +319,7 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   const int e = (int)hipGetLastError();
   if (e) return e;
   if (!a->big_info || !a->big_chunk || !a->big_items || !a->big_items_count) return (int)hipErrorInvalidValue;
-  const dim3 per_entry((unsigned)((a->n + 255) / 256));
+  const dim3 per_entry(min((unsigned)((a->n + 255) / 256), BIG_ENTRY_GRID));
   big_setup_kernel<<<per_entry, dim3(256), 0, stream>>>(*a);
   big_count_kernel<<<dim3(B2C_BIG_GRID), dim3(256), 0, stream>>>(*a);
   big_sum_kernel<<<per_entry, dim3(256), 0, stream>>>(*a);
