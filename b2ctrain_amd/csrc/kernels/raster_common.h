@@ -35,11 +35,14 @@ __device__ __forceinline__ float fragment_alpha(float sigma, float log2_op) {
 // of the mask is set when the splat's ellipse {sigma <= power} can reach a pixel centre of quadrant (qx, qy).
 // sigma = ah dx^2 + ch dy^2 + b dx dy (ah = c00 / 2, ch = c11 / 2) is convex, so its minimum over the box
 // spanned by the quadrant's pixel centres is 0 when the centre lies inside and is otherwise attained on an
-// edge, where it is a clamped one-dimensional minimum. The box minimum is at most sigma at any pixel centre
+// edge that the centre lies beyond (sigma falls along the segment from the minimising point to the centre,
+// so that segment leaves the box there): the left edge only if the centre is left of it, and so on - at most
+// one vertical and one horizontal edge, where the minimum is a clamped one-dimensional one. The box minimum is at most sigma at any pixel centre
 // of the quadrant; it is compared with power less a margin of 1e-5 of the terms' magnitude, far above the
 // rounding of this evaluation and of the per-pixel one, so a quadrant is dropped only when no pixel of it
 // can pass the cutoff. A fragment in a dropped quadrant would have had alpha = 0, so culling changes no
-// result. Degenerate conics keep every quadrant. (x0, y0) is the tile's first pixel centre.
+// result. Degenerate conics and a non-finite centre keep every quadrant. (x0, y0) is the tile's first
+// pixel centre.
 __device__ __forceinline__ float edge_sigma_lb(float ah, float b, float ch, float dx, float dy) {
   const float t1 = ah * dx * dx, t2 = ch * dy * dy, t3 = b * dx * dy;
   return (t1 + t2 + t3) - 1e-5f * (fabsf(t1) + fabsf(t2) + fabsf(t3));
@@ -47,7 +50,7 @@ __device__ __forceinline__ float edge_sigma_lb(float ah, float b, float ch, floa
 
 __device__ __forceinline__ uint32_t quadrant_mask(float mx, float my, float ah, float b, float ch, float power,
                                                   float x0, float y0) {
-  if (!(ah > 0.f && ch > 0.f)) return 0xFu;
+  if (!(ah > 0.f && ch > 0.f) || !(mx - mx == 0.f) || !(my - my == 0.f)) return 0xFu;
   const float ky = -b / (2.f * ch), kx = -b / (2.f * ah);  // minimising dy for a given dx, and dx for dy
   const float ex[4] = {x0 - mx, x0 + 3.f - mx, x0 + 4.f - mx, x0 + 7.f - mx};
   const float ey[4] = {y0 - my, y0 + 3.f - my, y0 + 4.f - my, y0 + 7.f - my};
@@ -57,13 +60,14 @@ __device__ __forceinline__ uint32_t quadrant_mask(float mx, float my, float ah, 
 #pragma unroll
     for (int qx = 0; qx < 2; qx++) {
       const float xlo = ex[2 * qx], xhi = ex[2 * qx + 1], ylo = ey[2 * qy], yhi = ey[2 * qy + 1];
-      const bool inside = xlo <= 0.f && xhi >= 0.f && ylo <= 0.f && yhi >= 0.f;
-      const float m0 = edge_sigma_lb(ah, b, ch, xlo, fminf(fmaxf(ky * xlo, ylo), yhi));
-      const float m1 = edge_sigma_lb(ah, b, ch, xhi, fminf(fmaxf(ky * xhi, ylo), yhi));
-      const float m2 = edge_sigma_lb(ah, b, ch, fminf(fmaxf(kx * ylo, xlo), xhi), ylo);
-      const float m3 = edge_sigma_lb(ah, b, ch, fminf(fmaxf(kx * yhi, xlo), xhi), yhi);
-      const bool reach = !(m0 > power) || !(m1 > power) || !(m2 > power) || !(m3 > power);  // NaN keeps it
-      mask |= (inside || reach) ? 1u << (2 * qy + qx) : 0u;
+      // the centre is left of the box when xlo > 0, right of it when xhi < 0 (above / below likewise)
+      const bool fv = (xlo > 0.f) | (xhi < 0.f), fh = (ylo > 0.f) | (yhi < 0.f);
+      const float xe = xlo > 0.f ? xlo : xhi, ye = ylo > 0.f ? ylo : yhi;
+      const float mv = edge_sigma_lb(ah, b, ch, xe, fminf(fmaxf(ky * xe, ylo), yhi));
+      const float mh = edge_sigma_lb(ah, b, ch, fminf(fmaxf(kx * ye, xlo), xhi), ye);
+      // inside: neither edge faces the centre; a NaN edge minimum keeps the quadrant (bitwise: no branches)
+      const bool reach = (!fv & !fh) | (fv & !(mv > power)) | (fh & !(mh > power));
+      mask |= reach ? 1u << (2 * qy + qx) : 0u;
     }
   }
   return mask;
