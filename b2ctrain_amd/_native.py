@@ -16,6 +16,7 @@ LIB_PATH = os.environ.get("B2C_HIP_LIB") or os.path.join(HERE, "lib", "libb2c_hi
 
 GRAD_LANES = 13
 RT_W = 8
+GRAD_ACCUMULATE, GRAD_SPARSE = 1, 2  # b2c_optimizer_grad / b2c_train_step flags (include/b2c.h)
 
 
 class Camera(C.Structure):
@@ -264,16 +265,17 @@ class Renderer:
         check(self.L.b2c_rasterize_backward(self.ctx, self.model, C.byref(self.render_opts(**kw)), mode, grad_scale),
               "rasterize_backward")
 
-    def vjp(self, accumulate=False, active_deg=None, **kw):
+    def vjp(self, accumulate=False, active_deg=None, sparse=False, **kw):
+        flags = (GRAD_ACCUMULATE if accumulate else 0) | (GRAD_SPARSE if sparse else 0)
         check(self.L.b2c_optimizer_grad(self.ctx, self.model, C.byref(self.render_opts(**kw)),
-                                        self.degree if active_deg is None else active_deg, int(accumulate)),
+                                        self.degree if active_deg is None else active_deg, flags),
               "optimizer_grad")
 
     def step(self, mode=1, grad_scale=None, accumulate=False, timed=False, cam=None, bg=None):
         gs = 3.0 * self.W * self.H if grad_scale is None else grad_scale
         t = StepTimes() if timed else None
         check(self.L.b2c_train_step(self.ctx, self.model, self.view, C.byref(self.render_opts(cam=cam, bg=bg)),
-                                    C.byref(self.loss_opts(gs, bg)), mode, int(accumulate),
+                                    C.byref(self.loss_opts(gs, bg)), mode, GRAD_ACCUMULATE if accumulate else 0,
                                     C.byref(t) if timed else None), "train_step")
         return t.as_dict() if timed else None
 

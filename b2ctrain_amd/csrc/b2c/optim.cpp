@@ -22,6 +22,7 @@ void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t
   a.tile_count = ctx.tile_count;
   a.grad_out = op.grad_out;
   a.accumulate = op.grad_accumulate ? 1 : 0;
+  a.sparse = op.sparse ? 1 : 0;
   a.refine_norm = m.refine_norm.ptr;
   a.vis_count = m.vis_count.ptr;
   LAUNCH_CHECK(b2c_hip_vjp(&a, stream));

@@ -325,7 +325,7 @@ int b2c_rasterize_backward(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, i
   });
 }
 
-int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int active_deg, int accumulate) {
+int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int active_deg, int flags) {
   return guarded([&] {
     const size_t per = 11 + 3 * (size_t)m->m.K();
     const size_t need = (size_t)m->m.n * per;
@@ -339,13 +339,14 @@ int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int a
     op.cam = to_params(*o).cam;
     op.active_sh_degree = active_deg;
     op.grad_out = c->grads.ptr;
-    op.grad_accumulate = accumulate != 0;
+    op.grad_accumulate = (flags & B2C_GRAD_ACCUMULATE) != 0;
+    op.sparse = (flags & B2C_GRAD_SPARSE) != 0;
     b2c::optimizer_step(c->ctx, m->m, op, c->stream);
   });
 }
 
 int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
-                   int mode, int accumulate, b2c_step_times* times) {
+                   int mode, int flags, b2c_step_times* times) {
   return guarded([&] {
     const b2c::RenderParams p = to_params(*ro);
     b2c::LossParams lp = to_loss(*lo);
@@ -381,7 +382,8 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
     op.cam = p.cam;
     op.active_sh_degree = p.sh_degree;
     op.grad_out = c->grads.ptr;
-    op.grad_accumulate = accumulate != 0;
+    op.grad_accumulate = (flags & B2C_GRAD_ACCUMULATE) != 0;
+    op.sparse = (flags & B2C_GRAD_SPARSE) != 0;
     b2c::optimizer_step(c->ctx, m->m, op, s);
     b2c::accumulate_loss(c->ctx, s);
     mark(6);

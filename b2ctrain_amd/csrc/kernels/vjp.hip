@@ -2,7 +2,8 @@
 // write of 292-296): one thread per splat turns the 13 screen-space gradient lanes into parameter
 // gradients [pos3, opacity, quat4, log-scale3, SH 3K]. Reads and clears v_splat and vis_flag (the
 // consumed-and-zeroed contract of optim.cu:110-121). accumulate = 1 adds into grad_out so gradients of
-// several views can be summed; 0 overwrites like the reference.
+// several views can be summed; 0 overwrites like the reference, and with sparse set leaves the rows of splats
+// without gradient alone as the reference's early return does (optim.cu:148).
 // Evaluated without FMA contraction, in the operation order of the reference's VJP: the chain through the
 // 2x2 inverse and the 3x3 covariance amplifies rounding differences by the conic's condition number
 // (large for the thin splats of the stress configuration), so the kernel keeps IEEE single-op rounding.
@@ -288,6 +289,9 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   if (a.accumulate) {
     for (int j = threadIdx.x; j < nout; j += VJP_BLOCK)
       if (s_vis[j / PER]) o[j] += s_buf[j];
+  } else if (a.sparse) {  // the reference returns before the grad_out write for these splats
+    for (int j = threadIdx.x; j < nout; j += VJP_BLOCK)
+      if (s_vis[j / PER]) o[j] = s_buf[j];
   } else {
     for (int j = threadIdx.x; j < nout / 4; j += VJP_BLOCK)
       reinterpret_cast<float4*>(o)[j] = reinterpret_cast<const float4*>(s_buf)[j];

@@ -110,13 +110,19 @@ int b2c_photometric_loss(b2c_ctx* c, const b2c_view* v, const b2c_loss_opts* o);
 int b2c_accumulate_loss(b2c_ctx* c);
 /* rasterize_backward (mode 0) / rasterize_backward_tc (mode 1, divides by grad_scale) (src/gpu/render.h:105-109). */
 int b2c_rasterize_backward(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int mode, float grad_scale);
+/* Flags of the gradient write: B2C_GRAD_ACCUMULATE sums into the "grads" buffer instead of overwriting it (this
+ * build's extension for several views); B2C_GRAD_SPARSE leaves the rows of splats without a gradient this step
+ * untouched (OptimParams::sparse, optim.cu:148: the kernel returns before the grad_out write). */
+#define B2C_GRAD_ACCUMULATE 1
+#define B2C_GRAD_SPARSE 2
 /* optimizer_step with grad_out = the context's "grads" buffer [n][11 + 3K] (src/gpu/optim.h:50,
- * optim.cu:292-296); accumulate = 1 sums into it instead of overwriting. */
-int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int active_deg, int accumulate);
+ * optim.cu:292-296); flags as above. */
+int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int active_deg, int flags);
 /* One training step as trainer.cpp:487-529 orders it (forward, loss with grad_scale, backward in `mode`,
- * projection VJP), loss_accum[0..1] zeroed first. times may be NULL (no events recorded). */
+ * projection VJP with the gradient flags above); the step's loss replaces loss_accum[0] (loss_accum[1] = 0).
+ * times may be NULL (no events recorded). */
 int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
-                   int mode, int accumulate, b2c_step_times* times);
+                   int mode, int flags, b2c_step_times* times);
 
 #ifdef __cplusplus
 }

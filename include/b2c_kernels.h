@@ -223,7 +223,8 @@ typedef struct b2c_vjp_args {
   uint32_t* vis_flag;
   const uint32_t* tile_count;
   float* grad_out;            /* [n][11 + 3K] */
-  int accumulate;
+  int accumulate;             /* add into grad_out (rows of splats without gradient unchanged) */
+  int sparse;                 /* leave the rows of splats without gradient unchanged (optim.cu:148) */
   float* refine_norm;         /* [n] or NULL: max(., clamp(g[9], 0, 1e32)) (optim.cu:175-176) */
   float* vis_count;           /* [n] or NULL: += visible (optim.cu:174) */
 } b2c_vjp_args;

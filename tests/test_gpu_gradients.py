@@ -89,3 +89,35 @@ def test_fd_config1():
     emit(f"  checked {checked} skipped {skipped} worst rel {worst:.2e}")
     assert checked > 60
     assert not bad, f"{len(bad)} mismatches, e.g. {bad[:5]}"
+
+
+def test_sparse_gradient_write_leaves_rows_without_gradient():
+    """OptimParams::sparse on the gradient-export path (optim.cu:148: the kernel returns before the grad_out
+    write when a splat has no gradient this step): rows of such splats keep whatever the buffer held, every
+    other row is the dense result. The backward is deterministic, so the same step is run twice."""
+    sc = S.config3(n=40_000)
+    sc.bg = (0.4, 0.3, 0.2)
+    gs = 3.0 * sc.W * sc.H
+    r = _native.Renderer(sc)
+    try:
+        def step_grads(sparse, fill=None):
+            r.forward()
+            r.loss(grad_scale=gs)
+            r.backward(mode=1, grad_scale=gs)
+            if fill is not None:
+                r.write("grads", fill)
+            r.vjp(sparse=sparse)
+            return r.read("grads")
+        dense = step_grads(False)  # also allocates the buffer
+        sentinel = np.full(dense.shape, 12345.0, np.float32)
+        sparse = step_grads(True, fill=sentinel)
+        dense2 = step_grads(False)
+    finally:
+        r.close()
+    assert np.array_equal(dense, dense2)
+    kept = (sparse == sentinel).all(1)
+    written = (sparse == dense).all(1)
+    assert (kept | written).all(), f"rows neither kept nor written: {np.flatnonzero(~(kept | written))[:10]}"
+    assert (dense[kept] == 0).all(), "a kept row had a gradient"
+    emit(f"sparse: {int(kept.sum())} rows kept, {int(written.sum())} written of {len(dense)}")
+    assert kept.sum() > 1000 and written.sum() > 1000  # both cases exercised
