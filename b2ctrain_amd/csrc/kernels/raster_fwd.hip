@@ -95,7 +95,9 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     // power >= +0, since its tile test passed and sigma >= 0 for a positive-definite conic, and sigma is
     // never -0: c00 dx^2 + c11 dy^2 >= +0 and +0 + -0 = +0; a NaN sigma fails either way), bitwise & so the
     // compiler does not branch on the compares; the exp is kept out of an exec-masked branch (a lane with
-    // sigma < 0 has its alpha discarded by the select); only a valid fragment can stop a lane.
+    // sigma < 0 has its alpha discarded by the select); only a valid fragment can stop a lane. A fragment is
+    // composited (vis > 0) exactly when it is valid and does not stop the lane: a valid alpha is at least
+    // 1/255 and a live lane's T is above the cutoff.
 #define B2C_COMPOSITE(off, next)                                                                       \
   do {                                                                                                 \
     const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + (off));                                \
@@ -114,7 +116,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     g += col.y * vis;                                                                                  \
     b += col.z * vis;                                                                                  \
     T = stop ? T : next_T;                                                                             \
-    last_off = vis > 0.f ? (off) : last_off;                                                           \
+    last_off = (valid & !stop) ? (off) : last_off;                                                     \
     (off) = my_list[next];                                                                             \
   } while (0)
     for (uint32_t i = 0; i < n_iter; i += 2) {
