@@ -67,40 +67,78 @@ __device__ __forceinline__ PixelIn load_in(const b2c_loss_args& a, int c, float 
 // The raw words one step of the walk reads from memory: the input row (this lane's column and, for lanes
 // 0-9, the 10 columns past 64), the SSIM row's weight inputs and L1 operands, and the output row's
 // operands. They are fetched one step ahead so the loads overlap the previous step's arithmetic.
+// Every field is loaded unconditionally and converted only where it is used: a conversion next to its
+// load (say of an optional weight, under a branch) would make the wave wait for all loads in flight,
+// the next step's prefetch included.
 struct StepRaw {
   float p_in, p_in2, p_ss, p_out, a_out;
   uint32_t g_in, g_in2, g_ss, g_out;
-  float w_ss, w_out;
+  uint32_t w_ss, w_out;  // weight bytes (without weights: a byte of gt, unused)
 };
 
-__device__ __forceinline__ StepRaw fetch_step(const b2c_loss_args& a, int c, int x0, int y0, int lane, int r) {
-  StepRaw f{};
-  const int y_in = y0 - 2 * HALO + r, xs = x0 - HALO + lane;
-  const int xi = x0 - 2 * HALO + lane;
-  if (in_image(a, xi, y_in)) {
-    const int pix = y_in * a.W + xi;
-    f.p_in = a.pred[(size_t)pix * 4 + c];
-    f.g_in = a.gt[pix];
-  }
-  if (lane < 2 * HALO && in_image(a, xi + 64, y_in)) {
-    const int pix = y_in * a.W + xi + 64;
-    f.p_in2 = a.pred[(size_t)pix * 4 + c];
-    f.g_in2 = a.gt[pix];
-  }
-  const int ys = y_in - HALO, yo = y_in - 2 * HALO;
-  if (r >= 2 * HALO && in_image(a, xs, ys)) {
-    const int pix = ys * a.W + xs;
-    f.p_ss = a.pred[(size_t)pix * 4 + c];
-    f.g_ss = a.gt[pix];
-    f.w_ss = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
-  }
-  if (r >= 4 * HALO && in_image(a, xs, yo)) {
-    const int pix = yo * a.W + xs;
-    f.p_out = a.pred[(size_t)pix * 4 + c];
-    if (c == 0 && a.alpha_lane) f.a_out = a.pred[(size_t)pix * 4 + 3];
-    f.g_out = a.gt[pix];
-    f.w_out = a.weights ? a.weights[pix] * (1.f / 255.f) : 1.f;
-  }
+// Buffer views of the inputs. A load adds the row's byte offset (wave-uniform, a scalar register) to the
+// lane's column offset (fixed for the whole walk), so it costs no per-lane address arithmetic. Rows and
+// columns are clamped into the image, so every load is in bounds; a pixel outside the image is read from
+// its clamped neighbour and then discarded by the caller's in-image test (zero padding).
+constexpr uint32_t BUF_WORD3 = 0x00020000u;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+struct LossBufs {
+  __amdgpu_buffer_rsrc_t pred, gt, w;
+};
+
+__device__ __forceinline__ LossBufs loss_bufs(const b2c_loss_args& a) {
+  const uint32_t P = (uint32_t)a.W * (uint32_t)a.H;  // the launcher checks 16 P < 2^32
+  LossBufs b;
+  b.pred = __builtin_amdgcn_make_buffer_rsrc((void*)a.pred, (short)0, (int)(P * 16u), (int)BUF_WORD3);
+  b.gt = __builtin_amdgcn_make_buffer_rsrc((void*)a.gt, (short)0, (int)(P * 4u), (int)BUF_WORD3);
+  b.w = __builtin_amdgcn_make_buffer_rsrc((void*)(a.weights ? a.weights : (const uint8_t*)a.gt), (short)0, (int)P,
+                                          (int)BUF_WORD3);
+  return b;
+}
+
+// This lane's clamped columns: the input column, the input column 64 further (used by lanes 0-9), and the
+// statistics / output column.
+struct LaneCols {
+  uint32_t in, in2, s;
+};
+
+__device__ __forceinline__ float ld_pred(const LossBufs& b, uint32_t col, int c, uint32_t row_words) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(b.pred, (int)(col * 16u + 4u * (uint32_t)c),
+                                                              (int)(row_words * 16u), 0));
+}
+
+__device__ __forceinline__ uint32_t ld_gt(const LossBufs& b, uint32_t col, uint32_t row_words) {
+  return __builtin_amdgcn_raw_buffer_load_b32(b.gt, (int)(col * 4u), (int)(row_words * 4u), 0);
+}
+
+__device__ __forceinline__ uint32_t ld_weight(const LossBufs& b, uint32_t col, uint32_t row_words) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(b.w, (int)col, (int)row_words, 0);
+}
+
+__device__ __forceinline__ float weight_of(const b2c_loss_args& a, uint32_t raw) {
+  return a.weights ? (float)raw * (1.f / 255.f) : 1.f;
+}
+
+__device__ __forceinline__ int clamp_row(const b2c_loss_args& a, int y) { return min(max(y, 0), a.H - 1); }
+
+__device__ __forceinline__ StepRaw fetch_step(const b2c_loss_args& a, const LossBufs& b, const LaneCols& lc, int c,
+                                              int y0, int r) {
+  StepRaw f;
+  const int y_in = y0 - 2 * HALO + r;
+  const uint32_t ri = (uint32_t)clamp_row(a, y_in) * (uint32_t)a.W;
+  const uint32_t rs = (uint32_t)clamp_row(a, y_in - HALO) * (uint32_t)a.W;
+  const uint32_t ro = (uint32_t)clamp_row(a, y_in - 2 * HALO) * (uint32_t)a.W;
+  f.p_in = ld_pred(b, lc.in, c, ri);
+  f.g_in = ld_gt(b, lc.in, ri);
+  f.p_in2 = ld_pred(b, lc.in2, c, ri);
+  f.g_in2 = ld_gt(b, lc.in2, ri);
+  f.p_ss = ld_pred(b, lc.s, c, rs);
+  f.g_ss = ld_gt(b, lc.s, rs);
+  f.w_ss = ld_weight(b, lc.s, rs);
+  f.p_out = ld_pred(b, lc.s, c, ro);
+  f.a_out = ld_pred(b, lc.s, 3, ro);
+  f.g_out = ld_gt(b, lc.s, ro);
+  f.w_out = ld_weight(b, lc.s, ro);
   return f;
 }
 
@@ -123,6 +161,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
   const int W = a.W, H = a.H;
   const float bg_c = a.composite ? a.bg[c] : 0.f;
   const float norm = a.scale / (3.f * (float)W * (float)H);
+  const float alpha_norm = a.match_alpha_weight * a.scale / ((float)W * (float)H);
   // statistics are accumulated for p - c1 and g - c2 (values at the strip centre): variances and
   // covariances are shift-invariant, and in the gradient 2p*blur(B) - 2*blur(B*mu1) the shift cancels
   // exactly, so both lose far less to fp32 cancellation (loss.cu:122-170)
@@ -137,25 +176,30 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
   float ring1[11][5];  // horizontal blur of the statistics, by row mod 11
   float ring2[11][3];  // horizontal blur of the partial maps, by row mod 11
   float loss_local = 0.f;
-  StepRaw nxt = fetch_step(a, c, x0, y0, lane, 0);
+  const LossBufs bufs = loss_bufs(a);
+  const int xi0 = x0 - 2 * HALO + lane;
+  const LaneCols lc{(uint32_t)min(max(xi0, 0), W - 1), (uint32_t)min(xi0 + 64, W - 1), (uint32_t)min(max(xs, 0), W - 1)};
+  StepRaw nxt = fetch_step(a, bufs, lc, c, y0, 0);
   for (int base = 0; base < ROWS; base += 11) {
 #pragma unroll
     for (int j = 0; j < 11; j++) {
       const int r = base + j;
       const int buf = r & 1;
       const StepRaw cur = nxt;
-      if (r + 1 < ROWS) nxt = fetch_step(a, c, x0, y0, lane, r + 1);
+      if (r + 1 < ROWS) nxt = fetch_step(a, bufs, lc, c, y0, r + 1);
       // ---- input row y_in: columns x0 - 10 .. x0 + 63
       const int y_in = y0 - 2 * HALO + r;
       {
         const int xi = x0 - 2 * HALO + lane;
         const bool v1 = in_image(a, xi, y_in);
-        s_p[buf][lane] = (v1 ? cur.p_in : 0.f) - c1;
-        s_g[buf][lane] = (v1 ? gt_effective(cur.g_in, c, a.composite, bg_c) : 0.f) - c2;
+        const float x = (v1 ? cur.p_in : 0.f) - c1;
+        const float y = (v1 ? gt_effective(cur.g_in, c, a.composite, bg_c) : 0.f) - c2;
+        s_p[buf][lane] = x; s_g[buf][lane] = y;
         if (lane < 2 * HALO) {
           const bool v2 = in_image(a, xi + 64, y_in);
-          s_p[buf][64 + lane] = (v2 ? cur.p_in2 : 0.f) - c1;
-          s_g[buf][64 + lane] = (v2 ? gt_effective(cur.g_in2, c, a.composite, bg_c) : 0.f) - c2;
+          const float x2 = (v2 ? cur.p_in2 : 0.f) - c1;
+          const float y2 = (v2 ? gt_effective(cur.g_in2, c, a.composite, bg_c) : 0.f) - c2;
+          s_p[buf][64 + lane] = x2; s_g[buf][64 + lane] = y2;
         }
       }
       __syncthreads();
@@ -183,7 +227,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
         }
         float A = 0.f, B = 0.f, Bm = 0.f, Cc = 0.f, Cm = 0.f;
         if (in_image(a, xs, ys)) {
-          const float M = cur.w_ss * (a.mask ? gt_channel(cur.g_ss, 3) : 1.f) * norm;
+          const float M = weight_of(a, cur.w_ss) * (a.mask ? gt_channel(cur.g_ss, 3) : 1.f) * norm;
           const float mu1 = st[0] + c1, mu2 = st[2] + c2;
           const float mu1_sq = mu1 * mu1, mu2_sq = mu2 * mu2;
           const float s1_raw = st[1] - st[0] * st[0], s2_raw = st[3] - st[2] * st[2];
@@ -198,10 +242,12 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
             loss_local += M * (a.l1_w * fabsf(cur.p_ss - g) + a.ssim_w * ssim);
           }
           if (raw > -1.f && raw < 1.f) {
+            // one reciprocal for the three quotients (1 / B1 = B2 / (B1 B2), 1 / B2 = B1 / (B1 B2)); the
+            // SSIM value itself stays a correctly rounded quotient, so equal inputs give exactly 1
             const float k = M * a.ssim_w;
-            const float inv_BB = 1.f / (B1 * B2);
-            const float d_mu1 = 2.f * mu2 * A2 * inv_BB - 2.f * mu1 * ssim / B1;
-            const float d_s1 = s1_raw > 0.f ? -ssim / B2 : 0.f;
+            const float inv_BB = __builtin_amdgcn_rcpf(B1 * B2);
+            const float d_mu1 = 2.f * mu2 * A2 * inv_BB - 2.f * mu1 * ssim * (B2 * inv_BB);
+            const float d_s1 = s1_raw > 0.f ? -ssim * (B1 * inv_BB) : 0.f;
             const float d_s12 = 2.f * A1 * inv_BB;
             A = k * d_mu1; B = k * d_s1; Bm = B * st[0]; Cc = k * d_s12; Cm = Cc * st[2];
           }
@@ -238,7 +284,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
             const float p = cur.p_out, g = gt_effective(cur.g_out, c, a.composite, bg_c);
             const float ps = p - c1, gs = g - c2;
             const float gt_a = gt_channel(cur.g_out, 3);
-            const float M = cur.w_out * (a.mask ? gt_a : 1.f) * norm;
+            const float M = weight_of(a, cur.w_out) * (a.mask ? gt_a : 1.f) * norm;
             const float sgn = p > g ? 1.f : (p < g ? -1.f : 0.f);
             const float grad = M * a.l1_w * sgn + acc[0] + 2.f * ps * acc[1] + gs * acc[2];
             a.v_out[(size_t)pix * 4 + c] = grad * a.grad_scale;
@@ -247,7 +293,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
               if (a.alpha_lane) {
                 const float da = cur.a_out - gt_a;
                 const float sa = da > 0.f ? 1.f : (da < 0.f ? -1.f : 0.f);
-                const float Ma = cur.w_out * a.match_alpha_weight * a.scale / ((float)W * (float)H);
+                const float Ma = weight_of(a, cur.w_out) * alpha_norm;
                 va = Ma * sa * a.grad_scale;
                 loss_local += Ma * fabsf(da);
               }
@@ -347,6 +393,7 @@ int pick_strip_rows(int W, int H) {
 
 extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   if (a->W <= 0 || a->H <= 0) return 0;
+  if ((uint64_t)a->W * (uint64_t)a->H * 16u > 0xFFFFFFFFull) return (int)hipErrorInvalidValue;  // 32-bit buffer offsets
   if (a->assign && !a->partials) return (int)hipErrorInvalidValue;  // float atomics can only add
   Gauss11 g;
   double w[11], sum = 0.0;
