@@ -108,34 +108,58 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   constexpr int K = (DEG + 1) * (DEG + 1);
   constexpr int PER = 11 + 3 * K;
   __shared__ __attribute__((aligned(16))) float s_buf[VJP_BLOCK * PER];  // v_splat rows in, grad_out rows out
-  __shared__ uint32_t s_vis[VJP_BLOCK];
+  __shared__ uint32_t s_vis[VJP_BLOCK], s_any[VJP_BLOCK];
   const int i0 = blockIdx.x * VJP_BLOCK;
   const int i = i0 + threadIdx.x;
   const int rows = min(VJP_BLOCK, a.n - i0);
   const bool in_range = i < a.n;
-  const uint32_t vis = in_range ? a.vis_flag[i] : 0u;
-  if (vis) a.vis_flag[i] = 0u;
-  s_vis[threadIdx.x] = vis;
-  // the block's v_splat rows are one contiguous, 16-byte aligned stretch (VJP_BLOCK * 13 floats per block)
+  // Memory round trip 1: this splat's flag, tile count and statistics, and the block's v_splat rows (one
+  // contiguous, 16-byte aligned stretch of VJP_BLOCK * 13 floats), all issued before any is waited for.
+  uint32_t vis = 0u, tc = 0u;
+  float vcount = 0.f, rnorm = 0.f;
+  if (in_range) {
+    vis = a.vis_flag[i];
+    tc = a.tile_count[i];
+    if (a.vis_count) vcount = a.vis_count[i];
+    if (a.refine_norm) rnorm = a.refine_norm[i];
+  }
   const int nin = rows * GRAD_LANES;
   const float* vin = a.v_splat + (size_t)i0 * GRAD_LANES;
-  for (int j = threadIdx.x; j < nin / 4; j += VJP_BLOCK)
-    reinterpret_cast<float4*>(s_buf)[j] = reinterpret_cast<const float4*>(vin)[j];
-  for (int j = (nin & ~3) + threadIdx.x; j < nin; j += VJP_BLOCK) s_buf[j] = vin[j];
+  if (rows == VJP_BLOCK) {  // uniform: a whole block, a fixed number of loads per thread
+    constexpr int N4 = VJP_BLOCK * GRAD_LANES / 4, FULL = N4 / VJP_BLOCK, REM = N4 - FULL * VJP_BLOCK;
+    static_assert(VJP_BLOCK * GRAD_LANES % 4 == 0 && FULL == 3, "whole float4s per block, 3 + a remainder");
+    const float4* v4 = reinterpret_cast<const float4*>(vin) + threadIdx.x;
+    float4* b4 = reinterpret_cast<float4*>(s_buf) + threadIdx.x;
+    const bool rem = threadIdx.x < REM;
+    const float4 t0 = v4[0], t1 = v4[VJP_BLOCK], t2 = v4[2 * VJP_BLOCK];
+    float4 t3 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (rem) t3 = v4[3 * VJP_BLOCK];
+    b4[0] = t0; b4[VJP_BLOCK] = t1; b4[2 * VJP_BLOCK] = t2;
+    if (rem) b4[3 * VJP_BLOCK] = t3;
+  } else {
+    for (int j = threadIdx.x; j < nin / 4; j += VJP_BLOCK)
+      reinterpret_cast<float4*>(s_buf)[j] = reinterpret_cast<const float4*>(vin)[j];
+    for (int j = (nin & ~3) + threadIdx.x; j < nin; j += VJP_BLOCK) s_buf[j] = vin[j];
+  }
+  s_vis[threadIdx.x] = vis;
   __syncthreads();
-  // read then clear the consumed rows (optim.cu:110-121)
-  for (int j = threadIdx.x; j < rows * GRAD_LANES; j += VJP_BLOCK)
-    if (s_vis[j / GRAD_LANES]) a.v_splat[(size_t)i0 * GRAD_LANES + j] = 0.f;
   float g[GRAD_LANES];
 #pragma unroll
   for (int k = 0; k < GRAD_LANES; k++) g[k] = vis ? s_buf[threadIdx.x * GRAD_LANES + k] : 0.f;
-  __syncthreads();
-  const bool visible = vis != 0u && a.tile_count[i] != 0u;
-  if (a.vis_count && in_range) a.vis_count[i] += visible ? 1.f : 0.f;
+  __syncthreads();  // s_buf now holds the grad_out rows
+  // Update the statistics, then clear the consumed flag and rows (optim.cu:110-121). A barrier waits for
+  // every memory operation in flight, stores included, so these stores come after the barriers above and
+  // overlap the parameter loads below. The loaded words are all used before the clearing loop, whose
+  // store count is not known at compile time (a use after it would wait for every store).
+  const bool visible = vis != 0u && tc != 0u;
+  if (a.vis_count && in_range) a.vis_count[i] = vcount + (visible ? 1.f : 0.f);
   if (a.refine_norm && in_range) {
     const float rn = __builtin_isfinite(g[9]) ? fminf(fmaxf(g[9], 0.f), 1e32f) : 0.f;
-    a.refine_norm[i] = fmaxf(a.refine_norm[i], rn);
+    a.refine_norm[i] = fmaxf(rnorm, rn);
   }
+  if (vis) a.vis_flag[i] = 0u;
+  for (int j = threadIdx.x; j < rows * GRAD_LANES; j += VJP_BLOCK)
+    if (s_vis[j / GRAD_LANES]) a.v_splat[(size_t)i0 * GRAD_LANES + j] = 0.f;
   bool any = false;
 #pragma unroll
   for (int k = 0; k < GRAD_LANES; k++) if (k != 9 && g[k] != 0.f) any = true;
@@ -148,34 +172,37 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   float* out = s_buf + threadIdx.x * PER;
   bool done = false;
   if (any) {
+    // Memory round trip 2: the splat's parameters and all its SH coefficients, issued together
     const float4 po = reinterpret_cast<const float4*>(a.pos_op)[i];
     const float4 q = reinterpret_cast<const float4*>(a.quat)[i];
     const float4 ls = reinterpret_cast<const float4*>(a.lscale)[i];
+    const ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
+    float coef[3 * K];
+    sv.load_all<DEG>(i, coef);
+    const b2c_camera_gpu& cam = a.cam;
+    // The SH half needs only the view direction: it runs first, so the coefficients are dead before the
+    // projection's registers are live. Its row entries are zeroed below if the projection fails.
+    const float ux = po.x - cam.pos[0], uy = po.y - cam.pos[1], uz = po.z - cam.pos[2];
+    const float ul = sqrtf(ux * ux + uy * uy + uz * uz);
+    const float iul = 1.f / ul;
+    const float vx = ux * iul, vy = uy * iul, vz = uz * iul;
+    const int kmax = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
+    const float3 vc = make_float3(g[5], g[6], g[7]);
+    {
+      float basis[K];
+      sh_basis<DEG>(vx, vy, vz, basis);
+#pragma unroll
+      for (int k = 0; k < K; k++) {
+        const float bk = k < kmax ? basis[k] : 0.f;
+        out[11 + k * 3] = bk * vc.x; out[12 + k * 3] = bk * vc.y; out[13 + k * 3] = bk * vc.z;
+      }
+    }
+    float vvx, vvy, vvz;
+    sh_viewdir_vjp<DEG>(coef, vx, vy, vz, vc, a.active_deg, vvx, vvy, vvz);
+    const float vdot = vx * vvx + vy * vvy + vz * vvz;
+    const float msx = (vvx - vx * vdot) * (1.f / ul), msy = (vvy - vy * vdot) * (1.f / ul), msz = (vvz - vz * vdot) * (1.f / ul);
     const Proj pr = project_one(po, q, ls, a.cam);
     if (pr.ok) {
-      const b2c_camera_gpu& cam = a.cam;
-      const ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
-      const float ux = po.x - cam.pos[0], uy = po.y - cam.pos[1], uz = po.z - cam.pos[2];
-      const float ul = sqrtf(ux * ux + uy * uy + uz * uz);
-      const float iul = 1.f / ul;
-      const float vx = ux * iul, vy = uy * iul, vz = uz * iul;
-      const int kmax = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
-      const float3 vc = make_float3(g[5], g[6], g[7]);
-      {
-        float basis[K];
-        sh_basis<DEG>(vx, vy, vz, basis);
-#pragma unroll
-        for (int k = 0; k < K; k++) {
-          const float bk = k < kmax ? basis[k] : 0.f;
-          out[11 + k * 3] = bk * vc.x; out[12 + k * 3] = bk * vc.y; out[13 + k * 3] = bk * vc.z;
-        }
-      }
-      float vvx, vvy, vvz;
-      float coef[3 * K];
-      sv.load_all<DEG>(i, coef);
-      sh_viewdir_vjp<DEG>(coef, vx, vy, vz, vc, a.active_deg, vvx, vvy, vvz);
-      const float vdot = vx * vvx + vy * vvy + vz * vvz;
-      const float msx = (vvx - vx * vdot) * (1.f / ul), msy = (vvy - vy * vdot) * (1.f / ul), msz = (vvz - vz * vdot) * (1.f / ul);
       const float v_alpha = g[8];
       float g_op = v_alpha * 1.f * pr.comp_floor * pr.sig * (1.f - pr.sig);
       const Sym2 v_cov = inverse2x2_vjp(pr.conic, Sym2{g[2], 0.5f * g[3], g[4]});
@@ -281,17 +308,17 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
 #pragma unroll
     for (int k = 0; k < PER; k++) out[k] = 0.f;
   }
-  s_vis[threadIdx.x] = any ? 1u : 0u;
+  s_any[threadIdx.x] = any ? 1u : 0u;
   __syncthreads();
   // the block's grad_out rows: one contiguous stretch, 16-byte aligned (VJP_BLOCK * PER floats per block)
   float* o = a.grad_out + (size_t)i0 * PER;
   const int nout = rows * PER;
   if (a.accumulate) {
     for (int j = threadIdx.x; j < nout; j += VJP_BLOCK)
-      if (s_vis[j / PER]) o[j] += s_buf[j];
+      if (s_any[j / PER]) o[j] += s_buf[j];
   } else if (a.sparse) {  // the reference returns before the grad_out write for these splats
     for (int j = threadIdx.x; j < nout; j += VJP_BLOCK)
-      if (s_vis[j / PER]) o[j] = s_buf[j];
+      if (s_any[j / PER]) o[j] = s_buf[j];
   } else {
     for (int j = threadIdx.x; j < nout / 4; j += VJP_BLOCK)
       reinterpret_cast<float4*>(o)[j] = reinterpret_cast<const float4*>(s_buf)[j];
