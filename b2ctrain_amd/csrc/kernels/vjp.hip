@@ -147,10 +147,9 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
 #pragma unroll
   for (int k = 0; k < GRAD_LANES; k++) g[k] = vis ? s_buf[threadIdx.x * GRAD_LANES + k] : 0.f;
   __syncthreads();  // s_buf now holds the grad_out rows
-  // Update the statistics, then clear the consumed flag and rows (optim.cu:110-121). A barrier waits for
-  // every memory operation in flight, stores included, so these stores come after the barriers above and
-  // overlap the parameter loads below. The loaded words are all used before the clearing loop, whose
-  // store count is not known at compile time (a use after it would wait for every store).
+  // Update the statistics, then clear the consumed flag and rows (optim.cu:110-121). The loaded words are
+  // all used before the clearing loop: its store count is not known at compile time, so a use of an
+  // earlier load after it would wait for every memory operation in flight.
   const bool visible = vis != 0u && tc != 0u;
   if (a.vis_count && in_range) a.vis_count[i] = vcount + (visible ? 1.f : 0.f);
   if (a.refine_norm && in_range) {
