@@ -27,7 +27,7 @@ struct WaveRec {
   uint32_t bw;
 };
 
-template <int DEG>
+template <int DEG, bool HALF>
 __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a) {
   __shared__ WaveRec s_rec[PROJ_BLOCK];
   __shared__ uint32_t s_incl[PROJ_BLOCK];
@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       const int ka = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
       const ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
       float coef[3 * K];
-      sv.load_all<DEG>(i, coef);
+      sv.load_all<DEG, HALF>(i, coef);
       float cr = coef[0] * b[0], cg = coef[1] * b[0], cb = coef[2] * b[0];
 #pragma unroll
       for (int k = 1; k < K; k++) {
@@ -309,12 +309,17 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (!a->big_count || !a->big_list) return (int)hipErrorInvalidValue;
   clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);  // one launch for both
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);
-  switch (a->degree) {
-    case 0: project_kernel<0><<<grid, block, 0, stream>>>(*a); break;
-    case 1: project_kernel<1><<<grid, block, 0, stream>>>(*a); break;
-    case 2: project_kernel<2><<<grid, block, 0, stream>>>(*a); break;
-    case 3: project_kernel<3><<<grid, block, 0, stream>>>(*a); break;
-    default: project_kernel<4><<<grid, block, 0, stream>>>(*a); break;
+  const bool half = a->degree > 0 && !a->sh.hi32;  // fp16 bands
+  switch (a->degree * 2 + (half ? 1 : 0)) {
+    case 0: project_kernel<0, false><<<grid, block, 0, stream>>>(*a); break;
+    case 2: project_kernel<1, false><<<grid, block, 0, stream>>>(*a); break;
+    case 3: project_kernel<1, true><<<grid, block, 0, stream>>>(*a); break;
+    case 4: project_kernel<2, false><<<grid, block, 0, stream>>>(*a); break;
+    case 5: project_kernel<2, true><<<grid, block, 0, stream>>>(*a); break;
+    case 6: project_kernel<3, false><<<grid, block, 0, stream>>>(*a); break;
+    case 7: project_kernel<3, true><<<grid, block, 0, stream>>>(*a); break;
+    case 8: project_kernel<4, false><<<grid, block, 0, stream>>>(*a); break;
+    default: project_kernel<4, true><<<grid, block, 0, stream>>>(*a); break;
   }
   const int e = (int)hipGetLastError();
   if (e) return e;

@@ -103,7 +103,7 @@ __device__ __forceinline__ void sh_viewdir_vjp(const float* coef, float x, float
 // would touch one cache line per lane per instruction).
 constexpr int VJP_BLOCK = 128;
 
-template <int DEG>
+template <int DEG, bool HALF>
 __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   constexpr int K = (DEG + 1) * (DEG + 1);
   constexpr int PER = 11 + 3 * K;
@@ -177,7 +177,10 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
     const float4 ls = reinterpret_cast<const float4*>(a.lscale)[i];
     const ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
     float coef[3 * K];
-    sv.load_all<DEG>(i, coef);
+    if constexpr (HALF)
+      sv.load_all<DEG, true>(i, coef);
+    else
+      sv.load_all_either<DEG>(i, coef);
     const b2c_camera_gpu& cam = a.cam;
     // The SH half needs only the view direction: it runs first, so the coefficients are dead before the
     // projection's registers are live. Its row entries are zeroed below if the projection fails.
@@ -334,12 +337,17 @@ using namespace b2c::dev;
 extern "C" int b2c_hip_vjp(const b2c_vjp_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   const dim3 grid((unsigned)((a->n + VJP_BLOCK - 1) / VJP_BLOCK)), block(VJP_BLOCK);
-  switch (a->degree) {
-    case 0: vjp_kernel<0><<<grid, block, 0, stream>>>(*a); break;
-    case 1: vjp_kernel<1><<<grid, block, 0, stream>>>(*a); break;
-    case 2: vjp_kernel<2><<<grid, block, 0, stream>>>(*a); break;
-    case 3: vjp_kernel<3><<<grid, block, 0, stream>>>(*a); break;
-    case 4: vjp_kernel<4><<<grid, block, 0, stream>>>(*a); break;
+  const bool half = a->degree > 0 && !a->sh.hi32;  // fp16 bands
+  switch (a->degree * 2 + (half ? 1 : 0)) {
+    case 0: vjp_kernel<0, false><<<grid, block, 0, stream>>>(*a); break;
+    case 2: vjp_kernel<1, false><<<grid, block, 0, stream>>>(*a); break;
+    case 3: vjp_kernel<1, true><<<grid, block, 0, stream>>>(*a); break;
+    case 4: vjp_kernel<2, false><<<grid, block, 0, stream>>>(*a); break;
+    case 5: vjp_kernel<2, true><<<grid, block, 0, stream>>>(*a); break;
+    case 6: vjp_kernel<3, false><<<grid, block, 0, stream>>>(*a); break;
+    case 7: vjp_kernel<3, true><<<grid, block, 0, stream>>>(*a); break;
+    case 8: vjp_kernel<4, false><<<grid, block, 0, stream>>>(*a); break;
+    case 9: vjp_kernel<4, true><<<grid, block, 0, stream>>>(*a); break;
     default: return (int)hipErrorInvalidValue;
   }
   return (int)hipGetLastError();
