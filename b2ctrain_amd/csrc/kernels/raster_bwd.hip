@@ -597,35 +597,42 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
 // order: one wave step per such run, so no lane walks a long chain alone.
 constexpr uint32_t SHORT_SPAN = 4;
 
-__global__ void __launch_bounds__(256) isect_fixup_kernel(b2c_raster_bwd_args a) {
+__global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) {
   const uint32_t nwin = (a.num_isect + RED_WIN - 1u) / RED_WIN;
-  const uint32_t w = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t w = blockIdx.x * 64u + threadIdx.x;
   const int lane = threadIdx.x & 63;
   const float4* part = reinterpret_cast<const float4*>(a.isect_part);
-  bool owner = false;
-  uint32_t run = NO_RUN, last_win = 0;
-  if (w < nwin) {
-    const uint32_t f = a.isect_part_flags[w];
-    owner = (f & W_CONT_AFTER) && (f & W_HAS_HEAD);
-    if (owner) {
-      run = a.isect_vals[w * RED_WIN + RED_WIN - 1u];
-      // the run covers emit positions [head, head + tile_count)
-      const uint32_t head = __float_as_uint(part[(size_t)w * 6 + 5].w);
-      last_win = min((head + a.tile_count[run] - 1u) / RED_WIN, nwin - 1u);
-    }
-  }
+  // Memory round trip 1: the window's flags, last id and head slot, its own tail partials and the head
+  // partials of the next SHORT_SPAN windows. Round trip 2: the run's tile count and previous sums. Every
+  // load is unconditional, from a clamped window or id, so no branch splits the loads from their waits.
+  const uint32_t wc = min(w, nwin - 1u);
+  const uint32_t f = a.isect_part_flags[wc];
+  const uint32_t run_ld = a.isect_vals[min(wc * RED_WIN + RED_WIN - 1u, a.num_isect - 1u)];
+  const uint32_t head = __float_as_uint(part[(size_t)wc * 6 + 5].w);
+  float4 tail[3], nxt[SHORT_SPAN][3];
+#pragma unroll
+  for (int k = 0; k < 3; k++) tail[k] = part[(size_t)wc * 6 + 3 + k];
+#pragma unroll
+  for (uint32_t d = 1; d <= SHORT_SPAN; d++)
+#pragma unroll
+    for (int k = 0; k < 3; k++) nxt[d - 1][k] = part[(size_t)min(wc + d, nwin - 1u) * 6 + k];
+  const bool owner = w < nwin && (f & W_CONT_AFTER) && (f & W_HAS_HEAD);
+  const uint32_t run = owner ? run_ld : NO_RUN;
+  const uint32_t tc = a.tile_count[run_ld];
+  float old_s[RED_VALS];
+  prefetch_old(a, run_ld, old_s);
+  // the run covers emit positions [head, head + tile_count)
+  const uint32_t last_win = owner ? min((head + tc - 1u) / RED_WIN, nwin - 1u) : 0u;
   const bool short_run = owner && last_win - w <= SHORT_SPAN;
   if (short_run) {
     float v[RED_VALS];
 #pragma unroll
     for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
-    add_part(part + (size_t)w * 6 + 3, v);
+    add_part(tail, v);
 #pragma unroll
     for (uint32_t d = 1; d <= SHORT_SPAN; d++)
-      if (w + d <= last_win) add_part(part + (size_t)(w + d) * 6, v);  // the run's rows at the start of w + d
-    float old[RED_VALS];
-    prefetch_old(a, run, old);
-    finish_run(a, run, v, old);
+      if (w + d <= last_win) add_part(nxt[d - 1], v);  // the run's rows at the start of w + d
+    finish_run(a, run, v, old_s);
   }
   // long runs: every lane of the wave stays to here (no early exit), so the cross-lane sums are whole
   uint64_t longs = ballot64(owner && !short_run);
@@ -681,7 +688,7 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
     if (windows) {
       if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;
       isect_reduce_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
-      isect_fixup_kernel<<<dim3((windows + 255u) / 256u), dim3(256), 0, stream>>>(*a);
+      isect_fixup_kernel<<<dim3((windows + 63u) / 64u), dim3(64), 0, stream>>>(*a);
     }
   }
   return (int)hipGetLastError();
