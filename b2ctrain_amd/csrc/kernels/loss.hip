@@ -8,6 +8,7 @@
 #include "device_math.h"
 
 #include <stdlib.h>
+#include <string.h>
 
 namespace b2c {
 namespace dev {
@@ -16,7 +17,12 @@ namespace {
 constexpr int HALO = 5;
 constexpr float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
 
-struct Gauss11 { float w[11]; };
+// The 11 weights (double-precision exp(-d^2 / 4.5) normalised to sum 1, rounded to float), as compile-time
+// constants: passed as kernel arguments they took 11 scalar registers and the kernel spilled others. The
+// launcher checks them bitwise against its own computation.
+constexpr uint32_t GW_BITS[11] = {0x3a86cab6u, 0x3bf8ff01u, 0x3d13758cu, 0x3ddff87fu, 0x3e5a1e20u, 0x3e8832b0u,
+                                  0x3e5a1e20u, 0x3ddff87fu, 0x3d13758cu, 0x3bf8ff01u, 0x3a86cab6u};
+__device__ __forceinline__ float gw_tap(int d) { return __uint_as_float(GW_BITS[d]); }
 
 __device__ __forceinline__ float gt_channel(uint32_t packed, int c) {
   return (float)((packed >> (8 * c)) & 0xffu) * (1.f / 255.f);
@@ -146,7 +152,7 @@ __device__ __forceinline__ StepRaw fetch_step(const b2c_loss_args& a, const Loss
 // a strip are consecutive on their XCD, so the strip's input lines are read from that XCD's L2 three times
 // rather than from memory.
 template <int SH>
-__global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss11 gw, int strips_x, int nstrips) {
+__global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int strips_x, int nstrips) {
   constexpr int ROWS = SH + 4 * HALO;
   static_assert(ROWS % 11 == 0, "the row loop is unrolled by the ring length");
   __shared__ float s_p[2][64 + 2 * HALO], s_g[2][64 + 2 * HALO];  // one input row (double buffered)
@@ -207,7 +213,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
         float sx = 0.f, sx2 = 0.f, sy = 0.f, sy2 = 0.f, sxy = 0.f;
 #pragma unroll
         for (int d = 0; d < 11; d++) {
-          const float w = gw.w[d];
+          const float w = gw_tap(d);
           const float x = s_p[buf][lane + d], y = s_g[buf][lane + d];
           const float wx = w * x, wy = w * y;
           sx += wx; sx2 += wx * x; sy += wy; sy2 += wy * y; sxy += wx * y;
@@ -221,7 +227,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
 #pragma unroll
         for (int d = 0; d < 11; d++) {
           const int slot = (j + 1 + d) % 11;  // oldest row first
-          const float w = gw.w[d];
+          const float w = gw_tap(d);
 #pragma unroll
           for (int k = 0; k < 5; k++) st[k] += w * ring1[slot][k];
         }
@@ -263,7 +269,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
         if (out_lane) {
 #pragma unroll
           for (int d = 0; d < 11; d++) {
-            const float w = gw.w[d];
+            const float w = gw_tap(d);
 #pragma unroll
             for (int k = 0; k < 3; k++) ring2[j2][k] += w * s_pm[buf][k][lane - HALO + d];
           }
@@ -275,7 +281,7 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, Gauss1
 #pragma unroll
           for (int d = 0; d < 11; d++) {
             const int slot = (j2 + 1 + d) % 11;
-            const float w = gw.w[d];
+            const float w = gw_tap(d);
 #pragma unroll
             for (int k = 0; k < 3; k++) acc[k] += w * ring2[slot][k];
           }
@@ -395,23 +401,32 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   if (a->W <= 0 || a->H <= 0) return 0;
   if ((uint64_t)a->W * (uint64_t)a->H * 16u > 0xFFFFFFFFull) return (int)hipErrorInvalidValue;  // 32-bit buffer offsets
   if (a->assign && !a->partials) return (int)hipErrorInvalidValue;  // float atomics can only add
-  Gauss11 g;
-  double w[11], sum = 0.0;
-  for (int i = 0; i < 11; i++) {
-    const double x = i - 5.0;
-    w[i] = __builtin_exp(-x * x / (2.0 * 1.5 * 1.5));
-    sum += w[i];
-  }
-  for (int i = 0; i < 11; i++) g.w[i] = (float)(w[i] / sum);
+  // the kernel's constant weights must equal the double-precision Gaussian rounded to float
+  static const bool weights_ok = [] {
+    double w[11], sum = 0.0;
+    for (int i = 0; i < 11; i++) {
+      const double x = i - 5.0;
+      w[i] = __builtin_exp(-x * x / (2.0 * 1.5 * 1.5));
+      sum += w[i];
+    }
+    for (int i = 0; i < 11; i++) {
+      const float f = (float)(w[i] / sum);
+      uint32_t bits;
+      memcpy(&bits, &f, 4);
+      if (bits != GW_BITS[i]) return false;
+    }
+    return true;
+  }();
+  if (!weights_ok) return (int)hipErrorInvalidValue;
   const int strips_x = (a->W + SW - 1) / SW;
   const int sh = pick_strip_rows(a->W, a->H);
   const int nstrips = strips_x * ((a->H + sh - 1) / sh);
   const dim3 grid(8 * ((nstrips * 3 + 7) / 8)), block(64);
   switch (sh) {
-    case 35: photometric_kernel<35><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
-    case 46: photometric_kernel<46><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
-    case 57: photometric_kernel<57><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
-    default: photometric_kernel<79><<<grid, block, 0, stream>>>(*a, g, strips_x, nstrips); break;
+    case 35: photometric_kernel<35><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
+    case 46: photometric_kernel<46><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
+    case 57: photometric_kernel<57><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
+    default: photometric_kernel<79><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
   }
   if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum, a->assign);
   return (int)hipGetLastError();
