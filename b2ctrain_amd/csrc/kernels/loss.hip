@@ -77,7 +77,7 @@ __device__ __forceinline__ PixelIn load_in(const b2c_loss_args& a, int c, float 
 // load (say of an optional weight, under a branch) would make the wave wait for all loads in flight,
 // the next step's prefetch included.
 struct StepRaw {
-  float p_in, p_in2, p_ss, p_out, a_out;
+  float p_in, p_in2, a_out;
   uint32_t g_in, g_in2, g_ss, g_out;
   uint32_t w_ss, w_out;  // weight bytes (without weights: a byte of gt, unused)
 };
@@ -138,10 +138,8 @@ __device__ __forceinline__ StepRaw fetch_step(const b2c_loss_args& a, const Loss
   f.g_in = ld_gt(b, lc.in, ri);
   f.p_in2 = ld_pred(b, lc.in2, c, ri);
   f.g_in2 = ld_gt(b, lc.in2, ri);
-  f.p_ss = ld_pred(b, lc.s, c, rs);
   f.g_ss = ld_gt(b, lc.s, rs);
   f.w_ss = ld_weight(b, lc.s, rs);
-  f.p_out = ld_pred(b, lc.s, c, ro);
   f.a_out = ld_pred(b, lc.s, 3, ro);
   f.g_out = ld_gt(b, lc.s, ro);
   f.w_out = ld_weight(b, lc.s, ro);
@@ -156,6 +154,9 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int st
   constexpr int ROWS = SH + 4 * HALO;
   static_assert(ROWS % 11 == 0, "the row loop is unrolled by the ring length");
   __shared__ float s_p[2][64 + 2 * HALO], s_g[2][64 + 2 * HALO];  // one input row (double buffered)
+  // the last 11 input rows, unshifted: prediction and effective target, read back 5 rows later as the
+  // SSIM row's L1 operands and 10 rows later as the output row's (slot = row mod 11, static when unrolled)
+  __shared__ float s_rp[11][64 + 2 * HALO], s_rg[11][64 + 2 * HALO];
   __shared__ float s_pm[2][3][64];                                 // one partial-map row (double buffered)
   constexpr int NXCD = 8;
   const int per = (nstrips * 3 + NXCD - 1) / NXCD;  // work items per XCD
@@ -198,14 +199,14 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int st
       {
         const int xi = x0 - 2 * HALO + lane;
         const bool v1 = in_image(a, xi, y_in);
-        const float x = (v1 ? cur.p_in : 0.f) - c1;
-        const float y = (v1 ? gt_effective(cur.g_in, c, a.composite, bg_c) : 0.f) - c2;
-        s_p[buf][lane] = x; s_g[buf][lane] = y;
+        const float pr = v1 ? cur.p_in : 0.f, gr = v1 ? gt_effective(cur.g_in, c, a.composite, bg_c) : 0.f;
+        s_p[buf][lane] = pr - c1; s_g[buf][lane] = gr - c2;
+        s_rp[j][lane] = pr; s_rg[j][lane] = gr;
         if (lane < 2 * HALO) {
           const bool v2 = in_image(a, xi + 64, y_in);
-          const float x2 = (v2 ? cur.p_in2 : 0.f) - c1;
-          const float y2 = (v2 ? gt_effective(cur.g_in2, c, a.composite, bg_c) : 0.f) - c2;
-          s_p[buf][64 + lane] = x2; s_g[buf][64 + lane] = y2;
+          const float pr2 = v2 ? cur.p_in2 : 0.f, gr2 = v2 ? gt_effective(cur.g_in2, c, a.composite, bg_c) : 0.f;
+          s_p[buf][64 + lane] = pr2 - c1; s_g[buf][64 + lane] = gr2 - c2;
+          s_rp[j][64 + lane] = pr2; s_rg[j][64 + lane] = gr2;
         }
       }
       __syncthreads();
@@ -244,8 +245,9 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int st
           const float raw = (A1 * A2) / (B1 * B2);
           const float ssim = fminf(fmaxf(raw, -1.f), 1.f);
           if (out_lane && ys >= y0 && ys < y0 + SH) {
-            const float g = gt_effective(cur.g_ss, c, a.composite, bg_c);
-            loss_local += M * (a.l1_w * fabsf(cur.p_ss - g) + a.ssim_w * ssim);
+            const int slot = (j + 6) % 11;  // input row r - 5
+            const float g = s_rg[slot][lane + HALO];
+            loss_local += M * (a.l1_w * fabsf(s_rp[slot][lane + HALO] - g) + a.ssim_w * ssim);
           }
           if (raw > -1.f && raw < 1.f) {
             // one reciprocal for the three quotients (1 / B1 = B2 / (B1 B2), 1 / B2 = B1 / (B1 B2)); the
@@ -287,7 +289,8 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int st
           }
           if (out_lane && yo < H && xo < W) {
             const int pix = yo * W + xo;
-            const float p = cur.p_out, g = gt_effective(cur.g_out, c, a.composite, bg_c);
+            const int slot = (j + 1) % 11;  // input row r - 10
+            const float p = s_rp[slot][lane + HALO], g = s_rg[slot][lane + HALO];
             const float ps = p - c1, gs = g - c2;
             const float gt_a = gt_channel(cur.g_out, 3);
             const float M = weight_of(a, cur.w_out) * (a.mask ? gt_a : 1.f) * norm;
