@@ -352,24 +352,32 @@ __global__ void __launch_bounds__(256) emit_small_kernel(b2c_emit_args a, uint32
 // order), so each chunk writes its own stretch independently.
 __global__ void __launch_bounds__(256) emit_big_kernel(b2c_emit_args a, const uint32_t* __restrict__ big_base) {
   const int lane = lane_id();
-  const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
+  // wave-uniform (the compiler cannot see that threadIdx.x >> 6 is): the per-item chain uses scalar loads
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)((blockIdx.x * 256u + threadIdx.x) >> 6));
   const uint32_t nwaves = (gridDim.x * 256u) >> 6;
   const uint32_t items = *a.big_items_count;
   const uint32_t sentinel = (uint32_t)(a.tiles_x * a.tiles_y);
   for (uint32_t it = wave; it < items; it += nwaves) {
+    // three dependent memory round trips: the item; the entry's bbox, splat and chunk offsets; the splat's
+    // count, base and record. An entry past the capacity gets an empty range rather than a branch, so the
+    // compiler cannot sink the last loads behind the capacity check (a fourth round trip).
     const uint32_t code = a.big_items[it];
     const uint32_t e = code >> 5, k = code & 31u;
     const uint4 info = reinterpret_cast<const uint4*>(a.big_info)[e];
-    const uint32_t begin = k * info.w, end = min(begin + info.w, info.z);
     const uint32_t i = a.big_list[e];
-    const uint32_t cnt = a.tile_count[i];
-    const uint32_t base = big_base[i];
-    if (base + cnt > a.cap) continue;
     const uint32_t* chunk = a.big_chunk + (size_t)e * B2C_BIG_CHUNKS;
     const uint32_t off = chunk[k];
-    const uint32_t off_end = end < info.z ? chunk[k + 1] : cnt;
+    const uint32_t off_next = chunk[min(k + 1u, (uint32_t)B2C_BIG_CHUNKS - 1u)];
+    const uint32_t cnt = a.tile_count[i];
+    const uint32_t base = big_base[i];
     const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
     const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
+    // the record is used here, so its loads share the third round trip (instead of being sunk into the
+    // tile loop's guard)
+    asm volatile("" : : "v"(p0.x), "v"(p0.y), "v"(p0.z), "v"(p0.w), "v"(p1.x), "v"(p1.w));
+    const bool fits = base + cnt <= a.cap;
+    const uint32_t begin = k * info.w, end = fits ? min(begin + info.w, info.z) : begin;
+    const uint32_t off_end = fits ? (end < info.z ? off_next : cnt) : off;
     const Sym2 conic{p0.z, p0.w, p1.x};
     const int min_x = (int)(info.x & 0xFFFFu), min_y = (int)(info.x >> 16), bw = (int)info.y;
     uint32_t written = off;
