@@ -22,7 +22,7 @@ namespace {
 
 constexpr int SORT_THREADS = 256;
 constexpr int KPT_BIG = 16;  // keys per thread of a large sort (4096-key tiles)
-constexpr int KPT_SMALL = 4;  // below BIG_SORT_MIN keys (1024-key tiles)
+constexpr int KPT_SMALL = 8;  // below BIG_SORT_MIN keys (2048-key tiles)
 constexpr uint32_t BIG_SORT_MIN = 1u << 22;
 constexpr int RADIX = 256;
 constexpr int NWAVES = SORT_THREADS / 64;
