@@ -189,7 +189,9 @@ typedef struct b2c_raster_bwd_args {
 } b2c_raster_bwd_args;
 int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stream);
 
-/* ---- loss: photometric_kernel / photometric_loss (src/gpu/loss.cu:18-195,296-315) ---- */
+/* ---- loss: photometric_kernel / photometric_loss (src/gpu/loss.cu:18-195,296-315) ----
+ * Images up to 2^28 pixels (16 P bytes of out_rgba must fit 32-bit buffer offsets); larger ones return
+ * hipErrorInvalidValue. */
 typedef struct b2c_loss_args {
   const float* pred;          /* [P] float4 out_rgba */
   const uint32_t* gt;         /* [P] packed RGBA8 */
