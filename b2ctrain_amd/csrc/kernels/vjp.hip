@@ -101,7 +101,7 @@ __device__ __forceinline__ void sh_viewdir_vjp(const float* coef, float x, float
 // The per-splat rows of v_splat (13 floats) and grad_out (11 + 3K floats) are read and written through
 // LDS by the whole workgroup, so consecutive lanes touch consecutive addresses (a lane-per-row access
 // would touch one cache line per lane per instruction).
-constexpr int VJP_BLOCK = 128;
+constexpr int VJP_BLOCK = 64;
 
 template <int DEG, bool HALF>
 __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
