@@ -4,8 +4,8 @@ One step = one training step of the hot path on one view, inputs resident in HBM
 sort + forward raster + fused L1/SSIM/alpha loss + MFMA backward + projection VJP (trainer.cpp:487-529
 order, grad_out semantics). A new random background is drawn each step (trainer.cpp:470-471).
 
-Prints ONE JSON line. value = Gfrag/s = F_sweep / (t_forward + t_backward) (BASELINE.md's definition:
-F_sweep = sum over tiles of 64 x shrunk list length). Stage times come from hipEvents recorded on the
+Prints ONE JSON line. value = Gfrag/s = F_sweep / (t_forward + t_backward), with F_sweep = the sum over
+tiles of 64 x the tile's shrunk list length (the fragments the raster sweeps). Stage times come from hipEvents recorded on the
 context's stream around each stage; ms_per_step is the wall time of the K timed steps over K, bracketed by
 stream synchronisation.
 """
@@ -134,7 +134,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the path would shard "
-              "by screen tiles or by views, see DESIGN.md)", file=sys.stderr)
+              "by screen tiles or by views)", file=sys.stderr)
         sys.exit(2)
 
     from b2ctrain_amd import _native
