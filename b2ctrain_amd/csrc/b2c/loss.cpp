@@ -18,6 +18,7 @@ void photometric_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp,
   a.loss_accum = ctx.loss_accum.ptr;
   a.partials = ctx.loss_partials.ptr;
   a.assign = lp.assign_loss ? 1 : 0;
+  a.running = lp.running_sum ? 1 : 0;
   LAUNCH_CHECK(b2c_hip_photometric(&a, stream));
 }
 

@@ -30,6 +30,7 @@ struct LossParams {
   float normal_scale = 0.f;
   float grad_scale = 1.f;             // multiplies the per-pixel gradients (not the loss value)
   bool assign_loss = false;           // store into loss_accum[0] (and clear [1]) instead of adding
+  bool running_sum = false;           // with assign_loss: also apply accumulate_loss's update in the same launch
 };
 
 // Fused L1 + SSIM (+ alpha lane): gradient into ctx.v_out, loss added to ctx.loss_accum[0] (stored, with

@@ -351,6 +351,7 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
     const b2c::RenderParams p = to_params(*ro);
     b2c::LossParams lp = to_loss(*lo);
     lp.assign_loss = true;  // the step's loss replaces loss_accum[0..1] (no separate clear)
+    lp.running_sum = true;  // and accumulate_loss's running-sum update happens in the loss's last launch
     hipStream_t s = c->stream;
     auto mark = [&](int k) {
       if (times) HIP_CHECK(hipEventRecord(c->ev[k], s));
@@ -385,7 +386,6 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
     op.grad_accumulate = (flags & B2C_GRAD_ACCUMULATE) != 0;
     op.sparse = (flags & B2C_GRAD_SPARSE) != 0;
     b2c::optimizer_step(c->ctx, m->m, op, s);
-    b2c::accumulate_loss(c->ctx, s);
     mark(6);
     if (times) {
       HIP_CHECK(hipEventSynchronize(c->ev[6]));

@@ -326,7 +326,8 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int st
 
 // Fixed-order double-precision sum of the per-workgroup partials into loss_accum[0].
 __global__ void __launch_bounds__(1024) reduce_partials_kernel(const float* __restrict__ partials, int count,
-                                                                float* __restrict__ loss_accum, int assign) {
+                                                                float* __restrict__ loss_accum, int assign,
+                                                                int running) {
   __shared__ double s_red[16];
   double acc = 0.0;
   for (int i = threadIdx.x; i < count; i += 1024) acc += (double)partials[i];
@@ -340,6 +341,10 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const float* __re
     if (assign) {
       loss_accum[0] = (float)t;
       loss_accum[1] = 0.f;
+      if (running) {  // accumulate_kernel's update
+        loss_accum[2] += loss_accum[0] + loss_accum[1];
+        loss_accum[3] += 1.f;
+      }
     } else {
       loss_accum[0] = (float)((double)loss_accum[0] + t);
     }
@@ -404,6 +409,7 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   if (a->W <= 0 || a->H <= 0) return 0;
   if ((uint64_t)a->W * (uint64_t)a->H * 16u > 0xFFFFFFFFull) return (int)hipErrorInvalidValue;  // 32-bit buffer offsets
   if (a->assign && !a->partials) return (int)hipErrorInvalidValue;  // float atomics can only add
+  if (a->running && !a->assign) return (int)hipErrorInvalidValue;    // the running sum needs the final value
   // the kernel's constant weights must equal the double-precision Gaussian rounded to float
   static const bool weights_ok = [] {
     double w[11], sum = 0.0;
@@ -431,7 +437,8 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
     case 57: photometric_kernel<57><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
     default: photometric_kernel<79><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
   }
-  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum, a->assign);
+  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum, a->assign,
+                                                                 a->running);
   return (int)hipGetLastError();
 }
 

@@ -206,6 +206,9 @@ typedef struct b2c_loss_args {
                                  fixed order in double (deterministic); NULL = float atomics as the reference */
   int assign;                 /* with partials: loss_accum[0] = loss and loss_accum[1] = 0 (the second loss
                                  term, absent from this build) instead of adding, so the caller need not clear */
+  int running;                /* with assign: also loss_accum[2] += loss_accum[0] + loss_accum[1] and
+                                 loss_accum[3] += 1, the accumulate_kernel update (loss.cu:317,324), in the same
+                                 launch */
 } b2c_loss_args;
 size_t b2c_loss_partials(int W, int H);
 int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream);

@@ -25,3 +25,27 @@ def test_loss_each_strip_height(sh, monkeypatch):
         check_loss(r, sc, r.read("out_rgba"), 3.0 * sc.W * sc.H, bg)
     finally:
         r.close()
+
+
+def test_train_step_keeps_running_loss_sum():
+    """The training step keeps the reference's running loss sum (accumulate_kernel, loss.cu:317,324:
+    loss_accum[2] += loss_accum[0] + loss_accum[1], loss_accum[3] += 1), applied in the loss's last launch
+    instead of a kernel of its own: after two steps [2] is the float32 sum of the two step losses and [3]
+    is 2."""
+    import numpy as np
+    sc = S.config3(n=20_000)
+    sc.bg = (0.4, 0.3, 0.2)
+    emit("train step running loss sum")
+    r = _native.Renderer(sc)
+    try:
+        r.zero("loss_accum")
+        r.step(bg=sc.bg)
+        a1 = r.read("loss_accum").copy()
+        r.step(bg=sc.bg)
+        a2 = r.read("loss_accum").copy()
+    finally:
+        r.close()
+    assert a1[0] > 0 and a1[1] == 0 and a2[1] == 0
+    assert a1[3] == 1 and a2[3] == 2
+    assert a1[2] == np.float32(0) + (a1[0] + a1[1])
+    assert a2[2] == a1[2] + (a2[0] + a2[1])
