@@ -204,7 +204,7 @@ def main():
         "avg_launch_ms": round(mean["raster_bwd_ms"], 4),
         "mfma": {"achieved": round(mfma_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                  "frac": round(mfma_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
-        "note": ("VALU-issue bound (per-fragment replay; rocprofv3 SQ_INSTS_VALU gives 85% of the VALU issue "
+        "note": ("VALU-issue bound (per-fragment replay; rocprofv3 SQ_INSTS_VALU gives 91% of the VALU issue "
                  "slots, profiles/raster_step_cfg3_counters.md); HBM and MFMA fractions are low by design"),
     }
     # HBM rooflines of the stages the north star prices: projection, binning/sort, loss
