@@ -68,7 +68,8 @@ EXPORTS = [
     "b2c_hip_depth_keys",
     "b2c_scan_temp_bytes", "b2c_hip_scan_counts", "b2c_hip_emit", "b2c_hip_tile_ranges", "b2c_hip_raster_fwd",
     "b2c_hip_raster_bwd", "b2c_hip_photometric", "b2c_loss_partials", "b2c_hip_accumulate_loss", "b2c_hip_vjp",
-    "b2c_hip_fill_u32",
+    "b2c_hip_fill_u32", "b2c_hip_model_scatter", "b2c_hip_model_gather", "b2c_hip_planar_regrow",
+    "b2c_hip_model_set_floor",
 ]
 
 _lib = None
@@ -188,7 +189,9 @@ class Renderer:
     def upload(self, scene, floor=None):
         n = scene.n
         arrs = [np.ascontiguousarray(a, np.float32) for a in (scene.pos_op[:, :3], scene.lscale[:, :3], scene.quat,
-                                                              scene.pos_op[:, 3], scene.sh.reshape(n, -1))]
+                                                              scene.pos_op[:, 3], scene.sh.reshape(n, 3 * scene.K))]
+        if floor is None and scene.lscale[:, 3].any():  # the scene's own Mip-Splatting floor
+            floor = scene.lscale[:, 3]
         fl = None if floor is None else np.ascontiguousarray(floor, np.float32)
         check(self.L.b2c_model_upload(self.model, n, scene.degree, int(scene.sh_fp16), *[_ptr(a) for a in arrs], _ptr(fl)),
               "model_upload")

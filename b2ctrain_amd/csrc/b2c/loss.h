@@ -5,36 +5,42 @@
 
 namespace b2c {
 
-// A training view resident on the GPU (loss.h:7-18).
+// ViewGPU (loss.h:7-18): device pointers of one training image. The field set is the reference's; this
+// build reads rgba and weights.
 struct ViewGPU {
-  const uint32_t* rgba = nullptr;     // packed RGBA8 (premultiplied for transparent views)
-  const uint32_t* normals = nullptr;
-  const uint8_t* weights = nullptr;   // per-pixel loss weight (w / 255) or nullptr
-  const uint8_t* labels = nullptr;
+  const uint32_t* rgba = nullptr;     // target pixels, r | g << 8 | b << 16 | a << 24; colour already scaled by a
+                                      // when the view carries transparency
+  const uint32_t* normals = nullptr;  // feature-lane target (not read here)
+  const uint8_t* weights = nullptr;   // per-pixel weight byte, weight = byte / 255 (times LossParams::scale);
+                                      // nullptr: weight 1
+  const uint8_t* labels = nullptr;    // evidence-pass input (not read here)
   int W = 0, H = 0;
   bool has_alpha = false, masked = false;
   float alpha_coverage = 1.f;
   float normal_count = 0.f;
-  const float2* warp = nullptr;
+  const float2* warp = nullptr;       // render-side alignment field (not supported here)
   int warp_w = 0, warp_h = 0;
 };
 
+// LossParams (loss.h:20-30), plus two flags of this build for the fused training step.
 struct LossParams {
-  float l1_w = 0.8f, ssim_w = -0.2f;  // brush: (1 - ssim_weight), -ssim_weight
-  float bg[3] = {0, 0, 0};
-  bool composite = false;             // gt_eff = gt + (1 - gt.a) * bg
-  bool mask = false;                  // multiply the loss map by gt.a
-  bool alpha_lane = false;            // add match_alpha_weight * |pred.a - gt.a|
+  float l1_w = 0.8f, ssim_w = -0.2f;  // weights of |p - g| and of SSIM; the trainer passes 1 - w and -w
+  float bg[3] = {0, 0, 0};            // background the target is composited over when `composite`
+  bool composite = false;             // target colour becomes g + (1 - g.a) bg
+  bool mask = false;                  // each pixel's loss is multiplied by the target's alpha
+  bool alpha_lane = false;            // adds match_alpha_weight |p.a - g.a| (not masked)
   float match_alpha_weight = 0.1f;
-  float scale = 1.f;                  // multiplier on the whole photometric loss
-  float normal_scale = 0.f;
-  float grad_scale = 1.f;             // multiplies the per-pixel gradients (not the loss value)
-  bool assign_loss = false;           // store into loss_accum[0] (and clear [1]) instead of adding
-  bool running_sum = false;           // with assign_loss: also apply accumulate_loss's update in the same launch
+  float scale = 1.f;                  // factor on the photometric terms, applied where the weight is
+  float normal_scale = 0.f;           // feature-lane loss (not supported here)
+  float grad_scale = 1.f;             // factor on v_out only; the loss value is unscaled
+  bool assign_loss = false;           // loss_accum[0] = this loss and loss_accum[1] = 0, instead of adding
+  bool running_sum = false;           // with assign_loss: loss_accum[2] = loss_accum[0] + loss_accum[1] and
+                                      // loss_accum[3] = 1 in the same launch, which is what the trainer's
+                                      // per-step clear of [0..3] followed by accumulate_loss leaves
 };
 
-// Fused L1 + SSIM (+ alpha lane): gradient into ctx.v_out, loss added to ctx.loss_accum[0] (stored, with
-// loss_accum[1] cleared, when lp.assign_loss).
+// Fused L1 + SSIM (+ alpha lane): per-pixel gradient into ctx.v_out, the loss added to ctx.loss_accum[0]
+// (see assign_loss / running_sum).
 void photometric_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp, hipStream_t stream);
 void normal_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp, hipStream_t stream);
 // loss_accum[2] += loss_accum[0] + loss_accum[1]; loss_accum[3] += 1.

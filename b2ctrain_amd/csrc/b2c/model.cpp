@@ -1,13 +1,14 @@
-// Model upload / download / growth (replaces src/model.cu:8-118, the parts the rasterizer path needs).
+// Model storage (replaces the upload / download / growth parts of src/model.cu:8-118). The host side only
+// moves whole arrays: an upload copies the cloud's five field arrays into one device staging block and a
+// scatter kernel writes the float4 fields and the planar SH lanes (fp16 rounding on the device); a download
+// is the inverse gather; growth re-lays the planar lanes out with a kernel (kernels/model_io.hip).
 #include "model.h"
 
-#include <cmath>
-#include <cstring>
-#include <type_traits>
+#include <algorithm>
 
 namespace b2c {
 
-void SplatCloud::resize(size_t count, int degree) {
+void SplatCloud::resize(size_t count, int degree) {  // src/ply.cpp:15-22: zeros, identity rotations
   n = count;
   sh_degree = degree;
   pos.assign(n * 3, 0.f);
@@ -18,119 +19,121 @@ void SplatCloud::resize(size_t count, int degree) {
   for (size_t i = 0; i < n; i++) quat[i * 4] = 1.f;
 }
 
-uint16_t float_to_half_rne(float f) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+uint16_t float_to_half_rne(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+float half_to_float(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+
+namespace {
+
+// A cloud's field arrays back to back in one device block: pos, log_scale, quat, opacity, sh, floor.
+struct CloudStage {
+  DevBuf<float> block;
+  b2c_cloud_dev fields{};
+
+  CloudStage(size_t n, int K, bool with_floor) {
+    const size_t o_ls = 3 * n, o_q = o_ls + 3 * n, o_op = o_q + 4 * n, o_sh = o_op + n, o_fl = o_sh + 3 * (size_t)K * n;
+    block.reserve(std::max<size_t>(o_fl + (with_floor ? n : 0), 1));
+    float* b = block.ptr;
+    fields = b2c_cloud_dev{b, b + o_ls, b + o_q, b + o_op, b + o_sh, with_floor ? b + o_fl : nullptr};
+  }
+};
+
+template <typename T>
+void to_device(float* dst, const std::vector<T>& src, hipStream_t s) {
+  if (!src.empty()) HIP_CHECK(hipMemcpyAsync(dst, src.data(), src.size() * sizeof(T), hipMemcpyHostToDevice, s));
 }
 
-float half_to_float(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+template <typename T>
+void to_host(std::vector<T>& dst, const float* src, hipStream_t s) {
+  if (!dst.empty()) HIP_CHECK(hipMemcpyAsync(dst.data(), src, dst.size() * sizeof(T), hipMemcpyDeviceToHost, s));
+}
+
+// A planar [lanes][cap] array moved to a larger stride by the re-layout kernel (new slots zero).
+template <typename T>
+void regrow_planar(DevBuf<T>& buf, int lanes, int n, int old_cap, int new_cap, hipStream_t s) {
+  if (lanes <= 0) return;
+  DevBuf<T> wider;
+  wider.reserve((size_t)lanes * new_cap);
+  LAUNCH_CHECK(b2c_hip_planar_regrow(buf.ptr, wider.ptr, (int)sizeof(T), lanes, n, old_cap, new_cap, s));
+  HIP_CHECK(hipStreamSynchronize(s));  // the old array is freed on assignment
+  buf = std::move(wider);
+}
+
+}  // namespace
+
+b2c_model_dev Model::layout() const {
+  b2c_model_dev d{};
+  d.n = n; d.cap = cap; d.sh_lanes = 3 * K();
+  d.pos_op = reinterpret_cast<float*>(pos_op.ptr);
+  d.quat = reinterpret_cast<float*>(quat.ptr);
+  d.lscale = reinterpret_cast<float*>(lscale.ptr);
+  d.sh_dc = sh_dc.ptr;
+  d.sh_hi32 = sh_fp16 ? nullptr : sh_hi32.ptr;
+  d.sh_hi16 = sh_fp16 ? sh_hi.ptr : nullptr;
+  return d;
+}
 
 void Model::reserve(int want, hipStream_t stream) {
   if (want <= cap) return;
-  int ncap = cap ? cap : 1024;
-  while (ncap < want) ncap *= 2;
-  const int hi_lanes = (K() - 1) * 3;
-  auto grow_planar = [&](auto& b, int lanes) {
-    using T = std::remove_reference_t<decltype(*b.ptr)>;
-    if (lanes == 0) return;
-    DevBuf<T> nb;
-    nb.reserve((size_t)ncap * lanes);
-    nb.zero(stream);
-    if (b.ptr && n > 0)
-      HIP_CHECK(hipMemcpy2DAsync(nb.ptr, (size_t)ncap * sizeof(T), b.ptr, (size_t)cap * sizeof(T), (size_t)n * sizeof(T),
-                                 lanes, hipMemcpyDeviceToDevice, stream));
-    HIP_CHECK(hipStreamSynchronize(stream));
-    b = std::move(nb);
-  };
-  pos_op.reserve(ncap, true, stream);
-  quat.reserve(ncap, true, stream);
-  lscale.reserve(ncap, true, stream);
-  grow_planar(sh_dc, 3);
-  if (sh_fp16) grow_planar(sh_hi, hi_lanes); else grow_planar(sh_hi32, hi_lanes);
-  for (DevBuf<float>* b : {&refine_norm, &max_screen, &vis_count, &vis_weight}) {
-    b->reserve((size_t)ncap, true, stream);
-    LAUNCH_CHECK(b2c_hip_fill_u32(reinterpret_cast<uint32_t*>(b->ptr + cap), 0u, (size_t)(ncap - cap), stream));
+  int grown = std::max(cap, 1024);
+  while (grown < want) grown *= 2;
+  for (DevBuf<float4>* f : {&pos_op, &quat, &lscale}) f->reserve((size_t)grown, true, stream);
+  const int bands = 3 * (K() - 1);
+  regrow_planar(sh_dc, 3, n, cap, grown, stream);
+  if (sh_fp16) regrow_planar(sh_hi, bands, n, cap, grown, stream);
+  else regrow_planar(sh_hi32, bands, n, cap, grown, stream);
+  for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight}) {
+    st->reserve((size_t)grown, true, stream);
+    LAUNCH_CHECK(b2c_hip_fill_u32(reinterpret_cast<uint32_t*>(st->ptr + cap), 0u, (size_t)(grown - cap), stream));
   }
-  cap = ncap;
+  cap = grown;
 }
 
-void Model::upload(const SplatCloud& c, hipStream_t stream) {
+void Model::upload(const SplatCloud& c, hipStream_t stream, const float* floor) {
   degree = c.sh_degree;
   n = (int)c.n;
   cap = 0;
-  pos_op.free(); quat.free(); lscale.free(); sh_dc.free(); sh_hi.free(); sh_hi32.free();
-  refine_norm.free(); max_screen.free(); vis_count.free(); vis_weight.free();
-  reserve(n > 0 ? n : 1, stream);
-  std::vector<float4> p(n), q(n), s(n);
-  for (int i = 0; i < n; i++) {
-    p[i] = make_float4(c.pos[i * 3], c.pos[i * 3 + 1], c.pos[i * 3 + 2], c.opacity[i]);
-    q[i] = make_float4(c.quat[i * 4], c.quat[i * 4 + 1], c.quat[i * 4 + 2], c.quat[i * 4 + 3]);
-    s[i] = make_float4(c.log_scale[i * 3], c.log_scale[i * 3 + 1], c.log_scale[i * 3 + 2], 0.f);
-  }
-  if (n) {
-    HIP_CHECK(hipMemcpyAsync(pos_op.ptr, p.data(), n * sizeof(float4), hipMemcpyHostToDevice, stream));
-    HIP_CHECK(hipMemcpyAsync(quat.ptr, q.data(), n * sizeof(float4), hipMemcpyHostToDevice, stream));
-    HIP_CHECK(hipMemcpyAsync(lscale.ptr, s.data(), n * sizeof(float4), hipMemcpyHostToDevice, stream));
-  }
-  const int K = this->K(), hi = (K - 1) * 3;
-  std::vector<float> dc((size_t)cap * 3, 0.f), rest((size_t)cap * hi, 0.f);
-  for (int i = 0; i < n; i++) {
-    for (int k = 0; k < 3; k++) dc[(size_t)k * cap + i] = c.sh[(size_t)i * K * 3 + k];
-    for (int k = 0; k < hi; k++) rest[(size_t)k * cap + i] = c.sh[(size_t)i * K * 3 + 3 + k];
-  }
-  HIP_CHECK(hipMemcpyAsync(sh_dc.ptr, dc.data(), dc.size() * sizeof(float), hipMemcpyHostToDevice, stream));
-  if (hi > 0) {
-    if (sh_fp16) {
-      std::vector<uint16_t> h(rest.size());
-      for (size_t j = 0; j < rest.size(); j++) h[j] = float_to_half_rne(rest[j]);
-      HIP_CHECK(hipMemcpyAsync(sh_hi.ptr, h.data(), h.size() * sizeof(uint16_t), hipMemcpyHostToDevice, stream));
-      HIP_CHECK(hipStreamSynchronize(stream));
-    } else {
-      HIP_CHECK(hipMemcpyAsync(sh_hi32.ptr, rest.data(), rest.size() * sizeof(float), hipMemcpyHostToDevice, stream));
-    }
-  }
-  HIP_CHECK(hipStreamSynchronize(stream));
+  for (DevBuf<float4>* f : {&pos_op, &quat, &lscale}) f->free();
+  sh_dc.free(); sh_hi.free(); sh_hi32.free();
+  for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight}) st->free();
+  reserve(std::max(n, 1), stream);
+  CloudStage stage(c.n, K(), floor != nullptr);
+  to_device(stage.fields.pos, c.pos, stream);
+  to_device(stage.fields.log_scale, c.log_scale, stream);
+  to_device(stage.fields.quat, c.quat, stream);
+  to_device(stage.fields.opacity, c.opacity, stream);
+  to_device(stage.fields.sh, c.sh, stream);
+  if (floor && n) HIP_CHECK(hipMemcpyAsync(stage.fields.floor_, floor, n * sizeof(float), hipMemcpyHostToDevice, stream));
+  const b2c_model_dev dst = layout();
+  LAUNCH_CHECK(b2c_hip_model_scatter(&stage.fields, &dst, stream));
   zero_stats(stream);
-  HIP_CHECK(hipStreamSynchronize(stream));
+  HIP_CHECK(hipStreamSynchronize(stream));  // the stage and the caller's arrays may go away now
 }
 
 SplatCloud Model::download(hipStream_t stream) const {
   SplatCloud c;
   c.resize((size_t)n, degree);
-  auto p = pos_op.download(n, stream);
-  auto q = quat.download(n, stream);
-  auto s = lscale.download(n, stream);
-  const int K = this->K(), hi = (K - 1) * 3;
-  auto dc = sh_dc.download((size_t)cap * 3, stream);
-  std::vector<float> rest;
-  if (hi > 0) {
-    if (sh_fp16) {
-      auto h = sh_hi.download((size_t)cap * hi, stream);
-      rest.resize(h.size());
-      for (size_t j = 0; j < h.size(); j++) rest[j] = half_to_float(h[j]);
-    } else {
-      rest = sh_hi32.download((size_t)cap * hi, stream);
-    }
-  }
-  for (int i = 0; i < n; i++) {
-    c.pos[i * 3] = p[i].x; c.pos[i * 3 + 1] = p[i].y; c.pos[i * 3 + 2] = p[i].z; c.opacity[i] = p[i].w;
-    c.quat[i * 4] = q[i].x; c.quat[i * 4 + 1] = q[i].y; c.quat[i * 4 + 2] = q[i].z; c.quat[i * 4 + 3] = q[i].w;
-    c.log_scale[i * 3] = s[i].x; c.log_scale[i * 3 + 1] = s[i].y; c.log_scale[i * 3 + 2] = s[i].z;
-    for (int k = 0; k < 3; k++) c.sh[(size_t)i * K * 3 + k] = dc[(size_t)k * cap + i];
-    for (int k = 0; k < hi; k++) c.sh[(size_t)i * K * 3 + 3 + k] = rest[(size_t)k * cap + i];
-  }
+  CloudStage stage(c.n, K(), false);
+  const b2c_model_dev src = layout();
+  LAUNCH_CHECK(b2c_hip_model_gather(&src, &stage.fields, stream));
+  to_host(c.pos, stage.fields.pos, stream);
+  to_host(c.log_scale, stage.fields.log_scale, stream);
+  to_host(c.quat, stage.fields.quat, stream);
+  to_host(c.opacity, stage.fields.opacity, stream);
+  to_host(c.sh, stage.fields.sh, stream);
+  HIP_CHECK(hipStreamSynchronize(stream));
   return c;
 }
 
 void Model::set_floor(const std::vector<float>& f, hipStream_t stream) {
   if ((int)f.size() != n) throw std::runtime_error("set_floor: expected one floor value per splat");
-  auto s = lscale.download(n, stream);
-  for (int i = 0; i < n; i++) s[i].w = f[i];
-  if (n) HIP_CHECK(hipMemcpyAsync(lscale.ptr, s.data(), n * sizeof(float4), hipMemcpyHostToDevice, stream));
+  DevBuf<float> staged;
+  staged.upload(f, stream);
+  LAUNCH_CHECK(b2c_hip_model_set_floor(reinterpret_cast<float*>(lscale.ptr), staged.ptr, n, stream));
   HIP_CHECK(hipStreamSynchronize(stream));
 }
 
 void Model::zero_stats(hipStream_t stream) {
-  refine_norm.zero(stream); max_screen.zero(stream); vis_count.zero(stream); vis_weight.zero(stream);
+  for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight}) st->zero(stream);
 }
 
 }  // namespace b2c

@@ -1,5 +1,6 @@
-// Splat model and its host cloud (replaces src/model.h:8-40 and the SplatCloud of src/ply.h:10-42, path
-// fields only). Layout is the reference's, unchanged, because refine / cage / evidence code reads it:
+// Splat model and its host cloud (replaces src/model.h:8-40 and the SplatCloud of src/ply.h:10-42, the
+// fields the rasterizer uses). The device layout is the reference's, unchanged, because refine / cage /
+// evidence code reads it:
 //   pos_op : float4 (mean x, y, z, opacity logit)
 //   quat   : float4 (w, x, y, z), unnormalised
 //   lscale : float4 (log sx, log sy, log sz, floor f), f frozen (0 = none)
@@ -52,14 +53,18 @@ struct Model {
     return b;
   }
   int K() const { return sh_coeffs_for_degree(degree); }
-  // Ensure capacity for `want` splats (doubling from 1024), preserving contents (model.cu:8-42).
+  // Capacity for `want` splats, doubling from 1024 (the reference's growth policy, model.cu:8-42); the
+  // first n splats keep their values, planar slots past n read as zero.
   void reserve(int want, hipStream_t stream = nullptr);
-  // Upload a cloud (model.cu:44-80): lscale.w = 0, fp16 bands rounded to nearest even, stats zeroed.
-  void upload(const SplatCloud& c, hipStream_t stream = nullptr);
+  // Replace the model by a cloud (model.cu:44-80): bands rounded to nearest even when stored as fp16,
+  // statistics zeroed, lscale.w = floor[i] (0 without a floor, as the reference uploads).
+  void upload(const SplatCloud& c, hipStream_t stream = nullptr, const float* floor = nullptr);
   SplatCloud download(hipStream_t stream = nullptr) const;
   // Set the frozen per-splat floor f (lscale.w); not part of the reference's upload.
   void set_floor(const std::vector<float>& f, hipStream_t stream = nullptr);
   void zero_stats(hipStream_t stream = nullptr);
+  // The device layout as the launcher layer takes it.
+  b2c_model_dev layout() const;
 };
 
 // IEEE binary16 encode (round to nearest even) / decode on the host.

@@ -161,9 +161,10 @@ void emit_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
 }  // namespace
 
 void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
-  if (m.n == 0) {
+  if (m.n == 0) {  // no lists: every range and list end is empty, so the raster kernels touch no row
     ctx.num_isect = 0;
     ctx.tile_ranges.zero(stream);
+    ctx.tile_end.zero(stream, (size_t)ctx.n_tiles + 1);
     return;
   }
   const int n = m.n;

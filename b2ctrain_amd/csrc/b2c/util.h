@@ -1,5 +1,6 @@
-// Host utilities of the drop-in API (replaces src/gpu/util.cuh:1-57 host parts): error checking, owning
-// device buffers, pinned host buffers. Device math lives in kernels/device_math.h.
+// Host utilities of the drop-in API: error checking, owning device buffers and pinned host buffers. The
+// reference keeps these in src/gpu/util.cuh:1-65; the buffer types keep the member names its callers use
+// (ptr, count, reserve, zero, upload, download, bytes). Device math lives in kernels/device_math.h.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -13,15 +14,16 @@
 
 namespace b2c {
 
-#define HIP_CHECK(expr)                                                                                     \
-  do {                                                                                                      \
-    hipError_t _e = (expr);                                                                                 \
-    if (_e != hipSuccess)                                                                                   \
-      throw std::runtime_error(std::string("HIP error ") + hipGetErrorString(_e) + " at " + __FILE__ + ":" + \
-                               std::to_string(__LINE__));                                                   \
+[[noreturn]] inline void hip_fail(hipError_t e, const char* file, int line) {
+  throw std::runtime_error(std::string("HIP error ") + hipGetErrorString(e) + " at " + file + ":" + std::to_string(line));
+}
+#define HIP_CHECK(expr)                                   \
+  do {                                                    \
+    const hipError_t b2c_rc_ = (expr);                    \
+    if (b2c_rc_ != hipSuccess) ::b2c::hip_fail(b2c_rc_, __FILE__, __LINE__); \
   } while (0)
-// Launchers return hipError_t as int.
-#define LAUNCH_CHECK(expr) HIP_CHECK((hipError_t)(expr))
+// The launcher layer returns hipError_t as int.
+#define LAUNCH_CHECK(expr) HIP_CHECK(static_cast<hipError_t>(expr))
 
 constexpr int TILE_W = 16;   // loss tile (util.cuh:17)
 constexpr int TILE_PX = TILE_W * TILE_W;
@@ -32,84 +34,123 @@ constexpr uint32_t GRAD_LANES = 13;
 
 inline int div_up(size_t a, int b) { return (int)((a + b - 1) / b); }
 
-// Owning device buffer (util.cuh:26-57 semantics): move-only, reserve grows (contents discarded unless
-// keep), freed in the destructor.
+// Untyped device allocation. Growth allocates the new block first, copies the old contents on the stream
+// when asked to, and frees the old block only after the stream has drained (a queued kernel may still
+// read it). It never shrinks.
+struct DeviceBlock {
+  void* base = nullptr;
+  size_t size = 0;  // bytes
+
+  void release() noexcept {
+    if (base) (void)hipFree(base);
+    base = nullptr;
+    size = 0;
+  }
+  void grow_to(size_t want, bool preserve, hipStream_t stream) {
+    if (want <= size) return;
+    void* fresh = nullptr;
+    HIP_CHECK(hipMalloc(&fresh, want));
+    if (base) {
+      if (preserve && size) HIP_CHECK(hipMemcpyAsync(fresh, base, size, hipMemcpyDeviceToDevice, stream));
+      HIP_CHECK(hipStreamSynchronize(stream));
+      (void)hipFree(base);
+    }
+    base = fresh;
+    size = want;
+  }
+  // Zero `bytes` from the start with the fill kernel (capturable; a memset node is not).
+  void clear(size_t bytes, hipStream_t stream) const {
+    if (!base || !bytes) return;
+    if (bytes % 4) HIP_CHECK(hipMemsetAsync(base, 0, bytes, stream));
+    else LAUNCH_CHECK(b2c_hip_fill_u32(static_cast<uint32_t*>(base), 0u, bytes / 4, stream));
+  }
+};
+
+// Typed, move-only owner of a device array (the reference's DevBuf semantics: reserve grows and discards
+// the contents unless `keep`, the destructor frees).
 template <typename T>
 struct DevBuf {
   T* ptr = nullptr;
   size_t count = 0;
+
   DevBuf() = default;
   DevBuf(const DevBuf&) = delete;
   DevBuf& operator=(const DevBuf&) = delete;
-  DevBuf(DevBuf&& o) noexcept : ptr(o.ptr), count(o.count) { o.ptr = nullptr; o.count = 0; }
+  DevBuf(DevBuf&& o) noexcept { take(o); }
   DevBuf& operator=(DevBuf&& o) noexcept {
-    free();
-    ptr = o.ptr; count = o.count;
-    o.ptr = nullptr; o.count = 0;
+    if (this != &o) {
+      free();
+      take(o);
+    }
     return *this;
   }
   ~DevBuf() { free(); }
-  void free() {
-    if (ptr) (void)hipFree(ptr);
+
+  void free() noexcept {
+    DeviceBlock b = block();
+    b.release();
     ptr = nullptr;
     count = 0;
   }
   void reserve(size_t n, bool keep = false, hipStream_t stream = nullptr) {
     if (n <= count) return;
-    T* np = nullptr;
-    HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&np), n * sizeof(T)));
-    if (keep && ptr && count) HIP_CHECK(hipMemcpyAsync(np, ptr, count * sizeof(T), hipMemcpyDeviceToDevice, stream));
-    if (ptr) {
-      HIP_CHECK(hipStreamSynchronize(stream));
-      (void)hipFree(ptr);
-    }
-    ptr = np;
+    DeviceBlock b = block();
+    b.grow_to(n * sizeof(T), keep, stream);
+    ptr = static_cast<T*>(b.base);
     count = n;
   }
-  // Zero the first n entries with a fill kernel (safe inside captured graphs, unlike a memset node).
-  void zero(hipStream_t stream = nullptr, size_t n = (size_t)-1) {
-    if (!ptr) return;
-    const size_t bytes = (n == (size_t)-1 ? count : n) * sizeof(T);
-    if (bytes % 4 == 0)
-      LAUNCH_CHECK(b2c_hip_fill_u32(reinterpret_cast<uint32_t*>(ptr), 0u, bytes / 4, stream));
-    else
-      HIP_CHECK(hipMemsetAsync(ptr, 0, bytes, stream));
-  }
+  void zero(hipStream_t stream = nullptr, size_t n = (size_t)-1) { block().clear((n == (size_t)-1 ? count : n) * sizeof(T), stream); }
   void upload(const T* src, size_t n, hipStream_t stream = nullptr) {
     reserve(n);
-    HIP_CHECK(hipMemcpyAsync(ptr, src, n * sizeof(T), hipMemcpyHostToDevice, stream));
+    if (n) HIP_CHECK(hipMemcpyAsync(ptr, src, n * sizeof(T), hipMemcpyHostToDevice, stream));
   }
   void upload(const std::vector<T>& v, hipStream_t stream = nullptr) { upload(v.data(), v.size(), stream); }
   std::vector<T> download(size_t n = (size_t)-1, hipStream_t stream = nullptr) const {
-    if (n == (size_t)-1) n = count;
-    std::vector<T> v(n);
-    if (n) {
-      HIP_CHECK(hipMemcpyAsync(v.data(), ptr, n * sizeof(T), hipMemcpyDeviceToHost, stream));
+    std::vector<T> host(n == (size_t)-1 ? count : n);
+    if (!host.empty()) {
+      HIP_CHECK(hipMemcpyAsync(host.data(), ptr, host.size() * sizeof(T), hipMemcpyDeviceToHost, stream));
       HIP_CHECK(hipStreamSynchronize(stream));
     }
-    return v;
+    return host;
   }
   size_t bytes() const { return count * sizeof(T); }
   operator T*() const { return ptr; }
+
+ private:
+  DeviceBlock block() const { return DeviceBlock{ptr, count * sizeof(T)}; }
+  void take(DevBuf& o) noexcept {
+    ptr = o.ptr;
+    count = o.count;
+    o.ptr = nullptr;
+    o.count = 0;
+  }
 };
 
-// Pinned host buffer for readbacks (util.cuh:59-65).
+// Pinned (page-locked) host array for device-to-host readbacks; grows, never shrinks.
 template <typename T>
 struct PinnedBuf {
   T* ptr = nullptr;
   size_t count = 0;
+
   PinnedBuf() = default;
   PinnedBuf(const PinnedBuf&) = delete;
   PinnedBuf& operator=(const PinnedBuf&) = delete;
+  ~PinnedBuf() { drop(); }
+
   void reserve(size_t n) {
     if (n <= count) return;
-    if (ptr) (void)hipHostFree(ptr);
-    ptr = nullptr;
-    HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&ptr), n * sizeof(T), hipHostMallocDefault));
+    drop();
+    void* p = nullptr;
+    HIP_CHECK(hipHostMalloc(&p, n * sizeof(T), hipHostMallocDefault));
+    ptr = static_cast<T*>(p);
     count = n;
   }
-  ~PinnedBuf() {
+
+ private:
+  void drop() noexcept {
     if (ptr) (void)hipHostFree(ptr);
+    ptr = nullptr;
+    count = 0;
   }
 };
 

@@ -152,8 +152,7 @@ int b2c_model_upload(b2c_model* m, int n, int degree, int sh_fp16, const float* 
     std::memcpy(c.opacity.data(), opacity, sizeof(float) * n);
     std::memcpy(c.sh.data(), sh, sizeof(float) * 3 * (size_t)c.K() * n);
     m->m.sh_fp16 = sh_fp16 != 0;
-    m->m.upload(c);
-    if (floor_) m->m.set_floor(std::vector<float>(floor_, floor_ + n));
+    m->m.upload(c, nullptr, floor_);
   });
 }
 
@@ -351,7 +350,7 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
     const b2c::RenderParams p = to_params(*ro);
     b2c::LossParams lp = to_loss(*lo);
     lp.assign_loss = true;  // the step's loss replaces loss_accum[0..1] (no separate clear)
-    lp.running_sum = true;  // and accumulate_loss's running-sum update happens in the loss's last launch
+    lp.running_sum = true;  // and [2..3] become what the trainer's per-step clear + accumulate_loss leave
     hipStream_t s = c->stream;
     auto mark = [&](int k) {
       if (times) HIP_CHECK(hipEventRecord(c->ev[k], s));

@@ -134,27 +134,46 @@ __device__ __forceinline__ void extent_from_conic(Sym2 conic, float power, float
   ey = sqrtf(2.f * power * conic.c00 * inv_detc);
 }
 
-// Real SH basis in Sloan order up to degree 4 (splat_math.cuh:122-145) into b[0 .. (deg+1)^2).
-template <int DEG>
-__device__ __forceinline__ void sh_basis(float vx, float vy, float vz, float* b) {
+// Forward-mode derivative along the three components of a direction: value v and partials (x, y, z).
+// sh_basis instantiated on it yields each basis function's gradient with its value, which the projection
+// VJP contracts into d(colour)/d(view direction).
+struct Dual3 {
+  float v, x, y, z;
+};
+__device__ __forceinline__ Dual3 operator+(Dual3 a, Dual3 b) { return {a.v + b.v, a.x + b.x, a.y + b.y, a.z + b.z}; }
+__device__ __forceinline__ Dual3 operator-(Dual3 a, Dual3 b) { return {a.v - b.v, a.x - b.x, a.y - b.y, a.z - b.z}; }
+__device__ __forceinline__ Dual3 operator+(Dual3 a, float k) { return {a.v + k, a.x, a.y, a.z}; }
+__device__ __forceinline__ Dual3 operator-(Dual3 a, float k) { return {a.v - k, a.x, a.y, a.z}; }
+__device__ __forceinline__ Dual3 operator*(float k, Dual3 a) { return {k * a.v, k * a.x, k * a.y, k * a.z}; }
+__device__ __forceinline__ Dual3 operator*(Dual3 a, Dual3 b) {
+  return {a.v * b.v, a.v * b.x + a.x * b.v, a.v * b.y + a.y * b.v, a.v * b.z + a.z * b.v};
+}
+
+// Real SH basis in Sloan order up to degree 4 (the constants and recurrences of splat_math.cuh:122-145)
+// into b[0 .. (deg+1)^2). T = float gives the values; T = Dual3 the values and their gradients.
+template <int DEG, typename T>
+__device__ __forceinline__ void sh_basis(T vx, T vy, T vz, T* b) {
 #pragma clang fp contract(off)
-  b[0] = SH_C0;
+  b[0] = T{} + SH_C0;
   if constexpr (DEG >= 1) {
     const float f0a = 0.4886025f;
     b[1] = -f0a * vy; b[2] = f0a * vz; b[3] = -f0a * vx;
     if constexpr (DEG >= 2) {
-      float z2 = vz * vz, f0b = -1.0925485f * vz, f1a = 0.54627424f;
-      float fc1 = vx * vx - vy * vy, fs1 = 2.f * vx * vy;
+      T z2 = vz * vz, f0b = -1.0925485f * vz;
+      const float f1a = 0.54627424f;
+      T fc1 = vx * vx - vy * vy, fs1 = 2.f * vx * vy;
       b[4] = f1a * fs1; b[5] = f0b * vy; b[6] = 0.9461747f * z2 - 0.31539157f; b[7] = f0b * vx; b[8] = f1a * fc1;
       if constexpr (DEG >= 3) {
-        float f0c = -2.285229f * z2 + 0.4570458f, f1b = 1.4453057f * vz, f2a = -0.5900436f;
-        float fc2 = vx * fc1 - vy * fs1, fs2 = vx * fs1 + vy * fc1;
+        T f0c = -2.285229f * z2 + 0.4570458f, f1b = 1.4453057f * vz;
+        const float f2a = -0.5900436f;
+        T fc2 = vx * fc1 - vy * fs1, fs2 = vx * fs1 + vy * fc1;
         b[9] = f2a * fs2; b[10] = f1b * fs1; b[11] = f0c * vy; b[12] = vz * (1.8658817f * z2 - 1.119529f);
         b[13] = f0c * vx; b[14] = f1b * fc1; b[15] = f2a * fc2;
         if constexpr (DEG >= 4) {
-          float f0d = vz * (-4.683326f * z2 + 2.0071396f), f1c = 3.3116114f * z2 - 0.47308735f;
-          float f2b = -1.7701308f * vz, f3a = 0.62583575f;
-          float fc3 = vx * fc2 - vy * fs2, fs3 = vx * fs2 + vy * fc2;
+          T f0d = vz * (-4.683326f * z2 + 2.0071396f), f1c = 3.3116114f * z2 - 0.47308735f;
+          T f2b = -1.7701308f * vz;
+          const float f3a = 0.62583575f;
+          T fc3 = vx * fc2 - vy * fs2, fs3 = vx * fs2 + vy * fc2;
           b[16] = f3a * fs3; b[17] = f2b * fs2; b[18] = f1c * fs1; b[19] = f0d * vy;
           b[20] = 1.9843135f * vz * b[12] - 1.0062306f * b[6];
           b[21] = f0d * vx; b[22] = f1c * fc1; b[23] = f2b * fc2; b[24] = f3a * fc3;

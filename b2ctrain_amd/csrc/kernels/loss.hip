@@ -341,9 +341,9 @@ __global__ void __launch_bounds__(1024) reduce_partials_kernel(const float* __re
     if (assign) {
       loss_accum[0] = (float)t;
       loss_accum[1] = 0.f;
-      if (running) {  // accumulate_kernel's update
-        loss_accum[2] += loss_accum[0] + loss_accum[1];
-        loss_accum[3] += 1.f;
+      if (running) {  // the trainer clears [0..3] each step, then accumulate_kernel adds: [2] = [0] + [1], [3] = 1
+        loss_accum[2] = loss_accum[0] + loss_accum[1];
+        loss_accum[3] = 1.f;
       }
     } else {
       loss_accum[0] = (float)((double)loss_accum[0] + t);

@@ -5,7 +5,7 @@
 #pragma clang fp contract(off)
 #include "b2c_kernels.h"
 #include "device_math.h"
-#include "project_one.h"
+#include "screen_splat.h"
 #include "raster_common.h"
 
 namespace b2c {
@@ -43,25 +43,24 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
     const float4 po = reinterpret_cast<const float4*>(a.pos_op)[i];
     const float4 q = reinterpret_cast<const float4*>(a.quat)[i];
     const float4 ls = reinterpret_cast<const float4*>(a.lscale)[i];
-    Proj pr = project_one(po, q, ls, a.cam);
+    const ScreenSplat pr = screen_splat(po, q, ls, a.cam);
     if (!pr.ok) {
       a.tile_count[i] = 0u;
     } else {
-      const float power = det_logf(pr.opac * 255.f);
-      bb = tile_bbox(pr.mean2d[0], pr.mean2d[1], pr.ex, pr.ey, a.tiles_x, a.tiles_y);
+      const float power = det_logf(pr.opacity * 255.f);
+      bb = tile_bbox(pr.px, pr.py, pr.ex, pr.ey, a.tiles_x, a.tiles_y);
       const int bw = bb.max_x - bb.min_x, bh = bb.max_y - bb.min_y;
       big = bw * bh > 32;
       small = !big;
       if (small) {
         area = (uint32_t)(bw * bh);
-        s_rec[threadIdx.x] = WaveRec{pr.mean2d[0], pr.mean2d[1], pr.conic.c00, pr.conic.c01, pr.conic.c11, power,
+        s_rec[threadIdx.x] = WaveRec{pr.px, pr.py, pr.conic.c00, pr.conic.c01, pr.conic.c11, power,
                                      (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), (uint32_t)bw};
       }
-      // SH colour, view direction camera -> splat (project.cu:44-55)
-      float vx = po.x - a.cam.pos[0], vy = po.y - a.cam.pos[1], vz = po.z - a.cam.pos[2];
-      float vl = sqrtf(vx * vx + vy * vy + vz * vz);
-      float inv = 1.f / fmaxf(vl, 1e-12f);
-      vx = vx * inv; vy = vy * inv; vz = vz * inv;
+      // SH colour at the camera-to-splat direction (project.cu:44-55)
+      const float vl = sqrtf((pr.d[0] * pr.d[0] + pr.d[1] * pr.d[1]) + pr.d[2] * pr.d[2]);
+      const float inv = 1.f / fmaxf(vl, 1e-12f);
+      const float vx = pr.d[0] * inv, vy = pr.d[1] * inv, vz = pr.d[2] * inv;
       constexpr int K = (DEG + 1) * (DEG + 1);
       float b[K];
       sh_basis<DEG>(vx, vy, vz, b);
@@ -82,16 +81,16 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       cr = __builtin_isfinite(cr) ? fminf(fmaxf(cr, -100.f), 100.f) : 0.f;
       cg = __builtin_isfinite(cg) ? fminf(fmaxf(cg, -100.f), 100.f) : 0.f;
       cb = __builtin_isfinite(cb) ? fminf(fmaxf(cb, -100.f), 100.f) : 0.f;
-      reinterpret_cast<float4*>(a.proj0)[i] = make_float4(pr.mean2d[0], pr.mean2d[1], pr.conic.c00, pr.conic.c01);
-      reinterpret_cast<float4*>(a.proj1)[i] = make_float4(pr.conic.c11, pr.opac, pr.mc[2], power);
+      reinterpret_cast<float4*>(a.proj0)[i] = make_float4(pr.px, pr.py, pr.conic.c00, pr.conic.c01);
+      reinterpret_cast<float4*>(a.proj1)[i] = make_float4(pr.conic.c11, pr.opacity, pr.c[2], power);
       reinterpret_cast<float4*>(a.proj2)[i] = make_float4(cr, cg, cb, 0.f);
       reinterpret_cast<float2*>(a.proj3)[i] = make_float2(0.f, 0.f);
       if (a.raster_rec) {  // halving the conic diagonal is exact: the raster evaluates the reference's sigma
         float4* rec = reinterpret_cast<float4*>(a.raster_rec) + (size_t)i * 4;
         const uint32_t sgn = (cr >= 0.f ? 1u : 0u) | (cg >= 0.f ? 2u : 0u) | (cb >= 0.f ? 4u : 0u);
-        rec[0] = make_float4(pr.mean2d[0], pr.mean2d[1], 0.5f * pr.conic.c00, pr.conic.c01);
-        rec[1] = make_float4(0.5f * pr.conic.c11, pr.opac, power, __uint_as_float(sgn));
-        rec[2] = make_float4(fmaxf(cr, 0.f), fmaxf(cg, 0.f), fmaxf(cb, 0.f), log2_opacity(pr.opac));
+        rec[0] = make_float4(pr.px, pr.py, 0.5f * pr.conic.c00, pr.conic.c01);
+        rec[1] = make_float4(0.5f * pr.conic.c11, pr.opacity, power, __uint_as_float(sgn));
+        rec[2] = make_float4(fmaxf(cr, 0.f), fmaxf(cg, 0.f), fmaxf(cb, 0.f), log2_opacity(pr.opacity));
         rec[3] = make_float4(0.f, 0.f, 0.f, 0.f);  // unused; whole lines are written (no partial-line writes)
       }
       if (a.max_screen) {

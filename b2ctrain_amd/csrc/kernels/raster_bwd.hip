@@ -1,9 +1,9 @@
-// Backward through compositing: per-pixel reverse replay from the shrunk range end (T_before = T/(1-alpha),
-// running colour remainder S), then a per-splat reduction of the fragment gradients over the tile's 64
-// pixels, accumulated into v_splat[n][13] with one global atomic per lane per (tile, contributing splat).
+// Backward through compositing: per-pixel reverse replay from the shrunk range end (the transmittance
+// recovered as T / (1 - alpha), the colour behind carried as one scalar contracted with v_rgb), then a
+// per-splat reduction of the fragment gradients over the tile's 64 pixels into v_splat[n][13].
 //
-// mode 0 (replaces raster_bwd_kernel, src/gpu/raster_bwd.cu:10-156): the 13 lanes + blend weight are
-//   reduced with wave64 butterfly shuffles, fp32 throughout. The correctness anchor.
+// mode 0 (replaces raster_bwd_kernel, src/gpu/raster_bwd.cu:10-156): per-fragment gradient lanes summed over
+//   the wave by shuffles, fp32 throughout. The correctness anchor.
 // mode 1 (replaces raster_bwd_tc_kernel, src/gpu/raster_bwd_tc.cu:29-225): each lane writes four scalars
 //   per fragment (vis, v_alpha*gauss, v_sigma, refine) for a group of 16 splats; the reduction over pixels
 //   is the product basis^T (16 x 64 px) * S (64 px x 16 splats) on v_mfma_f32_16x16x32_f16, with both
@@ -51,103 +51,101 @@ __device__ __forceinline__ PixelState load_pixel(const b2c_raster_bwd_args& a, i
   return s;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
+// ------------------------------------------------------------------------------------------------------
+// mode 0: the fp32 anchor
+// ------------------------------------------------------------------------------------------------------
+// The replay walks each pixel's list back to front carrying its transmittance T (T before a fragment is
+// T after it over 1 - alpha) and one scalar Q: the sum over the composited fragments behind of
+// vis * (colour . v_rgb), started at the background / alpha term -v_o_w. Then for a fragment
+// dL/dalpha = T_before (colour . v_rgb) - Q / (1 - alpha), the colour remainder contracted with v_rgb once
+// instead of carried per channel. Each lane's eleven per-fragment values (g0..g9 and the blend weight) are
+// summed over the wave by a shuffle-down tree and lane 0 adds them to v_splat with float atomics, the
+// reference's accumulation (raster_bwd.cu:130-139). The order of those atomic adds varies between runs; the
+// mode-1 path below is the deterministic one. The per-splat inputs come from proj0..2 (the reference's
+// buffers), not from the raster record the other kernels read, so this path also checks that record.
+constexpr int ANCHOR_VALS = 11;
+
+__device__ __forceinline__ float wave_total_to_lane0(float v) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o);
   return v;
 }
 
-// ------------------------------------------------------------------------------------------------------
-// mode 0: fp32 butterfly reduction
-// ------------------------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args a) {
-  __shared__ float4 s0[64], s1[64], s2[64];
-  __shared__ uint32_t s_gid[64];
+  __shared__ float4 s_geo[64], s_shape[64], s_rgb[64];  // proj0, proj1, proj2 of the batch's splats
+  __shared__ uint32_t s_id[64];
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
   const uint2 range = reinterpret_cast<const uint2*>(a.tile_ranges)[tile];
   if (range.y <= range.x) return;
   const int lane = threadIdx.x;
-  const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
-  const int px = tx * RT_W + (lane & 7), py = ty * RT_W + (lane >> 3);
-  PixelState ps = load_pixel(a, px, py, range.x);
+  const int px = (tile % a.tiles_x) * RT_W + (lane & 7), py = (tile / a.tiles_x) * RT_W + (lane >> 3);
+  const PixelState ps = load_pixel(a, px, py, range.x);
   const float Wf = (float)a.W, Hf = (float)a.H;
-  float Sx = 0.f, Sy = 0.f, Sz = 0.f;
-  const float4* proj0 = reinterpret_cast<const float4*>(a.proj0);
-  const float4* proj1 = reinterpret_cast<const float4*>(a.proj1);
-  const float4* proj2 = reinterpret_cast<const float4*>(a.proj2);
-  for (uint32_t batch_end = range.y; batch_end > range.x;) {
-    const uint32_t batch_start = batch_end > range.x + 64 ? batch_end - 64 : range.x;
-    const uint32_t count = batch_end - batch_start;
-    __syncthreads();
-    if ((uint32_t)lane < count) {
-      const uint32_t gid = a.vals_sorted[batch_start + lane];
-      s_gid[lane] = gid;
-      s0[lane] = proj0[gid];
-      s1[lane] = proj1[gid];
-      s2[lane] = proj2[gid];
+  float T = ps.T;
+  float Q = -ps.v_o_w;
+  for (uint32_t hi = range.y; hi > range.x;) {
+    const uint32_t lo = hi - range.x > 64u ? hi - 64u : range.x;
+    const int count = (int)(hi - lo);
+    __syncthreads();  // the previous batch is consumed
+    if (lane < count) {
+      const uint32_t id = a.vals_sorted[lo + lane];
+      s_id[lane] = id;
+      s_geo[lane] = reinterpret_cast<const float4*>(a.proj0)[id];
+      s_shape[lane] = reinterpret_cast<const float4*>(a.proj1)[id];
+      s_rgb[lane] = reinterpret_cast<const float4*>(a.proj2)[id];
     }
     __syncthreads();
-    for (int j = (int)count - 1; j >= 0; j--) {
-      const uint32_t idx = batch_start + j;
-      float g[GRAD_LANES];
+    for (int j = count - 1; j >= 0; j--) {
+      const float4 geo = s_geo[j], shape = s_shape[j];  // (mx, my, c00, c01), (c11, opacity, depth, power)
+      const float sigma = calc_sigma(ps.pcx, ps.pcy, geo.z, geo.w, shape.x, geo.x, geo.y);
+      const bool in = ps.inside && lo + (uint32_t)j < ps.last && sigma >= 0.f && sigma <= shape.w;
+      if (ballot64(in) == 0ull) continue;  // uniform
+      float val[ANCHOR_VALS];
 #pragma unroll
-      for (int k = 0; k < GRAD_LANES; k++) g[k] = 0.f;
-      float visw = 0.f;
-      bool contrib = ps.inside && idx < ps.last;
-      if (contrib) {
-        const float4 p0 = s0[j], p1 = s1[j];
-        const float dx = ps.pcx - p0.x, dy = ps.pcy - p0.y;
-        const float sigma = calc_sigma(ps.pcx, ps.pcy, p0.z, p0.w, p1.x, p0.x, p0.y);
-        contrib = sigma >= 0.f && sigma <= p1.w;
-        if (contrib) {
-          const float gauss = gauss_weight(sigma);
-          const float araw = fragment_alpha(sigma, log2_opacity(p1.y));
-          const float alpha = fminf(ALPHA_MAX, araw);
-          const float ra = 1.f / (1.f - alpha);
-          const float T_before = ps.T * ra;
-          const float vis = alpha * T_before;
-          const float4 col = s2[j];
-          const float cr = fmaxf(col.x, 0.f), cg = fmaxf(col.y, 0.f), cb = fmaxf(col.z, 0.f);
-          g[5] = col.x >= 0.f ? vis * ps.vo.x : 0.f;
-          g[6] = col.y >= 0.f ? vis * ps.vo.y : 0.f;
-          g[7] = col.z >= 0.f ? vis * ps.vo.z : 0.f;
-          const float v_alpha = (T_before * cr - Sx * ra) * ps.vo.x + (T_before * cg - Sy * ra) * ps.vo.y +
-                                (T_before * cb - Sz * ra) * ps.vo.z + ps.v_o_w * ra;
+      for (int k = 0; k < ANCHOR_VALS; k++) val[k] = 0.f;
+      if (in) {
+        const float4 col = s_rgb[j];
+        const float araw = fragment_alpha(sigma, log2_opacity(shape.y));
+        const float alpha = fminf(ALPHA_MAX, araw);
+        const float keep = 1.f - alpha;
+        const float Tb = T / keep;
+        const float vis = alpha * Tb;
+        const float cv = fmaxf(col.x, 0.f) * ps.vo.x + fmaxf(col.y, 0.f) * ps.vo.y + fmaxf(col.z, 0.f) * ps.vo.z;
+        const float v_alpha = Tb * cv - Q / keep;
+        if (araw <= ALPHA_MAX) {  // a clamped alpha does not depend on sigma
+          const float dx = ps.pcx - geo.x, dy = ps.pcy - geo.y;
           const float v_sigma = -alpha * v_alpha;
-          if (araw <= ALPHA_MAX) {
-            g[2] = 0.5f * v_sigma * dx * dx;
-            g[3] = v_sigma * dx * dy;
-            g[4] = 0.5f * v_sigma * dy * dy;
-            g[0] = -v_sigma * (p0.z * dx + p0.w * dy);
-            g[1] = -v_sigma * (p0.w * dx + p1.x * dy);
-            g[8] = v_alpha * gauss;
-            g[9] = sqrtf(g[0] * Wf * g[0] * Wf + g[1] * Hf * g[1] * Hf) * ps.inv_final_a;
-          }
-          Sx += cr * vis; Sy += cg * vis; Sz += cb * vis;
-          ps.T = T_before;
-          visw = vis;
+          const float gmx = -v_sigma * (geo.z * dx + geo.w * dy), gmy = -v_sigma * (geo.w * dx + shape.x * dy);
+          val[0] = gmx;
+          val[1] = gmy;
+          val[2] = 0.5f * v_sigma * dx * dx;
+          val[3] = v_sigma * dx * dy;
+          val[4] = 0.5f * v_sigma * dy * dy;
+          val[8] = v_alpha * gauss_weight(sigma);
+          val[9] = sqrtf((gmx * Wf) * (gmx * Wf) + (gmy * Hf) * (gmy * Hf)) * ps.inv_final_a;
         }
+        val[5] = col.x >= 0.f ? vis * ps.vo.x : 0.f;
+        val[6] = col.y >= 0.f ? vis * ps.vo.y : 0.f;
+        val[7] = col.z >= 0.f ? vis * ps.vo.z : 0.f;
+        val[10] = vis;
+        T = Tb;
+        Q = Q + vis * cv;
       }
-      if (ballot64(contrib) == 0) continue;
-      const float sv = wave_sum(visw);
-      float sums[GRAD_LANES];
 #pragma unroll
-      for (int k = 0; k < GRAD_LANES; k++) sums[k] = wave_sum(g[k]);
+      for (int k = 0; k < ANCHOR_VALS; k++) val[k] = wave_total_to_lane0(val[k]);
       if (lane == 0) {
-        const uint32_t gid = s_gid[j];
-        a.vis_flag[gid] = 1u;
-        if (a.vis_weight) atomicAdd(a.vis_weight + gid, sv);
-        float* dst = a.v_splat + (size_t)gid * GRAD_LANES;
+        const uint32_t id = s_id[j];
+        a.vis_flag[id] = 1u;
+        if (a.vis_weight) atomicAdd(a.vis_weight + id, val[10]);
+        float* dst = a.v_splat + (size_t)id * GRAD_LANES;
 #pragma unroll
-        for (int k = 0; k < GRAD_LANES; k++) {
-          const float v = sums[k] * a.inv_gscale;
-          if (v != 0.f) atomicAdd(dst + k, v);
-        }
+        for (int k = 0; k < 10; k++)
+          if (val[k] != 0.f) atomicAdd(dst + k, val[k] * a.inv_gscale);
       }
     }
-    batch_end = batch_start;
+    hi = lo;
   }
 }
 

@@ -4,98 +4,40 @@
 // consumed-and-zeroed contract of optim.cu:110-121). accumulate = 1 adds into grad_out so gradients of
 // several views can be summed; 0 overwrites like the reference, and with sparse set leaves the rows of splats
 // without gradient alone as the reference's early return does (optim.cu:148).
-// Evaluated without FMA contraction, in the operation order of the reference's VJP: the chain through the
-// 2x2 inverse and the 3x3 covariance amplifies rounding differences by the conic's condition number
-// (large for the thin splats of the stress configuration), so the kernel keeps IEEE single-op rounding.
+// The chain is derived here from the semi-axis form of the projection (screen_splat.h): from the conic to
+// the screen covariance, to the image-plane semi-axes u_j, and from those to the semi-axis lengths, the
+// camera-frame rotation, the Jacobian scale and the ray tangents; the colour's view-direction term comes
+// from the SH basis evaluated on dual numbers. No world-space covariance is formed. Evaluated without FMA
+// contraction (the culling decisions of the recomputed projection must match the forward's bit for bit).
 #pragma clang fp contract(off)
 #include "b2c_kernels.h"
 #include "device_math.h"
-#include "project_one.h"
+#include "screen_splat.h"
 
 namespace b2c {
 namespace dev {
 namespace {
 
-__device__ __forceinline__ float4 apply_normalize_vjp(float4 q, float4 g) {  // optim.cu:10-21
-  const float lsq = q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w;
-  const float l = sqrtf(lsq);
-  const float inv = 1.f / (l * lsq);
-  const float qw = q.x, qx = q.y, qy = q.z, qz = q.w;
-  const float gw = g.x, gx = g.y, gy = g.z, gz = g.w;
-  const float cc0 = -qw * qx, cc1 = -qx * qy, cc2 = -qy * qw, cs0 = -qw * qz, cs1 = -qx * qz, cs2 = -qy * qz;
-  return make_float4(((lsq - qw * qw) * gw + cc0 * gx + cc2 * gy + cs0 * gz) * inv,
-                     (cc0 * gw + (lsq - qx * qx) * gx + cc1 * gy + cs1 * gz) * inv,
-                     (cc2 * gw + cc1 * gx + (lsq - qy * qy) * gy + cs2 * gz) * inv,
-                     (cs0 * gw + cs1 * gx + cs2 * gy + (lsq - qz * qz) * gz) * inv);
+// d L / d q for the unit quaternion q = (w, v) of R(q), given G = d L / d R (row major). Writing
+// a = (G21 - G12, G02 - G20, G10 - G01) for the axial vector of G - G^T and S = G + G^T:
+//   d L / d w = 2 v . a,   d L / d v = 2 (w a + S v - 2 tr(G) v),
+// from differentiating R = (w^2 - v.v) I + 2 v v^T + 2 w [v]x entrywise on the unit sphere's embedding.
+__device__ __forceinline__ float4 rotation_vjp(float w, float x, float y, float z, const float* G) {
+  const float ax = G[7] - G[5], ay = G[2] - G[6], az = G[3] - G[1];
+  const float tr2 = 2.f * ((G[0] + G[4]) + G[8]);
+  const float s01 = G[1] + G[3], s02 = G[2] + G[6], s12 = G[5] + G[7];
+  const float svx = 2.f * G[0] * x + s01 * y + s02 * z;
+  const float svy = s01 * x + 2.f * G[4] * y + s12 * z;
+  const float svz = s02 * x + s12 * y + 2.f * G[8] * z;
+  return make_float4(2.f * ((x * ax + y * ay) + z * az), 2.f * (w * ax + svx - tr2 * x), 2.f * (w * ay + svy - tr2 * y),
+                     2.f * (w * az + svz - tr2 * z));
 }
 
-__device__ __forceinline__ float4 quat_to_mat_vjp(float qw, float qx, float qy, float qz, const float* m) {  // optim.cu:24-33
-  const float v00 = m[0], v01 = m[1], v02 = m[2], v10 = m[3], v11 = m[4], v12 = m[5], v20 = m[6], v21 = m[7], v22 = m[8];
-  const float w_grad = qx * (v21 - v12) + qy * (v02 - v20) + qz * (v10 - v01);
-  const float x_grad = -2.f * qx * (v11 + v22) + qy * (v10 + v01) + qz * (v20 + v02) + qw * (v21 - v12);
-  const float y_grad = qx * (v10 + v01) - 2.f * qy * (v00 + v22) + qz * (v21 + v12) + qw * (v02 - v20);
-  const float z_grad = qx * (v20 + v02) + qy * (v21 + v12) - 2.f * qz * (v00 + v11) + qw * (v10 - v01);
-  return make_float4(2.f * w_grad, 2.f * x_grad, 2.f * y_grad, 2.f * z_grad);
-}
-
-__device__ __forceinline__ Sym2 inverse2x2_vjp(Sym2 minv, Sym2 v) {  // optim.cu:35-45
-  const float tmp00 = -minv.c00 * v.c00 + -minv.c01 * v.c01;
-  const float tmp01 = -minv.c01 * v.c00 + -minv.c11 * v.c01;
-  const float tmp10 = -minv.c00 * v.c01 + -minv.c01 * v.c11;
-  const float tmp11 = -minv.c01 * v.c01 + -minv.c11 * v.c11;
-  Sym2 r;
-  r.c00 = tmp00 * minv.c00 + tmp10 * minv.c01;
-  r.c01 = tmp01 * minv.c00 + tmp11 * minv.c01;
-  r.c11 = tmp01 * minv.c01 + tmp11 * minv.c11;
-  return r;
-}
-
-// d colour / d view direction (optim.cu:48-88); dotc(k) = sum_ch c[k][ch] * vc[ch].
-template <int DEG>
-__device__ __forceinline__ void sh_viewdir_vjp(const float* coef, float x, float y, float z, float3 vc, int active,
-                                               float& gx, float& gy, float& gz) {
-  gx = gy = gz = 0.f;
-  auto dotc = [&](int k) { return coef[k * 3] * vc.x + coef[k * 3 + 1] * vc.y + coef[k * 3 + 2] * vc.z; };
-  if constexpr (DEG >= 1) if (active >= 1) {
-    const float f0a = 0.4886025f;
-    const float s_n1 = dotc(1), s_z0 = dotc(2), s_p1 = dotc(3);
-    gx += -f0a * s_p1; gy += -f0a * s_n1; gz += f0a * s_z0;
-    if constexpr (DEG >= 2) if (active >= 2) {
-      const float c2 = -1.0925485f, f1a = 0.54627424f;
-      const float s_n2 = dotc(4), s_n1b = dotc(5), s_z0b = dotc(6), s_p1b = dotc(7), s_p2 = dotc(8);
-      gx += 2.f * f1a * y * s_n2 + c2 * z * s_p1b + 2.f * f1a * x * s_p2;
-      gy += 2.f * f1a * x * s_n2 + c2 * z * s_n1b - 2.f * f1a * y * s_p2;
-      gz += c2 * y * s_n1b + 2.f * 0.9461747f * z * s_z0b + c2 * x * s_p1b;
-      if constexpr (DEG >= 3) if (active >= 3) {
-        const float z2 = z * z, x2 = x * x, y2 = y * y;
-        const float f2a = -0.5900436f, c1b = 1.4453057f, c0c = -2.285229f;
-        const float f1b = c1b * z, f0c = c0c * z2 + 0.4570458f, f0c_dz = 2.f * c0c * z;
-        const float s_n3 = dotc(9), s_n2c = dotc(10), s_n1c = dotc(11), s_z0c = dotc(12), s_p1c = dotc(13),
-                    s_p2c = dotc(14), s_p3 = dotc(15);
-        const float d12_z = 3.f * 1.8658817f * z2 - 1.119529f;
-        gx += f2a * 6.f * x * y * s_n3 + 2.f * f1b * y * s_n2c + f0c * s_p1c + 2.f * f1b * x * s_p2c + f2a * 3.f * (x2 - y2) * s_p3;
-        gy += f2a * 3.f * (x2 - y2) * s_n3 + 2.f * f1b * x * s_n2c + f0c * s_n1c + (-2.f) * f1b * y * s_p2c + f2a * (-6.f) * x * y * s_p3;
-        gz += 2.f * c1b * x * y * s_n2c + f0c_dz * y * s_n1c + d12_z * s_z0c + f0c_dz * x * s_p1c + c1b * (x2 - y2) * s_p2c;
-        if constexpr (DEG >= 4) if (active >= 4) {
-          const float fc1 = x2 - y2, fs1 = 2.f * x * y, fc2 = x * fc1 - y * fs1, fs2 = x * fs1 + y * fc1;
-          const float f0d = z * (-4.683326f * z2 + 2.0071396f), f0d_dz = -14.049978f * z2 + 2.0071396f;
-          const float f1c = 3.3116114f * z2 - 0.47308735f, f1c_dz = 2.f * 3.3116114f * z;
-          const float f2b_c = -1.7701308f, f2b = f2b_c * z, f3a = 0.62583575f;
-          const float p12 = z * (1.8658817f * z2 - 1.119529f), dp12 = 3.f * 1.8658817f * z2 - 1.119529f;
-          const float dp6 = 2.f * 0.9461747f * z;
-          const float dp20 = 1.9843135f * (p12 + z * dp12) - 1.0062306f * dp6;
-          const float s_n4 = dotc(16), s_n3d = dotc(17), s_n2d = dotc(18), s_n1d = dotc(19), s_z0d = dotc(20),
-                      s_p1d = dotc(21), s_p2d = dotc(22), s_p3d = dotc(23), s_p4 = dotc(24);
-          gx += f3a * 4.f * fs2 * s_n4 + f2b * 3.f * fs1 * s_n3d + f1c * 2.f * y * s_n2d + f0d * s_p1d + f1c * 2.f * x * s_p2d +
-                f2b * 3.f * fc1 * s_p3d + f3a * 4.f * fc2 * s_p4;
-          gy += f3a * 4.f * fc2 * s_n4 + f2b * 3.f * fc1 * s_n3d + f1c * 2.f * x * s_n2d + f0d * s_n1d + f1c * (-2.f) * y * s_p2d +
-                f2b * (-3.f) * fs1 * s_p3d + f3a * (-4.f) * fs2 * s_p4;
-          gz += f2b_c * fs2 * s_n3d + f1c_dz * fs1 * s_n2d + f0d_dz * y * s_n1d + dp20 * s_z0d + f0d_dz * x * s_p1d +
-                f1c_dz * fc1 * s_p2d + f2b_c * fc2 * s_p3d;
-        }
-      }
-    }
-  }
+// Through the normalisation q / |q|: the gradient's component along q vanishes, the rest scales by 1/|q|.
+__device__ __forceinline__ float4 unit_quat_vjp(float4 qn, float inv_len, float4 g) {
+  const float along = ((qn.x * g.x + qn.y * g.y) + qn.z * g.z) + qn.w * g.w;
+  return make_float4((g.x - qn.x * along) * inv_len, (g.y - qn.y * along) * inv_len, (g.z - qn.z * along) * inv_len,
+                     (g.w - qn.w * along) * inv_len);
 }
 
 // The per-splat rows of v_splat (13 floats) and grad_out (11 + 3K floats) are read and written through
@@ -182,127 +124,108 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
     else
       sv.load_all_either<DEG>(i, coef);
     const b2c_camera_gpu& cam = a.cam;
-    // The SH half needs only the view direction: it runs first, so the coefficients are dead before the
-    // projection's registers are live. Its row entries are zeroed below if the projection fails.
-    const float ux = po.x - cam.pos[0], uy = po.y - cam.pos[1], uz = po.z - cam.pos[2];
-    const float ul = sqrtf(ux * ux + uy * uy + uz * uz);
-    const float iul = 1.f / ul;
-    const float vx = ux * iul, vy = uy * iul, vz = uz * iul;
+    // the camera-to-splat vector, as screen_splat forms it
+    const float dvx = po.x - cam.pos[0], dvy = po.y - cam.pos[1], dvz = po.z - cam.pos[2];
+    const float dl = sqrtf((dvx * dvx + dvy * dvy) + dvz * dvz);
+    const float idl = 1.f / dl;
     const int kmax = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
-    const float3 vc = make_float3(g[5], g[6], g[7]);
+    const float vcr = g[5], vcg = g[6], vcb = g[7];
+    // Colour = sum_k coef_k Y_k(dir) + 0.5: the SH rows are Y_k * v_rgb, and the direction gradient is
+    // sum_k (coef_k . v_rgb) grad Y_k, taken on dual numbers; the SH half runs first, so the
+    // coefficients are dead before the projection's registers are live.
+    float gdx = 0.f, gdy = 0.f, gdz = 0.f;
     {
-      float basis[K];
-      sh_basis<DEG>(vx, vy, vz, basis);
+      float wk[K];
+#pragma unroll
+      for (int k = 0; k < K; k++) wk[k] = k < kmax ? (coef[3 * k] * vcr + coef[3 * k + 1] * vcg) + coef[3 * k + 2] * vcb : 0.f;
+      Dual3 yk[K];
+      sh_basis<DEG>(Dual3{dvx * idl, 1.f, 0.f, 0.f}, Dual3{dvy * idl, 0.f, 1.f, 0.f}, Dual3{dvz * idl, 0.f, 0.f, 1.f}, yk);
 #pragma unroll
       for (int k = 0; k < K; k++) {
-        const float bk = k < kmax ? basis[k] : 0.f;
-        out[11 + k * 3] = bk * vc.x; out[12 + k * 3] = bk * vc.y; out[13 + k * 3] = bk * vc.z;
+        const float y = k < kmax ? yk[k].v : 0.f;
+        out[11 + 3 * k] = y * vcr; out[12 + 3 * k] = y * vcg; out[13 + 3 * k] = y * vcb;
+        gdx = gdx + wk[k] * yk[k].x; gdy = gdy + wk[k] * yk[k].y; gdz = gdz + wk[k] * yk[k].z;
       }
     }
-    float vvx, vvy, vvz;
-    sh_viewdir_vjp<DEG>(coef, vx, vy, vz, vc, a.active_deg, vvx, vvy, vvz);
-    const float vdot = vx * vvx + vy * vvy + vz * vvz;
-    const float msx = (vvx - vx * vdot) * (1.f / ul), msy = (vvy - vy * vdot) * (1.f / ul), msz = (vvz - vz * vdot) * (1.f / ul);
-    const Proj pr = project_one(po, q, ls, a.cam);
-    if (pr.ok) {
-      const float v_alpha = g[8];
-      float g_op = v_alpha * 1.f * pr.comp_floor * pr.sig * (1.f - pr.sig);
-      const Sym2 v_cov = inverse2x2_vjp(pr.conic, Sym2{g[2], 0.5f * g[3], g[4]});
-      const float* Rv = cam.R;
-      float M[9];
+    const ScreenSplat sp = screen_splat(po, q, ls, cam);
+    if (sp.ok) {
+      // dir = d / |d|: only the gradient's part across dir moves it
+      const float ux = dvx * idl, uy = dvy * idl, uz = dvz * idl;
+      const float radial = (ux * gdx + uy * gdy) + uz * gdz;
+      const float gsx = (gdx - ux * radial) * idl, gsy = (gdy - uy * radial) * idl, gsz = (gdz - uz * radial) * idl;
+      // Conic C = Sigma'^-1: dL/dSigma' = -C Gc C (Gc = [[g2, g3/2], [g3/2, g4]]), and Sigma' = U U^T + 0.3 I gives
+      // dL/du_j = 2 dL/dSigma' u_j = -2 C Gc (C u_j). C u_j is formed as adj(Sigma') u_j / det with
+      // adj(Sigma') u_j = sum_{k != j} (u_j x u_k) (uy_k, -ux_k) + 0.3 u_j: for the long axis of an elongated
+      // footprint, C u_j is small and the conic's entries would leave it as the difference of two nearly
+      // equal products. With u_j = (jx e_j, jy f_j) a_j, e_j = W0j - tx W2j and f_j = W1j - ty W2j, collect
+      // the gradients of the semi-axis lengths, of W, and of jx, jy, tx, ty.
+      const float idet = sp.idet;
+      const float h = 0.5f * g[3];
+      const float xs[3][3] = {{0.f, sp.cross[0], sp.cross[1]}, {-sp.cross[0], 0.f, sp.cross[2]}, {-sp.cross[1], -sp.cross[2], 0.f}};
+      float gaxis[3], gW[9];
+      float gjx = 0.f, gjy = 0.f, gtx = 0.f, gty = 0.f;
 #pragma unroll
-      for (int r = 0; r < 3; r++) {
-        M[r * 3] = pr.Rq.m[r * 3] * pr.s[0]; M[r * 3 + 1] = pr.Rq.m[r * 3 + 1] * pr.s[1]; M[r * 3 + 2] = pr.Rq.m[r * 3 + 2] * pr.s[2];
-      }
-      float covar[9];
+      for (int j = 0; j < 3; j++) {
+        float ax_ = 0.3f * sp.ux[j], ay_ = 0.3f * sp.uy[j];
 #pragma unroll
-      for (int r = 0; r < 3; r++)
-#pragma unroll
-        for (int cc = 0; cc < 3; cc++) covar[r * 3 + cc] = M[r * 3] * M[cc * 3] + M[r * 3 + 1] * M[cc * 3 + 1] + M[r * 3 + 2] * M[cc * 3 + 2];
-      float RvC[9];
-#pragma unroll
-      for (int r = 0; r < 3; r++)
-#pragma unroll
-        for (int cc = 0; cc < 3; cc++) RvC[r * 3 + cc] = Rv[r * 3] * covar[cc] + Rv[r * 3 + 1] * covar[3 + cc] + Rv[r * 3 + 2] * covar[6 + cc];
-      float cov_c[9];
-#pragma unroll
-      for (int r = 0; r < 3; r++)
-#pragma unroll
-        for (int cc = 0; cc < 3; cc++) cov_c[r * 3 + cc] = RvC[r * 3] * Rv[cc * 3] + RvC[r * 3 + 1] * Rv[cc * 3 + 1] + RvC[r * 3 + 2] * Rv[cc * 3 + 2];
-      const float mcx = pr.mc[0], mcy = pr.mc[1], mcz = pr.mc[2];
-      const float inv_z = 1.f / mcz, inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z;
-      const float v2x = g[0], v2y = g[1];
-      const float vcov[2][2] = {{v_cov.c00, v_cov.c01}, {v_cov.c01, v_cov.c11}};
-      float tmp[2][3];
-#pragma unroll
-      for (int r = 0; r < 2; r++)
-#pragma unroll
-        for (int j = 0; j < 3; j++) tmp[r][j] = vcov[r][0] * pr.J[j] + vcov[r][1] * pr.J[3 + j];
-      auto rowdot = [&](int r, int cr) { return tmp[r][0] * cov_c[cr * 3] + tmp[r][1] * cov_c[cr * 3 + 1] + tmp[r][2] * cov_c[cr * 3 + 2]; };
-      const float vj00 = 2.f * rowdot(0, 0), vj11 = 2.f * rowdot(1, 1), vj20 = 2.f * rowdot(0, 2), vj21 = 2.f * rowdot(1, 2);
-      const float rx = mcx * inv_z, ry = mcy * inv_z;
-      const float txc = mcz * fminf(fmaxf(rx, cam.lim_neg_x), cam.lim_pos_x), tyc = mcz * fminf(fmaxf(ry, cam.lim_neg_y), cam.lim_pos_y);
-      float v_mx = cam.fx * inv_z * v2x, v_my = cam.fy * inv_z * v2y;
-      float v_mz = -(cam.fx * mcx * v2x + cam.fy * mcy * v2y) * inv_z2;
-      if (!pr.clamp_x) v_mx += -cam.fx * inv_z2 * vj20; else v_mz += -cam.fx * inv_z3 * vj20 * txc;
-      if (!pr.clamp_y) v_my += -cam.fy * inv_z2 * vj21; else v_mz += -cam.fy * inv_z3 * vj21 * tyc;
-      v_mz += -cam.fx * inv_z2 * vj00 - cam.fy * inv_z2 * vj11 + 2.f * cam.fx * txc * inv_z3 * vj20 + 2.f * cam.fy * tyc * inv_z3 * vj21;
-      float vcc[9];
-#pragma unroll
-      for (int r = 0; r < 3; r++)
-#pragma unroll
-        for (int cc = 0; cc < 3; cc++) {
-          float s = 0.f;
-#pragma unroll
-          for (int p = 0; p < 2; p++)
-#pragma unroll
-            for (int q2 = 0; q2 < 2; q2++) s += pr.J[p * 3 + r] * vcov[p][q2] * pr.J[q2 * 3 + cc];
-          vcc[r * 3 + cc] = s;
+        for (int k = 0; k < 3; k++) {
+          if (k == j) continue;
+          ax_ = ax_ + xs[j][k] * sp.uy[k];
+          ay_ = ay_ - xs[j][k] * sp.ux[k];
         }
-      float t1[9];
-#pragma unroll
-      for (int r = 0; r < 3; r++)
-#pragma unroll
-        for (int cc = 0; cc < 3; cc++) t1[r * 3 + cc] = Rv[r] * vcc[cc] + Rv[3 + r] * vcc[3 + cc] + Rv[6 + r] * vcc[6 + cc];
-      float v_covar[9];
-#pragma unroll
-      for (int r = 0; r < 3; r++)
-#pragma unroll
-        for (int cc = 0; cc < 3; cc++) v_covar[r * 3 + cc] = t1[r * 3] * Rv[cc] + t1[r * 3 + 1] * Rv[3 + cc] + t1[r * 3 + 2] * Rv[6 + cc];
-      float v_M[9];
-#pragma unroll
-      for (int r = 0; r < 3; r++)
-#pragma unroll
-        for (int cc = 0; cc < 3; cc++)
-          v_M[r * 3 + cc] = 2.f * (v_covar[r * 3] * M[cc] + v_covar[r * 3 + 1] * M[3 + cc] + v_covar[r * 3 + 2] * M[6 + cc]);
-      float gpx = Rv[0] * v_mx + Rv[3] * v_my + Rv[6] * v_mz + msx;
-      float gpy = Rv[1] * v_mx + Rv[4] * v_my + Rv[7] * v_mz + msy;
-      float gpz = Rv[2] * v_mx + Rv[5] * v_my + Rv[8] * v_mz + msz;
-      const float f2 = ls.w * ls.w;
-      const float vs0 = pr.Rq.m[0] * v_M[0] + pr.Rq.m[3] * v_M[3] + pr.Rq.m[6] * v_M[6];
-      const float vs1 = pr.Rq.m[1] * v_M[1] + pr.Rq.m[4] * v_M[4] + pr.Rq.m[7] * v_M[7];
-      const float vs2 = pr.Rq.m[2] * v_M[2] + pr.Rq.m[5] * v_M[5] + pr.Rq.m[8] * v_M[8];
-      float glx = vs0 * pr.s2_raw[0] / pr.s[0] + v_alpha * pr.opac * f2 / (pr.s2_raw[0] + f2);
-      float gly = vs1 * pr.s2_raw[1] / pr.s[1] + v_alpha * pr.opac * f2 / (pr.s2_raw[1] + f2);
-      float glz = vs2 * pr.s2_raw[2] / pr.s[2] + v_alpha * pr.opac * f2 / (pr.s2_raw[2] + f2);
-      float vR[9];
-#pragma unroll
-      for (int r = 0; r < 3; r++) {
-        vR[r * 3] = v_M[r * 3] * pr.s[0]; vR[r * 3 + 1] = v_M[r * 3 + 1] * pr.s[1]; vR[r * 3 + 2] = v_M[r * 3 + 2] * pr.s[2];
+        const float cux = ax_ * idet, cuy = ay_ * idet;  // C u_j
+        const float vx = g[2] * cux + h * cuy, vy = h * cux + g[4] * cuy;
+        const float gux = -2.f * (sp.cov.c11 * vx - sp.cov.c01 * vy) * idet;
+        const float guy = -2.f * (sp.cov.c00 * vy - sp.cov.c01 * vx) * idet;
+        const float e = sp.w.m[j] - sp.tx * sp.w.m[6 + j], f = sp.w.m[3 + j] - sp.ty * sp.w.m[6 + j];
+        gaxis[j] = gux * sp.jx * e + guy * sp.jy * f;
+        const float ke = gux * sp.jx * sp.axis[j], kf = guy * sp.jy * sp.axis[j];  // dL/de_j, dL/df_j
+        gW[j] = ke;
+        gW[3 + j] = kf;
+        gW[6 + j] = -(sp.tx * ke + sp.ty * kf);
+        gjx = gjx + gux * e * sp.axis[j];
+        gjy = gjy + guy * f * sp.axis[j];
+        gtx = gtx - ke * sp.w.m[6 + j];
+        gty = gty - kf * sp.w.m[6 + j];
       }
-      const float qn2 = q.x * q.x + q.y * q.y + q.z * q.z + q.w * q.w;
-      const float inv_qn = 1.f / sqrtf(qn2);
-      const float4 qg = quat_to_mat_vjp(q.x * inv_qn, q.y * inv_qn, q.z * inv_qn, q.w * inv_qn, vR);
-      float4 gq = apply_normalize_vjp(q, qg);
-      const bool ok = finite3(gpx, gpy, gpz) && __builtin_isfinite(g_op) && finite3(glx, gly, glz) &&
+      // Pinhole: px = fx x/z + cx, jx = fx/z, tx = x/z unless clamped (likewise y). Camera-frame centre:
+      const float iz = 1.f / sp.c[2];
+      const float ax = g[0] * cam.fx + (sp.clip_x ? 0.f : gtx);  // dL/d(x/z)
+      const float ay = g[1] * cam.fy + (sp.clip_y ? 0.f : gty);
+      const float gcx = ax * iz, gcy = ay * iz;
+      const float gcz = -iz * (((gjx * sp.jx + gjy * sp.jy) + ax * sp.tx_raw) + ay * sp.ty_raw);
+      // c = R_view (p - o): world gradient R_view^T gc, plus the view direction's share
+      const float* Rv = cam.R;
+      float gpx = ((Rv[0] * gcx + Rv[3] * gcy) + Rv[6] * gcz) + gsx;
+      float gpy = ((Rv[1] * gcx + Rv[4] * gcy) + Rv[7] * gcz) + gsy;
+      float gpz = ((Rv[2] * gcx + Rv[5] * gcy) + Rv[8] * gcz) + gsz;
+      // W = R_view R(q): dL/dR = R_view^T gW
+      float gR[9];
+#pragma unroll
+      for (int r = 0; r < 3; r++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) gR[3 * r + j] = (Rv[r] * gW[j] + Rv[3 + r] * gW[3 + j]) + Rv[6 + r] * gW[6 + j];
+      // semi-axes a_j = sqrt(exp(2 l_j) + f^2), and the floor's opacity factor prod_j sqrt(var_j / (var_j + f^2))
+      const float v_op = g[8];
+      const float f2 = ls.w * ls.w;
+      float gl[3];
+#pragma unroll
+      for (int j = 0; j < 3; j++)
+        gl[j] = gaxis[j] * sp.var[j] / sp.axis[j] + v_op * sp.opacity * f2 / (sp.var[j] + f2);
+      float g_logit = v_op * sp.floor_comp * sp.sig * (1.f - sp.sig);
+      const float qn2 = ((q.x * q.x + q.y * q.y) + q.z * q.z) + q.w * q.w;
+      const float iq = 1.f / sqrtf(qn2);
+      const float4 qn = make_float4(q.x * iq, q.y * iq, q.z * iq, q.w * iq);
+      float4 gq = unit_quat_vjp(qn, iq, rotation_vjp(qn.x, qn.y, qn.z, qn.w, gR));
+      const bool ok = finite3(gpx, gpy, gpz) && __builtin_isfinite(g_logit) && finite3(gl[0], gl[1], gl[2]) &&
                       __builtin_isfinite(gq.x + gq.y + gq.z + gq.w);
       if (!ok) {
-        gpx = gpy = gpz = g_op = glx = gly = glz = 0.f;
+        gpx = gpy = gpz = g_logit = gl[0] = gl[1] = gl[2] = 0.f;
         gq = make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      out[0] = gpx; out[1] = gpy; out[2] = gpz; out[3] = g_op;
+      out[0] = gpx; out[1] = gpy; out[2] = gpz; out[3] = g_logit;
       out[4] = gq.x; out[5] = gq.y; out[6] = gq.z; out[7] = gq.w;
-      out[8] = glx; out[9] = gly; out[10] = glz;
+      out[8] = gl[0]; out[9] = gl[1]; out[10] = gl[2];
       done = true;
     }
   }

@@ -238,6 +238,43 @@ int b2c_hip_vjp(const b2c_vjp_args* a, hipStream_t stream);
 /* ---- utilities ---- */
 int b2c_hip_fill_u32(uint32_t* p, uint32_t value, size_t count, hipStream_t stream);
 
+/* ---- model storage (src/model.cu:8-102 defines the layout these fill and read back) ---- */
+/* A splat cloud in device memory, one array per field (brush's SplatCloud layout, src/ply.h:10-42):
+ * pos [n][3], log_scale [n][3], quat [n][4] (w, x, y, z), opacity [n] (logit), sh [n][3K]
+ * coefficient-major, floor_ [n] or NULL. */
+typedef struct b2c_cloud_dev {
+  float* pos;
+  float* log_scale;
+  float* quat;
+  float* opacity;
+  float* sh;
+  float* floor_;
+} b2c_cloud_dev;
+
+/* The Model's device layout: float4 pos_op / quat / lscale [cap], planar SH with stride cap: sh_dc
+ * [3][cap] fp32, bands [3K - 3][cap] in sh_hi32 (fp32) or sh_hi16 (IEEE binary16). */
+typedef struct b2c_model_dev {
+  int n, cap, sh_lanes; /* sh_lanes = 3K */
+  float* pos_op;
+  float* quat;
+  float* lscale;
+  float* sh_dc;
+  float* sh_hi32;
+  uint16_t* sh_hi16;
+} b2c_model_dev;
+
+/* Cloud -> model (Model::upload, model.cu:41-80): lscale.w = floor_[i] (0 when floor_ is NULL), bands
+ * rounded to nearest even when stored as fp16. Model slots n .. cap are left untouched. */
+int b2c_hip_model_scatter(const b2c_cloud_dev* src, const b2c_model_dev* dst, hipStream_t stream);
+/* Model -> cloud (Model::download, model.cu:82-102); fp16 bands widen exactly. floor_ may be NULL. */
+int b2c_hip_model_gather(const b2c_model_dev* src, const b2c_cloud_dev* dst, hipStream_t stream);
+/* Planar re-layout for capacity growth: dst[l * new_cap + i] = src[l * old_cap + i] for i < n, 0 for
+ * n <= i < new_cap, over `lanes` lanes of elem_bytes (2 or 4) each. */
+int b2c_hip_planar_regrow(const void* src, void* dst, int elem_bytes, int lanes, int n, int old_cap, int new_cap,
+                          hipStream_t stream);
+/* lscale[i].w = floor_[i] for i < n (the frozen Mip-Splatting floor). */
+int b2c_hip_model_set_floor(float* lscale, const float* floor_, int n, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

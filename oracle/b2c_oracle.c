@@ -164,7 +164,8 @@ static void sh_basis_f(int deg, float vx, float vy, float vz, float* b) {
 
 static int imin(int a, int b) { return a < b ? a : b; }
 
-/* Everything project_one produces that the VJP needs (splat_math.cuh:199-217). */
+/* Everything the projection produces that the VJP needs (splat_math.cuh:199-217 lists the same
+ * quantities). */
 typedef struct {
   float mc[3], s[3], s2_raw[3], comp_floor;
   float Rq[9], J[6];
@@ -176,74 +177,92 @@ typedef struct {
   int ok;
 } proj_t;
 
-/* splat_math.cuh:224-293 with mip = false. rsqrtf of the reference becomes 1/sqrtf (IEEE both sides),
- * __expf/__logf become the Cephes functions above. */
+/* The projection of splat_math.cuh:224-293 (mip off), in the operation sequence of the HIP kernel's
+ * screen_splat (b2ctrain_amd/csrc/kernels/screen_splat.h), so that, compiled without FMA contraction,
+ * centre, conic, opacity, power and extent agree bit for bit: the camera-frame centre R (p - o) from the
+ * camera centre o; per-axis variances exp(2 l) and semi-axes sqrt(var + f^2); the floor's opacity factor
+ * as a product of per-axis ratios; the image-plane semi-axes u_j = (fx/z (W0j - tx W2j) a_j,
+ * fy/z (W1j - ty W2j) a_j) with W = R_view R(q) and (tx, ty) the clamped tangents; the screen covariance
+ * sum_j u_j u_j^T + 0.3 I with its determinant by Cauchy-Binet (no cancellation for elongated footprints,
+ * where the reference's c00 c11 - c01^2 loses digits). The reference's rsqrtf is 1/sqrtf here and its __expf/__logf the Cephes
+ * functions above; the reference's x * (1/z) tangents are true quotients. */
 static void project_one(const float* po, const float* q, const float* ls, const orc_cam_t* cam, proj_t* r) {
   r->ok = 0;
   const float* Rv = cam->R;
-  float mcx = Rv[0] * po[0] + Rv[1] * po[1] + Rv[2] * po[2];
-  float mcy = Rv[3] * po[0] + Rv[4] * po[1] + Rv[5] * po[2];
-  float mcz = Rv[6] * po[0] + Rv[7] * po[1] + Rv[8] * po[2];
-  mcx = mcx + cam->t[0]; mcy = mcy + cam->t[1]; mcz = mcz + cam->t[2];
-  r->mc[0] = mcx; r->mc[1] = mcy; r->mc[2] = mcz;
-  if (!(finitef(mcx) && finitef(mcy) && finitef(mcz) && mcz <= 1e10f)) return;
-  if (!(mcz >= 0.01f)) return;
-  float s2x = orc_expf(2.f * ls[0]), s2y = orc_expf(2.f * ls[1]), s2z = orc_expf(2.f * ls[2]);
-  r->s2_raw[0] = s2x; r->s2_raw[1] = s2y; r->s2_raw[2] = s2z;
-  float f2 = ls[3] * ls[3];
-  float s2fx = s2x + f2, s2fy = s2y + f2, s2fz = s2z + f2;
-  r->s[0] = sqrtf(s2fx); r->s[1] = sqrtf(s2fy); r->s[2] = sqrtf(s2fz);
-  r->comp_floor = ls[3] > 0.f ? sqrtf((s2x * s2y * s2z) / (s2fx * s2fy * s2fz)) : 1.f;
+  const float d[3] = {po[0] - cam->pos[0], po[1] - cam->pos[1], po[2] - cam->pos[2]};
+  for (int k = 0; k < 3; k++) r->mc[k] = (Rv[3 * k] * d[0] + Rv[3 * k + 1] * d[1]) + Rv[3 * k + 2] * d[2];
+  const float z = r->mc[2];
+  if (!(finitef(r->mc[0]) && finitef(r->mc[1]) && finitef(z) && z <= 1e10f)) return;
+  if (!(z >= 0.01f)) return;
+  const float f2 = ls[3] * ls[3];
+  float keep = 1.f;
+  for (int j = 0; j < 3; j++) {
+    r->s2_raw[j] = orc_expf(2.f * ls[j]);
+    const float vf = r->s2_raw[j] + f2;
+    r->s[j] = sqrtf(vf);
+    keep = keep * (r->s2_raw[j] / vf);
+  }
+  r->comp_floor = ls[3] > 0.f ? sqrtf(keep) : 1.f;
   if (!(finitef(r->s[0]) && finitef(r->s[1]) && finitef(r->s[2]))) return;
-  float qn2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
+  const float qn2 = ((q[0] * q[0] + q[1] * q[1]) + q[2] * q[2]) + q[3] * q[3];
   if (!(qn2 >= 1e-6f && finitef(qn2))) return;
   if (!finitef(po[3])) return;
-  float inv_qn = 1.f / sqrtf(qn2);
-  float qn[4] = {q[0] * inv_qn, q[1] * inv_qn, q[2] * inv_qn, q[3] * inv_qn};
+  const float iq = 1.f / sqrtf(qn2);
+  const float qn[4] = {q[0] * iq, q[1] * iq, q[2] * iq, q[3] * iq};
   quat_to_mat(qn, r->Rq);
-  float M[9];
-  mat3_mul(Rv, r->Rq, M);
-  for (int i = 0; i < 3; i++) { M[i * 3] *= r->s[0]; M[i * 3 + 1] *= r->s[1]; M[i * 3 + 2] *= r->s[2]; }
-  float inv_z = 1.f / mcz;
-  float rx = mcx * inv_z, ry = mcy * inv_z;
-  float cxr = fminf(fmaxf(rx, cam->lim_neg_x), cam->lim_pos_x), cyr = fminf(fmaxf(ry, cam->lim_neg_y), cam->lim_pos_y);
-  r->clamp_x = !(rx <= cam->lim_pos_x && rx >= cam->lim_neg_x);
-  r->clamp_y = !(ry <= cam->lim_pos_y && ry >= cam->lim_neg_y);
-  float dx = cam->fx * inv_z, dy = cam->fy * inv_z;
-  r->J[0] = dx; r->J[1] = 0.f; r->J[2] = -dx * cxr;
-  r->J[3] = 0.f; r->J[4] = dy; r->J[5] = -dy * cyr;
-  float V[6];
-  for (int i = 0; i < 2; i++)
-    for (int j = 0; j < 3; j++) V[i * 3 + j] = r->J[i * 3] * M[j] + r->J[i * 3 + 1] * M[3 + j] + r->J[i * 3 + 2] * M[6 + j];
-  sym2 raw;
-  raw.c00 = V[0] * V[0] + V[1] * V[1] + V[2] * V[2];
-  raw.c01 = V[0] * V[3] + V[1] * V[4] + V[2] * V[5];
-  raw.c11 = V[3] * V[3] + V[4] * V[4] + V[5] * V[5];
-  float max_abs = fmaxf(fabsf(raw.c00), fmaxf(fabsf(raw.c01), fabsf(raw.c11)));
-  if (max_abs > 1e18f) { float k = 1e18f / max_abs; raw.c00 *= k; raw.c01 *= k; raw.c11 *= k; }
-  sym2 cov = raw;
-  cov.c00 += 0.3f; cov.c11 += 0.3f;
-  r->cov = cov;
+  const float tx_raw = r->mc[0] / z, ty_raw = r->mc[1] / z;
+  r->clamp_x = !(tx_raw <= cam->lim_pos_x && tx_raw >= cam->lim_neg_x);
+  r->clamp_y = !(ty_raw <= cam->lim_pos_y && ty_raw >= cam->lim_neg_y);
+  const float tx = fminf(fmaxf(tx_raw, cam->lim_neg_x), cam->lim_pos_x);
+  const float ty = fminf(fmaxf(ty_raw, cam->lim_neg_y), cam->lim_pos_y);
+  const float jx = cam->fx / z, jy = cam->fy / z;
+  r->J[0] = jx; r->J[1] = 0.f; r->J[2] = -jx * tx;
+  r->J[3] = 0.f; r->J[4] = jy; r->J[5] = -jy * ty;
+  float ux[3], uy[3], q00 = 0.f, q01 = 0.f, q11 = 0.f;
+  for (int j = 0; j < 3; j++) {
+    float w[3];
+    for (int k = 0; k < 3; k++) w[k] = (Rv[3 * k] * r->Rq[j] + Rv[3 * k + 1] * r->Rq[3 + j]) + Rv[3 * k + 2] * r->Rq[6 + j];
+    ux[j] = jx * ((w[0] - tx * w[2]) * r->s[j]);
+    uy[j] = jy * ((w[1] - ty * w[2]) * r->s[j]);
+    q00 = q00 + ux[j] * ux[j];
+    q01 = q01 + ux[j] * uy[j];
+    q11 = q11 + uy[j] * uy[j];
+  }
+  const float big = fmaxf(fabsf(q00), fmaxf(fabsf(q01), fabsf(q11)));
+  if (big > 1e18f) {
+    const float k = sqrtf(1e18f / big);
+    q00 = q01 = q11 = 0.f;
+    for (int j = 0; j < 3; j++) {
+      ux[j] = ux[j] * k;
+      uy[j] = uy[j] * k;
+      q00 = q00 + ux[j] * ux[j];
+      q01 = q01 + ux[j] * uy[j];
+      q11 = q11 + uy[j] * uy[j];
+    }
+  }
+  /* det(U U^T + 0.3 I) by Cauchy-Binet: sum of squared 2D cross products + 0.3 tr + 0.09 */
+  const float x01 = ux[0] * uy[1] - uy[0] * ux[1], x02 = ux[0] * uy[2] - uy[0] * ux[2], x12 = ux[1] * uy[2] - uy[1] * ux[2];
+  const float dil = 0.3f;
+  const float det = ((x01 * x01 + x02 * x02) + x12 * x12) + dil * (q00 + q11) + dil * dil;
+  const float c00 = q00 + dil, c01 = q01, c11 = q11 + dil;
+  r->cov.c00 = c00; r->cov.c01 = c01; r->cov.c11 = c11;
   r->sig = 1.f / (1.f + orc_expf(-po[3]));
-  r->opac = r->sig * 1.f * r->comp_floor;
-  if (!(finitef(cov.c00) && finitef(cov.c01) && finitef(cov.c11))) return;
-  float det = cov.c00 * cov.c11 - cov.c01 * cov.c01;
+  r->opac = r->sig * r->comp_floor;
+  if (!(finitef(c00) && finitef(c01) && finitef(c11) && finitef(det))) return;
   if (!(det > 0.f)) return;
-  float inv_det = 1.f / det;
-  r->conic.c00 = cov.c11 * inv_det; r->conic.c01 = -cov.c01 * inv_det; r->conic.c11 = cov.c00 * inv_det;
-  r->mean2d[0] = cam->fx * rx + cam->cx; r->mean2d[1] = cam->fy * ry + cam->cy;
+  const float idet = 1.f / det;
+  r->conic.c00 = c11 * idet; r->conic.c01 = -c01 * idet; r->conic.c11 = c00 * idet;
+  r->mean2d[0] = cam->fx * tx_raw + cam->cx; r->mean2d[1] = cam->fy * ty_raw + cam->cy;
   if (!(r->opac >= ALPHA_CUTOFF)) return;
-  float power = orc_logf(r->opac * 255.f);
-  float detc = r->conic.c00 * r->conic.c11 - r->conic.c01 * r->conic.c01;
+  const float power = orc_logf(r->opac * 255.f);
+  const float detc = r->conic.c00 * r->conic.c11 - r->conic.c01 * r->conic.c01;
   if (!(detc > 0.f)) return;
-  float inv_detc = 1.f / detc;
-  r->ex = sqrtf(2.f * power * r->conic.c11 * inv_detc);
-  r->ey = sqrtf(2.f * power * r->conic.c00 * inv_detc);
+  const float idetc = 1.f / detc;
+  r->ex = sqrtf(2.f * power * r->conic.c11 * idetc);
+  r->ey = sqrtf(2.f * power * r->conic.c00 * idetc);
   if (!(r->ex >= 0.f && r->ey >= 0.f)) return;
-  int on_screen = r->mean2d[0] + r->ex > 0.f && r->mean2d[0] - r->ex < (float)cam->W && r->mean2d[1] + r->ey > 0.f &&
-                  r->mean2d[1] - r->ey < (float)cam->H;
-  if (!on_screen) return;
-  r->ok = 1;
+  r->ok = r->mean2d[0] + r->ex > 0.f && r->mean2d[0] - r->ex < (float)cam->W && r->mean2d[1] + r->ey > 0.f &&
+          r->mean2d[1] - r->ey < (float)cam->H;
 }
 
 int orc_tile_bits(int n_tiles) {
@@ -627,83 +646,48 @@ void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], c
 }
 
 /* ------------------------------------------------------------------------------------------------
- * Projection VJP (optim.cu:10-97, 148-253) with the grad_out write (292-296).
+ * Projection VJP (optim.cu:99-253) with the grad_out write (292-296), evaluated in double precision from
+ * the float32 parameters and screen-space gradients: the accurate reference the HIP kernel's float32 VJP
+ * is measured against. It follows the reference's chain through the world-space covariance
+ * Sigma = M M^T (M = R(q) diag(s)) and the camera-frame covariance R_view Sigma R_view^T, a different
+ * route from the kernel's (which differentiates the image-plane semi-axes). The colour's view-direction
+ * term is a central difference of the double-precision SH basis on the unit sphere's tangent plane.
+ * Splats culled by the float32 projection (the forward's decision) get zero rows.
  * ---------------------------------------------------------------------------------------------- */
-static void apply_normalize_vjp(const float q[4], const float g[4], float out[4]) { /* optim.cu:10-21 */
-  float lsq = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
-  float l = sqrtf(lsq);
-  float inv = 1.f / (l * lsq);
-  float qw = q[0], qx = q[1], qy = q[2], qz = q[3];
-  float gw = g[0], gx = g[1], gy = g[2], gz = g[3];
-  float cc0 = -qw * qx, cc1 = -qx * qy, cc2 = -qy * qw, cs0 = -qw * qz, cs1 = -qx * qz, cs2 = -qy * qz;
-  out[0] = ((lsq - qw * qw) * gw + cc0 * gx + cc2 * gy + cs0 * gz) * inv;
-  out[1] = (cc0 * gw + (lsq - qx * qx) * gx + cc1 * gy + cs1 * gz) * inv;
-  out[2] = (cc2 * gw + cc1 * gx + (lsq - qy * qy) * gy + cs2 * gz) * inv;
-  out[3] = (cs0 * gw + cs1 * gx + cs2 * gy + (lsq - qz * qz) * gz) * inv;
+typedef struct { double m[9]; } dmat3;
+
+static dmat3 dm_mul(dmat3 A, dmat3 B) {
+  dmat3 C;
+  for (int r = 0; r < 3; r++)
+    for (int c = 0; c < 3; c++) C.m[3 * r + c] = A.m[3 * r] * B.m[c] + A.m[3 * r + 1] * B.m[3 + c] + A.m[3 * r + 2] * B.m[6 + c];
+  return C;
 }
 
-static void quat_to_mat_vjp(const float q[4], const float* m, float out[4]) { /* optim.cu:24-33 */
-  float qw = q[0], qx = q[1], qy = q[2], qz = q[3];
-  float v00 = m[0], v01 = m[1], v02 = m[2], v10 = m[3], v11 = m[4], v12 = m[5], v20 = m[6], v21 = m[7], v22 = m[8];
-  float w_grad = qx * (v21 - v12) + qy * (v02 - v20) + qz * (v10 - v01);
-  float x_grad = -2.f * qx * (v11 + v22) + qy * (v10 + v01) + qz * (v20 + v02) + qw * (v21 - v12);
-  float y_grad = qx * (v10 + v01) - 2.f * qy * (v00 + v22) + qz * (v21 + v12) + qw * (v02 - v20);
-  float z_grad = qx * (v20 + v02) + qy * (v21 + v12) - 2.f * qz * (v00 + v11) + qw * (v10 - v01);
-  out[0] = 2.f * w_grad; out[1] = 2.f * x_grad; out[2] = 2.f * y_grad; out[3] = 2.f * z_grad;
+static dmat3 dm_t(dmat3 A) {
+  dmat3 T;
+  for (int r = 0; r < 3; r++)
+    for (int c = 0; c < 3; c++) T.m[3 * r + c] = A.m[3 * c + r];
+  return T;
 }
 
-static sym2 inverse2x2_vjp(sym2 minv, sym2 v) { /* optim.cu:35-45 */
-  float tmp00 = -minv.c00 * v.c00 + -minv.c01 * v.c01;
-  float tmp01 = -minv.c01 * v.c00 + -minv.c11 * v.c01;
-  float tmp10 = -minv.c00 * v.c01 + -minv.c01 * v.c11;
-  float tmp11 = -minv.c01 * v.c01 + -minv.c11 * v.c11;
-  sym2 r;
-  r.c00 = tmp00 * minv.c00 + tmp10 * minv.c01;
-  r.c01 = tmp01 * minv.c00 + tmp11 * minv.c01;
-  r.c11 = tmp01 * minv.c01 + tmp11 * minv.c11;
-  return r;
+static dmat3 dm_rot(const double q[4]) { /* unit quaternion (w, x, y, z) */
+  const double w = q[0], x = q[1], y = q[2], z = q[3];
+  dmat3 R = {{1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y),
+              2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x),
+              2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)}};
+  return R;
 }
 
-/* optim.cu:48-88: d colour / d view direction, c[k][ch] coefficient-major. */
-static void sh_viewdir_vjp(int deg, const float* c, float x, float y, float z, const float vc[3], float g[3]) {
-  float gx = 0.f, gy = 0.f, gz = 0.f;
-#define DOTC(k) (c[(k) * 3] * vc[0] + c[(k) * 3 + 1] * vc[1] + c[(k) * 3 + 2] * vc[2])
-  if (deg >= 1) {
-    const float f0a = 0.4886025f;
-    float s_n1 = DOTC(1), s_z0 = DOTC(2), s_p1 = DOTC(3);
-    gx += -f0a * s_p1; gy += -f0a * s_n1; gz += f0a * s_z0;
-    if (deg >= 2) {
-      const float c2 = -1.0925485f, f1a = 0.54627424f;
-      float s_n2 = DOTC(4), s_n1b = DOTC(5), s_z0b = DOTC(6), s_p1b = DOTC(7), s_p2 = DOTC(8);
-      gx += 2.f * f1a * y * s_n2 + c2 * z * s_p1b + 2.f * f1a * x * s_p2;
-      gy += 2.f * f1a * x * s_n2 + c2 * z * s_n1b - 2.f * f1a * y * s_p2;
-      gz += c2 * y * s_n1b + 2.f * 0.9461747f * z * s_z0b + c2 * x * s_p1b;
-      if (deg >= 3) {
-        float z2 = z * z, x2 = x * x, y2 = y * y;
-        const float f2a = -0.5900436f, c1b = 1.4453057f, c0c = -2.285229f;
-        float f1b = c1b * z, f0c = c0c * z2 + 0.4570458f, f0c_dz = 2.f * c0c * z;
-        float s_n3 = DOTC(9), s_n2c = DOTC(10), s_n1c = DOTC(11), s_z0c = DOTC(12), s_p1c = DOTC(13), s_p2c = DOTC(14), s_p3 = DOTC(15);
-        float d12_z = 3.f * 1.8658817f * z2 - 1.119529f;
-        gx += f2a * 6.f * x * y * s_n3 + 2.f * f1b * y * s_n2c + f0c * s_p1c + 2.f * f1b * x * s_p2c + f2a * 3.f * (x2 - y2) * s_p3;
-        gy += f2a * 3.f * (x2 - y2) * s_n3 + 2.f * f1b * x * s_n2c + f0c * s_n1c + (-2.f) * f1b * y * s_p2c + f2a * (-6.f) * x * y * s_p3;
-        gz += 2.f * c1b * x * y * s_n2c + f0c_dz * y * s_n1c + d12_z * s_z0c + f0c_dz * x * s_p1c + c1b * (x2 - y2) * s_p2c;
-        if (deg >= 4) {
-          float fc1 = x2 - y2, fs1 = 2.f * x * y, fc2 = x * fc1 - y * fs1, fs2 = x * fs1 + y * fc1;
-          float f0d = z * (-4.683326f * z2 + 2.0071396f), f0d_dz = -14.049978f * z2 + 2.0071396f;
-          float f1c = 3.3116114f * z2 - 0.47308735f, f1c_dz = 2.f * 3.3116114f * z;
-          const float f2b_c = -1.7701308f; float f2b = f2b_c * z; const float f3a = 0.62583575f;
-          float p12 = z * (1.8658817f * z2 - 1.119529f), dp12 = 3.f * 1.8658817f * z2 - 1.119529f, dp6 = 2.f * 0.9461747f * z;
-          float dp20 = 1.9843135f * (p12 + z * dp12) - 1.0062306f * dp6;
-          float s_n4 = DOTC(16), s_n3d = DOTC(17), s_n2d = DOTC(18), s_n1d = DOTC(19), s_z0d = DOTC(20), s_p1d = DOTC(21), s_p2d = DOTC(22), s_p3d = DOTC(23), s_p4 = DOTC(24);
-          gx += f3a * 4.f * fs2 * s_n4 + f2b * 3.f * fs1 * s_n3d + f1c * 2.f * y * s_n2d + f0d * s_p1d + f1c * 2.f * x * s_p2d + f2b * 3.f * fc1 * s_p3d + f3a * 4.f * fc2 * s_p4;
-          gy += f3a * 4.f * fc2 * s_n4 + f2b * 3.f * fc1 * s_n3d + f1c * 2.f * x * s_n2d + f0d * s_n1d + f1c * (-2.f) * y * s_p2d + f2b * (-3.f) * fs1 * s_p3d + f3a * (-4.f) * fs2 * s_p4;
-          gz += f2b_c * fs2 * s_n3d + f1c_dz * fs1 * s_n2d + f0d_dz * y * s_n1d + dp20 * s_z0d + f0d_dz * x * s_p1d + f1c_dz * fc1 * s_p2d + f2b_c * fc2 * s_p3d;
-        }
-      }
-    }
-  }
-#undef DOTC
-  g[0] = gx; g[1] = gy; g[2] = gz;
+static void sh_basis_d(int deg, double x, double y, double z, double* b);
+
+/* colour(dir) . vc for the splat's coefficients (active degree deg) */
+static double sh_colour_dot(int deg, const float* c, const double dir[3], const double vc[3]) {
+  double b[25];
+  sh_basis_d(deg, dir[0], dir[1], dir[2], b);
+  double acc = 0.0;
+  const int K = (deg + 1) * (deg + 1);
+  for (int k = 0; k < K; k++) acc += b[k] * (c[3 * k] * vc[0] + c[3 * k + 1] * vc[1] + c[3 * k + 2] * vc[2]);
+  return acc;
 }
 
 void orc_vjp(const orc_model_t* m, const orc_cam_t* cam, int active_deg, const float* v_splat, const uint32_t* vis_flag,
@@ -713,110 +697,148 @@ void orc_vjp(const orc_model_t* m, const orc_cam_t* cam, int active_deg, const f
   if (deg < 0) deg = 0;
   const int kmax = (deg + 1) * (deg + 1);
   const int per = 11 + 3 * K;
+  dmat3 Rv;
+  for (int k = 0; k < 9; k++) Rv.m[k] = cam->R[k];
+  const dmat3 RvT = dm_t(Rv);
+  const double fx = cam->fx, fy = cam->fy;
   for (int i = 0; i < m->n; i++) {
     float* o = grad_out + (size_t)i * per;
     for (int k = 0; k < per; k++) o[k] = 0.f;
-    uint32_t vis = vis_flag[i];
-    int visible = vis != 0u && tile_count[i] != 0u;
-    float g[GRAD_LANES];
-    for (int k = 0; k < GRAD_LANES; k++) g[k] = vis ? v_splat[(size_t)i * GRAD_LANES + k] : 0.f;
-    int any = 0;
-    for (int k = 0; k < GRAD_LANES; k++) if (k != 9 && g[k] != 0.f) any = 1;
-    any = any && visible;
-    for (int k = 0; k < GRAD_LANES; k++) if (!finitef(g[k])) any = 0;
-    if (!any) continue;
-    const float* po = m->pos_op + (size_t)i * 4; const float* q = m->quat + (size_t)i * 4;
+    const float* gl = v_splat + (size_t)i * GRAD_LANES;
+    const int visible = vis_flag[i] != 0u && tile_count[i] != 0u;
+    int any = 0, finite = 1;
+    for (int k = 0; k < GRAD_LANES; k++) {
+      const float v = vis_flag[i] ? gl[k] : 0.f;
+      if (k != 9 && v != 0.f) any = 1;
+      if (!finitef(v)) finite = 0;
+    }
+    if (!(any && visible && finite)) continue; /* optim.cu:110-148 */
+    const float* po = m->pos_op + (size_t)i * 4;
+    const float* qf = m->quat + (size_t)i * 4;
     const float* ls = m->lscale + (size_t)i * 4;
     proj_t pr;
-    project_one(po, q, ls, cam, &pr);
+    project_one(po, qf, ls, cam, &pr);
     if (!pr.ok) continue;
-    float basis[25];
-    for (int k = 0; k < 25; k++) basis[k] = 0.f;
-    float ux = po[0] - cam->pos[0], uy = po[1] - cam->pos[1], uz = po[2] - cam->pos[2];
-    float ul = sqrtf(ux * ux + uy * uy + uz * uz);
-    float iul = 1.f / ul;
-    float vx = ux * iul, vy = uy * iul, vz = uz * iul;
-    sh_basis_f(deg, vx, vy, vz, basis);
-    for (int k = kmax; k < 25; k++) basis[k] = 0.f;
-    float vc[3] = {g[5], g[6], g[7]};
-    float v_v[3];
-    sh_viewdir_vjp(deg, m->sh + (size_t)i * K * 3, vx, vy, vz, vc, v_v);
-    float vdot = vx * v_v[0] + vy * v_v[1] + vz * v_v[2];
-    float v_mean_sh[3] = {(v_v[0] - vx * vdot) * (1.f / ul), (v_v[1] - vy * vdot) * (1.f / ul), (v_v[2] - vz * vdot) * (1.f / ul)};
-    float v_alpha = g[8];
-    float g_op = v_alpha * 1.f * pr.comp_floor * pr.sig * (1.f - pr.sig);
-    sym2 v_inv = {g[2], 0.5f * g[3], g[4]};
-    sym2 v_cov = inverse2x2_vjp(pr.conic, v_inv);
-    const float* Rv = cam->R;
-    float M[9];
-    for (int r = 0; r < 3; r++) { M[r * 3] = pr.Rq[r * 3] * pr.s[0]; M[r * 3 + 1] = pr.Rq[r * 3 + 1] * pr.s[1]; M[r * 3 + 2] = pr.Rq[r * 3 + 2] * pr.s[2]; }
-    float covar[9];
-    for (int r = 0; r < 3; r++)
-      for (int cc = 0; cc < 3; cc++) covar[r * 3 + cc] = M[r * 3] * M[cc * 3] + M[r * 3 + 1] * M[cc * 3 + 1] + M[r * 3 + 2] * M[cc * 3 + 2];
-    float RvC[9];
-    mat3_mul(Rv, covar, RvC);
-    float cov_c[9];
-    for (int r = 0; r < 3; r++)
-      for (int cc = 0; cc < 3; cc++) cov_c[r * 3 + cc] = RvC[r * 3] * Rv[cc * 3] + RvC[r * 3 + 1] * Rv[cc * 3 + 1] + RvC[r * 3 + 2] * Rv[cc * 3 + 2];
-    float mcx = pr.mc[0], mcy = pr.mc[1], mcz = pr.mc[2];
-    float inv_z = 1.f / mcz, inv_z2 = inv_z * inv_z, inv_z3 = inv_z2 * inv_z;
-    float v2x = g[0], v2y = g[1];
-    float vcov[2][2] = {{v_cov.c00, v_cov.c01}, {v_cov.c01, v_cov.c11}};
-    float tmp[2][3];
-    for (int r = 0; r < 2; r++)
-      for (int j = 0; j < 3; j++) tmp[r][j] = vcov[r][0] * pr.J[j] + vcov[r][1] * pr.J[3 + j];
-#define ROWDOT(r, cr) (tmp[r][0] * cov_c[(cr) * 3] + tmp[r][1] * cov_c[(cr) * 3 + 1] + tmp[r][2] * cov_c[(cr) * 3 + 2])
-    float vj00 = 2.f * ROWDOT(0, 0), vj11 = 2.f * ROWDOT(1, 1), vj20 = 2.f * ROWDOT(0, 2), vj21 = 2.f * ROWDOT(1, 2);
-#undef ROWDOT
-    float rx = mcx * inv_z, ry = mcy * inv_z;
-    float txc = mcz * fminf(fmaxf(rx, cam->lim_neg_x), cam->lim_pos_x), tyc = mcz * fminf(fmaxf(ry, cam->lim_neg_y), cam->lim_pos_y);
-    float v_mx = cam->fx * inv_z * v2x, v_my = cam->fy * inv_z * v2y;
-    float v_mz = -(cam->fx * mcx * v2x + cam->fy * mcy * v2y) * inv_z2;
-    if (!pr.clamp_x) v_mx += -cam->fx * inv_z2 * vj20; else v_mz += -cam->fx * inv_z3 * vj20 * txc;
-    if (!pr.clamp_y) v_my += -cam->fy * inv_z2 * vj21; else v_mz += -cam->fy * inv_z3 * vj21 * tyc;
-    v_mz += -cam->fx * inv_z2 * vj00 - cam->fy * inv_z2 * vj11 + 2.f * cam->fx * txc * inv_z3 * vj20 + 2.f * cam->fy * tyc * inv_z3 * vj21;
-    float vcc[9];
-    for (int r = 0; r < 3; r++)
-      for (int cc = 0; cc < 3; cc++) {
-        float s = 0.f;
-        for (int a = 0; a < 2; a++)
-          for (int b = 0; b < 2; b++) s += pr.J[a * 3 + r] * vcov[a][b] * pr.J[b * 3 + cc];
-        vcc[r * 3 + cc] = s;
+    double g[GRAD_LANES];
+    for (int k = 0; k < GRAD_LANES; k++) g[k] = gl[k];
+    /* ---- SH coefficients and the view-direction term */
+    const double dv[3] = {(double)po[0] - cam->pos[0], (double)po[1] - cam->pos[1], (double)po[2] - cam->pos[2]};
+    const double dlen = sqrt(dv[0] * dv[0] + dv[1] * dv[1] + dv[2] * dv[2]);
+    const double dir[3] = {dv[0] / dlen, dv[1] / dlen, dv[2] / dlen};
+    const double vc[3] = {g[5], g[6], g[7]};
+    double basis[25];
+    sh_basis_d(deg, dir[0], dir[1], dir[2], basis);
+    for (int k = 0; k < kmax; k++)
+      for (int ch = 0; ch < 3; ch++) o[11 + 3 * k + ch] = (float)(basis[k] * vc[ch]);
+    double gpos[3] = {0, 0, 0};
+    { /* d(colour . vc)/d p: moving p by dp turns dir by (I - dir dir^T) dp / |d| */
+      const float* coef = m->sh + (size_t)i * K * 3;
+      const double h = 1e-6;
+      for (int a = 0; a < 3; a++) {
+        double dp[3] = {dv[0], dv[1], dv[2]}, dm[3] = {dv[0], dv[1], dv[2]};
+        dp[a] += h * dlen;
+        dm[a] -= h * dlen;
+        const double lp = sqrt(dp[0] * dp[0] + dp[1] * dp[1] + dp[2] * dp[2]);
+        const double lm = sqrt(dm[0] * dm[0] + dm[1] * dm[1] + dm[2] * dm[2]);
+        const double up[3] = {dp[0] / lp, dp[1] / lp, dp[2] / lp}, um[3] = {dm[0] / lm, dm[1] / lm, dm[2] / lm};
+        gpos[a] = (sh_colour_dot(deg, coef, up, vc) - sh_colour_dot(deg, coef, um, vc)) / (2.0 * h * dlen);
       }
-    float t1[9];
+    }
+    /* ---- the covariance chain */
+    const double qn2 = (double)qf[0] * qf[0] + (double)qf[1] * qf[1] + (double)qf[2] * qf[2] + (double)qf[3] * qf[3];
+    const double qlen = sqrt(qn2);
+    const double qn[4] = {qf[0] / qlen, qf[1] / qlen, qf[2] / qlen, qf[3] / qlen};
+    const dmat3 Rq = dm_rot(qn);
+    const double f2 = (double)ls[3] * ls[3];
+    double var[3], sc[3];
+    for (int j = 0; j < 3; j++) {
+      var[j] = exp(2.0 * (double)ls[j]);
+      sc[j] = sqrt(var[j] + f2);
+    }
+    dmat3 M;
     for (int r = 0; r < 3; r++)
-      for (int cc = 0; cc < 3; cc++) t1[r * 3 + cc] = Rv[r] * vcc[cc] + Rv[3 + r] * vcc[3 + cc] + Rv[6 + r] * vcc[6 + cc];
-    float v_covar[9];
-    mat3_mul(t1, Rv, v_covar);
-    float v_M[9];
-    mat3_mul(v_covar, M, v_M);
-    for (int k = 0; k < 9; k++) v_M[k] *= 2.f;
-    /* g_pos = Rv^T v_mean_c + v_mean_sh */
-    float gpx = Rv[0] * v_mx + Rv[3] * v_my + Rv[6] * v_mz;
-    float gpy = Rv[1] * v_mx + Rv[4] * v_my + Rv[7] * v_mz;
-    float gpz = Rv[2] * v_mx + Rv[5] * v_my + Rv[8] * v_mz;
-    gpx = gpx + v_mean_sh[0]; gpy = gpy + v_mean_sh[1]; gpz = gpz + v_mean_sh[2];
-    float f2 = ls[3] * ls[3];
-    float vs0 = pr.Rq[0] * v_M[0] + pr.Rq[3] * v_M[3] + pr.Rq[6] * v_M[6];
-    float vs1 = pr.Rq[1] * v_M[1] + pr.Rq[4] * v_M[4] + pr.Rq[7] * v_M[7];
-    float vs2 = pr.Rq[2] * v_M[2] + pr.Rq[5] * v_M[5] + pr.Rq[8] * v_M[8];
-    float glx = vs0 * pr.s2_raw[0] / pr.s[0] + v_alpha * pr.opac * f2 / (pr.s2_raw[0] + f2);
-    float gly = vs1 * pr.s2_raw[1] / pr.s[1] + v_alpha * pr.opac * f2 / (pr.s2_raw[1] + f2);
-    float glz = vs2 * pr.s2_raw[2] / pr.s[2] + v_alpha * pr.opac * f2 / (pr.s2_raw[2] + f2);
-    float vR[9];
-    for (int r = 0; r < 3; r++) { vR[r * 3] = v_M[r * 3] * pr.s[0]; vR[r * 3 + 1] = v_M[r * 3 + 1] * pr.s[1]; vR[r * 3 + 2] = v_M[r * 3 + 2] * pr.s[2]; }
-    float qn2 = q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3];
-    float inv_qn = 1.f / sqrtf(qn2);
-    float qn[4] = {q[0] * inv_qn, q[1] * inv_qn, q[2] * inv_qn, q[3] * inv_qn};
-    float qg[4], gq[4];
-    quat_to_mat_vjp(qn, vR, qg);
-    apply_normalize_vjp(q, qg, gq);
-    int ok = finitef(gpx) && finitef(gpy) && finitef(gpz) && finitef(g_op) && finitef(glx) && finitef(gly) && finitef(glz) &&
-             finitef(gq[0] + gq[1] + gq[2] + gq[3]);
-    if (!ok) { gpx = gpy = gpz = g_op = glx = gly = glz = 0.f; gq[0] = gq[1] = gq[2] = gq[3] = 0.f; }
-    o[0] = gpx; o[1] = gpy; o[2] = gpz; o[3] = g_op; o[4] = gq[0]; o[5] = gq[1]; o[6] = gq[2]; o[7] = gq[3];
-    o[8] = glx; o[9] = gly; o[10] = glz;
-    for (int k = 0; k < K; k++) { o[11 + k * 3] = basis[k] * vc[0]; o[12 + k * 3] = basis[k] * vc[1]; o[13 + k * 3] = basis[k] * vc[2]; }
+      for (int j = 0; j < 3; j++) M.m[3 * r + j] = Rq.m[3 * r + j] * sc[j];
+    const dmat3 Sigma = dm_mul(M, dm_t(M));
+    const dmat3 Sc = dm_mul(dm_mul(Rv, Sigma), RvT);
+    double mc[3];
+    for (int r = 0; r < 3; r++) mc[r] = Rv.m[3 * r] * po[0] + Rv.m[3 * r + 1] * po[1] + Rv.m[3 * r + 2] * po[2] + cam->t[r];
+    const double z = mc[2], tx = mc[0] / z, ty = mc[1] / z;
+    const int clip_x = !(tx <= cam->lim_pos_x && tx >= cam->lim_neg_x);
+    const int clip_y = !(ty <= cam->lim_pos_y && ty >= cam->lim_neg_y);
+    const double txc = fmin(fmax(tx, cam->lim_neg_x), cam->lim_pos_x), tyc = fmin(fmax(ty, cam->lim_neg_y), cam->lim_pos_y);
+    const double J[2][3] = {{fx / z, 0.0, -fx * txc / z}, {0.0, fy / z, -fy * tyc / z}};
+    double cov[2][2];
+    for (int a = 0; a < 2; a++)
+      for (int b = 0; b < 2; b++) {
+        double acc = 0.0;
+        for (int r = 0; r < 3; r++)
+          for (int c = 0; c < 3; c++) acc += J[a][r] * Sc.m[3 * r + c] * J[b][c];
+        cov[a][b] = acc + (a == b ? 0.3 : 0.0);
+      }
+    const double det = cov[0][0] * cov[1][1] - cov[0][1] * cov[1][0];
+    const double Cn[2][2] = {{cov[1][1] / det, -cov[0][1] / det}, {-cov[1][0] / det, cov[0][0] / det}};
+    /* dL/dcov = -C Gc C, Gc the symmetric conic gradient (off-diagonal lane g3 counts both entries) */
+    const double Gc[2][2] = {{g[2], 0.5 * g[3]}, {0.5 * g[3], g[4]}};
+    double T2[2][2], Gcov[2][2];
+    for (int a = 0; a < 2; a++)
+      for (int b = 0; b < 2; b++) T2[a][b] = Cn[a][0] * Gc[0][b] + Cn[a][1] * Gc[1][b];
+    for (int a = 0; a < 2; a++)
+      for (int b = 0; b < 2; b++) Gcov[a][b] = -(T2[a][0] * Cn[0][b] + T2[a][1] * Cn[1][b]);
+    /* cov = J Sc J^T: dL/dJ = 2 Gcov J Sc, dL/dSc = J^T Gcov J */
+    double GJ[2][3];
+    for (int a = 0; a < 2; a++)
+      for (int c = 0; c < 3; c++) {
+        double acc = 0.0;
+        for (int b = 0; b < 2; b++)
+          for (int r = 0; r < 3; r++) acc += Gcov[a][b] * J[b][r] * Sc.m[3 * r + c];
+        GJ[a][c] = 2.0 * acc;
+      }
+    dmat3 GSc;
+    for (int r = 0; r < 3; r++)
+      for (int c = 0; c < 3; c++) {
+        double acc = 0.0;
+        for (int a = 0; a < 2; a++)
+          for (int b = 0; b < 2; b++) acc += J[a][r] * Gcov[a][b] * J[b][c];
+        GSc.m[3 * r + c] = acc;
+      }
+    /* pinhole: mean2d = (fx tx + cx, fy ty + cy); J00 = fx/z, J02 = -fx txc/z with txc = tx unless clamped */
+    double gmc[3];
+    gmc[0] = fx / z * g[0] + (clip_x ? 0.0 : -fx / (z * z) * GJ[0][2]);
+    gmc[1] = fy / z * g[1] + (clip_y ? 0.0 : -fy / (z * z) * GJ[1][2]);
+    gmc[2] = -fx * mc[0] / (z * z) * g[0] - fy * mc[1] / (z * z) * g[1] - fx / (z * z) * GJ[0][0] - fy / (z * z) * GJ[1][1] +
+             GJ[0][2] * (fx * txc / (z * z) + (clip_x ? 0.0 : fx * tx / (z * z))) +
+             GJ[1][2] * (fy * tyc / (z * z) + (clip_y ? 0.0 : fy * ty / (z * z)));
+    for (int a = 0; a < 3; a++) gpos[a] += RvT.m[3 * a] * gmc[0] + RvT.m[3 * a + 1] * gmc[1] + RvT.m[3 * a + 2] * gmc[2];
+    /* Sc = R_view Sigma R_view^T, Sigma = M M^T */
+    const dmat3 GSigma = dm_mul(dm_mul(RvT, GSc), Rv);
+    dmat3 GM = dm_mul(GSigma, M);
+    for (int k = 0; k < 9; k++) GM.m[k] *= 2.0;
+    /* M = R(q) diag(s): dL/ds_j = column j of R(q) . column j of GM; dL/dR = GM diag(s) */
+    double glog[3];
+    const double opac = pr.opac, sigm = pr.sig;
+    for (int j = 0; j < 3; j++) {
+      const double gs = Rq.m[j] * GM.m[j] + Rq.m[3 + j] * GM.m[3 + j] + Rq.m[6 + j] * GM.m[6 + j];
+      glog[j] = gs * var[j] / sc[j] + g[8] * opac * f2 / (var[j] + f2);
+    }
+    dmat3 GR;
+    for (int r = 0; r < 3; r++)
+      for (int j = 0; j < 3; j++) GR.m[3 * r + j] = GM.m[3 * r + j] * sc[j];
+    /* quaternion: entrywise derivatives of R(q) (optim.cu:24-33), then through q / |q| (optim.cu:10-21) */
+    const double w = qn[0], x = qn[1], y = qn[2], zq = qn[3];
+    const double* G = GR.m;
+    double gqn[4];
+    gqn[0] = 2 * (x * (G[7] - G[5]) + y * (G[2] - G[6]) + zq * (G[3] - G[1]));
+    gqn[1] = 2 * (-2 * x * (G[4] + G[8]) + y * (G[3] + G[1]) + zq * (G[6] + G[2]) + w * (G[7] - G[5]));
+    gqn[2] = 2 * (x * (G[3] + G[1]) - 2 * y * (G[0] + G[8]) + zq * (G[7] + G[5]) + w * (G[2] - G[6]));
+    gqn[3] = 2 * (x * (G[6] + G[2]) + y * (G[7] + G[5]) - 2 * zq * (G[0] + G[4]) + w * (G[3] - G[1]));
+    const double along = qn[0] * gqn[0] + qn[1] * gqn[1] + qn[2] * gqn[2] + qn[3] * gqn[3];
+    double gq[4];
+    for (int k = 0; k < 4; k++) gq[k] = (gqn[k] - qn[k] * along) / qlen;
+    const double glogit = g[8] * pr.comp_floor * sigm * (1.0 - sigm);
+    const double outv[11] = {gpos[0], gpos[1], gpos[2], glogit, gq[0], gq[1], gq[2], gq[3], glog[0], glog[1], glog[2]};
+    int ok = 1;
+    for (int k = 0; k < 11; k++) ok = ok && isfinite(outv[k]);
+    for (int k = 0; k < 11; k++) o[k] = ok ? (float)outv[k] : 0.f;
   }
 }
 

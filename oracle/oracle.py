@@ -266,6 +266,8 @@ def ref_loss(scene, params=None, camd=None, bg=None, want_img=False, floor=None,
     bg = np.asarray(scene.bg if bg is None else bg, np.float64)
     img = np.zeros((scene.W * scene.H, 4), np.float64) if want_img else None
     arrs = [np.ascontiguousarray(params[k], np.float64) for k in ("pos", "log_scale", "quat", "opacity", "sh")]
+    if floor is None and scene.lscale[:, 3].any():  # the scene's own Mip-Splatting floor
+        floor = scene.lscale[:, 3]
     fl = None if floor is None else np.ascontiguousarray(floor, np.float64)
     loss = lib().orc_ref_loss(scene.n, scene.degree, *[_ptr(a) for a in arrs], _ptr(fl), C.byref(cam), scene.W,
                               scene.H, _ptr(bg), _ptr(np.ascontiguousarray(scene.gt, np.uint32)), _ptr(scene.weights),
