@@ -256,14 +256,22 @@ def config3(seed: int | None = None, n: int = 1_000_000, masked: bool = False) -
                  composite=not masked, mask=masked, alpha_lane=not masked, match_alpha_weight=0.1, scale=1.5)
 
 
-def config4(seed: int | None = None, n: int = 3_000_000) -> Scene:
-    """3M splats, SH4, 1920x1080; a slab 0.5 deep facing the camera (high depth complexity); 8 poses."""
+def config4(seed: int | None = None, n: int = 3_000_000, shrink: int = 1) -> Scene:
+    """3M splats, SH4, 1920x1080; a slab 0.5 deep facing the camera (high depth complexity); 8 poses
+    (``extra_cams``, the first is ``cam``).
+
+    ``shrink`` = k > 1 is the same workload cut to a k-th of the size in each image direction: the slab's
+    width and height and the image's divide by k, the splat count by k^2; the focal length, the splat sizes,
+    the depths and the density per unit of slab area are unchanged, so every pixel still sees the same
+    depth complexity (fragments per pixel) through a narrower field of view."""
     rng = np.random.default_rng(0xB2C0 + 4 if seed is None else seed)
-    W, H = 1920, 1080
+    k = int(shrink)
+    n = n if k == 1 else n // (k * k)
+    W, H = 1920 // k, 1080 // k
     f = 1000.0
     pos = np.empty((n, 3))
-    pos[:, 0] = rng.uniform(-2.2, 2.2, n)
-    pos[:, 1] = rng.uniform(-1.25, 1.25, n)
+    pos[:, 0] = rng.uniform(-2.2 / k, 2.2 / k, n)
+    pos[:, 1] = rng.uniform(-1.25 / k, 1.25 / k, n)
     pos[:, 2] = rng.uniform(-0.25, 0.25, n)
     op = rng.normal(-2.0, 1.0, n)
     pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
@@ -280,7 +288,8 @@ def config4(seed: int | None = None, n: int = 3_000_000) -> Scene:
         cams.append(Camera(W, H, f, f, W / 2.0, H / 2.0, R, t))
     img = _smooth_target(rng, W, H).reshape(-1, 3)
     gt = _pack_rgba(img[:, 0], img[:, 1], img[:, 2], np.ones(W * H))
-    return Scene("cfg4", 4, pos_op, _rand_quat(rng, n), lscale, sh, cams[0], gt, extra_cams=cams)
+    name = "cfg4" if k == 1 else f"cfg4/{k}"
+    return Scene(name, 4, pos_op, _rand_quat(rng, n), lscale, sh, cams[0], gt, extra_cams=cams)
 
 
 def config5(seed: int | None = None, n: int = 500_000) -> Scene:
@@ -308,11 +317,14 @@ def config5(seed: int | None = None, n: int = 500_000) -> Scene:
     return Scene("cfg5", 3, pos_op, _rand_quat(rng, n), lscale, _fp16_bands(sh), cam, gt, sh_fp16=True)
 
 
-def fd_scene(seed: int, n: int = 24, masked: bool = False, degree: int = 2) -> Scene:
+def fd_scene(seed: int, n: int = 24, masked: bool = False, degree: int = 2, floor: bool = False) -> Scene:
     """The reference FD harness scene shape (tests/tests.cpp:23-59): 48x40, fx=fy=40, SH degree 2,
     means in [-0.6,0.6]x[-0.5,0.5]x[1.5,2.5], scales 0.05-0.13, jittered quaternions, opacity logits
     in [-2, 2], random RGBA target with u8 weights in [64, 255]. Transparent views use composite +
-    alpha lane (match weight 0.3), masked views the mask with scale 1.7 (tests.cpp:67-71)."""
+    alpha lane (match weight 0.3), masked views the mask with scale 1.7 (tests.cpp:67-71).
+
+    ``floor=True`` gives every splat a Mip-Splatting floor f in [0.02, 0.06] (``lscale[:, 3]``), the
+    frozen minimum scale of splat_math.cuh:232-237 that the reference's upload leaves at 0."""
     rng = np.random.default_rng(seed)
     W, H = 48, 40
     K = (degree + 1) ** 2
@@ -328,14 +340,56 @@ def fd_scene(seed: int, n: int = 24, masked: bool = False, degree: int = 2) -> S
     sh[:, 0, :] = un(n, 3) * 1.5
     if K > 1:
         sh[:, 1:, :] = un(n, K - 1, 3) * 0.3
+    if floor:
+        lscale[:, 3] = 0.02 + 0.04 * u(n)
     R, t = np.eye(3, dtype=np.float32).reshape(9), np.zeros(3, np.float32)
     cam = Camera(W, H, 40.0, 40.0, W / 2.0, H / 2.0, R, t)
     rgba = (u(W * H, 4) * 255).astype(np.uint32)
     gt = rgba[:, 0] | (rgba[:, 1] << 8) | (rgba[:, 2] << 16) | (rgba[:, 3] << 24)
     weights = (64 + u(W * H) * 191).astype(np.uint8)
-    return Scene(f"fd{seed}{'m' if masked else 't'}", degree, pos_op, quat, lscale, sh, cam, gt.astype(np.uint32),
+    tag = ("m" if masked else "t") + ("f" if floor else "")
+    return Scene(f"fd{seed}{tag}", degree, pos_op, quat, lscale, sh, cam, gt.astype(np.uint32),
                  weights, composite=not masked, mask=masked, alpha_lane=not masked, match_alpha_weight=0.3,
                  scale=1.7 if masked else 1.0, bg=(0.2, 0.1, 0.3))
+
+
+def clamp_scene(seed: int, n: int = 24, degree: int = 2) -> Scene:
+    """FD-harness camera and target with half the splats centred beyond the EWA Jacobian's tangent clamp
+    (x/z or y/z outside 15% past the frame, render.h:21-22): large splats (scales 0.22-0.36 at depth
+    ~2) whose centres lie left, right, above or below the frame but whose footprints reach into it, so
+    the clamped Jacobian and its VJP branches decide their gradients."""
+    sc = fd_scene(seed, n=n, degree=degree)
+    rng = np.random.default_rng(seed + 7919)
+    m = n // 2
+    z = 2.0 + (rng.random(m) * 2 - 1) * 0.3
+    side = rng.integers(0, 4, m)
+    # the limits are (1.15 W - cx) / fx = 0.78 and (1.15 H - cy) / fy = 0.65 for the 48x40, f = 40 camera
+    along = 0.82 + 0.3 * rng.random(m)
+    across = (rng.random(m) * 2 - 1) * 0.4
+    tx = np.where(side == 0, along, np.where(side == 1, -along, across))
+    ty = np.where(side == 2, along * 0.85, np.where(side == 3, -along * 0.85, across * 0.8))
+    sc.pos_op[:m, 0] = (tx * z).astype(np.float32)
+    sc.pos_op[:m, 1] = (ty * z).astype(np.float32)
+    sc.pos_op[:m, 2] = z.astype(np.float32)
+    sc.pos_op[:m, 3] = (rng.random(m) * 2.0 + 0.5).astype(np.float32)
+    sc.lscale[:m, :3] = np.log(0.22 + 0.14 * rng.random((m, 3))).astype(np.float32)
+    sc.name = f"clamp{seed}"
+    return sc
+
+
+def multiview_fd_scene(seed: int, views: int = 3, degree: int = 2) -> Scene:
+    """An FD-harness scene seen from ``views`` poses (``extra_cams``): the identity camera and small
+    rotations / translations of it, all framing the splats. The target image is shared by the views."""
+    sc = fd_scene(seed, degree=degree)
+    cams = [sc.cam]
+    for v in range(1, views):
+        ang = 0.12 * v * (1 if v % 2 else -1)
+        eye = (2.0 * math.sin(ang), 0.1 * v, 2.0 - 2.0 * math.cos(ang))
+        R, t = look_at(eye, (0.0, 0.0, 2.0))
+        cams.append(Camera(sc.W, sc.H, 40.0, 40.0, sc.W / 2.0, sc.H / 2.0, R, t))
+    sc.extra_cams = cams
+    sc.name = f"mv{seed}x{views}"
+    return sc
 
 
 CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}

@@ -6,14 +6,22 @@ mismatch names its stage. Tolerances:
 * projection outputs, tile counts, hit info, depth order, count scan, tile key/value lists and tile
   ranges: bit-exact (integer / index work and the fp32 projection both sides evaluate identically);
 * rendered RGBA: max abs error <= 1e-4 vs the fp32 oracle (the GPU uses the hardware exponential; observed
-  ~2e-7 at config 1 and ~1e-5 over the long lists of config 3 at full size);
+  ~2e-7 at config 1 and ~1e-5 over the long lists of config 3 at full size) at every pixel whose last
+  composited fragment agrees; at most 1e-5 of the pixels may terminate one fragment apart (T (1 - alpha)
+  within rounding of the 1e-4 stop: the render's non-smooth points, where the extra fragment's whole
+  contribution differs);
+* rendered RGBA against the double-precision brute force (the reference's tests/reference.cpp algorithm,
+  oracle orc_ref_loss) directly: max abs error <= 1e-4 (check_rgba_fp64);
 * loss value: relative 1e-4 (the kernel evaluates SSIM in fp32, where sigma^2 = E[x^2] - mu^2 cancels;
-  the oracle in fp64); per-pixel gradient: <= 1e-4 of the largest |v_out|, allowed to miss in at most 1e-4
-  of the entries;
+  the oracle in fp64); per-pixel gradient: <= LOSS_GRAD_TOL of the largest |v_out| everywhere except where
+  the L1 term's sign flips, i.e. where the prediction equals the effective target to 1e-6 (the fp32 and
+  fp64 evaluations of p - g may then round to opposite signs); the count above 1e-4 is reported;
 * v_splat: <= 2e-3 of each lane's largest |value| (float atomics sum in arbitrary order; mode 1 reduces
-  through fp16 hi/lo MFMA products);
-* parameter gradients from the GPU's own v_splat: <= 1e-3 of each column's largest |value| (the kernel
-  contracts to FMA, the oracle does not; the projection VJP has cancellation-prone terms, observed ~1e-4).
+  through fp16 hi/lo MFMA products), and per-entry relative error percentiles over the entries above
+  1e-3 of their lane's maximum: 99th percentile <= 1e-3;
+* parameter gradients from the GPU's own v_splat: <= 1e-3 of each column's largest |value| (two different
+  derivations of the projection VJP, the kernel's from the semi-axis form and the oracle's restating the
+  reference's world-covariance chain), and per-entry relative error percentiles as for v_splat.
 """
 from __future__ import annotations
 
@@ -56,14 +64,55 @@ def check_forward(r, pr, bn, W, H, bg, tol=1e-4):
     rgba = r.read("out_rgba")
     T = r.read("out_feat")[:, 3]
     last = r.read("last_idx")
-    err = float(np.abs(rgba - fw["out_rgba"]).max()) if len(rgba) else 0.0
-    assert err <= tol, f"rgba max abs err {err}"
-    mism = float((last != fw["last_idx"]).mean())
-    assert mism <= 1e-4, f"last_idx mismatch fraction {mism}"
+    d = np.abs(rgba - fw["out_rgba"]).max(axis=1) if len(rgba) else np.zeros(0)
+    # a termination flip: T (1 - alpha) lands within rounding of the 1e-4 stop on one side only, and one
+    # side composites a fragment more (its whole contribution differs: a non-smooth point of the render)
+    flip = last != fw["last_idx"]
+    err = float(d[~flip].max()) if (~flip).any() else 0.0
+    assert err <= tol, f"rgba max abs err {err} outside termination flips"
+    assert flip.mean() <= 1e-5, f"last_idx mismatch fraction {flip.mean()}"
+    if flip.any():
+        emit(f"    {int(flip.sum())} termination flips of {len(last)} pixels (rgba differs by up to {float(d[flip].max()):.2e})")
     ranges = r.read("tile_ranges")
     rm = float((ranges != fw["tile_ranges"]).any(1).mean())
     assert rm <= 1e-3, f"shrunk tile range mismatch fraction {rm}"
     return dict(out_rgba=rgba, out_T=T, last_idx=last, tile_ranges=ranges, err=err)
+
+
+# Per-entry bound on v_out relative to its largest entry. The fp32 SSIM statistics (sigma^2 = E[x^2] -
+# mu^2 over 11x11 windows) cancel in nearly flat windows: observed worst 6.1e-4 at 1080p (135 of 8.3M
+# entries above 1e-4).
+LOSS_GRAD_TOL = 1e-3
+
+
+def effective_target(scene, bg):
+    """The loss's per-channel target (rgb composited over bg for transparent views, and alpha)."""
+    g = np.ascontiguousarray(scene.gt, np.uint32)
+    ch = np.stack([(g >> np.uint32(8 * k)) & np.uint32(0xFF) for k in range(4)], 1).astype(np.float32) / np.float32(255)
+    if scene.composite:
+        ch[:, :3] += (1 - ch[:, 3:4]) * np.asarray(bg, np.float32)[None, :]
+    return ch
+
+
+def rel_percentiles(got, ref, floor_frac=1e-3):
+    """Per-entry relative error over the entries whose |ref| exceeds floor_frac of their column's max."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    col = np.abs(ref).max(axis=0, keepdims=True)
+    sel = np.abs(ref) > floor_frac * col
+    if not sel.any():
+        return dict(p50=0.0, p99=0.0, max=0.0, n=0)
+    rel = np.abs(got - ref)[sel] / np.abs(ref)[sel]
+    return dict(p50=float(np.percentile(rel, 50)), p99=float(np.percentile(rel, 99)), max=float(rel.max()),
+                n=int(sel.sum()))
+
+
+def check_rgba_fp64(rgba, scene, bg, tol=1e-4):
+    """GPU image against the double-precision brute-force render (every splat, every pixel, no tiles)."""
+    _, img = O.ref_loss(scene, bg=bg, want_img=True)
+    err = float(np.abs(np.asarray(rgba, np.float64) - img).max())
+    assert err <= tol, f"rgba vs fp64 brute force: max abs err {err:.3e}"
+    return err
 
 
 def check_loss(r, scene, rgba, grad_scale, bg):
@@ -72,8 +121,12 @@ def check_loss(r, scene, rgba, grad_scale, bg):
     assert abs(loss - ref) <= 1e-4 * abs(ref) + 1e-9, f"loss {loss} vs oracle {ref}"
     v = r.read("v_out")
     scale = float(np.abs(v_ref).max()) + 1e-30
-    bad = np.abs(v - v_ref) > 1e-4 * scale
-    assert bad.mean() <= 1e-4, f"v_out: {bad.sum()} entries off (max {np.abs(v - v_ref).max() / scale:.2e} rel)"
+    diff = np.abs(v - v_ref) / scale
+    flip = np.abs(np.asarray(rgba, np.float32) - effective_target(scene, bg)) < 1e-6
+    worst = float(np.where(flip, 0.0, diff).max()) if diff.size else 0.0
+    emit(f"    v_out: worst {worst:.2e} of max outside {int((flip & (diff > LOSS_GRAD_TOL)).sum())} L1 sign flips; "
+         f"{int((diff > 1e-4).sum())} of {diff.size} entries above 1e-4")
+    assert worst <= LOSS_GRAD_TOL, f"v_out: worst error {worst:.2e} of the largest gradient beyond L1 sign flips"
     return loss, v
 
 
@@ -92,6 +145,10 @@ def check_backward(r, scene, pr, bn, fw, v_out, W, H, bg, mode, grad_scale):
     err = np.abs(vs - ref_vs) / lane_scale
     worst = float(err.max()) if err.size else 0.0
     assert worst <= 2e-3, f"v_splat mode {mode}: worst lane-relative err {worst:.2e} at lane {int(err.max(0).argmax())}"
+    pc = rel_percentiles(vs[:, :10], ref_vs[:, :10])
+    emit(f"    v_splat lane-max err {worst:.2e}; per-entry rel p50 {pc['p50']:.1e} p99 {pc['p99']:.1e} "
+         f"max {pc['max']:.1e} over {pc['n']}")
+    assert pc["p99"] <= 1e-3, f"v_splat per-entry 99th percentile rel err {pc['p99']:.2e}"
     return vs, vf, worst
 
 
@@ -106,13 +163,19 @@ def check_vjp(r, scene, camd, vs, vf, tile_count):
         i, k = np.unravel_index(int(rel.argmax()), rel.shape)
         raise AssertionError(f"grads vs oracle VJP (same v_splat): {err:.2e} at splat {i} column {k}: "
                              f"gpu {g[i, k]:.6g} oracle {ref[i, k]:.6g} column max {col[k]:.3g}")
+    pc = rel_percentiles(g, ref)
+    emit(f"    grads column-max err {err:.2e}; per-entry rel p50 {pc['p50']:.1e} p99 {pc['p99']:.1e} "
+         f"max {pc['max']:.1e} over {pc['n']}")
+    assert pc["p99"] <= 1e-3, f"grads per-entry 99th percentile rel err {pc['p99']:.2e}"
     assert not r.read("vis_flag").any(), "vis_flag not cleared by the VJP"
     assert not r.read("v_splat").any(), "v_splat not cleared by the VJP"
     return g
 
 
-def full_check(scene, mode=1, bg=None, loss=True, backward=True):
-    """Run every stage on the GPU and check it; returns a dict of GPU outputs."""
+def full_check(scene, mode=1, bg=None, loss=True, backward=True, fp64_rgba=False):
+    """Run every stage on the GPU and check it; returns a dict of GPU outputs. fp64_rgba also checks the
+    image directly against the double-precision brute force (small scenes: it visits every splat per
+    pixel)."""
     bg = scene.bg if bg is None else bg
     W, H = scene.W, scene.H
     gs = 3.0 * W * H if mode == 1 else 1.0
@@ -129,6 +192,9 @@ def full_check(scene, mode=1, bg=None, loss=True, backward=True):
         r.raster_fwd(bg=bg)
         fw = check_forward(r, pr, bn, W, H, bg)
         out = dict(M=bn["M"], rgba_err=fw["err"])
+        if fp64_rgba:
+            out["rgba_err64"] = check_rgba_fp64(fw["out_rgba"], scene, bg)
+            emit(f"    rgba vs fp64 brute force {out['rgba_err64']:.2e}")
         if loss:
             emit(f"  [{scene.name}] loss")
             out["loss"], v = check_loss(r, scene, fw["out_rgba"], gs, bg)

@@ -2,23 +2,21 @@
 finite differences of the fp64 brute-force oracle, the reference's own gradient test
 (tests/tests.cpp:386-442) with the north-star bar: relative error <= 1e-3. As in the reference, a sample
 whose finite differences at eps and 4*eps disagree by more than 10% sits on a non-smooth point (a fragment
-crossing the 1/255 cutoff or the transmittance stop) and is skipped; gradients below 1e-9 in absolute
-difference are compared absolutely."""
+crossing the 1/255 cutoff or the transmittance stop) and is skipped (tests/fd_util.py states the absolute
+floor). Beyond the reference's scenes (SH degree 2, no floor, no clamped splat) the cases cover SH degrees
+3 and 4, the Mip-Splatting floor, splats past the tangent clamp and the fp32 anchor backward."""
 import numpy as np
 import pytest
 
 from b2ctrain_amd import _native
 from b2ctrain_amd import scenes as S
-from oracle import oracle as O
+from tests.fd_util import fd_compare
 from tests.gpu_harness import emit
 
 pytestmark = pytest.mark.gpu
 
-REL_TOL = 1e-3
-ABS_FLOOR = 1e-9
 
-
-def fd_compare(scene, mode, every=2, sh_every=5, eps=1e-5, max_splats=None):
+def gpu_gradients(scene, mode=1):
     r = _native.Renderer(scene)
     gs = 3.0 * scene.W * scene.H if mode == 1 else 1.0
     try:
@@ -28,67 +26,61 @@ def fd_compare(scene, mode, every=2, sh_every=5, eps=1e-5, max_splats=None):
         r.zero("vis_flag")
         r.backward(mode=mode, grad_scale=gs)
         r.vjp()
-        an = r.read("grads")
+        return r.read("grads")
     finally:
         r.close()
-    P0 = O.scene_params64(scene)
-    per = 11 + 3 * scene.K
-    bad, checked, skipped, worst = [], 0, 0, 0.0
-    n = scene.n if max_splats is None else min(scene.n, max_splats)
-    for i in range(0, n, every):
-        for q in range(per):
-            if q >= 11 and (q - 11) % sh_every:
-                continue
 
-            def at(delta):
-                P = {k: v.copy() for k, v in P0.items()}
-                if q < 3:
-                    P["pos"][i, q] += delta
-                elif q == 3:
-                    P["opacity"][i] += delta
-                elif q < 8:
-                    P["quat"][i, q - 4] += delta
-                elif q < 11:
-                    P["log_scale"][i, q - 8] += delta
-                else:
-                    P["sh"][i, q - 11] += delta
-                return O.ref_loss(scene, params=P)
 
-            fd = (at(eps) - at(-eps)) / (2 * eps)
-            fd4 = (at(4 * eps) - at(-4 * eps)) / (8 * eps)
-            if abs(fd - fd4) > 0.1 * max(abs(fd), abs(fd4)) + 1e-9:
-                skipped += 1
-                continue
-            a = float(an[i, q])
-            d = abs(fd - a)
-            den = max(abs(fd), abs(a))
-            rel = d / den if den > 0 else 0.0
-            checked += 1
-            if rel > REL_TOL and d > ABS_FLOOR:
-                bad.append((i, q, a, fd, rel))
-            if d > ABS_FLOOR:
-                worst = max(worst, rel)
-    return checked, skipped, bad, worst
+def run_fd(scene, mode=1, min_checked=150, **kw):
+    an = gpu_gradients(scene, mode)
+    checked, skipped, bad, worst = fd_compare(scene, an, **kw)
+    emit(f"  checked {checked} skipped {skipped} worst rel {worst:.2e}")
+    assert checked > min_checked
+    assert not bad, f"{len(bad)} mismatches, e.g. {bad[:5]}"
 
 
 @pytest.mark.parametrize("seed,masked,degree", [(1234, False, 2), (1235, True, 2), (1236, False, 3)])
 def test_fd_harness_scenes(seed, masked, degree):
     sc = S.fd_scene(seed, masked=masked, degree=degree)
     emit(f"FD {sc.name} deg={degree}")
-    checked, skipped, bad, worst = fd_compare(sc, mode=1)
-    emit(f"  checked {checked} skipped {skipped} worst rel {worst:.2e}")
-    assert checked > 150
-    assert not bad, f"{len(bad)} mismatches, e.g. {bad[:5]}"
+    run_fd(sc)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_fd_mip_floor(masked):
+    """Every splat has a Mip-Splatting floor (lscale.w > 0): the floor enters the semi-axes and the
+    opacity factor of the projection and both VJP terms of the log-scale gradient."""
+    sc = S.fd_scene(1238 + 3 * masked, floor=True, masked=masked, degree=3 if masked else 2)
+    emit(f"FD {sc.name} floor")
+    run_fd(sc)
+
+
+def test_fd_sh_degree4():
+    sc = S.fd_scene(1239, degree=4)
+    emit(f"FD {sc.name} SH4")
+    run_fd(sc, sh_every=3)
+
+
+def test_fd_tangent_clamp():
+    """Half the splats are centred past the EWA Jacobian's tangent clamp; every parameter of those is
+    checked (the clamped branches of the pinhole VJP)."""
+    sc = S.clamp_scene(1240)
+    emit(f"FD {sc.name}: clamped splats")
+    run_fd(sc, every=1, sh_every=7, max_splats=sc.n // 2, min_checked=100)
 
 
 def test_fd_config1():
     sc = S.config1()
     sc.bg = (0.3, 0.3, 0.3)
     emit("FD config1 (every 128th splat)")
-    checked, skipped, bad, worst = fd_compare(sc, mode=1, every=128)
-    emit(f"  checked {checked} skipped {skipped} worst rel {worst:.2e}")
-    assert checked > 60
-    assert not bad, f"{len(bad)} mismatches, e.g. {bad[:5]}"
+    run_fd(sc, every=128, min_checked=60)
+
+
+def test_fd_fp32_anchor_backward():
+    """The fp32 anchor backward (mode 0) through the same FD bar."""
+    sc = S.fd_scene(1236, degree=3)
+    emit(f"FD {sc.name} mode 0")
+    run_fd(sc, mode=0)
 
 
 def test_sparse_gradient_write_leaves_rows_without_gradient():

@@ -1,9 +1,12 @@
 """GPU parity: every stage of the HIP path against the CPU oracle (tests/gpu_harness.py states the bars),
-on the five BASELINE configurations (reduced splat counts where the CPU oracle would be slow, full size for
-configuration 3) and on the reference's FD-harness scene shape."""
+on the five BASELINE configurations (configurations 2, 3 and 5 also at full size; 4 at 30k splats here
+and as an 8-view workload in test_gpu_multiview.py), on the reference's FD-harness scene shape and on
+scenes with a Mip-Splatting floor, SH degree 4 and splats past the tangent clamp. The small scenes also
+check the image directly against the double-precision brute force."""
 import numpy as np
 import pytest
 
+from b2ctrain_amd import _native
 from b2ctrain_amd import scenes as S
 from tests.gpu_harness import emit, full_check
 
@@ -15,7 +18,7 @@ def test_config1_all_stages(mode):
     sc = S.config1()
     sc.bg = (0.25, 0.5, 0.75)
     emit(f"config1 mode={mode}")
-    out = full_check(sc, mode=mode)
+    out = full_check(sc, mode=mode, fp64_rgba=True)
     assert out["M"] > 1000
 
 
@@ -23,13 +26,48 @@ def test_config1_all_stages(mode):
 def test_fd_scene_all_stages(seed, masked, degree):
     sc = S.fd_scene(seed, masked=masked, degree=degree)
     emit(f"fd scene {sc.name} deg={degree}")
-    full_check(sc, mode=1)
+    full_check(sc, mode=1, fp64_rgba=True)
 
 
-def test_config2_subset():
-    sc = S.config2(n=20_000)
+@pytest.mark.parametrize("make", [lambda: S.fd_scene(1238, floor=True), lambda: S.fd_scene(1241, degree=3, floor=True, masked=True),
+                                  lambda: S.clamp_scene(1240), lambda: S.fd_scene(1239, degree=4)],
+                         ids=["floor", "floor_masked", "clamp", "sh4"])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_extension_scenes_all_stages(make, mode):
+    """Projection bit-exact with a nonzero floor on every splat, with clamped Jacobians and at SH degree 4;
+    every later stage at its bar, in both backward modes."""
+    sc = make()
+    emit(f"{sc.name} mode={mode}")
+    out = full_check(sc, mode=mode, fp64_rgba=True)
+    assert out["M"] > 50
+
+
+def test_empty_model():
+    """A model with no splats (every one pruned): forward, loss, both backward modes and the VJP run and
+    leave a background-only image, with no list to walk."""
+    sc = S.fd_scene(1234).subset(0)
+    emit("empty model")
+    r = _native.Renderer(sc)
+    try:
+        r.forward()
+        rgba = r.read("out_rgba")
+        assert np.allclose(rgba[:, :3], np.asarray(sc.bg, np.float32)) and (rgba[:, 3] == 0).all()
+        assert r.info().num_isect == 0
+        r.loss(grad_scale=3.0 * sc.W * sc.H)
+        for mode in (0, 1):
+            r.backward(mode=mode, grad_scale=3.0 * sc.W * sc.H)
+        r.vjp()
+        r.step()
+        r.sync()
+    finally:
+        r.close()
+
+
+@pytest.mark.timeout(600)
+def test_config2_full_size():
+    sc = S.config2()
     sc.bg = (0.1, 0.1, 0.1)
-    emit("config2 n=20000")
+    emit("config2 full size (100k splats, 800x800, SH3)")
     full_check(sc, mode=1)
 
 
@@ -54,6 +92,17 @@ def test_config5_subset_fp16_big_splats():
     assert out["M"] > 0
 
 
+@pytest.mark.timeout(900)
+def test_config5_full_size():
+    """500k splats at 3840x2160 with fp16 bands, ~25k huge anisotropic splats (62M intersections): far
+    beyond the initial intersection capacity, tile lists thousands long, sentinel-free big-splat emit."""
+    sc = S.config5()
+    emit("config5 full size (500k splats, 3840x2160, fp16 bands)")
+    out = full_check(sc, mode=1)
+    assert out["M"] > 1 << 25
+
+
+@pytest.mark.timeout(600)
 def test_config3_full_size():
     sc = S.config3()
     sc.bg = (0.5, 0.5, 0.5)

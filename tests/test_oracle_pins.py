@@ -153,25 +153,32 @@ def test_tile_hit_is_the_exact_box_test():
 
 # ---------------------------------------------------------------------------------------------- projection
 def _ewa_numpy(scene, camd):
-    """Independent fp64 EWA projection: cov3d = R S S R^T, Jacobian of the pinhole map by central
-    differences, cov2d = J W cov3d W^T J^T + 0.3 I."""
+    """Independent fp64 EWA projection: per-axis scale sqrt(exp(2 l) + f^2) with the Mip-Splatting floor f
+    and the opacity factor sqrt(prod exp(2 l) / prod (exp(2 l) + f^2)) (splat_math.cuh:232-237), cov3d =
+    R S S R^T, the Jacobian of the pinhole map by central differences at the centre with its tangent
+    clamped to 15% past the frame (render.h:21-22: the clamped Jacobian is the pinhole map's Jacobian at
+    the clamped point), cov2d = J W cov3d W^T J^T + 0.3 I."""
     Rv = np.asarray(camd["R"], np.float64).reshape(3, 3)
     t = np.asarray(camd["t"], np.float64)
     fx, fy, cx, cy = (float(camd[k]) for k in ("fx", "fy", "cx", "cy"))
+    lim = [float(camd[k]) for k in ("lim_neg_x", "lim_pos_x", "lim_neg_y", "lim_pos_y")]
     out = []
     for i in range(scene.n):
         p = scene.pos_op[i, :3].astype(np.float64)
         mc = Rv @ p + t
         q = scene.quat[i].astype(np.float64)
         Rq = Rotation.from_quat([q[1], q[2], q[3], q[0]]).as_matrix()
-        s = np.exp(scene.lscale[i, :3].astype(np.float64))
-        cov3 = Rq @ np.diag(s * s) @ Rq.T
+        var = np.exp(2.0 * scene.lscale[i, :3].astype(np.float64))
+        f2 = float(scene.lscale[i, 3]) ** 2
+        cov3 = Rq @ np.diag(var + f2) @ Rq.T
+        comp = math.sqrt(np.prod(var) / np.prod(var + f2))
         f = lambda v: np.array([fx * v[0] / v[2] + cx, fy * v[1] / v[2] + cy])
+        at = np.array([np.clip(mc[0] / mc[2], lim[0], lim[1]) * mc[2], np.clip(mc[1] / mc[2], lim[2], lim[3]) * mc[2], mc[2]])
         h = 1e-6 * mc[2]
-        J = np.stack([(f(mc + h * e) - f(mc - h * e)) / (2 * h) for e in np.eye(3)], 1)
+        J = np.stack([(f(at + h * e) - f(at - h * e)) / (2 * h) for e in np.eye(3)], 1)
         cov2 = J @ Rv @ cov3 @ Rv.T @ J.T + 0.3 * np.eye(2)
         conic = np.linalg.inv(cov2)
-        op = 1 / (1 + math.exp(-float(scene.pos_op[i, 3])))
+        op = comp / (1 + math.exp(-float(scene.pos_op[i, 3])))
         d = p - np.asarray(camd["pos"], np.float64)
         d /= np.linalg.norm(d)
         basis = np.array([_real_sh_3dgs(l, m, d) for l in range(scene.degree + 1) for m in range(-l, l + 1)])
@@ -180,19 +187,21 @@ def _ewa_numpy(scene, camd):
     return out
 
 
-@pytest.mark.parametrize("make", [lambda: S.config1(), lambda: S.fd_scene(1236, degree=3), lambda: S.config2(n=300)])
+@pytest.mark.parametrize("make", [lambda: S.config1(), lambda: S.fd_scene(1236, degree=3), lambda: S.config2(n=300),
+                                  lambda: S.fd_scene(1238, floor=True), lambda: S.fd_scene(1239, degree=4),
+                                  lambda: S.clamp_scene(1240)],
+                         ids=["cfg1", "fd1236", "cfg2", "floor", "sh4", "clamp"])
 def test_projection_matches_numpy_ewa(make):
     sc = make()
     camd = S.camera_gpu(sc.cam)
     pr = O.project(sc, camd)
     ref = _ewa_numpy(sc, camd)
-    checked = 0
+    checked = clamped = 0
     for i, (m2, conic, op, z, col, mc) in enumerate(ref):
         if pr["tile_count"][i] == 0:
             continue
         rx, ry = mc[0] / mc[2], mc[1] / mc[2]
-        if not (camd["lim_neg_x"] < rx < camd["lim_pos_x"] and camd["lim_neg_y"] < ry < camd["lim_pos_y"]):
-            continue  # the tangent clamp changes J; the numerical Jacobian is unclamped
+        clamped += not (camd["lim_neg_x"] < rx < camd["lim_pos_x"] and camd["lim_neg_y"] < ry < camd["lim_pos_y"])
         p0, p1, p2 = pr["proj0"][i], pr["proj1"][i], pr["proj2"][i]
         assert np.allclose(p0[:2], m2, rtol=1e-5, atol=1e-3)
         got = np.array([[p0[2], p0[3]], [p0[3], p1[0]]])
@@ -202,6 +211,10 @@ def test_projection_matches_numpy_ewa(make):
         assert np.allclose(p2[:3], col, atol=1e-5)
         checked += 1
     assert checked >= 10
+    if sc.name.startswith("clamp"):
+        assert clamped >= 8  # the clamped Jacobian is what is being checked
+    if sc.lscale[:, 3].any():
+        assert (pr["proj1"][pr["tile_count"] > 0, 1] < 1 / (1 + np.exp(-sc.pos_op[pr["tile_count"] > 0, 3])) * 0.999).all()
 
 
 # ---------------------------------------------------------------------------------------------- binning
