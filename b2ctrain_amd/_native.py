@@ -69,7 +69,7 @@ EXPORTS = [
     "b2c_scan_temp_bytes", "b2c_hip_scan_counts", "b2c_hip_emit", "b2c_hip_tile_ranges", "b2c_hip_raster_fwd",
     "b2c_hip_raster_bwd", "b2c_hip_photometric", "b2c_loss_partials", "b2c_hip_accumulate_loss", "b2c_hip_vjp",
     "b2c_hip_fill_u32", "b2c_hip_model_scatter", "b2c_hip_model_gather", "b2c_hip_planar_regrow",
-    "b2c_hip_model_set_floor",
+    "b2c_hip_model_set_floor", "b2c_hip_photometric_noalloc",
 ]
 
 _lib = None

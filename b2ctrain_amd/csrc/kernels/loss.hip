@@ -10,6 +10,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 namespace b2c {
 namespace dev {
 namespace {
@@ -440,6 +442,47 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum, a->assign,
                                                                  a->running);
   return (int)hipGetLastError();
+}
+
+// ---- allocation-free entry point: the per-workgroup partials live in a fixed device array ----
+// Each GPU the library runs on holds its own copy of `scratch` until the process ends. Host code must not
+// pass the array's name to a kernel (on the host it is only a stand-in symbol): the device address comes
+// from hipGetSymbolAddress, once per device with that device current, and is kept per device.
+static __device__ __align__(256) float scratch[B2C_LOSS_STATIC_PARTIALS];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[MAX_DEVICES] = {};
+
+hipError_t device_scratch(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int b2c_hip_photometric_noalloc(const b2c_loss_args* a, hipStream_t stream) {
+  if (a->W <= 0 || a->H <= 0) return 0;
+  if (b2c_loss_partials(a->W, a->H) > (size_t)B2C_LOSS_STATIC_PARTIALS) return (int)hipErrorInvalidValue;
+  float* partials = nullptr;
+  const hipError_t e = device_scratch(&partials);
+  if (e != hipSuccess) return (int)e;
+  b2c_loss_args b = *a;
+  b.partials = partials;  // every entry the reduce reads is written by this call's workgroups first
+  return b2c_hip_photometric(&b, stream);
 }
 
 extern "C" size_t b2c_loss_partials(int W, int H) {

@@ -213,6 +213,17 @@ typedef struct b2c_loss_args {
 size_t b2c_loss_partials(int W, int H);
 int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream);
 
+/* Allocation-free variant of b2c_hip_photometric. It has no counterpart in the reference: it is for callers
+ * that cannot allocate device memory or pass a workspace (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). a->partials is ignored; the per-workgroup partial sums live in a
+ * fixed device array of B2C_LOSS_STATIC_PARTIALS floats (1 MiB) that each GPU holds for the life of the
+ * process, so images with b2c_loss_partials(W, H) above that (about 160 megapixels) are rejected with
+ * hipErrorInvalidValue before any work is queued. No hipMalloc, hipFree or allocating routine is called.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller. Results are bit-identical to b2c_hip_photometric. */
+#define B2C_LOSS_STATIC_PARTIALS (1 << 18)
+int b2c_hip_photometric_noalloc(const b2c_loss_args* a, hipStream_t stream);
+
 /* accumulate_kernel (loss.cu:317,324): a[2] += a[0] + a[1]; a[3] += 1. */
 int b2c_hip_accumulate_loss(float* loss_accum, hipStream_t stream);
 

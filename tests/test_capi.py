@@ -50,3 +50,16 @@ def test_temp_sizes_are_monotone():
     sizes = [L.b2c_radix_sort_temp_bytes(n) for n in (1, 4096, 4097, 1 << 20, 1 << 24)]
     assert sizes == sorted(sizes) and sizes[0] > 0
     assert L.b2c_scan_temp_bytes(1 << 20) >= 4 * 256
+
+
+def test_noalloc_loss_rejects_images_beyond_its_scratch():
+    """The allocation-free loss checks the image against its fixed partials array before any HIP call."""
+    import ctypes as C
+    L = _native.lib()
+    L.b2c_loss_partials.restype = C.c_size_t
+    W = H = 32768
+    assert L.b2c_loss_partials(W, H) > (1 << 18)
+    args = (C.c_char * 256)()  # a zeroed b2c_loss_args: null pointers, then W and H
+    C.memmove(C.addressof(args) + 3 * C.sizeof(C.c_void_p), (C.c_int * 2)(W, H), 8)
+    L.b2c_hip_photometric_noalloc.argtypes = [C.c_void_p, C.c_void_p]
+    assert L.b2c_hip_photometric_noalloc(C.addressof(args), None) == 1  # hipErrorInvalidValue

@@ -1,0 +1,80 @@
+"""The allocation-free loss entry point (b2c_hip_photometric_noalloc, include/b2c_kernels.h) against the
+regular one (b2c_hip_photometric with a caller-provided partials workspace), called through the C ABI on
+device buffers from torch: two calls in a row, the second on a smaller image, each bit-identical to the
+regular entry point in the loss value and every per-pixel gradient. The regular entry point runs first on
+each input, then the allocation-free one, so its fixed scratch holds the previous call's partials (stale
+contents must not leak into the result)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from b2ctrain_amd import _native
+from tests.gpu_harness import emit
+
+pytestmark = pytest.mark.gpu
+
+
+class LossArgs(C.Structure):
+    _fields_ = [("pred", C.c_void_p), ("gt", C.c_void_p), ("weights", C.c_void_p), ("W", C.c_int), ("H", C.c_int),
+                ("l1_w", C.c_float), ("ssim_w", C.c_float), ("bg", C.c_float * 3), ("composite", C.c_int),
+                ("mask", C.c_int), ("alpha_lane", C.c_int), ("match_alpha_weight", C.c_float), ("scale", C.c_float),
+                ("grad_scale", C.c_float), ("v_out", C.c_void_p), ("loss_accum", C.c_void_p), ("partials", C.c_void_p),
+                ("assign", C.c_int), ("running", C.c_int)]
+
+
+def _inputs(W, H, seed, weights):
+    import torch
+    g = np.random.default_rng(seed)
+    P = W * H
+    pred = g.random((P, 4), dtype=np.float32)
+    gt = g.integers(0, 1 << 32, P, dtype=np.uint64).astype(np.uint32)
+    dev = torch.device("cuda:0")
+    t = dict(pred=torch.from_numpy(pred).to(dev), gt=torch.from_numpy(gt.view(np.int32)).to(dev),
+             v_out=torch.zeros((P, 4), dtype=torch.float32, device=dev),
+             acc=torch.zeros(16, dtype=torch.float32, device=dev))
+    t["w"] = torch.from_numpy(g.integers(85, 256, P).astype(np.uint8)).to(dev) if weights else None
+    return t
+
+
+def _call(fn, t, W, H, opts, partials):
+    import torch
+    a = LossArgs()
+    a.pred, a.gt = t["pred"].data_ptr(), t["gt"].data_ptr()
+    a.weights = t["w"].data_ptr() if t["w"] is not None else None
+    a.W, a.H = W, H
+    a.l1_w, a.ssim_w = 0.8, -0.2
+    for k in range(3):
+        a.bg[k] = opts["bg"][k]
+    a.composite, a.mask, a.alpha_lane = opts["composite"], opts["mask"], opts["alpha_lane"]
+    a.match_alpha_weight, a.scale, a.grad_scale = 0.1, opts["scale"], 3.0 * W * H
+    t["v_out"].zero_()
+    t["acc"].fill_(0.25)  # assign mode overwrites [0..3]
+    a.v_out, a.loss_accum = t["v_out"].data_ptr(), t["acc"].data_ptr()
+    a.partials = partials
+    a.assign, a.running = 1, 1
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = fn(C.byref(a), C.c_void_p(stream))
+    assert rc == 0, f"launcher returned {rc}"
+    torch.cuda.synchronize()
+    return t["v_out"].cpu().numpy().copy(), t["acc"].cpu().numpy().copy()
+
+
+def test_noalloc_loss_matches_workspace_loss_twice():
+    import torch
+    L = _native.lib()
+    L.b2c_hip_photometric.argtypes = [C.c_void_p, C.c_void_p]
+    L.b2c_hip_photometric_noalloc.argtypes = [C.c_void_p, C.c_void_p]
+    L.b2c_loss_partials.restype = C.c_size_t
+    cases = [(1920, 1080, dict(bg=(0.4, 0.3, 0.2), composite=1, mask=0, alpha_lane=1, scale=1.5), True),
+             (640, 360, dict(bg=(0.0, 0.0, 0.0), composite=0, mask=1, alpha_lane=0, scale=1.0), False)]
+    for k, (W, H, opts, weights) in enumerate(cases):
+        emit(f"no-alloc loss call {k + 1}: {W}x{H}")
+        t = _inputs(W, H, 100 + k, weights)
+        ws = torch.empty(int(L.b2c_loss_partials(W, H)), dtype=torch.float32, device="cuda:0")
+        v_ref, acc_ref = _call(L.b2c_hip_photometric, t, W, H, opts, ws.data_ptr())
+        v_na, acc_na = _call(L.b2c_hip_photometric_noalloc, t, W, H, opts, None)
+        assert acc_ref[0] > 0 and acc_ref[3] == 1
+        assert np.array_equal(acc_na[:4], acc_ref[:4]), (acc_na[:4], acc_ref[:4])
+        assert np.array_equal(v_na, v_ref), f"{int((v_na != v_ref).sum())} gradient entries differ"
+        assert np.abs(v_ref).max() > 0
