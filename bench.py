@@ -1,18 +1,27 @@
-"""Benchmark of the MI355X splat rasterizer on BASELINE.json's metric configuration (config 3).
+"""Benchmark of the MI355X splat rasterizer on BASELINE.json's metric configuration (config 3 by default).
 
-One step = one training step of the hot path on one view, inputs resident in HBM: projection + binning/
-sort + forward raster + fused L1/SSIM/alpha loss + MFMA backward + projection VJP (trainer.cpp:487-529
-order, grad_out semantics). A new random background is drawn each step (trainer.cpp:470-471).
+One step = one training step of the hot path, inputs resident in HBM: projection + binning/sort + forward
+raster + fused L1/SSIM/alpha loss + MFMA backward + projection VJP (the order of trainer.cpp:487-529, grad_out
+semantics), on every view of the configuration (config 4: 8 camera poses, gradients accumulated over them).
+A new random background is drawn each step (trainer.cpp:470-471).
 
 Prints ONE JSON line. value = Gfrag/s = F_sweep / (t_forward + t_backward), with F_sweep = the sum over
-tiles of 64 x the tile's shrunk list length (the fragments the raster sweeps). Stage times come from hipEvents recorded on the
-context's stream around each stage; ms_per_step is the wall time of the K timed steps over K, bracketed by
-stream synchronisation.
+tiles of 64 x the tile's shrunk list length (the fragments both raster passes sweep), summed over the views.
+Stage times come from hipEvents recorded on the context's stream around each stage; ms_per_step is the wall
+time of the K timed steps over K, bracketed by stream synchronisation.
+
+Two CPU baselines are timed on this host (not the optimisation target):
+* cpu_baseline: the fp32 tiled CPU restatement (oracle/b2c_oracle.c) of the forward and backward raster over
+  the GPU's own tile lists, OpenMP over tiles on the host threads this process may use;
+* cpu_reference_algorithm: the reference's own CPU algorithm (tests/reference.cpp:34-143 restated: fp64,
+  every depth-sorted splat tested at every pixel, one thread) on a bounded sample of pixels spread over the
+  frame, extrapolated to the whole frame.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -26,30 +35,39 @@ METRIC = "raster fwd+bwd ms/step @1M splats 1080p; Gfrag/s; % HBM roofline"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
+WORKLOADS = {
+    1: "BASELINE config 1: 1,024 splats, SH0, 64x64, fused L1+SSIM",
+    2: "BASELINE config 2: 100k splats, SH3, 800x800, fused L1+SSIM",
+    3: "BASELINE config 3: 1M splats, SH3, 1920x1080, fused L1+SSIM (11-tap) + alpha lane, per-pixel weights, "
+       "elliptic alpha, random per-step background; MFMA backward; projection VJP",
+    4: "BASELINE config 4: 3M splats, SH4, 1920x1080 slab (~190 composited fragments/px), 8 camera poses per step "
+       "with gradients accumulated",
+    5: "BASELINE config 5: 500k splats, 3840x2160, SH3 with fp16 bands, 5% huge anisotropic splats",
+}
+DEFAULT_SPLATS = {1: 1024, 2: 100_000, 3: 1_000_000, 4: 3_000_000, 5: 500_000}
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
 def projection_bytes(n, n_ok, sh_bytes):
-    # all splats: pos_op + quat + lscale (48 B) and tile_count (4 B); splats that pass: SH coefficients,
-    # proj0..2 (48 B), proj3 (8 B), hit_info (8 B), max_screen read + write (8 B)
+    """All splats: pos_op + quat + lscale (48 B) and tile_count (4 B); splats that pass: SH coefficients,
+    proj0..2 (48 B), proj3 (8 B), hit_info (8 B), max_screen read + write (8 B)."""
     return n * 52 + n_ok * (sh_bytes + 72)
 
 
 def binning_bytes(n, m, tile_bits):
-    """Algorithmic bytes of binning: depth keys (read proj1 z + tile_count, write key/value), 4 depth-sort
-    passes (16 B per splat each), the count scan in depth order (12 B per splat), the emit (20 B per splat +
-    8 B per intersection), ceil(tile_bits / 8) tile-sort passes (24 B per intersection each: key and two
-    values, read and written) and the range pass (4 B per intersection)."""
-    tile_passes = (int(tile_bits) + 7) // 8
-    return n * (8 + 8) + 4 * 16 * n + 12 * n + 20 * n + 8 * m + tile_passes * 24 * m + 4 * m
+    """The survey's algorithmic bytes for the sorts, scan and emit (independent of this design's extra
+    passes): 4 depth-sort passes of 16 B per splat, ceil(tile_bits / 8) tile-sort passes of 16 B per
+    intersection, the count scan (8 B per splat) and the emit (20 B per splat + 8 B per intersection)."""
+    return 4 * 16 * n + ((int(tile_bits) + 7) // 8) * 16 * m + 8 * n + 20 * n + 8 * m
 
 
-def read_traffic(kernel):
+def read_traffic(kernel, config):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE in
     KiB per dispatch, scaled by the plain-copy calibration recorded in the same file); None if absent."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_cfg3_traffic.txt")
+    path = os.path.join(ROOT, "profiles", f"{kernel}_cfg{config}_traffic.txt")
     if not os.path.exists(path):
         return None
     kv = {}
@@ -65,49 +83,85 @@ def read_traffic(kernel):
     return int((fetch + write) * 1024)
 
 
-def cpu_baseline(r, scene, bg):
-    """The CPU port (oracle, fp32 tiled restatement, one host core) timed on the same frame: forward raster
-    + backward raster over the GPU's own tile lists and per-pixel loss gradient. Returns the frame's
-    composited-fragment count (F_contrib) and the cpu_baseline record."""
+def cpu_info():
+    model, logical = "unknown", os.cpu_count()
+    fields = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                fields.setdefault(k, v)
+    except OSError:
+        pass
+    model = fields.get("model name", model)
+    return {"cpu_model": model, "cpu_vendor": fields.get("vendor_id"), "cpu_family": fields.get("cpu family"),
+            "cpu_model_id": fields.get("model"), "host_logical_cpus": logical,
+            "host_cpus_usable": len(os.sched_getaffinity(0))}
+
+
+def host_threads():
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
+def f_sweep_of(r):
+    ranges = r.read("tile_ranges").astype(np.int64)
+    return int(64 * (ranges[:, 1] - ranges[:, 0]).clip(min=0).sum())
+
+
+def cpu_baselines(r, scene, bg, f_sweep):
+    """Both CPU baselines on the frame the context last rendered (one view)."""
     from oracle import oracle as O
 
     W, H = scene.W, scene.H
-    tx, ty, T, _ = O.tile_geometry(W, H)
-    keys = r.read("keys_sorted")
     pr = {k: r.read(k) for k in ("proj0", "proj1", "proj2")}
+    keys = r.read("keys_sorted")
+    tx, ty, T, _ = O.tile_geometry(W, H)
     tiles = np.arange(T, dtype=np.uint32)
     ranges = np.stack([np.searchsorted(keys, tiles, "left"), np.searchsorted(keys, tiles, "right")], 1).astype(np.uint32)
     ranges[ranges[:, 0] == ranges[:, 1]] = 0
     bn = {"vals_sorted": r.read("vals_sorted"), "tile_ranges": ranges}
     v_out = r.read("v_out")
-    t0 = time.perf_counter()
-    fw = O.raster_fwd(pr, bn, W, H, bg)
-    t1 = time.perf_counter()
-    O.raster_bwd(pr, bn, fw, v_out, W, H, bg, scene.n, inv_gscale=1.0 / (3.0 * W * H))
-    t2 = time.perf_counter()
-    shr = fw["tile_ranges"].astype(np.int64)
-    f_sweep = int(64 * (shr[:, 1] - shr[:, 0]).clip(min=0).sum())
-    secs = (t1 - t0) + (t2 - t1)
-    return fw["f_contrib"], {
-        "value": f_sweep / secs / 1e9,
+    threads = host_threads()
+    O.set_threads(threads)
+    try:
+        t0 = time.perf_counter()
+        fw = O.raster_fwd(pr, bn, W, H, bg)
+        t1 = time.perf_counter()
+        O.raster_bwd(pr, bn, fw, v_out, W, H, bg, scene.n, inv_gscale=1.0 / (3.0 * W * H))
+        t2 = time.perf_counter()
+    finally:
+        O.set_threads(1)
+    tiled = {
+        "value": round(f_sweep / (t2 - t0) / 1e9, 4),
+        "unit": "Gfrag/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one full frame of the workload (F_sweep={f_sweep}): forward {t1 - t0:.2f} s + backward {t2 - t1:.2f} s "
+                  f"of the fp32 tiled CPU restatement (oracle/b2c_oracle.c) over the GPU's own tile lists, OpenMP over "
+                  f"tiles on {threads} host threads",
+        **cpu_info(),
+    }
+    # the reference's CPU algorithm: fp64 brute force, one thread, ~400 pixels spread over the frame
+    P = W * H
+    stride = max(2, P // 400)
+    n_sample = (P + stride - 1) // stride
+    secs = O.ref_render_sample_seconds(scene, stride, bg=bg)
+    frame_s = secs * P / n_sample
+    ref = {
+        "value": f_sweep / frame_s / 1e9,
         "unit": "Gfrag/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"one full config-3 frame (F_sweep={f_sweep}): forward {t1 - t0:.2f} s + backward {t2 - t1:.2f} s "
-                  "of the fp32 tiled CPU restatement (oracle/b2c_oracle.c), single thread",
-        "cpu_model": _cpu_model(),
-        "host_threads_available": os.cpu_count(),
+        "sample": f"{n_sample} pixels (every {stride}th, row-major) of one frame rendered by the reference's CPU "
+                  f"algorithm (tests/reference.cpp:34-143 restated in oracle/b2c_oracle.c: fp64, every depth-sorted "
+                  f"splat tested at every pixel) in {secs:.1f} s on one thread; whole frame extrapolated to "
+                  f"{frame_s:.0f} s",
+        "frame_seconds": round(frame_s, 1),
     }
-
-
-def _cpu_model():
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+    return fw["f_contrib"], tiled, ref
 
 
 def main():
@@ -115,7 +169,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--splats", type=int, default=1_000_000)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(WORKLOADS))
+    ap.add_argument("--splats", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--mode", type=int, default=1, help="backward: 1 = MFMA reduction, 0 = fp32 reduction")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -140,80 +195,89 @@ def main():
     from b2ctrain_amd import _native
     from b2ctrain_amd import scenes as S
 
-    log(f"bench: generating config 3 ({args.splats} splats)")
-    scene = S.config3(n=args.splats)
+    cfg = args.config
+    n = args.splats or DEFAULT_SPLATS[cfg]
+    log(f"bench: generating config {cfg} ({n} splats)")
+    scene = S.config1() if cfg == 1 else S.CONFIGS[cfg](n=n)
+    views = scene.extra_cams or [scene.cam]
     W, H = scene.W, scene.H
     r = _native.Renderer(scene)
     rng = np.random.default_rng(7)
     bgs = [tuple(float(x) for x in rng.random(3)) for _ in range(args.warmup + args.steps)]
 
+    def step(k, timed=False):
+        st = None
+        for v, cam in enumerate(views):
+            t = r.step(mode=args.mode, bg=bgs[k], cam=cam, accumulate=v > 0, timed=timed)
+            if timed:
+                st = t if st is None else {key: st[key] + t[key] for key in st}
+        return st
+
     log("bench: warmup")
     for k in range(args.warmup):
-        r.step(mode=args.mode, bg=bgs[k], timed=True)
+        step(k, timed=True)
     r.sync()
     # The timed region runs the steps as a training loop does: no per-stage events (reading them back
-    # would drain the stream at the end of every step). The per-stage breakdown comes from a second pass
+    # would drain the stream at the end of every view). The per-stage breakdown comes from a second pass
     # over the same backgrounds with hipEvents recorded on the context's stream.
     log("bench: timed steps")
     t0 = time.perf_counter()
     for k in range(args.steps):
-        r.step(mode=args.mode, bg=bgs[args.warmup + k])
+        step(args.warmup + k)
     r.sync()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
     log("bench: per-stage events")
-    stages = [r.step(mode=args.mode, bg=bgs[args.warmup + k], timed=True) for k in range(args.steps)]
+    stages = [step(args.warmup + k, timed=True) for k in range(args.steps)]
     r.sync()
     med = {k: float(np.median([s[k] for s in stages])) for k in stages[0]}
     mean = {k: float(np.mean([s[k] for s in stages])) for k in stages[0]}
 
-    # fragment counts of the last step (deterministic lists)
-    ranges = r.read("tile_ranges").astype(np.int64)
-    keys = r.read("keys_sorted")
-    tiles = np.arange(ranges.shape[0])
-    first = np.searchsorted(keys, tiles, "left")
-    f_sweep = int(64 * (ranges[:, 1] - first).clip(min=0).sum())
-    info = r.info()
-    tc = r.read("tile_count")
-    n_ok = int((tc > 0).sum())
+    # fragment and intersection counts of one more step, view by view (deterministic lists)
+    f_sweep = m_total = n_ok = 0
+    tile_bits = 0
+    for v, cam in enumerate(views):
+        r.step(mode=args.mode, bg=bgs[-1], cam=cam, accumulate=v > 0)
+        f_sweep += f_sweep_of(r)
+        info = r.info()
+        m_total += int(info.num_isect)
+        tile_bits = int(info.tile_bits)
+        n_ok += int((r.read("tile_count") > 0).sum())
     t_fb = mean["forward_ms"] + mean["backward_ms"]
     gfrag = f_sweep / (t_fb * 1e-3) / 1e9
 
     # Roofline of the dominant kernel, the MFMA backward raster (raster_bwd_mfma_kernel), timed alone with
     # hipEvents on the context's stream. Algorithmic bytes per launch: per composited-range intersection its
-    # list entry, emit position and projected splat (4 + 4 + 48 B) plus its gradient row (48 B, written);
-    # per intersection past the shrunk end its zero row (48 B); per pixel out_rgba, out_feat, last_idx and
-    # v_out (52 B). MFMA: 8 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
+    # list entry, emit position and projected splat (4 + 4 + 48 B) plus its gradient row (48 B, written); per
+    # intersection past the shrunk end its zero row (48 B); per pixel out_rgba, out_feat, last_idx and v_out
+    # (52 B). MFMA: 8 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
     m_shrunk = f_sweep // 64
-    m_total = int(info.num_isect)
-    bwd_bytes = 104 * m_shrunk + 48 * (m_total - m_shrunk) + 52 * W * H
+    nv = len(views)
+    bwd_bytes = 104 * m_shrunk + 48 * (m_total - m_shrunk) + 52 * W * H * nv
     t_bwd = mean["raster_bwd_ms"] * 1e-3
     bwd_gbs = bwd_bytes / t_bwd / 1e9
-    groups = int(np.ceil(m_shrunk / 8.0))
-    mfma_tflops = groups * 8 * 16384 / t_bwd / 1e12
-    traffic = read_traffic("raster_bwd_mfma_kernel")
+    mfma_tflops = math.ceil(m_shrunk / 8.0) * 8 * 16384 / t_bwd / 1e12
     roofline = {
         "kernel": "raster_bwd_mfma_kernel",
-        "bound": "hbm",
+        "bound": "valu",
         "achieved": round(bwd_gbs, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(bwd_gbs / HBM_PEAK_GBS, 4),
-        "traffic": traffic,
+        "traffic": read_traffic("raster_bwd_mfma_kernel", cfg),
         "algorithmic_bytes": bwd_bytes,
-        "avg_launch_ms": round(mean["raster_bwd_ms"], 4),
+        "avg_launch_ms": round(mean["raster_bwd_ms"] / nv, 4),
         "mfma": {"achieved": round(mfma_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                  "frac": round(mfma_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
-        "note": ("VALU-issue bound (per-fragment replay; rocprofv3 SQ_INSTS_VALU gives 91% of the VALU issue "
-                 "slots, profiles/raster_step_cfg3_counters.md); HBM and MFMA fractions are low by design"),
+        "note": ("the per-fragment replay issues VALU instructions in most cycles (rocprofv3 SQ_INSTS_VALU, "
+                 "profiles/raster_step_cfg3_counters.md): the kernel is bound by VALU issue; achieved/peak/frac "
+                 "are its algorithmic HBM bytes against 8 TB/s and the mfma entry its matrix-core rate"),
     }
-    # HBM rooflines of the stages the north star prices: projection, binning/sort, loss
-    proj_bytes = projection_bytes(scene.n, n_ok, 4 * 3 * scene.K)
-    bin_bytes = binning_bytes(scene.n, m_total, info.tile_bits)
-    loss_bytes = 37 * W * H
+    sh_bytes = 4 * 3 + (2 if scene.sh_fp16 else 4) * 3 * (scene.K - 1)
     stage_rooflines = {}
-    for name, nbytes, key in (("projection", proj_bytes, "project_ms"), ("binning_sort", bin_bytes, "bin_ms"),
-                              ("loss", loss_bytes, "loss_ms")):
+    for name, nbytes, key in (("projection", projection_bytes(scene.n * nv, n_ok, sh_bytes), "project_ms"),
+                              ("binning_sort", binning_bytes(scene.n * nv, m_total, tile_bits), "bin_ms"),
+                              ("loss", 37 * W * H * nv, "loss_ms")):
         gbs = nbytes / (mean[key] * 1e-3) / 1e9
         stage_rooflines[name] = {"bound": "hbm", "algorithmic_bytes": int(nbytes), "ms": round(mean[key], 4),
                                  "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -232,14 +296,14 @@ def main():
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
-            "workload": "BASELINE config 3: 1M splats, SH3, 1920x1080, fused L1+SSIM (11-tap) + alpha lane, "
-                        "per-pixel weights, elliptic alpha, random per-step background; MFMA backward; projection VJP",
+            "workload": WORKLOADS[cfg],
             "splats": scene.n,
+            "views_per_step": nv,
             "splats_projected": n_ok,
             "sh_degree": scene.degree,
             "width": W,
             "height": H,
-            "isects": int(info.num_isect),
+            "isects": m_total,
             "F_sweep": f_sweep,
             "backward": "mfma" if args.mode == 1 else "fp32",
             "parallelism": "single GPU",
@@ -253,13 +317,13 @@ def main():
         "stage_rooflines": stage_rooflines,
     }
     if not args.no_cpu_baseline:
-        log("bench: CPU baseline (oracle port, one core)")
-        r.step(mode=args.mode, bg=bgs[-1])
+        log("bench: CPU baselines (tiled port on all host threads; reference algorithm on a pixel sample)")
+        r.step(mode=args.mode, bg=bgs[-1], cam=views[0])
         r.sync()
-        f_contrib, out["cpu_baseline"] = cpu_baseline(r, scene, bgs[-1])
+        fs0 = f_sweep_of(r)
+        f_contrib, out["cpu_baseline"], out["cpu_reference_algorithm"] = cpu_baselines(r, scene, bgs[-1], fs0)
         # composited fragments of that frame, counted by the CPU port over the GPU's own lists
-        out["config"]["F_contrib"] = f_contrib
-        out["gfrag_contrib_per_s"] = round(f_contrib / (t_fb * 1e-3) / 1e9, 3)
+        out["config"]["F_contrib_view0"] = f_contrib
     else:
         out["cpu_baseline"] = None
     r.close()

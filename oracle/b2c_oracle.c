@@ -4,11 +4,13 @@
  * Build: gcc -O2 -std=c11 -ffp-contract=off (oracle/Makefile). Contraction must stay off: the
  * projection and binning below are bit-exact restatements that the HIP kernels must reproduce.
  */
+#define _POSIX_C_SOURCE 199309L /* clock_gettime */
 #include "b2c_oracle.h"
 
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #define RT_W 8
 #define ALPHA_CUTOFF (1.0f / 255.0f) /* splat_math.cuh:7 */
@@ -425,10 +427,25 @@ uint32_t orc_bin(int n, const uint32_t* tile_count, const uint32_t* hit_info, co
 static uint64_t g_fwd_contrib = 0;
 uint64_t orc_last_fwd_contrib(void) { return g_fwd_contrib; }
 
+/* Host threads of the tiled raster passes (OpenMP over tiles). 1 (the default) keeps the backward's
+ * double-precision sums in a fixed order; more threads add them atomically in a varying order. */
+static int g_threads = 1;
+void orc_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+
+static inline void acc_add(double* p, double v) {
+  if (g_threads > 1) {
+#pragma omp atomic
+    *p += v;
+  } else {
+    *p += v;
+  }
+}
+
 void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], uint32_t* tile_ranges,
                     const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
                     float* out_rgba, float* out_T, uint32_t* last_idx) {
   uint64_t contrib = 0;
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 16) reduction(+ : contrib)
   for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
     int tx = tile % tiles_x, ty = tile / tiles_x;
     uint32_t rx = tile_ranges[tile * 2], ry = tile_ranges[tile * 2 + 1];
@@ -590,6 +607,7 @@ void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], c
                     const float* out_rgba, const float* out_T, const uint32_t* last_idx, const float* v_out,
                     float inv_gscale, double* v_splat, uint32_t* vis_flag, double* vis_weight) {
   const float Wf = (float)W, Hf = (float)H;
+#pragma omp parallel for num_threads(g_threads) schedule(dynamic, 16)
   for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
     int tx = tile % tiles_x, ty = tile / tiles_x;
     uint32_t rx = tile_ranges[tile * 2], ry = tile_ranges[tile * 2 + 1];
@@ -637,9 +655,9 @@ void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], c
         }
         Sx += cr * vis; Sy += cg * vis; Sz += cb * vis;
         T = T_before;
-        vis_flag[gid] = 1u;
-        vis_weight[gid] += (double)vis;
-        for (int k = 0; k < GRAD_LANES; k++) v_splat[(size_t)gid * GRAD_LANES + k] += (double)g[k] * (double)inv_gscale;
+        vis_flag[gid] = 1u; /* every writer stores the same value */
+        acc_add(&vis_weight[gid], (double)vis);
+        for (int k = 0; k < GRAD_LANES; k++) acc_add(&v_splat[(size_t)gid * GRAD_LANES + k], (double)g[k] * (double)inv_gscale);
       }
     }
   }
@@ -877,6 +895,39 @@ static int depth_cmp(const void* a, const void* b) {
   return *(const int*)a - *(const int*)b;
 }
 
+/* Rows [y0, y1) of the brute-force render (reference.cpp:84-104): every depth-sorted projected splat is
+ * tested at every pixel; with stride > 1 only the pixels whose row-major index is a multiple of it. */
+static void ref_composite(const dproj_t* pr, const int* order, int no, int W, int y0, int y1, const double bg[3],
+                          double* imgd, size_t stride) {
+  for (int py = y0; py < y1; py++)
+    for (int px = 0; px < W; px++) {
+      if (stride > 1 && ((size_t)py * W + px) % stride) continue;
+      double T = 1, r = 0, g = 0, b = 0, pcx = px + 0.5, pcy = py + 0.5;
+      for (int oi = 0; oi < no; oi++) {
+        const dproj_t* q = &pr[order[oi]];
+        double dx = pcx - q->mx, dy = pcy - q->my;
+        double sigma = 0.5 * (q->c00 * dx * dx + q->c11 * dy * dy) + q->c01 * dx * dy;
+        double alpha = fmin(0.999, q->opac * exp(-sigma));
+        if (!(sigma >= 0 && alpha >= 1.0 / 255.0)) continue;
+        double nT = T * (1 - alpha);
+        if (nT <= 1e-4) break;
+        double vis = alpha * T;
+        r += fmax(q->r, 0.0) * vis; g += fmax(q->g, 0.0) * vis; b += fmax(q->b, 0.0) * vis;
+        T = nT;
+      }
+      size_t o = (size_t)py * W + px;
+      imgd[o * 4] = r + T * bg[0]; imgd[o * 4 + 1] = g + T * bg[1]; imgd[o * 4 + 2] = b + T * bg[2]; imgd[o * 4 + 3] = 1 - T;
+    }
+}
+
+/* A bounded sample of the brute force for the CPU baseline: with a stride above 1, orc_ref_loss renders
+ * only every stride-th pixel (row-major), times that (orc_ref_composite_seconds) and returns 0 without the
+ * loss. */
+static size_t g_ref_stride = 1;
+static double g_ref_composite_s = 0.0;
+void orc_ref_set_sample(uint64_t stride) { g_ref_stride = stride > 1 ? (size_t)stride : 1; }
+double orc_ref_composite_seconds(void) { return g_ref_composite_s; }
+
 double orc_ref_loss(int n, int degree, const double* pos, const double* log_scale, const double* quat, const double* opacity,
                     const double* sh, const double* floor_, const orc_cam_t* cam, int W, int H, const double bg[3],
                     const uint32_t* gt, const uint8_t* weights, int composite, int mask, int alpha_lane, double l1_w,
@@ -955,24 +1006,17 @@ double orc_ref_loss(int n, int degree, const double* pos, const double* log_scal
   const size_t P = (size_t)W * H;
   float* img = (float*)malloc(sizeof(float) * P * 4);
   double* imgd = (double*)malloc(sizeof(double) * P * 4);
-  for (int py = 0; py < H; py++)
-    for (int px = 0; px < W; px++) {
-      double T = 1, r = 0, g = 0, b = 0, pcx = px + 0.5, pcy = py + 0.5;
-      for (int oi = 0; oi < no; oi++) {
-        const dproj_t* q = &pr[order[oi]];
-        double dx = pcx - q->mx, dy = pcy - q->my;
-        double sigma = 0.5 * (q->c00 * dx * dx + q->c11 * dy * dy) + q->c01 * dx * dy;
-        double alpha = fmin(0.999, q->opac * exp(-sigma));
-        if (!(sigma >= 0 && alpha >= 1.0 / 255.0)) continue;
-        double nT = T * (1 - alpha);
-        if (nT <= 1e-4) break;
-        double vis = alpha * T;
-        r += fmax(q->r, 0.0) * vis; g += fmax(q->g, 0.0) * vis; b += fmax(q->b, 0.0) * vis;
-        T = nT;
-      }
-      size_t o = (size_t)py * W + px;
-      imgd[o * 4] = r + T * bg[0]; imgd[o * 4 + 1] = g + T * bg[1]; imgd[o * 4 + 2] = b + T * bg[2]; imgd[o * 4 + 3] = 1 - T;
-    }
+  if (g_ref_stride > 1) { /* bounded sample: every g_ref_stride-th pixel, then no loss */
+    struct timespec t0, t1;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    ref_composite(pr, order, no, W, 0, H, bg, imgd, g_ref_stride);
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    g_ref_composite_s = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+    if (out_img) memcpy(out_img, imgd, sizeof(double) * P * 4);
+    free(img); free(imgd); free(order); free(pr);
+    return 0.0;
+  }
+  ref_composite(pr, order, no, W, 0, H, bg, imgd, 1);
   if (out_img) memcpy(out_img, imgd, sizeof(double) * P * 4);
   /* loss in double over the double image (reference.cpp:105-131) */
   double w[11];

@@ -115,6 +115,15 @@ double orc_ref_loss(int n, int degree, const double* pos, const double* log_scal
                     int composite, int mask, int alpha_lane, double l1_w, double ssim_w,
                     double match_alpha_weight, double scale, int float_exp, double* out_img);
 
+/* Bounded sample for the CPU baseline: after orc_ref_set_sample(s) with s > 1, orc_ref_loss renders only the
+ * pixels whose row-major index is a multiple of s, skips the loss (returns 0) and records the compositing
+ * time, read by orc_ref_composite_seconds(); orc_ref_set_sample(1) restores the full loss. */
+void orc_ref_set_sample(uint64_t stride);
+double orc_ref_composite_seconds(void);
+
+/* Host threads of orc_raster_fwd / orc_raster_bwd (OpenMP over tiles); 1 by default (fixed summation order). */
+void orc_set_threads(int n);
+
 /* ---- internal pieces exported for the pinning tests ---- */
 void orc_sh_basis_f(int deg, float x, float y, float z, float* out);      /* splat_math.cuh:122-145 */
 void orc_sh_basis_d(int deg, double x, double y, double z, double* out);  /* reference.cpp:16-30 (+ degree 4) */

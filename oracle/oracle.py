@@ -86,7 +86,29 @@ def lib():
         _lib.orc_ref_loss.argtypes = [C.c_int, C.c_int] + [p] * 6 + [C.POINTER(OrcCam), C.c_int, C.c_int, p, p, p,
                                                                     C.c_int, C.c_int, C.c_int] + [C.c_double] * 4 + [
                                                                     C.c_int, p]
+        _lib.orc_ref_set_sample.restype = None
+        _lib.orc_ref_set_sample.argtypes = [C.c_uint64]
+        _lib.orc_ref_composite_seconds.restype = C.c_double
+        _lib.orc_set_threads.restype = None
+        _lib.orc_set_threads.argtypes = [C.c_int]
     return _lib
+
+
+def set_threads(n: int) -> None:
+    """Host threads of the tiled raster passes (1 = fixed summation order, the tests' setting)."""
+    lib().orc_set_threads(int(n))
+
+
+def ref_render_sample_seconds(scene, stride, bg=None) -> float:
+    """Time the fp64 brute-force render (the reference's CPU algorithm, one thread) over every stride-th
+    pixel: the compositing seconds (projection and depth sort excluded)."""
+    L = lib()
+    L.orc_ref_set_sample(int(stride))
+    try:
+        ref_loss(scene, bg=bg)
+        return float(L.orc_ref_composite_seconds())
+    finally:
+        L.orc_ref_set_sample(1)
 
 
 def ref_available() -> bool:
