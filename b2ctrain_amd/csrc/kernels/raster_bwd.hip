@@ -99,7 +99,9 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
     __syncthreads();
     for (int j = count - 1; j >= 0; j--) {
       const float4 geo = s_geo[j], shape = s_shape[j];  // (mx, my, c00, c01), (c11, opacity, depth, power)
-      const float sigma = calc_sigma(ps.pcx, ps.pcy, geo.z, geo.w, shape.x, geo.x, geo.y);
+      // halving c00 and c11 is exact: the same sigma as the forward's
+      const FragGeom fg = frag_geom(geo.x, geo.y, 0.5f * geo.z, geo.w, 0.5f * shape.x, ps.pcx, ps.pcy);
+      const float sigma = fg.sigma;
       const bool in = ps.inside && lo + (uint32_t)j < ps.last && sigma >= 0.f && sigma <= shape.w;
       if (ballot64(in) == 0ull) continue;  // uniform
       float val[ANCHOR_VALS];
@@ -115,9 +117,11 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
         const float cv = fmaxf(col.x, 0.f) * ps.vo.x + fmaxf(col.y, 0.f) * ps.vo.y + fmaxf(col.z, 0.f) * ps.vo.z;
         const float v_alpha = Tb * cv - Q / keep;
         if (araw <= ALPHA_MAX) {  // a clamped alpha does not depend on sigma
-          const float dx = ps.pcx - geo.x, dy = ps.pcy - geo.y;
+          const float dx = fg.dx, dy = fg.dy;
           const float v_sigma = -alpha * v_alpha;
-          const float gmx = -v_sigma * (geo.z * dx + geo.w * dy), gmy = -v_sigma * (geo.w * dx + shape.x * dy);
+          // d sigma / d mean = -(d sigma / d d) = -(2a dx + b dy, b dx + 2c dy)
+          const float gmx = -v_sigma * __builtin_fmaf(0.5f * geo.z, dx, fg.lin);
+          const float gmy = -v_sigma * __builtin_fmaf(geo.w, dx, fg.cdy + fg.cdy);
           val[0] = gmx;
           val[1] = gmy;
           val[2] = 0.5f * v_sigma * dx * dx;
@@ -317,19 +321,11 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
         {
           const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + jj * 16);
           const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + jj * 16);
-          const float dx = ps.pcx - g0.x, dy = ps.pcy - g0.y;
-          float sigma, t1, t2, c01dx;
-          {
-#pragma clang fp contract(off)
-            // = 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy, bit for bit (halving is exact)
-            t1 = g0.z * dx;
-            t2 = g1.x * dy;
-            c01dx = g0.w * dx;
-            sigma = (t1 * dx + t2 * dy) + c01dx * dy;
-          }
+          const FragGeom fg = frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, ps.pcx, ps.pcy);
+          const float sigma = fg.sigma;
           // 0 <= sigma <= power as one unsigned compare of the bit patterns: every listed splat has
           // power >= +0 (its tile test passed, and sigma >= 0 for a positive-definite conic), and sigma is
-          // never -0 (c00 dx^2 + c11 dy^2 >= +0 and +0 + -0 = +0); a NaN sigma fails either way
+          // never -0 (frag_geom's addend (c dy) dy is +0 when dy is); a NaN sigma fails either way
           const bool in = live_px & (jj < last_rel) & (__float_as_uint(sigma) <= __float_as_uint(g1.z));
           {  // straight-line: a lane without this fragment computes zeros (alpha = 0)
             // a lane without this fragment runs the same arithmetic with alpha = 0: ra = 1, vis = 0,
@@ -344,7 +340,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             const float v_alpha = Tb * cv - ra * Q;
             const float v_sigma = araw <= ALPHA_MAX ? -alpha * v_alpha : 0.f;  // clamped: no sigma gradient
             // refine statistic: |d(loss)/d(mean2d)| scaled to pixels, over the final alpha
-            const float gx = 2.f * t1 + g0.w * dy, gy = c01dx + 2.f * t2;
+            const float gx = __builtin_fmaf(g0.z, fg.dx, fg.lin), gy = __builtin_fmaf(g0.w, fg.dx, fg.cdy + fg.cdy);
             o_r = fabsf(v_sigma) * __builtin_amdgcn_sqrtf(gx * gx + rho * gy * gy) * r_scale;
             o_vis = vis;
             o_vs = v_sigma;

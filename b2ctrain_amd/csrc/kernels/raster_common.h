@@ -18,6 +18,27 @@ __device__ __forceinline__ int xcd_tile(int block, int n_tiles) {
 
 constexpr float LOG2E = 1.44269504088896341f;
 
+// A fragment's Mahalanobis half-distance sigma = a dx^2 + b dx dy + c dy^2 (a = c00 / 2, b = c01,
+// c = c11 / 2; d = pixel centre - splat centre), evaluated as dx (a dx + b dy) + (c dy) dy with two fused
+// multiply-adds. The forward, both backward modes and the CPU restatement (oracle/b2c_oracle.c) evaluate
+// exactly this sequence, so every fragment's cutoff decision 0 <= sigma <= power agrees everywhere. lin =
+// a dx + b dy and cdy = c dy are kept for the backward: d sigma / d dx = lin + a dx, d sigma / d dy =
+// b dx + 2 cdy.
+struct FragGeom {
+  float dx, dy, lin, cdy, sigma;
+};
+
+__device__ __forceinline__ FragGeom frag_geom(float mx, float my, float a, float b, float c, float pcx, float pcy) {
+#pragma clang fp contract(off)
+  FragGeom f;
+  f.dx = pcx - mx;
+  f.dy = pcy - my;
+  f.lin = __builtin_fmaf(a, f.dx, b * f.dy);
+  f.cdy = c * f.dy;
+  f.sigma = __builtin_fmaf(f.dx, f.lin, f.cdy * f.dy);
+  return f;
+}
+
 // e^-sigma on the hardware exponential (v_exp_f32 is 2^x): the Gaussian factor of the opacity gradient.
 __device__ __forceinline__ float gauss_weight(float sigma) { return __builtin_amdgcn_exp2f(sigma * -LOG2E); }
 

@@ -19,14 +19,10 @@ namespace {
 // The loop is branch-free: a lane that has terminated, has run out of its list, or whose fragment fails
 // the cutoff contributes alpha = 0, which leaves T, the colour and the last index unchanged. Per splat the
 // LDS holds (mx, my, c00/2, c01), (c11/2, log2 opacity, power, 0) and the colour clamped at 0, staged from
-// the projection's 64-byte per-splat record (one cache line per gather); halving c00 and c11 is exact, so
-// sigma is the reference's 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy bit for bit (uncontracted).
-// The reference's sigma 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy, uncontracted, from (mx, my, c00 / 2, c01) and
-// (c11 / 2, ...): halving c00 and c11 is exact, so the result is bit for bit the same.
+// the projection's 64-byte per-splat record (one cache line per gather); sigma is frag_geom's
+// (raster_common.h) from (mx, my, c00 / 2, c01) and c11 / 2.
 __device__ __forceinline__ float splat_sigma(float4 g0, float4 g1, float pcx, float pcy) {
-#pragma clang fp contract(off)
-  const float dx = pcx - g0.x, dy = pcy - g0.y;
-  return ((g0.z * dx) * dx + (g1.x * dy) * dy) + (g0.w * dx) * dy;
+  return frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, pcx, pcy).sigma;
 }
 
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
@@ -93,7 +89,8 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     uint32_t off0 = my_list[0], off1 = my_list[1];
     // One step: 0 <= sigma <= power as one unsigned compare of the bit patterns (every listed splat has
     // power >= +0, since its tile test passed and sigma >= 0 for a positive-definite conic, and sigma is
-    // never -0: c00 dx^2 + c11 dy^2 >= +0 and +0 + -0 = +0; a NaN sigma fails either way), bitwise & so the
+    // never -0 for one: dx and dy are +0 or nonzero, and with dy = +0 the addend (c dy) dy is +0, with dx =
+    // +0 the sum is (c dy) dy >= +0; a NaN sigma fails either way), bitwise & so the
     // compiler does not branch on the compares; the exp is kept out of an exec-masked branch (a lane with
     // sigma < 0 has its alpha discarded by the select); only a valid fragment can stop a lane. A fragment is
     // composited (vis > 0) exactly when it is valid and does not stop the lane: a valid alpha is at least

@@ -423,6 +423,21 @@ uint32_t orc_bin(int n, const uint32_t* tile_count, const uint32_t* hit_info, co
  * Forward raster (raster_fwd.cu:8-71). Each pixel walks its tile's list front to back; the whole
  * tile's early exit only skips pixels that are already done, so a per-pixel loop is equivalent.
  * ---------------------------------------------------------------------------------------------- */
+/* A fragment's sigma as the raster kernels evaluate it (raster_common.h frag_geom): with a = c00 / 2,
+ * b = c01, c = c11 / 2, sigma = fma(dx, fma(a, dx, b dy), (c dy) dy); halving is exact. The reference's
+ * 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy (raster_fwd.cu:44) is the same quantity rounded differently. */
+static float frag_sigma(float dx, float dy, float c00, float c01, float c11) {
+  const float a = 0.5f * c00, c = 0.5f * c11;
+  const float lin = fmaf(a, dx, c01 * dy);
+  const float cdy = c * dy;
+  return fmaf(dx, lin, cdy * dy);
+}
+
+void orc_frag_sigma(int n, const float* dx, const float* dy, const float* c00, const float* c01, const float* c11,
+                    float* out) {
+  for (int i = 0; i < n; i++) out[i] = frag_sigma(dx[i], dy[i], c00[i], c01[i], c11[i]);
+}
+
 /* Fragments the last orc_raster_fwd call composited (F_contrib: alpha >= 1/255, before termination). */
 static uint64_t g_fwd_contrib = 0;
 uint64_t orc_last_fwd_contrib(void) { return g_fwd_contrib; }
@@ -460,7 +475,7 @@ void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], u
         uint32_t gid = vals_sorted[idx];
         const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
         float dx = pcx - a[0], dy = pcy - a[1];
-        float sigma = 0.5f * (a[2] * dx * dx + c[0] * dy * dy) + a[3] * dx * dy;
+        float sigma = frag_sigma(dx, dy, a[2], a[3], c[0]);
         if (sigma < 0.f || sigma > c[3]) continue;
         float alpha = fminf(ALPHA_MAX, c[1] * expf(-sigma));
         float next_T = T * (1.f - alpha);
@@ -628,7 +643,7 @@ void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], c
         uint32_t gid = vals_sorted[idx];
         const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
         float dx = pcx - a[0], dy = pcy - a[1];
-        float sigma = 0.5f * (a[2] * dx * dx + c[0] * dy * dy) + a[3] * dx * dy;
+        float sigma = frag_sigma(dx, dy, a[2], a[3], c[0]);
         if (!(sigma >= 0.f && sigma <= c[3])) continue;
         float g[GRAD_LANES];
         for (int k = 0; k < GRAD_LANES; k++) g[k] = 0.f;

@@ -125,6 +125,9 @@ double orc_ref_composite_seconds(void);
 void orc_set_threads(int n);
 
 /* ---- internal pieces exported for the pinning tests ---- */
+/* The raster kernels' fragment sigma from pixel-minus-centre offsets and the conic (c00, c01, c11). */
+void orc_frag_sigma(int n, const float* dx, const float* dy, const float* c00, const float* c01, const float* c11,
+                    float* out);
 void orc_sh_basis_f(int deg, float x, float y, float z, float* out);      /* splat_math.cuh:122-145 */
 void orc_sh_basis_d(int deg, double x, double y, double z, double* out);  /* reference.cpp:16-30 (+ degree 4) */
 void orc_quat_to_mat(const float* q, float* R);                           /* util.cuh:235-243 */

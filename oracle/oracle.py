@@ -89,9 +89,19 @@ def lib():
         _lib.orc_ref_set_sample.restype = None
         _lib.orc_ref_set_sample.argtypes = [C.c_uint64]
         _lib.orc_ref_composite_seconds.restype = C.c_double
+        _lib.orc_frag_sigma.restype = None
+        _lib.orc_frag_sigma.argtypes = [C.c_int] + [p] * 6
         _lib.orc_set_threads.restype = None
         _lib.orc_set_threads.argtypes = [C.c_int]
     return _lib
+
+
+def frag_sigma(dx, dy, c00, c01, c11):
+    """The raster kernels' fragment sigma (float32 arrays of one shape)."""
+    arrs = [np.ascontiguousarray(np.broadcast_to(v, np.shape(dx)), np.float32).ravel() for v in (dx, dy, c00, c01, c11)]
+    out = np.empty(arrs[0].size, np.float32)
+    lib().orc_frag_sigma(out.size, *[_ptr(a) for a in arrs], _ptr(out))
+    return out.reshape(np.shape(dx))
 
 
 def set_threads(n: int) -> None:

@@ -1,12 +1,15 @@
 """The forward raster's quadrant culling test (quadrant_mask in b2ctrain_amd/csrc/kernels/raster_common.h),
-restated in float32 numpy, must be conservative: a quadrant with a pixel centre where the reference's
-sigma (src/gpu/raster_fwd.cu:44-50, 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy, uncontracted fp32) passes
-0 <= sigma <= power must keep its bit. Checked by brute force over all 64 pixel centres on random splats,
+restated in float32 numpy, must be conservative: a quadrant with a pixel centre where the raster kernels'
+fp32 sigma (frag_geom: dx (a dx + b dy) + (c dy) dy with two fused multiply-adds, evaluated here by the
+oracle's C restatement; the reference's src/gpu/raster_fwd.cu:44-50 rounds the same quantity differently)
+passes 0 <= sigma <= power must keep its bit. Checked by brute force over all 64 pixel centres on random splats,
 including needle-thin ellipses (axis ratio up to 1e5) whose terms cancel, splats centred inside, on the
 edges and far outside the tile, and adversarially: power set to the fp32 sigma of one pixel, which puts
 that pixel exactly on the cutoff. The GPU parity tests check the device code itself (a wrongly culled
 fragment changes the rendered colour by at least alpha = 1/255 of its weight)."""
 import numpy as np
+
+from oracle import oracle as O
 
 f32 = np.float32
 
@@ -66,7 +69,7 @@ def quadrant_mask_all_edges(mx, my, ah, b, ch, power, x0, y0):
 def sigma_at(mx, my, c00, c01, c11, x0, y0, i, j):
     dx = (x0 + f32(i)) - mx
     dy = (y0 + f32(j)) - my
-    return ((f32(0.5) * c00 * dx) * dx + (f32(0.5) * c11 * dy) * dy) + (c01 * dx) * dy
+    return O.frag_sigma(dx, dy, c00, c01, c11)
 
 
 def pixel_truth(mx, my, c00, c01, c11, power, x0, y0):
@@ -74,9 +77,7 @@ def pixel_truth(mx, my, c00, c01, c11, power, x0, y0):
     truth = np.zeros(mx.shape, np.uint32)
     for j in range(8):
         for i in range(8):
-            dx = (x0 + f32(i)) - mx
-            dy = (y0 + f32(j)) - my
-            sig = ((f32(0.5) * c00 * dx) * dx + (f32(0.5) * c11 * dy) * dy) + (c01 * dx) * dy
+            sig = sigma_at(mx, my, c00, c01, c11, x0, y0, i, j)
             hit = (sig >= 0) & (sig <= power)
             truth |= np.where(hit, np.uint32(1 << (2 * (j // 4) + i // 4)), np.uint32(0))
     return truth
