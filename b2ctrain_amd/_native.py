@@ -41,6 +41,27 @@ class LossOpts(C.Structure):
                 ("grad_scale", C.c_float)]
 
 
+class AdamOpts(C.Structure):
+    _fields_ = [("t", C.c_int), ("sparse", C.c_int), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+                ("lr_mean", C.c_float), ("lr_rot", C.c_float), ("lr_scale", C.c_float), ("lr_opac", C.c_float),
+                ("lr_dc", C.c_float), ("lr_sh_rest", C.c_float), ("noise_weight", C.c_float),
+                ("noise_clamp", C.c_float), ("seed", C.c_uint32), ("step", C.c_uint32)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+def adam_opts(**kw) -> AdamOpts:
+    """The reference's OptimParams defaults (b2c_adam_defaults), then any field given by keyword."""
+    a = AdamOpts()
+    lib().b2c_adam_defaults(C.byref(a))
+    for k, v in kw.items():
+        if not hasattr(a, k):
+            raise KeyError(k)
+        setattr(a, k, v)
+    return a
+
+
 class CtxInfo(C.Structure):
     _fields_ = [("W", C.c_int), ("H", C.c_int), ("tiles_x", C.c_int), ("tiles_y", C.c_int), ("n_tiles", C.c_int),
                 ("tile_bits", C.c_int), ("num_isect", C.c_uint32), ("isect_cap", C.c_uint64)]
@@ -63,6 +84,8 @@ EXPORTS = [
     "b2c_ctx_zero", "b2c_ctx_synchronize", "b2c_ctx_stream", "b2c_view_create",
     "b2c_view_destroy", "b2c_render_forward", "b2c_project_splats", "b2c_bin_and_sort", "b2c_rasterize_forward",
     "b2c_photometric_loss", "b2c_accumulate_loss", "b2c_rasterize_backward", "b2c_optimizer_grad", "b2c_train_step",
+    "b2c_model_write", "b2c_model_zero_optimizer", "b2c_model_adam_t", "b2c_adam_defaults", "b2c_optimizer_step",
+    "b2c_train_step_adam", "b2c_adam_step_constants",
     # launcher layer
     "b2c_hip_project", "b2c_radix_sort_temp_bytes", "b2c_hip_radix_sort_pairs", "b2c_hip_radix_sort_kv2",
     "b2c_hip_depth_keys",
@@ -113,6 +136,14 @@ def lib():
         L.b2c_rasterize_backward.argtypes = [p, p, C.POINTER(RenderOpts), i, f]
         L.b2c_optimizer_grad.argtypes = [p, p, C.POINTER(RenderOpts), i, i]
         L.b2c_train_step.argtypes = [p, p, p, C.POINTER(RenderOpts), C.POINTER(LossOpts), i, i, C.POINTER(StepTimes)]
+        L.b2c_model_write.argtypes = [p, C.c_char_p, p, C.c_size_t]
+        L.b2c_model_zero_optimizer.argtypes = [p]
+        L.b2c_model_adam_t.argtypes = [p, C.POINTER(i)]
+        L.b2c_adam_defaults.argtypes = [C.POINTER(AdamOpts)]
+        L.b2c_adam_defaults.restype = None
+        L.b2c_optimizer_step.argtypes = [p, p, C.POINTER(RenderOpts), C.POINTER(AdamOpts)]
+        L.b2c_train_step_adam.argtypes = [p, p, p, C.POINTER(RenderOpts), C.POINTER(LossOpts), i, C.POINTER(AdamOpts),
+                                          C.POINTER(StepTimes)]
         L.b2c_radix_sort_temp_bytes.restype = C.c_size_t
         L.b2c_radix_sort_temp_bytes.argtypes = [C.c_uint32]
         L.b2c_scan_temp_bytes.restype = C.c_size_t
@@ -167,6 +198,9 @@ _FIELD_SPEC = {
     "out_feat": (np.float32, (4,), "P"), "last_idx": (np.uint32, (), "P"), "v_out": (np.float32, (4,), "P"),
     "v_splat": (np.float32, (GRAD_LANES,), "n"), "vis_flag": (np.uint32, (), "n"), "loss_accum": (np.float32, (16,), "1"),
 }
+
+
+_FLOAT4_FIELDS = ("pos_op", "quat", "lscale", "m_pos_op", "v_pos_op", "m_quat", "v_quat", "m_lscale", "v_lscale")
 
 
 class Renderer:
@@ -274,6 +308,30 @@ class Renderer:
                                         self.degree if active_deg is None else active_deg, flags),
               "optimizer_grad")
 
+    def adam(self, opts: AdamOpts | None = None, **kw):
+        """optimizer_step without grad_out: the projection VJP fused with the Adam update of the model."""
+        a = adam_opts() if opts is None else opts
+        check(self.L.b2c_optimizer_step(self.ctx, self.model, C.byref(self.render_opts(**kw)), C.byref(a)),
+              "optimizer_step")
+
+    def step_adam(self, opts: AdamOpts | None = None, mode=1, grad_scale=None, timed=False, cam=None, bg=None):
+        """One complete training iteration ending in the fused update (b2c_train_step_adam)."""
+        gs = 3.0 * self.W * self.H if grad_scale is None else grad_scale
+        a = adam_opts() if opts is None else opts
+        t = StepTimes() if timed else None
+        check(self.L.b2c_train_step_adam(self.ctx, self.model, self.view, C.byref(self.render_opts(cam=cam, bg=bg)),
+                                         C.byref(self.loss_opts(gs, bg)), mode, C.byref(a),
+                                         C.byref(t) if timed else None), "train_step_adam")
+        return t.as_dict() if timed else None
+
+    def adam_t(self) -> int:
+        t = C.c_int(0)
+        check(self.L.b2c_model_adam_t(self.model, C.byref(t)), "model_adam_t")
+        return t.value
+
+    def zero_optimizer(self):
+        check(self.L.b2c_model_zero_optimizer(self.model), "model_zero_optimizer")
+
     def step(self, mode=1, grad_scale=None, accumulate=False, timed=False, cam=None, bg=None):
         gs = 3.0 * self.W * self.H if grad_scale is None else grad_scale
         t = StepTimes() if timed else None
@@ -310,9 +368,67 @@ class Renderer:
         check(self.L.b2c_ctx_zero(self.ctx, field.encode()), f"zero {field}")
 
     def read_model(self, field):
-        out = np.empty((self.n, 4) if field in ("pos_op", "quat", "lscale") else (self.n,), np.float32)
+        dt = np.uint32 if field == "last_step" else np.float32
+        out = np.empty((self.n, 4) if field in _FLOAT4_FIELDS else (self.n,), dt)
         check(self.L.b2c_model_read(self.model, field.encode(), _ptr(out), out.nbytes), f"model_read {field}")
         return out
+
+    def write_model(self, field, arr):
+        a = np.ascontiguousarray(arr)
+        check(self.L.b2c_model_write(self.model, field.encode(), _ptr(a), a.nbytes), f"model_write {field}")
+
+    def _planar(self, name):
+        """A planar [lanes][cap] SH array (parameters or first moments) as [n][lanes] float32."""
+        half = name.endswith("_hi")
+        _, size = self.device_ptr(name, model=True)
+        lanes = 3 if name.endswith("_dc") else 3 * ((self.degree + 1) ** 2 - 1)
+        cap = size // (lanes * (2 if half else 4))
+        raw = np.empty((lanes, cap), np.uint16 if half else np.float32)
+        check(self.L.b2c_model_read(self.model, name.encode(), _ptr(raw), raw.nbytes), f"model_read {name}")
+        vals = raw.view(np.float16).astype(np.float32) if half else raw
+        return np.ascontiguousarray(vals[:, : self.n].T), cap
+
+    def _write_planar(self, name, vals):
+        half = name.endswith("_hi")
+        _, size = self.device_ptr(name, model=True)
+        lanes = vals.shape[1]
+        cap = size // (lanes * (2 if half else 4))
+        raw = np.zeros((lanes, cap), np.float32)
+        raw[:, : self.n] = vals.T
+        raw = raw.astype(np.float16).view(np.uint16) if half else raw
+        self.write_model(name, np.ascontiguousarray(raw))
+
+    def _band_names(self, sh_fp16):
+        return ("sh_hi", "m_sh_hi") if sh_fp16 else ("sh_hi32", "m_sh_hi32")
+
+    def model_state(self):
+        """Parameters and Adam state in host layouts: float4 fields [n][4], SH and their first moments
+        coefficient-major [n][K][3] (binary16 bands widened), v_sh [n], last_step [n]."""
+        st = {f: self.read_model(f) for f in _FLOAT4_FIELDS}
+        st["v_sh"] = self.read_model("v_sh")
+        st["last_step"] = self.read_model("last_step")
+        K = (self.degree + 1) ** 2
+        hi, mhi = self._band_names(self.scene.sh_fp16)
+        for key, dc, bands in (("sh", "sh_dc", hi), ("m_sh", "m_sh_dc", mhi)):
+            flat = np.zeros((self.n, 3 * K), np.float32)
+            flat[:, :3] = self._planar(dc)[0]
+            if K > 1:
+                flat[:, 3:] = self._planar(bands)[0]
+            st[key] = flat.reshape(self.n, K, 3)
+        return st
+
+    def set_model_state(self, st):
+        """Write back what model_state returns (any subset of its keys)."""
+        K = (self.degree + 1) ** 2
+        hi, mhi = self._band_names(self.scene.sh_fp16)
+        for f, a in st.items():
+            if f in ("sh", "m_sh"):
+                flat = np.asarray(a, np.float32).reshape(self.n, 3 * K)
+                self._write_planar("sh_dc" if f == "sh" else "m_sh_dc", flat[:, :3])
+                if K > 1:
+                    self._write_planar(hi if f == "sh" else mhi, flat[:, 3:])
+            else:
+                self.write_model(f, np.asarray(a, np.uint32 if f == "last_step" else np.float32))
 
     def device_ptr(self, field, model=False):
         """Device address and byte size of a context (or model) buffer."""

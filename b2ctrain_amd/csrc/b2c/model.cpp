@@ -1,7 +1,8 @@
-// Model storage (replaces the upload / download / growth parts of src/model.cu:8-118). The host side only
-// moves whole arrays: an upload copies the cloud's five field arrays into one device staging block and a
-// scatter kernel writes the float4 fields and the planar SH lanes (fp16 rounding on the device); a download
-// is the inverse gather; growth re-lays the planar lanes out with a kernel (kernels/model_io.hip).
+// Model storage (replaces the upload / download / growth / optimizer-reset parts of src/model.cu:8-118).
+// The host side only moves whole arrays: an upload copies the cloud's five field arrays into one device
+// staging block and a scatter kernel writes the float4 fields and the planar SH lanes (fp16 rounding on
+// the device); a download is the inverse gather; growth re-lays the planar lanes out with a kernel
+// (kernels/model_io.hip) and starts the new slots' statistics and Adam moments at zero.
 #include "model.h"
 
 #include <algorithm>
@@ -81,10 +82,21 @@ void Model::reserve(int want, hipStream_t stream) {
   regrow_planar(sh_dc, 3, n, cap, grown, stream);
   if (sh_fp16) regrow_planar(sh_hi, bands, n, cap, grown, stream);
   else regrow_planar(sh_hi32, bands, n, cap, grown, stream);
-  for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight}) {
+  // Per-splat arrays keep their first cap entries; the new ones start at zero (statistics, moments).
+  const size_t fresh = (size_t)(grown - cap);
+  for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight, &v_sh}) {
     st->reserve((size_t)grown, true, stream);
-    LAUNCH_CHECK(b2c_hip_fill_u32(reinterpret_cast<uint32_t*>(st->ptr + cap), 0u, (size_t)(grown - cap), stream));
+    LAUNCH_CHECK(b2c_hip_fill_u32(reinterpret_cast<uint32_t*>(st->ptr + cap), 0u, fresh, stream));
   }
+  last_step.reserve((size_t)grown, true, stream);
+  LAUNCH_CHECK(b2c_hip_fill_u32(last_step.ptr + cap, 0u, fresh, stream));
+  for (DevBuf<float4>* mo : {&m_pos_op, &v_pos_op, &m_quat, &v_quat, &m_lscale, &v_lscale}) {
+    mo->reserve((size_t)grown, true, stream);
+    LAUNCH_CHECK(b2c_hip_fill_u32(reinterpret_cast<uint32_t*>(mo->ptr + cap), 0u, 4 * fresh, stream));
+  }
+  regrow_planar(m_sh_dc, 3, n, cap, grown, stream);
+  if (sh_fp16) regrow_planar(m_sh_hi, bands, n, cap, grown, stream);
+  else regrow_planar(m_sh_hi32, bands, n, cap, grown, stream);
   cap = grown;
 }
 
@@ -92,9 +104,12 @@ void Model::upload(const SplatCloud& c, hipStream_t stream, const float* floor) 
   degree = c.sh_degree;
   n = (int)c.n;
   cap = 0;
-  for (DevBuf<float4>* f : {&pos_op, &quat, &lscale}) f->free();
-  sh_dc.free(); sh_hi.free(); sh_hi32.free();
-  for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight}) st->free();
+  for (DevBuf<float4>* f : {&pos_op, &quat, &lscale, &m_pos_op, &v_pos_op, &m_quat, &v_quat, &m_lscale, &v_lscale})
+    f->free();
+  for (DevBuf<float>* f : {&sh_dc, &sh_hi32, &m_sh_dc, &m_sh_hi32}) f->free();
+  sh_hi.free(); m_sh_hi.free();
+  for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight, &v_sh}) st->free();
+  last_step.free();
   reserve(std::max(n, 1), stream);
   CloudStage stage(c.n, K(), floor != nullptr);
   to_device(stage.fields.pos, c.pos, stream);
@@ -105,6 +120,7 @@ void Model::upload(const SplatCloud& c, hipStream_t stream, const float* floor) 
   if (floor && n) HIP_CHECK(hipMemcpyAsync(stage.fields.floor_, floor, n * sizeof(float), hipMemcpyHostToDevice, stream));
   const b2c_model_dev dst = layout();
   LAUNCH_CHECK(b2c_hip_model_scatter(&stage.fields, &dst, stream));
+  zero_optimizer(stream);
   zero_stats(stream);
   HIP_CHECK(hipStreamSynchronize(stream));  // the stage and the caller's arrays may go away now
 }
@@ -134,6 +150,29 @@ void Model::set_floor(const std::vector<float>& f, hipStream_t stream) {
 
 void Model::zero_stats(hipStream_t stream) {
   for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight}) st->zero(stream);
+}
+
+void Model::zero_optimizer(hipStream_t stream) {
+  for (DevBuf<float4>* mo : {&m_pos_op, &v_pos_op, &m_quat, &v_quat, &m_lscale, &v_lscale}) mo->zero(stream);
+  for (DevBuf<float>* f : {&m_sh_dc, &m_sh_hi32, &v_sh}) f->zero(stream);
+  m_sh_hi.zero(stream);
+  last_step.zero(stream);
+  adam_t = 0;
+}
+
+b2c_adam_state Model::adam_state() const {
+  b2c_adam_state s{};
+  s.m_pos_op = reinterpret_cast<float*>(m_pos_op.ptr);
+  s.v_pos_op = reinterpret_cast<float*>(v_pos_op.ptr);
+  s.m_quat = reinterpret_cast<float*>(m_quat.ptr);
+  s.v_quat = reinterpret_cast<float*>(v_quat.ptr);
+  s.m_lscale = reinterpret_cast<float*>(m_lscale.ptr);
+  s.v_lscale = reinterpret_cast<float*>(v_lscale.ptr);
+  const ShBuf m = m_sh();
+  s.m_sh = b2c_sh_planes{m.dc, sh_fp16 ? m.hi : nullptr, sh_fp16 ? nullptr : m.hi32, m.stride};
+  s.v_sh = v_sh.ptr;
+  s.last_step = last_step.ptr;
+  return s;
 }
 
 }  // namespace b2c

@@ -36,6 +36,7 @@ struct ShBuf {
   float* hi32 = nullptr;
   size_t stride = 0;
   b2c_sh_view view() const { return b2c_sh_view{dc, hi, hi32, stride}; }
+  b2c_sh_planes planes() const { return b2c_sh_planes{dc, hi, hi32, stride}; }
 };
 
 struct Model {
@@ -46,10 +47,23 @@ struct Model {
   DevBuf<uint16_t> sh_hi;
   // statistics updated as side effects of the path (model.h:27-30)
   DevBuf<float> refine_norm, max_screen, vis_count, vis_weight;
+  // Adam state (model.h:19-28): first / second moments beside each float4 array; SH first moments in the
+  // SH's planar layout and band precision; v_sh one second moment per splat; last_step the Adam step of
+  // each splat's last update (lazy sparse Adam, 0 = never); adam_t the step counter the trainer advances.
+  DevBuf<float4> m_pos_op, v_pos_op, m_quat, v_quat, m_lscale, v_lscale;
+  DevBuf<float> m_sh_dc, m_sh_hi32, v_sh;
+  DevBuf<uint16_t> m_sh_hi;
+  DevBuf<uint32_t> last_step;
+  int adam_t = 0;
 
   ShBuf sh() const {
     ShBuf b;
     b.dc = sh_dc.ptr; b.hi = sh_hi.ptr; b.hi32 = sh_hi32.ptr; b.stride = (size_t)cap;
+    return b;
+  }
+  ShBuf m_sh() const {
+    ShBuf b;
+    b.dc = m_sh_dc.ptr; b.hi = m_sh_hi.ptr; b.hi32 = m_sh_hi32.ptr; b.stride = (size_t)cap;
     return b;
   }
   int K() const { return sh_coeffs_for_degree(degree); }
@@ -63,6 +77,10 @@ struct Model {
   // Set the frozen per-splat floor f (lscale.w); not part of the reference's upload.
   void set_floor(const std::vector<float>& f, hipStream_t stream = nullptr);
   void zero_stats(hipStream_t stream = nullptr);
+  // Moments, v_sh and last_step to zero, adam_t = 0 (model.cu:104-107).
+  void zero_optimizer(hipStream_t stream = nullptr);
+  // The Adam state as the fused optimizer kernel takes it.
+  b2c_adam_state adam_state() const;
   // The device layout as the launcher layer takes it.
   b2c_model_dev layout() const;
 };

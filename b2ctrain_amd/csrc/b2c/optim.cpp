@@ -1,20 +1,20 @@
-// optimizer_step, gradient path (replaces src/gpu/optim.cu:434-442 launch + 99-253, 292-296).
+// optimizer_step (replaces src/gpu/optim.cu:379-392 and the kernel body 99-377): one launch of the fused
+// VJP kernel (kernels/vjp.hip), in gradient mode when grad_out is set, else in update mode.
 #include "optim.h"
 
 namespace b2c {
 
 void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t stream) {
   if (m.n == 0) return;
-  if (!op.grad_out) throw std::runtime_error("optimizer_step: the Adam update is not part of this build (set grad_out)");
   if (op.mip || op.pos_override || op.quat_override || op.lscale_override || op.sh_frame || op.canon_rot || op.spa_z ||
-      op.stretch_w || op.g_app_out || op.g_pos_out)
+      op.stretch_w || op.g_app_out || op.g_pos_out || op.frozen || op.update_mask)
     throw std::runtime_error("optimizer_step: deformation / sparsify / appearance extensions are not supported by this build");
   if (m.degree < 0 || m.degree > 4) throw std::runtime_error("bad degree");
   b2c_vjp_args a{};
   a.n = m.n; a.degree = m.degree; a.active_deg = op.active_sh_degree;
-  a.pos_op = reinterpret_cast<const float*>(m.pos_op.ptr);
-  a.quat = reinterpret_cast<const float*>(m.quat.ptr);
-  a.lscale = reinterpret_cast<const float*>(m.lscale.ptr);
+  a.pos_op = reinterpret_cast<float*>(m.pos_op.ptr);
+  a.quat = reinterpret_cast<float*>(m.quat.ptr);
+  a.lscale = reinterpret_cast<float*>(m.lscale.ptr);
   a.sh = m.sh().view();
   a.cam = op.cam.dev();
   a.v_splat = ctx.v_splat;
@@ -25,6 +25,25 @@ void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t
   a.sparse = op.sparse ? 1 : 0;
   a.refine_norm = m.refine_norm.ptr;
   a.vis_count = m.vis_count.ptr;
+  if (!op.grad_out) {
+    if (op.t < 1) throw std::runtime_error("optimizer_step: the Adam step t must be >= 1");
+    if (!(op.beta1 >= 0.f && op.beta1 < 1.f && op.beta2 > 0.f && op.beta2 < 1.f))
+      throw std::runtime_error("optimizer_step: beta1 must lie in [0, 1) and beta2 in (0, 1)");
+    const ShBuf sh = m.sh();
+    a.sh_out = b2c_sh_planes{sh.dc, m.sh_fp16 ? sh.hi : nullptr, m.sh_fp16 ? nullptr : sh.hi32, sh.stride};
+    a.sh.hi16 = a.sh_out.hi16;
+    a.sh.hi32 = a.sh_out.hi32;
+    a.adam = m.adam_state();
+    b2c_adam_step& s = a.step;
+    s.t = op.t;
+    s.sparse = op.sparse ? 1 : 0;
+    s.beta1 = op.beta1; s.beta2 = op.beta2; s.eps = op.eps;
+    s.lr_mean = op.lr_mean; s.lr_rot = op.lr_rot; s.lr_scale = op.lr_scale; s.lr_opac = op.lr_opac;
+    s.lr_dc = op.lr_dc; s.lr_sh_rest = op.lr_sh_rest;
+    s.noise_weight = op.noise_weight; s.noise_clamp = op.noise_clamp;
+    s.seed = op.seed; s.step = op.step;
+    b2c_adam_step_constants(&s);
+  }
   LAUNCH_CHECK(b2c_hip_vjp(&a, stream));
 }
 

@@ -1,7 +1,9 @@
-// Optimizer API of the drop-in (replaces src/gpu/optim.h:1-52). This build implements the gradient part:
-// optimizer_step with grad_out set runs the projection VJP and writes [n][11 + 3K] parameter gradients
-// (pos3, opacity, quat4, log-scale3, SH), exactly the reference's test path (optim.cu:292-296). The Adam
-// update, MCMC noise and the cage / sparsify extensions are outside this build and throw when requested.
+// Optimizer API of the drop-in (replaces src/gpu/optim.h:1-52). optimizer_step runs the projection VJP
+// and then either writes [n][11 + 3K] parameter gradients (pos3, opacity, quat4, log-scale3, SH) when
+// grad_out is set (the reference's test path, optim.cu:292-296), or applies the fused update: Adam with
+// bias correction, the lazy catch-up of sparse Adam, the SH moments with stochastically rounded fp16 bands,
+// and MCMC noise on the means (optim.cu:298-377). The cage / sparsify / appearance extensions
+// (pos_override .. g_app_out) are outside this build and throw when requested.
 #pragma once
 #include "render.h"
 
@@ -34,7 +36,8 @@ struct OptimParams {
   bool grad_accumulate = false;  // this build: add into grad_out (gradients summed over several views)
 };
 
-// Projection backward; consumes and clears ctx.v_splat / ctx.vis_flag; updates Model::vis_count / refine_norm.
+// Projection backward + update; consumes and clears ctx.v_splat / ctx.vis_flag; updates Model::vis_count /
+// refine_norm. Without grad_out it writes the model's parameters and Adam state (op.t >= 1).
 void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t stream);
 
 }  // namespace b2c

@@ -56,6 +56,29 @@ b2c::Camera to_camera(const b2c_camera& c) {
   return cam;
 }
 
+int train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
+               int mode, int flags, const b2c_adam_opts* adam, b2c_step_times* times);
+b2c::RenderParams to_params(const b2c_render_opts& o);
+
+// OptimParams of an update step (optim.h:6-20 fields; op.t = ++model.adam_t when t is 0, trainer.cpp:512).
+b2c::OptimParams to_optim(const b2c_render_opts& ro, const b2c_adam_opts& a, b2c::Model& m) {
+  b2c::OptimParams op;
+  op.cam = to_params(ro).cam;
+  op.active_sh_degree = ro.sh_degree;
+  if (a.t < 0) throw std::runtime_error("optimizer_step: negative Adam step");
+  if (!(a.beta1 >= 0.f && a.beta1 < 1.f && a.beta2 > 0.f && a.beta2 < 1.f))
+    throw std::runtime_error("optimizer_step: beta1 must lie in [0, 1) and beta2 in (0, 1)");
+  op.t = a.t > 0 ? a.t : m.adam_t + 1;
+  m.adam_t = op.t;
+  op.beta1 = a.beta1; op.beta2 = a.beta2; op.eps = a.eps;
+  op.lr_mean = a.lr_mean; op.lr_rot = a.lr_rot; op.lr_scale = a.lr_scale; op.lr_opac = a.lr_opac;
+  op.lr_dc = a.lr_dc; op.lr_sh_rest = a.lr_sh_rest;
+  op.noise_weight = a.noise_weight; op.noise_clamp = a.noise_clamp;
+  op.seed = a.seed; op.step = a.step;
+  op.sparse = a.sparse != 0;
+  return op;
+}
+
 b2c::RenderParams to_params(const b2c_render_opts& o) {
   b2c::RenderParams p;
   p.cam = b2c::CameraGPU::from(to_camera(o.cam), o.W, o.H);
@@ -160,12 +183,28 @@ namespace {
 Field model_field(const b2c_model* m, const std::string& name) {
   const b2c::Model& x = m->m;
   const size_t n = (size_t)x.n;
+  const size_t cap = (size_t)x.cap, bands = 3 * (size_t)(x.K() - 1);
   std::map<std::string, Field> f = {
       {"pos_op", {x.pos_op.ptr, n * 16}},         {"quat", {x.quat.ptr, n * 16}},
       {"lscale", {x.lscale.ptr, n * 16}},         {"vis_weight", {x.vis_weight.ptr, n * 4}},
       {"vis_count", {x.vis_count.ptr, n * 4}},    {"refine_norm", {x.refine_norm.ptr, n * 4}},
       {"max_screen", {x.max_screen.ptr, n * 4}},
+      {"m_pos_op", {x.m_pos_op.ptr, n * 16}},     {"v_pos_op", {x.v_pos_op.ptr, n * 16}},
+      {"m_quat", {x.m_quat.ptr, n * 16}},         {"v_quat", {x.v_quat.ptr, n * 16}},
+      {"m_lscale", {x.m_lscale.ptr, n * 16}},     {"v_lscale", {x.v_lscale.ptr, n * 16}},
+      {"v_sh", {x.v_sh.ptr, n * 4}},              {"last_step", {x.last_step.ptr, n * 4}},
+      // planar [lanes][cap] arrays, whole
+      {"sh_dc", {x.sh_dc.ptr, 3 * cap * 4}},      {"m_sh_dc", {x.m_sh_dc.ptr, 3 * cap * 4}},
   };
+  if (bands) {
+    if (x.sh_fp16) {
+      f["sh_hi"] = {x.sh_hi.ptr, bands * cap * 2};
+      f["m_sh_hi"] = {x.m_sh_hi.ptr, bands * cap * 2};
+    } else {
+      f["sh_hi32"] = {x.sh_hi32.ptr, bands * cap * 4};
+      f["m_sh_hi32"] = {x.m_sh_hi32.ptr, bands * cap * 4};
+    }
+  }
   auto it = f.find(name);
   if (it == f.end()) throw std::runtime_error("unknown model field: " + name);
   return it->second;
@@ -179,6 +218,26 @@ int b2c_model_read(const b2c_model* m, const char* field, void* host, size_t byt
     HIP_CHECK(hipDeviceSynchronize());
     HIP_CHECK(hipMemcpy(host, f.ptr, bytes, hipMemcpyDeviceToHost));
   });
+}
+
+int b2c_model_write(b2c_model* m, const char* field, const void* host, size_t bytes) {
+  return guarded([&] {
+    const Field f = model_field(m, field);
+    if (bytes > f.bytes) throw std::runtime_error(std::string("model_write: too many bytes for ") + field);
+    HIP_CHECK(hipDeviceSynchronize());
+    HIP_CHECK(hipMemcpy(f.ptr, host, bytes, hipMemcpyHostToDevice));
+  });
+}
+
+int b2c_model_zero_optimizer(b2c_model* m) {
+  return guarded([&] {
+    m->m.zero_optimizer(nullptr);
+    HIP_CHECK(hipDeviceSynchronize());
+  });
+}
+
+int b2c_model_adam_t(const b2c_model* m, int* t) {
+  return guarded([&] { *t = m->m.adam_t; });
 }
 
 int b2c_model_device_ptr(const b2c_model* m, const char* field, void** ptr, size_t* bytes) {
@@ -344,8 +403,41 @@ int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int a
   });
 }
 
+void b2c_adam_defaults(b2c_adam_opts* a) {
+  const b2c::OptimParams d{};
+  *a = b2c_adam_opts{};
+  a->t = 0;
+  a->sparse = 0;
+  a->beta1 = d.beta1; a->beta2 = d.beta2; a->eps = d.eps;
+  a->lr_mean = d.lr_mean; a->lr_rot = d.lr_rot; a->lr_scale = d.lr_scale; a->lr_opac = d.lr_opac;
+  a->lr_dc = d.lr_dc; a->lr_sh_rest = d.lr_sh_rest;
+  a->noise_weight = d.noise_weight; a->noise_clamp = d.noise_clamp;
+  a->seed = d.seed; a->step = d.step;
+}
+
+int b2c_optimizer_step(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, const b2c_adam_opts* a) {
+  return guarded([&] {
+    b2c::OptimParams op = to_optim(*o, *a, m->m);
+    b2c::optimizer_step(c->ctx, m->m, op, c->stream);
+  });
+}
+
 int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
                    int mode, int flags, b2c_step_times* times) {
+  return train_step(c, m, v, ro, lo, mode, flags, nullptr, times);
+}
+
+int b2c_train_step_adam(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro,
+                        const b2c_loss_opts* lo, int mode, const b2c_adam_opts* a, b2c_step_times* times) {
+  return train_step(c, m, v, ro, lo, mode, 0, a, times);
+}
+
+}  // extern "C"
+
+namespace {
+
+int train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
+               int mode, int flags, const b2c_adam_opts* adam, b2c_step_times* times) {
   return guarded([&] {
     const b2c::RenderParams p = to_params(*ro);
     b2c::LossParams lp = to_loss(*lo);
@@ -356,12 +448,14 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
       if (times) HIP_CHECK(hipEventRecord(c->ev[k], s));
     };
     const size_t per = 11 + 3 * (size_t)m->m.K();
-    if (c->grads.count < (size_t)m->m.n * per || c->degree != m->m.degree) {
+    if (!adam && (c->grads.count < (size_t)m->m.n * per || c->degree != m->m.degree)) {
       c->grads.free();
       c->grads.reserve((size_t)m->m.n * per);
       c->grads.zero(s);
       c->degree = m->m.degree;
     }
+    // the update's parameters are checked (and the step counter advanced) before any work is queued
+    b2c::OptimParams op = adam ? to_optim(*ro, *adam, m->m) : b2c::OptimParams{};
     mark(0);
     b2c::project_splats(c->ctx, m->m, p, s);
     mark(1);
@@ -378,12 +472,13 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
       b2c::rasterize_backward_tc(c->ctx, m->m, p, lp.grad_scale, s);
     c->ctx.bwd_split_event = nullptr;
     mark(5);
-    b2c::OptimParams op;
-    op.cam = p.cam;
-    op.active_sh_degree = p.sh_degree;
-    op.grad_out = c->grads.ptr;
-    op.grad_accumulate = (flags & B2C_GRAD_ACCUMULATE) != 0;
-    op.sparse = (flags & B2C_GRAD_SPARSE) != 0;
+    if (!adam) {
+      op.cam = p.cam;
+      op.active_sh_degree = p.sh_degree;
+      op.grad_out = c->grads.ptr;
+      op.grad_accumulate = (flags & B2C_GRAD_ACCUMULATE) != 0;
+      op.sparse = (flags & B2C_GRAD_SPARSE) != 0;
+    }
     b2c::optimizer_step(c->ctx, m->m, op, s);
     mark(6);
     if (times) {
@@ -403,4 +498,4 @@ int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render
   });
 }
 
-}  // extern "C"
+}  // namespace

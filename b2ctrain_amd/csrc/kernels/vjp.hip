@@ -1,18 +1,23 @@
-// Projection VJP (replaces the gradient half of optim_kernel, src/gpu/optim.cu:99-253, with the grad_out
-// write of 292-296): one thread per splat turns the 13 screen-space gradient lanes into parameter
-// gradients [pos3, opacity, quat4, log-scale3, SH 3K]. Reads and clears v_splat and vis_flag (the
-// consumed-and-zeroed contract of optim.cu:110-121). accumulate = 1 adds into grad_out so gradients of
-// several views can be summed; 0 overwrites like the reference, and with sparse set leaves the rows of splats
-// without gradient alone as the reference's early return does (optim.cu:148).
+// Projection VJP and fused optimizer (replaces optim_kernel, src/gpu/optim.cu:99-377): one thread per
+// splat turns the 13 screen-space gradient lanes into parameter gradients [pos3, opacity, quat4,
+// log-scale3, SH 3K]. Reads and clears v_splat and vis_flag (the consumed-and-zeroed contract of
+// optim.cu:110-121). With grad_out set the gradients are written (optim.cu:292-296): accumulate = 1 adds
+// into grad_out so gradients of several views can be summed; 0 overwrites like the reference, and with
+// sparse set leaves the rows of splats without gradient alone as the reference's early return does
+// (optim.cu:148). Without grad_out the same gradient row feeds the Adam / lazy sparse Adam / MCMC noise
+// update of the splat's parameters (adam_update below).
 // The chain is derived here from the semi-axis form of the projection (screen_splat.h): from the conic to
 // the screen covariance, to the image-plane semi-axes u_j, and from those to the semi-axis lengths, the
 // camera-frame rotation, the Jacobian scale and the ray tangents; the colour's view-direction term comes
 // from the SH basis evaluated on dual numbers. No world-space covariance is formed. Evaluated without FMA
 // contraction (the culling decisions of the recomputed projection must match the forward's bit for bit).
 #pragma clang fp contract(off)
+#include <cmath>
+
 #include "b2c_kernels.h"
 #include "device_math.h"
 #include "screen_splat.h"
+#include "adam_math.h"
 
 namespace b2c {
 namespace dev {
@@ -45,7 +50,155 @@ __device__ __forceinline__ float4 unit_quat_vjp(float4 qn, float inv_len, float4
 // would touch one cache line per lane per instruction).
 constexpr int VJP_BLOCK = 64;
 
+// One Adam step on one parameter, after the lazy catch-up (optim.cu:301-315). A splat last updated s + 1
+// steps ago would, under dense Adam with zero gradient, have seen its moments decay to beta1^s m and
+// beta2^s v and moved by lr sum_{k=1..s} (beta1^k m) / sqrt(beta2^k v) = lr drift m / sqrt(v), with
+// drift = r (1 - r^s) / (1 - r) and r = beta1 / sqrt(beta2) (the bias corrections held at this step's).
+struct CatchUp {
+  float skipped, d1, d2, drift;
+};
+
+__device__ __forceinline__ void adam_param(float& p, float& m, float& v, float g, float lr, const b2c_adam_step& s,
+                                           const CatchUp& cu) {
+  if (cu.skipped > 0.f) {
+    p = p - ((lr * cu.drift) * (m * s.bc1)) / (sqrtf(v * s.bc2) + s.eps);
+    m = m * cu.d1;
+    v = v * cu.d2;
+  }
+  m = s.beta1 * m + (1.f - s.beta1) * g;
+  v = s.beta2 * v + ((1.f - s.beta2) * g) * g;
+  p = p - (lr * (m * s.bc1)) / (sqrtf(v * s.bc2) + s.eps);
+}
+
+__device__ __forceinline__ void adam_param4(float4& p, float4& m, float4& v, float4 g, float4 lr, const b2c_adam_step& s,
+                                            const CatchUp& cu) {
+  adam_param(p.x, m.x, v.x, g.x, lr.x, s, cu);
+  adam_param(p.y, m.y, v.y, g.y, lr.y, s, cu);
+  adam_param(p.z, m.z, v.z, g.z, lr.z, s, cu);
+  adam_param(p.w, m.w, v.w, g.w, lr.w, s, cu);
+}
+
+// The fused optimizer (optim.cu:298-377) for splat i, given its gradient row g = [pos3, opacity logit,
+// quat4, log-scale3, SH 3K] as the VJP built it, bsq = sum_k Y_k^2 over the active basis and the colour
+// gradient (vcx, vcy, vcz) (both zero when the splat has no gradient):
+//   - Adam with bias correction on pos_op (lr_mean for the mean, lr_opac for the logit), quat (lr_rot) and
+//     the log scales (lr_scale; the frozen floor lscale.w and its moments stay as they are / zero);
+//   - the SH: a first moment per lane, one second moment per splat from the lane-mean squared gradient
+//     bsq |vc|^2 / 3K, lr_dc on the DC lanes and lr_sh_rest above; fp16 bands stored with stochastic rounding;
+//   - in sparse mode the lazy catch-up of the steps the splat skipped, and last_step = t;
+//   - MCMC noise on the means of visible splats: N(0, 1) per axis times noise_weight (1 - opacity)^150,
+//     clamped to +-noise_clamp (optim.cu:361-375).
 template <int DEG, bool HALF>
+__device__ __forceinline__ void adam_update(const b2c_vjp_args& a, int i, const float* g, bool visible, float bsq,
+                                            float vcx, float vcy, float vcz) {
+  constexpr int K = (DEG + 1) * (DEG + 1);
+  const b2c_adam_step& s = a.step;
+  const b2c_adam_state& st = a.adam;
+  CatchUp cu{0.f, 1.f, 1.f, 0.f};
+  if (s.sparse) {
+    const uint32_t last = st.last_step[i];
+    cu.skipped = last == 0u ? 0.f : fmaxf(((float)s.t - (float)last) - 1.f, 0.f);
+    st.last_step[i] = (uint32_t)s.t;
+    if (cu.skipped > 0.f) {
+      cu.d1 = det_expf(cu.skipped * s.ln_beta1);
+      cu.d2 = det_expf(cu.skipped * s.ln_beta2);
+      cu.drift = (s.ratio * (1.f - det_expf(cu.skipped * s.ln_ratio))) / (1.f - s.ratio);
+    }
+  }
+  float4* const P4 = reinterpret_cast<float4*>(a.pos_op);
+  float4* const Q4 = reinterpret_cast<float4*>(a.quat);
+  float4* const L4 = reinterpret_cast<float4*>(a.lscale);
+  float4 po = P4[i], q = Q4[i], ls = L4[i];
+  {
+    float4 m = reinterpret_cast<float4*>(st.m_pos_op)[i], v = reinterpret_cast<float4*>(st.v_pos_op)[i];
+    adam_param4(po, m, v, make_float4(g[0], g[1], g[2], g[3]), make_float4(s.lr_mean, s.lr_mean, s.lr_mean, s.lr_opac),
+                s, cu);
+    reinterpret_cast<float4*>(st.m_pos_op)[i] = m;
+    reinterpret_cast<float4*>(st.v_pos_op)[i] = v;
+  }
+  {
+    float4 m = reinterpret_cast<float4*>(st.m_quat)[i], v = reinterpret_cast<float4*>(st.v_quat)[i];
+    adam_param4(q, m, v, make_float4(g[4], g[5], g[6], g[7]), make_float4(s.lr_rot, s.lr_rot, s.lr_rot, s.lr_rot), s, cu);
+    reinterpret_cast<float4*>(st.m_quat)[i] = m;
+    reinterpret_cast<float4*>(st.v_quat)[i] = v;
+    Q4[i] = q;
+  }
+  {
+    float4 m = reinterpret_cast<float4*>(st.m_lscale)[i], v = reinterpret_cast<float4*>(st.v_lscale)[i];
+    adam_param(ls.x, m.x, v.x, g[8], s.lr_scale, s, cu);
+    adam_param(ls.y, m.y, v.y, g[9], s.lr_scale, s, cu);
+    adam_param(ls.z, m.z, v.z, g[10], s.lr_scale, s, cu);
+    m.w = 0.f;
+    v.w = 0.f;
+    reinterpret_cast<float4*>(st.m_lscale)[i] = m;
+    reinterpret_cast<float4*>(st.v_lscale)[i] = v;
+    L4[i] = ls;
+  }
+  {
+    const float gsq = (bsq * ((vcx * vcx + vcy * vcy) + vcz * vcz)) * (1.f / (float)(3 * K));
+    float vsh = st.v_sh[i] * cu.d2;
+    const float denom_old = cu.skipped > 0.f ? (cu.drift * s.bc1) / (sqrtf(vsh * s.bc2) + s.eps) : 0.f;
+    vsh = s.beta2 * vsh + (1.f - s.beta2) * gsq;
+    st.v_sh[i] = vsh;
+    const float denom = s.bc1 / (sqrtf(vsh * s.bc2) + s.eps);
+    const uint32_t sr_seed = (s.seed ^ (s.step * 0x9E3779B9u)) ^ 0x5A5A5A5Au;
+    const b2c_sh_planes& pw = a.sh_out;
+    const b2c_sh_planes& mw = st.m_sh;
+#pragma unroll
+    for (int lane = 0; lane < 3 * K; lane++) {
+      const float lrk = lane < 3 ? s.lr_dc : s.lr_sh_rest;
+      const size_t o = (size_t)(lane < 3 ? lane : lane - 3) * pw.stride + i;
+      float p, m;
+      if (lane < 3) {
+        p = pw.dc[o];
+        m = mw.dc[o];
+      } else if constexpr (HALF) {
+        p = f16_value(pw.hi16[o]);
+        m = f16_value(mw.hi16[o]);
+      } else {
+        p = pw.hi32[o];
+        m = mw.hi32[o];
+      }
+      if (cu.skipped > 0.f) {
+        p = p - (lrk * denom_old) * m;
+        m = m * cu.d1;
+      }
+      m = s.beta1 * m + (1.f - s.beta1) * g[11 + lane];
+      p = p - (lrk * denom) * m;
+      if (lane < 3) {
+        mw.dc[o] = m;
+        pw.dc[o] = p;
+      } else if constexpr (HALF) {
+        mw.hi16[o] = f16_bits(m);
+        pw.hi16[o] = f16_stochastic(p, hash_unit(sr_seed, (uint32_t)i, (uint32_t)lane));
+      } else {
+        mw.hi32[o] = m;
+        pw.hi32[o] = p;
+      }
+    }
+  }
+  if (s.noise_weight > 0.f && visible) {
+    const float sig = 1.f / (1.f + det_expf(-po.w));
+    float comp = 1.f;
+    if (ls.w > 0.f) {  // the floor's opacity factor, as the projection forms it
+      const float f2 = ls.w * ls.w;
+      const float vx = det_expf(2.f * ls.x), vy = det_expf(2.f * ls.y), vz = det_expf(2.f * ls.z);
+      comp = sqrtf(((vx / (vx + f2)) * (vy / (vy + f2))) * (vz / (vz + f2)));
+    }
+    const float o = fminf(fmaxf(sig * comp, 0.f), 1.f);
+    const float w = fminf(fmaxf(det_expf(150.f * det_logf(1.f - o)), 0.f), 1.f) * s.noise_weight;
+    if (w > 0.f) {
+      const uint32_t ns = s.seed ^ (s.step * 0x9E3779B9u);
+      const float cl = s.noise_clamp;
+      po.x = po.x + fminf(fmaxf(hash_gauss(ns, (uint32_t)i, 0u) * w, -cl), cl);
+      po.y = po.y + fminf(fmaxf(hash_gauss(ns, (uint32_t)i, 1u) * w, -cl), cl);
+      po.z = po.z + fminf(fmaxf(hash_gauss(ns, (uint32_t)i, 2u) * w, -cl), cl);
+    }
+  }
+  P4[i] = po;
+}
+
+template <int DEG, bool HALF, bool ADAM>
 __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   constexpr int K = (DEG + 1) * (DEG + 1);
   constexpr int PER = 11 + 3 * K;
@@ -112,6 +265,7 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   // register array stays live across the projection VJP
   float* out = s_buf + threadIdx.x * PER;
   bool done = false;
+  float bsq_done = 0.f;
   if (any) {
     // Memory round trip 2: the splat's parameters and all its SH coefficients, issued together
     const float4 po = reinterpret_cast<const float4*>(a.pos_op)[i];
@@ -134,6 +288,7 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
     // sum_k (coef_k . v_rgb) grad Y_k, taken on dual numbers; the SH half runs first, so the
     // coefficients are dead before the projection's registers are live.
     float gdx = 0.f, gdy = 0.f, gdz = 0.f;
+    float bsq = 0.f;  // sum of the squared basis values (the SH second moment's share, optim.cu:337-339)
     {
       float wk[K];
 #pragma unroll
@@ -144,6 +299,7 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
       for (int k = 0; k < K; k++) {
         const float y = k < kmax ? yk[k].v : 0.f;
         out[11 + 3 * k] = y * vcr; out[12 + 3 * k] = y * vcg; out[13 + 3 * k] = y * vcb;
+        if constexpr (ADAM) bsq = bsq + y * y;
         gdx = gdx + wk[k] * yk[k].x; gdy = gdy + wk[k] * yk[k].y; gdz = gdz + wk[k] * yk[k].z;
       }
     }
@@ -227,11 +383,19 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
       out[4] = gq.x; out[5] = gq.y; out[6] = gq.z; out[7] = gq.w;
       out[8] = gl[0]; out[9] = gl[1]; out[10] = gl[2];
       done = true;
+      if constexpr (ADAM) bsq_done = bsq;
     }
   }
   if (!done) {
 #pragma unroll
     for (int k = 0; k < PER; k++) out[k] = 0.f;
+  }
+  if constexpr (ADAM) {
+    // the fused update of optim.cu:298-377 on this splat's gradient row; no barrier follows, so
+    // threads without work leave here (sparse mode: splats without gradient keep all their state)
+    if (!in_range || (a.step.sparse && !any)) return;
+    adam_update<DEG, HALF>(a, i, out, visible, bsq_done, done ? g[5] : 0.f, done ? g[6] : 0.f, done ? g[7] : 0.f);
+    return;
   }
   s_any[threadIdx.x] = any ? 1u : 0u;
   __syncthreads();
@@ -257,21 +421,53 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
 
 using namespace b2c::dev;
 
+namespace {
+template <bool ADAM>
+hipError_t launch_vjp(const b2c_vjp_args& a, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.n + VJP_BLOCK - 1) / VJP_BLOCK)), block(VJP_BLOCK);
+  const bool half = a.degree > 0 && !a.sh.hi32;  // fp16 bands
+  switch (a.degree * 2 + (half ? 1 : 0)) {
+    case 0: vjp_kernel<0, false, ADAM><<<grid, block, 0, stream>>>(a); break;
+    case 2: vjp_kernel<1, false, ADAM><<<grid, block, 0, stream>>>(a); break;
+    case 3: vjp_kernel<1, true, ADAM><<<grid, block, 0, stream>>>(a); break;
+    case 4: vjp_kernel<2, false, ADAM><<<grid, block, 0, stream>>>(a); break;
+    case 5: vjp_kernel<2, true, ADAM><<<grid, block, 0, stream>>>(a); break;
+    case 6: vjp_kernel<3, false, ADAM><<<grid, block, 0, stream>>>(a); break;
+    case 7: vjp_kernel<3, true, ADAM><<<grid, block, 0, stream>>>(a); break;
+    case 8: vjp_kernel<4, false, ADAM><<<grid, block, 0, stream>>>(a); break;
+    case 9: vjp_kernel<4, true, ADAM><<<grid, block, 0, stream>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
 extern "C" int b2c_hip_vjp(const b2c_vjp_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
-  const dim3 grid((unsigned)((a->n + VJP_BLOCK - 1) / VJP_BLOCK)), block(VJP_BLOCK);
-  const bool half = a->degree > 0 && !a->sh.hi32;  // fp16 bands
-  switch (a->degree * 2 + (half ? 1 : 0)) {
-    case 0: vjp_kernel<0, false><<<grid, block, 0, stream>>>(*a); break;
-    case 2: vjp_kernel<1, false><<<grid, block, 0, stream>>>(*a); break;
-    case 3: vjp_kernel<1, true><<<grid, block, 0, stream>>>(*a); break;
-    case 4: vjp_kernel<2, false><<<grid, block, 0, stream>>>(*a); break;
-    case 5: vjp_kernel<2, true><<<grid, block, 0, stream>>>(*a); break;
-    case 6: vjp_kernel<3, false><<<grid, block, 0, stream>>>(*a); break;
-    case 7: vjp_kernel<3, true><<<grid, block, 0, stream>>>(*a); break;
-    case 8: vjp_kernel<4, false><<<grid, block, 0, stream>>>(*a); break;
-    case 9: vjp_kernel<4, true><<<grid, block, 0, stream>>>(*a); break;
-    default: return (int)hipErrorInvalidValue;
+  if (a->grad_out) return (int)launch_vjp<false>(*a, stream);
+  // the update writes the parameters, their moments and (sparse) last_step; the SH it writes are the ones it reads
+  const b2c_adam_state& st = a->adam;
+  if (!a->pos_op || !a->quat || !a->lscale || !st.m_pos_op || !st.v_pos_op || !st.m_quat || !st.v_quat ||
+      !st.m_lscale || !st.v_lscale || !st.v_sh || !st.m_sh.dc || (a->step.sparse && !st.last_step) ||
+      a->sh_out.dc != a->sh.dc || a->sh_out.stride != a->sh.stride || st.m_sh.stride != a->sh.stride)
+    return (int)hipErrorInvalidValue;
+  if (a->degree > 0) {
+    const bool half = !a->sh.hi32;
+    if (half ? (!a->sh_out.hi16 || a->sh_out.hi16 != a->sh.hi16 || !st.m_sh.hi16)
+             : (a->sh_out.hi32 != a->sh.hi32 || !st.m_sh.hi32))
+      return (int)hipErrorInvalidValue;
   }
-  return (int)hipGetLastError();
+  if (a->step.t < 1) return (int)hipErrorInvalidValue;
+  return (int)launch_vjp<true>(*a, stream);
+}
+
+extern "C" void b2c_adam_step_constants(b2c_adam_step* s) {
+  const double b1 = s->beta1, b2 = s->beta2, t = s->t;
+  s->bc1 = (float)(1.0 / (1.0 - std::pow(b1, t)));
+  s->bc2 = (float)(1.0 / (1.0 - std::pow(b2, t)));
+  s->ln_beta1 = (float)std::log(b1);
+  s->ln_beta2 = (float)std::log(b2);
+  const double r = b1 / std::sqrt(b2);
+  s->ratio = (float)r;
+  s->ln_ratio = (float)std::log(r);
 }

@@ -72,6 +72,17 @@ int b2c_model_upload(b2c_model* m, int n, int degree, int sh_fp16, const float* 
                      const float* quat, const float* opacity, const float* sh, const float* floor_);
 /* Copy a model buffer to host: "pos_op", "quat", "lscale", "vis_weight", "vis_count", "refine_norm", "max_screen". */
 int b2c_model_read(const b2c_model* m, const char* field, void* host, size_t bytes);
+/* Copy host memory into a model buffer (same names as b2c_model_read, plus the Adam state and planar arrays
+ * below). Synchronous. For callers that restore a checkpoint's optimizer state, and for tests. */
+int b2c_model_write(b2c_model* m, const char* field, const void* host, size_t bytes);
+/* Model::zero_optimizer (src/model.cu:104-107): moments, v_sh and last_step to zero, adam_t = 0. */
+int b2c_model_zero_optimizer(b2c_model* m);
+/* Model::adam_t: the last Adam step taken (0 after upload / zero_optimizer). */
+int b2c_model_adam_t(const b2c_model* m, int* t);
+/* Field names of the Adam state (src/model.h:19-28): "m_pos_op", "v_pos_op", "m_quat", "v_quat", "m_lscale",
+ * "v_lscale" (float4 [n]), "v_sh" (float [n]), "last_step" (uint32 [n]); planar arrays, whole [lanes][cap]:
+ * "sh_dc", "m_sh_dc" (fp32, 3 lanes) and "sh_hi" / "m_sh_hi" (binary16) or "sh_hi32" / "m_sh_hi32" (fp32)
+ * for the 3K - 3 band lanes, by the model's band storage. */
 /* Device address and size of a model buffer (same names), and the planar SH view the kernels take: for
  * FFI callers that launch their own kernels on the model, as the reference's refine / cage code reads
  * Model fields directly (src/model.h:14-40). */
@@ -118,11 +129,29 @@ int b2c_rasterize_backward(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, i
 /* optimizer_step with grad_out = the context's "grads" buffer [n][11 + 3K] (src/gpu/optim.h:50,
  * optim.cu:292-296); flags as above. */
 int b2c_optimizer_grad(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int active_deg, int flags);
+/* The update half of OptimParams (src/gpu/optim.h:6-20, 36); b2c_adam_defaults fills the reference's
+ * defaults. t = 0 takes the model's step counter plus one (op.t = ++model.adam_t, trainer.cpp:512). */
+typedef struct b2c_adam_opts {
+  int t;
+  int sparse; /* lazy sparse Adam: splats without gradient keep their state and catch up when next seen */
+  float beta1, beta2, eps;
+  float lr_mean, lr_rot, lr_scale, lr_opac, lr_dc, lr_sh_rest;
+  float noise_weight, noise_clamp; /* MCMC noise on the means; weight 0 disables */
+  uint32_t seed, step;
+} b2c_adam_opts;
+void b2c_adam_defaults(b2c_adam_opts* a);
+/* optimizer_step without grad_out (src/gpu/optim.h:50, optim.cu:99-377): the projection VJP and the fused
+ * Adam / lazy sparse Adam / MCMC noise update of the model. The active SH degree is o->sh_degree. */
+int b2c_optimizer_step(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, const b2c_adam_opts* a);
 /* One training step as trainer.cpp:487-529 orders it (forward, loss with grad_scale, backward in `mode`,
  * projection VJP with the gradient flags above); the step's loss replaces loss_accum[0] (loss_accum[1] = 0).
  * times may be NULL (no events recorded). */
 int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
                    int mode, int flags, b2c_step_times* times);
+/* The same step ending in the fused update (b2c_optimizer_step) instead of the gradient write: a complete
+ * training iteration (trainer.cpp:487-529). times->vjp_ms then covers the VJP with the update. */
+int b2c_train_step_adam(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro,
+                        const b2c_loss_opts* lo, int mode, const b2c_adam_opts* a, b2c_step_times* times);
 
 #ifdef __cplusplus
 }

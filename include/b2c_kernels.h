@@ -227,12 +227,45 @@ int b2c_hip_photometric_noalloc(const b2c_loss_args* a, hipStream_t stream);
 /* accumulate_kernel (loss.cu:317,324): a[2] += a[0] + a[1]; a[3] += 1. */
 int b2c_hip_accumulate_loss(float* loss_accum, hipStream_t stream);
 
-/* ---- projection VJP: optim_kernel's gradient part with op.grad_out (src/gpu/optim.cu:99-253,292-296) ----
- * Reads and clears v_splat / vis_flag. accumulate = 1 adds into grad_out instead of overwriting (for
- * gradients summed over several views). */
+/* Writable planar SH arrays (the same layout as b2c_sh_view): parameters or their first moments. */
+typedef struct b2c_sh_planes {
+  float* dc;
+  uint16_t* hi16;
+  float* hi32;
+  size_t stride;
+} b2c_sh_planes;
+
+/* Adam state of a model (src/model.h:19-28): moments beside each parameter array. */
+typedef struct b2c_adam_state {
+  float* m_pos_op, *v_pos_op, *m_quat, *v_quat, *m_lscale, *v_lscale; /* [n] float4 each */
+  b2c_sh_planes m_sh;  /* SH first moments, in the SH's own layout and band precision */
+  float* v_sh;         /* [n] one second moment per splat, the mean over its SH lanes */
+  uint32_t* last_step; /* [n] Adam step of the splat's last update (sparse mode); 0 = never */
+} b2c_adam_state;
+
+/* One Adam step's constants (OptimParams, src/gpu/optim.h:10-20). The step-dependent factors are formed
+ * on the host in double precision by b2c_adam_step_constants: bc1 = 1 / (1 - beta1^t), bc2 likewise;
+ * ln_beta1 / ln_beta2 = ln beta, ratio = beta1 / sqrt(beta2) and ln_ratio = ln ratio give the lazy
+ * catch-up's powers beta^s = e^(s ln beta) per splat. */
+typedef struct b2c_adam_step {
+  int t;
+  int sparse;
+  float beta1, beta2, eps;
+  float bc1, bc2, ln_beta1, ln_beta2, ratio, ln_ratio;
+  float lr_mean, lr_rot, lr_scale, lr_opac, lr_dc, lr_sh_rest;
+  float noise_weight, noise_clamp; /* MCMC noise on the means: weight 0 disables */
+  uint32_t seed, step;             /* noise and stochastic-rounding streams */
+} b2c_adam_step;
+void b2c_adam_step_constants(b2c_adam_step* s);
+
+/* ---- projection VJP: optim_kernel's gradient part (src/gpu/optim.cu:99-253) ----
+ * Reads and clears v_splat / vis_flag. With grad_out set, writes the parameter gradients
+ * (optim.cu:292-296); accumulate = 1 adds into grad_out instead of overwriting (for gradients summed over
+ * several views). With grad_out NULL, applies the fused Adam update of optim.cu:298-377 instead: the
+ * parameters (pos_op, quat, lscale, sh) are then written, and adam / step must be set. */
 typedef struct b2c_vjp_args {
   int n, degree, active_deg;
-  const float* pos_op, *quat, *lscale;
+  float* pos_op, *quat, *lscale;
   b2c_sh_view sh;
   b2c_camera_gpu cam;
   float* v_splat;
@@ -243,6 +276,9 @@ typedef struct b2c_vjp_args {
   int sparse;                 /* leave the rows of splats without gradient unchanged (optim.cu:148) */
   float* refine_norm;         /* [n] or NULL: max(., clamp(g[9], 0, 1e32)) (optim.cu:175-176) */
   float* vis_count;           /* [n] or NULL: += visible (optim.cu:174) */
+  b2c_sh_planes sh_out;       /* the SH as written by the update (the arrays of sh) */
+  b2c_adam_state adam;
+  b2c_adam_step step;
 } b2c_vjp_args;
 int b2c_hip_vjp(const b2c_vjp_args* a, hipStream_t stream);
 

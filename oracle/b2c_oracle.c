@@ -1072,6 +1072,11 @@ double orc_ref_loss(int n, int degree, const double* pos, const double* log_scal
  * Exports of internal pieces so the tests can pin them against closed forms.
  * ---------------------------------------------------------------------------------------------- */
 void orc_sh_basis_f(int deg, float x, float y, float z, float* out) { sh_basis_f(deg, x, y, z, out); }
+int orc_project_ok(const float* po, const float* q, const float* ls, const orc_cam_t* cam) {
+  proj_t r;
+  project_one(po, q, ls, cam, &r);
+  return r.ok;
+}
 void orc_sh_basis_d(int deg, double x, double y, double z, double* out) { sh_basis_d(deg, x, y, z, out); }
 void orc_quat_to_mat(const float* q, float* R) { quat_to_mat(q, R); }
 int orc_tile_hit(float rmin_x, float rmin_y, float rmax_x, float rmax_y, float mx, float my, float c00, float c01,

@@ -129,10 +129,52 @@ void orc_set_threads(int n);
 void orc_frag_sigma(int n, const float* dx, const float* dy, const float* c00, const float* c01, const float* c11,
                     float* out);
 void orc_sh_basis_f(int deg, float x, float y, float z, float* out);      /* splat_math.cuh:122-145 */
+/* The projection's cull decision for one splat (pr.ok of splat_math.cuh:224-293). */
+int orc_project_ok(const float* po, const float* q, const float* ls, const orc_cam_t* cam);
 void orc_sh_basis_d(int deg, double x, double y, double z, double* out);  /* reference.cpp:16-30 (+ degree 4) */
 void orc_quat_to_mat(const float* q, float* R);                           /* util.cuh:235-243 */
 int orc_tile_hit(float rmin_x, float rmin_y, float rmax_x, float rmax_y, float mx, float my, float c00, float c01,
                  float c11, float power);                                 /* splat_math.cuh:27-41 */
+
+/* ---- fused optimizer (optim.cu:104-148, 298-377), restated in oracle/orc_adam.c ---- */
+/* One Adam step's constants (b2c_adam_step of include/b2c_kernels.h, field for field). */
+typedef struct {
+  int t, sparse;
+  float beta1, beta2, eps;
+  float bc1, bc2, ln_beta1, ln_beta2, ratio, ln_ratio;
+  float lr_mean, lr_rot, lr_scale, lr_opac, lr_dc, lr_sh_rest;
+  float noise_weight, noise_clamp;
+  uint32_t seed, step;
+} orc_adam_step_t;
+
+/* bc1 = 1 / (1 - beta1^t), bc2 likewise, ln beta1, ln beta2, ratio = beta1 / sqrt(beta2), ln ratio:
+ * formed in double, rounded to float. */
+void orc_adam_constants(orc_adam_step_t* s);
+
+/* A model with its Adam state in host arrays: float4 fields [n][4]; SH and their first moments
+ * coefficient-major [n][K][3]. sh_half = 1: the band lanes (k >= 1) hold binary16 values (as floats) and
+ * are stored back as the model stores them (parameters stochastically rounded, moments to nearest). */
+typedef struct {
+  int n, degree, sh_half;
+  float* pos_op, *quat, *lscale, *sh;
+  float* m_pos_op, *v_pos_op, *m_quat, *v_quat, *m_lscale, *v_lscale;
+  float* m_sh, *v_sh;
+  uint32_t* last_step;
+} orc_adam_model_t;
+
+/* The update of every splat from its gradient row grads [n][11 + 3K] (the projection VJP's output for this
+ * v_splat), v_splat [n][13], vis_flag and tile_count as the optimizer reads them (optim.cu:104-148). */
+void orc_adam_update(orc_adam_model_t* m, const orc_cam_t* cam, int active_deg, const float* v_splat,
+                     const uint32_t* vis_flag, const uint32_t* tile_count, const float* grads,
+                     const orc_adam_step_t* s);
+
+/* Pieces of the update exported for the pinning tests. */
+float orc_hash_unit(uint32_t a, uint32_t b, uint32_t c);   /* util.cuh:106-112 */
+float orc_hash_gauss(uint32_t a, uint32_t b, uint32_t c);  /* util.cuh:114-117 */
+float orc_cos_turns(float u);                              /* cos(2 pi u), u in [0, 1) */
+uint16_t orc_f16_bits(float v);                            /* binary16, round to nearest even */
+float orc_f16_value(uint16_t h);
+uint16_t orc_f16_stochastic(float v, float u01);           /* util.cuh:148-162 */
 
 #ifdef __cplusplus
 }

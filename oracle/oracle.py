@@ -37,6 +37,20 @@ class OrcLoss(C.Structure):
                 ("scale", C.c_float), ("grad_scale", C.c_float)]
 
 
+class OrcAdamStep(C.Structure):
+    _fields_ = [("t", C.c_int), ("sparse", C.c_int), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
+                ("bc1", C.c_float), ("bc2", C.c_float), ("ln_beta1", C.c_float), ("ln_beta2", C.c_float),
+                ("ratio", C.c_float), ("ln_ratio", C.c_float), ("lr_mean", C.c_float), ("lr_rot", C.c_float),
+                ("lr_scale", C.c_float), ("lr_opac", C.c_float), ("lr_dc", C.c_float), ("lr_sh_rest", C.c_float),
+                ("noise_weight", C.c_float), ("noise_clamp", C.c_float), ("seed", C.c_uint32), ("step", C.c_uint32)]
+
+
+class OrcAdamModel(C.Structure):
+    _fields_ = [("n", C.c_int), ("degree", C.c_int), ("sh_half", C.c_int)] + [
+        (k, C.c_void_p) for k in ("pos_op", "quat", "lscale", "sh", "m_pos_op", "v_pos_op", "m_quat", "v_quat",
+                                  "m_lscale", "v_lscale", "m_sh", "v_sh", "last_step")]
+
+
 _lib = None
 _ref = None
 
@@ -93,6 +107,20 @@ def lib():
         _lib.orc_frag_sigma.argtypes = [C.c_int] + [p] * 6
         _lib.orc_set_threads.restype = None
         _lib.orc_set_threads.argtypes = [C.c_int]
+        _lib.orc_project_ok.restype = C.c_int
+        _lib.orc_project_ok.argtypes = [p, p, p, C.POINTER(OrcCam)]
+        _lib.orc_adam_constants.restype = None
+        _lib.orc_adam_constants.argtypes = [C.POINTER(OrcAdamStep)]
+        _lib.orc_adam_update.restype = None
+        _lib.orc_adam_update.argtypes = [C.POINTER(OrcAdamModel), C.POINTER(OrcCam), C.c_int, p, p, p, p,
+                                         C.POINTER(OrcAdamStep)]
+        u32 = C.c_uint32
+        _lib.orc_hash_unit.restype = f; _lib.orc_hash_unit.argtypes = [u32, u32, u32]
+        _lib.orc_hash_gauss.restype = f; _lib.orc_hash_gauss.argtypes = [u32, u32, u32]
+        _lib.orc_cos_turns.restype = f; _lib.orc_cos_turns.argtypes = [f]
+        _lib.orc_f16_bits.restype = C.c_uint16; _lib.orc_f16_bits.argtypes = [f]
+        _lib.orc_f16_value.restype = f; _lib.orc_f16_value.argtypes = [C.c_uint16]
+        _lib.orc_f16_stochastic.restype = C.c_uint16; _lib.orc_f16_stochastic.argtypes = [f, f]
     return _lib
 
 
@@ -351,3 +379,67 @@ def quat_to_mat(q):
 def tile_hit(rect, mean, conic, power) -> bool:
     return bool(lib().orc_tile_hit(*[float(x) for x in rect], float(mean[0]), float(mean[1]), *[float(c) for c in conic],
                                    float(power)))
+
+
+# ---- fused optimizer (orc_adam.c: optim.cu:104-148, 298-377) ----
+
+# OptimParams defaults (src/gpu/optim.h:10-20)
+ADAM_DEFAULTS = dict(t=1, sparse=0, beta1=0.9, beta2=0.999, eps=1e-15, lr_mean=0.0, lr_rot=2e-3, lr_scale=5e-3,
+                     lr_opac=0.012, lr_dc=2e-3, lr_sh_rest=2e-4, noise_weight=0.0, noise_clamp=0.0, seed=42, step=0)
+ADAM_STATE_KEYS = ("pos_op", "quat", "lscale", "sh", "m_pos_op", "v_pos_op", "m_quat", "v_quat", "m_lscale",
+                   "v_lscale", "m_sh", "v_sh", "last_step")
+
+
+def adam_step(**kw) -> OrcAdamStep:
+    """One step's constants: the defaults, the given fields, then the derived bias corrections and logs."""
+    s = OrcAdamStep()
+    vals = dict(ADAM_DEFAULTS)
+    vals.update(kw)
+    for k, v in vals.items():
+        setattr(s, k, v)
+    lib().orc_adam_constants(C.byref(s))
+    return s
+
+
+def adam_update(state, degree, sh_half, camd, v_splat, vis_flag, tile_count, grads, step: OrcAdamStep,
+                active_deg=None):
+    """The update of every splat (a new state dict; the input is not modified). state holds the keys of
+    ADAM_STATE_KEYS: float4 fields [n][4], sh / m_sh [n][K][3], v_sh [n], last_step [n]."""
+    out = {k: np.array(state[k], np.uint32 if k == "last_step" else np.float32, copy=True, order="C")
+           for k in ADAM_STATE_KEYS}
+    n = out["pos_op"].shape[0]
+    m = OrcAdamModel(n, degree, int(sh_half), *[_ptr(out[k]) for k in ADAM_STATE_KEYS])
+    cam = make_cam(camd)
+    keep = [_in(v_splat, np.float32), _in(vis_flag, np.uint32), _in(tile_count, np.uint32), _in(grads, np.float32)]
+    lib().orc_adam_update(C.byref(m), C.byref(cam), degree if active_deg is None else active_deg,
+                          *[_ptr(a) for a in keep], C.byref(step))
+    return out
+
+
+def project_ok(po, q, ls, camd) -> bool:
+    arrs = [_in(a, np.float32) for a in (po, q, ls)]
+    return bool(lib().orc_project_ok(*[_ptr(a) for a in arrs], C.byref(make_cam(camd))))
+
+
+def hash_unit(a, b, c) -> float:
+    return lib().orc_hash_unit(a, b, c)
+
+
+def hash_gauss(a, b, c) -> float:
+    return lib().orc_hash_gauss(a, b, c)
+
+
+def cos_turns(u) -> float:
+    return lib().orc_cos_turns(u)
+
+
+def f16_bits(v) -> int:
+    return lib().orc_f16_bits(v)
+
+
+def f16_value(h) -> float:
+    return lib().orc_f16_value(h)
+
+
+def f16_stochastic(v, u01) -> int:
+    return lib().orc_f16_stochastic(v, u01)
