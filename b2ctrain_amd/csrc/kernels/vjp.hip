@@ -88,95 +88,74 @@ __device__ __forceinline__ void adam_param4(float4& p, float4& m, float4& v, flo
 //   - in sparse mode the lazy catch-up of the steps the splat skipped, and last_step = t;
 //   - MCMC noise on the means of visible splats: N(0, 1) per axis times noise_weight (1 - opacity)^150,
 //     clamped to +-noise_clamp (optim.cu:361-375).
+// A splat's float4 parameters with their moments, v_sh and last_step: loaded by the update kernel in its first
+// memory round trip, together with the screen-space gradient, so their latency overlaps the VJP.
+struct SplatState {
+  float4 po, q, ls, mp, vp, mq, vq, ml, vl;
+  float vsh;
+  uint32_t last;
+};
+
+__device__ __forceinline__ SplatState load_state(const b2c_vjp_args& a, int i) {
+  const b2c_adam_state& st = a.adam;
+  SplatState x;
+  x.po = reinterpret_cast<const float4*>(a.pos_op)[i];
+  x.q = reinterpret_cast<const float4*>(a.quat)[i];
+  x.ls = reinterpret_cast<const float4*>(a.lscale)[i];
+  x.mp = reinterpret_cast<const float4*>(st.m_pos_op)[i];
+  x.vp = reinterpret_cast<const float4*>(st.v_pos_op)[i];
+  x.mq = reinterpret_cast<const float4*>(st.m_quat)[i];
+  x.vq = reinterpret_cast<const float4*>(st.v_quat)[i];
+  x.ml = reinterpret_cast<const float4*>(st.m_lscale)[i];
+  x.vl = reinterpret_cast<const float4*>(st.v_lscale)[i];
+  x.vsh = st.v_sh[i];
+  x.last = a.step.sparse ? st.last_step[i] : 0u;
+  return x;
+}
+
 template <int DEG, bool HALF>
 __device__ __forceinline__ void adam_update(const b2c_vjp_args& a, int i, const float* g, bool visible, float bsq,
-                                            float vcx, float vcy, float vcz) {
+                                            float vcx, float vcy, float vcz, const SplatState& x) {
   constexpr int K = (DEG + 1) * (DEG + 1);
+  constexpr int L = 3 * K;
   const b2c_adam_step& s = a.step;
   const b2c_adam_state& st = a.adam;
+  float4* const P4 = reinterpret_cast<float4*>(a.pos_op);
+  float4* const Q4 = reinterpret_cast<float4*>(a.quat);
+  float4* const L4 = reinterpret_cast<float4*>(a.lscale);
+  float4* const MP = reinterpret_cast<float4*>(st.m_pos_op);
+  float4* const VP = reinterpret_cast<float4*>(st.v_pos_op);
+  float4* const MQ = reinterpret_cast<float4*>(st.m_quat);
+  float4* const VQ = reinterpret_cast<float4*>(st.v_quat);
+  float4* const ML = reinterpret_cast<float4*>(st.m_lscale);
+  float4* const VL = reinterpret_cast<float4*>(st.v_lscale);
+  // The per-splat words were loaded before the VJP (load_state); every store here follows all loads,
+  // since a store the compiler cannot prove disjoint from a later load holds that load back.
+  float4 po = x.po, q = x.q, ls = x.ls, mp = x.mp, vp = x.vp, mq = x.mq, vq = x.vq, ml = x.ml, vl = x.vl;
+  float vsh = x.vsh;
+  const uint32_t last = x.last;
   CatchUp cu{0.f, 1.f, 1.f, 0.f};
   if (s.sparse) {
-    const uint32_t last = st.last_step[i];
     cu.skipped = last == 0u ? 0.f : fmaxf(((float)s.t - (float)last) - 1.f, 0.f);
-    st.last_step[i] = (uint32_t)s.t;
     if (cu.skipped > 0.f) {
       cu.d1 = det_expf(cu.skipped * s.ln_beta1);
       cu.d2 = det_expf(cu.skipped * s.ln_beta2);
       cu.drift = (s.ratio * (1.f - det_expf(cu.skipped * s.ln_ratio))) / (1.f - s.ratio);
     }
   }
-  float4* const P4 = reinterpret_cast<float4*>(a.pos_op);
-  float4* const Q4 = reinterpret_cast<float4*>(a.quat);
-  float4* const L4 = reinterpret_cast<float4*>(a.lscale);
-  float4 po = P4[i], q = Q4[i], ls = L4[i];
-  {
-    float4 m = reinterpret_cast<float4*>(st.m_pos_op)[i], v = reinterpret_cast<float4*>(st.v_pos_op)[i];
-    adam_param4(po, m, v, make_float4(g[0], g[1], g[2], g[3]), make_float4(s.lr_mean, s.lr_mean, s.lr_mean, s.lr_opac),
-                s, cu);
-    reinterpret_cast<float4*>(st.m_pos_op)[i] = m;
-    reinterpret_cast<float4*>(st.v_pos_op)[i] = v;
-  }
-  {
-    float4 m = reinterpret_cast<float4*>(st.m_quat)[i], v = reinterpret_cast<float4*>(st.v_quat)[i];
-    adam_param4(q, m, v, make_float4(g[4], g[5], g[6], g[7]), make_float4(s.lr_rot, s.lr_rot, s.lr_rot, s.lr_rot), s, cu);
-    reinterpret_cast<float4*>(st.m_quat)[i] = m;
-    reinterpret_cast<float4*>(st.v_quat)[i] = v;
-    Q4[i] = q;
-  }
-  {
-    float4 m = reinterpret_cast<float4*>(st.m_lscale)[i], v = reinterpret_cast<float4*>(st.v_lscale)[i];
-    adam_param(ls.x, m.x, v.x, g[8], s.lr_scale, s, cu);
-    adam_param(ls.y, m.y, v.y, g[9], s.lr_scale, s, cu);
-    adam_param(ls.z, m.z, v.z, g[10], s.lr_scale, s, cu);
-    m.w = 0.f;
-    v.w = 0.f;
-    reinterpret_cast<float4*>(st.m_lscale)[i] = m;
-    reinterpret_cast<float4*>(st.v_lscale)[i] = v;
-    L4[i] = ls;
-  }
-  {
-    const float gsq = (bsq * ((vcx * vcx + vcy * vcy) + vcz * vcz)) * (1.f / (float)(3 * K));
-    float vsh = st.v_sh[i] * cu.d2;
-    const float denom_old = cu.skipped > 0.f ? (cu.drift * s.bc1) / (sqrtf(vsh * s.bc2) + s.eps) : 0.f;
-    vsh = s.beta2 * vsh + (1.f - s.beta2) * gsq;
-    st.v_sh[i] = vsh;
-    const float denom = s.bc1 / (sqrtf(vsh * s.bc2) + s.eps);
-    const uint32_t sr_seed = (s.seed ^ (s.step * 0x9E3779B9u)) ^ 0x5A5A5A5Au;
-    const b2c_sh_planes& pw = a.sh_out;
-    const b2c_sh_planes& mw = st.m_sh;
-#pragma unroll
-    for (int lane = 0; lane < 3 * K; lane++) {
-      const float lrk = lane < 3 ? s.lr_dc : s.lr_sh_rest;
-      const size_t o = (size_t)(lane < 3 ? lane : lane - 3) * pw.stride + i;
-      float p, m;
-      if (lane < 3) {
-        p = pw.dc[o];
-        m = mw.dc[o];
-      } else if constexpr (HALF) {
-        p = f16_value(pw.hi16[o]);
-        m = f16_value(mw.hi16[o]);
-      } else {
-        p = pw.hi32[o];
-        m = mw.hi32[o];
-      }
-      if (cu.skipped > 0.f) {
-        p = p - (lrk * denom_old) * m;
-        m = m * cu.d1;
-      }
-      m = s.beta1 * m + (1.f - s.beta1) * g[11 + lane];
-      p = p - (lrk * denom) * m;
-      if (lane < 3) {
-        mw.dc[o] = m;
-        pw.dc[o] = p;
-      } else if constexpr (HALF) {
-        mw.hi16[o] = f16_bits(m);
-        pw.hi16[o] = f16_stochastic(p, hash_unit(sr_seed, (uint32_t)i, (uint32_t)lane));
-      } else {
-        mw.hi32[o] = m;
-        pw.hi32[o] = p;
-      }
-    }
-  }
+  adam_param4(po, mp, vp, make_float4(g[0], g[1], g[2], g[3]), make_float4(s.lr_mean, s.lr_mean, s.lr_mean, s.lr_opac),
+              s, cu);
+  adam_param4(q, mq, vq, make_float4(g[4], g[5], g[6], g[7]), make_float4(s.lr_rot, s.lr_rot, s.lr_rot, s.lr_rot), s, cu);
+  adam_param(ls.x, ml.x, vl.x, g[8], s.lr_scale, s, cu);
+  adam_param(ls.y, ml.y, vl.y, g[9], s.lr_scale, s, cu);
+  adam_param(ls.z, ml.z, vl.z, g[10], s.lr_scale, s, cu);
+  ml.w = 0.f;
+  vl.w = 0.f;
+  const float gsq = (bsq * ((vcx * vcx + vcy * vcy) + vcz * vcz)) * (1.f / (float)L);
+  vsh = vsh * cu.d2;
+  const float denom_old = cu.skipped > 0.f ? (cu.drift * s.bc1) / (sqrtf(vsh * s.bc2) + s.eps) : 0.f;
+  vsh = s.beta2 * vsh + (1.f - s.beta2) * gsq;
+  const float denom = s.bc1 / (sqrtf(vsh * s.bc2) + s.eps);
   if (s.noise_weight > 0.f && visible) {
     const float sig = 1.f / (1.f + det_expf(-po.w));
     float comp = 1.f;
@@ -195,7 +174,60 @@ __device__ __forceinline__ void adam_update(const b2c_vjp_args& a, int i, const 
       po.z = po.z + fminf(fmaxf(hash_gauss(ns, (uint32_t)i, 2u) * w, -cl), cl);
     }
   }
-  P4[i] = po;
+  P4[i] = po; Q4[i] = q; L4[i] = ls;
+  MP[i] = mp; VP[i] = vp; MQ[i] = mq; VQ[i] = vq; ML[i] = ml; VL[i] = vl;
+  st.v_sh[i] = vsh;
+  if (s.sparse) st.last_step[i] = (uint32_t)s.t;
+  // The SH lanes (planar, coalesced across the wave) in chunks: a chunk's parameters and moments are all
+  // loaded before any of its stores, so each chunk is one memory round trip.
+  const uint32_t sr_seed = (s.seed ^ (s.step * 0x9E3779B9u)) ^ 0x5A5A5A5Au;
+  const b2c_sh_planes& pw = a.sh_out;
+  const b2c_sh_planes& mw = st.m_sh;
+  constexpr int CH = 16;
+#pragma unroll
+  for (int c0 = 0; c0 < L; c0 += CH) {
+    float p[CH], m[CH];
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+      const int lane = c0 + j;
+      if (lane >= L) break;
+      const size_t o = (size_t)(lane < 3 ? lane : lane - 3) * pw.stride + i;
+      if (lane < 3) {
+        p[j] = pw.dc[o];
+        m[j] = mw.dc[o];
+      } else if constexpr (HALF) {
+        p[j] = f16_value(pw.hi16[o]);
+        m[j] = f16_value(mw.hi16[o]);
+      } else {
+        p[j] = pw.hi32[o];
+        m[j] = mw.hi32[o];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+      const int lane = c0 + j;
+      if (lane >= L) break;
+      const float lrk = lane < 3 ? s.lr_dc : s.lr_sh_rest;
+      const size_t o = (size_t)(lane < 3 ? lane : lane - 3) * pw.stride + i;
+      float pj = p[j], mj = m[j];
+      if (cu.skipped > 0.f) {
+        pj = pj - (lrk * denom_old) * mj;
+        mj = mj * cu.d1;
+      }
+      mj = s.beta1 * mj + (1.f - s.beta1) * g[11 + lane];
+      pj = pj - (lrk * denom) * mj;
+      if (lane < 3) {
+        mw.dc[o] = mj;
+        pw.dc[o] = pj;
+      } else if constexpr (HALF) {
+        mw.hi16[o] = f16_bits(mj);
+        pw.hi16[o] = f16_stochastic(pj, hash_unit(sr_seed, (uint32_t)i, (uint32_t)lane));
+      } else {
+        mw.hi32[o] = mj;
+        pw.hi32[o] = pj;
+      }
+    }
+  }
 }
 
 template <int DEG, bool HALF, bool ADAM>
@@ -212,11 +244,13 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   // contiguous, 16-byte aligned stretch of VJP_BLOCK * 13 floats), all issued before any is waited for.
   uint32_t vis = 0u, tc = 0u;
   float vcount = 0.f, rnorm = 0.f;
+  SplatState pre{};  // the update's per-splat words
   if (in_range) {
     vis = a.vis_flag[i];
     tc = a.tile_count[i];
     if (a.vis_count) vcount = a.vis_count[i];
     if (a.refine_norm) rnorm = a.refine_norm[i];
+    if constexpr (ADAM) pre = load_state(a, i);
   }
   const int nin = rows * GRAD_LANES;
   const float* vin = a.v_splat + (size_t)i0 * GRAD_LANES;
@@ -267,10 +301,11 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   bool done = false;
   float bsq_done = 0.f;
   if (any) {
-    // Memory round trip 2: the splat's parameters and all its SH coefficients, issued together
-    const float4 po = reinterpret_cast<const float4*>(a.pos_op)[i];
-    const float4 q = reinterpret_cast<const float4*>(a.quat)[i];
-    const float4 ls = reinterpret_cast<const float4*>(a.lscale)[i];
+    // Memory round trip 2: the splat's parameters (already loaded for the update) and all its SH
+    // coefficients, issued together
+    const float4 po = ADAM ? pre.po : reinterpret_cast<const float4*>(a.pos_op)[i];
+    const float4 q = ADAM ? pre.q : reinterpret_cast<const float4*>(a.quat)[i];
+    const float4 ls = ADAM ? pre.ls : reinterpret_cast<const float4*>(a.lscale)[i];
     const ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
     float coef[3 * K];
     if constexpr (HALF)
@@ -394,7 +429,7 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
     // the fused update of optim.cu:298-377 on this splat's gradient row; no barrier follows, so
     // threads without work leave here (sparse mode: splats without gradient keep all their state)
     if (!in_range || (a.step.sparse && !any)) return;
-    adam_update<DEG, HALF>(a, i, out, visible, bsq_done, done ? g[5] : 0.f, done ? g[6] : 0.f, done ? g[7] : 0.f);
+    adam_update<DEG, HALF>(a, i, out, visible, bsq_done, done ? g[5] : 0.f, done ? g[6] : 0.f, done ? g[7] : 0.f, pre);
     return;
   }
   s_any[threadIdx.x] = any ? 1u : 0u;

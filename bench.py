@@ -10,6 +10,10 @@ tiles of 64 x the tile's shrunk list length (the fragments both raster passes sw
 Stage times come from hipEvents recorded on the context's stream around each stage; ms_per_step is the wall
 time of the K timed steps over K, bracketed by stream synchronisation.
 
+training_iteration reports a complete training iteration besides: the same step ending in the fused Adam /
+lazy sparse Adam / MCMC update instead of the gradient export (dense and sparse), with the update kernel's
+HBM roofline.
+
 Two CPU baselines are timed on this host (not the optimisation target):
 * cpu_baseline: the fp32 tiled CPU restatement (oracle/b2c_oracle.c) of the forward and backward raster over
   the GPU's own tile lists, OpenMP over tiles on the host threads this process may use;
@@ -62,6 +66,16 @@ def binning_bytes(n, m, tile_bits):
     passes): 4 depth-sort passes of 16 B per splat, ceil(tile_bits / 8) tile-sort passes of 16 B per
     intersection, the count scan (8 B per splat) and the emit (20 B per splat + 8 B per intersection)."""
     return 4 * 16 * n + ((int(tile_bits) + 7) // 8) * 16 * m + 8 * n + 20 * n + 8 * m
+
+
+def update_bytes(n, sh_bytes):
+    """The fused optimizer's algorithmic bytes over n splats, dense mode: per splat the 13 v_splat lanes,
+    vis_flag, tile_count, vis_count and refine_norm are read (68 B); the parameters (48 B), their moments
+    (96 B), the SH and their first moments (2 S) and v_sh (4 B) are read and written; v_splat, vis_flag,
+    vis_count and refine_norm are written back (64 B). Reads of the SH by the VJP itself are not counted
+    again."""
+    rw = 48 + 96 + 2 * sh_bytes + 4
+    return n * (68 + 2 * rw + 64)
 
 
 def read_traffic(kernel, config):
@@ -326,6 +340,32 @@ def main():
         out["config"]["F_contrib_view0"] = f_contrib
     else:
         out["cpu_baseline"] = None
+    # A complete training iteration: the same step ending in the fused Adam / MCMC update instead of the
+    # gradient export (b2c_train_step_adam, one update per view as the reference's trainer takes them),
+    # with the reference trainer's defaults (lr_mean 2e-5, noise weight lr_mean * 50). Dense, then sparse.
+    sh_mom = 4 * 3 + (2 if scene.sh_fp16 else 4) * 3 * (scene.K - 1)
+    upd = {}
+    for sparse in (False, True):
+        opts = _native.adam_opts(t=0, sparse=int(sparse), lr_mean=2e-5, noise_weight=1e-3, noise_clamp=0.01,
+                                 seed=7)
+        times = []
+        log(f"bench: training iterations with the fused update ({'sparse' if sparse else 'dense'})")
+        for k in range(args.warmup + min(args.steps, 30)):
+            opts.step = k
+            for cam in views:
+                t = r.step_adam(opts, mode=args.mode, bg=bgs[k % len(bgs)], cam=cam, timed=True)
+                if k >= args.warmup:
+                    times.append(t)
+        um = {key: float(np.mean([t[key] for t in times])) for key in times[0]}
+        upd["sparse" if sparse else "dense"] = {"iteration_ms": round(um["total_ms"] * nv, 4),
+                                                "vjp_update_ms": round(um["vjp_ms"], 4)}
+    ub = update_bytes(scene.n, sh_mom)
+    t_upd = upd["dense"]["vjp_update_ms"] * 1e-3
+    upd["dense"]["roofline"] = {"kernel": "vjp_kernel (update mode)", "bound": "hbm",
+                                "algorithmic_bytes": ub, "achieved": round(ub / t_upd / 1e9, 1),
+                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(ub / t_upd / 1e9 / HBM_PEAK_GBS, 4)}
+    out["training_iteration"] = upd
     r.close()
     print(json.dumps(out), flush=True)
 
