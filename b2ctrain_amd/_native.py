@@ -32,13 +32,14 @@ class CameraGPU(C.Structure):
 
 class RenderOpts(C.Structure):
     _fields_ = [("cam", Camera), ("W", C.c_int), ("H", C.c_int), ("bg", C.c_float * 3), ("sh_degree", C.c_int),
-                ("bwd_info", C.c_int)]
+                ("bwd_info", C.c_int), ("feat_mode", C.c_int), ("feat_buffer", C.c_void_p), ("hollow_z", C.c_void_p),
+                ("hollow_margin", C.c_float), ("hollow_lam", C.c_float)]
 
 
 class LossOpts(C.Structure):
     _fields_ = [("l1_w", C.c_float), ("ssim_w", C.c_float), ("bg", C.c_float * 3), ("composite", C.c_int),
                 ("mask", C.c_int), ("alpha_lane", C.c_int), ("match_alpha_weight", C.c_float), ("scale", C.c_float),
-                ("grad_scale", C.c_float)]
+                ("grad_scale", C.c_float), ("normal_scale", C.c_float)]
 
 
 class AdamOpts(C.Structure):
@@ -85,14 +86,16 @@ EXPORTS = [
     "b2c_view_destroy", "b2c_render_forward", "b2c_project_splats", "b2c_bin_and_sort", "b2c_rasterize_forward",
     "b2c_photometric_loss", "b2c_accumulate_loss", "b2c_rasterize_backward", "b2c_optimizer_grad", "b2c_train_step",
     "b2c_model_write", "b2c_model_zero_optimizer", "b2c_model_adam_t", "b2c_adam_defaults", "b2c_optimizer_step",
-    "b2c_train_step_adam", "b2c_adam_step_constants",
+    "b2c_train_step_adam", "b2c_adam_step_constants", "b2c_view_set_normals", "b2c_device_upload",
+    "b2c_device_free", "b2c_normal_loss", "b2c_hollow_loss", "b2c_eval_metrics",
     # launcher layer
     "b2c_hip_project", "b2c_radix_sort_temp_bytes", "b2c_hip_radix_sort_pairs", "b2c_hip_radix_sort_kv2",
     "b2c_hip_depth_keys",
     "b2c_scan_temp_bytes", "b2c_hip_scan_counts", "b2c_hip_emit", "b2c_hip_tile_ranges", "b2c_hip_raster_fwd",
     "b2c_hip_raster_bwd", "b2c_hip_photometric", "b2c_loss_partials", "b2c_hip_accumulate_loss", "b2c_hip_vjp",
     "b2c_hip_fill_u32", "b2c_hip_model_scatter", "b2c_hip_model_gather", "b2c_hip_planar_regrow",
-    "b2c_hip_model_set_floor", "b2c_hip_photometric_noalloc",
+    "b2c_hip_model_set_floor", "b2c_hip_photometric_noalloc", "b2c_aux_partials", "b2c_hip_normal_loss",
+    "b2c_hip_hollow_loss", "b2c_hip_eval_metrics", "b2c_hip_step_loss_sums",
 ]
 
 _lib = None
@@ -144,6 +147,14 @@ def lib():
         L.b2c_optimizer_step.argtypes = [p, p, C.POINTER(RenderOpts), C.POINTER(AdamOpts)]
         L.b2c_train_step_adam.argtypes = [p, p, p, C.POINTER(RenderOpts), C.POINTER(LossOpts), i, C.POINTER(AdamOpts),
                                           C.POINTER(StepTimes)]
+        L.b2c_view_set_normals.argtypes = [p, p]
+        L.b2c_device_upload.restype = p
+        L.b2c_device_upload.argtypes = [p, C.c_size_t]
+        L.b2c_device_free.argtypes = [p]
+        L.b2c_device_free.restype = None
+        L.b2c_normal_loss.argtypes = [p, p, C.POINTER(LossOpts)]
+        L.b2c_hollow_loss.argtypes = [p, f]
+        L.b2c_eval_metrics.argtypes = [p, p, i]
         L.b2c_radix_sort_temp_bytes.restype = C.c_size_t
         L.b2c_radix_sort_temp_bytes.argtypes = [C.c_uint32]
         L.b2c_scan_temp_bytes.restype = C.c_size_t
@@ -197,7 +208,30 @@ _FIELD_SPEC = {
     "vals_sorted": (np.uint32, (), "M"), "tile_ranges": (np.uint32, (2,), "T"), "out_rgba": (np.float32, (4,), "P"),
     "out_feat": (np.float32, (4,), "P"), "last_idx": (np.uint32, (), "P"), "v_out": (np.float32, (4,), "P"),
     "v_splat": (np.float32, (GRAD_LANES,), "n"), "vis_flag": (np.uint32, (), "n"), "loss_accum": (np.float32, (16,), "1"),
+    "v_feat": (np.float32, (4,), "P"), "hollow_pen": (np.float32, (), "P"),
 }
+
+
+class DeviceArray:
+    """A device copy of a host array (b2c_device_upload), freed with the object."""
+
+    def __init__(self, arr):
+        self.L = lib()
+        a = np.ascontiguousarray(arr)
+        self.ptr = self.L.b2c_device_upload(_ptr(a), a.nbytes)
+        if not self.ptr:
+            raise RuntimeError(self.L.b2c_last_error().decode())
+
+    def free(self):
+        if self.ptr:
+            self.L.b2c_device_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 _FLOAT4_FIELDS = ("pos_op", "quat", "lscale", "m_pos_op", "v_pos_op", "m_quat", "v_quat", "m_lscale", "v_lscale")
@@ -216,9 +250,17 @@ class Renderer:
         if not self.ctx:
             raise RuntimeError(self.L.b2c_last_error().decode())
         self.view = None
+        self.feat_mode = 0        # render options every stage call uses unless given: FeatureMode
+        self.feat_buffer = None   # DeviceArray [n][3] for feat_mode 2
+        self.hollow = None        # DeviceArray [P] of reference depths, or None
+        self.hollow_margin, self.hollow_lam = 0.05, 0.0
+        self.normal_scale = 0.0
         self.upload(scene)
         check(self.L.b2c_ctx_setup(self.ctx, self.W, self.H, scene.n), "ctx_setup")
-        self.set_target(scene.gt, scene.weights)
+        self.set_target(scene.gt, scene.weights, scene.normals)
+        if scene.feat_mode or scene.hollow_z is not None:
+            self.set_features(scene.feat_mode, scene.feat_buffer, scene.hollow_z, scene.hollow_margin,
+                              scene.hollow_lam, scene.normal_scale)
 
     def upload(self, scene, floor=None):
         n = scene.n
@@ -232,7 +274,7 @@ class Renderer:
         self.n = n
         self.degree = scene.degree
 
-    def set_target(self, gt, weights=None):
+    def set_target(self, gt, weights=None, normals=None):
         if self.view:
             self.L.b2c_view_destroy(self.view)
         g = np.ascontiguousarray(gt, np.uint32)
@@ -240,8 +282,21 @@ class Renderer:
         self.view = self.L.b2c_view_create(self.W, self.H, _ptr(g), _ptr(w))
         if not self.view:
             raise RuntimeError(self.L.b2c_last_error().decode())
+        if normals is not None:
+            nm = np.ascontiguousarray(normals, np.uint32)
+            check(self.L.b2c_view_set_normals(self.view, _ptr(nm)), "view_set_normals")
+
+    def set_features(self, mode=0, buffer=None, hollow_z=None, hollow_margin=0.05, hollow_lam=0.0, normal_scale=0.0):
+        """Feature lanes (0 none, 1 normals, 2 buffer [n][3]), the hollow loss's reference depths [P] and
+        weights, and the normal loss weight, for every following call."""
+        self.feat_mode = int(mode)
+        self.feat_buffer = None if buffer is None else DeviceArray(np.asarray(buffer, np.float32))
+        self.hollow = None if hollow_z is None else DeviceArray(np.asarray(hollow_z, np.float32))
+        self.hollow_margin, self.hollow_lam = float(hollow_margin), float(hollow_lam)
+        self.normal_scale = float(normal_scale)
 
     def close(self):
+        self.feat_buffer = self.hollow = None
         if self.view:
             self.L.b2c_view_destroy(self.view)
         if self.ctx:
@@ -266,6 +321,10 @@ class Renderer:
             o.bg[k] = float(b[k])
         o.sh_degree = self.degree if sh_degree is None else sh_degree
         o.bwd_info = int(bwd_info)
+        o.feat_mode = self.feat_mode
+        o.feat_buffer = self.feat_buffer.ptr if self.feat_buffer is not None else None
+        o.hollow_z = self.hollow.ptr if self.hollow is not None else None
+        o.hollow_margin, o.hollow_lam = self.hollow_margin, self.hollow_lam
         return o
 
     def loss_opts(self, grad_scale=1.0, bg=None) -> LossOpts:
@@ -277,6 +336,7 @@ class Renderer:
             lo.bg[k] = float(b[k])
         lo.composite, lo.mask, lo.alpha_lane = int(s.composite), int(s.mask), int(s.alpha_lane)
         lo.match_alpha_weight, lo.scale, lo.grad_scale = s.match_alpha_weight, s.scale, grad_scale
+        lo.normal_scale = self.normal_scale
         return lo
 
     # -- stages
@@ -297,6 +357,15 @@ class Renderer:
             self.zero("loss_accum")
         check(self.L.b2c_photometric_loss(self.ctx, self.view, C.byref(self.loss_opts(grad_scale, bg))), "photometric_loss")
         return float(self.read("loss_accum")[0])
+
+    def normal_loss(self, grad_scale=1.0):
+        check(self.L.b2c_normal_loss(self.ctx, self.view, C.byref(self.loss_opts(grad_scale))), "normal_loss")
+
+    def hollow_loss(self, lam=None):
+        check(self.L.b2c_hollow_loss(self.ctx, self.hollow_lam if lam is None else lam), "hollow_loss")
+
+    def eval_metrics(self, mask_weighted=False):
+        check(self.L.b2c_eval_metrics(self.ctx, self.view, int(mask_weighted)), "eval_metrics")
 
     def backward(self, mode=1, grad_scale=1.0, **kw):
         check(self.L.b2c_rasterize_backward(self.ctx, self.model, C.byref(self.render_opts(**kw)), mode, grad_scale),

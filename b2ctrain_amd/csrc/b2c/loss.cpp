@@ -1,4 +1,4 @@
-// Loss entry points (replaces src/gpu/loss.cu:296-380).
+// Loss entry points (replaces src/gpu/loss.cu:296-338).
 #include "loss.h"
 
 namespace b2c {
@@ -24,14 +24,35 @@ void photometric_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp,
 
 void accumulate_loss(RenderCtx& ctx, hipStream_t stream) { LAUNCH_CHECK(b2c_hip_accumulate_loss(ctx.loss_accum.ptr, stream)); }
 
-void normal_loss(RenderCtx&, const ViewGPU&, const LossParams&, hipStream_t) {
-  throw std::runtime_error("normal_loss: feature lanes are not supported by this build");
+void normal_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp, hipStream_t stream) {
+  if (!view.normals) throw std::runtime_error("normal_loss: the view has no normal map");
+  b2c_normal_loss_args a{};
+  a.feat = reinterpret_cast<const float*>(ctx.out_feat.ptr);
+  a.normals = view.normals;
+  a.weights = view.weights;
+  a.W = ctx.W; a.H = ctx.H;
+  a.scale = lp.normal_scale;
+  a.grad_scale = lp.grad_scale;
+  a.v_feat = reinterpret_cast<float*>(ctx.v_feat.ptr);
+  a.loss_accum = ctx.loss_accum.ptr;
+  a.partials = ctx.aux_partials.ptr;
+  LAUNCH_CHECK(b2c_hip_normal_loss(&a, stream));
 }
-void hollow_loss(RenderCtx&, float, hipStream_t) {
-  throw std::runtime_error("hollow_loss: not supported by this build");
+
+void hollow_loss(RenderCtx& ctx, float lam, hipStream_t stream) {
+  LAUNCH_CHECK(b2c_hip_hollow_loss(ctx.hollow_pen.ptr, ctx.W, ctx.H, lam, ctx.loss_accum.ptr, ctx.aux_partials.ptr,
+                                   stream));
 }
-void eval_metrics(RenderCtx&, const ViewGPU&, bool, hipStream_t) {
-  throw std::runtime_error("eval_metrics: not supported by this build");
+
+void eval_metrics(RenderCtx& ctx, const ViewGPU& view, bool mask_weighted, hipStream_t stream) {
+  b2c_eval_args a{};
+  a.pred = reinterpret_cast<const float*>(ctx.out_rgba.ptr);
+  a.gt = view.rgba;
+  a.W = ctx.W; a.H = ctx.H;
+  a.mask_weighted = mask_weighted ? 1 : 0;
+  a.loss_accum = ctx.loss_accum.ptr;
+  a.partials = ctx.aux_partials.ptr;
+  LAUNCH_CHECK(b2c_hip_eval_metrics(&a, stream));
 }
 
 }  // namespace b2c

@@ -70,8 +70,11 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   tile_ranges.reserve((size_t)n_tiles); tile_end.reserve((size_t)n_tiles + 1);
   const size_t npx = (size_t)W * H;
   out_rgba.reserve(npx); out_feat.reserve(npx); last_idx.reserve(npx); v_out.reserve(npx);
+  hollow_pen.reserve(npx);
+  if (v_feat.count < npx) { v_feat.reserve(npx); v_feat.zero(stream); }  // read by a FEAT backward
   loss_accum.reserve(16);
   loss_partials.reserve(b2c_loss_partials(W, H));
+  aux_partials.reserve(b2c_aux_partials(W, H));
   h_count.reserve(4);
   if (isect_cap == 0) ensure_isect_capacity((size_t)1 << 22, stream);
   const size_t need_tmp = std::max({b2c_radix_sort_temp_bytes((uint32_t)nn), b2c_radix_sort_temp_bytes((uint32_t)isect_cap),
@@ -87,8 +90,9 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
   keys_sorted.reserve(ncap, false, stream); vals_sorted.reserve(ncap, false, stream);
   isect_alt_k.reserve(ncap, false, stream); isect_alt_v.reserve(ncap, false, stream);
   isect_alt_v2.reserve(ncap, false, stream);
-  slot_sorted.reserve(ncap, false, stream); isect_rows.reserve(ncap * 3, false, stream);
-  isect_part.reserve((ncap / 256 + 1) * 6, false, stream); isect_part_flags.reserve(ncap / 256 + 1, false, stream);
+  // rows: 3 float4 (4 with feature lanes); window partials: 2 x 3 float4 (2 x 4)
+  slot_sorted.reserve(ncap, false, stream); isect_rows.reserve(ncap * 4, false, stream);
+  isect_part.reserve((ncap / 256 + 1) * 8, false, stream); isect_part_flags.reserve(ncap / 256 + 1, false, stream);
   isect_cap = ncap;
   sort_tmp.reserve(b2c_radix_sort_temp_bytes((uint32_t)ncap));
 }
@@ -96,11 +100,14 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
 namespace {
 
 void check_supported(const RenderParams& p) {
-  if (p.feat != FeatureMode::None) throw std::runtime_error("render: feature lanes (normals/buffer) are not supported by this build");
+  if (p.feat == FeatureMode::Buffer && !p.feat_buffer) throw std::runtime_error("render: FeatureMode::Buffer needs feat_buffer");
   if (p.mip) throw std::runtime_error("render: mip filtering is not supported (the reference trainer rejects it too)");
   if (p.warp || p.pos_override || p.quat_override || p.lscale_override || p.sh_frame || p.app || p.col_base)
     throw std::runtime_error("render: warp / deformation overrides / appearance are not supported by this build");
-  if (p.hollow_z) throw std::runtime_error("render: the hollow loss is not supported by this build");
+}
+
+int feat_mode(const RenderParams& p) {
+  return p.feat == FeatureMode::Normals ? 1 : (p.feat == FeatureMode::Buffer ? 2 : 0);
 }
 
 }  // namespace
@@ -129,6 +136,8 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   a.big_chunk = ctx.big_chunk.ptr;
   a.big_items = ctx.big_items.ptr;
   a.big_items_count = ctx.counters.ptr + 2;
+  a.feat_mode = feat_mode(p);
+  a.feat_buffer = p.feat_buffer;
   LAUNCH_CHECK(b2c_hip_project(&a, stream));
 }
 
@@ -216,6 +225,10 @@ void rasterize_forward(RenderCtx& ctx, const RenderParams& p, hipStream_t stream
   a.out_rgba = reinterpret_cast<float*>(ctx.out_rgba.ptr);
   a.out_feat = reinterpret_cast<float*>(ctx.out_feat.ptr);
   a.last_idx = ctx.last_idx;
+  a.feat = p.feat != FeatureMode::None ? 1 : 0;
+  a.hollow_z = p.hollow_z;
+  a.hollow_margin = p.hollow_margin;
+  a.hollow_pen = ctx.hollow_pen.ptr;
   LAUNCH_CHECK(b2c_hip_raster_fwd(&a, stream));
 }
 
@@ -227,7 +240,9 @@ void render_forward(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
 
 namespace {
 
-void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, float inv_gscale, hipStream_t stream) {
+// grad_scale: the factor v_out carries (1 for mode 0); the hollow term is scaled to match
+// (raster_bwd_tc.cu:208).
+void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, float grad_scale, hipStream_t stream) {
   check_supported(p);
   b2c_raster_bwd_args a{};
   a.tile_ranges = reinterpret_cast<const uint32_t*>(ctx.tile_ranges.ptr);
@@ -242,7 +257,7 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.v_out = reinterpret_cast<const float*>(ctx.v_out.ptr);
   a.W = ctx.W; a.H = ctx.H; a.tiles_x = ctx.tiles_x; a.tiles_y = ctx.tiles_y;
   for (int k = 0; k < 3; k++) a.bg[k] = p.bg[k];
-  a.inv_gscale = inv_gscale;
+  a.inv_gscale = 1.f / grad_scale;
   a.mode = mode;
   a.v_splat = ctx.v_splat;
   a.vis_flag = ctx.vis_flag;
@@ -256,6 +271,12 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.isect_part = reinterpret_cast<float*>(ctx.isect_part.ptr);
   a.isect_part_flags = ctx.isect_part_flags;
   a.split_event = ctx.bwd_split_event;
+  a.feat = p.feat != FeatureMode::None ? 1 : 0;
+  a.v_feat = reinterpret_cast<const float*>(ctx.v_feat.ptr);
+  a.proj3 = reinterpret_cast<const float*>(ctx.proj3.ptr);
+  a.hollow_z = p.hollow_z;
+  a.hollow_margin = p.hollow_margin;
+  a.hollow_lam = p.hollow_lam * grad_scale;
   LAUNCH_CHECK(b2c_hip_raster_bwd(&a, stream));
 }
 
@@ -266,7 +287,7 @@ void rasterize_backward(RenderCtx& ctx, const Model& m, const RenderParams& p, h
 }
 
 void rasterize_backward_tc(RenderCtx& ctx, const Model& m, const RenderParams& p, float grad_scale, hipStream_t stream) {
-  backward(ctx, m, p, 1, 1.f / grad_scale, stream);
+  backward(ctx, m, p, 1, grad_scale, stream);
 }
 
 }  // namespace b2c

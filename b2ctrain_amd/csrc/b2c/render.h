@@ -1,8 +1,7 @@
 // Rendering API of the drop-in (replaces src/gpu/render.h:1-111 and src/dataset/camera.h:8-36): same
 // type names, fields and entry points, hipStream_t in place of cudaStream_t. Features outside this build's
-// scope (feature lanes, hollow loss, render-side warp, articulated/cage overrides, pose-dependent
-// appearance, mip filtering) keep their RenderParams fields so callers compile, and make the entry points
-// throw std::runtime_error when set.
+// scope (render-side warp, articulated/cage overrides, pose-dependent appearance, mip filtering) keep their
+// RenderParams fields so callers compile, and make the entry points throw std::runtime_error when set.
 #pragma once
 #include "model.h"
 
@@ -36,8 +35,8 @@ struct RenderParams {
   CameraGPU cam;
   float bg[3] = {0, 0, 0};
   int sh_degree = 3;  // active degree (<= model degree)
-  FeatureMode feat = FeatureMode::None;
-  const float* feat_buffer = nullptr;
+  FeatureMode feat = FeatureMode::None;  // Normals: camera-space pseudo-normals; Buffer: feat_buffer
+  const float* feat_buffer = nullptr;    // [n][3] device, FeatureMode::Buffer
   bool mip = false;
   bool bwd_info = true;  // write per-pixel last index / shrink tile ranges
   const float2* warp = nullptr;
@@ -49,6 +48,9 @@ struct RenderParams {
   const float4* app = nullptr;
   float4* col_base = nullptr;
   bool app_add = false;
+  // Hollow loss: per-pixel reference depth of the body surface (camera z, +inf = none) [W*H] device; a
+  // fragment at depth z is penalised by clamp((z - z_ref - margin) / margin, 0, 1) times its blend weight,
+  // summed per pixel into ctx.hollow_pen; hollow_lam = dL/d(penalised weight) per pixel (before grad_scale).
   const float* hollow_z = nullptr;
   float hollow_margin = 0.05f;
   float hollow_lam = 0.f;
@@ -96,6 +98,7 @@ struct RenderCtx {
   DevBuf<uint32_t> isect_part_flags;  // per 256-row window
   DevBuf<unsigned char> sort_tmp;
   DevBuf<float> loss_partials;  // per-workgroup loss sums, reduced in a fixed order
+  DevBuf<float> aux_partials;   // the same for normal_loss, hollow_loss and eval_metrics
   hipEvent_t bwd_split_event = nullptr;  // if set: recorded between the backward raster kernel and its reduce
   hipEvent_t count_event = nullptr;      // owned: recorded after the intersection count's copy to h_count
 

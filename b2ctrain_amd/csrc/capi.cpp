@@ -23,7 +23,7 @@ struct b2c_ctx {
 };
 
 struct b2c_view {
-  b2c::DevBuf<uint32_t> rgba;
+  b2c::DevBuf<uint32_t> rgba, normals;
   b2c::DevBuf<uint8_t> weights;
   b2c::ViewGPU view;
 };
@@ -85,6 +85,12 @@ b2c::RenderParams to_params(const b2c_render_opts& o) {
   for (int k = 0; k < 3; k++) p.bg[k] = o.bg[k];
   p.sh_degree = o.sh_degree;
   p.bwd_info = o.bwd_info != 0;
+  if (o.feat_mode < 0 || o.feat_mode > 2) throw std::runtime_error("render opts: feat_mode must be 0, 1 or 2");
+  p.feat = o.feat_mode == 1 ? b2c::FeatureMode::Normals : (o.feat_mode == 2 ? b2c::FeatureMode::Buffer : b2c::FeatureMode::None);
+  p.feat_buffer = o.feat_buffer;
+  p.hollow_z = o.hollow_z;
+  p.hollow_margin = o.hollow_margin;
+  p.hollow_lam = o.hollow_lam;
   return p;
 }
 
@@ -94,6 +100,7 @@ b2c::LossParams to_loss(const b2c_loss_opts& o) {
   for (int k = 0; k < 3; k++) lp.bg[k] = o.bg[k];
   lp.composite = o.composite != 0; lp.mask = o.mask != 0; lp.alpha_lane = o.alpha_lane != 0;
   lp.match_alpha_weight = o.match_alpha_weight; lp.scale = o.scale; lp.grad_scale = o.grad_scale;
+  lp.normal_scale = o.normal_scale;
   return lp;
 }
 
@@ -125,6 +132,8 @@ Field ctx_field(b2c_ctx* c, const std::string& name) {
       {"tile_ranges", {x.tile_ranges.ptr, (size_t)x.n_tiles * 8}},
       {"out_rgba", {x.out_rgba.ptr, P * 16}},
       {"out_feat", {x.out_feat.ptr, P * 16}},
+      {"v_feat", {x.v_feat.ptr, P * 16}},
+      {"hollow_pen", {x.hollow_pen.ptr, P * 4}},
       {"last_idx", {x.last_idx.ptr, P * 4}},
       {"v_out", {x.v_out.ptr, P * 16}},
       {"v_splat", {x.v_splat.ptr, n * b2c::GRAD_LANES * 4}},
@@ -347,6 +356,48 @@ b2c_view* b2c_view_create(int W, int H, const uint32_t* rgba, const uint8_t* wei
 
 void b2c_view_destroy(b2c_view* v) { delete v; }
 
+int b2c_view_set_normals(b2c_view* v, const uint32_t* normals) {
+  return guarded([&] {
+    const size_t P = (size_t)v->view.W * v->view.H;
+    if (normals) {
+      v->normals.upload(normals, P);
+      HIP_CHECK(hipDeviceSynchronize());
+      v->view.normals = v->normals.ptr;
+    } else {
+      v->view.normals = nullptr;
+    }
+  });
+}
+
+void* b2c_device_upload(const void* host, size_t bytes) {
+  void* d = nullptr;
+  const int rc = guarded([&] {
+    HIP_CHECK(hipMalloc(&d, bytes ? bytes : 1));
+    if (bytes) HIP_CHECK(hipMemcpy(d, host, bytes, hipMemcpyHostToDevice));
+  });
+  if (rc && d) {
+    (void)hipFree(d);
+    d = nullptr;
+  }
+  return d;
+}
+
+void b2c_device_free(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+int b2c_normal_loss(b2c_ctx* c, const b2c_view* v, const b2c_loss_opts* o) {
+  return guarded([&] { b2c::normal_loss(c->ctx, v->view, to_loss(*o), c->stream); });
+}
+
+int b2c_hollow_loss(b2c_ctx* c, float lam) {
+  return guarded([&] { b2c::hollow_loss(c->ctx, lam, c->stream); });
+}
+
+int b2c_eval_metrics(b2c_ctx* c, const b2c_view* v, int mask_weighted) {
+  return guarded([&] { b2c::eval_metrics(c->ctx, v->view, mask_weighted != 0, c->stream); });
+}
+
 int b2c_render_forward(b2c_ctx* c, const b2c_model* m, const b2c_render_opts* o) {
   return guarded([&] { b2c::render_forward(c->ctx, m->m, to_params(*o), c->stream); });
 }
@@ -463,7 +514,14 @@ int train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opt
     mark(2);
     b2c::rasterize_forward(c->ctx, p, s);
     mark(3);
+    // the trainer's loss order (trainer.cpp:502-505): photometric, normal-map, hollow, then the step sums
+    const bool normals_on = p.feat == b2c::FeatureMode::Normals && lp.normal_scale > 0.f && v->view.normals;
+    const bool hollow_on = p.hollow_z && p.hollow_lam != 0.f;
+    lp.running_sum = !(normals_on || hollow_on);
     b2c::photometric_loss(c->ctx, v->view, lp, s);
+    if (normals_on) b2c::normal_loss(c->ctx, v->view, lp, s);
+    if (hollow_on) b2c::hollow_loss(c->ctx, p.hollow_lam, s);
+    if (!lp.running_sum) LAUNCH_CHECK(b2c_hip_step_loss_sums(c->ctx.loss_accum.ptr, s));
     mark(4);
     c->ctx.bwd_split_event = (times && mode != 0) ? c->ev[7] : nullptr;
     if (mode == 0)

@@ -6,6 +6,7 @@
 // by the same arithmetic (the reference's early exit, loss.cu:51-74, is an optimisation only).
 #include "b2c_kernels.h"
 #include "device_math.h"
+#include "ssim_common.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -16,19 +17,6 @@ namespace b2c {
 namespace dev {
 namespace {
 
-constexpr int HALO = 5;
-constexpr float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f;
-
-// The 11 weights (double-precision exp(-d^2 / 4.5) normalised to sum 1, rounded to float), as compile-time
-// constants: passed as kernel arguments they took 11 scalar registers and the kernel spilled others. The
-// launcher checks them bitwise against its own computation.
-constexpr uint32_t GW_BITS[11] = {0x3a86cab6u, 0x3bf8ff01u, 0x3d13758cu, 0x3ddff87fu, 0x3e5a1e20u, 0x3e8832b0u,
-                                  0x3e5a1e20u, 0x3ddff87fu, 0x3d13758cu, 0x3bf8ff01u, 0x3a86cab6u};
-__device__ __forceinline__ float gw_tap(int d) { return __uint_as_float(GW_BITS[d]); }
-
-__device__ __forceinline__ float gt_channel(uint32_t packed, int c) {
-  return (float)((packed >> (8 * c)) & 0xffu) * (1.f / 255.f);
-}
 
 // Effective target of channel c (loss.cu:85-87), uncontracted: the L1 sign compares the prediction with
 // exactly this fp32 value, so it must round the same way everywhere.
@@ -358,6 +346,11 @@ __global__ void accumulate_kernel(float* acc) {
   acc[3] += 1.f;
 }
 
+__global__ void step_sums_kernel(float* acc) {
+  acc[2] = acc[0] + acc[1];
+  acc[3] = 1.f;
+}
+
 }  // namespace
 }  // namespace dev
 }  // namespace b2c
@@ -483,6 +476,11 @@ extern "C" int b2c_hip_photometric_noalloc(const b2c_loss_args* a, hipStream_t s
   b2c_loss_args b = *a;
   b.partials = partials;  // every entry the reduce reads is written by this call's workgroups first
   return b2c_hip_photometric(&b, stream);
+}
+
+extern "C" int b2c_hip_step_loss_sums(float* loss_accum, hipStream_t stream) {
+  step_sums_kernel<<<1, 1, 0, stream>>>(loss_accum);
+  return (int)hipGetLastError();
 }
 
 extern "C" size_t b2c_loss_partials(int W, int H) {

@@ -1,7 +1,8 @@
-// Projection (replaces src/gpu/project.cu:8-126): one thread per splat, EWA projection, SH colour, exact
-// ellipse/8x8-tile test over the splat's tile bounding box. Splats with more than 32 bbox tiles are not
-// counted inline (one thread walking hundreds of tiles stalls its whole wave): they are appended to a
-// list and counted in parallel chunks of their bbox, one wave per chunk.
+// Projection (replaces src/gpu/project.cu:8-126): one thread per splat, EWA projection, SH colour, the
+// feature lanes (pseudo-normal or a caller's buffer), exact ellipse/8x8-tile test over the splat's tile
+// bounding box. Splats with more than 32 bbox tiles are not counted inline (one thread walking hundreds of
+// tiles stalls its whole wave): they are appended to a list and counted in parallel chunks of their bbox,
+// one wave per chunk.
 #pragma clang fp contract(off)
 #include "b2c_kernels.h"
 #include "device_math.h"
@@ -81,17 +82,40 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       cr = __builtin_isfinite(cr) ? fminf(fmaxf(cr, -100.f), 100.f) : 0.f;
       cg = __builtin_isfinite(cg) ? fminf(fmaxf(cg, -100.f), 100.f) : 0.f;
       cb = __builtin_isfinite(cb) ? fminf(fmaxf(cb, -100.f), 100.f) : 0.f;
+      float f0 = 0.f, f1 = 0.f, f2 = 0.f;
+      if (a.feat_mode == 1) {
+        // the pseudo-normal (project.cu:63-71): the local axis of the smallest log scale (the first of
+        // equal ones), a column of R(q), as a unit vector turned towards the camera, in camera coordinates
+        const int ax = (ls.x <= ls.y && ls.x <= ls.z) ? 0 : (ls.y <= ls.z ? 1 : 2);
+        const float nx = pr.rot.m[ax], ny = pr.rot.m[3 + ax], nz = pr.rot.m[6 + ax];
+        const float il = 1.f / fmaxf(sqrtf((nx * nx + ny * ny) + nz * nz), 1e-12f);
+        const float sx = nx * il, sy = ny * il, sz = nz * il;
+        // pr.d runs from the camera to the splat: the axis faces the camera when it points against it
+        const float face = ((sx * -pr.d[0] + sy * -pr.d[1]) + sz * -pr.d[2]) >= 0.f ? 1.f : -1.f;
+        const float wx = sx * face, wy = sy * face, wz = sz * face;
+        const float* R = a.cam.R;
+        f0 = (R[0] * wx + R[1] * wy) + R[2] * wz;
+        f1 = (R[3] * wx + R[4] * wy) + R[5] * wz;
+        f2 = (R[6] * wx + R[7] * wy) + R[8] * wz;
+      } else if (a.feat_mode == 2) {  // a caller's per-splat feature, clamped as a colour is
+        f0 = a.feat_buffer[(size_t)i * 3];
+        f1 = a.feat_buffer[(size_t)i * 3 + 1];
+        f2 = a.feat_buffer[(size_t)i * 3 + 2];
+        f0 = __builtin_isfinite(f0) ? fminf(fmaxf(f0, -100.f), 100.f) : 0.f;
+        f1 = __builtin_isfinite(f1) ? fminf(fmaxf(f1, -100.f), 100.f) : 0.f;
+        f2 = __builtin_isfinite(f2) ? fminf(fmaxf(f2, -100.f), 100.f) : 0.f;
+      }
       reinterpret_cast<float4*>(a.proj0)[i] = make_float4(pr.px, pr.py, pr.conic.c00, pr.conic.c01);
       reinterpret_cast<float4*>(a.proj1)[i] = make_float4(pr.conic.c11, pr.opacity, pr.c[2], power);
-      reinterpret_cast<float4*>(a.proj2)[i] = make_float4(cr, cg, cb, 0.f);
-      reinterpret_cast<float2*>(a.proj3)[i] = make_float2(0.f, 0.f);
+      reinterpret_cast<float4*>(a.proj2)[i] = make_float4(cr, cg, cb, f0);
+      reinterpret_cast<float2*>(a.proj3)[i] = make_float2(f1, f2);
       if (a.raster_rec) {  // halving the conic diagonal is exact: the raster evaluates the reference's sigma
         float4* rec = reinterpret_cast<float4*>(a.raster_rec) + (size_t)i * 4;
         const uint32_t sgn = (cr >= 0.f ? 1u : 0u) | (cg >= 0.f ? 2u : 0u) | (cb >= 0.f ? 4u : 0u);
         rec[0] = make_float4(pr.px, pr.py, 0.5f * pr.conic.c00, pr.conic.c01);
         rec[1] = make_float4(0.5f * pr.conic.c11, pr.opacity, power, __uint_as_float(sgn));
         rec[2] = make_float4(fmaxf(cr, 0.f), fmaxf(cg, 0.f), fmaxf(cb, 0.f), log2_opacity(pr.opacity));
-        rec[3] = make_float4(0.f, 0.f, 0.f, 0.f);  // unused; whole lines are written (no partial-line writes)
+        rec[3] = make_float4(f0, f1, f2, pr.c[2]);  // read by the feature and hollow-loss variants only
       }
       if (a.max_screen) {
         float ms = fmaxf(pr.ex / (float)a.cam.W, pr.ey / (float)a.cam.H);
@@ -306,6 +330,7 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
   if (!a->big_count || !a->big_list) return (int)hipErrorInvalidValue;
+  if (a->feat_mode < 0 || a->feat_mode > 2 || (a->feat_mode == 2 && !a->feat_buffer)) return (int)hipErrorInvalidValue;
   clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);  // one launch for both
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);
   const bool half = a->degree > 0 && !a->sh.hi32;  // fp16 bands

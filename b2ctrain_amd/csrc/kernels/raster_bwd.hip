@@ -27,8 +27,11 @@ struct PixelState {
   float T, inv_final_a, v_o_w;
   float4 vo;
   uint32_t last;
+  float4 vf;      // dL/d(feature lanes) (FEAT)
+  HollowRef href;  // the pixel's reference surface (HOLLOW)
 };
 
+template <bool FEAT, bool HOLLOW>
 __device__ __forceinline__ PixelState load_pixel(const b2c_raster_bwd_args& a, int px, int py, uint32_t range_x) {
   PixelState s;
   s.inside = px < a.W && py < a.H;
@@ -37,17 +40,21 @@ __device__ __forceinline__ PixelState load_pixel(const b2c_raster_bwd_args& a, i
   s.T = 0.f;
   s.last = range_x;
   s.vo = make_float4(0.f, 0.f, 0.f, 0.f);
+  s.vf = make_float4(0.f, 0.f, 0.f, 0.f);
   s.v_o_w = 0.f;
-  float final_a = 0.f;
+  float final_a = 0.f, z_ref = __builtin_inff();
   if (s.inside) {
     const int pix = py * a.W + px;
     final_a = reinterpret_cast<const float4*>(a.out_rgba)[pix].w;
     s.T = reinterpret_cast<const float4*>(a.out_feat)[pix].w;
     s.last = a.last_idx[pix];
     s.vo = reinterpret_cast<const float4*>(a.v_out)[pix];
+    if constexpr (FEAT) s.vf = reinterpret_cast<const float4*>(a.v_feat)[pix];
+    if constexpr (HOLLOW) z_ref = a.hollow_z[pix];
     s.v_o_w = (s.vo.w - (a.bg[0] * s.vo.x + a.bg[1] * s.vo.y + a.bg[2] * s.vo.z)) * s.T;
   }
   s.inv_final_a = 1.f / fmaxf(final_a, 1e-5f);
+  s.href = hollow_ref(z_ref, a.hollow_margin);
   return s;
 }
 
@@ -63,7 +70,12 @@ __device__ __forceinline__ PixelState load_pixel(const b2c_raster_bwd_args& a, i
 // reference's accumulation (raster_bwd.cu:130-139). The order of those atomic adds varies between runs; the
 // mode-1 path below is the deterministic one. The per-splat inputs come from proj0..2 (the reference's
 // buffers), not from the raster record the other kernels read, so this path also checks that record.
-constexpr int ANCHOR_VALS = 11;
+//
+// Feature lanes (FEAT) are composited like the colour but without a background, so their share of
+// dL/dalpha folds into the same scalar: (colour . v_rgb) becomes (colour . v_rgb + feature . v_feat), and
+// the splat's feature gradient is the sum of vis * v_feat. The hollow penalty (HOLLOW) adds
+// lam (T_before h - S_h / (1 - alpha)) to dL/dalpha, with S_h the vis-weighted penalty of the fragments
+// behind (raster_bwd.cu:101); the refine statistic keeps the dL/dalpha without it.
 
 __device__ __forceinline__ float wave_total_to_lane0(float v) {
 #pragma unroll
@@ -71,8 +83,12 @@ __device__ __forceinline__ float wave_total_to_lane0(float v) {
   return v;
 }
 
+template <bool FEAT, bool HOLLOW>
 __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args a) {
+  // per-fragment sums: g0..g9, the blend weight, and with FEAT the three feature lanes
+  constexpr int ANCHOR_VALS = FEAT ? 14 : 11;
   __shared__ float4 s_geo[64], s_shape[64], s_rgb[64];  // proj0, proj1, proj2 of the batch's splats
+  __shared__ float2 s_f3[FEAT ? 64 : 1];                  // proj3 (feature y, z)
   __shared__ uint32_t s_id[64];
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
@@ -81,10 +97,11 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
   if (range.y <= range.x) return;
   const int lane = threadIdx.x;
   const int px = (tile % a.tiles_x) * RT_W + (lane & 7), py = (tile / a.tiles_x) * RT_W + (lane >> 3);
-  const PixelState ps = load_pixel(a, px, py, range.x);
+  const PixelState ps = load_pixel<FEAT, HOLLOW>(a, px, py, range.x);
   const float Wf = (float)a.W, Hf = (float)a.H;
   float T = ps.T;
   float Q = -ps.v_o_w;
+  float Sh = 0.f;  // sum over composited fragments behind of vis * penalty
   for (uint32_t hi = range.y; hi > range.x;) {
     const uint32_t lo = hi - range.x > 64u ? hi - 64u : range.x;
     const int count = (int)(hi - lo);
@@ -95,6 +112,7 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
       s_geo[lane] = reinterpret_cast<const float4*>(a.proj0)[id];
       s_shape[lane] = reinterpret_cast<const float4*>(a.proj1)[id];
       s_rgb[lane] = reinterpret_cast<const float4*>(a.proj2)[id];
+      if constexpr (FEAT) s_f3[lane] = reinterpret_cast<const float2*>(a.proj3)[id];
     }
     __syncthreads();
     for (int j = count - 1; j >= 0; j--) {
@@ -114,28 +132,47 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
         const float keep = 1.f - alpha;
         const float Tb = T / keep;
         const float vis = alpha * Tb;
-        const float cv = fmaxf(col.x, 0.f) * ps.vo.x + fmaxf(col.y, 0.f) * ps.vo.y + fmaxf(col.z, 0.f) * ps.vo.z;
-        const float v_alpha = Tb * cv - Q / keep;
+        float cv = fmaxf(col.x, 0.f) * ps.vo.x + fmaxf(col.y, 0.f) * ps.vo.y + fmaxf(col.z, 0.f) * ps.vo.z;
+        if constexpr (FEAT) {
+          const float2 f12 = s_f3[j];
+          cv = cv + (col.w * ps.vf.x + f12.x * ps.vf.y + f12.y * ps.vf.z);
+        }
+        const float v_alpha_photo = Tb * cv - Q / keep;
+        float v_alpha = v_alpha_photo, hh = 0.f;
+        if constexpr (HOLLOW) {
+          hh = hollow_h(shape.z, ps.href);
+          v_alpha = v_alpha + a.hollow_lam * (Tb * hh - Sh / keep);
+        }
         if (araw <= ALPHA_MAX) {  // a clamped alpha does not depend on sigma
           const float dx = fg.dx, dy = fg.dy;
           const float v_sigma = -alpha * v_alpha;
           // d sigma / d mean = -(d sigma / d d) = -(2a dx + b dy, b dx + 2c dy)
-          const float gmx = -v_sigma * __builtin_fmaf(0.5f * geo.z, dx, fg.lin);
-          const float gmy = -v_sigma * __builtin_fmaf(geo.w, dx, fg.cdy + fg.cdy);
+          const float ex = __builtin_fmaf(0.5f * geo.z, dx, fg.lin), ey = __builtin_fmaf(geo.w, dx, fg.cdy + fg.cdy);
+          const float gmx = -v_sigma * ex;
+          const float gmy = -v_sigma * ey;
           val[0] = gmx;
           val[1] = gmy;
           val[2] = 0.5f * v_sigma * dx * dx;
           val[3] = v_sigma * dx * dy;
           val[4] = 0.5f * v_sigma * dy * dy;
           val[8] = v_alpha * gauss_weight(sigma);
-          val[9] = sqrtf((gmx * Wf) * (gmx * Wf) + (gmy * Hf) * (gmy * Hf)) * ps.inv_final_a;
+          // the refine statistic: the mean gradient of the photometric (and feature) terms only
+          const float vsp = -alpha * v_alpha_photo;
+          const float px_ = -vsp * ex, py_ = -vsp * ey;
+          val[9] = sqrtf((px_ * Wf) * (px_ * Wf) + (py_ * Hf) * (py_ * Hf)) * ps.inv_final_a;
         }
         val[5] = col.x >= 0.f ? vis * ps.vo.x : 0.f;
         val[6] = col.y >= 0.f ? vis * ps.vo.y : 0.f;
         val[7] = col.z >= 0.f ? vis * ps.vo.z : 0.f;
         val[10] = vis;
+        if constexpr (FEAT) {
+          val[11] = vis * ps.vf.x;
+          val[12] = vis * ps.vf.y;
+          val[13] = vis * ps.vf.z;
+        }
         T = Tb;
         Q = Q + vis * cv;
+        if constexpr (HOLLOW) Sh = Sh + vis * hh;
       }
 #pragma unroll
       for (int k = 0; k < ANCHOR_VALS; k++) val[k] = wave_total_to_lane0(val[k]);
@@ -147,6 +184,11 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
 #pragma unroll
         for (int k = 0; k < 10; k++)
           if (val[k] != 0.f) atomicAdd(dst + k, val[k] * a.inv_gscale);
+        if constexpr (FEAT) {
+#pragma unroll
+          for (int k = 0; k < 3; k++)
+            if (val[11 + k] != 0.f) atomicAdd(dst + 10 + k, val[11 + k] * a.inv_gscale);
+        }
       }
     }
     hi = lo;
@@ -164,9 +206,12 @@ constexpr int G = 8;       // splats per MFMA group
 constexpr int SROW = 68;   // pixel stride of the per-fragment scalar rows (64 + 4: spreads the B reads over banks)
 // (tile, splat) row: raw moments of the tile's fragments about the tile centre, 12 floats in three 16-byte
 // quarters, each written by one lane with one store: sum v_sigma * [v, u^2, uv, v^2] | sum v_sigma * [1, u],
-// sum vis, refine sum | sum vis * v_rgb, the tile id (bits)
-constexpr int ROW = 12;
-// basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero), 6 one, 7 u, 8 v, 9 u^2, 10 uv, 11 v^2, 12-15 zero
+// sum vis, refine sum | sum vis * v_rgb, the tile id (bits); with feature lanes a fourth quarter
+// sum vis * v_feat, 0. Rows are ROW_FLOATS<FEAT> floats apart.
+template <bool FEAT>
+constexpr int ROW_FLOATS = FEAT ? 16 : 12;
+// basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero without FEAT), 6 one, 7 u, 8 v, 9 u^2, 10 uv,
+// 11 v^2, 12-15 zero
 constexpr int B_ONE = 6, B_U = 7, B_V = 8, B_UU = 9, B_UV = 10, B_VV = 11;
 
 // DPP controls (GCN/CDNA): row_shr:n = 0x110 + n, row_ror:n = 0x120 + n, row_bcast:15 = 0x142,
@@ -227,10 +272,14 @@ __device__ __forceinline__ void load8(const float* p, float* x) {
 // product: refine, fp16 only), with hi/lo fp16 splits so ~22 bits of the fp32 inputs survive. The opacity lane needs
 // no product of its own: where a fragment is unclamped v_alpha * gauss = -v_sigma / opacity, and both are
 // zero where it is clamped, so g8 = -(sum v_sigma) / opacity.
+template <bool FEAT, bool HOLLOW>
 __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args a) {
+  constexpr bool EXT = FEAT || HOLLOW;
+  constexpr int ROW = ROW_FLOATS<FEAT>;
   __shared__ float4 s_g0[BATCH];   // (mx, my, c00 / 2, c01)
   __shared__ float4 s_g1[BATCH];   // (c11 / 2, opacity, power, log2 opacity)
   __shared__ float4 s_col[BATCH];  // (max(r, 0), max(g, 0), max(b, 0), sign bits of r, g, b)
+  __shared__ float4 s_ext[EXT ? BATCH : 1];  // (feature xyz, camera depth)
   __shared__ uint32_t s_slot[BATCH];
   __shared__ __attribute__((aligned(16))) float sS[3 * G][SROW];  // rows 0-7 vis, 8-15 v_sigma, 16-23 refine
   const int n_tiles = a.tiles_x * a.tiles_y;
@@ -245,11 +294,13 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   for (uint32_t i = max(range.y, range.x) + lane; i < full_end; i += 64) {
     float4* r = rows + (size_t)a.slot_sorted[i] * (ROW / 4);
     r[0] = r[1] = r[2] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (FEAT) r[3] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (tile == n_tiles - 1) {
     for (uint32_t i = a.tile_end[n_tiles] + lane; i < a.num_isect; i += 64) {
       float4* r = rows + (size_t)a.slot_sorted[i] * (ROW / 4);
       r[0] = r[1] = r[2] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (FEAT) r[3] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
   if (range.y <= range.x) return;
@@ -257,7 +308,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   const int lx = lane & 7, ly = lane >> 3;
   const int px = tx * RT_W + lx, py = ty * RT_W + ly;
   const float u = lx + 0.5f - RT_W * 0.5f, v = ly + 0.5f - RT_W * 0.5f;
-  PixelState ps = load_pixel(a, px, py, range.x);
+  PixelState ps = load_pixel<FEAT, HOLLOW>(a, px, py, range.x);
   // refine: sqrt(W^2 gx^2 + H^2 gy^2) = W sqrt(gx^2 + rho gy^2), W folded into the per-pixel scale
   const float rho = ((float)a.H * (float)a.H) / ((float)a.W * (float)a.W);
   const float r_scale = ps.inv_final_a * R_SCALE * (float)a.W;
@@ -268,7 +319,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   half8 A_hi[2], A_lo[2];
   {
     float* bm = &sS[0][0];  // [16][SROW]
-    const float row[16] = {cv_x, cv_y, cv_z, 0.f, 0.f, 0.f, 1.f, u, v, u * u, u * v, v * v, 0.f, 0.f, 0.f, 0.f};
+    const float row[16] = {cv_x, cv_y, cv_z, ps.vf.x, ps.vf.y, ps.vf.z, 1.f, u, v, u * u, u * v, v * v, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int m = 0; m < 16; m++) bm[m * SROW + lane] = row[m];
     __syncthreads();
@@ -283,6 +334,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 
   float T = ps.T;
   float Q = -ps.v_o_w;  // sum over composited splats behind of (colour . v_rgb) * vis, minus the v_o_w term
+  float Sh = 0.f;       // HOLLOW: sum over composited splats behind of vis * penalty
   const bool live_px = ps.inside;
   for (uint32_t batch_end = range.y; batch_end > range.x;) {
     const uint32_t batch_start = batch_end > range.x + BATCH ? batch_end - BATCH : range.x;
@@ -297,10 +349,12 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       s_g0[lane] = rec[0];
       s_g1[lane] = make_float4(r1.x, r1.y, r1.z, r2.w);
       s_col[lane] = make_float4(r2.x, r2.y, r2.z, r1.w);
+      if constexpr (EXT) s_ext[lane] = rec[3];
     } else if (lane < ngroups * G) {  // pad the last group with null splats, never composited: power = 0
       s_g0[lane] = make_float4(0.f, 0.f, 0.f, 0.f);  // and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1)
       s_g1[lane] = make_float4(1.f, 1.f, 0.f, 0.f);
       s_col[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (EXT) s_ext[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
     for (int grp = ngroups - 1; grp >= 0; grp--) {
@@ -313,6 +367,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       const char* lds_g0 = reinterpret_cast<const char*>(s_g0) + goff;
       const char* lds_g1 = reinterpret_cast<const char*>(s_g1) + goff;
       const char* lds_col = reinterpret_cast<const char*>(s_col) + goff;
+      const char* lds_ext = reinterpret_cast<const char*>(s_ext) + goff;
       // the last list index of the group this pixel composited, relative to the group start
       const int last_rel = (int)ps.last - (int)(batch_start + (uint32_t)gbase);
 #pragma unroll
@@ -336,16 +391,28 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             const float Tb = T * ra;
             const float vis = alpha * Tb;
             const float4 col = *reinterpret_cast<const float4*>(lds_col + jj * 16);
-            const float cv = col.x * cv_x + col.y * cv_y + col.z * cv_z;
-            const float v_alpha = Tb * cv - ra * Q;
-            const float v_sigma = araw <= ALPHA_MAX ? -alpha * v_alpha : 0.f;  // clamped: no sigma gradient
-            // refine statistic: |d(loss)/d(mean2d)| scaled to pixels, over the final alpha
+            float cv = col.x * cv_x + col.y * cv_y + col.z * cv_z;
+            float4 ext = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (EXT) ext = *reinterpret_cast<const float4*>(lds_ext + jj * 16);
+            if constexpr (FEAT) cv = cv + (ext.x * ps.vf.x + ext.y * ps.vf.y + ext.z * ps.vf.z);
+            const float v_alpha_photo = Tb * cv - ra * Q;
+            float v_alpha = v_alpha_photo, hh = 0.f;
+            if constexpr (HOLLOW) {
+              hh = hollow_h(ext.w, ps.href);
+              v_alpha = v_alpha + a.hollow_lam * (Tb * hh - ra * Sh);
+            }
+            const bool unclamped = araw <= ALPHA_MAX;  // clamped: no sigma gradient
+            const float v_sigma = unclamped ? -alpha * v_alpha : 0.f;
+            // refine statistic: |d(loss)/d(mean2d)| scaled to pixels, over the final alpha, from the
+            // photometric (and feature) terms only
+            const float v_sigma_photo = HOLLOW ? (unclamped ? -alpha * v_alpha_photo : 0.f) : v_sigma;
             const float gx = __builtin_fmaf(g0.z, fg.dx, fg.lin), gy = __builtin_fmaf(g0.w, fg.dx, fg.cdy + fg.cdy);
-            o_r = fabsf(v_sigma) * __builtin_amdgcn_sqrtf(gx * gx + rho * gy * gy) * r_scale;
+            o_r = fabsf(v_sigma_photo) * __builtin_amdgcn_sqrtf(gx * gx + rho * gy * gy) * r_scale;
             o_vis = vis;
             o_vs = v_sigma;
             T = Tb;
             Q = Q + vis * cv;
+            if constexpr (HOLLOW) Sh = Sh + vis * hh;
           }
         }
         sS[jj][lane] = o_vis;
@@ -381,11 +448,17 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
         // row_ror:8 within each row of 16 lanes: lane nl gets lane nl ^ 8 (every lane takes part)
         const float sv = __uint_as_float(dpp_u32<0x128, 0xF>(__float_as_uint(dv[2]), 0u));
         const float svu = __uint_as_float(dpp_u32<0x128, 0xF>(__float_as_uint(dv[3]), 0u));
+        // FEAT: the vis column's rows 3-5 (sum vis * v_feat) sit in lane (j, kg 0) row 3 and lane (j, kg 1)
+        // rows 4-5; the first moves 16 lanes up to join the others
+        float fx = 0.f;
+        if constexpr (FEAT) fx = __shfl_up(dv[3], 16);
         if (j < gcount) {
           float4* row = reinterpret_cast<float4*>(a.isect_rows) + (size_t)s_slot[gbase + j] * (ROW / 4);
           if (nl >= G && kg == 2) row[0] = make_float4(dv[0], dv[1], dv[2], dv[3]);
           if (nl < G && kg == 1) row[1] = make_float4(sv, svu, dv[2], d1[2]);
           if (nl < G && kg == 0) row[2] = make_float4(dv[0], dv[1], dv[2], __uint_as_float((uint32_t)tile));
+          if constexpr (FEAT)
+            if (nl < G && kg == 1) row[3] = make_float4(fx, dv[0], dv[1], 0.f);
         }
       }
     }
@@ -408,7 +481,13 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 //    runs over many windows).
 // Every window does the same amount of work whatever the run lengths (splats spanning thousands of tiles
 // do not serialise), and the summation order is fixed: the result is deterministic.
-constexpr int RED_VALS = 11;  // g0..g9 and the blend-weight sum
+// Values carried per row: g0..g9 and the blend-weight sum, and with FEAT the three feature lanes (g10..g12).
+template <bool FEAT>
+constexpr int RED_VALS = FEAT ? 14 : 11;
+// Partial-sum quarters per run piece (three or four float4) and per window (two pieces: the window's first
+// run and its last run; the last piece's third quarter carries the head slot in .w).
+template <bool FEAT>
+constexpr int PART_Q = FEAT ? 4 : 3;
 constexpr uint32_t NO_RUN = 0xFFFFFFFFu;
 constexpr uint32_t W_CONT_BEFORE = 1u, W_CONT_AFTER = 2u, W_HAS_HEAD = 4u;
 constexpr int RED_SUB = 4;                  // 64-row sub-windows per reduce wave
@@ -416,17 +495,18 @@ constexpr uint32_t RED_WIN = 64u * RED_SUB;  // rows per window (one wave)
 
 // One Hillis-Steele step of the segmented scan: add the partial of the DPP source lane when it lies in
 // the same run (runs are contiguous, so equal ids at both ends mean no run boundary in between).
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void seg_scan_step(uint32_t id, float (&v)[RED_VALS]) {
+template <int CTRL, int ROW_MASK, int NV>
+__device__ __forceinline__ void seg_scan_step(uint32_t id, float (&v)[NV]) {
   const bool same = dpp_u32<CTRL, ROW_MASK>(id, NO_RUN) == id;
 #pragma unroll
-  for (int k = 0; k < RED_VALS; k++) {
+  for (int k = 0; k < NV; k++) {
     const float t = __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v[k]), 0u));
     v[k] = same ? v[k] + t : v[k];
   }
 }
 
-__device__ __forceinline__ void seg_scan(uint32_t id, float (&v)[RED_VALS]) {
+template <int NV>
+__device__ __forceinline__ void seg_scan(uint32_t id, float (&v)[NV]) {
   seg_scan_step<0x111, 0xF>(id, v);  // row_shr:1
   seg_scan_step<0x112, 0xF>(id, v);  // row_shr:2
   seg_scan_step<0x114, 0xF>(id, v);  // row_shr:4
@@ -435,34 +515,51 @@ __device__ __forceinline__ void seg_scan(uint32_t id, float (&v)[RED_VALS]) {
   seg_scan_step<0x143, 0xC>(id, v);  // row_bcast:31 into rows 2 and 3
 }
 
-__device__ __forceinline__ void prefetch_old(const b2c_raster_bwd_args& a, uint32_t id, float (&old)[RED_VALS]) {
+template <bool FEAT>
+__device__ __forceinline__ void prefetch_old(const b2c_raster_bwd_args& a, uint32_t id, float (&old)[RED_VALS<FEAT>]) {
   const float* dst = a.v_splat + (size_t)id * GRAD_LANES;
 #pragma unroll
   for (int k = 0; k < 10; k++) old[k] = dst[k];
   old[10] = a.vis_weight ? a.vis_weight[id] : 0.f;
+  if constexpr (FEAT) {
+#pragma unroll
+    for (int k = 0; k < 3; k++) old[11 + k] = dst[10 + k];
+  }
 }
 
 // Adds a finished run's sums to v_splat / vis_weight (previous contents in `old`) and flags the splat.
-__device__ __forceinline__ void finish_run(const b2c_raster_bwd_args& a, uint32_t id, const float (&v)[RED_VALS],
-                                           const float (&old)[RED_VALS]) {
+template <bool FEAT>
+__device__ __forceinline__ void finish_run(const b2c_raster_bwd_args& a, uint32_t id, const float (&v)[RED_VALS<FEAT>],
+                                           const float (&old)[RED_VALS<FEAT>]) {
   if (!(v[10] > 0.f)) return;  // no composited fragment: every lane of the run is zero
   float* dst = a.v_splat + (size_t)id * GRAD_LANES;
 #pragma unroll
   for (int k = 0; k < 10; k++) dst[k] = old[k] + v[k];
+  if constexpr (FEAT) {
+#pragma unroll
+    for (int k = 0; k < 3; k++) dst[10 + k] = old[11 + k] + v[11 + k];
+  }
   a.vis_flag[id] = 1u;
   if (a.vis_weight) a.vis_weight[id] = old[10] + v[10];
 }
 
-__device__ __forceinline__ void store_part(float4* p, const float (&v)[RED_VALS]) {
+template <bool FEAT>
+__device__ __forceinline__ void store_part(float4* p, const float (&v)[RED_VALS<FEAT>]) {
   p[0] = make_float4(v[0], v[1], v[2], v[3]);
   p[1] = make_float4(v[4], v[5], v[6], v[7]);
   p[2] = make_float4(v[8], v[9], v[10], 0.f);
+  if constexpr (FEAT) p[3] = make_float4(v[11], v[12], v[13], 0.f);
 }
 
-__device__ __forceinline__ void add_part(const float4* p, float (&v)[RED_VALS]) {
+template <bool FEAT>
+__device__ __forceinline__ void add_part(const float4* p, float (&v)[RED_VALS<FEAT>]) {
   const float4 q0 = p[0], q1 = p[1], q2 = p[2];
   v[0] += q0.x; v[1] += q0.y; v[2] += q0.z; v[3] += q0.w; v[4] += q1.x; v[5] += q1.y; v[6] += q1.z; v[7] += q1.w;
   v[8] += q2.x; v[9] += q2.y; v[10] += q2.z;
+  if constexpr (FEAT) {
+    const float4 q3 = p[3];
+    v[11] += q3.x; v[12] += q3.y; v[13] += q3.z;
+  }
 }
 
 // Gradient lanes g0..g9 and the blend-weight sum of one (tile, splat) row from its raw moments about the
@@ -470,9 +567,10 @@ __device__ __forceinline__ void add_part(const float4* p, float (&v)[RED_VALS]) 
 // splat centre relative to the tile centre, the first and second moments of v_sigma about the splat centre
 // give the mean and conic gradients, the vis moments the colour gradients, and where a fragment is
 // unclamped v_alpha * gauss = -v_sigma / opacity gives g8. The tile id rides in the row's last float.
+template <bool FEAT>
 __device__ __forceinline__ void row_gradients(const b2c_raster_bwd_args& a, uint32_t s, uint32_t id,
-                                              float (&v)[RED_VALS]) {
-  const float4* rw = reinterpret_cast<const float4*>(a.isect_rows) + (size_t)s * (ROW / 4);
+                                              float (&v)[RED_VALS<FEAT>]) {
+  const float4* rw = reinterpret_cast<const float4*>(a.isect_rows) + (size_t)s * (ROW_FLOATS<FEAT> / 4);
   const float4 q0 = rw[0], q1 = rw[1], q2 = rw[2];
   const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)id * 4;
   const float4 r0 = rec[0], r1 = rec[1];  // (mx, my, c00 / 2, c01), (c11 / 2, opacity, power, sign bits)
@@ -497,9 +595,18 @@ __device__ __forceinline__ void row_gradients(const b2c_raster_bwd_args& a, uint
   v[8] = -sv / r1.y * sc;
   v[9] = q1.w * (1.f / R_SCALE) * sc;  // the raster pre-scales refine terms into the fp16 range
   v[10] = q1.z;
+  if constexpr (FEAT) {
+    const float4 q3 = rw[3];
+    v[11] = q3.x * sc;
+    v[12] = q3.y * sc;
+    v[13] = q3.z * sc;
+  }
 }
 
+template <bool FEAT>
 __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a) {
+  constexpr int RED_VALS = ::b2c::dev::RED_VALS<FEAT>;
+  constexpr int PQ = PART_Q<FEAT>;
   const uint32_t m = a.num_isect;
   const int lane = threadIdx.x & 63;
   const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
@@ -516,7 +623,7 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
   uint32_t carry_head = 0;
   uint32_t prev_id = before;
   bool window_cont_before = false, window_has_head = false;
-  float4* part = reinterpret_cast<float4*>(a.isect_part) + (size_t)w * 6;
+  float4* part = reinterpret_cast<float4*>(a.isect_part) + (size_t)w * (2 * PQ);
   for (int sub = 0; sub < RED_SUB; sub++) {
     const uint32_t lo = wlo + 64u * (uint32_t)sub;
     if (lo >= m) break;
@@ -527,7 +634,7 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
     float v[RED_VALS];
 #pragma unroll
     for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
-    if (valid) row_gradients(a, s, id, v);
+    if (valid) row_gradients<FEAT>(a, s, id, v);
     const uint32_t prev = dpp_u32<0x138, 0xF>(id, prev_id);  // wave_shr:1; lane 0 gets the row before
     const bool head = valid && id != prev;
     const uint64_t heads = ballot64(head);
@@ -551,15 +658,15 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
     const bool crosses_window = cont_after && sub == RED_SUB - 1;
     const bool complete = tail && !(is_first && first_from_before);
     float old[RED_VALS];
-    if (complete) prefetch_old(a, id, old);
+    if (complete) prefetch_old<FEAT>(a, id, old);
     seg_scan(valid ? id : NO_RUN, v);
     if (cont_before && sub > 0 && in_first) {  // the run carried from the previous sub-window
 #pragma unroll
       for (int k = 0; k < RED_VALS; k++) v[k] += carry[k];
     }
-    if (complete) finish_run(a, id, v, old);
+    if (complete) finish_run<FEAT>(a, id, v, old);
     if (is_first && first_from_before && (!cont_after || !last_is_first || sub == RED_SUB - 1))
-      store_part(part, v);  // the window's first piece ends here (or spans the whole window)
+      store_part<FEAT>(part, v);  // the window's first piece ends here (or spans the whole window)
     // the last run of the sub-window continues: carry it, or leave it for the fixup at the window's edge
     const uint32_t last_head = lo + 63u - (heads ? (uint32_t)__builtin_clzll(heads) : 63u);
     const bool last_from_before = last_is_first ? first_from_before : false;
@@ -570,8 +677,8 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
         carry_from_before = last_from_before;
         carry_head = (heads && !(last_is_first && cont_before)) ? last_head : carry_head;
       } else if (is_last && !last_from_before) {  // a run that starts in this window: sums and head slot
-        store_part(part + 3, v);
-        part[5].w = __uint_as_float((heads && !(last_is_first && cont_before)) ? last_head : carry_head);
+        store_part<FEAT>(part + PQ, v);
+        part[PQ + 2].w = __uint_as_float((heads && !(last_is_first && cont_before)) ? last_head : carry_head);
       }
     }
     prev_id = id63;
@@ -591,7 +698,10 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
 // order: one wave step per such run, so no lane walks a long chain alone.
 constexpr uint32_t SHORT_SPAN = 4;
 
+template <bool FEAT>
 __global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) {
+  constexpr int RED_VALS = ::b2c::dev::RED_VALS<FEAT>;
+  constexpr int PQ = PART_Q<FEAT>;
   const uint32_t nwin = (a.num_isect + RED_WIN - 1u) / RED_WIN;
   const uint32_t w = blockIdx.x * 64u + threadIdx.x;
   const int lane = threadIdx.x & 63;
@@ -602,19 +712,19 @@ __global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) 
   const uint32_t wc = min(w, nwin - 1u);
   const uint32_t f = a.isect_part_flags[wc];
   const uint32_t run_ld = a.isect_vals[min(wc * RED_WIN + RED_WIN - 1u, a.num_isect - 1u)];
-  const uint32_t head = __float_as_uint(part[(size_t)wc * 6 + 5].w);
-  float4 tail[3], nxt[SHORT_SPAN][3];
+  const uint32_t head = __float_as_uint(part[(size_t)wc * (2 * PQ) + PQ + 2].w);
+  float4 tail[PQ], nxt[SHORT_SPAN][PQ];
 #pragma unroll
-  for (int k = 0; k < 3; k++) tail[k] = part[(size_t)wc * 6 + 3 + k];
+  for (int k = 0; k < PQ; k++) tail[k] = part[(size_t)wc * (2 * PQ) + PQ + k];
 #pragma unroll
   for (uint32_t d = 1; d <= SHORT_SPAN; d++)
 #pragma unroll
-    for (int k = 0; k < 3; k++) nxt[d - 1][k] = part[(size_t)min(wc + d, nwin - 1u) * 6 + k];
+    for (int k = 0; k < PQ; k++) nxt[d - 1][k] = part[(size_t)min(wc + d, nwin - 1u) * (2 * PQ) + k];
   const bool owner = w < nwin && (f & W_CONT_AFTER) && (f & W_HAS_HEAD);
   const uint32_t run = owner ? run_ld : NO_RUN;
   const uint32_t tc = a.tile_count[run_ld];
   float old_s[RED_VALS];
-  prefetch_old(a, run_ld, old_s);
+  prefetch_old<FEAT>(a, run_ld, old_s);
   // the run covers emit positions [head, head + tile_count)
   const uint32_t last_win = owner ? min((head + tc - 1u) / RED_WIN, nwin - 1u) : 0u;
   const bool short_run = owner && last_win - w <= SHORT_SPAN;
@@ -622,11 +732,11 @@ __global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) 
     float v[RED_VALS];
 #pragma unroll
     for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
-    add_part(tail, v);
+    add_part<FEAT>(tail, v);
 #pragma unroll
     for (uint32_t d = 1; d <= SHORT_SPAN; d++)
-      if (w + d <= last_win) add_part(nxt[d - 1], v);  // the run's rows at the start of w + d
-    finish_run(a, run, v, old_s);
+      if (w + d <= last_win) add_part<FEAT>(nxt[d - 1], v);  // the run's rows at the start of w + d
+    finish_run<FEAT>(a, run, v, old_s);
   }
   // long runs: every lane of the wave stays to here (no early exit), so the cross-lane sums are whole
   uint64_t longs = ballot64(owner && !short_run);
@@ -641,7 +751,7 @@ __global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) 
     for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
     for (uint32_t x0 = lw + 1; x0 <= llast; x0 += 64u) {
       const uint32_t x = x0 + (uint32_t)lane;
-      if (x <= llast) add_part(part + (size_t)x * 6, v);
+      if (x <= llast) add_part<FEAT>(part + (size_t)x * (2 * PQ), v);
     }
 #pragma unroll
     for (int k = 0; k < RED_VALS; k++) {
@@ -649,10 +759,10 @@ __global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) 
       for (int o = 32; o >= 1; o >>= 1) v[k] += __shfl_xor(v[k], o);
     }
     if (lane == src) {
-      add_part(part + (size_t)lw * 6 + 3, v);
+      add_part<FEAT>(part + (size_t)lw * (2 * PQ) + PQ, v);
       float old[RED_VALS];
-      prefetch_old(a, lrun, old);
-      finish_run(a, lrun, v, old);
+      prefetch_old<FEAT>(a, lrun, old);
+      finish_run<FEAT>(a, lrun, v, old);
     }
   }
 }
@@ -667,13 +777,28 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
   const int n_tiles = a->tiles_x * a->tiles_y;
   if (n_tiles <= 0) return 0;
   const dim3 grid(NUM_XCD * xcd_tiles_per(n_tiles)), block(64);
+  const bool feat = a->feat != 0, hollow = a->hollow_z != nullptr && a->hollow_lam != 0.f;
+  if (feat && !a->v_feat) return (int)hipErrorInvalidValue;
   if (a->mode == 0) {
-    raster_bwd_fp32_kernel<<<grid, block, 0, stream>>>(*a);
+    if (feat && !a->proj3) return (int)hipErrorInvalidValue;
+    if (feat) {
+      if (hollow) raster_bwd_fp32_kernel<true, true><<<grid, block, 0, stream>>>(*a);
+      else raster_bwd_fp32_kernel<true, false><<<grid, block, 0, stream>>>(*a);
+    } else {
+      if (hollow) raster_bwd_fp32_kernel<false, true><<<grid, block, 0, stream>>>(*a);
+      else raster_bwd_fp32_kernel<false, false><<<grid, block, 0, stream>>>(*a);
+    }
   } else {
     if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->tile_count ||
         !a->raster_rec)
       return (int)hipErrorInvalidValue;
-    raster_bwd_mfma_kernel<<<grid, block, 0, stream>>>(*a);
+    if (feat) {
+      if (hollow) raster_bwd_mfma_kernel<true, true><<<grid, block, 0, stream>>>(*a);
+      else raster_bwd_mfma_kernel<true, false><<<grid, block, 0, stream>>>(*a);
+    } else {
+      if (hollow) raster_bwd_mfma_kernel<false, true><<<grid, block, 0, stream>>>(*a);
+      else raster_bwd_mfma_kernel<false, false><<<grid, block, 0, stream>>>(*a);
+    }
     if (a->split_event) {
       const int e = (int)hipEventRecord(static_cast<hipEvent_t>(a->split_event), stream);
       if (e) return e;
@@ -681,8 +806,13 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
     const uint32_t windows = (a->num_isect + RED_WIN - 1u) / RED_WIN;
     if (windows) {
       if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;
-      isect_reduce_kernel<<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
-      isect_fixup_kernel<<<dim3((windows + 63u) / 64u), dim3(64), 0, stream>>>(*a);
+      if (feat) {
+        isect_reduce_kernel<true><<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
+        isect_fixup_kernel<true><<<dim3((windows + 63u) / 64u), dim3(64), 0, stream>>>(*a);
+      } else {
+        isect_reduce_kernel<false><<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
+        isect_fixup_kernel<false><<<dim3((windows + 63u) / 64u), dim3(64), 0, stream>>>(*a);
+      }
     }
   }
   return (int)hipGetLastError();

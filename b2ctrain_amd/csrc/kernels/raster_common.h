@@ -52,6 +52,22 @@ __device__ __forceinline__ float fragment_alpha(float sigma, float log2_op) {
   return __builtin_amdgcn_exp2f(__builtin_fmaf(sigma, -LOG2E, log2_op));
 }
 
+// Hollow loss (splat_math.cuh:14-17): a fragment at camera depth z behind a pixel's reference surface
+// z_ref is penalised by h = clamp((z - z_ref - margin) / margin, 0, 1) (margin floored at 1e-4), and 0 when
+// that quotient is not finite (no surface: z_ref = +inf). Evaluated as (z - (z_ref + margin)) / margin with
+// the reciprocal taken once per pixel: the same value up to rounding, and the same bits in the forward,
+// both backward modes and the CPU restatement.
+struct HollowRef {
+  float zm, inv_m;  // z_ref + margin, 1 / max(margin, 1e-4)
+};
+__device__ __forceinline__ HollowRef hollow_ref(float z_ref, float margin) {
+  return HollowRef{z_ref + margin, 1.f / fmaxf(margin, 1e-4f)};
+}
+__device__ __forceinline__ float hollow_h(float z, HollowRef h) {
+  const float d = (z - h.zm) * h.inv_m;
+  return __builtin_isfinite(d) ? fminf(fmaxf(d, 0.f), 1.f) : 0.f;
+}
+
 // Quadrant culling. A raster wave covers an 8x8 tile as four 4x4 quadrants of 16 lanes; bit q = 2 qy + qx
 // of the mask is set when the splat's ellipse {sigma <= power} can reach a pixel centre of quadrant (qx, qy).
 // sigma = ah dx^2 + ch dy^2 + b dx dy (ah = c00 / 2, ch = c11 / 2) is convex, so its minimum over the box

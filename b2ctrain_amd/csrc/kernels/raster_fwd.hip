@@ -1,9 +1,9 @@
-// Forward compositing (replaces src/gpu/raster_fwd.cu:8-90, FEAT none, HOLLOW none): one wave64 per 8x8
-// tile, one lane per pixel, the tile's depth-ordered list staged through LDS 64 splats at a time and
-// split per 4x4 quadrant,
+// Forward compositing (replaces src/gpu/raster_fwd.cu:8-90): one wave64 per 8x8 tile, one lane per pixel,
+// the tile's depth-ordered list staged through LDS 64 splats at a time and split per 4x4 quadrant,
 // front-to-back alpha blending with the 1/255 cutoff (sigma <= power), the 0.999 clamp and the 1e-4
 // transmittance stop. The whole wave leaves as soon as every lane is done. With bwd_info the tile's range
-// end is shrunk to one past the last fragment any pixel composited.
+// end is shrunk to one past the last fragment any pixel composited. FEAT composites the three feature
+// lanes as the colour is (without background); HOLLOW sums each pixel's hollow penalty.
 #include "b2c_kernels.h"
 #include "raster_common.h"
 
@@ -25,9 +25,12 @@ __device__ __forceinline__ float splat_sigma(float4 g0, float4 g1, float pcx, fl
   return frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, pcx, pcy).sigma;
 }
 
+template <bool FEAT, bool HOLLOW>
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
+  constexpr bool EXT = FEAT || HOLLOW;
   // slot 64 is a null splat (no fragment passes) that pads the shorter quadrant lists
   __shared__ float4 s_g0[65], s_g1[65], s_col[65];
+  __shared__ float4 s_ext[EXT ? 65 : 1];  // (feature xyz, camera depth)
   __shared__ uint32_t s_list[4][66];  // per quadrant: LDS byte offsets of its splats, in depth order
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
@@ -42,6 +45,9 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   uint2* ranges = reinterpret_cast<uint2*>(a.tile_ranges);
   const uint2 range = ranges[tile];
   float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
+  float f0 = 0.f, f1 = 0.f, f2 = 0.f, pen = 0.f;
+  HollowRef href{};
+  if constexpr (HOLLOW) href = hollow_ref(inside ? a.hollow_z[py * a.W + px] : __builtin_inff(), a.hollow_margin);
   bool live = inside;
   uint32_t last = range.x;
   if (lane < 8) s_list[lane >> 1][64 + (lane & 1)] = 64u * 16u;  // read by the last pair's prefetch
@@ -49,10 +55,12 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     s_g0[64] = make_float4(0.f, 0.f, 0.f, 0.f);
     s_g1[64] = make_float4(1.f, 0.f, 0.f, 0.f);
     s_col[64] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (EXT) s_ext[64] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   const char* lds_g0 = reinterpret_cast<const char*>(s_g0);
   const char* lds_g1 = reinterpret_cast<const char*>(s_g1);
   const char* lds_col = reinterpret_cast<const char*>(s_col);
+  const char* lds_ext = reinterpret_cast<const char*>(s_ext);
   constexpr uint32_t NO_OFF = 0xFFFFFFFFu;
   for (uint32_t start = range.x; start < range.y; start += 64) {
     if (ballot64(live) == 0) break;
@@ -66,6 +74,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
       s_g0[lane] = r0;
       s_g1[lane] = make_float4(r1.x, r2.w, r1.z, 0.f);
       s_col[lane] = r2;
+      if constexpr (EXT) s_ext[lane] = rec[3];
       qmask = quadrant_mask(r0.x, r0.y, r0.z, r0.w, r1.x, r1.z, x0, y0);
     }
     // per-quadrant lists: the lanes with bit qq set, in lane (depth) order, padded with the null splat
@@ -112,6 +121,15 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     r += col.x * vis;                                                                                  \
     g += col.y * vis;                                                                                  \
     b += col.z * vis;                                                                                  \
+    if constexpr (EXT) {                                                                               \
+      const float4 ext = *reinterpret_cast<const float4*>(lds_ext + (off));                            \
+      if constexpr (FEAT) {                                                                            \
+        f0 += ext.x * vis;                                                                             \
+        f1 += ext.y * vis;                                                                             \
+        f2 += ext.z * vis;                                                                             \
+      }                                                                                                \
+      if constexpr (HOLLOW) pen += vis * hollow_h(ext.w, href);                                        \
+    }                                                                                                  \
     T = stop ? T : next_T;                                                                             \
     last_off = (valid & !stop) ? (off) : last_off;                                                     \
     (off) = my_list[next];                                                                             \
@@ -126,7 +144,8 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   if (inside) {
     const int pix = py * a.W + px;
     reinterpret_cast<float4*>(a.out_rgba)[pix] = make_float4(r + T * a.bg[0], g + T * a.bg[1], b + T * a.bg[2], 1.f - T);
-    reinterpret_cast<float4*>(a.out_feat)[pix] = make_float4(0.f, 0.f, 0.f, T);
+    reinterpret_cast<float4*>(a.out_feat)[pix] = make_float4(f0, f1, f2, T);
+    if constexpr (HOLLOW) a.hollow_pen[pix] = pen;
     if (a.bwd_info) a.last_idx[pix] = last;
   }
   if (a.bwd_info) {
@@ -146,7 +165,15 @@ using namespace b2c::dev;
 extern "C" int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream) {
   const int n_tiles = a->tiles_x * a->tiles_y;
   if (n_tiles <= 0) return 0;
-  if (!a->raster_rec) return (int)hipErrorInvalidValue;
-  raster_fwd_kernel<<<dim3(NUM_XCD * xcd_tiles_per(n_tiles)), dim3(64), 0, stream>>>(*a);
+  if (!a->raster_rec || (a->hollow_z && !a->hollow_pen)) return (int)hipErrorInvalidValue;
+  const dim3 grid(NUM_XCD * xcd_tiles_per(n_tiles)), block(64);
+  const bool hollow = a->hollow_z != nullptr;
+  if (a->feat) {
+    if (hollow) raster_fwd_kernel<true, true><<<grid, block, 0, stream>>>(*a);
+    else raster_fwd_kernel<true, false><<<grid, block, 0, stream>>>(*a);
+  } else {
+    if (hollow) raster_fwd_kernel<false, true><<<grid, block, 0, stream>>>(*a);
+    else raster_fwd_kernel<false, false><<<grid, block, 0, stream>>>(*a);
+  }
   return (int)hipGetLastError();
 }

@@ -396,6 +396,23 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
       for (int r = 0; r < 3; r++)
 #pragma unroll
         for (int j = 0; j < 3; j++) gR[3 * r + j] = (Rv[r] * gW[j] + Rv[3 + r] * gW[3 + j]) + Rv[6 + r] * gW[6 + j];
+      // Feature lanes (optim.cu:235-250): the pseudo-normal f = R_view (s u), u = c / |c| with c the column
+      // of R(q) along the smallest log scale and s = +-1 its facing sign (locally constant), so
+      // dL/dc = s (I - u u^T) R_view^T dL/df / |c|, which joins that column of dL/dR(q).
+      if (g[10] != 0.f || g[11] != 0.f || g[12] != 0.f) {
+        const int ax = (ls.x <= ls.y && ls.x <= ls.z) ? 0 : (ls.y <= ls.z ? 1 : 2);
+        const float nx = sp.rot.m[ax], ny = sp.rot.m[3 + ax], nz = sp.rot.m[6 + ax];
+        const float il = 1.f / fmaxf(sqrtf((nx * nx + ny * ny) + nz * nz), 1e-12f);
+        const float ux = nx * il, uy = ny * il, uz = nz * il;
+        const float face = ((ux * -dvx + uy * -dvy) + uz * -dvz) >= 0.f ? 1.f : -1.f;
+        const float bx = ((Rv[0] * g[10] + Rv[3] * g[11]) + Rv[6] * g[12]) * face;
+        const float by = ((Rv[1] * g[10] + Rv[4] * g[11]) + Rv[7] * g[12]) * face;
+        const float bz = ((Rv[2] * g[10] + Rv[5] * g[11]) + Rv[8] * g[12]) * face;
+        const float along = (ux * bx + uy * by) + uz * bz;
+        gR[ax] = gR[ax] + (bx - ux * along) * il;
+        gR[3 + ax] = gR[3 + ax] + (by - uy * along) * il;
+        gR[6 + ax] = gR[6 + ax] + (bz - uz * along) * il;
+      }
       // semi-axes a_j = sqrt(exp(2 l_j) + f^2), and the floor's opacity factor prod_j sqrt(var_j / (var_j + f^2))
       const float v_op = g[8];
       const float f2 = ls.w * ls.w;

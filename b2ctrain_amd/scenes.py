@@ -88,6 +88,14 @@ class Scene:
     scale: float = 1.0
     bg: tuple = (0.0, 0.0, 0.0)
     extra_cams: list = field(default_factory=list)
+    # feature lanes and the losses on them (render.h:27-63, loss.h:20-30)
+    feat_mode: int = 0                 # 0 none, 1 pseudo-normals, 2 feat_buffer
+    feat_buffer: np.ndarray | None = None  # [n][3] float32 with feat_mode 2
+    normals: np.ndarray | None = None  # [P] packed RGBA8 normal map (ViewGPU::normals)
+    normal_scale: float = 0.0          # normal_loss weight
+    hollow_z: np.ndarray | None = None  # [P] float32 reference surface depth (+inf = none)
+    hollow_margin: float = 0.05
+    hollow_lam: float = 0.0
 
     @property
     def n(self) -> int:
@@ -351,6 +359,32 @@ def fd_scene(seed: int, n: int = 24, masked: bool = False, degree: int = 2, floo
     return Scene(f"fd{seed}{tag}", degree, pos_op, quat, lscale, sh, cam, gt.astype(np.uint32),
                  weights, composite=not masked, mask=masked, alpha_lane=not masked, match_alpha_weight=0.3,
                  scale=1.7 if masked else 1.0, bg=(0.2, 0.1, 0.3))
+
+
+def fd_feature_scene(seed: int, n: int = 24, masked: bool = False, normals: bool = False, hollow: bool = False,
+                     degree: int = 2) -> Scene:
+    """The FD harness's normal and hollow configurations (tests/tests.cpp:23-59, 66-76, 386-391) on an
+    FD-harness scene: a random normal map opaque on about 70% of the pixels, normal_scale = 0.05 / 100
+    (normal_loss_weight over the view's normal count); a reference depth 1.9 + 0.25 sin(0.4 x) +
+    0.2 cos(0.3 y) with a 6x6 corner of no surface (+inf), margin 0.05, lam = 0.7 / (W H)."""
+    sc = fd_scene(seed, n=n, masked=masked, degree=degree)
+    rng = np.random.default_rng(seed + 104729)
+    W, H = sc.W, sc.H
+    if normals:
+        rgb = (rng.random((W * H, 3)) * 255).astype(np.uint32)
+        a = np.where(rng.random(W * H) > 0.3, 255, 0).astype(np.uint32)
+        sc.normals = (rgb[:, 0] | (rgb[:, 1] << 8) | (rgb[:, 2] << 16) | (a << 24)).astype(np.uint32)
+        sc.feat_mode = 1
+        sc.normal_scale = 0.05 / 100.0
+    if hollow:
+        y, x = np.mgrid[0:H, 0:W]
+        z = 1.9 + 0.25 * np.sin(x * 0.4) + 0.2 * np.cos(y * 0.3)
+        z[(x < 6) & (y < 6)] = np.inf
+        sc.hollow_z = z.astype(np.float32).reshape(-1)
+        sc.hollow_margin = 0.05
+        sc.hollow_lam = 0.7 / (W * H)
+    sc.name = sc.name + ("n" if normals else "") + ("h" if hollow else "")
+    return sc
 
 
 def clamp_scene(seed: int, n: int = 24, degree: int = 2) -> Scene:

@@ -37,6 +37,10 @@ typedef struct b2c_render_opts {
   float bg[3];
   int sh_degree;
   int bwd_info;
+  int feat_mode;            /* FeatureMode: 0 none, 1 normals (camera-space pseudo-normals), 2 buffer */
+  const float* feat_buffer; /* device [n][3] with feat_mode 2 (b2c_device_upload) */
+  const float* hollow_z;    /* device [W*H] reference surface depth (+inf = none), or NULL: no hollow loss */
+  float hollow_margin, hollow_lam;
 } b2c_render_opts;
 
 /* LossParams (src/gpu/loss.h:20-30). */
@@ -45,6 +49,7 @@ typedef struct b2c_loss_opts {
   float bg[3];
   int composite, mask, alpha_lane;
   float match_alpha_weight, scale, grad_scale;
+  float normal_scale; /* normal_loss weight */
 } b2c_loss_opts;
 
 typedef struct b2c_ctx_info {
@@ -110,6 +115,11 @@ void* b2c_ctx_stream(b2c_ctx* c);
 /* A view: device copies of packed RGBA8 and optional u8 weights. */
 b2c_view* b2c_view_create(int W, int H, const uint32_t* rgba, const uint8_t* weights);
 void b2c_view_destroy(b2c_view* v);
+/* ViewGPU::normals: a device copy of a packed RGBA8 normal map [W*H] (NULL removes it). */
+int b2c_view_set_normals(b2c_view* v, const uint32_t* normals);
+/* A device copy of host memory (for RenderParams' device arrays: feat_buffer, hollow_z), and its release. */
+void* b2c_device_upload(const void* host, size_t bytes);
+void b2c_device_free(void* p);
 
 /* render_forward / project_splats / bin_and_sort / rasterize_forward (src/gpu/render.h:97-103). */
 int b2c_render_forward(b2c_ctx* c, const b2c_model* m, const b2c_render_opts* o);
@@ -119,6 +129,12 @@ int b2c_rasterize_forward(b2c_ctx* c, const b2c_render_opts* o);
 /* photometric_loss / accumulate_loss (src/gpu/loss.h:33-37). */
 int b2c_photometric_loss(b2c_ctx* c, const b2c_view* v, const b2c_loss_opts* o);
 int b2c_accumulate_loss(b2c_ctx* c);
+/* normal_loss / hollow_loss / eval_metrics (src/gpu/loss.h:35-41): the normal-map loss into loss_accum[1]
+ * with its gradient in "v_feat"; lam * sum of "hollow_pen" into loss_accum[0]; squared-error and SSIM
+ * sums of the 8-bit render into loss_accum[4] and [5]. */
+int b2c_normal_loss(b2c_ctx* c, const b2c_view* v, const b2c_loss_opts* o);
+int b2c_hollow_loss(b2c_ctx* c, float lam);
+int b2c_eval_metrics(b2c_ctx* c, const b2c_view* v, int mask_weighted);
 /* rasterize_backward (mode 0) / rasterize_backward_tc (mode 1, divides by grad_scale) (src/gpu/render.h:105-109). */
 int b2c_rasterize_backward(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, int mode, float grad_scale);
 /* Flags of the gradient write: B2C_GRAD_ACCUMULATE sums into the "grads" buffer instead of overwriting it (this
@@ -144,8 +160,11 @@ void b2c_adam_defaults(b2c_adam_opts* a);
  * Adam / lazy sparse Adam / MCMC noise update of the model. The active SH degree is o->sh_degree. */
 int b2c_optimizer_step(b2c_ctx* c, b2c_model* m, const b2c_render_opts* o, const b2c_adam_opts* a);
 /* One training step as trainer.cpp:487-529 orders it (forward, loss with grad_scale, backward in `mode`,
- * projection VJP with the gradient flags above); the step's loss replaces loss_accum[0] (loss_accum[1] = 0).
- * times may be NULL (no events recorded). */
+ * projection VJP with the gradient flags above). The losses follow trainer.cpp:502-505: photometric, then
+ * the normal-map loss when ro->feat_mode = 1, lo->normal_scale > 0 and the view has a normal map, then the
+ * hollow loss when ro->hollow_z is set and hollow_lam != 0; loss_accum then holds [photometric + hollow,
+ * normal, their sum, 1], what the trainer's per-step clear and accumulate_loss leave. times may be NULL
+ * (no events recorded). */
 int b2c_train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
                    int mode, int flags, b2c_step_times* times);
 /* The same step ending in the fused update (b2c_optimizer_step) instead of the gradient write: a complete

@@ -55,13 +55,17 @@ typedef struct b2c_project_args {
   uint32_t* hit_info;  /* [n] uint2 (hit mask or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24) */
   float* max_screen;   /* [n] or NULL: max(., max(ex/W, ey/H)) (project.cu:82-83) */
   float* raster_rec;   /* [n][16]: the raster kernels' per-splat record, one 64-byte line: (mx, my, c00/2, c01),
-                          (c11/2, opacity, power, sign bits of r, g, b), (max(r,0), max(g,0), max(b,0), log2 opacity), 0 */
+                          (c11/2, opacity, power, sign bits of r, g, b), (max(r,0), max(g,0), max(b,0), log2 opacity),
+                          (feat.x, feat.y, feat.z, camera depth) */
   uint32_t* big_list;  /* [n] scratch: splats whose bbox exceeds 32 tiles */
   uint32_t* big_count; /* [1] scratch counter */
   uint32_t* big_info;  /* [n][4] scratch: per big-list entry, bbox origin, width, area, chunk length */
   uint32_t* big_chunk; /* [n][B2C_BIG_CHUNKS] scratch: per-chunk exclusive hit offsets of each entry */
   uint32_t* big_items; /* [n][B2C_BIG_CHUNKS] scratch: work items (entry << 5 | chunk) */
   uint32_t* big_items_count; /* [1] scratch counter */
+  int feat_mode;       /* FeatureMode (render.h:27): 0 none, 1 normals (the camera-space pseudo-normal: the
+                          shortest semi-axis, turned to face the camera), 2 buffer (feat_buffer, clamped) */
+  const float* feat_buffer; /* [n][3] when feat_mode = 2 */
 } b2c_project_args;
 
 /* At most this many chunks per big splat (one wave each); and the grid (workgroups of 256) that the
@@ -134,7 +138,9 @@ int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_
 
 /* ---- rasterization ---- */
 
-/* raster_fwd_kernel<FEAT=none, BWD, HOLLOW=none> / rasterize_forward (src/gpu/raster_fwd.cu:8-90). */
+/* raster_fwd_kernel<FEAT, BWD, HOLLOW> / rasterize_forward (src/gpu/raster_fwd.cu:8-90). With feat the
+ * feature lanes are composited into out_feat.xyz (no background term); with hollow_z each pixel's penalty
+ * sum of vis * clamp((z - z_ref - margin) / max(margin, 1e-4), 0, 1) goes to hollow_pen. */
 typedef struct b2c_raster_fwd_args {
   uint32_t* tile_ranges;      /* [n_tiles] uint2; .y shrunk in place when bwd_info */
   const uint32_t* vals_sorted;
@@ -146,6 +152,10 @@ typedef struct b2c_raster_fwd_args {
   float* out_rgba;            /* [P] float4 */
   float* out_feat;            /* [P] float4 (feat xyz, T) */
   uint32_t* last_idx;         /* [P] */
+  int feat;                   /* composite the feature lanes (raster_rec[3].xyz) */
+  const float* hollow_z;      /* [P] reference surface depth (+inf = none) or NULL */
+  float hollow_margin;
+  float* hollow_pen;          /* [P] with hollow_z */
 } b2c_raster_fwd_args;
 int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream);
 
@@ -182,10 +192,17 @@ typedef struct b2c_raster_bwd_args {
   const uint32_t* isect_vals; /* [M] splat id of emit position s (the emit kernel's values) */
   const uint32_t* tile_count; /* [n] intersections per splat (the length of its run of emit positions) */
   const uint32_t* tile_end;   /* [n_tiles + 1] list end before the forward's shrink; [n_tiles] = sentinel start */
-  float* isect_rows;          /* [M][12] scratch */
-  float* isect_part;          /* [ceil(M / 256)][24] scratch: partial sums of runs crossing 256-row windows */
+  float* isect_rows;          /* [M][16] scratch (12 floats a row are used without feat) */
+  float* isect_part;          /* [ceil(M / 256)][32] scratch: partial sums of runs crossing 256-row windows */
   uint32_t* isect_part_flags; /* [ceil(M / 256)] scratch */
   void* split_event;          /* optional hipEvent_t recorded between the raster kernel and the reduce */
+  /* feature lanes and hollow loss (raster_bwd.cu:84-110, raster_bwd_tc.cu:126-141) */
+  int feat;                   /* v_feat back through the composited feature lanes, into v_splat[10..12] */
+  const float* v_feat;        /* [P] float4 with feat */
+  const float* proj3;         /* [n] float2 (feature y, z): mode 0 with feat */
+  const float* hollow_z;      /* [P] or NULL */
+  float hollow_margin;
+  float hollow_lam;           /* dL / d(penalised weight) per pixel in v_out's units (times grad_scale) */
 } b2c_raster_bwd_args;
 int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stream);
 
@@ -226,6 +243,46 @@ int b2c_hip_photometric_noalloc(const b2c_loss_args* a, hipStream_t stream);
 
 /* accumulate_kernel (loss.cu:317,324): a[2] += a[0] + a[1]; a[3] += 1. */
 int b2c_hip_accumulate_loss(float* loss_accum, hipStream_t stream);
+/* a[2] = a[0] + a[1]; a[3] = 1: what the trainer's per-step clear of a[0..3] followed by accumulate_kernel
+ * leaves, for a step whose losses were assigned rather than added. */
+int b2c_hip_step_loss_sums(float* loss_accum, hipStream_t stream);
+
+/* ---- the other losses (src/gpu/loss.cu:197-293, 317-338) ----
+ * Each sums its per-workgroup partials in a fixed order in double precision (deterministic); `partials` is
+ * scratch of b2c_aux_partials(W, H) floats. */
+size_t b2c_aux_partials(int W, int H);
+
+/* normal_loss_kernel (loss.cu:206-238): for pixels whose normal-map alpha is above 127, scale * w *
+ * (|p - g|_1 + 1 - cos(p, g)) with g decoded as [+X, -Y, -Z]; the gradient (times grad_scale) to v_feat
+ * (zero elsewhere), the loss added to loss_accum[1]. */
+typedef struct b2c_normal_loss_args {
+  const float* feat;          /* [P] float4 out_feat */
+  const uint32_t* normals;    /* [P] packed RGBA8 normal map */
+  const uint8_t* weights;     /* [P] or NULL */
+  int W, H;
+  float scale, grad_scale;
+  float* v_feat;              /* [P] float4 */
+  float* loss_accum;
+  float* partials;
+} b2c_normal_loss_args;
+int b2c_hip_normal_loss(const b2c_normal_loss_args* a, hipStream_t stream);
+
+/* hollow_reduce_kernel (loss.cu:197-204): loss_accum[0] += lam * sum(hollow_pen). */
+int b2c_hip_hollow_loss(const float* hollow_pen, int W, int H, float lam, float* loss_accum, float* partials,
+                        hipStream_t stream);
+
+/* eval_kernel (loss.cu:240-286): prediction quantised to 8 bits (clamped to [0, 1]), per channel the sums of
+ * the squared error and of the clamped 11-tap SSIM (zero padding), each weighted by the target alpha when
+ * mask_weighted; loss_accum[4] += sum of squares, loss_accum[5] += sum of SSIM. */
+typedef struct b2c_eval_args {
+  const float* pred;          /* [P] float4 out_rgba */
+  const uint32_t* gt;         /* [P] packed RGBA8 */
+  int W, H;
+  int mask_weighted;
+  float* loss_accum;
+  float* partials;
+} b2c_eval_args;
+int b2c_hip_eval_metrics(const b2c_eval_args* a, hipStream_t stream);
 
 /* Writable planar SH arrays (the same layout as b2c_sh_view): parameters or their first moments. */
 typedef struct b2c_sh_planes {

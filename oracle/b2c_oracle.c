@@ -274,8 +274,9 @@ int orc_tile_bits(int n_tiles) {
 }
 
 /* project.cu:8-84 (DEG from the model, FEAT none). */
-void orc_project(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int tiles_x, int tiles_y, float* proj0,
-                 float* proj1, float* proj2, float* proj3, uint32_t* tile_count, uint32_t* hit_info) {
+void orc_project_feat(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int tiles_x, int tiles_y, float* proj0,
+                      float* proj1, float* proj2, float* proj3, uint32_t* tile_count, uint32_t* hit_info, int feat_mode,
+                      const float* feat_buffer) {
   const int K = (m->degree + 1) * (m->degree + 1);
   int deg = active_deg < m->degree ? active_deg : m->degree;
   if (deg < 0) deg = 0;
@@ -323,9 +324,35 @@ void orc_project(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int
     float* p0 = proj0 + (size_t)i * 4; float* p1 = proj1 + (size_t)i * 4; float* p2 = proj2 + (size_t)i * 4;
     p0[0] = pr.mean2d[0]; p0[1] = pr.mean2d[1]; p0[2] = pr.conic.c00; p0[3] = pr.conic.c01;
     p1[0] = pr.conic.c11; p1[1] = pr.opac; p1[2] = pr.mc[2]; p1[3] = power;
-    p2[0] = cr; p2[1] = cg; p2[2] = cb; p2[3] = 0.f;
-    proj3[(size_t)i * 2] = 0.f; proj3[(size_t)i * 2 + 1] = 0.f;
+    /* feature lanes (project.cu:63-77) */
+    float f0 = 0.f, f1 = 0.f, f2 = 0.f;
+    const float* ls = m->lscale + (size_t)i * 4;
+    if (feat_mode == 1) {
+      const int ax = (ls[0] <= ls[1] && ls[0] <= ls[2]) ? 0 : (ls[1] <= ls[2] ? 1 : 2);
+      const float nx = pr.Rq[ax], ny = pr.Rq[3 + ax], nz = pr.Rq[6 + ax];
+      const float il = 1.f / fmaxf(sqrtf((nx * nx + ny * ny) + nz * nz), 1e-12f);
+      const float sx = nx * il, sy = ny * il, sz = nz * il;
+      const float d0 = po[0] - cam->pos[0], d1 = po[1] - cam->pos[1], d2 = po[2] - cam->pos[2];
+      const float face = ((sx * -d0 + sy * -d1) + sz * -d2) >= 0.f ? 1.f : -1.f;
+      const float wx = sx * face, wy = sy * face, wz = sz * face;
+      const float* Rv = cam->R;
+      f0 = (Rv[0] * wx + Rv[1] * wy) + Rv[2] * wz;
+      f1 = (Rv[3] * wx + Rv[4] * wy) + Rv[5] * wz;
+      f2 = (Rv[6] * wx + Rv[7] * wy) + Rv[8] * wz;
+    } else if (feat_mode == 2) {
+      f0 = feat_buffer[(size_t)i * 3]; f1 = feat_buffer[(size_t)i * 3 + 1]; f2 = feat_buffer[(size_t)i * 3 + 2];
+      f0 = finitef(f0) ? fminf(fmaxf(f0, -100.f), 100.f) : 0.f;
+      f1 = finitef(f1) ? fminf(fmaxf(f1, -100.f), 100.f) : 0.f;
+      f2 = finitef(f2) ? fminf(fmaxf(f2, -100.f), 100.f) : 0.f;
+    }
+    p2[0] = cr; p2[1] = cg; p2[2] = cb; p2[3] = f0;
+    proj3[(size_t)i * 2] = f1; proj3[(size_t)i * 2 + 1] = f2;
   }
+}
+
+void orc_project(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int tiles_x, int tiles_y, float* proj0,
+                 float* proj1, float* proj2, float* proj3, uint32_t* tile_count, uint32_t* hit_info) {
+  orc_project_feat(m, cam, active_deg, tiles_x, tiles_y, proj0, proj1, proj2, proj3, tile_count, hit_info, 0, NULL);
 }
 
 /* ------------------------------------------------------------------------------------------------
@@ -456,9 +483,27 @@ static inline void acc_add(double* p, double v) {
   }
 }
 
+/* The hollow penalty of a fragment at depth z over a pixel's reference depth z_ref (splat_math.cuh:14-17),
+ * as the HIP kernels evaluate it: (z - (z_ref + margin)) times 1 / max(margin, 1e-4), clamped to [0, 1],
+ * 0 when not finite. */
+static float hollow_pen_of(float z, float z_ref, float margin) {
+  const float zm = z_ref + margin, inv = 1.f / fmaxf(margin, 1e-4f);
+  const float d = (z - zm) * inv;
+  return finitef(d) ? fminf(fmaxf(d, 0.f), 1.f) : 0.f;
+}
+
 void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], uint32_t* tile_ranges,
                     const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
                     float* out_rgba, float* out_T, uint32_t* last_idx) {
+  orc_raster_fwd_ext(W, H, tiles_x, tiles_y, bg, tile_ranges, vals_sorted, proj0, proj1, proj2, out_rgba, out_T, last_idx,
+                     NULL);
+}
+
+void orc_raster_fwd_ext(int W, int H, int tiles_x, int tiles_y, const float bg[3], uint32_t* tile_ranges,
+                        const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
+                        float* out_rgba, float* out_T, uint32_t* last_idx, const orc_ext_t* ext) {
+  const int feat = ext && ext->feat;
+  const float* hz = ext ? ext->hollow_z : NULL;
   uint64_t contrib = 0;
 #pragma omp parallel for num_threads(g_threads) schedule(dynamic, 16) reduction(+ : contrib)
   for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
@@ -469,7 +514,8 @@ void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], u
       int px = tx * RT_W + l % RT_W, py = ty * RT_W + l / RT_W;
       if (!(px < W && py < H)) continue;
       float pcx = px + 0.5f, pcy = py + 0.5f;
-      float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
+      float T = 1.f, r = 0.f, g = 0.f, b = 0.f, f0 = 0.f, f1 = 0.f, f2 = 0.f, pen = 0.f;
+      const float z_ref = hz ? hz[(size_t)py * W + px] : INFINITY;
       uint32_t last = rx;
       for (uint32_t idx = rx; idx < ry; idx++) {
         uint32_t gid = vals_sorted[idx];
@@ -483,6 +529,11 @@ void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], u
         float vis = alpha * T;
         const float* col = proj2 + (size_t)gid * 4;
         r += fmaxf(col[0], 0.f) * vis; g += fmaxf(col[1], 0.f) * vis; b += fmaxf(col[2], 0.f) * vis;
+        if (feat) {
+          const float* f12 = ext->proj3 + (size_t)gid * 2;
+          f0 += col[3] * vis; f1 += f12[0] * vis; f2 += f12[1] * vis;
+        }
+        if (hz) pen += vis * hollow_pen_of(c[2], z_ref, ext->hollow_margin);
         T = next_T;
         last = idx + 1;
         contrib++;
@@ -492,6 +543,8 @@ void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], u
       out_rgba[pix * 4 + 3] = 1.f - T;
       out_T[pix] = T;
       last_idx[pix] = last;
+      if (feat && ext->out_feat) { ext->out_feat[pix * 3] = f0; ext->out_feat[pix * 3 + 1] = f1; ext->out_feat[pix * 3 + 2] = f2; }
+      if (hz && ext->hollow_pen) ext->hollow_pen[pix] = pen;
       if (last > max_last) max_last = last;
     }
     tile_ranges[tile * 2 + 1] = max_last;
@@ -621,6 +674,20 @@ void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], c
                     const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
                     const float* out_rgba, const float* out_T, const uint32_t* last_idx, const float* v_out,
                     float inv_gscale, double* v_splat, uint32_t* vis_flag, double* vis_weight) {
+  orc_raster_bwd_ext(W, H, tiles_x, tiles_y, bg, tile_ranges, vals_sorted, proj0, proj1, proj2, out_rgba, out_T, last_idx,
+                     v_out, inv_gscale, v_splat, vis_flag, vis_weight, NULL);
+}
+
+/* raster_bwd.cu:37-139 with the feature lanes (FEAT: v_feat back through the composited features into
+ * v_splat[10..12] and into dL/dalpha) and the hollow penalty (HOLLOW: lam (T_before h - S_h / (1 - alpha))
+ * added to dL/dalpha, the refine statistic kept photometric). */
+void orc_raster_bwd_ext(int W, int H, int tiles_x, int tiles_y, const float bg[3], const uint32_t* tile_ranges,
+                        const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
+                        const float* out_rgba, const float* out_T, const uint32_t* last_idx, const float* v_out,
+                        float inv_gscale, double* v_splat, uint32_t* vis_flag, double* vis_weight, const orc_ext_t* ext) {
+  const int feat = ext && ext->feat;
+  const float* hz = ext ? ext->hollow_z : NULL;
+  const float lam = ext ? ext->hollow_lam : 0.f;
   const float Wf = (float)W, Hf = (float)H;
 #pragma omp parallel for num_threads(g_threads) schedule(dynamic, 16)
   for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
@@ -636,7 +703,9 @@ void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], c
       uint32_t last = last_idx[pix];
       const float* vo = v_out + pix * 4;
       float v_o_w = (vo[3] - (bg[0] * vo[0] + bg[1] * vo[1] + bg[2] * vo[2])) * T;
-      float Sx = 0.f, Sy = 0.f, Sz = 0.f;
+      float Sx = 0.f, Sy = 0.f, Sz = 0.f, Sf0 = 0.f, Sf1 = 0.f, Sf2 = 0.f, Sh = 0.f;
+      const float* vf = feat ? ext->v_feat + pix * 4 : NULL;
+      const float z_ref = hz ? hz[pix] : INFINITY;
       const float inv_final_a = 1.f / fmaxf(final_a, 1e-5f);
       for (uint32_t idx = ry; idx-- > rx;) {
         if (!(idx < last)) continue;
@@ -659,16 +728,30 @@ void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], c
         g[7] = col[2] >= 0.f ? vis * vo[2] : 0.f;
         float v_alpha = (T_before * cr - Sx * ra) * vo[0] + (T_before * cg - Sy * ra) * vo[1] +
                         (T_before * cb - Sz * ra) * vo[2] + v_o_w * ra;
+        float fx = 0.f, fy = 0.f, fz = 0.f, hh = 0.f;
+        if (feat) {
+          fx = col[3]; fy = ext->proj3[(size_t)gid * 2]; fz = ext->proj3[(size_t)gid * 2 + 1];
+          g[10] = vis * vf[0]; g[11] = vis * vf[1]; g[12] = vis * vf[2];
+          v_alpha += (T_before * fx - Sf0 * ra) * vf[0] + (T_before * fy - Sf1 * ra) * vf[1] + (T_before * fz - Sf2 * ra) * vf[2];
+        }
+        const float v_sigma_photo = -alpha * v_alpha;
+        if (hz) {
+          hh = hollow_pen_of(c[2], z_ref, ext->hollow_margin);
+          v_alpha += lam * (T_before * hh - Sh * ra);
+        }
         float v_sigma = -alpha * v_alpha;
         if (c[1] * gauss <= ALPHA_MAX) {
           g[2] = 0.5f * v_sigma * dx * dx; g[3] = v_sigma * dx * dy; g[4] = 0.5f * v_sigma * dy * dy;
           g[0] = -v_sigma * (a[2] * dx + a[3] * dy);
           g[1] = -v_sigma * (a[3] * dx + c[0] * dy);
           g[8] = v_alpha * gauss;
-          float len = sqrtf(g[0] * Wf * g[0] * Wf + g[1] * Hf * g[1] * Hf);
+          const float rx_ = -v_sigma_photo * (a[2] * dx + a[3] * dy), ry_ = -v_sigma_photo * (a[3] * dx + c[0] * dy);
+          float len = sqrtf(rx_ * Wf * rx_ * Wf + ry_ * Hf * ry_ * Hf);
           g[9] = len * inv_final_a;
         }
         Sx += cr * vis; Sy += cg * vis; Sz += cb * vis;
+        if (feat) { Sf0 += fx * vis; Sf1 += fy * vis; Sf2 += fz * vis; }
+        if (hz) Sh += hh * vis;
         T = T_before;
         vis_flag[gid] = 1u; /* every writer stores the same value */
         acc_add(&vis_weight[gid], (double)vis);
@@ -856,6 +939,19 @@ void orc_vjp(const orc_model_t* m, const orc_cam_t* cam, int active_deg, const f
     dmat3 GR;
     for (int r = 0; r < 3; r++)
       for (int j = 0; j < 3; j++) GR.m[3 * r + j] = GM.m[3 * r + j] * sc[j];
+    /* feature lanes (optim.cu:235-250): the pseudo-normal R_view (s u), u = c / |c| with c the column of
+     * R(q) along the smallest log scale and s the facing sign, so dL/dc = s (I - u u^T) R_view^T g_f / |c| */
+    if (g[10] != 0.0 || g[11] != 0.0 || g[12] != 0.0) {
+      const int ax = (ls[0] <= ls[1] && ls[0] <= ls[2]) ? 0 : (ls[1] <= ls[2] ? 1 : 2);
+      const double cv[3] = {Rq.m[ax], Rq.m[3 + ax], Rq.m[6 + ax]};
+      const double cl = fmax(sqrt(cv[0] * cv[0] + cv[1] * cv[1] + cv[2] * cv[2]), 1e-12);
+      const double u[3] = {cv[0] / cl, cv[1] / cl, cv[2] / cl};
+      const double face = -(dv[0] * u[0] + dv[1] * u[1] + dv[2] * u[2]) >= 0.0 ? 1.0 : -1.0;
+      double bu[3];
+      for (int r = 0; r < 3; r++) bu[r] = face * (RvT.m[3 * r] * g[10] + RvT.m[3 * r + 1] * g[11] + RvT.m[3 * r + 2] * g[12]);
+      const double along = u[0] * bu[0] + u[1] * bu[1] + u[2] * bu[2];
+      for (int r = 0; r < 3; r++) GR.m[3 * r + ax] += (bu[r] - u[r] * along) / cl;
+    }
     /* quaternion: entrywise derivatives of R(q) (optim.cu:24-33), then through q / |q| (optim.cu:10-21) */
     const double w = qn[0], x = qn[1], y = qn[2], zq = qn[3];
     const double* G = GR.m;
@@ -900,7 +996,7 @@ static void sh_basis_d(int deg, double x, double y, double z, double* b) { /* re
   }
 }
 
-typedef struct { int ok; double mx, my, c00, c01, c11, opac, depth, r, g, b; } dproj_t;
+typedef struct { int ok; double mx, my, c00, c01, c11, opac, depth, r, g, b, f[3]; } dproj_t;
 
 static const dproj_t* g_sort_pr;
 static int depth_cmp(const void* a, const void* b) {
@@ -913,11 +1009,13 @@ static int depth_cmp(const void* a, const void* b) {
 /* Rows [y0, y1) of the brute-force render (reference.cpp:84-104): every depth-sorted projected splat is
  * tested at every pixel; with stride > 1 only the pixels whose row-major index is a multiple of it. */
 static void ref_composite(const dproj_t* pr, const int* order, int no, int W, int y0, int y1, const double bg[3],
-                          double* imgd, size_t stride) {
+                          double* imgd, size_t stride, double* featd, const float* hollow_z, double hollow_margin,
+                          double* hollow_sum) {
   for (int py = y0; py < y1; py++)
     for (int px = 0; px < W; px++) {
       if (stride > 1 && ((size_t)py * W + px) % stride) continue;
-      double T = 1, r = 0, g = 0, b = 0, pcx = px + 0.5, pcy = py + 0.5;
+      double T = 1, r = 0, g = 0, b = 0, pcx = px + 0.5, pcy = py + 0.5, f0 = 0, f1 = 0, f2 = 0;
+      const double zr = hollow_z ? (double)hollow_z[(size_t)py * W + px] : 0.0;
       for (int oi = 0; oi < no; oi++) {
         const dproj_t* q = &pr[order[oi]];
         double dx = pcx - q->mx, dy = pcy - q->my;
@@ -928,10 +1026,16 @@ static void ref_composite(const dproj_t* pr, const int* order, int no, int W, in
         if (nT <= 1e-4) break;
         double vis = alpha * T;
         r += fmax(q->r, 0.0) * vis; g += fmax(q->g, 0.0) * vis; b += fmax(q->b, 0.0) * vis;
+        f0 += q->f[0] * vis; f1 += q->f[1] * vis; f2 += q->f[2] * vis;
+        if (hollow_z) { /* reference.cpp:100 */
+          const double d = (q->depth - zr - hollow_margin) / fmax(hollow_margin, 1e-4);
+          if (isfinite(d)) *hollow_sum += vis * fmin(fmax(d, 0.0), 1.0);
+        }
         T = nT;
       }
       size_t o = (size_t)py * W + px;
       imgd[o * 4] = r + T * bg[0]; imgd[o * 4 + 1] = g + T * bg[1]; imgd[o * 4 + 2] = b + T * bg[2]; imgd[o * 4 + 3] = 1 - T;
+      if (featd) { featd[o * 3] = f0; featd[o * 3 + 1] = f1; featd[o * 3 + 2] = f2; }
     }
 }
 
@@ -947,6 +1051,17 @@ double orc_ref_loss(int n, int degree, const double* pos, const double* log_scal
                     const double* sh, const double* floor_, const orc_cam_t* cam, int W, int H, const double bg[3],
                     const uint32_t* gt, const uint8_t* weights, int composite, int mask, int alpha_lane, double l1_w,
                     double ssim_w, double match_alpha_weight, double scale, int float_exp, double* out_img) {
+  return orc_ref_loss_ext(n, degree, pos, log_scale, quat, opacity, sh, floor_, cam, W, H, bg, gt, weights, composite, mask,
+                          alpha_lane, l1_w, ssim_w, match_alpha_weight, scale, float_exp, out_img, NULL);
+}
+
+double orc_ref_loss_ext(int n, int degree, const double* pos, const double* log_scale, const double* quat,
+                        const double* opacity, const double* sh, const double* floor_, const orc_cam_t* cam, int W, int H,
+                        const double bg[3], const uint32_t* gt, const uint8_t* weights, int composite, int mask,
+                        int alpha_lane, double l1_w, double ssim_w, double match_alpha_weight, double scale, int float_exp,
+                        double* out_img, const orc_ref_ext_t* rx) {
+  const int normals = rx && rx->normals;
+  const float* hollow_z = rx ? rx->hollow_z : NULL;
   double R[9];
   for (int i = 0; i < 9; i++) R[i] = cam->R[i];
   const double fx = cam->fx, fy = cam->fy, cx = cam->cx, cy = cam->cy;
@@ -1010,6 +1125,16 @@ double orc_ref_loss(int n, int degree, const double* pos, const double* log_scal
     q.r = fmin(fmax(col[0] + 0.5, -100.0), 100.0);
     q.g = fmin(fmax(col[1] + 0.5, -100.0), 100.0);
     q.b = fmin(fmax(col[2] + 0.5, -100.0), 100.0);
+    q.f[0] = q.f[1] = q.f[2] = 0.0;
+    if (normals) { /* reference.cpp:75-83: the camera-facing shortest local axis in camera space */
+      const double* l = log_scale + (size_t)i * 3;
+      const int ax = (l[0] <= l[1] && l[0] <= l[2]) ? 0 : (l[1] <= l[2] ? 1 : 2);
+      const double a[3] = {Rq[ax], Rq[3 + ax], Rq[6 + ax]};
+      const double al = sqrt(a[0] * a[0] + a[1] * a[1] + a[2] * a[2]);
+      const double u[3] = {a[0] / al, a[1] / al, a[2] / al};
+      const double face = ((cam->pos[0] - mean[0]) * u[0] + (cam->pos[1] - mean[1]) * u[1] + (cam->pos[2] - mean[2]) * u[2]) >= 0 ? 1.0 : -1.0;
+      for (int r = 0; r < 3; r++) q.f[r] = R[r * 3] * u[0] * face + R[r * 3 + 1] * u[1] * face + R[r * 3 + 2] * u[2] * face;
+    }
     q.ok = 1;
     pr[i] = q;
   }
@@ -1024,14 +1149,16 @@ double orc_ref_loss(int n, int degree, const double* pos, const double* log_scal
   if (g_ref_stride > 1) { /* bounded sample: every g_ref_stride-th pixel, then no loss */
     struct timespec t0, t1;
     clock_gettime(CLOCK_MONOTONIC, &t0);
-    ref_composite(pr, order, no, W, 0, H, bg, imgd, g_ref_stride);
+    ref_composite(pr, order, no, W, 0, H, bg, imgd, g_ref_stride, NULL, NULL, 0.0, NULL);
     clock_gettime(CLOCK_MONOTONIC, &t1);
     g_ref_composite_s = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
     if (out_img) memcpy(out_img, imgd, sizeof(double) * P * 4);
     free(img); free(imgd); free(order); free(pr);
     return 0.0;
   }
-  ref_composite(pr, order, no, W, 0, H, bg, imgd, 1);
+  double* featd = normals ? (double*)malloc(sizeof(double) * P * 3) : NULL;
+  double hollow_sum = 0.0;
+  ref_composite(pr, order, no, W, 0, H, bg, imgd, 1, featd, hollow_z, rx ? rx->hollow_margin : 0.0, &hollow_sum);
   if (out_img) memcpy(out_img, imgd, sizeof(double) * P * 4);
   /* loss in double over the double image (reference.cpp:105-131) */
   double w[11];
@@ -1064,8 +1191,119 @@ double orc_ref_loss(int n, int degree, const double* pos, const double* log_scal
       double wp = weights ? weights[i] / 255.0 : 1.0;
       loss += wp * match_alpha_weight * scale / (double)(W * H) * fabs(imgd[i * 4 + 3] - gtc_div(gt[i], 3));
     }
+  if (normals && rx->normal_scale > 0)
+    for (size_t i = 0; i < P; i++) { /* reference.cpp:134-141 */
+      const uint32_t g = rx->gtn[i];
+      if (((g >> 24) & 0xffu) <= 127u) continue;
+      const double wp = weights ? weights[i] / 255.0 : 1.0;
+      const double gx = (g & 0xffu) * (2.0 / 255.0) - 1, gy = 1 - ((g >> 8) & 0xffu) * (2.0 / 255.0), gz = 1 - ((g >> 16) & 0xffu) * (2.0 / 255.0);
+      const double px = featd[i * 3], py = featd[i * 3 + 1], pz = featd[i * 3 + 2];
+      const double pl = fmax(sqrt(px * px + py * py + pz * pz), 1e-6), gl = fmax(sqrt(gx * gx + gy * gy + gz * gz), 1e-6);
+      loss += rx->normal_scale * wp * (fabs(px - gx) + fabs(py - gy) + fabs(pz - gz) + 1 - (px * gx + py * gy + pz * gz) / (pl * gl));
+    }
+  if (hollow_z) loss += rx->hollow_lam * hollow_sum;
+  free(featd);
   free(X); free(img); free(imgd); free(order); free(pr);
   return loss;
+}
+
+/* ------------------------------------------------------------------------------------------------
+ * The other losses (loss.cu:197-293), per pixel in single precision exactly as the HIP kernels evaluate
+ * them (the per-pixel outputs bit for bit), the sums in double.
+ * ---------------------------------------------------------------------------------------------- */
+double orc_normal_loss(int W, int H, const float* feat, const uint32_t* normals, const uint8_t* weights, float scale,
+                       float grad_scale, float* v_feat) {
+  double loss = 0.0;
+  for (size_t pix = 0; pix < (size_t)W * H; pix++) {
+    const uint32_t nm = normals[pix];
+    float* out = v_feat + pix * 4;
+    out[0] = out[1] = out[2] = out[3] = 0.f;
+    if (((nm >> 24) & 0xffu) <= 127u) continue;
+    const float wp = weights ? (float)weights[pix] * (1.f / 255.f) : 1.f;
+    const float k = scale * wp;
+    const float nx = (float)(nm & 0xffu) * (2.f / 255.f) - 1.f;
+    const float ny = 1.f - (float)((nm >> 8) & 0xffu) * (2.f / 255.f);
+    const float nz = 1.f - (float)((nm >> 16) & 0xffu) * (2.f / 255.f);
+    const float* f = feat + pix * 4;
+    const float pl = fmaxf(sqrtf((f[0] * f[0] + f[1] * f[1]) + f[2] * f[2]), 1e-6f);
+    const float nl = fmaxf(sqrtf((nx * nx + ny * ny) + nz * nz), 1e-6f);
+    const float dot = (f[0] * nx + f[1] * ny) + f[2] * nz;
+    const float plnl = pl * nl;
+    const float dx = f[0] - nx, dy = f[1] - ny, dz = f[2] - nz;
+    loss += (double)(k * ((((fabsf(dx) + fabsf(dy)) + fabsf(dz)) + 1.f) - dot / plnl));
+    const float inv = 1.f / plnl, radial = dot / ((pl * pl) * plnl);
+    const float kg = k * grad_scale;
+    const float sx = dx > 0.f ? 1.f : (dx < 0.f ? -1.f : 0.f);
+    const float sy = dy > 0.f ? 1.f : (dy < 0.f ? -1.f : 0.f);
+    const float sz = dz > 0.f ? 1.f : (dz < 0.f ? -1.f : 0.f);
+    out[0] = kg * ((sx - nx * inv) + f[0] * radial);
+    out[1] = kg * ((sy - ny * inv) + f[1] * radial);
+    out[2] = kg * ((sz - nz * inv) + f[2] * radial);
+  }
+  return loss;
+}
+
+double orc_hollow_sum(int npix, const float* pen) {
+  double s = 0.0;
+  for (int i = 0; i < npix; i++) s += (double)pen[i];
+  return s;
+}
+
+/* loss.cu:240-286: 8-bit prediction (clamped to [0, 1], rounded half to even), per channel and pixel the
+ * squared error and the clamped SSIM of the 11-tap window (zero padding), alpha-weighted when
+ * mask_weighted; the horizontal then vertical passes in the kernel's float order. */
+void orc_eval(int W, int H, const float* pred, const uint32_t* gt, int mask_weighted, double* sum_se, double* sum_ssim) {
+  double wd[11];
+  gauss11(wd);
+  float w[11];
+  for (int d = 0; d < 11; d++) w[d] = (float)wd[d];
+  const size_t P = (size_t)W * H;
+  float* p = (float*)malloc(sizeof(float) * P);
+  float* g = (float*)malloc(sizeof(float) * P);
+  float* hs = (float*)malloc(sizeof(float) * P * 5);
+  double se_t = 0.0, ss_t = 0.0;
+  for (int c = 0; c < 3; c++) {
+    for (size_t i = 0; i < P; i++) {
+      const float pc = pred[i * 4 + c];
+      p[i] = rintf(fminf(fmaxf(pc, 0.f), 1.f) * 255.f) / 255.f;
+      g[i] = gt_chan_f(gt[i], c);
+    }
+    for (int y = 0; y < H; y++)
+      for (int x = 0; x < W; x++) {
+        float sx = 0.f, sxx = 0.f, sy = 0.f, syy = 0.f, sxy = 0.f;
+        for (int d = 0; d < 11; d++) {
+          const int xx = x - 5 + d;
+          const float xv = (xx >= 0 && xx < W) ? p[(size_t)y * W + xx] : 0.f;
+          const float yv = (xx >= 0 && xx < W) ? g[(size_t)y * W + xx] : 0.f;
+          sx = sx + w[d] * xv; sxx = sxx + (w[d] * xv) * xv; sy = sy + w[d] * yv; syy = syy + (w[d] * yv) * yv;
+          sxy = sxy + (w[d] * xv) * yv;
+        }
+        float* h = hs + ((size_t)y * W + x) * 5;
+        h[0] = sx; h[1] = sxx; h[2] = sy; h[3] = syy; h[4] = sxy;
+      }
+    for (int y = 0; y < H; y++)
+      for (int x = 0; x < W; x++) {
+        float st[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int d = 0; d < 11; d++) {
+          const int yy = y - 5 + d;
+          for (int k = 0; k < 5; k++) st[k] = st[k] + w[d] * ((yy >= 0 && yy < H) ? hs[((size_t)yy * W + x) * 5 + k] : 0.f);
+        }
+        const float mu1 = st[0], mu2 = st[2];
+        const float s1 = fmaxf(0.f, st[1] - mu1 * mu1), s2 = fmaxf(0.f, st[3] - mu2 * mu2), s12 = st[4] - mu1 * mu2;
+        const float C1 = 0.01f * 0.01f, C2 = 0.03f * 0.03f; /* as the kernels form them */
+        const float num = ((2.f * mu1) * mu2 + C1) * (2.f * s12 + C2);
+        const float den = ((mu1 * mu1 + mu2 * mu2) + C1) * ((s1 + s2) + C2);
+        const float ssim = fminf(fmaxf(num / den, -1.f), 1.f);
+        const size_t i = (size_t)y * W + x;
+        const float d = fabsf(p[i] - g[i]);
+        const float m = mask_weighted ? gt_chan_f(gt[i], 3) : 1.f;
+        se_t += (double)((d * m) * (d * m));
+        ss_t += (double)(ssim * m);
+      }
+  }
+  *sum_se = se_t;
+  *sum_ssim = ss_t;
+  free(p); free(g); free(hs);
 }
 
 /* ------------------------------------------------------------------------------------------------

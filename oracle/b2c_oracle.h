@@ -57,6 +57,27 @@ typedef struct {
 float orc_expf(float x);
 float orc_logf(float x);
 
+/* Feature lanes and hollow loss of the tiled path (render.h:33-63): feat composites / back-propagates the
+ * features in proj2.w and proj3; hollow_z (per pixel, +inf = no surface) adds the hollow penalty. */
+typedef struct {
+  int feat;
+  const float* proj3;     /* [n][2] */
+  const float* hollow_z;  /* [P] or NULL */
+  float hollow_margin, hollow_lam;
+  float* out_feat;        /* forward: [P][3] or NULL */
+  float* hollow_pen;      /* forward: [P] or NULL */
+  const float* v_feat;    /* backward: [P][4] */
+} orc_ext_t;
+
+/* The fp64 brute force's normals and hollow terms (tests/reference.h:8-16). */
+typedef struct {
+  int normals;
+  const uint32_t* gtn;    /* [P] packed normal map */
+  double normal_scale;
+  const float* hollow_z;  /* [P] or NULL */
+  double hollow_lam, hollow_margin;
+} orc_ref_ext_t;
+
 /* ---- fp32 tiled path ---- */
 
 /* RenderCtx::setup tile geometry (src/gpu/render.cu:5-8). */
@@ -67,6 +88,11 @@ int orc_tile_bits(int n_tiles);
 void orc_project(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int tiles_x, int tiles_y,
                  float* proj0, float* proj1, float* proj2, float* proj3,
                  uint32_t* tile_count, uint32_t* hit_info /* [n][2] */);
+
+/* The same with the feature lanes (feat_mode 1: pseudo-normals, 2: feat_buffer [n][3], project.cu:63-77). */
+void orc_project_feat(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int tiles_x, int tiles_y,
+                      float* proj0, float* proj1, float* proj2, float* proj3, uint32_t* tile_count, uint32_t* hit_info,
+                      int feat_mode, const float* feat_buffer);
 
 /* binning.cu:109-143: depth sort (stable on z bits, culled last), count scan in depth order, emit
  * in depth order, stable sort by tile id, per-tile ranges. Returns M (number of intersections).
@@ -82,6 +108,10 @@ void orc_raster_fwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], u
                     const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
                     float* out_rgba, float* out_T, uint32_t* last_idx);
 
+void orc_raster_fwd_ext(int W, int H, int tiles_x, int tiles_y, const float bg[3], uint32_t* tile_ranges,
+                        const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
+                        float* out_rgba, float* out_T, uint32_t* last_idx, const orc_ext_t* ext);
+
 /* loss.cu:18-195 restated over the whole image in double precision (zero padding, 11-tap
  * Gaussian sigma 1.5 normalised, loss.cu:296-303). pred is [P][4] float (rgb + alpha), gt packed
  * RGBA8, weights u8 or NULL. Returns the loss value; writes v_out [P][4] (scaled by grad_scale)
@@ -96,6 +126,19 @@ void orc_raster_bwd(int W, int H, int tiles_x, int tiles_y, const float bg[3], c
                     const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
                     const float* out_rgba, const float* out_T, const uint32_t* last_idx, const float* v_out,
                     float inv_gscale, double* v_splat, uint32_t* vis_flag, double* vis_weight);
+
+void orc_raster_bwd_ext(int W, int H, int tiles_x, int tiles_y, const float bg[3], const uint32_t* tile_ranges,
+                        const uint32_t* vals_sorted, const float* proj0, const float* proj1, const float* proj2,
+                        const float* out_rgba, const float* out_T, const uint32_t* last_idx, const float* v_out,
+                        float inv_gscale, double* v_splat, uint32_t* vis_flag, double* vis_weight, const orc_ext_t* ext);
+
+/* loss.cu:206-238: returns the normal loss, writes v_feat [P][4]. */
+double orc_normal_loss(int W, int H, const float* feat, const uint32_t* normals, const uint8_t* weights, float scale,
+                       float grad_scale, float* v_feat);
+/* loss.cu:197-204 without lam: the sum of the per-pixel penalties. */
+double orc_hollow_sum(int npix, const float* pen);
+/* loss.cu:240-286: sums of the squared error and of SSIM over pixels and channels. */
+void orc_eval(int W, int H, const float* pred, const uint32_t* gt, int mask_weighted, double* sum_se, double* sum_ssim);
 
 /* optim.cu:99-253 + grad_out (292-296): projection VJP, fp32. grad_out [n][11 + 3K]. */
 void orc_vjp(const orc_model_t* m, const orc_cam_t* cam, int active_deg, const float* v_splat,
@@ -114,6 +157,12 @@ double orc_ref_loss(int n, int degree, const double* pos, const double* log_scal
                     int W, int H, const double bg[3], const uint32_t* gt, const uint8_t* weights,
                     int composite, int mask, int alpha_lane, double l1_w, double ssim_w,
                     double match_alpha_weight, double scale, int float_exp, double* out_img);
+
+double orc_ref_loss_ext(int n, int degree, const double* pos, const double* log_scale, const double* quat,
+                        const double* opacity, const double* sh, const double* floor_, const orc_cam_t* cam, int W, int H,
+                        const double bg[3], const uint32_t* gt, const uint8_t* weights, int composite, int mask,
+                        int alpha_lane, double l1_w, double ssim_w, double match_alpha_weight, double scale, int float_exp,
+                        double* out_img, const orc_ref_ext_t* rx);
 
 /* Bounded sample for the CPU baseline: after orc_ref_set_sample(s) with s > 1, orc_ref_loss renders only the
  * pixels whose row-major index is a multiple of s, skips the loss (returns 0) and records the compositing

@@ -37,6 +37,16 @@ class OrcLoss(C.Structure):
                 ("scale", C.c_float), ("grad_scale", C.c_float)]
 
 
+class OrcExt(C.Structure):
+    _fields_ = [("feat", C.c_int), ("proj3", C.c_void_p), ("hollow_z", C.c_void_p), ("hollow_margin", C.c_float),
+                ("hollow_lam", C.c_float), ("out_feat", C.c_void_p), ("hollow_pen", C.c_void_p), ("v_feat", C.c_void_p)]
+
+
+class OrcRefExt(C.Structure):
+    _fields_ = [("normals", C.c_int), ("gtn", C.c_void_p), ("normal_scale", C.c_double), ("hollow_z", C.c_void_p),
+                ("hollow_lam", C.c_double), ("hollow_margin", C.c_double)]
+
+
 class OrcAdamStep(C.Structure):
     _fields_ = [("t", C.c_int), ("sparse", C.c_int), ("beta1", C.c_float), ("beta2", C.c_float), ("eps", C.c_float),
                 ("bc1", C.c_float), ("bc2", C.c_float), ("ln_beta1", C.c_float), ("ln_beta2", C.c_float),
@@ -107,6 +117,23 @@ def lib():
         _lib.orc_frag_sigma.argtypes = [C.c_int] + [p] * 6
         _lib.orc_set_threads.restype = None
         _lib.orc_set_threads.argtypes = [C.c_int]
+        _lib.orc_project_feat.restype = None
+        _lib.orc_project_feat.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcCam), C.c_int, C.c_int, C.c_int] + [p] * 6 + [
+            C.c_int, p]
+        _lib.orc_raster_fwd_ext.restype = None
+        _lib.orc_raster_fwd_ext.argtypes = [C.c_int] * 4 + [p] * 9 + [C.POINTER(OrcExt)]
+        _lib.orc_raster_bwd_ext.restype = None
+        _lib.orc_raster_bwd_ext.argtypes = [C.c_int] * 4 + [p] * 10 + [f, p, p, p, C.POINTER(OrcExt)]
+        _lib.orc_normal_loss.restype = C.c_double
+        _lib.orc_normal_loss.argtypes = [C.c_int, C.c_int, p, p, p, f, f, p]
+        _lib.orc_hollow_sum.restype = C.c_double
+        _lib.orc_hollow_sum.argtypes = [C.c_int, p]
+        _lib.orc_eval.restype = None
+        _lib.orc_eval.argtypes = [C.c_int, C.c_int, p, p, C.c_int, p, p]
+        _lib.orc_ref_loss_ext.restype = C.c_double
+        _lib.orc_ref_loss_ext.argtypes = [C.c_int, C.c_int] + [p] * 6 + [C.POINTER(OrcCam), C.c_int, C.c_int, p, p, p,
+                                                                        C.c_int, C.c_int, C.c_int] + [C.c_double] * 4 + [
+                                                                        C.c_int, p, C.POINTER(OrcRefExt)]
         _lib.orc_project_ok.restype = C.c_int
         _lib.orc_project_ok.argtypes = [p, p, p, C.POINTER(OrcCam)]
         _lib.orc_adam_constants.restype = None
@@ -163,6 +190,9 @@ def ref_lib():
         _ref.ref_reference_loss.restype = C.c_double
         _ref.ref_reference_loss.argtypes = [C.c_int, C.c_int] + [p] * 5 + [C.c_int, C.c_int, p, p] + [C.c_float] * 4 + [
             p, p, p, C.c_int, C.c_int, C.c_int] + [C.c_double] * 4
+        _ref.ref_reference_loss_ext.restype = C.c_double
+        _ref.ref_reference_loss_ext.argtypes = _ref.ref_reference_loss.argtypes + [p, C.c_double, p, C.c_double,
+                                                                                   C.c_double]
     return _ref
 
 
@@ -223,7 +253,7 @@ def tile_geometry(W, H):
 
 
 def project(scene, camd, active_deg=None):
-    from b2ctrain_amd.scenes import camera_gpu  # noqa: F401 (camd built by the caller)
+    """Projection with the scene's feature mode (scene.feat_mode / feat_buffer)."""
     n = scene.n
     tx, ty, _, _ = tile_geometry(camd["W"], camd["H"])
     out = dict(proj0=np.zeros((n, 4), np.float32), proj1=np.zeros((n, 4), np.float32),
@@ -231,9 +261,21 @@ def project(scene, camd, active_deg=None):
                tile_count=np.zeros(n, np.uint32), hit_info=np.zeros((n, 2), np.uint32))
     m = _Model(scene)
     cam = make_cam(camd)
-    lib().orc_project(C.byref(m.m), C.byref(cam), scene.degree if active_deg is None else active_deg, tx, ty,
-                      *[_ptr(out[k]) for k in ("proj0", "proj1", "proj2", "proj3", "tile_count", "hit_info")])
+    fb = None if scene.feat_buffer is None else _in(scene.feat_buffer, np.float32)
+    lib().orc_project_feat(C.byref(m.m), C.byref(cam), scene.degree if active_deg is None else active_deg, tx, ty,
+                           *[_ptr(out[k]) for k in ("proj0", "proj1", "proj2", "proj3", "tile_count", "hit_info")],
+                           int(scene.feat_mode), _ptr(fb))
     return out
+
+
+def _ext(feat=False, proj3=None, hollow_z=None, margin=0.05, lam=0.0, out_feat=None, hollow_pen=None, v_feat=None):
+    e = OrcExt()
+    e.feat = int(feat)
+    e.proj3 = _ptr(proj3)
+    e.hollow_z = _ptr(hollow_z)
+    e.hollow_margin, e.hollow_lam = margin, lam
+    e.out_feat, e.hollow_pen, e.v_feat = _ptr(out_feat), _ptr(hollow_pen), _ptr(v_feat)
+    return e
 
 
 def bin_(pr, W, H):
@@ -249,14 +291,19 @@ def bin_(pr, W, H):
     return out
 
 
-def raster_fwd(pr, bn, W, H, bg):
+def raster_fwd(pr, bn, W, H, bg, feat=False, hollow_z=None, hollow_margin=0.05):
+    """Forward compositing; with feat also out_feat [P][3], with hollow_z the per-pixel hollow_pen [P]."""
     tx, ty, T, _ = tile_geometry(W, H)
     P = W * H
     ranges = bn["tile_ranges"].copy()
-    out = dict(out_rgba=np.zeros((P, 4), np.float32), out_T=np.zeros(P, np.float32), last_idx=np.zeros(P, np.uint32))
+    out = dict(out_rgba=np.zeros((P, 4), np.float32), out_T=np.zeros(P, np.float32), last_idx=np.zeros(P, np.uint32),
+               out_feat=np.zeros((P, 3), np.float32), hollow_pen=np.zeros(P, np.float32))
     bgv = np.asarray(bg, np.float32)
-    lib().orc_raster_fwd(W, H, tx, ty, _ptr(bgv), _ptr(ranges), _ptr(bn["vals_sorted"]), _ptr(pr["proj0"]),
-                         _ptr(pr["proj1"]), _ptr(pr["proj2"]), *[_ptr(out[k]) for k in ("out_rgba", "out_T", "last_idx")])
+    hz = None if hollow_z is None else _in(hollow_z, np.float32)
+    ext = _ext(feat, _in(pr["proj3"], np.float32), hz, hollow_margin, 0.0, out["out_feat"], out["hollow_pen"])
+    lib().orc_raster_fwd_ext(W, H, tx, ty, _ptr(bgv), _ptr(ranges), _ptr(bn["vals_sorted"]), _ptr(pr["proj0"]),
+                             _ptr(pr["proj1"]), _ptr(pr["proj2"]),
+                             *[_ptr(out[k]) for k in ("out_rgba", "out_T", "last_idx")], C.byref(ext))
     out["tile_ranges"] = ranges
     out["f_contrib"] = int(lib().orc_last_fwd_contrib())
     return out
@@ -271,18 +318,47 @@ def photometric(scene, pred, grad_scale=1.0, bg=None, want_grad=True):
     return loss, v_out
 
 
-def raster_bwd(pr, bn, fw, v_out, W, H, bg, n, inv_gscale=1.0):
+def raster_bwd(pr, bn, fw, v_out, W, H, bg, n, inv_gscale=1.0, v_feat=None, hollow_z=None, hollow_margin=0.05,
+               hollow_lam=0.0):
+    """Backward; v_feat [P][4] turns the feature lanes on, hollow_z the hollow term (lam in v_out's units)."""
     tx, ty, T, _ = tile_geometry(W, H)
     v_splat = np.zeros((n, GRAD_LANES), np.float64)
     vis_flag = np.zeros(n, np.uint32)
     vis_weight = np.zeros(n, np.float64)
     bgv = np.asarray(bg, np.float32)
     u32, f32 = np.uint32, np.float32
-    lib().orc_raster_bwd(W, H, tx, ty, _ptr(bgv), _ptr(_in(fw["tile_ranges"], u32)), _ptr(_in(bn["vals_sorted"], u32)),
-                         _ptr(_in(pr["proj0"], f32)), _ptr(_in(pr["proj1"], f32)), _ptr(_in(pr["proj2"], f32)),
-                         _ptr(_in(fw["out_rgba"], f32)), _ptr(_in(fw["out_T"], f32)), _ptr(_in(fw["last_idx"], u32)),
-                         _ptr(_in(v_out, f32)), inv_gscale, _ptr(v_splat), _ptr(vis_flag), _ptr(vis_weight))
+    vf = None if v_feat is None else _in(v_feat, f32)
+    hz = None if hollow_z is None else _in(hollow_z, f32)
+    ext = _ext(vf is not None, _in(pr["proj3"], f32), hz, hollow_margin, hollow_lam, v_feat=vf)
+    lib().orc_raster_bwd_ext(W, H, tx, ty, _ptr(bgv), _ptr(_in(fw["tile_ranges"], u32)),
+                             _ptr(_in(bn["vals_sorted"], u32)), _ptr(_in(pr["proj0"], f32)), _ptr(_in(pr["proj1"], f32)),
+                             _ptr(_in(pr["proj2"], f32)), _ptr(_in(fw["out_rgba"], f32)), _ptr(_in(fw["out_T"], f32)),
+                             _ptr(_in(fw["last_idx"], u32)), _ptr(_in(v_out, f32)), inv_gscale, _ptr(v_splat),
+                             _ptr(vis_flag), _ptr(vis_weight), C.byref(ext))
     return v_splat, vis_flag, vis_weight
+
+
+def normal_loss(W, H, feat4, normals, weights, scale, grad_scale=1.0):
+    """(loss, v_feat [P][4]) of loss.cu:206-238; feat4 is out_feat [P][4] (or [P][3])."""
+    f = np.zeros((W * H, 4), np.float32)
+    f[:, :3] = np.asarray(feat4, np.float32).reshape(W * H, -1)[:, :3]
+    v = np.zeros((W * H, 4), np.float32)
+    w = None if weights is None else _in(weights, np.uint8)
+    loss = lib().orc_normal_loss(W, H, _ptr(f), _ptr(_in(normals, np.uint32)), _ptr(w), scale, grad_scale, _ptr(v))
+    return loss, v
+
+
+def hollow_sum(pen):
+    p = _in(pen, np.float32).reshape(-1)
+    return lib().orc_hollow_sum(p.size, _ptr(p))
+
+
+def eval_metrics(W, H, pred, gt, mask_weighted=False):
+    """(sum of squared errors, sum of SSIM) over pixels and channels of loss.cu:240-286."""
+    se, ss = C.c_double(0), C.c_double(0)
+    lib().orc_eval(W, H, _ptr(_in(pred, np.float32)), _ptr(_in(gt, np.uint32)), int(mask_weighted), C.byref(se),
+                   C.byref(ss))
+    return se.value, ss.value
 
 
 def vjp(scene, camd, v_splat, vis_flag, tile_count, active_deg=None):
@@ -305,11 +381,24 @@ def pipeline(scene, camd=None, bg=None, grad_scale=1.0):
     W, H = camd["W"], camd["H"]
     pr = project(scene, camd)
     bn = bin_(pr, W, H)
-    fw = raster_fwd(pr, bn, W, H, bg)
+    feat = scene.feat_mode != 0
+    fw = raster_fwd(pr, bn, W, H, bg, feat=feat, hollow_z=scene.hollow_z, hollow_margin=scene.hollow_margin)
     loss, v_out = photometric(scene, fw["out_rgba"], grad_scale=grad_scale, bg=bg)
-    v_splat, vis_flag, vis_weight = raster_bwd(pr, bn, fw, v_out, W, H, bg, scene.n, inv_gscale=1.0 / grad_scale)
+    v_feat = None
+    if feat:
+        nloss, v_feat = (0.0, np.zeros((W * H, 4), np.float32))
+        if scene.normals is not None and scene.normal_scale > 0:
+            nloss, v_feat = normal_loss(W, H, fw["out_feat"], scene.normals, scene.weights, scene.normal_scale,
+                                        grad_scale)
+        loss += nloss
+    if scene.hollow_z is not None:
+        loss += scene.hollow_lam * hollow_sum(fw["hollow_pen"])
+    v_splat, vis_flag, vis_weight = raster_bwd(pr, bn, fw, v_out, W, H, bg, scene.n, inv_gscale=1.0 / grad_scale,
+                                               v_feat=v_feat, hollow_z=scene.hollow_z,
+                                               hollow_margin=scene.hollow_margin,
+                                               hollow_lam=scene.hollow_lam * grad_scale)
     grads = vjp(scene, camd, v_splat, vis_flag, pr["tile_count"])
-    return dict(proj=pr, bin=bn, fwd=fw, loss=loss, v_out=v_out, v_splat=v_splat, vis_flag=vis_flag,
+    return dict(proj=pr, bin=bn, fwd=fw, loss=loss, v_out=v_out, v_feat=v_feat, v_splat=v_splat, vis_flag=vis_flag,
                 vis_weight=vis_weight, grads=grads)
 
 
@@ -329,10 +418,17 @@ def ref_loss(scene, params=None, camd=None, bg=None, want_img=False, floor=None,
     if floor is None and scene.lscale[:, 3].any():  # the scene's own Mip-Splatting floor
         floor = scene.lscale[:, 3]
     fl = None if floor is None else np.ascontiguousarray(floor, np.float64)
-    loss = lib().orc_ref_loss(scene.n, scene.degree, *[_ptr(a) for a in arrs], _ptr(fl), C.byref(cam), scene.W,
-                              scene.H, _ptr(bg), _ptr(np.ascontiguousarray(scene.gt, np.uint32)), _ptr(scene.weights),
-                              int(scene.composite), int(scene.mask), int(scene.alpha_lane), scene.l1_w, scene.ssim_w,
-                              scene.match_alpha_weight, scene.scale, int(float_exp), _ptr(img))
+    rx = OrcRefExt()
+    gtn = None if scene.normals is None else _in(scene.normals, np.uint32)
+    hz = None if scene.hollow_z is None else _in(scene.hollow_z, np.float32)
+    rx.normals = int(scene.feat_mode == 1 and gtn is not None)
+    rx.gtn, rx.normal_scale = _ptr(gtn), scene.normal_scale
+    rx.hollow_z, rx.hollow_lam, rx.hollow_margin = _ptr(hz), scene.hollow_lam, scene.hollow_margin
+    loss = lib().orc_ref_loss_ext(scene.n, scene.degree, *[_ptr(a) for a in arrs], _ptr(fl), C.byref(cam), scene.W,
+                                  scene.H, _ptr(bg), _ptr(np.ascontiguousarray(scene.gt, np.uint32)),
+                                  _ptr(scene.weights), int(scene.composite), int(scene.mask), int(scene.alpha_lane),
+                                  scene.l1_w, scene.ssim_w, scene.match_alpha_weight, scene.scale, int(float_exp),
+                                  _ptr(img), C.byref(rx))
     return (loss, img) if want_img else loss
 
 
@@ -349,11 +445,15 @@ def reference_loss(scene, bg=None):
     cam = scene.cam
     arrs = [np.ascontiguousarray(a, np.float32) for a in (scene.pos_op[:, :3], scene.lscale[:, :3], scene.quat,
                                                           scene.pos_op[:, 3], scene.sh.reshape(scene.n, -1))]
-    return r.ref_reference_loss(scene.n, scene.degree, *[_ptr(a) for a in arrs], scene.W, scene.H,
-                                _ptr(np.ascontiguousarray(cam.R, np.float32)), _ptr(np.ascontiguousarray(cam.t, np.float32)),
-                                cam.fx, cam.fy, cam.cx, cam.cy, _ptr(bgv), _ptr(np.ascontiguousarray(scene.gt, np.uint32)),
-                                _ptr(scene.weights), int(scene.composite), int(scene.mask), int(scene.alpha_lane),
-                                scene.l1_w, scene.ssim_w, scene.match_alpha_weight, scene.scale)
+    gtn = _in(scene.normals, np.uint32) if (scene.feat_mode == 1 and scene.normals is not None) else None
+    hz = None if scene.hollow_z is None else _in(scene.hollow_z, np.float32)
+    return r.ref_reference_loss_ext(scene.n, scene.degree, *[_ptr(a) for a in arrs], scene.W, scene.H,
+                                    _ptr(np.ascontiguousarray(cam.R, np.float32)),
+                                    _ptr(np.ascontiguousarray(cam.t, np.float32)), cam.fx, cam.fy, cam.cx, cam.cy,
+                                    _ptr(bgv), _ptr(np.ascontiguousarray(scene.gt, np.uint32)), _ptr(scene.weights),
+                                    int(scene.composite), int(scene.mask), int(scene.alpha_lane), scene.l1_w,
+                                    scene.ssim_w, scene.match_alpha_weight, scene.scale, _ptr(gtn), scene.normal_scale,
+                                    _ptr(hz), scene.hollow_lam, scene.hollow_margin)
 
 
 # ---- internal pieces (for the pinning tests) -----------------------------------------------------------

@@ -7,11 +7,34 @@
 
 #include "reference.h"
 
+extern "C" double ref_reference_loss_ext(int n, int degree, const float* pos, const float* log_scale,
+                                         const float* quat, const float* opacity, const float* sh, int W, int H,
+                                         const float* R, const float* t, float fx, float fy, float cx, float cy,
+                                         const double* bg, const uint32_t* gt, const uint8_t* wts, int composite,
+                                         int mask, int alpha_lane, double l1_w, double ssim_w,
+                                         double match_alpha_weight, double scale, const uint32_t* gtn,
+                                         double normal_scale, const float* hollow_z, double hollow_lam,
+                                         double hollow_margin);
+
 extern "C" double ref_reference_loss(int n, int degree, const float* pos, const float* log_scale, const float* quat,
                                      const float* opacity, const float* sh, int W, int H, const float* R,
                                      const float* t, float fx, float fy, float cx, float cy, const double* bg,
                                      const uint32_t* gt, const uint8_t* wts, int composite, int mask, int alpha_lane,
                                      double l1_w, double ssim_w, double match_alpha_weight, double scale) {
+  return ref_reference_loss_ext(n, degree, pos, log_scale, quat, opacity, sh, W, H, R, t, fx, fy, cx, cy, bg, gt, wts,
+                                composite, mask, alpha_lane, l1_w, ssim_w, match_alpha_weight, scale, nullptr, 0.0,
+                                nullptr, 0.0, 0.05);
+}
+
+// The same with the normal-map term (gtn non-NULL: RefParams::normals) and the hollow term (hollow_z non-NULL).
+extern "C" double ref_reference_loss_ext(int n, int degree, const float* pos, const float* log_scale,
+                                         const float* quat, const float* opacity, const float* sh, int W, int H,
+                                         const float* R, const float* t, float fx, float fy, float cx, float cy,
+                                         const double* bg, const uint32_t* gt, const uint8_t* wts, int composite,
+                                         int mask, int alpha_lane, double l1_w, double ssim_w,
+                                         double match_alpha_weight, double scale, const uint32_t* gtn,
+                                         double normal_scale, const float* hollow_z, double hollow_lam,
+                                         double hollow_margin) {
   b2c::SplatCloud c;
   c.resize((size_t)n, degree);
   const int K = c.K();
@@ -30,8 +53,18 @@ extern "C" double ref_reference_loss(int n, int degree, const float* pos, const 
   for (int i = 0; i < 3; i++) p.cam.t[i] = t[i];
   p.cam.update_pos();
   for (int i = 0; i < 3; i++) p.bg[i] = bg[i];
-  p.composite = composite != 0; p.mask = mask != 0; p.alpha_lane = alpha_lane != 0; p.normals = false;
-  p.l1_w = l1_w; p.ssim_w = ssim_w; p.match_alpha_weight = match_alpha_weight; p.scale = scale; p.normal_scale = 0;
-  p.gt = &g; p.gtn = nullptr; p.wts = wts ? &w : nullptr;
+  p.composite = composite != 0; p.mask = mask != 0; p.alpha_lane = alpha_lane != 0; p.normals = gtn != nullptr;
+  p.l1_w = l1_w; p.ssim_w = ssim_w; p.match_alpha_weight = match_alpha_weight; p.scale = scale;
+  p.normal_scale = gtn ? normal_scale : 0.0;
+  std::vector<uint32_t> gn;
+  if (gtn) gn.assign(gtn, gtn + (size_t)W * H);
+  std::vector<float> hz;
+  if (hollow_z) hz.assign(hollow_z, hollow_z + (size_t)W * H);
+  p.gt = &g; p.gtn = gtn ? &gn : nullptr; p.wts = wts ? &w : nullptr;
+  if (hollow_z) {
+    p.hollow_z = &hz;
+    p.hollow_lam = hollow_lam;
+    p.hollow_margin = hollow_margin;
+  }
   return reference_loss(c, p);
 }

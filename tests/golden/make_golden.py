@@ -42,6 +42,12 @@ def scene_list():
     s = S.config1()
     s.bg = (0.3, 0.2, 0.1)
     out.append(s)
+    # the harness's normal and hollow configurations (tests.cpp:386-391): normals on a transparent view;
+    # hollow on the transparent, masked and normals views
+    out.append(S.fd_feature_scene(1236, normals=True))
+    out.append(S.fd_feature_scene(1234, hollow=True))
+    out.append(S.fd_feature_scene(1235, masked=True, hollow=True))
+    out.append(S.fd_feature_scene(1236, normals=True, hollow=True))
     return out
 
 
@@ -52,10 +58,12 @@ def ref_loss(sc, P):
     sc2.lscale = np.concatenate([P["log_scale"], np.zeros((sc.n, 1), np.float32)], 1)
     sc2.quat = P["quat"]
     sc2.sh = P["sh"].reshape(sc.n, sc.K, 3)
-    return O.reference_loss(sc2)
+    return O.reference_loss(sc2)  # with the scene's normal map and hollow depths
 
 
 def fd_samples(sc, every=2, sh_every=5):
+    """Central differences as tests.cpp:413-428 takes them; with the hollow loss the mean lanes are left out
+    (tests.cpp:418-421: the loss's depth dependence is not part of the analytic gradient)."""
     per = 11 + 3 * sc.K
     P0 = dict(pos=sc.pos_op[:, :3].copy(), opacity=sc.pos_op[:, 3].copy(), quat=sc.quat.copy(),
               log_scale=sc.lscale[:, :3].copy(), sh=sc.sh.reshape(sc.n, -1).copy())
@@ -63,6 +71,8 @@ def fd_samples(sc, every=2, sh_every=5):
     for i in range(0, sc.n, every):
         for q in range(per):
             if q >= 11 and (q - 11) % sh_every:
+                continue
+            if sc.hollow_z is not None and q < 3:
                 continue
             if q < 3:
                 key, j = "pos", (i, q)
@@ -108,6 +118,12 @@ def main():
             lossw=np.array([sc.l1_w, sc.ssim_w, sc.match_alpha_weight, sc.scale], np.float64),
             ref_loss=np.float64(loss),
         )
+        if sc.feat_mode == 1:
+            rec["normals"] = np.asarray(sc.normals, np.uint32)
+            rec["normal_scale"] = np.float64(sc.normal_scale)
+        if sc.hollow_z is not None:
+            rec["hollow_z"] = np.asarray(sc.hollow_z, np.float32)
+            rec["hollow"] = np.array([sc.hollow_lam, sc.hollow_margin], np.float64)
         if with_fd:
             rec["fd_index"], rec["fd_eps"], rec["fd_4eps"] = fd_samples(sc)
         path = os.path.join(HERE, f"ref_{sc.name}.npz")

@@ -32,6 +32,13 @@ def load(path):
     sc = S.Scene(str(z["name"]), deg, pos_op, z["quat"].copy(), lscale, z["sh"].reshape(n, K, 3).copy(), cam,
                  z["gt"].copy(), w.copy() if w.size else None, composite=comp, mask=mask, alpha_lane=alpha,
                  match_alpha_weight=match, scale=scale, l1_w=l1, ssim_w=ssim, bg=tuple(float(v) for v in z["bg"]))
+    if "normals" in z.files:  # the harness's normal configuration (tests.cpp:386-391)
+        sc.feat_mode = 1
+        sc.normals = z["normals"].copy()
+        sc.normal_scale = float(z["normal_scale"])
+    if "hollow_z" in z.files:
+        sc.hollow_z = z["hollow_z"].copy()
+        sc.hollow_lam, sc.hollow_margin = (float(v) for v in z["hollow"])
     fd = None
     if "fd_index" in z.files:
         fd = dict(index=z["fd_index"], eps=z["fd_eps"], eps4=z["fd_4eps"])

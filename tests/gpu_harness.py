@@ -37,11 +37,11 @@ def emit(msg):
 
 def check_projection(r, scene, camd):
     pr = O.project(scene, camd)
-    g = {k: r.read(k) for k in ("proj0", "proj1", "proj2", "tile_count", "hit_info")}
+    g = {k: r.read(k) for k in ("proj0", "proj1", "proj2", "proj3", "tile_count", "hit_info")}
     assert np.array_equal(g["tile_count"], pr["tile_count"]), \
         f"tile_count differs at {np.flatnonzero(g['tile_count'] != pr['tile_count'])[:10]}"
     ok = pr["tile_count"] > 0
-    for k in ("proj0", "proj1", "proj2"):
+    for k in ("proj0", "proj1", "proj2", "proj3"):  # proj2.w and proj3: the feature lanes
         a, b = g[k][ok], pr[k][ok]
         bad = ~((a == b) | (np.isnan(a) & np.isnan(b)))
         assert not bad.any(), f"{k} differs for splats {np.flatnonzero(ok)[np.flatnonzero(bad.any(1))[:10]]}"
@@ -59,10 +59,14 @@ def check_binning(r, pr, W, H):
     return bn
 
 
-def check_forward(r, pr, bn, W, H, bg, tol=1e-4):
-    fw = O.raster_fwd(pr, bn, W, H, bg)
+def check_forward(r, pr, bn, W, H, bg, tol=1e-4, scene=None):
+    feat = scene is not None and scene.feat_mode != 0
+    hz = None if scene is None else scene.hollow_z
+    fw = O.raster_fwd(pr, bn, W, H, bg, feat=feat, hollow_z=hz,
+                      hollow_margin=0.05 if scene is None else scene.hollow_margin)
     rgba = r.read("out_rgba")
-    T = r.read("out_feat")[:, 3]
+    of = r.read("out_feat")
+    T = of[:, 3]
     last = r.read("last_idx")
     d = np.abs(rgba - fw["out_rgba"]).max(axis=1) if len(rgba) else np.zeros(0)
     # a termination flip: T (1 - alpha) lands within rounding of the 1e-4 stop on one side only, and one
@@ -76,7 +80,20 @@ def check_forward(r, pr, bn, W, H, bg, tol=1e-4):
     ranges = r.read("tile_ranges")
     rm = float((ranges != fw["tile_ranges"]).any(1).mean())
     assert rm <= 1e-3, f"shrunk tile range mismatch fraction {rm}"
-    return dict(out_rgba=rgba, out_T=T, last_idx=last, tile_ranges=ranges, err=err)
+    out = dict(out_rgba=rgba, out_T=T, last_idx=last, tile_ranges=ranges, err=err, out_feat4=of)
+    if feat:  # the feature lanes composite like the colour (features are unit vectors or clamped to 100)
+        fe = np.abs(of[:, :3] - fw["out_feat"]).max(axis=1)
+        ferr = float(fe[~flip].max()) if (~flip).any() else 0.0
+        emit(f"    out_feat max abs err {ferr:.2e}")
+        assert ferr <= tol, f"out_feat max abs err {ferr}"
+    if hz is not None:
+        pen = r.read("hollow_pen")
+        pe = np.abs(pen - fw["hollow_pen"])
+        perr = float(pe[~flip].max()) if (~flip).any() else 0.0
+        emit(f"    hollow_pen max abs err {perr:.2e}")
+        assert perr <= tol, f"hollow_pen max abs err {perr}"
+        out["hollow_pen"] = pen
+    return out
 
 
 # Per-entry bound on v_out relative to its largest entry. The fp32 SSIM statistics (sigma^2 = E[x^2] -
@@ -130,7 +147,34 @@ def check_loss(r, scene, rgba, grad_scale, bg):
     return loss, v
 
 
-def check_backward(r, scene, pr, bn, fw, v_out, W, H, bg, mode, grad_scale):
+def check_aux_losses(r, scene, fw, grad_scale):
+    """normal_loss (v_feat bit for bit and the loss against the oracle fed the GPU's out_feat) and
+    hollow_loss (lam times the oracle's sum of the GPU's per-pixel penalties). Returns the GPU v_feat."""
+    W, H = scene.W, scene.H
+    v_feat = None
+    if scene.feat_mode == 1 and scene.normals is not None and scene.normal_scale > 0:
+        before = float(r.read("loss_accum")[1])
+        r.normal_loss(grad_scale=grad_scale)
+        got = float(r.read("loss_accum")[1]) - before
+        ref, v_ref = O.normal_loss(W, H, fw["out_feat4"], scene.normals, scene.weights, scene.normal_scale, grad_scale)
+        v_feat = r.read("v_feat")
+        assert abs(got - ref) <= 1e-6 * abs(ref) + 1e-9, f"normal loss {got} vs oracle {ref}"
+        assert np.array_equal(v_feat.view(np.uint32), v_ref.view(np.uint32)), \
+            f"v_feat differs at {np.flatnonzero((v_feat != v_ref).any(1))[:10]}"
+        emit(f"    normal loss {got:.6g} (oracle {ref:.6g}), v_feat bit-exact")
+    elif scene.feat_mode:
+        v_feat = r.read("v_feat")
+    if scene.hollow_z is not None:
+        before = float(r.read("loss_accum")[0])
+        r.hollow_loss()
+        got = float(r.read("loss_accum")[0]) - before
+        ref = scene.hollow_lam * O.hollow_sum(fw["hollow_pen"])
+        assert abs(got - ref) <= 1e-5 * abs(ref) + 1e-9, f"hollow loss {got} vs oracle {ref}"
+        emit(f"    hollow loss {got:.6g} (oracle {ref:.6g})")
+    return v_feat
+
+
+def check_backward(r, scene, pr, bn, fw, v_out, W, H, bg, mode, grad_scale, v_feat=None):
     r.zero("v_splat")
     r.zero("vis_flag")
     r.backward(mode=mode, grad_scale=grad_scale)
@@ -139,13 +183,16 @@ def check_backward(r, scene, pr, bn, fw, v_out, W, H, bg, mode, grad_scale):
     inv = 1.0 / grad_scale if mode == 1 else 1.0
     ref_vs, ref_vf, _ = O.raster_bwd(pr, bn, dict(tile_ranges=fw["tile_ranges"], out_rgba=fw["out_rgba"],
                                                   out_T=fw["out_T"], last_idx=fw["last_idx"]), v_out, W, H, bg,
-                                     scene.n, inv_gscale=inv)
+                                     scene.n, inv_gscale=inv, v_feat=v_feat if scene.feat_mode else None,
+                                     hollow_z=scene.hollow_z, hollow_margin=scene.hollow_margin,
+                                     hollow_lam=scene.hollow_lam * grad_scale)
     assert np.array_equal(vf, ref_vf), f"vis_flag differs for {np.flatnonzero(vf != ref_vf)[:10]}"
     lane_scale = np.abs(ref_vs).max(axis=0) + 1e-30
     err = np.abs(vs - ref_vs) / lane_scale
     worst = float(err.max()) if err.size else 0.0
     assert worst <= 2e-3, f"v_splat mode {mode}: worst lane-relative err {worst:.2e} at lane {int(err.max(0).argmax())}"
-    pc = rel_percentiles(vs[:, :10], ref_vs[:, :10])
+    lanes = 13 if scene.feat_mode else 10
+    pc = rel_percentiles(vs[:, :lanes], ref_vs[:, :lanes])
     emit(f"    v_splat lane-max err {worst:.2e}; per-entry rel p50 {pc['p50']:.1e} p99 {pc['p99']:.1e} "
          f"max {pc['max']:.1e} over {pc['n']}")
     assert pc["p99"] <= 1e-3, f"v_splat per-entry 99th percentile rel err {pc['p99']:.2e}"
@@ -190,7 +237,7 @@ def full_check(scene, mode=1, bg=None, loss=True, backward=True, fp64_rgba=False
         bn = check_binning(r, pr, W, H)
         emit(f"  [{scene.name}] forward (M={bn['M']})")
         r.raster_fwd(bg=bg)
-        fw = check_forward(r, pr, bn, W, H, bg)
+        fw = check_forward(r, pr, bn, W, H, bg, scene=scene)
         out = dict(M=bn["M"], rgba_err=fw["err"])
         if fp64_rgba:
             out["rgba_err64"] = check_rgba_fp64(fw["out_rgba"], scene, bg)
@@ -198,9 +245,10 @@ def full_check(scene, mode=1, bg=None, loss=True, backward=True, fp64_rgba=False
         if loss:
             emit(f"  [{scene.name}] loss")
             out["loss"], v = check_loss(r, scene, fw["out_rgba"], gs, bg)
+            v_feat = check_aux_losses(r, scene, fw, gs)
             if backward:
                 emit(f"  [{scene.name}] backward mode {mode}")
-                vs, vf, out["v_splat_err"] = check_backward(r, scene, pr, bn, fw, v, W, H, bg, mode, gs)
+                vs, vf, out["v_splat_err"] = check_backward(r, scene, pr, bn, fw, v, W, H, bg, mode, gs, v_feat)
                 emit(f"  [{scene.name}] vjp")
                 out["grads"] = check_vjp(r, scene, camd, vs, vf, pr["tile_count"])
         return out
