@@ -237,6 +237,19 @@ struct ShView {
 // Row-major 3x3 helpers and the quaternion rotation (util.cuh:218-243).
 struct Mat3 { float m[9]; };
 
+// The axis of the smallest of three log scales (the first of equal ones), as three exclusive flags, so a
+// column of a matrix is picked with selects: a runtime index into a register array would move the array
+// (and the struct holding it) to scratch memory.
+struct AxisPick {
+  bool x, y, z;
+  __device__ __forceinline__ float of(float a, float b, float c) const { return x ? a : (y ? b : c); }
+};
+__device__ __forceinline__ AxisPick smallest_axis(float lx, float ly, float lz) {
+  const bool x = lx <= ly && lx <= lz;
+  const bool y = !x && ly <= lz;
+  return AxisPick{x, y, !x && !y};
+}
+
 __device__ __forceinline__ Mat3 mat3_mul(const Mat3& A, const Mat3& B) {
 #pragma clang fp contract(off)
   Mat3 C;

@@ -86,8 +86,9 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       if (a.feat_mode == 1) {
         // the pseudo-normal (project.cu:63-71): the local axis of the smallest log scale (the first of
         // equal ones), a column of R(q), as a unit vector turned towards the camera, in camera coordinates
-        const int ax = (ls.x <= ls.y && ls.x <= ls.z) ? 0 : (ls.y <= ls.z ? 1 : 2);
-        const float nx = pr.rot.m[ax], ny = pr.rot.m[3 + ax], nz = pr.rot.m[6 + ax];
+        const AxisPick ax = smallest_axis(ls.x, ls.y, ls.z);
+        const float* m = pr.rot.m;
+        const float nx = ax.of(m[0], m[1], m[2]), ny = ax.of(m[3], m[4], m[5]), nz = ax.of(m[6], m[7], m[8]);
         const float il = 1.f / fmaxf(sqrtf((nx * nx + ny * ny) + nz * nz), 1e-12f);
         const float sx = nx * il, sy = ny * il, sz = nz * il;
         // pr.d runs from the camera to the splat: the axis faces the camera when it points against it
@@ -115,7 +116,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
         rec[0] = make_float4(pr.px, pr.py, 0.5f * pr.conic.c00, pr.conic.c01);
         rec[1] = make_float4(0.5f * pr.conic.c11, pr.opacity, power, __uint_as_float(sgn));
         rec[2] = make_float4(fmaxf(cr, 0.f), fmaxf(cg, 0.f), fmaxf(cb, 0.f), log2_opacity(pr.opacity));
-        rec[3] = make_float4(f0, f1, f2, pr.c[2]);  // read by the feature and hollow-loss variants only
+        rec[3] = make_float4(f0, f1, f2, pr.c[2]);  // read by the feature and hollow-loss variants and the depth probe
       }
       if (a.max_screen) {
         float ms = fmaxf(pr.ex / (float)a.cam.W, pr.ey / (float)a.cam.H);

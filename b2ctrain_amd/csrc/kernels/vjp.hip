@@ -400,8 +400,9 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
       // of R(q) along the smallest log scale and s = +-1 its facing sign (locally constant), so
       // dL/dc = s (I - u u^T) R_view^T dL/df / |c|, which joins that column of dL/dR(q).
       if (g[10] != 0.f || g[11] != 0.f || g[12] != 0.f) {
-        const int ax = (ls.x <= ls.y && ls.x <= ls.z) ? 0 : (ls.y <= ls.z ? 1 : 2);
-        const float nx = sp.rot.m[ax], ny = sp.rot.m[3 + ax], nz = sp.rot.m[6 + ax];
+        const AxisPick ax = smallest_axis(ls.x, ls.y, ls.z);
+        const float* m = sp.rot.m;
+        const float nx = ax.of(m[0], m[1], m[2]), ny = ax.of(m[3], m[4], m[5]), nz = ax.of(m[6], m[7], m[8]);
         const float il = 1.f / fmaxf(sqrtf((nx * nx + ny * ny) + nz * nz), 1e-12f);
         const float ux = nx * il, uy = ny * il, uz = nz * il;
         const float face = ((ux * -dvx + uy * -dvy) + uz * -dvz) >= 0.f ? 1.f : -1.f;
@@ -409,9 +410,14 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
         const float by = ((Rv[1] * g[10] + Rv[4] * g[11]) + Rv[7] * g[12]) * face;
         const float bz = ((Rv[2] * g[10] + Rv[5] * g[11]) + Rv[8] * g[12]) * face;
         const float along = (ux * bx + uy * by) + uz * bz;
-        gR[ax] = gR[ax] + (bx - ux * along) * il;
-        gR[3 + ax] = gR[3 + ax] + (by - uy * along) * il;
-        gR[6 + ax] = gR[6 + ax] + (bz - uz * along) * il;
+        const float cx = (bx - ux * along) * il, cy = (by - uy * along) * il, cz = (bz - uz * along) * il;
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+          const bool on = j == 0 ? ax.x : (j == 1 ? ax.y : ax.z);
+          gR[j] = on ? gR[j] + cx : gR[j];
+          gR[3 + j] = on ? gR[3 + j] + cy : gR[3 + j];
+          gR[6 + j] = on ? gR[6 + j] + cz : gR[6 + j];
+        }
       }
       // semi-axes a_j = sqrt(exp(2 l_j) + f^2), and the floor's opacity factor prod_j sqrt(var_j / (var_j + f^2))
       const float v_op = g[8];
