@@ -130,6 +130,8 @@ def lib():
         _lib.orc_hollow_sum.argtypes = [C.c_int, p]
         _lib.orc_eval.restype = None
         _lib.orc_eval.argtypes = [C.c_int, C.c_int, p, p, C.c_int, p, p]
+        _lib.orc_evidence_view.argtypes = [C.c_int] * 4 + [p] * 11 + [C.c_int, f, p, p]
+        _lib.orc_probe.argtypes = [C.c_int] * 4 + [p] * 4 + [f, f, p, f, p]
         _lib.orc_ref_loss_ext.restype = C.c_double
         _lib.orc_ref_loss_ext.argtypes = [C.c_int, C.c_int] + [p] * 6 + [C.POINTER(OrcCam), C.c_int, C.c_int, p, p, p,
                                                                         C.c_int, C.c_int, C.c_int] + [C.c_double] * 4 + [
@@ -278,6 +280,16 @@ def _ext(feat=False, proj3=None, hollow_z=None, margin=0.05, lam=0.0, out_feat=N
     return e
 
 
+def _proj3(pr, feat):
+    """The feature lanes 1-2 of a projection; only the feature variants read them, and a projection read
+    back without them (proj0..2 only) serves every other call."""
+    if "proj3" in pr:
+        return _in(pr["proj3"], np.float32)
+    if feat:
+        raise ValueError("feature lanes need the projection's proj3")
+    return None
+
+
 def bin_(pr, W, H):
     n = pr["tile_count"].shape[0]
     tx, ty, T, _ = tile_geometry(W, H)
@@ -300,7 +312,7 @@ def raster_fwd(pr, bn, W, H, bg, feat=False, hollow_z=None, hollow_margin=0.05):
                out_feat=np.zeros((P, 3), np.float32), hollow_pen=np.zeros(P, np.float32))
     bgv = np.asarray(bg, np.float32)
     hz = None if hollow_z is None else _in(hollow_z, np.float32)
-    ext = _ext(feat, _in(pr["proj3"], np.float32), hz, hollow_margin, 0.0, out["out_feat"], out["hollow_pen"])
+    ext = _ext(feat, _proj3(pr, feat), hz, hollow_margin, 0.0, out["out_feat"], out["hollow_pen"])
     lib().orc_raster_fwd_ext(W, H, tx, ty, _ptr(bgv), _ptr(ranges), _ptr(bn["vals_sorted"]), _ptr(pr["proj0"]),
                              _ptr(pr["proj1"]), _ptr(pr["proj2"]),
                              *[_ptr(out[k]) for k in ("out_rgba", "out_T", "last_idx")], C.byref(ext))
@@ -329,7 +341,7 @@ def raster_bwd(pr, bn, fw, v_out, W, H, bg, n, inv_gscale=1.0, v_feat=None, holl
     u32, f32 = np.uint32, np.float32
     vf = None if v_feat is None else _in(v_feat, f32)
     hz = None if hollow_z is None else _in(hollow_z, f32)
-    ext = _ext(vf is not None, _in(pr["proj3"], f32), hz, hollow_margin, hollow_lam, v_feat=vf)
+    ext = _ext(vf is not None, _proj3(pr, vf is not None), hz, hollow_margin, hollow_lam, v_feat=vf)
     lib().orc_raster_bwd_ext(W, H, tx, ty, _ptr(bgv), _ptr(_in(fw["tile_ranges"], u32)),
                              _ptr(_in(bn["vals_sorted"], u32)), _ptr(_in(pr["proj0"], f32)), _ptr(_in(pr["proj1"], f32)),
                              _ptr(_in(pr["proj2"], f32)), _ptr(_in(fw["out_rgba"], f32)), _ptr(_in(fw["out_T"], f32)),
@@ -359,6 +371,76 @@ def eval_metrics(W, H, pred, gt, mask_weighted=False):
     lib().orc_eval(W, H, _ptr(_in(pred, np.float32)), _ptr(_in(gt, np.uint32)), int(mask_weighted), C.byref(se),
                    C.byref(ss))
     return se.value, ss.value
+
+
+LABEL_BINS = 32
+
+
+def evidence_view(pr, bn, fw, W, H, gt, weights=None, normals=None, labels=None, masked_has_alpha=False,
+                  normal_weight=0.0, n=None):
+    """One view's evidence sums [n][3] = (w_in, err, w_all) and, with labels, the class votes [n][32], from
+    the forward's outputs fw (tile_ranges, out_rgba, last_idx and, with normals, out_feat [P][3])."""
+    tx, ty, _, _ = tile_geometry(W, H)
+    u32, f32 = np.uint32, np.float32
+    n = pr["proj0"].shape[0] if n is None else n
+    acc = np.zeros((n, 3), np.float64)
+    lab_acc = np.zeros((n, LABEL_BINS), np.float64) if labels is not None else None
+    feat = None
+    if normals is not None:
+        feat = _in(np.asarray(fw["out_feat"])[:, :3], f32)
+    lib().orc_evidence_view(W, H, tx, ty, _ptr(_in(fw["tile_ranges"], u32)), _ptr(_in(bn["vals_sorted"], u32)),
+                            _ptr(_in(pr["proj0"], f32)), _ptr(_in(pr["proj1"], f32)), _ptr(_in(fw["out_rgba"], f32)),
+                            _ptr(feat), _ptr(_in(fw["last_idx"], u32)), _ptr(_in(gt, u32)),
+                            _ptr(None if normals is None else _in(normals, u32)),
+                            _ptr(None if weights is None else _in(weights, np.uint8)),
+                            _ptr(None if labels is None else _in(labels, np.uint8)), int(bool(masked_has_alpha)),
+                            float(normal_weight), _ptr(acc), _ptr(lab_acc))
+    return acc, lab_acc
+
+
+def evidence_fold(ev, view_acc, pos, cam_pos):
+    """fold_view_kernel (evidence.cu:114-126) in double: ev [n][8] += (w_in, w_all, err, -, w_in dir, w_in^2)."""
+    w_in, err, w_all = view_acc[:, 0], view_acc[:, 1], view_acc[:, 2]
+    ev[:, 0] += w_in
+    ev[:, 1] += w_all
+    ev[:, 2] += err
+    ev[:, 7] += w_in * w_in
+    d = np.asarray(cam_pos, np.float64)[None, :] - np.asarray(pos, np.float64)[:, :3]
+    l = np.maximum(np.linalg.norm(d, axis=1), 1e-12)
+    ev[:, 4:7] += (w_in / l)[:, None] * d
+    return ev
+
+
+def evidence_export(ev):
+    """download_evidence (evidence.cu:236-249): [n][7] with views = (sum w_in)^2 / sum w_in^2."""
+    out = np.zeros((ev.shape[0], 7), np.float64)
+    out[:, 0:3] = ev[:, 0:3]
+    pos = ev[:, 7] > 0
+    out[pos, 3] = ev[pos, 0] ** 2 / ev[pos, 7]
+    out[:, 4:7] = ev[:, 4:7]
+    return out
+
+
+def label_winners(lab_acc):
+    """download_labels (evidence.cu:251-264): [n][2] = (first class with the largest vote, its share)."""
+    total = lab_acc.sum(1)
+    win = np.argmax(lab_acc, 1)
+    out = np.zeros((lab_acc.shape[0], 2), np.float64)
+    ok = total > 0
+    out[ok, 0] = win[ok]
+    out[ok, 1] = lab_acc[ok, win[ok]] / total[ok]
+    return out
+
+
+def probe(pr, bn, W, H, tau, delta, ref_z=None, margin=0.0, tile_ranges=None):
+    """probe_kernel (probe.cu:7-45): [P][4] = (A, z_first, deep, behind)."""
+    tx, ty, _, _ = tile_geometry(W, H)
+    out = np.zeros((W * H, 4), np.float32)
+    ranges = bn["tile_ranges"] if tile_ranges is None else tile_ranges
+    lib().orc_probe(W, H, tx, ty, _ptr(_in(ranges, np.uint32)), _ptr(_in(bn["vals_sorted"], np.uint32)),
+                    _ptr(_in(pr["proj0"], np.float32)), _ptr(_in(pr["proj1"], np.float32)), float(tau), float(delta),
+                    _ptr(None if ref_z is None else _in(ref_z, np.float32)), float(margin), _ptr(out))
+    return out
 
 
 def vjp(scene, camd, v_splat, vis_flag, tile_count, active_deg=None):
