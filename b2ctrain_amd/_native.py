@@ -96,6 +96,9 @@ EXPORTS = [
     "b2c_hip_fill_u32", "b2c_hip_model_scatter", "b2c_hip_model_gather", "b2c_hip_planar_regrow",
     "b2c_hip_model_set_floor", "b2c_hip_photometric_noalloc", "b2c_aux_partials", "b2c_hip_normal_loss",
     "b2c_hip_hollow_loss", "b2c_hip_eval_metrics", "b2c_hip_step_loss_sums",
+    "b2c_view_set_labels", "b2c_view_set_flags", "b2c_compute_evidence", "b2c_download_evidence",
+    "b2c_download_labels", "b2c_probe_depth", "b2c_device_download", "b2c_hip_evidence_view",
+    "b2c_hip_evidence_fold", "b2c_hip_probe_depth",
 ]
 
 _lib = None
@@ -155,6 +158,13 @@ def lib():
         L.b2c_normal_loss.argtypes = [p, p, C.POINTER(LossOpts)]
         L.b2c_hollow_loss.argtypes = [p, f]
         L.b2c_eval_metrics.argtypes = [p, p, i]
+        L.b2c_view_set_labels.argtypes = [p, p]
+        L.b2c_view_set_flags.argtypes = [p, i, i, f, f]
+        L.b2c_compute_evidence.argtypes = [p, p, C.POINTER(p), C.POINTER(Camera), i, f, i]
+        L.b2c_download_evidence.argtypes = [p, p]
+        L.b2c_download_labels.argtypes = [p, p]
+        L.b2c_probe_depth.argtypes = [p, f, f, p, f, p]
+        L.b2c_device_download.argtypes = [p, p, C.c_size_t]
         L.b2c_radix_sort_temp_bytes.restype = C.c_size_t
         L.b2c_radix_sort_temp_bytes.argtypes = [C.c_uint32]
         L.b2c_scan_temp_bytes.restype = C.c_size_t
@@ -230,6 +240,36 @@ class DeviceArray:
     def __del__(self):
         try:
             self.free()
+        except Exception:
+            pass
+
+
+class View:
+    """A target view (b2c_view): packed RGBA8 pixels, optional weight bytes, normal map and label plane, and
+    the has_alpha / masked flags."""
+
+    def __init__(self, W, H, gt, weights=None, normals=None, labels=None, has_alpha=False, masked=False):
+        self.L = lib()
+        self.W, self.H = W, H
+        g = np.ascontiguousarray(gt, np.uint32)
+        w = None if weights is None else np.ascontiguousarray(weights, np.uint8)
+        self.ptr = self.L.b2c_view_create(W, H, _ptr(g), _ptr(w))
+        if not self.ptr:
+            raise RuntimeError(self.L.b2c_last_error().decode())
+        if normals is not None:
+            check(self.L.b2c_view_set_normals(self.ptr, _ptr(np.ascontiguousarray(normals, np.uint32))), "view_set_normals")
+        if labels is not None:
+            check(self.L.b2c_view_set_labels(self.ptr, _ptr(np.ascontiguousarray(labels, np.uint8))), "view_set_labels")
+        check(self.L.b2c_view_set_flags(self.ptr, int(has_alpha), int(masked), 1.0, 0.0), "view_set_flags")
+
+    def close(self):
+        if self.ptr:
+            self.L.b2c_view_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
         except Exception:
             pass
 
@@ -408,6 +448,44 @@ class Renderer:
                                     C.byref(self.loss_opts(gs, bg)), mode, GRAD_ACCUMULATE if accumulate else 0,
                                     C.byref(t) if timed else None), "train_step")
         return t.as_dict() if timed else None
+
+    # -- tile-list replays
+    def compute_evidence(self, views, cams, normal_weight=0.0, export_labels=False, download=True):
+        """compute_evidence over View objects and their cameras; returns download_evidence [n][7] (None
+        without download)."""
+        if len(views) != len(cams):
+            raise ValueError("one camera per view")
+        vp = (C.c_void_p * len(views))(*[v.ptr for v in views])
+        cs = (Camera * len(cams))(*[camera_struct(c) for c in cams])
+        check(self.L.b2c_compute_evidence(self.ctx, self.model, vp, cs, len(views), float(normal_weight),
+                                          int(export_labels)), "compute_evidence")
+        return self.download_evidence() if download else None
+
+    def download_evidence(self):
+        out = np.zeros((self.n, 7), np.float32)
+        check(self.L.b2c_download_evidence(self.model, _ptr(out)), "download_evidence")
+        return out
+
+    def download_labels(self):
+        out = np.zeros((self.n, 2), np.float32)
+        check(self.L.b2c_download_labels(self.model, _ptr(out)), "download_labels")
+        return out
+
+    def probe_depth(self, tau, delta, ref_z=None, margin=0.0):
+        """probe_depth on the context's current lists (after forward, or project + bin): [P][4] float32."""
+        P = self.W * self.H
+        out = DeviceArray(np.zeros((P, 4), np.float32))
+        rz = None if ref_z is None else DeviceArray(np.asarray(ref_z, np.float32).reshape(P))
+        try:
+            check(self.L.b2c_probe_depth(self.ctx, float(tau), float(delta), None if rz is None else rz.ptr,
+                                         float(margin), out.ptr), "probe_depth")
+            host = np.empty((P, 4), np.float32)
+            check(self.L.b2c_device_download(_ptr(host), out.ptr, host.nbytes), "device_download")
+            return host
+        finally:
+            out.free()
+            if rz is not None:
+                rz.free()
 
     # -- buffers
     def info(self) -> CtxInfo:

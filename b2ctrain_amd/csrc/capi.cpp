@@ -1,10 +1,13 @@
 // C ABI over the C++ drop-in API (declared in include/b2c.h).
 #include "b2c.h"
 
+#include <algorithm>
 #include <cstring>
+#include <vector>
 #include <map>
 #include <string>
 
+#include "b2c/evidence.h"
 #include "b2c/loss.h"
 #include "b2c/optim.h"
 #include "b2c/render.h"
@@ -24,7 +27,7 @@ struct b2c_ctx {
 
 struct b2c_view {
   b2c::DevBuf<uint32_t> rgba, normals;
-  b2c::DevBuf<uint8_t> weights;
+  b2c::DevBuf<uint8_t> weights, labels;
   b2c::ViewGPU view;
 };
 
@@ -366,6 +369,72 @@ int b2c_view_set_normals(b2c_view* v, const uint32_t* normals) {
     } else {
       v->view.normals = nullptr;
     }
+  });
+}
+
+int b2c_view_set_labels(b2c_view* v, const uint8_t* labels) {
+  return guarded([&] {
+    const size_t P = (size_t)v->view.W * v->view.H;
+    if (labels) {
+      v->labels.upload(labels, P);
+      HIP_CHECK(hipDeviceSynchronize());
+      v->view.labels = v->labels.ptr;
+    } else {
+      v->view.labels = nullptr;
+    }
+  });
+}
+
+int b2c_view_set_flags(b2c_view* v, int has_alpha, int masked, float alpha_coverage, float normal_count) {
+  return guarded([&] {
+    v->view.has_alpha = has_alpha != 0;
+    v->view.masked = masked != 0;
+    v->view.alpha_coverage = alpha_coverage;
+    v->view.normal_count = normal_count;
+  });
+}
+
+int b2c_compute_evidence(b2c_ctx* c, const b2c_model* m, const b2c_view* const* views, const b2c_camera* cams,
+                         int nviews, float normal_weight, int export_labels) {
+  return guarded([&] {
+    std::vector<b2c::ViewGPU> vs;
+    std::vector<b2c::Camera> cs;
+    for (int v = 0; v < nviews; v++) {
+      vs.push_back(views[v]->view);
+      cs.push_back(to_camera(cams[v]));
+    }
+    b2c::EvidenceParams p;
+    p.evidence_normal_weight = normal_weight;
+    p.export_labels = export_labels != 0;
+    b2c::compute_evidence(c->ctx, m->m, vs, cs, p, c->stream);
+  });
+}
+
+int b2c_download_evidence(const b2c_model* m, float* out) {
+  return guarded([&] {
+    const std::vector<float> e = b2c::download_evidence(m->m, nullptr);
+    std::copy(e.begin(), e.end(), out);
+  });
+}
+
+int b2c_download_labels(const b2c_model* m, float* out) {
+  return guarded([&] {
+    const std::vector<float> l = b2c::download_labels(m->m, nullptr);
+    std::copy(l.begin(), l.end(), out);
+  });
+}
+
+int b2c_probe_depth(b2c_ctx* c, float tau, float delta, const float* ref_z, float margin, float* out) {
+  return guarded([&] {
+    b2c::probe_depth(c->ctx, tau, delta, ref_z, margin, reinterpret_cast<float4*>(out), c->stream);
+    HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+int b2c_device_download(void* host, const void* dev, size_t bytes) {
+  return guarded([&] {
+    HIP_CHECK(hipDeviceSynchronize());
+    if (bytes) HIP_CHECK(hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost));
   });
 }
 

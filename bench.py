@@ -366,6 +366,29 @@ def main():
                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(ub / t_upd / 1e9 / HBM_PEAK_GBS, 4)}
     out["training_iteration"] = upd
+    # The tile-list replays on the first view: compute_evidence with the label vote (a class plane of
+    # 64x64-pixel blocks) and probe_depth, as wall time of the synchronous calls (the evidence call renders
+    # the view itself, as the reference's does). Kernel durations are in the rocprofv3 summaries.
+    log("bench: evidence and probe replays")
+    pix = np.arange(W * H)
+    labels = (((pix % W) // 64 + 3 * ((pix // W) // 64)) % 29).astype(np.uint8)
+    view = _native.View(W, H, scene.gt, scene.weights, labels=labels, has_alpha=True, masked=False)
+    ev_t, pr_t = [], []
+    for k in range(8):
+        t0 = time.perf_counter()
+        r.compute_evidence([view], [views[0]], export_labels=True, download=False)
+        ev_t.append(time.perf_counter() - t0)
+    r.forward(bg=(0.0, 0.0, 0.0), cam=views[0])
+    r.sync()
+    for k in range(8):
+        t0 = time.perf_counter()
+        r.probe_depth(0.5, 0.1)
+        pr_t.append(time.perf_counter() - t0)
+    view.close()
+    out["replays"] = {"evidence_view_ms": round(float(np.median(ev_t[2:])) * 1e3, 4),
+                      "probe_ms": round(float(np.median(pr_t[2:])) * 1e3, 4),
+                      "note": "median wall time of the synchronous calls; evidence includes rendering the view, "
+                              "probe includes allocating and downloading its [P][4] output"}
     r.close()
     print(json.dumps(out), flush=True)
 

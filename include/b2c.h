@@ -117,9 +117,26 @@ b2c_view* b2c_view_create(int W, int H, const uint32_t* rgba, const uint8_t* wei
 void b2c_view_destroy(b2c_view* v);
 /* ViewGPU::normals: a device copy of a packed RGBA8 normal map [W*H] (NULL removes it). */
 int b2c_view_set_normals(b2c_view* v, const uint32_t* normals);
-/* A device copy of host memory (for RenderParams' device arrays: feat_buffer, hollow_z), and its release. */
+/* ViewGPU::labels: a device copy of per-pixel class ids [W*H] (NULL removes them), read by the evidence pass. */
+int b2c_view_set_labels(b2c_view* v, const uint8_t* labels);
+/* ViewGPU's flags (src/gpu/loss.h:13-15). */
+int b2c_view_set_flags(b2c_view* v, int has_alpha, int masked, float alpha_coverage, float normal_count);
+/* A device copy of host memory (for RenderParams' device arrays: feat_buffer, hollow_z), a device-to-host
+ * copy, and the release. */
 void* b2c_device_upload(const void* host, size_t bytes);
+int b2c_device_download(void* host, const void* dev, size_t bytes);
 void b2c_device_free(void* p);
+
+/* compute_evidence / download_evidence / download_labels (src/train/evidence.h:10-22) over nviews views and
+ * their cameras: the evidence [n][7] = (w_in, w_all, err, views, dir xyz) and, with export_labels, the label
+ * vote [n][2] = (winning class, share). Synchronous; the accumulators are module-level, as the reference's. */
+int b2c_compute_evidence(b2c_ctx* c, const b2c_model* m, const b2c_view* const* views, const b2c_camera* cams,
+                         int nviews, float normal_weight, int export_labels);
+int b2c_download_evidence(const b2c_model* m, float* out);
+int b2c_download_labels(const b2c_model* m, float* out);
+/* probe_depth (src/gpu/probe.h:6-11) after b2c_project_splats + b2c_bin_and_sort: out is a device array of
+ * W*H float4 (b2c_device_upload), ref_z a device array or NULL. Synchronous. */
+int b2c_probe_depth(b2c_ctx* c, float tau, float delta, const float* ref_z, float margin, float* out);
 
 /* render_forward / project_splats / bin_and_sort / rasterize_forward (src/gpu/render.h:97-103). */
 int b2c_render_forward(b2c_ctx* c, const b2c_model* m, const b2c_render_opts* o);

@@ -284,6 +284,52 @@ typedef struct b2c_eval_args {
 } b2c_eval_args;
 int b2c_hip_eval_metrics(const b2c_eval_args* a, hipStream_t stream);
 
+/* ---- tile-list consumers: evidence / label vote (src/train/evidence.cu:47-183) and the depth probe
+ * (src/gpu/probe.cu:7-53) ---- */
+#define B2C_LABEL_BINS 32      /* class ids >= this are ignored (evidence.cu:39) */
+#define B2C_EVIDENCE_STRIDE 8  /* floats per splat of the evidence accumulator: w_in, w_all, err, -, dir xyz, sum w_in^2 */
+
+/* One view's replay after a forward with bwd_info (shrunk ranges, last_idx): view_acc[i] += per splat the
+ * sums over its composited fragments of vis * (m, m * res, k) with m = target alpha * w, res the pixel's mean
+ * absolute colour residual (+ normal_weight times the normal residual when normals are given), k =
+ * (target alpha if masked_has_alpha else 1) * w; with labels, label_acc[i][class] += vis * k for the pixel's
+ * class (< B2C_LABEL_BINS). Float atomics, as the reference. */
+typedef struct b2c_evidence_args {
+  const uint32_t* tile_ranges;
+  const uint32_t* vals_sorted;
+  const float* raster_rec;    /* [n][16] from b2c_hip_project */
+  const float* out_rgba, *out_feat;
+  const uint32_t* last_idx;
+  const uint32_t* gt;         /* [P] packed RGBA8 */
+  const uint32_t* normals;    /* [P] normal map or NULL */
+  const uint8_t* weights;     /* [P] or NULL */
+  const uint8_t* labels;      /* [P] class ids or NULL */
+  int W, H, tiles_x, tiles_y;
+  int masked_has_alpha;
+  float normal_weight;
+  float* view_acc;            /* [n][3] (w_in, err, w_all), zeroed by the caller per view */
+  float* label_acc;           /* [n][B2C_LABEL_BINS] or NULL */
+} b2c_evidence_args;
+int b2c_hip_evidence_view(const b2c_evidence_args* a, hipStream_t stream);
+/* fold_view_kernel (evidence.cu:114-126): evidence[i] (B2C_EVIDENCE_STRIDE floats) += w_in, w_all, err; [7] +=
+ * w_in^2; [4..6] += w_in * the unit vector from the splat to cam_pos. */
+int b2c_hip_evidence_fold(int n, const float* view_acc, const float* pos_op, const float cam_pos[3], float* evidence,
+                          hipStream_t stream);
+
+/* probe_kernel (probe.cu:7-53) after projection and binning: out[pix] = (accumulated alpha, the depth where it
+ * first reaches tau (tau <= 0: the alpha-weighted mean depth, +inf under 5% coverage), the weight from more
+ * than delta behind that depth, the weight from more than margin behind ref_z (NULL: none)). */
+typedef struct b2c_probe_args {
+  const uint32_t* tile_ranges;
+  const uint32_t* vals_sorted;
+  const float* raster_rec;
+  int W, H, tiles_x, tiles_y;
+  float tau, delta, margin;
+  const float* ref_z;         /* [P] or NULL */
+  float* out;                 /* [P] float4 */
+} b2c_probe_args;
+int b2c_hip_probe_depth(const b2c_probe_args* a, hipStream_t stream);
+
 /* Writable planar SH arrays (the same layout as b2c_sh_view): parameters or their first moments. */
 typedef struct b2c_sh_planes {
   float* dc;

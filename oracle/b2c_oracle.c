@@ -1307,6 +1307,102 @@ void orc_eval(int W, int H, const float* pred, const uint32_t* gt, int mask_weig
 }
 
 /* ------------------------------------------------------------------------------------------------
+ * Replays of a rendered view's tile lists (evidence.cu:47-112, 141-183, probe.cu:7-45): per pixel the
+ * forward's own walk, in single precision, with the forward oracle's alpha; the per-splat sums in double.
+ * ---------------------------------------------------------------------------------------------- */
+static float byte_f(uint32_t p, int c) { return (float)((p >> (8 * c)) & 0xffu) * (1.f / 255.f); }
+
+void orc_evidence_view(int W, int H, int tiles_x, int tiles_y, const uint32_t* tile_ranges, const uint32_t* vals_sorted,
+                       const float* proj0, const float* proj1, const float* out_rgba, const float* out_feat,
+                       const uint32_t* last_idx, const uint32_t* gt, const uint32_t* normals, const uint8_t* weights,
+                       const uint8_t* labels, int masked_has_alpha, float normal_weight, double* view_acc,
+                       double* label_acc) {
+  for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const uint32_t rx = tile_ranges[tile * 2], ry = tile_ranges[tile * 2 + 1];
+    for (int l = 0; l < RT_W * RT_W; l++) {
+      const int px = tx * RT_W + l % RT_W, py = ty * RT_W + l / RT_W;
+      if (!(px < W && py < H)) continue;
+      const size_t pix = (size_t)py * W + px;
+      const uint32_t g = gt[pix];
+      const float ga = byte_f(g, 3);
+      const float wp = weights ? (float)weights[pix] * (1.f / 255.f) : 1.f;
+      const float* o = out_rgba + pix * 4;
+      float res = (fabsf(o[0] - byte_f(g, 0)) + fabsf(o[1] - byte_f(g, 1)) + fabsf(o[2] - byte_f(g, 2))) * (1.f / 3.f);
+      if (normals && normal_weight > 0.f && ((normals[pix] >> 24) & 0xffu) > 127u) { /* loss.cu:218-223 */
+        const uint32_t gn = normals[pix];
+        const float nx = (float)(gn & 0xffu) * (2.f / 255.f) - 1.f;
+        const float ny = 1.f - (float)((gn >> 8) & 0xffu) * (2.f / 255.f);
+        const float nz = 1.f - (float)((gn >> 16) & 0xffu) * (2.f / 255.f);
+        const float* f = out_feat + pix * 3;
+        const float pl = fmaxf(sqrtf(f[0] * f[0] + f[1] * f[1] + f[2] * f[2]), 1e-6f);
+        const float nl = fmaxf(sqrtf(nx * nx + ny * ny + nz * nz), 1e-6f);
+        const float nres = fabsf(f[0] - nx) + fabsf(f[1] - ny) + fabsf(f[2] - nz) + 1.f -
+                           (f[0] * nx + f[1] * ny + f[2] * nz) / (pl * nl);
+        res += normal_weight * nres;
+      }
+      const float m = ga * wp, mres = m * res, k = (masked_has_alpha ? ga : 1.f) * wp;
+      const int lab = labels ? (int)labels[pix] : -1;
+      const int vote = label_acc && lab >= 0 && lab < ORC_LABEL_BINS && k != 0.f;
+      const float pcx = px + 0.5f, pcy = py + 0.5f;
+      const uint32_t last = last_idx[pix];
+      float T = 1.f;
+      for (uint32_t idx = rx; idx < ry && idx < last; idx++) {
+        const uint32_t gid = vals_sorted[idx];
+        const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
+        const float sigma = frag_sigma(pcx - a[0], pcy - a[1], a[2], a[3], c[0]);
+        if (sigma < 0.f || sigma > c[3]) continue;
+        const float alpha = fminf(ALPHA_MAX, c[1] * expf(-sigma));
+        const float vis = alpha * T;
+        T *= 1.f - alpha;
+        view_acc[(size_t)gid * 3] += (double)vis * m;
+        view_acc[(size_t)gid * 3 + 1] += (double)vis * mres;
+        view_acc[(size_t)gid * 3 + 2] += (double)vis * k;
+        if (vote) label_acc[(size_t)gid * ORC_LABEL_BINS + lab] += (double)vis * k;
+      }
+    }
+  }
+}
+
+void orc_probe(int W, int H, int tiles_x, int tiles_y, const uint32_t* tile_ranges, const uint32_t* vals_sorted,
+               const float* proj0, const float* proj1, float tau, float delta, const float* ref_z, float margin,
+               float* out) {
+  const int mean_mode = tau <= 0.f;
+  for (int tile = 0; tile < tiles_x * tiles_y; tile++) {
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const uint32_t rx = tile_ranges[tile * 2], ry = tile_ranges[tile * 2 + 1];
+    for (int l = 0; l < RT_W * RT_W; l++) {
+      const int px = tx * RT_W + l % RT_W, py = ty * RT_W + l / RT_W;
+      if (!(px < W && py < H)) continue;
+      const size_t pix = (size_t)py * W + px;
+      const float pcx = px + 0.5f, pcy = py + 0.5f;
+      const float zr = ref_z ? ref_z[pix] : INFINITY;
+      float T = 1.f, z_first = INFINITY, deep = 0.f, behind = 0.f, zsum = 0.f;
+      for (uint32_t idx = rx; idx < ry; idx++) {
+        const uint32_t gid = vals_sorted[idx];
+        const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
+        const float sigma = frag_sigma(pcx - a[0], pcy - a[1], a[2], a[3], c[0]);
+        if (sigma < 0.f || sigma > c[3]) continue;
+        const float alpha = fminf(ALPHA_MAX, c[1] * expf(-sigma));
+        const float next_T = T * (1.f - alpha);
+        if (next_T <= T_CUTOFF) break;
+        const float vis = alpha * T, z = c[2];
+        if (finitef(z_first) && z > z_first + delta) deep += vis;
+        if (z > zr + margin) behind += vis;
+        if (mean_mode) zsum = fmaf(vis, z, zsum);
+        T = next_T;
+        if (!finitef(z_first) && 1.f - T >= tau) z_first = z;
+      }
+      if (mean_mode) z_first = (1.f - T) > 0.05f ? zsum / (1.f - T) : INFINITY;
+      out[pix * 4] = 1.f - T;
+      out[pix * 4 + 1] = z_first;
+      out[pix * 4 + 2] = deep;
+      out[pix * 4 + 3] = behind;
+    }
+  }
+}
+
+/* ------------------------------------------------------------------------------------------------
  * Exports of internal pieces so the tests can pin them against closed forms.
  * ---------------------------------------------------------------------------------------------- */
 void orc_sh_basis_f(int deg, float x, float y, float z, float* out) { sh_basis_f(deg, x, y, z, out); }

@@ -140,6 +140,21 @@ double orc_hollow_sum(int npix, const float* pen);
 /* loss.cu:240-286: sums of the squared error and of SSIM over pixels and channels. */
 void orc_eval(int W, int H, const float* pred, const uint32_t* gt, int mask_weighted, double* sum_se, double* sum_ssim);
 
+#define ORC_LABEL_BINS 32 /* evidence.cu:38 */
+/* evidence_kernel and label_vote_kernel (evidence.cu:47-112, 141-183) of one rendered view, given the forward's
+ * tile_ranges, out_rgba [P][4], out_feat [P][3] (read when normals and normal_weight > 0) and last_idx:
+ * view_acc [n][3] += (w_in, err, w_all) and, when labels and label_acc are given, label_acc [n][32] += the
+ * per-class weight. Caller zeroes. */
+void orc_evidence_view(int W, int H, int tiles_x, int tiles_y, const uint32_t* tile_ranges, const uint32_t* vals_sorted,
+                       const float* proj0, const float* proj1, const float* out_rgba, const float* out_feat,
+                       const uint32_t* last_idx, const uint32_t* gt, const uint32_t* normals, const uint8_t* weights,
+                       const uint8_t* labels, int masked_has_alpha, float normal_weight, double* view_acc,
+                       double* label_acc);
+/* probe_kernel (probe.cu:7-45): out [P][4] = (A, z_first, deep, behind); ref_z may be NULL. */
+void orc_probe(int W, int H, int tiles_x, int tiles_y, const uint32_t* tile_ranges, const uint32_t* vals_sorted,
+               const float* proj0, const float* proj1, float tau, float delta, const float* ref_z, float margin,
+               float* out);
+
 /* optim.cu:99-253 + grad_out (292-296): projection VJP, fp32. grad_out [n][11 + 3K]. */
 void orc_vjp(const orc_model_t* m, const orc_cam_t* cam, int active_deg, const float* v_splat,
              const uint32_t* vis_flag, const uint32_t* tile_count, float* grad_out);
