@@ -77,6 +77,20 @@ class StepTimes(C.Structure):
         return {k: float(getattr(self, k)) for k, _ in self._fields_}
 
 
+PLY_FIELDS = ["pos", "log_scale", "quat", "opacity", "sh", "evidence", "labels", "fill", "gate", "gate_s", "open"]
+PLY_BLOCKS = {"evidence": 7, "labels": 2, "fill": 1, "gate": 2, "gate_s": 1, "open": 4}
+
+
+class PlyInfo(C.Structure):
+    _fields_ = [("n", C.c_int64), ("sh_degree", C.c_int), ("binary", C.c_int)] + \
+               [(f, C.c_int) for f in ("has_scales", "has_evidence", "has_labels", "has_fill", "has_gate",
+                                       "has_gate_s", "has_open")]
+
+
+class PlyArrays(C.Structure):
+    _fields_ = [(f, C.c_void_p) for f in PLY_FIELDS]
+
+
 # Every symbol include/b2c.h and include/b2c_kernels.h declare.
 EXPORTS = [
     "b2c_last_error", "b2c_get_device_count", "b2c_camera_gpu_from", "b2c_model_create", "b2c_model_destroy",
@@ -99,6 +113,8 @@ EXPORTS = [
     "b2c_view_set_labels", "b2c_view_set_flags", "b2c_compute_evidence", "b2c_download_evidence",
     "b2c_download_labels", "b2c_probe_depth", "b2c_device_download", "b2c_hip_evidence_view",
     "b2c_hip_evidence_fold", "b2c_hip_probe_depth",
+    "b2c_ply_info_get", "b2c_ply_read", "b2c_ply_write", "b2c_ply_is_vertex_only", "b2c_ply_comments",
+    "b2c_model_load_ply", "b2c_model_save_ply", "b2c_hip_ply_decode", "b2c_hip_ply_encode",
 ]
 
 _lib = None
@@ -165,6 +181,13 @@ def lib():
         L.b2c_download_labels.argtypes = [p, p]
         L.b2c_probe_depth.argtypes = [p, f, f, p, f, p]
         L.b2c_device_download.argtypes = [p, p, C.c_size_t]
+        L.b2c_ply_info_get.argtypes = [C.c_char_p, C.POINTER(PlyInfo)]
+        L.b2c_ply_read.argtypes = [C.c_char_p, C.POINTER(PlyArrays)]
+        L.b2c_ply_write.argtypes = [C.c_char_p, C.POINTER(PlyInfo), C.POINTER(PlyArrays), C.c_char_p]
+        L.b2c_ply_is_vertex_only.argtypes = [C.c_char_p]
+        L.b2c_ply_comments.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]
+        L.b2c_model_load_ply.argtypes = [p, C.c_char_p, i, C.POINTER(i)]
+        L.b2c_model_save_ply.argtypes = [p, C.c_char_p, C.c_char_p, C.POINTER(PlyInfo), C.POINTER(PlyArrays)]
         L.b2c_radix_sort_temp_bytes.restype = C.c_size_t
         L.b2c_radix_sort_temp_bytes.argtypes = [C.c_uint32]
         L.b2c_scan_temp_bytes.restype = C.c_size_t
@@ -201,6 +224,67 @@ def camera_gpu_from(cam, W=None, H=None) -> dict:
                 fx=np.float32(g.fx), fy=np.float32(g.fy), cx=np.float32(g.cx), cy=np.float32(g.cy), W=g.W, H=g.H,
                 lim_pos_x=np.float32(g.lim_pos_x), lim_pos_y=np.float32(g.lim_pos_y),
                 lim_neg_x=np.float32(g.lim_neg_x), lim_neg_y=np.float32(g.lim_neg_y))
+
+
+def _ply_arrays(arrs):
+    pa = PlyArrays()
+    for f in PLY_FIELDS:
+        a = arrs.get(f)
+        setattr(pa, f, None if a is None else a.ctypes.data)
+    return pa
+
+
+def ply_info(path) -> dict:
+    """read_ply's view of a file without its rows: n, sh_degree, binary and the has_* flags."""
+    info = PlyInfo()
+    check(lib().b2c_ply_info_get(os.fsencode(path), C.byref(info)), "ply_info")
+    return {f: (int(getattr(info, f)) if f in ("n", "sh_degree") else bool(getattr(info, f))) for f, _ in info._fields_}
+
+
+def ply_read(path) -> dict:
+    """read_ply on the host: a cloud dict (pos, log_scale, quat, opacity, sh [n][K][3], the optional blocks)."""
+    info = ply_info(path)
+    n, K = info["n"], (info["sh_degree"] + 1) ** 2
+    c = dict(n=n, sh_degree=info["sh_degree"], has_scales=info["has_scales"],
+             pos=np.zeros((n, 3), np.float32), log_scale=np.zeros((n, 3), np.float32),
+             quat=np.zeros((n, 4), np.float32), opacity=np.zeros(n, np.float32), sh=np.zeros((n, K, 3), np.float32))
+    for b, w in PLY_BLOCKS.items():
+        if info["has_" + b]:
+            c[b] = np.zeros((n, w) if w > 1 else n, np.float32)
+    check(lib().b2c_ply_read(os.fsencode(path), C.byref(_ply_arrays(c))), "ply_read")
+    return c
+
+
+def _ply_desc(c):
+    d = PlyInfo()
+    d.n, d.sh_degree, d.binary = int(c["n"]), int(c["sh_degree"]), 1
+    for b in PLY_BLOCKS:
+        setattr(d, "has_" + b, int(b in c))
+    arrs = {f: np.ascontiguousarray(c[f], np.float32) for f in PLY_FIELDS if f in c}
+    return d, arrs
+
+
+def ply_write(path, c, comments=()):
+    """write_ply of a cloud dict (see ply_read)."""
+    d, arrs = _ply_desc(c)
+    cm = "\n".join(comments).encode() if comments else None
+    check(lib().b2c_ply_write(os.fsencode(path), C.byref(d), C.byref(_ply_arrays(arrs)), cm), "ply_write")
+
+
+def ply_is_vertex_only(path) -> bool:
+    r = lib().b2c_ply_is_vertex_only(os.fsencode(path))
+    if r < 0:
+        raise RuntimeError(lib().b2c_last_error().decode())
+    return bool(r)
+
+
+def ply_comments(path) -> list:
+    need = C.c_size_t()
+    check(lib().b2c_ply_comments(os.fsencode(path), None, 0, C.byref(need)), "ply_comments")
+    buf = C.create_string_buffer(need.value)
+    check(lib().b2c_ply_comments(os.fsencode(path), buf, need.value, None), "ply_comments")
+    text = buf.value.decode("latin-1")
+    return text.split("\n") if text else []
 
 
 def device_count() -> int:
@@ -309,6 +393,7 @@ class Renderer:
         if floor is None and scene.lscale[:, 3].any():  # the scene's own Mip-Splatting floor
             floor = scene.lscale[:, 3]
         fl = None if floor is None else np.ascontiguousarray(floor, np.float32)
+        self.sh_fp16 = bool(scene.sh_fp16)
         check(self.L.b2c_model_upload(self.model, n, scene.degree, int(scene.sh_fp16), *[_ptr(a) for a in arrs], _ptr(fl)),
               "model_upload")
         self.n = n
@@ -449,6 +534,28 @@ class Renderer:
                                     C.byref(t) if timed else None), "train_step")
         return t.as_dict() if timed else None
 
+    # -- ply
+    def load_ply(self, path, sh_fp16=False):
+        """Replace the model by a ply file, decoded on the device (b2c_model_load_ply); sizes the context for
+        it. Returns the file's has_scales."""
+        hs = C.c_int(0)
+        check(self.L.b2c_model_load_ply(self.model, os.fsencode(path), int(sh_fp16), C.byref(hs)), "model_load_ply")
+        info = ply_info(path)
+        self.n, self.degree, self.sh_fp16 = info["n"], info["sh_degree"], bool(sh_fp16)
+        check(self.L.b2c_ctx_setup(self.ctx, self.W, self.H, max(self.n, 1)), "ctx_setup")
+        return bool(hs.value)
+
+    def save_ply(self, path, comments=(), extras=None):
+        """write_ply of the model, encoded on the device (b2c_model_save_ply); extras: a dict of optional
+        blocks (evidence, labels, fill, gate, gate_s, open) with [n] rows."""
+        cm = "\n".join(comments).encode() if comments else None
+        if extras:
+            d, arrs = _ply_desc(dict(extras, n=self.n, sh_degree=self.degree))
+            check(self.L.b2c_model_save_ply(self.model, os.fsencode(path), cm, C.byref(d), C.byref(_ply_arrays(arrs))),
+                  "model_save_ply")
+        else:
+            check(self.L.b2c_model_save_ply(self.model, os.fsencode(path), cm, None, None), "model_save_ply")
+
     # -- tile-list replays
     def compute_evidence(self, views, cams, normal_weight=0.0, export_labels=False, download=True):
         """compute_evidence over View objects and their cameras; returns download_evidence [n][7] (None
@@ -555,7 +662,7 @@ class Renderer:
         st["v_sh"] = self.read_model("v_sh")
         st["last_step"] = self.read_model("last_step")
         K = (self.degree + 1) ** 2
-        hi, mhi = self._band_names(self.scene.sh_fp16)
+        hi, mhi = self._band_names(self.sh_fp16)
         for key, dc, bands in (("sh", "sh_dc", hi), ("m_sh", "m_sh_dc", mhi)):
             flat = np.zeros((self.n, 3 * K), np.float32)
             flat[:, :3] = self._planar(dc)[0]
@@ -567,7 +674,7 @@ class Renderer:
     def set_model_state(self, st):
         """Write back what model_state returns (any subset of its keys)."""
         K = (self.degree + 1) ** 2
-        hi, mhi = self._band_names(self.scene.sh_fp16)
+        hi, mhi = self._band_names(self.sh_fp16)
         for f, a in st.items():
             if f in ("sh", "m_sh"):
                 flat = np.asarray(a, np.float32).reshape(self.n, 3 * K)

@@ -9,7 +9,7 @@
 
 namespace b2c {
 
-void SplatCloud::resize(size_t count, int degree) {  // src/ply.cpp:15-22: zeros, identity rotations
+void SplatCloud::resize(size_t count, int degree) {
   n = count;
   sh_degree = degree;
   pos.assign(n * 3, 0.f);
@@ -18,6 +18,15 @@ void SplatCloud::resize(size_t count, int degree) {  // src/ply.cpp:15-22: zeros
   opacity.assign(n, 0.f);
   sh.assign(n * (size_t)K() * 3, 0.f);
   for (size_t i = 0; i < n; i++) quat[i * 4] = 1.f;
+  const auto block = [&](bool on, std::vector<float>& v, size_t per, float fill_value) {
+    if (on) v.assign(n * per, fill_value);
+  };
+  block(has_evidence, evidence, 7, 0.f);
+  block(has_labels, labels, 2, 0.f);
+  block(has_fill, fill, 1, 0.f);
+  block(has_gate, gate, 2, -1.f);
+  block(has_gate_s, gate_s, 1, 0.f);
+  block(has_open, open, 4, 0.f);
 }
 
 uint16_t float_to_half_rne(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
@@ -100,9 +109,9 @@ void Model::reserve(int want, hipStream_t stream) {
   cap = grown;
 }
 
-void Model::upload(const SplatCloud& c, hipStream_t stream, const float* floor) {
-  degree = c.sh_degree;
-  n = (int)c.n;
+void Model::reset(int count, int deg, hipStream_t stream) {
+  degree = deg;
+  n = count;
   cap = 0;
   for (DevBuf<float4>* f : {&pos_op, &quat, &lscale, &m_pos_op, &v_pos_op, &m_quat, &v_quat, &m_lscale, &v_lscale})
     f->free();
@@ -111,6 +120,10 @@ void Model::upload(const SplatCloud& c, hipStream_t stream, const float* floor) 
   for (DevBuf<float>* st : {&refine_norm, &max_screen, &vis_count, &vis_weight, &v_sh}) st->free();
   last_step.free();
   reserve(std::max(n, 1), stream);
+}
+
+void Model::upload(const SplatCloud& c, hipStream_t stream, const float* floor) {
+  reset((int)c.n, c.sh_degree, stream);
   CloudStage stage(c.n, K(), floor != nullptr);
   to_device(stage.fields.pos, c.pos, stream);
   to_device(stage.fields.log_scale, c.log_scale, stream);

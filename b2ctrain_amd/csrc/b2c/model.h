@@ -16,7 +16,9 @@ namespace b2c {
 constexpr float SH_C0 = 0.28209479177387814f;
 inline int sh_coeffs_for_degree(int d) { return (d + 1) * (d + 1); }
 
-// Host-side splat cloud in brush's parameterisation (src/ply.h:10-42, the fields the rasterizer uses).
+// Host-side splat cloud in brush's parameterisation (src/ply.h:10-42): the fields the rasterizer uses and
+// the optional per-splat blocks a ply carries beside them (the evidence and label exports, the cage
+// fields), which the model does not hold.
 struct SplatCloud {
   size_t n = 0;
   int sh_degree = 0;
@@ -25,8 +27,23 @@ struct SplatCloud {
   std::vector<float> quat;       // [n][4] (w, x, y, z)
   std::vector<float> opacity;    // [n] logit
   std::vector<float> sh;         // [n][K][3] coefficient-major
+  bool has_scales = true;        // false: the file had no scale_* (a point cloud; scales to be initialised)
+  bool has_evidence = false;
+  std::vector<float> evidence;   // [n][7] w_in, w_all, err, views, dir xyz (download_evidence)
+  bool has_labels = false;
+  std::vector<float> labels;     // [n][2] class id, share (download_labels)
+  bool has_fill = false;
+  std::vector<float> fill;       // [n] cage_fill
+  bool has_gate = false;
+  std::vector<float> gate;       // [n][2] cage_gate_a, cage_gate_b (-1 when absent)
+  bool has_gate_s = false;
+  std::vector<float> gate_s;     // [n] cage_gate_s
+  bool has_open = false;
+  std::vector<float> open;       // [n][4] open_r, open_g, open_b, open_dopacity
   int K() const { return sh_coeffs_for_degree(sh_degree); }
-  void resize(size_t count, int degree);  // src/ply.cpp:15-22: zero, identity quaternions
+  // src/ply.cpp:15-22: every array sized for `count` splats and zeroed, identity quaternions, the gate
+  // pair -1; the optional blocks sized only when their flag is set.
+  void resize(size_t count, int degree);
 };
 
 // Planar SH view handed to the kernels (ShBuf, util.cuh:129-164).
@@ -70,6 +87,9 @@ struct Model {
   // Capacity for `want` splats, doubling from 1024 (the reference's growth policy, model.cu:8-42); the
   // first n splats keep their values, planar slots past n read as zero.
   void reserve(int want, hipStream_t stream = nullptr);
+  // Drop every array and size the model for `count` splats of SH degree `deg` (contents undefined until
+  // written: upload and the ply loader fill them, then zero the statistics and the optimizer state).
+  void reset(int count, int deg, hipStream_t stream = nullptr);
   // Replace the model by a cloud (model.cu:44-80): bands rounded to nearest even when stored as fp16,
   // statistics zeroed, lscale.w = floor[i] (0 without a floor, as the reference uploads).
   void upload(const SplatCloud& c, hipStream_t stream = nullptr, const float* floor = nullptr);

@@ -10,6 +10,7 @@
 #include "b2c/evidence.h"
 #include "b2c/loss.h"
 #include "b2c/optim.h"
+#include "b2c/ply.h"
 #include "b2c/render.h"
 
 struct b2c_model {
@@ -435,6 +436,139 @@ int b2c_device_download(void* host, const void* dev, size_t bytes) {
   return guarded([&] {
     HIP_CHECK(hipDeviceSynchronize());
     if (bytes) HIP_CHECK(hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost));
+  });
+}
+
+extern "C++" {
+namespace {
+std::vector<std::string> split_lines(const char* text) {
+  std::vector<std::string> out;
+  if (!text) return out;
+  std::string cur;
+  for (const char* p = text; *p; p++) {
+    if (*p == '\n') {
+      out.push_back(cur);
+      cur.clear();
+    } else {
+      cur += *p;
+    }
+  }
+  if (!cur.empty()) out.push_back(cur);
+  return out;
+}
+
+void info_of(const b2c::SplatCloud& c, bool binary, b2c_ply_info* out) {
+  out->n = (int64_t)c.n;
+  out->sh_degree = c.sh_degree;
+  out->binary = binary;
+  out->has_scales = c.has_scales;
+  out->has_evidence = c.has_evidence;
+  out->has_labels = c.has_labels;
+  out->has_fill = c.has_fill;
+  out->has_gate = c.has_gate;
+  out->has_gate_s = c.has_gate_s;
+  out->has_open = c.has_open;
+}
+
+// The optional blocks of a cloud, flagged by desc, copied from host arrays.
+void extras_from(const b2c_ply_info* desc, const b2c_ply_arrays* in, b2c::SplatCloud& c) {
+  if (!desc || !in) return;
+  const auto take = [&](int flag, float* src, bool& has, std::vector<float>& dst, size_t width) {
+    has = flag != 0;
+    if (!has) return;
+    if (!src) throw std::runtime_error("ply: a flagged optional block has no array");
+    dst.assign(src, src + c.n * width);
+  };
+  take(desc->has_evidence, in->evidence, c.has_evidence, c.evidence, 7);
+  take(desc->has_labels, in->labels, c.has_labels, c.labels, 2);
+  take(desc->has_fill, in->fill, c.has_fill, c.fill, 1);
+  take(desc->has_gate, in->gate, c.has_gate, c.gate, 2);
+  take(desc->has_gate_s, in->gate_s, c.has_gate_s, c.gate_s, 1);
+  take(desc->has_open, in->open, c.has_open, c.open, 4);
+}
+}  // namespace
+}  // extern "C++"
+
+int b2c_ply_info_get(const char* path, b2c_ply_info* out) {
+  return guarded([&] { info_of(b2c::read_ply_shape(path), b2c::read_ply_header(path).binary, out); });
+}
+
+int b2c_ply_read(const char* path, const b2c_ply_arrays* out) {
+  return guarded([&] {
+    const b2c::SplatCloud c = b2c::read_ply(path);
+    const auto give = [](float* dst, const std::vector<float>& v) {
+      if (dst && !v.empty()) std::memcpy(dst, v.data(), v.size() * sizeof(float));
+    };
+    give(out->pos, c.pos);
+    give(out->log_scale, c.log_scale);
+    give(out->quat, c.quat);
+    give(out->opacity, c.opacity);
+    give(out->sh, c.sh);
+    give(out->evidence, c.evidence);
+    give(out->labels, c.labels);
+    give(out->fill, c.fill);
+    give(out->gate, c.gate);
+    give(out->gate_s, c.gate_s);
+    give(out->open, c.open);
+  });
+}
+
+int b2c_ply_write(const char* path, const b2c_ply_info* desc, const b2c_ply_arrays* in, const char* comments) {
+  return guarded([&] {
+    if (desc->n < 0 || desc->sh_degree < 0 || desc->sh_degree > 4) throw std::runtime_error("ply_write: bad n or degree");
+    b2c::SplatCloud c;
+    c.resize((size_t)desc->n, desc->sh_degree);
+    const auto copy = [&](std::vector<float>& dst, const float* src) {
+      if (!src) throw std::runtime_error("ply_write: missing a base array");
+      std::memcpy(dst.data(), src, dst.size() * sizeof(float));
+    };
+    copy(c.pos, in->pos);
+    copy(c.log_scale, in->log_scale);
+    copy(c.quat, in->quat);
+    copy(c.opacity, in->opacity);
+    copy(c.sh, in->sh);
+    extras_from(desc, in, c);
+    b2c::write_ply(path, c, split_lines(comments));
+  });
+}
+
+int b2c_ply_is_vertex_only(const char* path) {
+  int r = -1;
+  const int rc = guarded([&] { r = b2c::ply_is_vertex_only(path) ? 1 : 0; });
+  return rc ? -1 : r;
+}
+
+int b2c_ply_comments(const char* path, char* buf, size_t cap, size_t* needed) {
+  return guarded([&] {
+    std::string all;
+    for (const std::string& c : b2c::read_ply_comments(path)) {
+      if (!all.empty()) all += '\n';
+      all += c;
+    }
+    if (needed) *needed = all.size() + 1;
+    if (buf && cap) {
+      const size_t k = std::min(cap - 1, all.size());
+      std::memcpy(buf, all.data(), k);
+      buf[k] = 0;
+    }
+  });
+}
+
+int b2c_model_load_ply(b2c_model* m, const char* path, int sh_fp16, int* has_scales) {
+  return guarded([&] {
+    m->m.sh_fp16 = sh_fp16 != 0;
+    const bool s = b2c::load_ply(m->m, path, nullptr);
+    if (has_scales) *has_scales = s;
+  });
+}
+
+int b2c_model_save_ply(const b2c_model* m, const char* path, const char* comments, const b2c_ply_info* extras_desc,
+                       const b2c_ply_arrays* extras) {
+  return guarded([&] {
+    b2c::SplatCloud x;
+    x.n = (size_t)m->m.n;
+    extras_from(extras_desc, extras, x);
+    b2c::save_ply(m->m, path, split_lines(comments), extras_desc ? &x : nullptr, nullptr);
   });
 }
 

@@ -127,6 +127,37 @@ void* b2c_device_upload(const void* host, size_t bytes);
 int b2c_device_download(void* host, const void* dev, size_t bytes);
 void b2c_device_free(void* p);
 
+/* ---- Splat clouds in brush's ply layout (src/ply.h:12-49) ---- */
+typedef struct b2c_ply_info {
+  int64_t n;
+  int sh_degree;
+  int binary; /* binary_little_endian (else ascii) */
+  int has_scales, has_evidence, has_labels, has_fill, has_gate, has_gate_s, has_open;
+} b2c_ply_info;
+/* Host arrays of a cloud (SplatCloud's, coefficient-major SH [n][K][3]); NULL skips an array on read and
+ * marks an optional block absent on write. */
+typedef struct b2c_ply_arrays {
+  float *pos, *log_scale, *quat, *opacity, *sh;
+  float *evidence, *labels, *fill, *gate, *gate_s, *open;
+} b2c_ply_arrays;
+/* read_ply's view of a file without reading the rows: count, degree, flags (and its errors). */
+int b2c_ply_info_get(const char* path, b2c_ply_info* out);
+/* read_ply (src/ply.cpp:85-170) into caller-sized host arrays. */
+int b2c_ply_read(const char* path, const b2c_ply_arrays* out);
+/* write_ply (src/ply.cpp:180-226): desc gives n, sh_degree and the has_* flags of the optional blocks;
+ * comments is '\n'-separated (or NULL). */
+int b2c_ply_write(const char* path, const b2c_ply_info* desc, const b2c_ply_arrays* in, const char* comments);
+/* ply_is_vertex_only (src/ply.cpp:63-83): 1 or 0 (-1 on an internal error). */
+int b2c_ply_is_vertex_only(const char* path);
+/* read_ply_comments joined by '\n' into buf (truncated to cap - 1 bytes; *needed = full length + 1). */
+int b2c_ply_comments(const char* path, char* buf, size_t cap, size_t* needed);
+/* Device-direct ply load into a model (Model::upload of read_ply without the host cloud; the rows are
+ * decoded on the GPU) and save (write_ply of the model, rows encoded on the GPU). extras: optional blocks
+ * as host arrays, flagged in extras_desc (both may be NULL). */
+int b2c_model_load_ply(b2c_model* m, const char* path, int sh_fp16, int* has_scales);
+int b2c_model_save_ply(const b2c_model* m, const char* path, const char* comments, const b2c_ply_info* extras_desc,
+                       const b2c_ply_arrays* extras);
+
 /* compute_evidence / download_evidence / download_labels (src/train/evidence.h:10-22) over nviews views and
  * their cameras: the evidence [n][7] = (w_in, w_all, err, views, dir xyz) and, with export_labels, the label
  * vote [n][2] = (winning class, share). Synchronous; the accumulators are module-level, as the reference's. */

@@ -425,6 +425,46 @@ int b2c_hip_planar_regrow(const void* src, void* dst, int elem_bytes, int lanes,
 /* lscale[i].w = floor_[i] for i < n (the frozen Mip-Splatting floor). */
 int b2c_hip_model_set_floor(float* lscale, const float* floor_, int n, hipStream_t stream);
 
+/* ---- PLY rows <-> model (replaces the per-row loops of src/ply.cpp:127-160 and 188-224) ----
+ * A binary little-endian ply's vertex rows are decoded on the device straight into the model layout, and
+ * the model is encoded into the rows write_ply lays out. Targets of the decode, in this order:
+ * x y z, scale_0..2, rot_0..3, opacity, f_dc_0..2, the colour fallback (red/r, green/g, blue/b), then
+ * f_rest_0 .. f_rest_(3(K-1)-1) (channel-major: every red band, then green, then blue). */
+#define B2C_PLY_T_POS 0
+#define B2C_PLY_T_SCALE 3
+#define B2C_PLY_T_ROT 6
+#define B2C_PLY_T_OPACITY 10
+#define B2C_PLY_T_DC 11
+#define B2C_PLY_T_RGB 14
+#define B2C_PLY_T_REST 17
+#define B2C_PLY_TARGETS (B2C_PLY_T_REST + 72) /* SH degree 4: 3 x 24 rest coefficients */
+/* Property types (src/ply.cpp:27-36). */
+enum { B2C_PLY_F32 = 0, B2C_PLY_F64, B2C_PLY_U8, B2C_PLY_I8, B2C_PLY_U16, B2C_PLY_I16, B2C_PLY_U32, B2C_PLY_I32 };
+
+typedef struct b2c_ply_decode_args {
+  const uint8_t* rows; /* `count` rows of row_bytes each (readable for 4 bytes past the last row) */
+  uint32_t row_bytes;
+  int count, first; /* the rows are model splats first .. first + count - 1 */
+  int16_t col[B2C_PLY_TARGETS]; /* byte offset of each target within a row, -1 = absent (its default) */
+  uint8_t type[B2C_PLY_TARGETS];
+  int rgb_dc;        /* 1: no f_dc_*; DC = ((colour * rgb_scale) - 0.5) / SH_C0 in double */
+  double rgb_scale;  /* 1/255 for uchar, 1/65535 for ushort, else 1 (the red column's type) */
+  b2c_model_dev model; /* n = the whole file's splat count; sh_lanes = 3K */
+} b2c_ply_decode_args;
+int b2c_hip_ply_decode(const b2c_ply_decode_args* a, hipStream_t stream);
+
+/* Rows of write_ply's layout for model splats first .. first + count - 1: x y z, scale_0..2, opacity,
+ * the unit quaternion (identity when its norm is not above 1e-32), f_dc_0..2, f_rest channel-major, then
+ * the optional blocks from device arrays (NULL = not written): evidence [n][7], labels [n][2], fill [n],
+ * gate [n][2], gate_s [n], open [n][4]. row_floats must equal the count of written columns. */
+typedef struct b2c_ply_encode_args {
+  b2c_model_dev model;
+  int count, first, row_floats;
+  const float *evidence, *labels, *fill, *gate, *gate_s, *open;
+  float* rows; /* [count][row_floats] */
+} b2c_ply_encode_args;
+int b2c_hip_ply_encode(const b2c_ply_encode_args* a, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

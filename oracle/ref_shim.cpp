@@ -68,3 +68,92 @@ extern "C" double ref_reference_loss_ext(int n, int degree, const float* pos, co
   }
   return reference_loss(c, p);
 }
+
+// ---- The reference's ply reader and writer (src/ply.cpp), for the ply fixtures under tests/golden/ply/ ----
+// Each returns 0, or 1 with the reference's error message in err (cap bytes).
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "ply.h"
+
+namespace {
+int ply_error(const std::exception& e, char* err, size_t cap) {
+  if (err && cap) {
+    std::strncpy(err, e.what(), cap - 1);
+    err[cap - 1] = 0;
+  }
+  return 1;
+}
+}  // namespace
+
+// flags: has_scales, has_evidence, has_labels, has_fill, has_gate, has_gate_s, has_open
+extern "C" int ref_ply_info(const char* path, long long* n, int* degree, int* flags, char* err, size_t cap) {
+  try {
+    const b2c::SplatCloud c = b2c::read_ply(path);
+    *n = (long long)c.n;
+    *degree = c.sh_degree;
+    const bool f[7] = {c.has_scales, c.has_evidence, c.has_labels, c.has_fill, c.has_gate, c.has_gate_s, c.has_open};
+    for (int k = 0; k < 7; k++) flags[k] = f[k];
+    return 0;
+  } catch (const std::exception& e) {
+    return ply_error(e, err, cap);
+  }
+}
+
+// arrays: pos, log_scale, quat, opacity, sh, evidence, labels, fill, gate, gate_s, open (NULL = skip)
+extern "C" int ref_ply_read(const char* path, float** arrays, char* err, size_t cap) {
+  try {
+    const b2c::SplatCloud c = b2c::read_ply(path);
+    const std::vector<float>* src[11] = {&c.pos, &c.log_scale, &c.quat, &c.opacity, &c.sh, &c.evidence,
+                                         &c.labels, &c.fill, &c.gate, &c.gate_s, &c.open};
+    for (int k = 0; k < 11; k++)
+      if (arrays[k] && !src[k]->empty()) std::memcpy(arrays[k], src[k]->data(), src[k]->size() * sizeof(float));
+    return 0;
+  } catch (const std::exception& e) {
+    return ply_error(e, err, cap);
+  }
+}
+
+// flags as ref_ply_info (has_scales ignored); comments '\n'-separated or NULL
+extern "C" int ref_ply_write(const char* path, long long n, int degree, const int* flags, float* const* arrays,
+                             const char* comments, char* err, size_t cap) {
+  try {
+    b2c::SplatCloud c;
+    c.has_evidence = flags[1]; c.has_labels = flags[2]; c.has_fill = flags[3]; c.has_gate = flags[4];
+    c.has_gate_s = flags[5]; c.has_open = flags[6];
+    c.resize((size_t)n, degree);
+    std::vector<float>* dst[11] = {&c.pos, &c.log_scale, &c.quat, &c.opacity, &c.sh, &c.evidence,
+                                   &c.labels, &c.fill, &c.gate, &c.gate_s, &c.open};
+    for (int k = 0; k < 11; k++)
+      if (arrays[k] && !dst[k]->empty()) std::memcpy(dst[k]->data(), arrays[k], dst[k]->size() * sizeof(float));
+    std::vector<std::string> cm;
+    if (comments) {
+      std::string cur;
+      for (const char* p = comments; *p; p++) {
+        if (*p == '\n') { cm.push_back(cur); cur.clear(); } else { cur += *p; }
+      }
+      if (!cur.empty()) cm.push_back(cur);
+    }
+    b2c::write_ply(path, c, cm);
+    return 0;
+  } catch (const std::exception& e) {
+    return ply_error(e, err, cap);
+  }
+}
+
+extern "C" int ref_ply_is_vertex_only(const char* path) { return b2c::ply_is_vertex_only(path) ? 1 : 0; }
+
+extern "C" int ref_ply_comments(const char* path, char* buf, size_t cap) {
+  std::string all;
+  for (const std::string& s : b2c::read_ply_comments(path)) {
+    if (!all.empty()) all += '\n';
+    all += s;
+  }
+  if (cap) {
+    const size_t k = std::min(cap - 1, all.size());
+    std::memcpy(buf, all.data(), k);
+    buf[k] = 0;
+  }
+  return (int)all.size();
+}
