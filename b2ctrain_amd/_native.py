@@ -87,6 +87,17 @@ class PlyInfo(C.Structure):
                                        "has_gate_s", "has_open")]
 
 
+class DatasetOpts(C.Structure):
+    _fields_ = [("source", C.c_char_p), ("max_frames", C.c_int), ("max_resolution", C.c_uint),
+                ("eval_split_every", C.c_int), ("subsample_frames", C.c_int), ("alpha_mode", C.c_int)]
+
+
+class ViewInfo(C.Structure):
+    _fields_ = [("w", C.c_int), ("h", C.c_int), ("cam", Camera), ("has_alpha", C.c_int), ("masked", C.c_int),
+                ("has_normals", C.c_int), ("has_weights", C.c_int), ("has_labels", C.c_int),
+                ("alpha_coverage", C.c_float), ("normal_mask_count", C.c_double), ("name", C.c_char * 256)]
+
+
 class PlyArrays(C.Structure):
     _fields_ = [(f, C.c_void_p) for f in PLY_FIELDS]
 
@@ -115,6 +126,8 @@ EXPORTS = [
     "b2c_hip_evidence_fold", "b2c_hip_probe_depth",
     "b2c_ply_info_get", "b2c_ply_read", "b2c_ply_write", "b2c_ply_is_vertex_only", "b2c_ply_comments",
     "b2c_model_load_ply", "b2c_model_save_ply", "b2c_hip_ply_decode", "b2c_hip_ply_encode",
+    "b2c_png_decode", "b2c_dataset_load", "b2c_dataset_destroy", "b2c_dataset_count", "b2c_dataset_view_info",
+    "b2c_dataset_view_read", "b2c_dataset_view_upload", "b2c_dataset_points", "b2c_dataset_summary",
 ]
 
 _lib = None
@@ -188,6 +201,18 @@ def lib():
         L.b2c_ply_comments.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]
         L.b2c_model_load_ply.argtypes = [p, C.c_char_p, i, C.POINTER(i)]
         L.b2c_model_save_ply.argtypes = [p, C.c_char_p, C.c_char_p, C.POINTER(PlyInfo), C.POINTER(PlyArrays)]
+        L.b2c_png_decode.argtypes = [C.c_char_p, C.POINTER(i), C.POINTER(i), C.POINTER(i), p, C.c_size_t]
+        L.b2c_dataset_load.restype = p
+        L.b2c_dataset_load.argtypes = [C.POINTER(DatasetOpts)]
+        L.b2c_dataset_destroy.argtypes = [p]
+        L.b2c_dataset_destroy.restype = None
+        L.b2c_dataset_count.argtypes = [p, i]
+        L.b2c_dataset_view_info.argtypes = [p, i, i, C.POINTER(ViewInfo)]
+        L.b2c_dataset_view_read.argtypes = [p, i, i, p, p, p, p]
+        L.b2c_dataset_view_upload.restype = p
+        L.b2c_dataset_view_upload.argtypes = [p, i, i]
+        L.b2c_dataset_points.argtypes = [p, p, p, C.POINTER(C.c_int64)]
+        L.b2c_dataset_summary.argtypes = [p, C.c_char_p, C.c_size_t, C.POINTER(i)]
         L.b2c_radix_sort_temp_bytes.restype = C.c_size_t
         L.b2c_radix_sort_temp_bytes.argtypes = [C.c_uint32]
         L.b2c_scan_temp_bytes.restype = C.c_size_t
@@ -285,6 +310,89 @@ def ply_comments(path) -> list:
     check(lib().b2c_ply_comments(os.fsencode(path), buf, need.value, None), "ply_comments")
     text = buf.value.decode("latin-1")
     return text.split("\n") if text else []
+
+
+def png_decode(path):
+    """The loader's PNG decoder: (rgba [h][w][4] uint8, channels in the file)."""
+    w, h, ch = C.c_int(), C.c_int(), C.c_int()
+    check(lib().b2c_png_decode(os.fsencode(path), C.byref(w), C.byref(h), C.byref(ch), None, 0), "png_decode")
+    out = np.zeros((h.value, w.value, 4), np.uint8)
+    check(lib().b2c_png_decode(os.fsencode(path), C.byref(w), C.byref(h), C.byref(ch), _ptr(out), out.nbytes),
+          "png_decode")
+    return out, ch.value
+
+
+class Dataset:
+    """load_dataset through the C ABI (b2c_dataset_*): views by split (0 train, 1 eval)."""
+
+    def __init__(self, source, max_frames=None, max_resolution=1920, eval_split_every=None, subsample_frames=None,
+                 alpha_mode=None):
+        self.L = lib()
+        o = DatasetOpts()
+        o.source = os.fsencode(source)
+        o.max_frames = -1 if max_frames is None else int(max_frames)
+        o.max_resolution = int(max_resolution)
+        o.eval_split_every = -1 if eval_split_every is None else int(eval_split_every)
+        o.subsample_frames = -1 if subsample_frames is None else int(subsample_frames)
+        o.alpha_mode = {None: -1, "masked": 0, "transparent": 1}[alpha_mode]
+        self.ptr = self.L.b2c_dataset_load(C.byref(o))
+        if not self.ptr:
+            raise RuntimeError(self.L.b2c_last_error().decode())
+
+    def count(self, split=0):
+        return self.L.b2c_dataset_count(self.ptr, split)
+
+    def info(self, split, i):
+        v = ViewInfo()
+        check(self.L.b2c_dataset_view_info(self.ptr, split, i, C.byref(v)), "dataset_view_info")
+        return v
+
+    def planes(self, split, i):
+        v = self.info(split, i)
+        P = v.w * v.h
+        out = dict(rgba=np.zeros(P, np.uint32))
+        if v.has_normals:
+            out["normals"] = np.zeros(P, np.uint32)
+        if v.has_weights:
+            out["weights"] = np.zeros(P, np.uint8)
+        if v.has_labels:
+            out["labels"] = np.zeros(P, np.uint8)
+        check(self.L.b2c_dataset_view_read(self.ptr, split, i, *[_ptr(out.get(k)) for k in ("rgba", "normals",
+                                                                                          "weights", "labels")]),
+              "dataset_view_read")
+        return out
+
+    def upload(self, split, i):
+        """A device view (b2c_view handle) of a dataset view."""
+        h = self.L.b2c_dataset_view_upload(self.ptr, split, i)
+        if not h:
+            raise RuntimeError(self.L.b2c_last_error().decode())
+        return h
+
+    def points(self):
+        n = C.c_int64()
+        check(self.L.b2c_dataset_points(self.ptr, None, None, C.byref(n)), "dataset_points")
+        xyz, rgb = np.zeros((n.value, 3), np.float32), np.zeros((n.value, 3), np.uint8)
+        check(self.L.b2c_dataset_points(self.ptr, _ptr(xyz), _ptr(rgb), C.byref(n)), "dataset_points")
+        return xyz, rgb
+
+    def summary(self):
+        buf = C.create_string_buffer(8192)
+        counts = (C.c_int * 5)()
+        check(self.L.b2c_dataset_summary(self.ptr, buf, 8192, counts), "dataset_summary")
+        root, name, init = buf.value.decode().split("\n")
+        return dict(root=root, name=name, init_ply=init, counts=list(counts))
+
+    def close(self):
+        if self.ptr:
+            self.L.b2c_dataset_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def device_count() -> int:

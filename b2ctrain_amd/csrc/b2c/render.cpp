@@ -23,6 +23,16 @@ void Camera::update_pos() {
   pos[2] = -(R[2] * t[0] + R[5] * t[1] + R[8] * t[2]);
 }
 
+void Camera::rescale(int new_w, int new_h) {
+  const float sx = (float)new_w / (float)width, sy = (float)new_h / (float)height;
+  fx *= sx;
+  cx *= sx;
+  fy *= sy;
+  cy *= sy;
+  width = new_w;
+  height = new_h;
+}
+
 CameraGPU CameraGPU::from(const Camera& c, int W, int H) {
   CameraGPU g;
   for (int i = 0; i < 9; i++) g.R[i] = c.R[i];

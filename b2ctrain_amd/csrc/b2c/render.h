@@ -16,6 +16,9 @@ struct Camera {
   float pos[3] = {0, 0, 0};
   void set_w2c_quat(float qw, float qx, float qy, float qz, float tx, float ty, float tz);
   void update_pos();  // pos = -R^T t
+  // Intrinsics for a new image size (camera.h:30-34): fx, cx scaled by new_w / width, fy, cy by new_h / height.
+  void rescale(int new_w, int new_h);
+  float focal_px() const { return 0.5f * (fx + fy); }
 };
 
 struct CameraGPU {

@@ -7,10 +7,12 @@
 #include <map>
 #include <string>
 
+#include "b2c/dataset.h"
 #include "b2c/evidence.h"
 #include "b2c/loss.h"
 #include "b2c/optim.h"
 #include "b2c/ply.h"
+#include "b2c/png.h"
 #include "b2c/render.h"
 
 struct b2c_model {
@@ -24,6 +26,10 @@ struct b2c_ctx {
   int n = 0;
   int degree = 0;
   hipEvent_t ev[8] = {};
+};
+
+struct b2c_dataset {
+  b2c::Dataset ds;
 };
 
 struct b2c_view {
@@ -550,6 +556,140 @@ int b2c_ply_comments(const char* path, char* buf, size_t cap, size_t* needed) {
       const size_t k = std::min(cap - 1, all.size());
       std::memcpy(buf, all.data(), k);
       buf[k] = 0;
+    }
+  });
+}
+
+int b2c_png_decode(const char* path, int* w, int* h, int* channels, uint8_t* rgba, size_t rgba_bytes) {
+  return guarded([&] {
+    const b2c::DecodedImage d = b2c::decode_png(path);
+    *w = d.w;
+    *h = d.h;
+    *channels = d.channels_in_file;
+    if (rgba) {
+      if (rgba_bytes < d.rgba.size()) throw std::runtime_error("png_decode: output buffer too small");
+      std::memcpy(rgba, d.rgba.data(), d.rgba.size());
+    }
+  });
+}
+
+b2c_dataset* b2c_dataset_load(const b2c_dataset_opts* o) {
+  b2c_dataset* d = new b2c_dataset();
+  const int rc = guarded([&] {
+    b2c::DatasetOptions opt;
+    opt.source = o->source ? o->source : "";
+    if (o->max_frames >= 0) opt.max_frames = (uint32_t)o->max_frames;
+    opt.max_resolution = o->max_resolution;
+    if (o->eval_split_every >= 0) opt.eval_split_every = (uint32_t)o->eval_split_every;
+    if (o->subsample_frames >= 0) opt.subsample_frames = (uint32_t)o->subsample_frames;
+    if (o->alpha_mode >= 0) opt.alpha_mode = o->alpha_mode == 0 ? b2c::AlphaMode::Masked : b2c::AlphaMode::Transparent;
+    d->ds = b2c::load_dataset(opt);
+  });
+  if (rc) {
+    delete d;
+    return nullptr;
+  }
+  return d;
+}
+
+void b2c_dataset_destroy(b2c_dataset* d) { delete d; }
+
+int b2c_dataset_count(const b2c_dataset* d, int split) {
+  return split == 0 ? (int)d->ds.train.size() : split == 1 ? (int)d->ds.eval.size() : -1;
+}
+
+extern "C++" {
+namespace {
+const b2c::View& dataset_view(const b2c_dataset* d, int split, int i) {
+  const std::vector<b2c::View>& v = split == 0 ? d->ds.train : d->ds.eval;
+  if ((split != 0 && split != 1) || i < 0 || (size_t)i >= v.size()) throw std::runtime_error("dataset: no such view");
+  return v[(size_t)i];
+}
+}  // namespace
+}  // extern "C++"
+
+int b2c_dataset_view_info(const b2c_dataset* d, int split, int i, b2c_view_info* out) {
+  return guarded([&] {
+    const b2c::View& v = dataset_view(d, split, i);
+    *out = b2c_view_info{};
+    out->w = v.w;
+    out->h = v.h;
+    out->cam.width = v.cam.width;
+    out->cam.height = v.cam.height;
+    out->cam.fx = v.cam.fx;
+    out->cam.fy = v.cam.fy;
+    out->cam.cx = v.cam.cx;
+    out->cam.cy = v.cam.cy;
+    std::copy(v.cam.R, v.cam.R + 9, out->cam.R);
+    std::copy(v.cam.t, v.cam.t + 3, out->cam.t);
+    out->has_alpha = v.has_alpha;
+    out->masked = v.mode == b2c::AlphaMode::Masked;
+    out->has_normals = v.has_normals();
+    out->has_weights = v.has_weights();
+    out->has_labels = v.has_labels();
+    out->alpha_coverage = v.alpha_coverage;
+    out->normal_mask_count = v.normal_mask_count;
+    std::snprintf(out->name, sizeof out->name, "%s", v.name.c_str());
+  });
+}
+
+int b2c_dataset_view_read(const b2c_dataset* d, int split, int i, uint32_t* rgba, uint32_t* normals, uint8_t* weights,
+                          uint8_t* labels) {
+  return guarded([&] {
+    const b2c::View& v = dataset_view(d, split, i);
+    if (rgba) std::copy(v.rgba.begin(), v.rgba.end(), rgba);
+    if (normals) std::copy(v.normals.begin(), v.normals.end(), normals);
+    if (weights) std::copy(v.weights.begin(), v.weights.end(), weights);
+    if (labels) std::copy(v.labels.begin(), v.labels.end(), labels);
+  });
+}
+
+b2c_view* b2c_dataset_view_upload(const b2c_dataset* d, int split, int i) {
+  b2c_view* out = nullptr;
+  const int rc = guarded([&] {
+    const b2c::View& v = dataset_view(d, split, i);
+    out = b2c_view_create(v.w, v.h, v.rgba.data(), v.has_weights() ? v.weights.data() : nullptr);
+    if (!out) throw std::runtime_error(b2c_last_error());
+    if (v.has_normals() && b2c_view_set_normals(out, v.normals.data())) throw std::runtime_error(b2c_last_error());
+    if (v.has_labels() && b2c_view_set_labels(out, v.labels.data())) throw std::runtime_error(b2c_last_error());
+    b2c_view_set_flags(out, v.has_alpha, v.mode == b2c::AlphaMode::Masked, v.alpha_coverage, (float)v.normal_mask_count);
+  });
+  if (rc && out) {
+    b2c_view_destroy(out);
+    out = nullptr;
+  }
+  return out;
+}
+
+int b2c_dataset_points(const b2c_dataset* d, float* xyz, uint8_t* rgb, int64_t* count) {
+  return guarded([&] {
+    const std::vector<b2c::Point3D>& p = d->ds.points;
+    if (count) *count = (int64_t)p.size();
+    for (size_t k = 0; k < p.size(); k++) {
+      if (xyz) {
+        xyz[k * 3] = p[k].x;
+        xyz[k * 3 + 1] = p[k].y;
+        xyz[k * 3 + 2] = p[k].z;
+      }
+      if (rgb) {
+        rgb[k * 3] = p[k].r;
+        rgb[k * 3 + 1] = p[k].g;
+        rgb[k * 3 + 2] = p[k].b;
+      }
+    }
+  });
+}
+
+int b2c_dataset_summary(const b2c_dataset* d, char* buf, size_t cap, int* counts) {
+  return guarded([&] {
+    const std::string s = d->ds.root + "\n" + d->ds.name + "\n" + d->ds.init_ply;
+    if (buf && cap) std::snprintf(buf, cap, "%s", s.c_str());
+    if (counts) {
+      counts[0] = d->ds.n_masked;
+      counts[1] = d->ds.n_transparent;
+      counts[2] = d->ds.n_weighted;
+      counts[3] = d->ds.n_normals;
+      counts[4] = d->ds.n_labels;
     }
   });
 }

@@ -158,6 +158,46 @@ int b2c_model_load_ply(b2c_model* m, const char* path, int sh_fp16, int* has_sca
 int b2c_model_save_ply(const b2c_model* m, const char* path, const char* comments, const b2c_ply_info* extras_desc,
                        const b2c_ply_arrays* extras);
 
+/* ---- COLMAP datasets (src/dataset/views.h:38, colmap.h:30): PNG frames and sidecars at their own size ---- */
+typedef struct b2c_dataset b2c_dataset; /* b2c::Dataset */
+typedef struct b2c_dataset_opts {
+  const char* source;
+  int max_frames;           /* < 0: all */
+  unsigned max_resolution;  /* the reference's default is 1920 */
+  int eval_split_every;     /* < 0: no eval split */
+  int subsample_frames;     /* < 0: every frame */
+  int alpha_mode;           /* -1 per view (masks/ sidecar: masked), 0 masked, 1 transparent */
+} b2c_dataset_opts;
+typedef struct b2c_view_info {
+  int w, h;
+  b2c_camera cam; /* at the loaded resolution */
+  int has_alpha, masked, has_normals, has_weights, has_labels;
+  float alpha_coverage;
+  double normal_mask_count;
+  char name[256];
+} b2c_view_info;
+/* load_dataset (views.cpp:74-253); NULL on failure (message in b2c_last_error). JPEG frames and frames
+ * needing resampling are rejected. */
+b2c_dataset* b2c_dataset_load(const b2c_dataset_opts* o);
+void b2c_dataset_destroy(b2c_dataset* d);
+/* split 0: train, 1: eval. */
+int b2c_dataset_count(const b2c_dataset* d, int split);
+int b2c_dataset_view_info(const b2c_dataset* d, int split, int i, b2c_view_info* out);
+/* The view's packed planes into host arrays of w*h (NULL skips; an absent plane is not written). */
+int b2c_dataset_view_read(const b2c_dataset* d, int split, int i, uint32_t* rgba, uint32_t* normals, uint8_t* weights,
+                          uint8_t* labels);
+/* A device view (ViewGPU) of a dataset view with its planes and flags, ready for the loss and evidence. */
+b2c_view* b2c_dataset_view_upload(const b2c_dataset* d, int split, int i);
+/* points3D.txt: *count points (xyz float [count][3], rgb uint8 [count][3]; NULL arrays to query the count). */
+int b2c_dataset_points(const b2c_dataset* d, float* xyz, uint8_t* rgb, int64_t* count);
+/* root, name and the initial ply path ('\n'-separated) into buf; counts[5] = masked, transparent, weighted,
+ * normals, labels views. */
+int b2c_dataset_summary(const b2c_dataset* d, char* buf, size_t cap, int* counts);
+
+/* The loader's PNG decoder: *w, *h, *channels (in the file) and, when rgba is not NULL, the image as 8-bit
+ * RGBA [h][w][4] (rgba_bytes must hold it). */
+int b2c_png_decode(const char* path, int* w, int* h, int* channels, uint8_t* rgba, size_t rgba_bytes);
+
 /* compute_evidence / download_evidence / download_labels (src/train/evidence.h:10-22) over nviews views and
  * their cameras: the evidence [n][7] = (w_in, w_all, err, views, dir xyz) and, with export_labels, the label
  * vote [n][2] = (winning class, share). Synchronous; the accumulators are module-level, as the reference's. */

@@ -157,3 +157,73 @@ extern "C" int ref_ply_comments(const char* path, char* buf, size_t cap) {
   }
   return (int)all.size();
 }
+
+// ---- The reference's dataset loader (src/dataset/views.cpp, colmap.cpp), for tests/golden/colmap/ ----
+#include "dataset/views.h"
+
+namespace {
+b2c::Dataset g_dataset;
+const b2c::View& dataset_view(int split, int i) { return split == 0 ? g_dataset.train.at(i) : g_dataset.eval.at(i); }
+}  // namespace
+
+// max_frames, eval_every, subsample < 0: unset; alpha_mode -1 unset, 0 masked, 1 transparent
+extern "C" int ref_dataset_load(const char* source, int max_frames, unsigned max_res, int eval_every, int subsample,
+                                int alpha_mode, char* err, size_t cap) {
+  try {
+    b2c::Config cfg;
+    cfg.source = source;
+    if (max_frames >= 0) cfg.max_frames = (uint32_t)max_frames;
+    cfg.max_resolution = max_res;
+    if (eval_every >= 0) cfg.eval_split_every = (uint32_t)eval_every;
+    if (subsample >= 0) cfg.subsample_frames = (uint32_t)subsample;
+    if (alpha_mode >= 0) cfg.alpha_mode = alpha_mode == 0 ? b2c::AlphaMode::Masked : b2c::AlphaMode::Transparent;
+    g_dataset = b2c::load_dataset(cfg);
+    return 0;
+  } catch (const std::exception& e) {
+    return ply_error(e, err, cap);
+  }
+}
+
+extern "C" int ref_dataset_count(int split) { return (int)(split == 0 ? g_dataset.train.size() : g_dataset.eval.size()); }
+
+// ints: w, h, cam width, cam height, has_alpha, masked, has_normals, has_weights, has_labels
+// floats: fx fy cx cy R[9] t[3] pos[3] alpha_coverage
+extern "C" void ref_dataset_view(int split, int i, int* ints, float* floats, double* normal_mask_count, char* name,
+                                 size_t cap) {
+  const b2c::View& v = dataset_view(split, i);
+  const int iv[9] = {v.w, v.h, v.cam.width, v.cam.height, v.has_alpha, v.mode == b2c::AlphaMode::Masked,
+                     v.has_normals(), v.has_weights(), v.has_labels()};
+  for (int k = 0; k < 9; k++) ints[k] = iv[k];
+  floats[0] = v.cam.fx; floats[1] = v.cam.fy; floats[2] = v.cam.cx; floats[3] = v.cam.cy;
+  for (int k = 0; k < 9; k++) floats[4 + k] = v.cam.R[k];
+  for (int k = 0; k < 3; k++) { floats[13 + k] = v.cam.t[k]; floats[16 + k] = v.cam.pos[k]; }
+  floats[19] = v.alpha_coverage;
+  *normal_mask_count = v.normal_mask_count;
+  std::strncpy(name, v.name.c_str(), cap - 1);
+  name[cap - 1] = 0;
+}
+
+extern "C" void ref_dataset_view_arrays(int split, int i, uint32_t* rgba, uint32_t* normals, uint8_t* weights,
+                                        uint8_t* labels) {
+  const b2c::View& v = dataset_view(split, i);
+  std::memcpy(rgba, v.rgba.data(), v.rgba.size() * 4);
+  if (!v.normals.empty()) std::memcpy(normals, v.normals.data(), v.normals.size() * 4);
+  if (!v.weights.empty()) std::memcpy(weights, v.weights.data(), v.weights.size());
+  if (!v.labels.empty()) std::memcpy(labels, v.labels.data(), v.labels.size());
+}
+
+// counts: masked, transparent, weighted, normals, labels; text: root \n name \n init_ply
+extern "C" long long ref_dataset_summary(int* counts, char* text, size_t cap, float* xyz, uint8_t* rgb) {
+  const int c[5] = {g_dataset.n_masked, g_dataset.n_transparent, g_dataset.n_weighted, g_dataset.n_normals,
+                    g_dataset.n_labels};
+  for (int k = 0; k < 5; k++) counts[k] = c[k];
+  const std::string s = g_dataset.root + "\n" + g_dataset.name + "\n" + g_dataset.init_ply;
+  std::strncpy(text, s.c_str(), cap - 1);
+  text[cap - 1] = 0;
+  for (size_t k = 0; k < g_dataset.points.size(); k++) {
+    const b2c::Point3D& p = g_dataset.points[k];
+    if (xyz) { xyz[k * 3] = p.x; xyz[k * 3 + 1] = p.y; xyz[k * 3 + 2] = p.z; }
+    if (rgb) { rgb[k * 3] = p.r; rgb[k * 3 + 1] = p.g; rgb[k * 3 + 2] = p.b; }
+  }
+  return (long long)g_dataset.points.size();
+}
