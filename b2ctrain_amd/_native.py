@@ -123,7 +123,7 @@ EXPORTS = [
     "b2c_hip_hollow_loss", "b2c_hip_eval_metrics", "b2c_hip_step_loss_sums",
     "b2c_view_set_labels", "b2c_view_set_flags", "b2c_compute_evidence", "b2c_download_evidence",
     "b2c_download_labels", "b2c_probe_depth", "b2c_device_download", "b2c_hip_evidence_view",
-    "b2c_hip_evidence_fold", "b2c_hip_probe_depth",
+    "b2c_hip_evidence_sum", "b2c_hip_probe_depth",
     "b2c_ply_info_get", "b2c_ply_read", "b2c_ply_write", "b2c_ply_is_vertex_only", "b2c_ply_comments",
     "b2c_model_load_ply", "b2c_model_save_ply", "b2c_hip_ply_decode", "b2c_hip_ply_encode",
     "b2c_png_decode", "b2c_dataset_load", "b2c_dataset_destroy", "b2c_dataset_count", "b2c_dataset_view_info",

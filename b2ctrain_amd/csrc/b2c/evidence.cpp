@@ -35,7 +35,6 @@ void compute_evidence(RenderCtx& ctx, const Model& m, const std::vector<ViewGPU>
     rp.feat = (use_normals && view.normals) ? FeatureMode::Normals : FeatureMode::None;
     render_forward(ctx, m, rp, stream);
     if (m.n == 0) continue;
-    g_view_acc.zero(stream, (size_t)m.n * 3);
     b2c_evidence_args a{};
     a.tile_ranges = reinterpret_cast<const uint32_t*>(ctx.tile_ranges.ptr);
     a.vals_sorted = ctx.vals_sorted;
@@ -50,11 +49,22 @@ void compute_evidence(RenderCtx& ctx, const Model& m, const std::vector<ViewGPU>
     a.W = ctx.W; a.H = ctx.H; a.tiles_x = ctx.tiles_x; a.tiles_y = ctx.tiles_y;
     a.masked_has_alpha = (view.masked && view.has_alpha) ? 1 : 0;
     a.normal_weight = cfg.evidence_normal_weight;
-    a.view_acc = g_view_acc.ptr;
+    a.slot_sorted = ctx.slot_sorted;
+    a.tile_end = ctx.tile_end;
+    a.num_isect = ctx.num_isect;
+    a.rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);  // the backward's row buffer, free between passes
     a.label_acc = g_labels_valid ? g_labels.ptr : nullptr;
     LAUNCH_CHECK(b2c_hip_evidence_view(&a, stream));
-    LAUNCH_CHECK(b2c_hip_evidence_fold(m.n, g_view_acc.ptr, reinterpret_cast<const float*>(m.pos_op.ptr), cams[v].pos,
-                                       g_evidence.ptr, stream));
+    b2c_evidence_sum_args sa{};
+    sa.n = m.n;
+    sa.m = ctx.num_isect;
+    sa.ids = ctx.vals;
+    sa.rows = a.rows;
+    sa.view_acc = g_view_acc.ptr;
+    sa.pos_op = reinterpret_cast<const float*>(m.pos_op.ptr);
+    for (int k = 0; k < 3; k++) sa.cam_pos[k] = cams[v].pos[k];
+    sa.evidence = g_evidence.ptr;
+    LAUNCH_CHECK(b2c_hip_evidence_sum(&sa, stream));
   }
   HIP_CHECK(hipStreamSynchronize(stream));
 }

@@ -28,7 +28,9 @@ struct WaveRec {
   uint32_t bw;
 };
 
-template <int DEG, bool HALF>
+// FEAT: feature lanes (feat_mode 1 or 2); the plain variant writes zeros there and keeps the registers the
+// pseudo-normal would hold free (one more resident wave per SIMD at SH degree 3).
+template <int DEG, bool HALF, bool FEAT>
 __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a) {
   __shared__ WaveRec s_rec[PROJ_BLOCK];
   __shared__ uint32_t s_incl[PROJ_BLOCK];
@@ -83,7 +85,8 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       cg = __builtin_isfinite(cg) ? fminf(fmaxf(cg, -100.f), 100.f) : 0.f;
       cb = __builtin_isfinite(cb) ? fminf(fmaxf(cb, -100.f), 100.f) : 0.f;
       float f0 = 0.f, f1 = 0.f, f2 = 0.f;
-      if (a.feat_mode == 1) {
+      if (!FEAT) {
+      } else if (a.feat_mode == 1) {
         // the pseudo-normal (project.cu:63-71): the local axis of the smallest log scale (the first of
         // equal ones), a column of R(q), as a unit vector turned towards the camera, in camera coordinates
         const AxisPick ax = smallest_axis(ls.x, ls.y, ls.z);
@@ -327,6 +330,21 @@ extern "C" int b2c_hip_fill_u32(uint32_t* p, uint32_t value, size_t count, hipSt
   return (int)hipGetLastError();
 }
 
+template <bool FEAT>
+void launch_project(const b2c_project_args& a, dim3 grid, dim3 block, bool half, hipStream_t stream) {
+  switch (a.degree * 2 + (half ? 1 : 0)) {
+    case 0: project_kernel<0, false, FEAT><<<grid, block, 0, stream>>>(a); break;
+    case 2: project_kernel<1, false, FEAT><<<grid, block, 0, stream>>>(a); break;
+    case 3: project_kernel<1, true, FEAT><<<grid, block, 0, stream>>>(a); break;
+    case 4: project_kernel<2, false, FEAT><<<grid, block, 0, stream>>>(a); break;
+    case 5: project_kernel<2, true, FEAT><<<grid, block, 0, stream>>>(a); break;
+    case 6: project_kernel<3, false, FEAT><<<grid, block, 0, stream>>>(a); break;
+    case 7: project_kernel<3, true, FEAT><<<grid, block, 0, stream>>>(a); break;
+    case 8: project_kernel<4, false, FEAT><<<grid, block, 0, stream>>>(a); break;
+    default: project_kernel<4, true, FEAT><<<grid, block, 0, stream>>>(a); break;
+  }
+}
+
 extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
@@ -335,17 +353,8 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);  // one launch for both
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);
   const bool half = a->degree > 0 && !a->sh.hi32;  // fp16 bands
-  switch (a->degree * 2 + (half ? 1 : 0)) {
-    case 0: project_kernel<0, false><<<grid, block, 0, stream>>>(*a); break;
-    case 2: project_kernel<1, false><<<grid, block, 0, stream>>>(*a); break;
-    case 3: project_kernel<1, true><<<grid, block, 0, stream>>>(*a); break;
-    case 4: project_kernel<2, false><<<grid, block, 0, stream>>>(*a); break;
-    case 5: project_kernel<2, true><<<grid, block, 0, stream>>>(*a); break;
-    case 6: project_kernel<3, false><<<grid, block, 0, stream>>>(*a); break;
-    case 7: project_kernel<3, true><<<grid, block, 0, stream>>>(*a); break;
-    case 8: project_kernel<4, false><<<grid, block, 0, stream>>>(*a); break;
-    default: project_kernel<4, true><<<grid, block, 0, stream>>>(*a); break;
-  }
+  if (a->feat_mode) launch_project<true>(*a, grid, block, half, stream);
+  else launch_project<false>(*a, grid, block, half, stream);
   const int e = (int)hipGetLastError();
   if (e) return e;
   if (!a->big_info || !a->big_chunk || !a->big_items || !a->big_items_count) return (int)hipErrorInvalidValue;

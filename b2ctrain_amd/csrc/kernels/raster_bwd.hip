@@ -214,13 +214,6 @@ constexpr int ROW_FLOATS = FEAT ? 16 : 12;
 // 11 v^2, 12-15 zero
 constexpr int B_ONE = 6, B_U = 7, B_V = 8, B_UU = 9, B_UV = 10, B_VV = 11;
 
-// DPP controls (GCN/CDNA): row_shr:n = 0x110 + n, row_ror:n = 0x120 + n, row_bcast:15 = 0x142,
-// row_bcast:31 = 0x143, wave_shl:1 = 0x130, wave_shr:1 = 0x138. Lanes whose source is outside the row mask or
-// the wave get `fill`.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t x, uint32_t fill) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)x, CTRL, ROW_MASK, 0xF, false);
-}
 
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -488,32 +481,10 @@ constexpr int RED_VALS = FEAT ? 14 : 11;
 // run and its last run; the last piece's third quarter carries the head slot in .w).
 template <bool FEAT>
 constexpr int PART_Q = FEAT ? 4 : 3;
-constexpr uint32_t NO_RUN = 0xFFFFFFFFu;
 constexpr uint32_t W_CONT_BEFORE = 1u, W_CONT_AFTER = 2u, W_HAS_HEAD = 4u;
 constexpr int RED_SUB = 4;                  // 64-row sub-windows per reduce wave
 constexpr uint32_t RED_WIN = 64u * RED_SUB;  // rows per window (one wave)
 
-// One Hillis-Steele step of the segmented scan: add the partial of the DPP source lane when it lies in
-// the same run (runs are contiguous, so equal ids at both ends mean no run boundary in between).
-template <int CTRL, int ROW_MASK, int NV>
-__device__ __forceinline__ void seg_scan_step(uint32_t id, float (&v)[NV]) {
-  const bool same = dpp_u32<CTRL, ROW_MASK>(id, NO_RUN) == id;
-#pragma unroll
-  for (int k = 0; k < NV; k++) {
-    const float t = __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v[k]), 0u));
-    v[k] = same ? v[k] + t : v[k];
-  }
-}
-
-template <int NV>
-__device__ __forceinline__ void seg_scan(uint32_t id, float (&v)[NV]) {
-  seg_scan_step<0x111, 0xF>(id, v);  // row_shr:1
-  seg_scan_step<0x112, 0xF>(id, v);  // row_shr:2
-  seg_scan_step<0x114, 0xF>(id, v);  // row_shr:4
-  seg_scan_step<0x118, 0xF>(id, v);  // row_shr:8
-  seg_scan_step<0x142, 0xA>(id, v);  // row_bcast:15 into rows 1 and 3
-  seg_scan_step<0x143, 0xC>(id, v);  // row_bcast:31 into rows 2 and 3
-}
 
 template <bool FEAT>
 __device__ __forceinline__ void prefetch_old(const b2c_raster_bwd_args& a, uint32_t id, float (&old)[RED_VALS<FEAT>]) {

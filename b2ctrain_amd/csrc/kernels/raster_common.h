@@ -110,5 +110,38 @@ __device__ __forceinline__ uint32_t quadrant_mask(float mx, float my, float ah, 
   return mask;
 }
 
+// DPP controls (GCN/CDNA): row_shr:n = 0x110 + n, row_ror:n = 0x120 + n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143, wave_shl:1 = 0x130, wave_shr:1 = 0x138. Lanes whose source is outside the row mask or
+// the wave get `fill`.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x, uint32_t fill) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+
+constexpr uint32_t NO_RUN = 0xFFFFFFFFu;  // the run id of a lane outside every run
+
+// One Hillis-Steele step of a segmented inclusive scan across the wave: add the partial of the DPP source
+// lane when it lies in the same run (runs are contiguous, so equal ids at both ends mean no run boundary in
+// between).
+template <int CTRL, int ROW_MASK, int NV>
+__device__ __forceinline__ void seg_scan_step(uint32_t id, float (&v)[NV]) {
+  const bool same = dpp_u32<CTRL, ROW_MASK>(id, NO_RUN) == id;
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    const float t = __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v[k]), 0u));
+    v[k] = same ? v[k] + t : v[k];
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void seg_scan(uint32_t id, float (&v)[NV]) {
+  seg_scan_step<0x111, 0xF>(id, v);  // row_shr:1
+  seg_scan_step<0x112, 0xF>(id, v);  // row_shr:2
+  seg_scan_step<0x114, 0xF>(id, v);  // row_shr:4
+  seg_scan_step<0x118, 0xF>(id, v);  // row_shr:8
+  seg_scan_step<0x142, 0xA>(id, v);  // row_bcast:15 into rows 1 and 3
+  seg_scan_step<0x143, 0xC>(id, v);  // row_bcast:31 into rows 2 and 3
+}
+
 }  // namespace dev
 }  // namespace b2c

@@ -20,22 +20,38 @@ __device__ __forceinline__ float byte_chan(uint32_t p, int c) { return (float)((
 // res the mean absolute colour residual of the render (plus the weighted normal residual with FEAT), and
 // k = (target alpha if the view is masked with alpha, else 1) * weight. Each lane replays its pixel's list
 // up to last_idx and writes every fragment's blend weight vis into a [64 splats][64 pixels] LDS matrix; the
-// lane of splat j then contracts row j with the pixel vectors (m, m res, k) and adds the three sums to the
-// view accumulator (float atomics, once per (tile, splat), as the reference adds them). With LABELS the
-// same rows are summed per class over the tile's distinct label values into the splat's class bins.
+// lane of splat j then contracts row j with the pixel vectors (m, m res, k) and stores the three sums as the
+// (tile, splat) row at the entry's emit position (the reference adds them to the splat with float atomics,
+// which MI355X performs past the per-XCD L2; evidence_reduce_kernel sums each splat's rows instead). With
+// LABELS the tile's distinct classes are found once (ballots: labels are spatially coherent, a tile usually
+// holds one or two), each with a pixel vector k * [pixel in the class]; the same rows are contracted with
+// those vectors and added to the splat's class bins with float atomics. Classes beyond the first MAXC of a
+// tile take a slower pass over the pixels.
+constexpr int MAXC = 4;  // classes per tile with their own pixel vector
+
 template <bool FEAT, bool LABELS>
 __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
   __shared__ float4 s_g0[64], s_g1[64];
   __shared__ uint32_t s_id[64];
   __shared__ float s_vis[64 * VSTRIDE];
   __shared__ float s_m[64], s_mr[64], s_k[64];
-  __shared__ uint32_t s_lab[64];
+  __shared__ float s_kc[LABELS ? MAXC : 1][64];  // k of the pixels of the tile's c-th class, else 0
+  __shared__ uint32_t s_lab[64];                 // class of the pixels beyond the first MAXC classes
+  __shared__ uint32_t s_slot[64];
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
   const uint2 range = reinterpret_cast<const uint2*>(a.tile_ranges)[tile];
-  if (range.y <= range.x) return;
   const int lane = threadIdx.x;
+  float4* rows = reinterpret_cast<float4*>(a.rows);
+  // entries past the shrunk end composited nowhere: zero rows; the last tile's wave also zeroes the rows of
+  // the sentinel entries (in no tile's list)
+  for (uint32_t i = max(range.y, range.x) + lane; i < a.tile_end[tile]; i += 64)
+    rows[a.slot_sorted[i]] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (tile == n_tiles - 1)
+    for (uint32_t i = a.tile_end[n_tiles] + lane; i < a.num_isect; i += 64)
+      rows[a.slot_sorted[i]] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (range.y <= range.x) return;
   const int px = (tile % a.tiles_x) * RT_W + (lane & 7), py = (tile / a.tiles_x) * RT_W + (lane >> 3);
   const bool inside = px < a.W && py < a.H;
   const float pcx = px + 0.5f, pcy = py + 0.5f;
@@ -73,7 +89,24 @@ __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
   s_m[lane] = m;
   s_mr[lane] = mres;
   s_k[lane] = k;
-  if constexpr (LABELS) s_lab[lane] = lab;
+  uint32_t cls[MAXC] = {0u, 0u, 0u, 0u};  // wave-uniform: the tile's first classes, in pixel order
+  int ncls = 0;
+  bool rest = false;  // a pixel's class is not among them
+  if constexpr (LABELS) {
+    uint64_t todo = ballot64(lab != LABEL_NONE);
+    int my_c = -1;
+    while (todo != 0ull && ncls < MAXC) {
+      const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)lab, __builtin_ctzll(todo));
+      const uint64_t hit = ballot64(lab == b);
+      if (lab == b) my_c = ncls;
+      cls[ncls++] = b;
+      todo &= ~hit;
+    }
+    rest = todo != 0ull;
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) s_kc[c][lane] = my_c == c ? k : 0.f;
+    s_lab[lane] = my_c < 0 ? lab : LABEL_NONE;
+  }
   float T = 1.f;
   for (uint32_t start = range.x; start < range.y; start += 64) {
     const uint32_t count = min(64u, range.y - start);
@@ -81,6 +114,7 @@ __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
     if ((uint32_t)lane < count) {
       const uint32_t gid = a.vals_sorted[start + lane];
       s_id[lane] = gid;
+      s_slot[lane] = a.slot_sorted[start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
       const float4 r1 = rec[1], r2 = rec[2];
       s_g0[lane] = rec[0];
@@ -107,47 +141,89 @@ __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
         a1 += v * s_mr[p];
         a2 += v * s_k[p];
       }
-      float* dst = a.view_acc + (size_t)s_id[lane] * 3;
-      if (a0 != 0.f) atomicAdd(dst, a0);
-      if (a1 != 0.f) atomicAdd(dst + 1, a1);
-      if (a2 != 0.f) atomicAdd(dst + 2, a2);
+      rows[s_slot[lane]] = make_float4(a0, a1, a2, 0.f);
       if constexpr (LABELS) {
-        // the tile's distinct classes, one pass each (labels are spatially coherent: usually one or two)
-        uint64_t todo = ~0ull;
-        while (true) {
-          uint32_t b = LABEL_NONE;
-          for (int p = 0; p < 64; p++)
-            if (((todo >> p) & 1ull) && s_lab[p] != LABEL_NONE) { b = s_lab[p]; break; }
-          if (b == LABEL_NONE) break;
-          float sum = 0.f;
-          for (int p = 0; p < 64; p++)
-            if (s_lab[p] == b) {
-              sum += row[p] * s_k[p];
-              todo &= ~(1ull << p);
-            }
-          if (sum != 0.f) atomicAdd(a.label_acc + (size_t)s_id[lane] * B2C_LABEL_BINS + b, sum);
+        float* bins = a.label_acc + (size_t)s_id[lane] * B2C_LABEL_BINS;
+        if (ncls == 1) {
+          float c0 = 0.f;
+#pragma unroll 8
+          for (int p = 0; p < 64; p++) c0 += row[p] * s_kc[0][p];
+          if (c0 != 0.f) atomicAdd(bins + cls[0], c0);
+        } else if (ncls > 1) {
+          float cc[MAXC] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+          for (int p = 0; p < 64; p++) {
+            const float v = row[p];
+#pragma unroll
+            for (int c = 0; c < MAXC; c++) cc[c] += v * s_kc[c][p];
+          }
+#pragma unroll
+          for (int c = 0; c < MAXC; c++)
+            if (c < ncls && cc[c] != 0.f) atomicAdd(bins + cls[c], cc[c]);
+        }
+        if (rest) {  // classes past the first MAXC of the tile: one pass each
+          uint64_t todo = ~0ull;
+          while (true) {
+            uint32_t b = LABEL_NONE;
+            for (int p = 0; p < 64; p++)
+              if (((todo >> p) & 1ull) && s_lab[p] != LABEL_NONE) {
+                b = s_lab[p];
+                break;
+              }
+            if (b == LABEL_NONE) break;
+            float sum = 0.f;
+            for (int p = 0; p < 64; p++)
+              if (s_lab[p] == b) {
+                sum += row[p] * s_k[p];
+                todo &= ~(1ull << p);
+              }
+            if (sum != 0.f) atomicAdd(bins + b, sum);
+          }
         }
       }
     }
   }
 }
 
+// The view's per-splat sums: one lane per emit position, a segmented inclusive scan across the wave over
+// the splat ids of the emit order (a splat's rows are contiguous), and the last lane of each run piece adds
+// the piece's sums to the splat's view accumulator (one float atomic per piece and value: about one per
+// splat instead of one per (tile, splat) pair).
+__global__ void __launch_bounds__(256) evidence_reduce_kernel(b2c_evidence_sum_args a) {
+  const uint32_t s = blockIdx.x * 256u + threadIdx.x;
+  const bool valid = s < a.m;
+  const uint32_t id = valid ? a.ids[s] : NO_RUN;
+  float v[3] = {0.f, 0.f, 0.f};
+  if (valid) {
+    const float4 r = reinterpret_cast<const float4*>(a.rows)[s];
+    v[0] = r.x;
+    v[1] = r.y;
+    v[2] = r.z;
+  }
+  seg_scan(id, v);
+  const uint32_t next = dpp_u32<0x130, 0xF>(id, NO_RUN);  // wave_shl:1: the next lane's id (lane 63: none)
+  if (valid && next != id && id < (uint32_t)a.n) {
+    float* dst = a.view_acc + (size_t)id * 3;
+#pragma unroll
+    for (int k = 0; k < 3; k++)
+      if (v[k] != 0.f) atomicAdd(dst + k, v[k]);
+  }
+}
+
 // fold_view_kernel (evidence.cu:114-126): the view's sums into the running evidence: w_in, w_all, err, the
 // sum of w_in^2 (for the effective view count) and the w_in-weighted unit direction towards the camera.
-__global__ void __launch_bounds__(256) fold_view_kernel(int n, const float* __restrict__ view_acc,
-                                                        const float* __restrict__ pos_op, float cx, float cy, float cz,
-                                                        float* __restrict__ ev) {
+__global__ void __launch_bounds__(256) fold_view_kernel(b2c_evidence_sum_args a) {
   const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float w_in = view_acc[(size_t)i * 3], err = view_acc[(size_t)i * 3 + 1], w_all = view_acc[(size_t)i * 3 + 2];
-  float* e = ev + (size_t)i * B2C_EVIDENCE_STRIDE;
+  if (i >= a.n) return;
+  const float w_in = a.view_acc[(size_t)i * 3], err = a.view_acc[(size_t)i * 3 + 1], w_all = a.view_acc[(size_t)i * 3 + 2];
+  float* e = a.evidence + (size_t)i * B2C_EVIDENCE_STRIDE;
   e[0] += w_in;
   e[1] += w_all;
   e[2] += err;
   e[7] += w_in * w_in;
   if (w_in != 0.f) {
-    const float4 p = reinterpret_cast<const float4*>(pos_op)[i];
-    const float dx = cx - p.x, dy = cy - p.y, dz = cz - p.z;
+    const float4 p = reinterpret_cast<const float4*>(a.pos_op)[i];
+    const float dx = a.cam_pos[0] - p.x, dy = a.cam_pos[1] - p.y, dz = a.cam_pos[2] - p.z;
     const float il = 1.f / fmaxf(sqrtf(dx * dx + dy * dy + dz * dz), 1e-12f);
     e[4] += w_in * dx * il;
     e[5] += w_in * dy * il;
@@ -218,7 +294,8 @@ using namespace b2c::dev;
 extern "C" int b2c_hip_evidence_view(const b2c_evidence_args* a, hipStream_t stream) {
   const int n_tiles = a->tiles_x * a->tiles_y;
   if (n_tiles <= 0) return 0;
-  if (!a->raster_rec || !a->view_acc || !a->gt || !a->out_rgba || !a->last_idx) return (int)hipErrorInvalidValue;
+  if (!a->raster_rec || !a->rows || !a->slot_sorted || !a->tile_end || !a->gt || !a->out_rgba || !a->last_idx)
+    return (int)hipErrorInvalidValue;
   const bool feat = a->normals && a->normal_weight > 0.f;
   const bool labels = a->labels && a->label_acc;
   if (feat && !a->out_feat) return (int)hipErrorInvalidValue;
@@ -233,11 +310,13 @@ extern "C" int b2c_hip_evidence_view(const b2c_evidence_args* a, hipStream_t str
   return (int)hipGetLastError();
 }
 
-extern "C" int b2c_hip_evidence_fold(int n, const float* view_acc, const float* pos_op, const float cam_pos[3],
-                                     float* evidence, hipStream_t stream) {
-  if (n <= 0) return 0;
-  fold_view_kernel<<<(n + 255) / 256, 256, 0, stream>>>(n, view_acc, pos_op, cam_pos[0], cam_pos[1], cam_pos[2],
-                                                       evidence);
+extern "C" int b2c_hip_evidence_sum(const b2c_evidence_sum_args* a, hipStream_t stream) {
+  if (a->n <= 0) return 0;
+  if (!a->ids || !a->rows || !a->view_acc || !a->pos_op || !a->evidence) return (int)hipErrorInvalidValue;
+  const int fill = b2c_hip_fill_u32(reinterpret_cast<uint32_t*>(a->view_acc), 0u, (size_t)a->n * 3, stream);
+  if (fill) return fill;
+  if (a->m) evidence_reduce_kernel<<<(a->m + 255) / 256, 256, 0, stream>>>(*a);
+  fold_view_kernel<<<(a->n + 255) / 256, 256, 0, stream>>>(*a);
   return (int)hipGetLastError();
 }
 

@@ -289,11 +289,13 @@ int b2c_hip_eval_metrics(const b2c_eval_args* a, hipStream_t stream);
 #define B2C_LABEL_BINS 32      /* class ids >= this are ignored (evidence.cu:39) */
 #define B2C_EVIDENCE_STRIDE 8  /* floats per splat of the evidence accumulator: w_in, w_all, err, -, dir xyz, sum w_in^2 */
 
-/* One view's replay after a forward with bwd_info (shrunk ranges, last_idx): view_acc[i] += per splat the
- * sums over its composited fragments of vis * (m, m * res, k) with m = target alpha * w, res the pixel's mean
- * absolute colour residual (+ normal_weight times the normal residual when normals are given), k =
- * (target alpha if masked_has_alpha else 1) * w; with labels, label_acc[i][class] += vis * k for the pixel's
- * class (< B2C_LABEL_BINS). Float atomics, as the reference. */
+/* One view's replay after a forward with bwd_info (shrunk ranges, last_idx, slot_sorted, tile_end): for each
+ * (tile, splat) list entry, rows[slot] = (the sums over the tile's composited fragments of vis * m,
+ * vis * m * res, vis * k, 0) at the entry's emit position, with m = target alpha * w, res the pixel's mean
+ * absolute colour residual (+ normal_weight times the normal residual when normals are given), k = (target
+ * alpha if masked_has_alpha else 1) * w; entries past a tile's shrunk end (and the sentinel entries) get zero
+ * rows. With labels, label_acc[i][class] += vis * k for the pixel's class (< B2C_LABEL_BINS), float
+ * atomics. */
 typedef struct b2c_evidence_args {
   const uint32_t* tile_ranges;
   const uint32_t* vals_sorted;
@@ -307,14 +309,29 @@ typedef struct b2c_evidence_args {
   int W, H, tiles_x, tiles_y;
   int masked_has_alpha;
   float normal_weight;
-  float* view_acc;            /* [n][3] (w_in, err, w_all), zeroed by the caller per view */
+  const uint32_t* slot_sorted; /* [M] emit position of list entry i */
+  const uint32_t* tile_end;   /* [tiles + 1] list ends before the forward shrank them; [tiles] = sentinel start */
+  uint32_t num_isect;
+  float* rows;                /* [M][4] at emit positions */
   float* label_acc;           /* [n][B2C_LABEL_BINS] or NULL */
 } b2c_evidence_args;
 int b2c_hip_evidence_view(const b2c_evidence_args* a, hipStream_t stream);
-/* fold_view_kernel (evidence.cu:114-126): evidence[i] (B2C_EVIDENCE_STRIDE floats) += w_in, w_all, err; [7] +=
- * w_in^2; [4..6] += w_in * the unit vector from the splat to cam_pos. */
-int b2c_hip_evidence_fold(int n, const float* view_acc, const float* pos_op, const float cam_pos[3], float* evidence,
-                          hipStream_t stream);
+/* The view's per-splat sums from the rows (view_acc[i] = (w_in, err, w_all): a segmented scan over the emit
+ * order, whose splat ids are `ids`, and one float atomic per run piece and value), folded into the evidence
+ * as fold_view_kernel does (evidence.cu:114-126): evidence[i] (B2C_EVIDENCE_STRIDE floats) += w_in, w_all,
+ * err; [7] += w_in^2; [4..6] += w_in * the unit vector from the splat to cam_pos. view_acc is scratch,
+ * cleared here. */
+typedef struct b2c_evidence_sum_args {
+  int n;
+  uint32_t m;                 /* intersections */
+  const uint32_t* ids;        /* [M] splat id of emit position s */
+  const float* rows;          /* [M][4] */
+  float* view_acc;            /* [n][3] scratch */
+  const float* pos_op;        /* [n] float4 */
+  float cam_pos[3];
+  float* evidence;            /* [n][B2C_EVIDENCE_STRIDE] */
+} b2c_evidence_sum_args;
+int b2c_hip_evidence_sum(const b2c_evidence_sum_args* a, hipStream_t stream);
 
 /* probe_kernel (probe.cu:7-53) after projection and binning: out[pix] = (accumulated alpha, the depth where it
  * first reaches tau (tau <= 0: the alpha-weighted mean depth, +inf under 5% coverage), the weight from more
