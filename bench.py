@@ -336,8 +336,11 @@ def main():
         r.sync()
         fs0 = f_sweep_of(r)
         f_contrib, out["cpu_baseline"], out["cpu_reference_algorithm"] = cpu_baselines(r, scene, bgs[-1], fs0)
-        # composited fragments of that frame, counted by the CPU port over the GPU's own lists
+        # composited fragments of that frame, counted by the CPU port over the GPU's own lists, and the rate
+        # of composited fragments through the forward and backward (F_contrib / (t_fwd + t_bwd), one view)
         out["config"]["F_contrib_view0"] = f_contrib
+        if nv == 1:
+            out["contrib_gfrag_per_s"] = round(f_contrib / (t_fb * 1e-3) / 1e9, 3)
     else:
         out["cpu_baseline"] = None
     # A complete training iteration: the same step ending in the fused Adam / MCMC update instead of the
