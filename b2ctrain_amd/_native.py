@@ -402,7 +402,7 @@ def device_count() -> int:
 
 
 _FIELD_SPEC = {
-    # name: (dtype, per-element shape, size key)  size key: n splats, P pixels, M isects, T tiles
+    # name: (dtype, per-element shape, size key)  size key: n splats, P pixels, M isects, T tiles (T1: T + 1)
     "proj0": (np.float32, (4,), "n"), "proj1": (np.float32, (4,), "n"), "proj2": (np.float32, (4,), "n"),
     "proj3": (np.float32, (2,), "n"), "raster_rec": (np.float32, (16,), "n"), "tile_count": (np.uint32, (), "n"), "tile_off": (np.uint32, (), "n"),
     "hit_info": (np.uint32, (2,), "n"), "order": (np.uint32, (), "n"), "depth_keys_sorted": (np.uint32, (), "n"),
@@ -411,6 +411,8 @@ _FIELD_SPEC = {
     "out_feat": (np.float32, (4,), "P"), "last_idx": (np.uint32, (), "P"), "v_out": (np.float32, (4,), "P"),
     "v_splat": (np.float32, (GRAD_LANES,), "n"), "vis_flag": (np.uint32, (), "n"), "loss_accum": (np.float32, (16,), "1"),
     "v_feat": (np.float32, (4,), "P"), "hollow_pen": (np.float32, (), "P"),
+    "slot_sorted": (np.uint32, (), "M"), "tile_end": (np.uint32, (), "T1"),
+    "isect_rows": (np.float32, (12,), "M"),
 }
 
 
@@ -710,7 +712,8 @@ class Renderer:
 
     def _count(self, key):
         inf = self.info()
-        return {"n": self.n, "P": self.W * self.H, "M": inf.num_isect, "T": inf.n_tiles, "1": 1}[key]
+        return {"n": self.n, "P": self.W * self.H, "M": inf.num_isect, "T": inf.n_tiles, "T1": inf.n_tiles + 1,
+                "1": 1}[key]
 
     def read(self, field):
         if field == "grads":

@@ -50,8 +50,8 @@ void compute_evidence(RenderCtx& ctx, const Model& m, const std::vector<ViewGPU>
     a.masked_has_alpha = (view.masked && view.has_alpha) ? 1 : 0;
     a.normal_weight = cfg.evidence_normal_weight;
     a.slot_sorted = ctx.slot_sorted;
-    a.tile_end = ctx.tile_end;
     a.num_isect = ctx.num_isect;
+    a.row_tag = ctx.next_row_tag(4, stream);
     a.rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);  // the backward's row buffer, free between passes
     a.label_acc = g_labels_valid ? g_labels.ptr : nullptr;
     LAUNCH_CHECK(b2c_hip_evidence_view(&a, stream));
@@ -60,6 +60,7 @@ void compute_evidence(RenderCtx& ctx, const Model& m, const std::vector<ViewGPU>
     sa.m = ctx.num_isect;
     sa.ids = ctx.vals;
     sa.rows = a.rows;
+    sa.row_tag = a.row_tag;
     sa.view_acc = g_view_acc.ptr;
     sa.pos_op = reinterpret_cast<const float*>(m.pos_op.ptr);
     for (int k = 0; k < 3; k++) sa.cam_pos[k] = cams[v].pos[k];

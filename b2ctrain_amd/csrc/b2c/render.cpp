@@ -3,6 +3,7 @@
 #include "render.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 
 namespace b2c {
@@ -90,6 +91,23 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   const size_t need_tmp = std::max({b2c_radix_sort_temp_bytes((uint32_t)nn), b2c_radix_sort_temp_bytes((uint32_t)isect_cap),
                                     b2c_scan_temp_bytes((uint32_t)nn)});
   sort_tmp.reserve(need_tmp);
+}
+
+uint32_t RenderCtx::next_row_tag(int row_floats, hipStream_t stream) {
+  uint32_t limit = tile_bits >= 31 ? 1u : (1u << (32 - tile_bits)) - 1u;  // generations that fit the tag
+  if (const char* env = getenv("B2C_ROW_GEN_LIMIT")) {  // a shorter epoch, for tests
+    const long v = atol(env);
+    if (v >= 1 && (uint32_t)v < limit) limit = (uint32_t)v;
+  }
+  const uint32_t key = (uint32_t)row_floats | ((uint32_t)tile_bits << 8);
+  if (row_epoch_buf != isect_rows.ptr || key != row_epoch_key || row_gen >= limit) {
+    isect_rows.zero(stream);
+    row_gen = 0;
+    row_epoch_key = key;
+    row_epoch_buf = isect_rows.ptr;
+  }
+  row_gen++;
+  return row_gen << tile_bits;
 }
 
 void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
@@ -276,8 +294,9 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.slot_sorted = ctx.slot_sorted;
   a.isect_vals = ctx.vals;
   a.tile_count = ctx.tile_count;
-  a.tile_end = ctx.tile_end;
   a.isect_rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);
+  a.tile_mask = (1u << ctx.tile_bits) - 1u;
+  if (mode == 1 && ctx.num_isect) a.row_tag = ctx.next_row_tag(p.feat != FeatureMode::None ? 16 : 12, stream);
   a.isect_part = reinterpret_cast<float*>(ctx.isect_part.ptr);
   a.isect_part_flags = ctx.isect_part_flags;
   a.split_event = ctx.bwd_split_event;

@@ -94,7 +94,8 @@ struct RenderCtx {
   DevBuf<uint32_t> depth_alt_k, depth_alt_v, isect_alt_k, isect_alt_v, isect_alt_v2;
   // Intersection bookkeeping of the atomic-free backward: slot_sorted[i] = emit position of list entry i
   // (the tile sort sorts positions; a splat's emit positions are contiguous), tile_end[t] = the tile's
-  // list end before the forward shrinks it, isect_rows[slot] = that (tile, splat)'s 12-float gradient row.
+  // list end before the forward shrinks it, isect_rows[slot] = that (tile, splat)'s 12-float gradient row
+  // (or the evidence pass's 4-float row), written only for the entries of the shrunk ranges.
   DevBuf<uint32_t> slot_sorted, tile_end;
   DevBuf<float4> isect_rows;
   DevBuf<float4> isect_part;          // per 256-row window: partial sums of runs crossing the window's edges
@@ -111,6 +112,16 @@ struct RenderCtx {
   ~RenderCtx();
   void setup(int W, int H, int n_splats, hipStream_t stream);
   void ensure_isect_capacity(size_t m, hipStream_t stream);
+  // Row tags. Every row a pass writes carries the pass's tag (generation << tile_bits, or'd with the
+  // tile) and the readers take a row as this pass's only when the tag matches, so rows of pairs past a
+  // shrunk end are neither written nor cleared. A tag is never handed out twice while rows written under
+  // it can remain: the buffer is cleared (fill kernel) when it was reallocated, when the row layout
+  // (floats per row) or tile_bits changed, and when the generation field is used up; the generation then
+  // restarts at 1.
+  uint32_t next_row_tag(int row_floats, hipStream_t stream);
+  uint32_t row_gen = 0;                 // last generation of the current epoch
+  uint32_t row_epoch_key = 0;           // row floats | tile_bits << 8 of the current epoch
+  const void* row_epoch_buf = nullptr;  // isect_rows.ptr the epoch's clear covered
 };
 
 // Full forward: projection, binning, sort, rasterisation. Leaves outputs in ctx.

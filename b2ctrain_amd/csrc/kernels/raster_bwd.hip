@@ -206,8 +206,8 @@ constexpr int G = 8;       // splats per MFMA group
 constexpr int SROW = 68;   // pixel stride of the per-fragment scalar rows (64 + 4: spreads the B reads over banks)
 // (tile, splat) row: raw moments of the tile's fragments about the tile centre, 12 floats in three 16-byte
 // quarters, each written by one lane with one store: sum v_sigma * [v, u^2, uv, v^2] | sum v_sigma * [1, u],
-// sum vis, refine sum | sum vis * v_rgb, the tile id (bits); with feature lanes a fourth quarter
-// sum vis * v_feat, 0. Rows are ROW_FLOATS<FEAT> floats apart.
+// sum vis, refine sum | sum vis * v_rgb, the tag word row_tag | tile (bits); with feature lanes a fourth
+// quarter sum vis * v_feat, 0. Rows are ROW_FLOATS<FEAT> floats apart.
 template <bool FEAT>
 constexpr int ROW_FLOATS = FEAT ? 16 : 12;
 // basis rows (M) of operand A: 0-2 v_rgb, 3-5 v_feat (zero without FEAT), 6 one, 7 u, 8 v, 9 u^2, 10 uv,
@@ -279,23 +279,8 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
   const uint2 range = reinterpret_cast<const uint2*>(a.tile_ranges)[tile];
-  const uint32_t full_end = a.tile_end[tile];
   const int lane = threadIdx.x;
-  float4* rows = reinterpret_cast<float4*>(a.isect_rows);
-  // pairs past the shrunk end never composited: zero rows, so the reduce reads no stale data; the last
-  // tile's wave also clears the rows of sentinel keys (in no tile's list)
-  for (uint32_t i = max(range.y, range.x) + lane; i < full_end; i += 64) {
-    float4* r = rows + (size_t)a.slot_sorted[i] * (ROW / 4);
-    r[0] = r[1] = r[2] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if constexpr (FEAT) r[3] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  if (tile == n_tiles - 1) {
-    for (uint32_t i = a.tile_end[n_tiles] + lane; i < a.num_isect; i += 64) {
-      float4* r = rows + (size_t)a.slot_sorted[i] * (ROW / 4);
-      r[0] = r[1] = r[2] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if constexpr (FEAT) r[3] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
+  // pairs past the shrunk end never composited: they get no row, and the reduce does not read theirs
   if (range.y <= range.x) return;
   const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
   const int lx = lane & 7, ly = lane >> 3;
@@ -432,7 +417,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       // (tile, splat) row's raw moments (the reduce turns them into gradients), one 16-byte quarter each:
       // (j + 8, kg 2) the v_sigma column's rows 8-11; (j, kg 1) the v_sigma column's rows 6-7, taken from
       // lane j + 8 of its row of 16 lanes, then the vis column's row 6 and the refine product's row 6;
-      // (j, kg 0) the vis column's rows 0-2 and the tile id.
+      // (j, kg 0) the vis column's rows 0-2 and the tag word.
       {
         const int j = nl & (G - 1);
         float dv[4];
@@ -449,7 +434,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
           float4* row = reinterpret_cast<float4*>(a.isect_rows) + (size_t)s_slot[gbase + j] * (ROW / 4);
           if (nl >= G && kg == 2) row[0] = make_float4(dv[0], dv[1], dv[2], dv[3]);
           if (nl < G && kg == 1) row[1] = make_float4(sv, svu, dv[2], d1[2]);
-          if (nl < G && kg == 0) row[2] = make_float4(dv[0], dv[1], dv[2], __uint_as_float((uint32_t)tile));
+          if (nl < G && kg == 0) row[2] = make_float4(dv[0], dv[1], dv[2], __uint_as_float(a.row_tag | (uint32_t)tile));
           if constexpr (FEAT)
             if (nl < G && kg == 1) row[3] = make_float4(fx, dv[0], dv[1], 0.f);
         }
@@ -463,8 +448,9 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 // isect_vals[slot] (the emitted splat id) names the run, so this is a segmented reduction over a
 // contiguous array, in two kernels:
 //  * isect_reduce_kernel: one wave per aligned window of RED_WIN = 256 rows, walked as four 64-row
-//    sub-windows (coalesced 48-byte rows), each a segmented inclusive scan across lanes on DPP row shifts
-//    and row broadcasts; the sums of a run that continues into the next sub-window are carried in
+//    sub-windows (coalesced 48-byte rows; a row without this pass's tag, a pair past its tile's shrunk end,
+//    counts as zero), each a segmented inclusive scan across lanes on DPP row shifts and row broadcasts;
+//    the sums of a run that continues into the next sub-window are carried in
 //    registers. A run that starts and ends inside the window is finished there: its last lane adds the
 //    sums to v_splat[0..9], vis_weight and vis_flag (the raster_bwd_tc.cu:195-198 updates, without
 //    atomics). A run crossing a window edge leaves its per-window partial sums in isect_part (first run of
@@ -537,15 +523,17 @@ __device__ __forceinline__ void add_part(const float4* p, float (&v)[RED_VALS<FE
 // tile centre (raster_bwd_tc.cu:172-198 accumulates the same quantities per fragment): with (mx, my) the
 // splat centre relative to the tile centre, the first and second moments of v_sigma about the splat centre
 // give the mean and conic gradients, the vis moments the colour gradients, and where a fragment is
-// unclamped v_alpha * gauss = -v_sigma / opacity gives g8. The tile id rides in the row's last float.
+// unclamped v_alpha * gauss = -v_sigma / opacity gives g8. The row's tag word holds the tile; returns
+// whether the tag is this pass's (otherwise the row was not written by it and v is to be discarded).
 template <bool FEAT>
-__device__ __forceinline__ void row_gradients(const b2c_raster_bwd_args& a, uint32_t s, uint32_t id,
+__device__ __forceinline__ bool row_gradients(const b2c_raster_bwd_args& a, uint32_t s, uint32_t id,
                                               float (&v)[RED_VALS<FEAT>]) {
   const float4* rw = reinterpret_cast<const float4*>(a.isect_rows) + (size_t)s * (ROW_FLOATS<FEAT> / 4);
   const float4 q0 = rw[0], q1 = rw[1], q2 = rw[2];
   const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)id * 4;
   const float4 r0 = rec[0], r1 = rec[1];  // (mx, my, c00 / 2, c01), (c11 / 2, opacity, power, sign bits)
-  const uint32_t t = __float_as_uint(q2.w);  // the tile (a zero row: tile 0, and every moment is zero)
+  const uint32_t word = __float_as_uint(q2.w);
+  const uint32_t t = word & a.tile_mask;
   const uint32_t ty = t / (uint32_t)a.tiles_x, tx = t - ty * (uint32_t)a.tiles_x;
   const float mx = r0.x - ((float)(tx * RT_W) + RT_W * 0.5f), my = r0.y - ((float)(ty * RT_W) + RT_W * 0.5f);
   const float sv = q1.x, svu = q1.y, svv = q0.x, svuu = q0.y, svuv = q0.z, svvv = q0.w;
@@ -572,6 +560,7 @@ __device__ __forceinline__ void row_gradients(const b2c_raster_bwd_args& a, uint
     v[12] = q3.y * sc;
     v[13] = q3.z * sc;
   }
+  return (word & ~a.tile_mask) == a.row_tag;
 }
 
 template <bool FEAT>
@@ -603,9 +592,10 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
     const uint32_t id = valid ? ids[s] : NO_RUN;
     const uint32_t next_id = lo + 64u < m ? ids[lo + 64u] : NO_RUN;
     float v[RED_VALS];
+    // a row without this pass's tag (a pair past its tile's shrunk end, or a sentinel) counts as zero
+    const bool live = row_gradients<FEAT>(a, valid ? s : 0u, valid ? id : 0u, v) && valid;
 #pragma unroll
-    for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
-    if (valid) row_gradients<FEAT>(a, s, id, v);
+    for (int k = 0; k < RED_VALS; k++) v[k] = live ? v[k] : 0.f;
     const uint32_t prev = dpp_u32<0x138, 0xF>(id, prev_id);  // wave_shr:1; lane 0 gets the row before
     const bool head = valid && id != prev;
     const uint64_t heads = ballot64(head);
@@ -760,8 +750,9 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
       else raster_bwd_fp32_kernel<false, false><<<grid, block, 0, stream>>>(*a);
     }
   } else {
-    if (!a->slot_sorted || !a->tile_end || !a->isect_rows || !a->isect_vals || !a->tile_count ||
-        !a->raster_rec)
+    if (!a->slot_sorted || !a->isect_rows || !a->isect_vals || !a->tile_count || !a->raster_rec)
+      return (int)hipErrorInvalidValue;
+    if (a->num_isect && (a->row_tag == 0u || (a->row_tag & a->tile_mask) != 0u))
       return (int)hipErrorInvalidValue;
     if (feat) {
       if (hollow) raster_bwd_mfma_kernel<true, true><<<grid, block, 0, stream>>>(*a);

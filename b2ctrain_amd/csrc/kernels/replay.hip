@@ -44,13 +44,8 @@ __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
   const uint2 range = reinterpret_cast<const uint2*>(a.tile_ranges)[tile];
   const int lane = threadIdx.x;
   float4* rows = reinterpret_cast<float4*>(a.rows);
-  // entries past the shrunk end composited nowhere: zero rows; the last tile's wave also zeroes the rows of
-  // the sentinel entries (in no tile's list)
-  for (uint32_t i = max(range.y, range.x) + lane; i < a.tile_end[tile]; i += 64)
-    rows[a.slot_sorted[i]] = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (tile == n_tiles - 1)
-    for (uint32_t i = a.tile_end[n_tiles] + lane; i < a.num_isect; i += 64)
-      rows[a.slot_sorted[i]] = make_float4(0.f, 0.f, 0.f, 0.f);
+  // entries past the shrunk end composited nowhere: they get no row (the sum reads a row without this
+  // pass's tag as zero)
   if (range.y <= range.x) return;
   const int px = (tile % a.tiles_x) * RT_W + (lane & 7), py = (tile / a.tiles_x) * RT_W + (lane >> 3);
   const bool inside = px < a.W && py < a.H;
@@ -141,7 +136,7 @@ __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
         a1 += v * s_mr[p];
         a2 += v * s_k[p];
       }
-      rows[s_slot[lane]] = make_float4(a0, a1, a2, 0.f);
+      rows[s_slot[lane]] = make_float4(a0, a1, a2, __uint_as_float(a.row_tag));
       if constexpr (LABELS) {
         float* bins = a.label_acc + (size_t)s_id[lane] * B2C_LABEL_BINS;
         if (ncls == 1) {
@@ -194,8 +189,8 @@ __global__ void __launch_bounds__(256) evidence_reduce_kernel(b2c_evidence_sum_a
   const bool valid = s < a.m;
   const uint32_t id = valid ? a.ids[s] : NO_RUN;
   float v[3] = {0.f, 0.f, 0.f};
-  if (valid) {
-    const float4 r = reinterpret_cast<const float4*>(a.rows)[s];
+  const float4 r = reinterpret_cast<const float4*>(a.rows)[valid ? s : 0u];
+  if (valid && __float_as_uint(r.w) == a.row_tag) {  // another tag: past its tile's shrunk end, zero
     v[0] = r.x;
     v[1] = r.y;
     v[2] = r.z;
@@ -294,7 +289,7 @@ using namespace b2c::dev;
 extern "C" int b2c_hip_evidence_view(const b2c_evidence_args* a, hipStream_t stream) {
   const int n_tiles = a->tiles_x * a->tiles_y;
   if (n_tiles <= 0) return 0;
-  if (!a->raster_rec || !a->rows || !a->slot_sorted || !a->tile_end || !a->gt || !a->out_rgba || !a->last_idx)
+  if (!a->raster_rec || !a->rows || !a->slot_sorted || !a->gt || !a->out_rgba || !a->last_idx || a->row_tag == 0u)
     return (int)hipErrorInvalidValue;
   const bool feat = a->normals && a->normal_weight > 0.f;
   const bool labels = a->labels && a->label_acc;
@@ -312,7 +307,8 @@ extern "C" int b2c_hip_evidence_view(const b2c_evidence_args* a, hipStream_t str
 
 extern "C" int b2c_hip_evidence_sum(const b2c_evidence_sum_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
-  if (!a->ids || !a->rows || !a->view_acc || !a->pos_op || !a->evidence) return (int)hipErrorInvalidValue;
+  if (!a->ids || !a->rows || !a->view_acc || !a->pos_op || !a->evidence || a->row_tag == 0u)
+    return (int)hipErrorInvalidValue;
   const int fill = b2c_hip_fill_u32(reinterpret_cast<uint32_t*>(a->view_acc), 0u, (size_t)a->n * 3, stream);
   if (fill) return fill;
   if (a->m) evidence_reduce_kernel<<<(a->m + 255) / 256, 256, 0, stream>>>(*a);

@@ -167,10 +167,14 @@ int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream);
  * Mode 0 accumulates into v_splat / vis_weight with float atomics, as the reference does. Mode 1 uses no
  * atomics: each (tile, splat) pair writes a 12-float row of raw moments about the tile centre (sum v_sigma
  * * [v, u^2, uv, v^2] | sum v_sigma * [1, u], sum of blend weights, refine sum | sum vis * v_rgb, tile id) to
- * isect_rows[slot_sorted[i]] (rows of pairs past the shrunk range end are written as zeros); the rows of
- * one splat are then a contiguous run in emit order, which a segmented reduction turns into gradient
- * lanes (tile centre from the tile id stored in the row), sums in a fixed order and adds to v_splat, vis_weight and
- * vis_flag. The result is deterministic. */
+ * isect_rows[slot_sorted[i]] for the entries of the shrunk ranges, with the tag word row_tag | tile in its
+ * last float; the rows of one splat are then a contiguous run in emit order, which a segmented reduction
+ * turns into gradient lanes (tile centre from the tag's tile bits), sums in a fixed order and adds to
+ * v_splat, vis_weight and vis_flag. A row whose tag bits (outside tile_mask) differ from row_tag was not
+ * written by this pass (a pair past its tile's shrunk end, or a sentinel entry) and counts as zero, so
+ * those rows are neither written nor cleared. The caller passes a row_tag that no row of the buffer holds
+ * unless this pass wrote it (a fresh tag per pass; the buffer cleared before a tag repeats and whenever the
+ * row layout or tile_mask changes). The result is deterministic. */
 typedef struct b2c_raster_bwd_args {
   const uint32_t* tile_ranges;
   const uint32_t* vals_sorted;
@@ -191,8 +195,9 @@ typedef struct b2c_raster_bwd_args {
   const uint32_t* slot_sorted;/* [M] emit position of list entry i */
   const uint32_t* isect_vals; /* [M] splat id of emit position s (the emit kernel's values) */
   const uint32_t* tile_count; /* [n] intersections per splat (the length of its run of emit positions) */
-  const uint32_t* tile_end;   /* [n_tiles + 1] list end before the forward's shrink; [n_tiles] = sentinel start */
   float* isect_rows;          /* [M][16] scratch (12 floats a row are used without feat) */
+  uint32_t row_tag;           /* this pass's tag bits (none inside tile_mask, not 0) */
+  uint32_t tile_mask;         /* tag bits that hold the tile id: 2^tile_bits - 1, tile ids < 2^tile_bits */
   float* isect_part;          /* [ceil(M / 256)][32] scratch: partial sums of runs crossing 256-row windows */
   uint32_t* isect_part_flags; /* [ceil(M / 256)] scratch */
   void* split_event;          /* optional hipEvent_t recorded between the raster kernel and the reduce */
@@ -289,13 +294,14 @@ int b2c_hip_eval_metrics(const b2c_eval_args* a, hipStream_t stream);
 #define B2C_LABEL_BINS 32      /* class ids >= this are ignored (evidence.cu:39) */
 #define B2C_EVIDENCE_STRIDE 8  /* floats per splat of the evidence accumulator: w_in, w_all, err, -, dir xyz, sum w_in^2 */
 
-/* One view's replay after a forward with bwd_info (shrunk ranges, last_idx, slot_sorted, tile_end): for each
- * (tile, splat) list entry, rows[slot] = (the sums over the tile's composited fragments of vis * m,
- * vis * m * res, vis * k, 0) at the entry's emit position, with m = target alpha * w, res the pixel's mean
+/* One view's replay after a forward with bwd_info (shrunk ranges, last_idx): for each entry of a tile's shrunk
+ * range, rows[slot_sorted[i]] = (the sums over the tile's composited fragments of vis * m,
+ * vis * m * res, vis * k, row_tag as bits) at the entry's emit position, with m = target alpha * w, res the pixel's mean
  * absolute colour residual (+ normal_weight times the normal residual when normals are given), k = (target
- * alpha if masked_has_alpha else 1) * w; entries past a tile's shrunk end (and the sentinel entries) get zero
- * rows. With labels, label_acc[i][class] += vis * k for the pixel's class (< B2C_LABEL_BINS), float
- * atomics. */
+ * alpha if masked_has_alpha else 1) * w; entries past a tile's shrunk end (and the sentinel entries) get no
+ * row (b2c_hip_evidence_sum reads rows tagged with another row_tag as zero; the tag contract is the
+ * backward's, b2c_raster_bwd_args). With labels, label_acc[i][class] += vis * k for the pixel's class
+ * (< B2C_LABEL_BINS), float atomics. */
 typedef struct b2c_evidence_args {
   const uint32_t* tile_ranges;
   const uint32_t* vals_sorted;
@@ -310,9 +316,9 @@ typedef struct b2c_evidence_args {
   int masked_has_alpha;
   float normal_weight;
   const uint32_t* slot_sorted; /* [M] emit position of list entry i */
-  const uint32_t* tile_end;   /* [tiles + 1] list ends before the forward shrank them; [tiles] = sentinel start */
   uint32_t num_isect;
   float* rows;                /* [M][4] at emit positions */
+  uint32_t row_tag;           /* this pass's tag (see b2c_raster_bwd_args) */
   float* label_acc;           /* [n][B2C_LABEL_BINS] or NULL */
 } b2c_evidence_args;
 int b2c_hip_evidence_view(const b2c_evidence_args* a, hipStream_t stream);
@@ -325,7 +331,8 @@ typedef struct b2c_evidence_sum_args {
   int n;
   uint32_t m;                 /* intersections */
   const uint32_t* ids;        /* [M] splat id of emit position s */
-  const float* rows;          /* [M][4] */
+  const float* rows;          /* [M][4]: row s counts when its .w bits equal row_tag */
+  uint32_t row_tag;
   float* view_acc;            /* [n][3] scratch */
   const float* pos_op;        /* [n] float4 */
   float cam_pos[3];

@@ -1,0 +1,115 @@
+"""The row buffer of the atomic-free backward and of the evidence pass holds rows only for the (tile, splat)
+pairs inside the tiles' shrunk ranges. Every row a pass writes carries the pass's tag (a generation, or'd with
+the tile id for the backward's rows); the reductions take a row as the pass's own only when its tag matches,
+so rows past a shrunk end are neither written nor cleared. The context clears the buffer before a tag could
+repeat (at reallocation, when the row layout or the tile bits change, and when the generations run out).
+
+Checked here: poisoning the whole row buffer with NaN before a pass leaves v_splat and vis_weight bit-identical
+and the evidence finite and equal to rounding (its sums use float atomics), so no row past a shrunk end is
+read and every row inside one is written; and passes over changing lists on one context, with the generations
+cut to 1 or 2 per epoch (B2C_ROW_GEN_LIMIT) and an evidence pass switching the row layout in between, give
+the gradients of a fresh context bit for bit."""
+import numpy as np
+import pytest
+
+from b2ctrain_amd import _native
+from b2ctrain_amd import scenes as S
+from tests.gpu_harness import emit
+
+pytestmark = pytest.mark.gpu
+
+
+def _occluded_scene():
+    """Config 4's dense slab cut to an eighth in each image direction (the same depth complexity): most of
+    each tile's list lies behind its last contributor."""
+    return S.config4(shrink=8)
+
+
+def _view_grads(r, sc, cam, gs, poison=False):
+    r.forward(cam=cam)
+    r.loss(grad_scale=gs)
+    r.zero("v_splat")
+    r.zero("vis_flag")
+    r.write_model("vis_weight", np.zeros(sc.n, np.float32))
+    if poison:
+        r.write("isect_rows", np.full((r.info().num_isect, 12), np.nan, np.float32))
+    r.backward(mode=1, grad_scale=gs, cam=cam)
+    return r.read("v_splat"), r.read_model("vis_weight"), r.read("vis_flag")
+
+
+def test_occluded_lists_are_mostly_past_the_shrunk_end():
+    sc = _occluded_scene()
+    r = _native.Renderer(sc)
+    try:
+        r.forward()
+        ranges, tile_end = r.read("tile_ranges").astype(np.int64), r.read("tile_end").astype(np.int64)
+        live = np.clip(ranges[:, 1] - ranges[:, 0], 0, None).sum()
+        total = r.info().num_isect
+        emit(f"    {sc.name}: {1 - live / total:.0%} of {total} list entries lie past their tile's shrunk end")
+        assert live < 0.7 * total and (tile_end[:-1] >= ranges[:, 1]).all()
+    finally:
+        r.close()
+
+
+@pytest.mark.parametrize("make", [_occluded_scene, lambda: S.config2(n=20_000)], ids=["occluded", "config2"])
+def test_backward_reads_no_row_past_the_shrunk_end(make):
+    sc = make()
+    emit(f"poisoned rows, backward {sc.name}")
+    r = _native.Renderer(sc)
+    gs = 3.0 * sc.W * sc.H
+    try:
+        clean = _view_grads(r, sc, sc.cam, gs)
+        poisoned = _view_grads(r, sc, sc.cam, gs, poison=True)
+        for a, b in zip(clean, poisoned):
+            assert np.array_equal(a, b)
+        assert np.isfinite(poisoned[0]).all() and (poisoned[2] != 0).sum() > 100
+    finally:
+        r.close()
+
+
+def test_evidence_reads_no_row_past_the_shrunk_end():
+    sc = _occluded_scene()
+    emit(f"poisoned rows, evidence {sc.name}")
+    r = _native.Renderer(sc)
+    v = _native.View(sc.W, sc.H, sc.gt, sc.weights, has_alpha=True)
+    try:
+        ev = r.compute_evidence([v], [sc.cam])
+        r.write("isect_rows", np.full((r.info().num_isect, 12), np.nan, np.float32))
+        ev2 = r.compute_evidence([v], [sc.cam])
+        # a NaN row read anywhere would make its splat's sums NaN; the sums add run pieces with float
+        # atomics in no fixed order, so the two runs agree to rounding, not bit for bit
+        assert np.isfinite(ev2).all() and (ev2[:, 2] > 0).sum() > 100
+        assert np.allclose(ev2, ev, rtol=1e-5, atol=1e-6 * np.abs(ev).max())
+    finally:
+        v.close()
+        r.close()
+
+
+@pytest.mark.parametrize("limit", ["1", "2"])
+def test_tag_epochs_on_changing_lists(limit, monkeypatch):
+    """With one generation per epoch every pass must clear the buffer first: a pass over another view's
+    lists would otherwise read the previous view's rows as its own (they carry the same tag)."""
+    monkeypatch.setenv("B2C_ROW_GEN_LIMIT", limit)
+    sc = _occluded_scene()
+    cams = sc.extra_cams[:3]
+    gs = 3.0 * sc.W * sc.H
+    emit(f"tag epochs of {limit} generation(s), {sc.name}, {len(cams)} views")
+    fresh = []
+    for cam in cams:
+        r = _native.Renderer(sc)
+        try:
+            fresh.append(_view_grads(r, sc, cam, gs))
+        finally:
+            r.close()
+    r = _native.Renderer(sc)
+    v = _native.View(sc.W, sc.H, sc.gt, sc.weights, has_alpha=True)
+    try:
+        for rnd in range(2):
+            for i, cam in enumerate(cams):
+                got = _view_grads(r, sc, cam, gs)
+                for a, b in zip(got, fresh[i]):
+                    assert np.array_equal(a, b), (rnd, i)
+            r.compute_evidence([v], [cams[0]])  # the evidence rows' layout: the next pass starts an epoch
+    finally:
+        v.close()
+        r.close()
