@@ -262,12 +262,12 @@ def main():
 
     # Roofline of the dominant kernel, the MFMA backward raster (raster_bwd_mfma_kernel), timed alone with
     # hipEvents on the context's stream. Algorithmic bytes per launch: per composited-range intersection its
-    # list entry, emit position and projected splat (4 + 4 + 48 B) plus its gradient row (48 B, written); per
-    # intersection past the shrunk end its zero row (48 B); per pixel out_rgba, out_feat, last_idx and v_out
-    # (52 B). MFMA: 8 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
+    # list entry, emit position and projected splat (4 + 4 + 48 B) plus its gradient row (48 B, written; the
+    # intersections past the shrunk end get no row); per pixel out_rgba, out_feat, last_idx and v_out (52 B).
+    # MFMA: 8 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
     m_shrunk = f_sweep // 64
     nv = len(views)
-    bwd_bytes = 104 * m_shrunk + 48 * (m_total - m_shrunk) + 52 * W * H * nv
+    bwd_bytes = 104 * m_shrunk + 52 * W * H * nv
     t_bwd = mean["raster_bwd_ms"] * 1e-3
     bwd_gbs = bwd_bytes / t_bwd / 1e9
     mfma_tflops = math.ceil(m_shrunk / 8.0) * 8 * 16384 / t_bwd / 1e12
