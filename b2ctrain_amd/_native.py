@@ -405,7 +405,7 @@ _FIELD_SPEC = {
     # name: (dtype, per-element shape, size key)  size key: n splats, P pixels, M isects, T tiles (T1: T + 1)
     "proj0": (np.float32, (4,), "n"), "proj1": (np.float32, (4,), "n"), "proj2": (np.float32, (4,), "n"),
     "proj3": (np.float32, (2,), "n"), "raster_rec": (np.float32, (16,), "n"), "tile_count": (np.uint32, (), "n"), "tile_off": (np.uint32, (), "n"),
-    "hit_info": (np.uint32, (2,), "n"), "order": (np.uint32, (), "n"), "depth_keys_sorted": (np.uint32, (), "n"),
+    "hit_info": (np.uint32, (2,), "n"), "hit_wide": (np.uint32, (2,), "n"), "order": (np.uint32, (), "n"), "depth_keys_sorted": (np.uint32, (), "n"),
     "keys": (np.uint32, (), "M"), "vals": (np.uint32, (), "M"), "keys_sorted": (np.uint32, (), "M"),
     "vals_sorted": (np.uint32, (), "M"), "tile_ranges": (np.uint32, (2,), "T"), "out_rgba": (np.float32, (4,), "P"),
     "out_feat": (np.float32, (4,), "P"), "last_idx": (np.uint32, (), "P"), "v_out": (np.float32, (4,), "P"),

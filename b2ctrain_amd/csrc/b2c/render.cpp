@@ -70,7 +70,7 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   if (depth_bits > 20) depth_bits = 20;
   const size_t nn = (size_t)(n > 0 ? n : 1);
   proj0.reserve(nn); proj1.reserve(nn); proj2.reserve(nn); proj3.reserve(nn); raster_rec.reserve(nn * 4);
-  tile_count.reserve(nn); tile_off.reserve(nn); hit_info.reserve(nn);
+  tile_count.reserve(nn); tile_off.reserve(nn); hit_info.reserve(nn); hit_wide.reserve(nn);
   depth_keys.reserve(nn); depth_keys_sorted.reserve(nn); order_in.reserve(nn); order.reserve(nn);
   depth_alt_k.reserve(nn); depth_alt_v.reserve(nn);
   big_list.reserve(nn); big_base.reserve(nn); big_info.reserve(nn); big_chunk.reserve(nn * B2C_BIG_CHUNKS);
@@ -157,6 +157,7 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   a.raster_rec = reinterpret_cast<float*>(ctx.raster_rec.ptr);
   a.tile_count = ctx.tile_count.ptr;
   a.hit_info = reinterpret_cast<uint32_t*>(ctx.hit_info.ptr);
+  a.hit_wide = reinterpret_cast<uint32_t*>(ctx.hit_wide.ptr);
   a.max_screen = m.max_screen.ptr;
   a.big_list = ctx.big_list.ptr;
   a.big_count = ctx.counters.ptr;
@@ -179,6 +180,7 @@ void emit_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   b2c_emit_args e{};
   e.n = m.n; e.order = ctx.order; e.tile_count = ctx.tile_count; e.tile_off = ctx.tile_off;
   e.hit_info = reinterpret_cast<const uint32_t*>(ctx.hit_info.ptr);
+  e.hit_wide = reinterpret_cast<const uint32_t*>(ctx.hit_wide.ptr);
   e.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr); e.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
   e.tiles_x = ctx.tiles_x; e.tiles_y = ctx.tiles_y; e.cap = cap;
   e.keys = ctx.keys; e.vals = ctx.vals;

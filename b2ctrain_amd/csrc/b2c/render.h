@@ -68,6 +68,8 @@ struct RenderCtx {
   DevBuf<float4> raster_rec;           // [n][4]: the raster kernels' 64-byte per-splat record (same values)
   DevBuf<uint32_t> tile_count, tile_off;  // hit count; inclusive scan in depth order
   DevBuf<uint2> hit_info;                 // (hit mask within the bbox or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24)
+  DevBuf<uint2> hit_wide;                 // where hit_info's mask word is 0xFFFFFFFF: the 64-bit mask of a bbox
+                                          // of at most 64 tiles, or (0, 0) beyond 64 tiles
   DevBuf<uint32_t> depth_keys, depth_keys_sorted, order_in, order;  // depth sort
   DevBuf<uint32_t> count_perm;  // kept for layout compatibility; the count scan gathers in place
   // intersections

@@ -133,6 +133,7 @@ Field ctx_field(b2c_ctx* c, const std::string& name) {
       {"tile_count", {x.tile_count.ptr, n * 4}},
       {"tile_off", {x.tile_off.ptr, n * 4}},
       {"hit_info", {x.hit_info.ptr, n * 8}},
+      {"hit_wide", {x.hit_wide.ptr, n * 8}},
       {"order", {x.order.ptr, n * 4}},
       {"depth_keys_sorted", {x.depth_keys_sorted.ptr, n * 4}},
       {"keys", {x.keys.ptr, M * 4}},

@@ -301,33 +301,48 @@ __device__ __forceinline__ uint32_t select_bit(uint32_t m, uint32_t k) {
   return pos;
 }
 
+// Position of the k-th set bit (k < popcount) of the 64-bit mask (hi, lo).
+__device__ __forceinline__ uint32_t select_bit64(uint32_t lo, uint32_t hi, uint32_t k) {
+  const uint32_t pl = (uint32_t)__builtin_popcount(lo);
+  const bool up = k >= pl;
+  return select_bit(up ? hi : lo, up ? k - pl : k) + (up ? 32u : 0u);
+}
+
 // Small splats: each wave takes 64 consecutive depth ranks, whose slot ranges [tile_off - count, tile_off)
 // are adjacent (big splats' ranges, filled by emit_big_kernel, interleave). The wave's intersections are
 // dealt to the lanes round-robin: intersection q belongs to the last rank whose running start is <= q (a
 // binary search over the wave's 64 starts in LDS) and is the k-th set bit of that splat's hit mask
-// (row-major bbox order). Every lane does the same work and consecutive lanes write consecutive slots.
-// Big splats only record their base.
+// (row-major bbox order; a bbox of up to 64 tiles: the mask of hit_info or of hit_wide). Every lane does
+// the same work and consecutive lanes write consecutive slots. Big splats only record their base.
 __global__ void __launch_bounds__(256) emit_small_kernel(b2c_emit_args a, uint32_t* __restrict__ big_base) {
-  __shared__ uint32_t s_start[4][64], s_base[4][64], s_mask[4][64], s_info[4][64], s_id[4][64];
+  __shared__ uint32_t s_start[4][64], s_base[4][64], s_mask[4][64], s_mask_hi[4][64], s_info[4][64], s_id[4][64];
   const int w = threadIdx.x >> 6, lane = lane_id();
   const int r = blockIdx.x * 256 + threadIdx.x;
   uint32_t i = 0, cnt = 0, base = 0;
-  uint2 hi = make_uint2(0u, 0u);
+  uint2 hi = make_uint2(0u, 0u), wide = make_uint2(0u, 0u);
+  bool big = false;
   if (r < a.n) {
     i = a.order[r];
     cnt = a.tile_count[i];
     if (cnt) {
       base = a.tile_off[r] - cnt;
       hi = reinterpret_cast<const uint2*>(a.hit_info)[i];
-      if (hi.x == 0xFFFFFFFFu) big_base[i] = base;
+      if (hi.x == 0xFFFFFFFFu) {
+        wide = reinterpret_cast<const uint2*>(a.hit_wide)[i];
+        big = (wide.x | wide.y) == 0u;  // a splat with hits and no mask: over 64 bbox tiles
+        if (big) big_base[i] = base;
+      } else {
+        wide = make_uint2(hi.x, 0u);
+      }
     }
   }
-  const uint32_t c = (cnt && hi.x != 0xFFFFFFFFu && base + cnt <= a.cap) ? cnt : 0u;
+  const uint32_t c = (cnt && !big && base + cnt <= a.cap) ? cnt : 0u;
   const uint32_t incl = wave_incl_scan(c);
   const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
   s_start[w][lane] = incl - c;
   s_base[w][lane] = base;
-  s_mask[w][lane] = hi.x;
+  s_mask[w][lane] = wide.x;
+  s_mask_hi[w][lane] = wide.y;
   s_info[w][lane] = hi.y;
   s_id[w][lane] = i;
   __syncthreads();
@@ -339,7 +354,7 @@ __global__ void __launch_bounds__(256) emit_small_kernel(b2c_emit_args a, uint32
     const uint32_t k = q - s_start[w][j];
     const uint32_t info = s_info[w][j];
     const uint32_t min_x = info & 0xFFFu, min_y = (info >> 12) & 0xFFFu, bw = info >> 24;
-    const uint32_t bit = select_bit(s_mask[w][j], k);
+    const uint32_t bit = select_bit64(s_mask[w][j], s_mask_hi[w][j], k);
     const uint32_t row = bit / bw;
     const uint32_t slot = s_base[w][j] + k;
     a.keys[slot] = (min_y + row) * (uint32_t)a.tiles_x + min_x + (bit - row * bw);
@@ -564,7 +579,8 @@ extern "C" int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t*
 
 extern "C" int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
-  if (!a->big_info || !a->big_chunk || !a->big_items || !a->big_items_count) return (int)hipErrorInvalidValue;
+  if (!a->big_info || !a->big_chunk || !a->big_items || !a->big_items_count || !a->hit_wide)
+    return (int)hipErrorInvalidValue;
   emit_small_kernel<<<dim3((a->n + 255) / 256), dim3(256), 0, stream>>>(*a, a->big_base);
   emit_big_kernel<<<dim3(B2C_BIG_GRID), dim3(256), 0, stream>>>(*a, a->big_base);
   return (int)hipGetLastError();

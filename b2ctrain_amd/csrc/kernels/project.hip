@@ -1,8 +1,9 @@
 // Projection (replaces src/gpu/project.cu:8-126): one thread per splat, EWA projection, SH colour, the
 // feature lanes (pseudo-normal or a caller's buffer), exact ellipse/8x8-tile test over the splat's tile
-// bounding box. Splats with more than 32 bbox tiles are not counted inline (one thread walking hundreds of
-// tiles stalls its whole wave): they are appended to a list and counted in parallel chunks of their bbox,
-// one wave per chunk.
+// bounding box. Splats of at most 64 bbox tiles (the reference's limit is 32, a warp's mask) are tested by
+// the wave together, into a 64-bit hit mask; splats with more than 64 bbox tiles are not counted inline
+// (one thread walking hundreds of tiles stalls its whole wave): they are appended to a list and counted in
+// parallel chunks of their bbox, one wave per chunk.
 #pragma clang fp contract(off)
 #include "b2c_kernels.h"
 #include "device_math.h"
@@ -18,7 +19,7 @@ namespace {
 // slower). One big-list append per workgroup (same-address atomics serialise).
 constexpr int PROJ_BLOCK = 256;
 
-// Tile tests of the wave's small splats (bbox of at most 32 tiles) are shared out over all 64 lanes: the
+// Tile tests of the wave's small splats (bbox of at most 64 tiles) are shared out over all 64 lanes: the
 // splats' bbox areas are prefix-summed across the wave, test t goes to lane t mod 64, which finds the
 // owning splat by binary search over the prefix and sets the hit bit in the owner's mask in LDS. A wave
 // then costs ceil(sum of areas / 64) tile tests per lane instead of its largest bbox.
@@ -34,7 +35,7 @@ template <int DEG, bool HALF, bool FEAT>
 __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a) {
   __shared__ WaveRec s_rec[PROJ_BLOCK];
   __shared__ uint32_t s_incl[PROJ_BLOCK];
-  __shared__ uint32_t s_mask[PROJ_BLOCK];
+  __shared__ uint32_t s_mask[2][PROJ_BLOCK];  // hit mask bits 0-31, 32-63
   const int i = blockIdx.x * PROJ_BLOCK + threadIdx.x;
   const int lane = lane_id();
   const int wbase = threadIdx.x & ~63;
@@ -53,7 +54,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       const float power = det_logf(pr.opacity * 255.f);
       bb = tile_bbox(pr.px, pr.py, pr.ex, pr.ey, a.tiles_x, a.tiles_y);
       const int bw = bb.max_x - bb.min_x, bh = bb.max_y - bb.min_y;
-      big = bw * bh > 32;
+      big = bw * bh > 64;
       small = !big;
       if (small) {
         area = (uint32_t)(bw * bh);
@@ -136,7 +137,8 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
   }
   const uint32_t total = __shfl(incl, 63);
   s_incl[threadIdx.x] = incl;
-  s_mask[threadIdx.x] = 0u;
+  s_mask[0][threadIdx.x] = 0u;
+  s_mask[1][threadIdx.x] = 0u;
   __syncthreads();
   for (uint32_t t0 = 0; t0 < total; t0 += 64) {
     const uint32_t t = t0 + (uint32_t)lane;
@@ -156,21 +158,20 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       const int ty = (int)(rec.origin >> 16) + (int)row;
       const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
       if (tile_hit(rx, ry, rx + RT_W, ry + RT_W, rec.mx, rec.my, Sym2{rec.c00, rec.c01, rec.c11}, rec.power))
-        atomicOr(&s_mask[wbase + owner], 1u << bit);
+        atomicOr(&s_mask[bit >> 5][wbase + owner], 1u << (bit & 31u));
     }
   }
   __syncthreads();
-  if (small) {
-    const uint32_t mask = s_mask[threadIdx.x];
-    a.tile_count[i] = (uint32_t)__popc(mask);
-    // A 32-tile bbox with every tile hit encodes to the same mask as "recompute" (0xFFFFFFFF); the
-    // emit then treats it as a big splat (binning.cu:37,75), so it goes on the big list too.
-    big = mask == 0xFFFFFFFFu;
-    reinterpret_cast<uint2*>(a.hit_info)[i] =
-        make_uint2(mask, (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)(bb.max_x - bb.min_x) << 24));
-  } else if (big) {
-    reinterpret_cast<uint2*>(a.hit_info)[i] =
-        make_uint2(0xFFFFFFFFu, (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)(bb.max_x - bb.min_x) << 24));
+  if (small || big) {
+    const uint32_t info = (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 12) | ((uint32_t)(bb.max_x - bb.min_x) << 24);
+    const uint32_t lo = small ? s_mask[0][threadIdx.x] : 0u, hi = small ? s_mask[1][threadIdx.x] : 0u;
+    // The mask word of hit_info keeps the reference's meaning (binning.cu:37): the mask of a bbox of at
+    // most 32 tiles, or 0xFFFFFFFF ("recompute"). A bbox of 33 to 64 tiles, or a full 32-tile mask (which
+    // reads as "recompute"), keeps its mask in hit_wide; a big splat marks hit_wide (0, 0).
+    const bool wide = big || area > 32u || lo == 0xFFFFFFFFu;
+    reinterpret_cast<uint2*>(a.hit_info)[i] = make_uint2(wide ? 0xFFFFFFFFu : lo, info);
+    if (wide) reinterpret_cast<uint2*>(a.hit_wide)[i] = make_uint2(lo, hi);
+    if (small) a.tile_count[i] = (uint32_t)(__popc(lo) + __popc(hi));
   }
   // workgroup-aggregated append of big splats: one device-scope atomic per workgroup (contended atomics
   // on one address are serialised at the memory side and cost ~10 ns each)
@@ -348,7 +349,7 @@ void launch_project(const b2c_project_args& a, dim3 grid, dim3 block, bool half,
 extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
-  if (!a->big_count || !a->big_list) return (int)hipErrorInvalidValue;
+  if (!a->big_count || !a->big_list || !a->hit_wide) return (int)hipErrorInvalidValue;
   if (a->feat_mode < 0 || a->feat_mode > 2 || (a->feat_mode == 2 && !a->feat_buffer)) return (int)hipErrorInvalidValue;
   clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);  // one launch for both
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);

@@ -53,11 +53,14 @@ typedef struct b2c_project_args {
   float* proj3;        /* [n] float2 (feat.y, feat.z) */
   uint32_t* tile_count;/* [n] */
   uint32_t* hit_info;  /* [n] uint2 (hit mask or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24) */
+  uint32_t* hit_wide;  /* [n] uint2, written where hit_info's mask word is 0xFFFFFFFF: the 64-bit hit mask
+                          (low word first, bits in row-major bbox order) of a bbox of at most 64 tiles, or
+                          (0, 0) for a bbox of more than 64 tiles */
   float* max_screen;   /* [n] or NULL: max(., max(ex/W, ey/H)) (project.cu:82-83) */
   float* raster_rec;   /* [n][16]: the raster kernels' per-splat record, one 64-byte line: (mx, my, c00/2, c01),
                           (c11/2, opacity, power, sign bits of r, g, b), (max(r,0), max(g,0), max(b,0), log2 opacity),
                           (feat.x, feat.y, feat.z, camera depth) */
-  uint32_t* big_list;  /* [n] scratch: splats whose bbox exceeds 32 tiles */
+  uint32_t* big_list;  /* [n] scratch: splats whose bbox exceeds 64 tiles */
   uint32_t* big_count; /* [1] scratch counter */
   uint32_t* big_info;  /* [n][4] scratch: per big-list entry, bbox origin, width, area, chunk length */
   uint32_t* big_chunk; /* [n][B2C_BIG_CHUNKS] scratch: per-chunk exclusive hit offsets of each entry */
@@ -108,14 +111,17 @@ size_t b2c_scan_temp_bytes(uint32_t n);
 int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
                         uint32_t* total_dev, void* temp, size_t temp_bytes, hipStream_t stream);
 
-/* emit_kernel (binning.cu:25-93): intersections in depth order, key = tile id, val = splat index. Small
- * splats (hit mask) are emitted by one thread each, walking the set bits of the mask; splats with more
- * than 32 bbox tiles by one wave per chunk of their bbox (the chunks b2c_hip_project counted), in
- * row-major order. Slots a big splat does not fill get key = n_tiles (cannot happen when the counts come
+/* emit_kernel (binning.cu:25-93): intersections in depth order, key = tile id, val = splat index. Splats of
+ * at most 64 bbox tiles (the hit mask of hit_info, or of hit_wide for 33 to 64 tiles and for a full
+ * 32-tile mask) are dealt out over the lanes of a wave, each intersection the k-th set bit of its splat's
+ * mask; splats with more than 64 bbox tiles are emitted by one wave per chunk of their bbox (the chunks
+ * b2c_hip_project counted), in row-major order: the reference's serial re-test of every splat over 32
+ * tiles gives the same lists, since the bbox and the tile test are the projection's. Slots a big splat does not fill get key = n_tiles (cannot happen when the counts come
  * from b2c_hip_project; kept as the reference's guard). */
 typedef struct b2c_emit_args {
   int n;
   const uint32_t* order, *tile_count, *tile_off, *hit_info;
+  const uint32_t* hit_wide;             /* from b2c_hip_project */
   const float* proj0, *proj1;
   int tiles_x, tiles_y;
   uint32_t cap;

@@ -46,6 +46,13 @@ def check_projection(r, scene, camd):
         bad = ~((a == b) | (np.isnan(a) & np.isnan(b)))
         assert not bad.any(), f"{k} differs for splats {np.flatnonzero(ok)[np.flatnonzero(bad.any(1))[:10]]}"
     assert np.array_equal(g["hit_info"][ok], pr["hit_info"][ok]), "hit_info differs"
+    # where the reference's mask word says "recompute", hit_wide holds the 64-bit mask of a bbox of at most 64
+    # tiles (as many bits as hits) or (0, 0) beyond 64 tiles; the emitted lists check the bits' positions
+    rec = ok & (pr["hit_info"][:, 0] == 0xFFFFFFFF)
+    wide = r.read("hit_wide")[rec]
+    bits = np.unpackbits(wide.view(np.uint8), axis=1).sum(1)
+    none = (wide == 0).all(1)
+    assert ((bits == pr["tile_count"][rec]) | none).all(), "hit_wide bit counts differ from tile_count"
     return {**pr, **{k: g[k] for k in g}}
 
 
