@@ -11,7 +11,8 @@ namespace b2c {
 namespace dev {
 namespace {
 
-constexpr int VSTRIDE = 65;  // row stride of the [splat][pixel] weight matrix in LDS (conflict-free columns)
+constexpr int VSTRIDE = 68;  // row stride of the [splat][pixel] weight matrix in LDS (16-byte rows; a row's
+                             // 16-byte reads by consecutive lanes start 4 banks apart)
 constexpr uint32_t LABEL_NONE = 0xFFFFFFFFu;  // a pixel that takes no part in the label vote
 
 __device__ __forceinline__ float byte_chan(uint32_t p, int c) { return (float)((p >> (8 * c)) & 0xffu) * (1.f / 255.f); }
@@ -33,9 +34,9 @@ template <bool FEAT, bool LABELS>
 __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
   __shared__ float4 s_g0[64], s_g1[64];
   __shared__ uint32_t s_id[64];
-  __shared__ float s_vis[64 * VSTRIDE];
-  __shared__ float s_m[64], s_mr[64], s_k[64];
-  __shared__ float s_kc[LABELS ? MAXC : 1][64];  // k of the pixels of the tile's c-th class, else 0
+  __shared__ __attribute__((aligned(16))) float s_vis[64 * VSTRIDE];
+  __shared__ __attribute__((aligned(16))) float s_m[64], s_mr[64], s_k[64];
+  __shared__ __attribute__((aligned(16))) float s_kc[LABELS ? MAXC : 1][64];  // k of the tile's c-th class's pixels, else 0
   __shared__ uint32_t s_lab[64];                 // class of the pixels beyond the first MAXC classes
   __shared__ uint32_t s_slot[64];
   const int n_tiles = a.tiles_x * a.tiles_y;
@@ -128,29 +129,39 @@ __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
     __syncthreads();
     if ((uint32_t)lane < count) {
       const float* row = s_vis + lane * VSTRIDE;
+      // four pixels per 16-byte LDS read: the row, and the pixel vectors (broadcast to every lane)
+      const float4* row4 = reinterpret_cast<const float4*>(row);
       float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-#pragma unroll 8
-      for (int p = 0; p < 64; p++) {
-        const float v = row[p];
-        a0 += v * s_m[p];
-        a1 += v * s_mr[p];
-        a2 += v * s_k[p];
+#pragma unroll 4
+      for (int q = 0; q < 16; q++) {
+        const float4 v = row4[q];
+        const float4 m4 = reinterpret_cast<const float4*>(s_m)[q], r4 = reinterpret_cast<const float4*>(s_mr)[q],
+                     k4 = reinterpret_cast<const float4*>(s_k)[q];
+        a0 += v.x * m4.x; a0 += v.y * m4.y; a0 += v.z * m4.z; a0 += v.w * m4.w;
+        a1 += v.x * r4.x; a1 += v.y * r4.y; a1 += v.z * r4.z; a1 += v.w * r4.w;
+        a2 += v.x * k4.x; a2 += v.y * k4.y; a2 += v.z * k4.z; a2 += v.w * k4.w;
       }
       rows[s_slot[lane]] = make_float4(a0, a1, a2, __uint_as_float(a.row_tag));
       if constexpr (LABELS) {
         float* bins = a.label_acc + (size_t)s_id[lane] * B2C_LABEL_BINS;
         if (ncls == 1) {
           float c0 = 0.f;
-#pragma unroll 8
-          for (int p = 0; p < 64; p++) c0 += row[p] * s_kc[0][p];
+#pragma unroll 4
+          for (int q = 0; q < 16; q++) {
+            const float4 v = row4[q], k4 = reinterpret_cast<const float4*>(s_kc[0])[q];
+            c0 += v.x * k4.x; c0 += v.y * k4.y; c0 += v.z * k4.z; c0 += v.w * k4.w;
+          }
           if (c0 != 0.f) atomicAdd(bins + cls[0], c0);
         } else if (ncls > 1) {
           float cc[MAXC] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-          for (int p = 0; p < 64; p++) {
-            const float v = row[p];
+#pragma unroll 2
+          for (int q = 0; q < 16; q++) {
+            const float4 v = row4[q];
 #pragma unroll
-            for (int c = 0; c < MAXC; c++) cc[c] += v * s_kc[c][p];
+            for (int c = 0; c < MAXC; c++) {
+              const float4 k4 = reinterpret_cast<const float4*>(s_kc[c])[q];
+              cc[c] += v.x * k4.x; cc[c] += v.y * k4.y; cc[c] += v.z * k4.z; cc[c] += v.w * k4.w;
+            }
           }
 #pragma unroll
           for (int c = 0; c < MAXC; c++)
