@@ -152,10 +152,13 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   a.sh = m.sh().view();
   a.cam = p.cam.dev();
   a.tiles_x = ctx.tiles_x; a.tiles_y = ctx.tiles_y;
-  a.proj0 = reinterpret_cast<float*>(ctx.proj0.ptr); a.proj1 = reinterpret_cast<float*>(ctx.proj1.ptr);
-  a.proj2 = reinterpret_cast<float*>(ctx.proj2.ptr); a.proj3 = reinterpret_cast<float*>(ctx.proj3.ptr);
+  if (p.write_proj) {
+    a.proj0 = reinterpret_cast<float*>(ctx.proj0.ptr); a.proj1 = reinterpret_cast<float*>(ctx.proj1.ptr);
+    a.proj2 = reinterpret_cast<float*>(ctx.proj2.ptr); a.proj3 = reinterpret_cast<float*>(ctx.proj3.ptr);
+  }
   a.raster_rec = reinterpret_cast<float*>(ctx.raster_rec.ptr);
   a.tile_count = ctx.tile_count.ptr;
+  a.depth_bits = ctx.depth_keys.ptr;  // made the depth keys in place by the binning
   a.hit_info = reinterpret_cast<uint32_t*>(ctx.hit_info.ptr);
   a.hit_wide = reinterpret_cast<uint32_t*>(ctx.hit_wide.ptr);
   a.max_screen = m.max_screen.ptr;
@@ -181,7 +184,7 @@ void emit_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   e.n = m.n; e.order = ctx.order; e.tile_count = ctx.tile_count; e.tile_off = ctx.tile_off;
   e.hit_info = reinterpret_cast<const uint32_t*>(ctx.hit_info.ptr);
   e.hit_wide = reinterpret_cast<const uint32_t*>(ctx.hit_wide.ptr);
-  e.proj0 = reinterpret_cast<const float*>(ctx.proj0.ptr); e.proj1 = reinterpret_cast<const float*>(ctx.proj1.ptr);
+  e.raster_rec = reinterpret_cast<const float*>(ctx.raster_rec.ptr);
   e.tiles_x = ctx.tiles_x; e.tiles_y = ctx.tiles_y; e.cap = cap;
   e.keys = ctx.keys; e.vals = ctx.vals;
   e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
@@ -208,7 +211,7 @@ void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   }
   const int n = m.n;
   // 1. depth sort of the splats (culled ones sort last), stable on the 32 z bits
-  LAUNCH_CHECK(b2c_hip_depth_keys(n, ctx.tile_count, reinterpret_cast<const float*>(ctx.proj1.ptr), ctx.depth_keys,
+  LAUNCH_CHECK(b2c_hip_depth_keys(n, ctx.tile_count, ctx.depth_keys, ctx.depth_keys,
                                   ctx.order_in, stream));
   LAUNCH_CHECK(b2c_hip_radix_sort_pairs(ctx.depth_keys, ctx.order_in, ctx.depth_keys_sorted, ctx.order, ctx.depth_alt_k,
                                         ctx.depth_alt_v, (uint32_t)n, nullptr, 0, 32, ctx.sort_tmp.ptr,

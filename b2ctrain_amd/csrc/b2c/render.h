@@ -42,6 +42,9 @@ struct RenderParams {
   const float* feat_buffer = nullptr;    // [n][3] device, FeatureMode::Buffer
   bool mip = false;
   bool bwd_info = true;  // write per-pixel last index / shrink tile ranges
+  // Write proj0..3, the reference's projection buffers. The raster, binning and replay kernels read only the
+  // 64-byte raster record, so a caller that does not read proj0..3 (the fused training step) can skip them.
+  bool write_proj = true;
   const float2* warp = nullptr;
   int warp_w = 0, warp_h = 0;
   const float4* pos_override = nullptr;

@@ -834,7 +834,8 @@ namespace {
 int train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opts* ro, const b2c_loss_opts* lo,
                int mode, int flags, const b2c_adam_opts* adam, b2c_step_times* times) {
   return guarded([&] {
-    const b2c::RenderParams p = to_params(*ro);
+    b2c::RenderParams p = to_params(*ro);
+    p.write_proj = mode == 0;  // only the fp32 backward reads proj0..3; the step leaves them unwritten otherwise
     b2c::LossParams lp = to_loss(*lo);
     lp.assign_loss = true;  // the step's loss replaces loss_accum[0..1] (no separate clear)
     lp.running_sum = true;  // and [2..3] become what the trainer's per-step clear + accumulate_loss leave

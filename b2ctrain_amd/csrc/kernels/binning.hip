@@ -225,11 +225,11 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
 }
 
 __global__ void __launch_bounds__(256) depth_keys_kernel(int n, const uint32_t* __restrict__ tile_count,
-                                                         const float4* __restrict__ proj1, uint32_t* __restrict__ keys,
+                                                         const uint32_t* depth_bits, uint32_t* keys,
                                                          uint32_t* __restrict__ vals) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
-  keys[i] = tile_count[i] ? __float_as_uint(proj1[i].z) : 0xFFFFFFFFu;
+  keys[i] = tile_count[i] ? depth_bits[i] : 0xFFFFFFFFu;  // in place when keys is depth_bits
   vals[i] = (uint32_t)i;
 }
 
@@ -385,15 +385,13 @@ __global__ void __launch_bounds__(256) emit_big_kernel(b2c_emit_args a, const ui
     const uint32_t off_next = chunk[min(k + 1u, (uint32_t)B2C_BIG_CHUNKS - 1u)];
     const uint32_t cnt = a.tile_count[i];
     const uint32_t base = big_base[i];
-    const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
-    const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
+    const SplatRecGeom g = splat_rec_geom(a.raster_rec, i);
     // the record is used here, so its loads share the third round trip (instead of being sunk into the
     // tile loop's guard)
-    asm volatile("" : : "v"(p0.x), "v"(p0.y), "v"(p0.z), "v"(p0.w), "v"(p1.x), "v"(p1.w));
+    asm volatile("" : : "v"(g.mx), "v"(g.my), "v"(g.conic.c00), "v"(g.conic.c01), "v"(g.conic.c11), "v"(g.power));
     const bool fits = base + cnt <= a.cap;
     const uint32_t begin = k * info.w, end = fits ? min(begin + info.w, info.z) : begin;
     const uint32_t off_end = fits ? (end < info.z ? off_next : cnt) : off;
-    const Sym2 conic{p0.z, p0.w, p1.x};
     const int min_x = (int)(info.x & 0xFFFFu), min_y = (int)(info.x >> 16), bw = (int)info.y;
     uint32_t written = off;
     for (uint32_t b0 = begin; b0 < end; b0 += 64) {
@@ -404,7 +402,7 @@ __global__ void __launch_bounds__(256) emit_big_kernel(b2c_emit_args a, const ui
         tx = min_x + (int)(b % (uint32_t)bw);
         ty = min_y + (int)(b / (uint32_t)bw);
         const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
-        h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, p0.x, p0.y, conic, p1.w);
+        h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, g.mx, g.my, g.conic, g.power);
       }
       const uint64_t mk = ballot64(h);
       if (h) {
@@ -556,10 +554,10 @@ extern "C" int b2c_hip_radix_sort_pairs(const uint32_t* keys_in, const uint32_t*
                                 n_dev, begin_bit, end_bit, temp, temp_bytes, stream);
 }
 
-extern "C" int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const float* proj1, uint32_t* keys, uint32_t* vals,
+extern "C" int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const uint32_t* depth_bits, uint32_t* keys, uint32_t* vals,
                                   hipStream_t stream) {
   if (n <= 0) return 0;
-  depth_keys_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(n, tile_count, reinterpret_cast<const float4*>(proj1),
+  depth_keys_kernel<<<dim3((n + 255) / 256), dim3(256), 0, stream>>>(n, tile_count, depth_bits,
                                                                       keys, vals);
   return (int)hipGetLastError();
 }

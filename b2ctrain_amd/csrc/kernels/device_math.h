@@ -20,6 +20,19 @@ constexpr float SH_C0 = 0.28209479177387814f;
 
 struct Sym2 { float c00, c01, c11; };
 
+// The projected splat's centre, conic and cutoff power from its 64-byte raster record ((mx, my, c00 / 2,
+// c01), (c11 / 2, opacity, power, .)): doubling the stored halves restores the conic exactly.
+struct SplatRecGeom {
+  float mx, my;
+  Sym2 conic;
+  float power;
+};
+__device__ __forceinline__ SplatRecGeom splat_rec_geom(const float* raster_rec, uint32_t i) {
+  const float4* rec = reinterpret_cast<const float4*>(raster_rec) + (size_t)i * 4;
+  const float4 r0 = rec[0], r1 = rec[1];
+  return SplatRecGeom{r0.x, r0.y, Sym2{2.f * r0.z, r0.w, 2.f * r1.x}, r1.z};
+}
+
 // Cephes expf (S. L. Moshier, Cephes Math Library, single/expf.c): n = round(x / ln2), r = x - n ln2 with
 // ln2 split in two constants (Cody-Waite), degree-6 polynomial for e^r, scaled by 2^n. Inputs below -86
 // return 0 so no subnormal is produced; above 88 return +inf.

@@ -110,11 +110,14 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
         f1 = __builtin_isfinite(f1) ? fminf(fmaxf(f1, -100.f), 100.f) : 0.f;
         f2 = __builtin_isfinite(f2) ? fminf(fmaxf(f2, -100.f), 100.f) : 0.f;
       }
-      reinterpret_cast<float4*>(a.proj0)[i] = make_float4(pr.px, pr.py, pr.conic.c00, pr.conic.c01);
-      reinterpret_cast<float4*>(a.proj1)[i] = make_float4(pr.conic.c11, pr.opacity, pr.c[2], power);
-      reinterpret_cast<float4*>(a.proj2)[i] = make_float4(cr, cg, cb, f0);
-      reinterpret_cast<float2*>(a.proj3)[i] = make_float2(f1, f2);
-      if (a.raster_rec) {  // halving the conic diagonal is exact: the raster evaluates the reference's sigma
+      a.depth_bits[i] = __float_as_uint(pr.c[2]);
+      if (a.proj0) {  // the reference's projection buffers, for callers that read them
+        reinterpret_cast<float4*>(a.proj0)[i] = make_float4(pr.px, pr.py, pr.conic.c00, pr.conic.c01);
+        reinterpret_cast<float4*>(a.proj1)[i] = make_float4(pr.conic.c11, pr.opacity, pr.c[2], power);
+        reinterpret_cast<float4*>(a.proj2)[i] = make_float4(cr, cg, cb, f0);
+        reinterpret_cast<float2*>(a.proj3)[i] = make_float2(f1, f2);
+      }
+      {  // halving the conic diagonal is exact: the raster evaluates the reference's sigma
         float4* rec = reinterpret_cast<float4*>(a.raster_rec) + (size_t)i * 4;
         const uint32_t sgn = (cr >= 0.f ? 1u : 0u) | (cg >= 0.f ? 2u : 0u) | (cb >= 0.f ? 4u : 0u);
         rec[0] = make_float4(pr.px, pr.py, 0.5f * pr.conic.c00, pr.conic.c01);
@@ -203,11 +206,10 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
 // length and appends its items, big_count_kernel the per-chunk hits, big_sum_kernel the per-chunk
 // exclusive offsets (used by the emit) and the tile count.
 __device__ __forceinline__ uint4 big_bbox_info(const b2c_project_args& a, uint32_t i) {
-  const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
-  const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
+  const SplatRecGeom g = splat_rec_geom(a.raster_rec, i);
   float ex, ey;
-  extent_from_conic(Sym2{p0.z, p0.w, p1.x}, p1.w, ex, ey);
-  const TileBox bb = tile_bbox(p0.x, p0.y, ex, ey, a.tiles_x, a.tiles_y);
+  extent_from_conic(g.conic, g.power, ex, ey);
+  const TileBox bb = tile_bbox(g.mx, g.my, ex, ey, a.tiles_x, a.tiles_y);
   const uint32_t bw = (uint32_t)(bb.max_x - bb.min_x);
   const uint32_t area = bw * (uint32_t)(bb.max_y - bb.min_y);
   const uint32_t per = (area + B2C_BIG_CHUNKS - 1) / B2C_BIG_CHUNKS;
@@ -271,9 +273,7 @@ __global__ void __launch_bounds__(256) big_count_kernel(b2c_project_args a) {
     const uint4 info = reinterpret_cast<const uint4*>(a.big_info)[e];
     const uint32_t i = a.big_list[e];
     const uint32_t begin = k * info.w, end = min(begin + info.w, info.z);
-    const float4 p0 = reinterpret_cast<const float4*>(a.proj0)[i];
-    const float4 p1 = reinterpret_cast<const float4*>(a.proj1)[i];
-    const Sym2 conic{p0.z, p0.w, p1.x};
+    const SplatRecGeom g = splat_rec_geom(a.raster_rec, i);
     const int min_x = (int)(info.x & 0xFFFFu), min_y = (int)(info.x >> 16), bw = (int)info.y;
     uint32_t hits = 0;
     for (uint32_t b0 = begin; b0 < end; b0 += 64) {
@@ -282,7 +282,7 @@ __global__ void __launch_bounds__(256) big_count_kernel(b2c_project_args a) {
       if (b < end) {
         const int tx = min_x + (int)(b % (uint32_t)bw), ty = min_y + (int)(b / (uint32_t)bw);
         const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
-        h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, p0.x, p0.y, conic, p1.w);
+        h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, g.mx, g.my, g.conic, g.power);
       }
       hits += popc64(ballot64(h));
     }
@@ -349,7 +349,7 @@ void launch_project(const b2c_project_args& a, dim3 grid, dim3 block, bool half,
 extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
-  if (!a->big_count || !a->big_list || !a->hit_wide) return (int)hipErrorInvalidValue;
+  if (!a->big_count || !a->big_list || !a->hit_wide || !a->raster_rec || !a->depth_bits) return (int)hipErrorInvalidValue;
   if (a->feat_mode < 0 || a->feat_mode > 2 || (a->feat_mode == 2 && !a->feat_buffer)) return (int)hipErrorInvalidValue;
   clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);  // one launch for both
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);

@@ -47,11 +47,12 @@ typedef struct b2c_project_args {
   b2c_sh_view sh;
   b2c_camera_gpu cam;
   int tiles_x, tiles_y;
-  float* proj0;        /* [n] float4 (x, y, c00, c01) */
+  float* proj0;        /* [n] float4 (x, y, c00, c01); proj0..3 may all be NULL (not written) */
   float* proj1;        /* [n] float4 (c11, opacity, depth, power) */
   float* proj2;        /* [n] float4 (r, g, b, feat.x) */
   float* proj3;        /* [n] float2 (feat.y, feat.z) */
   uint32_t* tile_count;/* [n] */
+  uint32_t* depth_bits;/* [n]: the bits of each projected splat's camera depth (proj1.z), for the depth keys */
   uint32_t* hit_info;  /* [n] uint2 (hit mask or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24) */
   uint32_t* hit_wide;  /* [n] uint2, written where hit_info's mask word is 0xFFFFFFFF: the 64-bit hit mask
                           (low word first, bits in row-major bbox order) of a bbox of at most 64 tiles, or
@@ -99,8 +100,9 @@ int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* vals_in, con
                            uint32_t* vals_alt, uint32_t* vals2_alt, uint32_t n, const uint32_t* n_dev, int begin_bit,
                            int end_bit, void* temp, size_t temp_bytes, hipStream_t stream);
 
-/* depth_keys_kernel (binning.cu:10-15): key = bits of view z if tile_count > 0 else 0xFFFFFFFF, val = index. */
-int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const float* proj1, uint32_t* keys, uint32_t* vals,
+/* depth_keys_kernel (binning.cu:10-15): key = bits of view z if tile_count > 0 else 0xFFFFFFFF, val = index;
+ * the depth bits come from b2c_hip_project's depth_bits (keys may be that array: the update is in place). */
+int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const uint32_t* depth_bits, uint32_t* keys, uint32_t* vals,
                        hipStream_t stream);
 
 /* Scratch bytes of b2c_hip_scan_counts for n splats. */
@@ -122,7 +124,7 @@ typedef struct b2c_emit_args {
   int n;
   const uint32_t* order, *tile_count, *tile_off, *hit_info;
   const uint32_t* hit_wide;             /* from b2c_hip_project */
-  const float* proj0, *proj1;
+  const float* raster_rec;              /* [n][16] from b2c_hip_project: the big splats' centre, conic, power */
   int tiles_x, tiles_y;
   uint32_t cap;
   uint32_t* keys, *vals;

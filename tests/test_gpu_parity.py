@@ -112,3 +112,23 @@ def test_config3_full_size():
     # before the host had the count ran short, and were redone after growing the buffers
     assert out["M"] > 1 << 22
     assert np.isfinite(out["grads"]).all()
+
+
+def test_train_step_reads_only_the_raster_record():
+    """The fused training step does not write proj0..3 (the binning, raster and replay kernels read the
+    64-byte raster record): with proj0..3 poisoned it builds the same lists as render_forward, which writes
+    them, and leaves the poison in place."""
+    sc = S.config3(n=20_000)
+    emit("train step without proj0..3")
+    r = _native.Renderer(sc)
+    try:
+        r.forward()
+        want = {k: r.read(k) for k in ("keys_sorted", "vals_sorted", "tile_ranges", "tile_count")}
+        for k, w in (("proj0", 4), ("proj1", 4), ("proj2", 4), ("proj3", 2)):
+            r.write(k, np.full((sc.n, w), np.nan, np.float32))
+        r.step(bg=sc.bg)
+        for k, w in want.items():
+            assert np.array_equal(r.read(k), w), k
+        assert np.isnan(r.read("proj0")).all() and np.isnan(r.read("proj3")).all()
+    finally:
+        r.close()
