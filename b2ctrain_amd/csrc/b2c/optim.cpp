@@ -45,6 +45,8 @@ void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t
     b2c_adam_step_constants(&s);
   }
   LAUNCH_CHECK(b2c_hip_vjp(&a, stream));
+  // every row a backward wrote came with its splat's vis_flag, and the VJP cleared those rows
+  ctx.v_splat_zero = true;
 }
 
 }  // namespace b2c

@@ -76,7 +76,12 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   big_list.reserve(nn); big_base.reserve(nn); big_info.reserve(nn); big_chunk.reserve(nn * B2C_BIG_CHUNKS);
   big_items.reserve(nn * B2C_BIG_CHUNKS);
   counters.reserve(4);
-  if (v_splat.count < nn * GRAD_LANES) { v_splat.reserve(nn * GRAD_LANES); v_splat.zero(stream); }
+  if (v_splat.count < nn * GRAD_LANES) {
+    v_splat.reserve(nn * GRAD_LANES);
+    v_splat.zero(stream);
+    v_splat_zero = true;
+    v_splat_foreign = false;
+  }
   if (vis_flag.count < nn) { vis_flag.reserve(nn); vis_flag.zero(stream); }
   tile_ranges.reserve((size_t)n_tiles); tile_end.reserve((size_t)n_tiles + 1);
   const size_t npx = (size_t)W * H;
@@ -293,6 +298,7 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.inv_gscale = 1.f / grad_scale;
   a.mode = mode;
   a.v_splat = ctx.v_splat;
+  a.v_splat_zero = ctx.v_splat_known_zero() ? 1 : 0;
   a.vis_flag = ctx.vis_flag;
   a.vis_weight = m.vis_weight.ptr;
   a.num_isect = ctx.num_isect;
@@ -312,6 +318,7 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.hollow_margin = p.hollow_margin;
   a.hollow_lam = p.hollow_lam * grad_scale;
   LAUNCH_CHECK(b2c_hip_raster_bwd(&a, stream));
+  ctx.v_splat_zero = false;
 }
 
 }  // namespace

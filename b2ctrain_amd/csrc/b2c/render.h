@@ -88,6 +88,15 @@ struct RenderCtx {
   DevBuf<uint32_t> last_idx;  // one past the last contributing intersection per pixel
   // backward
   DevBuf<float> v_splat;      // [n][13]: xy(2) conic(3) rgb(3) opac(1) refine(1) feat(3)
+  // The MFMA backward stores its sums without reading v_splat when v_splat is known to be all zero:
+  // v_splat_zero is set where v_splat is cleared (allocation, a caller's zero, and the projection VJP,
+  // which clears every row whose vis_flag the backward set) and cleared by a backward. A caller's write of
+  // v_splat or vis_flag may leave rows the VJP does not clear (v_splat_foreign, until the caller zeroes
+  // v_splat); a caller holding the device pointer may write at any time (v_splat_shared, for good).
+  bool v_splat_zero = true;
+  bool v_splat_foreign = false;
+  bool v_splat_shared = false;
+  bool v_splat_known_zero() const { return v_splat_zero && !v_splat_foreign && !v_splat_shared; }
   DevBuf<uint32_t> vis_flag;  // [n]
   DevBuf<float4> v_out;       // dL/d(rgba) per pixel
   DevBuf<float4> v_feat;

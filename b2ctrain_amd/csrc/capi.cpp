@@ -311,6 +311,8 @@ int b2c_ctx_device_ptr(b2c_ctx* c, const char* field, void** ptr, size_t* bytes)
     const Field f = ctx_field(c, field);
     *ptr = f.ptr;
     if (bytes) *bytes = f.bytes;
+    const std::string name(field);
+    if (name == "v_splat" || name == "vis_flag") c->ctx.v_splat_shared = true;  // it may be written outside
   });
 }
 
@@ -329,6 +331,11 @@ int b2c_ctx_write(b2c_ctx* c, const char* field, const void* host, size_t bytes)
     if (bytes > f.bytes) throw std::runtime_error(std::string("ctx_write: too many bytes for ") + field);
     HIP_CHECK(hipStreamSynchronize(c->stream));
     if (bytes) HIP_CHECK(hipMemcpy(f.ptr, host, bytes, hipMemcpyHostToDevice));
+    const std::string name(field);
+    if (name == "v_splat" || name == "vis_flag") {
+      c->ctx.v_splat_zero = false;
+      c->ctx.v_splat_foreign = true;
+    }
   });
 }
 
@@ -337,6 +344,10 @@ int b2c_ctx_zero(b2c_ctx* c, const char* field) {
     Field f = ctx_field(c, field);
     if (f.bytes % 4) throw std::runtime_error("ctx_zero: field size not a multiple of 4");
     if (f.bytes) LAUNCH_CHECK(b2c_hip_fill_u32(static_cast<uint32_t*>(f.ptr), 0u, f.bytes / 4, c->stream));
+    if (std::string(field) == "v_splat") {
+      c->ctx.v_splat_zero = true;
+      c->ctx.v_splat_foreign = false;
+    }
   });
 }
 

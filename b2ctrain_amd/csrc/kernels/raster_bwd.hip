@@ -475,12 +475,13 @@ constexpr uint32_t RED_WIN = 64u * RED_SUB;  // rows per window (one wave)
 template <bool FEAT>
 __device__ __forceinline__ void prefetch_old(const b2c_raster_bwd_args& a, uint32_t id, float (&old)[RED_VALS<FEAT>]) {
   const float* dst = a.v_splat + (size_t)id * GRAD_LANES;
+  const bool zero = a.v_splat_zero != 0;  // uniform
 #pragma unroll
-  for (int k = 0; k < 10; k++) old[k] = dst[k];
+  for (int k = 0; k < 10; k++) old[k] = zero ? 0.f : dst[k];
   old[10] = a.vis_weight ? a.vis_weight[id] : 0.f;
   if constexpr (FEAT) {
 #pragma unroll
-    for (int k = 0; k < 3; k++) old[11 + k] = dst[10 + k];
+    for (int k = 0; k < 3; k++) old[11 + k] = zero ? 0.f : dst[10 + k];
   }
 }
 

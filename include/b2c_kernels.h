@@ -196,6 +196,9 @@ typedef struct b2c_raster_bwd_args {
   float inv_gscale;
   int mode;
   float* v_splat;             /* [n][13], accumulated */
+  int v_splat_zero;           /* mode 1: the caller knows v_splat is all zero on entry (the invariant of the
+                                 reference's training step, optim.cu:111-121): the sums are stored without
+                                 reading it */
   uint32_t* vis_flag;         /* [n] */
   float* vis_weight;          /* [n] or NULL */
   /* mode 1 only */

@@ -132,3 +132,37 @@ def test_train_step_reads_only_the_raster_record():
         assert np.isnan(r.read("proj0")).all() and np.isnan(r.read("proj3")).all()
     finally:
         r.close()
+
+
+def test_backward_adds_into_v_splat_unless_it_is_known_zero():
+    """Each backward adds its sums into v_splat, as the reference's atomicAdds do. The MFMA backward stores
+    without reading v_splat only where the context knows it is all zero (after a zero, or after the VJP that
+    consumed it and no write of the caller's since), so passes in a row, and passes after a caller's write,
+    still add."""
+    sc = S.config2(n=20_000)
+    emit("v_splat accumulation")
+    gs = 3.0 * sc.W * sc.H
+    r = _native.Renderer(sc)
+    try:
+        r.forward()
+        r.loss(grad_scale=gs)
+        r.zero("v_splat")
+        r.zero("vis_flag")
+        r.backward(mode=1, grad_scale=gs)
+        one = r.read("v_splat").copy()
+        assert (one != 0).any(axis=1).sum() > 1000
+        r.backward(mode=1, grad_scale=gs)
+        assert np.array_equal(r.read("v_splat"), one + one)
+        r.write("v_splat", np.ones_like(one))
+        r.backward(mode=1, grad_scale=gs)
+        assert np.array_equal(r.read("v_splat"), np.float32(1) + one)
+        r.vjp()  # clears the rows it consumed; the caller's ones on the other rows remain, and still count
+        left = r.read("v_splat").copy()
+        r.backward(mode=1, grad_scale=gs)
+        assert np.array_equal(r.read("v_splat"), left + one)
+        r.zero("v_splat")
+        r.vjp()
+        r.backward(mode=1, grad_scale=gs)
+        assert np.array_equal(r.read("v_splat"), one)
+    finally:
+        r.close()
