@@ -125,6 +125,15 @@ def f_sweep_of(r):
     return int(64 * (ranges[:, 1] - ranges[:, 0]).clip(min=0).sum())
 
 
+def cpu_baseline_frame(r, scene, mode, bg, cam):
+    """Both CPU baselines on one frame of the benchmark's own training step: (F_sweep, cpu_baselines(...))."""
+    r.step(mode=mode, bg=bg, cam=cam)
+    r.project(cam=cam, bg=bg)  # the step leaves proj0..3 unwritten; the CPU legs read them
+    r.sync()
+    f_sweep = f_sweep_of(r)
+    return f_sweep, cpu_baselines(r, scene, bg, f_sweep)
+
+
 def cpu_baselines(r, scene, bg, f_sweep):
     """Both CPU baselines on the frame the context last rendered (one view)."""
     from oracle import oracle as O
@@ -332,10 +341,8 @@ def main():
     }
     if not args.no_cpu_baseline:
         log("bench: CPU baselines (tiled port on all host threads; reference algorithm on a pixel sample)")
-        r.step(mode=args.mode, bg=bgs[-1], cam=views[0])
-        r.sync()
-        fs0 = f_sweep_of(r)
-        f_contrib, out["cpu_baseline"], out["cpu_reference_algorithm"] = cpu_baselines(r, scene, bgs[-1], fs0)
+        fs0, (f_contrib, out["cpu_baseline"], out["cpu_reference_algorithm"]) = cpu_baseline_frame(
+            r, scene, args.mode, bgs[-1], views[0])
         # composited fragments of that frame, counted by the CPU port over the GPU's own lists, and the rate
         # of composited fragments through the forward and backward (F_contrib / (t_fwd + t_bwd), one view)
         out["config"]["F_contrib_view0"] = f_contrib
