@@ -113,3 +113,31 @@ def test_tag_epochs_on_changing_lists(limit, monkeypatch):
     finally:
         v.close()
         r.close()
+
+
+def test_tag_epochs_across_row_layouts(monkeypatch):
+    """Backward passes with and without feature lanes (16- and 12-float rows) alternate on one context; each
+    layout change starts an epoch, and every pass gives the gradients of a fresh context."""
+    monkeypatch.setenv("B2C_ROW_GEN_LIMIT", "3")
+    sc = _occluded_scene()
+    gs = 3.0 * sc.W * sc.H
+    emit(f"row layouts, {sc.name}")
+
+    def run(r, feat):
+        r.set_features(mode=2 if feat else 0, buffer=np.tile([0.2, -0.4, 0.9], (sc.n, 1)) if feat else None)
+        return _view_grads(r, sc, sc.cam, gs)
+
+    fresh = {}
+    for feat in (False, True):
+        r = _native.Renderer(sc)
+        try:
+            fresh[feat] = run(r, feat)
+        finally:
+            r.close()
+    r = _native.Renderer(sc)
+    try:
+        for feat in (False, True, True, False, True, False, False):
+            for a, b in zip(run(r, feat), fresh[feat]):
+                assert np.array_equal(a, b), feat
+    finally:
+        r.close()
