@@ -241,51 +241,93 @@ __global__ void __launch_bounds__(256) fold_view_kernel(b2c_evidence_sum_args a)
 // alpha, the depth at which it first reaches tau (tau <= 0: the alpha-weighted mean depth, when the pixel is
 // more than 5% covered), the weight arriving from more than delta behind that first surface, and the weight
 // from more than margin behind the reference depth (if given). The transmittance stop ends a pixel as in the
-// forward.
+// forward, and the walk is the forward's: per 4x4 quadrant lists of each batch (a splat whose ellipse cannot
+// reach a quadrant composites nothing there), two list entries per step, no branch per fragment.
 __global__ void __launch_bounds__(64) probe_kernel(b2c_probe_args a) {
-  __shared__ float4 s_g0[64], s_g1[64];
+  // lanes by quadrant as in the forward: lane 16 q + p is pixel p (row-major 4x4) of quadrant q; slot 64
+  // is a null splat that pads the shorter quadrant lists
+  __shared__ float4 s_g0[65], s_g1[65];
+  __shared__ uint32_t s_list[4][66];  // per quadrant: LDS byte offsets of its splats, in depth order
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
   const uint2 range = reinterpret_cast<const uint2*>(a.tile_ranges)[tile];
   const int lane = threadIdx.x;
-  const int px = (tile % a.tiles_x) * RT_W + (lane & 7), py = (tile / a.tiles_x) * RT_W + (lane >> 3);
+  const int q = lane >> 4, p = lane & 15;
+  const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
+  const int px = tx * RT_W + (q & 1) * 4 + (p & 3), py = ty * RT_W + (q >> 1) * 4 + (p >> 2);
+  const float x0 = tx * RT_W + 0.5f, y0 = ty * RT_W + 0.5f;  // the tile's first pixel centre
   const bool inside = px < a.W && py < a.H;
   const float pcx = px + 0.5f, pcy = py + 0.5f;
   const bool mean_mode = a.tau <= 0.f;
   float T = 1.f, z_first = __builtin_inff(), deep = 0.f, behind = 0.f, zsum = 0.f;
   const float zr = (inside && a.ref_z) ? a.ref_z[py * a.W + px] : __builtin_inff();
   bool live = inside;
+  if (lane < 8) s_list[lane >> 1][64 + (lane & 1)] = 64u * 16u;  // read by the last pair's prefetch
+  if (lane == 0) {  // power = 0 and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1): fails the cutoff
+    s_g0[64] = make_float4(0.f, 0.f, 0.f, 0.f);
+    s_g1[64] = make_float4(1.f, 0.f, 0.f, 0.f);
+  }
+  const char* lds_g0 = reinterpret_cast<const char*>(s_g0);
+  const char* lds_g1 = reinterpret_cast<const char*>(s_g1);
   for (uint32_t start = range.x; start < range.y; start += 64) {
     if (ballot64(live) == 0ull) break;
-    const uint32_t count = min(64u, range.y - start);
+    const uint32_t remaining = min(64u, range.y - start);
     __syncthreads();
-    if ((uint32_t)lane < count) {
+    uint32_t qmask = 0;
+    if ((uint32_t)lane < remaining) {
       const uint32_t gid = a.vals_sorted[start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
-      const float4 r1 = rec[1], r2 = rec[2], r3 = rec[3];
-      s_g0[lane] = rec[0];
+      const float4 r0 = rec[0], r1 = rec[1], r2 = rec[2], r3 = rec[3];
+      s_g0[lane] = r0;
       s_g1[lane] = make_float4(r1.x, r2.w, r1.z, r3.w);  // (c11 / 2, log2 opacity, power, depth)
+      qmask = quadrant_mask(r0.x, r0.y, r0.z, r0.w, r1.x, r1.z, x0, y0);
     }
+    uint32_t n_iter = 0;
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) {
+      const bool mine = (qmask >> qq) & 1u;
+      const uint64_t bal = ballot64(mine);
+      const uint32_t c = popc64(bal);
+      if (mine) s_list[qq][popc64(bal & below)] = (uint32_t)lane * 16u;
+      if ((uint32_t)lane >= c) s_list[qq][lane] = 64u * 16u;
+      n_iter = max(n_iter, c);
+    }
+    n_iter = __builtin_amdgcn_readfirstlane(n_iter);
     __syncthreads();
-    for (uint32_t j = 0; j < count; j++) {
-      const float4 g0 = s_g0[j], g1 = s_g1[j];
-      const float sigma = frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, pcx, pcy).sigma;
-      if (!live || !(sigma >= 0.f && sigma <= g1.z)) continue;
-      const float alpha = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));
-      const float next_T = T * (1.f - alpha);
-      if (next_T <= T_CUTOFF) {
-        live = false;
-        continue;
-      }
-      const float vis = alpha * T;
-      const float z = g1.w;
-      if (__builtin_isfinite(z_first) && z > z_first + a.delta) deep += vis;
-      if (z > zr + a.margin) behind += vis;
-      if (mean_mode) zsum = fmaf(vis, z, zsum);
-      T = next_T;
-      if (!__builtin_isfinite(z_first) && 1.f - T >= a.tau) z_first = z;
+    const uint32_t* my_list = s_list[q];
+    uint32_t off0 = my_list[0], off1 = my_list[1];
+    // One step, straight-line as in the forward: an invalid fragment, a stopped lane or a null splat
+    // contributes alpha = 0 and leaves every sum unchanged. A composited fragment (valid and not stopping the
+    // lane) adds its weight to the depth sums and may set z_first.
+#define B2C_PROBE_STEP(off, next)                                                                       \
+  do {                                                                                                  \
+    const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + (off));                                 \
+    const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + (off));                                 \
+    const float sigma = frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, pcx, pcy).sigma;                        \
+    const bool valid = live & (__float_as_uint(sigma) <= __float_as_uint(g1.z));                        \
+    float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));                                         \
+    asm volatile("" : "+v"(a_cl));                                                                      \
+    const float alpha = valid ? a_cl : 0.f;                                                             \
+    const float next_T = T * (1.f - alpha);                                                             \
+    const bool stop = next_T <= T_CUTOFF;                                                               \
+    live = live & !stop;                                                                                \
+    const bool comp = valid & !stop;                                                                    \
+    const float vis = comp ? alpha * T : 0.f;                                                           \
+    const float z = g1.w;                                                                               \
+    deep += (__builtin_isfinite(z_first) & (z > z_first + a.delta)) ? vis : 0.f;                        \
+    behind += (z > zr + a.margin) ? vis : 0.f;                                                          \
+    zsum = comp ? fmaf(vis, z, zsum) : zsum;                                                            \
+    T = comp ? next_T : T;                                                                              \
+    z_first = (comp & !__builtin_isfinite(z_first) & (1.f - T >= a.tau)) ? z : z_first;                \
+    (off) = my_list[next];                                                                              \
+  } while (0)
+    for (uint32_t i = 0; i < n_iter; i += 2) {
+      B2C_PROBE_STEP(off0, i + 2);
+      B2C_PROBE_STEP(off1, i + 3);
     }
+#undef B2C_PROBE_STEP
   }
   if (mean_mode) z_first = (1.f - T) > 0.05f ? zsum / (1.f - T) : __builtin_inff();
   if (inside) reinterpret_cast<float4*>(a.out)[py * a.W + px] = make_float4(1.f - T, z_first, deep, behind);
