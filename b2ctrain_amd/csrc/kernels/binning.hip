@@ -142,7 +142,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     const uint32_t* __restrict__ digit_total) {
   constexpr uint32_t TILE = SORT_THREADS * KPT, CHUNK = 64 * KPT;
   __shared__ uint32_t s_key[TILE];
-  __shared__ uint32_t s_val[NV][TILE];
+  __shared__ uint32_t s_val[TILE];  // one value array staged at a time (with NV = 2 the second follows the first)
   __shared__ uint32_t s_gbase[RADIX];  // global position of the tile's first key of each digit
   __shared__ uint32_t s_loff[RADIX];   // local (staging) offset of each digit
   __shared__ uint32_t s_wcnt[NWAVES][RADIX];
@@ -202,14 +202,14 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     }
   }
   __syncthreads();
-  // 5. stage sorted by digit
+  // 5. stage sorted by digit: the keys and the first value array (the staging offsets go to rank[])
 #pragma unroll
   for (int r = 0; r < KPT; r++) {
     if (w * CHUNK + (uint32_t)r * 64 + lane < tile_n) {
       const uint32_t lp = wc[(key[r] >> shift) & dmask] + rank[r];
+      rank[r] = lp;
       s_key[lp] = key[r];
-#pragma unroll
-      for (int v = 0; v < NV; v++) s_val[v][lp] = val[v][r];
+      s_val[lp] = val[0][r];
     }
   }
   __syncthreads();
@@ -219,8 +219,18 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     const uint32_t d = (k >> shift) & dmask;
     const uint32_t g = s_gbase[d] + (j - s_loff[d]);
     keys_out[g] = k;
-    vals_out[g] = s_val[0][j];
-    if constexpr (NV > 1) vals2_out[g] = s_val[1][j];
+    vals_out[g] = s_val[j];
+  }
+  if constexpr (NV > 1) {  // 7. the second value array through the same staging buffer
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < KPT; r++)
+      if (w * CHUNK + (uint32_t)r * 64 + lane < tile_n) s_val[rank[r]] = val[1][r];
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < tile_n; j += SORT_THREADS) {
+      const uint32_t d = (s_key[j] >> shift) & dmask;
+      vals2_out[s_gbase[d] + (j - s_loff[d])] = s_val[j];
+    }
   }
 }
 
