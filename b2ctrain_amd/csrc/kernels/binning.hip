@@ -10,7 +10,7 @@
 //   for large sorts and 4 for small ones (enough workgroups to cover the chip).
 // * Count scan: reduce-then-scan of tile_count gathered in depth order, four contiguous entries a thread;
 //   each workgroup of the second pass sums its predecessors' totals itself (no middle kernel).
-// * Emit: small splats one thread each over the set bits of their hit mask; splats whose bbox exceeds 32
+// * Emit: small splats one thread each over the set bits of their hit mask; splats whose bbox exceeds 64
 //   tiles one wave per chunk of the bbox, in row-major order.
 #pragma clang fp contract(off)
 #include "b2c_kernels.h"

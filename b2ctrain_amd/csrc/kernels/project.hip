@@ -197,7 +197,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
   if (big) a.big_list[s_base + s_wcount[w] + mbcnt64(bm)] = (uint32_t)i;
 }
 
-// Big splats (bbox over 32 tiles) are counted in parallel chunks of their row-major bbox order: an entry
+// Big splats (bbox over 64 tiles) are counted in parallel chunks of their row-major bbox order: an entry
 // of the big list with area A gets ceil(A / len) chunks of len tiles, len = 64 up to 64 * B2C_BIG_CHUNKS
 // tiles and longer (a multiple of 64) beyond, so no splat has more than B2C_BIG_CHUNKS chunks. Each chunk
 // is one work item of a flat item list (filled in any order: items are independent), processed by one
