@@ -107,12 +107,21 @@ uint32_t RenderCtx::next_row_tag(int row_floats, hipStream_t stream) {
   const uint32_t key = (uint32_t)row_floats | ((uint32_t)tile_bits << 8);
   if (row_epoch_buf != isect_rows.ptr || key != row_epoch_key || row_gen >= limit) {
     isect_rows.zero(stream);
+    row_live.zero(stream);
     row_gen = 0;
     row_epoch_key = key;
     row_epoch_buf = isect_rows.ptr;
   }
   row_gen++;
   return row_gen << tile_bits;
+}
+
+bool RenderCtx::use_row_live() const {
+  if (const char* env = getenv("B2C_ROW_LIVE")) {
+    if (env[0] == '0') return false;
+    if (env[0] == '1') return true;
+  }
+  return (size_t)num_isect > (size_t)4 * (size_t)W * (size_t)H;
 }
 
 void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
@@ -125,6 +134,7 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
   isect_alt_v2.reserve(ncap, false, stream);
   // rows: 3 float4 (4 with feature lanes); window partials: 2 x 3 float4 (2 x 4)
   slot_sorted.reserve(ncap, false, stream); isect_rows.reserve(ncap * 4, false, stream);
+  row_live.reserve(ncap, false, stream);
   isect_part.reserve((ncap / 256 + 1) * 8, false, stream); isect_part_flags.reserve(ncap / 256 + 1, false, stream);
   isect_cap = ncap;
   sort_tmp.reserve(b2c_radix_sort_temp_bytes((uint32_t)ncap));
@@ -307,7 +317,10 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.tile_count = ctx.tile_count;
   a.isect_rows = reinterpret_cast<float*>(ctx.isect_rows.ptr);
   a.tile_mask = (1u << ctx.tile_bits) - 1u;
-  if (mode == 1 && ctx.num_isect) a.row_tag = ctx.next_row_tag(p.feat != FeatureMode::None ? 16 : 12, stream);
+  if (mode == 1 && ctx.num_isect) {
+    a.row_tag = ctx.next_row_tag(p.feat != FeatureMode::None ? 16 : 12, stream);
+    if (ctx.use_row_live()) a.row_live = ctx.row_live;
+  }
   a.isect_part = reinterpret_cast<float*>(ctx.isect_part.ptr);
   a.isect_part_flags = ctx.isect_part_flags;
   a.split_event = ctx.bwd_split_event;

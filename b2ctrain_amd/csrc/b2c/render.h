@@ -109,9 +109,11 @@ struct RenderCtx {
   // Intersection bookkeeping of the atomic-free backward: slot_sorted[i] = emit position of list entry i
   // (the tile sort sorts positions; a splat's emit positions are contiguous), tile_end[t] = the tile's
   // list end before the forward shrinks it, isect_rows[slot] = that (tile, splat)'s 12-float gradient row
-  // (or the evidence pass's 4-float row), written only for the entries of the shrunk ranges.
+  // (or the evidence pass's 4-float row), written only for the entries of the shrunk ranges; row_live[slot]
+  // = the tag word of a row the backward wrote, when it runs with the live-row index (sparse lists).
   DevBuf<uint32_t> slot_sorted, tile_end;
   DevBuf<float4> isect_rows;
+  DevBuf<uint32_t> row_live;
   DevBuf<float4> isect_part;          // per 256-row window: partial sums of runs crossing the window's edges
   DevBuf<uint32_t> isect_part_flags;  // per 256-row window
   DevBuf<unsigned char> sort_tmp;
@@ -131,8 +133,13 @@ struct RenderCtx {
   // shrunk end are neither written nor cleared. A tag is never handed out twice while rows written under
   // it can remain: the buffer is cleared (fill kernel) when it was reallocated, when the row layout
   // (floats per row) or tile_bits changed, and when the generation field is used up; the generation then
-  // restarts at 1.
+  // restarts at 1. row_live holds the same tags and is cleared with the rows.
   uint32_t next_row_tag(int row_floats, hipStream_t stream);
+  // Whether the MFMA backward's reduce reads rows through row_live: when the lists are long against the
+  // image (more than 4 intersections per pixel) most pairs lie past their tile's shrunk end, and reading
+  // a 4-byte tag per row instead of the 48-byte row saves most of the reduce's traffic. B2C_ROW_LIVE = 0
+  // or 1 forces the choice.
+  bool use_row_live() const;
   uint32_t row_gen = 0;                 // last generation of the current epoch
   uint32_t row_epoch_key = 0;           // row floats | tile_bits << 8 of the current epoch
   const void* row_epoch_buf = nullptr;  // isect_rows.ptr the epoch's clear covered

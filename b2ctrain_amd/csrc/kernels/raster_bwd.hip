@@ -434,7 +434,10 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
           float4* row = reinterpret_cast<float4*>(a.isect_rows) + (size_t)s_slot[gbase + j] * (ROW / 4);
           if (nl >= G && kg == 2) row[0] = make_float4(dv[0], dv[1], dv[2], dv[3]);
           if (nl < G && kg == 1) row[1] = make_float4(sv, svu, dv[2], d1[2]);
-          if (nl < G && kg == 0) row[2] = make_float4(dv[0], dv[1], dv[2], __uint_as_float(a.row_tag | (uint32_t)tile));
+          if (nl < G && kg == 0) {
+            row[2] = make_float4(dv[0], dv[1], dv[2], __uint_as_float(a.row_tag | (uint32_t)tile));
+            if (a.row_live) a.row_live[s_slot[gbase + j]] = a.row_tag | (uint32_t)tile;
+          }
           if constexpr (FEAT)
             if (nl < G && kg == 1) row[3] = make_float4(fx, dv[0], dv[1], 0.f);
         }
@@ -593,8 +596,18 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
     const uint32_t id = valid ? ids[s] : NO_RUN;
     const uint32_t next_id = lo + 64u < m ? ids[lo + 64u] : NO_RUN;
     float v[RED_VALS];
-    // a row without this pass's tag (a pair past its tile's shrunk end, or a sentinel) counts as zero
-    const bool live = row_gradients<FEAT>(a, valid ? s : 0u, valid ? id : 0u, v) && valid;
+    // a row without this pass's tag (a pair past its tile's shrunk end, or a sentinel) counts as zero; with
+    // the live-row index only the rows it marks are read
+    bool live;
+    if (a.row_live) {
+#pragma unroll
+      for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
+      const uint32_t word = valid ? a.row_live[s] : 0u;
+      live = valid && (word & ~a.tile_mask) == a.row_tag;
+      if (live) live = row_gradients<FEAT>(a, s, id, v);
+    } else {
+      live = row_gradients<FEAT>(a, valid ? s : 0u, valid ? id : 0u, v) && valid;
+    }
 #pragma unroll
     for (int k = 0; k < RED_VALS; k++) v[k] = live ? v[k] : 0.f;
     const uint32_t prev = dpp_u32<0x138, 0xF>(id, prev_id);  // wave_shr:1; lane 0 gets the row before
@@ -619,10 +632,14 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
     const bool is_last = lane == 63;
     const bool crosses_window = cont_after && sub == RED_SUB - 1;
     const bool complete = tail && !(is_first && first_from_before);
+    // a sub-window without a row of this pass scans to zeros: skip the scan (wave-uniform); a run ending in
+    // it then has sums only if it carries some from the previous sub-window
+    const bool any_live = ballot64(live) != 0ull;
+    const bool carried = cont_before && sub > 0 && in_first;
     float old[RED_VALS];
-    if (complete) prefetch_old<FEAT>(a, id, old);
-    seg_scan(valid ? id : NO_RUN, v);
-    if (cont_before && sub > 0 && in_first) {  // the run carried from the previous sub-window
+    if (complete && (any_live || (carried && carry[10] > 0.f))) prefetch_old<FEAT>(a, id, old);
+    if (any_live) seg_scan(valid ? id : NO_RUN, v);
+    if (carried) {  // the run carried from the previous sub-window
 #pragma unroll
       for (int k = 0; k < RED_VALS; k++) v[k] += carry[k];
     }

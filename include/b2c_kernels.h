@@ -209,6 +209,10 @@ typedef struct b2c_raster_bwd_args {
   float* isect_rows;          /* [M][16] scratch (12 floats a row are used without feat) */
   uint32_t row_tag;           /* this pass's tag bits (none inside tile_mask, not 0) */
   uint32_t tile_mask;         /* tag bits that hold the tile id: 2^tile_bits - 1, tile ids < 2^tile_bits */
+  uint32_t* row_live;         /* [M] or NULL: when given, each written row's tag word is also stored here at
+                                 the row's emit position, and the reduce reads only the rows whose word here
+                                 is this pass's tag (lists shrunk to a small share of their pairs leave most
+                                 rows unread). Same tag contract as isect_rows (cleared with it). */
   float* isect_part;          /* [ceil(M / 256)][32] scratch: partial sums of runs crossing 256-row windows */
   uint32_t* isect_part_flags; /* [ceil(M / 256)] scratch */
   void* split_event;          /* optional hipEvent_t recorded between the raster kernel and the reduce */

@@ -4,6 +4,10 @@ the tile id for the backward's rows); the reductions take a row as the pass's ow
 so rows past a shrunk end are neither written nor cleared. The context clears the buffer before a tag could
 repeat (at reallocation, when the row layout or the tile bits change, and when the generations run out).
 
+The MFMA backward's reduce either reads every row's tag from the row itself or, with the live-row index
+(B2C_ROW_LIVE = 1, the context's choice for long lists), reads a 4-byte tag per row from row_live and only the
+rows it marks; the backward tests run both ways, and the two give the same gradients bit for bit.
+
 Checked here: poisoning the whole row buffer with NaN before a pass leaves v_splat and vis_weight bit-identical
 and the evidence finite and equal to rounding (its sums use float atomics), so no row past a shrunk end is
 read and every row inside one is written; and passes over changing lists on one context, with the generations
@@ -17,6 +21,8 @@ from b2ctrain_amd import scenes as S
 from tests.gpu_harness import emit
 
 pytestmark = pytest.mark.gpu
+
+live_index = pytest.mark.parametrize("row_live", ["0", "1"], ids=["rows", "live-index"])
 
 
 def _occluded_scene():
@@ -51,8 +57,10 @@ def test_occluded_lists_are_mostly_past_the_shrunk_end():
         r.close()
 
 
+@live_index
 @pytest.mark.parametrize("make", [_occluded_scene, lambda: S.config2(n=20_000)], ids=["occluded", "config2"])
-def test_backward_reads_no_row_past_the_shrunk_end(make):
+def test_backward_reads_no_row_past_the_shrunk_end(make, row_live, monkeypatch):
+    monkeypatch.setenv("B2C_ROW_LIVE", row_live)
     sc = make()
     emit(f"poisoned rows, backward {sc.name}")
     r = _native.Renderer(sc)
@@ -85,11 +93,31 @@ def test_evidence_reads_no_row_past_the_shrunk_end():
         r.close()
 
 
+@pytest.mark.parametrize("make", [_occluded_scene, lambda: S.config2(n=20_000)], ids=["occluded", "config2"])
+def test_live_row_index_gives_the_same_gradients(make, monkeypatch):
+    sc = make()
+    emit(f"live-row index against full row reads, {sc.name}")
+    gs = 3.0 * sc.W * sc.H
+    got = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("B2C_ROW_LIVE", mode)
+        r = _native.Renderer(sc)
+        try:
+            got[mode] = _view_grads(r, sc, sc.cam, gs, poison=True)
+        finally:
+            r.close()
+    for a, b in zip(got["0"], got["1"]):
+        assert np.array_equal(a, b)
+    assert (got["1"][2] != 0).sum() > 100
+
+
+@live_index
 @pytest.mark.parametrize("limit", ["1", "2"])
-def test_tag_epochs_on_changing_lists(limit, monkeypatch):
+def test_tag_epochs_on_changing_lists(limit, row_live, monkeypatch):
     """With one generation per epoch every pass must clear the buffer first: a pass over another view's
     lists would otherwise read the previous view's rows as its own (they carry the same tag)."""
     monkeypatch.setenv("B2C_ROW_GEN_LIMIT", limit)
+    monkeypatch.setenv("B2C_ROW_LIVE", row_live)
     sc = _occluded_scene()
     cams = sc.extra_cams[:3]
     gs = 3.0 * sc.W * sc.H
@@ -115,10 +143,12 @@ def test_tag_epochs_on_changing_lists(limit, monkeypatch):
         r.close()
 
 
-def test_tag_epochs_across_row_layouts(monkeypatch):
+@live_index
+def test_tag_epochs_across_row_layouts(row_live, monkeypatch):
     """Backward passes with and without feature lanes (16- and 12-float rows) alternate on one context; each
     layout change starts an epoch, and every pass gives the gradients of a fresh context."""
     monkeypatch.setenv("B2C_ROW_GEN_LIMIT", "3")
+    monkeypatch.setenv("B2C_ROW_LIVE", row_live)
     sc = _occluded_scene()
     gs = 3.0 * sc.W * sc.H
     emit(f"row layouts, {sc.name}")
