@@ -79,15 +79,16 @@ __device__ __forceinline__ uint32_t live_count(uint32_t cap, const uint32_t* n_d
   return n < cap ? n : cap;
 }
 
-// Per-tile digit histogram. Every thread loads its KPT keys first, then counts them with LDS atomics.
-template <int KPT>
+// Per-tile digit histogram (R = 256 or 512 digits). Every thread loads its KPT keys first, then counts them
+// with LDS atomics.
+template <int KPT, int R>
 __global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __restrict__ keys, uint32_t cap,
                                                               const uint32_t* __restrict__ n_dev, int shift, int bits,
                                                               uint32_t* __restrict__ block_hist, uint32_t nblocks) {
   constexpr uint32_t TILE = SORT_THREADS * KPT;
-  __shared__ uint32_t hist[RADIX];
+  __shared__ uint32_t hist[R];
   const uint32_t n = live_count(cap, n_dev);
-  hist[threadIdx.x] = 0;
+  for (int t = threadIdx.x; t < R; t += SORT_THREADS) hist[t] = 0;
   __syncthreads();
   const uint32_t base = blockIdx.x * TILE;
   if (base < n) {  // a tile past the live count (n_dev) reports zeros
@@ -105,7 +106,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __
     }
   }
   __syncthreads();
-  block_hist[(size_t)threadIdx.x * nblocks + blockIdx.x] = hist[threadIdx.x];
+  for (int t = threadIdx.x; t < R; t += SORT_THREADS) block_hist[(size_t)t * nblocks + blockIdx.x] = hist[t];
 }
 
 // One workgroup per digit: exclusive scan of the digit's per-tile counts (each thread a contiguous run of
@@ -133,8 +134,8 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scan_digits(uint32_t* __re
 // per-digit counts in LDS across rounds); per-wave offsets then give each key its position in an LDS
 // staging buffer sorted by digit, which is written out in order: each digit's keys of this tile form one
 // contiguous run in the output, so consecutive lanes write consecutive addresses. NV = 1 or 2 value arrays
-// ride along with the keys.
-template <int NV, int KPT>
+// ride along with the keys. R = 256 or 512 digits (8- or 9-bit passes); thread t owns digits t R/256 ...
+template <int NV, int KPT, int R>
 __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, const uint32_t* __restrict__ vals2_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out, uint32_t* __restrict__ vals2_out, uint32_t cap,
@@ -143,9 +144,10 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
   constexpr uint32_t TILE = SORT_THREADS * KPT, CHUNK = 64 * KPT;
   __shared__ uint32_t s_key[TILE];
   __shared__ uint32_t s_val[TILE];  // one value array staged at a time (with NV = 2 the second follows the first)
-  __shared__ uint32_t s_gbase[RADIX];  // global position of the tile's first key of each digit
-  __shared__ uint32_t s_loff[RADIX];   // local (staging) offset of each digit
-  __shared__ uint32_t s_wcnt[NWAVES][RADIX];
+  constexpr int DPT = R / SORT_THREADS;  // digits per thread
+  __shared__ uint32_t s_gbase[R];  // global position of the tile's first key of each digit
+  __shared__ uint32_t s_loff[R];   // local (staging) offset of each digit
+  __shared__ uint32_t s_wcnt[NWAVES][R];
   __shared__ uint32_t s_wsum[NWAVES];
   const uint32_t n = live_count(cap, n_dev);
   const uint32_t base = blockIdx.x * TILE;
@@ -163,17 +165,31 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     val[0][r] = valid ? (vals_in ? vals_in[base + li] : base + li) : 0u;  // no values: sort the positions
     if constexpr (NV > 1) val[1][r] = valid ? vals2_in[base + li] : 0u;
   }
-  {  // 2. thread t owns digit t: global base and local offset of the digit in this tile
-    const uint32_t t = threadIdx.x;
-    uint32_t tot;
-    const uint32_t digit_start = block_excl_scan(digit_total[t], s_wsum, tot);
-    const uint32_t mine = block_hist[(size_t)t * nblocks + blockIdx.x];
-    const uint32_t next = blockIdx.x + 1 < nblocks ? block_hist[(size_t)t * nblocks + blockIdx.x + 1] : digit_total[t];
-    const uint32_t loff = block_excl_scan(next - mine, s_wsum, tot);
-    s_gbase[t] = digit_start + mine;
-    s_loff[t] = loff;
+  {  // 2. thread t owns digits t DPT .. t DPT + DPT - 1: global base and local offset of each in this tile
+    uint32_t tot_d[DPT], mine[DPT], cnt[DPT], tot_sum = 0, cnt_sum = 0;
 #pragma unroll
-    for (int k = 0; k < NWAVES; k++) s_wcnt[k][t] = 0u;
+    for (int j = 0; j < DPT; j++) {
+      const uint32_t d = threadIdx.x * DPT + j;
+      tot_d[j] = digit_total[d];
+      mine[j] = block_hist[(size_t)d * nblocks + blockIdx.x];
+      const uint32_t next = blockIdx.x + 1 < nblocks ? block_hist[(size_t)d * nblocks + blockIdx.x + 1] : tot_d[j];
+      cnt[j] = next - mine[j];
+      tot_sum += tot_d[j];
+      cnt_sum += cnt[j];
+    }
+    uint32_t tot;
+    uint32_t digit_start = block_excl_scan(tot_sum, s_wsum, tot);
+    uint32_t loff = block_excl_scan(cnt_sum, s_wsum, tot);
+#pragma unroll
+    for (int j = 0; j < DPT; j++) {
+      const uint32_t d = threadIdx.x * DPT + j;
+      s_gbase[d] = digit_start + mine[j];
+      s_loff[d] = loff;
+      digit_start += tot_d[j];
+      loff += cnt[j];
+#pragma unroll
+      for (int k = 0; k < NWAVES; k++) s_wcnt[k][d] = 0u;
+    }
   }
   __syncthreads();
   // 3. rank within the wave: rank = keys of the same digit earlier in this wave's stretch. All lanes read
@@ -191,13 +207,15 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     rank[r] = before + lt;
   }
   __syncthreads();
-  {  // 4. thread t owns digit t: per-wave counts become staging offsets
-    const uint32_t t = threadIdx.x;
-    uint32_t run = s_loff[t];
+  // 4. per-wave counts become staging offsets
+#pragma unroll
+  for (int j = 0; j < DPT; j++) {
+    const uint32_t d = threadIdx.x * DPT + j;
+    uint32_t run = s_loff[d];
 #pragma unroll
     for (int k = 0; k < NWAVES; k++) {
-      const uint32_t c = s_wcnt[k][t];
-      s_wcnt[k][t] = run;
+      const uint32_t c = s_wcnt[k][d];
+      s_wcnt[k][d] = run;
       run += c;
     }
   }
@@ -493,19 +511,19 @@ inline uint32_t sort_blocks(uint32_t n, int kpt) {
 }
 inline uint32_t scan_blocks(uint32_t n) { return (n + SCAN_TILE - 1) / SCAN_TILE; }
 
-template <int KPT>
+template <int KPT, int R>
 void sort_pass(const uint32_t* src_k, const uint32_t* src_v, const uint32_t* src_v2, uint32_t* dk, uint32_t* dv,
                uint32_t* dv2, uint32_t n, const uint32_t* n_dev, int shift, int bits, uint32_t* block_hist,
                uint32_t* digit_total, hipStream_t stream) {
   const uint32_t nb = sort_blocks(n, KPT);
-  radix_upsweep<KPT><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, n, n_dev, shift, bits, block_hist, nb);
-  radix_scan_digits<<<dim3(RADIX), dim3(SORT_THREADS), 0, stream>>>(block_hist, nb, digit_total);
+  radix_upsweep<KPT, R><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, n, n_dev, shift, bits, block_hist, nb);
+  radix_scan_digits<<<dim3(R), dim3(SORT_THREADS), 0, stream>>>(block_hist, nb, digit_total);
   if (src_v2)
-    radix_scatter<2, KPT><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev,
-                                                                        shift, bits, block_hist, nb, digit_total);
+    radix_scatter<2, KPT, R><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev,
+                                                                           shift, bits, block_hist, nb, digit_total);
   else
-    radix_scatter<1, KPT><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, nullptr, dk, dv, nullptr, n, n_dev,
-                                                                        shift, bits, block_hist, nb, digit_total);
+    radix_scatter<1, KPT, R><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, nullptr, dk, dv, nullptr, n,
+                                                                           n_dev, shift, bits, block_hist, nb, digit_total);
 }
 
 }  // namespace
@@ -515,9 +533,11 @@ void sort_pass(const uint32_t* src_k, const uint32_t* src_v, const uint32_t* src
 using namespace b2c::dev;
 
 extern "C" size_t b2c_radix_sort_temp_bytes(uint32_t n) {
-  // sized for the smaller tiles, so the bound is monotone in n whichever tile size a sort of n picks
-  const size_t nb = sort_blocks(n > 0 ? n : 1, KPT_SMALL);
-  return (nb * RADIX + RADIX) * sizeof(uint32_t);
+  // the larger of the small-tile 8-bit and the large-tile 9-bit histograms, so the bound is monotone in n
+  // whichever tile size and digit width a sort of n picks
+  const size_t nb_small = sort_blocks(n > 0 ? n : 1, KPT_SMALL), nb_big = sort_blocks(n > 0 ? n : 1, KPT_BIG);
+  const size_t hist = nb_small * RADIX > nb_big * 2 * RADIX ? nb_small * RADIX : nb_big * 2 * RADIX;
+  return (hist + 2 * RADIX) * sizeof(uint32_t);
 }
 
 extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* vals_in, const uint32_t* vals2_in,
@@ -530,25 +550,39 @@ extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* v
   if (two && (!vals2_out || !vals2_alt)) return (int)hipErrorInvalidValue;
   const int kpt = sort_kpt(n);
   uint32_t* block_hist = static_cast<uint32_t*>(temp);
-  uint32_t* digit_total = block_hist + (size_t)sort_blocks(n, kpt) * RADIX;
-  const int passes = (end_bit - begin_bit + 7) / 8;
+  uint32_t* digit_total = block_hist + (size_t)sort_blocks(n, kpt) * (kpt == KPT_BIG ? 2 * RADIX : RADIX);
+  // 8-bit digits; a large sort whose key width is a few bits over a multiple of 8 (17-bit tile keys at 4K)
+  // widens the first passes to 9 bits instead of running a pass for the remainder
+  const int width = end_bit - begin_bit;
+  int passes = (width + 7) / 8, wide = 0;
+  if (kpt == KPT_BIG && (width + 8) / 9 < passes) {
+    passes = (width + 8) / 9;
+    wide = width - 8 * passes;  // passes of 9 bits, the rest 8 (fewer where the width runs out)
+  }
   const uint32_t* src_k = keys_in;
   const uint32_t* src_v = vals_in;
   const uint32_t* src_v2 = vals2_in;
+  int shift = begin_bit;
   for (int p = 0; p < passes; p++) {
-    const int shift = begin_bit + 8 * p;
-    const int bits = end_bit - shift < 8 ? end_bit - shift : 8;
+    const int want = p < wide ? 9 : 8;
+    const int bits = end_bit - shift < want ? end_bit - shift : want;
     // route the passes so that the last one lands in the output buffers
     const bool to_out = ((passes - 1 - p) % 2) == 0;
     uint32_t* dk = to_out ? keys_out : keys_alt;
     uint32_t* dv = to_out ? vals_out : vals_alt;
     uint32_t* dv2 = two ? (to_out ? vals2_out : vals2_alt) : nullptr;
-    if (kpt == KPT_BIG)
-      sort_pass<KPT_BIG>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total, stream);
+    if (kpt == KPT_BIG && bits > 8)
+      sort_pass<KPT_BIG, 2 * RADIX>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total,
+                                    stream);
+    else if (kpt == KPT_BIG)
+      sort_pass<KPT_BIG, RADIX>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total,
+                                stream);
     else
-      sort_pass<KPT_SMALL>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total, stream);
+      sort_pass<KPT_SMALL, RADIX>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total,
+                                  stream);
     int e = (int)hipGetLastError();
     if (e) return e;
+    shift += bits;
     src_k = dk;
     src_v = dv;
     src_v2 = dv2;

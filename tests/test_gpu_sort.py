@@ -65,6 +65,11 @@ CASES = [  # (n, key generator, begin, end)
     (5_000_003, "tile15", 0, 15),
     (9_700_000, "tile15", 0, 15),
     (200_000, "rand32", 8, 20),
+    # large sorts whose width is just over a multiple of 8 bits take 9-bit digits: one 9-bit pass for 9
+    # bits, 9 + 8 for 17 (4K tile keys), 9 + 9 + 8 for 26 (from bit 3)
+    (4_500_000, "tile17", 0, 17),
+    (4_194_304, "rand32", 0, 9),
+    (4_200_001, "rand32", 3, 29),
 ]
 
 
@@ -75,6 +80,8 @@ def _keys(kind, n, rng):
         return rng.integers(0, 37, n).astype(np.uint32) * np.uint32(0x01010101)
     if kind == "tile15":
         return rng.integers(0, 32400, n).astype(np.uint32)
+    if kind == "tile17":  # 3840x2160: 129,600 tiles, and the sentinel key
+        return rng.integers(0, 129_601, n).astype(np.uint32)
     if kind == "depth":  # view-z bits in [1, 10) and 40% culled splats at 0xFFFFFFFF
         z = rng.uniform(1.0, 10.0, n).astype(np.float32).view(np.uint32)
         return np.where(rng.random(n) < 0.4, np.uint32(0xFFFFFFFF), z).astype(np.uint32)
@@ -101,6 +108,20 @@ def test_radix_sort_two_values_positions(n):
     print(f"kv2 n={n}", flush=True)
     got = _sort(keys, None, vals2, 0, 15)
     exp = _expect(keys, None, vals2, 0, 15)
+    for g, e in zip(got, exp):
+        assert np.array_equal(g, e)
+
+
+def test_radix_sort_two_values_positions_17_bits():
+    """The 4K tile pass: 17-bit keys in a 9-bit and an 8-bit pass, positions and a second value array, a live
+    count below the capacity."""
+    n, live = 6_000_000, 5_100_007
+    rng = np.random.default_rng(17)
+    keys = _keys("tile17", n, rng)
+    vals2 = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    print(f"kv2 17 bits n={n} live={live}", flush=True)
+    got = _sort(keys, None, vals2, 0, 17, live=live)
+    exp = _expect(keys, None, vals2, 0, 17, live=live)
     for g, e in zip(got, exp):
         assert np.array_equal(g, e)
 
