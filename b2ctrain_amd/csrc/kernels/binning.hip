@@ -24,6 +24,8 @@ constexpr int SORT_THREADS = 256;
 constexpr int KPT_BIG = 16;  // keys per thread of a large sort (4096-key tiles)
 constexpr int KPT_SMALL = 8;  // below BIG_SORT_MIN keys (2048-key tiles)
 constexpr uint32_t BIG_SORT_MIN = 1u << 22;
+constexpr int KPT_HUGE = 32;  // from HUGE_SORT_MIN keys (8192-key tiles)
+constexpr uint32_t HUGE_SORT_MIN = 1u << 25;
 constexpr int RADIX = 256;
 constexpr int NWAVES = SORT_THREADS / 64;
 constexpr int SCAN_PER = 4;                         // count scan: contiguous entries per thread
@@ -504,7 +506,7 @@ __global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const ui
   }
 }
 
-inline int sort_kpt(uint32_t n) { return n >= BIG_SORT_MIN ? KPT_BIG : KPT_SMALL; }
+inline int sort_kpt(uint32_t n) { return n >= HUGE_SORT_MIN ? KPT_HUGE : n >= BIG_SORT_MIN ? KPT_BIG : KPT_SMALL; }
 inline uint32_t sort_blocks(uint32_t n, int kpt) {
   const uint32_t tile = (uint32_t)(SORT_THREADS * kpt);
   return (n + tile - 1) / tile;
@@ -550,12 +552,12 @@ extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* v
   if (two && (!vals2_out || !vals2_alt)) return (int)hipErrorInvalidValue;
   const int kpt = sort_kpt(n);
   uint32_t* block_hist = static_cast<uint32_t*>(temp);
-  uint32_t* digit_total = block_hist + (size_t)sort_blocks(n, kpt) * (kpt == KPT_BIG ? 2 * RADIX : RADIX);
+  uint32_t* digit_total = block_hist + (size_t)sort_blocks(n, kpt) * (kpt != KPT_SMALL ? 2 * RADIX : RADIX);
   // 8-bit digits; a large sort whose key width is a few bits over a multiple of 8 (17-bit tile keys at 4K)
   // widens the first passes to 9 bits instead of running a pass for the remainder
   const int width = end_bit - begin_bit;
   int passes = (width + 7) / 8, wide = 0;
-  if (kpt == KPT_BIG && (width + 8) / 9 < passes) {
+  if (kpt != KPT_SMALL && (width + 8) / 9 < passes) {
     passes = (width + 8) / 9;
     wide = width - 8 * passes;  // passes of 9 bits, the rest 8 (fewer where the width runs out)
   }
@@ -571,7 +573,13 @@ extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* v
     uint32_t* dk = to_out ? keys_out : keys_alt;
     uint32_t* dv = to_out ? vals_out : vals_alt;
     uint32_t* dv2 = two ? (to_out ? vals2_out : vals2_alt) : nullptr;
-    if (kpt == KPT_BIG && bits > 8)
+    if (kpt == KPT_HUGE && bits > 8)
+      sort_pass<KPT_HUGE, 2 * RADIX>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total,
+                                     stream);
+    else if (kpt == KPT_HUGE)
+      sort_pass<KPT_HUGE, RADIX>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total,
+                                 stream);
+    else if (kpt == KPT_BIG && bits > 8)
       sort_pass<KPT_BIG, 2 * RADIX>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev, shift, bits, block_hist, digit_total,
                                     stream);
     else if (kpt == KPT_BIG)

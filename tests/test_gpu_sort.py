@@ -112,10 +112,10 @@ def test_radix_sort_two_values_positions(n):
         assert np.array_equal(g, e)
 
 
-def test_radix_sort_two_values_positions_17_bits():
+@pytest.mark.parametrize("n,live", [(6_000_000, 5_100_007), (36_000_000, 34_000_001)])
+def test_radix_sort_two_values_positions_17_bits(n, live):
     """The 4K tile pass: 17-bit keys in a 9-bit and an 8-bit pass, positions and a second value array, a live
-    count below the capacity."""
-    n, live = 6_000_000, 5_100_007
+    count below the capacity (4096- and, from 2^25 keys, 8192-key tiles)."""
     rng = np.random.default_rng(17)
     keys = _keys("tile17", n, rng)
     vals2 = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
