@@ -567,7 +567,8 @@ __device__ __forceinline__ bool row_gradients(const b2c_raster_bwd_args& a, uint
   return (word & ~a.tile_mask) == a.row_tag;
 }
 
-template <bool FEAT>
+// LIVE: rows are read through the live-row index (a.row_live).
+template <bool FEAT, bool LIVE>
 __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a) {
   constexpr int RED_VALS = ::b2c::dev::RED_VALS<FEAT>;
   constexpr int PQ = PART_Q<FEAT>;
@@ -588,21 +589,41 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
   uint32_t prev_id = before;
   bool window_cont_before = false, window_has_head = false;
   float4* part = reinterpret_cast<float4*>(a.isect_part) + (size_t)w * (2 * PQ);
+  // with the live-row index, where most rows are not read, the next sub-window's splat ids and live-row
+  // words are loaded while this one is processed (without it, the row loads dominate and this measured
+  // slower)
+  uint32_t nxt_id = NO_RUN, nxt_word = 0u;
+  if (LIVE && wlo + lane < m) {
+    nxt_id = ids[wlo + lane];
+    nxt_word = a.row_live[wlo + lane];
+  }
   for (int sub = 0; sub < RED_SUB; sub++) {
     const uint32_t lo = wlo + 64u * (uint32_t)sub;
     if (lo >= m) break;
     const uint32_t s = lo + lane;
     const bool valid = s < m;
-    const uint32_t id = valid ? ids[s] : NO_RUN;
+    uint32_t id, word = 0u;
+    if constexpr (LIVE) {
+      id = nxt_id;  // valid ? ids[s] : NO_RUN
+      word = nxt_word;
+      const uint32_t s1 = s + 64u;
+      const bool more = sub + 1 < RED_SUB && s1 < m;
+      nxt_id = more ? ids[s1] : NO_RUN;
+      nxt_word = more ? a.row_live[s1] : 0u;
+    } else {
+      id = valid ? ids[s] : NO_RUN;
+    }
     const uint32_t next_id = lo + 64u < m ? ids[lo + 64u] : NO_RUN;
     float v[RED_VALS];
     // a row without this pass's tag (a pair past its tile's shrunk end, or a sentinel) counts as zero; with
     // the live-row index only the rows it marks are read
     bool live;
-    if (a.row_live) {
+    // the kernel without the index keeps the test as a runtime branch (never taken: the host passes no
+    // index to it); the compiler's schedule of that form measured 3 us faster at 6M rows than without it
+    if (LIVE || a.row_live) {
+      if (!LIVE) word = valid ? a.row_live[s] : 0u;
 #pragma unroll
       for (int k = 0; k < RED_VALS; k++) v[k] = 0.f;
-      const uint32_t word = valid ? a.row_live[s] : 0u;
       live = valid && (word & ~a.tile_mask) == a.row_tag;
       if (live) live = row_gradients<FEAT>(a, s, id, v);
     } else {
@@ -786,11 +807,15 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
     const uint32_t windows = (a->num_isect + RED_WIN - 1u) / RED_WIN;
     if (windows) {
       if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;
+      const dim3 rgrid((windows + 3u) / 4u), rblock(256);
+      const bool live = a->row_live != nullptr;
       if (feat) {
-        isect_reduce_kernel<true><<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
+        if (live) isect_reduce_kernel<true, true><<<rgrid, rblock, 0, stream>>>(*a);
+        else isect_reduce_kernel<true, false><<<rgrid, rblock, 0, stream>>>(*a);
         isect_fixup_kernel<true><<<dim3((windows + 63u) / 64u), dim3(64), 0, stream>>>(*a);
       } else {
-        isect_reduce_kernel<false><<<dim3((windows + 3u) / 4u), dim3(256), 0, stream>>>(*a);
+        if (live) isect_reduce_kernel<false, true><<<rgrid, rblock, 0, stream>>>(*a);
+        else isect_reduce_kernel<false, false><<<rgrid, rblock, 0, stream>>>(*a);
         isect_fixup_kernel<false><<<dim3((windows + 63u) / 64u), dim3(64), 0, stream>>>(*a);
       }
     }
