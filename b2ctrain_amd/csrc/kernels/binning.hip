@@ -465,6 +465,8 @@ __device__ __forceinline__ void clear_tiles(uint2* ranges, uint32_t* tile_end, u
   }
 }
 
+constexpr uint32_t RANGE_KEYS = 4;
+
 __global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const uint32_t* __restrict__ m_dev,
                                                           const uint32_t* __restrict__ keys,
                                                           const uint32_t* __restrict__ slot_sorted,
@@ -481,28 +483,44 @@ __global__ void __launch_bounds__(256) tile_ranges_kernel(uint32_t cap, const ui
     if (i == 0 && tile_end) tile_end[n_tiles] = 0u;
     return;
   }
-  if (i >= m) return;
-  if (slot_sorted) vals_sorted[i] = vals[slot_sorted[i]];
-  const uint32_t tile = keys[i];
-  const uint32_t prev = i == 0 ? 0xFFFFFFFFu : keys[i - 1];
-  if (i == 0 || tile != prev) {
-    // tiles after the previous run (or from 0) up to this run (or the end), which no key names
-    clear_tiles(ranges, tile_end, i == 0 ? 0u : min(prev + 1u, n_tiles), min(tile, n_tiles));
-    if (tile < n_tiles) ranges[tile].x = i;
-    if (i > 0 && prev < n_tiles) {
-      ranges[prev].y = i;
-      if (tile_end) tile_end[prev] = i;
-    }
-    // start of the run of sentinel keys (emit shortfall of big splats), which sorts last
-    if (tile_end && tile >= n_tiles && (i == 0 || prev < n_tiles)) tile_end[n_tiles] = i;
+  // RANGE_KEYS consecutive keys per thread (one 16-byte load where all are live), and the key before them
+  const uint32_t i0 = i * RANGE_KEYS;
+  if (i0 >= m) return;
+  uint32_t k[RANGE_KEYS];
+  if (i0 + RANGE_KEYS <= m) {
+    const uint4 q = reinterpret_cast<const uint4*>(keys)[i];
+    k[0] = q.x; k[1] = q.y; k[2] = q.z; k[3] = q.w;
+  } else {
+#pragma unroll
+    for (uint32_t j = 0; j < RANGE_KEYS; j++) k[j] = i0 + j < m ? keys[i0 + j] : 0u;
   }
-  if (i == m - 1 && tile < n_tiles) {
-    ranges[tile].y = m;
-    clear_tiles(ranges, tile_end, tile + 1u, n_tiles);
-    if (tile_end) {
-      tile_end[tile] = m;
-      tile_end[n_tiles] = m;  // no sentinel keys
+  uint32_t prev = i0 == 0 ? 0xFFFFFFFFu : keys[i0 - 1];
+#pragma unroll
+  for (uint32_t j = 0; j < RANGE_KEYS; j++) {
+    const uint32_t ii = i0 + j;
+    if (ii >= m) break;
+    if (slot_sorted) vals_sorted[ii] = vals[slot_sorted[ii]];
+    const uint32_t tile = k[j];
+    if (ii == 0 || tile != prev) {
+      // tiles after the previous run (or from 0) up to this run (or the end), which no key names
+      clear_tiles(ranges, tile_end, ii == 0 ? 0u : min(prev + 1u, n_tiles), min(tile, n_tiles));
+      if (tile < n_tiles) ranges[tile].x = ii;
+      if (ii > 0 && prev < n_tiles) {
+        ranges[prev].y = ii;
+        if (tile_end) tile_end[prev] = ii;
+      }
+      // start of the run of sentinel keys (emit shortfall of big splats), which sorts last
+      if (tile_end && tile >= n_tiles && (ii == 0 || prev < n_tiles)) tile_end[n_tiles] = ii;
     }
+    if (ii == m - 1 && tile < n_tiles) {
+      ranges[tile].y = m;
+      clear_tiles(ranges, tile_end, tile + 1u, n_tiles);
+      if (tile_end) {
+        tile_end[tile] = m;
+        tile_end[n_tiles] = m;  // no sentinel keys
+      }
+    }
+    prev = tile;
   }
 }
 
@@ -641,8 +659,9 @@ extern "C" int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint
                                    uint32_t n_tiles, uint32_t* ranges, uint32_t* tile_end, hipStream_t stream) {
   if (n_tiles == 0) return 0;
   if (slot_sorted && (!vals || !vals_sorted)) return (int)hipErrorInvalidValue;
+  if (reinterpret_cast<uintptr_t>(keys_sorted) % 16u) return (int)hipErrorInvalidValue;  // read 16 bytes at a time
   // at least enough threads to clear every tile when there are no keys
-  const uint32_t threads = max(m, min(n_tiles, 65536u));
+  const uint32_t threads = max((m + RANGE_KEYS - 1u) / RANGE_KEYS, min(n_tiles, 65536u));
   tile_ranges_kernel<<<dim3((threads + 255) / 256), dim3(256), 0, stream>>>(m, m_dev, keys_sorted, slot_sorted, vals,
                                                                             vals_sorted, n_tiles,
                                                                             reinterpret_cast<uint2*>(ranges), tile_end);

@@ -139,7 +139,8 @@ int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream);
  * tile_end[t] = last (may be NULL; a copy the forward does not shrink; n_tiles + 1 entries, the last = the
  * position where the sentinel keys of an emit shortfall start, m if there are none). When slot_sorted is set (the
  * permutation from an index sort of the emitted keys), also writes vals_sorted[i] = vals[slot_sorted[i]]:
- * the splat ids in list order, as the reference's key-value sort leaves them. */
+ * the splat ids in list order, as the reference's key-value sort leaves them. keys_sorted must be 16-byte
+ * aligned. */
 int b2c_hip_tile_ranges(uint32_t m, const uint32_t* m_dev, const uint32_t* keys_sorted, const uint32_t* slot_sorted,
                         const uint32_t* vals, uint32_t* vals_sorted, uint32_t n_tiles, uint32_t* ranges,
                         uint32_t* tile_end, hipStream_t stream);
