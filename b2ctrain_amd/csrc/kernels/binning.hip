@@ -81,12 +81,15 @@ __device__ __forceinline__ uint32_t live_count(uint32_t cap, const uint32_t* n_d
   return n < cap ? n : cap;
 }
 
-// Per-tile digit histogram (R = 256 or 512 digits). Every thread loads its KPT keys first, then counts them
-// with LDS atomics.
+// Per-tile digit histogram (R = 256 or 512 digits). Thread t loads the KPT consecutive keys [t KPT, t KPT +
+// KPT) of the tile (16-byte loads) and counts runs of one digit in registers, adding each run to the LDS
+// histogram with one atomic: tile keys in emit order come in runs (a splat's tiles along a bbox row), which
+// would otherwise serialise on the same LDS word.
 template <int KPT, int R>
 __global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __restrict__ keys, uint32_t cap,
                                                               const uint32_t* __restrict__ n_dev, int shift, int bits,
                                                               uint32_t* __restrict__ block_hist, uint32_t nblocks) {
+  static_assert(KPT % 4 == 0, "keys are loaded four at a time");
   constexpr uint32_t TILE = SORT_THREADS * KPT;
   __shared__ uint32_t hist[R];
   const uint32_t n = live_count(cap, n_dev);
@@ -95,17 +98,32 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __
   const uint32_t base = blockIdx.x * TILE;
   if (base < n) {  // a tile past the live count (n_dev) reports zeros
     const uint32_t dmask = (1u << bits) - 1u;
+    const uint32_t first = base + threadIdx.x * (uint32_t)KPT;
     uint32_t key[KPT];
+    if (first + KPT <= n) {
 #pragma unroll
-    for (int r = 0; r < KPT; r++) {
-      const uint32_t idx = base + (uint32_t)r * SORT_THREADS + threadIdx.x;
-      key[r] = idx < n ? keys[idx] : 0u;
-    }
+      for (int q = 0; q < KPT / 4; q++) {
+        const uint4 v = reinterpret_cast<const uint4*>(keys + first)[q];
+        key[4 * q] = v.x; key[4 * q + 1] = v.y; key[4 * q + 2] = v.z; key[4 * q + 3] = v.w;
+      }
+    } else {
 #pragma unroll
-    for (int r = 0; r < KPT; r++) {
-      const uint32_t idx = base + (uint32_t)r * SORT_THREADS + threadIdx.x;
-      if (idx < n) atomicAdd(&hist[(key[r] >> shift) & dmask], 1u);
+      for (int r = 0; r < KPT; r++) key[r] = first + r < n ? keys[first + r] : 0u;
     }
+    uint32_t run_d = (key[0] >> shift) & dmask, run_c = first < n ? 1u : 0u;
+#pragma unroll
+    for (int r = 1; r < KPT; r++) {
+      const uint32_t d = (key[r] >> shift) & dmask;
+      const uint32_t live = first + r < n ? 1u : 0u;
+      if (d == run_d) {
+        run_c += live;
+      } else {
+        if (run_c) atomicAdd(&hist[run_d], run_c);
+        run_d = d;
+        run_c = live;
+      }
+    }
+    if (run_c) atomicAdd(&hist[run_d], run_c);
   }
   __syncthreads();
   for (int t = threadIdx.x; t < R; t += SORT_THREADS) block_hist[(size_t)t * nblocks + blockIdx.x] = hist[t];
@@ -566,6 +584,9 @@ extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* v
                                       int begin_bit, int end_bit, void* temp, size_t temp_bytes, hipStream_t stream) {
   if (n == 0 || end_bit <= begin_bit) return 0;
   if (temp_bytes < b2c_radix_sort_temp_bytes(n) || begin_bit < 0 || end_bit > 32) return (int)hipErrorInvalidValue;
+  // the histogram pass reads the keys 16 bytes at a time
+  if ((reinterpret_cast<uintptr_t>(keys_in) | reinterpret_cast<uintptr_t>(keys_out) | reinterpret_cast<uintptr_t>(keys_alt)) % 16u)
+    return (int)hipErrorInvalidValue;
   const bool two = vals2_in != nullptr;
   if (two && (!vals2_out || !vals2_alt)) return (int)hipErrorInvalidValue;
   const int kpt = sort_kpt(n);

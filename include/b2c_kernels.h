@@ -88,7 +88,7 @@ size_t b2c_radix_sort_temp_bytes(uint32_t n);
  * buffers of n entries; the inputs are not modified. vals_in may be NULL: the values are then the input
  * positions 0 .. n-1 (vals_out receives the sorting permutation). n_dev (may be NULL) points at a device
  * copy of n: the launch covers n entries, the kernels read the live count from n_dev when it is set (n is
- * then the capacity). */
+ * then the capacity). The key buffers (keys_in, keys_out, keys_alt) must be 16-byte aligned. */
 int b2c_hip_radix_sort_pairs(const uint32_t* keys_in, const uint32_t* vals_in, uint32_t* keys_out, uint32_t* vals_out,
                              uint32_t* keys_alt, uint32_t* vals_alt, uint32_t n, const uint32_t* n_dev, int begin_bit,
                              int end_bit, void* temp, size_t temp_bytes, hipStream_t stream);
