@@ -225,10 +225,9 @@ void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
     return;
   }
   const int n = m.n;
-  // 1. depth sort of the splats (culled ones sort last), stable on the 32 z bits
-  LAUNCH_CHECK(b2c_hip_depth_keys(n, ctx.tile_count, ctx.depth_keys, ctx.depth_keys,
-                                  ctx.order_in, stream));
-  LAUNCH_CHECK(b2c_hip_radix_sort_pairs(ctx.depth_keys, ctx.order_in, ctx.depth_keys_sorted, ctx.order, ctx.depth_alt_k,
+  // 1. depth sort of the splats (culled ones sort last), stable on the 32 z bits: the projection wrote the
+  // keys (depth bits, or 0xFFFFFFFF without tiles), and the sort carries the splat indices itself
+  LAUNCH_CHECK(b2c_hip_radix_sort_pairs(ctx.depth_keys, nullptr, ctx.depth_keys_sorted, ctx.order, ctx.depth_alt_k,
                                         ctx.depth_alt_v, (uint32_t)n, nullptr, 0, 32, ctx.sort_tmp.ptr,
                                         ctx.sort_tmp.bytes(), stream));
   // 2. inclusive scan of the tile counts in depth order; the total comes back to the host (binning.cu:125-133)

@@ -50,6 +50,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
     const ScreenSplat pr = screen_splat(po, q, ls, a.cam);
     if (!pr.ok) {
       a.tile_count[i] = 0u;
+      a.depth_bits[i] = 0xFFFFFFFFu;  // no tiles: sorts last
     } else {
       const float power = det_logf(pr.opacity * 255.f);
       bb = tile_bbox(pr.px, pr.py, pr.ex, pr.ey, a.tiles_x, a.tiles_y);
@@ -174,7 +175,11 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
     const bool wide = big || area > 32u || lo == 0xFFFFFFFFu;
     reinterpret_cast<uint2*>(a.hit_info)[i] = make_uint2(wide ? 0xFFFFFFFFu : lo, info);
     if (wide) reinterpret_cast<uint2*>(a.hit_wide)[i] = make_uint2(lo, hi);
-    if (small) a.tile_count[i] = (uint32_t)(__popc(lo) + __popc(hi));
+    if (small) {
+      const uint32_t count = (uint32_t)(__popc(lo) + __popc(hi));
+      a.tile_count[i] = count;
+      if (count == 0u) a.depth_bits[i] = 0xFFFFFFFFu;  // no tiles: sorts last
+    }
   }
   // workgroup-aggregated append of big splats: one device-scope atomic per workgroup (contended atomics
   // on one address are serialised at the memory side and cost ~10 ns each)
@@ -303,6 +308,7 @@ __global__ void __launch_bounds__(256) big_sum_kernel(b2c_project_args a) {
       run += h;
     }
     a.tile_count[a.big_list[e]] = run;
+    if (run == 0u) a.depth_bits[a.big_list[e]] = 0xFFFFFFFFu;  // no tiles: sorts last
   }
 }
 

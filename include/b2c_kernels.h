@@ -52,7 +52,8 @@ typedef struct b2c_project_args {
   float* proj2;        /* [n] float4 (r, g, b, feat.x) */
   float* proj3;        /* [n] float2 (feat.y, feat.z) */
   uint32_t* tile_count;/* [n] */
-  uint32_t* depth_bits;/* [n]: the bits of each projected splat's camera depth (proj1.z), for the depth keys */
+  uint32_t* depth_bits;/* [n]: the depth sort key of each splat (b2c_hip_depth_keys' keys, formed here): the bits
+                          of its camera depth (proj1.z), or 0xFFFFFFFF for a splat without tiles */
   uint32_t* hit_info;  /* [n] uint2 (hit mask or 0xFFFFFFFF, min_x | min_y << 12 | bw << 24) */
   uint32_t* hit_wide;  /* [n] uint2, written where hit_info's mask word is 0xFFFFFFFF: the 64-bit hit mask
                           (low word first, bits in row-major bbox order) of a bbox of at most 64 tiles, or
