@@ -92,6 +92,7 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   loss_partials.reserve(b2c_loss_partials(W, H));
   aux_partials.reserve(b2c_aux_partials(W, H));
   h_count.reserve(4);
+  HIP_CHECK(hipHostGetDevicePointer(reinterpret_cast<void**>(&h_count_dev), h_count.ptr, 0));
   if (isect_cap == 0) ensure_isect_capacity((size_t)1 << 22, stream);
   const size_t need_tmp = std::max({b2c_radix_sort_temp_bytes((uint32_t)nn), b2c_radix_sort_temp_bytes((uint32_t)isect_cap),
                                     b2c_scan_temp_bytes((uint32_t)nn)});
@@ -231,19 +232,19 @@ void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
                                         ctx.depth_alt_v, (uint32_t)n, nullptr, 0, 32, ctx.sort_tmp.ptr,
                                         ctx.sort_tmp.bytes(), stream));
   // 2. inclusive scan of the tile counts in depth order; the total comes back to the host (binning.cu:125-133)
-  LAUNCH_CHECK(b2c_hip_scan_counts(n, ctx.order, ctx.tile_count, ctx.tile_off, ctx.counters.ptr + 1, ctx.sort_tmp.ptr,
-                                   ctx.sort_tmp.bytes(), stream));
   constexpr uint32_t NO_COUNT = 0xFFFFFFFFu;  // not a possible total (the emit capacity is far below it)
   volatile uint32_t* h_total = ctx.h_count.ptr;
-  *h_total = NO_COUNT;  // the previous copy into it completed in the previous call
-  HIP_CHECK(hipMemcpyAsync(ctx.h_count.ptr, ctx.counters.ptr + 1, sizeof(uint32_t), hipMemcpyDeviceToHost, stream));
+  *h_total = NO_COUNT;  // the previous store into it completed in the previous call
+  // the scan's last workgroup stores the total into the pinned word as well (no copy launch)
+  LAUNCH_CHECK(b2c_hip_scan_counts_host(n, ctx.order, ctx.tile_count, ctx.tile_off, ctx.counters.ptr + 1,
+                                        ctx.h_count_dev, ctx.sort_tmp.ptr, ctx.sort_tmp.bytes(), stream));
   HIP_CHECK(hipEventRecord(ctx.count_event, stream));
   // 3-4 are queued before the host has the total: they are sized for the current capacity and read the
   // live count on the device (the emit skips splats whose slots would not fit), so the GPU does not idle
   // while the count travels to the host. A total beyond the capacity grows the buffers and runs them again.
   emit_and_sort(ctx, m, stream);
   HIP_CHECK(hipEventSynchronize(ctx.count_event));
-  // the copy has completed; without the event's fence its value may reach host memory a little later
+  // the scan has completed; without the event's fence its value may reach host memory a little later
   for (int spin = 0; *h_total == NO_COUNT && spin < (1 << 20); spin++) {
   }
   if (*h_total == NO_COUNT) HIP_CHECK(hipStreamSynchronize(stream));  // full fence, then it must be there

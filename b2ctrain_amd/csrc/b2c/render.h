@@ -80,6 +80,7 @@ struct RenderCtx {
   size_t isect_cap = 0;
   uint32_t num_isect = 0;
   PinnedBuf<uint32_t> h_count;
+  uint32_t* h_count_dev = nullptr;  // h_count's device address (the count scan stores the total there)
   // per tile / per pixel
   DevBuf<uint2> tile_ranges;
   DevBuf<float4> out_rgba;  // final rgb (with bg) + alpha

@@ -313,7 +313,7 @@ __global__ void __launch_bounds__(SORT_THREADS) scan_down(int n, const uint32_t*
                                                           const uint32_t* __restrict__ tile_count,
                                                           const uint32_t* __restrict__ block_sums,
                                                           uint32_t* __restrict__ tile_off,
-                                                          uint32_t* __restrict__ total_dev) {
+                                                          uint32_t* __restrict__ total_dev, uint32_t* total_host) {
   __shared__ uint32_t s_wsum[NWAVES];
   const uint32_t first = blockIdx.x * (uint32_t)SCAN_TILE + threadIdx.x * SCAN_PER;
   uint32_t c[SCAN_PER];
@@ -332,7 +332,11 @@ __global__ void __launch_bounds__(SORT_THREADS) scan_down(int n, const uint32_t*
     run += c[k];
     if (first + k < (uint32_t)n) tile_off[first + k] = run;
   }
-  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *total_dev = offset + tot;
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) {
+    *total_dev = offset + tot;
+    // straight into the caller's pinned host word (a system-scope vector store), instead of a copy launch
+    if (total_host) __hip_atomic_store(total_host, offset + tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 // Position of the k-th set bit (k counted from 0) of m, by halving: five popcounts.
@@ -655,15 +659,25 @@ extern "C" int b2c_hip_depth_keys(int n, const uint32_t* tile_count, const uint3
 
 extern "C" size_t b2c_scan_temp_bytes(uint32_t n) { return ((size_t)scan_blocks(n > 0 ? n : 1) + 1) * sizeof(uint32_t); }
 
-extern "C" int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
-                                   uint32_t* total_dev, void* temp, size_t temp_bytes, hipStream_t stream) {
-  if (n <= 0) return b2c_hip_fill_u32(total_dev, 0u, 1, stream);
+extern "C" int b2c_hip_scan_counts_host(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
+                                        uint32_t* total_dev, uint32_t* total_host, void* temp, size_t temp_bytes,
+                                        hipStream_t stream) {
+  if (n <= 0) {
+    if (total_host) return (int)hipErrorInvalidValue;  // nothing would write it
+    return b2c_hip_fill_u32(total_dev, 0u, 1, stream);
+  }
   if (temp_bytes < b2c_scan_temp_bytes((uint32_t)n)) return (int)hipErrorInvalidValue;
   const uint32_t nb = scan_blocks((uint32_t)n);
   uint32_t* block_sums = static_cast<uint32_t*>(temp);
   scan_reduce<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums);
-  scan_down<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums, tile_off, total_dev);
+  scan_down<<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(n, order, tile_count, block_sums, tile_off, total_dev,
+                                                          total_host);
   return (int)hipGetLastError();
+}
+
+extern "C" int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
+                                   uint32_t* total_dev, void* temp, size_t temp_bytes, hipStream_t stream) {
+  return b2c_hip_scan_counts_host(n, order, tile_count, tile_off, total_dev, nullptr, temp, temp_bytes, stream);
 }
 
 extern "C" int b2c_hip_emit(const b2c_emit_args* a, hipStream_t stream) {

@@ -114,6 +114,14 @@ size_t b2c_scan_temp_bytes(uint32_t n);
 int b2c_hip_scan_counts(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
                         uint32_t* total_dev, void* temp, size_t temp_bytes, hipStream_t stream);
 
+/* The same scan, also storing the total into total_host: pinned host memory (hipHostMalloc) given by its
+ * device address (hipHostGetDevicePointer). The reference copies the total back with cudaMemcpy
+ * (binning.cu:125-126); this delivers it from the scan's last workgroup without a copy launch. The value is
+ * visible to the host once the scan has completed (an event recorded after it); n must be positive. */
+int b2c_hip_scan_counts_host(int n, const uint32_t* order, const uint32_t* tile_count, uint32_t* tile_off,
+                             uint32_t* total_dev, uint32_t* total_host, void* temp, size_t temp_bytes,
+                             hipStream_t stream);
+
 /* emit_kernel (binning.cu:25-93): intersections in depth order, key = tile id, val = splat index. Splats of
  * at most 64 bbox tiles (the hit mask of hit_info, or of hit_wide for 33 to 64 tiles and for a full
  * 32-tile mask) are dealt out over the lanes of a wave, each intersection the k-th set bit of its splat's
