@@ -116,7 +116,7 @@ EXPORTS = [
     # launcher layer
     "b2c_hip_project", "b2c_radix_sort_temp_bytes", "b2c_hip_radix_sort_pairs", "b2c_hip_radix_sort_kv2",
     "b2c_hip_depth_keys",
-    "b2c_scan_temp_bytes", "b2c_hip_scan_counts", "b2c_hip_emit", "b2c_hip_tile_ranges", "b2c_hip_raster_fwd",
+    "b2c_scan_temp_bytes", "b2c_hip_scan_counts", "b2c_hip_scan_counts_host", "b2c_hip_emit", "b2c_hip_tile_ranges", "b2c_hip_raster_fwd",
     "b2c_hip_raster_bwd", "b2c_hip_photometric", "b2c_loss_partials", "b2c_hip_accumulate_loss", "b2c_hip_vjp",
     "b2c_hip_fill_u32", "b2c_hip_model_scatter", "b2c_hip_model_gather", "b2c_hip_planar_regrow",
     "b2c_hip_model_set_floor", "b2c_hip_photometric_noalloc", "b2c_aux_partials", "b2c_hip_normal_loss",
