@@ -78,9 +78,11 @@ struct PlyLayout {
 
 PlyLayout layout_of(const PlyHeader& h) {
   PlyLayout L;
+  // read_ply looks a group's other members up row by row (ply.cpp:150-166): a missing one is an error only
+  // for a file that has rows.
   const auto need = [&](const std::string& name) {
     const int c = h.find(name.c_str());
-    if (c < 0) ply_error("ply: missing property '%s'", name.c_str());
+    if (c < 0 && h.vertices > 0) ply_error("ply: missing property '%s'", name.c_str());
     return c;
   };
   const auto group = [&](int* out, const char* const* names, int count) {  // all or none
@@ -116,7 +118,8 @@ PlyLayout layout_of(const PlyHeader& h) {
     const int t = h.props[L.colour[0]].type;
     L.rgb_scale = t == B2C_PLY_U8 ? 1.0 / 255.0 : t == B2C_PLY_U16 ? 1.0 / 65535.0 : 1.0;
   }
-  if (L.rgb && (L.colour[1] < 0 || L.colour[2] < 0)) ply_error("ply: colour properties need all three channels");
+  if (L.rgb && (L.colour[1] < 0 || L.colour[2] < 0) && h.vertices > 0)
+    ply_error("ply: colour properties need all three channels");
   for (int j = 0; j < 3 * (K - 1); j++) L.rest.push_back(need(field("f_rest_", j)));
   L.has_evidence = group(L.evidence, EVIDENCE_FIELDS, 7);
   L.label = h.find("seg_label");
@@ -226,8 +229,10 @@ constexpr size_t DEC_ROWS_ALIGN = 64;             // chunks of whole decode work
 
 }  // namespace
 
+// A repeated property name resolves to its last occurrence, as read_ply's name -> column map does
+// (ply.cpp:96-97).
 int PlyHeader::find(const char* name) const {
-  for (size_t k = 0; k < props.size(); k++)
+  for (size_t k = props.size(); k-- > 0;)
     if (props[k].name == name) return (int)k;
   return -1;
 }

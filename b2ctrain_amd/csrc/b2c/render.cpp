@@ -139,6 +139,9 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
   isect_part.reserve((ncap / 256 + 1) * 8, false, stream); isect_part_flags.reserve(ncap / 256 + 1, false, stream);
   isect_cap = ncap;
   sort_tmp.reserve(b2c_radix_sort_temp_bytes((uint32_t)ncap));
+  // The new row buffers hold uninitialised memory, possibly at the address a previous epoch cleared
+  // (the allocator may hand a freed block back): force the next pass to start a new epoch.
+  row_epoch_buf = nullptr;
 }
 
 namespace {

@@ -267,7 +267,9 @@ int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream);
  * process, so images with b2c_loss_partials(W, H) above that (about 160 megapixels) are rejected with
  * hipErrorInvalidValue before any work is queued. No hipMalloc, hipFree or allocating routine is called.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (other streams, other host
- * threads) race and must be serialised by the caller. Results are bit-identical to b2c_hip_photometric. */
+ * threads) race and must be serialised by the caller. Results are bit-identical to b2c_hip_photometric
+ * called with a partials workspace (assign 0 or 1): that form sums the partials in the same fixed order;
+ * b2c_hip_photometric without a workspace adds per-wave float atomics in hardware order instead. */
 #define B2C_LOSS_STATIC_PARTIALS (1 << 18)
 int b2c_hip_photometric_noalloc(const b2c_loss_args* a, hipStream_t stream);
 

@@ -233,6 +233,7 @@ void orc_adam_update(orc_adam_model_t* m, const orc_cam_t* cam, int active_deg, 
                      const orc_adam_step_t* s);
 
 /* Pieces of the update exported for the pinning tests. */
+uint32_t orc_mix32(uint32_t x);                            /* util.cuh:106-110, the chain's finaliser */
 float orc_hash_unit(uint32_t a, uint32_t b, uint32_t c);   /* util.cuh:106-112 */
 float orc_hash_gauss(uint32_t a, uint32_t b, uint32_t c);  /* util.cuh:114-117 */
 float orc_cos_turns(float u);                              /* cos(2 pi u), u in [0, 1) */

@@ -145,6 +145,7 @@ def lib():
                                          C.POINTER(OrcAdamStep)]
         u32 = C.c_uint32
         _lib.orc_hash_unit.restype = f; _lib.orc_hash_unit.argtypes = [u32, u32, u32]
+        _lib.orc_mix32.restype = u32; _lib.orc_mix32.argtypes = [u32]
         _lib.orc_hash_gauss.restype = f; _lib.orc_hash_gauss.argtypes = [u32, u32, u32]
         _lib.orc_cos_turns.restype = f; _lib.orc_cos_turns.argtypes = [f]
         _lib.orc_f16_bits.restype = C.c_uint16; _lib.orc_f16_bits.argtypes = [f]
@@ -605,6 +606,10 @@ def project_ok(po, q, ls, camd) -> bool:
 
 def hash_unit(a, b, c) -> float:
     return lib().orc_hash_unit(a, b, c)
+
+
+def mix32(x):
+    return lib().orc_mix32(x)
 
 
 def hash_gauss(a, b, c) -> float:

@@ -27,6 +27,8 @@ static uint32_t mix32(uint32_t x) {
   return x;
 }
 
+uint32_t orc_mix32(uint32_t x) { return mix32(x); }
+
 float orc_hash_unit(uint32_t a, uint32_t b, uint32_t c) {
   const uint32_t h = mix32((a * 0x9E3779B1u) ^ mix32((b * 0x85EBCA77u) ^ mix32(c * 0xC2B2AE3Du)));
   return (float)(h >> 8) * (1.f / 16777216.f);

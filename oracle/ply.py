@@ -68,19 +68,27 @@ def parse_header(path):
     return dict(binary=binary, n=n, props=props, offset=offset)
 
 
+class _EmptyColumns(dict):
+    """Columns of a file with no rows: a name the header lacks reads as an empty column."""
+
+    def __missing__(self, key):
+        return np.zeros(0, np.float64)
+
+
 def read(path):
     h = parse_header(path)
     names = [p[0] for p in h["props"]]
     n = h["n"]
     if h["binary"]:
-        dt = np.dtype([(nm, t) for nm, t in h["props"]])
+        dt = np.dtype([(f"p{k}", t) for k, (_, t) in enumerate(h["props"])])
         with open(path, "rb") as f:
             f.seek(h["offset"])
             raw = f.read(n * dt.itemsize)
         if len(raw) < n * dt.itemsize:
             raise PlyError(f"ply: truncated file '{path}'")
         table = np.frombuffer(raw, dt, n)
-        col = {nm: table[nm].astype(np.float64) for nm in names}
+        # a repeated name resolves to its last column, as read_ply's name -> column map does (ply.cpp:96-97)
+        col = {nm: table[f"p{k}"].astype(np.float64) for k, nm in enumerate(names)}
     else:
         with open(path, "rb") as f:
             f.seek(h["offset"])
@@ -89,6 +97,8 @@ def read(path):
             raise PlyError(f"ply: truncated ascii file '{path}'")
         arr = np.array([float(v) for v in vals[: n * len(names)]], np.float64).reshape(n, len(names))
         col = {nm: arr[:, k] for k, nm in enumerate(names)}
+    if n == 0:  # read_ply looks members up per row: a file without rows needs none beyond the flags' first
+        col = _EmptyColumns(col)
     has = col.__contains__
     n_rest = 0
     while has(f"f_rest_{n_rest}"):

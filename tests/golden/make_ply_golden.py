@@ -201,6 +201,24 @@ def main():
     with open(os.path.join(OUT, "bad_not_ply.ply"), "wb") as f:
         f.write(b"solid mesh\nendsolid\n")
 
+    # a repeated property name: read_ply's name -> column map keeps the last column of that name
+    props = [("x", "float"), ("y", "float"), ("z", "float"), ("opacity", "float"), ("junk", "uchar"),
+             ("opacity", "short"), ("x", "double")]
+    dup = np.zeros(7, np.dtype([(f"p{k}", NP[t]) for k, (_, t) in enumerate(props)]))
+    for k, v in enumerate((np.arange(7) * 0.5, np.arange(7) * -1.0, np.arange(7) + 3.0, np.arange(7) * 0.25,
+                           np.arange(7) + 100, np.arange(7) * 7 - 20, np.arange(7) * 1.125 - 4)):
+        dup[f"p{k}"] = v
+    with open(os.path.join(OUT, "input_duplicate_names.ply"), "wb") as f:
+        f.write(header(props, 7))
+        f.write(dup.tobytes())
+    # files without rows whose optional groups are incomplete: read_ply looks the other members of a group up
+    # per row, so it accepts them
+    with open(os.path.join(OUT, "input_empty_partial_groups.ply"), "wb") as f:
+        f.write(header(xyz + [("scale_0", "float"), ("rot_0", "float"), ("rot_1", "float"), ("f_dc_0", "float"),
+                              ("ev_w_in", "float"), ("red", "uchar"), ("cage_gate_a", "float")], 0))
+    with open(os.path.join(OUT, "input_empty_red_only.ply"), "wb") as f:
+        f.write(header(xyz + [("red", "ushort"), ("seg_conf", "float")], 0))
+
     for fname in sorted(os.listdir(OUT)):
         if not fname.endswith(".ply"):
             continue

@@ -101,6 +101,42 @@ def test_hash_unit_is_uniform_and_lanes_independent():
     assert abs(np.corrcoef(a, c)[0, 1]) < 0.02
 
 
+def _lowbias32_inverse(x):
+    """The inverse of lowbias32 as C. Wellons publishes it with the hash in hash-prospector (lowbias32_r):
+    each xorshift is undone by xoring in the shifted word twice over, each multiply by the inverse of the
+    multiplier modulo 2^32."""
+    x = x.astype(np.uint32)
+    x ^= x >> np.uint32(16)
+    x = (x * np.uint32(0x43021123)).astype(np.uint32)
+    x ^= (x >> np.uint32(15)) ^ (x >> np.uint32(30))
+    x = (x * np.uint32(0x1D69E2A5)).astype(np.uint32)
+    x ^= x >> np.uint32(16)
+    return x
+
+
+def test_mix32_is_lowbias32():
+    """The finaliser of the random streams (util.cuh:106-110) is lowbias32: the published inverse undoes it
+    on every sampled word, and the published inverse multipliers are the modular inverses of the forward
+    ones the oracle must then use (checked here from the numbers alone)."""
+    assert (0x7FEB352D * 0x1D69E2A5) % 2 ** 32 == 1 and (0x846CA68B * 0x43021123) % 2 ** 32 == 1
+    words = np.concatenate([np.random.default_rng(11).integers(0, 2 ** 32, 20000, dtype=np.uint64),
+                            np.array([0, 1, 2, 0xFFFFFFFF, 0x80000000, 0x7FFFFFFF], np.uint64)]).astype(np.uint32)
+    mixed = np.array([O.mix32(int(w)) for w in words], np.uint32)
+    assert np.array_equal(_lowbias32_inverse(mixed), words)
+    assert O.mix32(0) == 0 and len(np.unique(mixed)) == len(np.unique(words))
+
+
+def test_hash_unit_chains_the_xxhash_primes():
+    """hash_unit(a, b, c) is the top 24 bits of mix32(a P1 ^ mix32(b P2 ^ mix32(c P3))) over 2^24, with
+    P1..P3 xxHash32's PRIME32_1..3 (2654435761, 2246822519, 3266489917 in its specification)."""
+    P1, P2, P3 = 2654435761, 2246822519, 3266489917
+    m = 2 ** 32
+    rng = np.random.default_rng(12)
+    for a, b, c in rng.integers(0, 2 ** 32, (3000, 3), dtype=np.uint64).tolist() + [[0, 0, 0], [1, 2, 3]]:
+        h = O.mix32((a * P1 % m) ^ O.mix32((b * P2 % m) ^ O.mix32(c * P3 % m)))
+        assert O.hash_unit(a, b, c) == (h >> 8) / 2.0 ** 24, (a, b, c)
+
+
 def test_hash_gauss_is_standard_normal():
     x = np.array([O.hash_gauss(77, i, c) for i in range(20000) for c in range(3)])
     assert abs(x.mean()) < 0.02 and abs(x.std() - 1.0) < 0.02

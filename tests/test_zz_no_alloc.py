@@ -1,7 +1,8 @@
 """The allocation-free loss entry point (b2c_hip_photometric_noalloc, include/b2c_kernels.h) against the
 regular one (b2c_hip_photometric with a caller-provided partials workspace), called through the C ABI on
 device buffers from torch: two calls in a row, the second on a smaller image, each bit-identical to the
-regular entry point in the loss value and every per-pixel gradient. The regular entry point runs first on
+regular entry point in the loss value and every per-pixel gradient, in assign mode (loss stored, running
+sum updated) and in add mode (loss added to loss_accum[0]). The regular entry point runs first on
 each input, then the allocation-free one, so its fixed scratch holds the previous call's partials (stale
 contents must not leak into the result)."""
 import ctypes as C
@@ -37,7 +38,7 @@ def _inputs(W, H, seed, weights):
     return t
 
 
-def _call(fn, t, W, H, opts, partials):
+def _call(fn, t, W, H, opts, partials, assign):
     import torch
     a = LossArgs()
     a.pred, a.gt = t["pred"].data_ptr(), t["gt"].data_ptr()
@@ -49,10 +50,10 @@ def _call(fn, t, W, H, opts, partials):
     a.composite, a.mask, a.alpha_lane = opts["composite"], opts["mask"], opts["alpha_lane"]
     a.match_alpha_weight, a.scale, a.grad_scale = 0.1, opts["scale"], 3.0 * W * H
     t["v_out"].zero_()
-    t["acc"].fill_(0.25)  # assign mode overwrites [0..3]
+    t["acc"].fill_(0.25)  # assign mode overwrites [0..3]; add mode adds to [0]
     a.v_out, a.loss_accum = t["v_out"].data_ptr(), t["acc"].data_ptr()
     a.partials = partials
-    a.assign, a.running = 1, 1
+    a.assign, a.running = assign, assign
     stream = torch.cuda.current_stream().cuda_stream
     rc = fn(C.byref(a), C.c_void_p(stream))
     assert rc == 0, f"launcher returned {rc}"
@@ -72,9 +73,10 @@ def test_noalloc_loss_matches_workspace_loss_twice():
         emit(f"no-alloc loss call {k + 1}: {W}x{H}")
         t = _inputs(W, H, 100 + k, weights)
         ws = torch.empty(int(L.b2c_loss_partials(W, H)), dtype=torch.float32, device="cuda:0")
-        v_ref, acc_ref = _call(L.b2c_hip_photometric, t, W, H, opts, ws.data_ptr())
-        v_na, acc_na = _call(L.b2c_hip_photometric_noalloc, t, W, H, opts, None)
-        assert acc_ref[0] > 0 and acc_ref[3] == 1
-        assert np.array_equal(acc_na[:4], acc_ref[:4]), (acc_na[:4], acc_ref[:4])
-        assert np.array_equal(v_na, v_ref), f"{int((v_na != v_ref).sum())} gradient entries differ"
-        assert np.abs(v_ref).max() > 0
+        for assign in (1, 0):
+            v_ref, acc_ref = _call(L.b2c_hip_photometric, t, W, H, opts, ws.data_ptr(), assign)
+            v_na, acc_na = _call(L.b2c_hip_photometric_noalloc, t, W, H, opts, None, assign)
+            assert acc_ref[0] > (0 if assign else 0.25) and acc_ref[3] == (1 if assign else 0.25)
+            assert np.array_equal(acc_na[:4], acc_ref[:4]), (assign, acc_na[:4], acc_ref[:4])
+            assert np.array_equal(v_na, v_ref), f"assign={assign}: {int((v_na != v_ref).sum())} gradient entries differ"
+            assert np.abs(v_ref).max() > 0
