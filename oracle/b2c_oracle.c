@@ -355,6 +355,18 @@ void orc_project(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int
   orc_project_feat(m, cam, active_deg, tiles_x, tiles_y, proj0, proj1, proj2, proj3, tile_count, hit_info, 0, NULL);
 }
 
+/* project.cu:82-83: every splat that survives project_one's culls (whatever its tile count) raises its
+ * max_screen to its larger screen-space half-extent as a fraction of the frame, max(ex / W, ey / H). */
+void orc_max_screen(const orc_model_t* m, const orc_cam_t* cam, float* max_screen) {
+  for (int i = 0; i < m->n; i++) {
+    proj_t pr;
+    project_one(m->pos_op + (size_t)i * 4, m->quat + (size_t)i * 4, m->lscale + (size_t)i * 4, cam, &pr);
+    if (!pr.ok) continue;
+    const float ms = fmaxf(pr.ex / (float)cam->W, pr.ey / (float)cam->H);
+    max_screen[i] = fmaxf(max_screen[i], ms);
+  }
+}
+
 /* ------------------------------------------------------------------------------------------------
  * Binning (binning.cu:10-143).
  * ---------------------------------------------------------------------------------------------- */

@@ -89,6 +89,10 @@ void orc_project(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int
                  float* proj0, float* proj1, float* proj2, float* proj3,
                  uint32_t* tile_count, uint32_t* hit_info /* [n][2] */);
 
+/* project.cu:82-83: max_screen[i] = max(max_screen[i], max(ex / W, ey / H)) for every splat that survives
+ * the projection's culls. */
+void orc_max_screen(const orc_model_t* m, const orc_cam_t* cam, float* max_screen);
+
 /* The same with the feature lanes (feat_mode 1: pseudo-normals, 2: feat_buffer [n][3], project.cu:63-77). */
 void orc_project_feat(const orc_model_t* m, const orc_cam_t* cam, int active_deg, int tiles_x, int tiles_y,
                       float* proj0, float* proj1, float* proj2, float* proj3, uint32_t* tile_count, uint32_t* hit_info,

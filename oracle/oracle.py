@@ -117,6 +117,8 @@ def lib():
         _lib.orc_frag_sigma.argtypes = [C.c_int] + [p] * 6
         _lib.orc_set_threads.restype = None
         _lib.orc_set_threads.argtypes = [C.c_int]
+        _lib.orc_max_screen.restype = None
+        _lib.orc_max_screen.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcCam), p]
         _lib.orc_project_feat.restype = None
         _lib.orc_project_feat.argtypes = [C.POINTER(OrcModel), C.POINTER(OrcCam), C.c_int, C.c_int, C.c_int] + [p] * 6 + [
             C.c_int, p]
@@ -269,6 +271,29 @@ def project(scene, camd, active_deg=None):
                            *[_ptr(out[k]) for k in ("proj0", "proj1", "proj2", "proj3", "tile_count", "hit_info")],
                            int(scene.feat_mode), _ptr(fb))
     return out
+
+
+def max_screen(scene, camd, init):
+    """The projection's max_screen side output (project.cu:82-83) over a starting array."""
+    out = np.array(init, np.float32, copy=True)
+    m = _Model(scene)  # holds the arrays the call reads
+    cam = make_cam(camd)
+    lib().orc_max_screen(C.byref(m.m), C.byref(cam), _ptr(out))
+    return out
+
+
+def refine_stats(v_splat, vis_flag, tile_count, vis_count, refine_norm):
+    """The refine statistics optim_kernel updates from a view's gradients before it clears them
+    (optim.cu:113,122-124): vis_count += 1 for a splat the backward flagged that has tiles; refine_norm =
+    max(refine_norm, lane 9 of v_splat clamped to [0, 1e32], non-finite as 0). Lane 9 is read only for
+    flagged splats (the others contribute 0)."""
+    vf = np.asarray(vis_flag) != 0
+    visible = vf & (np.asarray(tile_count) != 0)
+    vc = np.asarray(vis_count, np.float32) + visible.astype(np.float32)
+    g9 = np.where(vf, np.asarray(v_splat, np.float32)[:, 9], np.float32(0))
+    with np.errstate(invalid="ignore"):
+        rn = np.where(np.isfinite(g9), np.minimum(np.maximum(g9, np.float32(0)), np.float32(1e32)), np.float32(0))
+    return vc.astype(np.float32), np.maximum(np.asarray(refine_norm, np.float32), rn.astype(np.float32))
 
 
 def _ext(feat=False, proj3=None, hollow_z=None, margin=0.05, lam=0.0, out_feat=None, hollow_pen=None, v_feat=None):

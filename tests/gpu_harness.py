@@ -21,7 +21,13 @@ mismatch names its stage. Tolerances:
   1e-3 of their lane's maximum: 99th percentile <= 1e-3;
 * parameter gradients from the GPU's own v_splat: <= 1e-3 of each column's largest |value| (two different
   derivations of the projection VJP, the kernel's from the semi-axis form and the oracle's restating the
-  reference's world-covariance chain), and per-entry relative error percentiles as for v_splat.
+  reference's world-covariance chain), and per-entry relative error percentiles as for v_splat;
+* the side outputs the reference's refine pass reads (refine.cu:55-95): max_screen after the projection
+  (project.cu:82-83) bit-exact, raised from a nonzero starting array; vis_weight after the backward
+  (raster_bwd_tc.cu:177-195) at the v_splat bars, and conserved: its sum over splats equals the GPU
+  image's accumulated alpha sum(1 - T_final) to 1e-4; vis_count and refine_norm after the VJP
+  (optim.cu:113,122-124) bit-exact against the oracle's update of the same starting arrays from the GPU's
+  own v_splat and vis_flag.
 """
 from __future__ import annotations
 
@@ -33,6 +39,31 @@ from oracle import oracle as O
 
 def emit(msg):
     print(msg, flush=True)
+
+
+def seed_side_outputs(r, n, seed=7):
+    """Nonzero starting values for the per-splat statistics the hot path raises or adds to, so a check
+    sees the running maximum / count and not only a first write."""
+    rng = np.random.default_rng(seed)
+    init = {}
+    for k, hi in (("max_screen", 0.01), ("vis_count", 5.0), ("refine_norm", 1e-4)):
+        a = rng.uniform(0.0, hi, n).astype(np.float32)
+        if k == "vis_count":
+            a = np.floor(a)
+        a[::5] = 0.0
+        r.write_model(k, a)
+        init[k] = a
+    return init
+
+
+def check_max_screen(r, scene, camd, init):
+    got = r.read_model("max_screen")
+    want = O.max_screen(scene, camd, init)
+    bad = got.view(np.uint32) != want.view(np.uint32)
+    assert not bad.any(), f"max_screen differs for splats {np.flatnonzero(bad)[:10]}"
+    raised = int((want > init).sum())
+    emit(f"    max_screen bit-exact ({raised} of {scene.n} raised)")
+    assert raised > 0 or scene.n == 0
 
 
 def check_projection(r, scene, camd):
@@ -181,14 +212,29 @@ def check_aux_losses(r, scene, fw, grad_scale):
     return v_feat
 
 
+def check_vis_weight(got, ref, out_T):
+    """vis_weight against the oracle's at the v_splat bars, and its conservation on the GPU's own image."""
+    scale = float(np.abs(ref).max()) + 1e-30
+    worst = float((np.abs(got - ref) / scale).max()) if got.size else 0.0
+    pc = rel_percentiles(got[:, None], ref[:, None])
+    total = float(np.asarray(got, np.float64).sum())
+    alpha = float((1.0 - np.asarray(out_T, np.float64)).sum())
+    emit(f"    vis_weight max err {worst:.2e} of max; rel p99 {pc['p99']:.1e}; sum {total:.6g} vs image alpha {alpha:.6g}")
+    assert worst <= 2e-3, f"vis_weight: worst error {worst:.2e} of the largest"
+    assert pc["p99"] <= 1e-3, f"vis_weight per-entry 99th percentile rel err {pc['p99']:.2e}"
+    assert abs(total - alpha) <= 1e-4 * alpha + 1e-6, f"vis_weight sums to {total}, the image's alpha to {alpha}"
+
+
 def check_backward(r, scene, pr, bn, fw, v_out, W, H, bg, mode, grad_scale, v_feat=None):
     r.zero("v_splat")
     r.zero("vis_flag")
+    r.write_model("vis_weight", np.zeros(scene.n, np.float32))
     r.backward(mode=mode, grad_scale=grad_scale)
     vs = r.read("v_splat")
     vf = r.read("vis_flag")
+    vw = r.read_model("vis_weight")
     inv = 1.0 / grad_scale if mode == 1 else 1.0
-    ref_vs, ref_vf, _ = O.raster_bwd(pr, bn, dict(tile_ranges=fw["tile_ranges"], out_rgba=fw["out_rgba"],
+    ref_vs, ref_vf, ref_vw = O.raster_bwd(pr, bn, dict(tile_ranges=fw["tile_ranges"], out_rgba=fw["out_rgba"],
                                                   out_T=fw["out_T"], last_idx=fw["last_idx"]), v_out, W, H, bg,
                                      scene.n, inv_gscale=inv, v_feat=v_feat if scene.feat_mode else None,
                                      hollow_z=scene.hollow_z, hollow_margin=scene.hollow_margin,
@@ -203,12 +249,20 @@ def check_backward(r, scene, pr, bn, fw, v_out, W, H, bg, mode, grad_scale, v_fe
     emit(f"    v_splat lane-max err {worst:.2e}; per-entry rel p50 {pc['p50']:.1e} p99 {pc['p99']:.1e} "
          f"max {pc['max']:.1e} over {pc['n']}")
     assert pc["p99"] <= 1e-3, f"v_splat per-entry 99th percentile rel err {pc['p99']:.2e}"
+    check_vis_weight(vw, ref_vw, fw["out_T"])
     return vs, vf, worst
 
 
-def check_vjp(r, scene, camd, vs, vf, tile_count):
+def check_vjp(r, scene, camd, vs, vf, tile_count, init=None):
     r.vjp()
     g = r.read("grads")
+    if init is not None:  # the refine statistics, from the same v_splat and flags (optim.cu:113,122-124)
+        vc, rn = O.refine_stats(vs, vf, tile_count, init["vis_count"], init["refine_norm"])
+        for k, want in (("vis_count", vc), ("refine_norm", rn)):
+            got = r.read_model(k)
+            bad = got.view(np.uint32) != want.view(np.uint32)
+            assert not bad.any(), f"{k} differs for splats {np.flatnonzero(bad)[:10]}"
+        emit(f"    vis_count / refine_norm bit-exact ({int((vc > init['vis_count']).sum())} splats visible)")
     ref = O.vjp(scene, camd, vs, vf, tile_count)
     col = np.abs(ref).max(axis=0) + 1e-30
     rel = np.abs(g - ref) / col
@@ -236,9 +290,11 @@ def full_check(scene, mode=1, bg=None, loss=True, backward=True, fp64_rgba=False
     r = _native.Renderer(scene)
     try:
         camd = _native.camera_gpu_from(scene.cam)
+        init = seed_side_outputs(r, scene.n)
         emit(f"  [{scene.name}] projection")
         r.project(bg=bg)
         pr = check_projection(r, scene, camd)
+        check_max_screen(r, scene, camd, init["max_screen"])
         emit(f"  [{scene.name}] binning")
         r.bin()
         bn = check_binning(r, pr, W, H)
@@ -257,7 +313,7 @@ def full_check(scene, mode=1, bg=None, loss=True, backward=True, fp64_rgba=False
                 emit(f"  [{scene.name}] backward mode {mode}")
                 vs, vf, out["v_splat_err"] = check_backward(r, scene, pr, bn, fw, v, W, H, bg, mode, gs, v_feat)
                 emit(f"  [{scene.name}] vjp")
-                out["grads"] = check_vjp(r, scene, camd, vs, vf, pr["tile_count"])
+                out["grads"] = check_vjp(r, scene, camd, vs, vf, pr["tile_count"], init)
         return out
     finally:
         r.close()
