@@ -126,7 +126,7 @@ EXPORTS = [
     "b2c_hip_evidence_sum", "b2c_hip_probe_depth",
     "b2c_ply_info_get", "b2c_ply_read", "b2c_ply_write", "b2c_ply_is_vertex_only", "b2c_ply_comments",
     "b2c_model_load_ply", "b2c_model_save_ply", "b2c_hip_ply_decode", "b2c_hip_ply_encode",
-    "b2c_png_decode", "b2c_dataset_load", "b2c_dataset_destroy", "b2c_dataset_count", "b2c_dataset_view_info",
+    "b2c_png_decode", "b2c_image_decode", "b2c_image_resample", "b2c_dataset_load", "b2c_dataset_destroy", "b2c_dataset_count", "b2c_dataset_view_info",
     "b2c_dataset_view_read", "b2c_dataset_view_upload", "b2c_dataset_points", "b2c_dataset_summary",
 ]
 
@@ -202,6 +202,8 @@ def lib():
         L.b2c_model_load_ply.argtypes = [p, C.c_char_p, i, C.POINTER(i)]
         L.b2c_model_save_ply.argtypes = [p, C.c_char_p, C.c_char_p, C.POINTER(PlyInfo), C.POINTER(PlyArrays)]
         L.b2c_png_decode.argtypes = [C.c_char_p, C.POINTER(i), C.POINTER(i), C.POINTER(i), p, C.c_size_t]
+        L.b2c_image_decode.argtypes = [C.c_char_p, C.POINTER(i), C.POINTER(i), C.POINTER(i), p, C.c_size_t]
+        L.b2c_image_resample.argtypes = [p, i, i, p, i, i, i]
         L.b2c_dataset_load.restype = p
         L.b2c_dataset_load.argtypes = [C.POINTER(DatasetOpts)]
         L.b2c_dataset_destroy.argtypes = [p]
@@ -320,6 +322,28 @@ def png_decode(path):
     check(lib().b2c_png_decode(os.fsencode(path), C.byref(w), C.byref(h), C.byref(ch), _ptr(out), out.nbytes),
           "png_decode")
     return out, ch.value
+
+
+def image_decode(path):
+    """The loader's image decoder (PNG or JPEG): (rgba [h][w][4] uint8, channels in the file)."""
+    w, h, ch = C.c_int(), C.c_int(), C.c_int()
+    check(lib().b2c_image_decode(os.fsencode(path), C.byref(w), C.byref(h), C.byref(ch), None, 0), "image_decode")
+    out = np.zeros((h.value, w.value, 4), np.uint8)
+    check(lib().b2c_image_decode(os.fsencode(path), C.byref(w), C.byref(h), C.byref(ch), _ptr(out), out.nbytes),
+          "image_decode")
+    return out, ch.value
+
+
+RESAMPLE_FILTERS = {"triangle": 0, "mitchell": 1, "point": 2}
+
+
+def image_resample(rgba, nw, nh, filt):
+    """The loader's resize of an RGBA8 image [h][w][4] to [nh][nw][4] (filter: triangle, mitchell, point)."""
+    src = np.ascontiguousarray(rgba, np.uint8)
+    out = np.zeros((nh, nw, 4), np.uint8)
+    check(lib().b2c_image_resample(_ptr(src), src.shape[1], src.shape[0], _ptr(out), nw, nh,
+                                   RESAMPLE_FILTERS[filt]), "image_resample")
+    return out
 
 
 class Dataset:

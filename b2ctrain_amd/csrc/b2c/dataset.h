@@ -1,8 +1,8 @@
 // COLMAP text models and the dataset loader (replaces src/dataset/colmap.h:1-32, views.h:1-39 and the
 // Camera helpers of camera.h): cameras.txt / images.txt / points3D.txt, frames with their masks/, weights/,
 // normals/ and labels/ sidecars, packed into the RGBA8 views the loss reads. Frames and sidecars are PNG
-// (decoded by png.h); JPEG frames and frames that would need resampling (larger than max_resolution, or a
-// sidecar of another size) are rejected with an error naming the file.
+// (png.h) or JPEG (jpeg.h); frames over max_resolution and sidecars of another size are resampled
+// (resample.h) as the reference resamples them.
 #pragma once
 #include <cstdint>
 #include <map>
@@ -11,9 +11,14 @@
 #include <type_traits>
 #include <vector>
 
+#include "png.h"
 #include "render.h"
 
 namespace b2c {
+
+// A frame or sidecar file, PNG or JPEG by its signature, as 8-bit RGBA (the reference's
+// stbi_load(path, ..., 4), views.cpp:63-72).
+DecodedImage decode_image(const std::string& path);
 
 struct ColmapImage {
   int id = 0, camera_id = 0;

@@ -13,6 +13,7 @@
 #include "b2c/optim.h"
 #include "b2c/ply.h"
 #include "b2c/png.h"
+#include "b2c/resample.h"
 #include "b2c/render.h"
 
 struct b2c_model {
@@ -582,6 +583,27 @@ int b2c_png_decode(const char* path, int* w, int* h, int* channels, uint8_t* rgb
       if (rgba_bytes < d.rgba.size()) throw std::runtime_error("png_decode: output buffer too small");
       std::memcpy(rgba, d.rgba.data(), d.rgba.size());
     }
+  });
+}
+
+int b2c_image_decode(const char* path, int* w, int* h, int* channels, uint8_t* rgba, size_t rgba_bytes) {
+  return guarded([&] {
+    const b2c::DecodedImage d = b2c::decode_image(path);
+    *w = d.w;
+    *h = d.h;
+    *channels = d.channels_in_file;
+    if (rgba) {
+      if (rgba_bytes < d.rgba.size()) throw std::runtime_error("image_decode: output buffer too small");
+      std::memcpy(rgba, d.rgba.data(), d.rgba.size());
+    }
+  });
+}
+
+int b2c_image_resample(const uint8_t* src, int w, int h, uint8_t* dst, int nw, int nh, int filter) {
+  return guarded([&] {
+    if (filter < 0 || filter > 2) throw std::invalid_argument("image_resample: filter must be 0, 1 or 2");
+    const std::vector<uint8_t> out = b2c::resample_rgba8(src, w, h, nw, nh, (b2c::ResampleFilter)filter);
+    std::memcpy(dst, out.data(), out.size());
   });
 }
 

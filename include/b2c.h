@@ -198,6 +198,16 @@ int b2c_dataset_summary(const b2c_dataset* d, char* buf, size_t cap, int* counts
  * RGBA [h][w][4] (rgba_bytes must hold it). */
 int b2c_png_decode(const char* path, int* w, int* h, int* channels, uint8_t* rgba, size_t rgba_bytes);
 
+/* The loader's image decoder (the reference's stbi_load(path, &w, &h, &c, 4), views.cpp:63-72): PNG or JPEG
+ * (baseline, extended sequential or progressive Huffman, 8-bit) chosen by the file's signature; outputs as
+ * b2c_png_decode. */
+int b2c_image_decode(const char* path, int* w, int* h, int* channels, uint8_t* rgba, size_t rgba_bytes);
+
+/* The loader's resize (the reference's resize_rgba, views.cpp:73-78: stbir_resize of four independent 8-bit
+ * channels, edges clamped): src [h][w][4] to dst [nh][nw][4]; filter 0 triangle, 1 Mitchell, 2 point
+ * sample (views.cpp:158,169,191,202,209). */
+int b2c_image_resample(const uint8_t* src, int w, int h, uint8_t* dst, int nw, int nh, int filter);
+
 /* compute_evidence / download_evidence / download_labels (src/train/evidence.h:10-22) over nviews views and
  * their cameras: the evidence [n][7] = (w_in, w_all, err, views, dir xyz) and, with export_labels, the label
  * vote [n][2] = (winning class, share). Synchronous; the accumulators are module-level, as the reference's. */

@@ -227,3 +227,30 @@ extern "C" long long ref_dataset_summary(int* counts, char* text, size_t cap, fl
   }
   return (long long)g_dataset.points.size();
 }
+
+// ---- The reference loader's image decoder and resize (stb_image v2.30 / stb_image_resize2 v2.18 as
+// src/dataset/views.cpp compiles them), for the image fixtures under tests/golden/images/ ----
+#include "stb_image.h"
+#include "stb_image_resize2.h"
+
+// stbi_load(path, ..., 4): 0 and the image (rgba: w * h * 4 bytes when not NULL), or 1 with the reason.
+extern "C" int ref_image_load(const char* path, int* w, int* h, int* channels, uint8_t* rgba, size_t cap,
+                              char* err, size_t err_cap) {
+  unsigned char* p = stbi_load(path, w, h, channels, 4);
+  if (!p) {
+    std::strncpy(err, stbi_failure_reason(), err_cap - 1);
+    err[err_cap - 1] = 0;
+    return 1;
+  }
+  const size_t n = (size_t)*w * *h * 4;
+  if (rgba && cap >= n) std::memcpy(rgba, p, n);
+  stbi_image_free(p);
+  return 0;
+}
+
+// The loader's resize_rgba (views.cpp:73-78): filter 0 triangle, 1 Mitchell, 2 point sample.
+extern "C" int ref_image_resize(const uint8_t* src, int w, int h, uint8_t* dst, int nw, int nh, int filter) {
+  const stbir_filter f = filter == 0 ? STBIR_FILTER_TRIANGLE : filter == 1 ? STBIR_FILTER_MITCHELL
+                                                                         : STBIR_FILTER_POINT_SAMPLE;
+  return stbir_resize(src, w, h, 0, dst, nw, nh, 0, STBIR_4CHANNEL, STBIR_TYPE_UINT8, STBIR_EDGE_CLAMP, f) ? 0 : 1;
+}

@@ -11,8 +11,12 @@ hold (RGBA, RGB, grey and grey + alpha, palettes with and without tRNS, 16-bit s
 colour-key tRNS, Adam7 interlacing; the PNG files are written here byte by byte with zlib), masks (with
 the .mask suffix and upper-case names), weights (RGB luma and grey), labels and normals sidecars, the three
 pinhole camera models, a frame found by a recursive search, a frame whose file is missing, points3D.txt
-and splat / mesh plys. ``expected.npz`` holds every loaded view (planes, camera, flags) for two option
-sets: eval split every 3rd view, and a forced masked alpha mode with frame subsampling.
+and splat / mesh plys. ``scene_jpeg/`` holds JPEG frames (baseline 4:2:0 and 4:2:2 with restart markers,
+progressive 4:4:4, grey, CMYK) and a PNG frame of mixed sizes, with mask, weight, label and normal sidecars
+of other sizes than their frames (JPEG and PNG), the model at the dataset root. ``expected.npz`` holds every
+loaded view (planes, camera, flags) for each option set: eval splits, a forced masked alpha mode with frame
+subsampling, and resolution caps below the frame sizes (Mitchell-resampled frames; triangle-resampled masks
+and weights; point-sampled labels and normals).
 """
 from __future__ import annotations
 
@@ -176,19 +180,80 @@ def ref():
     return L
 
 
-OPTION_SETS = {  # name: (max_frames, max_resolution, eval_split_every, subsample_frames, alpha_mode)
-    "split3": (-1, 1920, 3, -1, -1),
-    "masked_sub2": (5, 1920, -1, 2, 0),
+OPTION_SETS = {  # name: (scene, max_frames, max_resolution, eval_split_every, subsample_frames, alpha_mode)
+    "split3": ("scene", -1, 1920, 3, -1, -1),
+    "masked_sub2": ("scene", 5, 1920, -1, 2, 0),
+    "cap16": ("scene", -1, 16, -1, -1, -1),  # every frame over the cap: Mitchell, sidecars follow the frame
+    "jpeg_split2": ("scene_jpeg", -1, 1920, 2, -1, -1),
+    "jpeg_cap32": ("scene_jpeg", -1, 32, -1, -1, -1),
 }
+
+
+def jpeg_bytes(pixels, mode, **kw):
+    """A JPEG of `pixels` written by PIL (libjpeg)."""
+    import io
+
+    from PIL import Image
+    buf = io.BytesIO()
+    Image.fromarray(pixels[..., 0] if pixels.shape[-1] == 1 else pixels, mode).save(buf, "JPEG", **kw)
+    return buf.getvalue()
+
+
+def smooth(rng, h, w, ch):
+    y, x = np.mgrid[0:h, 0:w]
+    out = np.zeros((h, w, ch))
+    for k in range(ch):
+        out[..., k] = 128 + 100 * np.sin(x / (3 + k) + y / (5 + 2 * k)) + rng.normal(0, 20, (h, w))
+    return np.clip(out, 0, 255).astype(np.uint8)
+
+
+def build_jpeg_scene(rng, root):
+    """JPEG frames (baseline 4:2:0 / 4:4:4, progressive, grey, CMYK) of mixed sizes, one PNG frame, and
+    sidecars of other sizes than their frames: every decode and resample path of the loader."""
+    if os.path.exists(root):
+        shutil.rmtree(root)
+    frames = {
+        "a_420.jpg": (40, 30, jpeg_bytes(smooth(rng, 30, 40, 3), "RGB", subsampling=2, quality=85)),
+        "b_444_prog.jpg": (36, 24, jpeg_bytes(smooth(rng, 24, 36, 3), "RGB", subsampling=0, progressive=True)),
+        "c_grey.jpg": (32, 20, jpeg_bytes(smooth(rng, 20, 32, 1), "L", quality=70)),
+        "d_cmyk.jpg": (30, 20, jpeg_bytes(smooth(rng, 20, 30, 4), "CMYK", quality=80)),
+        "e_big_422.jpg": (64, 40, jpeg_bytes(smooth(rng, 40, 64, 3), "RGB", subsampling=1, restart_marker_blocks=2)),
+        "f_rgba.png": (24, 16, png_bytes(rng.integers(0, 256, (16, 24, 4)), 6, 8)),
+    }
+    for name, (_, _, data) in frames.items():
+        write(os.path.join(root, "images", name), data)
+    # masks: a smaller grey JPEG (triangle enlarge), a larger PNG with alpha (triangle shrink)
+    write(os.path.join(root, "masks", "a_420.mask.jpg"), jpeg_bytes(smooth(rng, 15, 20, 1), "L"))
+    write(os.path.join(root, "masks", "e_big_422.png"), png_bytes(rng.integers(0, 256, (60, 96, 2)), 4, 8))
+    # weights: RGB at another size (luma after a triangle resample), grey JPEG
+    write(os.path.join(root, "weights", "b_444_prog.png"), png_bytes(rng.integers(0, 256, (12, 18, 3)), 2, 8))
+    write(os.path.join(root, "weights", "e_big_422.jpg"), jpeg_bytes(smooth(rng, 20, 32, 1), "L"))
+    # labels and normals: point-sampled from other sizes
+    write(os.path.join(root, "labels", "a_420.png"), png_bytes(rng.integers(0, 29, (45, 60, 1)), 0, 8))
+    write(os.path.join(root, "labels", "f_rgba.png"), png_bytes(rng.integers(0, 29, (8, 12, 1)), 0, 8))
+    write(os.path.join(root, "normals", "e_big_422.png"), png_bytes(rng.integers(0, 256, (20, 32, 4)), 6, 8))
+    write(os.path.join(root, "normals", "d_cmyk.jpg"), jpeg_bytes(smooth(rng, 40, 60, 3), "RGB"))
+    cams = ["1 PINHOLE 40 30 33.0 34.0 20.0 15.0", "2 SIMPLE_PINHOLE 36 24 30.0 18.0 12.0",
+            "3 PINHOLE 32 20 25.0 26.0 16.0 10.0", "4 OPENCV 30 20 24.0 24.5 15.0 10.0 0.1 0.01 0 0",
+            "5 PINHOLE 64 40 50.0 51.0 32.0 20.0", "6 PINHOLE 24 16 20.0 20.0 12.0 8.0"]
+    write(os.path.join(root, "cameras.txt"), ("\n".join(cams) + "\n").encode())
+    lines = []
+    for k, name in enumerate(sorted(frames)):
+        q = rng.normal(0, 1, 4)
+        t = rng.normal(0, 1, 3)
+        lines += [f"{k + 1} {q[0]:.9f} {q[1]:.9f} {q[2]:.9f} {q[3]:.9f} {t[0]:.9f} {t[1]:.9f} {t[2]:.9f} {k + 1} {name}",
+                  ""]
+    write(os.path.join(root, "images.txt"), ("\n".join(lines) + "\n").encode())
 
 
 def main():
     rng = np.random.default_rng(20261202)
-    scene = os.path.join(OUT, "scene")
-    build_scene(rng, scene)
+    build_scene(rng, os.path.join(OUT, "scene"))
+    build_jpeg_scene(np.random.default_rng(20261203), os.path.join(OUT, "scene_jpeg"))
     L = ref()
     expected = {}
-    for opt, (mf, mr, ev, sub, am) in OPTION_SETS.items():
+    for opt, (scene_dir, mf, mr, ev, sub, am) in OPTION_SETS.items():
+        scene = os.path.join(OUT, scene_dir)
         err = C.create_string_buffer(1024)
         if L.ref_dataset_load(scene.encode(), mf, mr, ev, sub, am, err, 1024):
             raise RuntimeError(err.value.decode())
@@ -221,9 +286,6 @@ def main():
                 expected[f"{key}/name"] = np.array(vname.value.decode())
                 for k, v in planes.items():
                     expected[f"{key}/{k}"] = v
-    # a frame beyond max_resolution: the reference resamples it (stb_image_resize2); this build rejects it
-    err = C.create_string_buffer(1024)
-    expected["small_res/ref_rc"] = np.int32(L.ref_dataset_load(scene.encode(), -1, 16, -1, -1, -1, err, 1024))
     np.savez_compressed(os.path.join(OUT, "expected.npz"), **expected)
     print("views:", {k: int(v) for k, v in expected.items() if k.endswith("count0") or k.endswith("count1")})
 

@@ -1,7 +1,9 @@
 """The COLMAP dataset loader on the host (include/b2c.h b2c_dataset_*, replacing src/dataset/views.cpp and
 colmap.cpp) against the reference's own loader: tests/golden/colmap/expected.npz holds what the compiled
 reference (with the stb_image decoder it vendors) loaded from tests/golden/colmap/scene/
-(tests/golden/make_colmap_golden.py). The PNG decoder is also checked against PIL.
+and scene_jpeg/ (tests/golden/make_colmap_golden.py): PNG and JPEG frames, sidecars of other sizes than their
+frames, and resolution caps, so every decode and resample path of the loader is compared. The PNG decoder is
+also checked against PIL.
 
 Bars: every view's planes, camera, flags, alpha coverage and normal-mask count bit-identical to the
 reference's; the same split, counts, points and initial ply."""
@@ -17,18 +19,25 @@ from b2ctrain_amd import _native as N
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "colmap")
 SCENE = os.path.join(GOLD, "scene")
 Z = np.load(os.path.join(GOLD, "expected.npz"), allow_pickle=False)
-OPTIONS = {"split3": dict(eval_split_every=3), "masked_sub2": dict(max_frames=5, subsample_frames=2,
-                                                                    alpha_mode="masked")}
+OPTIONS = {  # name: (scene directory, options) as tests/golden/make_colmap_golden.py loaded them
+    "split3": ("scene", dict(eval_split_every=3)),
+    "masked_sub2": ("scene", dict(max_frames=5, subsample_frames=2, alpha_mode="masked")),
+    "cap16": ("scene", dict(max_resolution=16)),
+    "jpeg_split2": ("scene_jpeg", dict(eval_split_every=2)),
+    "jpeg_cap32": ("scene_jpeg", dict(max_resolution=32)),
+}
 
 
 @pytest.mark.parametrize("opt", sorted(OPTIONS))
 def test_dataset_matches_the_reference(opt):
-    ds = N.Dataset(SCENE, **OPTIONS[opt])
+    scene, kw = OPTIONS[opt]
+    ds = N.Dataset(os.path.join(GOLD, scene), **kw)
     try:
         s = ds.summary()
         assert s["counts"] == list(Z[f"{opt}/counts"])
         assert s["name"] == str(Z[f"{opt}/name"])
-        assert os.path.relpath(s["init_ply"], s["root"]) == str(Z[f"{opt}/init_ply"])
+        init = os.path.relpath(s["init_ply"], s["root"]) if s["init_ply"] else ""
+        assert init == str(Z[f"{opt}/init_ply"])
         xyz, rgb = ds.points()
         assert np.array_equal(xyz, Z[f"{opt}/points_xyz"]) and np.array_equal(rgb, Z[f"{opt}/points_rgb"])
         for split in (0, 1):
@@ -52,12 +61,6 @@ def test_dataset_matches_the_reference(opt):
                     assert np.array_equal(got, want), (key, k)
     finally:
         ds.close()
-
-
-def test_frames_needing_resampling_are_rejected():
-    assert int(Z["small_res/ref_rc"]) == 0  # the reference resamples them (stb_image_resize2)
-    with pytest.raises(RuntimeError, match="resampling is not supported"):
-        N.Dataset(SCENE, max_resolution=16)
 
 
 def test_colmap_errors(tmp_path):
