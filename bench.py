@@ -15,8 +15,9 @@ lazy sparse Adam / MCMC update instead of the gradient export (dense and sparse)
 HBM roofline.
 
 Two CPU baselines are timed on this host (not the optimisation target):
-* cpu_baseline: the fp32 tiled CPU restatement (oracle/b2c_oracle.c) of the forward and backward raster over
-  the GPU's own tile lists, OpenMP over tiles on the host threads this process may use;
+* cpu_baseline: the fp32 tiled CPU restatement (oracle/b2c_oracle.c) of the whole step (projection, binning,
+  forward, loss, backward, VJP) on one frame, the raster passes OpenMP over tiles on the host threads this
+  process may use;
 * cpu_reference_algorithm: the reference's own CPU algorithm (tests/reference.cpp:34-143 restated: fp64,
   every depth-sorted splat tested at every pixel, one thread) on a bounded sample of pixels spread over the
   frame, extrapolated to the whole frame.
@@ -131,40 +132,49 @@ def cpu_baseline_frame(r, scene, mode, bg, cam):
     r.project(cam=cam, bg=bg)  # the step leaves proj0..3 unwritten; the CPU legs read them
     r.sync()
     f_sweep = f_sweep_of(r)
-    return f_sweep, cpu_baselines(r, scene, bg, f_sweep)
+    return f_sweep, cpu_baselines(r, scene.with_camera(cam), bg, f_sweep)
 
 
 def cpu_baselines(r, scene, bg, f_sweep):
-    """Both CPU baselines on the frame the context last rendered (one view)."""
+    """Both CPU baselines on the frame the context last rendered (one view, the step's camera and bg)."""
+    from b2ctrain_amd.scenes import camera_gpu
     from oracle import oracle as O
 
     W, H = scene.W, scene.H
-    pr = {k: r.read(k) for k in ("proj0", "proj1", "proj2")}
-    keys = r.read("keys_sorted")
-    tx, ty, T, _ = O.tile_geometry(W, H)
-    tiles = np.arange(T, dtype=np.uint32)
-    ranges = np.stack([np.searchsorted(keys, tiles, "left"), np.searchsorted(keys, tiles, "right")], 1).astype(np.uint32)
-    ranges[ranges[:, 0] == ranges[:, 1]] = 0
-    bn = {"vals_sorted": r.read("vals_sorted"), "tile_ranges": ranges}
-    v_out = r.read("v_out")
+    camd = camera_gpu(scene.cam)
+    gs = 3.0 * W * H
     threads = host_threads()
     O.set_threads(threads)
-    try:
-        t0 = time.perf_counter()
+    try:  # the whole tiled step of the fp32 CPU restatement, stage by stage, from the scene itself
+        t = [time.perf_counter()]
+        pr = O.project(scene, camd)
+        t.append(time.perf_counter())
+        bn = O.bin_(pr, W, H)
+        t.append(time.perf_counter())
         fw = O.raster_fwd(pr, bn, W, H, bg)
-        t1 = time.perf_counter()
-        O.raster_bwd(pr, bn, fw, v_out, W, H, bg, scene.n, inv_gscale=1.0 / (3.0 * W * H))
-        t2 = time.perf_counter()
+        t.append(time.perf_counter())
+        _, v_out = O.photometric(scene, fw["out_rgba"], grad_scale=gs, bg=bg)
+        t.append(time.perf_counter())
+        vs, vf, _ = O.raster_bwd(pr, bn, fw, v_out, W, H, bg, scene.n, inv_gscale=1.0 / gs)
+        t.append(time.perf_counter())
+        O.vjp(scene, camd, vs, vf, pr["tile_count"])
+        t.append(time.perf_counter())
     finally:
         O.set_threads(1)
+    sec = dict(zip(("project", "bin", "forward", "loss", "backward", "vjp"), np.diff(t)))
+    f_sweep_cpu = int(64 * (fw["tile_ranges"][:, 1].astype(np.int64) - fw["tile_ranges"][:, 0]).clip(min=0).sum())
     tiled = {
-        "value": round(f_sweep / (t2 - t0) / 1e9, 4),
+        "value": round(f_sweep_cpu / (sec["forward"] + sec["backward"]) / 1e9, 4),
         "unit": "Gfrag/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"one full frame of the workload (F_sweep={f_sweep}): forward {t1 - t0:.2f} s + backward {t2 - t1:.2f} s "
-                  f"of the fp32 tiled CPU restatement (oracle/b2c_oracle.c) over the GPU's own tile lists, OpenMP over "
-                  f"tiles on {threads} host threads",
+        "sample": f"one full frame of the workload (F_sweep={f_sweep_cpu}, the GPU's {f_sweep}): the whole tiled "
+                  f"step of the fp32 CPU restatement (oracle/b2c_oracle.c) from the scene: projection, binning "
+                  f"and sorts, forward, fused loss, backward, projection VJP; the forward and backward OpenMP over "
+                  f"tiles on {threads} host threads, the other stages on one; value = F_sweep / (forward + "
+                  f"backward) as the GPU's",
+        "stage_seconds": {k: round(v, 3) for k, v in sec.items()},
+        "step_seconds": round(sum(sec.values()), 3),
         **cpu_info(),
     }
     # the reference's CPU algorithm: fp64 brute force, one thread, ~400 pixels spread over the frame
@@ -343,7 +353,7 @@ def main():
         log("bench: CPU baselines (tiled port on all host threads; reference algorithm on a pixel sample)")
         fs0, (f_contrib, out["cpu_baseline"], out["cpu_reference_algorithm"]) = cpu_baseline_frame(
             r, scene, args.mode, bgs[-1], views[0])
-        # composited fragments of that frame, counted by the CPU port over the GPU's own lists, and the rate
+        # composited fragments of that frame, counted by the CPU port (its lists equal the GPU's), and the rate
         # of composited fragments through the forward and backward (F_contrib / (t_fwd + t_bwd), one view)
         out["config"]["F_contrib_view0"] = f_contrib
         if nv == 1:

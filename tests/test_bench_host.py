@@ -1,6 +1,5 @@
-"""bench.py's host-side legs on the CPU: the CPU-baseline leg run end to end over a stand-in for the GPU
-context that serves the oracle's own projection, lists and loss gradient (the buffers the leg reads back from
-the GPU), and the algorithmic byte formulas."""
+"""bench.py's host-side legs on the CPU: the CPU-baseline leg (the whole tiled step of the oracle from the scene)
+run end to end, and the algorithmic byte formulas."""
 import numpy as np
 
 import bench
@@ -34,6 +33,8 @@ def test_cpu_baseline_leg_runs_on_the_oracle():
     f_contrib, tiled, ref = bench.cpu_baselines(ctx, sc, bg, f_sweep)
     assert f_contrib == ctx.fw["f_contrib"] > 0
     assert tiled["value"] > 0 and tiled["kind"] == "port" and tiled["cores"] >= 1
+    assert set(tiled["stage_seconds"]) == {"project", "bin", "forward", "loss", "backward", "vjp"}
+    assert f"F_sweep={f_sweep}," in tiled["sample"]  # the CPU's own lists sweep the GPU's fragment count
     assert ref["value"] > 0 and ref["cores"] == 1
 
 

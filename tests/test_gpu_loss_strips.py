@@ -49,3 +49,47 @@ def test_train_step_loss_accumulators_per_step():
     for a in (a1, a2):
         assert a[0] > 0 and a[1] == 0 and a[2] == a[0] and a[3] == 1
     assert a1[0] != a2[0]  # a different background: a different loss
+
+
+def test_accumulate_loss_entry_points():
+    """accumulate_loss (loss.cu:317,324) through both layers of the C ABI: b2c_accumulate_loss on a context
+    and b2c_hip_accumulate_loss on a device buffer each do a[2] += a[0] + a[1] and a[3] += 1, leaving the other
+    entries, over a running sum of several steps: photometric_loss adds each step's loss into a cleared [0]."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+    sc = S.config2(n=5_000)
+    emit("accumulate_loss")
+    r = _native.Renderer(sc)
+    try:
+        start = np.arange(16, dtype=np.float32) * 0.5
+        start[2], start[3] = 0.0, 0.0
+        r.write("loss_accum", start)
+        r.forward()
+        losses = []
+        for step in range(3):
+            acc = r.read("loss_accum").copy()
+            acc[0], acc[1] = 0.0, 0.25 * step  # the trainer clears [0]; a second loss term in [1]
+            r.write("loss_accum", acc)
+            check_rc = r.L.b2c_photometric_loss(r.ctx, r.view, C.byref(r.loss_opts(3.0 * sc.W * sc.H, None)))
+            assert check_rc == 0
+            losses.append(float(r.read("loss_accum")[0]))
+            assert r.L.b2c_accumulate_loss(r.ctx) == 0
+        a = r.read("loss_accum")
+    finally:
+        r.close()
+    want2 = np.float32(0)
+    for step, l in enumerate(losses):
+        want2 = np.float32(want2 + np.float32(np.float32(l) + np.float32(0.25 * step)))
+    assert a[2] == want2 and a[3] == 3.0, (a[:4], want2)
+    assert np.array_equal(a[4:], start[4:])
+    # the launcher on a plain device buffer
+    L = _native.lib()
+    L.b2c_hip_accumulate_loss.argtypes = [C.c_void_p, C.c_void_p]
+    buf = torch.tensor([1.5, 2.25, 10.0, 4.0] + [9.0] * 12, dtype=torch.float32, device="cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    assert L.b2c_hip_accumulate_loss(C.c_void_p(buf.data_ptr()), C.c_void_p(stream)) == 0
+    torch.cuda.synchronize()
+    got = buf.cpu().numpy()
+    assert list(got[:4]) == [1.5, 2.25, 13.75, 5.0] and (got[4:] == 9.0).all()
