@@ -74,7 +74,7 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   depth_keys.reserve(nn); depth_keys_sorted.reserve(nn); order_in.reserve(nn); order.reserve(nn);
   depth_alt_k.reserve(nn); depth_alt_v.reserve(nn);
   big_list.reserve(nn); big_base.reserve(nn); big_info.reserve(nn); big_chunk.reserve(nn * B2C_BIG_CHUNKS);
-  big_items.reserve(nn * B2C_BIG_CHUNKS);
+  big_items.reserve(nn * B2C_BIG_CHUNKS); big_done.reserve(nn);
   counters.reserve(4);
   if (v_splat.count < nn * GRAD_LANES) {
     v_splat.reserve(nn * GRAD_LANES);
@@ -186,7 +186,8 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   a.big_info = reinterpret_cast<uint32_t*>(ctx.big_info.ptr);
   a.big_chunk = ctx.big_chunk.ptr;
   a.big_items = ctx.big_items.ptr;
-  a.big_items_count = ctx.counters.ptr + 2;
+  a.big_items_count = ctx.counters.ptr + 1;
+  a.big_done = ctx.big_done.ptr;
   a.feat_mode = feat_mode(p);
   a.feat_buffer = p.feat_buffer;
   LAUNCH_CHECK(b2c_hip_project(&a, stream));
@@ -195,10 +196,10 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
 namespace {
 
 // 3. emit in depth order, then a stable sort on the tile id alone keeps each tile's list in depth order;
-// 4. tile ranges. Sized for ctx.isect_cap; the live intersection count is read from counters[1].
+// 4. tile ranges. Sized for ctx.isect_cap; the live intersection count is read from counters[2].
 void emit_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   const uint32_t cap = (uint32_t)ctx.isect_cap;
-  const uint32_t* total_dev = ctx.counters.ptr + 1;
+  const uint32_t* total_dev = ctx.counters.ptr + 2;
   b2c_emit_args e{};
   e.n = m.n; e.order = ctx.order; e.tile_count = ctx.tile_count; e.tile_off = ctx.tile_off;
   e.hit_info = reinterpret_cast<const uint32_t*>(ctx.hit_info.ptr);
@@ -208,7 +209,7 @@ void emit_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   e.keys = ctx.keys; e.vals = ctx.vals;
   e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
   e.big_info = reinterpret_cast<const uint32_t*>(ctx.big_info.ptr); e.big_chunk = ctx.big_chunk;
-  e.big_items = ctx.big_items; e.big_items_count = ctx.counters.ptr + 2;
+  e.big_items = ctx.big_items; e.big_items_count = ctx.counters.ptr + 1;
   LAUNCH_CHECK(b2c_hip_emit(&e, stream));
   // The tile pass carries the emit positions next to the splat ids: the backward writes each (tile, splat)
   // gradient row at its emit position, where a splat's rows are contiguous.
@@ -239,7 +240,7 @@ void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   volatile uint32_t* h_total = ctx.h_count.ptr;
   *h_total = NO_COUNT;  // the previous store into it completed in the previous call
   // the scan's last workgroup stores the total into the pinned word as well (no copy launch)
-  LAUNCH_CHECK(b2c_hip_scan_counts_host(n, ctx.order, ctx.tile_count, ctx.tile_off, ctx.counters.ptr + 1,
+  LAUNCH_CHECK(b2c_hip_scan_counts_host(n, ctx.order, ctx.tile_count, ctx.tile_off, ctx.counters.ptr + 2,
                                         ctx.h_count_dev, ctx.sort_tmp.ptr, ctx.sort_tmp.bytes(), stream));
   HIP_CHECK(hipEventRecord(ctx.count_event, stream));
   // 3-4 are queued before the host has the total: they are sized for the current capacity and read the

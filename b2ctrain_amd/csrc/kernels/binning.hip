@@ -432,9 +432,13 @@ __global__ void __launch_bounds__(256) emit_big_kernel(b2c_emit_args a, const ui
     const uint32_t e = code >> 5, k = code & 31u;
     const uint4 info = reinterpret_cast<const uint4*>(a.big_info)[e];
     const uint32_t i = a.big_list[e];
+    // the chunk's offset in the splat's slots: the hits of the chunks before it (lane j holds chunk j's)
     const uint32_t* chunk = a.big_chunk + (size_t)e * B2C_BIG_CHUNKS;
-    const uint32_t off = chunk[k];
-    const uint32_t off_next = chunk[min(k + 1u, (uint32_t)B2C_BIG_CHUNKS - 1u)];
+    const uint32_t own = chunk[k];
+    uint32_t before = (uint32_t)lane < k ? chunk[lane] : 0u;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) before += __shfl_xor(before, o);  // every lane gets the sum
+    const uint32_t off = before, off_next = before + own;
     const uint32_t cnt = a.tile_count[i];
     const uint32_t base = big_base[i];
     const SplatRecGeom g = splat_rec_geom(a.raster_rec, i);

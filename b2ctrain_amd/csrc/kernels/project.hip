@@ -29,6 +29,19 @@ struct WaveRec {
   uint32_t bw;
 };
 
+// A big splat's entry (bbox origin min_x | min_y << 16, width, area, chunk length): ceil(area / len) chunks
+// of len tiles, len = 64 up to 64 * B2C_BIG_CHUNKS tiles and a multiple of 64 beyond, so no splat has more
+// than B2C_BIG_CHUNKS chunks.
+__device__ __forceinline__ uint4 big_bbox_of(const TileBox& bb) {
+  const uint32_t bw = (uint32_t)(bb.max_x - bb.min_x);
+  const uint32_t area = bw * (uint32_t)(bb.max_y - bb.min_y);
+  const uint32_t per = (area + B2C_BIG_CHUNKS - 1) / B2C_BIG_CHUNKS;
+  const uint32_t len = per <= 64u ? 64u : ((per + 63u) / 64u) * 64u;
+  return make_uint4((uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), bw, area, len);
+}
+
+__device__ __forceinline__ uint32_t big_nchunks(uint4 info) { return (info.z + info.w - 1u) / info.w; }
+
 // FEAT: feature lanes (feat_mode 1 or 2); the plain variant writes zeros there and keeps the registers the
 // pseudo-normal would hold free (one more resident wave per SIMD at SH degree 3).
 template <int DEG, bool HALF, bool FEAT>
@@ -181,25 +194,57 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       if (count == 0u) a.depth_bits[i] = 0xFFFFFFFFu;  // no tiles: sorts last
     }
   }
-  // workgroup-aggregated append of big splats: one device-scope atomic per workgroup (contended atomics
-  // on one address are serialised at the memory side and cost ~10 ns each)
-  __shared__ uint32_t s_wcount[PROJ_BLOCK / 64];
-  __shared__ uint32_t s_base;
+  // Big splats: a big-list entry each (bbox, chunk length) and one work item per chunk of the bbox, both
+  // appended with one device-scope atomic per workgroup (contended atomics on one address are serialised
+  // at the memory side and cost ~10 ns each).
   const uint64_t bm = ballot64(big);
-  const int w = threadIdx.x >> 6;
-  if (lane == 0) s_wcount[w] = popc64(bm);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t tot = 0;
-    for (int k = 0; k < PROJ_BLOCK / 64; k++) {
-      const uint32_t c = s_wcount[k];
-      s_wcount[k] = tot;
-      tot += c;
+  if (__syncthreads_or(big ? 1 : 0)) {  // uniform per workgroup: the barriers below are reached by all or none
+    __shared__ uint32_t s_wcount[PROJ_BLOCK / 64], s_witems[PROJ_BLOCK / 64];
+    __shared__ uint32_t s_base, s_item_base;
+    uint4 info = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t nch = 0;
+    if (big) {
+      info = big_bbox_of(bb);
+      nch = big_nchunks(info);
     }
-    s_base = tot ? atomicAdd(a.big_count, tot) : 0u;
+    uint32_t incl = nch;  // inclusive prefix of the chunk counts across the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t t = __shfl_up(incl, o);
+      if (lane >= o) incl += t;
+    }
+    const int w = threadIdx.x >> 6;
+    if (lane == 63) {
+      s_wcount[w] = popc64(bm);
+      s_witems[w] = incl;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t tot = 0, items = 0;
+      for (int k = 0; k < PROJ_BLOCK / 64; k++) {
+        const uint32_t c = s_wcount[k], it = s_witems[k];
+        s_wcount[k] = tot;
+        s_witems[k] = items;
+        tot += c;
+        items += it;
+      }
+      // both counters in one atomic: a second contended atomic per workgroup on the same cache line costs
+      // as much again (they are serialised at the memory side)
+      const unsigned long long got =
+          atomicAdd(reinterpret_cast<unsigned long long*>(a.big_count), (unsigned long long)tot | ((unsigned long long)items << 32));
+      s_base = (uint32_t)got;
+      s_item_base = (uint32_t)(got >> 32);
+    }
+    __syncthreads();
+    if (big) {
+      const uint32_t e = s_base + s_wcount[w] + mbcnt64(bm);
+      a.big_list[e] = (uint32_t)i;
+      reinterpret_cast<uint4*>(a.big_info)[e] = info;
+      a.big_done[e] = 0ull;
+      const uint32_t first = s_item_base + s_witems[w] + incl - nch;
+      for (uint32_t k = 0; k < nch; k++) a.big_items[first + k] = (e << 5) | k;
+    }
   }
-  __syncthreads();
-  if (big) a.big_list[s_base + s_wcount[w] + mbcnt64(bm)] = (uint32_t)i;
 }
 
 // Big splats (bbox over 64 tiles) are counted in parallel chunks of their row-major bbox order: an entry
@@ -207,66 +252,14 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
 // tiles and longer (a multiple of 64) beyond, so no splat has more than B2C_BIG_CHUNKS chunks. Each chunk
 // is one work item of a flat item list (filled in any order: items are independent), processed by one
 // wave that tests its tiles 64 at a time. A splat spanning thousands of tiles is spread over up to
-// B2C_BIG_CHUNKS waves instead of serialising one. big_setup_kernel records each entry's bbox and chunk
-// length and appends its items, big_count_kernel the per-chunk hits, big_sum_kernel the per-chunk
-// exclusive offsets (used by the emit) and the tile count.
-__device__ __forceinline__ uint4 big_bbox_info(const b2c_project_args& a, uint32_t i) {
-  const SplatRecGeom g = splat_rec_geom(a.raster_rec, i);
-  float ex, ey;
-  extent_from_conic(g.conic, g.power, ex, ey);
-  const TileBox bb = tile_bbox(g.mx, g.my, ex, ey, a.tiles_x, a.tiles_y);
-  const uint32_t bw = (uint32_t)(bb.max_x - bb.min_x);
-  const uint32_t area = bw * (uint32_t)(bb.max_y - bb.min_y);
-  const uint32_t per = (area + B2C_BIG_CHUNKS - 1) / B2C_BIG_CHUNKS;
-  const uint32_t len = per <= 64u ? 64u : ((per + 63u) / 64u) * 64u;
-  return make_uint4((uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), bw, area, len);
-}
+// B2C_BIG_CHUNKS waves instead of serialising one. project_kernel records each entry's bbox and chunk
+// length and appends its items; big_count_kernel counts the per-chunk hits (the emit sums those of the
+// chunks before its own for its offset) and the splat's tile count.
 
-__device__ __forceinline__ uint32_t big_nchunks(uint4 info) { return (info.z + info.w - 1u) / info.w; }
-
-// Grid-stride over the big list (its length is known on the device only): BIG_ENTRY_GRID workgroups.
-constexpr uint32_t BIG_ENTRY_GRID = 256;
-
-__global__ void __launch_bounds__(256) big_setup_kernel(b2c_project_args a) {
-  const uint32_t count = *a.big_count;
-  __shared__ uint32_t s_wsum[4];
-  __shared__ uint32_t s_base;
-  for (uint32_t e0 = blockIdx.x * 256u; e0 < count; e0 += BIG_ENTRY_GRID * 256u) {  // uniform per workgroup
-    const uint32_t e = e0 + threadIdx.x;
-    const bool live = e < count;
-    uint32_t nch = 0;
-    if (live) {
-      const uint4 info = big_bbox_info(a, a.big_list[e]);
-      reinterpret_cast<uint4*>(a.big_info)[e] = info;
-      nch = big_nchunks(info);
-    }
-    // workgroup-aggregated allocation of the items (one device-scope atomic per workgroup and stretch)
-    uint32_t incl = nch;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t t = __shfl_up(incl, o);
-      if (lane_id() >= o) incl += t;
-    }
-    const int w = threadIdx.x >> 6;
-    __syncthreads();  // s_wsum / s_base of the previous stretch are consumed
-    if (lane_id() == 63) s_wsum[w] = incl;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t tot = 0;
-      for (int k = 0; k < 4; k++) {
-        const uint32_t c = s_wsum[k];
-        s_wsum[k] = tot;
-        tot += c;
-      }
-      s_base = tot ? atomicAdd(a.big_items_count, tot) : 0u;
-    }
-    __syncthreads();
-    const uint32_t base = s_base + s_wsum[w] + incl - nch;
-    for (uint32_t k = 0; k < nch; k++) a.big_items[base + k] = (e << 5) | k;
-  }
-}
-
-// Hits of tiles [k * len, min((k + 1) * len, area)) of entry e's bbox, tested 64 at a time.
+// Hits of tiles [k * len, min((k + 1) * len, area)) of entry e's bbox, tested 64 at a time. Each chunk adds
+// 1 << 40 | hits to its entry's word in one relaxed atomic: the chunk whose add sees the other nch - 1
+// chunks already counted holds the entry's total in the returned value and writes the splat's tile count.
+// No chunk reads another's data, so no fence is needed (an agent-scope release writes the L2 back).
 __global__ void __launch_bounds__(256) big_count_kernel(b2c_project_args a) {
   const int lane = lane_id();
   const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
@@ -291,24 +284,16 @@ __global__ void __launch_bounds__(256) big_count_kernel(b2c_project_args a) {
       }
       hits += popc64(ballot64(h));
     }
-    if (lane == 0) a.big_chunk[(size_t)e * B2C_BIG_CHUNKS + k] = hits;
-  }
-}
-
-// Per entry: exclusive offsets of its chunks (in place) and the splat's tile count.
-__global__ void __launch_bounds__(256) big_sum_kernel(b2c_project_args a) {
-  const uint32_t count = *a.big_count;
-  for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < count; e += BIG_ENTRY_GRID * 256u) {
-    const uint32_t nch = big_nchunks(reinterpret_cast<const uint4*>(a.big_info)[e]);
-    uint32_t* c = a.big_chunk + (size_t)e * B2C_BIG_CHUNKS;
-    uint32_t run = 0;
-    for (uint32_t k = 0; k < nch; k++) {
-      const uint32_t h = c[k];
-      c[k] = run;
-      run += h;
+    if (lane == 0) {
+      a.big_chunk[(size_t)e * B2C_BIG_CHUNKS + k] = hits;
+      const unsigned long long before = atomicAdd(reinterpret_cast<unsigned long long*>(a.big_done + e),
+                                                  (1ull << 40) | (unsigned long long)hits);
+      if ((uint32_t)(before >> 40) + 1u == big_nchunks(info)) {
+        const uint32_t total = (uint32_t)(before & ((1ull << 40) - 1ull)) + hits;
+        a.tile_count[i] = total;
+        if (total == 0u) a.depth_bits[i] = 0xFFFFFFFFu;  // no tiles: sorts last
+      }
     }
-    a.tile_count[a.big_list[e]] = run;
-    if (run == 0u) a.depth_bits[a.big_list[e]] = 0xFFFFFFFFu;  // no tiles: sorts last
   }
 }
 
@@ -355,7 +340,10 @@ void launch_project(const b2c_project_args& a, dim3 grid, dim3 block, bool half,
 extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
-  if (!a->big_count || !a->big_list || !a->hit_wide || !a->raster_rec || !a->depth_bits) return (int)hipErrorInvalidValue;
+  if (!a->big_count || !a->big_list || !a->hit_wide || !a->raster_rec || !a->depth_bits || !a->big_info ||
+      !a->big_chunk || !a->big_items || !a->big_done || a->big_items_count != a->big_count + 1 ||
+      (reinterpret_cast<uintptr_t>(a->big_count) & 7u))
+    return (int)hipErrorInvalidValue;
   if (a->feat_mode < 0 || a->feat_mode > 2 || (a->feat_mode == 2 && !a->feat_buffer)) return (int)hipErrorInvalidValue;
   clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);  // one launch for both
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);
@@ -364,10 +352,6 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   else launch_project<false>(*a, grid, block, half, stream);
   const int e = (int)hipGetLastError();
   if (e) return e;
-  if (!a->big_info || !a->big_chunk || !a->big_items || !a->big_items_count) return (int)hipErrorInvalidValue;
-  const dim3 per_entry(min((unsigned)((a->n + 255) / 256), BIG_ENTRY_GRID));
-  big_setup_kernel<<<per_entry, dim3(256), 0, stream>>>(*a);
   big_count_kernel<<<dim3(B2C_BIG_GRID), dim3(256), 0, stream>>>(*a);
-  big_sum_kernel<<<per_entry, dim3(256), 0, stream>>>(*a);
   return (int)hipGetLastError();
 }

@@ -63,11 +63,12 @@ typedef struct b2c_project_args {
                           (c11/2, opacity, power, sign bits of r, g, b), (max(r,0), max(g,0), max(b,0), log2 opacity),
                           (feat.x, feat.y, feat.z, camera depth) */
   uint32_t* big_list;  /* [n] scratch: splats whose bbox exceeds 64 tiles */
-  uint32_t* big_count; /* [1] scratch counter */
+  uint32_t* big_count; /* [2] scratch counters, 8-byte aligned: [0] big-list entries, [1] big work items */
   uint32_t* big_info;  /* [n][4] scratch: per big-list entry, bbox origin, width, area, chunk length */
-  uint32_t* big_chunk; /* [n][B2C_BIG_CHUNKS] scratch: per-chunk exclusive hit offsets of each entry */
+  uint32_t* big_chunk; /* [n][B2C_BIG_CHUNKS] scratch: per-chunk hit counts of each entry */
   uint32_t* big_items; /* [n][B2C_BIG_CHUNKS] scratch: work items (entry << 5 | chunk) */
-  uint32_t* big_items_count; /* [1] scratch counter */
+  uint32_t* big_items_count; /* big_count + 1 (both are bumped in one 64-bit atomic) */
+  uint64_t* big_done;  /* [n] scratch: per big-list entry, chunks counted << 40 | hits so far */
   int feat_mode;       /* FeatureMode (render.h:27): 0 none, 1 normals (the camera-space pseudo-normal: the
                           shortest semi-axis, turned to face the camera), 2 buffer (feat_buffer, clamped) */
   const float* feat_buffer; /* [n][3] when feat_mode = 2 */
