@@ -16,6 +16,8 @@
 #include "b2c_kernels.h"
 #include "device_math.h"
 
+#include <algorithm>
+
 namespace b2c {
 namespace dev {
 namespace {
@@ -81,6 +83,15 @@ __device__ __forceinline__ uint32_t live_count(uint32_t cap, const uint32_t* n_d
   return n < cap ? n : cap;
 }
 
+// Tile of keys this workgroup sorts. Workgroup w runs on XCD w mod 8, so XCD x takes the contiguous tiles
+// [x per, (x + 1) per), per = ceil(nblocks / 8): a histogram row holds one entry per tile, and the entries of
+// neighbouring tiles, which share a cache line, are then written and read within one XCD's L2 instead of
+// as partial lines from eight. The grid has 8 per workgroups; those mapped past nblocks return.
+__device__ __forceinline__ uint32_t sort_tile(uint32_t nblocks) {
+  const uint32_t per = (nblocks + 7u) / 8u;
+  return (blockIdx.x & 7u) * per + (blockIdx.x >> 3);
+}
+
 // Per-tile digit histogram (R = 256 or 512 digits). Thread t loads the KPT consecutive keys [t KPT, t KPT +
 // KPT) of the tile (16-byte loads) and counts runs of one digit in registers, adding each run to the LDS
 // histogram with one atomic: tile keys in emit order come in runs (a splat's tiles along a bbox row), which
@@ -92,10 +103,12 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __
   static_assert(KPT % 4 == 0, "keys are loaded four at a time");
   constexpr uint32_t TILE = SORT_THREADS * KPT;
   __shared__ uint32_t hist[R];
+  const uint32_t tile = sort_tile(nblocks);
+  if (tile >= nblocks) return;
   const uint32_t n = live_count(cap, n_dev);
   for (int t = threadIdx.x; t < R; t += SORT_THREADS) hist[t] = 0;
   __syncthreads();
-  const uint32_t base = blockIdx.x * TILE;
+  const uint32_t base = tile * TILE;
   if (base < n) {  // a tile past the live count (n_dev) reports zeros
     const uint32_t dmask = (1u << bits) - 1u;
     const uint32_t first = base + threadIdx.x * (uint32_t)KPT;
@@ -126,7 +139,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __
     if (run_c) atomicAdd(&hist[run_d], run_c);
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < R; t += SORT_THREADS) block_hist[(size_t)t * nblocks + blockIdx.x] = hist[t];
+  for (int t = threadIdx.x; t < R; t += SORT_THREADS) block_hist[(size_t)t * nblocks + tile] = hist[t];
 }
 
 // One workgroup per digit: exclusive scan of the digit's per-tile counts (each thread a contiguous run of
@@ -165,12 +178,15 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
   __shared__ uint32_t s_key[TILE];
   __shared__ uint32_t s_val[TILE];  // one value array staged at a time (with NV = 2 the second follows the first)
   constexpr int DPT = R / SORT_THREADS;  // digits per thread
-  __shared__ uint32_t s_gbase[R];  // global position of the tile's first key of each digit
-  __shared__ uint32_t s_loff[R];   // local (staging) offset of each digit
+  // global position of the tile's first key of each digit minus its local (staging) offset: staging slot j
+  // of digit d goes to s_gdelta[d] + j
+  __shared__ uint32_t s_gdelta[R];
   __shared__ uint32_t s_wcnt[NWAVES][R];
   __shared__ uint32_t s_wsum[NWAVES];
+  const uint32_t tile = sort_tile(nblocks);
+  if (tile >= nblocks) return;
   const uint32_t n = live_count(cap, n_dev);
-  const uint32_t base = blockIdx.x * TILE;
+  const uint32_t base = tile * TILE;
   if (base >= n) return;
   const uint32_t tile_n = min(TILE, n - base);
   const int w = threadIdx.x >> 6, lane = lane_id();
@@ -185,14 +201,15 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
     val[0][r] = valid ? (vals_in ? vals_in[base + li] : base + li) : 0u;  // no values: sort the positions
     if constexpr (NV > 1) val[1][r] = valid ? vals2_in[base + li] : 0u;
   }
+  uint32_t loff_d[DPT];  // local (staging) offset of each of this thread's digits
   {  // 2. thread t owns digits t DPT .. t DPT + DPT - 1: global base and local offset of each in this tile
     uint32_t tot_d[DPT], mine[DPT], cnt[DPT], tot_sum = 0, cnt_sum = 0;
 #pragma unroll
     for (int j = 0; j < DPT; j++) {
       const uint32_t d = threadIdx.x * DPT + j;
       tot_d[j] = digit_total[d];
-      mine[j] = block_hist[(size_t)d * nblocks + blockIdx.x];
-      const uint32_t next = blockIdx.x + 1 < nblocks ? block_hist[(size_t)d * nblocks + blockIdx.x + 1] : tot_d[j];
+      mine[j] = block_hist[(size_t)d * nblocks + tile];
+      const uint32_t next = tile + 1 < nblocks ? block_hist[(size_t)d * nblocks + tile + 1] : tot_d[j];
       cnt[j] = next - mine[j];
       tot_sum += tot_d[j];
       cnt_sum += cnt[j];
@@ -203,8 +220,8 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
 #pragma unroll
     for (int j = 0; j < DPT; j++) {
       const uint32_t d = threadIdx.x * DPT + j;
-      s_gbase[d] = digit_start + mine[j];
-      s_loff[d] = loff;
+      s_gdelta[d] = digit_start + mine[j] - loff;
+      loff_d[j] = loff;
       digit_start += tot_d[j];
       loff += cnt[j];
 #pragma unroll
@@ -231,7 +248,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
 #pragma unroll
   for (int j = 0; j < DPT; j++) {
     const uint32_t d = threadIdx.x * DPT + j;
-    uint32_t run = s_loff[d];
+    uint32_t run = loff_d[j];
 #pragma unroll
     for (int k = 0; k < NWAVES; k++) {
       const uint32_t c = s_wcnt[k][d];
@@ -254,8 +271,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
   // 6. write out in digit runs
   for (uint32_t j = threadIdx.x; j < tile_n; j += SORT_THREADS) {
     const uint32_t k = s_key[j];
-    const uint32_t d = (k >> shift) & dmask;
-    const uint32_t g = s_gbase[d] + (j - s_loff[d]);
+    const uint32_t g = s_gdelta[(k >> shift) & dmask] + j;
     keys_out[g] = k;
     vals_out[g] = s_val[j];
   }
@@ -266,8 +282,7 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_scatter(
       if (w * CHUNK + (uint32_t)r * 64 + lane < tile_n) s_val[rank[r]] = val[1][r];
     __syncthreads();
     for (uint32_t j = threadIdx.x; j < tile_n; j += SORT_THREADS) {
-      const uint32_t d = (s_key[j] >> shift) & dmask;
-      vals2_out[s_gbase[d] + (j - s_loff[d])] = s_val[j];
+      vals2_out[s_gdelta[(s_key[j] >> shift) & dmask] + j] = s_val[j];
     }
   }
 }
@@ -562,14 +577,15 @@ void sort_pass(const uint32_t* src_k, const uint32_t* src_v, const uint32_t* src
                uint32_t* dv2, uint32_t n, const uint32_t* n_dev, int shift, int bits, uint32_t* block_hist,
                uint32_t* digit_total, hipStream_t stream) {
   const uint32_t nb = sort_blocks(n, KPT);
-  radix_upsweep<KPT, R><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, n, n_dev, shift, bits, block_hist, nb);
+  const dim3 grid(8u * ((nb + 7u) / 8u));  // sort_tile's XCD-contiguous mapping
+  radix_upsweep<KPT, R><<<grid, dim3(SORT_THREADS), 0, stream>>>(src_k, n, n_dev, shift, bits, block_hist, nb);
   radix_scan_digits<<<dim3(R), dim3(SORT_THREADS), 0, stream>>>(block_hist, nb, digit_total);
   if (src_v2)
-    radix_scatter<2, KPT, R><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev,
-                                                                           shift, bits, block_hist, nb, digit_total);
+    radix_scatter<2, KPT, R><<<grid, dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, src_v2, dk, dv, dv2, n, n_dev,
+                                                                       shift, bits, block_hist, nb, digit_total);
   else
-    radix_scatter<1, KPT, R><<<dim3(nb), dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, nullptr, dk, dv, nullptr, n,
-                                                                           n_dev, shift, bits, block_hist, nb, digit_total);
+    radix_scatter<1, KPT, R><<<grid, dim3(SORT_THREADS), 0, stream>>>(src_k, src_v, nullptr, dk, dv, nullptr, n,
+                                                                       n_dev, shift, bits, block_hist, nb, digit_total);
 }
 
 }  // namespace
@@ -582,7 +598,7 @@ extern "C" size_t b2c_radix_sort_temp_bytes(uint32_t n) {
   // the larger of the small-tile 8-bit and the large-tile 9-bit histograms, so the bound is monotone in n
   // whichever tile size and digit width a sort of n picks
   const size_t nb_small = sort_blocks(n > 0 ? n : 1, KPT_SMALL), nb_big = sort_blocks(n > 0 ? n : 1, KPT_BIG);
-  const size_t hist = nb_small * RADIX > nb_big * 2 * RADIX ? nb_small * RADIX : nb_big * 2 * RADIX;
+  const size_t hist = std::max(nb_small * RADIX, nb_big * 2 * RADIX);
   return (hist + 2 * RADIX) * sizeof(uint32_t);
 }
 

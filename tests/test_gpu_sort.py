@@ -1,5 +1,6 @@
 """The radix sort and the count scan called directly through the C ABI (include/b2c_kernels.h), against
-numpy's stable argsort and cumsum on seeded keys: both tile sizes of the sort (4096- and 1024-key tiles),
+numpy's stable argsort and cumsum on seeded keys: every tile size of the sort (2048-, 4096- and 8192-key
+tiles) and digit width (8 and 9 bits),
 partial bit ranges, a device-side live count, heavy digit skew (the culled 0xFFFFFFFF depth keys) and one
 or two value arrays, including the "no values: sort the positions" form the tile pass uses
 (src/gpu/binning.cu:116-118,140-142 sort with cub::DeviceRadixSort::SortPairs, which is stable)."""
@@ -70,6 +71,11 @@ CASES = [  # (n, key generator, begin, end)
     (4_500_000, "tile17", 0, 17),
     (4_194_304, "rand32", 0, 9),
     (4_200_001, "rand32", 3, 29),
+    # the ends of the 2048-key-tile range (2^22 keys and up take 4096-key tiles)
+    (262_144, "dup", 0, 32),
+    (4_194_303, "depth", 0, 32),
+    (500_000, "rand32", 3, 29),
+    (262_143, "depth", 0, 32),
 ]
 
 
@@ -112,6 +118,19 @@ def test_radix_sort_two_values_positions(n):
         assert np.array_equal(g, e)
 
 
+def test_radix_sort_two_values_32_bits():
+    """Positions sorted and a second value array carried over four 8-bit passes."""
+    n = 400_001
+    rng = np.random.default_rng(11)
+    keys = _keys("rand32", n, rng)
+    vals2 = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+    print(f"kv2 32 bits n={n}", flush=True)
+    got = _sort(keys, None, vals2, 0, 32)
+    exp = _expect(keys, None, vals2, 0, 32)
+    for g, e in zip(got, exp):
+        assert np.array_equal(g, e)
+
+
 @pytest.mark.parametrize("n,live", [(6_000_000, 5_100_007), (36_000_000, 34_000_001)])
 def test_radix_sort_two_values_positions_17_bits(n, live):
     """The 4K tile pass: 17-bit keys in a 9-bit and an 8-bit pass, positions and a second value array, a live
@@ -126,7 +145,7 @@ def test_radix_sort_two_values_positions_17_bits(n, live):
         assert np.array_equal(g, e)
 
 
-@pytest.mark.parametrize("cap,live", [(100_000, 70_001), (5_000_000, 4_100_000), (5_000, 0)])
+@pytest.mark.parametrize("cap,live", [(100_000, 70_001), (600_000, 410_001), (5_000_000, 4_100_000), (5_000, 0)])
 def test_radix_sort_device_live_count(cap, live):
     rng = np.random.default_rng(cap)
     keys = _keys("rand32", cap, rng)
