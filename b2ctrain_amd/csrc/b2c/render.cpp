@@ -74,7 +74,7 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   depth_keys.reserve(nn); depth_keys_sorted.reserve(nn); order_in.reserve(nn); order.reserve(nn);
   depth_alt_k.reserve(nn); depth_alt_v.reserve(nn);
   big_list.reserve(nn); big_base.reserve(nn); big_info.reserve(nn); big_chunk.reserve(nn * B2C_BIG_CHUNKS);
-  big_items.reserve(nn * B2C_BIG_CHUNKS); big_done.reserve(nn);
+  big_items.reserve(nn * B2C_BIG_CHUNKS);
   counters.reserve(4);
   if (v_splat.count < nn * GRAD_LANES) {
     v_splat.reserve(nn * GRAD_LANES);
@@ -187,7 +187,6 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   a.big_chunk = ctx.big_chunk.ptr;
   a.big_items = ctx.big_items.ptr;
   a.big_items_count = ctx.counters.ptr + 1;
-  a.big_done = ctx.big_done.ptr;
   a.feat_mode = feat_mode(p);
   a.feat_buffer = p.feat_buffer;
   LAUNCH_CHECK(b2c_hip_project(&a, stream));

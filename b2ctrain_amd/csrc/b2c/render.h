@@ -106,7 +106,6 @@ struct RenderCtx {
   DevBuf<uint32_t> big_list, big_base, counters;  // counters: [0] big splats, [1] big items, [2] intersections
   DevBuf<uint4> big_info;                         // per big-list entry: bbox and chunk length
   DevBuf<uint32_t> big_chunk, big_items;          // per big-list entry and chunk: hit offsets; work items
-  DevBuf<uint64_t> big_done;                      // per big-list entry: chunks counted << 40 | hits
   DevBuf<uint32_t> depth_alt_k, depth_alt_v, isect_alt_k, isect_alt_v, isect_alt_v2;
   // Intersection bookkeeping of the atomic-free backward: slot_sorted[i] = emit position of list entry i
   // (the tile sort sorts positions; a splat's emit positions are contiguous), tile_end[t] = the tile's

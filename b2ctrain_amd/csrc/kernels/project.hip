@@ -1,9 +1,9 @@
 // Projection (replaces src/gpu/project.cu:8-126): one thread per splat, EWA projection, SH colour, the
 // feature lanes (pseudo-normal or a caller's buffer), exact ellipse/8x8-tile test over the splat's tile
 // bounding box. Splats of at most 64 bbox tiles (the reference's limit is 32, a warp's mask) are tested by
-// the wave together, into a 64-bit hit mask; splats with more than 64 bbox tiles are not counted inline
-// (one thread walking hundreds of tiles stalls its whole wave): they are appended to a list and counted in
-// parallel chunks of their bbox, one wave per chunk.
+// the wave together, into a 64-bit hit mask; splats with more than 64 bbox tiles are not counted by their
+// own thread (one thread walking hundreds of tiles stalls its whole wave): they are appended to a list, and
+// the workgroup counts their bboxes in chunks of up to 64 * B2C_BIG_CHUNKS tiles, one wave per chunk.
 #pragma clang fp contract(off)
 #include "b2c_kernels.h"
 #include "device_math.h"
@@ -32,12 +32,15 @@ struct WaveRec {
 // A big splat's entry (bbox origin min_x | min_y << 16, width, area, chunk length): ceil(area / len) chunks
 // of len tiles, len = 64 up to 64 * B2C_BIG_CHUNKS tiles and a multiple of 64 beyond, so no splat has more
 // than B2C_BIG_CHUNKS chunks.
+__device__ __forceinline__ uint32_t big_bbox_of_len(uint32_t area) {
+  const uint32_t per = (area + B2C_BIG_CHUNKS - 1) / B2C_BIG_CHUNKS;
+  return per <= 64u ? 64u : ((per + 63u) / 64u) * 64u;
+}
+
 __device__ __forceinline__ uint4 big_bbox_of(const TileBox& bb) {
   const uint32_t bw = (uint32_t)(bb.max_x - bb.min_x);
   const uint32_t area = bw * (uint32_t)(bb.max_y - bb.min_y);
-  const uint32_t per = (area + B2C_BIG_CHUNKS - 1) / B2C_BIG_CHUNKS;
-  const uint32_t len = per <= 64u ? 64u : ((per + 63u) / 64u) * 64u;
-  return make_uint4((uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), bw, area, len);
+  return make_uint4((uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), bw, area, big_bbox_of_len(area));
 }
 
 __device__ __forceinline__ uint32_t big_nchunks(uint4 info) { return (info.z + info.w - 1u) / info.w; }
@@ -73,6 +76,10 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       if (small) {
         area = (uint32_t)(bw * bh);
         s_rec[threadIdx.x] = WaveRec{pr.px, pr.py, pr.conic.c00, pr.conic.c01, pr.conic.c11, power,
+                                     (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), (uint32_t)bw};
+      } else {  // big: the geometry as the emit reads it back from the raster record (halved diagonal)
+        s_rec[threadIdx.x] = WaveRec{pr.px, pr.py, 2.f * (0.5f * pr.conic.c00), pr.conic.c01,
+                                     2.f * (0.5f * pr.conic.c11), power,
                                      (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), (uint32_t)bw};
       }
       // SH colour at the camera-to-splat direction (project.cu:44-55)
@@ -196,11 +203,14 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
   }
   // Big splats: a big-list entry each (bbox, chunk length) and one work item per chunk of the bbox, both
   // appended with one device-scope atomic per workgroup (contended atomics on one address are serialised
-  // at the memory side and cost ~10 ns each).
+  // at the memory side and cost ~10 ns each). The workgroup then counts the hits of its own big splats'
+  // chunks, one wave per chunk (the emit needs each chunk's count), and writes their tile counts.
   const uint64_t bm = ballot64(big);
   if (__syncthreads_or(big ? 1 : 0)) {  // uniform per workgroup: the barriers below are reached by all or none
     __shared__ uint32_t s_wcount[PROJ_BLOCK / 64], s_witems[PROJ_BLOCK / 64];
-    __shared__ uint32_t s_base, s_item_base;
+    __shared__ uint32_t s_base, s_item_base, s_nbig, s_nitems;
+    // by workgroup-local big index: the thread (its s_rec slot), bbox area, first chunk, hits counted
+    __shared__ uint32_t s_bthread[PROJ_BLOCK], s_barea[PROJ_BLOCK], s_cstart[PROJ_BLOCK], s_btot[PROJ_BLOCK];
     uint4 info = make_uint4(0u, 0u, 0u, 0u);
     uint32_t nch = 0;
     if (big) {
@@ -234,65 +244,59 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
           atomicAdd(reinterpret_cast<unsigned long long*>(a.big_count), (unsigned long long)tot | ((unsigned long long)items << 32));
       s_base = (uint32_t)got;
       s_item_base = (uint32_t)(got >> 32);
+      s_nbig = tot;
+      s_nitems = items;
+    }
+    __syncthreads();
+    uint32_t lb = 0;  // workgroup-local big index
+    if (big) {
+      lb = s_wcount[w] + mbcnt64(bm);
+      const uint32_t e = s_base + lb;
+      a.big_list[e] = (uint32_t)i;
+      reinterpret_cast<uint4*>(a.big_info)[e] = info;
+      const uint32_t first = s_witems[w] + incl - nch;
+      for (uint32_t k = 0; k < nch; k++) a.big_items[s_item_base + first + k] = (e << 5) | k;
+      s_bthread[lb] = threadIdx.x;
+      s_barea[lb] = info.z;
+      s_cstart[lb] = first;
+      s_btot[lb] = 0u;
+    }
+    __syncthreads();
+    // chunk q of the workgroup's chunks goes to wave q mod 4; q is wave-uniform
+    const uint32_t nbig = s_nbig, nitems = s_nitems;
+    for (uint32_t q = (uint32_t)w; q < nitems; q += PROJ_BLOCK / 64) {
+      uint32_t lo = 0, hi = nbig - 1;  // the last local big whose first chunk is <= q
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1u) >> 1;
+        if (s_cstart[mid] <= q) lo = mid; else hi = mid - 1u;
+      }
+      const WaveRec rec = s_rec[s_bthread[lo]];
+      const uint32_t ar = s_barea[lo];
+      const uint32_t len = big_bbox_of_len(ar);
+      const uint32_t k = q - s_cstart[lo];
+      const uint32_t begin = k * len, end = min(begin + len, ar);
+      const int min_x = (int)(rec.origin & 0xFFFFu), min_y = (int)(rec.origin >> 16), rbw = (int)rec.bw;
+      uint32_t hits = 0;
+      for (uint32_t b0 = begin; b0 < end; b0 += 64) {
+        const uint32_t b = b0 + (uint32_t)lane;
+        bool h = false;
+        if (b < end) {
+          const int tx = min_x + (int)(b % (uint32_t)rbw), ty = min_y + (int)(b / (uint32_t)rbw);
+          const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
+          h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, rec.mx, rec.my, Sym2{rec.c00, rec.c01, rec.c11}, rec.power);
+        }
+        hits += popc64(ballot64(h));
+      }
+      if (lane == 0) {
+        a.big_chunk[(size_t)(s_base + lo) * B2C_BIG_CHUNKS + k] = hits;
+        atomicAdd(&s_btot[lo], hits);
+      }
     }
     __syncthreads();
     if (big) {
-      const uint32_t e = s_base + s_wcount[w] + mbcnt64(bm);
-      a.big_list[e] = (uint32_t)i;
-      reinterpret_cast<uint4*>(a.big_info)[e] = info;
-      a.big_done[e] = 0ull;
-      const uint32_t first = s_item_base + s_witems[w] + incl - nch;
-      for (uint32_t k = 0; k < nch; k++) a.big_items[first + k] = (e << 5) | k;
-    }
-  }
-}
-
-// Big splats (bbox over 64 tiles) are counted in parallel chunks of their row-major bbox order: an entry
-// of the big list with area A gets ceil(A / len) chunks of len tiles, len = 64 up to 64 * B2C_BIG_CHUNKS
-// tiles and longer (a multiple of 64) beyond, so no splat has more than B2C_BIG_CHUNKS chunks. Each chunk
-// is one work item of a flat item list (filled in any order: items are independent), processed by one
-// wave that tests its tiles 64 at a time. A splat spanning thousands of tiles is spread over up to
-// B2C_BIG_CHUNKS waves instead of serialising one. project_kernel records each entry's bbox and chunk
-// length and appends its items; big_count_kernel counts the per-chunk hits (the emit sums those of the
-// chunks before its own for its offset) and the splat's tile count.
-
-// Hits of tiles [k * len, min((k + 1) * len, area)) of entry e's bbox, tested 64 at a time. Each chunk adds
-// 1 << 40 | hits to its entry's word in one relaxed atomic: the chunk whose add sees the other nch - 1
-// chunks already counted holds the entry's total in the returned value and writes the splat's tile count.
-// No chunk reads another's data, so no fence is needed (an agent-scope release writes the L2 back).
-__global__ void __launch_bounds__(256) big_count_kernel(b2c_project_args a) {
-  const int lane = lane_id();
-  const uint32_t wave = (blockIdx.x * 256u + threadIdx.x) >> 6;
-  const uint32_t nwaves = (gridDim.x * 256u) >> 6;
-  const uint32_t items = *a.big_items_count;
-  for (uint32_t it = wave; it < items; it += nwaves) {
-    const uint32_t code = a.big_items[it];
-    const uint32_t e = code >> 5, k = code & 31u;
-    const uint4 info = reinterpret_cast<const uint4*>(a.big_info)[e];
-    const uint32_t i = a.big_list[e];
-    const uint32_t begin = k * info.w, end = min(begin + info.w, info.z);
-    const SplatRecGeom g = splat_rec_geom(a.raster_rec, i);
-    const int min_x = (int)(info.x & 0xFFFFu), min_y = (int)(info.x >> 16), bw = (int)info.y;
-    uint32_t hits = 0;
-    for (uint32_t b0 = begin; b0 < end; b0 += 64) {
-      const uint32_t b = b0 + (uint32_t)lane;
-      bool h = false;
-      if (b < end) {
-        const int tx = min_x + (int)(b % (uint32_t)bw), ty = min_y + (int)(b / (uint32_t)bw);
-        const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
-        h = tile_hit(rx, ry, rx + RT_W, ry + RT_W, g.mx, g.my, g.conic, g.power);
-      }
-      hits += popc64(ballot64(h));
-    }
-    if (lane == 0) {
-      a.big_chunk[(size_t)e * B2C_BIG_CHUNKS + k] = hits;
-      const unsigned long long before = atomicAdd(reinterpret_cast<unsigned long long*>(a.big_done + e),
-                                                  (1ull << 40) | (unsigned long long)hits);
-      if ((uint32_t)(before >> 40) + 1u == big_nchunks(info)) {
-        const uint32_t total = (uint32_t)(before & ((1ull << 40) - 1ull)) + hits;
-        a.tile_count[i] = total;
-        if (total == 0u) a.depth_bits[i] = 0xFFFFFFFFu;  // no tiles: sorts last
-      }
+      const uint32_t total = s_btot[lb];
+      a.tile_count[i] = total;
+      if (total == 0u) a.depth_bits[i] = 0xFFFFFFFFu;  // no tiles: sorts last
     }
   }
 }
@@ -341,7 +345,7 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   if (a->n <= 0) return 0;
   if (a->degree < 0 || a->degree > 4) return (int)hipErrorInvalidValue;
   if (!a->big_count || !a->big_list || !a->hit_wide || !a->raster_rec || !a->depth_bits || !a->big_info ||
-      !a->big_chunk || !a->big_items || !a->big_done || a->big_items_count != a->big_count + 1 ||
+      !a->big_chunk || !a->big_items || a->big_items_count != a->big_count + 1 ||
       (reinterpret_cast<uintptr_t>(a->big_count) & 7u))
     return (int)hipErrorInvalidValue;
   if (a->feat_mode < 0 || a->feat_mode > 2 || (a->feat_mode == 2 && !a->feat_buffer)) return (int)hipErrorInvalidValue;
@@ -350,8 +354,5 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
   const bool half = a->degree > 0 && !a->sh.hi32;  // fp16 bands
   if (a->feat_mode) launch_project<true>(*a, grid, block, half, stream);
   else launch_project<false>(*a, grid, block, half, stream);
-  const int e = (int)hipGetLastError();
-  if (e) return e;
-  big_count_kernel<<<dim3(B2C_BIG_GRID), dim3(256), 0, stream>>>(*a);
   return (int)hipGetLastError();
 }

@@ -68,7 +68,6 @@ typedef struct b2c_project_args {
   uint32_t* big_chunk; /* [n][B2C_BIG_CHUNKS] scratch: per-chunk hit counts of each entry */
   uint32_t* big_items; /* [n][B2C_BIG_CHUNKS] scratch: work items (entry << 5 | chunk) */
   uint32_t* big_items_count; /* big_count + 1 (both are bumped in one 64-bit atomic) */
-  uint64_t* big_done;  /* [n] scratch: per big-list entry, chunks counted << 40 | hits so far */
   int feat_mode;       /* FeatureMode (render.h:27): 0 none, 1 normals (the camera-space pseudo-normal: the
                           shortest semi-axis, turned to face the camera), 2 buffer (feat_buffer, clamped) */
   const float* feat_buffer; /* [n][3] when feat_mode = 2 */
