@@ -629,7 +629,10 @@ extern "C" int b2c_hip_radix_sort_kv2(const uint32_t* keys_in, const uint32_t* v
   const uint32_t* src_v2 = vals2_in;
   int shift = begin_bit;
   for (int p = 0; p < passes; p++) {
-    const int want = p < wide ? 9 : 8;
+    // 8-bit passes split the width evenly (13 bits: 7 + 6, not 8 + 5): the first pass's digit runs per
+    // tile are then twice as long, whole cache lines of keys instead of halves
+    const int even = (end_bit - shift + (passes - p) - 1) / (passes - p);
+    const int want = p < wide ? 9 : (even < 8 ? even : 8);
     const int bits = end_bit - shift < want ? end_bit - shift : want;
     // route the passes so that the last one lands in the output buffers
     const bool to_out = ((passes - 1 - p) % 2) == 0;
