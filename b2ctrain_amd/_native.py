@@ -450,6 +450,12 @@ class DeviceArray:
         if not self.ptr:
             raise RuntimeError(self.L.b2c_last_error().decode())
 
+    def download(self, dtype, shape):
+        """The device bytes as a host array (b2c_device_download: a synchronous copy)."""
+        host = np.empty(shape, dtype)
+        check(self.L.b2c_device_download(_ptr(host), self.ptr, host.nbytes), "device_download")
+        return host
+
     def free(self):
         if self.ptr:
             self.L.b2c_device_free(self.ptr)

@@ -36,11 +36,11 @@ __device__ __forceinline__ float gt_effective(uint32_t gp, int c, bool composite
 // one-row LDS buffer for the horizontal pass of the second blur, whose results fill a second register
 // ring; its vertical pass gives the gradient five rows further down. The loop is unrolled by 11 so that
 // the ring slots are static registers.
-// SH + 4 HALO input rows are walked per strip, a multiple of 11 (the ring length). Taller strips repeat
-// fewer halo rows but make fewer, longer waves; the launcher picks SH per image size (see pick_strip_rows).
+// SH + 4 HALO input rows are walked per strip (the unrolled loop runs whole rings of 11 rows and skips the
+// steps past the strip's last row). Taller strips repeat fewer halo rows but make fewer, longer waves; the
+// launcher picks SH per image size and device (see pick_strip_rows).
 constexpr int SW = 54;
-constexpr int SH_CHOICES[] = {35, 46, 57, 79};
-constexpr int SH_MIN = 35;
+constexpr int SH_MIN = 35, SH_MAX = 128;
 
 struct PixelIn {
   float p, g;
@@ -139,10 +139,12 @@ __device__ __forceinline__ StepRaw fetch_step(const b2c_loss_args& a, const Loss
 // Workgroup b runs on XCD b mod 8; each XCD gets a contiguous band of strips, and the three channel waves of
 // a strip are consecutive on their XCD, so the strip's input lines are read from that XCD's L2 three times
 // rather than from memory.
-template <int SH>
-__global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int strips_x, int nstrips) {
-  constexpr int ROWS = SH + 4 * HALO;
-  static_assert(ROWS % 11 == 0, "the row loop is unrolled by the ring length");
+__global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int strips_x, int nstrips, int SH) {
+  // rows walked: SH + 4 HALO rounded up to whole rings; the `extra` rows this adds are walked first, above
+  // the strip's top halo, and only loaded and blurred horizontally (their statistics rows lie outside
+  // every window of the strip, so the ring simply holds them until they are overwritten)
+  const int ROWS = (SH + 4 * HALO + 10) / 11 * 11;
+  const int extra = ROWS - (SH + 4 * HALO);
   __shared__ float s_p[2][64 + 2 * HALO], s_g[2][64 + 2 * HALO];  // one input row (double buffered)
   // the last 11 input rows, unshifted: prediction and effective target, read back 5 rows later as the
   // SSIM row's L1 operands and 10 rows later as the output row's (slot = row mod 11, static when unrolled)
@@ -176,14 +178,15 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int st
   const LossBufs bufs = loss_bufs(a);
   const int xi0 = x0 - 2 * HALO + lane;
   const LaneCols lc{(uint32_t)min(max(xi0, 0), W - 1), (uint32_t)min(xi0 + 64, W - 1), (uint32_t)min(max(xs, 0), W - 1)};
-  StepRaw nxt = fetch_step(a, bufs, lc, c, y0, 0);
+  StepRaw nxt = fetch_step(a, bufs, lc, c, y0, -extra);
   for (int base = 0; base < ROWS; base += 11) {
 #pragma unroll
     for (int j = 0; j < 11; j++) {
-      const int r = base + j;
-      const int buf = r & 1;
+      const int rw = base + j;   // step of the walk (ring slot j, LDS buffer rw & 1)
+      const int r = rw - extra;  // input row y0 - 10 + r
+      const int buf = rw & 1;
       const StepRaw cur = nxt;
-      if (r + 1 < ROWS) nxt = fetch_step(a, bufs, lc, c, y0, r + 1);
+      nxt = fetch_step(a, bufs, lc, c, y0, r + 1);  // clamped rows: in bounds past the strip's end too
       // ---- input row y_in: columns x0 - 10 .. x0 + 63
       const int y_in = y0 - 2 * HALO + r;
       {
@@ -359,38 +362,46 @@ using namespace b2c::dev;
 
 namespace {
 
-// Waves of the photometric kernel that fit on the device at once (per-CU occupancy from the runtime).
-int resident_waves() {
-  static int cached = 0;
-  if (cached) return cached;
+// SIMDs of the device and the waves of the photometric kernel each holds at once (per-CU occupancy from
+// the runtime; every workgroup is one wave).
+struct LossSlots {
+  int simds, per_simd;
+};
+
+LossSlots loss_slots() {
+  static LossSlots cached{0, 0};
+  if (cached.simds) return cached;
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, photometric_kernel<35>, 64, 0) != hipSuccess ||
-      cus <= 0 || per_cu <= 0) {
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, photometric_kernel, 64, 0) != hipSuccess || cus <= 0 ||
+      per_cu < 4) {
     (void)hipGetLastError();
-    return 256 * 12;  // MI355X: 256 CUs, 3 waves of this size per SIMD
+    return LossSlots{256 * 4, 3};  // MI355X: 256 CUs of 4 SIMDs, 3 waves of this size per SIMD
   }
-  cached = cus * per_cu;
+  cached = LossSlots{cus * 4, per_cu / 4};
   return cached;
 }
 
-// Strip height: every wave walks SH + 20 rows, so the kernel takes about (rounds of resident waves) x
-// (rows per walk); pick the height that minimises that product for this image.
-// B2C_LOSS_STRIP_ROWS (one of the SH_CHOICES) overrides the choice, for tests and tuning.
+// Strip height. Every wave walks SH + 20 rows rounded up to whole rings, so the kernel takes about (rounds
+// of resident waves) x (rows walked); pick the height in [SH_MIN, SH_MAX] that minimises it for this image
+// and device, the tallest on ties (fewer waves). The kernel is VALU-bound: at 1080p heights 39 and 46 (one
+// round, 66 rows walked) measured the same, 94.6 and 94.2 us, and 60 (under two waves per SIMD) 96.4 us.
+// B2C_LOSS_STRIP_ROWS (a height in that range) overrides the choice, for tests and tuning.
 int pick_strip_rows(int W, int H) {
   if (const char* env = getenv("B2C_LOSS_STRIP_ROWS")) {
     const int v = atoi(env);
-    for (int sh : SH_CHOICES)
-      if (v == sh) return sh;
+    if (v >= SH_MIN && v <= SH_MAX) return v;
   }
-  const int strips_x = (W + SW - 1) / SW, slots = resident_waves();
+  const LossSlots sl = loss_slots();
+  const long slots = (long)sl.simds * sl.per_simd;
+  const int strips_x = (W + SW - 1) / SW;
   int best = SH_MIN;
   long best_cost = -1;
-  for (int sh : SH_CHOICES) {
+  for (int sh = SH_MIN; sh <= SH_MAX; sh++) {
     const long waves = (long)strips_x * ((H + sh - 1) / sh) * 3;
-    const long cost = ((waves + slots - 1) / slots) * (sh + 4 * HALO);
-    if (best_cost < 0 || cost < best_cost) {
+    const long cost = ((waves + slots - 1) / slots) * ((sh + 4 * HALO + 10) / 11 * 11);
+    if (best_cost < 0 || cost <= best_cost) {
       best_cost = cost;
       best = sh;
     }
@@ -426,12 +437,7 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   const int sh = pick_strip_rows(a->W, a->H);
   const int nstrips = strips_x * ((a->H + sh - 1) / sh);
   const dim3 grid(8 * ((nstrips * 3 + 7) / 8)), block(64);
-  switch (sh) {
-    case 35: photometric_kernel<35><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
-    case 46: photometric_kernel<46><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
-    case 57: photometric_kernel<57><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
-    default: photometric_kernel<79><<<grid, block, 0, stream>>>(*a, strips_x, nstrips); break;
-  }
+  photometric_kernel<<<grid, block, 0, stream>>>(*a, strips_x, nstrips, sh);
   if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum, a->assign,
                                                                  a->running);
   return (int)hipGetLastError();

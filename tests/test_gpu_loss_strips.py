@@ -1,7 +1,8 @@
-"""The fused loss at every strip height the launcher can pick (b2ctrain_amd/csrc/kernels/loss.hip,
+"""The fused loss at strip heights across the range the launcher picks from (b2ctrain_amd/csrc/kernels/loss.hip,
 pick_strip_rows; forced through B2C_LOSS_STRIP_ROWS): loss value and per-pixel gradient against the CPU
 oracle (src/gpu/loss.cu:18-195 restated), on a 1920x1080 frame with per-pixel weights and the elliptic
-mask, so partial last strips and strip seams are all exercised."""
+mask, so partial last strips, strip seams and walks with and without extra rows before the top halo (the
+walk covers whole 11-row rings) are all exercised."""
 import pytest
 
 from b2ctrain_amd import _native
@@ -11,7 +12,7 @@ from tests.gpu_harness import check_loss, emit
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("sh", [35, 46, 57, 79])
+@pytest.mark.parametrize("sh", [35, 39, 46, 60, 79, 128])
 def test_loss_each_strip_height(sh, monkeypatch):
     monkeypatch.setenv("B2C_LOSS_STRIP_ROWS", str(sh))
     sc = S.config3(n=20_000, masked=True)
@@ -58,7 +59,6 @@ def test_accumulate_loss_entry_points():
     import ctypes as C
 
     import numpy as np
-    import torch
     sc = S.config2(n=5_000)
     emit("accumulate_loss")
     r = _native.Renderer(sc)
@@ -84,12 +84,13 @@ def test_accumulate_loss_entry_points():
         want2 = np.float32(want2 + np.float32(np.float32(l) + np.float32(0.25 * step)))
     assert a[2] == want2 and a[3] == 3.0, (a[:4], want2)
     assert np.array_equal(a[4:], start[4:])
-    # the launcher on a plain device buffer
+    # the launcher on a plain device buffer (the library's own allocation, the default stream)
     L = _native.lib()
     L.b2c_hip_accumulate_loss.argtypes = [C.c_void_p, C.c_void_p]
-    buf = torch.tensor([1.5, 2.25, 10.0, 4.0] + [9.0] * 12, dtype=torch.float32, device="cuda:0")
-    stream = torch.cuda.current_stream().cuda_stream
-    assert L.b2c_hip_accumulate_loss(C.c_void_p(buf.data_ptr()), C.c_void_p(stream)) == 0
-    torch.cuda.synchronize()
-    got = buf.cpu().numpy()
+    buf = _native.DeviceArray(np.array([1.5, 2.25, 10.0, 4.0] + [9.0] * 12, np.float32))
+    try:
+        assert L.b2c_hip_accumulate_loss(C.c_void_p(buf.ptr), None) == 0
+        got = buf.download(np.float32, 16)
+    finally:
+        buf.free()
     assert list(got[:4]) == [1.5, 2.25, 13.75, 5.0] and (got[4:] == 9.0).all()

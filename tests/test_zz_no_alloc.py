@@ -1,6 +1,6 @@
 """The allocation-free loss entry point (b2c_hip_photometric_noalloc, include/b2c_kernels.h) against the
 regular one (b2c_hip_photometric with a caller-provided partials workspace), called through the C ABI on
-device buffers from torch: two calls in a row, the second on a smaller image, each bit-identical to the
+device buffers of the library's own (b2c_device_upload, default stream): two calls in a row, the second on a smaller image, each bit-identical to the
 regular entry point in the loss value and every per-pixel gradient, in assign mode (loss stored, running
 sum updated) and in add mode (loss added to loss_accum[0]). The regular entry point runs first on
 each input, then the allocation-free one, so its fixed scratch holds the previous call's partials (stale
@@ -25,44 +25,40 @@ class LossArgs(C.Structure):
 
 
 def _inputs(W, H, seed, weights):
-    import torch
     g = np.random.default_rng(seed)
     P = W * H
     pred = g.random((P, 4), dtype=np.float32)
     gt = g.integers(0, 1 << 32, P, dtype=np.uint64).astype(np.uint32)
-    dev = torch.device("cuda:0")
-    t = dict(pred=torch.from_numpy(pred).to(dev), gt=torch.from_numpy(gt.view(np.int32)).to(dev),
-             v_out=torch.zeros((P, 4), dtype=torch.float32, device=dev),
-             acc=torch.zeros(16, dtype=torch.float32, device=dev))
-    t["w"] = torch.from_numpy(g.integers(85, 256, P).astype(np.uint8)).to(dev) if weights else None
+    t = dict(pred=_native.DeviceArray(pred), gt=_native.DeviceArray(gt))
+    t["w"] = _native.DeviceArray(g.integers(85, 256, P).astype(np.uint8)) if weights else None
     return t
 
 
 def _call(fn, t, W, H, opts, partials, assign):
-    import torch
     a = LossArgs()
-    a.pred, a.gt = t["pred"].data_ptr(), t["gt"].data_ptr()
-    a.weights = t["w"].data_ptr() if t["w"] is not None else None
+    a.pred, a.gt = t["pred"].ptr, t["gt"].ptr
+    a.weights = t["w"].ptr if t["w"] is not None else None
     a.W, a.H = W, H
     a.l1_w, a.ssim_w = 0.8, -0.2
     for k in range(3):
         a.bg[k] = opts["bg"][k]
     a.composite, a.mask, a.alpha_lane = opts["composite"], opts["mask"], opts["alpha_lane"]
     a.match_alpha_weight, a.scale, a.grad_scale = 0.1, opts["scale"], 3.0 * W * H
-    t["v_out"].zero_()
-    t["acc"].fill_(0.25)  # assign mode overwrites [0..3]; add mode adds to [0]
-    a.v_out, a.loss_accum = t["v_out"].data_ptr(), t["acc"].data_ptr()
-    a.partials = partials
-    a.assign, a.running = assign, assign
-    stream = torch.cuda.current_stream().cuda_stream
-    rc = fn(C.byref(a), C.c_void_p(stream))
-    assert rc == 0, f"launcher returned {rc}"
-    torch.cuda.synchronize()
-    return t["v_out"].cpu().numpy().copy(), t["acc"].cpu().numpy().copy()
+    v_out = _native.DeviceArray(np.zeros((W * H, 4), np.float32))
+    acc = _native.DeviceArray(np.full(16, 0.25, np.float32))  # assign mode overwrites [0..3]; add mode adds to [0]
+    try:
+        a.v_out, a.loss_accum = v_out.ptr, acc.ptr
+        a.partials = partials
+        a.assign, a.running = assign, assign
+        rc = fn(C.byref(a), None)  # the default stream; the downloads below wait for it
+        assert rc == 0, f"launcher returned {rc}"
+        return v_out.download(np.float32, (W * H, 4)), acc.download(np.float32, 16)
+    finally:
+        v_out.free()
+        acc.free()
 
 
 def test_noalloc_loss_matches_workspace_loss_twice():
-    import torch
     L = _native.lib()
     L.b2c_hip_photometric.argtypes = [C.c_void_p, C.c_void_p]
     L.b2c_hip_photometric_noalloc.argtypes = [C.c_void_p, C.c_void_p]
@@ -72,9 +68,9 @@ def test_noalloc_loss_matches_workspace_loss_twice():
     for k, (W, H, opts, weights) in enumerate(cases):
         emit(f"no-alloc loss call {k + 1}: {W}x{H}")
         t = _inputs(W, H, 100 + k, weights)
-        ws = torch.empty(int(L.b2c_loss_partials(W, H)), dtype=torch.float32, device="cuda:0")
+        ws = _native.DeviceArray(np.zeros(int(L.b2c_loss_partials(W, H)), np.float32))
         for assign in (1, 0):
-            v_ref, acc_ref = _call(L.b2c_hip_photometric, t, W, H, opts, ws.data_ptr(), assign)
+            v_ref, acc_ref = _call(L.b2c_hip_photometric, t, W, H, opts, ws.ptr, assign)
             v_na, acc_na = _call(L.b2c_hip_photometric_noalloc, t, W, H, opts, None, assign)
             assert acc_ref[0] > (0 if assign else 0.25) and acc_ref[3] == (1 if assign else 0.25)
             assert np.array_equal(acc_na[:4], acc_ref[:4]), (assign, acc_na[:4], acc_ref[:4])
