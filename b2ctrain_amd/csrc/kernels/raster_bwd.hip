@@ -450,8 +450,8 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
 // Per-splat sum of the (tile, splat) rows. In emit order the rows of one splat are one contiguous run and
 // isect_vals[slot] (the emitted splat id) names the run, so this is a segmented reduction over a
 // contiguous array, in two kernels:
-//  * isect_reduce_kernel: one wave per aligned window of RED_WIN = 256 rows, walked as four 64-row
-//    sub-windows (coalesced 48-byte rows; a row without this pass's tag, a pair past its tile's shrunk end,
+//  * isect_reduce_kernel: one wave per aligned window of RED_WIN rows (256, or 1024 with the live-row
+//    index), walked as 64-row sub-windows (coalesced 48-byte rows; a row without this pass's tag, a pair past its tile's shrunk end,
 //    counts as zero), each a segmented inclusive scan across lanes on DPP row shifts and row broadcasts;
 //    the sums of a run that continues into the next sub-window are carried in
 //    registers. A run that starts and ends inside the window is finished there: its last lane adds the
@@ -471,8 +471,14 @@ constexpr int RED_VALS = FEAT ? 14 : 11;
 template <bool FEAT>
 constexpr int PART_Q = FEAT ? 4 : 3;
 constexpr uint32_t W_CONT_BEFORE = 1u, W_CONT_AFTER = 2u, W_HAS_HEAD = 4u;
-constexpr int RED_SUB = 4;                  // 64-row sub-windows per reduce wave
-constexpr uint32_t RED_WIN = 64u * RED_SUB;  // rows per window (one wave)
+// 64-row sub-windows per reduce wave (one window): 4 when every row is read, 16 with the live-row index,
+// where most rows are skipped and longer windows leave fewer runs to the fixup (config 4: reduce 4.84 ->
+// 4.22 ms per 8-view step, config 5: 0.303 -> 0.281 ms; with every row read, 16 measured 127.6 against
+// 124.6 us at config 3).
+template <bool LIVE>
+constexpr int RED_SUB = LIVE ? 16 : 4;
+template <bool LIVE>
+constexpr uint32_t RED_WIN = 64u * RED_SUB<LIVE>;  // rows per window (one wave)
 
 
 template <bool FEAT>
@@ -575,7 +581,8 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
   const uint32_t m = a.num_isect;
   const int lane = threadIdx.x & 63;
   const uint32_t w = blockIdx.x * 4u + (threadIdx.x >> 6);
-  const uint32_t wlo = w * RED_WIN;
+  constexpr uint32_t WIN = RED_WIN<LIVE>;
+  const uint32_t wlo = w * WIN;
   if (wlo >= m) return;
   const uint32_t* ids = a.isect_vals;
   const uint32_t before = wlo == 0 ? NO_RUN : ids[wlo - 1];
@@ -597,7 +604,7 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
     nxt_id = ids[wlo + lane];
     nxt_word = a.row_live[wlo + lane];
   }
-  for (int sub = 0; sub < RED_SUB; sub++) {
+  for (int sub = 0; sub < RED_SUB<LIVE>; sub++) {
     const uint32_t lo = wlo + 64u * (uint32_t)sub;
     if (lo >= m) break;
     const uint32_t s = lo + lane;
@@ -607,7 +614,7 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
       id = nxt_id;  // valid ? ids[s] : NO_RUN
       word = nxt_word;
       const uint32_t s1 = s + 64u;
-      const bool more = sub + 1 < RED_SUB && s1 < m;
+      const bool more = sub + 1 < RED_SUB<LIVE> && s1 < m;
       nxt_id = more ? ids[s1] : NO_RUN;
       nxt_word = more ? a.row_live[s1] : 0u;
     } else {
@@ -651,7 +658,7 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
     const bool first_from_before = cont_before && (sub == 0 ? before != NO_RUN : carry_from_before);
     const bool is_first = lane == first_tail;
     const bool is_last = lane == 63;
-    const bool crosses_window = cont_after && sub == RED_SUB - 1;
+    const bool crosses_window = cont_after && sub == RED_SUB<LIVE> - 1;
     const bool complete = tail && !(is_first && first_from_before);
     // a sub-window without a row of this pass scans to zeros: skip the scan (wave-uniform); a run ending in
     // it then has sums only if it carries some from the previous sub-window
@@ -665,7 +672,7 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
       for (int k = 0; k < RED_VALS; k++) v[k] += carry[k];
     }
     if (complete) finish_run<FEAT>(a, id, v, old);
-    if (is_first && first_from_before && (!cont_after || !last_is_first || sub == RED_SUB - 1))
+    if (is_first && first_from_before && (!cont_after || !last_is_first || sub == RED_SUB<LIVE> - 1))
       store_part<FEAT>(part, v);  // the window's first piece ends here (or spans the whole window)
     // the last run of the sub-window continues: carry it, or leave it for the fixup at the window's edge
     const uint32_t last_head = lo + 63u - (heads ? (uint32_t)__builtin_clzll(heads) : 63u);
@@ -684,7 +691,7 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
     prev_id = id63;
     if (!cont_after) carry_from_before = false;
   }
-  const uint32_t wend = min(wlo + RED_WIN, m);
+  const uint32_t wend = min(wlo + WIN, m);
   const bool window_cont_after = wend < m && ids[wend - 1] == ids[wend];
   if (lane == 0)
     a.isect_part_flags[w] = (window_cont_before && before != NO_RUN ? W_CONT_BEFORE : 0u) |
@@ -698,11 +705,12 @@ __global__ void __launch_bounds__(256) isect_reduce_kernel(b2c_raster_bwd_args a
 // order: one wave step per such run, so no lane walks a long chain alone.
 constexpr uint32_t SHORT_SPAN = 4;
 
-template <bool FEAT>
+template <bool FEAT, bool LIVE>
 __global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) {
   constexpr int RED_VALS = ::b2c::dev::RED_VALS<FEAT>;
   constexpr int PQ = PART_Q<FEAT>;
-  const uint32_t nwin = (a.num_isect + RED_WIN - 1u) / RED_WIN;
+  constexpr uint32_t WIN = RED_WIN<LIVE>;
+  const uint32_t nwin = (a.num_isect + WIN - 1u) / WIN;
   const uint32_t w = blockIdx.x * 64u + threadIdx.x;
   const int lane = threadIdx.x & 63;
   const float4* part = reinterpret_cast<const float4*>(a.isect_part);
@@ -711,7 +719,7 @@ __global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) 
   // load is unconditional, from a clamped window or id, so no branch splits the loads from their waits.
   const uint32_t wc = min(w, nwin - 1u);
   const uint32_t f = a.isect_part_flags[wc];
-  const uint32_t run_ld = a.isect_vals[min(wc * RED_WIN + RED_WIN - 1u, a.num_isect - 1u)];
+  const uint32_t run_ld = a.isect_vals[min(wc * WIN + WIN - 1u, a.num_isect - 1u)];
   const uint32_t head = __float_as_uint(part[(size_t)wc * (2 * PQ) + PQ + 2].w);
   float4 tail[PQ], nxt[SHORT_SPAN][PQ];
 #pragma unroll
@@ -726,7 +734,7 @@ __global__ void __launch_bounds__(64) isect_fixup_kernel(b2c_raster_bwd_args a) 
   float old_s[RED_VALS];
   prefetch_old<FEAT>(a, run_ld, old_s);
   // the run covers emit positions [head, head + tile_count)
-  const uint32_t last_win = owner ? min((head + tc - 1u) / RED_WIN, nwin - 1u) : 0u;
+  const uint32_t last_win = owner ? min((head + tc - 1u) / WIN, nwin - 1u) : 0u;
   const bool short_run = owner && last_win - w <= SHORT_SPAN;
   if (short_run) {
     float v[RED_VALS];
@@ -804,19 +812,28 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
       const int e = (int)hipEventRecord(static_cast<hipEvent_t>(a->split_event), stream);
       if (e) return e;
     }
-    const uint32_t windows = (a->num_isect + RED_WIN - 1u) / RED_WIN;
+    const bool live = a->row_live != nullptr;
+    const uint32_t win = live ? RED_WIN<true> : RED_WIN<false>;
+    const uint32_t windows = (a->num_isect + win - 1u) / win;
     if (windows) {
       if (!a->isect_part || !a->isect_part_flags) return (int)hipErrorInvalidValue;
-      const dim3 rgrid((windows + 3u) / 4u), rblock(256);
-      const bool live = a->row_live != nullptr;
+      const dim3 rgrid((windows + 3u) / 4u), rblock(256), fgrid((windows + 63u) / 64u), fblock(64);
       if (feat) {
-        if (live) isect_reduce_kernel<true, true><<<rgrid, rblock, 0, stream>>>(*a);
-        else isect_reduce_kernel<true, false><<<rgrid, rblock, 0, stream>>>(*a);
-        isect_fixup_kernel<true><<<dim3((windows + 63u) / 64u), dim3(64), 0, stream>>>(*a);
+        if (live) {
+          isect_reduce_kernel<true, true><<<rgrid, rblock, 0, stream>>>(*a);
+          isect_fixup_kernel<true, true><<<fgrid, fblock, 0, stream>>>(*a);
+        } else {
+          isect_reduce_kernel<true, false><<<rgrid, rblock, 0, stream>>>(*a);
+          isect_fixup_kernel<true, false><<<fgrid, fblock, 0, stream>>>(*a);
+        }
       } else {
-        if (live) isect_reduce_kernel<false, true><<<rgrid, rblock, 0, stream>>>(*a);
-        else isect_reduce_kernel<false, false><<<rgrid, rblock, 0, stream>>>(*a);
-        isect_fixup_kernel<false><<<dim3((windows + 63u) / 64u), dim3(64), 0, stream>>>(*a);
+        if (live) {
+          isect_reduce_kernel<false, true><<<rgrid, rblock, 0, stream>>>(*a);
+          isect_fixup_kernel<false, true><<<fgrid, fblock, 0, stream>>>(*a);
+        } else {
+          isect_reduce_kernel<false, false><<<rgrid, rblock, 0, stream>>>(*a);
+          isect_fixup_kernel<false, false><<<fgrid, fblock, 0, stream>>>(*a);
+        }
       }
     }
   }

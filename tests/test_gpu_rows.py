@@ -6,7 +6,9 @@ repeat (at reallocation, when the row layout or the tile bits change, and when t
 
 The MFMA backward's reduce either reads every row's tag from the row itself or, with the live-row index
 (B2C_ROW_LIVE = 1, the context's choice for long lists), reads a 4-byte tag per row from row_live and only the
-rows it marks; the backward tests run both ways, and the two give the same gradients bit for bit.
+rows it marks; the backward tests run both ways. The two modes walk windows of different lengths (256 rows
+when every row is read, 1024 through the index), so a splat's run pieces are summed in different groupings
+and the two agree to float rounding; within one mode every result is reproducible bit for bit.
 
 Checked here: poisoning the whole row buffer with NaN before a pass leaves v_splat and vis_weight bit-identical
 and the evidence finite and equal to rounding (its sums use float atomics), so no row past a shrunk end is
@@ -106,8 +108,13 @@ def test_live_row_index_gives_the_same_gradients(make, monkeypatch):
             got[mode] = _view_grads(r, sc, sc.cam, gs, poison=True)
         finally:
             r.close()
-    for a, b in zip(got["0"], got["1"]):
-        assert np.array_equal(a, b)
+    # v_splat (per gradient lane) and vis_weight: the same sums, grouped differently; vis_flag exactly
+    for a, b in zip(got["0"][:2], got["1"][:2]):
+        a64, b64 = a.astype(np.float64), b.astype(np.float64)
+        scale = np.abs(a64).max(axis=0) + 1e-30
+        err = (np.abs(a64 - b64) / scale).max()
+        assert err <= 1e-5, err
+    assert np.array_equal(got["0"][2], got["1"][2])
     assert (got["1"][2] != 0).sum() > 100
 
 
