@@ -109,8 +109,12 @@ def cpu_info():
     except OSError:
         pass
     model = fields.get("model name", model)
+    # AMD's family numbers name the core generation where the model string does not (virtual machines
+    # often report only "AMD EPYC"): 0x19 Zen 3/4, 0x1A Zen 5
+    uarch = {("AuthenticAMD", "25"): "Zen 3 / Zen 4 (family 19h)",
+             ("AuthenticAMD", "26"): "Zen 5 (family 1Ah: EPYC 9005)"}.get((fields.get("vendor_id"), fields.get("cpu family")))
     return {"cpu_model": model, "cpu_vendor": fields.get("vendor_id"), "cpu_family": fields.get("cpu family"),
-            "cpu_model_id": fields.get("model"), "host_logical_cpus": logical,
+            "cpu_model_id": fields.get("model"), "cpu_microarchitecture": uarch, "host_logical_cpus": logical,
             "host_cpus_usable": len(os.sched_getaffinity(0))}
 
 
