@@ -25,6 +25,8 @@ void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t
   a.sparse = op.sparse ? 1 : 0;
   a.refine_norm = m.refine_norm.ptr;
   a.vis_count = m.vis_count.ptr;
+  a.vis_from_row = ctx.vis_in_rows ? 1 : 0;
+  a.vis_weight = m.vis_weight.ptr;
   if (!op.grad_out) {
     if (op.t < 1) throw std::runtime_error("optimizer_step: the Adam step t must be >= 1");
     if (!(op.beta1 >= 0.f && op.beta1 < 1.f && op.beta2 > 0.f && op.beta2 < 1.f))
@@ -45,8 +47,10 @@ void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t
     b2c_adam_step_constants(&s);
   }
   LAUNCH_CHECK(b2c_hip_vjp(&a, stream));
-  // every row a backward wrote came with its splat's vis_flag, and the VJP cleared those rows
+  // every row a backward wrote came with its splat's vis_flag (or, deferred, its lane-10 weight), and the
+  // VJP cleared those rows
   ctx.v_splat_zero = true;
+  ctx.vis_in_rows = false;
 }
 
 }  // namespace b2c

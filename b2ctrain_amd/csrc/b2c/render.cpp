@@ -81,6 +81,7 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
     v_splat.zero(stream);
     v_splat_zero = true;
     v_splat_foreign = false;
+    vis_in_rows = false;
   }
   if (vis_flag.count < nn) { vis_flag.reserve(nn); vis_flag.zero(stream); }
   tile_ranges.reserve((size_t)n_tiles); tile_end.reserve((size_t)n_tiles + 1);
@@ -295,6 +296,8 @@ namespace {
 // (raster_bwd_tc.cu:208).
 void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, float grad_scale, hipStream_t stream) {
   check_supported(p);
+  if (ctx.vis_in_rows)
+    throw std::logic_error("backward: the previous pass's visibility is still held in v_splat (run the VJP first)");
   b2c_raster_bwd_args a{};
   a.tile_ranges = reinterpret_cast<const uint32_t*>(ctx.tile_ranges.ptr);
   a.vals_sorted = ctx.vals_sorted;
@@ -333,8 +336,10 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   a.hollow_z = p.hollow_z;
   a.hollow_margin = p.hollow_margin;
   a.hollow_lam = p.hollow_lam * grad_scale;
+  a.defer_vis = ctx.defer_vis && mode == 1 && !a.feat && a.v_splat_zero ? 1 : 0;
   LAUNCH_CHECK(b2c_hip_raster_bwd(&a, stream));
   ctx.v_splat_zero = false;
+  ctx.vis_in_rows = a.defer_vis != 0;
 }
 
 }  // namespace

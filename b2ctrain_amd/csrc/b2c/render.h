@@ -98,6 +98,12 @@ struct RenderCtx {
   bool v_splat_foreign = false;
   bool v_splat_shared = false;
   bool v_splat_known_zero() const { return v_splat_zero && !v_splat_foreign && !v_splat_shared; }
+  // defer_vis (set by the fused training step around its backward): a mode-1 backward without feature
+  // lanes that finds v_splat known zero keeps each splat's blend-weight sum in v_splat lane 10 and leaves
+  // vis_flag and Model::vis_weight alone; vis_in_rows records that, until the projection VJP takes the flag
+  // and the weight from that lane.
+  bool defer_vis = false;
+  bool vis_in_rows = false;
   DevBuf<uint32_t> vis_flag;  // [n]
   DevBuf<float4> v_out;       // dL/d(rgba) per pixel
   DevBuf<float4> v_feat;

@@ -336,6 +336,7 @@ int b2c_ctx_write(b2c_ctx* c, const char* field, const void* host, size_t bytes)
     if (name == "v_splat" || name == "vis_flag") {
       c->ctx.v_splat_zero = false;
       c->ctx.v_splat_foreign = true;
+      c->ctx.vis_in_rows = false;  // the caller's rows replace a deferred pass's
     }
   });
 }
@@ -348,6 +349,7 @@ int b2c_ctx_zero(b2c_ctx* c, const char* field) {
     if (std::string(field) == "v_splat") {
       c->ctx.v_splat_zero = true;
       c->ctx.v_splat_foreign = false;
+      c->ctx.vis_in_rows = false;
     }
   });
 }
@@ -902,10 +904,18 @@ int train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opt
     if (!lp.running_sum) LAUNCH_CHECK(b2c_hip_step_loss_sums(c->ctx.loss_accum.ptr, s));
     mark(4);
     c->ctx.bwd_split_event = (times && mode != 0) ? c->ev[7] : nullptr;
-    if (mode == 0)
-      b2c::rasterize_backward(c->ctx, m->m, p, s);
-    else
-      b2c::rasterize_backward_tc(c->ctx, m->m, p, lp.grad_scale, s);
+    {
+      // the VJP below consumes the pass's visibility, so it may stay in v_splat (reset on every exit)
+      struct DeferVis {
+        b2c::RenderCtx& x;
+        ~DeferVis() { x.defer_vis = false; }
+      } scope{c->ctx};
+      c->ctx.defer_vis = true;
+      if (mode == 0)
+        b2c::rasterize_backward(c->ctx, m->m, p, s);
+      else
+        b2c::rasterize_backward_tc(c->ctx, m->m, p, lp.grad_scale, s);
+    }
     c->ctx.bwd_split_event = nullptr;
     mark(5);
     if (!adam) {

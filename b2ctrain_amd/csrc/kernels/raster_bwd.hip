@@ -487,14 +487,16 @@ __device__ __forceinline__ void prefetch_old(const b2c_raster_bwd_args& a, uint3
   const bool zero = a.v_splat_zero != 0;  // uniform
 #pragma unroll
   for (int k = 0; k < 10; k++) old[k] = zero ? 0.f : dst[k];
-  old[10] = a.vis_weight ? a.vis_weight[id] : 0.f;
+  old[10] = (a.vis_weight && !a.defer_vis) ? a.vis_weight[id] : 0.f;
   if constexpr (FEAT) {
 #pragma unroll
     for (int k = 0; k < 3; k++) old[11 + k] = zero ? 0.f : dst[10 + k];
   }
 }
 
-// Adds a finished run's sums to v_splat / vis_weight (previous contents in `old`) and flags the splat.
+// Adds a finished run's sums to v_splat / vis_weight (previous contents in `old`) and flags the splat; with
+// defer_vis (no feature lanes, v_splat known zero) the blend-weight sum goes to v_splat lane 10 instead, for
+// the projection VJP to flag the splat and add it to vis_weight.
 template <bool FEAT>
 __device__ __forceinline__ void finish_run(const b2c_raster_bwd_args& a, uint32_t id, const float (&v)[RED_VALS<FEAT>],
                                            const float (&old)[RED_VALS<FEAT>]) {
@@ -505,6 +507,11 @@ __device__ __forceinline__ void finish_run(const b2c_raster_bwd_args& a, uint32_
   if constexpr (FEAT) {
 #pragma unroll
     for (int k = 0; k < 3; k++) dst[10 + k] = old[11 + k] + v[11 + k];
+  } else {
+    if (a.defer_vis) {  // uniform
+      dst[10] = v[10];
+      return;
+    }
   }
   a.vis_flag[id] = 1u;
   if (a.vis_weight) a.vis_weight[id] = old[10] + v[10];
@@ -787,6 +794,7 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
   const dim3 grid(NUM_XCD * xcd_tiles_per(n_tiles)), block(64);
   const bool feat = a->feat != 0, hollow = a->hollow_z != nullptr && a->hollow_lam != 0.f;
   if (feat && !a->v_feat) return (int)hipErrorInvalidValue;
+  if (a->defer_vis && (a->mode != 1 || feat || !a->v_splat_zero)) return (int)hipErrorInvalidValue;
   if (a->mode == 0) {
     if (feat && !a->proj3) return (int)hipErrorInvalidValue;
     if (feat) {

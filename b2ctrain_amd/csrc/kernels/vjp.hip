@@ -243,10 +243,12 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   // Memory round trip 1: this splat's flag, tile count and statistics, and the block's v_splat rows (one
   // contiguous, 16-byte aligned stretch of VJP_BLOCK * 13 floats), all issued before any is waited for.
   uint32_t vis = 0u, tc = 0u;
-  float vcount = 0.f, rnorm = 0.f;
+  float vcount = 0.f, rnorm = 0.f, vweight = 0.f;
   SplatState pre{};  // the update's per-splat words
+  const bool from_row = a.vis_from_row != 0;  // uniform
   if (in_range) {
-    vis = a.vis_flag[i];
+    if (!from_row) vis = a.vis_flag[i];
+    else if (a.vis_weight) vweight = a.vis_weight[i];
     tc = a.tile_count[i];
     if (a.vis_count) vcount = a.vis_count[i];
     if (a.refine_norm) rnorm = a.refine_norm[i];
@@ -270,11 +272,14 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
       reinterpret_cast<float4*>(s_buf)[j] = reinterpret_cast<const float4*>(vin)[j];
     for (int j = (nin & ~3) + threadIdx.x; j < nin; j += VJP_BLOCK) s_buf[j] = vin[j];
   }
-  s_vis[threadIdx.x] = vis;
   __syncthreads();
+  // a backward run with defer_vis left the blend-weight sum in lane 10 (a feature lane, zero otherwise)
+  const float wsum = from_row && in_range ? s_buf[threadIdx.x * GRAD_LANES + 10] : 0.f;
+  if (from_row) vis = wsum > 0.f ? 1u : 0u;
   float g[GRAD_LANES];
 #pragma unroll
-  for (int k = 0; k < GRAD_LANES; k++) g[k] = vis ? s_buf[threadIdx.x * GRAD_LANES + k] : 0.f;
+  for (int k = 0; k < GRAD_LANES; k++) g[k] = vis && !(from_row && k == 10) ? s_buf[threadIdx.x * GRAD_LANES + k] : 0.f;
+  s_vis[threadIdx.x] = vis;
   __syncthreads();  // s_buf now holds the grad_out rows
   // Update the statistics, then clear the consumed flag and rows (optim.cu:110-121). The loaded words are
   // all used before the clearing loop: its store count is not known at compile time, so a use of an
@@ -285,7 +290,11 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
     const float rn = __builtin_isfinite(g[9]) ? fminf(fmaxf(g[9], 0.f), 1e32f) : 0.f;
     a.refine_norm[i] = fmaxf(rnorm, rn);
   }
-  if (vis) a.vis_flag[i] = 0u;
+  if (from_row) {
+    if (vis && a.vis_weight) a.vis_weight[i] = vweight + wsum;
+  } else if (vis) {
+    a.vis_flag[i] = 0u;
+  }
   for (int j = threadIdx.x; j < rows * GRAD_LANES; j += VJP_BLOCK)
     if (s_vis[j / GRAD_LANES]) a.v_splat[(size_t)i0 * GRAD_LANES + j] = 0.f;
   bool any = false;

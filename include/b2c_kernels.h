@@ -233,6 +233,11 @@ typedef struct b2c_raster_bwd_args {
   const float* hollow_z;      /* [P] or NULL */
   float hollow_margin;
   float hollow_lam;           /* dL / d(penalised weight) per pixel in v_out's units (times grad_scale) */
+  /* No reference counterpart (set by this build's fused training step only): mode 1 without feat, with
+   * v_splat_zero. Each visible splat's blend-weight sum is stored in v_splat lane 10 (a feature lane, unused
+   * without feat) and neither vis_flag nor vis_weight is touched; the projection VJP, run with vis_from_row,
+   * then derives the flag from that lane and adds it to vis_weight (the same sums as a pass without it). */
+  int defer_vis;
 } b2c_raster_bwd_args;
 int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stream);
 
@@ -430,6 +435,10 @@ typedef struct b2c_vjp_args {
   int sparse;                 /* leave the rows of splats without gradient unchanged (optim.cu:148) */
   float* refine_norm;         /* [n] or NULL: max(., clamp(g[9], 0, 1e32)) (optim.cu:175-176) */
   float* vis_count;           /* [n] or NULL: += visible (optim.cu:174) */
+  int vis_from_row;           /* after a backward with defer_vis: a splat is flagged iff its v_splat lane 10
+                                 (the blend-weight sum) is > 0, vis_flag is neither read nor cleared, and the
+                                 lane is added to vis_weight; no reference counterpart */
+  float* vis_weight;          /* [n] or NULL, with vis_from_row */
   b2c_sh_planes sh_out;       /* the SH as written by the update (the arrays of sh) */
   b2c_adam_state adam;
   b2c_adam_step step;

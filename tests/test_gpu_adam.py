@@ -115,9 +115,14 @@ def test_fused_update_matches_oracle(case):
     _run_case(sc, sparse, noise, t0, random_state=t0 > 1)
 
 
+STATS = ("vis_weight", "vis_count", "refine_norm")
+
+
 @pytest.mark.timeout(300)
 def test_train_step_adam_equals_the_staged_update():
-    """b2c_train_step_adam = forward, loss, backward, fused update; and t = 0 advances the model's counter."""
+    """b2c_train_step_adam = forward, loss, backward, fused update, with the same visibility statistics (the
+    fused step passes visibility to the update in the v_splat rows, the staged calls in vis_flag); and t = 0
+    advances the model's counter."""
     sc = S.config2(n=20_000)
     emit(f"adam train_step: {sc.n} splats")
     bg = (0.3, 0.2, 0.1)
@@ -136,8 +141,10 @@ def test_train_step_adam_equals_the_staged_update():
                 else:
                     r.step_adam(opts, bg=bg)
             assert r.adam_t() == 2
-            states.append(r.model_state())
+            st = r.model_state()
+            st.update({k: r.read_model(k) for k in STATS})
+            states.append(st)
         finally:
             r.close()
-    for key in O.ADAM_STATE_KEYS:
+    for key in O.ADAM_STATE_KEYS + STATS:
         assert _same(states[0][key], states[1][key]), key

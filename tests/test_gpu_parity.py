@@ -166,3 +166,44 @@ def test_backward_adds_into_v_splat_unless_it_is_known_zero():
         assert np.array_equal(r.read("v_splat"), one)
     finally:
         r.close()
+
+
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_train_step_equals_the_staged_gradient(accumulate):
+    """b2c_train_step = render, photometric loss, MFMA backward, gradient-mode VJP (trainer.cpp's step order).
+    The fused step carries each splat's visibility from the backward to the VJP in its v_splat row (the
+    blend-weight sum in lane 10) rather than in vis_flag; the staged calls use vis_flag. Over two steps (two
+    backgrounds; with accumulate the second adds into the first's grads) the gradients and the model's
+    vis_weight (from a nonzero start), vis_count and refine_norm agree bit for bit, and both paths leave
+    v_splat and vis_flag all zero."""
+    sc = S.config3(n=20_000)
+    gs = 3.0 * sc.W * sc.H
+    bgs = ((0.3, 0.2, 0.1), (0.1, 0.5, 0.2))
+    emit(f"train step vs staged gradient, accumulate={accumulate}")
+    got = []
+    for staged in (False, True):
+        r = _native.Renderer(sc)
+        try:
+            r.write_model("vis_weight", np.linspace(0.0, 2.0, sc.n, dtype=np.float32))
+            for k, bg in enumerate(bgs):
+                acc = accumulate and k > 0
+                if staged:
+                    r.forward(bg=bg)
+                    r.loss(grad_scale=gs, bg=bg)
+                    r.backward(mode=1, grad_scale=gs, bg=bg)
+                    r.vjp(accumulate=acc, bg=bg)
+                else:
+                    r.step(accumulate=acc, bg=bg)
+            out = {k: r.read(k) for k in ("grads", "v_splat", "vis_flag")}
+            out.update({k: r.read_model(k) for k in ("vis_weight", "vis_count", "refine_norm")})
+            got.append(out)
+        finally:
+            r.close()
+    fused, staged = got
+    for k in ("grads", "vis_weight", "vis_count", "refine_norm"):
+        assert np.array_equal(fused[k], staged[k]), f"{k}: {int((fused[k] != staged[k]).sum())} entries differ"
+    for out in got:
+        assert not out["v_splat"].any() and not out["vis_flag"].any()
+    seen = int((fused["vis_count"] > 0).sum())
+    emit(f"  {seen} splats visible; grads, vis_weight, vis_count and refine_norm identical")
+    assert seen > 1000
