@@ -437,6 +437,8 @@ _FIELD_SPEC = {
     "v_feat": (np.float32, (4,), "P"), "hollow_pen": (np.float32, (), "P"),
     "slot_sorted": (np.uint32, (), "M"), "tile_end": (np.uint32, (), "T1"),
     "isect_rows": (np.float32, (12,), "M"),
+    "cvals": (np.uint32, (), "M"), "cslots": (np.uint32, (), "M"), "clast": (np.uint32, (), "P"),
+    "cend": (np.uint32, (), "T"),
 }
 
 

@@ -87,6 +87,9 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   tile_ranges.reserve((size_t)n_tiles); tile_end.reserve((size_t)n_tiles + 1);
   const size_t npx = (size_t)W * H;
   out_rgba.reserve(npx); out_feat.reserve(npx); last_idx.reserve(npx); v_out.reserve(npx);
+  clast.reserve(npx); cend.reserve((size_t)n_tiles);
+  compact_ok = false;
+  if (const char* e = std::getenv("B2C_COMPACT_LISTS")) compact_lists = std::string(e) != "0";
   hollow_pen.reserve(npx);
   if (v_feat.count < npx) { v_feat.reserve(npx); v_feat.zero(stream); }  // read by a FEAT backward
   loss_accum.reserve(16);
@@ -136,6 +139,8 @@ void RenderCtx::ensure_isect_capacity(size_t m, hipStream_t stream) {
   isect_alt_v2.reserve(ncap, false, stream);
   // rows: 3 float4 (4 with feature lanes); window partials: 2 x 3 float4 (2 x 4)
   slot_sorted.reserve(ncap, false, stream); isect_rows.reserve(ncap * 4, false, stream);
+  cvals.reserve(ncap, false, stream); cslots.reserve(ncap, false, stream);
+  compact_ok = false;
   row_live.reserve(ncap, false, stream);
   isect_part.reserve((ncap / 256 + 1) * 8, false, stream); isect_part_flags.reserve(ncap / 256 + 1, false, stream);
   isect_cap = ncap;
@@ -223,6 +228,7 @@ void emit_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
 }  // namespace
 
 void bin_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
+  ctx.compact_ok = false;
   if (m.n == 0) {  // no lists: every range and list end is empty, so the raster kernels touch no row
     ctx.num_isect = 0;
     ctx.tile_ranges.zero(stream);
@@ -281,7 +287,13 @@ void rasterize_forward(RenderCtx& ctx, const RenderParams& p, hipStream_t stream
   a.hollow_z = p.hollow_z;
   a.hollow_margin = p.hollow_margin;
   a.hollow_pen = ctx.hollow_pen.ptr;
+  const bool compact = p.bwd_info && ctx.compact_lists;
+  if (compact) {
+    a.slot_sorted = ctx.slot_sorted;
+    a.cvals = ctx.cvals; a.cslots = ctx.cslots; a.clast = ctx.clast; a.cend = ctx.cend;
+  }
   LAUNCH_CHECK(b2c_hip_raster_fwd(&a, stream));
+  if (p.bwd_info) ctx.compact_ok = compact;
 }
 
 void render_forward(RenderCtx& ctx, const Model& m, const RenderParams& p, hipStream_t stream) {
@@ -326,6 +338,9 @@ void backward(RenderCtx& ctx, const Model& m, const RenderParams& p, int mode, f
   if (mode == 1 && ctx.num_isect) {
     a.row_tag = ctx.next_row_tag(p.feat != FeatureMode::None ? 16 : 12, stream);
     if (ctx.use_row_live()) a.row_live = ctx.row_live;
+  }
+  if (mode == 1 && ctx.compact_ok) {
+    a.cvals = ctx.cvals; a.cslots = ctx.cslots; a.clast = ctx.clast; a.cend = ctx.cend;
   }
   a.isect_part = reinterpret_cast<float*>(ctx.isect_part.ptr);
   a.isect_part_flags = ctx.isect_part_flags;

@@ -119,6 +119,13 @@ struct RenderCtx {
   // (or the evidence pass's 4-float row), written only for the entries of the shrunk ranges; row_live[slot]
   // = the tag word of a row the backward wrote, when it runs with the live-row index (sparse lists).
   DevBuf<uint32_t> slot_sorted, tile_end;
+  // The forward's compacted lists for the MFMA backward (the entries of each tile that some pixel
+  // composited: ids, emit positions, each pixel's end, each tile's end); compact_ok while they describe the
+  // current lists (set by a forward with bwd_info that wrote them, cleared by the binning). B2C_COMPACT_LISTS=0
+  // in the environment turns them off.
+  DevBuf<uint32_t> cvals, cslots, clast, cend;
+  bool compact_lists = true;
+  bool compact_ok = false;
   DevBuf<float4> isect_rows;
   DevBuf<uint32_t> row_live;
   DevBuf<float4> isect_part;          // per 256-row window: partial sums of runs crossing the window's edges

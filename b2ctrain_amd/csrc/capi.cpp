@@ -156,6 +156,10 @@ Field ctx_field(b2c_ctx* c, const std::string& name) {
       {"big_base", {x.big_base.ptr, n * 4}},
       {"counters", {x.counters.ptr, x.counters.bytes()}},
       {"slot_sorted", {x.slot_sorted.ptr, M * 4}},
+      {"cvals", {x.cvals.ptr, M * 4}},
+      {"cslots", {x.cslots.ptr, M * 4}},
+      {"clast", {x.clast.ptr, P * 4}},
+      {"cend", {x.cend.ptr, (size_t)x.n_tiles * 4}},
       {"tile_end", {x.tile_end.ptr, ((size_t)x.n_tiles + 1) * 4}},
       {"isect_rows", {x.isect_rows.ptr, M * 48}},
       {"depth_keys", {x.depth_keys.ptr, n * 4}},

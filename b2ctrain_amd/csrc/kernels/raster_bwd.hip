@@ -32,7 +32,8 @@ struct PixelState {
 };
 
 template <bool FEAT, bool HOLLOW>
-__device__ __forceinline__ PixelState load_pixel(const b2c_raster_bwd_args& a, int px, int py, uint32_t range_x) {
+__device__ __forceinline__ PixelState load_pixel(const b2c_raster_bwd_args& a, int px, int py, uint32_t range_x,
+                                                 const uint32_t* last_idx) {
   PixelState s;
   s.inside = px < a.W && py < a.H;
   s.pcx = px + 0.5f;
@@ -47,7 +48,7 @@ __device__ __forceinline__ PixelState load_pixel(const b2c_raster_bwd_args& a, i
     const int pix = py * a.W + px;
     final_a = reinterpret_cast<const float4*>(a.out_rgba)[pix].w;
     s.T = reinterpret_cast<const float4*>(a.out_feat)[pix].w;
-    s.last = a.last_idx[pix];
+    s.last = last_idx[pix];
     s.vo = reinterpret_cast<const float4*>(a.v_out)[pix];
     if constexpr (FEAT) s.vf = reinterpret_cast<const float4*>(a.v_feat)[pix];
     if constexpr (HOLLOW) z_ref = a.hollow_z[pix];
@@ -97,7 +98,7 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
   if (range.y <= range.x) return;
   const int lane = threadIdx.x;
   const int px = (tile % a.tiles_x) * RT_W + (lane & 7), py = (tile / a.tiles_x) * RT_W + (lane >> 3);
-  const PixelState ps = load_pixel<FEAT, HOLLOW>(a, px, py, range.x);
+  const PixelState ps = load_pixel<FEAT, HOLLOW>(a, px, py, range.x, a.last_idx);
   const float Wf = (float)a.W, Hf = (float)a.H;
   float T = ps.T;
   float Q = -ps.v_o_w;
@@ -278,15 +279,21 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
-  const uint2 range = reinterpret_cast<const uint2*>(a.tile_ranges)[tile];
+  // with the forward's compacted lists: the entries some pixel composited, the pixels' ends in them
+  const bool compact = a.cvals != nullptr;  // uniform
+  uint2 range = reinterpret_cast<const uint2*>(a.tile_ranges)[tile];
+  if (compact) range.y = a.cend[tile];
+  const uint32_t* list_vals = compact ? a.cvals : a.vals_sorted;
+  const uint32_t* list_slots = compact ? a.cslots : a.slot_sorted;
   const int lane = threadIdx.x;
-  // pairs past the shrunk end never composited: they get no row, and the reduce does not read theirs
+  // pairs past the shrunk end (or left out of the compacted list) never composited: they get no row, and the
+  // reduce does not read theirs
   if (range.y <= range.x) return;
   const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
   const int lx = lane & 7, ly = lane >> 3;
   const int px = tx * RT_W + lx, py = ty * RT_W + ly;
   const float u = lx + 0.5f - RT_W * 0.5f, v = ly + 0.5f - RT_W * 0.5f;
-  PixelState ps = load_pixel<FEAT, HOLLOW>(a, px, py, range.x);
+  PixelState ps = load_pixel<FEAT, HOLLOW>(a, px, py, range.x, compact ? a.clast : a.last_idx);
   // refine: sqrt(W^2 gx^2 + H^2 gy^2) = W sqrt(gx^2 + rho gy^2), W folded into the per-pixel scale
   const float rho = ((float)a.H * (float)a.H) / ((float)a.W * (float)a.W);
   const float r_scale = ps.inv_final_a * R_SCALE * (float)a.W;
@@ -320,8 +327,8 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
     __syncthreads();
     const int ngroups = (count + G - 1) / G;
     if (lane < count) {
-      const uint32_t gid = a.vals_sorted[batch_start + lane];
-      s_slot[lane] = a.slot_sorted[batch_start + lane];
+      const uint32_t gid = list_vals[batch_start + lane];
+      s_slot[lane] = list_slots[batch_start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
       const float4 r1 = rec[1], r2 = rec[2];
       s_g0[lane] = rec[0];
@@ -807,6 +814,7 @@ extern "C" int b2c_hip_raster_bwd(const b2c_raster_bwd_args* a, hipStream_t stre
   } else {
     if (!a->slot_sorted || !a->isect_rows || !a->isect_vals || !a->tile_count || !a->raster_rec)
       return (int)hipErrorInvalidValue;
+    if (a->cvals && (!a->cslots || !a->clast || !a->cend)) return (int)hipErrorInvalidValue;
     if (a->num_isect && (a->row_tag == 0u || (a->row_tag & a->tile_mask) != 0u))
       return (int)hipErrorInvalidValue;
     if (feat) {

@@ -25,7 +25,11 @@ __device__ __forceinline__ float splat_sigma(float4 g0, float4 g1, float pcx, fl
   return frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, pcx, pcy).sigma;
 }
 
-template <bool FEAT, bool HOLLOW>
+// COMPACT: the tile's compacted list for the MFMA backward (the entries some pixel composited). Each lane
+// marks the steps of its quadrant's list where it composited (one bit per step pair, even and odd steps
+// apart); after the batch the marks are OR-ed over the quadrant's 16 lanes, and splat j of the batch is kept
+// when some quadrant listing it composited it at its position in that quadrant's list.
+template <bool FEAT, bool HOLLOW, bool COMPACT>
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   constexpr bool EXT = FEAT || HOLLOW;
   // slot 64 is a null splat (no fragment passes) that pads the shorter quadrant lists
@@ -50,6 +54,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   if constexpr (HOLLOW) href = hollow_ref(inside ? a.hollow_z[py * a.W + px] : __builtin_inff(), a.hollow_margin);
   bool live = inside;
   uint32_t last = range.x;
+  uint32_t clast = range.x, cbase = 0;  // COMPACT: this pixel's end in the compacted list; entries kept so far
   if (lane < 8) s_list[lane >> 1][64 + (lane & 1)] = 64u * 16u;  // read by the last pair's prefetch
   if (lane == 0) {  // power = 0 and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1): fails the cutoff
     s_g0[64] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -66,9 +71,10 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     if (ballot64(live) == 0) break;
     const uint32_t remaining = min(64u, range.y - start);
     __syncthreads();
-    uint32_t qmask = 0;
+    uint32_t qmask = 0, gid = 0, gslot = 0;
     if ((uint32_t)lane < remaining) {
-      const uint32_t gid = a.vals_sorted[start + lane];
+      gid = a.vals_sorted[start + lane];
+      if constexpr (COMPACT) gslot = a.slot_sorted[start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
       const float4 r0 = rec[0], r1 = rec[1], r2 = rec[2];
       s_g0[lane] = r0;
@@ -80,10 +86,12 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     // per-quadrant lists: the lanes with bit qq set, in lane (depth) order, padded with the null splat
     uint32_t n_iter = 0;
     const uint64_t below = (1ull << lane) - 1ull;
+    uint64_t qbal[4];
 #pragma unroll
     for (int qq = 0; qq < 4; qq++) {
       const bool mine = (qmask >> qq) & 1u;
       const uint64_t bal = ballot64(mine);
+      qbal[qq] = bal;
       const uint32_t c = popc64(bal);
       if (mine) s_list[qq][popc64(bal & below)] = (uint32_t)lane * 16u;
       if ((uint32_t)lane >= c) s_list[qq][lane] = 64u * 16u;
@@ -96,6 +104,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     // reloaded with the entry two ahead at the end of its step, while the other step of the pair runs.
     uint32_t last_off = NO_OFF;  // LDS offset of this batch's last contributing splat
     uint32_t off0 = my_list[0], off1 = my_list[1];
+    uint32_t step_even = 0, step_odd = 0;  // COMPACT: bit k = this lane composited at step 2k (2k + 1)
     // One step: 0 <= sigma <= power as one unsigned compare of the bit patterns (every listed splat has
     // power >= +0, since its tile test passed and sigma >= 0 for a positive-definite conic, and sigma is
     // never -0 for one: dx and dy are +0 or nonzero, and with dy = +0 the addend (c dy) dy is +0, with dx =
@@ -104,7 +113,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     // sigma < 0 has its alpha discarded by the select); only a valid fragment can stop a lane. A fragment is
     // composited (vis > 0) exactly when it is valid and does not stop the lane: a valid alpha is at least
     // 1/255 and a live lane's T is above the cutoff.
-#define B2C_COMPOSITE(off, next)                                                                       \
+#define B2C_COMPOSITE(off, next, steps, sbit)                                                          \
   do {                                                                                                 \
     const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + (off));                                \
     const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + (off));                                \
@@ -132,14 +141,42 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     }                                                                                                  \
     T = stop ? T : next_T;                                                                             \
     last_off = (valid & !stop) ? (off) : last_off;                                                     \
+    if constexpr (COMPACT) (steps) = (valid & !stop) ? ((steps) | (sbit)) : (steps);                   \
     (off) = my_list[next];                                                                             \
   } while (0)
     for (uint32_t i = 0; i < n_iter; i += 2) {
-      B2C_COMPOSITE(off0, i + 2);
-      B2C_COMPOSITE(off1, i + 3);
+      const uint32_t sbit = 1u << (i >> 1);
+      B2C_COMPOSITE(off0, i + 2, step_even, sbit);
+      B2C_COMPOSITE(off1, i + 3, step_odd, sbit);
     }
 #undef B2C_COMPOSITE
     if (last_off != NO_OFF) last = start + (last_off >> 4) + 1u;
+    if constexpr (COMPACT) {
+      // the quadrant's marks (a DPP row is a quadrant's 16 lanes), then quadrant qq's from its first lane
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        step_even |= (uint32_t)__shfl_xor((int)step_even, o);
+        step_odd |= (uint32_t)__shfl_xor((int)step_odd, o);
+      }
+      bool kept = false;
+#pragma unroll
+      for (int qq = 0; qq < 4; qq++) {
+        const uint32_t se = (uint32_t)__builtin_amdgcn_readlane((int)step_even, 16 * qq);
+        const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)step_odd, 16 * qq);
+        const uint32_t pos = popc64(qbal[qq] & below);  // this splat's position in quadrant qq's list
+        const uint32_t sm = (pos & 1u) ? so : se;
+        kept = kept | ((((qmask >> qq) & 1u) != 0u) & (((sm >> (pos >> 1)) & 1u) != 0u));
+      }
+      const uint64_t keep = ballot64(kept);
+      if (kept) {
+        const uint32_t c = range.x + cbase + popc64(keep & below);
+        a.cvals[c] = gid;
+        a.cslots[c] = gslot;
+      }
+      // a lane that composited in this batch: its last composited splat is kept
+      if (last_off != NO_OFF) clast = range.x + cbase + popc64(keep & ((1ull << (last_off >> 4)) - 1ull)) + 1u;
+      cbase += popc64(keep);
+    }
   }
   if (inside) {
     const int pix = py * a.W + px;
@@ -147,6 +184,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     reinterpret_cast<float4*>(a.out_feat)[pix] = make_float4(f0, f1, f2, T);
     if constexpr (HOLLOW) a.hollow_pen[pix] = pen;
     if (a.bwd_info) a.last_idx[pix] = last;
+    if constexpr (COMPACT) a.clast[pix] = clast;
   }
   if (a.bwd_info) {
     uint32_t m = last;
@@ -154,6 +192,8 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     for (int o = 32; o >= 1; o >>= 1) m = max(m, (uint32_t)__shfl_xor(m, o));
     if (lane == 0) ranges[tile].y = m;
   }
+  if constexpr (COMPACT)
+    if (lane == 0) a.cend[tile] = range.x + cbase;
 }
 
 }  // namespace
@@ -168,12 +208,18 @@ extern "C" int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stre
   if (!a->raster_rec || (a->hollow_z && !a->hollow_pen)) return (int)hipErrorInvalidValue;
   const dim3 grid(NUM_XCD * xcd_tiles_per(n_tiles)), block(64);
   const bool hollow = a->hollow_z != nullptr;
-  if (a->feat) {
-    if (hollow) raster_fwd_kernel<true, true><<<grid, block, 0, stream>>>(*a);
-    else raster_fwd_kernel<true, false><<<grid, block, 0, stream>>>(*a);
-  } else {
-    if (hollow) raster_fwd_kernel<false, true><<<grid, block, 0, stream>>>(*a);
-    else raster_fwd_kernel<false, false><<<grid, block, 0, stream>>>(*a);
+  const bool compact = a->bwd_info && a->cvals != nullptr;
+  if (compact && (!a->cslots || !a->slot_sorted || !a->clast || !a->cend)) return (int)hipErrorInvalidValue;
+  const int variant = (a->feat ? 4 : 0) | (hollow ? 2 : 0) | (compact ? 1 : 0);
+  switch (variant) {
+    case 0: raster_fwd_kernel<false, false, false><<<grid, block, 0, stream>>>(*a); break;
+    case 1: raster_fwd_kernel<false, false, true><<<grid, block, 0, stream>>>(*a); break;
+    case 2: raster_fwd_kernel<false, true, false><<<grid, block, 0, stream>>>(*a); break;
+    case 3: raster_fwd_kernel<false, true, true><<<grid, block, 0, stream>>>(*a); break;
+    case 4: raster_fwd_kernel<true, false, false><<<grid, block, 0, stream>>>(*a); break;
+    case 5: raster_fwd_kernel<true, false, true><<<grid, block, 0, stream>>>(*a); break;
+    case 6: raster_fwd_kernel<true, true, false><<<grid, block, 0, stream>>>(*a); break;
+    default: raster_fwd_kernel<true, true, true><<<grid, block, 0, stream>>>(*a); break;
   }
   return (int)hipGetLastError();
 }

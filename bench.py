@@ -130,6 +130,13 @@ def f_sweep_of(r):
     return int(64 * (ranges[:, 1] - ranges[:, 0]).clip(min=0).sum())
 
 
+def kept_of(r):
+    """Entries of the forward's compacted lists (the ones some pixel composited), which the MFMA backward
+    walks."""
+    ranges = r.read("tile_ranges").astype(np.int64)
+    return int((r.read("cend").astype(np.int64) - ranges[:, 0]).clip(min=0).sum())
+
+
 def cpu_baseline_frame(r, scene, mode, bg, cam):
     """Both CPU baselines on one frame of the benchmark's own training step: (F_sweep, cpu_baselines(...))."""
     r.step(mode=mode, bg=bg, cam=cam)
@@ -271,11 +278,12 @@ def main():
     mean = {k: float(np.mean([s[k] for s in stages])) for k in stages[0]}
 
     # fragment and intersection counts of one more step, view by view (deterministic lists)
-    f_sweep = m_total = n_ok = 0
+    f_sweep = m_total = n_ok = m_kept = 0
     tile_bits = 0
     for v, cam in enumerate(views):
         r.step(mode=args.mode, bg=bgs[-1], cam=cam, accumulate=v > 0)
         f_sweep += f_sweep_of(r)
+        m_kept += kept_of(r)
         info = r.info()
         m_total += int(info.num_isect)
         tile_bits = int(info.tile_bits)
@@ -284,16 +292,16 @@ def main():
     gfrag = f_sweep / (t_fb * 1e-3) / 1e9
 
     # Roofline of the dominant kernel, the MFMA backward raster (raster_bwd_mfma_kernel), timed alone with
-    # hipEvents on the context's stream. Algorithmic bytes per launch: per composited-range intersection its
-    # list entry, emit position and projected splat (4 + 4 + 48 B) plus its gradient row (48 B, written; the
-    # intersections past the shrunk end get no row); per pixel out_rgba, out_feat, last_idx and v_out (52 B).
-    # MFMA: 8 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
+    # hipEvents on the context's stream. It walks the forward's compacted lists (the shrunk-range entries some
+    # pixel composited). Algorithmic bytes per launch: per walked entry its splat id, emit position and
+    # projected splat (4 + 4 + 48 B) plus its gradient row (48 B, written); per pixel out_rgba, out_feat, its
+    # list end and v_out (52 B). MFMA: 8 v_mfma_f32_16x16x32_f16 (16384 flop each) per group of 8 splats.
     m_shrunk = f_sweep // 64
     nv = len(views)
-    bwd_bytes = 104 * m_shrunk + 52 * W * H * nv
+    bwd_bytes = 104 * m_kept + 52 * W * H * nv
     t_bwd = mean["raster_bwd_ms"] * 1e-3
     bwd_gbs = bwd_bytes / t_bwd / 1e9
-    mfma_tflops = math.ceil(m_shrunk / 8.0) * 8 * 16384 / t_bwd / 1e12
+    mfma_tflops = math.ceil(m_kept / 8.0) * 8 * 16384 / t_bwd / 1e12
     roofline = {
         "kernel": "raster_bwd_mfma_kernel",
         "bound": "valu",
@@ -342,6 +350,7 @@ def main():
             "height": H,
             "isects": m_total,
             "F_sweep": f_sweep,
+            "bwd_entries": m_kept,
             "backward": "mfma" if args.mode == 1 else "fp32",
             "parallelism": "single GPU",
         },

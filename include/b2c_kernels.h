@@ -174,6 +174,15 @@ typedef struct b2c_raster_fwd_args {
   const float* hollow_z;      /* [P] reference surface depth (+inf = none) or NULL */
   float hollow_margin;
   float* hollow_pen;          /* [P] with hollow_z */
+  /* No reference counterpart (read by this build's MFMA backward): with bwd_info and cvals set, the forward
+   * also writes each tile's compacted list, the entries of its range that at least one pixel composited, in
+   * list order: their splat ids to cvals and their emit positions (from slot_sorted) to cslots at
+   * [range.x, cend[tile]), and per pixel clast, one past its last composited entry in that list (range.x when
+   * none). The entries left out have alpha = 0 at every pixel of the tile. */
+  const uint32_t* slot_sorted;
+  uint32_t* cvals, *cslots;   /* [M] */
+  uint32_t* clast;            /* [P] */
+  uint32_t* cend;             /* [n_tiles] */
 } b2c_raster_fwd_args;
 int b2c_hip_raster_fwd(const b2c_raster_fwd_args* a, hipStream_t stream);
 
@@ -233,6 +242,11 @@ typedef struct b2c_raster_bwd_args {
   const float* hollow_z;      /* [P] or NULL */
   float hollow_margin;
   float hollow_lam;           /* dL / d(penalised weight) per pixel in v_out's units (times grad_scale) */
+  /* mode 1, no reference counterpart: when cvals is set, the compacted lists of a forward run with them
+   * (b2c_raster_fwd_args) replace vals_sorted / slot_sorted / last_idx and the range end: tile t walks
+   * [tile_ranges[t].x, cend[t]) of cvals / cslots, each pixel up to its clast. The entries left out
+   * composited nowhere in the tile, so their rows are zero and stay unwritten. */
+  const uint32_t* cvals, *cslots, *clast, *cend;
   /* No reference counterpart (set by this build's fused training step only): mode 1 without feat, with
    * v_splat_zero. Each visible splat's blend-weight sum is stored in v_splat lane 10 (a feature lane, unused
    * without feat) and neither vis_flag nor vis_weight is touched; the projection VJP, run with vis_from_row,
