@@ -27,8 +27,9 @@ __device__ __forceinline__ float splat_sigma(float4 g0, float4 g1, float pcx, fl
 
 // COMPACT: the tile's compacted list for the MFMA backward (the entries some pixel composited). Each lane
 // marks the steps of its quadrant's list where it composited (one bit per step pair, even and odd steps
-// apart); after the batch the marks are OR-ed over the quadrant's 16 lanes, and splat j of the batch is kept
-// when some quadrant listing it composited it at its position in that quadrant's list.
+// apart); after the batch the marks are OR-ed over the quadrant's 16 lanes, each lane flags in LDS the
+// splats at four of its quadrant's list positions that the quadrant composited, and splat j of the batch
+// is kept when some quadrant flagged it.
 template <bool FEAT, bool HOLLOW, bool COMPACT>
 __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   constexpr bool EXT = FEAT || HOLLOW;
@@ -36,6 +37,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   __shared__ float4 s_g0[65], s_g1[65], s_col[65];
   __shared__ float4 s_ext[EXT ? 65 : 1];  // (feature xyz, camera depth)
   __shared__ uint32_t s_list[4][66];  // per quadrant: LDS byte offsets of its splats, in depth order
+  __shared__ uint32_t s_flag[COMPACT ? 65 : 1];  // COMPACT: splat j of the batch was composited (64: the null splat)
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
@@ -56,6 +58,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   uint32_t last = range.x;
   uint32_t clast = range.x, cbase = 0;  // COMPACT: this pixel's end in the compacted list; entries kept so far
   if (lane < 8) s_list[lane >> 1][64 + (lane & 1)] = 64u * 16u;  // read by the last pair's prefetch
+  if constexpr (COMPACT) s_flag[lane] = 0u;
   if (lane == 0) {  // power = 0 and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1): fails the cutoff
     s_g0[64] = make_float4(0.f, 0.f, 0.f, 0.f);
     s_g1[64] = make_float4(1.f, 0.f, 0.f, 0.f);
@@ -86,12 +89,10 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     // per-quadrant lists: the lanes with bit qq set, in lane (depth) order, padded with the null splat
     uint32_t n_iter = 0;
     const uint64_t below = (1ull << lane) - 1ull;
-    uint64_t qbal[4];
 #pragma unroll
     for (int qq = 0; qq < 4; qq++) {
       const bool mine = (qmask >> qq) & 1u;
       const uint64_t bal = ballot64(mine);
-      qbal[qq] = bal;
       const uint32_t c = popc64(bal);
       if (mine) s_list[qq][popc64(bal & below)] = (uint32_t)lane * 16u;
       if ((uint32_t)lane >= c) s_list[qq][lane] = 64u * 16u;
@@ -102,9 +103,12 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     const uint32_t* my_list = s_list[q];
     // The lists are walked in pairs (an odd count runs one null entry more); each offset register is
     // reloaded with the entry two ahead at the end of its step, while the other step of the pair runs.
-    uint32_t last_off = NO_OFF;  // LDS offset of this batch's last contributing splat
     uint32_t off0 = my_list[0], off1 = my_list[1];
-    uint32_t step_even = 0, step_odd = 0;  // COMPACT: bit k = this lane composited at step 2k (2k + 1)
+    // The steps this lane composited, as two shift registers (even and odd steps): each step shifts its
+    // register left and brings in 1 when the lane composited (a select and a shift-or), so after the batch's
+    // n_pairs step pairs bit b stands for pair n_pairs - 1 - b. They give the lane's last composited entry
+    // (and, COMPACT, the kept entries) without a select per step.
+    uint32_t marks_even = 0, marks_odd = 0;
     // One step: 0 <= sigma <= power as one unsigned compare of the bit patterns (every listed splat has
     // power >= +0, since its tile test passed and sigma >= 0 for a positive-definite conic, and sigma is
     // never -0 for one: dx and dy are +0 or nonzero, and with dy = +0 the addend (c dy) dy is +0, with dx =
@@ -113,7 +117,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     // sigma < 0 has its alpha discarded by the select); only a valid fragment can stop a lane. A fragment is
     // composited (vis > 0) exactly when it is valid and does not stop the lane: a valid alpha is at least
     // 1/255 and a live lane's T is above the cutoff.
-#define B2C_COMPOSITE(off, next, steps, sbit)                                                          \
+#define B2C_COMPOSITE(off, next, marks)                                                                \
   do {                                                                                                 \
     const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + (off));                                \
     const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + (off));                                \
@@ -140,33 +144,44 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
       if constexpr (HOLLOW) pen += vis * hollow_h(ext.w, href);                                        \
     }                                                                                                  \
     T = stop ? T : next_T;                                                                             \
-    last_off = (valid & !stop) ? (off) : last_off;                                                     \
-    if constexpr (COMPACT) (steps) = (valid & !stop) ? ((steps) | (sbit)) : (steps);                   \
+    (marks) = ((marks) << 1) | ((valid & !stop) ? 1u : 0u);                                           \
     (off) = my_list[next];                                                                             \
   } while (0)
     for (uint32_t i = 0; i < n_iter; i += 2) {
-      const uint32_t sbit = 1u << (i >> 1);
-      B2C_COMPOSITE(off0, i + 2, step_even, sbit);
-      B2C_COMPOSITE(off1, i + 3, step_odd, sbit);
+      B2C_COMPOSITE(off0, i + 2, marks_even);
+      B2C_COMPOSITE(off1, i + 3, marks_odd);
     }
 #undef B2C_COMPOSITE
-    if (last_off != NO_OFF) last = start + (last_off >> 4) + 1u;
+    const int n_pairs = (int)(n_iter + 1u) >> 1;
+    // this lane's last composited step (the latest pair is the lowest set bit), and its splat's LDS offset
+    uint32_t last_off = NO_OFF;
+    if (marks_even | marks_odd) {
+      const int se = marks_even ? 2 * (n_pairs - 1 - __builtin_ctz(marks_even)) : -2;
+      const int so = marks_odd ? 2 * (n_pairs - 1 - __builtin_ctz(marks_odd)) + 1 : -1;
+      last_off = my_list[max(se, so)];
+      last = start + (last_off >> 4) + 1u;
+    }
     if constexpr (COMPACT) {
-      // the quadrant's marks (a DPP row is a quadrant's 16 lanes), then quadrant qq's from its first lane
+      // the quadrant's marks: OR over its 16 lanes (one DPP row)
+      marks_even |= dpp_u32<0x128, 0xF>(marks_even, 0u);  // row_ror:8, 4, 2, 1
+      marks_odd |= dpp_u32<0x128, 0xF>(marks_odd, 0u);
+      marks_even |= dpp_u32<0x124, 0xF>(marks_even, 0u);
+      marks_odd |= dpp_u32<0x124, 0xF>(marks_odd, 0u);
+      marks_even |= dpp_u32<0x122, 0xF>(marks_even, 0u);
+      marks_odd |= dpp_u32<0x122, 0xF>(marks_odd, 0u);
+      marks_even |= dpp_u32<0x121, 0xF>(marks_even, 0u);
+      marks_odd |= dpp_u32<0x121, 0xF>(marks_odd, 0u);
+      // lane p of quadrant q flags the splats at positions p, p + 16, p + 32, p + 48 of q's list that q
+      // composited (position pos is pair pos / 2, bit n_pairs - 1 - pos / 2; its parity is p's)
+      const uint32_t m = (p & 1) ? marks_odd : marks_even;
 #pragma unroll
-      for (int o = 1; o < 16; o <<= 1) {
-        step_even |= (uint32_t)__shfl_xor((int)step_even, o);
-        step_odd |= (uint32_t)__shfl_xor((int)step_odd, o);
+      for (int j = 0; j < 4; j++) {
+        const int pos = p + 16 * j;
+        if (pos < (int)n_iter && ((m >> ((n_pairs - 1 - (pos >> 1)) & 31)) & 1u)) s_flag[my_list[pos] >> 4] = 1u;
       }
-      bool kept = false;
-#pragma unroll
-      for (int qq = 0; qq < 4; qq++) {
-        const uint32_t se = (uint32_t)__builtin_amdgcn_readlane((int)step_even, 16 * qq);
-        const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)step_odd, 16 * qq);
-        const uint32_t pos = popc64(qbal[qq] & below);  // this splat's position in quadrant qq's list
-        const uint32_t sm = (pos & 1u) ? so : se;
-        kept = kept | ((((qmask >> qq) & 1u) != 0u) & (((sm >> (pos >> 1)) & 1u) != 0u));
-      }
+      __syncthreads();
+      const bool kept = s_flag[lane] != 0u;
+      s_flag[lane] = 0u;  // cleared for the next batch (its flags are written after its lists are built)
       const uint64_t keep = ballot64(kept);
       if (kept) {
         const uint32_t c = range.x + cbase + popc64(keep & below);
