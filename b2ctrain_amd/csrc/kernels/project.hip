@@ -26,8 +26,14 @@ constexpr int PROJ_BLOCK = 256;
 struct WaveRec {
   float mx, my, c00, c01, c11, power;
   uint32_t origin;  // min_x | min_y << 16
-  uint32_t bw;
+  uint32_t bwm;     // bbox width (bits 0-15); a small splat's also (32768 / width + 1) << 16: bit / width =
+                    // (bit * that) >> 15 for every bit < 64 (width <= 64: the error bit / 32768 stays below
+                    // 1 / width)
 };
+
+__device__ __forceinline__ uint32_t pack_small_bw(int bw) {
+  return (uint32_t)bw | ((32768u / (uint32_t)max(bw, 1) + 1u) << 16);  // (an empty bbox has no tests)
+}
 
 // A big splat's entry (bbox origin min_x | min_y << 16, width, area, chunk length): ceil(area / len) chunks
 // of len tiles, len = 64 up to 64 * B2C_BIG_CHUNKS tiles and a multiple of 64 beyond, so no splat has more
@@ -76,7 +82,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       if (small) {
         area = (uint32_t)(bw * bh);
         s_rec[threadIdx.x] = WaveRec{pr.px, pr.py, pr.conic.c00, pr.conic.c01, pr.conic.c11, power,
-                                     (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), (uint32_t)bw};
+                                     (uint32_t)bb.min_x | ((uint32_t)bb.min_y << 16), pack_small_bw(bw)};
       } else {  // big: the geometry as the emit reads it back from the raster record (halved diagonal)
         s_rec[threadIdx.x] = WaveRec{pr.px, pr.py, 2.f * (0.5f * pr.conic.c00), pr.conic.c01,
                                      2.f * (0.5f * pr.conic.c11), power,
@@ -177,8 +183,9 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       const WaveRec rec = s_rec[wbase + owner];
       const uint32_t prev = owner == 0 ? 0u : s_incl[wbase + owner - 1];
       const uint32_t bit = t - prev;
-      const uint32_t row = bit / rec.bw;
-      const int tx = (int)(rec.origin & 0xFFFFu) + (int)(bit - row * rec.bw);
+      const uint32_t bw = rec.bwm & 0xFFFFu;
+      const uint32_t row = (bit * (rec.bwm >> 16)) >> 15;  // bit / bw
+      const int tx = (int)(rec.origin & 0xFFFFu) + (int)(bit - row * bw);
       const int ty = (int)(rec.origin >> 16) + (int)row;
       const float rx = tx * (float)RT_W, ry = ty * (float)RT_W;
       if (tile_hit(rx, ry, rx + RT_W, ry + RT_W, rec.mx, rec.my, Sym2{rec.c00, rec.c01, rec.c11}, rec.power))
@@ -275,7 +282,7 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       const uint32_t len = big_bbox_of_len(ar);
       const uint32_t k = q - s_cstart[lo];
       const uint32_t begin = k * len, end = min(begin + len, ar);
-      const int min_x = (int)(rec.origin & 0xFFFFu), min_y = (int)(rec.origin >> 16), rbw = (int)rec.bw;
+      const int min_x = (int)(rec.origin & 0xFFFFu), min_y = (int)(rec.origin >> 16), rbw = (int)(rec.bwm & 0xFFFFu);
       uint32_t hits = 0;
       for (uint32_t b0 = begin; b0 < end; b0 += 64) {
         const uint32_t b = b0 + (uint32_t)lane;
