@@ -19,7 +19,12 @@ void photometric_loss(RenderCtx& ctx, const ViewGPU& view, const LossParams& lp,
   a.partials = ctx.loss_partials.ptr;
   a.assign = lp.assign_loss ? 1 : 0;
   a.running = lp.running_sum ? 1 : 0;
+  // a sum still pending here belonged to a step that failed before its VJP: this loss replaces it
+  ctx.loss_pending = 0;
+  if (lp.defer_sum) a.defer_sum_count = &ctx.loss_pending;
   LAUNCH_CHECK(b2c_hip_photometric(&a, stream));
+  ctx.loss_pending_assign = a.assign;
+  ctx.loss_pending_running = a.running;
 }
 
 void accumulate_loss(RenderCtx& ctx, hipStream_t stream) { LAUNCH_CHECK(b2c_hip_accumulate_loss(ctx.loss_accum.ptr, stream)); }

@@ -37,6 +37,9 @@ struct LossParams {
   bool running_sum = false;           // with assign_loss: loss_accum[2] = loss_accum[0] + loss_accum[1] and
                                       // loss_accum[3] = 1 in the same launch, which is what the trainer's
                                       // per-step clear of [0..3] followed by accumulate_loss leaves
+  bool defer_sum = false;             // this build: leave the reduction of the per-workgroup partials to the
+                                      // next optimizer_step on the context (ctx.loss_pending), which runs it in
+                                      // the VJP's first workgroup instead of a launch of its own
 };
 
 // Fused L1 + SSIM (+ alpha lane): per-pixel gradient into ctx.v_out, the loss added to ctx.loss_accum[0]

@@ -26,6 +26,13 @@ void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t
   a.refine_norm = m.refine_norm.ptr;
   a.vis_count = m.vis_count.ptr;
   a.vis_from_row = ctx.vis_in_rows ? 1 : 0;
+  if (ctx.loss_pending) {
+    a.loss_partials = ctx.loss_partials.ptr;
+    a.loss_count = ctx.loss_pending;
+    a.loss_assign = ctx.loss_pending_assign;
+    a.loss_running = ctx.loss_pending_running;
+    a.loss_accum = ctx.loss_accum.ptr;
+  }
   a.vis_weight = m.vis_weight.ptr;
   if (!op.grad_out) {
     if (op.t < 1) throw std::runtime_error("optimizer_step: the Adam step t must be >= 1");
@@ -47,6 +54,7 @@ void optimizer_step(RenderCtx& ctx, Model& m, const OptimParams& op, hipStream_t
     b2c_adam_step_constants(&s);
   }
   LAUNCH_CHECK(b2c_hip_vjp(&a, stream));
+  ctx.loss_pending = 0;
   // every row a backward wrote came with its splat's vis_flag (or, deferred, its lane-10 weight), and the
   // VJP cleared those rows
   ctx.v_splat_zero = true;

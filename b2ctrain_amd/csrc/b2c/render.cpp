@@ -75,7 +75,11 @@ void RenderCtx::setup(int w, int h, int n, hipStream_t stream) {
   depth_alt_k.reserve(nn); depth_alt_v.reserve(nn);
   big_list.reserve(nn); big_base.reserve(nn); big_info.reserve(nn); big_chunk.reserve(nn * B2C_BIG_CHUNKS);
   big_items.reserve(nn * B2C_BIG_CHUNKS);
-  counters.reserve(4);
+  if (counters.count < 8) {
+    counters.reserve(8);
+    counters.zero(stream);  // both big-splat counter pairs start at zero
+    big_slot = 0;
+  }
   if (v_splat.count < nn * GRAD_LANES) {
     v_splat.reserve(nn * GRAD_LANES);
     v_splat.zero(stream);
@@ -188,11 +192,13 @@ void project_splats(RenderCtx& ctx, const Model& m, const RenderParams& p, hipSt
   a.hit_wide = reinterpret_cast<uint32_t*>(ctx.hit_wide.ptr);
   a.max_screen = m.max_screen.ptr;
   a.big_list = ctx.big_list.ptr;
-  a.big_count = ctx.counters.ptr;
+  ctx.big_slot ^= 1;  // this projection appends to the pair the previous one cleared, and clears the other
+  a.big_count = ctx.big_counters();
+  a.clear_next = ctx.counters.ptr + 4 * (ctx.big_slot ^ 1);
   a.big_info = reinterpret_cast<uint32_t*>(ctx.big_info.ptr);
   a.big_chunk = ctx.big_chunk.ptr;
   a.big_items = ctx.big_items.ptr;
-  a.big_items_count = ctx.counters.ptr + 1;
+  a.big_items_count = ctx.big_counters() + 1;
   a.feat_mode = feat_mode(p);
   a.feat_buffer = p.feat_buffer;
   LAUNCH_CHECK(b2c_hip_project(&a, stream));
@@ -212,9 +218,9 @@ void emit_and_sort(RenderCtx& ctx, const Model& m, hipStream_t stream) {
   e.raster_rec = reinterpret_cast<const float*>(ctx.raster_rec.ptr);
   e.tiles_x = ctx.tiles_x; e.tiles_y = ctx.tiles_y; e.cap = cap;
   e.keys = ctx.keys; e.vals = ctx.vals;
-  e.big_list = ctx.big_list; e.big_count = ctx.counters.ptr; e.big_base = ctx.big_base;
+  e.big_list = ctx.big_list; e.big_count = ctx.big_counters(); e.big_base = ctx.big_base;
   e.big_info = reinterpret_cast<const uint32_t*>(ctx.big_info.ptr); e.big_chunk = ctx.big_chunk;
-  e.big_items = ctx.big_items; e.big_items_count = ctx.counters.ptr + 1;
+  e.big_items = ctx.big_items; e.big_items_count = ctx.big_counters() + 1;
   LAUNCH_CHECK(b2c_hip_emit(&e, stream));
   // The tile pass carries the emit positions next to the splat ids: the backward writes each (tile, splat)
   // gradient row at its emit position, where a splat's rows are contiguous.

@@ -104,12 +104,20 @@ struct RenderCtx {
   // and the weight from that lane.
   bool defer_vis = false;
   bool vis_in_rows = false;
+  // A photometric loss run with defer_sum leaves its partials unreduced: loss_pending of them (with the
+  // assign / running flags), summed into loss_accum by the next optimizer_step's VJP.
+  int loss_pending = 0;
+  int loss_pending_assign = 0, loss_pending_running = 0;
   DevBuf<uint32_t> vis_flag;  // [n]
   DevBuf<float4> v_out;       // dL/d(rgba) per pixel
   DevBuf<float4> v_feat;
   DevBuf<float> loss_accum;   // [16] scalar accumulators
   // MI355X build scratch: big-splat list, sort ping-pong buffers, sort/scan temporaries, device counters
-  DevBuf<uint32_t> big_list, big_base, counters;  // counters: [0] big splats, [1] big items, [2] intersections
+  // counters: [0] big splats, [1] big items, [2] intersections, [4..5] the second big-splat pair: projections
+  // alternate between [0..1] and [4..5] (big_slot), each clearing the other for the next
+  DevBuf<uint32_t> big_list, big_base, counters;
+  int big_slot = 0;
+  uint32_t* big_counters() const { return counters.ptr + 4 * big_slot; }
   DevBuf<uint4> big_info;                         // per big-list entry: bbox and chunk length
   DevBuf<uint32_t> big_chunk, big_items;          // per big-list entry and chunk: hit offsets; work items
   DevBuf<uint32_t> depth_alt_k, depth_alt_v, isect_alt_k, isect_alt_v, isect_alt_v2;

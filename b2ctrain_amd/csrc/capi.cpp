@@ -902,6 +902,8 @@ int train_step(b2c_ctx* c, b2c_model* m, const b2c_view* v, const b2c_render_opt
     const bool normals_on = p.feat == b2c::FeatureMode::Normals && lp.normal_scale > 0.f && v->view.normals;
     const bool hollow_on = p.hollow_z && p.hollow_lam != 0.f;
     lp.running_sum = !(normals_on || hollow_on);
+    // the VJP below sums the loss's partials (no launch of its own) when nothing reads loss_accum before it
+    lp.defer_sum = lp.running_sum && m->m.n > 0;
     b2c::photometric_loss(c->ctx, v->view, lp, s);
     if (normals_on) b2c::normal_loss(c->ctx, v->view, lp, s);
     if (hollow_on) b2c::hollow_loss(c->ctx, p.hollow_lam, s);

@@ -7,6 +7,7 @@
 #include "b2c_kernels.h"
 #include "device_math.h"
 #include "ssim_common.h"
+#include "loss_sum.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -317,31 +318,11 @@ __global__ void __launch_bounds__(64) photometric_kernel(b2c_loss_args a, int st
   }
 }
 
-// Fixed-order double-precision sum of the per-workgroup partials into loss_accum[0].
-__global__ void __launch_bounds__(1024) reduce_partials_kernel(const float* __restrict__ partials, int count,
-                                                                float* __restrict__ loss_accum, int assign,
-                                                                int running) {
-  __shared__ double s_red[16];
-  double acc = 0.0;
-  for (int i = threadIdx.x; i < count; i += 1024) acc += (double)partials[i];
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
-  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    double t = 0.0;
-    for (int k = 0; k < 16; k++) t += s_red[k];
-    if (assign) {
-      loss_accum[0] = (float)t;
-      loss_accum[1] = 0.f;
-      if (running) {  // the trainer clears [0..3] each step, then accumulate_kernel adds: [2] = [0] + [1], [3] = 1
-        loss_accum[2] = loss_accum[0] + loss_accum[1];
-        loss_accum[3] = 1.f;
-      }
-    } else {
-      loss_accum[0] = (float)((double)loss_accum[0] + t);
-    }
-  }
+// Fixed-order double-precision sum of the per-workgroup partials into loss_accum[0] (one wave).
+__global__ void __launch_bounds__(64) reduce_partials_kernel(const float* __restrict__ partials, int count,
+                                                              float* __restrict__ loss_accum, int assign,
+                                                              int running) {
+  loss_partials_store(partials, count, loss_accum, assign, running);
 }
 
 __global__ void accumulate_kernel(float* acc) {
@@ -438,8 +419,10 @@ extern "C" int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream) {
   const int nstrips = strips_x * ((a->H + sh - 1) / sh);
   const dim3 grid(8 * ((nstrips * 3 + 7) / 8)), block(64);
   photometric_kernel<<<grid, block, 0, stream>>>(*a, strips_x, nstrips, sh);
-  if (a->partials) reduce_partials_kernel<<<1, 1024, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum, a->assign,
-                                                                 a->running);
+  if (a->partials && a->defer_sum_count)
+    *a->defer_sum_count = nstrips * 3;  // the caller reduces them later (loss_partials_store)
+  else if (a->partials)
+    reduce_partials_kernel<<<1, 64, 0, stream>>>(a->partials, nstrips * 3, a->loss_accum, a->assign, a->running);
   return (int)hipGetLastError();
 }
 
@@ -476,6 +459,7 @@ hipError_t device_scratch(float** out) {
 extern "C" int b2c_hip_photometric_noalloc(const b2c_loss_args* a, hipStream_t stream) {
   if (a->W <= 0 || a->H <= 0) return 0;
   if (b2c_loss_partials(a->W, a->H) > (size_t)B2C_LOSS_STATIC_PARTIALS) return (int)hipErrorInvalidValue;
+  if (a->defer_sum_count) return (int)hipErrorInvalidValue;  // its partials must be reduced before the next call
   float* partials = nullptr;
   const hipError_t e = device_scratch(&partials);
   if (e != hipSuccess) return (int)e;

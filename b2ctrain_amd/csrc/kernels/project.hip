@@ -61,6 +61,8 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
   const int i = blockIdx.x * PROJ_BLOCK + threadIdx.x;
   const int lane = lane_id();
   const int wbase = threadIdx.x & ~63;
+  // the pair of counters the next projection appends to (nothing touches it in this one)
+  if (a.clear_next && i == 0) *reinterpret_cast<unsigned long long*>(a.clear_next) = 0ull;
   bool big = false;
   bool small = false;
   uint32_t area = 0;
@@ -356,7 +358,9 @@ extern "C" int b2c_hip_project(const b2c_project_args* a, hipStream_t stream) {
       (reinterpret_cast<uintptr_t>(a->big_count) & 7u))
     return (int)hipErrorInvalidValue;
   if (a->feat_mode < 0 || a->feat_mode > 2 || (a->feat_mode == 2 && !a->feat_buffer)) return (int)hipErrorInvalidValue;
-  clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);  // one launch for both
+  if (a->clear_next && (reinterpret_cast<uintptr_t>(a->clear_next) & 7u)) return (int)hipErrorInvalidValue;
+  // the counters start at zero: cleared by a launch of their own, or (clear_next) by the previous projection
+  if (!a->clear_next) clear_counters_kernel<<<1, 1, 0, stream>>>(a->big_count, a->big_items_count);
   dim3 grid((unsigned)((a->n + PROJ_BLOCK - 1) / PROJ_BLOCK)), block(PROJ_BLOCK);
   const bool half = a->degree > 0 && !a->sh.hi32;  // fp16 bands
   if (a->feat_mode) launch_project<true>(*a, grid, block, half, stream);

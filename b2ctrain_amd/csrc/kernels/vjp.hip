@@ -18,6 +18,7 @@
 #include "device_math.h"
 #include "screen_splat.h"
 #include "adam_math.h"
+#include "loss_sum.h"
 
 namespace b2c {
 namespace dev {
@@ -239,6 +240,9 @@ __global__ void __launch_bounds__(VJP_BLOCK) vjp_kernel(b2c_vjp_args a) {
   const int i0 = blockIdx.x * VJP_BLOCK;
   const int i = i0 + threadIdx.x;
   const int rows = min(VJP_BLOCK, a.n - i0);
+  // a deferred loss reduction, in the first workgroup (one wave)
+  if (a.loss_partials && blockIdx.x == 0)
+    loss_partials_store(a.loss_partials, a.loss_count, a.loss_accum, a.loss_assign, a.loss_running);
   const bool in_range = i < a.n;
   // Memory round trip 1: this splat's flag, tile count and statistics, and the block's v_splat rows (one
   // contiguous, 16-byte aligned stretch of VJP_BLOCK * 13 floats), all issued before any is waited for.
@@ -510,6 +514,8 @@ hipError_t launch_vjp(const b2c_vjp_args& a, hipStream_t stream) {
 }  // namespace
 
 extern "C" int b2c_hip_vjp(const b2c_vjp_args* a, hipStream_t stream) {
+  static_assert(VJP_BLOCK == 64, "the deferred loss sum runs on the first workgroup's one wave");
+  if (a->loss_partials && (!a->loss_accum || a->n <= 0)) return (int)hipErrorInvalidValue;
   if (a->n <= 0) return 0;
   if (a->grad_out) return (int)launch_vjp<false>(*a, stream);
   // the update writes the parameters, their moments and (sparse) last_step; the SH it writes are the ones it reads

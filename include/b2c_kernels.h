@@ -71,6 +71,10 @@ typedef struct b2c_project_args {
   int feat_mode;       /* FeatureMode (render.h:27): 0 none, 1 normals (the camera-space pseudo-normal: the
                           shortest semi-axis, turned to face the camera), 2 buffer (feat_buffer, clamped) */
   const float* feat_buffer; /* [n][3] when feat_mode = 2 */
+  uint32_t* clear_next;     /* No reference counterpart: NULL, or a second pair of counters like big_count
+                               (8-byte aligned) that the next projection will use. When set, big_count and
+                               big_items_count must already be zero (the launcher then queues no clearing
+                               launch) and the kernel zeroes clear_next instead: callers alternate two pairs. */
 } b2c_project_args;
 
 /* At most this many chunks per big splat (one wave each); and the grid (workgroups of 256) that the
@@ -275,6 +279,10 @@ typedef struct b2c_loss_args {
   int running;                /* with assign: also loss_accum[2] += loss_accum[0] + loss_accum[1] and
                                  loss_accum[3] += 1, the accumulate_kernel update (loss.cu:317,324), in the same
                                  launch */
+  int* defer_sum_count;       /* No reference counterpart: NULL, or (with partials) a host int that receives the
+                                 number of partials; the reduction into loss_accum is then not launched, and the
+                                 caller hands it to b2c_hip_vjp (b2c_vjp_args.loss_partials). The allocation-free
+                                 variant rejects it. */
 } b2c_loss_args;
 size_t b2c_loss_partials(int W, int H);
 int b2c_hip_photometric(const b2c_loss_args* a, hipStream_t stream);
@@ -454,6 +462,11 @@ typedef struct b2c_vjp_args {
                                  lane is added to vis_weight; no reference counterpart */
   float* vis_weight;          /* [n] or NULL, with vis_from_row */
   b2c_sh_planes sh_out;       /* the SH as written by the update (the arrays of sh) */
+  /* No reference counterpart: a photometric loss launched with defer_sum_count, reduced into loss_accum by the
+   * first workgroup (the same fixed-order sum and stores as the loss's own reduction launch). NULL = none. */
+  const float* loss_partials;
+  int loss_count, loss_assign, loss_running;
+  float* loss_accum;
   b2c_adam_state adam;
   b2c_adam_step step;
 } b2c_vjp_args;

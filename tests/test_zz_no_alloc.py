@@ -21,7 +21,7 @@ class LossArgs(C.Structure):
                 ("l1_w", C.c_float), ("ssim_w", C.c_float), ("bg", C.c_float * 3), ("composite", C.c_int),
                 ("mask", C.c_int), ("alpha_lane", C.c_int), ("match_alpha_weight", C.c_float), ("scale", C.c_float),
                 ("grad_scale", C.c_float), ("v_out", C.c_void_p), ("loss_accum", C.c_void_p), ("partials", C.c_void_p),
-                ("assign", C.c_int), ("running", C.c_int)]
+                ("assign", C.c_int), ("running", C.c_int), ("defer_sum_count", C.c_void_p)]
 
 
 def _inputs(W, H, seed, weights):
