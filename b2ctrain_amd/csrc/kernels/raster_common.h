@@ -122,26 +122,66 @@ constexpr uint32_t NO_RUN = 0xFFFFFFFFu;  // the run id of a lane outside every 
 
 // One Hillis-Steele step of a segmented inclusive scan across the wave: add the partial of the DPP source
 // lane when it lies in the same run (runs are contiguous, so equal ids at both ends mean no run boundary in
-// between).
-template <int CTRL, int ROW_MASK, int NV>
-__device__ __forceinline__ void seg_scan_step(uint32_t id, float (&v)[NV]) {
-  const bool same = dpp_u32<CTRL, ROW_MASK>(id, NO_RUN) == id;
-#pragma unroll
-  for (int k = 0; k < NV; k++) {
-    const float t = __uint_as_float(dpp_u32<CTRL, ROW_MASK>(__float_as_uint(v[k]), 0u));
-    v[k] = same ? v[k] + t : v[k];
-  }
+// between). Each value takes one v_fmac_f32 whose first operand is read through the DPP shift: v += m * v[src],
+// with m = 1 when the source lane lies in the same run (and, for the row broadcasts, in a row the step
+// feeds) and 0 otherwise; a lane whose source is outside its row or the wave reads 0 (bound_ctrl). Adding
+// m * t with m in {0, 1} rounds exactly as the plain sum does. One asm block holds the step's values in a
+// fixed order, so a value's DPP read comes at least NV - 1 instructions after the previous step wrote it;
+// the leading s_nop gives the two wait states a DPP read needs after a VALU write of its source for the
+// first step.
+#define B2C_FD(i, C) "v_fmac_f32_dpp %" #i ", %" #i ", %[m] " C " row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+#define B2C_FD3(C) B2C_FD(0, C) B2C_FD(1, C) B2C_FD(2, C)
+#define B2C_FD11(C) \
+  B2C_FD3(C) B2C_FD(3, C) B2C_FD(4, C) B2C_FD(5, C) B2C_FD(6, C) B2C_FD(7, C) B2C_FD(8, C) B2C_FD(9, C) B2C_FD(10, C)
+#define B2C_FD14(C) B2C_FD11(C) B2C_FD(11, C) B2C_FD(12, C) B2C_FD(13, C)
+#define B2C_OP3(v) "+v"(v[0]), "+v"(v[1]), "+v"(v[2])
+#define B2C_OP11(v) \
+  B2C_OP3(v), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10])
+#define B2C_OP14(v) B2C_OP11(v), "+v"(v[11]), "+v"(v[12]), "+v"(v[13])
+#define B2C_SEG_STEP(C)                                                                      \
+  do {                                                                                       \
+    if constexpr (NV == 3)                                                                   \
+      asm("s_nop 1\n\t" B2C_FD3(C) : B2C_OP3(v) : [m] "v"(m));                               \
+    else if constexpr (NV == 11)                                                             \
+      asm("s_nop 1\n\t" B2C_FD11(C) : B2C_OP11(v) : [m] "v"(m));                             \
+    else                                                                                     \
+      asm("s_nop 1\n\t" B2C_FD14(C) : B2C_OP14(v) : [m] "v"(m));                             \
+  } while (0)
+
+// m for one step: 1 where the DPP source lane holds the same run id (and the lane lies in a row the step
+// feeds), else 0.
+template <int CTRL>
+__device__ __forceinline__ float seg_scan_m(uint32_t id, bool row_ok) {
+  const uint32_t src = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)id, CTRL, 0xF, 0xF, true);
+  return (row_ok && src == id) ? 1.f : 0.f;
 }
 
 template <int NV>
 __device__ __forceinline__ void seg_scan(uint32_t id, float (&v)[NV]) {
-  seg_scan_step<0x111, 0xF>(id, v);  // row_shr:1
-  seg_scan_step<0x112, 0xF>(id, v);  // row_shr:2
-  seg_scan_step<0x114, 0xF>(id, v);  // row_shr:4
-  seg_scan_step<0x118, 0xF>(id, v);  // row_shr:8
-  seg_scan_step<0x142, 0xA>(id, v);  // row_bcast:15 into rows 1 and 3
-  seg_scan_step<0x143, 0xC>(id, v);  // row_bcast:31 into rows 2 and 3
+  static_assert(NV == 3 || NV == 11 || NV == 14, "the scan's asm steps cover 3, 11 and 14 values");
+  const int lane = (int)__lane_id();
+  float m;
+  m = seg_scan_m<0x111>(id, true);  // row_shr:1
+  B2C_SEG_STEP("row_shr:1");
+  m = seg_scan_m<0x112>(id, true);  // row_shr:2
+  B2C_SEG_STEP("row_shr:2");
+  m = seg_scan_m<0x114>(id, true);  // row_shr:4
+  B2C_SEG_STEP("row_shr:4");
+  m = seg_scan_m<0x118>(id, true);  // row_shr:8
+  B2C_SEG_STEP("row_shr:8");
+  m = seg_scan_m<0x142>(id, (lane & 16) != 0);  // row_bcast:15 into rows 1 and 3
+  B2C_SEG_STEP("row_bcast:15");
+  m = seg_scan_m<0x143>(id, (lane & 32) != 0);  // row_bcast:31 into rows 2 and 3
+  B2C_SEG_STEP("row_bcast:31");
 }
+#undef B2C_SEG_STEP
+#undef B2C_OP14
+#undef B2C_OP11
+#undef B2C_OP3
+#undef B2C_FD14
+#undef B2C_FD11
+#undef B2C_FD3
+#undef B2C_FD
 
 }  // namespace dev
 }  // namespace b2c
