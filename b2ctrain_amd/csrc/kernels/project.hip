@@ -71,6 +71,12 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
     const float4 po = reinterpret_cast<const float4*>(a.pos_op)[i];
     const float4 q = reinterpret_cast<const float4*>(a.quat)[i];
     const float4 ls = reinterpret_cast<const float4*>(a.lscale)[i];
+    constexpr int K = (DEG + 1) * (DEG + 1);
+    float coef[3 * K];
+    {
+      const ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
+      sv.load_all<DEG, HALF>(i, coef);
+    }
     const ScreenSplat pr = screen_splat(po, q, ls, a.cam);
     if (!pr.ok) {
       a.tile_count[i] = 0u;
@@ -94,13 +100,9 @@ __global__ void __launch_bounds__(PROJ_BLOCK) project_kernel(b2c_project_args a)
       const float vl = sqrtf((pr.d[0] * pr.d[0] + pr.d[1] * pr.d[1]) + pr.d[2] * pr.d[2]);
       const float inv = 1.f / fmaxf(vl, 1e-12f);
       const float vx = pr.d[0] * inv, vy = pr.d[1] * inv, vz = pr.d[2] * inv;
-      constexpr int K = (DEG + 1) * (DEG + 1);
       float b[K];
       sh_basis<DEG>(vx, vy, vz, b);
       const int ka = a.active_deg >= DEG ? K : (a.active_deg + 1) * (a.active_deg + 1);
-      const ShView sv{a.sh.dc, reinterpret_cast<const _Float16*>(a.sh.hi16), a.sh.hi32, a.sh.stride};
-      float coef[3 * K];
-      sv.load_all<DEG, HALF>(i, coef);
       float cr = coef[0] * b[0], cg = coef[1] * b[0], cb = coef[2] * b[0];
 #pragma unroll
       for (int k = 1; k < K; k++) {
