@@ -99,6 +99,8 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
   const int lane = threadIdx.x;
   const int px = (tile % a.tiles_x) * RT_W + (lane & 7), py = (tile / a.tiles_x) * RT_W + (lane >> 3);
   const PixelState ps = load_pixel<FEAT, HOLLOW>(a, px, py, range.x, a.last_idx);
+  const float tcx = (tile % a.tiles_x) * RT_W + RT_W * 0.5f, tcy = (tile / a.tiles_x) * RT_W + RT_W * 0.5f;
+  const PixelPoly pp = pixel_poly(ps.pcx - tcx, ps.pcy - tcy);
   const float Wf = (float)a.W, Hf = (float)a.H;
   float T = ps.T;
   float Q = -ps.v_o_w;
@@ -118,10 +120,12 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
     __syncthreads();
     for (int j = count - 1; j >= 0; j--) {
       const float4 geo = s_geo[j], shape = s_shape[j];  // (mx, my, c00, c01), (c11, opacity, depth, power)
-      // halving c00 and c11 is exact: the same sigma as the forward's
+      // halving c00 and c11 is exact: the same sigma as the forward's (its tile-centred quadratic); the
+      // gradient terms use the offsets from the splat centre
       const FragGeom fg = frag_geom(geo.x, geo.y, 0.5f * geo.z, geo.w, 0.5f * shape.x, ps.pcx, ps.pcy);
-      const float sigma = fg.sigma;
-      const bool in = ps.inside && lo + (uint32_t)j < ps.last && sigma >= 0.f && sigma <= shape.w;
+      const float3 def = sigma_coefs(geo.x, geo.y, 0.5f * geo.z, geo.w, 0.5f * shape.x, tcx, tcy);
+      const float sigma = poly_sigma(0.5f * geo.z, geo.w, 0.5f * shape.x, def.x, def.y, def.z, pp);
+      const bool in = ps.inside && lo + (uint32_t)j < ps.last && sigma <= shape.w;
       if (ballot64(in) == 0ull) continue;  // uniform
       float val[ANCHOR_VALS];
 #pragma unroll
@@ -270,8 +274,8 @@ template <bool FEAT, bool HOLLOW>
 __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args a) {
   constexpr bool EXT = FEAT || HOLLOW;
   constexpr int ROW = ROW_FLOATS<FEAT>;
-  __shared__ float4 s_g0[BATCH];   // (mx, my, c00 / 2, c01)
-  __shared__ float4 s_g1[BATCH];   // (c11 / 2, opacity, power, log2 opacity)
+  __shared__ float4 s_g0[BATCH];   // (D, E, F, c00 / 2): sigma_coefs at this tile
+  __shared__ float4 s_g1[BATCH];   // (c01, c11 / 2, power, log2 opacity)
   __shared__ float4 s_col[BATCH];  // (max(r, 0), max(g, 0), max(b, 0), sign bits of r, g, b)
   __shared__ float4 s_ext[EXT ? BATCH : 1];  // (feature xyz, camera depth)
   __shared__ uint32_t s_slot[BATCH];
@@ -292,7 +296,10 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   const int tx = tile % a.tiles_x, ty = tile / a.tiles_x;
   const int lx = lane & 7, ly = lane >> 3;
   const int px = tx * RT_W + lx, py = ty * RT_W + ly;
-  const float u = lx + 0.5f - RT_W * 0.5f, v = ly + 0.5f - RT_W * 0.5f;
+  const float u = lx + 0.5f - RT_W * 0.5f, v = ly + 0.5f - RT_W * 0.5f;  // offset from the tile centre
+  const float tcx = tx * RT_W + RT_W * 0.5f, tcy = ty * RT_W + RT_W * 0.5f;
+  const PixelPoly pp = pixel_poly(u, v);
+  const float u2 = u + u, v2 = v + v;
   PixelState ps = load_pixel<FEAT, HOLLOW>(a, px, py, range.x, compact ? a.clast : a.last_idx);
   // refine: sqrt(W^2 gx^2 + H^2 gy^2) = W sqrt(gx^2 + rho gy^2), W folded into the per-pixel scale
   const float rho = ((float)a.H * (float)a.H) / ((float)a.W * (float)a.W);
@@ -330,14 +337,15 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
       const uint32_t gid = list_vals[batch_start + lane];
       s_slot[lane] = list_slots[batch_start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
-      const float4 r1 = rec[1], r2 = rec[2];
-      s_g0[lane] = rec[0];
-      s_g1[lane] = make_float4(r1.x, r1.y, r1.z, r2.w);
+      const float4 r0 = rec[0], r1 = rec[1], r2 = rec[2];
+      const float3 def = sigma_coefs(r0.x, r0.y, r0.z, r0.w, r1.x, tcx, tcy);
+      s_g0[lane] = make_float4(def.x, def.y, def.z, r0.z);
+      s_g1[lane] = make_float4(r0.w, r1.x, r1.z, r2.w);
       s_col[lane] = make_float4(r2.x, r2.y, r2.z, r1.w);
       if constexpr (EXT) s_ext[lane] = rec[3];
     } else if (lane < ngroups * G) {  // pad the last group with null splats, never composited: power = 0
-      s_g0[lane] = make_float4(0.f, 0.f, 0.f, 0.f);  // and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1)
-      s_g1[lane] = make_float4(1.f, 1.f, 0.f, 0.f);
+      s_g0[lane] = make_float4(0.f, 0.f, 1.f, 0.f);  // and sigma = F = 1
+      s_g1[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
       s_col[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
       if constexpr (EXT) s_ext[lane] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
@@ -361,12 +369,9 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
         {
           const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + jj * 16);
           const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + jj * 16);
-          const FragGeom fg = frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, ps.pcx, ps.pcy);
-          const float sigma = fg.sigma;
-          // 0 <= sigma <= power as one unsigned compare of the bit patterns: every listed splat has
-          // power >= +0 (its tile test passed, and sigma >= 0 for a positive-definite conic), and sigma is
-          // never -0 (frag_geom's addend (c dy) dy is +0 when dy is); a NaN sigma fails either way
-          const bool in = live_px & (jj < last_rel) & (__float_as_uint(sigma) <= __float_as_uint(g1.z));
+          const float sigma = poly_sigma(g0.w, g1.x, g1.y, g0.x, g0.y, g0.z, pp);
+          // the forward's test: sigma <= power (a NaN sigma fails)
+          const bool in = live_px & (jj < last_rel) & (sigma <= g1.z);
           {  // straight-line: a lane without this fragment computes zeros (alpha = 0)
             // a lane without this fragment runs the same arithmetic with alpha = 0: ra = 1, vis = 0,
             // v_sigma = 0 and T, Q unchanged (every operand stays finite)
@@ -391,7 +396,9 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
             // refine statistic: |d(loss)/d(mean2d)| scaled to pixels, over the final alpha, from the
             // photometric (and feature) terms only
             const float v_sigma_photo = HOLLOW ? (unclamped ? -alpha * v_alpha_photo : 0.f) : v_sigma;
-            const float gx = __builtin_fmaf(g0.z, fg.dx, fg.lin), gy = __builtin_fmaf(g0.w, fg.dx, fg.cdy + fg.cdy);
+            // the sigma gradient in pixels: 2a u + b v + D, b u + 2c v + E
+            const float gx = __builtin_fmaf(g0.w, u2, __builtin_fmaf(g1.x, v, g0.x));
+            const float gy = __builtin_fmaf(g1.x, u, __builtin_fmaf(g1.y, v2, g0.y));
             o_r = fabsf(v_sigma_photo) * __builtin_amdgcn_sqrtf(gx * gx + rho * gy * gy) * r_scale;
             o_vis = vis;
             o_vs = v_sigma;

@@ -39,6 +39,36 @@ __device__ __forceinline__ FragGeom frag_geom(float mx, float my, float a, float
   return f;
 }
 
+// A fragment's sigma as a quadratic in the pixel centre's offset (u, v) from its tile's centre: with
+// (mxr, myr) the splat centre relative to the tile centre and a = c00 / 2, b = c01, c = c11 / 2,
+//   sigma = a (u - mxr)^2 + b (u - mxr)(v - myr) + c (v - myr)^2 = a uu + b uv + c vv + D u + E v + F,
+// D = -(2a mxr + b myr), E = -(b mxr + 2c myr) and F the sigma at the tile centre (frag_geom's arithmetic at
+// dx = -mxr, dy = -myr). D, E and F are formed once per (splat, tile); a pixel then costs five fused
+// multiply-adds (u, v, uu, uv, vv are exact: u, v are +-0.5 .. +-3.5). Every kernel that tests or replays a
+// fragment (forward, both backward modes, evidence, depth probe) and the CPU restatement evaluate exactly
+// these operations, so all of them agree on which fragments pass. Rounding can leave sigma slightly
+// negative where the exact value is 0 (a pixel centre on the splat centre): a fragment passes when
+// sigma <= power, which keeps it, as the exact value would.
+struct PixelPoly {
+  float u, v, uu, uv, vv;
+};
+
+__device__ __forceinline__ PixelPoly pixel_poly(float u, float v) { return PixelPoly{u, v, u * u, u * v, v * v}; }
+
+__device__ __forceinline__ float3 sigma_coefs(float mx, float my, float a, float b, float c, float tcx, float tcy) {
+#pragma clang fp contract(off)
+  const float mxr = mx - tcx, myr = my - tcy;
+  const float D = -__builtin_fmaf(a + a, mxr, b * myr);
+  const float E = -__builtin_fmaf(b, mxr, (c + c) * myr);
+  const float F = __builtin_fmaf(mxr, __builtin_fmaf(a, mxr, b * myr), (c * myr) * myr);
+  return make_float3(D, E, F);
+}
+
+__device__ __forceinline__ float poly_sigma(float a, float b, float c, float D, float E, float F, const PixelPoly& pp) {
+  return __builtin_fmaf(a, pp.uu, __builtin_fmaf(b, pp.uv, __builtin_fmaf(c, pp.vv,
+                                                 __builtin_fmaf(D, pp.u, __builtin_fmaf(E, pp.v, F)))));
+}
+
 // e^-sigma on the hardware exponential (v_exp_f32 is 2^x): the Gaussian factor of the opacity gradient.
 __device__ __forceinline__ float gauss_weight(float sigma) { return __builtin_amdgcn_exp2f(sigma * -LOG2E); }
 
@@ -76,7 +106,10 @@ __device__ __forceinline__ float hollow_h(float z, HollowRef h) {
 // so that segment leaves the box there): the left edge only if the centre is left of it, and so on - at most
 // one vertical and one horizontal edge, where the minimum is a clamped one-dimensional one. The box minimum is at most sigma at any pixel centre
 // of the quadrant; it is compared with power less a margin of 1e-5 of the terms' magnitude, far above the
-// rounding of this evaluation and of the per-pixel one, so a quadrant is dropped only when no pixel of it
+// rounding of this evaluation. The per-pixel sigma (poly_sigma, the quadratic about the tile centre) rounds
+// on the scale of its own terms, which near the splat centre can be much larger than sigma's: power is
+// raised by 1e-5 of the sum of their magnitudes over the tile (the magnitudes of F, 3.5 |D|, 3.5 |E| and
+// 12.25 (a + |b| + c), with F, D, E bounded term by term). So a quadrant is dropped only when no pixel of it
 // can pass the cutoff. A fragment in a dropped quadrant would have had alpha = 0, so culling changes no
 // result. Degenerate conics and a non-finite centre keep every quadrant. (x0, y0) is the tile's first
 // pixel centre.
@@ -89,6 +122,10 @@ __device__ __forceinline__ uint32_t quadrant_mask(float mx, float my, float ah, 
                                                   float x0, float y0) {
   if (!(ah > 0.f && ch > 0.f) || !(mx - mx == 0.f) || !(my - my == 0.f)) return 0xFu;
   const float ky = -b / (2.f * ch), kx = -b / (2.f * ah);  // minimising dy for a given dx, and dx for dy
+  const float mxr = fabsf(mx - (x0 + 3.5f)), myr = fabsf(my - (y0 + 3.5f)), bb = fabsf(b);
+  const float scale = ((ah * mxr + bb * myr) * mxr + ch * myr * myr) +
+                      3.5f * ((2.f * ah + bb) * mxr + (bb + 2.f * ch) * myr) + 12.25f * (ah + bb + ch);
+  const float pw = power + 1e-5f * scale;
   const float ex[4] = {x0 - mx, x0 + 3.f - mx, x0 + 4.f - mx, x0 + 7.f - mx};
   const float ey[4] = {y0 - my, y0 + 3.f - my, y0 + 4.f - my, y0 + 7.f - my};
   uint32_t mask = 0;
@@ -103,7 +140,7 @@ __device__ __forceinline__ uint32_t quadrant_mask(float mx, float my, float ah, 
       const float mv = edge_sigma_lb(ah, b, ch, xe, fminf(fmaxf(ky * xe, ylo), yhi));
       const float mh = edge_sigma_lb(ah, b, ch, fminf(fmaxf(kx * ye, xlo), xhi), ye);
       // inside: neither edge faces the centre; a NaN edge minimum keeps the quadrant (bitwise: no branches)
-      const bool reach = (!fv & !fh) | (fv & !(mv > power)) | (fh & !(mh > power));
+      const bool reach = (!fv & !fh) | (fv & !(mv > pw)) | (fh & !(mh > pw));
       mask |= reach ? 1u << (2 * qy + qx) : 0u;
     }
   }

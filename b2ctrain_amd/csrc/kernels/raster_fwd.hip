@@ -18,12 +18,9 @@ namespace {
 // reaches no pixel of a quadrant would contribute alpha = 0 there, so the result equals the plain sweep.
 // The loop is branch-free: a lane that has terminated, has run out of its list, or whose fragment fails
 // the cutoff contributes alpha = 0, which leaves T, the colour and the last index unchanged. Per splat the
-// LDS holds (mx, my, c00/2, c01), (c11/2, log2 opacity, power, 0) and the colour clamped at 0, staged from
-// the projection's 64-byte per-splat record (one cache line per gather); sigma is frag_geom's
-// (raster_common.h) from (mx, my, c00 / 2, c01) and c11 / 2.
-__device__ __forceinline__ float splat_sigma(float4 g0, float4 g1, float pcx, float pcy) {
-  return frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, pcx, pcy).sigma;
-}
+// LDS holds (D, E, F, c00/2), (c01, log2 opacity, power, c11/2) and the colour clamped at 0, staged from
+// the projection's 64-byte per-splat record (one cache line per gather): sigma is the tile-centred
+// quadratic of raster_common.h (sigma_coefs once per splat and tile, poly_sigma per fragment).
 
 // COMPACT: the tile's compacted list for the MFMA backward (the entries some pixel composited). Each lane
 // marks the steps of its quadrant's list where it composited (one bit per step pair, even and odd steps
@@ -48,6 +45,8 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   const float x0 = tx * RT_W + 0.5f, y0 = ty * RT_W + 0.5f;  // the tile's first pixel centre
   const bool inside = px < a.W && py < a.H;
   const float pcx = px + 0.5f, pcy = py + 0.5f;
+  const float tcx = tx * RT_W + RT_W * 0.5f, tcy = ty * RT_W + RT_W * 0.5f;  // the tile centre
+  const PixelPoly pp = pixel_poly(pcx - tcx, pcy - tcy);
   uint2* ranges = reinterpret_cast<uint2*>(a.tile_ranges);
   const uint2 range = ranges[tile];
   float T = 1.f, r = 0.f, g = 0.f, b = 0.f;
@@ -59,9 +58,9 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
   uint32_t clast = range.x, cbase = 0;  // COMPACT: this pixel's end in the compacted list; entries kept so far
   if (lane < 8) s_list[lane >> 1][64 + (lane & 1)] = 64u * 16u;  // read by the last pair's prefetch
   if constexpr (COMPACT) s_flag[lane] = 0u;
-  if (lane == 0) {  // power = 0 and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1): fails the cutoff
-    s_g0[64] = make_float4(0.f, 0.f, 0.f, 0.f);
-    s_g1[64] = make_float4(1.f, 0.f, 0.f, 0.f);
+  if (lane == 0) {  // power = 0 and sigma = F = 1: fails the cutoff
+    s_g0[64] = make_float4(0.f, 0.f, 1.f, 0.f);
+    s_g1[64] = make_float4(0.f, 0.f, 0.f, 0.f);
     s_col[64] = make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (EXT) s_ext[64] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
@@ -80,8 +79,9 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
       if constexpr (COMPACT) gslot = a.slot_sorted[start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
       const float4 r0 = rec[0], r1 = rec[1], r2 = rec[2];
-      s_g0[lane] = r0;
-      s_g1[lane] = make_float4(r1.x, r2.w, r1.z, 0.f);
+      const float3 def = sigma_coefs(r0.x, r0.y, r0.z, r0.w, r1.x, tcx, tcy);
+      s_g0[lane] = make_float4(def.x, def.y, def.z, r0.z);
+      s_g1[lane] = make_float4(r0.w, r2.w, r1.z, r1.x);
       s_col[lane] = r2;
       if constexpr (EXT) s_ext[lane] = rec[3];
       qmask = quadrant_mask(r0.x, r0.y, r0.z, r0.w, r1.x, r1.z, x0, y0);
@@ -109,12 +109,9 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     // n_pairs step pairs bit b stands for pair n_pairs - 1 - b. They give the lane's last composited entry
     // (and, COMPACT, the kept entries) without a select per step.
     uint32_t marks_even = 0, marks_odd = 0;
-    // One step: 0 <= sigma <= power as one unsigned compare of the bit patterns (every listed splat has
-    // power >= +0, since its tile test passed and sigma >= 0 for a positive-definite conic, and sigma is
-    // never -0 for one: dx and dy are +0 or nonzero, and with dy = +0 the addend (c dy) dy is +0, with dx =
-    // +0 the sum is (c dy) dy >= +0; a NaN sigma fails either way), bitwise & so the
-    // compiler does not branch on the compares; the exp is kept out of an exec-masked branch (a lane with
-    // sigma < 0 has its alpha discarded by the select); only a valid fragment can stop a lane. A fragment is
+    // One step: sigma <= power (a NaN sigma fails), bitwise & so the compiler does not branch on the
+    // compares; the exp is kept out of an exec-masked branch (a lane whose fragment fails has its alpha
+    // discarded by the select); only a valid fragment can stop a lane. A fragment is
     // composited (vis > 0) exactly when it is valid and does not stop the lane: a valid alpha is at least
     // 1/255 and a live lane's T is above the cutoff.
 #define B2C_COMPOSITE(off, next, marks)                                                                \
@@ -122,8 +119,8 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + (off));                                \
     const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + (off));                                \
     const float4 col = *reinterpret_cast<const float4*>(lds_col + (off));                              \
-    const float sigma = splat_sigma(g0, g1, pcx, pcy);                                                 \
-    const bool valid = live & (__float_as_uint(sigma) <= __float_as_uint(g1.z));                       \
+    const float sigma = poly_sigma(g0.w, g1.x, g1.w, g0.x, g0.y, g0.z, pp);                            \
+    const bool valid = live & (sigma <= g1.z);                                                         \
     float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));                                        \
     asm volatile("" : "+v"(a_cl));                                                                     \
     const float alpha = valid ? a_cl : 0.f;                                                            \

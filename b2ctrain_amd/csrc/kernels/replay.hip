@@ -51,6 +51,8 @@ __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
   const int px = (tile % a.tiles_x) * RT_W + (lane & 7), py = (tile / a.tiles_x) * RT_W + (lane >> 3);
   const bool inside = px < a.W && py < a.H;
   const float pcx = px + 0.5f, pcy = py + 0.5f;
+  const float tcx = (tile % a.tiles_x) * RT_W + RT_W * 0.5f, tcy = (tile / a.tiles_x) * RT_W + RT_W * 0.5f;
+  const PixelPoly pp = pixel_poly(pcx - tcx, pcy - tcy);
   float m = 0.f, mres = 0.f, k = 0.f;
   uint32_t last = range.x, lab = LABEL_NONE;
   if (inside) {
@@ -112,15 +114,16 @@ __global__ void __launch_bounds__(64) evidence_kernel(b2c_evidence_args a) {
       s_id[lane] = gid;
       s_slot[lane] = a.slot_sorted[start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
-      const float4 r1 = rec[1], r2 = rec[2];
-      s_g0[lane] = rec[0];
-      s_g1[lane] = make_float4(r1.x, r2.w, r1.z, 0.f);  // (c11 / 2, log2 opacity, power)
+      const float4 r0 = rec[0], r1 = rec[1], r2 = rec[2];
+      const float3 def = sigma_coefs(r0.x, r0.y, r0.z, r0.w, r1.x, tcx, tcy);
+      s_g0[lane] = make_float4(def.x, def.y, def.z, r0.z);
+      s_g1[lane] = make_float4(r0.w, r2.w, r1.z, r1.x);  // (c01, log2 opacity, power, c11 / 2)
     }
     __syncthreads();
     for (uint32_t j = 0; j < count; j++) {
       const float4 g0 = s_g0[j], g1 = s_g1[j];
-      const float sigma = frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, pcx, pcy).sigma;
-      const bool valid = inside & (start + j < last) & (sigma >= 0.f) & (sigma <= g1.z);
+      const float sigma = poly_sigma(g0.w, g1.x, g1.w, g0.x, g0.y, g0.z, pp);
+      const bool valid = inside & (start + j < last) & (sigma <= g1.z);
       const float alpha = valid ? fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y)) : 0.f;
       const float vis = alpha * T;
       T = T * (1.f - alpha);
@@ -247,6 +250,7 @@ __global__ void __launch_bounds__(64) probe_kernel(b2c_probe_args a) {
   // lanes by quadrant as in the forward: lane 16 q + p is pixel p (row-major 4x4) of quadrant q; slot 64
   // is a null splat that pads the shorter quadrant lists
   __shared__ float4 s_g0[65], s_g1[65];
+  __shared__ float s_z[65];  // camera depth
   __shared__ uint32_t s_list[4][66];  // per quadrant: LDS byte offsets of its splats, in depth order
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
@@ -259,17 +263,21 @@ __global__ void __launch_bounds__(64) probe_kernel(b2c_probe_args a) {
   const float x0 = tx * RT_W + 0.5f, y0 = ty * RT_W + 0.5f;  // the tile's first pixel centre
   const bool inside = px < a.W && py < a.H;
   const float pcx = px + 0.5f, pcy = py + 0.5f;
+  const float tcx = tx * RT_W + RT_W * 0.5f, tcy = ty * RT_W + RT_W * 0.5f;  // the tile centre
+  const PixelPoly pp = pixel_poly(pcx - tcx, pcy - tcy);
   const bool mean_mode = a.tau <= 0.f;
   float T = 1.f, z_first = __builtin_inff(), deep = 0.f, behind = 0.f, zsum = 0.f;
   const float zr = (inside && a.ref_z) ? a.ref_z[py * a.W + px] : __builtin_inff();
   bool live = inside;
   if (lane < 8) s_list[lane >> 1][64 + (lane & 1)] = 64u * 16u;  // read by the last pair's prefetch
-  if (lane == 0) {  // power = 0 and sigma = (py + 0.5)^2 > 0 (c11 / 2 = 1): fails the cutoff
-    s_g0[64] = make_float4(0.f, 0.f, 0.f, 0.f);
-    s_g1[64] = make_float4(1.f, 0.f, 0.f, 0.f);
+  if (lane == 0) {  // power = 0 and sigma = F = 1: fails the cutoff
+    s_g0[64] = make_float4(0.f, 0.f, 1.f, 0.f);
+    s_g1[64] = make_float4(0.f, 0.f, 0.f, 0.f);
+    s_z[64] = 0.f;
   }
   const char* lds_g0 = reinterpret_cast<const char*>(s_g0);
   const char* lds_g1 = reinterpret_cast<const char*>(s_g1);
+  const char* lds_z = reinterpret_cast<const char*>(s_z);
   for (uint32_t start = range.x; start < range.y; start += 64) {
     if (ballot64(live) == 0ull) break;
     const uint32_t remaining = min(64u, range.y - start);
@@ -279,8 +287,10 @@ __global__ void __launch_bounds__(64) probe_kernel(b2c_probe_args a) {
       const uint32_t gid = a.vals_sorted[start + lane];
       const float4* rec = reinterpret_cast<const float4*>(a.raster_rec) + (size_t)gid * 4;
       const float4 r0 = rec[0], r1 = rec[1], r2 = rec[2], r3 = rec[3];
-      s_g0[lane] = r0;
-      s_g1[lane] = make_float4(r1.x, r2.w, r1.z, r3.w);  // (c11 / 2, log2 opacity, power, depth)
+      const float3 def = sigma_coefs(r0.x, r0.y, r0.z, r0.w, r1.x, tcx, tcy);
+      s_g0[lane] = make_float4(def.x, def.y, def.z, r0.z);
+      s_g1[lane] = make_float4(r0.w, r2.w, r1.z, r1.x);  // (c01, log2 opacity, power, c11 / 2)
+      s_z[lane] = r3.w;
       qmask = quadrant_mask(r0.x, r0.y, r0.z, r0.w, r1.x, r1.z, x0, y0);
     }
     uint32_t n_iter = 0;
@@ -305,8 +315,8 @@ __global__ void __launch_bounds__(64) probe_kernel(b2c_probe_args a) {
   do {                                                                                                  \
     const float4 g0 = *reinterpret_cast<const float4*>(lds_g0 + (off));                                 \
     const float4 g1 = *reinterpret_cast<const float4*>(lds_g1 + (off));                                 \
-    const float sigma = frag_geom(g0.x, g0.y, g0.z, g0.w, g1.x, pcx, pcy).sigma;                        \
-    const bool valid = live & (__float_as_uint(sigma) <= __float_as_uint(g1.z));                        \
+    const float sigma = poly_sigma(g0.w, g1.x, g1.w, g0.x, g0.y, g0.z, pp);                             \
+    const bool valid = live & (sigma <= g1.z);                                                          \
     float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));                                         \
     asm volatile("" : "+v"(a_cl));                                                                      \
     const float alpha = valid ? a_cl : 0.f;                                                             \
@@ -315,7 +325,7 @@ __global__ void __launch_bounds__(64) probe_kernel(b2c_probe_args a) {
     live = live & !stop;                                                                                \
     const bool comp = valid & !stop;                                                                    \
     const float vis = comp ? alpha * T : 0.f;                                                           \
-    const float z = g1.w;                                                                               \
+    const float z = *reinterpret_cast<const float*>(lds_z + ((off) >> 2));                              \
     deep += (__builtin_isfinite(z_first) & (z > z_first + a.delta)) ? vis : 0.f;                        \
     behind += (z > zr + a.margin) ? vis : 0.f;                                                          \
     zsum = comp ? fmaf(vis, z, zsum) : zsum;                                                            \

@@ -462,19 +462,29 @@ uint32_t orc_bin(int n, const uint32_t* tile_count, const uint32_t* hit_info, co
  * Forward raster (raster_fwd.cu:8-71). Each pixel walks its tile's list front to back; the whole
  * tile's early exit only skips pixels that are already done, so a per-pixel loop is equivalent.
  * ---------------------------------------------------------------------------------------------- */
-/* A fragment's sigma as the raster kernels evaluate it (raster_common.h frag_geom): with a = c00 / 2,
- * b = c01, c = c11 / 2, sigma = fma(dx, fma(a, dx, b dy), (c dy) dy); halving is exact. The reference's
- * 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy (raster_fwd.cu:44) is the same quantity rounded differently. */
-static float frag_sigma(float dx, float dy, float c00, float c01, float c11) {
-  const float a = 0.5f * c00, c = 0.5f * c11;
-  const float lin = fmaf(a, dx, c01 * dy);
-  const float cdy = c * dy;
-  return fmaf(dx, lin, cdy * dy);
+/* A fragment's sigma as the raster kernels evaluate it (raster_common.h sigma_coefs / poly_sigma): a
+ * quadratic in the pixel centre's offset (u, v) from its 8x8 tile's centre. With a = c00 / 2, b = c01,
+ * c = c11 / 2 (halving is exact) and (mxr, myr) the splat centre relative to the tile centre,
+ *   sigma = fma(a, uu, fma(b, uv, fma(c, vv, fma(D, u, fma(E, v, F))))),
+ *   D = -fma(2a, mxr, b myr), E = -fma(b, mxr, (2c) myr), F = fma(mxr, fma(a, mxr, b myr), (c myr) myr).
+ * The reference's 0.5 (c00 dx^2 + c11 dy^2) + c01 dx dy (raster_fwd.cu:44) is the same quantity rounded
+ * differently. A fragment passes when sigma <= power: rounding can leave sigma slightly below 0 where the
+ * exact value is 0, and such a fragment is kept, as the exact value would be. */
+static float frag_sigma(float mx, float my, float c00, float c01, float c11, float pcx, float pcy) {
+  const float a = 0.5f * c00, b = c01, c = 0.5f * c11;
+  const float tcx = floorf(pcx * (1.f / RT_W)) * RT_W + RT_W * 0.5f;
+  const float tcy = floorf(pcy * (1.f / RT_W)) * RT_W + RT_W * 0.5f;
+  const float mxr = mx - tcx, myr = my - tcy;
+  const float D = -fmaf(a + a, mxr, b * myr);
+  const float E = -fmaf(b, mxr, (c + c) * myr);
+  const float F = fmaf(mxr, fmaf(a, mxr, b * myr), (c * myr) * myr);
+  const float u = pcx - tcx, v = pcy - tcy;
+  return fmaf(a, u * u, fmaf(b, u * v, fmaf(c, v * v, fmaf(D, u, fmaf(E, v, F)))));
 }
 
-void orc_frag_sigma(int n, const float* dx, const float* dy, const float* c00, const float* c01, const float* c11,
-                    float* out) {
-  for (int i = 0; i < n; i++) out[i] = frag_sigma(dx[i], dy[i], c00[i], c01[i], c11[i]);
+void orc_frag_sigma(int n, const float* mx, const float* my, const float* c00, const float* c01, const float* c11,
+                    const float* pcx, const float* pcy, float* out) {
+  for (int i = 0; i < n; i++) out[i] = frag_sigma(mx[i], my[i], c00[i], c01[i], c11[i], pcx[i], pcy[i]);
 }
 
 /* Fragments the last orc_raster_fwd call composited (F_contrib: alpha >= 1/255, before termination). */
@@ -532,9 +542,8 @@ void orc_raster_fwd_ext(int W, int H, int tiles_x, int tiles_y, const float bg[3
       for (uint32_t idx = rx; idx < ry; idx++) {
         uint32_t gid = vals_sorted[idx];
         const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
-        float dx = pcx - a[0], dy = pcy - a[1];
-        float sigma = frag_sigma(dx, dy, a[2], a[3], c[0]);
-        if (sigma < 0.f || sigma > c[3]) continue;
+        float sigma = frag_sigma(a[0], a[1], a[2], a[3], c[0], pcx, pcy);
+        if (!(sigma <= c[3])) continue;
         float alpha = fminf(ALPHA_MAX, c[1] * expf(-sigma));
         float next_T = T * (1.f - alpha);
         if (next_T <= T_CUTOFF) break;
@@ -724,8 +733,8 @@ void orc_raster_bwd_ext(int W, int H, int tiles_x, int tiles_y, const float bg[3
         uint32_t gid = vals_sorted[idx];
         const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
         float dx = pcx - a[0], dy = pcy - a[1];
-        float sigma = frag_sigma(dx, dy, a[2], a[3], c[0]);
-        if (!(sigma >= 0.f && sigma <= c[3])) continue;
+        float sigma = frag_sigma(a[0], a[1], a[2], a[3], c[0], pcx, pcy);
+        if (!(sigma <= c[3])) continue;
         float g[GRAD_LANES];
         for (int k = 0; k < GRAD_LANES; k++) g[k] = 0.f;
         float gauss = expf(-sigma);
@@ -1362,8 +1371,8 @@ void orc_evidence_view(int W, int H, int tiles_x, int tiles_y, const uint32_t* t
       for (uint32_t idx = rx; idx < ry && idx < last; idx++) {
         const uint32_t gid = vals_sorted[idx];
         const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
-        const float sigma = frag_sigma(pcx - a[0], pcy - a[1], a[2], a[3], c[0]);
-        if (sigma < 0.f || sigma > c[3]) continue;
+        const float sigma = frag_sigma(a[0], a[1], a[2], a[3], c[0], pcx, pcy);
+        if (!(sigma <= c[3])) continue;
         const float alpha = fminf(ALPHA_MAX, c[1] * expf(-sigma));
         const float vis = alpha * T;
         T *= 1.f - alpha;
@@ -1393,8 +1402,8 @@ void orc_probe(int W, int H, int tiles_x, int tiles_y, const uint32_t* tile_rang
       for (uint32_t idx = rx; idx < ry; idx++) {
         const uint32_t gid = vals_sorted[idx];
         const float* a = proj0 + (size_t)gid * 4; const float* c = proj1 + (size_t)gid * 4;
-        const float sigma = frag_sigma(pcx - a[0], pcy - a[1], a[2], a[3], c[0]);
-        if (sigma < 0.f || sigma > c[3]) continue;
+        const float sigma = frag_sigma(a[0], a[1], a[2], a[3], c[0], pcx, pcy);
+        if (!(sigma <= c[3])) continue;
         const float alpha = fminf(ALPHA_MAX, c[1] * expf(-sigma));
         const float next_T = T * (1.f - alpha);
         if (next_T <= T_CUTOFF) break;

@@ -193,9 +193,10 @@ double orc_ref_composite_seconds(void);
 void orc_set_threads(int n);
 
 /* ---- internal pieces exported for the pinning tests ---- */
-/* The raster kernels' fragment sigma from pixel-minus-centre offsets and the conic (c00, c01, c11). */
-void orc_frag_sigma(int n, const float* dx, const float* dy, const float* c00, const float* c01, const float* c11,
-                    float* out);
+/* The raster kernels' fragment sigma of a splat (centre mx, my; conic c00, c01, c11) at a pixel centre
+ * (pcx, pcy): the quadratic about the centre of the pixel's 8x8 tile. */
+void orc_frag_sigma(int n, const float* mx, const float* my, const float* c00, const float* c01, const float* c11,
+                    const float* pcx, const float* pcy, float* out);
 void orc_sh_basis_f(int deg, float x, float y, float z, float* out);      /* splat_math.cuh:122-145 */
 /* The projection's cull decision for one splat (pr.ok of splat_math.cuh:224-293). */
 int orc_project_ok(const float* po, const float* q, const float* ls, const orc_cam_t* cam);

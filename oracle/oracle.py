@@ -114,7 +114,7 @@ def lib():
         _lib.orc_ref_set_sample.argtypes = [C.c_uint64]
         _lib.orc_ref_composite_seconds.restype = C.c_double
         _lib.orc_frag_sigma.restype = None
-        _lib.orc_frag_sigma.argtypes = [C.c_int] + [p] * 6
+        _lib.orc_frag_sigma.argtypes = [C.c_int] + [p] * 8
         _lib.orc_set_threads.restype = None
         _lib.orc_set_threads.argtypes = [C.c_int]
         _lib.orc_max_screen.restype = None
@@ -156,12 +156,15 @@ def lib():
     return _lib
 
 
-def frag_sigma(dx, dy, c00, c01, c11):
-    """The raster kernels' fragment sigma (float32 arrays of one shape)."""
-    arrs = [np.ascontiguousarray(np.broadcast_to(v, np.shape(dx)), np.float32).ravel() for v in (dx, dy, c00, c01, c11)]
+def frag_sigma(mx, my, c00, c01, c11, pcx, pcy):
+    """The raster kernels' fragment sigma of splats (centre mx, my; conic c00, c01, c11) at pixel centres
+    (pcx, pcy): the quadratic about the centre of the pixel's 8x8 tile (float32, broadcast to one shape)."""
+    vals = (mx, my, c00, c01, c11, pcx, pcy)
+    shape = np.broadcast_shapes(*[np.shape(v) for v in vals])
+    arrs = [np.ascontiguousarray(np.broadcast_to(np.asarray(v, np.float32), shape)).ravel() for v in vals]
     out = np.empty(arrs[0].size, np.float32)
     lib().orc_frag_sigma(out.size, *[_ptr(a) for a in arrs], _ptr(out))
-    return out.reshape(np.shape(dx))
+    return out.reshape(shape)
 
 
 def set_threads(n: int) -> None:

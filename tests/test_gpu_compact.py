@@ -6,7 +6,7 @@ that list instead (no reference counterpart; B2C_COMPACT_LISTS=0 turns it off).
 
 * The lists are exactly the composited entries: recomputed here from the GPU's own sorted lists, projection
   and per-pixel ends (last_idx) with the oracle's fragment sigma (the raster kernels' float ops), an entry is
-  kept when some pixel inside the image has it before its end with 0 <= sigma <= power.
+  kept when some pixel inside the image has it before its end with sigma <= power.
 * The gradients over the compacted lists equal those over the full ranges: the left-out entries change
   neither a pixel's transmittance nor its running colour sum (alpha = 0), and their zero rows sum to the same
   per-splat totals (compared as values, so a zero's sign may differ).
@@ -41,12 +41,9 @@ def _expected_lists(r, sc):
     py = (tile // tx)[:, None] * 8 + ly[None, :]
     inside = (px < W) & (py < H)
     pix = np.where(inside, py * W + px, 0)
-    sig = O.frag_sigma((px + 0.5).astype(np.float32) - p0[ids, 0][:, None],
-                       (py + 0.5).astype(np.float32) - p0[ids, 1][:, None],
-                       p0[ids, 2][:, None], p0[ids, 3][:, None], p1[ids, 0][:, None])
-    sb = sig.view(np.uint32)
-    pb = p1[ids, 3].astype(np.float32).view(np.uint32)[:, None]
-    comp = inside & (e[:, None] < last[pix]) & (sb <= pb)  # 0 <= sigma <= power as one unsigned compare
+    sig = O.frag_sigma(p0[ids, 0][:, None], p0[ids, 1][:, None], p0[ids, 2][:, None], p0[ids, 3][:, None],
+                       p1[ids, 0][:, None], (px + 0.5).astype(np.float32), (py + 0.5).astype(np.float32))
+    comp = inside & (e[:, None] < last[pix]) & (sig <= p1[ids, 3].astype(np.float32)[:, None])
     kept = comp.any(1)
     return dict(ranges=ranges, e=e[kept], tile=tile[kept], ids=ids[kept], slots=slots[e[kept]], last=last,
                 n_entries=int(inr.sum()))

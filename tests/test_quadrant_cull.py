@@ -1,8 +1,8 @@
 """The forward raster's quadrant culling test (quadrant_mask in b2ctrain_amd/csrc/kernels/raster_common.h),
 restated in float32 numpy, must be conservative: a quadrant with a pixel centre where the raster kernels'
-fp32 sigma (frag_geom: dx (a dx + b dy) + (c dy) dy with two fused multiply-adds, evaluated here by the
-oracle's C restatement; the reference's src/gpu/raster_fwd.cu:44-50 rounds the same quantity differently)
-passes 0 <= sigma <= power must keep its bit. Checked by brute force over all 64 pixel centres on random splats,
+fp32 sigma (the quadratic about the tile centre of sigma_coefs / poly_sigma, five fused multiply-adds,
+evaluated here by the oracle's C restatement; the reference's src/gpu/raster_fwd.cu:44-50 rounds the same
+quantity differently) passes sigma <= power must keep its bit. Checked by brute force over all 64 pixel centres on random splats,
 including needle-thin ellipses (axis ratio up to 1e5) whose terms cancel, splats centred inside, on the
 edges and far outside the tile, and adversarially: power set to the fp32 sigma of one pixel, which puts
 that pixel exactly on the cutoff. The GPU parity tests check the device code itself (a wrongly culled
@@ -21,10 +21,20 @@ def edge_lb(ah, b, ch, dx, dy):
     return (t1 + t2 + t3) - f32(1e-5) * (np.abs(t1) + np.abs(t2) + np.abs(t3))
 
 
+def poly_slack_power(mx, my, ah, b, ch, power, x0, y0):
+    """power raised by 1e-5 of the magnitude of the tile-centred quadratic's terms over the tile (the
+    per-pixel sigma's rounding scale), as quadrant_mask does."""
+    mxr, myr, bb = np.abs(mx - (x0 + f32(3.5))), np.abs(my - (y0 + f32(3.5))), np.abs(b)
+    scale = (((ah * mxr + bb * myr) * mxr + ch * myr * myr) +
+             f32(3.5) * ((f32(2) * ah + bb) * mxr + (bb + f32(2) * ch) * myr) + f32(12.25) * (ah + bb + ch))
+    return power + f32(1e-5) * scale
+
+
 def quadrant_mask(mx, my, ah, b, ch, power, x0, y0):
     """Restates raster_common.h's quadrant_mask: per quadrant, the centre inside the box, or the clamped
     minimum on the (at most one) vertical and (at most one) horizontal edge the centre lies beyond."""
     with np.errstate(all="ignore"):
+        power = poly_slack_power(mx, my, ah, b, ch, power, x0, y0)
         ky = -b / (f32(2) * ch)
         kx = -b / (f32(2) * ah)
         ex = [x0 - mx, x0 + f32(3) - mx, x0 + f32(4) - mx, x0 + f32(7) - mx]
@@ -48,6 +58,7 @@ def quadrant_mask(mx, my, ah, b, ch, power, x0, y0):
 def quadrant_mask_all_edges(mx, my, ah, b, ch, power, x0, y0):
     """The same bound taken over all four edges of each quadrant box (no facing-edge selection)."""
     with np.errstate(all="ignore"):
+        power = poly_slack_power(mx, my, ah, b, ch, power, x0, y0)
         ky = -b / (f32(2) * ch)
         kx = -b / (f32(2) * ah)
         ex = [x0 - mx, x0 + f32(3) - mx, x0 + f32(4) - mx, x0 + f32(7) - mx]
@@ -67,9 +78,7 @@ def quadrant_mask_all_edges(mx, my, ah, b, ch, power, x0, y0):
 
 
 def sigma_at(mx, my, c00, c01, c11, x0, y0, i, j):
-    dx = (x0 + f32(i)) - mx
-    dy = (y0 + f32(j)) - my
-    return O.frag_sigma(dx, dy, c00, c01, c11)
+    return O.frag_sigma(mx, my, c00, c01, c11, x0 + f32(i), y0 + f32(j))
 
 
 def pixel_truth(mx, my, c00, c01, c11, power, x0, y0):
@@ -78,7 +87,7 @@ def pixel_truth(mx, my, c00, c01, c11, power, x0, y0):
     for j in range(8):
         for i in range(8):
             sig = sigma_at(mx, my, c00, c01, c11, x0, y0, i, j)
-            hit = (sig >= 0) & (sig <= power)
+            hit = sig <= power
             truth |= np.where(hit, np.uint32(1 << (2 * (j // 4) + i // 4)), np.uint32(0))
     return truth
 
@@ -131,7 +140,7 @@ def test_quadrant_mask_keeps_pixels_exactly_on_the_cutoff():
         j = rng.integers(0, 8, mx.size)
         sig = sigma_at(mx, my, c00, c01, c11, x0, y0, i.astype(f32), j.astype(f32))
         power = np.where(sig >= 0, sig, f32(0)).astype(f32)  # pixel (i, j) passes with sigma == power
-        on = sig >= 0
+        on = sig <= power  # every pixel: one rounded below 0 passes against power 0
         qm = quadrant_mask(mx, my, f32(0.5) * c00, c01, f32(0.5) * c11, power, x0, y0)
         qbit = np.uint32(1) << (2 * (j // 4) + i // 4).astype(np.uint32)
         assert not (on & ((qm & qbit) == 0)).any(), "quadrant mask dropped a pixel on the cutoff"
