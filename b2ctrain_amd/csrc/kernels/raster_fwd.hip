@@ -111,7 +111,8 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     uint32_t marks_even = 0, marks_odd = 0;
     // One step: sigma <= power (a NaN sigma fails), bitwise & so the compiler does not branch on the
     // compares; the exp is kept out of an exec-masked branch (a lane whose fragment fails has its alpha
-    // discarded by the select); only a valid fragment can stop a lane. A fragment is
+    // discarded by the select); only a valid fragment can stop a lane. The transmittance after a fragment is
+    // fma(-alpha, T, T): T (1 - alpha) rounded once (the depth probe's walk does the same). A fragment is
     // composited (vis > 0) exactly when it is valid and does not stop the lane: a valid alpha is at least
     // 1/255 and a live lane's T is above the cutoff.
 #define B2C_COMPOSITE(off, next, marks)                                                                \
@@ -124,7 +125,7 @@ __global__ void __launch_bounds__(64) raster_fwd_kernel(b2c_raster_fwd_args a) {
     float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));                                        \
     asm volatile("" : "+v"(a_cl));                                                                     \
     const float alpha = valid ? a_cl : 0.f;                                                            \
-    const float next_T = T * (1.f - alpha);                                                            \
+    const float next_T = __builtin_fmaf(-alpha, T, T);                                                      \
     const bool stop = next_T <= T_CUTOFF;                                                              \
     live = live & !stop;                                                                               \
     const float vis = stop ? 0.f : alpha * T;                                                          \

@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(64) probe_kernel(b2c_probe_args a) {
     float a_cl = fminf(ALPHA_MAX, fragment_alpha(sigma, g1.y));                                         \
     asm volatile("" : "+v"(a_cl));                                                                      \
     const float alpha = valid ? a_cl : 0.f;                                                             \
-    const float next_T = T * (1.f - alpha);                                                             \
+    const float next_T = __builtin_fmaf(-alpha, T, T);                                                       \
     const bool stop = next_T <= T_CUTOFF;                                                               \
     live = live & !stop;                                                                                \
     const bool comp = valid & !stop;                                                                    \
