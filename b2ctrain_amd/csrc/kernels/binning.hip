@@ -143,21 +143,39 @@ __global__ void __launch_bounds__(SORT_THREADS) radix_upsweep(const uint32_t* __
 }
 
 // One workgroup per digit: exclusive scan of the digit's per-tile counts (each thread a contiguous run of
-// tiles), total into digit_total.
+// tiles), total into digit_total. Runs of up to SCAN_KEEP tiles (sorts of up to 2048 tiles: 8M keys at
+// 4096-key tiles) are read once and kept in registers; longer ones are read twice.
+constexpr uint32_t SCAN_KEEP = 8;
 __global__ void __launch_bounds__(SORT_THREADS) radix_scan_digits(uint32_t* __restrict__ block_hist, uint32_t nblocks,
                                                                   uint32_t* __restrict__ digit_total) {
   __shared__ uint32_t s_wsum[NWAVES];
   uint32_t* row = block_hist + (size_t)blockIdx.x * nblocks;
   const uint32_t per = (nblocks + SORT_THREADS - 1) / SORT_THREADS;
   const uint32_t lo = min(nblocks, threadIdx.x * per), hi = min(nblocks, lo + per);
-  uint32_t sum = 0;
-  for (uint32_t j = lo; j < hi; j++) sum += row[j];
   uint32_t tot;
-  uint32_t run = block_excl_scan(sum, s_wsum, tot);
-  for (uint32_t j = lo; j < hi; j++) {
-    const uint32_t v = row[j];
-    row[j] = run;
-    run += v;
+  if (per <= SCAN_KEEP) {  // uniform: the run stays in registers (one memory round trip)
+    uint32_t v[SCAN_KEEP];
+    uint32_t sum = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < SCAN_KEEP; k++) {
+      v[k] = lo + k < hi ? row[lo + k] : 0u;
+      sum += v[k];
+    }
+    uint32_t run = block_excl_scan(sum, s_wsum, tot);
+#pragma unroll
+    for (uint32_t k = 0; k < SCAN_KEEP; k++) {
+      if (lo + k < hi) row[lo + k] = run;
+      run += v[k];
+    }
+  } else {
+    uint32_t sum = 0;
+    for (uint32_t j = lo; j < hi; j++) sum += row[j];
+    uint32_t run = block_excl_scan(sum, s_wsum, tot);
+    for (uint32_t j = lo; j < hi; j++) {
+      const uint32_t v = row[j];
+      row[j] = run;
+      run += v;
+    }
   }
   if (threadIdx.x == 0) digit_total[blockIdx.x] = tot;
 }
