@@ -11,7 +11,7 @@ mis-ordered list, a wrong SSIM padding -- fails at least one test here.
 | orc_tile_hit               | splat_math.cuh:27-41                  | exact min of the quadratic over the box    |
 | orc_project                | project.cu:8-84, splat_math.cuh:224-293 | numpy fp64 EWA with a numerical Jacobian |
 | orc_bin                    | binning.cu:10-143                     | sortedness, stability, counts, no missed pixel-centre hit |
-| orc_raster_fwd             | raster_fwd.cu:8-71                    | fp64 brute force (pinned to the reference by the golden fixtures) |
+| orc_raster_fwd             | raster_fwd.cu:8-71                    | fp64 brute force (pinned to the reference by the golden fixtures), also with splats centred on pixel centres |
 | orc_photometric            | loss.cu:18-195, reference.cpp:106-131 | scipy.ndimage separable blur (zero padding); FD of v_out |
 | orc_raster_bwd + orc_vjp   | raster_bwd.cu, optim.cu:99-296        | reference FD fixtures (test_oracle_golden.py) |
 """
@@ -331,3 +331,48 @@ def test_photometric_value_and_gradient(seed, masked):
         b[p, c] -= h
         fd = (_photometric_numpy(sc, a, sc.bg) - _photometric_numpy(sc, b, sc.bg)) / (2 * h)
         assert abs(v[p, c] - fd) <= 2e-3 * abs(fd) + 1e-9, (p, c, v[p, c], fd)
+
+
+def _pixel_centred_scene(seed):
+    """Splats whose projections land exactly on pixel centres: camera at the origin looking down +z, fx = fy =
+    64, cx = cy = 32, splat means x = (k - 31.5) / 32 at depth z = 2, so 64 x / z + 32 = k + 0.5 in float
+    arithmetic. Small, mostly opaque, well separated, so each centre pixel's colour comes from one splat."""
+    rng = np.random.default_rng(seed)
+    W = H = 64
+    ks = rng.permutation(np.arange(2, 62, 5))
+    ls = rng.permutation(np.arange(2, 62, 5))
+    k, l = np.meshgrid(ks, ls)
+    k, l = k.ravel(), l.ravel()
+    n = k.size
+    pos = np.stack([(k - 31.5) / 32.0, (l - 31.5) / 32.0, np.full(n, 2.0)], 1)
+    op = rng.uniform(0.0, 3.0, n)  # opacity sigmoid(op): 0.5 .. 0.95
+    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
+    lscale = np.zeros((n, 4), np.float32)
+    lscale[:, :3] = rng.uniform(-4.5, -3.0, (n, 3))  # sigma 0.35 .. 1.6 px at depth 2, f = 64
+    sh = S._colour_to_dc(rng.random((n, 1, 3)))
+    cam = S.Camera(W, H, 64.0, 64.0, 32.0, 32.0, np.eye(3, dtype=np.float32).reshape(9), np.zeros(3, np.float32))
+    gt = S._pack_rgba(*rng.random((3, H * W)), np.ones(H * W))
+    return S.Scene("pixel-centred", 0, pos_op, S._rand_quat(rng, n), lscale, sh, cam, gt)
+
+
+@pytest.mark.parametrize("seed", [3, 11])
+def test_forward_keeps_fragments_at_the_splat_centre(seed):
+    """At a pixel centre on a splat's centre the exact sigma is 0. The tiled raster's sigma (the quadratic
+    about the tile centre) rounds there to a small value of either sign (about half of such pixels come out
+    below 0): the fragment passes when sigma <= power, as the exact value does, so the render equals the
+    fp64 brute force. A rule that also rejected sigma < 0 would drop those centre fragments (alpha 0.5 ..
+    0.95 of the pixel's colour)."""
+    sc = _pixel_centred_scene(seed)
+    sc.bg = (0.25, 0.5, 0.75)
+    out = O.pipeline(sc)
+    p0 = out["proj"]["proj0"]
+    vis = out["proj"]["tile_count"] > 0
+    assert vis.sum() == sc.n
+    # the centres really are pixel centres, and the quadratic rounds some of them below 0
+    assert np.array_equal(p0[:, 0] - np.floor(p0[:, 0]), np.full(sc.n, 0.5, np.float32))
+    assert np.array_equal(p0[:, 1] - np.floor(p0[:, 1]), np.full(sc.n, 0.5, np.float32))
+    sig = O.frag_sigma(p0[:, 0], p0[:, 1], p0[:, 2], p0[:, 3], out["proj"]["proj1"][:, 0], p0[:, 0], p0[:, 1])
+    assert (sig < 0).any() and (np.abs(sig) < 1e-4).all()
+    _, img = O.ref_loss(sc, want_img=True)
+    err = np.abs(out["fwd"]["out_rgba"] - img).max()
+    assert err <= 1e-4, err
