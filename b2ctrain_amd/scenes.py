@@ -325,6 +325,28 @@ def config5(seed: int | None = None, n: int = 500_000) -> Scene:
     return Scene("cfg5", 3, pos_op, _rand_quat(rng, n), lscale, _fp16_bands(sh), cam, gt, sh_fp16=True)
 
 
+def pixel_centred_scene(seed: int = 3) -> Scene:
+    """Splats whose projections land exactly on pixel centres: camera at the origin looking down +z, fx = fy =
+    64, cx = cy = 32, splat means x = (k - 31.5) / 32 at depth z = 2, so 64 x / z + 32 = k + 0.5 in float
+    arithmetic. Small, mostly opaque, well separated, so each centre pixel's colour comes from one splat."""
+    rng = np.random.default_rng(seed)
+    W = H = 64
+    ks = rng.permutation(np.arange(2, 62, 5))
+    ls = rng.permutation(np.arange(2, 62, 5))
+    k, l = np.meshgrid(ks, ls)
+    k, l = k.ravel(), l.ravel()
+    n = k.size
+    pos = np.stack([(k - 31.5) / 32.0, (l - 31.5) / 32.0, np.full(n, 2.0)], 1)
+    op = rng.uniform(0.0, 3.0, n)  # opacity sigmoid(op): 0.5 .. 0.95
+    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
+    lscale = np.zeros((n, 4), np.float32)
+    lscale[:, :3] = rng.uniform(-4.5, -3.0, (n, 3))  # sigma 0.35 .. 1.6 px at depth 2, f = 64
+    sh = _colour_to_dc(rng.random((n, 1, 3)))
+    cam = Camera(W, H, 64.0, 64.0, 32.0, 32.0, np.eye(3, dtype=np.float32).reshape(9), np.zeros(3, np.float32))
+    gt = _pack_rgba(*rng.random((3, H * W)), np.ones(H * W))
+    return Scene("pixel-centred", 0, pos_op, _rand_quat(rng, n), lscale, sh, cam, gt)
+
+
 def fd_scene(seed: int, n: int = 24, masked: bool = False, degree: int = 2, floor: bool = False) -> Scene:
     """The reference FD harness scene shape (tests/tests.cpp:23-59): 48x40, fx=fy=40, SH degree 2,
     means in [-0.6,0.6]x[-0.5,0.5]x[1.5,2.5], scales 0.05-0.13, jittered quaternions, opacity logits

@@ -42,6 +42,18 @@ def test_extension_scenes_all_stages(make, mode):
     assert out["M"] > 50
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_pixel_centred_splats_all_stages(mode):
+    """Every splat centred on a pixel centre, where the exact sigma is 0 and the tile-centred quadratic
+    rounds to a small value of either sign: the forward, both backward modes and the replays keep those
+    fragments (sigma <= power), so every stage matches the oracle and the image the fp64 brute force."""
+    sc = S.pixel_centred_scene(3)
+    sc.bg = (0.25, 0.5, 0.75)
+    emit(f"pixel-centred splats mode={mode}")
+    out = full_check(sc, mode=mode, fp64_rgba=True)
+    assert out["M"] >= sc.n
+
+
 def test_empty_model():
     """A model with no splats (every one pruned): forward, loss, both backward modes and the VJP run and
     leave a background-only image, with no list to walk."""

@@ -333,28 +333,6 @@ def test_photometric_value_and_gradient(seed, masked):
         assert abs(v[p, c] - fd) <= 2e-3 * abs(fd) + 1e-9, (p, c, v[p, c], fd)
 
 
-def _pixel_centred_scene(seed):
-    """Splats whose projections land exactly on pixel centres: camera at the origin looking down +z, fx = fy =
-    64, cx = cy = 32, splat means x = (k - 31.5) / 32 at depth z = 2, so 64 x / z + 32 = k + 0.5 in float
-    arithmetic. Small, mostly opaque, well separated, so each centre pixel's colour comes from one splat."""
-    rng = np.random.default_rng(seed)
-    W = H = 64
-    ks = rng.permutation(np.arange(2, 62, 5))
-    ls = rng.permutation(np.arange(2, 62, 5))
-    k, l = np.meshgrid(ks, ls)
-    k, l = k.ravel(), l.ravel()
-    n = k.size
-    pos = np.stack([(k - 31.5) / 32.0, (l - 31.5) / 32.0, np.full(n, 2.0)], 1)
-    op = rng.uniform(0.0, 3.0, n)  # opacity sigmoid(op): 0.5 .. 0.95
-    pos_op = np.concatenate([pos, op[:, None]], 1).astype(np.float32)
-    lscale = np.zeros((n, 4), np.float32)
-    lscale[:, :3] = rng.uniform(-4.5, -3.0, (n, 3))  # sigma 0.35 .. 1.6 px at depth 2, f = 64
-    sh = S._colour_to_dc(rng.random((n, 1, 3)))
-    cam = S.Camera(W, H, 64.0, 64.0, 32.0, 32.0, np.eye(3, dtype=np.float32).reshape(9), np.zeros(3, np.float32))
-    gt = S._pack_rgba(*rng.random((3, H * W)), np.ones(H * W))
-    return S.Scene("pixel-centred", 0, pos_op, S._rand_quat(rng, n), lscale, sh, cam, gt)
-
-
 @pytest.mark.parametrize("seed", [3, 11])
 def test_forward_keeps_fragments_at_the_splat_centre(seed):
     """At a pixel centre on a splat's centre the exact sigma is 0. The tiled raster's sigma (the quadratic
@@ -362,7 +340,7 @@ def test_forward_keeps_fragments_at_the_splat_centre(seed):
     below 0): the fragment passes when sigma <= power, as the exact value does, so the render equals the
     fp64 brute force. A rule that also rejected sigma < 0 would drop those centre fragments (alpha 0.5 ..
     0.95 of the pixel's colour)."""
-    sc = _pixel_centred_scene(seed)
+    sc = S.pixel_centred_scene(seed)
     sc.bg = (0.25, 0.5, 0.75)
     out = O.pipeline(sc)
     p0 = out["proj"]["proj0"]
