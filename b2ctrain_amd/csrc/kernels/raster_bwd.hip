@@ -206,9 +206,14 @@ __global__ void __launch_bounds__(64) raster_bwd_fp32_kernel(b2c_raster_bwd_args
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int BATCH = 64;  // splats staged in LDS per step
+// Splats staged in LDS per step: 48 keeps the plain kernel's LDS at 8 KB, so five one-wave workgroups fit
+// per SIMD instead of four (a batch is a whole number of groups, cut from the list end, so the groups of 8
+// are the same splats whatever the batch size).
+constexpr int BATCH = 48;
 constexpr int G = 8;       // splats per MFMA group
+static_assert(BATCH % G == 0, "batches of whole groups");
 constexpr int SROW = 68;   // pixel stride of the per-fragment scalar rows (64 + 4: spreads the B reads over banks)
+constexpr int SROW_H = 72;  // pixel stride of the fp16 refine rows (a multiple of 8: 16-byte aligned reads)
 // (tile, splat) row: raw moments of the tile's fragments about the tile centre, 12 floats in three 16-byte
 // quarters, each written by one lane with one store: sum v_sigma * [v, u^2, uv, v^2] | sum v_sigma * [1, u],
 // sum vis, refine sum | sum vis * v_rgb, the tag word row_tag | tile (bits); with feature lanes a fourth
@@ -246,24 +251,12 @@ __device__ __forceinline__ void split8(const float* x, half8& hi, half8& lo) {
   }
 }
 
-// fp16 only, truncated (the refine statistic: a sum of non-negative terms, under 2^-10 relative each).
-__device__ __forceinline__ half8 to_half8(const float* x) {
-  half8 h;
-#pragma unroll
-  for (int e = 0; e < 8; e += 2) {
-    const half2v p = pk_rtz(x[e], x[e + 1]);
-    h[e] = p.x;
-    h[e + 1] = p.y;
-  }
-  return h;
-}
-
 __device__ __forceinline__ void load8(const float* p, float* x) {
   const float4 q0 = reinterpret_cast<const float4*>(p)[0], q1 = reinterpret_cast<const float4*>(p)[1];
   x[0] = q0.x; x[1] = q0.y; x[2] = q0.z; x[3] = q0.w; x[4] = q1.x; x[5] = q1.y; x[6] = q1.z; x[7] = q1.w;
 }
 
-// One wave64 per 8x8 tile, one lane per pixel. The tile's list is replayed back to front in batches of 64
+// One wave64 per 8x8 tile, one lane per pixel. The tile's list is replayed back to front in batches of 48
 // splats staged in LDS and groups of 8: for each splat of a group every lane writes three scalars of its
 // fragment (blend weight vis, v_sigma, refine) into LDS; then two 16x16x32 f16 MFMA products per 32 pixels
 // contract them against the per-pixel basis (columns 0-7 vis, 8-15 v_sigma of the group's splats; second
@@ -279,7 +272,10 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
   __shared__ float4 s_col[BATCH];  // (max(r, 0), max(g, 0), max(b, 0), sign bits of r, g, b)
   __shared__ float4 s_ext[EXT ? BATCH : 1];  // (feature xyz, camera depth)
   __shared__ uint32_t s_slot[BATCH];
-  __shared__ __attribute__((aligned(16))) float sS[3 * G][SROW];  // rows 0-7 vis, 8-15 v_sigma, 16-23 refine
+  __shared__ __attribute__((aligned(16))) float sS[2 * G][SROW];  // rows 0-7 vis, 8-15 v_sigma
+  // the refine products, already the fp16 operand of their MFMA (truncated as the conversion of fp32 rows
+  // would be)
+  __shared__ __attribute__((aligned(16))) _Float16 sR[G][SROW_H];
   const int n_tiles = a.tiles_x * a.tiles_y;
   const int tile = xcd_tile(blockIdx.x, n_tiles);
   if (tile >= n_tiles) return;
@@ -409,7 +405,7 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
         }
         sS[jj][lane] = o_vis;
         sS[G + jj][lane] = o_vs;
-        sS[2 * G + jj][lane] = o_r;
+        sR[jj][lane] = pk_rtz(o_r, 0.f).x;
       }
       __syncthreads();
       // ---- reduction over the 64 pixels on MFMA
@@ -424,8 +420,8 @@ __global__ void __launch_bounds__(64) raster_bwd_mfma_kernel(b2c_raster_bwd_args
         d0_hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_hi, d0_hi, 0, 0, 0);
         d0_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], b_lo, d0_lo, 0, 0, 0);
         d0_lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_lo[kb], b_hi, d0_lo, 0, 0, 0);
-        load8(&sS[2 * G + (nl & (G - 1))][kb * 32 + kg * 8], x);  // columns 8-15 of d1 are unused
-        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], to_half8(x), d1, 0, 0, 0);
+        const half8 rb = *reinterpret_cast<const half8*>(&sR[nl & (G - 1)][kb * 32 + kg * 8]);  // columns 8-15 of d1 are unused
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A_hi[kb], rb, d1, 0, 0, 0);
       }
       // D layout: lane (nl, kg) holds rows 4 kg .. 4 kg + 3 of column nl. Three lanes per splat j store the
       // (tile, splat) row's raw moments (the reduce turns them into gradients), one 16-byte quarter each:
